@@ -1,0 +1,87 @@
+/*
+ * trnsparse_hip.h — C ABI of the MI355X (gfx950) trnsparse compute path.
+ *
+ * This is the drop-in boundary that replaces the reference's device seam:
+ * the `nki_*` entry points that `trnsparse/ops.py` lazily imports when the
+ * accelerator backend is active (trnsparse/nki/dispatch.py). Every function
+ *   - takes plain device pointers, sizes and dtype codes (no torch types),
+ *   - launches asynchronously on the caller's HIP stream (`stream`, a
+ *     hipStream_t passed as void*; NULL = the default stream),
+ *   - never allocates or frees caller memory and keeps no pointer after it
+ *     returns (workspace, when needed, is passed in by the caller),
+ *   - returns TSP_OK (0) or a negative status; the message of the last
+ *     failure on the calling thread is available from tsp_last_error().
+ * No C++ exception crosses this boundary.
+ *
+ * Structure arrays (row pointers, column indices) use int64 like the
+ * reference's torch.long tensors (trnsparse/formats.py); CSR entry points
+ * also accept int32 via `index_type`.
+ */
+#ifndef TRNSPARSE_HIP_H
+#define TRNSPARSE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------- */
+#define TSP_OK 0
+#define TSP_EINVAL (-1)       /* bad argument (shape, pointer, alignment)   */
+#define TSP_EUNSUPPORTED (-2) /* valid request this library does not serve  */
+#define TSP_EHIP (-3)         /* a HIP runtime call or kernel launch failed */
+
+/* ---- element type codes ---------------------------------------------- */
+#define TSP_F32 0
+#define TSP_F64 1
+#define TSP_BF16 2
+
+/* ---- index type codes (CSR) ------------------------------------------ */
+#define TSP_I32 0
+#define TSP_I64 1
+
+/* Library version as 100*major + minor. */
+int tsp_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* tsp_last_error(void);
+
+/* ======================================================================
+ * Block-sparse (BSR) x dense:  C[m, ncols] = A_bsr[m, n] @ B[n, ncols]
+ *
+ * Replaces nki_bsr_spmm / _BSRSpMMFunction forward
+ * (trnsparse/nki/dispatch.py:372-381, :304-328) and the torch spec
+ * _bsr_spmm_pytorch (trnsparse/ops.py:162-192).
+ *
+ * blocks            (n_blocks, block_size, block_size), row-major, `dtype`
+ * block_row_ptrs    (ceil(m/block_size)+1,) int64
+ * block_col_indices (n_blocks,) int64
+ * B                 (n, ncols) with row stride ldb (elements), `dtype`
+ * C                 (m, ncols) with row stride ldc, `out_dtype`; every
+ *                   element is written (no pre-zeroing needed)
+ * row_order         optional (ceil(m/block_size),) int32 permutation of the
+ *                   block rows, heaviest first (see tsp_bsr_row_order);
+ *                   only changes scheduling, never results. NULL = natural.
+ * dtype/out_dtype   TSP_F32/TSP_F32, TSP_BF16/{TSP_BF16,TSP_F32},
+ *                   TSP_F64/TSP_F64. Accumulation is fp32 (fp64 for F64).
+ * ==================================================================== */
+int tsp_bsr_spmm(const void* blocks, int dtype,
+                 const int64_t* block_row_ptrs, const int64_t* block_col_indices,
+                 int64_t n_blocks, int64_t block_size, int64_t m, int64_t n,
+                 const void* B, int64_t ldb, int64_t ncols,
+                 void* C, int64_t ldc, int out_dtype,
+                 const int32_t* row_order, void* stream);
+
+/* Heaviest-first ordering of block rows (counting sort by stored blocks per
+ * row, computed on the device). `order` receives n_block_rows int32. It is
+ * a scheduling plan for tsp_bsr_spmm, a property of the sparsity pattern
+ * only, and may be cached with it. */
+int tsp_bsr_row_order(const int64_t* block_row_ptrs, int64_t n_block_rows,
+                      int32_t* order, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRNSPARSE_HIP_H */

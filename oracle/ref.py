@@ -1,0 +1,211 @@
+"""CPU oracle for the trnsparse compute path — TEST INFRASTRUCTURE ONLY.
+
+Only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of
+`bench.py` may import this package, and only as the checker. The product
+(`trnsparse_amd`) never imports, calls or links anything here.
+
+Each function restates the reference semantics in numpy, accumulating in
+float64, so the GPU result can be judged against the exact value with a
+tolerance scaled by |A|.|B| (the dot-product error scale). Citations point
+into the reference tree (trnsci/trnsparse).
+
+How each function is pinned (tests/test_oracle.py):
+- bsr_from_dense / bsr_to_dense: brute-force per-block loops on tiny grids,
+  round trips, the empty-matrix case, padding of unaligned shapes.
+- bsr_spmm: closed form to_dense(A) @ B (numpy matmul), empty pattern -> 0.
+- csr_spmv / csr_spmm: scipy.sparse (independent implementation), the
+  reference's known answers [9, 16] and 7.0 (tests/test_ops.py:25-32, 61-67),
+  identity.
+- screened_mask / screened_spmm: threshold 0 -> A@B, 1e30 -> exact zeros,
+  hand-built values straddling fl32(1e-10) (torch's fp32 compare).
+- block_sparse_attention: dense masked softmax (numpy), a full mask equals
+  dense attention, empty block rows give zeros.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+# ------------------------------------------------------------------ BSR
+
+
+def bsr_from_dense(A: np.ndarray, b: int, threshold: float = 0.0):
+    """(blocks, col_idx, row_ptrs, shape) as formats.py:183-221 builds them.
+
+    Pad to a block multiple; block (i, j) is kept iff max|v| > threshold;
+    blocks are listed row-major (block columns ascending within a row).
+    """
+    m, n = A.shape
+    mp, np_ = -(-m // b) * b, -(-n // b) * b
+    P = np.zeros((mp, np_), dtype=A.dtype)
+    P[:m, :n] = A
+    mb, nbc = mp // b, np_ // b
+    grid = P.reshape(mb, b, nbc, b).transpose(0, 2, 1, 3)
+    keep = np.abs(grid).max(axis=(2, 3)) > threshold if mb and nbc else np.zeros((mb, nbc), bool)
+    row_ptrs = np.zeros(mb + 1, dtype=np.int64)
+    row_ptrs[1:] = np.cumsum(keep.sum(axis=1))
+    rows, cols = np.nonzero(keep)
+    blocks = np.ascontiguousarray(grid[rows, cols]) if len(rows) else np.zeros((0, b, b), A.dtype)
+    return blocks, cols.astype(np.int64), row_ptrs, (m, n)
+
+
+def bsr_to_dense(blocks, col_idx, row_ptrs, shape, b):
+    m, n = shape
+    mp, np_ = -(-m // b) * b, -(-n // b) * b
+    D = np.zeros((mp, np_), dtype=np.float64)
+    for i in range(len(row_ptrs) - 1):
+        for idx in range(row_ptrs[i], row_ptrs[i + 1]):
+            j = col_idx[idx]
+            D[i * b : (i + 1) * b, j * b : (j + 1) * b] = blocks[idx]
+    return D[:m, :n]
+
+
+def bsr_spmm(blocks, col_idx, row_ptrs, shape, b, B, absolute: bool = False):
+    """C = A @ B in float64 over stored blocks (reference ops.py:162-192).
+
+    With absolute=True returns |A| @ |B|, the per-element error scale.
+    """
+    m, n = shape
+    N = B.shape[1]
+    mb = len(row_ptrs) - 1
+    Bp = np.zeros((-(-n // b) * b, N))
+    Bp[:n] = np.abs(B) if absolute else B
+    C = np.zeros((mb * b, N))
+    for i in range(mb):
+        acc = C[i * b : (i + 1) * b]
+        for idx in range(row_ptrs[i], row_ptrs[i + 1]):
+            j = col_idx[idx]
+            blk = blocks[idx].astype(np.float64)
+            acc += (np.abs(blk) if absolute else blk) @ Bp[j * b : (j + 1) * b]
+    return C[:m]
+
+
+# ------------------------------------------------------------------ CSR
+
+
+def csr_rows(row_ptrs: np.ndarray) -> np.ndarray:
+    m = len(row_ptrs) - 1
+    return np.repeat(np.arange(m, dtype=np.int64), np.diff(row_ptrs))
+
+
+def csr_spmv(values, col_idx, row_ptrs, shape, x, alpha=1.0, y=None, beta=0.0, absolute=False):
+    """y = alpha*(A@x) [+ beta*y] in float64 (reference ops.py:30-48)."""
+    m, _ = shape
+    v = values.astype(np.float64)
+    xv = x.astype(np.float64)
+    if absolute:
+        v, xv = np.abs(v), np.abs(xv)
+    prod = v * xv[col_idx]
+    out = np.bincount(csr_rows(row_ptrs), weights=prod, minlength=m)
+    out = (abs(alpha) if absolute else alpha) * out
+    if y is not None and beta != 0.0:
+        yy = y.astype(np.float64)
+        out = out + ((abs(beta) * np.abs(yy)) if absolute else beta * yy)
+    return out
+
+
+def csr_spmm(values, col_idx, row_ptrs, shape, B, alpha=1.0, C=None, beta=0.0, absolute=False):
+    """C = alpha*(A@B) [+ beta*C] in float64 (reference ops.py:51-78)."""
+    m, _ = shape
+    v = values.astype(np.float64)
+    Bv = B.astype(np.float64)
+    if absolute:
+        v, Bv = np.abs(v), np.abs(Bv)
+    out = np.zeros((m, B.shape[1]))
+    np.add.at(out, csr_rows(row_ptrs), v[:, None] * Bv[col_idx])
+    out = (abs(alpha) if absolute else alpha) * out
+    if C is not None and beta != 0.0:
+        Cv = C.astype(np.float64)
+        out = out + ((abs(beta) * np.abs(Cv)) if absolute else beta * Cv)
+    return out
+
+
+# ------------------------------------------------------------- screened
+
+
+def screened_mask(diag: np.ndarray, threshold: float) -> np.ndarray:
+    """mask[i,j] = fl(Q_i*Q_j) > fl(sqrt(threshold)), Q = fl(sqrt(|d|)).
+
+    All three operations run in diag's precision (reference ops.py:273-276:
+    torch evaluates the product in the tensor dtype and converts the Python
+    float sqrt(threshold) to that dtype before comparing).
+    """
+    dt = diag.dtype
+    Q = np.sqrt(np.abs(diag)).astype(dt)
+    pair = np.multiply.outer(Q, Q).astype(dt)
+    return pair > dt.type(math.sqrt(threshold))
+
+
+def screened_spmm(A, diag, B, threshold, absolute=False):
+    """C = (A * mask) @ B in float64 (reference ops.py:262-277)."""
+    mask = screened_mask(diag, threshold)
+    Am = np.where(mask, A.astype(np.float64), 0.0)
+    Bv = B.astype(np.float64)
+    if absolute:
+        Am, Bv = np.abs(Am), np.abs(Bv)
+    return Am @ Bv
+
+
+# ------------------------------------------------------------ attention
+
+
+def block_sparse_attention(Q, K, V, row_ptrs, col_idx, b, scale):
+    """Block-sparse attention in float64 (reference ops.py:280-357).
+
+    The reference's pass 1 + reduction (tile max / stable exp-sum combined
+    into row_max, row_denom) computes the exact row max and softmax
+    denominator over the keys of the stored blocks; in float64 they are
+    formed directly here. A block listed twice counts twice, as there.
+    Returns (out, row_max, row_denom) with stats shaped (M_tiles, b).
+    Empty block rows: row_max 0, row_denom 1e-12, output 0.
+    """
+    S, D = Q.shape
+    Mt = S // b
+    q, k, v = (t.astype(np.float64) for t in (Q, K, V))
+    out = np.zeros((S, D))
+    rmax = np.zeros((Mt, b))
+    rden = np.full((Mt, b), 1e-12)
+    for m in range(Mt):
+        s, e = row_ptrs[m], row_ptrs[m + 1]
+        if s == e:
+            continue
+        cols = col_idx[s:e]
+        keys = np.concatenate([np.arange(c * b, (c + 1) * b) for c in cols])
+        sc = (q[m * b : (m + 1) * b] @ k[keys].T) * scale
+        mx = sc.max(axis=1)
+        p = np.exp(sc - mx[:, None])
+        den = np.maximum(p.sum(axis=1), 1e-12)
+        out[m * b : (m + 1) * b] = (p / den[:, None]) @ v[keys]
+        rmax[m] = mx
+        rden[m] = den
+    return out, rmax, rden
+
+
+def dense_masked_attention(Q, K, V, mask, scale):
+    """softmax(scale*Q@K^T masked to -inf off `mask`) @ V in float64
+    (the dense oracle of the reference, examples/block_sparse_attention.py:161-172)."""
+    sc = (Q.astype(np.float64) @ K.astype(np.float64).T) * scale
+    sc = np.where(mask, sc, -np.inf)
+    mx = sc.max(axis=1, keepdims=True)
+    p = np.exp(sc - mx)
+    p /= p.sum(axis=1, keepdims=True)
+    return p @ V.astype(np.float64)
+
+
+# ------------------------------------------------------------- metrics
+
+
+def scaled_error(got, ref, scale, floor: float = 1e-30) -> float:
+    """max_ij |got-ref| / (|A|.|B|)_ij — the dot-product error measure."""
+    got = np.asarray(got, dtype=np.float64)
+    return float(np.max(np.abs(got - ref) / np.maximum(scale, floor), initial=0.0))
+
+
+def rel_max_error(got, ref) -> float:
+    """max|got-ref| / max|ref|."""
+    got = np.asarray(got, dtype=np.float64)
+    den = float(np.max(np.abs(ref), initial=0.0))
+    num = float(np.max(np.abs(got - ref), initial=0.0))
+    return num / den if den > 0 else num

@@ -1,0 +1,157 @@
+"""GPU parity of bsr_spmm (HIP kernels via the C ABI) against the CPU oracle.
+
+Tolerances: fp32 max error <= 1e-4 and bf16 inputs
+<= 2e-2, both measured relative to the dot-product scale (|A|.|B|)_ij; the
+reference's own hardware tolerance (tests/test_nki_bsr.py:19, atol 1e-3,
+rtol 1e-4 vs dense A@B) is checked as well for fp32.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import trnsparse_amd as ts
+from oracle import ref
+from trnsparse_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-4
+TOL_BF16 = 2e-2
+
+
+def _oracle(A: ts.BSRMatrix, B: torch.Tensor, rows=None):
+    blocks = A.blocks.float().cpu().numpy() if A.dtype == torch.bfloat16 else A.blocks.cpu().numpy()
+    Bn = B.float().cpu().numpy() if B.dtype == torch.bfloat16 else B.cpu().numpy()
+    col = A.block_col_indices.cpu().numpy()
+    ptr = A.block_row_ptrs.cpu().numpy()
+    if rows is not None:  # restrict to a subset of block rows (full-size checks)
+        keep_blocks = np.concatenate([np.arange(ptr[i], ptr[i + 1]) for i in rows])
+        sub_ptr = np.zeros(len(rows) + 1, np.int64)
+        sub_ptr[1:] = np.cumsum([ptr[i + 1] - ptr[i] for i in rows])
+        blocks, col, ptr = blocks[keep_blocks], col[keep_blocks], sub_ptr
+        shape = (len(rows) * A.block_size, A.shape[1])
+    else:
+        shape = A.shape
+    exact = ref.bsr_spmm(blocks, col, ptr, shape, A.block_size, Bn)
+    scale = ref.bsr_spmm(blocks, col, ptr, shape, A.block_size, Bn, absolute=True)
+    return exact, scale
+
+
+def _block_random(m_blocks, n_blocks, b, density, seed):
+    torch.manual_seed(seed)
+    A = torch.zeros(m_blocks * b, n_blocks * b)
+    mask = torch.rand(m_blocks, n_blocks) < density
+    for i in range(m_blocks):
+        for j in range(n_blocks):
+            if mask[i, j]:
+                A[i * b : (i + 1) * b, j * b : (j + 1) * b] = torch.randn(b, b)
+    return A
+
+
+# reference grid: tests/test_nki_bsr.py:44-51 (seed 42)
+@pytest.mark.parametrize("m_blocks,n_blocks,N,density", [(2, 2, 128, 0.5), (4, 4, 128, 0.25), (3, 3, 256, 0.5), (4, 2, 128, 0.5)])
+def test_reference_grid(hip_backend, m_blocks, n_blocks, N, density):
+    A = _block_random(m_blocks, n_blocks, 128, density, seed=42)
+    bsr = ts.BSRMatrix.from_dense(A, block_size=128)
+    B = torch.randn(n_blocks * 128, N)
+    got = ts.bsr_spmm(bsr, B.cuda())
+    assert got.is_cuda and got.dtype == torch.float32 and got.shape == (m_blocks * 128, N)
+    exact, scale = _oracle(bsr, B)
+    assert ref.scaled_error(got.cpu().numpy(), exact, scale) <= TOL_F32
+    torch.testing.assert_close(got.cpu(), A @ B, atol=1e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize(
+    "shape,b,N,density",
+    [
+        ((24, 24), 8, 16, 0.5),  # reference tests/test_bsr.py:68-74 (generic kernel)
+        ((20, 14), 8, 10, 1.0),  # unaligned, :76-83
+        ((40, 40), 8, 12, 0.1),  # sparse, :85-93
+        ((200, 137), 128, 64, 1.0),  # unaligned 128-blocks (MFMA kernel bounds)
+        ((300, 260), 128, 10, 1.0),  # N not a multiple of 4 (padded B panels)
+        ((384, 256), 128, 200, 0.6),  # partial column tile
+        ((256, 256), 64, 96, 0.7),  # block size 64 (generic kernel)
+    ],
+)
+def test_shapes(hip_backend, shape, b, N, density):
+    g = torch.Generator().manual_seed(11)
+    A = torch.randn(*shape, generator=g) * (torch.rand(*shape, generator=g) < density)
+    bsr = ts.BSRMatrix.from_dense(A, block_size=b)
+    B = torch.randn(shape[1], N, generator=g)
+    got = ts.bsr_spmm(bsr, B.cuda()).cpu()
+    exact, scale = _oracle(bsr, B)
+    assert got.shape == (shape[0], N)
+    assert ref.scaled_error(got.numpy(), exact, scale) <= TOL_F32
+
+
+def test_empty_pattern_is_zero(hip_backend):
+    A = torch.zeros(256, 256)
+    bsr = ts.BSRMatrix.from_dense(A, block_size=128)
+    assert bsr.n_blocks == 0
+    got = ts.bsr_spmm(bsr, torch.randn(256, 64).cuda())
+    assert torch.count_nonzero(got).item() == 0
+
+
+def test_empty_rows_and_cpu_inputs(hip_backend):
+    """Block rows without blocks give zeros; host inputs come back on the host."""
+    A = _block_random(4, 4, 128, 0.5, seed=3)
+    A[128:256] = 0.0
+    bsr = ts.BSRMatrix.from_dense(A, block_size=128)
+    B = torch.randn(512, 128)
+    got = ts.bsr_spmm(bsr, B)
+    assert got.device.type == "cpu"
+    assert torch.count_nonzero(got[128:256]).item() == 0
+    exact, scale = _oracle(bsr, B)
+    assert ref.scaled_error(got.numpy(), exact, scale) <= TOL_F32
+
+
+def test_f64_generic(hip_backend):
+    A = _block_random(2, 3, 16, 0.6, seed=5).double()
+    bsr = ts.BSRMatrix.from_dense(A, block_size=16)
+    B = torch.randn(48, 7, dtype=torch.float64)
+    got = ts.bsr_spmm(bsr, B.cuda()).cpu()
+    torch.testing.assert_close(got, A @ B, rtol=1e-12, atol=1e-12)
+
+
+def test_dtype_mismatch_raises(hip_backend):
+    bsr = ts.BSRMatrix.from_dense(torch.randn(128, 128), block_size=128)
+    with pytest.raises(RuntimeError):
+        ts.bsr_spmm(bsr, torch.randn(128, 8, dtype=torch.float64).cuda())
+    with pytest.raises(AssertionError):
+        ts.bsr_spmm(bsr, torch.randn(64, 8).cuda())
+
+
+def test_cfg1_plumbing(hip_backend):
+    A, B, Ad = W.cfg1_bsr_plumbing()
+    assert A.n_blocks == 24
+    got = ts.bsr_spmm(A, B.cuda()).cpu()
+    exact, scale = _oracle(A, B)
+    assert ref.scaled_error(got.numpy(), exact, scale) <= TOL_F32
+
+
+def test_cfg3_fp32_full_size(hip_backend):
+    """16384^2, 10% block density, N=512: every 16th block row vs the oracle,
+    plus the full-size checksum property sum(C) = colsum(A) . rowsum(B)."""
+    A, B = W.cfg3_bsr()
+    C = ts.bsr_spmm(A, B.cuda())
+    rows = list(range(0, 128, 16)) + [1, 126, 127]
+    exact, scale = _oracle(A, B, rows=rows)
+    got = torch.cat([C[r * 128 : (r + 1) * 128] for r in rows]).cpu().numpy()
+    assert ref.scaled_error(got, exact, scale) <= TOL_F32
+    # linearity: C @ 1 = A @ (B @ 1) for every row, at full size
+    ones = torch.ones(B.shape[1], 1, dtype=torch.float64)
+    lhs = C.double().cpu() @ ones
+    rhs = ts.bsr_spmm(A, (B.double() @ ones).float().cuda()).double().cpu()
+    sc = torch.from_numpy(ref.bsr_spmm(A.blocks.numpy(), A.block_col_indices.numpy(), A.block_row_ptrs.numpy(), A.shape, 128, np.abs(B.numpy()).sum(1, keepdims=True), absolute=True))
+    assert ((lhs - rhs).abs() / sc.clamp_min(1e-30)).max().item() <= TOL_F32
+
+
+def test_repeat_calls_are_deterministic(hip_backend):
+    A, B = W.cfg3_bsr(nb=32, ncols=256)
+    Bd = B.cuda()
+    c1 = ts.bsr_spmm(A, Bd)
+    c2 = ts.bsr_spmm(A, Bd)
+    assert torch.equal(c1, c2)

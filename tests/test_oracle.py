@@ -1,0 +1,221 @@
+"""Pins of the CPU oracle (oracle/ref.py) against independent checks.
+
+Each check is chosen so that a plausible mistake in the oracle (a dropped
+block, a transposed operand, a wrong mask compare, a missing alpha/beta
+term, an off-by-one block row) fails: closed forms via dense numpy/scipy,
+the reference tests' known answers, brute force on tiny inputs.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import scipy.sparse as sp
+
+from oracle import ref
+
+
+def _block_random(mb, nb, b, density, seed):
+    rng = np.random.default_rng(seed)
+    keep = rng.random((mb, nb)) < density
+    A = np.zeros((mb * b, nb * b), np.float32)
+    for i in range(mb):
+        for j in range(nb):
+            if keep[i, j]:
+                A[i * b : (i + 1) * b, j * b : (j + 1) * b] = rng.standard_normal((b, b))
+    return A, keep
+
+
+# ------------------------------------------------------------------ BSR
+
+
+def test_bsr_from_dense_brute_force():
+    A, keep = _block_random(5, 4, 8, 0.4, seed=1)
+    blocks, col, ptr, shape = ref.bsr_from_dense(A, 8)
+    exp_cols, exp_ptr = [], [0]
+    for i in range(5):
+        for j in range(4):
+            if np.abs(A[i * 8 : (i + 1) * 8, j * 8 : (j + 1) * 8]).max() > 0:
+                exp_cols.append(j)
+        exp_ptr.append(len(exp_cols))
+    assert col.tolist() == exp_cols and ptr.tolist() == exp_ptr and shape == A.shape
+    assert col.dtype == np.int64 and ptr.dtype == np.int64
+    for idx, j in enumerate(exp_cols):
+        i = np.searchsorted(ptr, idx, side="right") - 1
+        np.testing.assert_array_equal(blocks[idx], A[i * 8 : (i + 1) * 8, j * 8 : (j + 1) * 8])
+
+
+def test_bsr_threshold_and_empty():
+    A = np.zeros((16, 16), np.float32)
+    blocks, col, ptr, _ = ref.bsr_from_dense(A, 8)
+    assert len(blocks) == 0 and ptr.tolist() == [0, 0, 0]
+    A[3, 12] = 0.5
+    _, col, ptr, _ = ref.bsr_from_dense(A, 8, threshold=0.5)
+    assert ptr.tolist() == [0, 0, 0]  # strict >
+    _, col, ptr, _ = ref.bsr_from_dense(A, 8, threshold=0.49)
+    assert ptr.tolist() == [0, 1, 1] and col.tolist() == [1]
+
+
+def test_bsr_roundtrip_unaligned():
+    rng = np.random.default_rng(2)
+    A = rng.standard_normal((20, 14)).astype(np.float32)
+    blocks, col, ptr, shape = ref.bsr_from_dense(A, 8)
+    assert shape == (20, 14) and len(ptr) == 4
+    np.testing.assert_array_equal(ref.bsr_to_dense(blocks, col, ptr, shape, 8), A)
+
+
+@pytest.mark.parametrize("shape,b,density", [((24, 24), 8, 0.5), ((20, 14), 8, 1.0), ((40, 40), 8, 0.1)])
+def test_bsr_spmm_closed_form(shape, b, density):
+    rng = np.random.default_rng(3)
+    A = rng.standard_normal(shape) * (rng.random(shape) < density)
+    B = rng.standard_normal((shape[1], 12))
+    blocks, col, ptr, sh = ref.bsr_from_dense(A, b)
+    np.testing.assert_allclose(ref.bsr_spmm(blocks, col, ptr, sh, b, B), A @ B, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(
+        ref.bsr_spmm(blocks, col, ptr, sh, b, B, absolute=True), np.abs(A) @ np.abs(B), rtol=1e-12
+    )
+
+
+def test_bsr_spmm_empty_pattern_is_zero():
+    A = np.zeros((16, 16))
+    blocks, col, ptr, sh = ref.bsr_from_dense(A, 8)
+    out = ref.bsr_spmm(blocks, col, ptr, sh, 8, np.ones((16, 8)))
+    assert out.shape == (16, 8) and not out.any()
+
+
+# ------------------------------------------------------------------ CSR
+
+
+def _csr(A):
+    s = sp.csr_matrix(A)
+    return s.data, s.indices.astype(np.int64), s.indptr.astype(np.int64), A.shape
+
+
+def test_spmv_known_answer_alpha_beta():
+    # reference tests/test_ops.py:25-32: 2*[2,3] + 0.5*[10,20] = [9, 16]
+    v, c, p, sh = _csr(np.array([[2.0, 0.0], [0.0, 3.0]]))
+    out = ref.csr_spmv(v, c, p, sh, np.ones(2), alpha=2.0, y=np.array([10.0, 20.0]), beta=0.5)
+    np.testing.assert_array_equal(out, [9.0, 16.0])
+    # y ignored when beta == 0
+    out = ref.csr_spmv(v, c, p, sh, np.ones(2), alpha=2.0, y=np.array([10.0, 20.0]), beta=0.0)
+    np.testing.assert_array_equal(out, [4.0, 6.0])
+
+
+def test_spmv_vs_scipy_with_empty_rows():
+    rng = np.random.default_rng(4)
+    A = rng.standard_normal((300, 200)) * (rng.random((300, 200)) < 0.03)
+    A[17] = 0.0
+    A[-1] = 0.0
+    v, c, p, sh = _csr(A)
+    x = rng.standard_normal(200)
+    np.testing.assert_allclose(ref.csr_spmv(v, c, p, sh, x), sp.csr_matrix(A) @ x, rtol=1e-12, atol=1e-12)
+
+
+def test_spmm_known_answer_and_scipy():
+    # reference tests/test_ops.py:61-67: 2*I@ones + 0.5*10 = 7
+    v, c, p, sh = _csr(np.eye(2))
+    out = ref.csr_spmm(v, c, p, sh, np.ones((2, 3)), alpha=2.0, C=np.full((2, 3), 10.0), beta=0.5)
+    np.testing.assert_array_equal(out, np.full((2, 3), 7.0))
+    rng = np.random.default_rng(5)
+    A = rng.standard_normal((200, 137)) * (rng.random((200, 137)) < 0.05)
+    B = rng.standard_normal((137, 64))
+    v, c, p, sh = _csr(A)
+    np.testing.assert_allclose(ref.csr_spmm(v, c, p, sh, B), A @ B, rtol=1e-12, atol=1e-12)
+
+
+# -------------------------------------------------------------- screened
+
+
+def test_screened_threshold_zero_is_matmul():
+    rng = np.random.default_rng(6)
+    A = rng.standard_normal((64, 64))
+    d = np.abs(rng.standard_normal(64)).astype(np.float32) + 0.1
+    B = rng.standard_normal((64, 16))
+    np.testing.assert_allclose(ref.screened_spmm(A, d, B, 0.0), A @ B, rtol=1e-12)
+
+
+def test_screened_huge_threshold_is_exact_zero():
+    rng = np.random.default_rng(7)
+    out = ref.screened_spmm(rng.standard_normal((64, 64)), np.abs(rng.standard_normal(64)).astype(np.float32),
+                            rng.standard_normal((64, 16)), 1e30)
+    assert not out.any()
+
+
+def test_screened_mask_is_fp32_compare():
+    """Q_i*Q_j equal to fl32(1e-10) is NOT kept for threshold 1e-20: torch
+    compares in fp32 (fl32(1e-10) > 1e-10 would hold in float64)."""
+    t32 = np.float32(1e-10)
+    above = np.nextafter(t32, np.float32(1))
+    # Q values whose fp32 product lands exactly on t32 / above: Q_0 = 1, Q_1 = product.
+    for target, keep in ((t32, False), (above, True)):
+        d = np.array([1.0, np.float32(target) ** 2], dtype=np.float32)
+        Q = np.sqrt(np.abs(d)).astype(np.float32)
+        if np.float32(Q[0] * Q[1]) != target:
+            pytest.skip("sqrt round trip does not land on the target")
+        mask = ref.screened_mask(d, 1e-20)
+        assert bool(mask[0, 1]) is keep and bool(mask[1, 0]) is keep
+    # the threshold conversion: float64 1e-10 vs its float32 rounding differ
+    assert float(t32) > 1e-10
+
+
+def test_screened_mask_matches_torch_semantics():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(8)
+    d = (10.0 ** rng.uniform(-14, 0, 512)).astype(np.float32)
+    for thr in (1e-20, 1e-12, 0.5e-9, 0.3):
+        Q = torch.sqrt(torch.abs(torch.from_numpy(d)))
+        tmask = ((Q.unsqueeze(-1) * Q.unsqueeze(0)) > math.sqrt(thr)).numpy()
+        np.testing.assert_array_equal(ref.screened_mask(d, thr), tmask)
+
+
+# ------------------------------------------------------------- attention
+
+
+def _local_block_mask(nb, window):
+    i = np.arange(nb)
+    return np.abs(i[:, None] - i[None, :]) <= window
+
+
+@pytest.mark.parametrize("S,D,window", [(256, 32, 1), (384, 64, 0), (512, 16, 2)])
+def test_attention_vs_dense_masked_softmax(S, D, window):
+    rng = np.random.default_rng(9)
+    b = 128
+    Q, K, V = (rng.standard_normal((S, D)) for _ in range(3))
+    bm = _local_block_mask(S // b, window)
+    ptr = np.zeros(S // b + 1, np.int64)
+    ptr[1:] = np.cumsum(bm.sum(1))
+    col = np.nonzero(bm)[1]
+    out, rmax, rden = ref.block_sparse_attention(Q, K, V, ptr, col, b, D**-0.5)
+    dense_mask = np.kron(bm, np.ones((b, b), bool))
+    np.testing.assert_allclose(out, ref.dense_masked_attention(Q, K, V, dense_mask, D**-0.5), rtol=1e-10, atol=1e-12)
+    # row_max is the true max of the visible scaled scores
+    sc = np.where(dense_mask, (Q @ K.T) * D**-0.5, -np.inf)
+    np.testing.assert_allclose(rmax.reshape(-1), sc.max(axis=1), rtol=1e-12)
+    np.testing.assert_allclose(rden.reshape(-1), np.exp(sc - sc.max(axis=1, keepdims=True)).sum(axis=1), rtol=1e-12)
+
+
+def test_attention_full_mask_is_dense_and_empty_rows_zero():
+    rng = np.random.default_rng(10)
+    S, D, b = 256, 32, 128
+    Q, K, V = (rng.standard_normal((S, D)) for _ in range(3))
+    ptr = np.array([0, 2, 4])
+    col = np.array([0, 1, 0, 1])
+    sc = (Q @ K.T) / math.sqrt(D)
+    p = np.exp(sc - sc.max(1, keepdims=True))
+    dense = (p / p.sum(1, keepdims=True)) @ V
+    out, _, _ = ref.block_sparse_attention(Q, K, V, ptr, col, b, D**-0.5)
+    np.testing.assert_allclose(out, dense, rtol=1e-10, atol=1e-12)
+    ptr = np.array([0, 0, 1])
+    col = np.array([1])
+    out, rmax, rden = ref.block_sparse_attention(Q, K, V, ptr, col, b, D**-0.5)
+    assert not out[:128].any() and not rmax[0].any() and np.all(rden[0] == 1e-12)
+
+
+def test_error_metrics():
+    ref_ = np.array([1.0, -2.0, 0.0])
+    got = np.array([1.0, -2.0 + 1e-3, 1e-6])
+    scale = np.array([1.0, 10.0, 1.0])
+    assert ref.scaled_error(got, ref_, scale) == pytest.approx(1e-4)
+    assert ref.rel_max_error(got, ref_) == pytest.approx(5e-4)

@@ -1,0 +1,96 @@
+"""ctypes binding of libtrnsparse_hip.so (C ABI: include/trnsparse_hip.h).
+
+Every entry point takes device pointers, sizes, dtype codes and a HIP
+stream handle; a nonzero status is turned into RuntimeError carrying
+`tsp_last_error()`. Loading fails loudly when the library has not been
+built: the HIP backend never falls back to another implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import threading
+
+import torch
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent.parent / "libtrnsparse_hip.so"
+
+TSP_F32, TSP_F64, TSP_BF16 = 0, 1, 2
+TSP_I32, TSP_I64 = 0, 1
+
+_DTYPE_CODE = {torch.float32: TSP_F32, torch.float64: TSP_F64, torch.bfloat16: TSP_BF16}
+_INDEX_CODE = {torch.int32: TSP_I32, torch.int64: TSP_I64}
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_INT = ctypes.c_int
+_DBL = ctypes.c_double
+
+# name -> (restype, argtypes); mirrors include/trnsparse_hip.h
+SIGNATURES: dict[str, tuple] = {
+    "tsp_version": (_INT, []),
+    "tsp_last_error": (ctypes.c_char_p, []),
+    "tsp_bsr_spmm": (
+        _INT,
+        [_P, _INT, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _INT, _P, _P],
+    ),
+    "tsp_bsr_row_order": (_INT, [_P, _I64, _P, _P]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library; raise RuntimeError if unavailable."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH.name} is not built; run `python -m trnsparse_amd.build_lib` "
+                    "(the HIP backend has no fallback)"
+                )
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def last_error() -> str:
+    return load().tsp_last_error().decode(errors="replace")
+
+
+def call(name: str, *args) -> None:
+    """Call a status-returning entry point; raise RuntimeError on failure."""
+    st = getattr(load(), name)(*args)
+    if st != 0:
+        raise RuntimeError(f"{name} failed with status {st}: {last_error()}")
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dt]
+    except KeyError:
+        raise RuntimeError(f"HIP backend does not support dtype {dt}") from None
+
+
+def index_code(dt: torch.dtype) -> int:
+    try:
+        return _INDEX_CODE[dt]
+    except KeyError:
+        raise RuntimeError(f"HIP backend needs int32 or int64 indices, got {dt}") from None
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

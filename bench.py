@@ -174,6 +174,45 @@ def bench_bsr_bf16(steps: int, warmup: int):
     }
 
 
+def bench_spmv(dist: str, index_bits: int, steps: int, warmup: int, cpu: bool = False):
+    """CSR SpMV at config 2: algorithmic HBM bytes / kernel time, L2+MALL
+    flushed before every timed launch (the working set fits in the MALL)."""
+    import numpy as np
+    import torch
+
+    import trnsparse_amd as ts
+    from trnsparse_amd import workloads as W
+
+    idt = np.int64 if index_bits == 64 else np.int32
+    v, c, p, x, shape = W.cfg2_csr(dist=dist, index_dtype=idt)
+    m, n = shape
+    nnz = len(v)
+    A = W.csr_matrix_from_arrays(v, c, p, shape, device="cuda")
+    xd = torch.from_numpy(x).cuda()
+    ib = index_bits // 8
+    byts = nnz * (4 + ib) + (m + 1) * ib + n * 4 + m * 4
+    flush = make_flush()
+    _, ev_ms = time_gpu(lambda: ts.spmv(A, xd), steps, warmup, flush=flush)
+    gbs = byts / (ev_ms * 1e-3) / 1e9
+    res = {
+        "name": f"csr_spmv cfg2 {dist} int{index_bits}",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "us": round(ev_ms * 1e3, 2),
+        "nnz": nnz,
+        "algorithmic_bytes": byts,
+        "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+    }
+    if cpu:
+        from oracle import build as oracle_c
+        from oracle import cpu_baseline as cb
+
+        secs = cb.time_call(lambda: oracle_c.csr_spmv_f32(v, c, p, m, x), reps=5, budget_s=10.0)
+        res["cpu_baseline"] = {"value": round(byts / secs / 1e9, 2), "unit": "GB/s", "cores": cb.threads(),
+                               "kind": "port", "sample": "full cfg2 matrix, oracle/csr_spmv.c fp32 OpenMP over rows"}
+    return res
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -206,11 +245,18 @@ def main(argv=None) -> int:
     head = bench_bsr_fp32(args.steps, args.warmup, cpu=not args.no_cpu)
     secondary = []
     if not args.no_secondary:
-        for fn in (bench_bsr_bf16,):
+        jobs = [
+            ("spmv poisson int64", lambda: bench_spmv("poisson", 64, 20, 3, cpu=not args.no_cpu)),
+            ("spmv poisson int32", lambda: bench_spmv("poisson", 32, 20, 3)),
+            ("spmv zipf int64", lambda: bench_spmv("zipf", 64, 10, 2)),
+            ("bsr bf16", lambda: bench_bsr_bf16(max(5, args.steps // 2), 3)),
+        ]
+        for name, fn in jobs:
             try:
-                secondary.append(fn(max(5, args.steps // 2), 3))
+                secondary.append(fn())
             except Exception as exc:  # report, do not hide
-                secondary.append({"name": fn.__name__, "error": repr(exc)})
+                secondary.append({"name": name, "error": repr(exc)})
+            print(f"# done: {name}", file=sys.stderr, flush=True)
 
     line = {
         "metric": "bsr_spmm effective GFLOP/s (nnz blocks) + % MFMA peak; CSR SpMV HBM GB/s",

@@ -80,6 +80,61 @@ int tsp_bsr_spmm(const void* blocks, int dtype,
 int tsp_bsr_row_order(const int64_t* block_row_ptrs, int64_t n_block_rows,
                       int32_t* order, void* stream);
 
+/* ======================================================================
+ * CSR sparse x dense (bandwidth-bound; no MFMA)
+ *
+ * Replaces the reference's spmv (trnsparse/ops.py:30-48, torch
+ * sparse_csr @ x) and spmm (ops.py:51-78; NKI nki_spmm,
+ * trnsparse/nki/dispatch.py:181-190, which densified A):
+ *   out = alpha * (A @ x)  [+ beta * y  when y != NULL and beta != 0]
+ * values (nnz,) `dtype` (TSP_F32 or TSP_F64, accumulated in that type),
+ * col_indices (nnz,) and row_ptrs (m+1,) both `index_type`.
+ * ==================================================================== */
+
+/* Number of int64 entries of the SpMV work-partition table for an m-row
+ * matrix with nnz stored entries (<0 on bad sizes). */
+int64_t tsp_csr_plan_size(int64_t m, int64_t nnz);
+
+/* Build the SpMV work-partition table (`windows`, tsp_csr_plan_size
+ * entries) from row_ptrs on the device. Depends only on the pattern. */
+int tsp_csr_plan(const void* row_ptrs, int index_type, int64_t m, int64_t nnz,
+                 int64_t* windows, void* stream);
+
+/* out (m,) = alpha * A @ x (+ beta * y); x (n,), y (m,) or NULL. */
+int tsp_csr_spmv(const void* values, int dtype, const void* col_indices,
+                 const void* row_ptrs, int index_type, int64_t m, int64_t n,
+                 int64_t nnz, const int64_t* windows, const void* x,
+                 double alpha, const void* y, double beta, void* out,
+                 void* stream);
+
+/* out (m, ncols; row stride ldo) = alpha * A @ B (+ beta * C);
+ * B (n, ncols; stride ldb), C (m, ncols; stride ldc) or NULL. */
+int tsp_csr_spmm(const void* values, int dtype, const void* col_indices,
+                 const void* row_ptrs, int index_type, int64_t m, int64_t n,
+                 int64_t nnz, const void* B, int64_t ldb, int64_t ncols,
+                 double alpha, const void* C, int64_t ldc, double beta,
+                 void* out, int64_t ldo, void* stream);
+
+/* ======================================================================
+ * Schwarz-screened dense SpMM:  C = (A * mask) @ B
+ *   Q = sqrt(|diag|), mask[i,k] = Q[i]*Q[k] > threshold_sqrt, evaluated in
+ *   diag's precision (diag_dtype TSP_F32 or TSP_F64; threshold_sqrt is
+ *   rounded to that precision), A (m, m; stride lda) and B (m, ncols;
+ *   stride ldb) `dtype` (TSP_F32 on the MFMA path, TSP_F64 generic),
+ *   C (m, ncols; stride ldc) written in full.
+ * Replaces nki_screened_spmm / _ScreenedSpMMFunction forward
+ * (trnsparse/nki/dispatch.py:384-494) and the torch spec
+ * (trnsparse/ops.py:262-277). `workspace` holds
+ * tsp_screened_workspace_size(m, diag_dtype) bytes (Q and per-tile maxima),
+ * 16-byte aligned.
+ * ==================================================================== */
+int64_t tsp_screened_workspace_size(int64_t m, int diag_dtype);
+
+int tsp_screened_spmm(const void* A, int dtype, int64_t lda, const void* diag,
+                      int diag_dtype, double threshold_sqrt, int64_t m,
+                      const void* B, int64_t ldb, int64_t ncols, void* C,
+                      int64_t ldc, void* workspace, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,144 @@
+"""GPU parity of screened_spmm (fused mask + fp32 MFMA GEMM) against the oracle.
+
+The mask is checked bit-exactly (A = ones, B = identity makes C the mask
+itself), including Q_i*Q_j landing exactly on fl32(sqrt(threshold)); values
+are checked against the float64 oracle with the dot-product error scale
+(fp32 tolerance 1e-4), plus the reference's own cases
+(tests/test_screening.py:76-133 and tests/test_nki_screened_spmm.py:33-55).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import trnsparse_amd as ts
+from oracle import ref
+from trnsparse_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def _check(A, diag, B, thr, got, rows=None):
+    An, dn, Bn = A.cpu().numpy(), diag.cpu().numpy(), B.cpu().numpy()
+    mask = ref.screened_mask(dn, thr)
+    if rows is not None:
+        mask, An, got = mask[rows], An[rows], got[rows]
+    Am = np.where(mask, An.astype(np.float64), 0.0)
+    exact = Am @ Bn.astype(np.float64)
+    scale = np.abs(Am) @ np.abs(Bn.astype(np.float64))
+    err = ref.scaled_error(got.cpu().numpy() if isinstance(got, torch.Tensor) else got, exact, scale)
+    assert err <= TOL, err
+
+
+def test_threshold_zero_equals_matmul(hip_backend):
+    torch.manual_seed(0)
+    n = 64
+    A = torch.randn(n, n)
+    diag = torch.abs(torch.randn(n)) + 0.1
+    B = torch.randn(n, 16)
+    got = ts.screened_spmm(A, diag, B.cuda(), threshold=0.0).cpu()
+    torch.testing.assert_close(got, A @ B, atol=1e-5, rtol=1e-5)
+
+
+def test_huge_threshold_exact_zeros(hip_backend):
+    torch.manual_seed(1)
+    n = 64
+    got = ts.screened_spmm(torch.randn(n, n), torch.abs(torch.randn(n)), torch.randn(n, 16).cuda(), threshold=1e30)
+    torch.testing.assert_close(got.cpu(), torch.zeros(n, 16), atol=0, rtol=0)
+
+
+def test_parity_vs_explicit_mask(hip_backend):
+    torch.manual_seed(2)
+    n = 64
+    A = torch.randn(n, n)
+    diag = torch.abs(torch.randn(n)) * 4.0
+    B = torch.randn(n, 16)
+    got = ts.screened_spmm(A, diag, B.cuda(), threshold=0.5).cpu()
+    Q = torch.sqrt(torch.abs(diag))
+    mask = (Q.unsqueeze(-1) * Q.unsqueeze(0)) > math.sqrt(0.5)
+    torch.testing.assert_close(got, (A * mask.to(A.dtype)) @ B, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("n,N,threshold", [(128, 128, 0.0), (128, 128, 0.5), (256, 128, 0.5), (256, 256, 0.1),
+                                           (200, 64, 0.3), (300, 130, 0.2)])
+def test_reference_hardware_grid(hip_backend, n, N, threshold):
+    torch.manual_seed(42)
+    A = torch.randn(n, n)
+    diag = torch.abs(torch.randn(n)) * 4.0 + 0.01
+    B = torch.randn(n, N)
+    got = ts.screened_spmm(A, diag, B.cuda(), threshold=threshold).cpu()
+    Q = torch.sqrt(torch.abs(diag))
+    mask = (Q.unsqueeze(-1) * Q.unsqueeze(0)) > math.sqrt(max(threshold, 0.0))
+    torch.testing.assert_close(got, (A * mask.to(A.dtype)) @ B, atol=1e-3, rtol=1e-4)
+    _check(A, diag, B, threshold, got)
+
+
+@pytest.mark.parametrize("diag_dtype", [torch.float32, torch.float64])
+def test_mask_bit_exact_at_threshold(hip_backend, diag_dtype):
+    """C = (ones * mask) @ I = mask; Q values put some products exactly on
+    the rounded threshold (not kept: strict >) and one ulp above (kept)."""
+    n = 384
+    rng = np.random.default_rng(5)
+    npdt = np.float32 if diag_dtype == torch.float32 else np.float64
+    t = npdt(math.sqrt(1e-20))  # threshold rounded to diag's precision
+    Q = (10.0 ** rng.uniform(-12, 0, n)).astype(npdt)
+    Q[0] = npdt(1.0)
+    Q[1] = t  # Q0*Q1 == t exactly
+    Q[2] = np.nextafter(t, npdt(1))  # one ulp above
+    Q[3] = np.nextafter(t, npdt(0))
+    diag = torch.from_numpy((Q.astype(np.float64) ** 2).astype(npdt))
+    Qr = np.sqrt(np.abs(diag.numpy())).astype(npdt)
+    A = torch.ones(n, n)
+    Bm = torch.eye(n)
+    got = ts.screened_spmm(A, diag, Bm.cuda(), threshold=1e-20).cpu().numpy()
+    expect = ref.screened_mask(diag.numpy(), 1e-20).astype(np.float32)
+    assert np.array_equal(got, expect)
+    if Qr[0] * Qr[1] == t:  # the square/sqrt round trip kept the value
+        assert got[0, 1] == 0.0
+
+
+def test_tile_skip_structured(hip_backend):
+    """Rows/cols 128..255 have tiny Q: every tile pair touching them is fully
+    masked and skipped; the result still equals the oracle."""
+    n = 512
+    g = torch.Generator().manual_seed(6)
+    diag = torch.rand(n, generator=g) + 0.5
+    diag[128:256] = 1e-30
+    A = torch.randn(n, n, generator=g)
+    B = torch.randn(n, 96, generator=g)
+    got = ts.screened_spmm(A, diag, B.cuda(), threshold=1e-12).cpu()
+    assert torch.count_nonzero(got[128:256]).item() == 0
+    _check(A, diag, B, 1e-12, got)
+
+
+def test_f64_generic_and_gradcheck(hip_backend):
+    torch.manual_seed(7)
+    n = 40
+    A = torch.randn(n, n, dtype=torch.float64, device="cuda", requires_grad=True)
+    diag = (torch.abs(torch.randn(n, dtype=torch.float64)) * 4.0 + 0.01).cuda()
+    B = torch.randn(n, 5, dtype=torch.float64, device="cuda", requires_grad=True)
+    got = ts.screened_spmm(A, diag, B, threshold=0.5)
+    Q = torch.sqrt(torch.abs(diag))
+    mask = ((Q.unsqueeze(-1) * Q.unsqueeze(0)) > math.sqrt(0.5)).double()
+    torch.testing.assert_close(got, (A * mask) @ B, rtol=1e-12, atol=1e-12)
+    assert torch.autograd.gradcheck(lambda a, b: ts.screened_spmm(a, diag, b, threshold=0.5), (A, B), eps=1e-6, atol=1e-6)
+
+
+def test_cfg4_full_size(hip_backend):
+    A, diag, B, thr = W.cfg4_screened()
+    got = ts.screened_spmm(A.cuda(), diag.cuda(), B.cuda(), threshold=thr).cpu()
+    rows = np.r_[0:128, 1000:1040, 2048:2176, 3968:4096]
+    _check(A, diag, B, thr, got, rows=rows)
+    # linearity at full size: C @ 1 = (A*mask) @ (B @ 1)
+    ones = torch.ones(B.shape[1], 1, dtype=torch.float64)
+    lhs = got.double() @ ones
+    rhs = ts.screened_spmm(A.cuda(), diag.cuda(), (B.double() @ ones).float().cuda(), threshold=thr).cpu().double()
+    mask = torch.from_numpy(ref.screened_mask(diag.numpy(), thr))
+    sc = (A.abs().double() * mask) @ (B.abs().double() @ ones)
+    assert ((lhs - rhs).abs() / sc).max().item() <= TOL

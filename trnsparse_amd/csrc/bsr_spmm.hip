@@ -28,35 +28,33 @@
 // as a longest-processing-time list scheduler within each XCD.
 #include "common.h"
 
+#include "mfma_f32.h"
+
 namespace {
 
-constexpr int BS = 128;          // block size served by the MFMA kernel
-constexpr int TN = 128;          // C columns per workgroup
-constexpr int KC = 32;           // k-slab per pipeline step
-constexpr int NTHR = 512;        // 8 wavefronts
-constexpr int A_LD = KC + 4;     // LDS row stride (floats) of the A slab [m][k]
-constexpr int B_LD = TN + 4;     // LDS row stride (floats) of the B slab [k][n]
-constexpr int A_SLAB = BS * A_LD;
-constexpr int B_SLAB = KC * B_LD;
-constexpr int STAGE = A_SLAB + B_SLAB;
+namespace T32 = tsp::f32tile;
+constexpr int BS = 128;  // block size served by the MFMA kernel
 
-// Load four consecutive B elements of row r starting at column c, zero-filled
-// outside [0,n) x [0,ncols). Vector path needs c%4==0, ldb%4==0, 16B base.
-__device__ inline f32x4 load_b4(const float* __restrict__ B, int64_t r, int64_t c, int64_t n,
-                                int64_t ncols, int64_t ldb) {
-  f32x4 v = {0.f, 0.f, 0.f, 0.f};
-  if (r < n) {
-    const float* p = B + r * ldb + c;
-    if (c + 3 < ncols) {
-      v = *(const f32x4*)p;
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (c + i < ncols) v[i] = p[i];
-    }
+// Slab source of one (block row, column tile) item: slab s is k-slab s%4 of
+// the (s/4)-th stored block of the row; B rows come straight from the
+// row-panel of that block's column (no gathered copy of B).
+struct BsrSlabs {
+  const float* __restrict__ blocks;
+  const int64_t* __restrict__ ci;
+  const float* __restrict__ B;
+  int64_t start, n, ncols, ldb, n0;
+  T32::Coords q;
+  __device__ void load(int s, f32x4& a0, f32x4& a1, f32x4& b0, f32x4& b1) const {
+    const int64_t idx = start + (s >> 2);
+    const int kk = (s & 3) * T32::KC;
+    const float* a = blocks + idx * (BS * BS) + kk;
+    a0 = *(const f32x4*)(a + q.ar * BS + q.ac);
+    a1 = *(const f32x4*)(a + (q.ar + 64) * BS + q.ac);
+    const int64_t brow = ci[idx] * BS + kk + q.br;
+    b0 = T32::load4_guard(B, brow, n0 + q.bc, n, ncols, ldb);
+    b1 = T32::load4_guard(B, brow + 16, n0 + q.bc, n, ncols, ldb);
   }
-  return v;
-}
+};
 
 template <typename OutT>
 __device__ inline OutT cvt_out(float v);
@@ -66,11 +64,11 @@ template <>
 __device__ inline uint16_t cvt_out<uint16_t>(float v) { return tsp::f32_to_bf16_bits(v); }
 
 template <typename OutT>
-__global__ __launch_bounds__(NTHR) void bsr_spmm_f32_mfma(
+__global__ __launch_bounds__(T32::NTHR) void bsr_spmm_f32_mfma(
     const float* __restrict__ blocks, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci,
     int64_t mb, int nt, int64_t m, int64_t n, const float* __restrict__ B, int64_t ldb,
     int64_t ncols, OutT* __restrict__ C, int64_t ldc, const int32_t* __restrict__ order) {
-  __shared__ __attribute__((aligned(16))) float lds[2 * STAGE];
+  __shared__ __attribute__((aligned(16))) float lds[T32::LDS_FLOATS];
 
   // ---- work item (XCD-aware, heaviest rows first)
   const int g = blockIdx.x;
@@ -79,89 +77,21 @@ __global__ __launch_bounds__(NTHR) void bsr_spmm_f32_mfma(
   if (k >= mb) return;
   const int ntile = slot % nt;
   const int64_t row = order ? (int64_t)order[k] : k;
-  const int64_t n0 = (int64_t)ntile * TN;
-  const int64_t start = rp[row];
-  const int nsteps = (int)(rp[row + 1] - start) * (BS / KC);
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
-  const int wm = w & 3, wn = w >> 2;
-  const int h = lane >> 5, l32 = lane & 31;
-
-  // ---- staging coordinates: A slab 128x32, B slab 32x128, 2 float4 each
-  const int ar = tid >> 3, ac = (tid & 7) * 4;
-  const int br = tid >> 5, bc = (tid & 31) * 4;
-
-  f32x4 ra0, ra1, rb0, rb1;
-  auto gload = [&](int s) {
-    const int64_t idx = start + (s >> 2);
-    const int kk = (s & 3) * KC;
-    const float* a = blocks + idx * (BS * BS) + kk;
-    ra0 = *(const f32x4*)(a + ar * BS + ac);
-    ra1 = *(const f32x4*)(a + (ar + 64) * BS + ac);
-    const int64_t brow = ci[idx] * BS + kk + br;
-    rb0 = load_b4(B, brow, n0 + bc, n, ncols, ldb);
-    rb1 = load_b4(B, brow + 16, n0 + bc, n, ncols, ldb);
-  };
-  auto lstore = [&](float* st) {
-    float* As = st;
-    float* Bs = st + A_SLAB;
-    *(f32x4*)(As + ar * A_LD + ac) = ra0;
-    *(f32x4*)(As + (ar + 64) * A_LD + ac) = ra1;
-    *(f32x4*)(Bs + br * B_LD + bc) = rb0;
-    *(f32x4*)(Bs + (br + 16) * B_LD + bc) = rb1;
-  };
+  BsrSlabs src;
+  src.blocks = blocks;
+  src.ci = ci;
+  src.B = B;
+  src.start = rp[row];
+  src.n = n;
+  src.ncols = ncols;
+  src.ldb = ldb;
+  src.n0 = (int64_t)ntile * T32::BN;
+  const int nsteps = (int)(rp[row + 1] - src.start) * (BS / T32::KC);
 
   f32x16 acc0 = {}, acc1 = {};
-  // MFMA k-step s of a group of 8 k values uses k = k0 + s (lanes 0-31) and
-  // k = k0 + 4 + s (lanes 32-63): each lane reads its 4 A values as one
-  // 16-byte LDS load. A and B use the same k permutation, so the sum is the
-  // plain dot product over the 8 values.
-  auto compute = [&](const float* st) {
-    const float* As = st;
-    const float* Bs = st + A_SLAB;
-#pragma unroll
-    for (int k0 = 0; k0 < KC; k0 += 8) {
-      const f32x4 a = *(const f32x4*)(As + (wm * 32 + l32) * A_LD + k0 + 4 * h);
-      const float* bp = Bs + (k0 + 4 * h) * B_LD + wn * 64 + l32;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const float b0 = bp[s * B_LD];
-        const float b1 = bp[s * B_LD + 32];
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b0, acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b1, acc1, 0, 0, 0);
-      }
-    }
-  };
-
-  if (nsteps > 0) {
-    gload(0);
-    lstore(lds);
-    __syncthreads();
-    for (int s = 0; s < nsteps; ++s) {
-      const float* cur = lds + (s & 1) * STAGE;
-      float* nxt = lds + ((s + 1) & 1) * STAGE;
-      const bool more = s + 1 < nsteps;
-      if (more) gload(s + 1);
-      compute(cur);
-      if (more) lstore(nxt);
-      __syncthreads();
-    }
-  }
-
-  // ---- epilogue: 32x32 accumulator layout, lane holds column l32 and rows
-  // 8*(v/4) + 4*h + v%4 for v = 0..15.
-  const int64_t rbase = row * BS + wm * 32 + 4 * h;
-  const int64_t c0 = n0 + wn * 64 + l32;
-#pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const int64_t r = rbase + 8 * (v >> 2) + (v & 3);
-    if (r < m) {
-      OutT* crow = C + r * ldc;
-      if (c0 < ncols) crow[c0] = cvt_out<OutT>(acc0[v]);
-      if (c0 + 32 < ncols) crow[c0 + 32] = cvt_out<OutT>(acc1[v]);
-    }
-  }
+  T32::run(src, nsteps, lds, src.q, acc0, acc1);
+  T32::store_tile(C, ldc, row * BS, src.n0, m, ncols, src.q, acc0, acc1, cvt_out<OutT>);
 }
 
 template <typename T, typename OutT>
@@ -262,10 +192,10 @@ extern "C" int tsp_bsr_spmm(const void* blocks, int dtype, const int64_t* block_
 
   if (dtype == TSP_F32 && block_size == BS && (ldb % 4) == 0 && ((uintptr_t)B % 16) == 0 &&
       ((uintptr_t)blocks % 16) == 0) {
-    const int64_t nt = tsp::ceil_div(ncols, TN);
+    const int64_t nt = tsp::ceil_div(ncols, T32::BN);
     const int64_t grid = tsp::ceil_div(mb, 8) * 8 * nt;
     if (grid > INT32_MAX || nt > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm: problem too large");
-    hipLaunchKernelGGL((bsr_spmm_f32_mfma<float>), dim3((unsigned)grid), dim3(NTHR), 0, st, (const float*)blocks,
+    hipLaunchKernelGGL((bsr_spmm_f32_mfma<float>), dim3((unsigned)grid), dim3(T32::NTHR), 0, st, (const float*)blocks,
                        block_row_ptrs, block_col_indices, mb, (int)nt, m, n, (const float*)B, ldb, ncols,
                        (float*)C, ldc, row_order);
     return tsp::check_launch("bsr_spmm_f32_mfma launch");

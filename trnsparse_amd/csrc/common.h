@@ -68,6 +68,6 @@ template <typename T> __device__ inline T group_sum(T v, int G) {
   return v;
 }
 
-inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace tsp

@@ -1,0 +1,303 @@
+// CSR SpMV and SpMM for gfx950 (bandwidth-bound; no MFMA).
+//
+// Semantics follow the reference (trnsparse/ops.py:30-48 spmv, :51-78 spmm):
+//   out = alpha * (A @ x)            then  + beta * y   only if y and beta != 0
+// alpha multiplies the finished row sum; y is read, never written.
+//
+// SpMV: work partition ("windows")
+//   A row r sits at position pos(r) = (row_ptrs[r] - row_ptrs[0]) + r on the
+//   merged rows+nonzeros axis, which is strictly increasing. Window k holds
+//   the rows with pos(r) in [k*CAP, (k+1)*CAP): at most CAP rows, and all but
+//   its last row end inside the window (fewer than CAP nonzeros before the
+//   last row starts). The table windows[k] = first row of window k is built
+//   in one pass on the device (each row writes the windows that begin at it)
+//   and depends only on the pattern, so callers cache it with the matrix.
+//
+// SpMV kernel: one 256-thread workgroup per window.
+//   1. stream the window's values and column indices with coalesced,
+//      non-temporal loads (8 per thread in flight), gather x (kept in L2 by
+//      the streaming hint), and stage the products plus the row offsets in
+//      LDS;
+//   2. reduce rows with G lanes per row (G = power of two filling the
+//      workgroup, up to a wavefront), xor-shuffle reduction inside the group;
+//   3. a last row longer than the LDS capacity is reduced by the whole
+//      workgroup (skewed / Zipf rows), wavefront shuffles + LDS across waves.
+//
+// SpMM: one wavefront per row, lanes across the columns of B (coalesced B
+// row reads), the row's (col, value) pairs loaded 64 at a time and broadcast
+// with shuffles.
+#include "common.h"
+
+namespace {
+
+constexpr int SPMV_THREADS = 256;
+constexpr int CAP = 2048;       // rows + nonzeros per window
+constexpr int LDS_CAP = 4096;   // staged products per window
+constexpr int UNROLL = 8;
+
+template <typename IdxT>
+__global__ __launch_bounds__(256) void csr_plan_kernel(const IdxT* __restrict__ ptr, int64_t m, int64_t nwin,
+                                                       int64_t* __restrict__ win) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r > m) return;
+  const int64_t base = (int64_t)ptr[0];
+  const int64_t pos = (int64_t)ptr[r] - base + r;
+  const int64_t prev = r == 0 ? -1 : (int64_t)ptr[r - 1] - base + (r - 1);
+  // windows k with prev < k*CAP <= pos start at row r
+  int64_t k = prev < 0 ? 0 : prev / CAP + 1;
+  const int64_t kend = pos / CAP;
+  for (; k <= kend && k < nwin; ++k) win[k] = r;
+  if (r == m) win[nwin] = m;
+}
+
+template <typename T> struct SpmvAcc { typedef float type; };
+template <> struct SpmvAcc<double> { typedef double type; };
+
+template <typename IdxT, typename T>
+__global__ __launch_bounds__(SPMV_THREADS) void csr_spmv_kernel(
+    const T* __restrict__ vals, const IdxT* __restrict__ cols, const IdxT* __restrict__ ptr,
+    const int64_t* __restrict__ win, const T* __restrict__ x, T alpha, const T* __restrict__ y, T beta,
+    T* __restrict__ out) {
+  typedef typename SpmvAcc<T>::type AccT;
+  __shared__ AccT prod[LDS_CAP];
+  __shared__ int offs[CAP + 1];
+  __shared__ AccT wsum[SPMV_THREADS / 64];
+
+  const int tid = threadIdx.x;
+  const int64_t r0 = win[blockIdx.x], r1 = win[blockIdx.x + 1];
+  if (r0 >= r1) return;
+  const int64_t p0 = (int64_t)ptr[r0];
+  const int64_t pend = (int64_t)ptr[r1];
+  const bool long_tail = pend - p0 > LDS_CAP;
+  const int64_t rs = long_tail ? r1 - 1 : r1;  // rows [r0, rs) go through LDS
+  const int nr = (int)(rs - r0);
+  const int n = (int)((int64_t)ptr[rs] - p0);  // < LDS_CAP by construction
+
+  // row offsets (relative to p0) for the staged rows
+  for (int i = tid; i <= nr; i += SPMV_THREADS) offs[i] = (int)((int64_t)ptr[r0 + i] - p0);
+
+  // products of the staged nonzeros
+  for (int base = 0; base < n; base += SPMV_THREADS * UNROLL) {
+    IdxT c[UNROLL];
+    T v[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int i = base + u * SPMV_THREADS + tid;
+      if (i < n) {
+        c[u] = tsp::ld_stream(cols + p0 + i);
+        v[u] = tsp::ld_stream(vals + p0 + i);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int i = base + u * SPMV_THREADS + tid;
+      if (i < n) prod[i] = (AccT)v[u] * (AccT)x[c[u]];
+    }
+  }
+  __syncthreads();
+
+  if (nr > 0) {
+    int G = 64;
+    while (G > 1 && G * nr > SPMV_THREADS) G >>= 1;
+    const int q = tid & (G - 1);
+    const int rows_per_pass = SPMV_THREADS / G;
+    const int npass = (nr + rows_per_pass - 1) / rows_per_pass;
+    // every lane runs every pass: the group reduction shuffles need the full wavefront
+    for (int pass = 0; pass < npass; ++pass) {
+      const int rr = pass * rows_per_pass + tid / G;
+      AccT s = 0;
+      if (rr < nr) {
+        const int a = offs[rr], e = offs[rr + 1];
+        for (int j = a + q; j < e; j += G) s += prod[j];
+      }
+      s = tsp::group_sum(s, G);
+      if (rr < nr && q == 0) {
+        const int64_t r = r0 + rr;
+        T res = alpha * (T)s;
+        if (y) res = res + beta * y[r];
+        out[r] = res;
+      }
+    }
+  }
+
+  if (long_tail) {
+    // whole-workgroup reduction of the last row
+    const int64_t r = r1 - 1;
+    const int64_t a = (int64_t)ptr[r], e = (int64_t)ptr[r + 1];
+    AccT s = 0;
+    for (int64_t j0 = a; j0 < e; j0 += SPMV_THREADS * UNROLL) {
+      IdxT c[UNROLL];
+      T v[UNROLL];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        const int64_t j = j0 + u * SPMV_THREADS + tid;
+        if (j < e) {
+          c[u] = tsp::ld_stream(cols + j);
+          v[u] = tsp::ld_stream(vals + j);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        const int64_t j = j0 + u * SPMV_THREADS + tid;
+        if (j < e) s += (AccT)v[u] * (AccT)x[c[u]];
+      }
+    }
+    s = tsp::wave_sum(s);
+    if ((tid & 63) == 0) wsum[tid >> 6] = s;
+    __syncthreads();
+    if (tid == 0) {
+      AccT t = 0;
+      for (int w = 0; w < SPMV_THREADS / 64; ++w) t += wsum[w];
+      T res = alpha * (T)t;
+      if (y) res = res + beta * y[r];
+      out[r] = res;
+    }
+  }
+}
+
+// SpMM: wavefront per row, NC column chunks of 64 per pass.
+template <typename IdxT, typename T, int NC>
+__global__ __launch_bounds__(256) void csr_spmm_kernel(
+    const T* __restrict__ vals, const IdxT* __restrict__ cols, const IdxT* __restrict__ ptr, int64_t m,
+    const T* __restrict__ B, int64_t ldb, int64_t ncols, T alpha, const T* __restrict__ Cin, int64_t ldci, T beta,
+    T* __restrict__ out, int64_t ldo) {
+  typedef typename SpmvAcc<T>::type AccT;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x / 64);
+  for (int64_t r = wave; r < m; r += nwaves) {
+    const int64_t a = (int64_t)ptr[r], e = (int64_t)ptr[r + 1];
+    for (int64_t c0 = 0; c0 < ncols; c0 += 64 * NC) {
+      AccT acc[NC];
+#pragma unroll
+      for (int u = 0; u < NC; ++u) acc[u] = 0;
+      for (int64_t e0 = a; e0 < e; e0 += 64) {
+        const int64_t my = e0 + lane;
+        int64_t cl = 0;
+        T vl = 0;
+        if (my < e) {
+          cl = (int64_t)cols[my];
+          vl = vals[my];
+        }
+        const int cnt = (int)((e - e0) < 64 ? (e - e0) : 64);
+#pragma unroll 4
+        for (int j = 0; j < cnt; ++j) {
+          const int64_t cj = __shfl(cl, j, 64);
+          const AccT vj = (AccT)__shfl(vl, j, 64);
+          const T* brow = B + cj * ldb + c0 + lane;
+#pragma unroll
+          for (int u = 0; u < NC; ++u)
+            if (c0 + 64 * u + lane < ncols) acc[u] += vj * (AccT)brow[64 * u];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < NC; ++u) {
+        const int64_t c = c0 + 64 * u + lane;
+        if (c < ncols) {
+          T res = alpha * (T)acc[u];
+          if (Cin) res = res + beta * Cin[r * ldci + c];
+          out[r * ldo + c] = res;
+        }
+      }
+    }
+  }
+}
+
+template <typename IdxT>
+int plan_launch(const void* row_ptrs, int64_t m, int64_t nwin, int64_t* win, hipStream_t st) {
+  const int64_t grid = tsp::ceil_div(m + 1, 256);
+  if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_plan: too many rows");
+  hipLaunchKernelGGL((csr_plan_kernel<IdxT>), dim3((unsigned)grid), dim3(256), 0, st, (const IdxT*)row_ptrs, m, nwin, win);
+  return tsp::check_launch("csr_plan launch");
+}
+
+template <typename IdxT, typename T>
+int spmv_launch(const void* values, const void* col, const void* rp, const int64_t* win, int64_t nwin, const void* x,
+                double alpha, const void* y, double beta, void* out, hipStream_t st) {
+  if (nwin > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_spmv: too many windows");
+  const T* yy = (y && beta != 0.0) ? (const T*)y : nullptr;
+  hipLaunchKernelGGL((csr_spmv_kernel<IdxT, T>), dim3((unsigned)nwin), dim3(SPMV_THREADS), 0, st, (const T*)values,
+                     (const IdxT*)col, (const IdxT*)rp, win, (const T*)x, (T)alpha, yy, (T)beta, (T*)out);
+  return tsp::check_launch("csr_spmv launch");
+}
+
+template <typename IdxT, typename T>
+int spmm_launch(const void* values, const void* col, const void* rp, int64_t m, const void* B, int64_t ldb,
+                int64_t ncols, double alpha, const void* C, int64_t ldc, double beta, void* out, int64_t ldo,
+                hipStream_t st) {
+  const T* cc = (C && beta != 0.0) ? (const T*)C : nullptr;
+  int64_t grid = tsp::ceil_div(m, 4);
+  if (grid > 65536) grid = 65536;
+#define TSP_SPMM(NC)                                                                                          \
+  hipLaunchKernelGGL((csr_spmm_kernel<IdxT, T, NC>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)values, \
+                     (const IdxT*)col, (const IdxT*)rp, m, (const T*)B, ldb, ncols, (T)alpha, cc, ldc, (T)beta,   \
+                     (T*)out, ldo)
+  if (ncols <= 64)
+    TSP_SPMM(1);
+  else if (ncols <= 128)
+    TSP_SPMM(2);
+  else
+    TSP_SPMM(4);
+#undef TSP_SPMM
+  return tsp::check_launch("csr_spmm launch");
+}
+
+int check_types(const char* who, int dtype, int index_type) {
+  if (dtype != TSP_F32 && dtype != TSP_F64) return tsp::fail(TSP_EUNSUPPORTED, "%s: dtype %d not supported (f32, f64)", who, dtype);
+  if (index_type != TSP_I32 && index_type != TSP_I64) return tsp::fail(TSP_EINVAL, "%s: bad index_type %d", who, index_type);
+  return TSP_OK;
+}
+
+}  // namespace
+
+extern "C" int64_t tsp_csr_plan_size(int64_t m, int64_t nnz) {
+  if (m < 0 || nnz < 0) return -1;
+  return (m + nnz) / CAP + 2;  // nwin + 1 entries
+}
+
+extern "C" int tsp_csr_plan(const void* row_ptrs, int index_type, int64_t m, int64_t nnz, int64_t* windows, void* stream) {
+  if (m < 0 || nnz < 0) return tsp::fail(TSP_EINVAL, "tsp_csr_plan: negative size");
+  if (index_type != TSP_I32 && index_type != TSP_I64) return tsp::fail(TSP_EINVAL, "tsp_csr_plan: bad index_type");
+  if (!row_ptrs || !windows) return tsp::fail(TSP_EINVAL, "tsp_csr_plan: null pointer");
+  const int64_t nwin = (m + nnz) / CAP + 1;
+  hipStream_t st = (hipStream_t)stream;
+  return index_type == TSP_I64 ? plan_launch<int64_t>(row_ptrs, m, nwin, windows, st)
+                               : plan_launch<int32_t>(row_ptrs, m, nwin, windows, st);
+}
+
+extern "C" int tsp_csr_spmv(const void* values, int dtype, const void* col_indices, const void* row_ptrs, int index_type,
+                            int64_t m, int64_t n, int64_t nnz, const int64_t* windows, const void* x, double alpha,
+                            const void* y, double beta, void* out, void* stream) {
+  int st0 = check_types("tsp_csr_spmv", dtype, index_type);
+  if (st0) return st0;
+  if (m < 0 || n < 0 || nnz < 0) return tsp::fail(TSP_EINVAL, "tsp_csr_spmv: negative size");
+  if (m == 0) return TSP_OK;
+  if (!row_ptrs || !windows || !out || (nnz > 0 && (!values || !col_indices || !x)))
+    return tsp::fail(TSP_EINVAL, "tsp_csr_spmv: null pointer");
+  const int64_t nwin = (m + nnz) / CAP + 1;
+  hipStream_t st = (hipStream_t)stream;
+  if (index_type == TSP_I64)
+    return dtype == TSP_F32 ? spmv_launch<int64_t, float>(values, col_indices, row_ptrs, windows, nwin, x, alpha, y, beta, out, st)
+                            : spmv_launch<int64_t, double>(values, col_indices, row_ptrs, windows, nwin, x, alpha, y, beta, out, st);
+  return dtype == TSP_F32 ? spmv_launch<int32_t, float>(values, col_indices, row_ptrs, windows, nwin, x, alpha, y, beta, out, st)
+                          : spmv_launch<int32_t, double>(values, col_indices, row_ptrs, windows, nwin, x, alpha, y, beta, out, st);
+}
+
+extern "C" int tsp_csr_spmm(const void* values, int dtype, const void* col_indices, const void* row_ptrs, int index_type,
+                            int64_t m, int64_t n, int64_t nnz, const void* B, int64_t ldb, int64_t ncols, double alpha,
+                            const void* C, int64_t ldc, double beta, void* out, int64_t ldo, void* stream) {
+  int st0 = check_types("tsp_csr_spmm", dtype, index_type);
+  if (st0) return st0;
+  if (m < 0 || n < 0 || nnz < 0 || ncols < 0) return tsp::fail(TSP_EINVAL, "tsp_csr_spmm: negative size");
+  if (ldb < ncols || ldo < ncols || (C && beta != 0.0 && ldc < ncols))
+    return tsp::fail(TSP_EINVAL, "tsp_csr_spmm: leading dimension < ncols");
+  if (m == 0 || ncols == 0) return TSP_OK;
+  if (!row_ptrs || !out || (nnz > 0 && (!values || !col_indices || !B)))
+    return tsp::fail(TSP_EINVAL, "tsp_csr_spmm: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  if (index_type == TSP_I64)
+    return dtype == TSP_F32 ? spmm_launch<int64_t, float>(values, col_indices, row_ptrs, m, B, ldb, ncols, alpha, C, ldc, beta, out, ldo, st)
+                            : spmm_launch<int64_t, double>(values, col_indices, row_ptrs, m, B, ldb, ncols, alpha, C, ldc, beta, out, ldo, st);
+  return dtype == TSP_F32 ? spmm_launch<int32_t, float>(values, col_indices, row_ptrs, m, B, ldb, ncols, alpha, C, ldc, beta, out, ldo, st)
+                          : spmm_launch<int32_t, double>(values, col_indices, row_ptrs, m, B, ldb, ncols, alpha, C, ldc, beta, out, ldo, st);
+}

@@ -170,3 +170,189 @@ def hip_bsr_spmm(A, B: torch.Tensor, out_dtype: torch.dtype | None = None) -> to
     return _BSRSpMMFunction.apply(
         A.blocks, A.block_col_indices, A.block_row_ptrs, A.shape, A.block_size, B, out_dtype, plan
     )
+
+
+# --------------------------------------------------------------------- CSR
+
+
+def _key(*ts):
+    return tuple((t.data_ptr(), t._version, t.numel(), t.dtype) for t in ts)
+
+
+def _csr_device(A, dev: torch.device):
+    """Device copies of (values, col_indices, row_ptrs) plus the SpMV window
+    table, cached on the CSRMatrix keyed by its tensors."""
+    key = (str(dev),) + _key(A.values, A.col_indices, A.row_ptrs)
+    cached = getattr(A, "_hip_csr", None)
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    m, n = A.shape
+    if A.row_ptrs.numel() != m + 1:
+        raise AssertionError(f"row_ptrs has {A.row_ptrs.numel()} entries, expected {m + 1}")
+    itype = A.col_indices.dtype if A.col_indices.dtype == A.row_ptrs.dtype else torch.int64
+    if itype not in (torch.int32, torch.int64):
+        itype = torch.int64
+    vals = _on(A.values, dev)
+    cols = _on(A.col_indices, dev, itype)
+    ptrs = _on(A.row_ptrs, dev, itype)
+    nnz = vals.numel()
+    size = _lib.load().tsp_csr_plan_size(m, nnz)
+    win = torch.empty(size, dtype=torch.int64, device=dev)
+    _lib.call("tsp_csr_plan", ptrs.data_ptr(), _lib.index_code(itype), m, nnz, win.data_ptr(), _lib.stream_handle(dev))
+    res = (vals, cols, ptrs, win)
+    try:
+        A._hip_csr = (key, res)
+    except AttributeError:
+        pass
+    return res
+
+
+def _csr_forward(vals, cols, ptrs, win, shape, X, alpha, Y, beta, dev):
+    m, n = shape
+    if vals.dtype != X.dtype:
+        raise RuntimeError(f"CSR values dtype {vals.dtype} and dense operand dtype {X.dtype} differ")
+    code = _lib.dtype_code(vals.dtype)
+    if code == _lib.TSP_BF16:
+        raise RuntimeError("HIP CSR kernels support float32 and float64 values")
+    icode = _lib.index_code(cols.dtype)
+    Xd = _on(X, dev)
+    use_y = Y is not None and beta != 0.0
+    Yd = _on(Y, dev, vals.dtype) if use_y else None
+    st = _lib.stream_handle(dev)
+    if Xd.dim() == 1:
+        out = torch.empty(m, dtype=vals.dtype, device=dev)
+        if use_y and Yd.shape != (m,):
+            Yd = Yd.expand(m).contiguous()
+        _lib.call("tsp_csr_spmv", vals.data_ptr(), code, cols.data_ptr(), ptrs.data_ptr(), icode, m, n, vals.numel(),
+                  win.data_ptr(), Xd.data_ptr(), float(alpha), _lib.ptr(Yd), float(beta), out.data_ptr(), st)
+        return out
+    ncols = Xd.shape[1]
+    out = torch.empty(m, ncols, dtype=vals.dtype, device=dev)
+    if use_y and Yd.shape != (m, ncols):
+        Yd = Yd.expand(m, ncols).contiguous()
+    _lib.call("tsp_csr_spmm", vals.data_ptr(), code, cols.data_ptr(), ptrs.data_ptr(), icode, m, n, vals.numel(),
+              Xd.data_ptr(), ncols, ncols, float(alpha), _lib.ptr(Yd), ncols, float(beta), out.data_ptr(), ncols, st)
+    return out
+
+
+class _CSRMatMulFunction(torch.autograd.Function):
+    """alpha * A @ X (+ beta * Y) for CSR A and dense X (vector or matrix).
+
+    Forward: the gfx950 SpMV / SpMM kernels. Backward (torch ops):
+      d values[p] = alpha * <dOut[row p], X[col p]>   (pattern fixed)
+      dX          = alpha * A^T @ dOut,   dY = beta * dOut
+    """
+
+    @staticmethod
+    def forward(ctx, values, col_indices, row_ptrs, shape, X, alpha, Y, beta, prepared):
+        vals, cols, ptrs, win = prepared
+        dev = vals.device
+        out = _csr_forward(vals, cols, ptrs, win, shape, X, alpha, Y, beta, dev)
+        ctx.save_for_backward(values, X)
+        ctx.pattern = (cols, ptrs)
+        ctx.shape, ctx.alpha, ctx.beta, ctx.has_y = shape, alpha, beta, Y is not None and beta != 0.0
+        ctx.y_meta = (Y.device, Y.dtype, Y.shape) if Y is not None else None
+        return out.to(X.device)
+
+    @staticmethod
+    def backward(ctx, g):
+        values, X = ctx.saved_tensors
+        cols, ptrs = ctx.pattern
+        dev = cols.device
+        m, n = ctx.shape
+        gd = g.to(dev)
+        Xd = X.to(dev)
+        rows = torch.repeat_interleave(torch.arange(m, device=dev), (ptrs[1:] - ptrs[:-1]).long())
+        c = cols.long()
+        gv = gx = gy = None
+        g2 = gd if gd.dim() == 2 else gd.unsqueeze(1)
+        X2 = Xd if Xd.dim() == 2 else Xd.unsqueeze(1)
+        if ctx.needs_input_grad[0]:
+            gv = (ctx.alpha * (g2[rows] * X2[c]).sum(dim=1)).to(values.device, values.dtype)
+        if ctx.needs_input_grad[4]:
+            vd = values.to(dev)
+            contrib = ctx.alpha * vd.unsqueeze(1) * g2[rows]
+            gx2 = torch.zeros(n, X2.shape[1], dtype=contrib.dtype, device=dev).index_add_(0, c, contrib)
+            gx = (gx2 if Xd.dim() == 2 else gx2.squeeze(1)).to(X.device, X.dtype)
+        if ctx.needs_input_grad[6] and ctx.has_y:
+            ydev, ydt, yshape = ctx.y_meta
+            gy = (ctx.beta * gd).sum_to_size(yshape).to(ydev, ydt)
+        return gv, None, None, None, gx, None, gy, None, None
+
+
+def _csr_apply(A, X, alpha, Y, beta):
+    dev = _target_device(X, A.values)
+    with torch.cuda.device(dev):
+        prepared = _csr_device(A, dev)
+        return _CSRMatMulFunction.apply(A.values, A.col_indices, A.row_ptrs, tuple(A.shape), X, alpha, Y, beta, prepared)
+
+
+def hip_spmv(A, x: torch.Tensor, alpha: float = 1.0, y: torch.Tensor | None = None, beta: float = 0.0) -> torch.Tensor:
+    """CSR SpMV entry point (the reference's spmv runs torch.sparse_csr @ x, ops.py:30-48)."""
+    return _csr_apply(A, x, alpha, y, beta)
+
+
+def hip_spmm(A, B: torch.Tensor, alpha: float = 1.0, C: torch.Tensor | None = None, beta: float = 0.0) -> torch.Tensor:
+    """CSR SpMM entry point (replaces nki_spmm, reference dispatch.py:181-190)."""
+    return _csr_apply(A, B, alpha, C, beta)
+
+
+# ---------------------------------------------------------------- screened
+
+
+def _screened_forward(A, diag, threshold, B, dev):
+    import math
+
+    M, K = A.shape
+    if A.dtype != B.dtype:
+        raise RuntimeError(f"screened_spmm: A dtype {A.dtype} and B dtype {B.dtype} differ")
+    if A.dtype not in (torch.float32, torch.float64):
+        raise RuntimeError(f"HIP screened_spmm supports float32 and float64, got {A.dtype}")
+    if diag.dtype not in (torch.float32, torch.float64):
+        raise RuntimeError(f"HIP screened_spmm needs float32 or float64 diag_integrals, got {diag.dtype}")
+    if B.dim() != 2 or B.shape[0] != K:
+        raise RuntimeError(f"screened_spmm: B shape {tuple(B.shape)} does not match A {tuple(A.shape)}")
+    Ad, Bd, dd = _on(A, dev), _on(B, dev), _on(diag, dev)
+    ncols = Bd.shape[1]
+    C = torch.empty(M, ncols, dtype=A.dtype, device=dev)
+    dcode = _lib.dtype_code(dd.dtype)
+    ws = torch.empty(max(1, _lib.load().tsp_screened_workspace_size(M, dcode)), dtype=torch.uint8, device=dev)
+    _lib.call("tsp_screened_spmm", Ad.data_ptr(), _lib.dtype_code(Ad.dtype), M, dd.data_ptr(), dcode,
+              math.sqrt(threshold), M, Bd.data_ptr(), ncols, ncols, C.data_ptr(), ncols, ws.data_ptr(),
+              _lib.stream_handle(dev))
+    return C
+
+
+class _ScreenedSpMMFunction(torch.autograd.Function):
+    """Autograd wrapper of the fused screened SpMM (reference dispatch.py:447-484).
+
+    Forward: the gfx950 kernel (mask applied while staging A tiles).
+    Backward (torch ops): dA = (dC @ B^T) * mask, dB = (A * mask)^T @ dC; no
+    gradient to diag_integrals or threshold (the mask is discrete).
+    """
+
+    @staticmethod
+    def forward(ctx, A, diag_integrals, threshold, B):
+        dev = _target_device(B, A, diag_integrals)
+        with torch.cuda.device(dev):
+            C = _screened_forward(A, diag_integrals, threshold, B, dev)
+        ctx.save_for_backward(A, diag_integrals, B)
+        ctx.threshold = threshold
+        return C.to(B.device)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        import math
+
+        A, diag, B = ctx.saved_tensors
+        Q = torch.sqrt(torch.abs(diag))
+        mask = ((Q.unsqueeze(-1) * Q.unsqueeze(0)) > math.sqrt(ctx.threshold)).to(A.dtype)
+        g = grad_out.to(A.device)
+        grad_A = (g @ B.to(A.device).T) * mask if ctx.needs_input_grad[0] else None
+        grad_B = ((A * mask).T @ g).to(B.device) if ctx.needs_input_grad[3] else None
+        return grad_A, None, None, grad_B
+
+
+def hip_screened_spmm(A, diag_integrals, B, threshold: float):
+    """Screened SpMM entry point (replaces nki_screened_spmm, reference dispatch.py:487-494)."""
+    return _ScreenedSpMMFunction.apply(A, diag_integrals, threshold, B)

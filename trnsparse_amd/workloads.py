@@ -88,7 +88,16 @@ def cfg2_csr(m: int = 1 << 20, n: int | None = None, dist: str = "poisson", seed
         lens = np.clip(rng.zipf(1.5, size=m), 1, 4096)
     else:
         raise ValueError(dist)
-    lens = np.minimum(lens, n).astype(np.int64)
+    values, cols, row_ptrs = random_csr(lens, n, rng)
+    x = rng.standard_normal(n, dtype=np.float32)
+    return values, cols.astype(index_dtype), row_ptrs.astype(index_dtype), x, (m, n)
+
+
+def random_csr(lens, n: int, rng: np.random.Generator):
+    """(values f32, col_idx int64, row_ptrs int64) with the given row lengths;
+    columns of a row distinct, sorted, uniform over [0, n); values N(0,1)."""
+    lens = np.minimum(np.asarray(lens, dtype=np.int64), n)
+    m = lens.shape[0]
     row_ptrs = np.zeros(m + 1, dtype=np.int64)
     np.cumsum(lens, out=row_ptrs[1:])
     nnz = int(row_ptrs[-1])
@@ -102,8 +111,7 @@ def cfg2_csr(m: int = 1 << 20, n: int | None = None, dist: str = "poisson", seed
         s, e = row_ptrs[r], row_ptrs[r + 1]
         cols[s:e] = np.sort(rng.choice(n, size=e - s, replace=False))
     values = rng.standard_normal(nnz, dtype=np.float32)
-    x = rng.standard_normal(n, dtype=np.float32)
-    return values, cols.astype(index_dtype), row_ptrs.astype(index_dtype), x, (m, n)
+    return values, cols, row_ptrs
 
 
 def csr_matrix_from_arrays(values, cols, row_ptrs, shape, device="cpu") -> CSRMatrix:

@@ -135,6 +135,29 @@ int tsp_screened_spmm(const void* A, int dtype, int64_t lda, const void* diag,
                       const void* B, int64_t ldb, int64_t ncols, void* C,
                       int64_t ldc, void* workspace, void* stream);
 
+/* ======================================================================
+ * Block-sparse attention forward, per head h < n_heads:
+ *   O[h] = softmax_rows(scale * Q[h] K[h]^T restricted to the stored mask
+ *          blocks) V[h]
+ * Q, K, V, O (n_heads, seq_len, head_dim) contiguous, `dtype` (TSP_BF16 on
+ * the MFMA path for block_size 128 and head_dim 64/128; TSP_F32, TSP_F64
+ * and other shapes on the generic path). The mask (block_row_ptrs with at
+ * least seq_len/block_size + 1 entries, block_col_indices) is shared by all
+ * heads; only its pattern is used. Rows of an empty block row, and rows past
+ * (seq_len/block_size)*block_size, are zero.
+ * row_max / row_denom (optional, both or neither): (n_heads,
+ * seq_len/block_size, block_size) in float (double for TSP_F64) — the row
+ * max of the scaled scores and the softmax denominator clamped at 1e-12
+ * (0 and 1e-12 for empty rows), saved for the backward pass.
+ * Replaces nki_bsr_attn_tiled (trnsparse/nki/dispatch.py:580-677) and the
+ * torch spec _block_sparse_attn_pytorch (trnsparse/ops.py:280-357).
+ * ==================================================================== */
+int tsp_bsa_fwd(const void* Q, const void* K, const void* V, int dtype,
+                int64_t n_heads, int64_t seq_len, int64_t head_dim,
+                const int64_t* block_row_ptrs, const int64_t* block_col_indices,
+                int64_t block_size, double scale, void* O, void* row_max,
+                void* row_denom, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -151,15 +151,18 @@ def screened_spmm(A, diag, B, threshold, absolute=False):
 # ------------------------------------------------------------ attention
 
 
-def block_sparse_attention(Q, K, V, row_ptrs, col_idx, b, scale):
+def block_sparse_attention(Q, K, V, row_ptrs, col_idx, b, scale, rows=None):
     """Block-sparse attention in float64 (reference ops.py:280-357).
 
     The reference's pass 1 + reduction (tile max / stable exp-sum combined
     into row_max, row_denom) computes the exact row max and softmax
     denominator over the keys of the stored blocks; in float64 they are
     formed directly here. A block listed twice counts twice, as there.
-    Returns (out, row_max, row_denom) with stats shaped (M_tiles, b).
-    Empty block rows: row_max 0, row_denom 1e-12, output 0.
+    Keys at or past seq_len do not exist (the reference slices K/V, which
+    come back short). `rows` restricts the work to some block rows (the
+    other rows are left zero). Returns (out, row_max, row_denom) with stats
+    shaped (M_tiles, b). Empty block rows: row_max 0, row_denom 1e-12,
+    output 0.
     """
     S, D = Q.shape
     Mt = S // b
@@ -167,12 +170,12 @@ def block_sparse_attention(Q, K, V, row_ptrs, col_idx, b, scale):
     out = np.zeros((S, D))
     rmax = np.zeros((Mt, b))
     rden = np.full((Mt, b), 1e-12)
-    for m in range(Mt):
+    for m in range(Mt) if rows is None else rows:
         s, e = row_ptrs[m], row_ptrs[m + 1]
         if s == e:
             continue
         cols = col_idx[s:e]
-        keys = np.concatenate([np.arange(c * b, (c + 1) * b) for c in cols])
+        keys = np.concatenate([np.arange(c * b, min((c + 1) * b, S)) for c in cols])
         sc = (q[m * b : (m + 1) * b] @ k[keys].T) * scale
         mx = sc.max(axis=1)
         p = np.exp(sc - mx[:, None])

@@ -1,0 +1,336 @@
+// Block-sparse attention forward for gfx950.
+//
+// Semantics follow the reference spec `_block_sparse_attn_pytorch`
+// (trnsparse/ops.py:280-357), per head:
+//   score(q, k) = (Q[q] . K[k]) * scale for keys k of the stored mask blocks
+//                 of q's block row (all b columns of a stored block)
+//   row_max     = max score, row_denom = max(sum exp(score - row_max), 1e-12)
+//   O[q]        = sum exp(score - row_max) / row_denom * V[k]
+// Empty block rows give O = 0, row_max = 0, row_denom = 1e-12 (:320-337).
+// Keys at or beyond seq_len do not exist (the reference's K slice is short).
+// The reference's two passes plus host reduction (and the NKI path's
+// device->host->device round trip, trnsparse/nki/dispatch.py:580-677)
+// become one pass with an online softmax; the stats are returned for the
+// autograd context.
+//
+// Kernels
+//   bsa_fwd_bf16_mfma<D>  bf16, 128-blocks, D in {64, 128}: one 256-thread
+//       workgroup per (head, 128-query block row); each wavefront owns 32
+//       queries. Scores are formed transposed, S^T = K Q^T, with
+//       v_mfma_f32_32x32x16_bf16 (A = K rows from LDS, B = the wave's Q rows
+//       held in registers), so a lane holds all scores of one query: the
+//       softmax needs one cross-lane shuffle. O^T = V^T P^T consumes P from
+//       registers (bf16) with V staged transposed in LDS. fp32 softmax with
+//       exp2, fp32 accumulation, bf16 output.
+//   bsa_fwd_generic<T>    fp32/fp64/bf16, any block size and head_dim: one
+//       thread per (query, 32-wide slice of head_dim), online softmax in
+//       the accumulation type (double for fp64).
+#include "common.h"
+
+namespace {
+
+constexpr float LOG2E = 1.4426950408889634f;
+
+// ------------------------------------------------------------------ generic
+
+template <typename T> struct AttnAcc { typedef float type; };
+template <> struct AttnAcc<double> { typedef double type; };
+
+template <typename T> __device__ inline typename AttnAcc<T>::type ld_acc(const T* p) { return (typename AttnAcc<T>::type)*p; }
+template <> __device__ inline float ld_acc<uint16_t>(const uint16_t* p) { return tsp::bf16_bits_to_f32(*p); }
+template <typename T> __device__ inline T st_cvt(typename AttnAcc<T>::type v) { return (T)v; }
+template <> __device__ inline uint16_t st_cvt<uint16_t>(float v) { return tsp::f32_to_bf16_bits(v); }
+
+__device__ inline float acc_exp(float v) { return __expf(v); }
+__device__ inline double acc_exp(double v) { return exp(v); }
+
+constexpr int GEN_DC = 32;  // head_dim slice per thread
+
+template <typename T>
+__global__ __launch_bounds__(128) void bsa_fwd_generic(
+    const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V, int64_t S, int64_t D,
+    int64_t head_stride, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci, int64_t b, int64_t Mt,
+    typename AttnAcc<T>::type scale, T* __restrict__ O, typename AttnAcc<T>::type* __restrict__ rmax,
+    typename AttnAcc<T>::type* __restrict__ rden) {
+  typedef typename AttnAcc<T>::type AccT;
+  // blockIdx.x: query chunk of 128 rows; blockIdx.y: head_dim slice; blockIdx.z: head
+  const int64_t head = blockIdx.z;
+  const int64_t q = (int64_t)blockIdx.x * 128 + threadIdx.x;
+  if (q >= Mt * b) return;
+  const int64_t d0 = (int64_t)blockIdx.y * GEN_DC;
+  const int64_t m = q / b;
+  const T* Qh = Q + head * head_stride;
+  const T* Kh = K + head * head_stride;
+  const T* Vh = V + head * head_stride;
+  AccT acc[GEN_DC];
+#pragma unroll
+  for (int i = 0; i < GEN_DC; ++i) acc[i] = 0;
+  AccT mrun = -INFINITY, lrun = 0;
+  const int64_t e = rp[m + 1];
+  for (int64_t idx = rp[m]; idx < e; ++idx) {
+    const int64_t k0 = ci[idx] * b;
+    for (int64_t k = k0; k < k0 + b && k < S; ++k) {
+      AccT s = 0;
+      for (int64_t d = 0; d < D; ++d) s += ld_acc(Qh + q * D + d) * ld_acc(Kh + k * D + d);
+      s *= scale;
+      const AccT mnew = s > mrun ? s : mrun;
+      const AccT alpha = acc_exp(mrun - mnew);
+      const AccT p = acc_exp(s - mnew);
+      lrun = lrun * alpha + p;
+#pragma unroll
+      for (int i = 0; i < GEN_DC; ++i) {
+        const AccT v = d0 + i < D ? ld_acc(Vh + k * D + d0 + i) : (AccT)0;
+        acc[i] = acc[i] * alpha + p * v;
+      }
+      mrun = mnew;
+    }
+  }
+  const bool empty = rp[m] == e;
+  const AccT den = lrun > (AccT)1e-12 ? lrun : (AccT)1e-12;
+  T* Oq = O + head * head_stride + q * D;
+#pragma unroll
+  for (int i = 0; i < GEN_DC; ++i)
+    if (d0 + i < D) Oq[d0 + i] = st_cvt<T>(empty ? (AccT)0 : acc[i] / den);
+  if (blockIdx.y == 0 && rmax) {
+    rmax[head * Mt * b + q] = empty ? (AccT)0 : mrun;
+    rden[head * Mt * b + q] = empty ? (AccT)1e-12 : den;
+  }
+}
+
+// ------------------------------------------------------------- bf16 MFMA
+
+constexpr int AB = 128;  // block size served by the MFMA kernel
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void bsa_fwd_bf16_mfma(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int64_t S,
+    int64_t head_stride, int64_t H, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci, int64_t Mt,
+    float scale_log2, uint16_t* __restrict__ O, float* __restrict__ rmax, float* __restrict__ rden) {
+  constexpr int KS = D / 16;      // k-steps of S^T = K Q^T
+  constexpr int K_LD = D + 8;     // LDS row stride (bf16) of K [key][d]
+  constexpr int V_LD = AB + 4;    // LDS row stride (bf16) of V^T [d][key]
+  constexpr int NU = D / 32;      // 32-wide d subtiles of O^T
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[AB * K_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[D * V_LD];
+
+  // XCD-aware order: XCD x walks heads x, x+8, ...; the block rows of one
+  // head run side by side and share that head's K/V in the XCD's L2.
+  const int64_t g = blockIdx.x;
+  const int64_t xcd = g & 7, slot = g >> 3;
+  const int64_t head = xcd + 8 * (slot / Mt);
+  const int64_t m = slot % Mt;
+  if (head >= H) return;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  const uint16_t* Qh = Q + head * head_stride;
+  const uint16_t* Kh = K + head * head_stride;
+  const uint16_t* Vh = V + head * head_stride;
+  const int64_t q = m * AB + w * 32 + l32;  // this lane's query (always < S: m < Mt)
+
+  // Q fragments for the B operand: Q[q][16s + 8h .. +7]
+  bf16x8 qf[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) qf[s] = *(const bf16x8*)(Qh + q * D + 16 * s + 8 * h);
+
+  f32x16 o[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) o[u] = f32x16{};
+  float mrun = -INFINITY, lrun = 0.f;
+
+  const int64_t e = rp[m + 1];
+  for (int64_t idx = rp[m]; idx < e; ++idx) {
+    const int64_t key0 = ci[idx] * AB;
+    __syncthreads();  // previous block's LDS reads are done
+    // ---- stage K block [key][d] and V block transposed [d][key] (4 keys x 8 d
+    // patches); rows past seq_len are zero. `full` (uniform) drops the guards.
+    const int nvalid = (int)((S - key0) < AB ? (S - key0) : AB);
+    const bool full = nvalid == AB;
+    u16x8 kreg[(AB * D / 8) / 256];
+#pragma unroll
+    for (int i = 0; i < (AB * D / 8) / 256; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c / (D / 8), col = (c % (D / 8)) * 8;
+      if (full || key < nvalid)
+        kreg[i] = *(const u16x8*)(Kh + (key0 + key) * D + col);
+      else
+        kreg[i] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < (AB * D / 8) / 256; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c / (D / 8), col = (c % (D / 8)) * 8;
+      *(u16x8*)(Ks + key * K_LD + col) = kreg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < (AB / 4) * (D / 8) / 256; ++i) {
+      const int p = tid + 256 * i;
+      const int kg = p % (AB / 4), dg = p / (AB / 4);
+      u16x8 r[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = 4 * kg + j;
+        if (full || key < nvalid)
+          r[j] = *(const u16x8*)(Vh + (key0 + key) * D + 8 * dg);
+        else
+          r[j] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int dd = 0; dd < 8; ++dd) {
+        typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+        u16x4 t = {r[0][dd], r[1][dd], r[2][dd], r[3][dd]};
+        *(u16x4*)(Vt + (8 * dg + dd) * V_LD + 4 * kg) = t;
+      }
+    }
+    __syncthreads();
+
+    // The block's 128 keys are taken as two halves of 64 (register budget):
+    // each half forms its S^T tiles, updates the online softmax and adds its
+    // P V contribution.
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      // ---- S^T tiles: keys 32t + 8*(v/4) + 4h + v%4 (t = 2*half + tt), query l32
+      f32x16 st[2];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int t = 2 * half + tt;
+        st[tt] = f32x16{};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const bf16x8 a = *(const bf16x8*)(Ks + (32 * t + l32) * K_LD + 16 * s + 8 * h);
+          st[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], st[tt], 0, 0, 0);
+        }
+      }
+      // ---- online softmax (log2 domain), keys past seq_len excluded
+      float mx = mrun;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = 32 * (2 * half + tt) + 8 * (v >> 2) + 4 * h + (v & 3);
+          const float val = (full || key < nvalid) ? st[tt][v] * scale_log2 : -INFINITY;
+          st[tt][v] = val;
+          mx = fmaxf(mx, val);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float alpha = mx == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(mrun - mx);
+      float lsum = 0.f;
+      bf16x8 pb[2][2];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float p = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st[tt][v] - mx);
+          lsum += p;
+          pb[tt][v >> 3][v & 7] = (__bf16)p;
+        }
+      }
+      lsum += __shfl_xor(lsum, 32, 64);
+      lrun = lrun * alpha + lsum;
+      mrun = mx;
+#pragma unroll
+      for (int u = 0; u < NU; ++u) o[u] *= alpha;
+      // ---- O^T += V^T P^T; k-step (t, a) covers keys 32t+16a+[0,16): lane
+      // half h supplies keys 4h+{0..3} and 8+4h+{0..3} (its own S^T rows).
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const uint16_t* vrow = Vt + (32 * u + l32) * V_LD;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          const int t = 2 * half + tt;
+#pragma unroll
+          for (int a = 0; a < 2; ++a) {
+            typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+            const u16x4 lo = *(const u16x4*)(vrow + 32 * t + 16 * a + 4 * h);
+            const u16x4 hi = *(const u16x4*)(vrow + 32 * t + 16 * a + 8 + 4 * h);
+            const u16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            o[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av), pb[tt][a], o[u], 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+
+  // ---- epilogue: O[q][32u + 8*(v/4) + 4h + v%4] = o / denom
+  const bool empty = rp[m] == e;
+  const float den = lrun > 1e-12f ? lrun : 1e-12f;
+  const float inv = empty ? 0.f : 1.f / den;
+  uint16_t* Oq = O + head * head_stride + q * D;
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+      u16x4 t;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t[i] = tsp::f32_to_bf16_bits(o[u][4 * g4 + i] * inv);
+      *(u16x4*)(Oq + 32 * u + 8 * g4 + 4 * h) = t;
+    }
+  }
+  if (h == 0 && rmax) {
+    const int64_t r = head * Mt * AB + q;
+    rmax[r] = empty ? 0.f : mrun * 0.69314718055994531f;
+    rden[r] = empty ? 1e-12f : den;
+  }
+}
+
+template <typename T>
+int launch_generic(const void* Q, const void* K, const void* V, int64_t H, int64_t S, int64_t D, const int64_t* rp,
+                   const int64_t* ci, int64_t b, int64_t Mt, double scale, void* O, void* rmax, void* rden,
+                   hipStream_t st) {
+  typedef typename AttnAcc<T>::type AccT;
+  const int64_t gx = tsp::ceil_div(Mt * b, 128), gy = tsp::ceil_div(D, GEN_DC);
+  if (gx > INT32_MAX || gy > 65535 || H > 65535) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_fwd: problem too large for the generic kernel");
+  hipLaunchKernelGGL((bsa_fwd_generic<T>), dim3((unsigned)gx, (unsigned)gy, (unsigned)H), dim3(128), 0, st, (const T*)Q,
+                     (const T*)K, (const T*)V, S, D, S * D, rp, ci, b, Mt, (AccT)scale, (T*)O, (AccT*)rmax, (AccT*)rden);
+  return tsp::check_launch("bsa_fwd_generic launch");
+}
+
+}  // namespace
+
+extern "C" int tsp_bsa_fwd(const void* Q, const void* K, const void* V, int dtype, int64_t n_heads, int64_t seq_len,
+                           int64_t head_dim, const int64_t* block_row_ptrs, const int64_t* block_col_indices,
+                           int64_t block_size, double scale, void* O, void* row_max, void* row_denom, void* stream) {
+  if (dtype != TSP_F32 && dtype != TSP_F64 && dtype != TSP_BF16)
+    return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_fwd: dtype %d not supported", dtype);
+  if (n_heads < 0 || seq_len < 0 || head_dim < 0 || block_size <= 0) return tsp::fail(TSP_EINVAL, "tsp_bsa_fwd: bad size");
+  if ((row_max == nullptr) != (row_denom == nullptr)) return tsp::fail(TSP_EINVAL, "tsp_bsa_fwd: row_max and row_denom go together");
+  const int64_t Mt = seq_len / block_size;
+  if (n_heads == 0 || seq_len == 0 || head_dim == 0) return TSP_OK;
+  if (!Q || !K || !V || !O || !block_row_ptrs || !block_col_indices) return tsp::fail(TSP_EINVAL, "tsp_bsa_fwd: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  // rows past Mt*block_size have no block row: zero output (the reference's out starts at zero)
+  if (Mt * block_size < seq_len) {
+    const int64_t es = dtype == TSP_F64 ? 8 : (dtype == TSP_F32 ? 4 : 2);
+    const int64_t tail = (seq_len - Mt * block_size) * head_dim * es;
+    for (int64_t hh = 0; hh < n_heads; ++hh) {
+      int rc = tsp::zero_fill((char*)O + (hh * seq_len + Mt * block_size) * head_dim * es, tail, st);
+      if (rc) return rc;
+    }
+  }
+  if (Mt == 0) return TSP_OK;
+  if (dtype == TSP_BF16 && block_size == AB && (head_dim == 64 || head_dim == 128) && ((uintptr_t)Q % 16) == 0 &&
+      ((uintptr_t)K % 16) == 0 && ((uintptr_t)V % 16) == 0 && ((uintptr_t)O % 8) == 0) {
+    const int64_t grid = tsp::ceil_div(n_heads, 8) * Mt * 8;
+    if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_fwd: problem too large");
+    const float sl2 = (float)(scale * 1.4426950408889634);
+    if (head_dim == 128)
+      hipLaunchKernelGGL((bsa_fwd_bf16_mfma<128>), dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)Q,
+                         (const uint16_t*)K, (const uint16_t*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs,
+                         block_col_indices, Mt, sl2, (uint16_t*)O, (float*)row_max, (float*)row_denom);
+    else
+      hipLaunchKernelGGL((bsa_fwd_bf16_mfma<64>), dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)Q,
+                         (const uint16_t*)K, (const uint16_t*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs,
+                         block_col_indices, Mt, sl2, (uint16_t*)O, (float*)row_max, (float*)row_denom);
+    return tsp::check_launch("bsa_fwd_bf16_mfma launch");
+  }
+  if (dtype == TSP_F64)
+    return launch_generic<double>(Q, K, V, n_heads, seq_len, head_dim, block_row_ptrs, block_col_indices, block_size, Mt,
+                                  scale, O, row_max, row_denom, st);
+  if (dtype == TSP_F32)
+    return launch_generic<float>(Q, K, V, n_heads, seq_len, head_dim, block_row_ptrs, block_col_indices, block_size, Mt,
+                                 scale, O, row_max, row_denom, st);
+  return launch_generic<uint16_t>(Q, K, V, n_heads, seq_len, head_dim, block_row_ptrs, block_col_indices, block_size,
+                                  Mt, scale, O, row_max, row_denom, st);
+}

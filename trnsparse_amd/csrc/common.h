@@ -26,6 +26,9 @@ int fail(int code, const char* fmt, ...);
 int check_hip(hipError_t e, const char* what);
 // Check the most recent launch on this thread.
 int check_launch(const char* what);
+// Zero `bytes` bytes at device pointer p with a fill kernel on `st` (used
+// instead of hipMemsetAsync so callers may capture the work in a HIP graph).
+int zero_fill(void* p, int64_t bytes, hipStream_t st);
 
 // ---------------------------------------------------------------- bf16
 // Round-to-nearest-even fp32 -> bf16 bit pattern (NaN kept quiet), the same

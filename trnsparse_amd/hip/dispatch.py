@@ -356,3 +356,42 @@ class _ScreenedSpMMFunction(torch.autograd.Function):
 def hip_screened_spmm(A, diag_integrals, B, threshold: float):
     """Screened SpMM entry point (replaces nki_screened_spmm, reference dispatch.py:487-494)."""
     return _ScreenedSpMMFunction.apply(A, diag_integrals, threshold, B)
+
+
+# --------------------------------------------------------------- attention
+
+
+def hip_block_sparse_attention(Q, K, V, mask_bsr, scale: float, return_stats: bool = False):
+    """Block-sparse attention forward (replaces nki_bsr_attn_tiled, reference
+    dispatch.py:580-677). Q/K/V (S, D) or (..., S, D) sharing one mask.
+    Honours `scale` (the reference NKI path used head_dim**-0.5 regardless).
+    Stats come back as (..., S // b, b) in float32 (float64 for float64 input).
+    """
+    if not (Q.shape == K.shape == V.shape):
+        raise RuntimeError(f"Q, K, V shapes differ: {tuple(Q.shape)}, {tuple(K.shape)}, {tuple(V.shape)}")
+    if not (Q.dtype == K.dtype == V.dtype):
+        raise RuntimeError("Q, K, V dtypes differ")
+    code = _lib.dtype_code(Q.dtype)
+    lead = Q.shape[:-2]
+    S, D = Q.shape[-2:]
+    b = mask_bsr.block_size
+    Mt = S // b
+    orig = Q.device
+    dev = _target_device(Q, K, V)
+    with torch.cuda.device(dev):
+        rp, ci, _ = _bsr_plan(mask_bsr.block_col_indices, mask_bsr.block_row_ptrs,
+                              mask_bsr.block_row_ptrs.numel() - 1, dev, holder=mask_bsr)
+        if rp.numel() < Mt + 1:
+            raise IndexError(f"mask has {rp.numel() - 1} block rows, attention needs {Mt}")
+        Qd, Kd, Vd = (_on(t, dev).reshape(-1, S, D) for t in (Q, K, V))
+        H = Qd.shape[0]
+        O = torch.empty_like(Qd)
+        sdt = torch.float64 if Q.dtype == torch.float64 else torch.float32
+        rmax = torch.empty(H, Mt, b, dtype=sdt, device=dev) if return_stats else None
+        rden = torch.empty(H, Mt, b, dtype=sdt, device=dev) if return_stats else None
+        _lib.call("tsp_bsa_fwd", Qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), code, H, S, D, rp.data_ptr(),
+                  ci.data_ptr(), b, float(scale), O.data_ptr(), _lib.ptr(rmax), _lib.ptr(rden), _lib.stream_handle(dev))
+    out = O.reshape(*lead, S, D).to(orig)
+    if not return_stats:
+        return out
+    return out, rmax.reshape(*lead, Mt, b).to(orig), rden.reshape(*lead, Mt, b).to(orig)

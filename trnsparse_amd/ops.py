@@ -388,8 +388,8 @@ class _AttnTiledFunction(torch.autograd.Function):
         lead = Q.shape[:-2]
         S, D = Q.shape[-2:]
         q, k, v, o, do = (t.reshape(-1, S, D) for t in (Q, K, V, O, dO))
-        rm = row_max.reshape(q.shape[0], -1)
-        rd = row_denom.reshape(q.shape[0], -1)
+        rm = row_max.reshape(q.shape[0], -1).to(Q.dtype)
+        rd = row_denom.reshape(q.shape[0], -1).to(Q.dtype)
         grads = [
             _block_sparse_attn_backward(q[h], k[h], v[h], o[h], do[h], ctx.handle, ctx.scale, rm[h], rd[h])
             for h in range(q.shape[0])

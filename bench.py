@@ -213,6 +213,77 @@ def bench_spmv(dist: str, index_bits: int, steps: int, warmup: int, cpu: bool = 
     return res
 
 
+def bench_screened(steps: int, warmup: int, cpu: bool = False):
+    """screened_spmm at config 4 (n=4096, threshold 1e-20): GFLOP/s counting
+    the 128x128 A tiles that are not fully screened, and dense-equivalent."""
+    import numpy as np
+    import torch
+
+    import trnsparse_amd as ts
+    from trnsparse_amd import workloads as W
+
+    A, diag, B, thr = W.cfg4_screened()
+    n = A.shape[0]
+    Q = torch.sqrt(torch.abs(diag))
+    qmax = Q.view(-1, 128).amax(dim=1)
+    active = int(((qmax[:, None] * qmax[None, :]) > np.float32(np.sqrt(thr))).sum())
+    flops = 2.0 * 128 * 128 * B.shape[1] * active
+    dense_flops = 2.0 * n * n * B.shape[1]
+    Ad, dd, Bd = A.cuda(), diag.cuda(), B.cuda()
+    _, ev_ms = time_gpu(lambda: ts.screened_spmm(Ad, dd, Bd, thr), steps, warmup)
+    tf = flops / (ev_ms * 1e-3) / 1e12
+    res = {
+        "name": "screened_spmm cfg4 n=4096 fp32",
+        "value": round(tf * 1e3, 1),
+        "unit": "GFLOP/s",
+        "us": round(ev_ms * 1e3, 1),
+        "active_tiles": active,
+        "dense_equiv_gflops": round(dense_flops / (ev_ms * 1e-3) / 1e9, 1),
+        "frac_fp32_mfma": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+    }
+    if cpu:
+        from oracle import cpu_baseline as cb
+
+        secs = cb.time_call(lambda: cb.screened_spmm(A, diag, B, thr), reps=3, budget_s=20.0)
+        res["cpu_baseline"] = {"value": round(flops / secs / 1e9, 2), "unit": "GFLOP/s", "cores": cb.threads(),
+                               "kind": "port", "sample": "full cfg4 through the reference's torch path (mask, A*mask, MKL sgemm)"}
+    return res
+
+
+def bench_attention(steps: int, warmup: int, cpu: bool = False):
+    """block_sparse_attention_tiled at config 5: 32 heads x 8192 x 128 bf16,
+    370 stored 128x128 blocks. FLOPs = 4 * nnzb * 128^2 * d * heads."""
+    import torch
+
+    import trnsparse_amd as ts
+    from trnsparse_amd import workloads as W
+
+    Q, K, V, mask = W.cfg5_attention()
+    H, S, D = Q.shape
+    flops = 4.0 * mask.n_blocks * 128 * 128 * D * H
+    byts = 4 * H * S * D * 2
+    Qd, Kd, Vd = Q.cuda(), K.cuda(), V.cuda()
+    _, ev_ms = time_gpu(lambda: ts.block_sparse_attention_tiled(Qd, Kd, Vd, mask), steps, warmup)
+    tf = flops / (ev_ms * 1e-3) / 1e12
+    res = {
+        "name": "block_sparse_attention cfg5 32x8192x128 bf16",
+        "value": round(tf * 1e3, 1),
+        "unit": "GFLOP/s",
+        "us": round(ev_ms * 1e3, 1),
+        "frac_bf16_mfma": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
+        "frac_hbm_min_bytes": round(byts / (ev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+    }
+    if cpu:
+        from oracle import cpu_baseline as cb
+
+        b = 128
+        ptr, col = mask.block_row_ptrs, mask.block_col_indices
+        secs = cb.time_call(lambda: cb.attention_head(Q[0], K[0], V[0], ptr, col, b, D**-0.5), reps=2, budget_s=20.0)
+        res["cpu_baseline"] = {"value": round(flops / H / secs / 1e9, 2), "unit": "GFLOP/s", "cores": cb.threads(),
+                               "kind": "port", "sample": "one head of cfg5 (bf16) through the reference's torch two-pass loops"}
+    return res
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -250,6 +321,8 @@ def main(argv=None) -> int:
             ("spmv poisson int32", lambda: bench_spmv("poisson", 32, 20, 3)),
             ("spmv zipf int64", lambda: bench_spmv("zipf", 64, 10, 2)),
             ("bsr bf16", lambda: bench_bsr_bf16(max(5, args.steps // 2), 3)),
+            ("screened", lambda: bench_screened(10, 2, cpu=not args.no_cpu)),
+            ("attention", lambda: bench_attention(10, 2, cpu=not args.no_cpu)),
         ]
         for name, fn in jobs:
             try:

@@ -155,3 +155,35 @@ def test_repeat_calls_are_deterministic(hip_backend):
     c1 = ts.bsr_spmm(A, Bd)
     c2 = ts.bsr_spmm(A, Bd)
     assert torch.equal(c1, c2)
+
+
+# ------------------------------------------------------------------ bf16
+
+
+@pytest.mark.parametrize("out_dtype", [None, torch.float32])
+@pytest.mark.parametrize(
+    "shape,N,density",
+    [((256, 256), 128, 0.5), ((512, 512), 256, 0.25), ((384, 384), 512, 0.5), ((512, 256), 128, 0.5),
+     ((200, 137), 64, 1.0), ((300, 260), 10, 1.0), ((384, 256), 200, 0.6)],
+)
+def test_bf16_mfma(hip_backend, shape, N, density, out_dtype):
+    g = torch.Generator().manual_seed(21)
+    A = (torch.randn(*shape, generator=g) * (torch.rand(*shape, generator=g) < density)).bfloat16()
+    bsr = ts.BSRMatrix.from_dense(A, block_size=128)
+    B = torch.randn(shape[1], N, generator=g).bfloat16()
+    got = ts.bsr_spmm(bsr, B.cuda(), out_dtype=out_dtype).cpu()
+    assert got.dtype == (out_dtype or torch.bfloat16) and got.shape == (shape[0], N)
+    exact, scale = _oracle(bsr, B)
+    assert ref.scaled_error(got.float().numpy(), exact, scale) <= TOL_BF16
+    if out_dtype == torch.float32:  # fp32 accumulation of exact bf16 products: near fp32 accuracy
+        assert ref.scaled_error(got.numpy(), exact, scale) <= TOL_F32
+
+
+def test_cfg3b_bf16_full_size(hip_backend):
+    A, B = W.cfg3_bsr(dtype=torch.bfloat16)
+    C = ts.bsr_spmm(A, B.cuda(), out_dtype=torch.float32)
+    assert C.dtype == torch.float32 and C.shape == (16384, 512)
+    rows = list(range(3, 128, 16)) + [0, 127]
+    exact, scale = _oracle(A, B, rows=rows)
+    got = torch.cat([C[r * 128 : (r + 1) * 128] for r in rows]).cpu().numpy()
+    assert ref.scaled_error(got, exact, scale) <= TOL_F32

@@ -17,6 +17,8 @@
 //                      over the row's blocks in 32-wide k-slabs staged through
 //                      a double-buffered LDS ring; the next slab's global
 //                      loads are in flight while the current one is consumed.
+//   bsr_spmm_bf16_mfma b == 128, bf16 in, fp32 accumulation, fp32/bf16 out
+//                      (v_mfma_f32_32x32x16_bf16, B slabs transposed in LDS).
 //   bsr_spmm_generic   any block size / dtype (f32, f64, bf16): one thread per
 //                      output element, a plain dot product over stored blocks.
 //
@@ -92,6 +94,120 @@ __global__ __launch_bounds__(T32::NTHR) void bsr_spmm_f32_mfma(
   f32x16 acc0 = {}, acc1 = {};
   T32::run(src, nsteps, lds, src.q, acc0, acc1);
   T32::store_tile(C, ldc, row * BS, src.n0, m, ncols, src.q, acc0, acc1, cvt_out<OutT>);
+}
+
+// ---------------------------------------------------------------- bf16 MFMA
+//
+// bsr_spmm_bf16_mfma: b == 128, bf16 operands, fp32 accumulation, fp32 or
+// bf16 output. Same tile (128x128 of C per workgroup, 8 waves of 32x64) and
+// scheduling as the fp32 kernel, with v_mfma_f32_32x32x16_bf16 on 64-wide
+// k-slabs. Both MFMA operands need 8 consecutive k per lane: A blocks are
+// [m][k] already; B panels are [k][n], so each B slab is transposed while
+// staged (4 k x 8 n register patches written as 8-byte rows of Bt[n][k]).
+namespace bf {
+constexpr int KC = 64;
+constexpr int LD = KC + 8;            // LDS row stride (bf16) of As[m][k] and Bt[n][k]
+constexpr int A_ELEMS = 128 * LD;
+constexpr int STAGE = 2 * A_ELEMS;    // As + Bt
+}  // namespace bf
+
+template <typename OutT>
+__global__ __launch_bounds__(512) void bsr_spmm_bf16_mfma(
+    const uint16_t* __restrict__ blocks, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci,
+    int64_t mb, int nt, int64_t m, int64_t n, const uint16_t* __restrict__ B, int64_t ldb, int64_t ncols,
+    OutT* __restrict__ C, int64_t ldc, const int32_t* __restrict__ order) {
+  typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * bf::STAGE];
+
+  const int g = blockIdx.x;
+  const int xcd = g & 7, slot = g >> 3;
+  const int64_t k = (int64_t)(slot / nt) * 8 + xcd;
+  if (k >= mb) return;
+  const int ntile = slot % nt;
+  const int64_t row = order ? (int64_t)order[k] : k;
+  const int64_t n0 = (int64_t)ntile * 128;
+  const int64_t start = rp[row];
+  const int nsteps = (int)(rp[row + 1] - start) * (BS / bf::KC);
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w & 3, wn = w >> 2, h = lane >> 5, l32 = lane & 31;
+  // staging: A slab 128 x 64 -> 2 chunks of 8 per thread; B slab 64 x 128 as
+  // 4k x 8n patches -> 256 patches, threads 0..255 one each
+  const int ar = tid >> 3, ac = (tid & 7) * 8;       // rows ar, ar+64
+  const int pk = (tid & 15) * 4, pn = (tid >> 4) * 8;  // patch (k 4, n 8), valid for tid < 256
+  const bool bstage = tid < 256;
+
+  u16x8 ra0, ra1, rb[4];
+  auto gload = [&](int s) {
+    const int64_t idx = start + (s >> 1);
+    const int kk = (s & 1) * bf::KC;
+    const uint16_t* a = blocks + idx * (BS * BS) + kk;
+    ra0 = *(const u16x8*)(a + ar * BS + ac);
+    ra1 = *(const u16x8*)(a + (ar + 64) * BS + ac);
+    if (bstage) {
+      const int64_t brow = ci[idx] * BS + kk + pk;
+      const int64_t c = n0 + pn;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        u16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (brow + j < n) {
+          const uint16_t* p = B + (brow + j) * ldb + c;
+          if (c + 7 < ncols) {
+            v = *(const u16x8*)p;
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              if (c + i < ncols) v[i] = p[i];
+          }
+        }
+        rb[j] = v;
+      }
+    }
+  };
+  auto lstore = [&](uint16_t* st) {
+    uint16_t* As = st;
+    uint16_t* Bt = st + bf::A_ELEMS;
+    *(u16x8*)(As + ar * bf::LD + ac) = ra0;
+    *(u16x8*)(As + (ar + 64) * bf::LD + ac) = ra1;
+    if (bstage) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const u16x4 t = {rb[0][i], rb[1][i], rb[2][i], rb[3][i]};
+        *(u16x4*)(Bt + (pn + i) * bf::LD + pk) = t;
+      }
+    }
+  };
+
+  f32x16 acc0 = {}, acc1 = {};
+  auto compute = [&](const uint16_t* st) {
+    const uint16_t* As = st;
+    const uint16_t* Bt = st + bf::A_ELEMS;
+#pragma unroll
+    for (int ks = 0; ks < bf::KC / 16; ++ks) {
+      const bf16x8 a = *(const bf16x8*)(As + (wm * 32 + l32) * bf::LD + 16 * ks + 8 * h);
+      const bf16x8 b0 = *(const bf16x8*)(Bt + (wn * 64 + l32) * bf::LD + 16 * ks + 8 * h);
+      const bf16x8 b1 = *(const bf16x8*)(Bt + (wn * 64 + 32 + l32) * bf::LD + 16 * ks + 8 * h);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b0, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b1, acc1, 0, 0, 0);
+    }
+  };
+
+  if (nsteps > 0) {
+    gload(0);
+    lstore(lds);
+    __syncthreads();
+    for (int s = 0; s < nsteps; ++s) {
+      const uint16_t* cur = lds + (s & 1) * bf::STAGE;
+      uint16_t* nxt = lds + ((s + 1) & 1) * bf::STAGE;
+      const bool more = s + 1 < nsteps;
+      if (more) gload(s + 1);
+      compute(cur);
+      if (more) lstore(nxt);
+      __syncthreads();
+    }
+  }
+  T32::Coords q;
+  T32::store_tile(C, ldc, row * BS, n0, m, ncols, q, acc0, acc1, cvt_out<OutT>);
 }
 
 template <typename T, typename OutT>
@@ -199,6 +315,21 @@ extern "C" int tsp_bsr_spmm(const void* blocks, int dtype, const int64_t* block_
                        block_row_ptrs, block_col_indices, mb, (int)nt, m, n, (const float*)B, ldb, ncols,
                        (float*)C, ldc, row_order);
     return tsp::check_launch("bsr_spmm_f32_mfma launch");
+  }
+  if (dtype == TSP_BF16 && block_size == BS && (ldb % 8) == 0 && ((uintptr_t)B % 16) == 0 &&
+      ((uintptr_t)blocks % 16) == 0) {
+    const int64_t nt = tsp::ceil_div(ncols, 128);
+    const int64_t grid = tsp::ceil_div(mb, 8) * 8 * nt;
+    if (grid > INT32_MAX || nt > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm: problem too large");
+    if (out_dtype == TSP_F32)
+      hipLaunchKernelGGL((bsr_spmm_bf16_mfma<float>), dim3((unsigned)grid), dim3(512), 0, st, (const uint16_t*)blocks,
+                         block_row_ptrs, block_col_indices, mb, (int)nt, m, n, (const uint16_t*)B, ldb, ncols, (float*)C,
+                         ldc, row_order);
+    else
+      hipLaunchKernelGGL((bsr_spmm_bf16_mfma<uint16_t>), dim3((unsigned)grid), dim3(512), 0, st,
+                         (const uint16_t*)blocks, block_row_ptrs, block_col_indices, mb, (int)nt, m, n,
+                         (const uint16_t*)B, ldb, ncols, (uint16_t*)C, ldc, row_order);
+    return tsp::check_launch("bsr_spmm_bf16_mfma launch");
   }
   if (dtype == TSP_F32) return launch_generic<float, float>(blocks, block_row_ptrs, block_col_indices, block_size, m, n, B, ldb, ncols, C, ldc, st);
   if (dtype == TSP_F64) return launch_generic<double, double>(blocks, block_row_ptrs, block_col_indices, block_size, m, n, B, ldb, ncols, C, ldc, st);

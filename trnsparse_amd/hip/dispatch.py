@@ -75,9 +75,10 @@ def _bsr_spmm_launch(blocks, rp, ci, order, shape, b, B, out_dtype, dev) -> torc
     blocks_d = _on(blocks, dev)
     B_d = _on(B, dev)
     ldb = ncols
-    if B_d.dtype == torch.float32 and b == 128 and ncols % 4:
-        # Row stride multiple of 4 floats for the vectorised B panel loads.
-        B_d = F.pad(B_d, (0, 4 - ncols % 4))
+    vec = {torch.float32: 4, torch.bfloat16: 8}.get(B_d.dtype)
+    if vec and b == 128 and ncols % vec:
+        # Row stride a multiple of 16 bytes for the vectorised B panel loads.
+        B_d = F.pad(B_d, (0, vec - ncols % vec))
         ldb = B_d.shape[1]
     C = torch.empty((m, ncols), dtype=out_dtype, device=dev)
     _lib.call(

@@ -46,11 +46,27 @@ def _events():
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
-def time_gpu(fn, steps: int, warmup: int, flush=None):
-    """(wall ms/step, event ms/step). With `flush`, each step is timed alone
-    after `flush()` evicts L2/MALL, and the event time is the median."""
+def prewarm(fn, seconds: float = 0.25):
+    """Run `fn` back to back for about `seconds` (untimed) so the GPU clocks
+    reach their sustained level before measuring; a cold MI355X measures
+    10-15% slow over the first tens of milliseconds."""
     import torch
 
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+
+
+def time_gpu(fn, steps: int, warmup: int, flush=None, prewarm_s: float = 0.25):
+    """(wall ms/step, event ms/step). With `flush`, each step is timed alone
+    after `flush()` evicts L2/MALL, and the event time is the median.
+    Untimed: a clock pre-warm of `prewarm_s` seconds, then `warmup` steps."""
+    import torch
+
+    if prewarm_s > 0:
+        prewarm(fn, prewarm_s)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -291,6 +307,8 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="headline only")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a plain 256 MiB device copy (known bytes) to calibrate PMC byte counters")
     args = ap.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -310,6 +328,14 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
+    if args.calibrate_copy:
+        a = torch.ones(1 << 26, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes_read": a.numel() * 4, "calibrate_copy_bytes_written": b.numel() * 4}))
+        return 0
     _lib.load()
     ts.set_backend("hip")
 
@@ -355,6 +381,7 @@ def main(argv=None) -> int:
         "roofline": head["roofline"],
         "cpu_baseline": head.get("cpu_baseline"),
         "secondary": secondary,
+        "timing": "HIP events on the launch stream; untimed 0.25 s clock pre-warm of the same op, then the W warmup steps",
     }
     print(json.dumps(line), flush=True)
     return 0

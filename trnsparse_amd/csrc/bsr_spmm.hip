@@ -14,20 +14,21 @@
 //                      (block row i, column tile t). 8 waves in a 4(M)x2(N)
 //                      grid, each wave a 32x64 sub-tile as two 32x32 MFMA
 //                      accumulators (v_mfma_f32_32x32x2_f32). The K loop runs
-//                      over the row's blocks in 32-wide k-slabs staged through
-//                      a double-buffered LDS ring; the next slab's global
-//                      loads are in flight while the current one is consumed.
+//                      over the row's blocks in 64-wide k-slabs staged through
+//                      a double-buffered LDS ring (137 KiB: one workgroup per
+//                      CU); the next slab's loads are in flight while the
+//                      current one is consumed.
 //   bsr_spmm_bf16_mfma b == 128, bf16 in, fp32 accumulation, fp32/bf16 out
 //                      (v_mfma_f32_32x32x16_bf16, B slabs transposed in LDS).
 //   bsr_spmm_generic   any block size / dtype (f32, f64, bf16): one thread per
 //                      output element, a plain dot product over stored blocks.
 //
-// Scheduling: the grid is mapped XCD-aware. Consecutive workgroup ids go
-// round-robin over the 8 XCDs, so item (row rank k, column tile t) is placed
-// on XCD k%8 with the column tiles of one block row in consecutive slots of
-// that XCD: the tiles sharing an A block run side by side on one L2. Rows are
-// visited heaviest first (tsp_bsr_row_order), so the hardware dispatcher acts
-// as a longest-processing-time list scheduler within each XCD.
+// Scheduling: rows are ranked heaviest first (tsp_bsr_row_order) and dealt
+// to the 8 XCDs in boustrophedon order; the column tiles of one block row sit
+// in consecutive slots of one XCD, so the tiles sharing an A block run side
+// by side on one L2 (mfma_f32.h, tile_item). With one workgroup per CU the
+// in-order hardware dispatcher is then a longest-processing-time list
+// scheduler within each XCD.
 #include "common.h"
 
 #include "mfma_f32.h"
@@ -35,26 +36,27 @@
 namespace {
 
 namespace T32 = tsp::f32tile;
-constexpr int BS = 128;  // block size served by the MFMA kernel
+constexpr int BS = 128;  // block size served by the MFMA kernels
+constexpr int KC = 64;   // fp32 k-slab (two slabs per stored block)
 
-// Slab source of one (block row, column tile) item: slab s is k-slab s%4 of
-// the (s/4)-th stored block of the row; B rows come straight from the
+// Slab source of one (block row, column tile) item: slab s is k-slab s%2 of
+// the (s/2)-th stored block of the row; B rows come straight from the
 // row-panel of that block's column (no gathered copy of B).
 struct BsrSlabs {
   const float* __restrict__ blocks;
   const int64_t* __restrict__ ci;
   const float* __restrict__ B;
   int64_t start, n, ncols, ldb, n0;
-  T32::Coords q;
-  __device__ void load(int s, f32x4& a0, f32x4& a1, f32x4& b0, f32x4& b1) const {
-    const int64_t idx = start + (s >> 2);
-    const int kk = (s & 3) * T32::KC;
-    const float* a = blocks + idx * (BS * BS) + kk;
-    a0 = *(const f32x4*)(a + q.ar * BS + q.ac);
-    a1 = *(const f32x4*)(a + (q.ar + 64) * BS + q.ac);
+  T32::Coords<KC> q;
+  __device__ void load(int s, f32x4 (&a)[T32::Slab<KC>::NA], f32x4 (&b)[T32::Slab<KC>::NB]) const {
+    const int64_t idx = start + s / (BS / KC);
+    const int kk = (s % (BS / KC)) * KC;
+    const float* ab = blocks + idx * (BS * BS) + kk + q.ac;
+#pragma unroll
+    for (int i = 0; i < T32::Slab<KC>::NA; ++i) a[i] = *(const f32x4*)(ab + (q.ar + i * q.astep) * BS);
     const int64_t brow = ci[idx] * BS + kk + q.br;
-    b0 = T32::load4_guard(B, brow, n0 + q.bc, n, ncols, ldb);
-    b1 = T32::load4_guard(B, brow + 16, n0 + q.bc, n, ncols, ldb);
+#pragma unroll
+    for (int i = 0; i < T32::Slab<KC>::NB; ++i) b[i] = T32::load4_guard(B, brow + 16 * i, n0 + q.bc, n, ncols, ldb);
   }
 };
 
@@ -70,15 +72,10 @@ __global__ __launch_bounds__(T32::NTHR) void bsr_spmm_f32_mfma(
     const float* __restrict__ blocks, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci,
     int64_t mb, int nt, int64_t m, int64_t n, const float* __restrict__ B, int64_t ldb,
     int64_t ncols, OutT* __restrict__ C, int64_t ldc, const int32_t* __restrict__ order) {
-  __shared__ __attribute__((aligned(16))) float lds[T32::LDS_FLOATS];
-
-  // ---- work item (XCD-aware, heaviest rows first)
-  const int g = blockIdx.x;
-  const int xcd = g & 7, slot = g >> 3;
-  const int64_t k = (int64_t)(slot / nt) * 8 + xcd;
-  if (k >= mb) return;
-  const int ntile = slot % nt;
-  const int64_t row = order ? (int64_t)order[k] : k;
+  __shared__ __attribute__((aligned(16))) float lds[T32::Slab<KC>::LDS_FLOATS];
+  int64_t row;
+  int ntile;
+  if (!T32::tile_item(blockIdx.x, mb, nt, order, row, ntile)) return;
 
   BsrSlabs src;
   src.blocks = blocks;
@@ -89,10 +86,10 @@ __global__ __launch_bounds__(T32::NTHR) void bsr_spmm_f32_mfma(
   src.ncols = ncols;
   src.ldb = ldb;
   src.n0 = (int64_t)ntile * T32::BN;
-  const int nsteps = (int)(rp[row + 1] - src.start) * (BS / T32::KC);
+  const int nsteps = (int)(rp[row + 1] - src.start) * (BS / KC);
 
   f32x16 acc0 = {}, acc1 = {};
-  T32::run(src, nsteps, lds, src.q, acc0, acc1);
+  T32::run<KC>(src, nsteps, lds, src.q, acc0, acc1);
   T32::store_tile(C, ldc, row * BS, src.n0, m, ncols, src.q, acc0, acc1, cvt_out<OutT>);
 }
 
@@ -119,12 +116,9 @@ __global__ __launch_bounds__(512) void bsr_spmm_bf16_mfma(
   typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * bf::STAGE];
 
-  const int g = blockIdx.x;
-  const int xcd = g & 7, slot = g >> 3;
-  const int64_t k = (int64_t)(slot / nt) * 8 + xcd;
-  if (k >= mb) return;
-  const int ntile = slot % nt;
-  const int64_t row = order ? (int64_t)order[k] : k;
+  int64_t row;
+  int ntile;
+  if (!T32::tile_item(blockIdx.x, mb, nt, order, row, ntile)) return;
   const int64_t n0 = (int64_t)ntile * 128;
   const int64_t start = rp[row];
   const int nsteps = (int)(rp[row + 1] - start) * (BS / bf::KC);
@@ -206,7 +200,7 @@ __global__ __launch_bounds__(512) void bsr_spmm_bf16_mfma(
       __syncthreads();
     }
   }
-  T32::Coords q;
+  T32::Coords<64> q;
   T32::store_tile(C, ldc, row * BS, n0, m, ncols, q, acc0, acc1, cvt_out<OutT>);
 }
 

@@ -1,13 +1,15 @@
 // fp32 MFMA tile core shared by the BSR SpMM and screened SpMM kernels.
 //
 // One 512-thread workgroup (8 wavefronts, 4(M) x 2(N)) accumulates a 128x128
-// fp32 tile of C over a sequence of 32-wide k-slabs. The caller supplies the
-// slab source: `src.load(s, a0, a1, b0, b1)` fetches slab s from global
-// memory into registers (A rows ar and ar+64, four k values at column ac; B
-// rows br and br+16, four n values at column bc — see the staging coordinates
-// below). Slabs pass through a double-buffered LDS ring: the loads of slab
-// s+1 are in flight while slab s feeds v_mfma_f32_32x32x2_f32; one barrier
-// per slab.
+// fp32 tile of C over a sequence of KC-wide k-slabs (KC = 32 or 64). The
+// caller supplies the slab source: `src.load(s, a, b)` fetches slab s from
+// global memory into registers — NA float4 of A (rows q.ar + i*q.astep, four
+// k values at column q.ac) and NB float4 of B (rows q.br + 16*i, four n
+// values at column q.bc). Slabs pass through a double-buffered LDS ring: the
+// loads of slab s+1 are in flight while slab s feeds v_mfma_f32_32x32x2_f32;
+// one barrier per slab. With KC = 64 the ring takes 137 KiB of LDS, so one
+// workgroup owns a CU and the hardware dispatcher schedules the grid in
+// order (longest-first lists stay longest-first).
 #pragma once
 
 #include "common.h"
@@ -17,23 +19,31 @@ namespace f32tile {
 
 constexpr int BM = 128;          // tile rows
 constexpr int BN = 128;          // tile columns
-constexpr int KC = 32;           // k-slab
 constexpr int NTHR = 512;        // 8 wavefronts
-constexpr int A_LD = KC + 4;     // LDS row stride (floats) of the A slab [m][k]
 constexpr int B_LD = BN + 4;     // LDS row stride (floats) of the B slab [k][n]
-constexpr int A_SLAB = BM * A_LD;
-constexpr int B_SLAB = KC * B_LD;
-constexpr int STAGE = A_SLAB + B_SLAB;
-constexpr int LDS_FLOATS = 2 * STAGE;
 
+// Geometry of a KC-wide k-slab.
+template <int KC>
+struct Slab {
+  static constexpr int A_LD = KC + 4;       // LDS row stride (floats) of the A slab [m][k]
+  static constexpr int A_SLAB = BM * A_LD;
+  static constexpr int B_SLAB = KC * B_LD;
+  static constexpr int STAGE = A_SLAB + B_SLAB;
+  static constexpr int LDS_FLOATS = 2 * STAGE;
+  static constexpr int NA = KC / 16;        // float4 of A per thread per slab
+  static constexpr int NB = KC / 16;        // float4 of B per thread per slab
+};
+
+template <int KC>
 struct Coords {
-  int ar, ac;  // A staging: rows ar, ar+64; k columns ac..ac+3
-  int br, bc;  // B staging: rows br, br+16; n columns bc..bc+3
+  int ar, ac, astep;  // A staging: rows ar + i*astep, k columns ac..ac+3
+  int br, bc;         // B staging: rows br + 16*i, n columns bc..bc+3
   int wm, wn, h, l32;
   __device__ Coords() {
     const int tid = threadIdx.x;
-    ar = tid >> 3;
-    ac = (tid & 7) * 4;
+    ar = tid / (KC / 4);
+    ac = (tid % (KC / 4)) * 4;
+    astep = NTHR / (KC / 4);
     br = tid >> 5;
     bc = (tid & 31) * 4;
     const int lane = tid & 63, w = tid >> 6;
@@ -45,26 +55,27 @@ struct Coords {
 };
 
 // Accumulate `nsteps` slabs into acc0 (columns wn*64 + l32) and acc1 (+32).
-template <class Src>
-__device__ inline void run(Src& src, int nsteps, float* lds, const Coords& q, f32x16& acc0, f32x16& acc1) {
-  f32x4 ra0, ra1, rb0, rb1;
+template <int KC, class Src>
+__device__ inline void run(Src& src, int nsteps, float* lds, const Coords<KC>& q, f32x16& acc0, f32x16& acc1) {
+  typedef Slab<KC> G;
+  f32x4 ra[G::NA], rb[G::NB];
   auto lstore = [&](float* st) {
     float* As = st;
-    float* Bs = st + A_SLAB;
-    *(f32x4*)(As + q.ar * A_LD + q.ac) = ra0;
-    *(f32x4*)(As + (q.ar + 64) * A_LD + q.ac) = ra1;
-    *(f32x4*)(Bs + q.br * B_LD + q.bc) = rb0;
-    *(f32x4*)(Bs + (q.br + 16) * B_LD + q.bc) = rb1;
+    float* Bs = st + G::A_SLAB;
+#pragma unroll
+    for (int i = 0; i < G::NA; ++i) *(f32x4*)(As + (q.ar + i * q.astep) * G::A_LD + q.ac) = ra[i];
+#pragma unroll
+    for (int i = 0; i < G::NB; ++i) *(f32x4*)(Bs + (q.br + 16 * i) * B_LD + q.bc) = rb[i];
   };
   // MFMA k-step s of a group of 8 k values uses k = k0 + s (lanes 0-31) and
   // k = k0 + 4 + s (lanes 32-63): a lane's 4 A values are one 16-byte LDS
   // load. A and B follow the same k order, so the sum is unchanged.
   auto compute = [&](const float* st) {
     const float* As = st;
-    const float* Bs = st + A_SLAB;
+    const float* Bs = st + G::A_SLAB;
 #pragma unroll
     for (int k0 = 0; k0 < KC; k0 += 8) {
-      const f32x4 a = *(const f32x4*)(As + (q.wm * 32 + q.l32) * A_LD + k0 + 4 * q.h);
+      const f32x4 a = *(const f32x4*)(As + (q.wm * 32 + q.l32) * G::A_LD + k0 + 4 * q.h);
       const float* bp = Bs + (k0 + 4 * q.h) * B_LD + q.wn * 64 + q.l32;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -76,14 +87,14 @@ __device__ inline void run(Src& src, int nsteps, float* lds, const Coords& q, f3
     }
   };
   if (nsteps <= 0) return;
-  src.load(0, ra0, ra1, rb0, rb1);
+  src.load(0, ra, rb);
   lstore(lds);
   __syncthreads();
   for (int s = 0; s < nsteps; ++s) {
-    const float* cur = lds + (s & 1) * STAGE;
-    float* nxt = lds + ((s + 1) & 1) * STAGE;
+    const float* cur = lds + (s & 1) * G::STAGE;
+    float* nxt = lds + ((s + 1) & 1) * G::STAGE;
     const bool more = s + 1 < nsteps;
-    if (more) src.load(s + 1, ra0, ra1, rb0, rb1);
+    if (more) src.load(s + 1, ra, rb);
     compute(cur);
     if (more) lstore(nxt);
     __syncthreads();
@@ -112,9 +123,10 @@ __device__ inline f32x4 load4_guard(const float* __restrict__ p0, int64_t r, int
 // Store the tile (accumulator layout: lane holds column l32 and rows
 // 8*(v/4) + 4*h + v%4, v = 0..15) to C rows [row0, row0+128) clipped to m,
 // columns [col0, col0+128) clipped to ncols.
-template <typename OutT, typename Cvt>
+template <typename OutT, typename Cvt, int KC>
 __device__ inline void store_tile(OutT* __restrict__ C, int64_t ldc, int64_t row0, int64_t col0, int64_t m,
-                                  int64_t ncols, const Coords& q, const f32x16& acc0, const f32x16& acc1, Cvt cvt) {
+                                  int64_t ncols, const Coords<KC>& q, const f32x16& acc0, const f32x16& acc1,
+                                  Cvt cvt) {
   const int64_t rbase = row0 + q.wm * 32 + 4 * q.h;
   const int64_t c0 = col0 + q.wn * 64 + q.l32;
 #pragma unroll
@@ -126,6 +138,24 @@ __device__ inline void store_tile(OutT* __restrict__ C, int64_t ldc, int64_t row
       if (c0 + 32 < ncols) crow[c0 + 32] = cvt(acc1[v]);
     }
   }
+}
+
+// Work item of a tiled launch over `mb` row tiles (ranked heaviest first by
+// `order`, or in natural order when it is null) and `nt` column tiles.
+// Consecutive workgroup ids go round-robin over the 8 XCDs: ranks are dealt
+// to XCDs in boustrophedon order (0..7, 15..8, 16..23, ...) so every XCD
+// gets an equal share of heavy and light rows, and the column tiles of one
+// row sit in consecutive slots of one XCD (they share its L2 for the A row
+// panel). Returns false for padding slots.
+__device__ inline bool tile_item(int64_t g, int64_t mb, int64_t nt, const int32_t* __restrict__ order,
+                                 int64_t& row, int& ntile) {
+  const int64_t xcd = g & 7, slot = g >> 3;
+  const int64_t rl = slot / nt;
+  ntile = (int)(slot - rl * nt);
+  const int64_t k = (rl & 1) ? 8 * rl + 7 - xcd : 8 * rl + xcd;
+  if (k >= mb) return false;
+  row = order ? (int64_t)order[k] : k;
+  return true;
 }
 
 }  // namespace f32tile

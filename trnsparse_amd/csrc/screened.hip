@@ -27,6 +27,7 @@ namespace {
 
 namespace T32 = tsp::f32tile;
 constexpr int TILE = 128;
+constexpr int KC = 64;
 
 template <typename QT>
 __device__ inline QT qsqrt(QT v);
@@ -63,10 +64,10 @@ struct ScreenedSlabs {
   const QT* __restrict__ Q;
   const QT* __restrict__ qmax;
   int64_t lda, ldb, m, ncols, row0, n0;
-  QT thr, qI, qa0, qa1;
+  QT thr, qI;
   int nkt;
   int kt;  // k tile of the current slab group (advanced as slabs are requested in order)
-  T32::Coords q;
+  T32::Coords<KC> q;
 
   __device__ bool active(int t) const { return qI * qmax[t] > thr; }
   __device__ int count() const {
@@ -74,24 +75,28 @@ struct ScreenedSlabs {
     for (int t = 0; t < nkt; ++t) c += active(t) ? 1 : 0;
     return c;
   }
-  __device__ void load(int s, f32x4& a0, f32x4& a1, f32x4& b0, f32x4& b1) {
-    if ((s & 3) == 0) {
+  __device__ void load(int s, f32x4 (&a)[T32::Slab<KC>::NA], f32x4 (&b)[T32::Slab<KC>::NB]) {
+    constexpr int PER = TILE / KC;  // slabs per k tile
+    if ((s % PER) == 0) {
       ++kt;
       while (!active(kt)) ++kt;
     }
-    const int kk = (s & 3) * T32::KC;
+    const int kk = (s % PER) * KC;
     const int64_t kc = (int64_t)kt * TILE + kk + q.ac;
-    a0 = T32::load4_guard(A, row0 + q.ar, kc, m, m, lda);
-    a1 = T32::load4_guard(A, row0 + q.ar + 64, kc, m, m, lda);
+    QT qk[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const QT qk = kc + i < m ? Q[kc + i] : (QT)0;
-      a0[i] *= (qa0 * qk > thr) ? 1.0f : 0.0f;
-      a1[i] *= (qa1 * qk > thr) ? 1.0f : 0.0f;
+    for (int i = 0; i < 4; ++i) qk[i] = kc + i < m ? Q[kc + i] : (QT)0;
+#pragma unroll
+    for (int j = 0; j < T32::Slab<KC>::NA; ++j) {
+      const int64_t r = row0 + q.ar + j * q.astep;
+      a[j] = T32::load4_guard(A, r, kc, m, m, lda);
+      const QT qa = r < m ? Q[r] : (QT)0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[j][i] *= (qa * qk[i] > thr) ? 1.0f : 0.0f;
     }
     const int64_t brow = (int64_t)kt * TILE + kk + q.br;
-    b0 = T32::load4_guard(B, brow, n0 + q.bc, m, ncols, ldb);
-    b1 = T32::load4_guard(B, brow + 16, n0 + q.bc, m, ncols, ldb);
+#pragma unroll
+    for (int j = 0; j < T32::Slab<KC>::NB; ++j) b[j] = T32::load4_guard(B, brow + 16 * j, n0 + q.bc, m, ncols, ldb);
   }
 };
 
@@ -100,13 +105,12 @@ __global__ __launch_bounds__(T32::NTHR) void screened_f32_mfma(
     const float* __restrict__ A, int64_t lda, const QT* __restrict__ Q, const QT* __restrict__ qmax, QT thr,
     int64_t m, const float* __restrict__ B, int64_t ldb, int64_t ncols, float* __restrict__ C, int64_t ldc, int nmt,
     int nnt) {
-  __shared__ __attribute__((aligned(16))) float lds[T32::LDS_FLOATS];
+  __shared__ __attribute__((aligned(16))) float lds[T32::Slab<KC>::LDS_FLOATS];
   // XCD-aware: the column tiles of one row panel of A share an XCD (and its L2).
-  const int g = blockIdx.x;
-  const int xcd = g & 7, slot = g >> 3;
-  const int mt = (slot / nnt) * 8 + xcd;
-  if (mt >= nmt) return;
-  const int nt = slot % nnt;
+  int64_t mt64;
+  int nt;
+  if (!T32::tile_item(blockIdx.x, nmt, nnt, nullptr, mt64, nt)) return;
+  const int mt = (int)mt64;
 
   ScreenedSlabs<QT> src;
   src.A = A;
@@ -123,12 +127,10 @@ __global__ __launch_bounds__(T32::NTHR) void screened_f32_mfma(
   src.qI = qmax[mt];
   src.nkt = (int)tsp::ceil_div(m, TILE);
   src.kt = -1;
-  src.qa0 = src.row0 + src.q.ar < m ? Q[src.row0 + src.q.ar] : (QT)0;
-  src.qa1 = src.row0 + src.q.ar + 64 < m ? Q[src.row0 + src.q.ar + 64] : (QT)0;
-  const int nsteps = src.count() * (TILE / T32::KC);
+  const int nsteps = src.count() * (TILE / KC);
 
   f32x16 acc0 = {}, acc1 = {};
-  T32::run(src, nsteps, lds, src.q, acc0, acc1);
+  T32::run<KC>(src, nsteps, lds, src.q, acc0, acc1);
   T32::store_tile(C, ldc, src.row0, src.n0, m, ncols, src.q, acc0, acc1, [](float v) { return v; });
 }
 

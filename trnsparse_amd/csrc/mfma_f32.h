@@ -5,11 +5,15 @@
 // caller supplies the slab source: `src.load(s, a, b)` fetches slab s from
 // global memory into registers — NA float4 of A (rows q.ar + i*q.astep, four
 // k values at column q.ac) and NB float4 of B (rows q.br + 16*i, four n
-// values at column q.bc). Slabs pass through a double-buffered LDS ring: the
-// loads of slab s+1 are in flight while slab s feeds v_mfma_f32_32x32x2_f32;
-// one barrier per slab. With KC = 64 the ring takes 137 KiB of LDS, so one
-// workgroup owns a CU and the hardware dispatcher schedules the grid in
-// order (longest-first lists stay longest-first).
+// values at column q.bc). Slabs pass through a double-buffered LDS ring fed
+// from registers: slab s+1 is written to LDS halfway through slab s's
+// v_mfma_f32_32x32x2_f32 work and the loads of slab s+2 are issued right
+// after, so LDS writes overlap MFMAs and every load has a slab of time to
+// land; within a slab the LDS operands of the next 8-k group are read while
+// the current group's MFMAs run. One barrier per slab. With KC = 64 the ring
+// takes 137 KiB of LDS, so one workgroup owns a CU and the hardware
+// dispatcher schedules the grid in order (longest-first lists stay
+// longest-first).
 #pragma once
 
 #include "common.h"
@@ -69,34 +73,64 @@ __device__ inline void run(Src& src, int nsteps, float* lds, const Coords<KC>& q
   };
   // MFMA k-step s of a group of 8 k values uses k = k0 + s (lanes 0-31) and
   // k = k0 + 4 + s (lanes 32-63): a lane's 4 A values are one 16-byte LDS
-  // load. A and B follow the same k order, so the sum is unchanged.
-  auto compute = [&](const float* st) {
+  // load. A and B follow the same k order, so the sum is unchanged. The
+  // operands of group g+1 are read from LDS while group g's 8 MFMAs run
+  // (register double buffering), so LDS latency stays off the MFMA pipe.
+  struct Ops {
+    f32x4 a;
+    float b0[4], b1[4];
+  };
+  auto fetch = [&](const float* st, int k0, Ops& o) {
     const float* As = st;
     const float* Bs = st + G::A_SLAB;
+    o.a = *(const f32x4*)(As + (q.wm * 32 + q.l32) * G::A_LD + k0 + 4 * q.h);
+    const float* bp = Bs + (k0 + 4 * q.h) * B_LD + q.wn * 64 + q.l32;
 #pragma unroll
-    for (int k0 = 0; k0 < KC; k0 += 8) {
-      const f32x4 a = *(const f32x4*)(As + (q.wm * 32 + q.l32) * G::A_LD + k0 + 4 * q.h);
-      const float* bp = Bs + (k0 + 4 * q.h) * B_LD + q.wn * 64 + q.l32;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const float b0 = bp[s * B_LD];
-        const float b1 = bp[s * B_LD + 32];
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b0, acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b1, acc1, 0, 0, 0);
-      }
+    for (int s = 0; s < 4; ++s) {
+      o.b0[s] = bp[s * B_LD];
+      o.b1[s] = bp[s * B_LD + 32];
     }
   };
+  auto mma = [&](const Ops& o) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(o.a[s], o.b0[s], acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(o.a[s], o.b1[s], acc1, 0, 0, 0);
+    }
+  };
+  // Groups [g0, g1) of one slab; operands of the next group are read while
+  // the current group's MFMAs run.
+  auto compute = [&](const float* st, int g0, int g1) {
+    Ops o[2];
+    fetch(st, 8 * g0, o[0]);
+#pragma unroll
+    for (int g = g0; g < g1; ++g) {
+      if (g + 1 < g1) fetch(st, 8 * (g + 1), o[(g + 1 - g0) & 1]);
+      // keep the scheduler from sinking the reads next to their MFMAs
+      __builtin_amdgcn_sched_barrier(0);
+      mma(o[(g - g0) & 1]);
+    }
+  };
+  // Pipeline: slab s+1 sits in registers (its global loads were issued half
+  // a slab into s-1) and is written to the other LDS buffer halfway through
+  // slab s's MFMAs, right before the loads of slab s+2 are issued. The LDS
+  // writes thus overlap MFMA work and each load has a full slab of time to
+  // arrive; one barrier per slab.
   if (nsteps <= 0) return;
+  constexpr int NG = KC / 8;
   src.load(0, ra, rb);
   lstore(lds);
+  if (nsteps > 1) src.load(1, ra, rb);
   __syncthreads();
   for (int s = 0; s < nsteps; ++s) {
     const float* cur = lds + (s & 1) * G::STAGE;
     float* nxt = lds + ((s + 1) & 1) * G::STAGE;
-    const bool more = s + 1 < nsteps;
-    if (more) src.load(s + 1, ra, rb);
-    compute(cur);
-    if (more) lstore(nxt);
+    compute(cur, 0, NG / 2);
+    if (s + 1 < nsteps) {
+      lstore(nxt);
+      if (s + 2 < nsteps) src.load(s + 2, ra, rb);
+    }
+    compute(cur, NG / 2, NG);
     __syncthreads();
   }
 }

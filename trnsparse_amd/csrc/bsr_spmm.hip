@@ -19,7 +19,9 @@
 //                      CU); the next slab's loads are in flight while the
 //                      current one is consumed.
 //   bsr_spmm_bf16_mfma b == 128, bf16 in, fp32 accumulation, fp32/bf16 out
-//                      (v_mfma_f32_32x32x16_bf16, B slabs transposed in LDS).
+//                      (v_mfma_f32_32x32x16_bf16, 64x32 wave tiles,
+//                      direct-to-LDS 4-deep ring, B operand through LDS
+//                      transpose reads).
 //   bsr_spmm_generic   any block size / dtype (f32, f64, bf16): one thread per
 //                      output element, a plain dot product over stored blocks.
 //
@@ -96,16 +98,70 @@ __global__ __launch_bounds__(T32::NTHR) void bsr_spmm_f32_mfma(
 // ---------------------------------------------------------------- bf16 MFMA
 //
 // bsr_spmm_bf16_mfma: b == 128, bf16 operands, fp32 accumulation, fp32 or
-// bf16 output. Same tile (128x128 of C per workgroup, 8 waves of 32x64) and
-// scheduling as the fp32 kernel, with v_mfma_f32_32x32x16_bf16 on 64-wide
-// k-slabs. Both MFMA operands need 8 consecutive k per lane: A blocks are
-// [m][k] already; B panels are [k][n], so each B slab is transposed while
-// staged (4 k x 8 n register patches written as 8-byte rows of Bt[n][k]).
+// bf16 output. Same tile (128x128 of C per workgroup) and scheduling as the
+// fp32 kernel, with v_mfma_f32_32x32x16_bf16 on 64-wide k-slabs; the 8 waves
+// form a 2(M) x 4(N) grid of 64x32 wave tiles. A bf16 slab is only ~512 MFMA
+// cycles per SIMD, far shorter than a memory round trip, so slabs stream
+// through a 4-deep LDS ring filled by direct global->LDS loads (no register
+// staging), issued 3 slabs ahead:
+//   A: global_load_lds_dwordx4 of the block (always in bounds);
+//   B: buffer_load_dwordx4 ... lds with a buffer resource over B, so rows
+//      past n read as zero (columns past ncols only feed output columns that
+//      are not stored).
+// B stays [k][n] in LDS and the MFMA B operand (8 consecutive k per lane) is
+// read with ds_read_b64_tr_b16: in each 16-lane group, lane i receives
+// element i%4 of the 8-byte pieces given by lanes 4t + i/4, t = 0..3, i.e.
+// column n_base + i of four consecutive k rows when lane j points at row
+// k0 + j/4, columns n_base + 4(j%4).
+// LDS budget (gfx950: 64 banks of 4 bytes; b128 reads ~256 B/clk per CU,
+// transpose reads half that): 16-byte chunks are XOR-swizzled so both read
+// kinds are conflict-free — A rows of 128 B: chunk ^ ((row/2) % 8), so 16
+// consecutive rows cover all 64 banks; B rows of 256 B: chunk ^ 4*(row % 4),
+// so the four k rows of one transpose read land on distinct banks. The
+// 64x32 wave tile puts the larger share of operand bytes on the fast b128
+// path (2 KB of A, 1 KB of B per 16-k step and two MFMAs).
 namespace bf {
 constexpr int KC = 64;
-constexpr int LD = KC + 8;            // LDS row stride (bf16) of As[m][k] and Bt[n][k]
-constexpr int A_ELEMS = 128 * LD;
-constexpr int STAGE = 2 * A_ELEMS;    // As + Bt
+constexpr int NST = 4;                     // LDS ring depth
+constexpr int A_BYTES = 128 * KC * 2;      // 16 KiB, rows of 128 B
+constexpr int B_BYTES = KC * 128 * 2;      // 16 KiB, rows of 256 B
+constexpr int STAGE = A_BYTES + B_BYTES;   // 32 KiB
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// The direct-to-LDS loads are issued from inline asm so that the compiler
+// does not track them: it cannot tell the ring stages apart and would
+// otherwise wait for every outstanding load before each LDS read. Their
+// completion is waited for explicitly (vmcnt) before the slab barrier.
+// M0 holds the wave's LDS destination; lane l writes 16 bytes at M0 + 16 l.
+__device__ inline void dma_global16(const void* g, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
+               "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory", "m0");
+}
+// Buffer form: out-of-range offsets (>= num_records) read as zero.
+__device__ inline void dma_buffer16(i32x4 rsrc, int voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc),
+               "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory", "m0");
+}
+// Low 32 bits of *p, waited for in place (all earlier loads included): the
+// compiler does not see this load either, so it never adds a wait for it
+// on the slab path.
+__device__ inline int load_lo32_sync(const void* p) {
+  int v;
+  asm volatile("global_load_dword %0, %1, off\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+// s_waitcnt immediate waiting for vmcnt <= N only (gfx9 encoding)
+template <int N>
+__device__ inline void wait_vm() {
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (((N >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8));
+}
+// Workgroup barrier without the fence of __syncthreads (which would wait for
+// all outstanding loads); the memory clobber keeps LDS reads on their side.
+__device__ inline void barrier() { asm volatile("s_barrier" ::: "memory"); }
 }  // namespace bf
 
 template <typename OutT>
@@ -113,95 +169,131 @@ __global__ __launch_bounds__(512) void bsr_spmm_bf16_mfma(
     const uint16_t* __restrict__ blocks, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci,
     int64_t mb, int nt, int64_t m, int64_t n, const uint16_t* __restrict__ B, int64_t ldb, int64_t ncols,
     OutT* __restrict__ C, int64_t ldc, const int32_t* __restrict__ order) {
-  typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * bf::STAGE];
-
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[bf::NST * bf::STAGE];
   int64_t row;
   int ntile;
   if (!T32::tile_item(blockIdx.x, mb, nt, order, row, ntile)) return;
   const int64_t n0 = (int64_t)ntile * 128;
   const int64_t start = rp[row];
-  const int nsteps = (int)(rp[row + 1] - start) * (BS / bf::KC);
+  const int nblk = (int)(rp[row + 1] - start);
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int wm = w & 3, wn = w >> 2, h = lane >> 5, l32 = lane & 31;
-  // staging: A slab 128 x 64 -> 2 chunks of 8 per thread; B slab 64 x 128 as
-  // 4k x 8n patches -> 256 patches, threads 0..255 one each
-  const int ar = tid >> 3, ac = (tid & 7) * 8;       // rows ar, ar+64
-  const int pk = (tid & 15) * 4, pn = (tid >> 4) * 8;  // patch (k 4, n 8), valid for tid < 256
-  const bool bstage = tid < 256;
+  const int wm = w & 1, wn = w >> 1, h = lane >> 5, l32 = lane & 31;
+  // buffer resource over B: base, stride 0, num_records = B's bytes, raw buffer
+  const uint64_t bbase = (uint64_t)(uintptr_t)B;
+  const bf::i32x4 brsrc = {(int)(uint32_t)bbase, (int)(uint32_t)(bbase >> 32) & 0xFFFF,
+                           (int)(uint32_t)(n * ldb * 2), 0x00020000};
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
 
-  u16x8 ra0, ra1, rb[4];
-  auto gload = [&](int s) {
-    const int64_t idx = start + (s >> 1);
+  // Column-block indices of the row, 64 at a time in one VGPR (lane i holds
+  // block cbase + i), read out with readlane: no scalar load (and its wait)
+  // on the slab path.
+  if (nblk <= 0) {
+    // empty block row: zero tile
+    f32x16 z = {};
+    T32::Coords<64> q;
+    T32::store_tile(C, ldc, row * BS, n0, m, ncols, q, z, z, cvt_out<OutT>);
+    return;
+  }
+  int cbase = 0;
+  auto load_cols = [&](int base) {
+    const int i = base + lane < nblk ? base + lane : nblk - 1;
+    return bf::load_lo32_sync(ci + start + i);
+  };
+  int cv = load_cols(0);
+  auto colblk = [&](int blk) {
+    if (blk - cbase >= 64) {
+      cbase = blk & ~63;
+      cv = load_cols(cbase);
+    }
+    return __builtin_amdgcn_readlane(cv, blk - cbase);
+  };
+
+  // ---- loads of slab s into ring stage s % NST: 2 A + 2 B wave instructions
+  auto issue = [&](int s) {
+    const int blk = s >> 1;
+    const int64_t idx = start + blk;
     const int kk = (s & 1) * bf::KC;
-    const uint16_t* a = blocks + idx * (BS * BS) + kk;
-    ra0 = *(const u16x8*)(a + ar * BS + ac);
-    ra1 = *(const u16x8*)(a + (ar + 64) * BS + ac);
-    if (bstage) {
-      const int64_t brow = ci[idx] * BS + kk + pk;
-      const int64_t c = n0 + pn;
+    const uint32_t st = lds0 + (s % bf::NST) * bf::STAGE;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        u16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (brow + j < n) {
-          const uint16_t* p = B + (brow + j) * ldb + c;
-          if (c + 7 < ncols) {
-            v = *(const u16x8*)p;
-          } else {
+    for (int q = 0; q < 2; ++q) {
+      const int i = 2 * w + q;                          // A rows [8i, 8i+8)
+      const int r = 8 * i + (lane >> 3);
+      const int c = (lane & 7) ^ ((r >> 1) & 7);        // logical chunk held at this lane's LDS slot
+      const uint16_t* g = blocks + idx * (BS * BS) + r * BS + kk + c * 8;
+      bf::dma_global16(g, st + i * 1024);
+    }
+    const int64_t brow0 = (int64_t)colblk(blk) * BS + kk;
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-              if (c + i < ncols) v[i] = p[i];
-          }
-        }
-        rb[j] = v;
-      }
+    for (int q = 0; q < 2; ++q) {
+      const int j = 2 * w + q;                          // B slab rows [4j, 4j+4)
+      const int rr = 4 * j + (lane >> 4);
+      const int c = (lane & 15) ^ (4 * (rr & 3));
+      const int64_t off = ((brow0 + rr) * ldb + n0 + c * 8) * 2;
+      bf::dma_buffer16(brsrc, (int)(uint32_t)off, st + bf::A_BYTES + j * 1024);
     }
   };
-  auto lstore = [&](uint16_t* st) {
-    uint16_t* As = st;
-    uint16_t* Bt = st + bf::A_ELEMS;
-    *(u16x8*)(As + ar * bf::LD + ac) = ra0;
-    *(u16x8*)(As + (ar + 64) * bf::LD + ac) = ra1;
-    if (bstage) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const u16x4 t = {rb[0][i], rb[1][i], rb[2][i], rb[3][i]};
-        *(u16x4*)(Bt + (pn + i) * bf::LD + pk) = t;
-      }
-    }
-  };
+
+  // ---- per-lane LDS read offsets (wave tile: rows wm*64 + [0,64), columns wn*32 + [0,32))
+  // A operand: rows am and am + 32 (same swizzle), logical chunk 2*ks + h
+  const int am = wm * 64 + l32;
+  const int asw = (am >> 1) & 7;
+  // B operand (tr reads): 16-lane group g = lane/16, lane j in group
+  const int gq = lane >> 4, jq = lane & 15;
+  const int bkq = 8 * (gq >> 1) + (jq >> 2);            // k row within the 16-k step (plus 4*kq)
+  const int ncol = wn * 32 + 16 * (gq & 1) + 4 * (jq & 3);
+  const int bsw = 4 * (jq >> 2);                        // 4 * (k row % 4)
 
   f32x16 acc0 = {}, acc1 = {};
-  auto compute = [&](const uint16_t* st) {
-    const uint16_t* As = st;
-    const uint16_t* Bt = st + bf::A_ELEMS;
+  auto compute = [&](const uint8_t* st) {
+    const uint8_t* As = st;
+    const uint8_t* Bs = st + bf::A_BYTES;
 #pragma unroll
     for (int ks = 0; ks < bf::KC / 16; ++ks) {
-      const bf16x8 a = *(const bf16x8*)(As + (wm * 32 + l32) * bf::LD + 16 * ks + 8 * h);
-      const bf16x8 b0 = *(const bf16x8*)(Bt + (wn * 64 + l32) * bf::LD + 16 * ks + 8 * h);
-      const bf16x8 b1 = *(const bf16x8*)(Bt + (wn * 64 + 32 + l32) * bf::LD + 16 * ks + 8 * h);
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b0, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b1, acc1, 0, 0, 0);
+      const int ca = ((2 * ks + h) ^ asw) * 16;
+      const bf16x8 a0 = *(const bf16x8*)(As + am * 128 + ca);
+      const bf16x8 a1 = *(const bf16x8*)(As + (am + 32) * 128 + ca);
+      bf::s16x4 v[2];
+#pragma unroll
+      for (int kq = 0; kq < 2; ++kq) {
+        const int rr = 16 * ks + bkq + 4 * kq;
+        const uint8_t* p = Bs + rr * 256 + (((ncol >> 3) ^ bsw) * 16) + (ncol & 4) * 2;
+        v[kq] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((bf::lds_s16x4*)(p));
+      }
+      // whole-vector reinterpretation: k = 4*kq + e (per-element bf16 casts
+      // of the i16 lanes are mis-packed by the compiler)
+      const bf16x8 bop = __builtin_bit_cast(bf16x8, __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7));
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, bop, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, bop, acc1, 0, 0, 0);
     }
   };
 
-  if (nsteps > 0) {
-    gload(0);
-    lstore(lds);
-    __syncthreads();
-    for (int s = 0; s < nsteps; ++s) {
-      const uint16_t* cur = lds + (s & 1) * bf::STAGE;
-      uint16_t* nxt = lds + ((s + 1) & 1) * bf::STAGE;
-      const bool more = s + 1 < nsteps;
-      if (more) gload(s + 1);
-      compute(cur);
-      if (more) lstore(nxt);
-      __syncthreads();
+  const int nsteps = nblk * (BS / bf::KC);
+  const int pre = nsteps < bf::NST - 1 ? nsteps : bf::NST - 1;
+  for (int s = 0; s < pre; ++s) issue(s);
+  for (int s = 0; s < nsteps; ++s) {
+    // this wave's loads of slab s are done when at most the later slabs' are in flight
+    if (s + 2 < nsteps)
+      bf::wait_vm<8>();
+    else if (s + 1 < nsteps)
+      bf::wait_vm<4>();
+    else
+      bf::wait_vm<0>();
+    bf::barrier();  // every wave's part of slab s is in LDS; stage (s-1)%NST is free
+    if (s + bf::NST - 1 < nsteps) issue(s + bf::NST - 1);
+    compute(lds + (s % bf::NST) * bf::STAGE);
+  }
+  // accumulator layout: lane holds column l32 and rows 8*(v/4) + 4*h + v%4
+  const int64_t r0 = row * BS + wm * 64 + 4 * h;
+  const int64_t c0 = n0 + wn * 32 + l32;
+  if (c0 < ncols) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
+      if (r < m) C[r * ldc + c0] = cvt_out<OutT>(acc0[v]);
+      if (r + 32 < m) C[(r + 32) * ldc + c0] = cvt_out<OutT>(acc1[v]);
     }
   }
-  T32::Coords<64> q;
-  T32::store_tile(C, ldc, row * BS, n0, m, ncols, q, acc0, acc1, cvt_out<OutT>);
 }
 
 template <typename T, typename OutT>
@@ -311,7 +403,8 @@ extern "C" int tsp_bsr_spmm(const void* blocks, int dtype, const int64_t* block_
     return tsp::check_launch("bsr_spmm_f32_mfma launch");
   }
   if (dtype == TSP_BF16 && block_size == BS && (ldb % 8) == 0 && ((uintptr_t)B % 16) == 0 &&
-      ((uintptr_t)blocks % 16) == 0) {
+      ((uintptr_t)blocks % 16) == 0 && (n + BS) * ldb * 2 + 2 * BS <= (int64_t)UINT32_MAX) {
+    // (the kernel's B offsets, rows < n + 128 and columns < ldb + 128, fit 32 bits)
     const int64_t nt = tsp::ceil_div(ncols, 128);
     const int64_t grid = tsp::ceil_div(mb, 8) * 8 * nt;
     if (grid > INT32_MAX || nt > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm: problem too large");

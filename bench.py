@@ -300,6 +300,35 @@ def bench_attention(steps: int, warmup: int, cpu: bool = False):
     return res
 
 
+def calibrate_gather():
+    """What the x gathers cost at cfg2. torch.index_select(x, 0, cols) with
+    cfg2's column indices (uniform over 1 M) and with sequential indices has
+    the same streaming traffic (16.8 M int64 indices read, 16.8 M fp32
+    written); only the gathers' locality differs. spmv is timed beside them.
+    Every launch is cold (L2 and MALL flushed)."""
+    import numpy as np
+    import torch
+
+    import trnsparse_amd as ts
+    from trnsparse_amd import workloads as W
+
+    v, c, p, x, shape = W.cfg2_csr(dist="poisson", index_dtype=np.int64)
+    m, n = shape
+    A = W.csr_matrix_from_arrays(v, c, p, shape, device="cuda")
+    xd = torch.from_numpy(x).cuda()
+    cols = torch.from_numpy(c).cuda()
+    seq = torch.arange(len(c), device="cuda", dtype=torch.int64) % n
+    flush = make_flush()
+    res = {"nnz": len(c), "n": n}
+    for name, fn in (("index_select_random_us", lambda: torch.index_select(xd, 0, cols)),
+                     ("index_select_sequential_us", lambda: torch.index_select(xd, 0, seq)),
+                     ("spmv_us", lambda: ts.spmv(A, xd))):
+        _, ms = time_gpu(fn, 15, 3, flush=flush)
+        res[name] = round(ms * 1e3, 2)
+    res["random_gather_penalty_us"] = round(res["index_select_random_us"] - res["index_select_sequential_us"], 2)
+    return res
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -309,6 +338,9 @@ def main(argv=None) -> int:
     ap.add_argument("--no-secondary", action="store_true", help="headline only")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device copy (known bytes) to calibrate PMC byte counters")
+    ap.add_argument("--calibrate-gather", action="store_true",
+                    help="run only the SpMV gather-floor calibration on cfg2 (torch index_select, random vs "
+                    "sequential indices, next to spmv)")
     args = ap.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -338,6 +370,9 @@ def main(argv=None) -> int:
         return 0
     _lib.load()
     ts.set_backend("hip")
+    if args.calibrate_gather:
+        print(json.dumps(calibrate_gather()), flush=True)
+        return 0
 
     head = bench_bsr_fp32(args.steps, args.warmup, cpu=not args.no_cpu)
     secondary = []

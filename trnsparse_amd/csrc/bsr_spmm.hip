@@ -120,9 +120,12 @@ __global__ __launch_bounds__(T32::NTHR) void bsr_spmm_f32_mfma(
 // so the four k rows of one transpose read land on distinct banks. The
 // 64x32 wave tile puts the larger share of operand bytes on the fast b128
 // path (2 KB of A, 1 KB of B per 16-k step and two MFMAs).
+#ifndef BF16_NST
+#define BF16_NST 4
+#endif
 namespace bf {
 constexpr int KC = 64;
-constexpr int NST = 4;                     // LDS ring depth
+constexpr int NST = BF16_NST;              // LDS ring depth
 constexpr int A_BYTES = 128 * KC * 2;      // 16 KiB, rows of 128 B
 constexpr int B_BYTES = KC * 128 * 2;      // 16 KiB, rows of 256 B
 constexpr int STAGE = A_BYTES + B_BYTES;   // 32 KiB
@@ -135,6 +138,9 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 // otherwise wait for every outstanding load before each LDS read. Their
 // completion is waited for explicitly (vmcnt) before the slab barrier.
 // M0 holds the wave's LDS destination; lane l writes 16 bytes at M0 + 16 l.
+// M0 is a reserved register, so its clobber is not tracked (hipcc warns);
+// nothing the compiler generates for this kernel reads M0 (checked in the
+// gfx950 assembly), so no value is lost across these statements.
 __device__ inline void dma_global16(const void* g, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
                "s"(__builtin_amdgcn_readfirstlane(lds_addr))
@@ -273,9 +279,13 @@ __global__ __launch_bounds__(512) void bsr_spmm_bf16_mfma(
   for (int s = 0; s < pre; ++s) issue(s);
   for (int s = 0; s < nsteps; ++s) {
     // this wave's loads of slab s are done when at most the later slabs' are in flight
-    if (s + 2 < nsteps)
+    // (4 loads per slab per wave; up to NST-2 later slabs may be in flight)
+    const int later = nsteps - 1 - s;
+    if (bf::NST >= 5 && later >= 3)
+      bf::wait_vm<12>();
+    else if (later >= 2)
       bf::wait_vm<8>();
-    else if (s + 1 < nsteps)
+    else if (later == 1)
       bf::wait_vm<4>();
     else
       bf::wait_vm<0>();

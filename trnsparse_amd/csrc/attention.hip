@@ -26,6 +26,7 @@
 //       thread per (query, 32-wide slice of head_dim), online softmax in
 //       the accumulation type (double for fp64).
 #include "common.h"
+#include "lds_dma.h"
 
 namespace {
 
@@ -275,6 +276,266 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_bf16_mfma(
   }
 }
 
+// ---------------------------------------------------------- bf16 MFMA, d=128
+//
+// bsa_fwd_bf16_d128: same work split and math as bsa_fwd_bf16_mfma (one
+// 256-thread workgroup per (head, 128-query block row), a wavefront per 32
+// queries, S^T = K Q^T with the wave's Q rows in registers, online softmax in
+// the exp2 domain, O^T += V^T P^T with P from registers), restructured so the
+// key blocks stream while the MFMAs run:
+//   * keys are consumed in 64-key halves that go through a 2-stage LDS ring
+//     (K half 16 KiB + V half 16 KiB per stage, 64 KiB per workgroup, two
+//     workgroups per CU), filled by direct global->LDS buffer loads issued one
+//     half ahead; rows at or past seq_len read as zero;
+//   * V stays [key][d] in LDS and the A operand of O^T += V^T P^T (8 keys of
+//     one d column per lane) comes from ds_read_b64_tr_b16;
+//   * 16-byte chunks are XOR-swizzled for conflict-free reads on the 64-bank
+//     LDS: K rows (b128 reads of 16 consecutive keys) chunk ^ (key % 16),
+//     V rows (transpose reads of 4 consecutive keys) chunk ^ 4*(key % 4);
+//   * each MFMA's LDS operand is read one step ahead.
+namespace att {
+constexpr int D = 128;
+constexpr int HK = 64;                 // keys per ring stage
+constexpr int ROWB = D * 2;            // bytes per K/V row
+constexpr int HBYTES = HK * ROWB;      // 16 KiB
+constexpr int STAGE = 2 * HBYTES;      // K half, then V half
+constexpr int NST = 2;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+}  // namespace att
+
+__global__ __launch_bounds__(256, 2) void bsa_fwd_bf16_d128(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int64_t S,
+    int64_t head_stride, int64_t H, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci, int64_t Mt,
+    float scale_log2, uint16_t* __restrict__ O, float* __restrict__ rmax, float* __restrict__ rden) {
+  using namespace att;
+  constexpr int KS = D / 16;  // k-steps of S^T = K Q^T
+  constexpr int NU = D / 32;  // 32-wide d subtiles of O^T
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
+
+  // XCD-aware order: XCD x walks heads x, x+8, ...; the block rows of one
+  // head run side by side and share that head's K/V in the XCD's L2.
+  const int64_t g = blockIdx.x;
+  const int64_t xcd = g & 7, slot = g >> 3;
+  const int64_t head = xcd + 8 * (slot / Mt);
+  const int64_t m = slot % Mt;
+  if (head >= H) return;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int gq = lane >> 4, jq = lane & 15;
+  const uint16_t* Qh = Q + head * head_stride;
+  const uint16_t* Kh = K + head * head_stride;
+  const uint16_t* Vh = V + head * head_stride;
+  const int64_t q = m * AB + w * 32 + l32;  // this lane's query (always < S: m < Mt)
+
+  // Q fragments for the B operand of S^T: Q[q][16s + 8h .. +7]
+  bf16x8 qf[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) qf[s] = *(const bf16x8*)(Qh + q * D + 16 * s + 8 * h);
+
+  f32x16 o[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) o[u] = f32x16{};
+  // mtrue: running max of the scaled scores (log2 domain); mref: the
+  // reference P and the sums are taken against (see the rescale below)
+  constexpr float RESCALE = 8.f;
+  float mtrue = -INFINITY, mref = -INFINITY, lrun = 0.f;
+
+  const int64_t start = rp[m];
+  const int nblk = (int)(rp[m + 1] - start);
+  const int nsteps = 2 * nblk;
+  const tsp::dma::i32x4 krs = tsp::dma::make_rsrc(Kh, (uint32_t)(S * D * 2));
+  const tsp::dma::i32x4 vrs = tsp::dma::make_rsrc(Vh, (uint32_t)(S * D * 2));
+  const uint32_t lds0 = tsp::dma::lds_addr(lds);
+
+  // key-block indices of the row, 64 at a time in one VGPR, read with readlane
+  int cbase = 0, cv = 0;
+  auto load_cols = [&](int base) {
+    const int i = base + lane < nblk ? base + lane : nblk - 1;
+    return tsp::dma::load_lo32_sync(ci + start + i);
+  };
+  if (nblk > 0) cv = load_cols(0);
+  auto colblk = [&](int blk) {
+    if (blk - cbase >= 64) {
+      cbase = blk & ~63;
+      cv = load_cols(cbase);
+    }
+    return __builtin_amdgcn_readlane(cv, blk - cbase);
+  };
+  auto first_key = [&](int s) { return (int64_t)colblk(s >> 1) * AB + HK * (s & 1); };
+
+  // ---- loads of half s into stage s % NST: 4 K + 4 V wave instructions
+  auto issue = [&](int s) {
+    const int64_t key0 = first_key(s);
+    const uint32_t st = lds0 + (s % NST) * STAGE;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const int j = 4 * w + qq;                 // rows [4j, 4j+4) of the half
+      const int rr = 4 * j + (lane >> 4);
+      const int p = lane & 15;                  // this lane's 16-byte slot in the row
+      const int64_t rowoff = (key0 + rr) * ROWB;
+      tsp::dma::buffer16(krs, (uint32_t)(rowoff + ((p ^ (rr & 15)) * 16)), st + j * 1024);
+      tsp::dma::buffer16(vrs, (uint32_t)(rowoff + ((p ^ (4 * (rr & 3))) * 16)), st + HBYTES + j * 1024);
+    }
+  };
+
+  // per-lane LDS offsets
+  // S^T A operand (K rows 32*tt + l32, d chunk 2*ks + h): chunk ^ (row % 16)
+  const int krow0 = l32, krow1 = 32 + l32;
+  // O^T A operand via transpose reads: lane j of 16-lane group gq points at
+  // key row kb + 8*r + 4*(gq>>1) + j/4 (r: which 4-key read), d column
+  // 32u + 16*(gq&1) + 4*(j%4); the swizzle term is 4*(j/4).
+  const int vrow = 4 * (gq >> 1) + (jq >> 2);
+  const int vsw = 4 * (jq >> 2);
+  const int vcol = 16 * (gq & 1) + 4 * (jq & 3);  // plus 32u
+
+  // per-lane byte offsets of the d chunk of K reads: chunk (2ks + h) ^ (row % 16)
+  // with row % 16 == l32 % 16 for both 32-key tiles
+  const int kx = (l32 & 15) ^ h;
+  // V transpose reads: byte offset within a row for d subtile u is
+  // ((4u + c0) ^ vsw) * 16 + (col & 4) * 2 = ((u ^ (vsw/4)) << 6) + c0 * 16 + ...
+  const int vlane = vrow * ROWB + ((vcol >> 3) & 3) * 16 + (vcol & 4) * 2;
+
+  auto compute = [&](const uint8_t* st, int64_t key0) {
+    const uint8_t* Ks = st + krow0 * ROWB;
+    const uint8_t* Vs = st + HBYTES + vlane;
+    auto kread = [&](int ks, int tile) {
+      return *(const bf16x8*)(Ks + tile * 32 * ROWB + (((2 * ks) ^ kx) * 16));
+    };
+    // ---- S^T tiles (keys 32*tt + 8*(v/4) + 4h + v%4, query l32): two
+    // independent accumulator chains, operands read one k-step ahead
+    f32x16 sc[2];
+    bf16x8 ka[2][2];
+    ka[0][0] = kread(0, 0);
+    ka[0][1] = kread(0, 1);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) {
+        ka[(ks + 1) & 1][0] = kread(ks + 1, 0);
+        ka[(ks + 1) & 1][1] = kread(ks + 1, 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks == 0) {
+        sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[0][0], qf[0], f32x16{}, 0, 0, 0);
+        sc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[0][1], qf[0], f32x16{}, 0, 0, 0);
+      } else {
+        sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[ks & 1][0], qf[ks], sc[0], 0, 0, 0);
+        sc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[ks & 1][1], qf[ks], sc[1], 0, 0, 0);
+      }
+    }
+    // ---- online softmax in the log2 domain (scale_log2 > 0, so the max of
+    // the raw scores scales to the max of the scaled ones); keys at or past
+    // seq_len (only in a block that crosses it) are excluded
+    if (key0 + HK > S) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          if (key0 + 32 * tt + 8 * (v >> 2) + 4 * h + (v & 3) >= S) sc[tt][v] = -INFINITY;
+    }
+    float mraw = sc[0][0];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) mraw = fmaxf(mraw, sc[tt][v]);
+    mraw = fmaxf(mraw, __shfl_xor(mraw, 32, 64));
+    mtrue = fmaxf(mtrue, mraw * scale_log2);
+    // Lazy rescaling: P is taken relative to a reference max mref that only
+    // moves when the true running max exceeds it by more than RESCALE (log2
+    // units), so P <= 2^RESCALE and o, l rarely need the multiply; o / l is
+    // the same quantity for any reference.
+    if (__builtin_amdgcn_ballot_w64(mtrue > mref + RESCALE) != 0) {
+      const bool move = mtrue > mref + RESCALE;
+      const float alpha = move ? (mref == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mref - mtrue)) : 1.f;
+      mref = move ? mtrue : mref;
+      lrun *= alpha;
+#pragma unroll
+      for (int u = 0; u < NU; ++u) o[u] *= alpha;
+    }
+    const float nmx = mref == -INFINITY ? 0.f : -mref;  // -inf scores give p = 0 either way
+    float lsum = 0.f;
+    bf16x8 pb[2][2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        typedef float f32x8 __attribute__((ext_vector_type(8)));
+        f32x8 pv;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tt][8 * a + i], scale_log2, nmx));
+          lsum += p;
+          pv[i] = p;
+        }
+        pb[tt][a] = __builtin_convertvector(pv, bf16x8);
+      }
+    }
+    lsum += __shfl_xor(lsum, 32, 64);
+    lrun += lsum;
+    // ---- O^T += V^T P^T. k-step (tt, a) covers keys 32tt + 16a + [0,16):
+    // MFMA k index i < 4 is key 32tt + 16a + 4h + i, i >= 4 is key
+    // 32tt + 16a + 8 + 4h + (i-4) — the lane's own S^T rows, so pb[tt][a]
+    // (values v = 8a .. 8a+7) is the matching B operand.
+    const int vx = vsw >> 2;
+    auto vread = [&](int tt, int a, int u) {
+      att::s16x4 r[2];
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const uint8_t* p = Vs + (32 * tt + 16 * a + 8 * rr) * ROWB + ((u ^ vx) << 6);
+        r[rr] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((att::lds_s16x4*)p);
+      }
+      return __builtin_bit_cast(bf16x8, __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    bf16x8 vb[2];
+    vb[0] = vread(0, 0, 0);
+#pragma unroll
+    for (int step = 0; step < 4 * NU; ++step) {
+      const int tt = step / (2 * NU), a = (step / NU) % 2, u = step % NU;
+      if (step + 1 < 4 * NU) {
+        const int s1 = step + 1;
+        vb[s1 & 1] = vread(s1 / (2 * NU), (s1 / NU) % 2, s1 % NU);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      o[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb[step & 1], pb[tt][a], o[u], 0, 0, 0);
+    }
+  };
+
+  if (nsteps > 0) issue(0);
+  for (int s = 0; s < nsteps; ++s) {
+    const int64_t key0 = first_key(s);
+    tsp::dma::wait_vm<0>();  // this wave's loads of half s are done
+    tsp::dma::barrier();     // every wave's part is in LDS; stage (s+1) % NST is free
+    if (s + 1 < nsteps) issue(s + 1);
+    compute(lds + (s % NST) * STAGE, key0);
+  }
+
+  // ---- epilogue: O[q][32u + 8*(v/4) + 4h + v%4] = o / l (both relative to
+  // mref); the returned denominator is relative to the true max
+  const bool empty = nblk == 0;
+  const float lref = lrun > 1e-12f ? lrun : 1e-12f;
+  const float inv = empty ? 0.f : 1.f / lref;
+  const float ltrue = mref == -INFINITY ? lrun : lrun * __builtin_amdgcn_exp2f(mref - mtrue);
+  const float den = ltrue > 1e-12f ? ltrue : 1e-12f;
+  uint16_t* Oq = O + head * head_stride + q * D;
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+      u16x4 t;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t[i] = tsp::f32_to_bf16_bits(o[u][4 * g4 + i] * inv);
+      *(u16x4*)(Oq + 32 * u + 8 * g4 + 4 * h) = t;
+    }
+  }
+  if (h == 0 && rmax) {
+    const int64_t r = head * Mt * AB + q;
+    rmax[r] = empty ? 0.f : mtrue * 0.69314718055994531f;
+    rden[r] = empty ? 1e-12f : den;
+  }
+}
+
 template <typename T>
 int launch_generic(const void* Q, const void* K, const void* V, int64_t H, int64_t S, int64_t D, const int64_t* rp,
                    const int64_t* ci, int64_t b, int64_t Mt, double scale, void* O, void* rmax, void* rden,
@@ -315,7 +576,11 @@ extern "C" int tsp_bsa_fwd(const void* Q, const void* K, const void* V, int dtyp
     const int64_t grid = tsp::ceil_div(n_heads, 8) * Mt * 8;
     if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_fwd: problem too large");
     const float sl2 = (float)(scale * 1.4426950408889634);
-    if (head_dim == 128)
+    if (head_dim == 128 && scale > 0 && (seq_len + AB) * head_dim * 2 <= (int64_t)UINT32_MAX)
+      hipLaunchKernelGGL(bsa_fwd_bf16_d128, dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)Q,
+                         (const uint16_t*)K, (const uint16_t*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs,
+                         block_col_indices, Mt, sl2, (uint16_t*)O, (float*)row_max, (float*)row_denom);
+    else if (head_dim == 128)
       hipLaunchKernelGGL((bsa_fwd_bf16_mfma<128>), dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)Q,
                          (const uint16_t*)K, (const uint16_t*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs,
                          block_col_indices, Mt, sl2, (uint16_t*)O, (float*)row_max, (float*)row_denom);

@@ -33,6 +33,7 @@
 // scheduler within each XCD.
 #include "common.h"
 
+#include "lds_dma.h"
 #include "mfma_f32.h"
 
 namespace {
@@ -130,44 +131,7 @@ constexpr int A_BYTES = 128 * KC * 2;      // 16 KiB, rows of 128 B
 constexpr int B_BYTES = KC * 128 * 2;      // 16 KiB, rows of 256 B
 constexpr int STAGE = A_BYTES + B_BYTES;   // 32 KiB
 typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
-// The direct-to-LDS loads are issued from inline asm so that the compiler
-// does not track them: it cannot tell the ring stages apart and would
-// otherwise wait for every outstanding load before each LDS read. Their
-// completion is waited for explicitly (vmcnt) before the slab barrier.
-// M0 holds the wave's LDS destination; lane l writes 16 bytes at M0 + 16 l.
-// M0 is a reserved register, so its clobber is not tracked (hipcc warns);
-// nothing the compiler generates for this kernel reads M0 (checked in the
-// gfx950 assembly), so no value is lost across these statements.
-__device__ inline void dma_global16(const void* g, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
-               "s"(__builtin_amdgcn_readfirstlane(lds_addr))
-               : "memory", "m0");
-}
-// Buffer form: out-of-range offsets (>= num_records) read as zero.
-__device__ inline void dma_buffer16(i32x4 rsrc, int voff, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc),
-               "s"(__builtin_amdgcn_readfirstlane(lds_addr))
-               : "memory", "m0");
-}
-// Low 32 bits of *p, waited for in place (all earlier loads included): the
-// compiler does not see this load either, so it never adds a wait for it
-// on the slab path.
-__device__ inline int load_lo32_sync(const void* p) {
-  int v;
-  asm volatile("global_load_dword %0, %1, off\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(p) : "memory");
-  return v;
-}
-// s_waitcnt immediate waiting for vmcnt <= N only (gfx9 encoding)
-template <int N>
-__device__ inline void wait_vm() {
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | (((N >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8));
-}
-// Workgroup barrier without the fence of __syncthreads (which would wait for
-// all outstanding loads); the memory clobber keeps LDS reads on their side.
-__device__ inline void barrier() { asm volatile("s_barrier" ::: "memory"); }
 }  // namespace bf
 
 template <typename OutT>
@@ -185,11 +149,9 @@ __global__ __launch_bounds__(512) void bsr_spmm_bf16_mfma(
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wm = w & 1, wn = w >> 1, h = lane >> 5, l32 = lane & 31;
-  // buffer resource over B: base, stride 0, num_records = B's bytes, raw buffer
-  const uint64_t bbase = (uint64_t)(uintptr_t)B;
-  const bf::i32x4 brsrc = {(int)(uint32_t)bbase, (int)(uint32_t)(bbase >> 32) & 0xFFFF,
-                           (int)(uint32_t)(n * ldb * 2), 0x00020000};
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
+  // buffer resource over B (rows past n read as zero)
+  const tsp::dma::i32x4 brsrc = tsp::dma::make_rsrc(B, (uint32_t)(n * ldb * 2));
+  const uint32_t lds0 = tsp::dma::lds_addr(lds);
 
   // Column-block indices of the row, 64 at a time in one VGPR (lane i holds
   // block cbase + i), read out with readlane: no scalar load (and its wait)
@@ -204,7 +166,7 @@ __global__ __launch_bounds__(512) void bsr_spmm_bf16_mfma(
   int cbase = 0;
   auto load_cols = [&](int base) {
     const int i = base + lane < nblk ? base + lane : nblk - 1;
-    return bf::load_lo32_sync(ci + start + i);
+    return tsp::dma::load_lo32_sync(ci + start + i);
   };
   int cv = load_cols(0);
   auto colblk = [&](int blk) {
@@ -227,7 +189,7 @@ __global__ __launch_bounds__(512) void bsr_spmm_bf16_mfma(
       const int r = 8 * i + (lane >> 3);
       const int c = (lane & 7) ^ ((r >> 1) & 7);        // logical chunk held at this lane's LDS slot
       const uint16_t* g = blocks + idx * (BS * BS) + r * BS + kk + c * 8;
-      bf::dma_global16(g, st + i * 1024);
+      tsp::dma::global16(g, st + i * 1024);
     }
     const int64_t brow0 = (int64_t)colblk(blk) * BS + kk;
 #pragma unroll
@@ -236,7 +198,7 @@ __global__ __launch_bounds__(512) void bsr_spmm_bf16_mfma(
       const int rr = 4 * j + (lane >> 4);
       const int c = (lane & 15) ^ (4 * (rr & 3));
       const int64_t off = ((brow0 + rr) * ldb + n0 + c * 8) * 2;
-      bf::dma_buffer16(brsrc, (int)(uint32_t)off, st + bf::A_BYTES + j * 1024);
+      tsp::dma::buffer16(brsrc, (uint32_t)off, st + bf::A_BYTES + j * 1024);
     }
   };
 
@@ -282,14 +244,14 @@ __global__ __launch_bounds__(512) void bsr_spmm_bf16_mfma(
     // (4 loads per slab per wave; up to NST-2 later slabs may be in flight)
     const int later = nsteps - 1 - s;
     if (bf::NST >= 5 && later >= 3)
-      bf::wait_vm<12>();
+      tsp::dma::wait_vm<12>();
     else if (later >= 2)
-      bf::wait_vm<8>();
+      tsp::dma::wait_vm<8>();
     else if (later == 1)
-      bf::wait_vm<4>();
+      tsp::dma::wait_vm<4>();
     else
-      bf::wait_vm<0>();
-    bf::barrier();  // every wave's part of slab s is in LDS; stage (s-1)%NST is free
+      tsp::dma::wait_vm<0>();
+    tsp::dma::barrier();  // every wave's part of slab s is in LDS; stage (s-1)%NST is free
     if (s + bf::NST - 1 < nsteps) issue(s + bf::NST - 1);
     compute(lds + (s % bf::NST) * bf::STAGE);
   }

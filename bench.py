@@ -11,7 +11,7 @@ call over the resident operands; FLOPs = 2 * n_blocks * 128^2 * 512
 (CSR SpMV HBM GB/s, bf16 bsr_spmm, screened_spmm, block-sparse attention),
 each timed with HIP events on the stream the kernel runs on.
 
-`roofline` is for the dominant kernel of the headline (bsr_spmm_f32_mfma):
+`roofline` is for the dominant kernel of the headline (bsr_spmm_f32_dma):
 achieved = algorithmic FLOPs per launch / average launch time from HIP
 events over the timed region, peak = 157.3 TFLOP/s (MI355X dense fp32
 matrix). `traffic` (HBM bytes per launch) comes from the committed
@@ -144,7 +144,7 @@ def bench_bsr_fp32(steps: int, warmup: int, cpu: bool):
             "peak": FP32_MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
-            "traffic": _traffic("bsr_spmm_f32_mfma", "cfg3a"),
+            "traffic": _traffic("bsr_spmm_f32_dma", "cfg3a"),
         },
     }
     if cpu:
@@ -300,6 +300,31 @@ def bench_attention(steps: int, warmup: int, cpu: bool = False):
     return res
 
 
+def calibrate_peaks():
+    """Achievable peaks on this box next to the spec ones: a 1 GiB device copy
+    (read + write bytes / time), and dense 8192^3 GEMMs in fp32 and bf16
+    through torch (hipBLASLt), each after the clock pre-warm."""
+    import torch
+
+    res = {}
+    a = torch.ones(1 << 28, device="cuda")
+    b = torch.empty_like(a)
+    _, ms = time_gpu(lambda: b.copy_(a), 20, 3)
+    res["copy_1GiB_GBps"] = round(2 * a.numel() * 4 / (ms * 1e-3) / 1e9, 1)
+    res["hbm_spec_GBps"] = HBM_PEAK_GBS
+    del a, b
+    n = 8192
+    for dt, name, peak in ((torch.float32, "fp32", FP32_MFMA_PEAK_TFLOPS), (torch.bfloat16, "bf16", BF16_MFMA_PEAK_TFLOPS)):
+        x = torch.randn(n, n, device="cuda").to(dt)
+        y = torch.randn(n, n, device="cuda").to(dt)
+        _, ms = time_gpu(lambda: x @ y, 10, 3)
+        tf = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+        res[f"gemm_{name}_8192_TFLOPs"] = round(tf, 1)
+        res[f"gemm_{name}_spec_TFLOPs"] = peak
+        res[f"gemm_{name}_frac_of_spec"] = round(tf / peak, 4)
+    return res
+
+
 def calibrate_gather():
     """What the x gathers cost at cfg2. torch.index_select(x, 0, cols) with
     cfg2's column indices (uniform over 1 M) and with sequential indices has
@@ -338,6 +363,9 @@ def main(argv=None) -> int:
     ap.add_argument("--no-secondary", action="store_true", help="headline only")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device copy (known bytes) to calibrate PMC byte counters")
+    ap.add_argument("--calibrate-peaks", action="store_true",
+                    help="run only the achievable-peak calibration: 1 GiB device copy, fp32 and bf16 dense "
+                    "GEMMs (torch/hipBLASLt) beside the spec peaks")
     ap.add_argument("--calibrate-gather", action="store_true",
                     help="run only the SpMV gather-floor calibration on cfg2 (torch index_select, random vs "
                     "sequential indices, next to spmv)")
@@ -360,6 +388,9 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
+    if args.calibrate_peaks:
+        print(json.dumps(calibrate_peaks()), flush=True)
+        return 0
     if args.calibrate_copy:
         a = torch.ones(1 << 26, device="cuda")
         b = torch.empty_like(a)

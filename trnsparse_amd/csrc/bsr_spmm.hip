@@ -96,6 +96,186 @@ __global__ __launch_bounds__(T32::NTHR) void bsr_spmm_f32_mfma(
   T32::store_tile(C, ldc, row * BS, src.n0, m, ncols, src.q, acc0, acc1, cvt_out<OutT>);
 }
 
+// ------------------------------------------------------- fp32 MFMA, streamed
+//
+// bsr_spmm_f32_dma<KC>: b == 128, fp32. Same tile (128x128 of C per
+// workgroup, one block row x one 128-column tile) and scheduling (tile_item:
+// heaviest rows first, boustrophedon over the XCDs) as bsr_spmm_f32_mfma,
+// restructured for issue efficiency:
+//   * 4 waves, each a 64x64 sub-tile as four independent 32x32
+//     v_mfma_f32_32x32x2_f32 accumulators: per 8 k a wave reads two 16-byte
+//     A fragments and eight 4-byte B values for 16 MFMAs;
+//   * KC-wide k-slabs of A (128 x KC) and B (KC x 128) stream through a
+//     2-stage LDS ring by direct global->LDS loads issued one slab ahead
+//     (a slab is ~KC*128 MFMA cycles per SIMD, ample time for the loads);
+//     B through a buffer resource, so rows past n read as zero;
+//   * k is permuted within each 8-k group as in the other MFMA kernels (lane
+//     half h takes k0 + 4h + s at k-step s), so a lane's four A values are one
+//     16-byte read;
+//   * swizzles for the 64-bank LDS: A rows of KC*4 bytes, chunk ^ (row % 16)
+//     for 256-byte rows or chunk ^ ((row / 2) % 8) for 128-byte rows, so 16
+//     consecutive rows of one b128 read cover all banks; B rows (512 B)
+//     chunk ^ 8*((k / 4) % 2), so the two lane halves (k rows 4 apart) of a
+//     4-byte read land in different bank halves.
+// KC = 64 (128 KiB ring, one workgroup per CU, so the in-order dispatcher
+// list-schedules the ranked rows) measured faster on cfg3a than KC = 32
+// (64 KiB, two workgroups per CU): 237 us vs 263 us.
+template <int KC_>
+struct F32S {
+  static constexpr int KC = KC_;
+  static constexpr int A_ROWB = KC * 4;
+  static constexpr int B_ROWB = 128 * 4;
+  static constexpr int A_BYTES = 128 * A_ROWB;
+  static constexpr int B_BYTES = KC * B_ROWB;
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int NST = 2;
+  static constexpr int CPR = A_ROWB / 16;     // 16-byte chunks per A row
+  // A: slot of logical chunk c in row r (an involution)
+  static __device__ int aswz(int c, int r) { return CPR == 16 ? (c ^ (r & 15)) : (c ^ ((r >> 1) & 7)); }
+};
+
+template <int KC_>
+__global__ __launch_bounds__(256) void bsr_spmm_f32_dma(
+    const float* __restrict__ blocks, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci,
+    int64_t mb, int nt, int64_t m, int64_t n, const float* __restrict__ B, int64_t ldb, int64_t ncols,
+    float* __restrict__ C, int64_t ldc, const int32_t* __restrict__ order) {
+  typedef F32S<KC_> G;
+  constexpr int SK = G::KC;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[G::NST * G::STAGE];
+  int64_t row;
+  int ntile;
+  if (!T32::tile_item(blockIdx.x, mb, nt, order, row, ntile)) return;
+  const int64_t n0 = (int64_t)ntile * 128;
+  const int64_t start = rp[row];
+  const int nblk = (int)(rp[row + 1] - start);
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w & 1, wn = w >> 1, h = lane >> 5, l32 = lane & 31;
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) acc[t][u] = f32x16{};
+
+  if (nblk > 0) {
+    const tsp::dma::i32x4 brsrc = tsp::dma::make_rsrc(B, (uint32_t)(n * ldb * 4));
+    const uint32_t lds0 = tsp::dma::lds_addr(lds);
+    int cbase = 0;
+    auto load_cols = [&](int base) {
+      const int i = base + lane < nblk ? base + lane : nblk - 1;
+      return tsp::dma::load_lo32_sync(ci + start + i);
+    };
+    int cv = load_cols(0);
+    auto colblk = [&](int blk) {
+      if (blk - cbase >= 64) {
+        cbase = blk & ~63;
+        cv = load_cols(cbase);
+      }
+      return __builtin_amdgcn_readlane(cv, blk - cbase);
+    };
+
+    // ---- loads of slab s into stage s % NST (1 KiB per wave instruction)
+    constexpr int A_INS = G::A_BYTES / 1024 / 4;  // per wave
+    constexpr int B_INS = G::B_BYTES / 1024 / 4;
+    constexpr int A_RPI = 1024 / G::A_ROWB;       // A rows per instruction
+    auto issue = [&](int s) {
+      constexpr int SPB = BS / SK;                // slabs per block
+      const int blk = s / SPB;
+      const int kk = (s % SPB) * SK;
+      const uint32_t st = lds0 + (s % G::NST) * G::STAGE;
+      const float* ablk = blocks + (start + blk) * (BS * BS) + kk;
+#pragma unroll
+      for (int q = 0; q < A_INS; ++q) {
+        const int i = A_INS * w + q;
+        const int r = A_RPI * i + lane / G::CPR;
+        const int c = G::aswz(lane % G::CPR, r);  // logical chunk held at this lane's slot
+        tsp::dma::global16(ablk + r * BS + c * 4, st + i * 1024);
+      }
+      const int64_t brow0 = (int64_t)colblk(blk) * BS + kk;
+#pragma unroll
+      for (int q = 0; q < B_INS; ++q) {
+        const int j = B_INS * w + q;              // B slab rows 2j, 2j+1
+        const int rr = 2 * j + (lane >> 5);
+        const int c = (lane & 31) ^ (8 * ((rr >> 2) & 1));
+        const int64_t off = ((brow0 + rr) * ldb + n0 + c * 4) * 4;
+        tsp::dma::buffer16(brsrc, (uint32_t)off, st + G::A_BYTES + j * 1024);
+      }
+    };
+
+    // per-lane LDS offsets: A rows wm*64 + 32t + l32 (the swizzle term is the
+    // same for both t); B columns wn*64 + 32u + l32, rows 8g + 4h + s
+    const int arow = wm * 64 + l32;
+    const int bcol = wn * 64 + l32;
+    int boff[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      boff[u] = ((((bcol + 32 * u) >> 2) ^ (8 * h)) * 16) + (bcol & 3) * 4 + 4 * h * G::B_ROWB;
+    struct Ops {
+      f32x4 a[2];
+      float b[2][4];
+    };
+    auto fetch = [&](const uint8_t* st, int g, Ops& o) {
+      const uint8_t* As = st + arow * G::A_ROWB + G::aswz(2 * g + h, arow) * 16;
+      o.a[0] = *(const f32x4*)(As);
+      o.a[1] = *(const f32x4*)(As + 32 * G::A_ROWB);
+      const uint8_t* Bs = st + G::A_BYTES + 8 * g * G::B_ROWB;
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) o.b[u][s] = *(const float*)(Bs + s * G::B_ROWB + boff[u]);
+    };
+    auto mma = [&](const Ops& o) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+            acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.a[t][s], o.b[u][s], acc[t][u], 0, 0, 0);
+    };
+    auto compute = [&](const uint8_t* st) {
+      Ops o[2];
+      fetch(st, 0, o[0]);
+#pragma unroll
+      for (int g = 0; g < SK / 8; ++g) {
+        if (g + 1 < SK / 8) fetch(st, g + 1, o[(g + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(o[g & 1]);
+      }
+    };
+
+    const int nsteps = nblk * (BS / SK);
+    issue(0);
+    for (int s = 0; s < nsteps; ++s) {
+      tsp::dma::wait_vm<0>();  // this wave's loads of slab s are done
+      tsp::dma::barrier();     // every wave's part is in LDS; stage (s+1) % NST is free
+      if (s + 1 < nsteps) issue(s + 1);
+      compute(lds + (s % G::NST) * G::STAGE);
+    }
+  }
+  // accumulator layout: lane holds column l32 and rows 8*(v/4) + 4*h + v%4
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int64_t r0 = row * BS + wm * 64 + 32 * t + 4 * h;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int64_t c = n0 + wn * 64 + 32 * u + l32;
+      if (c < ncols) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
+          if (r < m) C[r * ldc + c] = acc[t][u][v];
+        }
+      }
+    }
+  }
+}
+
+#ifndef F32_DMA_KC
+#define F32_DMA_KC 64
+#endif
+
 // ---------------------------------------------------------------- bf16 MFMA
 //
 // bsr_spmm_bf16_mfma: b == 128, bf16 operands, fp32 accumulation, fp32 or
@@ -364,6 +544,16 @@ extern "C" int tsp_bsr_spmm(const void* blocks, int dtype, const int64_t* block_
     return tsp::fail(TSP_EINVAL, "tsp_bsr_spmm: null pointer");
   const int64_t mb = tsp::ceil_div(m, block_size);
 
+  if (dtype == TSP_F32 && block_size == BS && (ldb % 4) == 0 && ((uintptr_t)B % 16) == 0 &&
+      ((uintptr_t)blocks % 16) == 0 && (n + BS) * ldb * 4 + 4 * BS <= (int64_t)UINT32_MAX) {
+    // (the kernel's B offsets, rows < n + 128 and columns < ldb + 128, fit 32 bits)
+    const int64_t nt = tsp::ceil_div(ncols, 128);
+    const int64_t grid = tsp::ceil_div(mb, 8) * 8 * nt;
+    if (grid > INT32_MAX || nt > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm: problem too large");
+    hipLaunchKernelGGL(bsr_spmm_f32_dma<F32_DMA_KC>, dim3((unsigned)grid), dim3(256), 0, st, (const float*)blocks, block_row_ptrs,
+                       block_col_indices, mb, (int)nt, m, n, (const float*)B, ldb, ncols, (float*)C, ldc, row_order);
+    return tsp::check_launch("bsr_spmm_f32_dma launch");
+  }
   if (dtype == TSP_F32 && block_size == BS && (ldb % 4) == 0 && ((uintptr_t)B % 16) == 0 &&
       ((uintptr_t)blocks % 16) == 0) {
     const int64_t nt = tsp::ceil_div(ncols, T32::BN);

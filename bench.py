@@ -8,7 +8,8 @@ peak"): bsr_spmm at config 3a — 16384x16384 in 128x128 blocks, 10% block
 density (1638 stored blocks), B 16384x512, fp32. One step = one bsr_spmm
 call over the resident operands; FLOPs = 2 * n_blocks * 128^2 * 512
 (stored blocks only). The `secondary` list carries the other configs
-(CSR SpMV HBM GB/s, bf16 bsr_spmm, screened_spmm, block-sparse attention),
+(CSR SpMV HBM GB/s, bf16 bsr_spmm, bsr_spmm backward, screened_spmm,
+block-sparse attention),
 each timed with HIP events on the stream the kernel runs on.
 
 `roofline` is for the dominant kernel of the headline (bsr_spmm_f32_dma):
@@ -188,6 +189,44 @@ def bench_bsr_bf16(steps: int, warmup: int):
         "frac_bf16_mfma": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
         "frac_hbm_min_bytes": round(byts / (ev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
     }
+
+
+def bench_bsr_backward(steps: int, warmup: int):
+    """Backward of bsr_spmm at config 3a (fp32): the two kernels the autograd
+    backward launches, each 27.48 GFLOP — tsp_bsr_sddmm (dA on the stored
+    pattern) and tsp_bsr_spmm_t (dB = A^T dC over the block-column view)."""
+    import torch
+
+    from trnsparse_amd import workloads as W
+    from trnsparse_amd.hip import _lib
+    from trnsparse_amd.hip import dispatch as D
+
+    A, B = W.cfg3_bsr(dtype=torch.float32)
+    m, n = A.shape
+    N = B.shape[1]
+    flops = 2.0 * A.n_blocks * 128 * 128 * N
+    dev = torch.device("cuda", torch.cuda.current_device())
+    blocks, Bd = A.blocks.to(dev), B.to(dev)
+    G = torch.randn(m, N, generator=torch.Generator().manual_seed(9)).to(dev)
+    rp = A.block_row_ptrs.to(dev)
+    ci = A.block_col_indices.to(dev)
+    brow, cp, cbid, crow, corder = D._bsr_bwd_plan(rp, ci, 128, 128, dev)
+    gb = torch.empty_like(blocks)
+    dB = torch.empty(n, N, device=dev)
+    st = _lib.stream_handle(dev)
+    code = _lib.dtype_code(torch.float32)
+    sddmm = lambda: _lib.call("tsp_bsr_sddmm", G.data_ptr(), N, m, Bd.data_ptr(), N, n, N, brow.data_ptr(),
+                              ci.data_ptr(), A.n_blocks, 128, code, gb.data_ptr(), st)
+    spmm_t = lambda: _lib.call("tsp_bsr_spmm_t", blocks.data_ptr(), code, cp.data_ptr(), cbid.data_ptr(),
+                               crow.data_ptr(), 128, 128, m, n, G.data_ptr(), N, N, dB.data_ptr(), N,
+                               corder.data_ptr(), st)
+    out = []
+    for name, fn in (("bsr_spmm backward dA (sddmm) cfg3a fp32", sddmm), ("bsr_spmm backward dB (A^T dC) cfg3a fp32", spmm_t)):
+        _, ms = time_gpu(fn, steps, warmup)
+        tf = flops / (ms * 1e-3) / 1e12
+        out.append({"name": name, "value": round(tf * 1e3, 1), "unit": "GFLOP/s", "us": round(ms * 1e3, 1),
+                    "frac_fp32_mfma": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)})
+    return out
 
 
 def bench_spmv(dist: str, index_bits: int, steps: int, warmup: int, cpu: bool = False):
@@ -413,12 +452,14 @@ def main(argv=None) -> int:
             ("spmv poisson int32", lambda: bench_spmv("poisson", 32, 20, 3)),
             ("spmv zipf int64", lambda: bench_spmv("zipf", 64, 10, 2)),
             ("bsr bf16", lambda: bench_bsr_bf16(max(5, args.steps // 2), 3)),
+            ("bsr backward", lambda: bench_bsr_backward(10, 2)),
             ("screened", lambda: bench_screened(10, 2, cpu=not args.no_cpu)),
             ("attention", lambda: bench_attention(10, 2, cpu=not args.no_cpu)),
         ]
         for name, fn in jobs:
             try:
-                secondary.append(fn())
+                r = fn()
+                secondary.extend(r if isinstance(r, list) else [r])
             except Exception as exc:  # report, do not hide
                 secondary.append({"name": name, "error": repr(exc)})
             print(f"# done: {name}", file=sys.stderr, flush=True)

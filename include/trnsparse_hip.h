@@ -81,6 +81,47 @@ int tsp_bsr_row_order(const int64_t* block_row_ptrs, int64_t n_block_rows,
                       int32_t* order, void* stream);
 
 /* ======================================================================
+ * Backward of C = A_bsr @ B.
+ *
+ * Replaces the backward of _BSRSpMMFunction
+ * (trnsparse/nki/dispatch.py:331-369: dA_k = dC_i B_j^T on the stored
+ * pattern, dB = A_dense^T dC), which gathers dense panels on the host.
+ *
+ * tsp_bsr_sddmm: grad_blocks[k] = G[rows of block row i_k] @ B[rows of block
+ *   column j_k]^T for every stored block k (rows past m of G and past n of B
+ *   count as zero); the SDDMM restricted to the pattern.
+ *   G            (m, ncols) row stride ldg (dC)
+ *   B            (n, ncols) row stride ldb
+ *   block_rows   (n_blocks,) int64 block row of each stored block
+ *   block_col_indices (n_blocks,) int64
+ *   grad_blocks  (n_blocks, block_size, block_size) row-major, every element
+ *                written. dtype TSP_F32 / TSP_F64 / TSP_BF16 for G, B and
+ *                grad_blocks (fp32 accumulation, fp64 for F64).
+ *
+ * tsp_bsr_spmm_t: out[n, ncols] = A_bsr^T @ X over the block-column view of
+ *   the pattern. col_ptrs (n_block_cols+1,) int64 with n_block_cols =
+ *   ceil(n/block_size); col_block_ids / col_block_rows (n_blocks,) int64 give,
+ *   column by column in increasing block-row order, the stored block index and
+ *   its block row (the sums run in that order). X is (m, ncols) row stride
+ *   ldx (rows past m count as zero); out (n, ncols) row stride ldo, every
+ *   element written. col_order: optional heaviest-first permutation of the
+ *   block columns (tsp_bsr_row_order on col_ptrs), scheduling only.
+ * ==================================================================== */
+int tsp_bsr_sddmm(const void* G, int64_t ldg, int64_t m,
+                  const void* B, int64_t ldb, int64_t n, int64_t ncols,
+                  const int64_t* block_rows, const int64_t* block_col_indices,
+                  int64_t n_blocks, int64_t block_size, int dtype,
+                  void* grad_blocks, void* stream);
+
+int tsp_bsr_spmm_t(const void* blocks, int dtype,
+                   const int64_t* col_ptrs, const int64_t* col_block_ids,
+                   const int64_t* col_block_rows, int64_t n_block_cols,
+                   int64_t block_size, int64_t m, int64_t n,
+                   const void* X, int64_t ldx, int64_t ncols,
+                   void* out, int64_t ldo, const int32_t* col_order,
+                   void* stream);
+
+/* ======================================================================
  * CSR sparse x dense (bandwidth-bound; no MFMA)
  *
  * Replaces the reference's spmv (trnsparse/ops.py:30-48, torch

@@ -13,6 +13,8 @@ How each function is pinned (tests/test_oracle.py):
 - bsr_from_dense / bsr_to_dense: brute-force per-block loops on tiny grids,
   round trips, the empty-matrix case, padding of unaligned shapes.
 - bsr_spmm: closed form to_dense(A) @ B (numpy matmul), empty pattern -> 0.
+- bsr_spmm_backward: torch float64 autograd through the dense product
+  to_dense(A) @ B (dA read back on the stored blocks), empty pattern -> 0.
 - csr_spmv / csr_spmm: scipy.sparse (independent implementation), the
   reference's known answers [9, 16] and 7.0 (tests/test_ops.py:25-32, 61-67),
   identity.
@@ -80,6 +82,35 @@ def bsr_spmm(blocks, col_idx, row_ptrs, shape, b, B, absolute: bool = False):
             blk = blocks[idx].astype(np.float64)
             acc += (np.abs(blk) if absolute else blk) @ Bp[j * b : (j + 1) * b]
     return C[:m]
+
+
+def bsr_spmm_backward(blocks, col_idx, row_ptrs, shape, b, B, G, absolute: bool = False):
+    """Gradients of C = A @ B for the upstream gradient G = dC, in float64
+    (reference autograd, trnsparse/nki/dispatch.py:331-369):
+      dA_k = G[rows of block row i] @ B[rows of block column j]^T per stored
+             block k = (i, j) (rows past m / n of the padded operands are 0)
+      dB   = A^T @ G
+    Returns (d_blocks (n_blocks, b, b), dB (n, N)). With absolute=True both
+    use |.| operands: the per-element error scales.
+    """
+    m, n = shape
+    N = B.shape[1]
+    mb = len(row_ptrs) - 1
+    nbc = -(-n // b)
+    f = np.abs if absolute else (lambda x: x)
+    Bp = np.zeros((nbc * b, N))
+    Bp[:n] = f(B)
+    Gp = np.zeros((mb * b, N))
+    Gp[:m] = f(G)
+    dblocks = np.zeros((len(col_idx), b, b))
+    dB = np.zeros((nbc * b, N))
+    for i in range(mb):
+        gi = Gp[i * b : (i + 1) * b]
+        for idx in range(row_ptrs[i], row_ptrs[i + 1]):
+            j = col_idx[idx]
+            dblocks[idx] = gi @ Bp[j * b : (j + 1) * b].T
+            dB[j * b : (j + 1) * b] += f(blocks[idx].astype(np.float64)).T @ gi
+    return dblocks, dB[:n]
 
 
 # ------------------------------------------------------------------ CSR

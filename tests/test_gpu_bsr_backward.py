@@ -1,0 +1,120 @@
+"""GPU parity of the bsr_spmm backward (tsp_bsr_sddmm for dA on the stored
+pattern, tsp_bsr_spmm_t for dB = A^T dC) against the CPU oracle
+(oracle.ref.bsr_spmm_backward, pinned to dense autograd on the CPU).
+
+Tolerances follow the forward: fp32 max error <= 1e-4 and bf16 <= 2e-2
+relative to the dot-product scale of each gradient element (|G|.|B| for dA,
+|A|^T.|G| for dB); fp64 <= 1e-10.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import trnsparse_amd as ts
+from oracle import ref
+from trnsparse_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2, torch.float64: 1e-10}
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy() if t.dtype == torch.bfloat16 else t.detach().cpu().numpy()
+
+
+def _grads(A: ts.BSRMatrix, B: torch.Tensor, G: torch.Tensor):
+    blocks = A.blocks.detach().clone().cuda().requires_grad_(True)
+    Bd = B.detach().clone().cuda().requires_grad_(True)
+    Ad = ts.BSRMatrix(blocks, A.block_col_indices, A.block_row_ptrs, A.shape, A.block_size)
+    C = ts.bsr_spmm(Ad, Bd)
+    C.backward(G.cuda().to(C.dtype))
+    return blocks.grad, Bd.grad
+
+
+def _check(A: ts.BSRMatrix, B: torch.Tensor, G: torch.Tensor, tol: float):
+    db, dB = _grads(A, B, G)
+    assert db.dtype == A.dtype and dB.dtype == B.dtype and dB.shape == B.shape
+    args = (_np(A.blocks), A.block_col_indices.numpy(), A.block_row_ptrs.numpy(), A.shape, A.block_size, _np(B), _np(G))
+    exact_b, exact_B = ref.bsr_spmm_backward(*args)
+    scale_b, scale_B = ref.bsr_spmm_backward(*args, absolute=True)
+    assert ref.scaled_error(_np(db), exact_b, scale_b) <= tol
+    assert ref.scaled_error(_np(dB), exact_B, scale_B) <= tol
+
+
+@pytest.mark.parametrize(
+    "shape,b,N,density,dtype",
+    [
+        ((256, 384), 128, 64, 0.5, torch.float32),     # MFMA kernels
+        ((512, 512), 128, 256, 0.3, torch.float32),
+        ((384, 256), 128, 200, 0.6, torch.float32),    # N % 64 != 0: zero-filled k tail
+        ((300, 260), 128, 12, 1.0, torch.float32),     # unaligned m, n (padded blocks)
+        ((300, 260), 128, 10, 1.0, torch.float32),     # N % 4 != 0: generic kernels
+        ((40, 40), 8, 12, 0.4, torch.float64),         # any block size, fp64
+        ((256, 256), 128, 64, 0.5, torch.bfloat16),
+    ],
+)
+def test_backward_matches_oracle(hip_backend, shape, b, N, density, dtype):
+    g = torch.Generator().manual_seed(31)
+    A = torch.randn(*shape, generator=g, dtype=torch.float64) * (torch.rand(*shape, generator=g) < density)
+    bsr = ts.BSRMatrix.from_dense(A.to(dtype), block_size=b)
+    B = torch.randn(shape[1], N, generator=g, dtype=torch.float64).to(dtype)
+    G = torch.randn(shape[0], N, generator=g, dtype=torch.float64).to(dtype)
+    _check(bsr, B, G, TOL[dtype])
+
+
+def test_backward_empty_rows_and_columns(hip_backend):
+    """Block rows and block columns without stored blocks: zero gradient rows
+    of dB, and dA only on the stored blocks."""
+    mask = torch.tensor([[True, False, False, True], [False, False, False, False], [True, False, True, False]])
+    bsr = W.bsr_from_block_mask(mask, 128)
+    g = torch.Generator().manual_seed(2)
+    bsr = ts.BSRMatrix(torch.randn(bsr.n_blocks, 128, 128, generator=g), bsr.block_col_indices, bsr.block_row_ptrs,
+                       bsr.shape, 128)
+    B = torch.randn(bsr.shape[1], 128, generator=g)
+    G = torch.randn(bsr.shape[0], 128, generator=g)
+    _check(bsr, B, G, TOL[torch.float32])
+    _, dB = _grads(bsr, B, G)
+    assert torch.count_nonzero(dB[128:256]).item() == 0  # block column 1 holds no blocks
+
+
+def test_backward_deterministic(hip_backend):
+    A, B = W.cfg3_bsr(nb=16, ncols=128, density=0.3)
+    G = torch.randn(A.shape[0], 128, generator=torch.Generator().manual_seed(5))
+    d1 = _grads(A, B, G)
+    d2 = _grads(A, B, G)
+    assert torch.equal(d1[0], d2[0]) and torch.equal(d1[1], d2[1])
+
+
+def test_cfg3a_backward_full_size(hip_backend):
+    """cfg3a (1638 blocks, N = 512): dA on a sample of blocks against the
+    closed form in float64, and dB through the size-independent identity
+    1^T dB 1 = (A 1) . (G 1) plus a sample of dB rows."""
+    A, B = W.cfg3_bsr(dtype=torch.float32)
+    G = torch.randn(A.shape[0], B.shape[1], generator=torch.Generator().manual_seed(9))
+    db, dB = _grads(A, B, G)
+    Gn, Bn = G.double().numpy(), B.double().numpy()
+    ptr, col = A.block_row_ptrs.numpy(), A.block_col_indices.numpy()
+    brow = np.repeat(np.arange(len(ptr) - 1), np.diff(ptr))
+    for k in (0, 1, 700, 1637):
+        i, j = brow[k], col[k]
+        exact = Gn[i * 128 : (i + 1) * 128] @ Bn[j * 128 : (j + 1) * 128].T
+        scale = np.abs(Gn[i * 128 : (i + 1) * 128]) @ np.abs(Bn[j * 128 : (j + 1) * 128]).T
+        assert ref.scaled_error(db[k].cpu().numpy(), exact, scale) <= TOL[torch.float32]
+    blocks = A.blocks.double().numpy()
+    rowsum_A = np.zeros(A.shape[0])
+    for k in range(len(col)):
+        rowsum_A[brow[k] * 128 : (brow[k] + 1) * 128] += blocks[k].sum(axis=1)
+    expect = rowsum_A @ Gn.sum(axis=1)
+    got = dB.double().sum().item()
+    bound = (np.abs(blocks).sum() * np.abs(Gn).max() * B.shape[1]) * 1e-6
+    assert abs(got - expect) <= bound
+    # a sample of dB rows: rows of block column j are sum_k A_k^T G_i
+    for j in (0, 64, 127):
+        ks = np.nonzero(col == j)[0]
+        exact = sum(blocks[k].T @ Gn[brow[k] * 128 : (brow[k] + 1) * 128] for k in ks)
+        scale = sum(np.abs(blocks[k]).T @ np.abs(Gn[brow[k] * 128 : (brow[k] + 1) * 128]) for k in ks)
+        assert ref.scaled_error(dB[j * 128 : (j + 1) * 128].cpu().numpy(), exact, scale) <= TOL[torch.float32]

@@ -11,6 +11,7 @@ from __future__ import annotations
 import math
 
 import numpy as np
+import torch
 import pytest
 import scipy.sparse as sp
 
@@ -83,6 +84,35 @@ def test_bsr_spmm_empty_pattern_is_zero():
     blocks, col, ptr, sh = ref.bsr_from_dense(A, 8)
     out = ref.bsr_spmm(blocks, col, ptr, sh, 8, np.ones((16, 8)))
     assert out.shape == (16, 8) and not out.any()
+
+
+@pytest.mark.parametrize("shape,b,density", [((24, 24), 8, 0.5), ((20, 14), 8, 1.0), ((40, 40), 8, 0.3)])
+def test_bsr_spmm_backward_vs_dense_autograd(shape, b, density):
+    """dA on the stored blocks and dB equal torch float64 autograd through
+    the dense product; the padding of unaligned blocks gets zero gradient."""
+    rng = np.random.default_rng(7)
+    A = rng.standard_normal(shape) * (rng.random(shape) < density)
+    B = rng.standard_normal((shape[1], 6))
+    G = rng.standard_normal((shape[0], 6))
+    blocks, col, ptr, sh = ref.bsr_from_dense(A, b)
+    dblk, dB = ref.bsr_spmm_backward(blocks, col, ptr, sh, b, B, G)
+    At = torch.tensor(A, requires_grad=True)
+    Bt = torch.tensor(B, requires_grad=True)
+    (At @ Bt).backward(torch.tensor(G))
+    np.testing.assert_allclose(dB, Bt.grad.numpy(), rtol=1e-12, atol=1e-12)
+    m, n = shape
+    for i in range(len(ptr) - 1):
+        for idx in range(ptr[i], ptr[i + 1]):
+            j = col[idx]
+            r1, c1 = min(b, m - i * b), min(b, n - j * b)
+            np.testing.assert_allclose(dblk[idx][:r1, :c1], At.grad.numpy()[i * b : i * b + r1, j * b : j * b + c1],
+                                       rtol=1e-12, atol=1e-12)
+            assert not dblk[idx][r1:].any() and not dblk[idx][:, c1:].any()
+    sd, sB = ref.bsr_spmm_backward(blocks, col, ptr, sh, b, B, G, absolute=True)
+    assert (sd >= np.abs(dblk) - 1e-12).all() and (sB >= np.abs(dB) - 1e-12).all()
+    Z = ref.bsr_from_dense(np.zeros((16, 16)), 8)
+    zd, zB = ref.bsr_spmm_backward(*Z, 8, np.ones((16, 3)), np.ones((16, 3)))
+    assert zd.shape == (0, 8, 8) and not zB.any()
 
 
 # ------------------------------------------------------------------ CSR

@@ -1,0 +1,406 @@
+// Backward of BSR SpMM for gfx950.
+//
+// For C = A_bsr @ B (reference autograd: trnsparse/nki/dispatch.py:331-369)
+//   dA_k = dC[rows of block row i] @ B[rows of block column j]^T   (stored k = (i, j))
+//   dB   = A^T @ dC
+// dA is an SDDMM restricted to the stored pattern (one 128x128 product with
+// K = N per stored block); dB is a BSR-transpose SpMM over the block-column
+// view of the pattern (col_ptrs / col_block_ids / col_block_rows, blocks of a
+// column in increasing block-row order, so every sum has a fixed order).
+//
+// Kernels
+//   bsr_sddmm_f32_dma    b == 128, fp32: one 256-thread workgroup per stored
+//                        block; 4 waves of 64x64 (four 32x32x2 MFMA
+//                        accumulators). 64-wide k-slabs (k = columns of dC
+//                        and B) of the two [128][64] row tiles stream through
+//                        a 2-stage LDS ring by direct global->LDS buffer loads
+//                        (rows past m / n and columns past N read as zero);
+//                        both MFMA operands are k-contiguous, so each is one
+//                        16-byte LDS read per 4 k-steps (k permuted within
+//                        each 8-k group as in the forward kernels).
+//   bsr_spmm_t_f32_dma   b == 128, fp32: C tile 128 (one block column of A,
+//                        i.e. 128 rows of dB) x 128 columns per workgroup,
+//                        walking the blocks of that column; A^T comes from
+//                        the untransposed blocks ([k][m] in LDS, 4-byte reads
+//                        like the forward B operand), dC rows of the block's
+//                        block row as the [k][n] operand. Scheduling as the
+//                        forward kernel (heaviest columns first, boustrophedon
+//                        over the XCDs, one workgroup per CU).
+//   bsr_sddmm_generic / bsr_spmm_t_generic   any block size, f32 / f64 / bf16
+//                        (accumulating in f32, f64 for f64): one thread per
+//                        output element.
+#include "common.h"
+
+#include "lds_dma.h"
+#include "mfma_f32.h"
+
+namespace {
+
+namespace T32 = tsp::f32tile;
+using tsp::dma::i32x4;
+constexpr int BS = 128;
+constexpr int KC = 64;
+constexpr int TROWB = KC * 4;            // row tile [128][64] fp32: 256-byte rows
+constexpr int KROWB = BS * 4;            // k tile [64][128] fp32: 512-byte rows
+constexpr int TILE = 128 * TROWB;        // 32 KiB (== KC * KROWB)
+constexpr int STAGE = 2 * TILE;          // 64 KiB
+constexpr int NST = 2;
+constexpr uint32_t OOB = 0xFFFFFFF0u;    // a buffer offset past any range: reads zero
+
+// ---- tile loads (each wave issues 8 of the 32 1-KiB instructions of a tile)
+// Row tile: rows [row0, row0+128) x columns [k0, k0+64) of a row-major fp32
+// matrix with row stride ld; 16-byte chunk c of row r sits in slot
+// c ^ (r % 16). Columns at or past kend read as zero.
+__device__ inline void dma_row_tile(i32x4 rs, int64_t row0, int64_t ld, int64_t k0, int64_t kend, uint32_t dst, int w,
+                                    int lane) {
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int i = 8 * w + q;
+    const int r = 4 * i + (lane >> 4);
+    const int c = (lane & 15) ^ (r & 15);
+    const int64_t col = k0 + c * 4;
+    const uint32_t off = col < kend ? (uint32_t)(((row0 + r) * ld + col) * 4) : OOB;
+    tsp::dma::buffer16(rs, off, dst + i * 1024);
+  }
+}
+// k tile: rows [krow0, krow0+64) x columns [n0, n0+128) of a row-major fp32
+// matrix with row stride ld; chunk c of row rr sits in slot c ^ 8*((rr/4)%2).
+__device__ inline void dma_k_tile(i32x4 rs, int64_t krow0, int64_t ld, int64_t n0, uint32_t dst, int w, int lane) {
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int j = 8 * w + q;
+    const int rr = 2 * j + (lane >> 5);
+    const int c = (lane & 31) ^ (8 * ((rr >> 2) & 1));
+    tsp::dma::buffer16(rs, (uint32_t)(((krow0 + rr) * ld + n0 + c * 4) * 4), dst + j * 1024);
+  }
+}
+// The same k tile from memory that is always in bounds.
+__device__ inline void dma_k_tile_global(const float* src, int64_t ld, uint32_t dst, int w, int lane) {
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int j = 8 * w + q;
+    const int rr = 2 * j + (lane >> 5);
+    const int c = (lane & 31) ^ (8 * ((rr >> 2) & 1));
+    tsp::dma::global16(src + rr * ld + c * 4, dst + j * 1024);
+  }
+}
+
+// ---- operand fragments for v_mfma_f32_32x32x2_f32 over one 8-k group g:
+// lane half h takes k = 8g + 4h + s at k-step s (s = 0..3).
+// From a row tile: row r -> the 4 values are one 16-byte read.
+__device__ inline f32x4 frag_row(const uint8_t* tile, int r, int g, int h) {
+  return *(const f32x4*)(tile + r * TROWB + (((2 * g + h) ^ (r & 15)) * 16));
+}
+// From a k tile: column c -> 4 values from rows 8g + 4h + s.
+__device__ inline void frag_k(const uint8_t* tile, int c, int g, int h, float (&v)[4]) {
+  const uint8_t* p = tile + (8 * g + 4 * h) * KROWB + ((((c >> 2) ^ (8 * h))) * 16) + (c & 3) * 4;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) v[s] = *(const float*)(p + s * KROWB);
+}
+
+struct Acc4 {
+  f32x16 a[2][2];
+  __device__ void zero() {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) a[t][u] = f32x16{};
+  }
+  __device__ void mma(const float (&x)[2][4], const float (&y)[2][4]) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) a[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(x[t][s], y[u][s], a[t][u], 0, 0, 0);
+  }
+};
+
+// ------------------------------------------------------------- dA (SDDMM)
+
+__global__ __launch_bounds__(256) void bsr_sddmm_f32_dma(const float* __restrict__ G, int64_t ldg, int64_t m,
+                                                         const float* __restrict__ B, int64_t ldb, int64_t n,
+                                                         int64_t ncols, const int64_t* __restrict__ brow,
+                                                         const int64_t* __restrict__ ci, int64_t nnzb,
+                                                         float* __restrict__ out) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
+  // XCD-aware: XCD x takes a contiguous range of stored blocks (same block
+  // rows, so the dC panel is shared in its L2)
+  const int64_t g = blockIdx.x, xcd = g & 7, slot = g >> 3;
+  const int64_t per = tsp::ceil_div(nnzb, 8);
+  const int64_t kb = xcd * per + slot;
+  if (slot >= per || kb >= nnzb) return;
+  const int64_t i = brow[kb], j = ci[kb];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w & 1, wn = w >> 1, h = lane >> 5, l32 = lane & 31;
+  const i32x4 rsg = tsp::dma::make_rsrc(G, (uint32_t)(m * ldg * 4));
+  const i32x4 rsb = tsp::dma::make_rsrc(B, (uint32_t)(n * ldb * 4));
+  const uint32_t lds0 = tsp::dma::lds_addr(lds);
+  auto issue = [&](int s) {
+    const uint32_t st = lds0 + (s % NST) * STAGE;
+    dma_row_tile(rsg, i * BS, ldg, (int64_t)s * KC, ncols, st, w, lane);
+    dma_row_tile(rsb, j * BS, ldb, (int64_t)s * KC, ncols, st + TILE, w, lane);
+  };
+  Acc4 acc;
+  acc.zero();
+  const int ar = wm * 64 + l32, br = wn * 64 + l32;
+  struct Ops {
+    float x[2][4], y[2][4];
+  };
+  auto fetch = [&](const uint8_t* st, int gg, Ops& o) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const f32x4 a = frag_row(st, ar + 32 * t, gg, h);
+      const f32x4 b = frag_row(st + TILE, br + 32 * t, gg, h);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        o.x[t][s] = a[s];
+        o.y[t][s] = b[s];
+      }
+    }
+  };
+  const int nsteps = (int)tsp::ceil_div(ncols, KC);
+  if (nsteps > 0) issue(0);
+  for (int s = 0; s < nsteps; ++s) {
+    tsp::dma::wait_vm<0>();
+    tsp::dma::barrier();
+    if (s + 1 < nsteps) issue(s + 1);
+    const uint8_t* st = lds + (s % NST) * STAGE;
+    Ops o[2];
+    fetch(st, 0, o[0]);
+#pragma unroll
+    for (int gg = 0; gg < KC / 8; ++gg) {
+      if (gg + 1 < KC / 8) fetch(st, gg + 1, o[(gg + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      acc.mma(o[gg & 1].x, o[gg & 1].y);
+    }
+  }
+  // dA block kb, row-major [r][c]: lane holds column l32 and rows 8*(v/4) + 4h + v%4
+  float* ob = out + kb * (BS * BS);
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = wm * 64 + 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
+        ob[r * BS + wn * 64 + 32 * u + l32] = acc.a[t][u][v];
+      }
+}
+
+// ------------------------------------------------------- dB (A^T @ dC)
+
+__global__ __launch_bounds__(256) void bsr_spmm_t_f32_dma(
+    const float* __restrict__ blocks, const int64_t* __restrict__ cp, const int64_t* __restrict__ cbid,
+    const int64_t* __restrict__ crow, int64_t nbc, int nt, const float* __restrict__ X, int64_t ldx, int64_t m,
+    int64_t ncols, float* __restrict__ out, int64_t ldo, int64_t n, const int32_t* __restrict__ order) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
+  int64_t col;
+  int ntile;
+  if (!T32::tile_item(blockIdx.x, nbc, nt, order, col, ntile)) return;
+  const int64_t n0 = (int64_t)ntile * BS;
+  const int64_t start = cp[col];
+  const int nblk = (int)(cp[col + 1] - start);
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w & 1, wn = w >> 1, h = lane >> 5, l32 = lane & 31;
+  Acc4 acc;
+  acc.zero();
+  if (nblk > 0) {
+    const i32x4 rsx = tsp::dma::make_rsrc(X, (uint32_t)(m * ldx * 4));
+    const uint32_t lds0 = tsp::dma::lds_addr(lds);
+    // block ids and block rows of the column, 64 at a time in one VGPR each
+    int cbase = 0;
+    auto load_ids = [&](int base, int& idv, int& rowv) {
+      const int64_t e = start + (base + lane < nblk ? base + lane : nblk - 1);
+      idv = tsp::dma::load_lo32_sync(cbid + e);
+      rowv = tsp::dma::load_lo32_sync(crow + e);
+    };
+    int idv, rowv;
+    load_ids(0, idv, rowv);
+    auto entry = [&](int b, int64_t& kb, int64_t& ib) {
+      if (b - cbase >= 64) {
+        cbase = b & ~63;
+        load_ids(cbase, idv, rowv);
+      }
+      kb = __builtin_amdgcn_readlane(idv, b - cbase);
+      ib = __builtin_amdgcn_readlane(rowv, b - cbase);
+    };
+    auto issue = [&](int s) {
+      int64_t kb, ib;
+      entry(s >> 1, kb, ib);
+      const int kk = (s & 1) * KC;
+      const uint32_t st = lds0 + (s % NST) * STAGE;
+      // A block rows [kk, kk+64) as the [k][m] operand of A^T
+      dma_k_tile_global(blocks + kb * (BS * BS) + kk * BS, BS, st, w, lane);
+      // dC rows ib*128 + kk .. +64 (past m: zero), columns n0 .. n0+128
+      dma_k_tile(rsx, ib * BS + kk, ldx, n0, st + TILE, w, lane);
+    };
+    const int ac = wm * 64 + l32, bc = wn * 64 + l32;
+    struct Ops {
+      float x[2][4], y[2][4];
+    };
+    auto fetch = [&](const uint8_t* st, int gg, Ops& o) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        frag_k(st, ac + 32 * t, gg, h, o.x[t]);
+        frag_k(st + TILE, bc + 32 * t, gg, h, o.y[t]);
+      }
+    };
+    const int nsteps = nblk * (BS / KC);
+    issue(0);
+    for (int s = 0; s < nsteps; ++s) {
+      tsp::dma::wait_vm<0>();
+      tsp::dma::barrier();
+      if (s + 1 < nsteps) issue(s + 1);
+      const uint8_t* st = lds + (s % NST) * STAGE;
+      Ops o[2];
+      fetch(st, 0, o[0]);
+#pragma unroll
+      for (int gg = 0; gg < KC / 8; ++gg) {
+        if (gg + 1 < KC / 8) fetch(st, gg + 1, o[(gg + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        acc.mma(o[gg & 1].x, o[gg & 1].y);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int64_t r0 = col * BS + wm * 64 + 32 * t + 4 * h;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int64_t c = n0 + wn * 64 + 32 * u + l32;
+      if (c < ncols) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
+          if (r < n) out[r * ldo + c] = acc.a[t][u][v];
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------ generic
+
+template <typename T> __device__ inline typename tsp::Acc<T>::type ldv(const T* p) { return (typename tsp::Acc<T>::type)*p; }
+template <> __device__ inline float ldv<uint16_t>(const uint16_t* p) { return tsp::bf16_bits_to_f32(*p); }
+template <typename T> __device__ inline T stv(typename tsp::Acc<T>::type v) { return (T)v; }
+template <> __device__ inline uint16_t stv<uint16_t>(float v) { return tsp::f32_to_bf16_bits(v); }
+
+// dA[k][r][c] = sum_t dC[i*b + r][t] * B[j*b + c][t] (rows past m / n are zero)
+template <typename T>
+__global__ __launch_bounds__(256) void bsr_sddmm_generic(const T* __restrict__ G, int64_t ldg, int64_t m,
+                                                         const T* __restrict__ B, int64_t ldb, int64_t n, int64_t ncols,
+                                                         const int64_t* __restrict__ brow, const int64_t* __restrict__ ci,
+                                                         int64_t nnzb, int64_t b, T* __restrict__ out) {
+  typedef typename tsp::Acc<T>::type AccT;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= nnzb * b * b) return;
+  const int64_t kb = e / (b * b), rc = e - kb * b * b, r = rc / b, c = rc - r * b;
+  const int64_t gr = brow[kb] * b + r, br = ci[kb] * b + c;
+  AccT acc = 0;
+  if (gr < m && br < n)
+    for (int64_t t = 0; t < ncols; ++t) acc += ldv(G + gr * ldg + t) * ldv(B + br * ldb + t);
+  out[e] = stv<T>(acc);
+}
+
+// dB[jb*b + r][c] = sum over blocks k of column jb: sum_t A_k[t][r] * dC[i_k*b + t][c]
+template <typename T>
+__global__ __launch_bounds__(256) void bsr_spmm_t_generic(const T* __restrict__ blocks, const int64_t* __restrict__ cp,
+                                                          const int64_t* __restrict__ cbid, const int64_t* __restrict__ crow,
+                                                          int64_t b, const T* __restrict__ X, int64_t ldx, int64_t m,
+                                                          int64_t ncols, T* __restrict__ out, int64_t ldo, int64_t n) {
+  typedef typename tsp::Acc<T>::type AccT;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n * ncols) return;
+  const int64_t row = e / ncols, c = e - row * ncols;
+  const int64_t jb = row / b, r = row - jb * b;
+  AccT acc = 0;
+  for (int64_t p = cp[jb]; p < cp[jb + 1]; ++p) {
+    const T* blk = blocks + cbid[p] * b * b;
+    const int64_t xr0 = crow[p] * b;
+    for (int64_t t = 0; t < b; ++t) {
+      if (xr0 + t >= m) break;
+      acc += ldv(blk + t * b + r) * ldv(X + (xr0 + t) * ldx + c);
+    }
+  }
+  out[row * ldo + c] = stv<T>(acc);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p % 16) == 0; }
+
+}  // namespace
+
+extern "C" int tsp_bsr_sddmm(const void* G, int64_t ldg, int64_t m, const void* B, int64_t ldb, int64_t n,
+                             int64_t ncols, const int64_t* block_rows, const int64_t* block_col_indices,
+                             int64_t n_blocks, int64_t block_size, int dtype, void* grad_blocks, void* stream) {
+  if (dtype != TSP_F32 && dtype != TSP_F64 && dtype != TSP_BF16)
+    return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_sddmm: dtype %d not supported", dtype);
+  if (block_size <= 0 || m < 0 || n < 0 || ncols < 0 || n_blocks < 0) return tsp::fail(TSP_EINVAL, "tsp_bsr_sddmm: bad size");
+  if (ldg < ncols || ldb < ncols) return tsp::fail(TSP_EINVAL, "tsp_bsr_sddmm: leading dimension < ncols");
+  if (n_blocks == 0) return TSP_OK;
+  if (!G || !B || !block_rows || !block_col_indices || !grad_blocks) return tsp::fail(TSP_EINVAL, "tsp_bsr_sddmm: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == TSP_F32 && block_size == BS && ncols % 4 == 0 && ldg % 4 == 0 && ldb % 4 == 0 && aligned16(G) &&
+      aligned16(B) && (m + BS) * ldg * 4 <= (int64_t)UINT32_MAX - 64 && (n + BS) * ldb * 4 <= (int64_t)UINT32_MAX - 64) {
+    const int64_t grid = tsp::ceil_div(n_blocks, 8) * 8;
+    if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_sddmm: too many blocks");
+    hipLaunchKernelGGL(bsr_sddmm_f32_dma, dim3((unsigned)grid), dim3(256), 0, st, (const float*)G, ldg, m,
+                       (const float*)B, ldb, n, ncols, block_rows, block_col_indices, n_blocks, (float*)grad_blocks);
+    return tsp::check_launch("bsr_sddmm_f32_dma launch");
+  }
+  const int64_t total = n_blocks * block_size * block_size;
+  const int64_t grid = tsp::ceil_div(total, 256);
+  if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_sddmm: too large for the generic kernel");
+#define SDDMM_GEN(T)                                                                                              \
+  hipLaunchKernelGGL((bsr_sddmm_generic<T>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)G, ldg, m, (const T*)B, \
+                     ldb, n, ncols, block_rows, block_col_indices, n_blocks, block_size, (T*)grad_blocks)
+  if (dtype == TSP_F32)
+    SDDMM_GEN(float);
+  else if (dtype == TSP_F64)
+    SDDMM_GEN(double);
+  else
+    SDDMM_GEN(uint16_t);
+#undef SDDMM_GEN
+  return tsp::check_launch("bsr_sddmm_generic launch");
+}
+
+extern "C" int tsp_bsr_spmm_t(const void* blocks, int dtype, const int64_t* col_ptrs, const int64_t* col_block_ids,
+                              const int64_t* col_block_rows, int64_t n_block_cols, int64_t block_size, int64_t m,
+                              int64_t n, const void* X, int64_t ldx, int64_t ncols, void* out, int64_t ldo,
+                              const int32_t* col_order, void* stream) {
+  if (dtype != TSP_F32 && dtype != TSP_F64 && dtype != TSP_BF16)
+    return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm_t: dtype %d not supported", dtype);
+  if (block_size <= 0 || m < 0 || n < 0 || ncols < 0 || n_block_cols < 0) return tsp::fail(TSP_EINVAL, "tsp_bsr_spmm_t: bad size");
+  if (ldx < ncols || ldo < ncols) return tsp::fail(TSP_EINVAL, "tsp_bsr_spmm_t: leading dimension < ncols");
+  if (n == 0 || ncols == 0) return TSP_OK;
+  if (n_block_cols != tsp::ceil_div(n, block_size)) return tsp::fail(TSP_EINVAL, "tsp_bsr_spmm_t: n_block_cols != ceil(n / block_size)");
+  // blocks is only read for stored blocks (it may be null for an empty pattern)
+  if (!col_ptrs || !col_block_ids || !col_block_rows || !out || !X) return tsp::fail(TSP_EINVAL, "tsp_bsr_spmm_t: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == TSP_F32 && block_size == BS && ldx % 4 == 0 && aligned16(X) && aligned16(blocks) &&
+      (m + BS) * ldx * 4 + 4 * BS <= (int64_t)UINT32_MAX) {
+    const int64_t nt = tsp::ceil_div(ncols, BS);
+    const int64_t grid = tsp::ceil_div(n_block_cols, 8) * 8 * nt;
+    if (grid > INT32_MAX || nt > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm_t: problem too large");
+    hipLaunchKernelGGL(bsr_spmm_t_f32_dma, dim3((unsigned)grid), dim3(256), 0, st, (const float*)blocks, col_ptrs,
+                       col_block_ids, col_block_rows, n_block_cols, (int)nt, (const float*)X, ldx, m, ncols, (float*)out,
+                       ldo, n, col_order);
+    return tsp::check_launch("bsr_spmm_t_f32_dma launch");
+  }
+  const int64_t grid = tsp::ceil_div(n * ncols, 256);
+  if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm_t: too large for the generic kernel");
+#define SPMMT_GEN(T)                                                                                                     \
+  hipLaunchKernelGGL((bsr_spmm_t_generic<T>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)blocks, col_ptrs,      \
+                     col_block_ids, col_block_rows, block_size, (const T*)X, ldx, m, ncols, (T*)out, ldo, n)
+  if (dtype == TSP_F32)
+    SPMMT_GEN(float);
+  else if (dtype == TSP_F64)
+    SPMMT_GEN(double);
+  else
+    SPMMT_GEN(uint16_t);
+#undef SPMMT_GEN
+  return tsp::check_launch("bsr_spmm_t_generic launch");
+}

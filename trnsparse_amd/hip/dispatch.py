@@ -106,9 +106,9 @@ def _bsr_spmm_launch(blocks, rp, ci, order, shape, b, B, out_dtype, dev) -> torc
 class _BSRSpMMFunction(torch.autograd.Function):
     """Autograd wrapper of BSR SpMM (reference dispatch.py:290-369).
 
-    Forward: the gfx950 kernel. Backward (torch ops on the device):
-      dA_blocks[k] = dC[row block of k] @ B[col block of k]^T
-      dB           = A^T @ dC  (per stored block, scattered by column block)
+    Forward: tsp_bsr_spmm. Backward, also on the device through the C ABI:
+      dA_blocks[k] = dC[row block of k] @ B[col block of k]^T   (tsp_bsr_sddmm)
+      dB           = A^T @ dC over the block-column view        (tsp_bsr_spmm_t)
     The pattern carries no gradient.
     """
 
@@ -140,25 +140,46 @@ class _BSRSpMMFunction(torch.autograd.Function):
         mb = rp.numel() - 1
         nbc = (n + b - 1) // b
         ncols = grad_out.shape[1]
-        work = torch.float64 if A_blocks.dtype == torch.float64 else torch.float32
-        blocks = A_blocks.to(dev, work)
-        go = torch.zeros(mb * b, ncols, dtype=work, device=dev)
-        go[:m] = grad_out.to(dev, work)
-        Bp = torch.zeros(nbc * b, ncols, dtype=work, device=dev)
-        Bp[:n] = B.to(dev, work)
-        counts = rp[1:] - rp[:-1]
-        rows = torch.repeat_interleave(torch.arange(mb, device=dev), counts)
-        go_panels = go.view(mb, b, ncols)[rows]
-        grad_blocks = grad_B = None
-        if ctx.needs_input_grad[0]:
-            B_panels = Bp.view(nbc, b, ncols)[ci]
-            grad_blocks = torch.bmm(go_panels, B_panels.transpose(1, 2).contiguous())
-            grad_blocks = grad_blocks.to(A_blocks.device, A_blocks.dtype)
-        if ctx.needs_input_grad[5]:
-            contrib = torch.bmm(blocks.transpose(1, 2).contiguous(), go_panels)
-            dB = torch.zeros(nbc, b, ncols, dtype=work, device=dev).index_add_(0, ci, contrib)
-            grad_B = dB.view(nbc * b, ncols)[:n].to(B.device, B.dtype)
+        dt = A_blocks.dtype
+        code = _lib.dtype_code(dt)
+        st = _lib.stream_handle(dev)
+        with torch.cuda.device(dev):
+            blocks = _on(A_blocks, dev)
+            G = _on(grad_out, dev, dt)
+            brow, cp, cbid, crow, corder = _bsr_bwd_plan(rp, ci, mb, nbc, dev)
+            grad_blocks = grad_B = None
+            if ctx.needs_input_grad[0]:
+                Bd = _on(B, dev, dt)
+                gb = torch.empty_like(blocks)
+                _lib.call("tsp_bsr_sddmm", G.data_ptr(), ncols, m, Bd.data_ptr(), ncols, n, ncols, brow.data_ptr(),
+                          ci.data_ptr(), blocks.shape[0], b, code, gb.data_ptr(), st)
+                grad_blocks = gb.to(A_blocks.device)
+            if ctx.needs_input_grad[5]:
+                dB = torch.empty(n, ncols, dtype=dt, device=dev)
+                _lib.call("tsp_bsr_spmm_t", blocks.data_ptr(), code, cp.data_ptr(), cbid.data_ptr(), crow.data_ptr(),
+                          nbc, b, m, n, G.data_ptr(), ncols, ncols, dB.data_ptr(), ncols, corder.data_ptr(), st)
+                grad_B = dB.to(B.device, B.dtype)
         return grad_blocks, None, None, None, None, grad_B, None, None
+
+
+def _bsr_bwd_plan(rp: torch.Tensor, ci: torch.Tensor, mb: int, nbc: int, dev: torch.device):
+    """Pattern views for the backward kernels, on the device: the block row of
+    every stored block, and the block-column view (col_ptrs; per column, in
+    increasing block-row order, the stored block index and its block row),
+    plus the heaviest-first order of the block columns."""
+    counts = rp[1:] - rp[:-1]
+    brow = torch.repeat_interleave(torch.arange(mb, device=dev, dtype=torch.int64), counts)
+    nnzb = ci.numel()
+    key = ci * max(mb, 1) + brow
+    cbid = torch.sort(key, stable=True).indices.to(torch.int64)
+    crow = brow[cbid].contiguous()
+    cp = torch.zeros(nbc + 1, dtype=torch.int64, device=dev)
+    if nnzb:
+        cp[1:] = torch.cumsum(torch.bincount(ci, minlength=nbc), 0)
+    corder = torch.empty(max(nbc, 1), dtype=torch.int32, device=dev)
+    if nbc:
+        _lib.call("tsp_bsr_row_order", cp.data_ptr(), nbc, corder.data_ptr(), _lib.stream_handle(dev))
+    return brow.contiguous(), cp, cbid.contiguous(), crow, corder
 
 
 def hip_bsr_spmm(A, B: torch.Tensor, out_dtype: torch.dtype | None = None) -> torch.Tensor:

@@ -63,9 +63,12 @@ __device__ inline void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | (((N >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// Workgroup barrier without the fence of __syncthreads (which would wait for
-// all outstanding loads); the memory clobber keeps LDS accesses on their side.
-__device__ inline void barrier() { asm volatile("s_barrier" ::: "memory"); }
+// Workgroup barrier without the vector-memory part of __syncthreads' fence
+// (which would wait for every outstanding load): it waits for the wave's own
+// LDS (and scalar) operations, so ordinary LDS writes before it are visible
+// after it, and the memory clobber keeps LDS accesses on their side. Loads
+// into LDS are waited for separately (wait_vm).
+__device__ inline void barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 }  // namespace dma
 }  // namespace tsp

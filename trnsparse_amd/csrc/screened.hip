@@ -18,9 +18,14 @@
 //
 // Kernels
 //   screened_q          Q and the per-128-row-tile maximum of Q (workspace).
-//   screened_f32_mfma   fp32, 128x128 C tile per workgroup on the shared MFMA
-//                       core (mfma_f32.h); the K loop visits active k-tiles.
+//   screened_f32_dma    fp32, 128x128 C tile per workgroup, streamed MFMA
+//                       structure (direct-to-LDS slab ring, 64x64 wave
+//                       tiles); the mask multiplies the A fragments after
+//                       their LDS read; the K loop visits active k-tiles.
+//   screened_f32_mfma   the register-staged variant on the shared MFMA core
+//                       (mfma_f32.h), for operands past 4 GiB.
 //   screened_generic    f64 or unaligned operands: one thread per output.
+#include "lds_dma.h"
 #include "mfma_f32.h"
 
 namespace {
@@ -134,6 +139,168 @@ __global__ __launch_bounds__(T32::NTHR) void screened_f32_mfma(
   T32::store_tile(C, ldc, src.row0, src.n0, m, ncols, src.q, acc0, acc1, [](float v) { return v; });
 }
 
+// screened_f32_dma<QT>: fp32 A and B, the streamed MFMA structure of
+// bsr_spmm_f32_dma (4 waves of 64x64 with four 32x32x2 accumulators each,
+// 64-wide k-slabs of A [128][64] and B [64][128] through a 2-stage LDS ring
+// by direct global->LDS buffer loads, one slab ahead; rows and columns past
+// m read as zero). The mask cannot be applied while staging, so it is
+// applied to the A fragments after their LDS read: a * (Q_i*Q_k > thr ? 1 : 0)
+// in diag's precision, with Q_k of the slab staged in LDS next to the ring.
+namespace sdma {
+constexpr int KROWB = TILE * 4;        // B tile rows: 512 B
+constexpr uint32_t OOB = 0xFFFFFFF0u;
+}  // namespace sdma
+
+template <typename QT, int SKC>
+__global__ __launch_bounds__(256) void screened_f32_dma(
+    const float* __restrict__ A, int64_t lda, const QT* __restrict__ Q, const QT* __restrict__ qmax, QT thr,
+    int64_t m, const float* __restrict__ B, int64_t ldb, int64_t ncols, float* __restrict__ C, int64_t ldc, int nmt,
+    int nnt) {
+  using sdma::KROWB;
+  using sdma::OOB;
+  constexpr int TROWB = SKC * 4;         // A tile rows
+  constexpr int CPR = TROWB / 16;        // 16-byte chunks per A row
+  constexpr int TBYTES = TILE * TROWB;   // A tile == B tile bytes
+  constexpr int STAGE = 2 * TBYTES;
+  constexpr int INS = TBYTES / 1024 / 4; // 1-KiB load instructions per wave per tile
+  constexpr int ARPI = 1024 / TROWB;     // A rows per instruction
+  // slot of logical chunk c in A row r: 16 consecutive rows of one b128 read
+  // cover all 64 banks
+  auto aswz = [](int c, int r) { return CPR == 16 ? (c ^ (r & 15)) : (c ^ ((r >> 1) & 7)); };
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
+  __shared__ __attribute__((aligned(16))) QT qs[2][SKC];
+  int64_t mt64;
+  int ntile;
+  if (!T32::tile_item(blockIdx.x, nmt, nnt, nullptr, mt64, ntile)) return;
+  const int mt = (int)mt64;
+  const int64_t row0 = (int64_t)mt * TILE, n0 = (int64_t)ntile * TILE;
+  const QT qI = qmax[mt];
+  const int nkt = (int)tsp::ceil_div(m, TILE);
+  auto active = [&](int t) { return qI * qmax[t] > thr; };
+  int nact = 0;
+  for (int t = 0; t < nkt; ++t) nact += active(t) ? 1 : 0;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w & 1, wn = w >> 1, h = lane >> 5, l32 = lane & 31;
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) acc[t][u] = f32x16{};
+
+  if (nact > 0) {
+    const tsp::dma::i32x4 rsa = tsp::dma::make_rsrc(A, (uint32_t)(m * lda * 4));
+    const tsp::dma::i32x4 rsb = tsp::dma::make_rsrc(B, (uint32_t)(m * ldb * 4));
+    const uint32_t lds0 = tsp::dma::lds_addr(lds);
+    const int arow = wm * 64 + l32;
+    QT qrow[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) qrow[t] = row0 + arow + 32 * t < m ? Q[row0 + arow + 32 * t] : (QT)0;
+
+    constexpr int SPT = TILE / SKC;  // slabs per k tile
+    int kt_issue = -1;               // k tile of the slabs being issued (advanced in order)
+    QT qnext = 0;
+    auto issue = [&](int s) {
+      if ((s % SPT) == 0) {
+        ++kt_issue;
+        while (!active(kt_issue)) ++kt_issue;
+      }
+      const int64_t k0 = (int64_t)kt_issue * TILE + (s % SPT) * SKC;
+      const uint32_t st = lds0 + (s & 1) * STAGE;
+#pragma unroll
+      for (int q = 0; q < INS; ++q) {
+        const int i = INS * w + q;
+        const int r = ARPI * i + lane / CPR;
+        const int c = aswz(lane % CPR, r);
+        const int64_t col = k0 + c * 4;
+        tsp::dma::buffer16(rsa, col < m ? (uint32_t)(((row0 + r) * lda + col) * 4) : OOB, st + i * 1024);
+      }
+#pragma unroll
+      for (int q = 0; q < INS; ++q) {
+        const int j = INS * w + q;
+        const int rr = 2 * j + (lane >> 5);
+        const int c = (lane & 31) ^ (8 * ((rr >> 2) & 1));
+        tsp::dma::buffer16(rsb, (uint32_t)(((k0 + rr) * ldb + n0 + c * 4) * 4), st + TBYTES + j * 1024);
+      }
+      if (w == 0 && lane < SKC) qnext = k0 + lane < m ? Q[k0 + lane] : (QT)0;  // into qs before its barrier
+    };
+    const int bcol = wn * 64 + l32;
+    int boff[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      boff[u] = ((((bcol + 32 * u) >> 2) ^ (8 * h)) * 16) + (bcol & 3) * 4 + 4 * h * KROWB;
+    struct Ops {
+      float a[2][4];
+      float b[2][4];
+    };
+    auto fetch = [&](const uint8_t* st, const QT* qk, int g, Ops& o) {
+      QT kq[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kq[s] = qk[8 * g + 4 * h + s];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int r = arow + 32 * t;
+        const f32x4 v = *(const f32x4*)(st + r * TROWB + aswz(2 * g + h, r) * 16);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) o.a[t][s] = v[s] * ((qrow[t] * kq[s] > thr) ? 1.0f : 0.0f);
+      }
+      const uint8_t* Bs = st + TBYTES + 8 * g * KROWB;
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) o.b[u][s] = *(const float*)(Bs + s * KROWB + boff[u]);
+    };
+    auto mma = [&](const Ops& o) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+            acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.a[t][s], o.b[u][s], acc[t][u], 0, 0, 0);
+    };
+
+    const int nsteps = nact * SPT;
+    issue(0);
+    if (w == 0 && lane < SKC) qs[0][lane] = qnext;
+    for (int s = 0; s < nsteps; ++s) {
+      tsp::dma::wait_vm<0>();  // this wave's loads of slab s are done
+      tsp::dma::barrier();     // slab s and its Q_k are visible; stage (s+1) % 2 is free
+      if (s + 1 < nsteps) issue(s + 1);
+      const uint8_t* st = lds + (s & 1) * STAGE;
+      const QT* qk = qs[s & 1];
+      Ops o[2];
+      fetch(st, qk, 0, o[0]);
+#pragma unroll
+      for (int g = 0; g < SKC / 8; ++g) {
+        if (g + 1 < SKC / 8) fetch(st, qk, g + 1, o[(g + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(o[g & 1]);
+      }
+      if (w == 0 && lane < SKC && s + 1 < nsteps) qs[(s + 1) & 1][lane] = qnext;
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int64_t r0 = row0 + wm * 64 + 32 * t + 4 * h;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int64_t c = n0 + wn * 64 + 32 * u + l32;
+      if (c < ncols) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
+          if (r < m) C[r * ldc + c] = acc[t][u][v];
+        }
+      }
+    }
+  }
+}
+
+#ifndef SCREENED_KC
+#define SCREENED_KC 32
+#endif
+
 template <typename T, typename QT>
 __global__ __launch_bounds__(256) void screened_generic(const T* __restrict__ A, int64_t lda, const QT* __restrict__ Q,
                                                        QT thr, int64_t m, const T* __restrict__ B, int64_t ldb,
@@ -162,6 +329,17 @@ int launch(const void* A, int dtype, int64_t lda, const void* diag, double thr_s
   hipLaunchKernelGGL((screened_q<QT>), dim3((unsigned)nmt), dim3(TILE), 0, st, (const QT*)diag, m, Q, qmax);
   int rc = tsp::check_launch("screened_q launch");
   if (rc) return rc;
+  if (dtype == TSP_F32 && (lda % 4) == 0 && (ldb % 4) == 0 && ((uintptr_t)A % 16) == 0 && ((uintptr_t)B % 16) == 0 &&
+      (m + TILE) * lda * 4 + 4 * TILE <= (int64_t)UINT32_MAX && (m + TILE) * ldb * 4 + 4 * TILE <= (int64_t)UINT32_MAX) {
+    // (the streamed kernel's buffer offsets fit 32 bits)
+    const int64_t nnt = tsp::ceil_div(ncols, TILE);
+    const int64_t grid = tsp::ceil_div(nmt, 8) * 8 * nnt;
+    if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_screened_spmm: problem too large");
+    hipLaunchKernelGGL((screened_f32_dma<QT, SCREENED_KC>), dim3((unsigned)grid), dim3(256), 0, st, (const float*)A, lda,
+                       (const QT*)Q, (const QT*)qmax, thr, m, (const float*)B, ldb, ncols, (float*)C, ldc, (int)nmt,
+                       (int)nnt);
+    return tsp::check_launch("screened_f32_dma launch");
+  }
   if (dtype == TSP_F32 && (lda % 4) == 0 && (ldb % 4) == 0 && ((uintptr_t)A % 16) == 0 && ((uintptr_t)B % 16) == 0) {
     const int64_t nnt = tsp::ceil_div(ncols, T32::BN);
     const int64_t grid = tsp::ceil_div(nmt, 8) * 8 * nnt;

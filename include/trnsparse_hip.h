@@ -199,6 +199,48 @@ int tsp_bsa_fwd(const void* Q, const void* K, const void* V, int dtype,
                 int64_t block_size, double scale, void* O, void* row_max,
                 void* row_denom, void* stream);
 
+/* ====================================================================
+ * Block-sparse attention backward, per head h < n_heads, from the forward's
+ * output O and row stats (row_max, row_denom as tsp_bsa_fwd writes them):
+ *   D[q]     = sum_d dO[q][d] O[q][d]
+ *   P[q][k]  = exp(scale * Q[q].K[k] - row_max[q]) / row_denom[q]
+ *   dS[q][k] = P[q][k] (dO[q].V[k] - D[q])
+ *   dQ = scale * dS K,  dK = scale * dS^T Q,  dV = P^T dO
+ * over the stored mask blocks of block rows < seq_len/block_size. Q, K, V,
+ * O, dO, dQ, dK, dV (n_heads, seq_len, head_dim) contiguous in `dtype`;
+ * every element of dQ, dK, dV is written (zero where no stored block
+ * reaches). The mask comes in both views: block_row_ptrs /
+ * block_col_indices (row view, >= seq_len/block_size + 1 pointers) and
+ * col_ptrs[n_block_cols + 1] / col_block_rows (column view: the block rows
+ * below seq_len/block_size storing each block column, any order).
+ *
+ * The column pass runs over a plan made on the host by tsp_bsa_bwd_plan
+ * from a host copy of col_ptrs: call it with plan = NULL to get its length
+ * (int32 entries), then again with a buffer of that length. Its header
+ * holds n_items, n_splits, n_partials; `plan` of tsp_bsa_bwd is a device
+ * copy of the whole plan. `workspace` holds
+ * tsp_bsa_bwd_workspace_size(n_heads, seq_len, n_partials) bytes.
+ * bf16 with block_size 128 and head_dim 128 runs on the MFMA kernels; other
+ * shapes and fp32/fp64 on the generic kernels (which ignore the plan).
+ * Replaces nki_bsr_attn_bwd (trnsparse/nki/dispatch.py:813-929; its host
+ * gathers _attn_bwd_gather, dispatch.py:680-810) and the torch backward
+ * _block_sparse_attn_backward (trnsparse/ops.py:360-473).
+ * ==================================================================== */
+int64_t tsp_bsa_bwd_plan(const int64_t* col_ptrs, int64_t n_block_cols,
+                         int64_t n_heads, int64_t seq_len, int64_t block_size,
+                         int32_t* plan, int64_t capacity);
+int64_t tsp_bsa_bwd_workspace_size(int64_t n_heads, int64_t seq_len,
+                                   int64_t n_partials);
+int tsp_bsa_bwd(const void* Q, const void* K, const void* V, const void* O,
+                const void* dO, int dtype, int64_t n_heads, int64_t seq_len,
+                int64_t head_dim, const int64_t* block_row_ptrs,
+                const int64_t* block_col_indices, const int64_t* col_ptrs,
+                const int64_t* col_block_rows, int64_t n_block_cols,
+                int64_t block_size, double scale, const void* row_max,
+                const void* row_denom, void* dQ, void* dK, void* dV,
+                const int32_t* plan, int64_t n_items, int64_t n_splits,
+                int64_t n_partials, void* workspace, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,6 +22,10 @@ How each function is pinned (tests/test_oracle.py):
   hand-built values straddling fl32(1e-10) (torch's fp32 compare).
 - block_sparse_attention: dense masked softmax (numpy), a full mask equals
   dense attention, empty block rows give zeros.
+- block_sparse_attention_backward: torch float64 autograd through a dense
+  masked softmax attention (empty block rows and rows past S // b give zero
+  output there, keys past S absent), on full, local, ragged and
+  empty-row masks; the absolute form bounds the signed one.
 """
 
 from __future__ import annotations
@@ -215,6 +219,51 @@ def block_sparse_attention(Q, K, V, row_ptrs, col_idx, b, scale, rows=None):
         rmax[m] = mx
         rden[m] = den
     return out, rmax, rden
+
+
+def block_sparse_attention_backward(Q, K, V, O, dO, row_ptrs, col_idx, b, scale, row_max=None, row_denom=None,
+                                    absolute=False, rows=None, cols=None):
+    """Tiled attention backward in float64 (reference ops.py:360-473).
+
+    D = rowsum(dO * O); per stored block (m, c) of block rows m < S // b,
+    P = exp(scale * Q_m K_c^T - row_max) / row_denom, dS = P * (dO_m V_c^T -
+    D), dQ_m += scale * dS K_c, dK_c += scale * dS^T Q_m, dV_c += P^T dO_m.
+    Keys at or past S do not exist (short K_c, V_c as in the reference's
+    slices). Stats default to the oracle forward's. `rows` / `cols` restrict
+    the dQ / (dK, dV) contributions to some block rows / block columns.
+    absolute=True returns the error scale of each gradient element instead:
+    dS replaced by P * (|dO V^T| + |D|) and Q, K, dO by their magnitudes.
+    Returns (dQ, dK, dV) of shape (S, D).
+    """
+    S, Dh = Q.shape
+    Mt = S // b
+    q, k, v, o, do = (np.asarray(t, dtype=np.float64) for t in (Q, K, V, O, dO))
+    if row_max is None or row_denom is None:
+        _, row_max, row_denom = block_sparse_attention(q, k, v, row_ptrs, col_idx, b, scale)
+    rmax = np.asarray(row_max, dtype=np.float64).reshape(-1)
+    rden = np.asarray(row_denom, dtype=np.float64).reshape(-1)
+    Dv = (do * o).sum(axis=1)
+    qx, kx, dox = (np.abs(t) for t in (q, k, do)) if absolute else (q, k, do)
+    dQ, dK, dV = np.zeros((S, Dh)), np.zeros((S, Dh)), np.zeros((S, Dh))
+    rows = None if rows is None else set(int(r) for r in rows)
+    cols = None if cols is None else set(int(c) for c in cols)
+    for m in range(Mt):
+        for idx in range(row_ptrs[m], row_ptrs[m + 1]):
+            c = int(col_idx[idx])
+            want_q = rows is None or m in rows
+            want_kv = cols is None or c in cols
+            if not (want_q or want_kv) or c * b >= S:
+                continue
+            qs, ks = slice(m * b, (m + 1) * b), slice(c * b, min((c + 1) * b, S))
+            P = np.exp((q[qs] @ k[ks].T) * scale - rmax[qs, None]) / rden[qs, None]
+            dp = do[qs] @ v[ks].T
+            dS = P * (np.abs(dp) + np.abs(Dv[qs])[:, None]) if absolute else P * (dp - Dv[qs, None])
+            if want_q:
+                dQ[qs] += (dS @ kx[ks]) * scale
+            if want_kv:
+                dK[ks] += (dS.T @ qx[qs]) * scale
+                dV[ks] += P.T @ dox[qs]
+    return dQ, dK, dV
 
 
 def dense_masked_attention(Q, K, V, mask, scale):

@@ -61,3 +61,67 @@ def test_argument_validation_is_host_side():
     assert st == -1 and b"block_size" in lib.tsp_last_error()
     st = lib.tsp_bsr_spmm(None, 7, None, None, 0, 128, 1, 1, None, 1, 1, None, 1, 0, None, None)
     assert st == -2
+
+
+def _plan(cp, H, S, b):
+    import numpy as np
+
+    from trnsparse_amd.hip import _lib
+
+    lib = _lib.load()
+    cp = np.ascontiguousarray(cp, dtype=np.int64)
+    n = lib.tsp_bsa_bwd_plan(cp.ctypes.data, len(cp) - 1, H, S, b, None, 0)
+    assert n >= 4
+    plan = np.zeros(n, np.int32)
+    assert lib.tsp_bsa_bwd_plan(cp.ctypes.data, len(cp) - 1, H, S, b, plan.ctypes.data, n) == n
+    ni, ns, npart, L = plan[:4]
+    items = plan[4 : 4 + 4 * ni].reshape(-1, 4)
+    splits = plan[4 + 4 * ni :].reshape(-1, 4)
+    assert len(splits) == ns
+    return items, splits, int(npart), int(L)
+
+
+@pytest.mark.skipif(not LIB.exists(), reason="library not built (run __graft_entry__.build())")
+@pytest.mark.parametrize(
+    "counts,H,S",
+    [
+        ([64, 63] + [4] * 62, 32, 8192),   # cfg5-like: two global key columns
+        ([8, 1, 0, 5], 1, 512),            # small: L = 4, columns split, an empty column
+        ([3, 0, 2], 2, 300),               # ragged S: 3 key block columns
+        ([2, 2], 1, 200),                  # mask narrower than S? (2 columns, S needs 2)
+        ([100] * 3, 64, 384),              # L capped at 64
+    ],
+)
+def test_attention_backward_plan(counts, H, S):
+    """tsp_bsa_bwd_plan (host code): every key block column is covered, each
+    column's block rows exactly once in contiguous segments of at most L,
+    split columns own consecutive partial slots, heaviest items first."""
+    import numpy as np
+
+    b = 128
+    cp = np.concatenate([[0], np.cumsum(counts)])
+    items, splits, npart, L = _plan(cp, H, S, b)
+    ncols = -(-S // b)
+    assert 4 <= L <= 64
+    w = items[:, 2] - items[:, 1]
+    assert (np.diff(w) <= 0).all()                       # heaviest first
+    assert (w <= L).all()
+    for c in range(ncols):
+        mine = items[items[:, 0] == c]
+        mine = mine[np.argsort(mine[:, 1])]
+        n = counts[c] if c < len(counts) else 0
+        lo = cp[c] if c < len(counts) else 0
+        assert len(mine) >= 1
+        assert mine[0, 1] == lo and mine[-1, 2] == lo + n
+        assert (mine[1:, 1] == mine[:-1, 2]).all()
+        if len(mine) == 1:
+            assert mine[0, 3] == -1 and n <= L
+        else:
+            sp = splits[splits[:, 0] == c]
+            assert len(sp) == 1 and sp[0, 2] == len(mine)
+            assert sorted(mine[:, 3]) == list(range(sp[0, 1], sp[0, 1] + sp[0, 2]))
+            assert (mine[:, 3] == np.arange(sp[0, 1], sp[0, 1] + sp[0, 2])).all()
+    assert set(items[:, 0]) == set(range(ncols))
+    assert npart == sum(int(s[2]) for s in splits)
+    if counts[0] == 64:                                  # cfg5: the global columns are cut
+        assert L == 24 and len(splits) == 2   # ceil(32 * 375 / 256 / 2)

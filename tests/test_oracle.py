@@ -243,6 +243,60 @@ def test_attention_full_mask_is_dense_and_empty_rows_zero():
     assert not out[:128].any() and not rmax[0].any() and np.all(rden[0] == 1e-12)
 
 
+def _torch_masked_attention(Q, K, V, visible, scale):
+    """Dense masked softmax attention; rows with no visible key give zero."""
+    sc = torch.where(visible, (Q @ K.T) * scale, torch.tensor(-math.inf, dtype=Q.dtype))
+    has = visible.any(dim=1, keepdim=True)
+    p = torch.softmax(torch.where(has, sc, torch.zeros_like(sc)), dim=1)
+    return torch.where(has, p @ V, torch.zeros_like(Q))
+
+
+@pytest.mark.parametrize(
+    "S,D,b,mask",
+    [
+        (256, 32, 128, [[1, 1], [1, 1]]),                      # full mask
+        (48, 8, 8, [[1, 1, 0, 0, 0, 1], [1, 1, 1, 0, 0, 0], [0, 1, 1, 1, 0, 0],
+                    [0, 0, 1, 1, 1, 0], [1, 0, 0, 1, 1, 1], [0, 0, 0, 0, 1, 1]]),
+        # ragged S (Mt = 5, block column 5 holds keys 40..43 only, block row 5
+        # has no queries), an empty block row (1)
+        (44, 6, 8, [[1, 0, 0, 0, 0, 1], [0, 0, 0, 0, 0, 0], [0, 1, 1, 0, 0, 0],
+                    [1, 0, 0, 1, 0, 1], [0, 0, 1, 1, 1, 1], [1, 1, 1, 1, 1, 1]]),
+    ],
+)
+def test_attention_backward_vs_dense_autograd(S, D, b, mask):
+    """dQ, dK, dV equal torch float64 autograd through dense masked softmax
+    attention on the same visibility (query q < (S // b) b sees key k < S
+    when block (q // b, k // b) is stored)."""
+    rng = np.random.default_rng(11)
+    Q, K, V, dO = (rng.standard_normal((S, D)) for _ in range(4))
+    bm = np.array(mask, bool)
+    ptr = np.zeros(bm.shape[0] + 1, np.int64)
+    ptr[1:] = np.cumsum(bm.sum(1))
+    col = np.nonzero(bm)[1].astype(np.int64)
+    scale = D**-0.5
+    O, _, _ = ref.block_sparse_attention(Q, K, V, ptr, col, b, scale)
+    dQ, dK, dV = ref.block_sparse_attention_backward(Q, K, V, O, dO, ptr, col, b, scale)
+    Mt = S // b
+    qi, ki = np.arange(S), np.arange(S)
+    visible = (qi[:, None] < Mt * b) & bm[np.minimum(qi // b, bm.shape[0] - 1)][:, ki // b]
+    Qt, Kt, Vt = (torch.tensor(t, requires_grad=True) for t in (Q, K, V))
+    out = _torch_masked_attention(Qt, Kt, Vt, torch.tensor(visible), scale)
+    np.testing.assert_allclose(out.detach().numpy(), O, rtol=1e-10, atol=1e-12)
+    out.backward(torch.tensor(dO))
+    for got, t in ((dQ, Qt), (dK, Kt), (dV, Vt)):
+        np.testing.assert_allclose(got, t.grad.numpy(), rtol=1e-9, atol=1e-11)
+    aQ, aK, aV = ref.block_sparse_attention_backward(Q, K, V, O, dO, ptr, col, b, scale, absolute=True)
+    assert (aQ >= np.abs(dQ) - 1e-12).all() and (aK >= np.abs(dK) - 1e-12).all() and (aV >= np.abs(dV) - 1e-12).all()
+    # restricting to some block rows / columns keeps exactly those contributions
+    rQ, _, _ = ref.block_sparse_attention_backward(Q, K, V, O, dO, ptr, col, b, scale, rows=[0], cols=[])
+    np.testing.assert_array_equal(rQ[:b], dQ[:b])
+    assert not rQ[b:].any()
+    _, cK, cV = ref.block_sparse_attention_backward(Q, K, V, O, dO, ptr, col, b, scale, rows=[], cols=[1])
+    np.testing.assert_allclose(cK[b : 2 * b], dK[b : 2 * b], rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(cV[b : 2 * b], dV[b : 2 * b], rtol=1e-12, atol=1e-14)
+    assert not cK[:b].any() and not cV[2 * b :].any()
+
+
 def test_error_metrics():
     ref_ = np.array([1.0, -2.0, 0.0])
     got = np.array([1.0, -2.0 + 1e-3, 1e-6])

@@ -1,0 +1,761 @@
+// Block-sparse attention backward for gfx950.
+//
+// Semantics follow the reference tiled backward (trnsparse/ops.py:360-473),
+// per head, with the forward's row stats (row_max in natural-log units of the
+// scaled scores, row_denom):
+//   D[q]      = sum_d dO[q][d] * O[q][d]
+//   P[q][k]   = exp(scale * Q[q].K[k] - row_max[q]) / row_denom[q]
+//   dS[q][k]  = P[q][k] * (dO[q].V[k] - D[q])
+//   dQ[q]    += scale * sum_k dS[q][k] K[k]      (k over q's stored blocks)
+//   dK[k]    += scale * sum_q dS[q][k] Q[q]      (q over the query blocks that
+//   dV[k]    += sum_q P[q][k] dO[q]               store k's block)
+// Rows of Q past the last full block row, and keys that no stored block
+// covers, get zero gradient. The reference's NKI kernels split this the same
+// way (row-first dQ, column-first dK/dV over a BSC view,
+// trnsparse/nki/kernels.py:295-524); its host gathers are not needed here.
+//
+// Kernels
+//   bsa_bwd_d             D in the accumulation type (f32; f64 for f64).
+//   bsa_bwd_dq_bf16_d128  bf16, b = 128, d = 128: workgroup per (head, query
+//       block row), wavefront per 32 queries; per 64-key half
+//       S^T = K Q^T and dP^T = V dO^T on v_mfma_f32_32x32x16_bf16 with the
+//       wave's Q and dO rows in registers, P and dS in registers, then
+//       dQ^T += K^T dS^T with K read through ds_read_b64_tr_b16. K/V halves
+//       stream through a 2-stage LDS ring by direct buffer loads one half
+//       ahead.
+//   bsa_bwd_dkdv_bf16_d128  same shapes: workgroup per (head, key block
+//       column) over the block-column view of the mask, wavefront per 32 keys;
+//       per 64-query half S = Q K^T and dP = dO V^T with the wave's K and V
+//       rows in registers, then dV^T += dO^T P and dK^T += Q^T dS with Q and
+//       dO read through transpose reads. Q/dO halves and their stats stream
+//       through a 2-stage LDS ring.
+//   bsa_bwd_dq_generic / bsa_bwd_dkdv_generic  any dtype / block size /
+//       head_dim: one thread per (row, 32-wide slice of head_dim).
+// Swizzle: K (row pass) and Q, dO (column pass) are read both as 16-byte rows
+// (16 consecutive keys of one chunk) and through transpose reads (4
+// consecutive keys, 4 chunks); slot = chunk ^ (((key % 4) << 2) | ((key / 4) %
+// 4)) is conflict-free for both on the 64-bank LDS. V in the row pass is only
+// read as rows: slot = chunk ^ (key % 16).
+#include "common.h"
+
+#include "lds_dma.h"
+
+namespace {
+
+constexpr float LOG2E = 1.4426950408889634f;
+
+template <typename T> struct AAcc { typedef float type; };
+template <> struct AAcc<double> { typedef double type; };
+template <typename T> __device__ inline typename AAcc<T>::type ld(const T* p) { return (typename AAcc<T>::type)*p; }
+template <> __device__ inline float ld<uint16_t>(const uint16_t* p) { return tsp::bf16_bits_to_f32(*p); }
+template <typename T> __device__ inline T st(typename AAcc<T>::type v) { return (T)v; }
+template <> __device__ inline uint16_t st<uint16_t>(float v) { return tsp::f32_to_bf16_bits(v); }
+__device__ inline float aexp(float v) { return __expf(v); }
+__device__ inline double aexp(double v) { return exp(v); }
+
+// ------------------------------------------------------------------ D
+
+template <typename T>
+__global__ __launch_bounds__(256) void bsa_bwd_d(const T* __restrict__ O, const T* __restrict__ dO, int64_t rows,
+                                                 int64_t D, typename AAcc<T>::type* __restrict__ Dout) {
+  typedef typename AAcc<T>::type AccT;
+  // one wavefront per row
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  AccT s = 0;
+  for (int64_t d = lane; d < D; d += 64) s += ld(O + r * D + d) * ld(dO + r * D + d);
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  if (lane == 0) Dout[r] = s;
+}
+
+// -------------------------------------------------------------- generic
+
+constexpr int GEN_DC = 32;
+
+// dQ: thread per (query, head_dim slice), walking the query's stored blocks.
+// Stats are (head, Mt * b); D is (head, S).
+template <typename T>
+__global__ __launch_bounds__(128) void bsa_bwd_dq_generic(
+    const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V, const T* __restrict__ dO, int64_t S,
+    int64_t D, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci, int64_t b, int64_t Mt,
+    typename AAcc<T>::type scale, const typename AAcc<T>::type* __restrict__ rmax,
+    const typename AAcc<T>::type* __restrict__ rden, const typename AAcc<T>::type* __restrict__ Dv, T* __restrict__ dQ) {
+  typedef typename AAcc<T>::type AccT;
+  const int64_t head = blockIdx.z;
+  const int64_t q = (int64_t)blockIdx.x * 128 + threadIdx.x;
+  if (q >= S) return;
+  const int64_t d0 = (int64_t)blockIdx.y * GEN_DC;
+  const int64_t hs = head * S * D;
+  AccT acc[GEN_DC];
+#pragma unroll
+  for (int i = 0; i < GEN_DC; ++i) acc[i] = 0;
+  const int64_t m = q / b;
+  if (m < Mt) {
+    const AccT mx = rmax[head * Mt * b + q], den = rden[head * Mt * b + q], Dq = Dv[head * S + q];
+    for (int64_t idx = rp[m]; idx < rp[m + 1]; ++idx) {
+      const int64_t key0 = ci[idx] * b;
+      for (int64_t key = key0; key < key0 + b && key < S; ++key) {
+        AccT s = 0, dp = 0;
+        for (int64_t d = 0; d < D; ++d) {
+          s += ld(Q + hs + q * D + d) * ld(K + hs + key * D + d);
+          dp += ld(dO + hs + q * D + d) * ld(V + hs + key * D + d);
+        }
+        const AccT p = aexp(s * scale - mx) / den;
+        const AccT ds = p * (dp - Dq) * scale;
+#pragma unroll
+        for (int i = 0; i < GEN_DC; ++i)
+          if (d0 + i < D) acc[i] += ds * ld(K + hs + key * D + d0 + i);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < GEN_DC; ++i)
+    if (d0 + i < D) dQ[hs + q * D + d0 + i] = st<T>(acc[i]);
+}
+
+// dK, dV: thread per (key, head_dim slice), walking the block rows that store
+// the key's block column (block-column view: cp[ncols + 1] / crow). Block
+// rows at or past Mt hold no queries of the forward and are skipped.
+template <typename T>
+__global__ __launch_bounds__(128) void bsa_bwd_dkdv_generic(
+    const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V, const T* __restrict__ dO, int64_t S,
+    int64_t D, const int64_t* __restrict__ cp, const int64_t* __restrict__ crow, int64_t ncols, int64_t b, int64_t Mt,
+    typename AAcc<T>::type scale, const typename AAcc<T>::type* __restrict__ rmax,
+    const typename AAcc<T>::type* __restrict__ rden, const typename AAcc<T>::type* __restrict__ Dv, T* __restrict__ dK,
+    T* __restrict__ dV) {
+  typedef typename AAcc<T>::type AccT;
+  const int64_t head = blockIdx.z;
+  const int64_t key = (int64_t)blockIdx.x * 128 + threadIdx.x;
+  if (key >= S) return;
+  const int64_t d0 = (int64_t)blockIdx.y * GEN_DC;
+  const int64_t hs = head * S * D;
+  AccT ak[GEN_DC], av[GEN_DC];
+#pragma unroll
+  for (int i = 0; i < GEN_DC; ++i) ak[i] = av[i] = 0;
+  const int64_t c = key / b;
+  if (c < ncols) {
+    for (int64_t p0 = cp[c]; p0 < cp[c + 1]; ++p0) {
+      const int64_t m = crow[p0];
+      if (m >= Mt) continue;
+      for (int64_t q = m * b; q < m * b + b; ++q) {
+        AccT s = 0, dp = 0;
+        for (int64_t d = 0; d < D; ++d) {
+          s += ld(Q + hs + q * D + d) * ld(K + hs + key * D + d);
+          dp += ld(dO + hs + q * D + d) * ld(V + hs + key * D + d);
+        }
+        const AccT p = aexp(s * scale - rmax[head * Mt * b + q]) / rden[head * Mt * b + q];
+        const AccT ds = p * (dp - Dv[head * S + q]) * scale;
+#pragma unroll
+        for (int i = 0; i < GEN_DC; ++i) {
+          if (d0 + i < D) {
+            av[i] += p * ld(dO + hs + q * D + d0 + i);
+            ak[i] += ds * ld(Q + hs + q * D + d0 + i);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < GEN_DC; ++i) {
+    if (d0 + i < D) {
+      dK[hs + key * D + d0 + i] = st<T>(ak[i]);
+      dV[hs + key * D + d0 + i] = st<T>(av[i]);
+    }
+  }
+}
+
+template <typename T>
+int launch_generic(const void* Q, const void* K, const void* V, const void* dO, int64_t H, int64_t S, int64_t D,
+                   const int64_t* rp, const int64_t* ci, const int64_t* cp, const int64_t* crow, int64_t ncols, int64_t b,
+                   int64_t Mt, double scale, const void* rmax, const void* rden, const void* Dv, void* dQ, void* dK, void* dV,
+                   hipStream_t stream) {
+  typedef typename AAcc<T>::type AccT;
+  const int64_t gx = tsp::ceil_div(S, 128), gy = tsp::ceil_div(D, GEN_DC);
+  if (gx > INT32_MAX || gy > 65535 || H > 65535) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_bwd: problem too large for the generic kernels");
+  hipLaunchKernelGGL((bsa_bwd_dq_generic<T>), dim3((unsigned)gx, (unsigned)gy, (unsigned)H), dim3(128), 0, stream,
+                     (const T*)Q, (const T*)K, (const T*)V, (const T*)dO, S, D, rp, ci, b, Mt, (AccT)scale,
+                     (const AccT*)rmax, (const AccT*)rden, (const AccT*)Dv, (T*)dQ);
+  int rc = tsp::check_launch("bsa_bwd_dq_generic launch");
+  if (rc) return rc;
+  hipLaunchKernelGGL((bsa_bwd_dkdv_generic<T>), dim3((unsigned)gx, (unsigned)gy, (unsigned)H), dim3(128), 0, stream,
+                     (const T*)Q, (const T*)K, (const T*)V, (const T*)dO, S, D, cp, crow, ncols, b, Mt, (AccT)scale,
+                     (const AccT*)rmax, (const AccT*)rden, (const AccT*)Dv, (T*)dK, (T*)dV);
+  return tsp::check_launch("bsa_bwd_dkdv_generic launch");
+}
+
+// ------------------------------------------------------- bf16 MFMA, d = 128
+
+namespace abw {
+constexpr int D = 128;
+constexpr int BS = 128;             // block size served by the MFMA kernels
+constexpr int HR = 64;              // rows (keys in the row pass, queries in the column pass) per ring stage
+constexpr int ROWB = D * 2;         // bytes per row
+constexpr int HBYTES = HR * ROWB;   // 16 KiB
+constexpr int KS = D / 16;          // k-steps over head_dim
+constexpr int NU = D / 32;          // 32-wide head_dim subtiles
+constexpr int SEG_MAX = 64;         // most block rows one column-pass item walks
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+
+// The 16-byte chunk c of stage row r sits in slot c ^ swz(r). Rows are read
+// as 16-byte pieces of 16 consecutive rows (one chunk) and through transpose
+// reads of 4 consecutive rows (4 chunks); swz is a bijection on r % 16 whose
+// low two bits follow r / 4 and high two bits r % 4, so both access forms hit
+// 16 (resp. 4 x 4) distinct slots.
+__host__ __device__ constexpr int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+// One wave's share (rows [16w, 16w + 16)) of a 64-row half starting at global
+// row row0 of the buffer `rs`, into the stage at LDS address dst.
+__device__ inline void dma_half(tsp::dma::i32x4 rs, int64_t row0, uint32_t dst, int w, int lane) {
+#pragma unroll
+  for (int qq = 0; qq < 4; ++qq) {
+    const int j = 4 * w + qq;
+    const int rr = 4 * j + (lane >> 4);
+    const int p = lane & 15;
+    tsp::dma::buffer16(rs, (uint32_t)((row0 + rr) * ROWB + ((p ^ swz(rr)) << 4)), dst + j * 1024);
+  }
+}
+
+// A operand of v_mfma_f32_32x32x16_bf16 from stage rows r0 + [0, 32) (lane
+// row r0 + l32), head_dim chunk 2 ks + h: lane offset l32 * ROWB, kx = swz(l32) ^ h.
+__device__ inline bf16x8 row_read(const uint8_t* base, int loff, int kx, int r0, int ks) {
+  return *(const bf16x8*)(base + loff + r0 * ROWB + (((2 * ks) ^ kx) << 4));
+}
+
+// A operand holding the transpose: rows (MFMA i) are head_dim 32u + l32 and
+// the 8 k values are stage rows r0 + 4h + {0..3} and r0 + 8 + 4h + {0..3}
+// (the k order of the lane's own accumulator rows), from two
+// ds_read_b64_tr_b16: lane j of 16-lane group gq points at row
+// r0 + 8 rr + 4 (gq / 2) + j / 4, column 32u + 16 (gq % 2) + 4 (j % 4).
+struct TrLane {
+  int off[2];
+  int xu;
+};
+__device__ inline TrLane tr_lane(int lane) {
+  const int gq = lane >> 4, jq = lane & 15;
+  const int c0 = 2 * (gq & 1) + ((jq & 3) >> 1);
+  TrLane t;
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int row = 8 * rr + 4 * (gq >> 1) + (jq >> 2);
+    t.off[rr] = row * ROWB + ((c0 ^ (swz(row) & 3)) << 4) + 8 * (jq & 1);
+  }
+  t.xu = jq >> 2;  // swz(row) >> 2
+  return t;
+}
+__device__ inline bf16x8 tr_read(const uint8_t* base, const TrLane& t, int r0, int u) {
+  s16x4 r[2];
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr)
+    r[rr] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + t.off[rr] + r0 * ROWB + ((u ^ t.xu) << 6)));
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7));
+}
+}  // namespace abw
+
+// Row pass: workgroup per (head, query block row m < Mt), XCD-aware order as
+// the forward (XCD x walks heads x, x + 8, ...; block rows of one head side by
+// side share its K/V in L2). Also computes D and leaves the per-query stats
+// for the column pass in qstat planes (log2e * row_max, 1 / row_denom, D).
+__global__ __launch_bounds__(256, 2) void bsa_bwd_dq_bf16_d128(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+    const uint16_t* __restrict__ O, const uint16_t* __restrict__ dO, int64_t S, int64_t H,
+    const int64_t* __restrict__ rp, const int64_t* __restrict__ ci, int64_t Mt, float scale_log2, float scale,
+    const float* __restrict__ rmax, const float* __restrict__ rden, float* __restrict__ qstat,
+    uint16_t* __restrict__ dQ) {
+  using namespace abw;
+  constexpr int STAGE = 2 * HBYTES;  // K half, V half
+  constexpr int NST = 2;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
+
+  const int64_t g = blockIdx.x;
+  const int64_t xcd = g & 7, slot = g >> 3;
+  const int64_t head = xcd + 8 * (slot / Mt);
+  const int64_t m = slot % Mt;
+  if (head >= H) return;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int64_t hs = head * S * D;
+  const int64_t q = m * BS + w * 32 + l32;  // < S since m < Mt
+
+  // Q and dO rows of the lane's query as B operands: [16 ks + 8 h, +8)
+  bf16x8 qf[KS], dof[KS];
+  float dsum = 0.f;
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    qf[s] = *(const bf16x8*)(Q + hs + q * D + 16 * s + 8 * h);
+    dof[s] = *(const bf16x8*)(dO + hs + q * D + 16 * s + 8 * h);
+    const bf16x8 of = *(const bf16x8*)(O + hs + q * D + 16 * s + 8 * h);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dsum += (float)dof[s][i] * (float)of[i];
+  }
+  const float Dq = dsum + __shfl_xor(dsum, 32, 64);
+  const float rml2 = rmax[head * Mt * BS + q] * LOG2E;
+  const float inv = 1.f / rden[head * Mt * BS + q];
+  if (h == 0) {
+    const int64_t HS = H * S;
+    qstat[head * S + q] = rml2;
+    qstat[HS + head * S + q] = inv;
+    qstat[2 * HS + head * S + q] = Dq;
+  }
+
+  f32x16 acc[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) acc[u] = f32x16{};
+
+  const int64_t start = rp[m];
+  const int nblk = (int)(rp[m + 1] - start);
+  const int nsteps = 2 * nblk;
+  const tsp::dma::i32x4 krs = tsp::dma::make_rsrc(K + hs, (uint32_t)(S * ROWB));
+  const tsp::dma::i32x4 vrs = tsp::dma::make_rsrc(V + hs, (uint32_t)(S * ROWB));
+  const uint32_t lds0 = tsp::dma::lds_addr(lds);
+
+  // key-block indices of the row, 64 at a time in one VGPR, read with readlane
+  int cbase = 0, cv = 0;
+  auto load_cols = [&](int base) {
+    const int i = base + lane < nblk ? base + lane : nblk - 1;
+    return tsp::dma::load_lo32_sync(ci + start + i);
+  };
+  if (nblk > 0) cv = load_cols(0);
+  auto first_key = [&](int s) {
+    const int blk = s >> 1;
+    if (blk - cbase >= 64) {
+      cbase = blk & ~63;
+      cv = load_cols(cbase);
+    }
+    return (int64_t)__builtin_amdgcn_readlane(cv, blk - cbase) * BS + HR * (s & 1);
+  };
+  auto issue = [&](int64_t key0, int s) {
+    const uint32_t st = lds0 + (s % NST) * STAGE;
+    dma_half(krs, key0, st, w, lane);
+    dma_half(vrs, key0, st + HBYTES, w, lane);
+  };
+
+  const int loff = l32 * ROWB;
+  const int kx = swz(l32) ^ h;
+  const TrLane trl = tr_lane(lane);
+  const float nrml2 = -rml2;
+
+  auto compute = [&](const uint8_t* st, int64_t key0) {
+    const uint8_t* Ks = st;
+    const uint8_t* Vs = st + HBYTES;
+    const bool tail = key0 + HR > S;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      // S^T and dP^T tiles: keys 32 tt + 8 (v / 4) + 4 h + v % 4, query l32
+      f32x16 sc = f32x16{}, dp = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_read(Ks, loff, kx, 32 * tt, ks), qf[ks], sc, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_read(Vs, loff, kx, 32 * tt, ks), dof[ks], dp, 0, 0, 0);
+      }
+      // P = exp(scale s - row_max) / row_denom, dS = P (dP - D); keys at or
+      // past S (zero rows of the stage) get P = 0
+      bf16x8 db[2];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        f32x8 dv;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int v = 8 * a + i;
+          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[v], scale_log2, nrml2)) * inv;
+          if (tail && key0 + 32 * tt + 8 * (v >> 2) + 4 * h + (v & 3) >= S) p = 0.f;
+          dv[i] = p * (dp[v] - Dq);
+        }
+        db[a] = __builtin_convertvector(dv, bf16x8);
+      }
+      // dQ^T += K^T dS^T over the tile's 32 keys (k-steps a = 0, 1)
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+          acc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_read(Ks, trl, 32 * tt + 16 * a, u), db[a], acc[u], 0, 0, 0);
+    }
+  };
+
+  if (nsteps > 0) issue(first_key(0), 0);
+  for (int s = 0; s < nsteps; ++s) {
+    const int64_t key0 = first_key(s);
+    tsp::dma::wait_vm<0>();  // this wave's loads of half s are done
+    tsp::dma::barrier();     // every wave's part is in LDS; the other stage is free
+    if (s + 1 < nsteps) issue(first_key(s + 1), s + 1);
+    compute(lds + (s % NST) * STAGE, key0);
+  }
+
+  // dQ[q][32 u + 8 g4 + 4 h + i] = scale * acc[u][4 g4 + i]
+  uint16_t* dq = dQ + hs + q * D;
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      u16x4 t;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t[i] = tsp::f32_to_bf16_bits(acc[u][4 * g4 + i] * scale);
+      *(u16x4*)(dq + 32 * u + 8 * g4 + 4 * h) = t;
+    }
+  }
+}
+
+// Column pass: one item = (block column, range [p0, p1) of its column view,
+// partial slot or -1) for every head; items heaviest first, heads of one XCD
+// inner (XCD x walks heads x, x + 8, ...). Wavefront w owns keys
+// col * 128 + 32 w + [0, 32) with the K and V rows in registers; 64-query
+// halves of Q, dO and their stats stream through a 3-stage LDS ring.
+// dK^T += scale Q^T dS and dV^T += dO^T P accumulate in registers; an item
+// covering a whole column writes bf16 dK / dV, a segment of a split column
+// writes fp32 partials that bsa_bwd_reduce sums in segment order.
+__global__ __launch_bounds__(256, 1) void bsa_bwd_dkdv_bf16_d128(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+    const uint16_t* __restrict__ dO, int64_t S, int64_t H, int nh, const int64_t* __restrict__ crow,
+    const int32_t* __restrict__ items, int n_partials, float scale_log2, float scale, const float* __restrict__ qstat,
+    uint16_t* __restrict__ dK, uint16_t* __restrict__ dV, float* __restrict__ partial) {
+  using namespace abw;
+  constexpr int STAGE = 2 * HBYTES + 1024;  // Q half, dO half, stats [4][64] floats
+  constexpr int NST = 3;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
+
+  const int64_t g = blockIdx.x;
+  const int64_t xcd = g & 7, slot = g >> 3;
+  const int64_t it = slot / nh;
+  const int64_t head = xcd + 8 * (slot % nh);
+  if (head >= H) return;
+  const int col = items[4 * it], p0 = items[4 * it + 1], p1 = items[4 * it + 2], pslot = items[4 * it + 3];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int64_t hs = head * S * D;
+  const int64_t key = (int64_t)col * BS + w * 32 + l32;
+  const bool kvalid = key < S;
+
+  bf16x8 kf[KS], vf[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    kf[s] = kvalid ? *(const bf16x8*)(K + hs + key * D + 16 * s + 8 * h) : bf16x8{};
+    vf[s] = kvalid ? *(const bf16x8*)(V + hs + key * D + 16 * s + 8 * h) : bf16x8{};
+  }
+  f32x16 dk[NU], dv[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) dk[u] = dv[u] = f32x16{};
+
+  const int nblk = p1 - p0;  // <= SEG_MAX
+  const int nsteps = 2 * nblk;
+  // block rows of the item, one per lane
+  const int rv = nblk > 0 ? tsp::dma::load_lo32_sync(crow + p0 + (lane < nblk ? lane : nblk - 1)) : 0;
+  const tsp::dma::i32x4 qrs = tsp::dma::make_rsrc(Q + hs, (uint32_t)(S * ROWB));
+  const tsp::dma::i32x4 ors = tsp::dma::make_rsrc(dO + hs, (uint32_t)(S * ROWB));
+  const uint32_t lds0 = tsp::dma::lds_addr(lds);
+  const int64_t HS = H * S;
+  const int splane = (lane >> 4) < 2 ? (lane >> 4) : 2;
+  const float* sbase = qstat + splane * HS + head * S + 4 * (lane & 15);
+
+  auto first_q = [&](int s) { return (int64_t)__builtin_amdgcn_readlane(rv, s >> 1) * BS + HR * (s & 1); };
+  auto issue = [&](int s) {
+    const int64_t q0 = first_q(s);
+    const uint32_t st = lds0 + (s % NST) * STAGE;
+    dma_half(qrs, q0, st, w, lane);
+    dma_half(ors, q0, st + HBYTES, w, lane);
+    if (w == 0) tsp::dma::global16(sbase + q0, st + 2 * HBYTES);
+  };
+
+  const int loff = l32 * ROWB;
+  const int kx = swz(l32) ^ h;
+  const TrLane trl = tr_lane(lane);
+
+  auto compute = [&](const uint8_t* st) {
+    const uint8_t* Qs = st;
+    const uint8_t* Os = st + HBYTES;
+    const float* stt = (const float*)(st + 2 * HBYTES);
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      // S and dP tiles: queries 32 qt + 8 (v / 4) + 4 h + v % 4, key l32
+      f32x16 sc = f32x16{}, dp = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_read(Qs, loff, kx, 32 * qt, ks), kf[ks], sc, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_read(Os, loff, kx, 32 * qt, ks), vf[ks], dp, 0, 0, 0);
+      }
+      bf16x8 pb[2], db[2];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        f32x8 pv, dsv;
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg) {
+          const int ql = 32 * qt + 8 * (2 * a + gg) + 4 * h;
+          const f32x4 rm = *(const f32x4*)(stt + ql);
+          const f32x4 iv = *(const f32x4*)(stt + 64 + ql);
+          const f32x4 dd = *(const f32x4*)(stt + 128 + ql);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int v = 8 * a + 4 * gg + i;
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[v], scale_log2, -rm[i])) * iv[i];
+            pv[4 * gg + i] = p;
+            dsv[4 * gg + i] = p * (dp[v] - dd[i]);
+          }
+        }
+        pb[a] = __builtin_convertvector(pv, bf16x8);
+        db[a] = __builtin_convertvector(dsv, bf16x8);
+      }
+      // dV^T += dO^T P and dK^T += Q^T dS over the tile's 32 queries
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+          dv[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_read(Os, trl, 32 * qt + 16 * a, u), pb[a], dv[u], 0, 0, 0);
+          dk[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_read(Qs, trl, 32 * qt + 16 * a, u), db[a], dk[u], 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  if (nsteps > 0) issue(0);
+  if (nsteps > 1) issue(1);
+  for (int s = 0; s < nsteps; ++s) {
+    // loads of half s are done once at most one half (8 or 9 loads) is outstanding
+    if (s + 1 < nsteps)
+      tsp::dma::wait_vm<8>();
+    else
+      tsp::dma::wait_vm<0>();
+    tsp::dma::barrier();  // every wave's part is in LDS; stage (s + 2) % 3 is free
+    if (s + 2 < nsteps) issue(s + 2);
+    compute(lds + (s % NST) * STAGE);
+  }
+
+  // lane holds dK^T / dV^T [32 u + 8 g4 + 4 h + i][key]
+  if (pslot < 0) {
+    if (!kvalid) return;
+    uint16_t* pk = dK + hs + key * D;
+    uint16_t* pv = dV + hs + key * D;
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        u16x4 tk, tv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          tk[i] = tsp::f32_to_bf16_bits(dk[u][4 * g4 + i] * scale);
+          tv[i] = tsp::f32_to_bf16_bits(dv[u][4 * g4 + i]);
+        }
+        *(u16x4*)(pk + 32 * u + 8 * g4 + 4 * h) = tk;
+        *(u16x4*)(pv + 32 * u + 8 * g4 + 4 * h) = tv;
+      }
+    }
+  } else {
+    float* pk = partial + ((head * n_partials + pslot) * 2) * (BS * D) + (w * 32 + l32) * D;
+    float* pv = pk + BS * D;
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        f32x4 tk, tv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          tk[i] = dk[u][4 * g4 + i] * scale;
+          tv[i] = dv[u][4 * g4 + i];
+        }
+        *(f32x4*)(pk + 32 * u + 8 * g4 + 4 * h) = tk;
+        *(f32x4*)(pv + 32 * u + 8 * g4 + 4 * h) = tv;
+      }
+    }
+  }
+}
+
+// dK / dV of the split columns: sum of the segments' partials in segment
+// order (deterministic), rounded to bf16. Workgroup per (split, head).
+__global__ __launch_bounds__(256) void bsa_bwd_reduce(const int32_t* __restrict__ splits, int n_partials, int64_t S,
+                                                      const float* __restrict__ partial, uint16_t* __restrict__ dK,
+                                                      uint16_t* __restrict__ dV) {
+  using namespace abw;
+  const int sp = blockIdx.x;
+  const int64_t head = blockIdx.y;
+  const int col = splits[4 * sp], slot0 = splits[4 * sp + 1], nseg = splits[4 * sp + 2];
+  const float* base = partial + (head * n_partials + slot0) * 2 * (BS * D);
+  for (int e = threadIdx.x; e < 2 * BS * (D / 4); e += 256) {
+    const int which = e / (BS * (D / 4));
+    const int r = (e / (D / 4)) % BS, d4 = e % (D / 4);
+    const int64_t key = (int64_t)col * BS + r;
+    if (key >= S) continue;
+    f32x4 sum = f32x4{};
+    for (int j = 0; j < nseg; ++j) sum += *(const f32x4*)(base + (j * 2 + which) * (BS * D) + r * D + 4 * d4);
+    u16x4 t;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[i] = tsp::f32_to_bf16_bits(sum[i]);
+    *(u16x4*)((which ? dV : dK) + (head * S + key) * D + 4 * d4) = t;
+  }
+}
+
+}  // namespace
+
+// Host-side plan of the column pass. Items cover every key block column
+// c < ceil(seq_len / block_size) (columns without stored blocks write zeros);
+// a column with more than L stored block rows is cut into ceil(n / L) nearly
+// equal segments with partial slots 0, 1, ... in column order. L follows the
+// work per CU (n_heads * blocks / 256 CUs, halved, clamped to [4, 64]) so
+// that no single item dominates. Items are sorted heaviest first (ties by
+// column). Layout (int32): n_items, n_splits, n_partials, L; items
+// (col, p_begin, p_end, slot or -1) x n_items; splits (col, slot0, n_seg, 0)
+// x n_splits.
+extern "C" int64_t tsp_bsa_bwd_plan(const int64_t* col_ptrs, int64_t n_block_cols, int64_t n_heads, int64_t seq_len,
+                                    int64_t block_size, int32_t* plan, int64_t capacity) {
+  if (n_block_cols < 0 || n_heads < 0 || seq_len < 0 || block_size <= 0 || (n_block_cols > 0 && !col_ptrs)) {
+    tsp::fail(TSP_EINVAL, "tsp_bsa_bwd_plan: bad argument");
+    return -1;
+  }
+  const int64_t ncols = tsp::ceil_div(seq_len, block_size);
+  int64_t nnzb = 0;
+  for (int64_t c = 0; c < ncols && c < n_block_cols; ++c) nnzb += col_ptrs[c + 1] - col_ptrs[c];
+  if (n_block_cols > 0 && col_ptrs[n_block_cols] > INT32_MAX) {
+    tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_bwd_plan: too many blocks");
+    return -1;
+  }
+  int64_t L = (int64_t)((double)n_heads * (double)nnzb / 256.0 / 2.0 + 0.999);
+  L = L < 4 ? 4 : (L > abw::SEG_MAX ? abw::SEG_MAX : L);
+  struct Item { int32_t col, p0, p1, slot, weight; };
+  Item* items = new Item[ncols + nnzb / L + 1];
+  int32_t* splits = new int32_t[4 * (nnzb / (L + 1) + 1)];
+  int64_t ni = 0, ns = 0, np = 0;
+  for (int64_t c = 0; c < ncols; ++c) {
+    const int64_t b0 = c < n_block_cols ? col_ptrs[c] : 0;
+    const int64_t n = c < n_block_cols ? col_ptrs[c + 1] - b0 : 0;
+    if (n <= L) {
+      items[ni++] = Item{(int32_t)c, (int32_t)b0, (int32_t)(b0 + n), -1, (int32_t)n};
+      continue;
+    }
+    const int64_t nseg = (n + L - 1) / L, base = n / nseg, rem = n % nseg;
+    splits[4 * ns] = (int32_t)c;
+    splits[4 * ns + 1] = (int32_t)np;
+    splits[4 * ns + 2] = (int32_t)nseg;
+    splits[4 * ns + 3] = 0;
+    ++ns;
+    int64_t p = b0;
+    for (int64_t j = 0; j < nseg; ++j) {
+      const int64_t len = base + (j < rem ? 1 : 0);
+      items[ni++] = Item{(int32_t)c, (int32_t)p, (int32_t)(p + len), (int32_t)(np + j), (int32_t)len};
+      p += len;
+    }
+    np += nseg;
+  }
+  // heaviest first, stable in column order (insertion into weight buckets)
+  const int64_t need = 4 + 4 * ni + 4 * ns;
+  if (plan && capacity >= need) {
+    plan[0] = (int32_t)ni;
+    plan[1] = (int32_t)ns;
+    plan[2] = (int32_t)np;
+    plan[3] = (int32_t)L;
+    int64_t o = 4;
+    for (int64_t wgt = L; wgt >= 0; --wgt)
+      for (int64_t i = 0; i < ni; ++i)
+        if (items[i].weight == wgt) {
+          plan[o++] = items[i].col;
+          plan[o++] = items[i].p0;
+          plan[o++] = items[i].p1;
+          plan[o++] = items[i].slot;
+        }
+    for (int64_t i = 0; i < 4 * ns; ++i) plan[o++] = splits[i];
+  }
+  delete[] items;
+  delete[] splits;
+  return need;
+}
+
+extern "C" int64_t tsp_bsa_bwd_workspace_size(int64_t n_heads, int64_t seq_len, int64_t n_partials) {
+  if (n_heads < 0 || seq_len < 0 || n_partials < 0) return -1;
+  return 16 * n_heads * seq_len + n_heads * n_partials * 2 * abw::BS * abw::D * 4;
+}
+
+extern "C" int tsp_bsa_bwd(const void* Q, const void* K, const void* V, const void* O, const void* dO, int dtype,
+                           int64_t n_heads, int64_t seq_len, int64_t head_dim, const int64_t* block_row_ptrs,
+                           const int64_t* block_col_indices, const int64_t* col_ptrs, const int64_t* col_block_rows,
+                           int64_t n_block_cols, int64_t block_size, double scale, const void* row_max,
+                           const void* row_denom, void* dQ, void* dK, void* dV, const int32_t* plan, int64_t n_items,
+                           int64_t n_splits, int64_t n_partials, void* workspace, void* stream) {
+  if (dtype != TSP_F32 && dtype != TSP_F64 && dtype != TSP_BF16)
+    return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_bwd: dtype %d not supported", dtype);
+  if (n_heads < 0 || seq_len < 0 || head_dim < 0 || block_size <= 0 || n_block_cols < 0 || n_items < 0 ||
+      n_splits < 0 || n_partials < 0)
+    return tsp::fail(TSP_EINVAL, "tsp_bsa_bwd: bad size");
+  if (n_heads == 0 || seq_len == 0 || head_dim == 0) return TSP_OK;
+  if (!Q || !K || !V || !O || !dO || !block_row_ptrs || !block_col_indices || !col_ptrs || !col_block_rows || !row_max ||
+      !row_denom || !dQ || !dK || !dV || !workspace)
+    return tsp::fail(TSP_EINVAL, "tsp_bsa_bwd: null pointer");
+  hipStream_t stream_ = (hipStream_t)stream;
+  const int64_t Mt = seq_len / block_size;
+  const int64_t rows = n_heads * seq_len;
+
+  const bool aligned = ((uintptr_t)Q % 16) == 0 && ((uintptr_t)K % 16) == 0 && ((uintptr_t)V % 16) == 0 &&
+                       ((uintptr_t)O % 16) == 0 && ((uintptr_t)dO % 16) == 0 && ((uintptr_t)dQ % 8) == 0 &&
+                       ((uintptr_t)dK % 8) == 0 && ((uintptr_t)dV % 8) == 0 && ((uintptr_t)workspace % 16) == 0;
+  if (dtype == TSP_BF16 && block_size == abw::BS && head_dim == abw::D && scale > 0 && plan && aligned &&
+      (seq_len + abw::BS) * abw::ROWB <= (int64_t)UINT32_MAX) {
+    if (n_items < tsp::ceil_div(seq_len, block_size))
+      return tsp::fail(TSP_EINVAL, "tsp_bsa_bwd: plan has %lld items for %lld key block columns", (long long)n_items,
+                       (long long)tsp::ceil_div(seq_len, block_size));
+    const int64_t nh = tsp::ceil_div(n_heads, 8);
+    const int64_t grid_a = nh * Mt * 8, grid_b = nh * n_items * 8;
+    if (grid_a > INT32_MAX || grid_b > INT32_MAX || n_splits > INT32_MAX || n_heads > 65535)
+      return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_bwd: problem too large");
+    const float sl2 = (float)(scale * 1.4426950408889634);
+    float* qstat = (float*)workspace;
+    float* partial = (float*)((char*)workspace + 16 * rows);
+    if (Mt * block_size < seq_len) {  // rows without a block row: zero dQ
+      const int64_t tail = (seq_len - Mt * block_size) * head_dim * 2;
+      for (int64_t hh = 0; hh < n_heads; ++hh) {
+        int rc = tsp::zero_fill((char*)dQ + (hh * seq_len + Mt * block_size) * head_dim * 2, tail, stream_);
+        if (rc) return rc;
+      }
+    }
+    if (grid_a > 0) {
+      hipLaunchKernelGGL(bsa_bwd_dq_bf16_d128, dim3((unsigned)grid_a), dim3(256), 0, stream_, (const uint16_t*)Q,
+                         (const uint16_t*)K, (const uint16_t*)V, (const uint16_t*)O, (const uint16_t*)dO, seq_len,
+                         n_heads, block_row_ptrs, block_col_indices, Mt, sl2, (float)scale, (const float*)row_max,
+                         (const float*)row_denom, qstat, (uint16_t*)dQ);
+      int rc = tsp::check_launch("bsa_bwd_dq_bf16_d128 launch");
+      if (rc) return rc;
+    }
+    if (grid_b > 0) {
+      hipLaunchKernelGGL(bsa_bwd_dkdv_bf16_d128, dim3((unsigned)grid_b), dim3(256), 0, stream_, (const uint16_t*)Q,
+                         (const uint16_t*)K, (const uint16_t*)V, (const uint16_t*)dO, seq_len, n_heads, (int)nh,
+                         col_block_rows, plan + 4, (int)n_partials, sl2, (float)scale, (const float*)qstat,
+                         (uint16_t*)dK, (uint16_t*)dV, partial);
+      int rc = tsp::check_launch("bsa_bwd_dkdv_bf16_d128 launch");
+      if (rc) return rc;
+    }
+    if (n_splits > 0) {
+      hipLaunchKernelGGL(bsa_bwd_reduce, dim3((unsigned)n_splits, (unsigned)n_heads), dim3(256), 0, stream_,
+                         plan + 4 + 4 * n_items, (int)n_partials, seq_len, (const float*)partial, (uint16_t*)dK,
+                         (uint16_t*)dV);
+      int rc = tsp::check_launch("bsa_bwd_reduce launch");
+      if (rc) return rc;
+    }
+    return TSP_OK;
+  }
+
+  // D = rowsum(dO * O) into the workspace
+  {
+    const int64_t grid = tsp::ceil_div(rows, 4);
+    if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_bwd: too many rows");
+    if (dtype == TSP_F32)
+      hipLaunchKernelGGL(bsa_bwd_d<float>, dim3((unsigned)grid), dim3(256), 0, stream_, (const float*)O, (const float*)dO,
+                         rows, head_dim, (float*)workspace);
+    else if (dtype == TSP_F64)
+      hipLaunchKernelGGL(bsa_bwd_d<double>, dim3((unsigned)grid), dim3(256), 0, stream_, (const double*)O,
+                         (const double*)dO, rows, head_dim, (double*)workspace);
+    else
+      hipLaunchKernelGGL(bsa_bwd_d<uint16_t>, dim3((unsigned)grid), dim3(256), 0, stream_, (const uint16_t*)O,
+                         (const uint16_t*)dO, rows, head_dim, (float*)workspace);
+    int rc = tsp::check_launch("bsa_bwd_d launch");
+    if (rc) return rc;
+  }
+  if (dtype == TSP_F64)
+    return launch_generic<double>(Q, K, V, dO, n_heads, seq_len, head_dim, block_row_ptrs, block_col_indices, col_ptrs,
+                                  col_block_rows, n_block_cols, block_size, Mt, scale, row_max, row_denom, workspace, dQ, dK, dV,
+                                  stream_);
+  if (dtype == TSP_F32)
+    return launch_generic<float>(Q, K, V, dO, n_heads, seq_len, head_dim, block_row_ptrs, block_col_indices, col_ptrs,
+                                 col_block_rows, n_block_cols, block_size, Mt, scale, row_max, row_denom, workspace, dQ, dK, dV, stream_);
+  return launch_generic<uint16_t>(Q, K, V, dO, n_heads, seq_len, head_dim, block_row_ptrs, block_col_indices, col_ptrs,
+                                  col_block_rows, n_block_cols, block_size, Mt, scale, row_max, row_denom, workspace, dQ, dK, dV,
+                                  stream_);
+}

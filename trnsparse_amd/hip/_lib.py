@@ -48,6 +48,13 @@ SIGNATURES: dict[str, tuple] = {
     "tsp_screened_workspace_size": (_I64, [_I64, _INT]),
     "tsp_screened_spmm": (_INT, [_P, _INT, _I64, _P, _INT, _DBL, _I64, _P, _I64, _I64, _P, _I64, _P, _P]),
     "tsp_bsa_fwd": (_INT, [_P, _P, _P, _INT, _I64, _I64, _I64, _P, _P, _I64, _DBL, _P, _P, _P, _P]),
+    "tsp_bsa_bwd_plan": (_I64, [_P, _I64, _I64, _I64, _I64, _P, _I64]),
+    "tsp_bsa_bwd_workspace_size": (_I64, [_I64, _I64, _I64]),
+    "tsp_bsa_bwd": (
+        _INT,
+        [_P, _P, _P, _P, _P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _DBL, _P, _P, _P, _P, _P,
+         _P, _I64, _I64, _I64, _P, _P],
+    ),
 }
 
 _lib = None

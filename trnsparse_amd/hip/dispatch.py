@@ -7,13 +7,16 @@ and the result is returned on the caller's device, as the reference's
 `_to_xla` / `.to(orig_device)` round trip does, dispatch.py:88-94),
 prepares the cached per-pattern plan, allocates outputs and calls the C ABI
 on the current HIP stream. Autograd wrappers keep the reference's
-signatures; their backward passes run as torch ops on the device.
+signatures; the BSR SpMM and attention backward passes call their own
+kernels through the C ABI, the screened SpMM backward (two dense masked
+products) runs as torch ops on the device.
 
 Kernel failures raise RuntimeError; nothing falls back to another path.
 """
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -417,3 +420,88 @@ def hip_block_sparse_attention(Q, K, V, mask_bsr, scale: float, return_stats: bo
     if not return_stats:
         return out
     return out, rmax.reshape(*lead, Mt, b).to(orig), rden.reshape(*lead, Mt, b).to(orig)
+
+
+def _attn_bwd_plan(mask_bsr, H: int, S: int, dev: torch.device):
+    """Column view of the mask restricted to the block rows below S // b and
+    the column-pass plan (tsp_bsa_bwd_plan), built on the host and copied to
+    the device. Cached on the mask's column-index tensor, keyed by the
+    pattern's identity and version and (H, S, device).
+
+    Returns (col_ptrs, col_block_rows, n_block_cols, plan, header) with
+    header = (n_items, n_splits, n_partials).
+    """
+    b = mask_bsr.block_size
+    Mt = S // b
+    ci_t, rp_t = mask_bsr.block_col_indices, mask_bsr.block_row_ptrs
+    key = (rp_t.data_ptr(), rp_t._version, rp_t.numel(), ci_t._version, ci_t.numel(), int(mask_bsr.shape[1]), H, S,
+           str(dev))
+    hit = getattr(ci_t, "_tsp_attn_bwd_plan", None)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    rp = rp_t.detach().to("cpu", torch.int64).numpy()
+    ci = ci_t.detach().to("cpu", torch.int64).numpy()
+    end = int(rp[Mt])
+    ci = ci[:end]
+    nbc = (int(mask_bsr.shape[1]) + b - 1) // b
+    if ci.size:
+        nbc = max(nbc, int(ci.max()) + 1)
+    brow = np.repeat(np.arange(Mt, dtype=np.int64), np.diff(rp[: Mt + 1]))
+    order = np.argsort(ci * max(Mt, 1) + brow, kind="stable")
+    crow = np.ascontiguousarray(brow[order])
+    cp = np.zeros(nbc + 1, dtype=np.int64)
+    if ci.size:
+        cp[1:] = np.cumsum(np.bincount(ci, minlength=nbc))
+    lib = _lib.load()
+    n = lib.tsp_bsa_bwd_plan(cp.ctypes.data, nbc, H, S, b, None, 0)
+    if n < 4:
+        raise RuntimeError(f"tsp_bsa_bwd_plan failed: {_lib.last_error()}")
+    plan = np.empty(n, dtype=np.int32)
+    if lib.tsp_bsa_bwd_plan(cp.ctypes.data, nbc, H, S, b, plan.ctypes.data, n) != n:
+        raise RuntimeError(f"tsp_bsa_bwd_plan failed: {_lib.last_error()}")
+    header = (int(plan[0]), int(plan[1]), int(plan[2]))
+    out = (torch.from_numpy(cp).to(dev), torch.from_numpy(crow if crow.size else np.zeros(1, np.int64)).to(dev), nbc,
+           torch.from_numpy(plan).to(dev), header)
+    try:
+        ci_t._tsp_attn_bwd_plan = (key, out)
+    except AttributeError:
+        pass
+    return out
+
+
+def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, row_max, row_denom):
+    """Block-sparse attention backward (replaces nki_bsr_attn_bwd, reference
+    dispatch.py:813-929, and the torch backward ops.py:360-473).
+
+    Q/K/V/O/dO (S, D) or (..., S, D) sharing one mask; row_max / row_denom
+    as hip_block_sparse_attention returns them. Returns (dQ, dK, dV).
+    """
+    if not (Q.shape == K.shape == V.shape == O.shape == dO.shape):
+        raise RuntimeError("Q, K, V, O, dO shapes differ")
+    dt = Q.dtype
+    code = _lib.dtype_code(dt)
+    lead = Q.shape[:-2]
+    S, D = Q.shape[-2:]
+    b = mask_bsr.block_size
+    Mt = S // b
+    orig = Q.device
+    dev = _target_device(Q, K, V, O, dO)
+    sdt = torch.float64 if dt == torch.float64 else torch.float32
+    with torch.cuda.device(dev):
+        mb = mask_bsr.block_row_ptrs.numel() - 1
+        if mb < Mt:
+            raise IndexError(f"mask has {mb} block rows, attention needs {Mt}")
+        rp, ci, _ = _bsr_plan(mask_bsr.block_col_indices, mask_bsr.block_row_ptrs, mb, dev, holder=mask_bsr)
+        q, k, v, o, do = (_on(t, dev, dt).reshape(-1, S, D) for t in (Q, K, V, O, dO))
+        H = q.shape[0]
+        cp, crow, nbc, plan, (n_items, n_splits, n_partials) = _attn_bwd_plan(mask_bsr, H, S, dev)
+        rm = _on(row_max, dev, sdt).reshape(H, Mt * b)
+        rd = _on(row_denom, dev, sdt).reshape(H, Mt * b)
+        dQ, dK, dV = (torch.empty_like(q) for _ in range(3))
+        ws = torch.empty(max(1, _lib.load().tsp_bsa_bwd_workspace_size(H, S, n_partials)), dtype=torch.uint8,
+                         device=dev)
+        _lib.call("tsp_bsa_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), code, H, S, D,
+                  rp.data_ptr(), ci.data_ptr(), cp.data_ptr(), crow.data_ptr(), nbc, b, float(scale), rm.data_ptr(),
+                  rd.data_ptr(), dQ.data_ptr(), dK.data_ptr(), dV.data_ptr(), plan.data_ptr(), n_items, n_splits,
+                  n_partials, ws.data_ptr(), _lib.stream_handle(dev))
+    return tuple(g.reshape(*lead, S, D).to(orig) for g in (dQ, dK, dV))

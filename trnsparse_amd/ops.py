@@ -364,7 +364,8 @@ class _AttnTiledFunction(torch.autograd.Function):
     """Autograd wrapper of tiled attention (reference ops.py:476-546).
 
     Forward runs the HIP kernel (or the torch two-pass spec) and saves
-    Q, K, V, O and the row stats; backward is the tiled torch backward.
+    Q, K, V, O and the row stats; backward runs the HIP backward kernels (or
+    the tiled torch backward on the "pytorch" backend).
     Q/K/V are (seq, d) or batched (..., seq, d) sharing one mask.
     """
 
@@ -385,6 +386,13 @@ class _AttnTiledFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dO):
         Q, K, V, O, row_max, row_denom = ctx.saved_tensors
+        if _use_hip():
+            from .hip.dispatch import hip_block_sparse_attention_backward
+
+            dQ, dK, dV = hip_block_sparse_attention_backward(
+                Q, K, V, O, dO.contiguous(), ctx.handle, ctx.scale, row_max, row_denom
+            )
+            return dQ, dK, dV, None, None, None, None, None
         lead = Q.shape[:-2]
         S, D = Q.shape[-2:]
         q, k, v, o, do = (t.reshape(-1, S, D) for t in (Q, K, V, O, dO))

@@ -339,6 +339,54 @@ def bench_attention(steps: int, warmup: int, cpu: bool = False):
     return res
 
 
+def bench_attention_backward(steps: int, warmup: int, cpu: bool = False):
+    """Backward of block_sparse_attention_tiled at config 5 (tsp_bsa_bwd: the
+    row pass for dQ, the column pass for dK / dV and the reduce of split
+    columns), from the forward's O and stats. Algorithmic FLOPs: the five
+    block products of the backward (S, dP = dO V^T, dV, dK, dQ), 10 * nnzb *
+    128^2 * d * heads; the kernels recompute S and dP in both passes (7
+    products)."""
+    import torch
+
+    from trnsparse_amd import workloads as W
+    from trnsparse_amd.hip import _lib
+    from trnsparse_amd.hip import dispatch as Dp
+
+    Q, K, V, mask = W.cfg5_attention()
+    H, S, D = Q.shape
+    flops = 10.0 * mask.n_blocks * 128 * 128 * D * H
+    dev = torch.device("cuda", torch.cuda.current_device())
+    Qd, Kd, Vd = Q.to(dev), K.to(dev), V.to(dev)
+    dO = torch.randn(Q.shape, generator=torch.Generator().manual_seed(14)).to(torch.bfloat16).to(dev)
+    O, rm, rd = Dp.hip_block_sparse_attention(Qd, Kd, Vd, mask, D**-0.5, return_stats=True)
+    rp, ci, _ = Dp._bsr_plan(mask.block_col_indices, mask.block_row_ptrs, S // 128, dev, holder=mask)
+    cp, crow, nbc, plan, (ni, ns, npart) = Dp._attn_bwd_plan(mask, H, S, dev)
+    dQ, dK, dV = (torch.empty_like(Qd) for _ in range(3))
+    ws = torch.empty(_lib.load().tsp_bsa_bwd_workspace_size(H, S, npart), dtype=torch.uint8, device=dev)
+    st = _lib.stream_handle(dev)
+    code = _lib.dtype_code(torch.bfloat16)
+    call = lambda: _lib.call("tsp_bsa_bwd", Qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), O.data_ptr(), dO.data_ptr(),
+                             code, H, S, D, rp.data_ptr(), ci.data_ptr(), cp.data_ptr(), crow.data_ptr(), nbc, 128,
+                             D**-0.5, rm.data_ptr(), rd.data_ptr(), dQ.data_ptr(), dK.data_ptr(), dV.data_ptr(),
+                             plan.data_ptr(), ni, ns, npart, ws.data_ptr(), st)
+    _, ms = time_gpu(call, steps, warmup)
+    tf = flops / (ms * 1e-3) / 1e12
+    res = {"name": "block_sparse_attention backward cfg5 32x8192x128 bf16", "value": round(tf * 1e3, 1),
+           "unit": "GFLOP/s", "us": round(ms * 1e3, 1), "frac_bf16_mfma": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
+           "split_columns": ns, "items": ni}
+    if cpu:
+        from oracle import cpu_baseline as cb
+
+        args = [t[0].cpu() for t in (Qd, Kd, Vd, O, dO)]
+        r0, d0 = rm[0].reshape(-1).cpu().to(torch.bfloat16), rd[0].reshape(-1).cpu().to(torch.bfloat16)
+        secs = cb.time_call(lambda: cb.attention_backward_head(*args, mask.block_row_ptrs, mask.block_col_indices, 128,
+                                                               D**-0.5, r0, d0), reps=2, budget_s=20.0)
+        res["cpu_baseline"] = {"value": round(flops / H / secs / 1e9, 2), "unit": "GFLOP/s", "cores": cb.threads(),
+                               "kind": "port",
+                               "sample": "one head of cfg5 (bf16) through the reference's torch backward loops"}
+    return res
+
+
 def calibrate_peaks():
     """Achievable peaks on this box next to the spec ones: a 1 GiB device copy
     (read + write bytes / time), and dense 8192^3 GEMMs in fp32 and bf16
@@ -455,6 +503,7 @@ def main(argv=None) -> int:
             ("bsr backward", lambda: bench_bsr_backward(10, 2)),
             ("screened", lambda: bench_screened(10, 2, cpu=not args.no_cpu)),
             ("attention", lambda: bench_attention(10, 2, cpu=not args.no_cpu)),
+            ("attention backward", lambda: bench_attention_backward(10, 2, cpu=not args.no_cpu)),
         ]
         for name, fn in jobs:
             try:

@@ -12,6 +12,8 @@ accumulators, the third-party call it makes):
 - screened:  trnsparse/ops.py:262-277 — materialised mask, A*mask, dense @.
 - attention: trnsparse/ops.py:280-357 — pass 1 tile stats, row reduction,
              pass 2 weighted accumulation, one head at a time.
+- attention_backward: trnsparse/ops.py:360-473 — D = rowsum(dO * O), then
+             per stored block P, dS and the three `+=` products, one head.
 """
 
 from __future__ import annotations
@@ -91,6 +93,30 @@ def attention_head(Q, K, V, row_ptrs, col_idx, b, scale):
             s = (qb @ K[c * b : (c + 1) * b].T) * scale
             out[m * b : (m + 1) * b] += (torch.exp(s - rm) / rd) @ V[c * b : (c + 1) * b]
     return out
+
+
+def attention_backward_head(Q, K, V, O, dO, row_ptrs, col_idx, b, scale, rmax, rden):
+    seq, d = Q.shape
+    Mt = seq // b
+    ptrs = row_ptrs.tolist()
+    cols = col_idx.tolist()
+    D = (dO * O).sum(dim=-1)
+    dQ, dK, dV = torch.zeros_like(Q), torch.zeros_like(K), torch.zeros_like(V)
+    for m in range(Mt):
+        s0, e0 = ptrs[m], ptrs[m + 1]
+        if s0 == e0:
+            continue
+        qs = slice(m * b, (m + 1) * b)
+        rm, rd, dd = rmax[qs].unsqueeze(1), rden[qs].unsqueeze(1), D[qs].unsqueeze(1)
+        for idx in range(s0, e0):
+            c = cols[idx]
+            ks = slice(c * b, (c + 1) * b)
+            P = torch.exp((Q[qs] @ K[ks].T) * scale - rm) / rd
+            dS = P * (dO[qs] @ V[ks].T - dd)
+            dQ[qs] += dS @ K[ks] * scale
+            dK[ks] += dS.T @ Q[qs] * scale
+            dV[ks] += P.T @ dO[qs]
+    return dQ, dK, dV
 
 
 def time_call(fn, reps: int = 3, budget_s: float = 30.0) -> float:

@@ -38,13 +38,19 @@ CFLAGS = [
 ]
 
 
+# Per-source extra flags. attention_bwd.hip: MFMA results in VGPRs (the
+# softmax-gradient VALU reads the S / dP tiles straight from the MFMA
+# destination; the default AGPR form costs a register move per element).
+EXTRA = {"attention_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _sources() -> list[pathlib.Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
 def _compile(src: pathlib.Path, verbose: bool) -> pathlib.Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *CFLAGS, *EXTRA.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

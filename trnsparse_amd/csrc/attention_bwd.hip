@@ -40,6 +40,8 @@
 
 #include "lds_dma.h"
 
+#include <utility>
+
 namespace {
 
 constexpr float LOG2E = 1.4426950408889634f;
@@ -253,13 +255,69 @@ __device__ inline bf16x8 tr_read(const uint8_t* base, const TrLane& t, int r0, i
     r[rr] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + t.off[rr] + r0 * ROWB + ((u ^ t.xu) << 6)));
   return __builtin_bit_cast(bf16x8, __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7));
 }
+// Address form of the two reads for the slot kernels. A stage starts at an
+// LDS address that is a multiple of 256 and rows are 256 bytes, so the
+// swizzled chunk bits (4-7) of a lane's address are free in the stage base:
+// per step one base per access kind is formed (row reads: stage + l32 * ROWB
+// + swz(l32)^h in bits 4-7; transpose reads: stage + off[rr] + xu in bits
+// 6-7) and each read is base ^ (k-step or subtile bits) plus a constant row
+// offset that the ds_read immediate absorbs.
+// Round 4 floats to bf16 (round to nearest even, v_cvt_pk_bf16_f32) as 4 halfwords.
+__device__ inline u16x4 bf16x4_rne(f32x4 v) {
+  return __builtin_bit_cast(u16x4, __builtin_convertvector(v, bf16x4));
+}
+
+// Keep a register operand that only MFMAs read in AGPRs (MFMA takes its A
+// and B operands from either file), leaving the VGPRs to values the VALU uses.
+__device__ inline void pin_agpr(bf16x8& v) {
+  u32x4 t = __builtin_bit_cast(u32x4, v);
+  asm volatile("" : "+a"(t));
+  v = __builtin_bit_cast(bf16x8, t);
+}
+
+typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
+__device__ inline bf16x8 lds_row(uint32_t rb, int ks, uint32_t off) {
+  return *(const lds_bf16x8*)(uintptr_t)((rb ^ (uint32_t)(ks << 5)) + off);
+}
+__device__ inline bf16x8 lds_trp(uint32_t tb0, uint32_t tb1, int u, uint32_t off) {
+  const s16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)((tb0 ^ (uint32_t)(u << 6)) + off));
+  const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)((tb1 ^ (uint32_t)(u << 6)) + off));
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7));
+}
 }  // namespace abw
+
+// Both passes run one wavefront per SIMD (a 256-thread workgroup per CU)
+// and issue their work in a fixed slot order: slot k is one MFMA whose LDS
+// operand was read PF slots earlier (a register ring, so LDS latency hides
+// behind the MFMAs of the same wave), plus a slice of the softmax-gradient
+// VALU work of the previous 32-row tile, so that the VALU runs while the
+// matrix core is busy. sched_barrier keeps the compiler from regrouping
+// the slots.
+constexpr int PF = 4;  // operand reads in flight
+
+// f(integral_constant<int, k>) for k = 0 .. N-1 in order, fully unrolled at
+// compile time (the slot loops are too long for the loop unroller).
+template <typename F, int... Ks>
+__device__ __attribute__((always_inline)) inline void static_for_impl(F&& f, std::integer_sequence<int, Ks...>) {
+  (f(std::integral_constant<int, Ks>{}), ...);
+}
+template <int N, typename F>
+__device__ __attribute__((always_inline)) inline void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 // Row pass: workgroup per (head, query block row m < Mt), XCD-aware order as
 // the forward (XCD x walks heads x, x + 8, ...; block rows of one head side by
-// side share its K/V in L2). Also computes D and leaves the per-query stats
-// for the column pass in qstat planes (log2e * row_max, 1 / row_denom, D).
-__global__ __launch_bounds__(256, 2) void bsa_bwd_dq_bf16_d128(
+// side share its K/V in L2). Wavefront w owns queries m * 128 + 32 w + [0, 32)
+// with their Q and dO rows in registers; 64-key halves of K and V stream
+// through a 4-stage LDS ring by direct buffer loads issued three halves ahead.
+// Per half, slots 0-31: S^T and dP^T tiles of the two 32-key tiles tt (16
+// MFMAs each, K / V rows as A, Q / dO as B); slots 16-39 also form P^T and
+// dS^T of tile 0 (slots 16-31) and tile 1 (32-39); slots 32-47: dQ^T += K^T
+// dS^T (K through transpose reads). Also computes D and leaves per-query
+// stats for the column pass: plane 0 r = log2e * row_max + log2 row_denom
+// (P = exp2(log2e * scale * s - r)), plane 1 D.
+__global__ __launch_bounds__(256, 1) void bsa_bwd_dq_bf16_d128(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     const uint16_t* __restrict__ O, const uint16_t* __restrict__ dO, int64_t S, int64_t H,
     const int64_t* __restrict__ rp, const int64_t* __restrict__ ci, int64_t Mt, float scale_log2, float scale,
@@ -267,7 +325,7 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_bf16_d128(
     uint16_t* __restrict__ dQ) {
   using namespace abw;
   constexpr int STAGE = 2 * HBYTES;  // K half, V half
-  constexpr int NST = 2;
+  constexpr int NST = 4;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
 
   const int64_t g = blockIdx.x;
@@ -281,26 +339,8 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_bf16_d128(
   const int64_t hs = head * S * D;
   const int64_t q = m * BS + w * 32 + l32;  // < S since m < Mt
 
-  // Q and dO rows of the lane's query as B operands: [16 ks + 8 h, +8)
-  bf16x8 qf[KS], dof[KS];
-  float dsum = 0.f;
-#pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    qf[s] = *(const bf16x8*)(Q + hs + q * D + 16 * s + 8 * h);
-    dof[s] = *(const bf16x8*)(dO + hs + q * D + 16 * s + 8 * h);
-    const bf16x8 of = *(const bf16x8*)(O + hs + q * D + 16 * s + 8 * h);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) dsum += (float)dof[s][i] * (float)of[i];
-  }
-  const float Dq = dsum + __shfl_xor(dsum, 32, 64);
-  const float rml2 = rmax[head * Mt * BS + q] * LOG2E;
-  const float inv = 1.f / rden[head * Mt * BS + q];
-  if (h == 0) {
-    const int64_t HS = H * S;
-    qstat[head * S + q] = rml2;
-    qstat[HS + head * S + q] = inv;
-    qstat[2 * HS + head * S + q] = Dq;
-  }
+  bf16x8 qf[KS], dof[KS];  // the lane's Q and dO rows (B operands), loaded below
+  float Dq = 0.f, rq = 0.f;
 
   f32x16 acc[NU];
 #pragma unroll
@@ -313,22 +353,24 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_bf16_d128(
   const tsp::dma::i32x4 vrs = tsp::dma::make_rsrc(V + hs, (uint32_t)(S * ROWB));
   const uint32_t lds0 = tsp::dma::lds_addr(lds);
 
-  // key-block indices of the row, 64 at a time in one VGPR, read with readlane
-  int cbase = 0, cv = 0;
+  // key-block indices of the row, 64 at a time in one VGPR, read with readlane;
+  // the load side (three halves ahead) and the compute side keep their own copy
   auto load_cols = [&](int base) {
     const int i = base + lane < nblk ? base + lane : nblk - 1;
     return tsp::dma::load_lo32_sync(ci + start + i);
   };
-  if (nblk > 0) cv = load_cols(0);
-  auto first_key = [&](int s) {
+  int cb_i = 0, cv_i = 0, cb_c = 0, cv_c = 0;
+  if (nblk > 0) cv_i = cv_c = load_cols(0);
+  auto key_of = [&](int s, int& cb, int& cv) {
     const int blk = s >> 1;
-    if (blk - cbase >= 64) {
-      cbase = blk & ~63;
-      cv = load_cols(cbase);
+    if (blk - cb >= 64) {
+      cb = blk & ~63;
+      cv = load_cols(cb);
     }
-    return (int64_t)__builtin_amdgcn_readlane(cv, blk - cbase) * BS + HR * (s & 1);
+    return (int64_t)__builtin_amdgcn_readlane(cv, blk - cb) * BS + HR * (s & 1);
   };
-  auto issue = [&](int64_t key0, int s) {
+  auto issue = [&](int s) {
+    const int64_t key0 = key_of(s, cb_i, cv_i);
     const uint32_t st = lds0 + (s % NST) * STAGE;
     dma_half(krs, key0, st, w, lane);
     dma_half(vrs, key0, st + HBYTES, w, lane);
@@ -337,52 +379,103 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_bf16_d128(
   const int loff = l32 * ROWB;
   const int kx = swz(l32) ^ h;
   const TrLane trl = tr_lane(lane);
-  const float nrml2 = -rml2;
+  float nr = 0.f;
 
-  auto compute = [&](const uint8_t* st, int64_t key0) {
-    const uint8_t* Ks = st;
-    const uint8_t* Vs = st + HBYTES;
+  auto compute = [&](uint32_t st, int64_t key0) {
     const bool tail = key0 + HR > S;
+    const uint32_t rb = st + (uint32_t)(loff + (kx << 4));
+    const uint32_t tb0 = st + (uint32_t)(trl.off[0] + (trl.xu << 6));
+    const uint32_t tb1 = st + (uint32_t)(trl.off[1] + (trl.xu << 6));
+    // slot -> LDS operand: 0-31 S^T / dP^T of tile k / 16 (even: K row, odd:
+    // V row, k-step (k % 16) / 2); 32-47 K^T for dQ of tile (k - 32) / 8,
+    // k-step a = (k / 4) % 2, head_dim subtile u = k % 4
+    auto fetch = [&](int k) -> bf16x8 {
+      if (k < 32) return lds_row(rb, (k & 15) >> 1, (k & 1) * HBYTES + 32 * (k >> 4) * ROWB);
+      const int j = k - 32;
+      return lds_trp(tb0, tb1, j & 3, (32 * (j >> 3) + 16 * ((j >> 2) & 1)) * ROWB);
+    };
+    f32x16 sc[2], dp[2];
+    float pd[2][16];
+    bf16x8 db[2][2];
+    bf16x8 ring[PF];
+    static_for<PF>([&](auto kc) __attribute__((always_inline)) { ring[decltype(kc)::value] = fetch(decltype(kc)::value); });
+    // dS^T element v of tile tt (key 32 tt + 8 (v / 4) + 4 h + v % 4)
+    auto ds_elem = [&](int tt, int v) {
+      float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tt][v], scale_log2, nr));
+      if (tail && key0 + 32 * tt + 8 * (v >> 2) + 4 * h + (v & 3) >= S) p = 0.f;
+      pd[tt][v] = p * (dp[tt][v] - Dq);
+      if ((v & 7) == 7) {
+        typedef float f32x8_ __attribute__((ext_vector_type(8)));
+        f32x8_ t;
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      // S^T and dP^T tiles: keys 32 tt + 8 (v / 4) + 4 h + v % 4, query l32
-      f32x16 sc = f32x16{}, dp = f32x16{};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_read(Ks, loff, kx, 32 * tt, ks), qf[ks], sc, 0, 0, 0);
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_read(Vs, loff, kx, 32 * tt, ks), dof[ks], dp, 0, 0, 0);
+        for (int i = 0; i < 8; ++i) t[i] = pd[tt][(v & 8) + i];
+        db[tt][v >> 3] = __builtin_convertvector(t, bf16x8);
       }
-      // P = exp(scale s - row_max) / row_denom, dS = P (dP - D); keys at or
-      // past S (zero rows of the stage) get P = 0
-      bf16x8 db[2];
-#pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        f32x8 dv;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int v = 8 * a + i;
-          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[v], scale_log2, nrml2)) * inv;
-          if (tail && key0 + 32 * tt + 8 * (v >> 2) + 4 * h + (v & 3) >= S) p = 0.f;
-          dv[i] = p * (dp[v] - Dq);
-        }
-        db[a] = __builtin_convertvector(dv, bf16x8);
+    };
+    static_for<48>([&](auto kc) __attribute__((always_inline)) {
+      constexpr int k = decltype(kc)::value;
+      const bf16x8 op = ring[k % PF];
+      if constexpr (k + PF < 48) ring[k % PF] = fetch(k + PF);
+      if constexpr (k < 32) {
+        constexpr int tt = k >> 4, ks = (k & 15) >> 1;
+        if constexpr (k & 1)
+          dp[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op, dof[ks], ks ? dp[tt] : f32x16{}, 0, 0, 0);
+        else
+          sc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op, qf[ks], ks ? sc[tt] : f32x16{}, 0, 0, 0);
+      } else {
+        constexpr int j = k - 32;
+        acc[j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op, db[j >> 3][(j >> 2) & 1], acc[j & 3], 0, 0, 0);
       }
-      // dQ^T += K^T dS^T over the tile's 32 keys (k-steps a = 0, 1)
-#pragma unroll
-      for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int u = 0; u < NU; ++u)
-          acc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_read(Ks, trl, 32 * tt + 16 * a, u), db[a], acc[u], 0, 0, 0);
-    }
+      if constexpr (k >= 16 && k < 32) ds_elem(0, k - 16);
+      if constexpr (k >= 32 && k < 40) {
+        ds_elem(1, 2 * (k - 32));
+        ds_elem(1, 2 * (k - 32) + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
   };
 
-  if (nsteps > 0) issue(first_key(0), 0);
+#pragma unroll
+  for (int s = 0; s < NST - 1; ++s)
+    if (s < nsteps) issue(s);
+  // Q, dO and O rows of the lane's query ([16 ks + 8 h, +8)) load behind the
+  // first halves; D and the stats for the column pass
+  float dsum = 0.f;
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    qf[s] = *(const bf16x8*)(Q + hs + q * D + 16 * s + 8 * h);
+    dof[s] = *(const bf16x8*)(dO + hs + q * D + 16 * s + 8 * h);
+    const bf16x8 of = *(const bf16x8*)(O + hs + q * D + 16 * s + 8 * h);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dsum += (float)dof[s][i] * (float)of[i];
+  }
+  Dq = dsum + __shfl_xor(dsum, 32, 64);
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    pin_agpr(qf[s]);
+    pin_agpr(dof[s]);
+  }
+  rq = rmax[head * Mt * BS + q] * LOG2E + __builtin_amdgcn_logf(rden[head * Mt * BS + q]);
+  nr = -rq;
+  if (h == 0) {
+    const int64_t HS = H * S;
+    qstat[head * S + q] = rq;
+    qstat[HS + head * S + q] = Dq;
+  }
   for (int s = 0; s < nsteps; ++s) {
-    const int64_t key0 = first_key(s);
-    tsp::dma::wait_vm<0>();  // this wave's loads of half s are done
-    tsp::dma::barrier();     // every wave's part is in LDS; the other stage is free
-    if (s + 1 < nsteps) issue(first_key(s + 1), s + 1);
-    compute(lds + (s % NST) * STAGE, key0);
+    const int64_t key0 = key_of(s, cb_c, cv_c);
+    // this wave's loads of half s are done once only the later halves (8
+    // loads each) are outstanding
+    const int ahead = nsteps - 1 - s < NST - 2 ? nsteps - 1 - s : NST - 2;
+    if (ahead >= 2)
+      tsp::dma::wait_vm<16>();
+    else if (ahead == 1)
+      tsp::dma::wait_vm<8>();
+    else
+      tsp::dma::wait_vm<0>();
+    tsp::dma::barrier();  // every wave's part is in LDS; stage (s - 1) % NST is free
+    if (s + NST - 1 < nsteps) issue(s + NST - 1);
+    compute(lds0 + (s % NST) * STAGE, key0);
   }
 
   // dQ[q][32 u + 8 g4 + 4 h + i] = scale * acc[u][4 g4 + i]
@@ -391,198 +484,296 @@ __global__ __launch_bounds__(256, 2) void bsa_bwd_dq_bf16_d128(
   for (int u = 0; u < NU; ++u) {
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
-      u16x4 t;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) t[i] = tsp::f32_to_bf16_bits(acc[u][4 * g4 + i] * scale);
-      *(u16x4*)(dq + 32 * u + 8 * g4 + 4 * h) = t;
+      const f32x4 t = {acc[u][4 * g4], acc[u][4 * g4 + 1], acc[u][4 * g4 + 2], acc[u][4 * g4 + 3]};
+      *(u16x4*)(dq + 32 * u + 8 * g4 + 4 * h) = bf16x4_rne(t * scale);
     }
   }
 }
 
-// Column pass: one item = (block column, range [p0, p1) of its column view,
-// partial slot or -1) for every head; items heaviest first, heads of one XCD
-// inner (XCD x walks heads x, x + 8, ...). Wavefront w owns keys
-// col * 128 + 32 w + [0, 32) with the K and V rows in registers; 64-query
-// halves of Q, dO and their stats stream through a 3-stage LDS ring.
-// dK^T += scale Q^T dS and dV^T += dO^T P accumulate in registers; an item
-// covering a whole column writes bf16 dK / dV, a segment of a split column
-// writes fp32 partials that bsa_bwd_reduce sums in segment order.
+// Column pass, persistent: 8 * G8 workgroups (G8 <= 32 per XCD, one per
+// CU); workgroup j of XCD x takes the slots j, j + G8, j + 2 G8, ... of its
+// XCD's slot list, slot s = (item s / nh, head x + 8 (s % nh)); an item is
+// (block column, range [p0, p1) of its column view, partial slot or -1) and
+// items are sorted heaviest first, so the round robin spreads the work. The
+// item records and their block rows (gathered from the column view) are
+// staged in LDS RCAP at a time; the 64-query halves of all items of a batch
+// form one stream through a 3-stage LDS ring (Q half, dO half and their
+// stats, direct buffer loads two halves ahead), so the loads of an item's
+// first halves overlap the previous item's last ones, and the next item's K
+// and V rows load during the current item's last half.
+// Wavefront w owns keys col * 128 + 32 w + [0, 32) with the K and V rows in
+// registers. Per half, slots 0-31: S and dP tiles of the two 32-query tiles
+// qt (Q / dO rows as A, K / V as B); slots 16-47 also form P and dS of tile 0
+// (16-31) and tile 1 (32-47), one element per slot; slots 32-63: dV^T +=
+// dO^T P and dK^T += Q^T dS (dO, Q through transpose reads). An item covering
+// a whole column writes bf16 dK / dV, a segment of a split column writes
+// fp32 partials that bsa_bwd_reduce sums in segment order.
+constexpr int RCAP = 64;  // item records staged per batch
 __global__ __launch_bounds__(256, 1) void bsa_bwd_dkdv_bf16_d128(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     const uint16_t* __restrict__ dO, int64_t S, int64_t H, int nh, const int64_t* __restrict__ crow,
-    const int32_t* __restrict__ items, int n_partials, float scale_log2, float scale, const float* __restrict__ qstat,
-    uint16_t* __restrict__ dK, uint16_t* __restrict__ dV, float* __restrict__ partial) {
+    const int32_t* __restrict__ items, int n_items, int n_partials, float scale_log2, float scale,
+    const float* __restrict__ qstat, uint16_t* __restrict__ dK, uint16_t* __restrict__ dV,
+    float* __restrict__ partial) {
   using namespace abw;
-  constexpr int STAGE = 2 * HBYTES + 1024;  // Q half, dO half, stats [4][64] floats
+  constexpr int STAGE = 2 * HBYTES + 1024;  // Q half, dO half, stats [4][64] floats (r, D, D, D)
   constexpr int NST = 3;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
+  __shared__ int32_t rhdr[RCAP][4];        // col, partial slot, n block rows (-1: no such head), head
+  __shared__ int32_t rrow[RCAP][SEG_MAX];  // block rows of the item
 
-  const int64_t g = blockIdx.x;
-  const int64_t xcd = g & 7, slot = g >> 3;
-  const int64_t it = slot / nh;
-  const int64_t head = xcd + 8 * (slot % nh);
-  if (head >= H) return;
-  const int col = items[4 * it], p0 = items[4 * it + 1], p1 = items[4 * it + 2], pslot = items[4 * it + 3];
-
+  const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3, G8 = gridDim.x >> 3;
+  const int64_t nslots = (int64_t)n_items * nh;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int h = lane >> 5, l32 = lane & 31;
-  const int64_t hs = head * S * D;
-  const int64_t key = (int64_t)col * BS + w * 32 + l32;
-  const bool kvalid = key < S;
-
-  bf16x8 kf[KS], vf[KS];
-#pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    kf[s] = kvalid ? *(const bf16x8*)(K + hs + key * D + 16 * s + 8 * h) : bf16x8{};
-    vf[s] = kvalid ? *(const bf16x8*)(V + hs + key * D + 16 * s + 8 * h) : bf16x8{};
-  }
-  f32x16 dk[NU], dv[NU];
-#pragma unroll
-  for (int u = 0; u < NU; ++u) dk[u] = dv[u] = f32x16{};
-
-  const int nblk = p1 - p0;  // <= SEG_MAX
-  const int nsteps = 2 * nblk;
-  // block rows of the item, one per lane
-  const int rv = nblk > 0 ? tsp::dma::load_lo32_sync(crow + p0 + (lane < nblk ? lane : nblk - 1)) : 0;
-  const tsp::dma::i32x4 qrs = tsp::dma::make_rsrc(Q + hs, (uint32_t)(S * ROWB));
-  const tsp::dma::i32x4 ors = tsp::dma::make_rsrc(dO + hs, (uint32_t)(S * ROWB));
-  const uint32_t lds0 = tsp::dma::lds_addr(lds);
   const int64_t HS = H * S;
-  const int splane = (lane >> 4) < 2 ? (lane >> 4) : 2;
-  const float* sbase = qstat + splane * HS + head * S + 4 * (lane & 15);
-
-  auto first_q = [&](int s) { return (int64_t)__builtin_amdgcn_readlane(rv, s >> 1) * BS + HR * (s & 1); };
-  auto issue = [&](int s) {
-    const int64_t q0 = first_q(s);
-    const uint32_t st = lds0 + (s % NST) * STAGE;
-    dma_half(qrs, q0, st, w, lane);
-    dma_half(ors, q0, st + HBYTES, w, lane);
-    if (w == 0) tsp::dma::global16(sbase + q0, st + 2 * HBYTES);
-  };
+  const uint32_t lds0 = tsp::dma::lds_addr(lds);
+  // per-item state (the compute lambda reads it)
+  f32x16 dk[NU], dv[NU];
+  bf16x8 kf[KS], vf[KS];  // the wave's K and V rows (B operands)
+  bf16x8 kn[KS], vn[KS];  // the next item's, loaded during the current item's last half
 
   const int loff = l32 * ROWB;
   const int kx = swz(l32) ^ h;
   const TrLane trl = tr_lane(lane);
 
-  auto compute = [&](const uint8_t* st) {
-    const uint8_t* Qs = st;
-    const uint8_t* Os = st + HBYTES;
-    const float* stt = (const float*)(st + 2 * HBYTES);
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      // S and dP tiles: queries 32 qt + 8 (v / 4) + 4 h + v % 4, key l32
-      f32x16 sc = f32x16{}, dp = f32x16{};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_read(Qs, loff, kx, 32 * qt, ks), kf[ks], sc, 0, 0, 0);
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row_read(Os, loff, kx, 32 * qt, ks), vf[ks], dp, 0, 0, 0);
+  auto compute = [&](uint32_t st) {
+    const uint32_t rb = st + (uint32_t)(loff + (kx << 4));
+    const uint32_t tb0 = st + (uint32_t)(trl.off[0] + (trl.xu << 6));
+    const uint32_t tb1 = st + (uint32_t)(trl.off[1] + (trl.xu << 6));
+    const uint32_t sb = st + 2 * HBYTES + 16 * h;
+    // slot -> LDS operand: 0-31 S / dP of tile k / 16 (even: Q row, odd: dO
+    // row, k-step (k % 16) / 2); 32-63 of tile (k - 32) / 16, k-step
+    // a = (k / 8) % 2, subtile u = (k / 2) % 4 (even: dO^T for dV, odd: Q^T for dK)
+    auto fetch = [&](int k) -> bf16x8 {
+      if (k < 32) return lds_row(rb, (k & 15) >> 1, (k & 1) * HBYTES + 32 * (k >> 4) * ROWB);
+      const int j = k - 32;
+      return lds_trp(tb0, tb1, (j >> 1) & 3, ((j & 1) ? 0 : HBYTES) + (32 * (j >> 4) + 16 * ((j >> 3) & 1)) * ROWB);
+    };
+    f32x16 sc[2], dp[2];
+    u32x4 pw[2][2], dw[2][2];  // bf16 pairs of P and dS, k order of the B operand
+    f32x4 rc, dc, rn, dn;      // stats of the current / next group of 4 queries
+    bf16x8 ring[PF];
+    static_for<PF>([&](auto kc) __attribute__((always_inline)) { ring[decltype(kc)::value] = fetch(decltype(kc)::value); });
+    // stats (r, D) of the queries 32 qt + 8 g + 4 h + [0, 4)
+    typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+    auto stats = [&](int qt, int gg) {
+      rn = *(const lds_f32x4*)(uintptr_t)(sb + 4 * (32 * qt + 8 * gg));
+      dn = *(const lds_f32x4*)(uintptr_t)(sb + 4 * (64 + 32 * qt + 8 * gg));
+    };
+    // P and dS elements v, v + 1 of tile qt (query 32 qt + 8 (v / 4) + 4 h + v % 4)
+    auto ds_pair = [&](int qt, int v) {
+      if ((v & 3) == 0) {
+        rc = rn;
+        dc = dn;
+        if (v < 12)
+          stats(qt, (v >> 2) + 1);
+        else if (qt == 0)
+          stats(1, 0);
       }
-      bf16x8 pb[2], db[2];
+      typedef float f32x2 __attribute__((ext_vector_type(2)));
+      typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+      f32x2 p, d;
 #pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        f32x8 pv, dsv;
-#pragma unroll
-        for (int gg = 0; gg < 2; ++gg) {
-          const int ql = 32 * qt + 8 * (2 * a + gg) + 4 * h;
-          const f32x4 rm = *(const f32x4*)(stt + ql);
-          const f32x4 iv = *(const f32x4*)(stt + 64 + ql);
-          const f32x4 dd = *(const f32x4*)(stt + 128 + ql);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int v = 8 * a + 4 * gg + i;
-            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[v], scale_log2, -rm[i])) * iv[i];
-            pv[4 * gg + i] = p;
-            dsv[4 * gg + i] = p * (dp[v] - dd[i]);
-          }
-        }
-        pb[a] = __builtin_convertvector(pv, bf16x8);
-        db[a] = __builtin_convertvector(dsv, bf16x8);
+      for (int i = 0; i < 2; ++i) {
+        const int e = v + i;
+        p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qt][e], scale_log2, -rc[e & 3]));
+        d[i] = p[i] * (dp[qt][e] - dc[e & 3]);
       }
-      // dV^T += dO^T P and dK^T += Q^T dS over the tile's 32 queries
-#pragma unroll
-      for (int a = 0; a < 2; ++a) {
-#pragma unroll
-        for (int u = 0; u < NU; ++u) {
-          dv[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_read(Os, trl, 32 * qt + 16 * a, u), pb[a], dv[u], 0, 0, 0);
-          dk[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_read(Qs, trl, 32 * qt + 16 * a, u), db[a], dk[u], 0, 0, 0);
-        }
+      pw[qt][v >> 3][(v & 7) >> 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(p, bf16x2));
+      dw[qt][v >> 3][(v & 7) >> 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(d, bf16x2));
+    };
+    static_for<64>([&](auto kc) __attribute__((always_inline)) {
+      constexpr int k = decltype(kc)::value;
+      const bf16x8 op = ring[k % PF];
+      if constexpr (k + PF < 64) ring[k % PF] = fetch(k + PF);
+      if constexpr (k == 12) stats(0, 0);
+      if constexpr (k < 32) {
+        constexpr int qt = k >> 4, ks = (k & 15) >> 1;
+        if constexpr (k & 1)
+          dp[qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op, vf[ks], ks ? dp[qt] : f32x16{}, 0, 0, 0);
+        else
+          sc[qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op, kf[ks], ks ? sc[qt] : f32x16{}, 0, 0, 0);
+      } else {
+        constexpr int j = k - 32, qt = j >> 4, a = (j >> 3) & 1, u = (j >> 1) & 3;
+        if constexpr (j & 1)
+          dk[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op, __builtin_bit_cast(bf16x8, dw[qt][a]), dk[u], 0, 0, 0);
+        else
+          dv[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op, __builtin_bit_cast(bf16x8, pw[qt][a]), dv[u], 0, 0, 0);
       }
+      if constexpr (k >= 16 && k < 48 && (k & 1) == 0) ds_pair((k - 16) >> 4, (k - 16) & 15);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  auto load_kv = [&](int col, int head, bf16x8* kr, bf16x8* vr) {
+    const int64_t key = (int64_t)col * BS + w * 32 + l32;
+    const bool kvalid = key < S;
+    const int64_t off = head * S * D + key * D + 8 * h;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      kr[s] = kvalid ? *(const bf16x8*)(K + off + 16 * s) : bf16x8{};
+      vr[s] = kvalid ? *(const bf16x8*)(V + off + 16 * s) : bf16x8{};
     }
   };
 
-  if (nsteps > 0) issue(0);
-  if (nsteps > 1) issue(1);
-  for (int s = 0; s < nsteps; ++s) {
-    // loads of half s are done once at most one half (8 or 9 loads) is outstanding
-    if (s + 1 < nsteps)
-      tsp::dma::wait_vm<8>();
-    else
-      tsp::dma::wait_vm<0>();
-    tsp::dma::barrier();  // every wave's part is in LDS; stage (s + 2) % 3 is free
-    if (s + 2 < nsteps) issue(s + 2);
-    compute(lds + (s % NST) * STAGE);
-  }
+  for (int64_t r0 = 0; j + r0 * G8 < nslots; r0 += RCAP) {
+    // ---- stage the batch's item records and block rows
+    const int64_t left = (nslots - j + G8 - 1) / G8 - r0;
+    const int R = (int)(left < RCAP ? left : RCAP);
+    __syncthreads();  // the previous batch's records and ring are no longer read
+    if (tid < R) {
+      const int64_t sl = j + (r0 + tid) * G8;
+      const int64_t it = sl / nh, head = xcd + 8 * (sl % nh);
+      rhdr[tid][0] = items[4 * it];
+      rhdr[tid][1] = items[4 * it + 3];
+      rhdr[tid][2] = head < H ? items[4 * it + 2] - items[4 * it + 1] : -1;
+      rhdr[tid][3] = (int32_t)head;
+    }
+    for (int e = tid; e < R * SEG_MAX; e += 256) {
+      const int r = e / SEG_MAX, i = e % SEG_MAX;
+      const int64_t sl = j + (r0 + r) * G8;
+      const int64_t it = sl / nh;
+      const int p0 = items[4 * it + 1], n = items[4 * it + 2] - p0;
+      if (i < n) rrow[r][i] = (int32_t)crow[p0 + i];
+    }
+    __syncthreads();
 
-  // lane holds dK^T / dV^T [32 u + 8 g4 + 4 h + i][key]
-  if (pslot < 0) {
-    if (!kvalid) return;
-    uint16_t* pk = dK + hs + key * D;
-    uint16_t* pv = dV + hs + key * D;
+    // ---- one stream of halves over the batch's items
+    auto nsteps_of = [&](int r) {
+      const int n = __builtin_amdgcn_readfirstlane(rhdr[r][2]);
+      return n > 0 ? 2 * n : 0;
+    };
+    int pr = 0, pt = 0, pc = 0;  // producer: item, half within it, halves issued
+    auto p_skip = [&]() {
+      while (pr < R && pt >= nsteps_of(pr)) {
+        ++pr;
+        pt = 0;
+      }
+    };
+    auto issue_next = [&]() {
+      if (pr >= R) return;
+      const int head = __builtin_amdgcn_readfirstlane(rhdr[pr][3]);
+      const int64_t q0 = (int64_t)__builtin_amdgcn_readfirstlane(rrow[pr][pt >> 1]) * BS + HR * (pt & 1);
+      const int64_t hs = (int64_t)head * S * D;
+      const uint32_t st = lds0 + (pc % NST) * STAGE;
+      dma_half(tsp::dma::make_rsrc(Q + hs, (uint32_t)(S * ROWB)), q0, st, w, lane);
+      dma_half(tsp::dma::make_rsrc(dO + hs, (uint32_t)(S * ROWB)), q0, st + HBYTES, w, lane);
+      if (w == 0)
+        tsp::dma::global16(qstat + ((lane >> 4) ? HS : 0) + (int64_t)head * S + 4 * (lane & 15) + q0,
+                           st + 2 * HBYTES);
+      ++pt;
+      ++pc;
+      p_skip();
+    };
+    p_skip();
+    issue_next();
+    issue_next();
+    int cc = 0;  // halves consumed
+    bool have_next = false;
+    for (int r = 0; r < R; ++r) {
+      const int nst = nsteps_of(r);
+      if (__builtin_amdgcn_readfirstlane(rhdr[r][2]) < 0) continue;  // head past H
+      const int col = __builtin_amdgcn_readfirstlane(rhdr[r][0]);
+      const int pslot = __builtin_amdgcn_readfirstlane(rhdr[r][1]);
+      const int head = __builtin_amdgcn_readfirstlane(rhdr[r][3]);
+      if (have_next) {
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        u16x4 tk, tv;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          tk[i] = tsp::f32_to_bf16_bits(dk[u][4 * g4 + i] * scale);
-          tv[i] = tsp::f32_to_bf16_bits(dv[u][4 * g4 + i]);
+        for (int s = 0; s < KS; ++s) {
+          kf[s] = kn[s];
+          vf[s] = vn[s];
         }
-        *(u16x4*)(pk + 32 * u + 8 * g4 + 4 * h) = tk;
-        *(u16x4*)(pv + 32 * u + 8 * g4 + 4 * h) = tv;
+      } else {
+        load_kv(col, head, kf, vf);
+      }
+      have_next = false;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        pin_agpr(kf[s]);
+        pin_agpr(vf[s]);
+      }
+#pragma unroll
+      for (int u = 0; u < NU; ++u) dk[u] = dv[u] = f32x16{};
+      for (int t = 0; t < nst; ++t) {
+        // loads of half cc are done once only the next half's (8 or 9
+        // loads) may be outstanding
+        if (pc > cc + 1)
+          tsp::dma::wait_vm<8>();
+        else
+          tsp::dma::wait_vm<0>();
+        tsp::dma::barrier();  // every wave's part is in LDS; stage (cc + 2) % 3 is free
+        issue_next();
+        if (t == nst - 1) {  // the next item's K and V rows
+          int rn = r + 1;
+          while (rn < R && __builtin_amdgcn_readfirstlane(rhdr[rn][2]) < 0) ++rn;
+          if (rn < R) {
+            load_kv(__builtin_amdgcn_readfirstlane(rhdr[rn][0]), __builtin_amdgcn_readfirstlane(rhdr[rn][3]), kn, vn);
+            have_next = true;
+          }
+        }
+        compute(lds0 + (cc % NST) * STAGE);
+        ++cc;
+      }
+
+      // lane holds dK^T / dV^T [32 u + 8 g4 + 4 h + i][key]
+      const int64_t key = (int64_t)col * BS + w * 32 + l32;
+      const int64_t hs = (int64_t)head * S * D;
+      if (pslot < 0) {
+        if (key < S) {
+          uint16_t* pk = dK + hs + key * D;
+          uint16_t* pv = dV + hs + key * D;
+#pragma unroll
+          for (int u = 0; u < NU; ++u) {
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              const f32x4 tk = {dk[u][4 * g4], dk[u][4 * g4 + 1], dk[u][4 * g4 + 2], dk[u][4 * g4 + 3]};
+              const f32x4 tv = {dv[u][4 * g4], dv[u][4 * g4 + 1], dv[u][4 * g4 + 2], dv[u][4 * g4 + 3]};
+              *(u16x4*)(pk + 32 * u + 8 * g4 + 4 * h) = bf16x4_rne(tk * scale);
+              *(u16x4*)(pv + 32 * u + 8 * g4 + 4 * h) = bf16x4_rne(tv);
+            }
+          }
+        }
+      } else {
+        float* pk = partial + (((int64_t)head * n_partials + pslot) * 2) * (BS * D) + (w * 32 + l32) * D;
+        float* pv = pk + BS * D;
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const f32x4 tk = {dk[u][4 * g4], dk[u][4 * g4 + 1], dk[u][4 * g4 + 2], dk[u][4 * g4 + 3]};
+            const f32x4 tv = {dv[u][4 * g4], dv[u][4 * g4 + 1], dv[u][4 * g4 + 2], dv[u][4 * g4 + 3]};
+            *(f32x4*)(pk + 32 * u + 8 * g4 + 4 * h) = tk * scale;
+            *(f32x4*)(pv + 32 * u + 8 * g4 + 4 * h) = tv;
+          }
+        }
       }
     }
-  } else {
-    float* pk = partial + ((head * n_partials + pslot) * 2) * (BS * D) + (w * 32 + l32) * D;
-    float* pv = pk + BS * D;
-#pragma unroll
-    for (int u = 0; u < NU; ++u) {
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        f32x4 tk, tv;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          tk[i] = dk[u][4 * g4 + i] * scale;
-          tv[i] = dv[u][4 * g4 + i];
-        }
-        *(f32x4*)(pk + 32 * u + 8 * g4 + 4 * h) = tk;
-        *(f32x4*)(pv + 32 * u + 8 * g4 + 4 * h) = tv;
-      }
-    }
+    tsp::dma::wait_vm<0>();
   }
 }
 
 // dK / dV of the split columns: sum of the segments' partials in segment
-// order (deterministic), rounded to bf16. Workgroup per (split, head).
+// order (deterministic), rounded to bf16. Workgroup per (split, 16-key chunk
+// of the column, head); thread per 4 consecutive head_dim values of one key
+// of dK or dV.
 __global__ __launch_bounds__(256) void bsa_bwd_reduce(const int32_t* __restrict__ splits, int n_partials, int64_t S,
                                                       const float* __restrict__ partial, uint16_t* __restrict__ dK,
                                                       uint16_t* __restrict__ dV) {
   using namespace abw;
-  const int sp = blockIdx.x;
+  const int sp = blockIdx.x >> 3, chunk = blockIdx.x & 7;
   const int64_t head = blockIdx.y;
   const int col = splits[4 * sp], slot0 = splits[4 * sp + 1], nseg = splits[4 * sp + 2];
   const float* base = partial + (head * n_partials + slot0) * 2 * (BS * D);
-  for (int e = threadIdx.x; e < 2 * BS * (D / 4); e += 256) {
-    const int which = e / (BS * (D / 4));
-    const int r = (e / (D / 4)) % BS, d4 = e % (D / 4);
+#pragma unroll
+  for (int e0 = 0; e0 < 2 * 16 * (D / 4); e0 += 256) {
+    const int e = e0 + threadIdx.x;
+    const int which = e / (16 * (D / 4));
+    const int r = chunk * 16 + (e / (D / 4)) % 16, d4 = e % (D / 4);
     const int64_t key = (int64_t)col * BS + r;
     if (key >= S) continue;
     f32x4 sum = f32x4{};
     for (int j = 0; j < nseg; ++j) sum += *(const f32x4*)(base + (j * 2 + which) * (BS * D) + r * D + 4 * d4);
-    u16x4 t;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) t[i] = tsp::f32_to_bf16_bits(sum[i]);
-    *(u16x4*)((which ? dV : dK) + (head * S + key) * D + 4 * d4) = t;
+    *(u16x4*)((which ? dV : dK) + (head * S + key) * D + 4 * d4) = bf16x4_rne(sum);
   }
 }
 
@@ -693,8 +884,8 @@ extern "C" int tsp_bsa_bwd(const void* Q, const void* K, const void* V, const vo
       return tsp::fail(TSP_EINVAL, "tsp_bsa_bwd: plan has %lld items for %lld key block columns", (long long)n_items,
                        (long long)tsp::ceil_div(seq_len, block_size));
     const int64_t nh = tsp::ceil_div(n_heads, 8);
-    const int64_t grid_a = nh * Mt * 8, grid_b = nh * n_items * 8;
-    if (grid_a > INT32_MAX || grid_b > INT32_MAX || n_splits > INT32_MAX || n_heads > 65535)
+    const int64_t grid_a = nh * Mt * 8;
+    if (grid_a > INT32_MAX || n_items * nh > INT32_MAX || 8 * n_splits > INT32_MAX || n_heads > 65535)
       return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_bwd: problem too large");
     const float sl2 = (float)(scale * 1.4426950408889634);
     float* qstat = (float*)workspace;
@@ -714,16 +905,18 @@ extern "C" int tsp_bsa_bwd(const void* Q, const void* K, const void* V, const vo
       int rc = tsp::check_launch("bsa_bwd_dq_bf16_d128 launch");
       if (rc) return rc;
     }
-    if (grid_b > 0) {
-      hipLaunchKernelGGL(bsa_bwd_dkdv_bf16_d128, dim3((unsigned)grid_b), dim3(256), 0, stream_, (const uint16_t*)Q,
+    if (n_items > 0) {
+      const int64_t nslots = n_items * nh;
+      const int64_t g8 = nslots < 32 ? nslots : 32;
+      hipLaunchKernelGGL(bsa_bwd_dkdv_bf16_d128, dim3((unsigned)(8 * g8)), dim3(256), 0, stream_, (const uint16_t*)Q,
                          (const uint16_t*)K, (const uint16_t*)V, (const uint16_t*)dO, seq_len, n_heads, (int)nh,
-                         col_block_rows, plan + 4, (int)n_partials, sl2, (float)scale, (const float*)qstat,
-                         (uint16_t*)dK, (uint16_t*)dV, partial);
+                         col_block_rows, plan + 4, (int)n_items, (int)n_partials, sl2, (float)scale,
+                         (const float*)qstat, (uint16_t*)dK, (uint16_t*)dV, partial);
       int rc = tsp::check_launch("bsa_bwd_dkdv_bf16_d128 launch");
       if (rc) return rc;
     }
     if (n_splits > 0) {
-      hipLaunchKernelGGL(bsa_bwd_reduce, dim3((unsigned)n_splits, (unsigned)n_heads), dim3(256), 0, stream_,
+      hipLaunchKernelGGL(bsa_bwd_reduce, dim3((unsigned)(8 * n_splits), (unsigned)n_heads), dim3(256), 0, stream_,
                          plan + 4 + 4 * n_items, (int)n_partials, seq_len, (const float*)partial, (uint16_t*)dK,
                          (uint16_t*)dV);
       int rc = tsp::check_launch("bsa_bwd_reduce launch");

@@ -387,6 +387,54 @@ def bench_attention_backward(steps: int, warmup: int, cpu: bool = False):
     return res
 
 
+def bench_formats(steps: int, warmup: int, cpu: bool = False):
+    """Device format construction at config 3's dense size (16384^2 fp32,
+    1638 nonzero 128x128 blocks): BSRMatrix.from_dense (algorithmic bytes:
+    read A once, read + write the kept blocks), formats.from_dense to CSR
+    (read A twice: count pass and fill pass; write values and int64
+    columns) and COOMatrix.to_csr of that matrix's entries (read rows, cols,
+    values; write columns, values and row pointers; the sort's own passes
+    are not counted). Each call includes its host read of the entry count."""
+    import torch
+
+    import trnsparse_amd as ts
+    from trnsparse_amd import workloads as W
+
+    A, _ = W.cfg3_bsr(dtype=torch.float32)
+    dev = torch.device("cuda", torch.cuda.current_device())
+    D = ts.BSRMatrix(A.blocks.to(dev), A.block_col_indices.to(dev), A.block_row_ptrs.to(dev), A.shape, 128).to_dense()
+    m, n = D.shape
+    kept = A.blocks.numel() * 4
+    out = []
+    _, ms = time_gpu(lambda: ts.BSRMatrix.from_dense(D, block_size=128), steps, warmup)
+    byts = m * n * 4 + 2 * kept
+    res = {"name": "BSRMatrix.from_dense cfg3 16384^2 fp32 (device)", "value": round(byts / (ms * 1e-3) / 1e9, 1),
+           "unit": "GB/s", "us": round(ms * 1e3, 1), "frac_hbm": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    if cpu:
+        from oracle import cpu_baseline as cb
+
+        Dc = D.cpu()
+        secs = cb.time_call(lambda: cb.bsr_from_dense(Dc, 128), reps=2, budget_s=20.0)
+        res["cpu_baseline"] = {"value": round(byts / secs / 1e9, 2), "unit": "GB/s", "cores": cb.threads(),
+                               "kind": "port", "sample": "the full cfg3 dense matrix through the reference's torch ops"}
+    out.append(res)
+    csr = ts.from_dense(D)
+    nnz = csr.nnz
+    _, ms = time_gpu(lambda: ts.from_dense(D), steps, warmup)
+    byts = 2 * m * n * 4 + nnz * 12 + (m + 1) * 8
+    out.append({"name": "formats.from_dense (CSR) cfg3 16384^2 fp32 (device)", "nnz": nnz,
+                "value": round(byts / (ms * 1e-3) / 1e9, 1), "unit": "GB/s", "us": round(ms * 1e3, 1),
+                "frac_hbm": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+    coo = csr.to_coo()
+    perm = torch.randperm(nnz, generator=torch.Generator().manual_seed(3)).to(dev)
+    shuffled = ts.COOMatrix(coo.values[perm], coo.row_indices[perm], coo.col_indices[perm], coo.shape)
+    _, ms = time_gpu(lambda: shuffled.to_csr(), steps, warmup)
+    byts = nnz * (8 + 8 + 4) + nnz * (8 + 4) + (m + 1) * 8
+    out.append({"name": "COOMatrix.to_csr cfg3 entries shuffled (device)", "nnz": nnz,
+                "value": round(byts / (ms * 1e-3) / 1e9, 1), "unit": "GB/s", "us": round(ms * 1e3, 1)})
+    return out
+
+
 def calibrate_peaks():
     """Achievable peaks on this box next to the spec ones: a 1 GiB device copy
     (read + write bytes / time), and dense 8192^3 GEMMs in fp32 and bf16
@@ -504,6 +552,7 @@ def main(argv=None) -> int:
             ("screened", lambda: bench_screened(10, 2, cpu=not args.no_cpu)),
             ("attention", lambda: bench_attention(10, 2, cpu=not args.no_cpu)),
             ("attention backward", lambda: bench_attention_backward(10, 2, cpu=not args.no_cpu)),
+            ("formats", lambda: bench_formats(5, 1, cpu=not args.no_cpu)),
         ]
         for name, fn in jobs:
             try:

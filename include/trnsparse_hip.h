@@ -241,6 +241,70 @@ int tsp_bsa_bwd(const void* Q, const void* K, const void* V, const void* O,
                 const int32_t* plan, int64_t n_items, int64_t n_splits,
                 int64_t n_partials, void* workspace, void* stream);
 
+/* ====================================================================
+ * Format construction on the device (bit-exact structure).
+ *
+ * Dense inputs are row-major with row stride lda (elements), dtype
+ * TSP_F32 / TSP_F64 / TSP_BF16; structure arrays are int64. A threshold
+ * compares in the matrix dtype after rounding to it (torch's comparison of
+ * a tensor with a Python float).
+ *
+ * BSR from dense (replaces BSRMatrix.from_dense, trnsparse/formats.py:
+ * 183-221), two calls with a host read of the block count between them:
+ *   tsp_bsr_from_dense_pattern: keep (ceil(m/b)*ceil(n/b) uint8, row-major
+ *     block grid) = [max |v| over the zero-padded block > threshold] (a NaN
+ *     makes the block not kept), row_ptrs (ceil(m/b)+1) = cumulative kept
+ *     counts; workspace: tsp_format_workspace_size(ceil(m/b)) bytes.
+ *   tsp_bsr_from_dense_fill: col_indices (n_blocks = row_ptrs[last]) in
+ *     increasing order within each block row, blocks (n_blocks, b, b)
+ *     row-major with the padding zero.
+ * tsp_bsr_to_dense (replaces BSRMatrix.to_dense, formats.py:233-251):
+ *   out (m, n), row stride ldo; each stored block (the last entry of a
+ *   repeated one) in place, zeros elsewhere.
+ * CSR from dense (replaces formats.from_dense, formats.py:269-278):
+ *   tsp_csr_from_dense_pattern: row_ptrs (m+1) of |v| > threshold
+ *     (workspace: tsp_format_workspace_size(m) bytes); then
+ *   tsp_csr_from_dense_fill: col_indices / values (row_ptrs[m]) in row
+ *     order, columns increasing.
+ * tsp_csr_to_dense (replaces CSRMatrix.to_dense, formats.py:49-52):
+ *   duplicate entries of a row add up in entry order.
+ * tsp_csr_row_indices (replaces the row expansion of CSRMatrix.to_coo,
+ *   formats.py:54-65): rows[k] = row of entry k.
+ * tsp_coo_to_csr (replaces COOMatrix.to_csr, formats.py:104-124): entries
+ *   sorted by row*n + col (stable), row_ptrs (m+1); workspace:
+ *   tsp_coo_to_csr_workspace_size(nnz, m, n) bytes.
+ * ==================================================================== */
+int64_t tsp_format_workspace_size(int64_t rows);
+int tsp_bsr_from_dense_pattern(const void* A, int dtype, int64_t lda, int64_t m,
+                               int64_t n, int64_t block_size, double threshold,
+                               uint8_t* keep, int64_t* row_ptrs,
+                               void* workspace, void* stream);
+int tsp_bsr_from_dense_fill(const void* A, int dtype, int64_t lda, int64_t m,
+                            int64_t n, int64_t block_size, const uint8_t* keep,
+                            const int64_t* row_ptrs, int64_t n_blocks,
+                            int64_t* col_indices, void* blocks, void* stream);
+int tsp_bsr_to_dense(const void* blocks, int dtype, const int64_t* row_ptrs,
+                     const int64_t* col_indices, int64_t n_blocks,
+                     int64_t block_size, int64_t m, int64_t n, void* out,
+                     int64_t ldo, void* stream);
+int tsp_csr_from_dense_pattern(const void* A, int dtype, int64_t lda, int64_t m,
+                               int64_t n, double threshold, int64_t* row_ptrs,
+                               void* workspace, void* stream);
+int tsp_csr_from_dense_fill(const void* A, int dtype, int64_t lda, int64_t m,
+                            int64_t n, double threshold, const int64_t* row_ptrs,
+                            int64_t* col_indices, void* values, void* stream);
+int tsp_csr_to_dense(const void* values, int dtype, const int64_t* col_indices,
+                     const int64_t* row_ptrs, int64_t m, int64_t n, void* out,
+                     int64_t ldo, void* stream);
+int tsp_csr_row_indices(const int64_t* row_ptrs, int64_t m, int64_t nnz,
+                        int64_t* rows, void* stream);
+int64_t tsp_coo_to_csr_workspace_size(int64_t nnz, int64_t m, int64_t n);
+int tsp_coo_to_csr(const void* values, int dtype, const int64_t* row_indices,
+                   const int64_t* col_indices, int64_t nnz, int64_t m,
+                   int64_t n, int64_t* row_ptrs, int64_t* col_out,
+                   void* values_out, void* workspace, int64_t workspace_bytes,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

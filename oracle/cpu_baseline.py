@@ -14,6 +14,8 @@ accumulators, the third-party call it makes):
              pass 2 weighted accumulation, one head at a time.
 - attention_backward: trnsparse/ops.py:360-473 — D = rowsum(dO * O), then
              per stored block P, dS and the three `+=` products, one head.
+- bsr_from_dense: trnsparse/formats.py:183-221 — pad, block-grid view
+             copy, amax of |v|, nonzero, boolean gather.
 """
 
 from __future__ import annotations
@@ -117,6 +119,22 @@ def attention_backward_head(Q, K, V, O, dO, row_ptrs, col_idx, b, scale, rmax, r
             dK[ks] += dS.T @ Q[qs] * scale
             dV[ks] += P.T @ dO[qs]
     return dQ, dK, dV
+
+
+def bsr_from_dense(A, b, threshold=0.0):
+    m, n = A.shape
+    mp, np_ = -(-m // b) * b, -(-n // b) * b
+    if (mp, np_) != (m, n):
+        P = torch.zeros(mp, np_, dtype=A.dtype)
+        P[:m, :n] = A
+        A = P
+    mb, nbc = mp // b, np_ // b
+    grid = A.reshape(mb, b, nbc, b).permute(0, 2, 1, 3).contiguous()
+    keep = grid.abs().amax(dim=(-2, -1)) > threshold
+    ptrs = torch.zeros(mb + 1, dtype=torch.long)
+    ptrs[1:] = keep.sum(dim=1).cumsum(dim=0)
+    cols = keep.nonzero(as_tuple=False)[:, 1].to(torch.long)
+    return grid[keep].contiguous(), cols, ptrs
 
 
 def time_call(fn, reps: int = 3, budget_s: float = 30.0) -> float:

@@ -13,6 +13,10 @@ How each function is pinned (tests/test_oracle.py):
 - bsr_from_dense / bsr_to_dense: brute-force per-block loops on tiny grids,
   round trips, the empty-matrix case, padding of unaligned shapes.
 - bsr_spmm: closed form to_dense(A) @ B (numpy matmul), empty pattern -> 0.
+- csr_from_dense: scipy.sparse (independent) for positive thresholds, a
+  brute-force double loop for negative ones (zeros kept) and NaN entries.
+- coo_to_csr: scipy.sparse for distinct coordinates, a brute-force sort of
+  (row, col, position) tuples with duplicates.
 - bsr_spmm_backward: torch float64 autograd through the dense product
   to_dense(A) @ B (dA read back on the stored blocks), empty pattern -> 0.
 - csr_spmv / csr_spmm: scipy.sparse (independent implementation), the
@@ -55,6 +59,30 @@ def bsr_from_dense(A: np.ndarray, b: int, threshold: float = 0.0):
     rows, cols = np.nonzero(keep)
     blocks = np.ascontiguousarray(grid[rows, cols]) if len(rows) else np.zeros((0, b, b), A.dtype)
     return blocks, cols.astype(np.int64), row_ptrs, (m, n)
+
+
+def csr_from_dense(A: np.ndarray, threshold: float = 0.0):
+    """(values, col_idx, row_ptrs) as formats.py:269-278 builds them: entries
+    with |v| > threshold (numpy compares in A's dtype), rows in order, columns
+    ascending (torch.where's row-major order, kept by the COO sort)."""
+    m, _ = A.shape
+    mask = np.abs(A) > threshold
+    rows, cols = np.nonzero(mask)
+    row_ptrs = np.zeros(m + 1, dtype=np.int64)
+    row_ptrs[1:] = np.cumsum(np.bincount(rows, minlength=m))
+    return A[mask], cols.astype(np.int64), row_ptrs
+
+
+def coo_to_csr(values, rows, cols, shape):
+    """(values, col_idx, row_ptrs) as formats.py:104-124 builds them: entries
+    ordered by the key row*n + col, equal keys in input order (a stable sort;
+    the reference's argsort leaves their order unspecified), row_ptrs the
+    cumulative row counts."""
+    m, n = shape
+    order = np.argsort(np.asarray(rows, np.int64) * n + np.asarray(cols, np.int64), kind="stable")
+    row_ptrs = np.zeros(m + 1, dtype=np.int64)
+    row_ptrs[1:] = np.cumsum(np.bincount(np.asarray(rows)[order], minlength=m)) if len(order) else 0
+    return np.asarray(values)[order], np.asarray(cols, np.int64)[order], row_ptrs
 
 
 def bsr_to_dense(blocks, col_idx, row_ptrs, shape, b):

@@ -115,6 +115,55 @@ def test_bsr_spmm_backward_vs_dense_autograd(shape, b, density):
     assert zd.shape == (0, 8, 8) and not zB.any()
 
 
+def test_csr_from_dense_vs_scipy_and_brute_force():
+    rng = np.random.default_rng(12)
+    A = rng.standard_normal((37, 53)) * (rng.random((37, 53)) < 0.3)
+    for thr in (0.0, 0.5):
+        v, c, p = ref.csr_from_dense(A, thr)
+        s = sp.csr_matrix(np.where(np.abs(A) > thr, A, 0.0))
+        s.sort_indices()
+        np.testing.assert_array_equal(p, s.indptr)
+        np.testing.assert_array_equal(c, s.indices)
+        np.testing.assert_array_equal(v, s.data)
+    B = A.copy()
+    B[3, 4] = np.nan
+    for thr in (-1.0, 0.25):  # negative: every finite entry (zeros too); NaN never passes
+        v, c, p = ref.csr_from_dense(B, thr)
+        ev, ec, ep = [], [], [0]
+        for i in range(B.shape[0]):
+            for j in range(B.shape[1]):
+                if abs(B[i, j]) > thr:
+                    ev.append(B[i, j])
+                    ec.append(j)
+            ep.append(len(ec))
+        np.testing.assert_array_equal(p, ep)
+        np.testing.assert_array_equal(c, ec)
+        np.testing.assert_array_equal(v, ev)
+
+
+def test_coo_to_csr_vs_scipy_and_brute_force():
+    rng = np.random.default_rng(13)
+    m, n, nnz = 40, 30, 300
+    flat = rng.choice(m * n, nnz, replace=False)  # distinct coordinates, shuffled
+    rows, cols = flat // n, flat % n
+    vals = rng.standard_normal(nnz)
+    v, c, p = ref.coo_to_csr(vals, rows, cols, (m, n))
+    s = sp.coo_matrix((vals, (rows, cols)), shape=(m, n)).tocsr()
+    s.sort_indices()
+    np.testing.assert_array_equal(p, s.indptr)
+    np.testing.assert_array_equal(c, s.indices)
+    np.testing.assert_array_equal(v, s.data)
+    # duplicates keep their input order
+    rows = rng.integers(0, 5, 80)
+    cols = rng.integers(0, 3, 80)
+    vals = np.arange(80.0)
+    v, c, p = ref.coo_to_csr(vals, rows, cols, (5, 3))
+    order = [t[2] for t in sorted((int(r), int(cc), k) for k, (r, cc) in enumerate(zip(rows, cols)))]
+    np.testing.assert_array_equal(v, vals[order])
+    np.testing.assert_array_equal(c, cols[order])
+    np.testing.assert_array_equal(p, np.concatenate([[0], np.cumsum(np.bincount(rows, minlength=5))]))
+
+
 # ------------------------------------------------------------------ CSR
 
 

@@ -1,0 +1,701 @@
+// Device-side sparse format construction (reference trnsparse/formats.py),
+// bit-exact in structure with the reference's rules:
+//   BSR from_dense (formats.py:183-221): pad to a block multiple with zeros,
+//     keep block (i, j) iff max |v| over the padded block > threshold (a NaN
+//     in the block makes the max NaN: not kept), block rows in order, block
+//     columns increasing within a row, blocks copied row-major with the
+//     padding zero.
+//   BSR to_dense (formats.py:233-251): every stored block written in place
+//     (a later entry of the same block wins, as the reference's loop), the
+//     rest zero, cropped to the unpadded shape.
+//   CSR from_dense (formats.py:269-278): keep |v| > threshold, rows in order,
+//     columns increasing (torch.where order, then the COO sort by row*n+col).
+//   COO to_csr (formats.py:104-124): entries sorted by the key row*n + col
+//     (stable: equal keys keep their input order), row_ptrs = cumulative
+//     row counts.
+//   CSR to_coo (formats.py:54-65): row index of every entry.
+//   CSR to_dense (formats.py:49-52, torch sparse_csr to_dense): duplicate
+//     entries of a row add up in entry order.
+// Thresholds compare in the matrix dtype with the threshold rounded to it,
+// as torch compares a tensor with a Python float (double -> float -> bf16
+// for bf16).
+//
+// All of it is HBM-bound integer / byte work: no MFMA. Kernels read the
+// dense matrix with 16-byte loads where the row stride and base allow.
+#include "common.h"
+
+#include <rocprim/device/device_radix_sort.hpp>
+
+namespace {
+
+// ------------------------------------------------------------ element ops
+
+template <typename T> struct Ops;
+template <> struct Ops<float> {
+  typedef float thr_t;
+  static __device__ bool gt(float v, float t) { return fabsf(v) > t; }
+  static __device__ bool nan(float v) { return v != v; }
+};
+template <> struct Ops<double> {
+  typedef double thr_t;
+  static __device__ bool gt(double v, double t) { return fabs(v) > t; }
+  static __device__ bool nan(double v) { return v != v; }
+};
+template <> struct Ops<uint16_t> {  // bf16 bits
+  typedef float thr_t;              // the bf16-rounded threshold, exact in float
+  static __device__ bool gt(uint16_t v, float t) { return tsp::bf16_bits_to_f32(v & 0x7fff) > t; }
+  static __device__ bool nan(uint16_t v) { return (v & 0x7fff) > 0x7f80; }
+};
+
+template <typename T> typename Ops<T>::thr_t round_threshold(double t);
+template <> float round_threshold<float>(double t) { return (float)t; }
+template <> double round_threshold<double>(double t) { return t; }
+template <> float round_threshold<uint16_t>(double t) { return tsp::bf16_bits_to_f32(tsp::f32_to_bf16_bits((float)t)); }
+
+// ------------------------------------------------------------------- scan
+
+// out[0] = 0, out[i + 1] = sum_{k <= i} counts[i]; one workgroup of 1024.
+__global__ __launch_bounds__(1024) void exclusive_scan_kernel(const int64_t* __restrict__ counts, int64_t n,
+                                                              int64_t* __restrict__ out) {
+  __shared__ int64_t part[1024];
+  __shared__ int64_t carry;
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    carry = 0;
+    out[0] = 0;
+  }
+  __syncthreads();
+  for (int64_t base = 0; base < n; base += 1024) {
+    const int64_t i = base + tid;
+    int64_t v = i < n ? counts[i] : 0;
+    part[tid] = v;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {  // Hillis-Steele inclusive scan
+      const int64_t add = tid >= o ? part[tid - o] : 0;
+      __syncthreads();
+      part[tid] += add;
+      __syncthreads();
+    }
+    if (i < n) out[i + 1] = carry + part[tid];
+    __syncthreads();
+    if (tid == 1023) carry += part[1023];
+    __syncthreads();
+  }
+}
+
+int scan_counts(const int64_t* counts, int64_t n, int64_t* out, hipStream_t st) {
+  hipLaunchKernelGGL(exclusive_scan_kernel, dim3(1), dim3(1024), 0, st, counts, n, out);
+  return tsp::check_launch("exclusive_scan launch");
+}
+
+// Vector width (elements) of 16-byte loads for a row-major matrix with row
+// stride ld elements at base p; 1 when the rows are not 16-byte aligned.
+template <typename T> int vec_width(const void* p, int64_t ld) {
+  const int v = 16 / (int)sizeof(T);
+  return (((uintptr_t)p % 16) == 0 && ld % v == 0) ? v : 1;
+}
+
+template <typename T, int V> struct alignas(sizeof(T) * V) Vec { T e[V]; };
+
+template <typename T, int V> __device__ inline Vec<T, V> load_vec(const T* p) {
+  if constexpr (V == 1) {
+    return Vec<T, V>{{*p}};
+  } else {
+    return *(const Vec<T, V>*)p;  // 16-byte aligned by construction
+  }
+}
+
+// ------------------------------------------------------------ BSR from dense
+
+// keep[i * nbc + j] for every block of the padded grid; one workgroup per
+// block, threads over V-element pieces of the block's rows.
+template <typename T, int V>
+__global__ __launch_bounds__(256) void bsr_keep_kernel(const T* __restrict__ A, int64_t lda, int64_t m, int64_t n,
+                                                       int64_t b, int64_t nbc, typename Ops<T>::thr_t thr,
+                                                       uint8_t* __restrict__ keep) {
+  const int64_t blk = blockIdx.x;
+  const int64_t i = blk / nbc, j = blk % nbc;
+  const int64_t r0 = i * b, c0 = j * b;
+  const int64_t rows = m - r0 < b ? m - r0 : b, cols = n - c0 < b ? n - c0 : b;
+  const int64_t pieces = b / V;  // b % V == 0 on the vector path
+  int gt = 0, nan = 0;
+  for (int64_t e = threadIdx.x; e < rows * pieces; e += 256) {
+    const int64_t r = e / pieces, c = (e % pieces) * V;
+    if (c >= cols) continue;
+    const T* p = A + (r0 + r) * lda + c0 + c;
+    if (V > 1 && c + V <= cols) {
+      const Vec<T, V> v = load_vec<T, V>(p);
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        gt |= Ops<T>::gt(v.e[k], thr);
+        nan |= Ops<T>::nan(v.e[k]);
+      }
+    } else {
+      for (int64_t k = 0; k < V && c + k < cols; ++k) {
+        gt |= Ops<T>::gt(p[k], thr);
+        nan |= Ops<T>::nan(p[k]);
+      }
+    }
+  }
+  gt = __syncthreads_or(gt);
+  nan = __syncthreads_or(nan);
+  if (threadIdx.x == 0) {
+    // the zero padding of an edge block takes part in the max
+    const bool padded = rows < b || cols < b;
+    const bool pad_gt = padded && (typename Ops<T>::thr_t)0 > thr;
+    keep[blk] = (!nan && (gt || pad_gt)) ? 1 : 0;
+  }
+}
+
+// counts[i] = number of kept blocks in block row i; one wavefront per row.
+__global__ __launch_bounds__(256) void row_count_u8_kernel(const uint8_t* __restrict__ keep, int64_t rows,
+                                                           int64_t cols, int64_t* __restrict__ counts) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  int64_t c = 0;
+  for (int64_t j = lane; j < cols; j += 64) c += keep[r * cols + j];
+  c = tsp::wave_sum(c);
+  if (lane == 0) counts[r] = c;
+}
+
+// col_indices of block row i (kept columns in increasing order), one
+// workgroup per block row: prefix sums of the keep flags in chunks of 256.
+__global__ __launch_bounds__(256) void bsr_cols_kernel(const uint8_t* __restrict__ keep, int64_t nbc,
+                                                       const int64_t* __restrict__ row_ptrs,
+                                                       int64_t* __restrict__ col_indices) {
+  __shared__ int part[256];
+  const int64_t i = blockIdx.x;
+  const int tid = threadIdx.x;
+  int64_t pos = row_ptrs[i];
+  for (int64_t base = 0; base < nbc; base += 256) {
+    const int64_t j = base + tid;
+    const int f = j < nbc ? keep[i * nbc + j] : 0;
+    part[tid] = f;
+    __syncthreads();
+    for (int o = 1; o < 256; o <<= 1) {
+      const int add = tid >= o ? part[tid - o] : 0;
+      __syncthreads();
+      part[tid] += add;
+      __syncthreads();
+    }
+    if (f) col_indices[pos + part[tid] - 1] = j;
+    pos += part[255];
+    __syncthreads();
+  }
+}
+
+// block row of stored block k: the last i with row_ptrs[i] <= k.
+__device__ inline int64_t block_row_of(const int64_t* __restrict__ row_ptrs, int64_t mb, int64_t k) {
+  int64_t lo = 0, hi = mb;  // row_ptrs[lo] <= k < row_ptrs[hi]
+  while (hi - lo > 1) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (row_ptrs[mid] <= k)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+// blocks[k] = the padded b x b block (i_k, col_indices[k]) of A; one
+// workgroup per stored block.
+template <typename T, int V>
+__global__ __launch_bounds__(256) void bsr_gather_kernel(const T* __restrict__ A, int64_t lda, int64_t m, int64_t n,
+                                                         int64_t b, int64_t mb, const int64_t* __restrict__ row_ptrs,
+                                                         const int64_t* __restrict__ col_indices,
+                                                         T* __restrict__ blocks) {
+  const int64_t k = blockIdx.x;
+  const int64_t i = block_row_of(row_ptrs, mb, k), j = col_indices[k];
+  const int64_t r0 = i * b, c0 = j * b;
+  const int64_t rows = m - r0 < b ? m - r0 : b, cols = n - c0 < b ? n - c0 : b;
+  const int64_t pieces = b / V;
+  T* out = blocks + k * b * b;
+  for (int64_t e = threadIdx.x; e < b * pieces; e += 256) {
+    const int64_t r = e / pieces, c = (e % pieces) * V;
+    Vec<T, V> v;
+    if (V > 1 && r < rows && c + V <= cols) {
+      v = load_vec<T, V>(A + (r0 + r) * lda + c0 + c);
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < V; ++kk) v.e[kk] = (r < rows && c + kk < cols) ? A[(r0 + r) * lda + c0 + c + kk] : T(0);
+    }
+    *(Vec<T, V>*)(out + r * b + c) = v;
+  }
+}
+
+// ------------------------------------------------------------- BSR to dense
+
+// out (m x n, row stride ldo): workgroup per output block (i, j); the last
+// stored entry of block row i with column j supplies it, else zeros.
+template <typename T>
+__global__ __launch_bounds__(256) void bsr_to_dense_kernel(const T* __restrict__ blocks,
+                                                           const int64_t* __restrict__ row_ptrs,
+                                                           const int64_t* __restrict__ col_indices, int64_t b,
+                                                           int64_t nbc, int64_t m, int64_t n, T* __restrict__ out,
+                                                           int64_t ldo) {
+  __shared__ unsigned long long found;  // 1 + index of the last match, 0: none
+  const int64_t blk = blockIdx.x;
+  const int64_t i = blk / nbc, j = blk % nbc;
+  if (threadIdx.x == 0) found = 0;
+  __syncthreads();
+  const int64_t s = row_ptrs[i], e = row_ptrs[i + 1];
+  for (int64_t k = s + threadIdx.x; k < e; k += 256)
+    if (col_indices[k] == j) atomicMax(&found, (unsigned long long)(k + 1));
+  __syncthreads();
+  const int64_t k = (int64_t)found - 1;
+  const int64_t r0 = i * b, c0 = j * b;
+  const int64_t rows = m - r0 < b ? m - r0 : b, cols = n - c0 < b ? n - c0 : b;
+  for (int64_t t = threadIdx.x; t < rows * cols; t += 256) {
+    const int64_t r = t / cols, c = t % cols;
+    out[(r0 + r) * ldo + c0 + c] = k >= 0 ? blocks[k * b * b + r * b + c] : T(0);
+  }
+}
+
+// ------------------------------------------------------------ CSR from dense
+
+// counts[r] = #{c : |A[r][c]| > thr}; one wavefront per row.
+template <typename T, int V>
+__global__ __launch_bounds__(256) void csr_count_kernel(const T* __restrict__ A, int64_t lda, int64_t m, int64_t n,
+                                                        typename Ops<T>::thr_t thr, int64_t* __restrict__ counts) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= m) return;
+  const T* row = A + r * lda;
+  int64_t c = 0;
+  for (int64_t base = (int64_t)lane * V; base < n; base += 64 * V) {
+    if (V > 1 && base + V <= n) {
+      const Vec<T, V> v = load_vec<T, V>(row + base);
+#pragma unroll
+      for (int k = 0; k < V; ++k) c += Ops<T>::gt(v.e[k], thr);
+    } else {
+      for (int64_t k = 0; k < V && base + k < n; ++k) c += Ops<T>::gt(row[base + k], thr);
+    }
+  }
+  c = tsp::wave_sum(c);
+  if (lane == 0) counts[r] = c;
+}
+
+// col_indices / values of row r in column order; one wavefront per row:
+// per 64*V-column chunk, a lane's kept count, an exclusive scan over lanes,
+// then each lane writes its kept entries in order.
+template <typename T, int V>
+__global__ __launch_bounds__(256) void csr_fill_kernel(const T* __restrict__ A, int64_t lda, int64_t m, int64_t n,
+                                                       typename Ops<T>::thr_t thr, const int64_t* __restrict__ row_ptrs,
+                                                       int64_t* __restrict__ col_indices, T* __restrict__ values) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= m) return;
+  const T* row = A + r * lda;
+  int64_t pos = row_ptrs[r];
+  for (int64_t chunk = 0; chunk < n; chunk += 64 * V) {
+    const int64_t base = chunk + (int64_t)lane * V;
+    Vec<T, V> v;
+    int cnt = 0;
+    if (V > 1 && base + V <= n) {
+      v = load_vec<T, V>(row + base);
+    } else {
+#pragma unroll
+      for (int k = 0; k < V; ++k) v.e[k] = base + k < n ? row[base + k] : T(0);
+    }
+    unsigned keepm = 0;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      const bool f = base + k < n && Ops<T>::gt(v.e[k], thr);
+      keepm |= (unsigned)f << k;
+      cnt += f;
+    }
+    // exclusive scan of cnt over the wavefront
+    int incl = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += t;
+    }
+    const int total = __shfl(incl, 63, 64);
+    int64_t w = pos + incl - cnt;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      if (keepm & (1u << k)) {
+        col_indices[w] = base + k;
+        values[w] = v.e[k];
+        ++w;
+      }
+    }
+    pos += total;
+  }
+}
+
+// ------------------------------------------------------------- CSR to dense
+
+// out zeroed beforehand; thread per row adds its entries in order.
+template <typename T>
+__global__ __launch_bounds__(256) void csr_to_dense_kernel(const T* __restrict__ values,
+                                                           const int64_t* __restrict__ col_indices,
+                                                           const int64_t* __restrict__ row_ptrs, int64_t m,
+                                                           T* __restrict__ out, int64_t ldo) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= m) return;
+  for (int64_t k = row_ptrs[r]; k < row_ptrs[r + 1]; ++k) {
+    T* p = out + r * ldo + col_indices[k];
+    if constexpr (sizeof(T) == 2)
+      *p = tsp::f32_to_bf16_bits(tsp::bf16_bits_to_f32(*p) + tsp::bf16_bits_to_f32(values[k]));
+    else
+      *p += values[k];
+  }
+}
+
+// out[r][c] = 0 for r < m, c < n (row stride ldo); thread per element.
+template <typename T>
+__global__ __launch_bounds__(256) void zero_rows_kernel(T* __restrict__ out, int64_t m, int64_t n, int64_t ldo) {
+  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < m * n; t += (int64_t)gridDim.x * 256)
+    out[(t / n) * ldo + t % n] = T(0);
+}
+
+// ------------------------------------------------------------- CSR -> COO
+
+// rows[k] = the row of entry k: the last r with row_ptrs[r] <= k.
+__global__ __launch_bounds__(256) void csr_rows_kernel(const int64_t* __restrict__ row_ptrs, int64_t m, int64_t nnz,
+                                                       int64_t* __restrict__ rows) {
+  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (k >= nnz) return;
+  rows[k] = block_row_of(row_ptrs, m, k);
+}
+
+// ------------------------------------------------------------- COO -> CSR
+
+__global__ __launch_bounds__(256) void coo_keys_kernel(const int64_t* __restrict__ rows,
+                                                       const int64_t* __restrict__ cols, int64_t nnz, int64_t n,
+                                                       uint64_t* __restrict__ keys, int64_t* __restrict__ idx) {
+  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (k >= nnz) return;
+  keys[k] = (uint64_t)(rows[k] * n + cols[k]);
+  idx[k] = k;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void coo_gather_kernel(const int64_t* __restrict__ perm,
+                                                         const int64_t* __restrict__ cols, const T* __restrict__ vals,
+                                                         int64_t nnz, int64_t* __restrict__ cols_out,
+                                                         T* __restrict__ vals_out) {
+  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (k >= nnz) return;
+  const int64_t p = perm[k];
+  cols_out[k] = cols[p];
+  vals_out[k] = vals[p];
+}
+
+// row_ptrs[r] = first k with sorted key >= r * n (r = 0 .. m).
+__global__ __launch_bounds__(256) void coo_row_ptrs_kernel(const uint64_t* __restrict__ keys, int64_t nnz, int64_t m,
+                                                           int64_t n, int64_t* __restrict__ row_ptrs) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r > m) return;
+  const uint64_t key = (uint64_t)(r * n);
+  int64_t lo = 0, hi = nnz;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (keys[mid] < key)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  row_ptrs[r] = lo;
+}
+
+int key_bits(int64_t m, int64_t n) {
+  const uint64_t maxkey = (uint64_t)(m * n);  // keys < m * n
+  int bits = 1;
+  while (bits < 64 && (maxkey >> bits) != 0) ++bits;
+  return bits;
+}
+
+int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+
+// ------------------------------------------------------------- dispatch
+
+int elem_size(int dtype) { return dtype == TSP_F64 ? 8 : (dtype == TSP_F32 ? 4 : 2); }
+
+bool dtype_ok(int dtype) { return dtype == TSP_F32 || dtype == TSP_F64 || dtype == TSP_BF16; }
+
+template <typename T>
+int bsr_pattern_t(const void* A, int64_t lda, int64_t m, int64_t n, int64_t b, double threshold, uint8_t* keep,
+                  int64_t* row_ptrs, int64_t* counts, hipStream_t st) {
+  const int64_t mb = tsp::ceil_div(m, b), nbc = tsp::ceil_div(n, b);
+  const auto thr = round_threshold<T>(threshold);
+  const int64_t nblk = mb * nbc;
+  if (nblk > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "bsr from_dense: too many blocks");
+  if (nblk > 0) {
+    const int V = 16 / (int)sizeof(T);
+    if (vec_width<T>(A, lda) == V && b % V == 0)
+      hipLaunchKernelGGL((bsr_keep_kernel<T, 16 / sizeof(T)>), dim3((unsigned)nblk), dim3(256), 0, st, (const T*)A,
+                         lda, m, n, b, nbc, thr, keep);
+    else
+      hipLaunchKernelGGL((bsr_keep_kernel<T, 1>), dim3((unsigned)nblk), dim3(256), 0, st, (const T*)A, lda, m, n, b,
+                         nbc, thr, keep);
+    int rc = tsp::check_launch("bsr_keep launch");
+    if (rc) return rc;
+    hipLaunchKernelGGL(row_count_u8_kernel, dim3((unsigned)tsp::ceil_div(mb, 4)), dim3(256), 0, st, keep, mb, nbc,
+                       counts);
+    rc = tsp::check_launch("row_count launch");
+    if (rc) return rc;
+  }
+  return scan_counts(counts, mb, row_ptrs, st);
+}
+
+template <typename T>
+int bsr_fill_t(const void* A, int64_t lda, int64_t m, int64_t n, int64_t b, const uint8_t* keep,
+               const int64_t* row_ptrs, int64_t n_blocks, int64_t* col_indices, void* blocks, hipStream_t st) {
+  const int64_t mb = tsp::ceil_div(m, b), nbc = tsp::ceil_div(n, b);
+  if (mb == 0 || n_blocks == 0) return TSP_OK;
+  if (mb > INT32_MAX || n_blocks > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "bsr from_dense: too many blocks");
+  hipLaunchKernelGGL(bsr_cols_kernel, dim3((unsigned)mb), dim3(256), 0, st, keep, nbc, row_ptrs, col_indices);
+  int rc = tsp::check_launch("bsr_cols launch");
+  if (rc) return rc;
+  const int V = 16 / (int)sizeof(T);
+  if (vec_width<T>(A, lda) == V && b % V == 0 && ((uintptr_t)blocks % 16) == 0)
+    hipLaunchKernelGGL((bsr_gather_kernel<T, 16 / sizeof(T)>), dim3((unsigned)n_blocks), dim3(256), 0, st,
+                       (const T*)A, lda, m, n, b, mb, row_ptrs, col_indices, (T*)blocks);
+  else
+    hipLaunchKernelGGL((bsr_gather_kernel<T, 1>), dim3((unsigned)n_blocks), dim3(256), 0, st, (const T*)A, lda, m,
+                       n, b, mb, row_ptrs, col_indices, (T*)blocks);
+  return tsp::check_launch("bsr_gather launch");
+}
+
+template <typename T>
+int csr_pattern_t(const void* A, int64_t lda, int64_t m, int64_t n, double threshold, int64_t* row_ptrs,
+                  int64_t* counts, hipStream_t st) {
+  const auto thr = round_threshold<T>(threshold);
+  if (m > 0) {
+    const int64_t g = tsp::ceil_div(m, 4);
+    if (g > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "csr from_dense: too many rows");
+    if (vec_width<T>(A, lda) > 1)
+      hipLaunchKernelGGL((csr_count_kernel<T, 16 / sizeof(T)>), dim3((unsigned)g), dim3(256), 0, st, (const T*)A, lda,
+                         m, n, thr, counts);
+    else
+      hipLaunchKernelGGL((csr_count_kernel<T, 1>), dim3((unsigned)g), dim3(256), 0, st, (const T*)A, lda, m, n, thr,
+                         counts);
+    int rc = tsp::check_launch("csr_count launch");
+    if (rc) return rc;
+  }
+  return scan_counts(counts, m, row_ptrs, st);
+}
+
+template <typename T>
+int csr_fill_t(const void* A, int64_t lda, int64_t m, int64_t n, double threshold, const int64_t* row_ptrs,
+               int64_t* col_indices, void* values, hipStream_t st) {
+  const auto thr = round_threshold<T>(threshold);
+  if (m == 0) return TSP_OK;
+  const int64_t g = tsp::ceil_div(m, 4);
+  if (g > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "csr from_dense: too many rows");
+  if (vec_width<T>(A, lda) > 1)
+    hipLaunchKernelGGL((csr_fill_kernel<T, 16 / sizeof(T)>), dim3((unsigned)g), dim3(256), 0, st, (const T*)A, lda, m,
+                       n, thr, row_ptrs, col_indices, (T*)values);
+  else
+    hipLaunchKernelGGL((csr_fill_kernel<T, 1>), dim3((unsigned)g), dim3(256), 0, st, (const T*)A, lda, m, n, thr,
+                       row_ptrs, col_indices, (T*)values);
+  return tsp::check_launch("csr_fill launch");
+}
+
+}  // namespace
+
+// Workspace of the from_dense pattern calls: block (or row) counts.
+extern "C" int64_t tsp_format_workspace_size(int64_t rows) {
+  if (rows < 0) return -1;
+  return 8 * (rows + 1);
+}
+
+extern "C" int tsp_bsr_from_dense_pattern(const void* A, int dtype, int64_t lda, int64_t m, int64_t n,
+                                          int64_t block_size, double threshold, uint8_t* keep, int64_t* row_ptrs,
+                                          void* workspace, void* stream) {
+  if (!dtype_ok(dtype)) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_from_dense_pattern: dtype %d", dtype);
+  if (m < 0 || n < 0 || block_size <= 0 || lda < n) return tsp::fail(TSP_EINVAL, "tsp_bsr_from_dense_pattern: bad size");
+  if (!row_ptrs || !workspace || (m > 0 && n > 0 && (!A || !keep)))
+    return tsp::fail(TSP_EINVAL, "tsp_bsr_from_dense_pattern: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  if (n == 0) {  // no block columns: every block row is empty
+    const int64_t mb = tsp::ceil_div(m, block_size);
+    int rc = tsp::zero_fill(workspace, 8 * mb, st);
+    if (rc) return rc;
+    return scan_counts((const int64_t*)workspace, mb, row_ptrs, st);
+  }
+  if (dtype == TSP_F32)
+    return bsr_pattern_t<float>(A, lda, m, n, block_size, threshold, keep, row_ptrs, (int64_t*)workspace, st);
+  if (dtype == TSP_F64)
+    return bsr_pattern_t<double>(A, lda, m, n, block_size, threshold, keep, row_ptrs, (int64_t*)workspace, st);
+  return bsr_pattern_t<uint16_t>(A, lda, m, n, block_size, threshold, keep, row_ptrs, (int64_t*)workspace, st);
+}
+
+extern "C" int tsp_bsr_from_dense_fill(const void* A, int dtype, int64_t lda, int64_t m, int64_t n, int64_t block_size,
+                                       const uint8_t* keep, const int64_t* row_ptrs, int64_t n_blocks,
+                                       int64_t* col_indices, void* blocks, void* stream) {
+  if (!dtype_ok(dtype)) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_from_dense_fill: dtype %d", dtype);
+  if (m < 0 || n < 0 || block_size <= 0 || lda < n || n_blocks < 0)
+    return tsp::fail(TSP_EINVAL, "tsp_bsr_from_dense_fill: bad size");
+  if (n_blocks == 0) return TSP_OK;
+  if (!A || !keep || !row_ptrs || !col_indices || !blocks) return tsp::fail(TSP_EINVAL, "tsp_bsr_from_dense_fill: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == TSP_F32)
+    return bsr_fill_t<float>(A, lda, m, n, block_size, keep, row_ptrs, n_blocks, col_indices, blocks, st);
+  if (dtype == TSP_F64)
+    return bsr_fill_t<double>(A, lda, m, n, block_size, keep, row_ptrs, n_blocks, col_indices, blocks, st);
+  return bsr_fill_t<uint16_t>(A, lda, m, n, block_size, keep, row_ptrs, n_blocks, col_indices, blocks, st);
+}
+
+extern "C" int tsp_bsr_to_dense(const void* blocks, int dtype, const int64_t* row_ptrs, const int64_t* col_indices,
+                                int64_t n_blocks, int64_t block_size, int64_t m, int64_t n, void* out, int64_t ldo,
+                                void* stream) {
+  if (!dtype_ok(dtype)) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_to_dense: dtype %d", dtype);
+  if (m < 0 || n < 0 || block_size <= 0 || ldo < n || n_blocks < 0) return tsp::fail(TSP_EINVAL, "tsp_bsr_to_dense: bad size");
+  if (m == 0 || n == 0) return TSP_OK;
+  if (!row_ptrs || !out || (n_blocks > 0 && (!blocks || !col_indices)))
+    return tsp::fail(TSP_EINVAL, "tsp_bsr_to_dense: null pointer");
+  const int64_t mb = tsp::ceil_div(m, block_size), nbc = tsp::ceil_div(n, block_size);
+  if (mb * nbc > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_to_dense: too many blocks");
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 g((unsigned)(mb * nbc));
+  if (dtype == TSP_F32)
+    hipLaunchKernelGGL(bsr_to_dense_kernel<float>, g, dim3(256), 0, st, (const float*)blocks, row_ptrs, col_indices,
+                       block_size, nbc, m, n, (float*)out, ldo);
+  else if (dtype == TSP_F64)
+    hipLaunchKernelGGL(bsr_to_dense_kernel<double>, g, dim3(256), 0, st, (const double*)blocks, row_ptrs, col_indices,
+                       block_size, nbc, m, n, (double*)out, ldo);
+  else
+    hipLaunchKernelGGL(bsr_to_dense_kernel<uint16_t>, g, dim3(256), 0, st, (const uint16_t*)blocks, row_ptrs,
+                       col_indices, block_size, nbc, m, n, (uint16_t*)out, ldo);
+  return tsp::check_launch("bsr_to_dense launch");
+}
+
+extern "C" int tsp_csr_from_dense_pattern(const void* A, int dtype, int64_t lda, int64_t m, int64_t n, double threshold,
+                                          int64_t* row_ptrs, void* workspace, void* stream) {
+  if (!dtype_ok(dtype)) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_from_dense_pattern: dtype %d", dtype);
+  if (m < 0 || n < 0 || lda < n) return tsp::fail(TSP_EINVAL, "tsp_csr_from_dense_pattern: bad size");
+  if (!row_ptrs || !workspace || (m > 0 && n > 0 && !A)) return tsp::fail(TSP_EINVAL, "tsp_csr_from_dense_pattern: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  if (n == 0) {
+    int rc = tsp::zero_fill(workspace, 8 * m, st);
+    if (rc) return rc;
+    return scan_counts((const int64_t*)workspace, m, row_ptrs, st);
+  }
+  if (dtype == TSP_F32) return csr_pattern_t<float>(A, lda, m, n, threshold, row_ptrs, (int64_t*)workspace, st);
+  if (dtype == TSP_F64) return csr_pattern_t<double>(A, lda, m, n, threshold, row_ptrs, (int64_t*)workspace, st);
+  return csr_pattern_t<uint16_t>(A, lda, m, n, threshold, row_ptrs, (int64_t*)workspace, st);
+}
+
+extern "C" int tsp_csr_from_dense_fill(const void* A, int dtype, int64_t lda, int64_t m, int64_t n, double threshold,
+                                       const int64_t* row_ptrs, int64_t* col_indices, void* values, void* stream) {
+  if (!dtype_ok(dtype)) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_from_dense_fill: dtype %d", dtype);
+  if (m < 0 || n < 0 || lda < n) return tsp::fail(TSP_EINVAL, "tsp_csr_from_dense_fill: bad size");
+  if (m == 0 || n == 0) return TSP_OK;
+  // col_indices / values may be null when no entry passes (nothing is written)
+  if (!A || !row_ptrs) return tsp::fail(TSP_EINVAL, "tsp_csr_from_dense_fill: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == TSP_F32) return csr_fill_t<float>(A, lda, m, n, threshold, row_ptrs, col_indices, values, st);
+  if (dtype == TSP_F64) return csr_fill_t<double>(A, lda, m, n, threshold, row_ptrs, col_indices, values, st);
+  return csr_fill_t<uint16_t>(A, lda, m, n, threshold, row_ptrs, col_indices, values, st);
+}
+
+extern "C" int tsp_csr_to_dense(const void* values, int dtype, const int64_t* col_indices, const int64_t* row_ptrs,
+                                int64_t m, int64_t n, void* out, int64_t ldo, void* stream) {
+  if (!dtype_ok(dtype)) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_to_dense: dtype %d", dtype);
+  if (m < 0 || n < 0 || ldo < n) return tsp::fail(TSP_EINVAL, "tsp_csr_to_dense: bad size");
+  if (m == 0 || n == 0) return TSP_OK;
+  if (!row_ptrs || !out) return tsp::fail(TSP_EINVAL, "tsp_csr_to_dense: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  if (ldo == n) {
+    int rc = tsp::zero_fill(out, m * n * elem_size(dtype), st);
+    if (rc) return rc;
+  } else {
+    const int64_t gz = tsp::ceil_div(m * n, 256) < 65536 ? tsp::ceil_div(m * n, 256) : 65536;
+    if (dtype == TSP_F32)
+      hipLaunchKernelGGL(zero_rows_kernel<float>, dim3((unsigned)gz), dim3(256), 0, st, (float*)out, m, n, ldo);
+    else if (dtype == TSP_F64)
+      hipLaunchKernelGGL(zero_rows_kernel<double>, dim3((unsigned)gz), dim3(256), 0, st, (double*)out, m, n, ldo);
+    else
+      hipLaunchKernelGGL(zero_rows_kernel<uint16_t>, dim3((unsigned)gz), dim3(256), 0, st, (uint16_t*)out, m, n, ldo);
+    int rc = tsp::check_launch("zero_rows launch");
+    if (rc) return rc;
+  }
+  const int64_t g = tsp::ceil_div(m, 256);
+  if (g > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_to_dense: too many rows");
+  if (dtype == TSP_F32)
+    hipLaunchKernelGGL(csr_to_dense_kernel<float>, dim3((unsigned)g), dim3(256), 0, st, (const float*)values,
+                       col_indices, row_ptrs, m, (float*)out, ldo);
+  else if (dtype == TSP_F64)
+    hipLaunchKernelGGL(csr_to_dense_kernel<double>, dim3((unsigned)g), dim3(256), 0, st, (const double*)values,
+                       col_indices, row_ptrs, m, (double*)out, ldo);
+  else
+    hipLaunchKernelGGL(csr_to_dense_kernel<uint16_t>, dim3((unsigned)g), dim3(256), 0, st, (const uint16_t*)values,
+                       col_indices, row_ptrs, m, (uint16_t*)out, ldo);
+  return tsp::check_launch("csr_to_dense launch");
+}
+
+extern "C" int tsp_csr_row_indices(const int64_t* row_ptrs, int64_t m, int64_t nnz, int64_t* rows, void* stream) {
+  if (m < 0 || nnz < 0) return tsp::fail(TSP_EINVAL, "tsp_csr_row_indices: bad size");
+  if (nnz == 0) return TSP_OK;
+  if (!row_ptrs || !rows) return tsp::fail(TSP_EINVAL, "tsp_csr_row_indices: null pointer");
+  const int64_t g = tsp::ceil_div(nnz, 256);
+  if (g > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_row_indices: too many entries");
+  hipLaunchKernelGGL(csr_rows_kernel, dim3((unsigned)g), dim3(256), 0, (hipStream_t)stream, row_ptrs, m, nnz, rows);
+  return tsp::check_launch("csr_rows launch");
+}
+
+extern "C" int64_t tsp_coo_to_csr_workspace_size(int64_t nnz, int64_t m, int64_t n) {
+  if (nnz < 0 || m < 0 || n < 0) return -1;
+  size_t tmp = 0;
+  if (nnz > 0) {
+    const int bits = key_bits(m, n);
+    if (rocprim::radix_sort_pairs(nullptr, tmp, (uint64_t*)nullptr, (uint64_t*)nullptr, (int64_t*)nullptr,
+                                  (int64_t*)nullptr, (size_t)nnz, 0, bits) != hipSuccess)
+      return -1;
+  }
+  return 4 * align256(8 * nnz) + align256((int64_t)tmp);
+}
+
+extern "C" int tsp_coo_to_csr(const void* values, int dtype, const int64_t* row_indices, const int64_t* col_indices,
+                              int64_t nnz, int64_t m, int64_t n, int64_t* row_ptrs, int64_t* col_out, void* values_out,
+                              void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!dtype_ok(dtype)) return tsp::fail(TSP_EUNSUPPORTED, "tsp_coo_to_csr: dtype %d", dtype);
+  if (nnz < 0 || m < 0 || n < 0) return tsp::fail(TSP_EINVAL, "tsp_coo_to_csr: bad size");
+  if (m > 0 && n > 0 && m > INT64_MAX / n) return tsp::fail(TSP_EUNSUPPORTED, "tsp_coo_to_csr: m * n overflows");
+  if (!row_ptrs) return tsp::fail(TSP_EINVAL, "tsp_coo_to_csr: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  if (nnz == 0) {
+    int rc = tsp::zero_fill(row_ptrs, 8 * (m + 1), st);
+    return rc;
+  }
+  if (!values || !row_indices || !col_indices || !col_out || !values_out || !workspace)
+    return tsp::fail(TSP_EINVAL, "tsp_coo_to_csr: null pointer");
+  if (workspace_bytes < tsp_coo_to_csr_workspace_size(nnz, m, n))
+    return tsp::fail(TSP_EINVAL, "tsp_coo_to_csr: workspace too small");
+  const int64_t g = tsp::ceil_div(nnz, 256);
+  if (g > INT32_MAX || tsp::ceil_div(m + 1, 256) > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_coo_to_csr: too large");
+  char* w = (char*)workspace;
+  uint64_t* keys = (uint64_t*)w;
+  uint64_t* keys_s = (uint64_t*)(w + align256(8 * nnz));
+  int64_t* idx = (int64_t*)(w + 2 * align256(8 * nnz));
+  int64_t* perm = (int64_t*)(w + 3 * align256(8 * nnz));
+  void* tmp = w + 4 * align256(8 * nnz);
+  size_t tmp_bytes = (size_t)(workspace_bytes - 4 * align256(8 * nnz));
+  hipLaunchKernelGGL(coo_keys_kernel, dim3((unsigned)g), dim3(256), 0, st, row_indices, col_indices, nnz, n, keys, idx);
+  int rc = tsp::check_launch("coo_keys launch");
+  if (rc) return rc;
+  if (rocprim::radix_sort_pairs(tmp, tmp_bytes, keys, keys_s, idx, perm, (size_t)nnz, 0, key_bits(m, n), st) !=
+      hipSuccess)
+    return tsp::check_hip(hipGetLastError(), "radix_sort_pairs");
+  rc = tsp::check_launch("radix_sort_pairs");
+  if (rc) return rc;
+  if (dtype == TSP_F32)
+    hipLaunchKernelGGL(coo_gather_kernel<float>, dim3((unsigned)g), dim3(256), 0, st, perm, col_indices,
+                       (const float*)values, nnz, col_out, (float*)values_out);
+  else if (dtype == TSP_F64)
+    hipLaunchKernelGGL(coo_gather_kernel<double>, dim3((unsigned)g), dim3(256), 0, st, perm, col_indices,
+                       (const double*)values, nnz, col_out, (double*)values_out);
+  else
+    hipLaunchKernelGGL(coo_gather_kernel<uint16_t>, dim3((unsigned)g), dim3(256), 0, st, perm, col_indices,
+                       (const uint16_t*)values, nnz, col_out, (uint16_t*)values_out);
+  rc = tsp::check_launch("coo_gather launch");
+  if (rc) return rc;
+  hipLaunchKernelGGL(coo_row_ptrs_kernel, dim3((unsigned)tsp::ceil_div(m + 1, 256)), dim3(256), 0, st, keys_s, nnz, m,
+                     n, row_ptrs);
+  return tsp::check_launch("coo_row_ptrs launch");
+}

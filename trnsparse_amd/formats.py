@@ -2,8 +2,11 @@
 
 Same dataclasses, fields, defaults and structure rules as the reference
 (trnsparse/formats.py). Structure tensors are int64 (torch.long) as there.
-Construction helpers are vectorised torch ops; they produce exactly the
-structure the reference produces:
+On the HIP backend, conversions whose input lives on the GPU (float32,
+float64, bfloat16 values) run as device kernels (`hip/formats.py`,
+`csrc/formats.hip`) and return device tensors; otherwise the helpers are
+vectorised torch ops. Both produce exactly the structure the reference
+produces:
 
 - `BSRMatrix.from_dense` (reference formats.py:183-221): pad to a block
   multiple, keep a block iff max|v| > threshold, row-major block order,
@@ -17,6 +20,18 @@ from __future__ import annotations
 from dataclasses import dataclass
 
 import torch
+
+from .backend import _use_hip
+
+
+def _device_formats(t: torch.Tensor):
+    """The device conversion module when `t` is a GPU tensor of a dtype the
+    kernels serve and the HIP backend is in effect, else None."""
+    if not (isinstance(t, torch.Tensor) and t.is_cuda and _use_hip()):
+        return None
+    from .hip import formats as hf
+
+    return hf if t.dtype in hf.DEVICE_DTYPES else None
 
 
 @dataclass
@@ -47,11 +62,19 @@ class CSRMatrix:
         return self.nnz / (self.shape[0] * self.shape[1])
 
     def to_dense(self) -> torch.Tensor:
+        hf = _device_formats(self.values)
+        if hf is not None:
+            return hf.csr_to_dense(self.values, self.col_indices, self.row_ptrs, self.shape)
         t = torch.sparse_csr_tensor(self.row_ptrs, self.col_indices, self.values, size=self.shape)
         return t.to_dense()
 
     def to_coo(self) -> COOMatrix:
         """COO view with row indices expanded from `row_ptrs` (reference :54-65)."""
+        hf = _device_formats(self.values)
+        if hf is not None:
+            rows = hf.csr_row_indices(self.row_ptrs, self.shape[0], self.nnz, self.values.device)
+            return COOMatrix(values=self.values.clone(), row_indices=rows, col_indices=self.col_indices.clone(),
+                             shape=self.shape)
         counts = (self.row_ptrs[1:] - self.row_ptrs[:-1]).to("cpu")
         rows = torch.repeat_interleave(torch.arange(self.shape[0], dtype=torch.long), counts)
         return COOMatrix(
@@ -95,6 +118,10 @@ class COOMatrix:
     def to_csr(self) -> CSRMatrix:
         """Sort by (row, col) and build row pointers (reference :104-124)."""
         m, n = self.shape
+        hf = _device_formats(self.values)
+        if hf is not None:
+            vals, cols, rp = hf.coo_to_csr(self.values, self.row_indices, self.col_indices, self.shape)
+            return CSRMatrix(values=vals, col_indices=cols, row_ptrs=rp, shape=self.shape)
         order = torch.argsort(self.row_indices * n + self.col_indices, stable=True)
         rows = self.row_indices[order]
         counts = torch.bincount(rows.to("cpu"), minlength=m)
@@ -157,6 +184,10 @@ class BSRMatrix:
         """Keep a block iff some element has |v| > threshold (reference :183-221)."""
         m, n = A.shape
         b = block_size
+        hf = _device_formats(A)
+        if hf is not None:
+            blocks, col_idx, row_ptrs = hf.bsr_from_dense(A, b, threshold)
+            return cls(blocks=blocks, block_col_indices=col_idx, block_row_ptrs=row_ptrs, shape=(m, n), block_size=b)
         m_pad, n_pad = _round_up(m, b), _round_up(n, b)
         if (m_pad, n_pad) != (m, n):
             padded = torch.zeros(m_pad, n_pad, dtype=A.dtype, device=A.device)
@@ -191,6 +222,9 @@ class BSRMatrix:
         """Scatter the stored blocks into a dense (M, N) tensor (reference :233-251)."""
         m, n = self.shape
         b = self.block_size
+        hf = _device_formats(self.blocks)
+        if hf is not None:
+            return hf.bsr_to_dense(self.blocks, self.block_row_ptrs, self.block_col_indices, self.shape, b)
         m_pad, n_pad = _round_up(m, b), _round_up(n, b)
         mb, nbc = m_pad // b, n_pad // b
         dev = self.blocks.device
@@ -215,6 +249,10 @@ class BSRMatrix:
 def from_dense(A: torch.Tensor, threshold: float = 0.0) -> CSRMatrix:
     """Dense -> CSR keeping |v| > threshold (reference formats.py:269-278)."""
     m, n = A.shape
+    hf = _device_formats(A)
+    if hf is not None:
+        vals, cols, rp = hf.csr_from_dense(A, threshold)
+        return CSRMatrix(values=vals, col_indices=cols, row_ptrs=rp, shape=(m, n))
     mask = torch.abs(A) > threshold
     rows, cols = torch.where(mask)
     coo = COOMatrix(values=A[mask], row_indices=rows, col_indices=cols, shape=(m, n))

@@ -48,6 +48,16 @@ SIGNATURES: dict[str, tuple] = {
     "tsp_screened_workspace_size": (_I64, [_I64, _INT]),
     "tsp_screened_spmm": (_INT, [_P, _INT, _I64, _P, _INT, _DBL, _I64, _P, _I64, _I64, _P, _I64, _P, _P]),
     "tsp_bsa_fwd": (_INT, [_P, _P, _P, _INT, _I64, _I64, _I64, _P, _P, _I64, _DBL, _P, _P, _P, _P]),
+    "tsp_format_workspace_size": (_I64, [_I64]),
+    "tsp_bsr_from_dense_pattern": (_INT, [_P, _INT, _I64, _I64, _I64, _I64, _DBL, _P, _P, _P, _P]),
+    "tsp_bsr_from_dense_fill": (_INT, [_P, _INT, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _P]),
+    "tsp_bsr_to_dense": (_INT, [_P, _INT, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P]),
+    "tsp_csr_from_dense_pattern": (_INT, [_P, _INT, _I64, _I64, _I64, _DBL, _P, _P, _P]),
+    "tsp_csr_from_dense_fill": (_INT, [_P, _INT, _I64, _I64, _I64, _DBL, _P, _P, _P, _P]),
+    "tsp_csr_to_dense": (_INT, [_P, _INT, _P, _P, _I64, _I64, _P, _I64, _P]),
+    "tsp_csr_row_indices": (_INT, [_P, _I64, _I64, _P, _P]),
+    "tsp_coo_to_csr_workspace_size": (_I64, [_I64, _I64, _I64]),
+    "tsp_coo_to_csr": (_INT, [_P, _INT, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "tsp_bsa_bwd_plan": (_I64, [_P, _I64, _I64, _I64, _I64, _P, _I64]),
     "tsp_bsa_bwd_workspace_size": (_I64, [_I64, _I64, _I64]),
     "tsp_bsa_bwd": (

@@ -97,13 +97,20 @@ def time_gpu(fn, steps: int, warmup: int, flush=None, prewarm_s: float = 0.25):
 
 
 def make_flush():
-    """Write 1 GiB to evict L2 and the 256 MiB MALL between timed reps."""
+    """Read 1 GiB to evict L2 and the 256 MiB MALL between timed reps.
+
+    A read (a sum over a buffer written once up front) leaves the caches
+    holding clean lines; a write flush would leave the MALL full of dirty
+    lines whose write-back the next kernel's misses pay for (measured: the
+    cold BSR-SpMV kernel 43.8 us after a 1 GiB fill, 22.6 us after a 1 GiB
+    read; the CSR SpMV, gather-bound, 136 vs 135 us)."""
     import torch
 
-    buf = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+    buf = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
 
     def flush():
-        buf.fill_(1.0)
+        torch.sum(buf)
 
     return flush
 
@@ -226,6 +233,68 @@ def bench_bsr_backward(steps: int, warmup: int):
         tf = flops / (ms * 1e-3) / 1e12
         out.append({"name": name, "value": round(tf * 1e3, 1), "unit": "GFLOP/s", "us": round(ms * 1e3, 1),
                     "frac_fp32_mfma": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)})
+    return out
+
+
+def bench_bsr_spmv(steps: int, warmup: int, cpu: bool = False):
+    """BSR times one vector (bsr_spmm with N = 1 -> tsp_bsr_spmv) on config
+    3's A (fp32, 1638 blocks = 107.4 MB), HBM-bound: algorithmic bytes =
+    blocks + x + y + structure, every launch cold (L2 and MALL flushed).
+    Then richardson_bsr on an SPD matrix of the same size (128 x 128 blocks
+    of 128, band 2 plus 502 symmetric pairs = 1638 blocks), K = 50: one fused
+    pass over A per step, A warm in the MALL across steps; bytes per step =
+    blocks + 3 vectors read + 1 written."""
+    import torch
+
+    import trnsparse_amd as ts
+    from trnsparse_amd import workloads as W
+
+    out = []
+    A, _ = W.cfg3_bsr(dtype=torch.float32)
+    m, n = A.shape
+    dev = torch.device("cuda", torch.cuda.current_device())
+    Ad = ts.BSRMatrix(A.blocks.to(dev), A.block_col_indices.to(dev), A.block_row_ptrs.to(dev), A.shape, 128)
+    x = torch.randn(n, 1, generator=torch.Generator().manual_seed(2)).to(dev)
+    flush = make_flush()
+    _, ms = time_gpu(lambda: ts.bsr_spmm(Ad, x), steps, warmup, flush=flush)
+    byts = A.blocks.numel() * 4 + (n + m) * 4 + (A.n_blocks + A.block_row_ptrs.numel()) * 8
+    res = {"name": "bsr_spmm N=1 (BSR-SpMV) cfg3 fp32, cold", "value": round(byts / (ms * 1e-3) / 1e9, 1),
+           "unit": "GB/s", "us": round(ms * 1e3, 1), "frac_hbm": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    if cpu:
+        from oracle import cpu_baseline as cb
+
+        xc = x.cpu()
+        ptr, col = A.block_row_ptrs, A.block_col_indices
+        secs = cb.time_call(lambda: cb.bsr_spmm(A.blocks, col, ptr, A.shape, 128, xc), reps=3, budget_s=10.0)
+        res["cpu_baseline"] = {"value": round(byts / secs / 1e9, 2), "unit": "GB/s", "cores": cb.threads(),
+                               "kind": "port", "sample": "the full cfg3 matvec through the reference's torch loop"}
+    out.append(res)
+    S, lo, hi = W.spd_bsr(nb=128, b=128, band=2, n_pairs=502)
+    Sd = ts.BSRMatrix(S.blocks.to(dev), S.block_col_indices.to(dev), S.block_row_ptrs.to(dev), S.shape, 128)
+    rhs = torch.randn(S.shape[0], generator=torch.Generator().manual_seed(3)).to(dev)
+    K = 50
+    _, ms = time_gpu(lambda: ts.richardson_bsr(Sd, rhs, 2.0 / (lo + hi), K=K), max(2, steps // 5), 1)
+    per = ms / (K + 1)  # K steps and the final residual pass
+    byts = S.blocks.numel() * 4 + 4 * S.shape[0] * 4
+    res = {"name": f"richardson_bsr K={K} SPD 16384^2 ({S.n_blocks} blocks) fp32, fused step",
+           "value": round(byts / (per * 1e-3) / 1e9, 1), "unit": "GB/s", "us_per_step": round(per * 1e3, 1),
+           "us_total": round(ms * 1e3, 1)}
+    if cpu:
+        from oracle import cpu_baseline as cb
+
+        ptr, col = S.block_row_ptrs, S.block_col_indices
+        rc = rhs.cpu()
+
+        def ref_steps(k=3):
+            xx = torch.zeros_like(rc)
+            for _ in range(k):
+                xx = xx + (2.0 / (lo + hi)) * (rc - cb.bsr_spmm(S.blocks, col, ptr, S.shape, 128, xx[:, None])[:, 0])
+            return xx
+
+        secs = cb.time_call(ref_steps, reps=2, budget_s=10.0) / 3
+        res["cpu_baseline"] = {"value": round(byts / secs / 1e9, 2), "unit": "GB/s", "cores": cb.threads(),
+                               "kind": "port", "sample": "3 Richardson steps through the reference's torch loop"}
+    out.append(res)
     return out
 
 
@@ -553,6 +622,7 @@ def main(argv=None) -> int:
             ("attention", lambda: bench_attention(10, 2, cpu=not args.no_cpu)),
             ("attention backward", lambda: bench_attention_backward(10, 2, cpu=not args.no_cpu)),
             ("formats", lambda: bench_formats(5, 1, cpu=not args.no_cpu)),
+            ("bsr spmv", lambda: bench_bsr_spmv(20, 3, cpu=not args.no_cpu)),
         ]
         for name, fn in jobs:
             try:

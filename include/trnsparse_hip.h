@@ -81,6 +81,24 @@ int tsp_bsr_row_order(const int64_t* block_row_ptrs, int64_t n_block_rows,
                       int32_t* order, void* stream);
 
 /* ======================================================================
+ * BSR times one vector, fused with a solver's vector update:
+ *   out[r] = alpha * (A_bsr x)[r] + beta * u[r] + gamma * v[r] + delta * w[r]
+ * for r < m; u, v, w (m,) are optional (NULL: term skipped). x (n,) is
+ * read as zero past n. out may alias u, v or w but not x. dtype of blocks,
+ * x, u, v, w and out: TSP_F32 / TSP_F64 / TSP_BF16 (fp32 accumulation, fp64
+ * for F64). row_order: optional heaviest-first block-row permutation.
+ * Replaces bsr_spmm with N = 1 (trnsparse/ops.py:162-192 as the reference's
+ * solvers call it, trnsparse/iterative.py:44-50) and the update statements
+ * of richardson_bsr / chebyshev_bsr (iterative.py:256-295, 200-253).
+ * ==================================================================== */
+int tsp_bsr_spmv(const void* blocks, int dtype, const int64_t* block_row_ptrs,
+                 const int64_t* block_col_indices, int64_t n_blocks,
+                 int64_t block_size, int64_t m, int64_t n, const void* x,
+                 double alpha, const void* u, double beta, const void* v,
+                 double gamma, const void* w, double delta, void* out,
+                 const int32_t* row_order, void* stream);
+
+/* ======================================================================
  * Backward of C = A_bsr @ B.
  *
  * Replaces the backward of _BSRSpMMFunction

@@ -26,6 +26,11 @@ How each function is pinned (tests/test_oracle.py):
   hand-built values straddling fl32(1e-10) (torch's fp32 compare).
 - block_sparse_attention: dense masked softmax (numpy), a full mask equals
   dense attention, empty block rows give zeros.
+- chebyshev_coeffs / chebyshev / richardson: closed forms — the
+  reference's recurrence gives alpha_k = (2/c) U_k(s)/U_{k+1}(s), beta_k =
+  U_{k-1}(s)/U_{k+1}(s) (s = d/c, U: Chebyshev polynomials of the second
+  kind) and the residual polynomial U_K((d - lam)/c) / U_K(s); both solvers
+  on diagonal matrices against their closed-form iterates.
 - block_sparse_attention_backward: torch float64 autograd through a dense
   masked softmax attention (empty block rows and rows past S // b give zero
   output there, keys past S absent), on full, local, ragged and
@@ -303,6 +308,55 @@ def dense_masked_attention(Q, K, V, mask, scale):
     p = np.exp(sc - mx)
     p /= p.sum(axis=1, keepdims=True)
     return p @ V.astype(np.float64)
+
+
+# ------------------------------------------------------------- solvers
+
+
+def chebyshev_coeffs(lam_min, lam_max, K, dtype=np.float32):
+    """(alpha, beta) of the fixed-step Chebyshev iteration in momentum form
+    as the reference computes them (iterative.py:148-197, after Barrett et
+    al., Templates, 1994, Algorithm 2.1): alpha_0 = 1/d and the generic step
+    from k = 1 on, which makes the residual polynomial the second-kind
+    U_K((d - lam)/c) / U_K(d/c); float64 recurrence, returned in `dtype`."""
+    c, d = (lam_max - lam_min) / 2.0, (lam_max + lam_min) / 2.0
+    alpha, beta = np.zeros(K), np.zeros(K)
+    if K:
+        alpha[0] = prev = 1.0 / d
+        for k in range(1, K):
+            t = (c * prev / 2.0) ** 2
+            alpha[k] = 1.0 / (d - t / prev)
+            beta[k] = alpha[k] * t / prev
+            prev = alpha[k]
+    return alpha.astype(dtype), beta.astype(dtype)
+
+
+def richardson(matvec, b, omega, K, x0=None):
+    """K steps of x <- x + omega (b - A x) in float64 (reference iterative.py:256-295)."""
+    x = np.zeros_like(b, dtype=np.float64) if x0 is None else np.array(x0, dtype=np.float64)
+    for _ in range(K):
+        x = x + omega * (b - matvec(x))
+    return x
+
+
+def chebyshev(matvec, b, alpha, beta, K, x0=None):
+    """K Chebyshev steps in float64 with the given coefficients (reference
+    iterative.py:200-253): x_{k+1} = x_k + alpha_k r_k + beta_k (x_k - x_{k-1})."""
+    x = np.zeros_like(b, dtype=np.float64) if x0 is None else np.array(x0, dtype=np.float64)
+    x_prev = x.copy()
+    for k in range(K):
+        x_new = x + float(alpha[k]) * (b - matvec(x))
+        if k > 0:
+            x_new = x_new + float(beta[k]) * (x - x_prev)
+        x_prev, x = x, x_new
+    return x
+
+
+def bsr_matvec(blocks, col_idx, row_ptrs, shape, b):
+    """x -> A x in float64 for a BSR matrix (the N = 1 case of bsr_spmm)."""
+    def mv(x):
+        return bsr_spmm(blocks, col_idx, row_ptrs, shape, b, np.asarray(x, dtype=np.float64)[:, None])[:, 0]
+    return mv
 
 
 # ------------------------------------------------------------- metrics

@@ -346,6 +346,85 @@ def test_attention_backward_vs_dense_autograd(S, D, b, mask):
     assert not cK[:b].any() and not cV[2 * b :].any()
 
 
+def _cheb_U(K, t):
+    """Chebyshev polynomial of the second kind U_K(t), closed forms:
+    sin((K+1) th) / sin th for t = cos th, sinh((K+1) th) / sinh th for
+    t = cosh th, U_K(-t) = (-1)^K U_K(t)."""
+    t = np.asarray(t, dtype=np.float64)
+    a = np.abs(t)
+    out = np.empty_like(a)
+    inside = a < 1
+    th = np.arccos(a[inside])
+    out[inside] = np.sin((K + 1) * th) / np.sin(th)
+    th = np.arccosh(np.maximum(a[~inside], 1.0))
+    out[~inside] = np.where(th > 0, np.sinh((K + 1) * th) / np.where(th > 0, np.sinh(th), 1.0), K + 1.0)
+    return out * np.where(t < 0, (-1.0) ** K, 1.0)
+
+
+@pytest.mark.parametrize("lo,hi,K", [(1.0, 10.0, 12), (0.5, 2.0, 30), (3.0, 3.5, 5)])
+def test_chebyshev_coeffs_closed_form(lo, hi, K):
+    """The reference's recurrence (alpha_0 = 1/d, then the generic step from
+    k = 1) has rho_k = c alpha_k / 2 = U_k(s) / U_{k+1}(s), s = d / c, so
+    alpha_k = (2/c) U_k(s)/U_{k+1}(s), beta_k = U_{k-1}(s)/U_{k+1}(s), and the
+    scalar error recurrence e_{k+1} = (1 - alpha_k lam) e_k + beta_k (e_k -
+    e_{k-1}), e_0 = 1, ends at U_K((d - lam)/c) / U_K(s): a Chebyshev
+    polynomial of the second kind."""
+    alpha, beta = ref.chebyshev_coeffs(lo, hi, K, dtype=np.float64)
+    c, d = (hi - lo) / 2, (hi + lo) / 2
+    s_ = d / c
+    k = np.arange(K)
+    np.testing.assert_allclose(alpha, (2 / c) * np.array([_cheb_U(int(i), s_)[()] / _cheb_U(int(i) + 1, s_)[()]
+                                                         for i in k]), rtol=1e-12)
+    np.testing.assert_allclose(beta[1:], [_cheb_U(int(i) - 1, s_)[()] / _cheb_U(int(i) + 1, s_)[()] for i in k[1:]],
+                               rtol=1e-12)
+    assert beta[0] == 0
+    lam = np.linspace(lo, hi, 17)
+    e_prev = e = np.ones_like(lam)
+    for i in range(K):
+        e_new = (1 - alpha[i] * lam) * e + (beta[i] * (e - e_prev) if i else 0.0)
+        e_prev, e = e, e_new
+    np.testing.assert_allclose(e, _cheb_U(K, (d - lam) / c) / _cheb_U(K, s_), rtol=1e-9, atol=1e-13)
+    a32, b32 = ref.chebyshev_coeffs(lo, hi, K)
+    assert a32.dtype == np.float32 and np.array_equal(a32, alpha.astype(np.float32))
+
+
+def test_solvers_on_diagonal_matrices_closed_form():
+    lam = np.array([1.0, 2.5, 4.0, 7.0])
+    b = np.array([1.0, -2.0, 0.5, 3.0])
+    mv = lambda x: lam * x
+    omega, K = 0.2, 9
+    np.testing.assert_allclose(ref.richardson(mv, b, omega, K), (1 - (1 - omega * lam) ** K) * b / lam, rtol=1e-12)
+    lo, hi, K = 1.0, 7.0, 6
+    alpha, beta = ref.chebyshev_coeffs(lo, hi, K, dtype=np.float64)
+    c, d = (hi - lo) / 2, (hi + lo) / 2
+    p = _cheb_U(K, (d - lam) / c) / _cheb_U(K, d / c)  # residual polynomial from x0 = 0
+    np.testing.assert_allclose(ref.chebyshev(mv, b, alpha, beta, K), (1 - p) * b / lam, rtol=1e-10)
+
+
+def test_package_solvers_match_oracle_on_cpu():
+    """The torch loops (CPU, pytorch backend) follow the reference's
+    statements; the coefficients agree bit for bit."""
+    import trnsparse_amd as ts
+    from trnsparse_amd import workloads as W
+
+    A, lo, hi = W.spd_bsr(nb=6, b=8, band=1, n_pairs=2, dtype=torch.float64)
+    a_t, b_t = ts.chebyshev_coeffs(lo, hi, 20)
+    a_o, b_o = ref.chebyshev_coeffs(lo, hi, 20)
+    assert np.array_equal(a_t.numpy(), a_o) and np.array_equal(b_t.numpy(), b_o)
+    mv = ref.bsr_matvec(A.blocks.numpy(), A.block_col_indices.numpy(), A.block_row_ptrs.numpy(), A.shape, 8)
+    rhs = torch.randn(48, generator=torch.Generator().manual_seed(1), dtype=torch.float64)
+    prev = ts.get_backend()
+    ts.set_backend("pytorch")
+    try:
+        x, K, rel = ts.richardson_bsr(A, rhs, 2.0 / (lo + hi), K=40)
+        np.testing.assert_allclose(x.numpy(), ref.richardson(mv, rhs.numpy(), 2.0 / (lo + hi), 40), rtol=1e-10)
+        x, K, rel = ts.chebyshev_bsr(A, rhs, lo, hi, K=20)
+        np.testing.assert_allclose(x.numpy(), ref.chebyshev(mv, rhs.numpy(), a_o, b_o, 20), rtol=1e-10)
+        assert K == 20 and rel < 1e-6
+    finally:
+        ts.set_backend(prev)
+
+
 def test_error_metrics():
     ref_ = np.array([1.0, -2.0, 0.0])
     got = np.array([1.0, -2.0 + 1e-3, 1e-6])

@@ -77,6 +77,14 @@ def _bsr_spmm_launch(blocks, rp, ci, order, shape, b, B, out_dtype, dev) -> torc
         raise RuntimeError(f"bsr_spmm: blocks dtype {blocks.dtype} and B dtype {B.dtype} differ")
     blocks_d = _on(blocks, dev)
     B_d = _on(B, dev)
+    if ncols == 1 and out_dtype == blocks.dtype:
+        # one vector: the bandwidth-bound BSR-SpMV kernel
+        x = B_d.reshape(-1)
+        C = torch.empty((m, 1), dtype=out_dtype, device=dev)
+        _lib.call("tsp_bsr_spmv", blocks_d.data_ptr(), _lib.dtype_code(blocks_d.dtype), rp.data_ptr(), ci.data_ptr(),
+                  blocks_d.shape[0], b, m, n, x.data_ptr(), 1.0, None, 0.0, None, 0.0, None, 0.0, C.data_ptr(),
+                  order.data_ptr() if order is not None else None, _lib.stream_handle(dev))
+        return C
     ldb = ncols
     vec = {torch.float32: 4, torch.bfloat16: 8}.get(B_d.dtype)
     if vec and b == 128 and ncols % vec:
@@ -183,6 +191,36 @@ def _bsr_bwd_plan(rp: torch.Tensor, ci: torch.Tensor, mb: int, nbc: int, dev: to
     if nbc:
         _lib.call("tsp_bsr_row_order", cp.data_ptr(), nbc, corder.data_ptr(), _lib.stream_handle(dev))
     return brow.contiguous(), cp, cbid.contiguous(), crow, corder
+
+
+def hip_bsr_matvec_update(A, x: torch.Tensor, alpha: float, out: torch.Tensor, u=None, beta: float = 0.0, v=None,
+                          gamma: float = 0.0, w=None, delta: float = 0.0) -> torch.Tensor:
+    """out = alpha * (A @ x) + beta * u + gamma * v + delta * w in one pass
+    over A (tsp_bsr_spmv). All vectors on one GPU in A's dtype; out must not
+    be x. Used by the fixed-step solvers."""
+    m, n = A.shape
+    dev = x.device
+    rp, ci, order = _bsr_plan(A.block_col_indices, A.block_row_ptrs, (m + A.block_size - 1) // A.block_size, dev,
+                              holder=A)
+    blocks = A.blocks if A.blocks.device == dev else _bsr_blocks_on(A, dev)
+    _lib.call("tsp_bsr_spmv", blocks.data_ptr(), _lib.dtype_code(blocks.dtype), rp.data_ptr(), ci.data_ptr(),
+              blocks.shape[0], A.block_size, m, n, x.data_ptr(), float(alpha), _lib.ptr(u), float(beta), _lib.ptr(v),
+              float(gamma), _lib.ptr(w), float(delta), out.data_ptr(), order.data_ptr(), _lib.stream_handle(dev))
+    return out
+
+
+def _bsr_blocks_on(A, dev):
+    """A's blocks on `dev`, cached on A (keyed by the tensor's identity and version)."""
+    key = (str(dev), A.blocks.data_ptr(), A.blocks._version)
+    cached = getattr(A, "_hip_blocks", None)
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    blocks = A.blocks.to(dev).contiguous()
+    try:
+        A._hip_blocks = (key, blocks)
+    except AttributeError:
+        pass
+    return blocks
 
 
 def hip_bsr_spmm(A, B: torch.Tensor, out_dtype: torch.dtype | None = None) -> torch.Tensor:

@@ -188,3 +188,47 @@ def cfg5_attention(heads: int = 32, seq: int = 8192, d: int = 128, dtype=torch.b
     V = torch.randn(heads, seq, d, generator=g).to(dtype)
     mask = cfg5_block_mask(seq // 128)
     return Q, K, V, bsr_from_block_mask(mask, 128)
+
+
+def spd_bsr(nb: int = 128, b: int = 128, band: int = 1, n_pairs: int = 0, dtype=torch.float32, seed: int = 6):
+    """(A, lam_min, lam_max): a symmetric positive definite BSR matrix for
+    the fixed-step solvers, nb x nb blocks of b x b, with its Gershgorin
+    eigenvalue bounds. Pattern: the block band |i - j| <= band plus n_pairs
+    random symmetric off-band pairs; off-diagonal values N(0,1)/sqrt(b)
+    (block (j, i) = block (i, j)^T), diagonal blocks symmetric N(0,1)/sqrt(b)
+    plus s I with s = 1.5 x the largest off-diagonal absolute row sum, so the
+    spectrum lies in [s - R, s + R] with R <= s / 1.5 (the bounds returned)."""
+    g = torch.Generator().manual_seed(seed)
+    pairs = {(i, j) for i in range(nb) for j in range(i + 1, min(nb, i + band + 1))}
+    while len(pairs) < nb * band - band * (band + 1) // 2 + n_pairs:
+        i, j = sorted(torch.randint(0, nb, (2,), generator=g).tolist())
+        if i != j:
+            pairs.add((i, j))
+    blocks = {}
+    for i, j in sorted(pairs):
+        Bij = torch.randn(b, b, generator=g, dtype=torch.float64) / b**0.5
+        blocks[(i, j)] = Bij
+        blocks[(j, i)] = Bij.T.contiguous()
+    for i in range(nb):
+        Bii = torch.randn(b, b, generator=g, dtype=torch.float64) / b**0.5
+        blocks[(i, i)] = (Bii + Bii.T) / 2
+    rowsum = torch.zeros(nb * b, dtype=torch.float64)
+    for (i, j), Bij in blocks.items():
+        a = Bij.abs().sum(dim=1)
+        if i == j:
+            a = a - Bij.diagonal().abs()
+        rowsum[i * b : (i + 1) * b] += a
+    R = float(rowsum.max())
+    shift = 1.5 * R
+    for i in range(nb):
+        blocks[(i, i)] = blocks[(i, i)] + shift * torch.eye(b, dtype=torch.float64)
+    diag_min = min(float(blocks[(i, i)].diagonal().min()) for i in range(nb))
+    diag_max = max(float(blocks[(i, i)].diagonal().max()) for i in range(nb))
+    keys = sorted(blocks)
+    ptrs = torch.zeros(nb + 1, dtype=torch.long)
+    for i, _ in keys:
+        ptrs[i + 1] += 1
+    ptrs = torch.cumsum(ptrs, 0)
+    A = BSRMatrix(torch.stack([blocks[k] for k in keys]).to(dtype), torch.tensor([j for _, j in keys]), ptrs,
+                  (nb * b, nb * b), b)
+    return A, diag_min - R, diag_max + R

@@ -504,6 +504,34 @@ def bench_formats(steps: int, warmup: int, cpu: bool = False):
     return out
 
 
+def bench_csr_ops(steps: int, warmup: int):
+    """The remaining CSR ops on the device at config 2 (1 M x 1 M, Poisson(16)
+    rows, 16.8 M entries, fp32 values, int64 indices): sparse_transpose
+    (row expansion + stable sort of (col, row) + gather), sparse_add(A, A^T)
+    (sort of 33.6 M keys + segmented sum) and spmv_symmetric (two CSR
+    SpMVs, the strict transpose cached). Reported in entries per second;
+    the sorts dominate the first two."""
+    import numpy as np
+    import torch
+
+    import trnsparse_amd as ts
+    from trnsparse_amd import workloads as W
+
+    v, c, p, x, shape = W.cfg2_csr(dist="poisson", index_dtype=np.int64)
+    A = ts.CSRMatrix(torch.from_numpy(v).cuda(), torch.from_numpy(c).cuda(), torch.from_numpy(p).cuda(), shape)
+    xd = torch.from_numpy(x).cuda()
+    nnz = A.nnz
+    T = ts.sparse_transpose(A)
+    out = []
+    for name, fn, ent in (("sparse_transpose", lambda: ts.sparse_transpose(A), nnz),
+                          ("sparse_add(A, A^T)", lambda: ts.sparse_add(A, T), 2 * nnz),
+                          ("spmv_symmetric (strict transpose cached)", lambda: ts.spmv_symmetric(A, xd), 2 * nnz)):
+        _, ms = time_gpu(fn, steps, warmup)
+        out.append({"name": f"{name} cfg2 1M^2 fp32 (device)", "value": round(ent / (ms * 1e-3) / 1e6, 1),
+                    "unit": "M entries/s", "us": round(ms * 1e3, 1)})
+    return out
+
+
 def calibrate_peaks():
     """Achievable peaks on this box next to the spec ones: a 1 GiB device copy
     (read + write bytes / time), and dense 8192^3 GEMMs in fp32 and bf16
@@ -623,6 +651,7 @@ def main(argv=None) -> int:
             ("attention backward", lambda: bench_attention_backward(10, 2, cpu=not args.no_cpu)),
             ("formats", lambda: bench_formats(5, 1, cpu=not args.no_cpu)),
             ("bsr spmv", lambda: bench_bsr_spmv(20, 3, cpu=not args.no_cpu)),
+            ("csr ops", lambda: bench_csr_ops(5, 1)),
         ]
         for name, fn in jobs:
             try:

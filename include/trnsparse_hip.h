@@ -317,6 +317,17 @@ int tsp_csr_to_dense(const void* values, int dtype, const int64_t* col_indices,
 int tsp_csr_row_indices(const int64_t* row_ptrs, int64_t m, int64_t nnz,
                         int64_t* rows, void* stream);
 int64_t tsp_coo_to_csr_workspace_size(int64_t nnz, int64_t m, int64_t n);
+/* tsp_coo_sum_to_csr: as tsp_coo_to_csr, but one entry per distinct
+ * (row, col) holding the sum of its duplicates in input order (explicit
+ * zeros kept) — the coalesce of sparse_add (trnsparse/ops.py:107-132).
+ * col_out / values_out have room for nnz entries; row_ptrs[m] is the
+ * number written. workspace: tsp_coo_sum_to_csr_workspace_size bytes. */
+int64_t tsp_coo_sum_to_csr_workspace_size(int64_t nnz, int64_t m, int64_t n);
+int tsp_coo_sum_to_csr(const void* values, int dtype, const int64_t* row_indices,
+                       const int64_t* col_indices, int64_t nnz, int64_t m,
+                       int64_t n, int64_t* row_ptrs, int64_t* col_out,
+                       void* values_out, void* workspace,
+                       int64_t workspace_bytes, void* stream);
 int tsp_coo_to_csr(const void* values, int dtype, const int64_t* row_indices,
                    const int64_t* col_indices, int64_t nnz, int64_t m,
                    int64_t n, int64_t* row_ptrs, int64_t* col_out,

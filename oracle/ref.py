@@ -17,6 +17,9 @@ How each function is pinned (tests/test_oracle.py):
   brute-force double loop for negative ones (zeros kept) and NaN entries.
 - coo_to_csr: scipy.sparse for distinct coordinates, a brute-force sort of
   (row, col, position) tuples with duplicates.
+- coo_sum_to_csr / sparse_add / csr_transpose / spmv_symmetric: scipy.sparse
+  sums and transposes (canonical: duplicates summed, sorted), a dense
+  (A + strict(A)^T) @ x for the symmetric SpMV.
 - bsr_spmm_backward: torch float64 autograd through the dense product
   to_dense(A) @ B (dA read back on the stored blocks), empty pattern -> 0.
 - csr_spmv / csr_spmm: scipy.sparse (independent implementation), the
@@ -88,6 +91,57 @@ def coo_to_csr(values, rows, cols, shape):
     row_ptrs = np.zeros(m + 1, dtype=np.int64)
     row_ptrs[1:] = np.cumsum(np.bincount(np.asarray(rows)[order], minlength=m)) if len(order) else 0
     return np.asarray(values)[order], np.asarray(cols, np.int64)[order], row_ptrs
+
+
+def coo_sum_to_csr(values, rows, cols, shape):
+    """Coalesced CSR: one entry per distinct (row, col), ordered by row*n + col,
+    holding the sum of its duplicates in input order (explicit zeros kept) —
+    torch's coalesce as sparse_add uses it (ops.py:107-132)."""
+    v, c, p = coo_to_csr(values, rows, cols, shape)
+    m, n = shape
+    rows_s = np.repeat(np.arange(m), np.diff(p))
+    keys = rows_s * n + c
+    if len(keys) == 0:
+        return v, c, p
+    head = np.ones(len(keys), bool)
+    head[1:] = keys[1:] != keys[:-1]
+    seg = np.cumsum(head) - 1
+    out_v = np.zeros(int(head.sum()), dtype=np.float64)
+    np.add.at(out_v, seg, np.asarray(v, np.float64))
+    out_c = c[head]
+    out_p = np.zeros(m + 1, dtype=np.int64)
+    out_p[1:] = np.cumsum(np.bincount(rows_s[head], minlength=m))
+    return out_v, out_c, out_p
+
+
+def sparse_add(A, B, alpha=1.0, beta=1.0):
+    """(values, col_idx, row_ptrs) of alpha A + beta B on the union pattern
+    (ops.py:107-132); A, B given as (values, col_idx, row_ptrs, shape)."""
+    (va, ca, pa, shape), (vb, cb, pb, _) = A, B
+    ra = np.repeat(np.arange(shape[0]), np.diff(pa))
+    rb = np.repeat(np.arange(shape[0]), np.diff(pb))
+    return coo_sum_to_csr(np.concatenate([alpha * np.asarray(va, np.float64), beta * np.asarray(vb, np.float64)]),
+                          np.concatenate([ra, rb]), np.concatenate([ca, cb]), shape)
+
+
+def csr_transpose(values, col_idx, row_ptrs, shape):
+    """CSR of A^T (ops.py:145-154): rows expanded, (col, row) keys sorted stably."""
+    m, n = shape
+    rows = np.repeat(np.arange(m), np.diff(row_ptrs))
+    return coo_to_csr(values, col_idx, rows, (n, m))
+
+
+def spmv_symmetric(values, col_idx, row_ptrs, shape, x, alpha=1.0, absolute=False):
+    """alpha (A x + S^T x), S = A's entries with row != col (ops.py:81-104), float64."""
+    m, _ = shape
+    rows = np.repeat(np.arange(m), np.diff(row_ptrs))
+    v = np.abs(np.asarray(values, np.float64)) if absolute else np.asarray(values, np.float64)
+    xv = np.abs(np.asarray(x, np.float64)) if absolute else np.asarray(x, np.float64)
+    y = np.zeros(m)
+    np.add.at(y, rows, v * xv[col_idx])
+    off = rows != col_idx
+    np.add.at(y, col_idx[off], v[off] * xv[rows[off]])
+    return abs(alpha) * y if absolute else alpha * y
 
 
 def bsr_to_dense(blocks, col_idx, row_ptrs, shape, b):

@@ -164,6 +164,43 @@ def test_coo_to_csr_vs_scipy_and_brute_force():
     np.testing.assert_array_equal(p, np.concatenate([[0], np.cumsum(np.bincount(rows, minlength=5))]))
 
 
+def test_sparse_add_transpose_symmetric_vs_scipy():
+    rng = np.random.default_rng(14)
+    m, n = 30, 30
+    A = rng.standard_normal((m, n)) * (rng.random((m, n)) < 0.2)
+    B = rng.standard_normal((m, n)) * (rng.random((m, n)) < 0.2)
+    ca, cb = sp.csr_matrix(A), sp.csr_matrix(B)
+    ta = (ca.data, ca.indices.astype(np.int64), ca.indptr.astype(np.int64), (m, n))
+    tb = (cb.data, cb.indices.astype(np.int64), cb.indptr.astype(np.int64), (m, n))
+    v, c, p = ref.sparse_add(ta, tb, 2.0, -0.5)
+    # union pattern (scipy drops exact cancellations; here none occur), values summed
+    want = sp.csr_matrix(2.0 * A - 0.5 * B)
+    want.sort_indices()
+    pattern = sp.csr_matrix((np.abs(A) + np.abs(B)) > 0)
+    np.testing.assert_array_equal(p, pattern.indptr)
+    np.testing.assert_array_equal(c, pattern.indices)
+    np.testing.assert_allclose(v, np.asarray((2.0 * A - 0.5 * B)[pattern.nonzero()]).ravel(), rtol=1e-12)
+    # duplicates inside one operand are summed too; a cancellation stays as an explicit zero
+    vd, cd, pd = ref.coo_sum_to_csr(np.array([1.0, 2.0, -1.0, 4.0]), np.array([0, 0, 0, 1]), np.array([2, 2, 2, 0]),
+                                    (2, 3))
+    np.testing.assert_array_equal(pd, [0, 1, 2])
+    np.testing.assert_array_equal(cd, [2, 0])
+    np.testing.assert_array_equal(vd, [2.0, 4.0])
+    vz, cz, pz = ref.coo_sum_to_csr(np.array([1.0, -1.0]), np.array([0, 0]), np.array([1, 1]), (1, 2))
+    assert len(vz) == 1 and vz[0] == 0.0
+    vt, ct, pt = ref.csr_transpose(*ta)
+    t = ca.T.tocsr()
+    t.sort_indices()
+    np.testing.assert_array_equal(pt, t.indptr)
+    np.testing.assert_array_equal(ct, t.indices)
+    np.testing.assert_array_equal(vt, t.data)
+    x = rng.standard_normal(n)
+    U = np.triu(A)
+    cu = sp.csr_matrix(U)
+    y = ref.spmv_symmetric(cu.data, cu.indices.astype(np.int64), cu.indptr.astype(np.int64), (m, n), x, alpha=1.5)
+    np.testing.assert_allclose(y, 1.5 * (U + np.triu(U, 1).T) @ x, rtol=1e-12, atol=1e-12)
+
+
 # ------------------------------------------------------------------ CSR
 
 

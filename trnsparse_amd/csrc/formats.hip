@@ -16,6 +16,10 @@
 //   CSR to_coo (formats.py:54-65): row index of every entry.
 //   CSR to_dense (formats.py:49-52, torch sparse_csr to_dense): duplicate
 //     entries of a row add up in entry order.
+//   COO to CSR with duplicates summed (the coalesce of sparse_add,
+//     ops.py:107-132): the sorted order above, one entry per distinct
+//     (row, col) holding the sum of its duplicates in input order; explicit
+//     zeros stay.
 // Thresholds compare in the matrix dtype with the threshold rounded to it,
 // as torch compares a tensor with a Python float (double -> float -> bf16
 // for bf16).
@@ -25,6 +29,7 @@
 #include "common.h"
 
 #include <rocprim/device/device_radix_sort.hpp>
+#include <rocprim/device/device_scan.hpp>
 
 namespace {
 
@@ -402,6 +407,54 @@ __global__ __launch_bounds__(256) void coo_row_ptrs_kernel(const uint64_t* __res
   row_ptrs[r] = lo;
 }
 
+// head[k] = 1 where sorted key k starts a run of equal keys
+__global__ __launch_bounds__(256) void run_heads_kernel(const uint64_t* __restrict__ keys, int64_t nnz,
+                                                        int64_t* __restrict__ head) {
+  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (k >= nnz) return;
+  head[k] = (k == 0 || keys[k] != keys[k - 1]) ? 1 : 0;
+}
+
+// for each run head k (seg[k] = its 1-based run index): the run's key, its
+// column and the sum of its values in sorted (= input, the sort is stable)
+// order
+template <typename T>
+__global__ __launch_bounds__(256) void run_sum_kernel(const uint64_t* __restrict__ keys,
+                                                      const int64_t* __restrict__ perm, const int64_t* __restrict__ seg,
+                                                      const int64_t* __restrict__ head, const T* __restrict__ vals,
+                                                      int64_t nnz, int64_t n, uint64_t* __restrict__ ukeys,
+                                                      int64_t* __restrict__ cols_out, T* __restrict__ vals_out) {
+  typedef typename tsp::Acc<T>::type AccT;
+  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (k >= nnz || !head[k]) return;
+  const int64_t s = seg[k] - 1;
+  const uint64_t key = keys[k];
+  AccT sum = tsp::to_acc(vals[perm[k]]);
+  for (int64_t t = k + 1; t < nnz && keys[t] == key; ++t) sum += tsp::to_acc(vals[perm[t]]);
+  ukeys[s] = key;
+  cols_out[s] = (int64_t)(key % (uint64_t)n);
+  vals_out[s] = tsp::from_acc<T>(sum);
+}
+
+// row_ptrs[r] = first run with key >= r * n, over the seg[nnz-1] runs
+__global__ __launch_bounds__(256) void run_row_ptrs_kernel(const uint64_t* __restrict__ ukeys,
+                                                           const int64_t* __restrict__ seg, int64_t nnz, int64_t m,
+                                                           int64_t n, int64_t* __restrict__ row_ptrs) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r > m) return;
+  const int64_t U = seg[nnz - 1];
+  const uint64_t key = (uint64_t)(r * n);
+  int64_t lo = 0, hi = U;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (ukeys[mid] < key)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  row_ptrs[r] = lo;
+}
+
 int key_bits(int64_t m, int64_t n) {
   const uint64_t maxkey = (uint64_t)(m * n);  // keys < m * n
   int bits = 1;
@@ -698,4 +751,74 @@ extern "C" int tsp_coo_to_csr(const void* values, int dtype, const int64_t* row_
   hipLaunchKernelGGL(coo_row_ptrs_kernel, dim3((unsigned)tsp::ceil_div(m + 1, 256)), dim3(256), 0, st, keys_s, nnz, m,
                      n, row_ptrs);
   return tsp::check_launch("coo_row_ptrs launch");
+}
+
+extern "C" int64_t tsp_coo_sum_to_csr_workspace_size(int64_t nnz, int64_t m, int64_t n) {
+  if (nnz < 0 || m < 0 || n < 0) return -1;
+  size_t sort_b = 0, scan_b = 0;
+  if (nnz > 0) {
+    if (rocprim::radix_sort_pairs(nullptr, sort_b, (uint64_t*)nullptr, (uint64_t*)nullptr, (int64_t*)nullptr,
+                                  (int64_t*)nullptr, (size_t)nnz, 0, key_bits(m, n)) != hipSuccess)
+      return -1;
+    if (rocprim::inclusive_scan(nullptr, scan_b, (int64_t*)nullptr, (int64_t*)nullptr, (size_t)nnz,
+                                rocprim::plus<int64_t>()) != hipSuccess)
+      return -1;
+  }
+  const size_t tmp = sort_b > scan_b ? sort_b : scan_b;
+  return 7 * align256(8 * nnz) + align256((int64_t)tmp);
+}
+
+extern "C" int tsp_coo_sum_to_csr(const void* values, int dtype, const int64_t* row_indices,
+                                  const int64_t* col_indices, int64_t nnz, int64_t m, int64_t n, int64_t* row_ptrs,
+                                  int64_t* col_out, void* values_out, void* workspace, int64_t workspace_bytes,
+                                  void* stream) {
+  if (!dtype_ok(dtype)) return tsp::fail(TSP_EUNSUPPORTED, "tsp_coo_sum_to_csr: dtype %d", dtype);
+  if (nnz < 0 || m < 0 || n < 0) return tsp::fail(TSP_EINVAL, "tsp_coo_sum_to_csr: bad size");
+  if (m > 0 && n > 0 && m > INT64_MAX / n) return tsp::fail(TSP_EUNSUPPORTED, "tsp_coo_sum_to_csr: m * n overflows");
+  if (!row_ptrs) return tsp::fail(TSP_EINVAL, "tsp_coo_sum_to_csr: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  if (nnz == 0) return tsp::zero_fill(row_ptrs, 8 * (m + 1), st);
+  if (!values || !row_indices || !col_indices || !col_out || !values_out || !workspace)
+    return tsp::fail(TSP_EINVAL, "tsp_coo_sum_to_csr: null pointer");
+  if (workspace_bytes < tsp_coo_sum_to_csr_workspace_size(nnz, m, n))
+    return tsp::fail(TSP_EINVAL, "tsp_coo_sum_to_csr: workspace too small");
+  const int64_t g = tsp::ceil_div(nnz, 256);
+  if (g > INT32_MAX || tsp::ceil_div(m + 1, 256) > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_coo_sum_to_csr: too large");
+  char* w = (char*)workspace;
+  const int64_t a = align256(8 * nnz);
+  uint64_t* keys = (uint64_t*)w;
+  uint64_t* keys_s = (uint64_t*)(w + a);
+  int64_t* idx = (int64_t*)(w + 2 * a);
+  int64_t* perm = (int64_t*)(w + 3 * a);
+  int64_t* head = (int64_t*)(w + 4 * a);
+  int64_t* seg = (int64_t*)(w + 5 * a);
+  uint64_t* ukeys = (uint64_t*)(w + 6 * a);
+  void* tmp = w + 7 * a;
+  size_t tmp_bytes = (size_t)(workspace_bytes - 7 * a);
+  hipLaunchKernelGGL(coo_keys_kernel, dim3((unsigned)g), dim3(256), 0, st, row_indices, col_indices, nnz, n, keys, idx);
+  int rc = tsp::check_launch("coo_keys launch");
+  if (rc) return rc;
+  if (rocprim::radix_sort_pairs(tmp, tmp_bytes, keys, keys_s, idx, perm, (size_t)nnz, 0, key_bits(m, n), st) !=
+      hipSuccess)
+    return tsp::check_hip(hipGetLastError(), "radix_sort_pairs");
+  hipLaunchKernelGGL(run_heads_kernel, dim3((unsigned)g), dim3(256), 0, st, keys_s, nnz, head);
+  rc = tsp::check_launch("run_heads launch");
+  if (rc) return rc;
+  tmp_bytes = (size_t)(workspace_bytes - 7 * a);
+  if (rocprim::inclusive_scan(tmp, tmp_bytes, head, seg, (size_t)nnz, rocprim::plus<int64_t>(), st) != hipSuccess)
+    return tsp::check_hip(hipGetLastError(), "inclusive_scan");
+  if (dtype == TSP_F32)
+    hipLaunchKernelGGL(run_sum_kernel<float>, dim3((unsigned)g), dim3(256), 0, st, keys_s, perm, seg, head,
+                       (const float*)values, nnz, n, ukeys, col_out, (float*)values_out);
+  else if (dtype == TSP_F64)
+    hipLaunchKernelGGL(run_sum_kernel<double>, dim3((unsigned)g), dim3(256), 0, st, keys_s, perm, seg, head,
+                       (const double*)values, nnz, n, ukeys, col_out, (double*)values_out);
+  else
+    hipLaunchKernelGGL(run_sum_kernel<uint16_t>, dim3((unsigned)g), dim3(256), 0, st, keys_s, perm, seg, head,
+                       (const uint16_t*)values, nnz, n, ukeys, col_out, (uint16_t*)values_out);
+  rc = tsp::check_launch("run_sum launch");
+  if (rc) return rc;
+  hipLaunchKernelGGL(run_row_ptrs_kernel, dim3((unsigned)tsp::ceil_div(m + 1, 256)), dim3(256), 0, st, ukeys, seg, nnz,
+                     m, n, row_ptrs);
+  return tsp::check_launch("run_row_ptrs launch");
 }

@@ -130,3 +130,26 @@ def coo_to_csr(values: torch.Tensor, row_indices: torch.Tensor, col_indices: tor
         _lib.call("tsp_coo_to_csr", v.data_ptr(), _lib.dtype_code(v.dtype), ri.data_ptr(), ci.data_ptr(), nnz, m, n,
                   rp.data_ptr(), col.data_ptr(), val.data_ptr(), ws.data_ptr(), wsb, _stream(dev))
     return val, col, rp
+
+
+def coo_sum_to_csr(values: torch.Tensor, row_indices: torch.Tensor, col_indices: torch.Tensor, shape):
+    """(values, col_indices, row_ptrs) with duplicate coordinates summed in
+    input order — the coalesce in sparse_add (reference ops.py:107-132)."""
+    m, n = shape
+    dev = values.device
+    v = values.contiguous()
+    ri = row_indices.to(dev, torch.int64).contiguous()
+    ci = col_indices.to(dev, torch.int64).contiguous()
+    nnz = v.shape[0]
+    with torch.cuda.device(dev):
+        rp = torch.empty(m + 1, dtype=torch.int64, device=dev)
+        col = torch.empty(max(nnz, 1), dtype=torch.int64, device=dev)
+        val = torch.empty(max(nnz, 1), dtype=v.dtype, device=dev)
+        wsb = _lib.load().tsp_coo_sum_to_csr_workspace_size(nnz, m, n)
+        if wsb < 0:
+            raise RuntimeError(f"tsp_coo_sum_to_csr_workspace_size failed: {_lib.last_error()}")
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+        _lib.call("tsp_coo_sum_to_csr", v.data_ptr(), _lib.dtype_code(v.dtype), ri.data_ptr(), ci.data_ptr(), nnz, m,
+                  n, rp.data_ptr(), col.data_ptr(), val.data_ptr(), ws.data_ptr(), wsb, _stream(dev))
+        u = int(rp[-1].item())
+    return val[:u].clone(), col[:u].clone(), rp

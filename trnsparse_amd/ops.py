@@ -76,9 +76,20 @@ def spmm(
 
 
 def spmv_symmetric(A: CSRMatrix, x: torch.Tensor, alpha: float = 1.0, uplo: str = "upper") -> torch.Tensor:
-    """Symmetric SpMV from one stored triangle (reference ops.py:81-104)."""
+    """Symmetric SpMV from one stored triangle (reference ops.py:81-104):
+    alpha * (A @ x + S^T @ x) with S the entries off the diagonal (duplicates
+    summed); `uplo` is accepted and unused, as there. On the HIP backend with
+    A on the GPU: S^T is built once on the device (transpose by a stable sort
+    of (col, row), cached on A) and the two products run as CSR SpMVs, the
+    second accumulating into the first."""
     m, n = A.shape
     assert m == n, "Matrix must be square for symmetric SpMV"
+    if _use_hip() and A.values.is_cuda:
+        from .hip.dispatch import hip_spmv
+
+        St = _strict_transpose(A)
+        y = hip_spmv(A, x, alpha)
+        return hip_spmv(St, x, alpha, y, 1.0)
     counts = A.row_ptrs[1:] - A.row_ptrs[:-1]
     rows = torch.repeat_interleave(torch.arange(m, device=counts.device), counts)
     cols = A.col_indices
@@ -89,9 +100,48 @@ def spmv_symmetric(A: CSRMatrix, x: torch.Tensor, alpha: float = 1.0, uplo: str 
     return alpha * (_as_torch_csr(A) @ x + strict_t.t() @ x)
 
 
+def _strict_transpose(A: CSRMatrix) -> CSRMatrix:
+    """CSR of the transpose of A's off-diagonal entries (duplicates summed),
+    on A's device; cached on A keyed by the identity and version of its
+    tensors."""
+    key = tuple((t.data_ptr(), t._version) for t in (A.values, A.col_indices, A.row_ptrs))
+    hit = getattr(A, "_strict_t", None)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    from .hip import formats as hf
+
+    coo = A.to_coo()
+    keep = coo.row_indices != coo.col_indices
+    vals, cols, rp = hf.coo_sum_to_csr(coo.values[keep], coo.col_indices[keep], coo.row_indices[keep],
+                                       (A.shape[1], A.shape[0]))
+    St = CSRMatrix(values=vals, col_indices=cols, row_ptrs=rp, shape=(A.shape[1], A.shape[0]))
+    try:
+        A._strict_t = (key, St)
+    except AttributeError:
+        pass
+    return St
+
+
 def sparse_add(A: CSRMatrix, B: CSRMatrix, alpha: float = 1.0, beta: float = 1.0) -> CSRMatrix:
-    """C = alpha*A + beta*B on the union pattern (reference ops.py:107-132)."""
+    """C = alpha*A + beta*B on the union pattern (reference ops.py:107-132).
+
+    Entries sorted by (row, col), one per distinct coordinate with its
+    duplicates summed (explicit zeros kept). On the HIP backend with A and
+    B on the GPU the coalesce is a device sort and segmented sum
+    (`tsp_coo_sum_to_csr`)."""
     assert A.shape == B.shape, f"Shape mismatch: {A.shape} vs {B.shape}"
+    if _use_hip() and A.values.is_cuda and B.values.is_cuda and A.values.dtype == B.values.dtype:
+        from .hip import formats as hf
+
+        if A.values.dtype in hf.DEVICE_DTYPES:
+            ca, cb = A.to_coo(), B.to_coo()
+            vals, cols, rp = hf.coo_sum_to_csr(
+                torch.cat([alpha * ca.values, beta * cb.values]),
+                torch.cat([ca.row_indices, cb.row_indices]),
+                torch.cat([ca.col_indices, cb.col_indices.to(ca.col_indices.device)]),
+                A.shape,
+            )
+            return CSRMatrix(values=vals, col_indices=cols, row_ptrs=rp, shape=A.shape)
     ca, cb = A.to_coo(), B.to_coo()
     idx = torch.stack(
         [torch.cat([ca.row_indices, cb.row_indices]), torch.cat([ca.col_indices, cb.col_indices])]
@@ -112,7 +162,8 @@ def sparse_scale(A: CSRMatrix, alpha: float) -> CSRMatrix:
 
 
 def sparse_transpose(A: CSRMatrix) -> CSRMatrix:
-    """CSR of A^T (reference ops.py:145-154)."""
+    """CSR of A^T (reference ops.py:145-154); on the device for GPU tensors
+    (row expansion and a stable sort by (col, row), through the formats)."""
     coo = A.to_coo()
     return COOMatrix(
         values=coo.values, row_indices=coo.col_indices, col_indices=coo.row_indices, shape=(A.shape[1], A.shape[0])

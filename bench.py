@@ -507,8 +507,9 @@ def bench_formats(steps: int, warmup: int, cpu: bool = False):
 def bench_csr_ops(steps: int, warmup: int):
     """The remaining CSR ops on the device at config 2 (1 M x 1 M, Poisson(16)
     rows, 16.8 M entries, fp32 values, int64 indices): sparse_transpose
-    (row expansion + stable sort of (col, row) + gather), sparse_add(A, A^T)
-    (sort of 33.6 M keys + segmented sum) and spmv_symmetric (two CSR
+    (stable sort of 32-bit column keys carrying (row, value)),
+    sparse_add(A, A^T) (sort of 33.6 M (row, col) keys carrying the values +
+    segmented sum) and spmv_symmetric (two CSR
     SpMVs, the strict transpose cached). Reported in entries per second;
     the sorts dominate the first two."""
     import numpy as np

@@ -334,6 +334,37 @@ int tsp_coo_to_csr(const void* values, int dtype, const int64_t* row_indices,
                    void* values_out, void* workspace, int64_t workspace_bytes,
                    void* stream);
 
+/* tsp_csr_transpose: CSR of A^T for A (m, n) in CSR — sparse_transpose
+ * (trnsparse/ops.py:145-154: COO swap + to_csr). The entries are stably
+ * sorted by column, so rows ascend within each output row and duplicates
+ * keep their input order: the reference's structure and values, bit for
+ * bit. out_row_ptrs (n+1,) int64, out_col / out_values (nnz,) (out_col
+ * int64 = the original rows). m, n <= 2^32. workspace:
+ * tsp_csr_transpose_workspace_size(nnz, m, n, dtype) bytes. */
+int64_t tsp_csr_transpose_workspace_size(int64_t nnz, int64_t m, int64_t n,
+                                         int dtype);
+/* tsp_csr_sum: the union sum of two CSR operands of shape (m, n) — the
+ * coalesce of sparse_add (trnsparse/ops.py:107-132) with the scaled values
+ * alpha*A.values / beta*B.values passed in (the caller scales them as torch
+ * does). One entry per distinct (row, col), sorted by (row, col), holding
+ * the sum of its duplicates in input order (A's entries before B's);
+ * explicit zeros kept. col_out / values_out have room for nnz_a + nnz_b
+ * entries; row_ptrs[m] is the number written. m, n, nnz_a + nnz_b <= 2^32.
+ * workspace: tsp_csr_sum_workspace_size bytes. */
+int64_t tsp_csr_sum_workspace_size(int64_t nnz_a, int64_t nnz_b, int64_t m,
+                                   int64_t n, int dtype);
+int tsp_csr_sum(const void* a_values, const int64_t* a_cols,
+                const int64_t* a_row_ptrs, int64_t nnz_a, const void* b_values,
+                const int64_t* b_cols, const int64_t* b_row_ptrs, int64_t nnz_b,
+                int dtype, int64_t m, int64_t n, int64_t* row_ptrs,
+                int64_t* col_out, void* values_out, void* workspace,
+                int64_t workspace_bytes, void* stream);
+int tsp_csr_transpose(const void* values, int dtype, const int64_t* col_indices,
+                      const int64_t* row_ptrs, int64_t m, int64_t n,
+                      int64_t nnz, int64_t* out_row_ptrs, int64_t* out_col,
+                      void* out_values, void* workspace,
+                      int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -71,16 +71,85 @@ def test_sparse_add_duplicates_and_cancellation(hip_backend):
     assert got.values.cpu().tolist() == [0.0, 3.0, 5.0]  # (0, 2): 1 + 2 - 3 kept as an explicit zero
 
 
+def test_sparse_add_unsorted_rows_with_repeats(hip_backend):
+    """Both operands with unsorted columns inside rows and repeated
+    coordinates (within A, within B and across): one entry per coordinate,
+    sorted, duplicates summed in input order (A's before B's) — bit-exact
+    against the CPU path, whose coalesce sorts the concatenated COO."""
+    g = torch.Generator().manual_seed(9)
+    m, n = 40, 7
+    def rand_csr(nnz):
+        rows = torch.sort(torch.randint(0, m, (nnz,), generator=g)).values
+        cols = torch.randint(0, n, (nnz,), generator=g)
+        vals = torch.randn(nnz, generator=g)
+        rp = torch.zeros(m + 1, dtype=torch.int64)
+        rp[1:] = torch.bincount(rows, minlength=m).cumsum(0)
+        return ts.CSRMatrix(vals, cols, rp, (m, n))
+    A, B = rand_csr(150), rand_csr(90)
+    got = ts.sparse_add(_cuda(A), _cuda(B), alpha=0.5, beta=3.0)
+    ts.set_backend("pytorch")
+    try:
+        want = ts.sparse_add(A, B, alpha=0.5, beta=3.0)
+    finally:
+        ts.set_backend("hip")
+    _same_structure(got, want)
+    np.testing.assert_allclose(got.values.cpu().double().numpy(), want.values.double().numpy(), rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_sparse_add_long_rows(hip_backend, dtype):
+    """Rows whose union holds more than 2048 entries (the workgroup-per-row
+    path, columns streamed through LDS in tiles) next to short and empty
+    rows; many repeats per column."""
+    g = torch.Generator().manual_seed(11)
+    m, n = 4, 600
+    def csr(counts):
+        rows = torch.repeat_interleave(torch.arange(m), torch.tensor(counts))
+        cols = torch.randint(0, n, (int(sum(counts)),), generator=g)
+        vals = torch.randn(int(sum(counts)), generator=g, dtype=torch.float64).to(dtype)
+        rp = torch.zeros(m + 1, dtype=torch.int64)
+        rp[1:] = torch.tensor(counts).cumsum(0)
+        return ts.CSRMatrix(vals, cols, rp, (m, n))
+    A, B = csr([3000, 10, 0, 5000]), csr([2500, 0, 0, 4100])
+    got = ts.sparse_add(_cuda(A), _cuda(B), alpha=1.0, beta=-2.0)
+    ts.set_backend("pytorch")
+    try:
+        want = ts.sparse_add(A, B, alpha=1.0, beta=-2.0)
+    finally:
+        ts.set_backend("hip")
+    _same_structure(got, want)
+    np.testing.assert_allclose(got.values.cpu().double().numpy(), want.values.double().numpy(),
+                               rtol=1e-5 if dtype == torch.float32 else 1e-12, atol=1e-5 if dtype == torch.float32 else 1e-12)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
 @pytest.mark.parametrize("m,n,density", [(300, 200, 0.05), (1, 40, 0.5), (50, 1, 0.5), (128, 128, 0.0)])
-def test_sparse_transpose_matches_cpu(hip_backend, m, n, density):
-    A = _csr(m, n, density, 3)
+def test_sparse_transpose_matches_cpu(hip_backend, dtype, m, n, density):
+    A = _csr(m, n, density, 3, dtype)
+    got = ts.sparse_transpose(_cuda(A))
+    assert got.values.is_cuda and got.values.dtype == dtype and got.shape == (n, m)
+    want = ts.sparse_transpose(A)
+    _same_structure(got, want)
+    assert torch.equal(got.values.cpu(), want.values)
+    v, c, p = ref.csr_transpose(A.values.float().numpy(), A.col_indices.numpy(), A.row_ptrs.numpy(), A.shape)
+    np.testing.assert_array_equal(got.row_ptrs.cpu().numpy(), p)
+    np.testing.assert_array_equal(got.col_indices.cpu().numpy(), c)
+
+
+def test_sparse_transpose_duplicates_and_unsorted_columns(hip_backend):
+    """A CSR with unsorted columns inside rows and repeated (row, col)
+    entries: rows ascend within each output row and repeats keep their input
+    order, as the reference's stable sort by (col, row) leaves them."""
+    vals = torch.arange(1.0, 10.0)
+    cols = torch.tensor([3, 0, 3, 1, 2, 2, 0, 3, 1])
+    rp = torch.tensor([0, 3, 3, 6, 9])  # row 1 empty
+    A = ts.CSRMatrix(vals, cols, rp, (4, 5))
     got = ts.sparse_transpose(_cuda(A))
     want = ts.sparse_transpose(A)
     _same_structure(got, want)
     assert torch.equal(got.values.cpu(), want.values)
-    v, c, p = ref.csr_transpose(A.values.numpy(), A.col_indices.numpy(), A.row_ptrs.numpy(), A.shape)
-    np.testing.assert_array_equal(got.row_ptrs.cpu().numpy(), p)
-    np.testing.assert_array_equal(got.col_indices.cpu().numpy(), c)
+    assert got.values.cpu().tolist() == [2.0, 7.0, 4.0, 9.0, 5.0, 6.0, 1.0, 3.0, 8.0]
+    assert got.row_ptrs.cpu().tolist() == [0, 2, 4, 6, 9, 9]
 
 
 @pytest.mark.parametrize("n,density", [(500, 0.02), (2048, 0.005)])

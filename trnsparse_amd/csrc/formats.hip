@@ -359,35 +359,79 @@ __global__ __launch_bounds__(256) void zero_rows_kernel(T* __restrict__ out, int
 
 // ------------------------------------------------------------- CSR -> COO
 
-// rows[k] = the row of entry k: the last r with row_ptrs[r] <= k.
-__global__ __launch_bounds__(256) void csr_rows_kernel(const int64_t* __restrict__ row_ptrs, int64_t m, int64_t nnz,
-                                                       int64_t* __restrict__ rows) {
-  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (k >= nnz) return;
-  rows[k] = block_row_of(row_ptrs, m, k);
+// Entry -> row for CSR entries: fn(k, r) with r = the row of entry k (the
+// last r with row_ptrs[r] <= k). A workgroup takes a tile of ETILE
+// consecutive entries; two searches of row_ptrs bound the tile's rows, and
+// when those span at most RSPAN row pointers they are staged in LDS, so each
+// entry's search is a short one there (otherwise over row_ptrs itself).
+constexpr int ETILE = 4096;
+constexpr int RSPAN = 2048;
+
+template <typename Fn>
+__global__ __launch_bounds__(256) void entry_rows_kernel(const int64_t* __restrict__ row_ptrs, int64_t m, int64_t nnz,
+                                                         Fn fn) {
+  __shared__ int64_t srp[RSPAN + 1];
+  __shared__ int64_t span[2];
+  const int64_t e0 = (int64_t)blockIdx.x * ETILE;
+  const int64_t e1 = e0 + ETILE < nnz ? e0 + ETILE : nnz;
+  if (threadIdx.x == 0) {
+    span[0] = block_row_of(row_ptrs, m, e0);
+    span[1] = block_row_of(row_ptrs, m, e1 - 1);
+  }
+  __syncthreads();
+  const int64_t rlo = span[0], nr = span[1] - rlo + 1;  // rows rlo .. rlo + nr - 1
+  const bool staged = nr <= RSPAN;
+  if (staged)
+    for (int64_t i = threadIdx.x; i <= nr; i += 256) srp[i] = row_ptrs[rlo + i];
+  __syncthreads();
+  for (int64_t k = e0 + threadIdx.x; k < e1; k += 256) {
+    int64_t r;
+    if (staged) {
+      int lo = 0, hi = (int)nr;  // srp[lo] <= k < srp[hi]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (srp[mid] <= k)
+          lo = mid;
+        else
+          hi = mid;
+      }
+      r = rlo + lo;
+    } else {
+      r = block_row_of(row_ptrs, m, k);
+    }
+    fn(k, r);
+  }
+}
+
+struct RowsOut {
+  int64_t* rows;
+  __device__ void operator()(int64_t k, int64_t r) const { rows[k] = r; }
+};
+
+template <typename Fn>
+int launch_entry_rows(const int64_t* row_ptrs, int64_t m, int64_t nnz, Fn fn, hipStream_t st, const char* what) {
+  const int64_t g = tsp::ceil_div(nnz, ETILE);
+  if (g > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "%s: too many entries", what);
+  hipLaunchKernelGGL(entry_rows_kernel<Fn>, dim3((unsigned)g), dim3(256), 0, st, row_ptrs, m, nnz, fn);
+  return tsp::check_launch(what);
 }
 
 // ------------------------------------------------------------- COO -> CSR
 
 __global__ __launch_bounds__(256) void coo_keys_kernel(const int64_t* __restrict__ rows,
                                                        const int64_t* __restrict__ cols, int64_t nnz, int64_t n,
-                                                       uint64_t* __restrict__ keys, int64_t* __restrict__ idx) {
+                                                       uint64_t* __restrict__ keys) {
   const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (k >= nnz) return;
   keys[k] = (uint64_t)(rows[k] * n + cols[k]);
-  idx[k] = k;
 }
 
-template <typename T>
-__global__ __launch_bounds__(256) void coo_gather_kernel(const int64_t* __restrict__ perm,
-                                                         const int64_t* __restrict__ cols, const T* __restrict__ vals,
-                                                         int64_t nnz, int64_t* __restrict__ cols_out,
-                                                         T* __restrict__ vals_out) {
+// column of each sorted key (key = row * n + col)
+__global__ __launch_bounds__(256) void key_cols_kernel(const uint64_t* __restrict__ keys, int64_t nnz, int64_t n,
+                                                       int64_t* __restrict__ cols_out) {
   const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (k >= nnz) return;
-  const int64_t p = perm[k];
-  cols_out[k] = cols[p];
-  vals_out[k] = vals[p];
+  cols_out[k] = (int64_t)(keys[k] % (uint64_t)n);
 }
 
 // row_ptrs[r] = first k with sorted key >= r * n (r = 0 .. m).
@@ -416,11 +460,21 @@ __global__ __launch_bounds__(256) void run_heads_kernel(const uint64_t* __restri
 }
 
 // for each run head k (seg[k] = its 1-based run index): the run's key, its
-// column and the sum of its values in sorted (= input, the sort is stable)
-// order
-template <typename T>
+// column and the sum of its values (sorted along with the keys) in sorted
+// (= input, the sort is stable) order
+// Keys: row * n + col, or (PACKED) row << 32 | col.
+template <bool PACKED>
+__device__ inline int64_t key_col(uint64_t key, int64_t n) {
+  return PACKED ? (int64_t)(key & 0xffffffffull) : (int64_t)(key % (uint64_t)n);
+}
+template <bool PACKED>
+__device__ inline uint64_t row_key(int64_t r, int64_t n) {
+  return PACKED ? (uint64_t)r << 32 : (uint64_t)(r * n);
+}
+
+template <typename T, bool PACKED = false>
 __global__ __launch_bounds__(256) void run_sum_kernel(const uint64_t* __restrict__ keys,
-                                                      const int64_t* __restrict__ perm, const int64_t* __restrict__ seg,
+                                                      const int64_t* __restrict__ seg,
                                                       const int64_t* __restrict__ head, const T* __restrict__ vals,
                                                       int64_t nnz, int64_t n, uint64_t* __restrict__ ukeys,
                                                       int64_t* __restrict__ cols_out, T* __restrict__ vals_out) {
@@ -429,21 +483,22 @@ __global__ __launch_bounds__(256) void run_sum_kernel(const uint64_t* __restrict
   if (k >= nnz || !head[k]) return;
   const int64_t s = seg[k] - 1;
   const uint64_t key = keys[k];
-  AccT sum = tsp::to_acc(vals[perm[k]]);
-  for (int64_t t = k + 1; t < nnz && keys[t] == key; ++t) sum += tsp::to_acc(vals[perm[t]]);
+  AccT sum = tsp::to_acc(vals[k]);
+  for (int64_t t = k + 1; t < nnz && keys[t] == key; ++t) sum += tsp::to_acc(vals[t]);
   ukeys[s] = key;
-  cols_out[s] = (int64_t)(key % (uint64_t)n);
+  cols_out[s] = key_col<PACKED>(key, n);
   vals_out[s] = tsp::from_acc<T>(sum);
 }
 
 // row_ptrs[r] = first run with key >= r * n, over the seg[nnz-1] runs
+template <bool PACKED = false>
 __global__ __launch_bounds__(256) void run_row_ptrs_kernel(const uint64_t* __restrict__ ukeys,
                                                            const int64_t* __restrict__ seg, int64_t nnz, int64_t m,
                                                            int64_t n, int64_t* __restrict__ row_ptrs) {
   const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (r > m) return;
   const int64_t U = seg[nnz - 1];
-  const uint64_t key = (uint64_t)(r * n);
+  const uint64_t key = row_key<PACKED>(r, n);
   int64_t lo = 0, hi = U;
   while (lo < hi) {
     const int64_t mid = (lo + hi) >> 1;
@@ -454,6 +509,299 @@ __global__ __launch_bounds__(256) void run_row_ptrs_kernel(const uint64_t* __res
   }
   row_ptrs[r] = lo;
 }
+
+// ------------------------------------------------------------- CSR sum
+//
+// Union sum of two CSR operands (the coalesce of sparse_add). Row r's
+// entries j = 0..n-1 are A's entries of the row followed by B's (input
+// order). Entry i heads its column when no earlier entry has the same
+// column; the heads are the output entries, ranked by column, each holding
+// the sum of its column's entries in input order — what a stable sort of the
+// concatenated COO by (row, col) followed by a run sum gives. Two passes
+// (count heads per row; after a scan, write them). Rows of up to SUM_CAP
+// entries are handled in batches of consecutive rows staged in LDS at once
+// (column with the head flag in bit 31); longer rows take a 256-thread
+// workgroup each that streams the row through LDS in tiles and keeps the
+// head flags in workspace.
+constexpr int SUM_CAP = 4096;
+constexpr int SUM_RPW = 64;
+constexpr int LONG_TILE = 4096;
+
+template <typename T>
+struct SumRow {
+  const T* av;
+  const int64_t* ac;
+  const T* bv;
+  const int64_t* bc;
+  int64_t a0, na, b0, n;
+  __device__ uint32_t col(int64_t j) const { return (uint32_t)(j < na ? ac[a0 + j] : bc[b0 + j - na]); }
+  __device__ typename tsp::Acc<T>::type val(int64_t j) const {
+    return tsp::to_acc(j < na ? av[a0 + j] : bv[b0 + j - na]);
+  }
+};
+
+template <typename T>
+__device__ inline SumRow<T> sum_row(const T* av, const int64_t* ac, const int64_t* ar, const T* bv, const int64_t* bc,
+                                    const int64_t* br, int64_t r) {
+  const int64_t a0 = ar[r], na = ar[r + 1] - a0, b0 = br[r];
+  return SumRow<T>{av, ac, bv, bc, a0, na, b0, na + (br[r + 1] - b0)};
+}
+
+// rows with n <= SUM_CAP: a 256-thread workgroup per chunk of SUM_RPW
+// consecutive rows, whose entries are staged in LDS at once (column with the
+// head flag in bit 31, value, chunk-local row) when they fit SUM_CAP, else
+// row by row; row offsets come from a wavefront scan of the row lengths
+template <typename T, bool WRITE>
+__global__ __launch_bounds__(256) void csr_sum_rows_kernel(const T* __restrict__ av, const int64_t* __restrict__ ac,
+                                                           const int64_t* __restrict__ ar, const T* __restrict__ bv,
+                                                           const int64_t* __restrict__ bc,
+                                                           const int64_t* __restrict__ br, int64_t m,
+                                                           int64_t* __restrict__ ucount,
+                                                           const int64_t* __restrict__ out_rp,
+                                                           int64_t* __restrict__ out_col, T* __restrict__ out_val) {
+  typedef typename tsp::Acc<T>::type AccT;
+  static_assert(SUM_RPW == 64, "one lane per row in the offset scan");
+  __shared__ uint32_t scol[SUM_CAP];
+  __shared__ uint8_t srow[SUM_CAP];  // chunk-local row of each staged entry
+  __shared__ AccT sval[WRITE ? SUM_CAP : 1];
+  __shared__ int64_t ua[SUM_RPW + 1], ub[SUM_RPW + 1];
+  __shared__ int32_t off[SUM_RPW + 1];  // chunk-local entry offsets (long rows count 0)
+  __shared__ int32_t cnt[SUM_RPW];
+  __shared__ int64_t orp[WRITE ? SUM_RPW : 1];  // output row starts
+  const int tid = threadIdx.x;
+  if (!WRITE && blockIdx.x == 0 && tid == 0) ucount[m] = 0;
+  for (int64_t r0 = (int64_t)blockIdx.x * SUM_RPW; r0 < m; r0 += (int64_t)gridDim.x * SUM_RPW) {
+    const int nr = (int)(m - r0 < SUM_RPW ? m - r0 : SUM_RPW);
+    __syncthreads();  // the previous chunk's LDS reads are done
+    if (tid <= nr) {
+      ua[tid] = ar[r0 + tid];
+      ub[tid] = br[r0 + tid];
+      if (WRITE && tid < nr) orp[tid] = out_rp[r0 + tid];
+    }
+    __syncthreads();
+    if (tid < 64) {
+      int32_t x = 0;
+      if (tid < nr) {
+        const int64_t l = (ua[tid + 1] - ua[tid]) + (ub[tid + 1] - ub[tid]);
+        x = l > SUM_CAP ? 0 : (int32_t)l;
+        cnt[tid] = 0;
+      }
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int32_t y = __shfl_up(x, o, 64);
+        if (tid >= o) x += y;
+      }
+      off[tid + 1] = x;
+      if (tid == 0) off[0] = 0;
+    }
+    __syncthreads();
+    const int32_t total = off[nr];
+    // rows [rb, re) staged together: all rows when they fit, else one by one
+    const bool whole = total <= SUM_CAP;
+    for (int rb = 0; rb < nr; rb = whole ? nr : rb + 1) {
+      const int re = whole ? nr : rb + 1;
+      const int32_t base = off[rb], tot = off[re] - base;
+      if (!whole) __syncthreads();  // the previous row's LDS reads are done
+      for (int e = tid; e < tot; e += 256) {
+        int lo = rb, hi = re;  // off[lo] - base <= e < off[hi] - base
+        while (hi - lo > 1) {
+          const int mid = (lo + hi) >> 1;
+          if (off[mid] - base <= e)
+            lo = mid;
+          else
+            hi = mid;
+        }
+        while (off[lo + 1] - base <= e) ++lo;  // skip rows without entries
+        const int64_t j = e - (off[lo] - base);
+        const int64_t na = ua[lo + 1] - ua[lo];
+        const int64_t src = j < na ? ua[lo] + j : ub[lo] + (j - na);
+        srow[e] = (uint8_t)lo;
+        scol[e] = (uint32_t)(j < na ? ac[src] : bc[src]);
+        if (WRITE) sval[e] = tsp::to_acc(j < na ? av[src] : bv[src]);
+      }
+      __syncthreads();
+      for (int e = tid; e < tot; e += 256) {
+        const int k = srow[e];
+        const uint32_t ci = scol[e] & 0x7fffffffu;
+        int dup = 0;
+        for (int j = off[k] - base; j < e; ++j) dup += (scol[j] & 0x7fffffffu) == ci;
+        if (dup == 0) {
+          scol[e] = ci | 0x80000000u;
+          if (!WRITE) atomicAdd(&cnt[k], 1);
+        }
+      }
+      __syncthreads();
+      if (WRITE) {
+        for (int e = tid; e < tot; e += 256) {
+          const uint32_t f = scol[e];
+          if (!(f >> 31)) continue;
+          const int k = srow[e];
+          const uint32_t ci = f & 0x7fffffffu;
+          int64_t rank = 0;
+          AccT sum = sval[e];
+          for (int j = off[k] - base; j < off[k + 1] - base; ++j) {
+            const uint32_t g = scol[j];
+            rank += (g >> 31) && (g & 0x7fffffffu) < ci;
+            if (j > e && (g & 0x7fffffffu) == ci) sum += sval[j];
+          }
+          const int64_t o = orp[k] + rank;
+          out_col[o] = (int64_t)ci;
+          out_val[o] = tsp::from_acc<T>(sum);
+        }
+      }
+    }
+    if (!WRITE) {
+      __syncthreads();
+      // long rows keep the count the long-row kernel writes
+      if (tid < nr && (ua[tid + 1] - ua[tid]) + (ub[tid + 1] - ub[tid]) <= SUM_CAP) ucount[r0 + tid] = cnt[tid];
+    }
+  }
+}
+
+// rows with n > SUM_CAP, one 256-thread workgroup each; hflag: a byte per
+// union entry (row r's entries at ar[r] + br[r] + j)
+template <typename T, bool WRITE>
+__global__ __launch_bounds__(256) void csr_sum_long_kernel(const T* __restrict__ av, const int64_t* __restrict__ ac,
+                                                           const int64_t* __restrict__ ar, const T* __restrict__ bv,
+                                                           const int64_t* __restrict__ bc,
+                                                           const int64_t* __restrict__ br, int64_t m,
+                                                           uint8_t* __restrict__ hflag, int64_t* __restrict__ ucount,
+                                                           const int64_t* __restrict__ out_rp,
+                                                           int64_t* __restrict__ out_col, T* __restrict__ out_val) {
+  typedef typename tsp::Acc<T>::type AccT;
+  __shared__ uint32_t tcol[LONG_TILE];
+  __shared__ uint8_t thead[LONG_TILE];
+  __shared__ AccT tval[LONG_TILE];
+  __shared__ int64_t part[4];
+  __shared__ int64_t longs[256];
+  __shared__ int nlong;
+  const int tid = threadIdx.x;
+  // chunks of 256 rows: the long ones are listed, then taken one at a time
+  for (int64_t c0 = (int64_t)blockIdx.x * 256; c0 < m; c0 += (int64_t)gridDim.x * 256) {
+    __syncthreads();
+    if (tid == 0) nlong = 0;
+    __syncthreads();
+    if (c0 + tid < m) {
+      const int64_t rr = c0 + tid;
+      if ((ar[rr + 1] - ar[rr]) + (br[rr + 1] - br[rr]) > SUM_CAP) longs[atomicAdd(&nlong, 1)] = rr;
+    }
+    __syncthreads();
+    const int nl = nlong;
+    for (int li = 0; li < nl; ++li) {
+      const int64_t r = longs[li];
+      const SumRow<T> R = sum_row(av, ac, ar, bv, bc, br, r);
+      const int64_t n = R.n;
+      uint8_t* hf = hflag + ar[r] + br[r];
+      int64_t heads = 0;
+      if (!WRITE) {
+        // head flags: i heads its column when no j < i has it
+        for (int64_t i0 = 0; i0 < n; i0 += 256) {
+          const int64_t i = i0 + tid;
+          const uint32_t ci = i < n ? R.col(i) : 0xffffffffu;
+          bool h = i < n;
+          for (int64_t t0 = 0; t0 < i0 + 256 && t0 < n; t0 += LONG_TILE) {
+            __syncthreads();
+            for (int64_t j = t0 + tid; j < t0 + LONG_TILE && j < n; j += 256) tcol[j - t0] = R.col(j);
+            __syncthreads();
+            const int64_t jend = i < t0 + LONG_TILE ? i : t0 + LONG_TILE;
+            for (int64_t j = t0; j < jend && h; ++j) h = tcol[j - t0] != ci;
+          }
+          if (i < n) hf[i] = h ? 1 : 0;
+          heads += h;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) heads += __shfl_xor(heads, o, 64);
+        __syncthreads();
+        if ((tid & 63) == 0) part[tid >> 6] = heads;
+        __syncthreads();
+        if (tid == 0) ucount[r] = part[0] + part[1] + part[2] + part[3];
+        __syncthreads();
+        continue;
+      }
+      // write: rank of each head among the heads (by column) and the sum of
+      // its column's entries, tile by tile in input order
+      for (int64_t i0 = 0; i0 < n; i0 += 256) {
+        const int64_t i = i0 + tid;
+        const bool h = i < n && hf[i];
+        const uint32_t ci = i < n ? R.col(i) : 0;
+        int64_t rank = 0;
+        AccT sum = 0;
+        for (int64_t t0 = 0; t0 < n; t0 += LONG_TILE) {
+          __syncthreads();
+          for (int64_t j = t0 + tid; j < t0 + LONG_TILE && j < n; j += 256) {
+            tcol[j - t0] = R.col(j);
+            thead[j - t0] = hf[j];
+            tval[j - t0] = R.val(j);
+          }
+          __syncthreads();
+          if (h) {
+            const int64_t len = n - t0 < LONG_TILE ? n - t0 : LONG_TILE;
+            for (int64_t j = 0; j < len; ++j) {
+              const uint32_t cj = tcol[j];
+              rank += thead[j] && cj < ci;
+              if (cj == ci && t0 + j >= i) sum = t0 + j == i ? tval[j] : sum + tval[j];
+            }
+          }
+        }
+        if (h) {
+          out_col[out_rp[r] + rank] = (int64_t)ci;
+          out_val[out_rp[r] + rank] = tsp::from_acc<T>(sum);
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- CSR transpose
+//
+// A (m x n) -> A^T: entries in CSR order are stably sorted by column alone
+// (32-bit keys), carrying (row, value) as the sort's payload, so within a
+// column the rows stay in increasing order and duplicates keep their input
+// order: the order of the reference's COO swap + sort by (col, row).
+template <typename T>
+struct RowVal {
+  uint32_t row;
+  T val;
+};
+
+template <typename T>
+struct TrKeys {
+  const int64_t* cols;
+  const T* vals;
+  uint32_t* keys;
+  RowVal<T>* payload;
+  __device__ void operator()(int64_t k, int64_t r) const {
+    keys[k] = (uint32_t)cols[k];
+    payload[k] = RowVal<T>{(uint32_t)r, vals[k]};
+  }
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void tr_unpack_kernel(const RowVal<T>* __restrict__ payload, int64_t nnz,
+                                                        int64_t* __restrict__ cols_out, T* __restrict__ vals_out) {
+  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (k >= nnz) return;
+  const RowVal<T> p = payload[k];
+  cols_out[k] = (int64_t)p.row;
+  vals_out[k] = p.val;
+}
+
+// row_ptrs[c] = first k with sorted column key >= c (c = 0 .. n)
+__global__ __launch_bounds__(256) void tr_row_ptrs_kernel(const uint32_t* __restrict__ keys, int64_t nnz, int64_t n,
+                                                          int64_t* __restrict__ row_ptrs) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c > n) return;
+  int64_t lo = 0, hi = nnz;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if ((int64_t)keys[mid] < c)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  row_ptrs[c] = lo;
+}
+
 
 int key_bits(int64_t m, int64_t n) {
   const uint64_t maxkey = (uint64_t)(m * n);  // keys < m * n
@@ -686,22 +1034,46 @@ extern "C" int tsp_csr_row_indices(const int64_t* row_ptrs, int64_t m, int64_t n
   if (m < 0 || nnz < 0) return tsp::fail(TSP_EINVAL, "tsp_csr_row_indices: bad size");
   if (nnz == 0) return TSP_OK;
   if (!row_ptrs || !rows) return tsp::fail(TSP_EINVAL, "tsp_csr_row_indices: null pointer");
-  const int64_t g = tsp::ceil_div(nnz, 256);
-  if (g > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_row_indices: too many entries");
-  hipLaunchKernelGGL(csr_rows_kernel, dim3((unsigned)g), dim3(256), 0, (hipStream_t)stream, row_ptrs, m, nnz, rows);
-  return tsp::check_launch("csr_rows launch");
+  return launch_entry_rows(row_ptrs, m, nnz, RowsOut{rows}, (hipStream_t)stream, "tsp_csr_row_indices");
 }
+
+namespace {
+
+// Stable radix sort of (key, value) pairs with the value type of `dtype`:
+// the values move with their keys, so no permutation has to be gathered
+// afterwards. tmp == nullptr queries the temporary size.
+template <typename K, typename V>
+hipError_t sort_pairs(void* tmp, size_t& tmp_bytes, const K* kin, K* kout, const V* vin, V* vout, int64_t nnz,
+                      int bits, hipStream_t st) {
+  return rocprim::radix_sort_pairs(tmp, tmp_bytes, kin, kout, vin, vout, (size_t)nnz, 0, bits, st);
+}
+
+template <typename K, typename F>
+hipError_t sort_pairs_dtype(int dtype, void* tmp, size_t& tmp_bytes, const K* kin, K* kout, const void* vin,
+                            void* vout, int64_t nnz, int bits, hipStream_t st) {
+  if (dtype == TSP_F32)
+    return sort_pairs(tmp, tmp_bytes, kin, kout, (const F*)vin, (F*)vout, nnz, bits, st);
+  if (dtype == TSP_F64)
+    return sort_pairs(tmp, tmp_bytes, kin, kout, (const double*)vin, (double*)vout, nnz, bits, st);
+  return sort_pairs(tmp, tmp_bytes, kin, kout, (const uint16_t*)vin, (uint16_t*)vout, nnz, bits, st);
+}
+
+int64_t coo_sort_tmp(int dtype, int64_t nnz, int bits) {
+  size_t tmp = 0;
+  if (nnz > 0 && sort_pairs_dtype<uint64_t, float>(dtype, nullptr, tmp, (const uint64_t*)nullptr, (uint64_t*)nullptr,
+                                                   nullptr, nullptr, nnz, bits, 0) != hipSuccess)
+    return -1;
+  return (int64_t)tmp;
+}
+
+}  // namespace
 
 extern "C" int64_t tsp_coo_to_csr_workspace_size(int64_t nnz, int64_t m, int64_t n) {
   if (nnz < 0 || m < 0 || n < 0) return -1;
-  size_t tmp = 0;
-  if (nnz > 0) {
-    const int bits = key_bits(m, n);
-    if (rocprim::radix_sort_pairs(nullptr, tmp, (uint64_t*)nullptr, (uint64_t*)nullptr, (int64_t*)nullptr,
-                                  (int64_t*)nullptr, (size_t)nnz, 0, bits) != hipSuccess)
-      return -1;
-  }
-  return 4 * align256(8 * nnz) + align256((int64_t)tmp);
+  // sized for the widest value type (fp64), which also covers fp32 / bf16
+  const int64_t tmp = coo_sort_tmp(TSP_F64, nnz, nnz > 0 ? key_bits(m, n) : 1);
+  if (tmp < 0) return -1;
+  return 2 * align256(8 * nnz) + align256(tmp);
 }
 
 extern "C" int tsp_coo_to_csr(const void* values, int dtype, const int64_t* row_indices, const int64_t* col_indices,
@@ -725,28 +1097,18 @@ extern "C" int tsp_coo_to_csr(const void* values, int dtype, const int64_t* row_
   char* w = (char*)workspace;
   uint64_t* keys = (uint64_t*)w;
   uint64_t* keys_s = (uint64_t*)(w + align256(8 * nnz));
-  int64_t* idx = (int64_t*)(w + 2 * align256(8 * nnz));
-  int64_t* perm = (int64_t*)(w + 3 * align256(8 * nnz));
-  void* tmp = w + 4 * align256(8 * nnz);
-  size_t tmp_bytes = (size_t)(workspace_bytes - 4 * align256(8 * nnz));
-  hipLaunchKernelGGL(coo_keys_kernel, dim3((unsigned)g), dim3(256), 0, st, row_indices, col_indices, nnz, n, keys, idx);
+  void* tmp = w + 2 * align256(8 * nnz);
+  size_t tmp_bytes = (size_t)(workspace_bytes - 2 * align256(8 * nnz));
+  hipLaunchKernelGGL(coo_keys_kernel, dim3((unsigned)g), dim3(256), 0, st, row_indices, col_indices, nnz, n, keys);
   int rc = tsp::check_launch("coo_keys launch");
   if (rc) return rc;
-  if (rocprim::radix_sort_pairs(tmp, tmp_bytes, keys, keys_s, idx, perm, (size_t)nnz, 0, key_bits(m, n), st) !=
-      hipSuccess)
+  if (sort_pairs_dtype<uint64_t, float>(dtype, tmp, tmp_bytes, keys, keys_s, values, values_out, nnz, key_bits(m, n),
+                                        st) != hipSuccess)
     return tsp::check_hip(hipGetLastError(), "radix_sort_pairs");
   rc = tsp::check_launch("radix_sort_pairs");
   if (rc) return rc;
-  if (dtype == TSP_F32)
-    hipLaunchKernelGGL(coo_gather_kernel<float>, dim3((unsigned)g), dim3(256), 0, st, perm, col_indices,
-                       (const float*)values, nnz, col_out, (float*)values_out);
-  else if (dtype == TSP_F64)
-    hipLaunchKernelGGL(coo_gather_kernel<double>, dim3((unsigned)g), dim3(256), 0, st, perm, col_indices,
-                       (const double*)values, nnz, col_out, (double*)values_out);
-  else
-    hipLaunchKernelGGL(coo_gather_kernel<uint16_t>, dim3((unsigned)g), dim3(256), 0, st, perm, col_indices,
-                       (const uint16_t*)values, nnz, col_out, (uint16_t*)values_out);
-  rc = tsp::check_launch("coo_gather launch");
+  hipLaunchKernelGGL(key_cols_kernel, dim3((unsigned)g), dim3(256), 0, st, keys_s, nnz, n, col_out);
+  rc = tsp::check_launch("key_cols launch");
   if (rc) return rc;
   hipLaunchKernelGGL(coo_row_ptrs_kernel, dim3((unsigned)tsp::ceil_div(m + 1, 256)), dim3(256), 0, st, keys_s, nnz, m,
                      n, row_ptrs);
@@ -755,17 +1117,14 @@ extern "C" int tsp_coo_to_csr(const void* values, int dtype, const int64_t* row_
 
 extern "C" int64_t tsp_coo_sum_to_csr_workspace_size(int64_t nnz, int64_t m, int64_t n) {
   if (nnz < 0 || m < 0 || n < 0) return -1;
-  size_t sort_b = 0, scan_b = 0;
-  if (nnz > 0) {
-    if (rocprim::radix_sort_pairs(nullptr, sort_b, (uint64_t*)nullptr, (uint64_t*)nullptr, (int64_t*)nullptr,
-                                  (int64_t*)nullptr, (size_t)nnz, 0, key_bits(m, n)) != hipSuccess)
-      return -1;
-    if (rocprim::inclusive_scan(nullptr, scan_b, (int64_t*)nullptr, (int64_t*)nullptr, (size_t)nnz,
-                                rocprim::plus<int64_t>()) != hipSuccess)
-      return -1;
-  }
-  const size_t tmp = sort_b > scan_b ? sort_b : scan_b;
-  return 7 * align256(8 * nnz) + align256((int64_t)tmp);
+  const int64_t sort_b = coo_sort_tmp(TSP_F64, nnz, nnz > 0 ? key_bits(m, n) : 1);
+  if (sort_b < 0) return -1;
+  size_t scan_b = 0;
+  if (nnz > 0 && rocprim::inclusive_scan(nullptr, scan_b, (int64_t*)nullptr, (int64_t*)nullptr, (size_t)nnz,
+                                         rocprim::plus<int64_t>()) != hipSuccess)
+    return -1;
+  const int64_t tmp = sort_b > (int64_t)scan_b ? sort_b : (int64_t)scan_b;
+  return 6 * align256(8 * nnz) + align256(tmp);
 }
 
 extern "C" int tsp_coo_sum_to_csr(const void* values, int dtype, const int64_t* row_indices,
@@ -788,37 +1147,203 @@ extern "C" int tsp_coo_sum_to_csr(const void* values, int dtype, const int64_t* 
   const int64_t a = align256(8 * nnz);
   uint64_t* keys = (uint64_t*)w;
   uint64_t* keys_s = (uint64_t*)(w + a);
-  int64_t* idx = (int64_t*)(w + 2 * a);
-  int64_t* perm = (int64_t*)(w + 3 * a);
-  int64_t* head = (int64_t*)(w + 4 * a);
-  int64_t* seg = (int64_t*)(w + 5 * a);
-  uint64_t* ukeys = (uint64_t*)(w + 6 * a);
-  void* tmp = w + 7 * a;
-  size_t tmp_bytes = (size_t)(workspace_bytes - 7 * a);
-  hipLaunchKernelGGL(coo_keys_kernel, dim3((unsigned)g), dim3(256), 0, st, row_indices, col_indices, nnz, n, keys, idx);
+  void* vals_s = w + 2 * a;  // values sorted with their keys (at most 8 bytes each)
+  int64_t* head = (int64_t*)(w + 3 * a);
+  int64_t* seg = (int64_t*)(w + 4 * a);
+  uint64_t* ukeys = (uint64_t*)(w + 5 * a);
+  void* tmp = w + 6 * a;
+  size_t tmp_bytes = (size_t)(workspace_bytes - 6 * a);
+  hipLaunchKernelGGL(coo_keys_kernel, dim3((unsigned)g), dim3(256), 0, st, row_indices, col_indices, nnz, n, keys);
   int rc = tsp::check_launch("coo_keys launch");
   if (rc) return rc;
-  if (rocprim::radix_sort_pairs(tmp, tmp_bytes, keys, keys_s, idx, perm, (size_t)nnz, 0, key_bits(m, n), st) !=
-      hipSuccess)
+  if (sort_pairs_dtype<uint64_t, float>(dtype, tmp, tmp_bytes, keys, keys_s, values, vals_s, nnz, key_bits(m, n),
+                                        st) != hipSuccess)
     return tsp::check_hip(hipGetLastError(), "radix_sort_pairs");
   hipLaunchKernelGGL(run_heads_kernel, dim3((unsigned)g), dim3(256), 0, st, keys_s, nnz, head);
   rc = tsp::check_launch("run_heads launch");
   if (rc) return rc;
-  tmp_bytes = (size_t)(workspace_bytes - 7 * a);
+  tmp_bytes = (size_t)(workspace_bytes - 6 * a);
   if (rocprim::inclusive_scan(tmp, tmp_bytes, head, seg, (size_t)nnz, rocprim::plus<int64_t>(), st) != hipSuccess)
     return tsp::check_hip(hipGetLastError(), "inclusive_scan");
   if (dtype == TSP_F32)
-    hipLaunchKernelGGL(run_sum_kernel<float>, dim3((unsigned)g), dim3(256), 0, st, keys_s, perm, seg, head,
-                       (const float*)values, nnz, n, ukeys, col_out, (float*)values_out);
+    hipLaunchKernelGGL(run_sum_kernel<float>, dim3((unsigned)g), dim3(256), 0, st, keys_s, seg, head,
+                       (const float*)vals_s, nnz, n, ukeys, col_out, (float*)values_out);
   else if (dtype == TSP_F64)
-    hipLaunchKernelGGL(run_sum_kernel<double>, dim3((unsigned)g), dim3(256), 0, st, keys_s, perm, seg, head,
-                       (const double*)values, nnz, n, ukeys, col_out, (double*)values_out);
+    hipLaunchKernelGGL(run_sum_kernel<double>, dim3((unsigned)g), dim3(256), 0, st, keys_s, seg, head,
+                       (const double*)vals_s, nnz, n, ukeys, col_out, (double*)values_out);
   else
-    hipLaunchKernelGGL(run_sum_kernel<uint16_t>, dim3((unsigned)g), dim3(256), 0, st, keys_s, perm, seg, head,
-                       (const uint16_t*)values, nnz, n, ukeys, col_out, (uint16_t*)values_out);
+    hipLaunchKernelGGL(run_sum_kernel<uint16_t>, dim3((unsigned)g), dim3(256), 0, st, keys_s, seg, head,
+                       (const uint16_t*)vals_s, nnz, n, ukeys, col_out, (uint16_t*)values_out);
   rc = tsp::check_launch("run_sum launch");
   if (rc) return rc;
-  hipLaunchKernelGGL(run_row_ptrs_kernel, dim3((unsigned)tsp::ceil_div(m + 1, 256)), dim3(256), 0, st, ukeys, seg, nnz,
+  hipLaunchKernelGGL(run_row_ptrs_kernel<false>, dim3((unsigned)tsp::ceil_div(m + 1, 256)), dim3(256), 0, st, ukeys, seg, nnz,
                      m, n, row_ptrs);
   return tsp::check_launch("run_row_ptrs launch");
+}
+
+namespace {
+
+template <typename T>
+int64_t tr_sort_tmp(int64_t nnz, int bits) {
+  size_t tmp = 0;
+  if (nnz > 0 && sort_pairs(nullptr, tmp, (const uint32_t*)nullptr, (uint32_t*)nullptr, (const RowVal<T>*)nullptr,
+                            (RowVal<T>*)nullptr, nnz, bits, 0) != hipSuccess)
+    return -1;
+  return (int64_t)tmp;
+}
+
+int col_bits(int64_t n) {  // bits of the largest column index n - 1
+  int bits = 1;
+  while (bits < 32 && ((uint64_t)(n > 0 ? n - 1 : 0) >> bits) != 0) ++bits;
+  return bits;
+}
+
+template <typename T>
+int csr_transpose_t(const T* values, const int64_t* col_indices, const int64_t* row_ptrs, int64_t m, int64_t n,
+                    int64_t nnz, int64_t* out_row_ptrs, int64_t* out_col, T* out_values, char* w,
+                    int64_t workspace_bytes, hipStream_t st) {
+  const int64_t g = tsp::ceil_div(nnz, 256);
+  const int64_t ka = align256(4 * nnz), pa = align256((int64_t)sizeof(RowVal<T>) * nnz);
+  uint32_t* keys = (uint32_t*)w;
+  uint32_t* keys_s = (uint32_t*)(w + ka);
+  RowVal<T>* pay = (RowVal<T>*)(w + 2 * ka);
+  RowVal<T>* pay_s = (RowVal<T>*)(w + 2 * ka + pa);
+  void* tmp = w + 2 * ka + 2 * pa;
+  size_t tmp_bytes = (size_t)(workspace_bytes - (2 * ka + 2 * pa));
+  int rc = launch_entry_rows(row_ptrs, m, nnz, TrKeys<T>{col_indices, values, keys, pay}, st, "tr_keys launch");
+  if (rc) return rc;
+  if (sort_pairs(tmp, tmp_bytes, (const uint32_t*)keys, keys_s, (const RowVal<T>*)pay, pay_s, nnz, col_bits(n), st) !=
+      hipSuccess)
+    return tsp::check_hip(hipGetLastError(), "radix_sort_pairs");
+  hipLaunchKernelGGL(tr_unpack_kernel<T>, dim3((unsigned)g), dim3(256), 0, st, (const RowVal<T>*)pay_s, nnz, out_col,
+                     out_values);
+  rc = tsp::check_launch("tr_unpack launch");
+  if (rc) return rc;
+  hipLaunchKernelGGL(tr_row_ptrs_kernel, dim3((unsigned)tsp::ceil_div(n + 1, 256)), dim3(256), 0, st,
+                     (const uint32_t*)keys_s, nnz, n, out_row_ptrs);
+  return tsp::check_launch("tr_row_ptrs launch");
+}
+
+}  // namespace
+
+extern "C" int64_t tsp_csr_transpose_workspace_size(int64_t nnz, int64_t m, int64_t n, int dtype) {
+  if (nnz < 0 || m < 0 || n < 0 || !dtype_ok(dtype)) return -1;
+  const int bits = col_bits(n);
+  int64_t tmp, pay;
+  if (dtype == TSP_F32) {
+    tmp = tr_sort_tmp<float>(nnz, bits);
+    pay = (int64_t)sizeof(RowVal<float>);
+  } else if (dtype == TSP_F64) {
+    tmp = tr_sort_tmp<double>(nnz, bits);
+    pay = (int64_t)sizeof(RowVal<double>);
+  } else {
+    tmp = tr_sort_tmp<uint16_t>(nnz, bits);
+    pay = (int64_t)sizeof(RowVal<uint16_t>);
+  }
+  if (tmp < 0) return -1;
+  return 2 * align256(4 * nnz) + 2 * align256(pay * nnz) + align256(tmp);
+}
+
+extern "C" int tsp_csr_transpose(const void* values, int dtype, const int64_t* col_indices, const int64_t* row_ptrs,
+                                 int64_t m, int64_t n, int64_t nnz, int64_t* out_row_ptrs, int64_t* out_col,
+                                 void* out_values, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!dtype_ok(dtype)) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_transpose: dtype %d", dtype);
+  if (nnz < 0 || m < 0 || n < 0) return tsp::fail(TSP_EINVAL, "tsp_csr_transpose: bad size");
+  if (m > UINT32_MAX || n > (int64_t)UINT32_MAX + 1)
+    return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_transpose: dimensions past 2^32");
+  if (!out_row_ptrs) return tsp::fail(TSP_EINVAL, "tsp_csr_transpose: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  if (nnz == 0) return tsp::zero_fill(out_row_ptrs, 8 * (n + 1), st);
+  if (!values || !col_indices || !row_ptrs || !out_col || !out_values || !workspace)
+    return tsp::fail(TSP_EINVAL, "tsp_csr_transpose: null pointer");
+  if (workspace_bytes < tsp_csr_transpose_workspace_size(nnz, m, n, dtype))
+    return tsp::fail(TSP_EINVAL, "tsp_csr_transpose: workspace too small");
+  if (tsp::ceil_div(nnz, 256) > INT32_MAX || tsp::ceil_div(n + 1, 256) > INT32_MAX)
+    return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_transpose: too large");
+  char* w = (char*)workspace;
+  if (dtype == TSP_F32)
+    return csr_transpose_t((const float*)values, col_indices, row_ptrs, m, n, nnz, out_row_ptrs, out_col,
+                           (float*)out_values, w, workspace_bytes, st);
+  if (dtype == TSP_F64)
+    return csr_transpose_t((const double*)values, col_indices, row_ptrs, m, n, nnz, out_row_ptrs, out_col,
+                           (double*)out_values, w, workspace_bytes, st);
+  return csr_transpose_t((const uint16_t*)values, col_indices, row_ptrs, m, n, nnz, out_row_ptrs, out_col,
+                         (uint16_t*)out_values, w, workspace_bytes, st);
+}
+
+namespace {
+
+int64_t sum_scan_tmp(int64_t m) {
+  size_t b = 0;
+  if (rocprim::exclusive_scan(nullptr, b, (int64_t*)nullptr, (int64_t*)nullptr, (int64_t)0, (size_t)(m + 1),
+                              rocprim::plus<int64_t>()) != hipSuccess)
+    return -1;
+  return (int64_t)b;
+}
+
+template <typename T>
+int csr_sum_t(const T* av, const int64_t* ac, const int64_t* ar, const T* bv, const int64_t* bc, const int64_t* br,
+              int64_t N, int64_t m, int64_t* row_ptrs, int64_t* col_out, T* values_out, char* w,
+              int64_t workspace_bytes, hipStream_t st) {
+  int64_t* ucount = (int64_t*)w;
+  uint8_t* hflag = (uint8_t*)(w + align256(8 * (m + 1)));
+  void* tmp = w + align256(8 * (m + 1)) + align256(N);
+  size_t tb = (size_t)(workspace_bytes - align256(8 * (m + 1)) - align256(N));
+  const int64_t chunks = tsp::ceil_div(m, SUM_RPW);
+  const unsigned g = (unsigned)(chunks < 65536 ? chunks : 65536);
+  const unsigned gl = (unsigned)(m < 1024 ? m : 1024);
+  hipLaunchKernelGGL((csr_sum_rows_kernel<T, false>), dim3(g), dim3(256), 0, st, av, ac, ar, bv, bc, br, m, ucount,
+                     (const int64_t*)nullptr, (int64_t*)nullptr, (T*)nullptr);
+  int rc = tsp::check_launch("csr_sum_rows (count) launch");
+  if (rc) return rc;
+  hipLaunchKernelGGL((csr_sum_long_kernel<T, false>), dim3(gl), dim3(256), 0, st, av, ac, ar, bv, bc, br, m, hflag,
+                     ucount, (const int64_t*)nullptr, (int64_t*)nullptr, (T*)nullptr);
+  rc = tsp::check_launch("csr_sum_long (count) launch");
+  if (rc) return rc;
+  if (rocprim::exclusive_scan(tmp, tb, ucount, row_ptrs, (int64_t)0, (size_t)(m + 1), rocprim::plus<int64_t>(), st) !=
+      hipSuccess)
+    return tsp::check_hip(hipGetLastError(), "exclusive_scan");
+  hipLaunchKernelGGL((csr_sum_rows_kernel<T, true>), dim3(g), dim3(256), 0, st, av, ac, ar, bv, bc, br, m,
+                     (int64_t*)nullptr, (const int64_t*)row_ptrs, col_out, values_out);
+  rc = tsp::check_launch("csr_sum_rows (write) launch");
+  if (rc) return rc;
+  hipLaunchKernelGGL((csr_sum_long_kernel<T, true>), dim3(gl), dim3(256), 0, st, av, ac, ar, bv, bc, br, m, hflag,
+                     (int64_t*)nullptr, (const int64_t*)row_ptrs, col_out, values_out);
+  return tsp::check_launch("csr_sum_long (write) launch");
+}
+
+}  // namespace
+
+extern "C" int64_t tsp_csr_sum_workspace_size(int64_t nnz_a, int64_t nnz_b, int64_t m, int64_t n, int dtype) {
+  if (nnz_a < 0 || nnz_b < 0 || m < 0 || n < 0 || !dtype_ok(dtype)) return -1;
+  const int64_t tmp = sum_scan_tmp(m);
+  if (tmp < 0) return -1;
+  return align256(8 * (m + 1)) + align256(nnz_a + nnz_b) + align256(tmp);
+}
+
+extern "C" int tsp_csr_sum(const void* a_values, const int64_t* a_cols, const int64_t* a_row_ptrs, int64_t nnz_a,
+                           const void* b_values, const int64_t* b_cols, const int64_t* b_row_ptrs, int64_t nnz_b,
+                           int dtype, int64_t m, int64_t n, int64_t* row_ptrs, int64_t* col_out, void* values_out,
+                           void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!dtype_ok(dtype)) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_sum: dtype %d", dtype);
+  if (nnz_a < 0 || nnz_b < 0 || m < 0 || n < 0) return tsp::fail(TSP_EINVAL, "tsp_csr_sum: bad size");
+  if (m > UINT32_MAX || n > (int64_t)UINT32_MAX + 1 || nnz_a + nnz_b > UINT32_MAX)
+    return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_sum: sizes past 2^32");
+  if (!row_ptrs) return tsp::fail(TSP_EINVAL, "tsp_csr_sum: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  if (nnz_a + nnz_b == 0) return tsp::zero_fill(row_ptrs, 8 * (m + 1), st);
+  if (!a_row_ptrs || !b_row_ptrs || !col_out || !values_out || !workspace ||
+      (nnz_a > 0 && (!a_values || !a_cols)) || (nnz_b > 0 && (!b_values || !b_cols)))
+    return tsp::fail(TSP_EINVAL, "tsp_csr_sum: null pointer");
+  if (workspace_bytes < tsp_csr_sum_workspace_size(nnz_a, nnz_b, m, n, dtype))
+    return tsp::fail(TSP_EINVAL, "tsp_csr_sum: workspace too small");
+  char* w = (char*)workspace;
+  if (dtype == TSP_F32)
+    return csr_sum_t((const float*)a_values, a_cols, a_row_ptrs, (const float*)b_values, b_cols, b_row_ptrs, nnz_a + nnz_b, m,
+                     row_ptrs, col_out, (float*)values_out, w, workspace_bytes, st);
+  if (dtype == TSP_F64)
+    return csr_sum_t((const double*)a_values, a_cols, a_row_ptrs, (const double*)b_values, b_cols, b_row_ptrs, nnz_a + nnz_b, m,
+                     row_ptrs, col_out, (double*)values_out, w, workspace_bytes, st);
+  return csr_sum_t((const uint16_t*)a_values, a_cols, a_row_ptrs, (const uint16_t*)b_values, b_cols, b_row_ptrs, nnz_a + nnz_b, m,
+                   row_ptrs, col_out, (uint16_t*)values_out, w, workspace_bytes, st);
 }

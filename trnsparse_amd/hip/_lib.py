@@ -64,6 +64,10 @@ SIGNATURES: dict[str, tuple] = {
     "tsp_coo_to_csr": (_INT, [_P, _INT, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "tsp_coo_sum_to_csr_workspace_size": (_I64, [_I64, _I64, _I64]),
     "tsp_coo_sum_to_csr": (_INT, [_P, _INT, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
+    "tsp_csr_transpose_workspace_size": (_I64, [_I64, _I64, _I64, _INT]),
+    "tsp_csr_sum_workspace_size": (_I64, [_I64, _I64, _I64, _I64, _INT]),
+    "tsp_csr_sum": (_INT, [_P, _P, _P, _I64, _P, _P, _P, _I64, _INT, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
+    "tsp_csr_transpose": (_INT, [_P, _INT, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "tsp_bsa_bwd_plan": (_I64, [_P, _I64, _I64, _I64, _I64, _P, _I64]),
     "tsp_bsa_bwd_workspace_size": (_I64, [_I64, _I64, _I64]),
     "tsp_bsa_bwd": (

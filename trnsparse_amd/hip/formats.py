@@ -153,3 +153,55 @@ def coo_sum_to_csr(values: torch.Tensor, row_indices: torch.Tensor, col_indices:
                   n, rp.data_ptr(), col.data_ptr(), val.data_ptr(), ws.data_ptr(), wsb, _stream(dev))
         u = int(rp[-1].item())
     return val[:u].clone(), col[:u].clone(), rp
+
+
+def csr_transpose(values: torch.Tensor, col_indices: torch.Tensor, row_ptrs: torch.Tensor, shape):
+    """(values, col_indices, row_ptrs) of A^T (reference ops.py:145-154): a
+    stable device sort of the entries by column, rows carried along."""
+    m, n = shape
+    dev = values.device
+    v = values.contiguous()
+    ci = col_indices.to(dev, torch.int64).contiguous()
+    rp = row_ptrs.to(dev, torch.int64).contiguous()
+    nnz = v.shape[0]
+    code = _lib.dtype_code(v.dtype)
+    with torch.cuda.device(dev):
+        out_rp = torch.empty(n + 1, dtype=torch.int64, device=dev)
+        out_col = torch.empty(nnz, dtype=torch.int64, device=dev)
+        out_val = torch.empty(nnz, dtype=v.dtype, device=dev)
+        wsb = _lib.load().tsp_csr_transpose_workspace_size(nnz, m, n, code)
+        if wsb < 0:
+            raise RuntimeError(f"tsp_csr_transpose_workspace_size failed: {_lib.last_error()}")
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+        _lib.call("tsp_csr_transpose", v.data_ptr(), code, ci.data_ptr(), rp.data_ptr(), m, n, nnz, out_rp.data_ptr(),
+                  out_col.data_ptr(), out_val.data_ptr(), ws.data_ptr(), wsb, _stream(dev))
+    return out_val, out_col, out_rp
+
+
+def csr_sum(a_values: torch.Tensor, a_cols: torch.Tensor, a_row_ptrs: torch.Tensor, b_values: torch.Tensor,
+            b_cols: torch.Tensor, b_row_ptrs: torch.Tensor, shape):
+    """(values, col_indices, row_ptrs) of the union sum of two CSR operands
+    with duplicates summed in input order (the coalesce in sparse_add,
+    reference ops.py:107-132): per row, A's entries then B's, stably sorted
+    by column on the device."""
+    m, n = shape
+    dev = a_values.device
+    av, bv = a_values.contiguous(), b_values.to(dev).contiguous()
+    ac, bc = (c.to(dev, torch.int64).contiguous() for c in (a_cols, b_cols))
+    ar, br = (r.to(dev, torch.int64).contiguous() for r in (a_row_ptrs, b_row_ptrs))
+    na, nb = av.shape[0], bv.shape[0]
+    code = _lib.dtype_code(av.dtype)
+    with torch.cuda.device(dev):
+        rp = torch.empty(m + 1, dtype=torch.int64, device=dev)
+        col = torch.empty(max(na + nb, 1), dtype=torch.int64, device=dev)
+        val = torch.empty(max(na + nb, 1), dtype=av.dtype, device=dev)
+        wsb = _lib.load().tsp_csr_sum_workspace_size(na, nb, m, n, code)
+        if wsb < 0:
+            raise RuntimeError(f"tsp_csr_sum_workspace_size failed: {_lib.last_error()}")
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+        _lib.call("tsp_csr_sum", av.data_ptr(), ac.data_ptr(), ar.data_ptr(), na, bv.data_ptr(), bc.data_ptr(),
+                  br.data_ptr(), nb, code, m, n, rp.data_ptr(), col.data_ptr(), val.data_ptr(), ws.data_ptr(), wsb,
+                  _stream(dev))
+        u = int(rp[-1].item())
+    return val[:u].clone(), col[:u].clone(), rp
+

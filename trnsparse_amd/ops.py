@@ -127,20 +127,16 @@ def sparse_add(A: CSRMatrix, B: CSRMatrix, alpha: float = 1.0, beta: float = 1.0
 
     Entries sorted by (row, col), one per distinct coordinate with its
     duplicates summed (explicit zeros kept). On the HIP backend with A and
-    B on the GPU the coalesce is a device sort and segmented sum
-    (`tsp_coo_sum_to_csr`)."""
+    B on the GPU the coalesce runs on the device (`tsp_csr_sum`: each row's
+    entries of A then B, stably sorted by column, runs summed); the values
+    are scaled by torch first, as in the reference."""
     assert A.shape == B.shape, f"Shape mismatch: {A.shape} vs {B.shape}"
     if _use_hip() and A.values.is_cuda and B.values.is_cuda and A.values.dtype == B.values.dtype:
         from .hip import formats as hf
 
         if A.values.dtype in hf.DEVICE_DTYPES:
-            ca, cb = A.to_coo(), B.to_coo()
-            vals, cols, rp = hf.coo_sum_to_csr(
-                torch.cat([alpha * ca.values, beta * cb.values]),
-                torch.cat([ca.row_indices, cb.row_indices]),
-                torch.cat([ca.col_indices, cb.col_indices.to(ca.col_indices.device)]),
-                A.shape,
-            )
+            vals, cols, rp = hf.csr_sum(alpha * A.values, A.col_indices, A.row_ptrs, beta * B.values,
+                                        B.col_indices, B.row_ptrs, A.shape)
             return CSRMatrix(values=vals, col_indices=cols, row_ptrs=rp, shape=A.shape)
     ca, cb = A.to_coo(), B.to_coo()
     idx = torch.stack(
@@ -162,8 +158,16 @@ def sparse_scale(A: CSRMatrix, alpha: float) -> CSRMatrix:
 
 
 def sparse_transpose(A: CSRMatrix) -> CSRMatrix:
-    """CSR of A^T (reference ops.py:145-154); on the device for GPU tensors
-    (row expansion and a stable sort by (col, row), through the formats)."""
+    """CSR of A^T (reference ops.py:145-154). On the HIP backend with A on
+    the GPU: a stable device sort of the entries by column with the rows
+    carried along (`tsp_csr_transpose`), the same order as the reference's
+    sort by (col, row)."""
+    if _use_hip() and A.values.is_cuda:
+        from .hip import formats as hf
+
+        if A.values.dtype in hf.DEVICE_DTYPES:
+            vals, cols, rp = hf.csr_transpose(A.values, A.col_indices, A.row_ptrs, A.shape)
+            return CSRMatrix(values=vals, col_indices=cols, row_ptrs=rp, shape=(A.shape[1], A.shape[0]))
     coo = A.to_coo()
     return COOMatrix(
         values=coo.values, row_indices=coo.col_indices, col_indices=coo.row_indices, shape=(A.shape[1], A.shape[0])

@@ -61,6 +61,13 @@ def test_argument_validation_is_host_side():
     assert st == -1 and b"block_size" in lib.tsp_last_error()
     st = lib.tsp_bsr_spmm(None, 7, None, None, 0, 128, 1, 1, None, 1, 1, None, 1, 0, None, None)
     assert st == -2
+    # CSR structure ops: entries without rows, bad dtype, short workspace
+    assert lib.tsp_csr_row_indices(None, 0, 5, None, None) == -1
+    assert lib.tsp_csr_transpose(None, 0, None, None, 0, 4, 5, None, None, None, None, 0, None) == -1
+    assert lib.tsp_csr_transpose(None, 9, None, None, 3, 4, 5, None, None, None, None, 0, None) == -2
+    assert lib.tsp_csr_sum(None, None, None, 2, None, None, None, 0, 0, 0, 4, None, None, None, None, 0, None) == -1
+    assert lib.tsp_csr_transpose_workspace_size(10, 3, 4, 9) == -1 and lib.tsp_csr_sum_workspace_size(-1, 0, 3, 4, 0) == -1
+    assert lib.tsp_csr_sum(None, None, None, 1, None, None, None, 1, 0, 2, 4, None, None, None, None, 0, None) == -1
 
 
 def _plan(cp, H, S, b):

@@ -1031,7 +1031,7 @@ extern "C" int tsp_csr_to_dense(const void* values, int dtype, const int64_t* co
 }
 
 extern "C" int tsp_csr_row_indices(const int64_t* row_ptrs, int64_t m, int64_t nnz, int64_t* rows, void* stream) {
-  if (m < 0 || nnz < 0) return tsp::fail(TSP_EINVAL, "tsp_csr_row_indices: bad size");
+  if (m < 0 || nnz < 0 || (m == 0 && nnz > 0)) return tsp::fail(TSP_EINVAL, "tsp_csr_row_indices: bad size");
   if (nnz == 0) return TSP_OK;
   if (!row_ptrs || !rows) return tsp::fail(TSP_EINVAL, "tsp_csr_row_indices: null pointer");
   return launch_entry_rows(row_ptrs, m, nnz, RowsOut{rows}, (hipStream_t)stream, "tsp_csr_row_indices");
@@ -1248,7 +1248,7 @@ extern "C" int tsp_csr_transpose(const void* values, int dtype, const int64_t* c
                                  int64_t m, int64_t n, int64_t nnz, int64_t* out_row_ptrs, int64_t* out_col,
                                  void* out_values, void* workspace, int64_t workspace_bytes, void* stream) {
   if (!dtype_ok(dtype)) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_transpose: dtype %d", dtype);
-  if (nnz < 0 || m < 0 || n < 0) return tsp::fail(TSP_EINVAL, "tsp_csr_transpose: bad size");
+  if (nnz < 0 || m < 0 || n < 0 || (m == 0 && nnz > 0)) return tsp::fail(TSP_EINVAL, "tsp_csr_transpose: bad size");
   if (m > UINT32_MAX || n > (int64_t)UINT32_MAX + 1)
     return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_transpose: dimensions past 2^32");
   if (!out_row_ptrs) return tsp::fail(TSP_EINVAL, "tsp_csr_transpose: null pointer");
@@ -1326,7 +1326,8 @@ extern "C" int tsp_csr_sum(const void* a_values, const int64_t* a_cols, const in
                            int dtype, int64_t m, int64_t n, int64_t* row_ptrs, int64_t* col_out, void* values_out,
                            void* workspace, int64_t workspace_bytes, void* stream) {
   if (!dtype_ok(dtype)) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_sum: dtype %d", dtype);
-  if (nnz_a < 0 || nnz_b < 0 || m < 0 || n < 0) return tsp::fail(TSP_EINVAL, "tsp_csr_sum: bad size");
+  if (nnz_a < 0 || nnz_b < 0 || m < 0 || n < 0 || (m == 0 && nnz_a + nnz_b > 0))
+    return tsp::fail(TSP_EINVAL, "tsp_csr_sum: bad size");
   if (m > UINT32_MAX || n > (int64_t)UINT32_MAX + 1 || nnz_a + nnz_b > UINT32_MAX)
     return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_sum: sizes past 2^32");
   if (!row_ptrs) return tsp::fail(TSP_EINVAL, "tsp_csr_sum: null pointer");

@@ -98,11 +98,12 @@ def test_sparse_add_unsorted_rows_with_repeats(hip_backend):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 def test_sparse_add_long_rows(hip_backend, dtype):
-    """Rows whose union holds more than 2048 entries (the workgroup-per-row
-    path, columns streamed through LDS in tiles) next to short and empty
-    rows; many repeats per column."""
+    """Rows of every size class of the device coalesce: more than 4096
+    entries (a workgroup per row, streamed through LDS in tiles), 65-4096
+    (staged in LDS with their neighbours), at most 64 (a wavefront sort) and
+    empty; many repeats per column."""
     g = torch.Generator().manual_seed(11)
-    m, n = 4, 600
+    m, n = 6, 600
     def csr(counts):
         rows = torch.repeat_interleave(torch.arange(m), torch.tensor(counts))
         cols = torch.randint(0, n, (int(sum(counts)),), generator=g)
@@ -110,7 +111,7 @@ def test_sparse_add_long_rows(hip_backend, dtype):
         rp = torch.zeros(m + 1, dtype=torch.int64)
         rp[1:] = torch.tensor(counts).cumsum(0)
         return ts.CSRMatrix(vals, cols, rp, (m, n))
-    A, B = csr([3000, 10, 0, 5000]), csr([2500, 0, 0, 4100])
+    A, B = csr([3000, 10, 0, 5000, 80, 1500]), csr([2500, 0, 0, 4100, 30, 900])
     got = ts.sparse_add(_cuda(A), _cuda(B), alpha=1.0, beta=-2.0)
     ts.set_backend("pytorch")
     try:

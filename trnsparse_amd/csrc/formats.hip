@@ -518,11 +518,11 @@ __global__ __launch_bounds__(256) void run_row_ptrs_kernel(const uint64_t* __res
 // column; the heads are the output entries, ranked by column, each holding
 // the sum of its column's entries in input order — what a stable sort of the
 // concatenated COO by (row, col) followed by a run sum gives. Two passes
-// (count heads per row; after a scan, write them). Rows of up to SUM_CAP
-// entries are handled in batches of consecutive rows staged in LDS at once
-// (column with the head flag in bit 31); longer rows take a 256-thread
-// workgroup each that streams the row through LDS in tiles and keeps the
-// head flags in workspace.
+// (count heads per row; after a scan, write them). Rows of at most 64
+// entries take a wavefront each and sort their entries across its lanes;
+// rows of up to SUM_CAP entries are staged in LDS with their neighbours in
+// 64-row chunks; longer rows take a 256-thread workgroup each that streams
+// the row through LDS in tiles and keeps the head flags in workspace.
 constexpr int SUM_CAP = 4096;
 constexpr int SUM_RPW = 64;
 constexpr int LONG_TILE = 4096;
@@ -545,6 +545,110 @@ __device__ inline SumRow<T> sum_row(const T* av, const int64_t* ac, const int64_
                                     const int64_t* br, int64_t r) {
   const int64_t a0 = ar[r], na = ar[r + 1] - a0, b0 = br[r];
   return SumRow<T>{av, ac, bv, bc, a0, na, b0, na + (br[r + 1] - b0)};
+}
+
+// rows with n <= 64: a wavefront takes two rows at a time. Each row's
+// (column, position) keys are sorted across lanes by a bitonic network —
+// both rows side by side in the two 32-lane halves when both hold at most
+// 32 entries, else one row at a time over all 64 lanes — so heads, their
+// ranks (a ballot prefix count) and each run (the lanes that follow with
+// the same column, in input order) come from lane shuffles. Keys are 32-bit
+// (column << 6 | position) when the columns fit 26 bits, else 64-bit.
+constexpr int WAVE_ROW = 64;
+
+template <typename K>
+__device__ inline K sum_key(uint32_t c, int pos) {
+  return sizeof(K) == 4 ? (K)((c << 6) | (uint32_t)pos) : (K)(((uint64_t)c << 32) | (uint64_t)pos);
+}
+template <typename K>
+__device__ inline uint32_t key_col_of(K k) {
+  return sizeof(K) == 4 ? (uint32_t)(k >> 6) : (uint32_t)((uint64_t)k >> 32);
+}
+
+// sort keys across groups of G lanes (G = 32: each half on its own)
+template <typename K, int G>
+__device__ inline K lane_sort(K key, int lane) {
+  const int l = lane & (G - 1);  // position within the group: every group sorts ascending
+#pragma unroll
+  for (int k = 2; k <= G; k <<= 1)
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const K other = __shfl_xor(key, j, 64);
+      const bool keep_min = ((l & j) == 0) == ((l & k) == 0);
+      key = keep_min ? (other < key ? other : key) : (other > key ? other : key);
+    }
+  return key;
+}
+
+template <typename T, bool WRITE, typename K>
+__global__ __launch_bounds__(256) void csr_sum_wave_kernel(const T* __restrict__ av, const int64_t* __restrict__ ac,
+                                                           const int64_t* __restrict__ ar, const T* __restrict__ bv,
+                                                           const int64_t* __restrict__ bc,
+                                                           const int64_t* __restrict__ br, int64_t m,
+                                                           int64_t* __restrict__ ucount,
+                                                           const int64_t* __restrict__ out_rp,
+                                                           int64_t* __restrict__ out_col, T* __restrict__ out_val) {
+  typedef typename tsp::Acc<T>::type AccT;
+  const int lane = threadIdx.x & 63;
+  const int64_t nw = (int64_t)gridDim.x * 4;
+  for (int64_t rb = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 2; rb < m; rb += nw * 2) {
+    int64_t a0[2], na[2], b0[2];
+    int n[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      n[i] = -1;  // not this kernel's row
+      if (rb + i < m) {
+        a0[i] = ar[rb + i];
+        na[i] = ar[rb + i + 1] - a0[i];
+        b0[i] = br[rb + i];
+        const int64_t nn = na[i] + (br[rb + i + 1] - b0[i]);
+        if (nn <= WAVE_ROW) n[i] = (int)nn;
+      }
+    }
+    const bool halves = n[0] <= 32 && n[1] <= 32;
+    // process the rows: both at once in the halves, or one after the other
+    for (int pass = 0; pass < (halves ? 1 : 2); ++pass) {
+      const int i = halves ? (lane >> 5) : pass;  // this lane's row
+      const int pos = halves ? (lane & 31) : lane;
+      const int nr = n[i];
+      if (!halves && nr < 0) continue;  // uniform: the whole wave serves row `pass`
+      const int64_t r = rb + i;
+      K key = (K)~(K)0;  // padding sorts after every entry
+      AccT v = 0;
+      if (pos < nr) {
+        const bool in_a = pos < na[i];
+        const uint32_t c = (uint32_t)(in_a ? ac[a0[i] + pos] : bc[b0[i] + pos - na[i]]);
+        v = tsp::to_acc(in_a ? av[a0[i] + pos] : bv[b0[i] + pos - na[i]]);
+        key = sum_key<K>(c, pos);  // equal columns keep input order
+      }
+      key = halves ? lane_sort<K, 32>(key, lane) : lane_sort<K, 64>(key, lane);
+      const int base = halves ? (lane & 32) : 0;  // first lane of this row's group
+      const uint32_t col = key_col_of(key);
+      const AccT sv = __shfl(v, base + (int)(key & 63), 64);
+      const uint32_t prev = __shfl_up(col, 1, 64);
+      const bool head = pos < nr && (pos == 0 || prev != col);
+      const uint64_t hb_all = __builtin_amdgcn_ballot_w64(head);
+      const uint64_t hb = halves ? (hb_all >> base) & 0xffffffffull : hb_all;
+      if (!WRITE) {
+        if (pos == 0 && nr >= 0) ucount[r] = __popcll(hb);
+        continue;
+      }
+      AccT sum = sv;
+      bool open = head;
+      for (int k = 1; k < WAVE_ROW; ++k) {
+        if (__builtin_amdgcn_ballot_w64(open) == 0) break;
+        const uint32_t c2 = __shfl_down(col, k, 64);
+        const AccT v2 = __shfl_down(sv, k, 64);
+        open = open && pos + k < nr && c2 == col;
+        if (open) sum += v2;
+      }
+      if (head) {
+        const int64_t o = out_rp[r] + __popcll(hb & ((1ull << pos) - 1));
+        out_col[o] = (int64_t)col;
+        out_val[o] = tsp::from_acc<T>(sum);
+      }
+    }
+  }
 }
 
 // rows with n <= SUM_CAP: a 256-thread workgroup per chunk of SUM_RPW
@@ -583,7 +687,7 @@ __global__ __launch_bounds__(256) void csr_sum_rows_kernel(const T* __restrict__
       int32_t x = 0;
       if (tid < nr) {
         const int64_t l = (ua[tid + 1] - ua[tid]) + (ub[tid + 1] - ub[tid]);
-        x = l > SUM_CAP ? 0 : (int32_t)l;
+        x = (l > SUM_CAP || l <= WAVE_ROW) ? 0 : (int32_t)l;  // the other kernels' rows
         cnt[tid] = 0;
       }
 #pragma unroll
@@ -653,7 +757,10 @@ __global__ __launch_bounds__(256) void csr_sum_rows_kernel(const T* __restrict__
     if (!WRITE) {
       __syncthreads();
       // long rows keep the count the long-row kernel writes
-      if (tid < nr && (ua[tid + 1] - ua[tid]) + (ub[tid + 1] - ub[tid]) <= SUM_CAP) ucount[r0 + tid] = cnt[tid];
+      if (tid < nr) {
+        const int64_t l = (ua[tid + 1] - ua[tid]) + (ub[tid + 1] - ub[tid]);
+        if (l > WAVE_ROW && l <= SUM_CAP) ucount[r0 + tid] = cnt[tid];
+      }
     }
   }
 }
@@ -1283,7 +1390,7 @@ int64_t sum_scan_tmp(int64_t m) {
 
 template <typename T>
 int csr_sum_t(const T* av, const int64_t* ac, const int64_t* ar, const T* bv, const int64_t* bc, const int64_t* br,
-              int64_t N, int64_t m, int64_t* row_ptrs, int64_t* col_out, T* values_out, char* w,
+              int64_t N, int64_t m, int64_t n, int64_t* row_ptrs, int64_t* col_out, T* values_out, char* w,
               int64_t workspace_bytes, hipStream_t st) {
   int64_t* ucount = (int64_t*)w;
   uint8_t* hflag = (uint8_t*)(w + align256(8 * (m + 1)));
@@ -1292,6 +1399,16 @@ int csr_sum_t(const T* av, const int64_t* ac, const int64_t* ar, const T* bv, co
   const int64_t chunks = tsp::ceil_div(m, SUM_RPW);
   const unsigned g = (unsigned)(chunks < 65536 ? chunks : 65536);
   const unsigned gl = (unsigned)(m < 1024 ? m : 1024);
+  const unsigned gw = (unsigned)(tsp::ceil_div(m, 8) < 65536 ? tsp::ceil_div(m, 8) : 65536);
+  const bool key32 = col_bits(n) <= 26;
+  if (key32)
+    hipLaunchKernelGGL((csr_sum_wave_kernel<T, false, uint32_t>), dim3(gw), dim3(256), 0, st, av, ac, ar, bv, bc, br,
+                       m, ucount, (const int64_t*)nullptr, (int64_t*)nullptr, (T*)nullptr);
+  else
+    hipLaunchKernelGGL((csr_sum_wave_kernel<T, false, uint64_t>), dim3(gw), dim3(256), 0, st, av, ac, ar, bv, bc, br,
+                       m, ucount, (const int64_t*)nullptr, (int64_t*)nullptr, (T*)nullptr);
+  int rc0 = tsp::check_launch("csr_sum_wave (count) launch");
+  if (rc0) return rc0;
   hipLaunchKernelGGL((csr_sum_rows_kernel<T, false>), dim3(g), dim3(256), 0, st, av, ac, ar, bv, bc, br, m, ucount,
                      (const int64_t*)nullptr, (int64_t*)nullptr, (T*)nullptr);
   int rc = tsp::check_launch("csr_sum_rows (count) launch");
@@ -1303,6 +1420,14 @@ int csr_sum_t(const T* av, const int64_t* ac, const int64_t* ar, const T* bv, co
   if (rocprim::exclusive_scan(tmp, tb, ucount, row_ptrs, (int64_t)0, (size_t)(m + 1), rocprim::plus<int64_t>(), st) !=
       hipSuccess)
     return tsp::check_hip(hipGetLastError(), "exclusive_scan");
+  if (key32)
+    hipLaunchKernelGGL((csr_sum_wave_kernel<T, true, uint32_t>), dim3(gw), dim3(256), 0, st, av, ac, ar, bv, bc, br, m,
+                       (int64_t*)nullptr, (const int64_t*)row_ptrs, col_out, values_out);
+  else
+    hipLaunchKernelGGL((csr_sum_wave_kernel<T, true, uint64_t>), dim3(gw), dim3(256), 0, st, av, ac, ar, bv, bc, br, m,
+                       (int64_t*)nullptr, (const int64_t*)row_ptrs, col_out, values_out);
+  rc = tsp::check_launch("csr_sum_wave (write) launch");
+  if (rc) return rc;
   hipLaunchKernelGGL((csr_sum_rows_kernel<T, true>), dim3(g), dim3(256), 0, st, av, ac, ar, bv, bc, br, m,
                      (int64_t*)nullptr, (const int64_t*)row_ptrs, col_out, values_out);
   rc = tsp::check_launch("csr_sum_rows (write) launch");
@@ -1340,11 +1465,11 @@ extern "C" int tsp_csr_sum(const void* a_values, const int64_t* a_cols, const in
     return tsp::fail(TSP_EINVAL, "tsp_csr_sum: workspace too small");
   char* w = (char*)workspace;
   if (dtype == TSP_F32)
-    return csr_sum_t((const float*)a_values, a_cols, a_row_ptrs, (const float*)b_values, b_cols, b_row_ptrs, nnz_a + nnz_b, m,
+    return csr_sum_t((const float*)a_values, a_cols, a_row_ptrs, (const float*)b_values, b_cols, b_row_ptrs, nnz_a + nnz_b, m, n,
                      row_ptrs, col_out, (float*)values_out, w, workspace_bytes, st);
   if (dtype == TSP_F64)
-    return csr_sum_t((const double*)a_values, a_cols, a_row_ptrs, (const double*)b_values, b_cols, b_row_ptrs, nnz_a + nnz_b, m,
+    return csr_sum_t((const double*)a_values, a_cols, a_row_ptrs, (const double*)b_values, b_cols, b_row_ptrs, nnz_a + nnz_b, m, n,
                      row_ptrs, col_out, (double*)values_out, w, workspace_bytes, st);
-  return csr_sum_t((const uint16_t*)a_values, a_cols, a_row_ptrs, (const uint16_t*)b_values, b_cols, b_row_ptrs, nnz_a + nnz_b, m,
+  return csr_sum_t((const uint16_t*)a_values, a_cols, a_row_ptrs, (const uint16_t*)b_values, b_cols, b_row_ptrs, nnz_a + nnz_b, m, n,
                    row_ptrs, col_out, (uint16_t*)values_out, w, workspace_bytes, st);
 }

@@ -152,7 +152,7 @@ def coo_sum_to_csr(values: torch.Tensor, row_indices: torch.Tensor, col_indices:
         _lib.call("tsp_coo_sum_to_csr", v.data_ptr(), _lib.dtype_code(v.dtype), ri.data_ptr(), ci.data_ptr(), nnz, m,
                   n, rp.data_ptr(), col.data_ptr(), val.data_ptr(), ws.data_ptr(), wsb, _stream(dev))
         u = int(rp[-1].item())
-    return val[:u].clone(), col[:u].clone(), rp
+    return val[:u], col[:u], rp
 
 
 def csr_transpose(values: torch.Tensor, col_indices: torch.Tensor, row_ptrs: torch.Tensor, shape):
@@ -203,5 +203,6 @@ def csr_sum(a_values: torch.Tensor, a_cols: torch.Tensor, a_row_ptrs: torch.Tens
                   br.data_ptr(), nb, code, m, n, rp.data_ptr(), col.data_ptr(), val.data_ptr(), ws.data_ptr(), wsb,
                   _stream(dev))
         u = int(rp[-1].item())
-    return val[:u].clone(), col[:u].clone(), rp
+    # leading views of the outputs (sized for the union without repeats)
+    return val[:u], col[:u], rp
 

@@ -135,8 +135,10 @@ def sparse_add(A: CSRMatrix, B: CSRMatrix, alpha: float = 1.0, beta: float = 1.0
         from .hip import formats as hf
 
         if A.values.dtype in hf.DEVICE_DTYPES:
-            vals, cols, rp = hf.csr_sum(alpha * A.values, A.col_indices, A.row_ptrs, beta * B.values,
-                                        B.col_indices, B.row_ptrs, A.shape)
+            # (x * 1.0 is x bit for bit, so a unit factor is not applied)
+            av = A.values if alpha == 1.0 else alpha * A.values
+            bv = B.values if beta == 1.0 else beta * B.values
+            vals, cols, rp = hf.csr_sum(av, A.col_indices, A.row_ptrs, bv, B.col_indices, B.row_ptrs, A.shape)
             return CSRMatrix(values=vals, col_indices=cols, row_ptrs=rp, shape=A.shape)
     ca, cb = A.to_coo(), B.to_coo()
     idx = torch.stack(

@@ -116,6 +116,45 @@ def test_f64_generic(hip_backend):
     torch.testing.assert_close(got, A @ B, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize(
+    "shape,N,density",
+    [((512, 384), 256, 0.5),     # fp64 MFMA kernel, aligned
+     ((300, 260), 130, 0.6),     # ragged m, n, N (B rows past n read as zero, N padded to even)
+     ((384, 512), 7, 1.0),       # narrow N
+     ((256, 256), 128, 0.0)],    # empty pattern
+)
+def test_f64_mfma(hip_backend, shape, N, density):
+    """fp64 with block size 128 runs v_mfma_f64_16x16x4_f64; against the
+    float64 oracle within 1e-12 of the dot-product scale."""
+    g = torch.Generator().manual_seed(shape[0] + N)
+    A = torch.randn(*shape, generator=g, dtype=torch.float64) * (torch.rand(*shape, generator=g) < density)
+    bsr = ts.BSRMatrix.from_dense(A, block_size=128)
+    B = torch.randn(shape[1], N, generator=g, dtype=torch.float64)
+    got = ts.bsr_spmm(bsr, B.cuda()).cpu()
+    assert got.dtype == torch.float64 and got.shape == (shape[0], N)
+    if bsr.n_blocks == 0:
+        assert torch.count_nonzero(got).item() == 0
+        return
+    exact, scale = _oracle(bsr, B)
+    assert ref.scaled_error(got.numpy(), exact[: shape[0]], scale[: shape[0]]) <= 1e-12
+
+
+def test_f64_mfma_empty_rows_and_cfg3_rows(hip_backend):
+    """cfg3's pattern in fp64 (32 block rows): every row against the oracle;
+    block rows without blocks give exact zeros."""
+    A, B = W.cfg3_bsr(nb=32, ncols=256, dtype=torch.float64)
+    got = ts.bsr_spmm(A, B.cuda()).cpu()
+    exact, scale = _oracle(A, B)
+    assert ref.scaled_error(got.numpy(), exact, scale) <= 1e-12
+    mask = torch.tensor([[True, False, True], [False, False, False], [False, True, False]])
+    E = W.bsr_from_block_mask(mask, 128, blocks=torch.randn(3, 128, 128, dtype=torch.float64))
+    Bz = torch.randn(384, 64, dtype=torch.float64)
+    out = ts.bsr_spmm(E, Bz.cuda()).cpu()
+    assert torch.count_nonzero(out[128:256]).item() == 0
+    ex, sc = _oracle(E, Bz)
+    assert ref.scaled_error(out.numpy(), ex, sc) <= 1e-12
+
+
 def test_dtype_mismatch_raises(hip_backend):
     bsr = ts.BSRMatrix.from_dense(torch.randn(128, 128), block_size=128)
     with pytest.raises(RuntimeError):

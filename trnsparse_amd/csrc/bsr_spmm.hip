@@ -22,6 +22,8 @@
 //                      (v_mfma_f32_32x32x16_bf16, 64x32 wave tiles,
 //                      direct-to-LDS 4-deep ring, B operand through LDS
 //                      transpose reads).
+//   bsr_spmm_f64_dma   b == 128, fp64 (v_mfma_f64_16x16x4_f64, the streamed
+//                      structure of bsr_spmm_f32_dma).
 //   bsr_spmm_generic   any block size / dtype (f32, f64, bf16): one thread per
 //                      output element, a plain dot product over stored blocks.
 //
@@ -275,6 +277,177 @@ __global__ __launch_bounds__(256) void bsr_spmm_f32_dma(
 #ifndef F32_DMA_KC
 #define F32_DMA_KC 64
 #endif
+
+// ------------------------------------------------------- fp64 MFMA, streamed
+//
+// bsr_spmm_f64_dma: b == 128, fp64. The tile, scheduling and slab ring of
+// bsr_spmm_f32_dma with v_mfma_f64_16x16x4_f64 (64 cycles per MFMA, the
+// same cadence per slab as the fp32 kernel's 32x32x2):
+//   * 4 waves, each a 64x64 sub-tile as 4x4 independent 16x16 accumulators;
+//   * 32-wide k-slabs: A [128][32] (256-byte rows) and B [32][128] (1 KiB
+//     rows) through a 2-stage direct-to-LDS ring (128 KiB), B through a
+//     buffer resource so rows past n read as zero;
+//   * k permuted within a slab: the MFMA's k slot g (lanes 16g..16g+15)
+//     takes k = 8g + s at k-step s, so a lane's A values for two k-steps
+//     are one 16-byte read;
+//   * swizzles: A chunk ^ (row % 16) (16 rows of one read cover all banks),
+//     B chunk ^ 8*((k / 8) % 2) (the four k slots' rows, 8 apart, in
+//     different bank halves).
+namespace f64k {
+constexpr int KC = 32;
+constexpr int A_ROWB = KC * 8;        // 256
+constexpr int B_ROWB = 128 * 8;       // 1024
+constexpr int A_BYTES = 128 * A_ROWB;  // 32 KiB
+constexpr int B_BYTES = KC * B_ROWB;   // 32 KiB
+constexpr int STAGE = A_BYTES + B_BYTES;
+constexpr int NST = 2;
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
+}  // namespace f64k
+
+__global__ __launch_bounds__(256) void bsr_spmm_f64_dma(
+    const double* __restrict__ blocks, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci,
+    int64_t mb, int nt, int64_t m, int64_t n, const double* __restrict__ B, int64_t ldb, int64_t ncols,
+    double* __restrict__ C, int64_t ldc, const int32_t* __restrict__ order) {
+  using f64k::A_ROWB;
+  using f64k::B_ROWB;
+  using f64k::A_BYTES;
+  using f64k::NST;
+  using f64k::STAGE;
+  using f64k::f64x2;
+  using f64k::f64x4;
+  constexpr int FKC = f64k::KC;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
+  int64_t row;
+  int ntile;
+  if (!T32::tile_item(blockIdx.x, mb, nt, order, row, ntile)) return;
+  const int64_t n0 = (int64_t)ntile * 128;
+  const int64_t start = rp[row];
+  const int nblk = (int)(rp[row + 1] - start);
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w & 1, wn = w >> 1, g = lane >> 4, l16 = lane & 15;
+
+  f64x4 acc[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[t][u] = f64x4{};
+
+  if (nblk > 0) {
+    const tsp::dma::i32x4 brsrc = tsp::dma::make_rsrc(B, (uint32_t)(n * ldb * 8));
+    const uint32_t lds0 = tsp::dma::lds_addr(lds);
+    int cbase = 0;
+    auto load_cols = [&](int base) {
+      const int i = base + lane < nblk ? base + lane : nblk - 1;
+      return tsp::dma::load_lo32_sync(ci + start + i);
+    };
+    int cv = load_cols(0);
+    auto colblk = [&](int blk) {
+      if (blk - cbase >= 64) {
+        cbase = blk & ~63;
+        cv = load_cols(cbase);
+      }
+      return __builtin_amdgcn_readlane(cv, blk - cbase);
+    };
+
+    // ---- loads of slab s into stage s % NST: 8 A + 8 B wave instructions
+    constexpr int SPB = BS / FKC;  // slabs per block
+    auto issue = [&](int s) {
+      const int blk = s / SPB;
+      const int kk = (s % SPB) * FKC;
+      const uint32_t st = lds0 + (s % NST) * STAGE;
+      const double* ablk = blocks + (start + blk) * (BS * BS) + kk;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int i = 8 * w + q;                   // A rows [4i, 4i+4)
+        const int r = 4 * i + (lane >> 4);
+        const int c = (lane & 15) ^ (r & 15);      // logical chunk held at this lane's slot
+        tsp::dma::global16(ablk + r * BS + c * 2, st + i * 1024);
+      }
+      const int64_t brow0 = (int64_t)colblk(blk) * BS + kk;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int j = 8 * w + q;                   // B slab row j, 64 chunks of 16 bytes
+        const int c = lane ^ (8 * ((j >> 3) & 1));
+        const int64_t off = ((brow0 + j) * ldb + n0 + c * 2) * 8;
+        tsp::dma::buffer16(brsrc, (uint32_t)off, st + A_BYTES + j * 1024);
+      }
+    };
+
+    // per-lane LDS byte offsets. A: rows wm*64 + 16t + l16 (row % 16 == l16);
+    // a pair p of k-steps (k = 8g + 2p, 8g + 2p + 1) is logical chunk 4g + p
+    const int abase = (wm * 64 + l16) * A_ROWB;
+    // B: k rows 8g + s, columns wn*64 + 16u + l16 -> chunk (col / 2) ^ 8*(g % 2), half col % 2
+    int bcoff[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int col = wn * 64 + 16 * u + l16;
+      bcoff[u] = (((col >> 1) ^ (8 * (g & 1))) * 16) + (col & 1) * 8;
+    }
+    struct Ops {
+      f64x2 a[4];     // a[t] = k-steps 2p, 2p+1 of row tile t
+      double b[2][4]; // b[s][u]
+    };
+    auto fetch = [&](const uint8_t* st, int p, Ops& o) {
+      const uint8_t* As = st + abase + (((4 * g + p) ^ l16) * 16);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) o.a[t] = *(const f64x2*)(As + 16 * t * A_ROWB);
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const uint8_t* Bs = st + A_BYTES + (8 * g + 2 * p + s2) * B_ROWB;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) o.b[s2][u] = *(const double*)(Bs + bcoff[u]);
+      }
+    };
+    auto mma = [&](const Ops& o) {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            acc[t][u] = __builtin_amdgcn_mfma_f64_16x16x4f64(o.a[t][s2], o.b[s2][u], acc[t][u], 0, 0, 0);
+    };
+    auto compute = [&](const uint8_t* st) {
+      Ops o[2];
+      fetch(st, 0, o[0]);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        if (p + 1 < 4) fetch(st, p + 1, o[(p + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(o[p & 1]);
+      }
+    };
+
+    const int nsteps = nblk * SPB;
+    issue(0);
+    for (int s = 0; s < nsteps; ++s) {
+      tsp::dma::wait_vm<0>();  // this wave's loads of slab s are done
+      tsp::dma::barrier();     // every wave's part is in LDS; stage (s+1) % NST is free
+      if (s + 1 < nsteps) issue(s + 1);
+      compute(lds + (s % NST) * STAGE);
+    }
+  }
+  // accumulator layout of v_mfma_f64_16x16x4_f64 (checked on the device):
+  // lane holds column l16 and rows g + 4*v (unlike the fp32 16x16 forms,
+  // whose lane group g owns the 4 consecutive rows 4*g .. 4*g + 3)
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int64_t r0 = row * BS + wm * 64 + 16 * t + g;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t c = n0 + wn * 64 + 16 * u + l16;
+      if (c < ncols) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int64_t r = r0 + 4 * v;
+          if (r < m) C[r * ldc + c] = acc[t][u][v];
+        }
+      }
+    }
+  }
+}
 
 // ---------------------------------------------------------------- bf16 MFMA
 //
@@ -579,6 +752,16 @@ extern "C" int tsp_bsr_spmm(const void* blocks, int dtype, const int64_t* block_
                          (const uint16_t*)blocks, block_row_ptrs, block_col_indices, mb, (int)nt, m, n,
                          (const uint16_t*)B, ldb, ncols, (uint16_t*)C, ldc, row_order);
     return tsp::check_launch("bsr_spmm_bf16_mfma launch");
+  }
+  if (dtype == TSP_F64 && block_size == BS && (ldb % 2) == 0 && ((uintptr_t)B % 16) == 0 &&
+      ((uintptr_t)blocks % 16) == 0 && (n + BS) * ldb * 8 + 8 * BS <= (int64_t)UINT32_MAX) {
+    // (the kernel's B offsets, rows < n + 128 and columns < ldb + 128, fit 32 bits)
+    const int64_t nt = tsp::ceil_div(ncols, 128);
+    const int64_t grid = tsp::ceil_div(mb, 8) * 8 * nt;
+    if (grid > INT32_MAX || nt > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm: problem too large");
+    hipLaunchKernelGGL(bsr_spmm_f64_dma, dim3((unsigned)grid), dim3(256), 0, st, (const double*)blocks, block_row_ptrs,
+                       block_col_indices, mb, (int)nt, m, n, (const double*)B, ldb, ncols, (double*)C, ldc, row_order);
+    return tsp::check_launch("bsr_spmm_f64_dma launch");
   }
   if (dtype == TSP_F32) return launch_generic<float, float>(blocks, block_row_ptrs, block_col_indices, block_size, m, n, B, ldb, ncols, C, ldc, st);
   if (dtype == TSP_F64) return launch_generic<double, double>(blocks, block_row_ptrs, block_col_indices, block_size, m, n, B, ldb, ncols, C, ldc, st);

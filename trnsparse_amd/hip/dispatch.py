@@ -86,7 +86,7 @@ def _bsr_spmm_launch(blocks, rp, ci, order, shape, b, B, out_dtype, dev) -> torc
                   order.data_ptr() if order is not None else None, _lib.stream_handle(dev))
         return C
     ldb = ncols
-    vec = {torch.float32: 4, torch.bfloat16: 8}.get(B_d.dtype)
+    vec = {torch.float32: 4, torch.bfloat16: 8, torch.float64: 2}.get(B_d.dtype)
     if vec and b == 128 and ncols % vec:
         # Row stride a multiple of 16 bytes for the vectorised B panel loads.
         B_d = F.pad(B_d, (0, vec - ncols % vec))

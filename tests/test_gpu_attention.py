@@ -3,8 +3,9 @@
 Masks follow the reference's builders (local window, dilated, global tokens;
 examples/block_sparse_attention.py:49-109) and the BASELINE config-5 mask.
 Error measure: |O - O_exact| / (P |V|)_ij with the float64 oracle's softmax
-weights P — fp32 inputs <= 1e-4 (generic kernel), bf16 inputs <= 2e-2 (MFMA
-kernel, oracle run on the exact bf16 values). The reference's hardware test
+weights P — fp32 inputs <= 1e-4 (fp32 MFMA kernel for b = 128 and D in
+{64, 128}, generic kernel otherwise), bf16 inputs <= 2e-2 (MFMA kernel,
+oracle run on the exact bf16 values). The reference's hardware test
 tolerance (tests/test_nki_attn.py:63-67, atol 1e-3 / rtol 1e-4 against the
 torch path) is checked for fp32 as well.
 """
@@ -89,6 +90,46 @@ def test_bf16_mfma(hip_backend, S, D, mask):
     assert _err(got.float().cpu().numpy(), out, sc) <= TOL_BF16
     np.testing.assert_allclose(rmax.cpu().numpy(), em, rtol=1e-3, atol=1e-3)
     np.testing.assert_allclose(rden.cpu().numpy(), ed, rtol=2e-2)
+
+
+@pytest.mark.parametrize("S,D,mask,H", [
+    (512, 128, local_mask(4, 2), 1), (1024, 128, global_mask(8, 1, 2), 9),
+    (700, 128, torch.ones(6, 6, dtype=torch.bool), 2), (640, 64, W.cfg5_block_mask(5), 3),
+    (300, 64, local_mask(3, 1), 1), (512, 64, torch.ones(4, 4, dtype=torch.bool), 8),
+])
+def test_fp32_mfma(hip_backend, S, D, mask, H):
+    """fp32, b = 128, D in {64, 128} runs bsa_fwd_f32_mfma: ragged S (keys
+    past S inside a stored block), more heads than a multiple of 8, and
+    queries with wide score ranges (the running max moves by more than the
+    lazy-rescale threshold)."""
+    g = torch.Generator().manual_seed(15)
+    Q, K, V = (torch.randn(H, S, D, generator=g) for _ in range(3))
+    Q[:, ::7] *= 8
+    mask_bsr = W.bsr_from_block_mask(mask, 128)
+    got, rmax, rden = hip_block_sparse_attention(Q.cuda(), K.cuda(), V.cuda(), mask_bsr, D**-0.5, return_stats=True)
+    assert got.dtype == torch.float32
+    for hh in range(H):
+        out, em, ed, sc = _oracle(Q[hh], K[hh], V[hh], mask_bsr, D**-0.5)
+        assert _err(got[hh].cpu().numpy(), out, sc) <= TOL_F32
+        np.testing.assert_allclose(rmax[hh].cpu().numpy(), em, rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(rden[hh].cpu().numpy(), ed, rtol=1e-4)
+
+
+def test_fp32_mfma_long_row(hip_backend):
+    """A block row with more than 64 stored blocks (the kernel reads the
+    row's block columns 64 at a time)."""
+    nb, D = 67, 64
+    S = nb * 128
+    mask = local_mask(nb, 0)
+    mask[1, :] = True
+    mask_bsr = W.bsr_from_block_mask(mask, 128)
+    g = torch.Generator().manual_seed(16)
+    Q, K, V = (torch.randn(S, D, generator=g) for _ in range(3))
+    got = ts.block_sparse_attention_tiled(Q.cuda(), K.cuda(), V.cuda(), mask_bsr).cpu()
+    rows = [0, 1, 2, 66]
+    out, _, _, sc = _oracle(Q, K, V, mask_bsr, D**-0.5, rows=rows)
+    sel = np.concatenate([np.arange(r * 128, (r + 1) * 128) for r in rows])
+    assert _err(got.numpy()[sel], out[sel], sc[sel]) <= TOL_F32
 
 
 def test_empty_rows_ragged_seq_and_scale(hip_backend):

@@ -22,6 +22,8 @@
 //       softmax needs one cross-lane shuffle. O^T = V^T P^T consumes P from
 //       registers (bf16) with V staged transposed in LDS. fp32 softmax with
 //       exp2, fp32 accumulation, bf16 output.
+//   bsa_fwd_f32_mfma<D>   fp32, 128-blocks, D in {64, 128}: the same work
+//       split on v_mfma_f32_32x32x2_f32 with K/V streamed through an LDS ring.
 //   bsa_fwd_generic<T>    fp32/fp64/bf16, any block size and head_dim: one
 //       thread per (query, 32-wide slice of head_dim), online softmax in
 //       the accumulation type (double for fp64).
@@ -536,6 +538,245 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_bf16_d128(
   }
 }
 
+// ---------------------------------------------------------------- fp32 MFMA
+//
+// bsa_fwd_f32_mfma<D>: fp32, 128-blocks, D in {64, 128}. The work split and
+// math of the bf16 kernels (one 256-thread workgroup per (head, 128-query
+// block row), a wavefront per 32 queries, S^T = K Q^T with the wave's Q rows
+// in registers, online softmax in the exp2 domain with lazy rescaling,
+// O^T += V^T P^T with P from registers) on v_mfma_f32_32x32x2_f32:
+//   * keys stream through a 2-stage LDS ring of HK = 4096 / D keys per stage
+//     (K rows then V rows, 32 KiB per stage, 64 KiB per workgroup, two
+//     workgroups per CU), filled by direct global->LDS buffer loads issued
+//     one stage ahead; rows at or past seq_len read as zero;
+//   * S^T: the MFMA k index is the head dimension; at step 4t + c lane half h
+//     supplies d = 8t + 4h + c, so one b128 LDS read of a K row feeds four
+//     MFMAs and Q[q][8t + 4h .. +3] is the matching register fragment. K
+//     rows are stored 16-byte chunk ^ (key % 16) (conflict-free reads of one
+//     chunk from 32 rows);
+//   * O^T: row r of d subtile u is d = NU*r + u, so a lane's A operands for
+//     all NU subtiles are one contiguous read V[key][NU*l32 .. +NU) and its
+//     outputs cover 4*NU consecutive d; the k index is the key: at step s
+//     lane half h supplies key 8*(s/4) + 4h + s%4 of the 32-key tile, which
+//     is its own S^T element s, so P is consumed where it was computed.
+namespace attf {
+template <int D>
+struct Cfg {
+  static constexpr int HK = 4096 / D;       // keys per ring stage
+  static constexpr int ROWB = D * 4;        // bytes per K/V row
+  static constexpr int HBYTES = HK * ROWB;  // 16 KiB of K (or V) per stage
+  static constexpr int STAGE = 2 * HBYTES;
+  static constexpr int NST = 2;
+  static constexpr int NT = HK / 32;        // 32-key S^T tiles per stage
+  static constexpr int NU = D / 32;         // d subtiles of O^T
+  static constexpr int KT = D / 8;          // b128 K reads per S^T tile
+  static constexpr int SPB = AB / HK;       // stages per key block
+};
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+template <int NU> struct VRow;
+template <> struct VRow<4> { typedef f32x4 type; };
+template <> struct VRow<2> { typedef f32x2 type; };
+}  // namespace attf
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void bsa_fwd_f32_mfma(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V, int64_t S,
+    int64_t head_stride, int64_t H, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci, int64_t Mt,
+    float scale_log2, float* __restrict__ O, float* __restrict__ rmax, float* __restrict__ rden) {
+  typedef attf::Cfg<D> C;
+  constexpr int HK = C::HK, ROWB = C::ROWB, HBYTES = C::HBYTES, STAGE = C::STAGE, NST = C::NST;
+  constexpr int NT = C::NT, NU = C::NU, KT = C::KT, SPB = C::SPB;
+  typedef typename attf::VRow<NU>::type vrow_t;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
+
+  // XCD-aware order: XCD x walks heads x, x+8, ...; the block rows of one
+  // head run side by side and share that head's K/V in the XCD's L2.
+  const int64_t g = blockIdx.x;
+  const int64_t xcd = g & 7, slot = g >> 3;
+  const int64_t head = xcd + 8 * (slot / Mt);
+  const int64_t m = slot % Mt;
+  if (head >= H) return;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  const float* Qh = Q + head * head_stride;
+  const float* Kh = K + head * head_stride;
+  const float* Vh = V + head * head_stride;
+  const int64_t q = m * AB + w * 32 + l32;  // this lane's query (always < S: m < Mt)
+
+  // B operand of S^T: Q[q][8t + 4h + c] at step 4t + c
+  f32x4 qf[KT];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) qf[t] = *(const f32x4*)(Qh + q * D + 8 * t + 4 * h);
+
+  f32x16 o[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) o[u] = f32x16{};
+  // mtrue: running max of the scaled scores (log2 domain); mref: the
+  // reference P and the sums are taken against (lazy rescaling, below)
+  constexpr float RESCALE = 8.f;
+  float mtrue = -INFINITY, mref = -INFINITY, lrun = 0.f;
+
+  const int64_t start = rp[m];
+  const int nblk = (int)(rp[m + 1] - start);
+  const int nsteps = SPB * nblk;
+  const tsp::dma::i32x4 krs = tsp::dma::make_rsrc(Kh, (uint32_t)(S * D * 4));
+  const tsp::dma::i32x4 vrs = tsp::dma::make_rsrc(Vh, (uint32_t)(S * D * 4));
+  const uint32_t lds0 = tsp::dma::lds_addr(lds);
+
+  // key-block indices of the row, 64 at a time in one VGPR, read with readlane
+  int cbase = 0, cv = 0;
+  auto load_cols = [&](int base) {
+    const int i = base + lane < nblk ? base + lane : nblk - 1;
+    return tsp::dma::load_lo32_sync(ci + start + i);
+  };
+  if (nblk > 0) cv = load_cols(0);
+  auto colblk = [&](int blk) {
+    if (blk - cbase >= 64) {
+      cbase = blk & ~63;
+      cv = load_cols(cbase);
+    }
+    return __builtin_amdgcn_readlane(cv, blk - cbase);
+  };
+  auto first_key = [&](int s) { return (int64_t)colblk(s / SPB) * AB + HK * (s % SPB); };
+
+  // ---- loads of stage s: 16 K + 16 V instructions of 1 KiB, 4 + 4 per wave
+  auto issue = [&](int s) {
+    constexpr int LPR = D / 4, RPI = 64 / LPR;  // lanes per row, rows per instruction
+    const int64_t key0 = first_key(s);
+    const uint32_t st = lds0 + (s % NST) * STAGE;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const int j = 4 * w + qq;
+      const int rr = RPI * j + lane / LPR;  // row of the stage
+      const int p = lane % LPR;             // this lane's 16-byte slot in the row
+      const uint32_t rowoff = (uint32_t)((key0 + rr) * ROWB);
+      tsp::dma::buffer16(krs, rowoff + ((p ^ (rr & 15)) * 16), st + j * 1024);
+      tsp::dma::buffer16(vrs, rowoff + p * 16, st + HBYTES + j * 1024);
+    }
+  };
+
+  const int kx = l32 & 15;  // K swizzle term: row % 16 for rows 32tt + l32
+  auto compute = [&](const uint8_t* st, int64_t key0) {
+    const uint8_t* Ks = st + l32 * ROWB;
+    const uint8_t* Vs = st + HBYTES + 4 * h * ROWB + l32 * NU * 4;
+    auto kread = [&](int tt, int t) { return *(const f32x4*)(Ks + tt * 32 * ROWB + (((2 * t + h) ^ kx) * 16)); };
+    auto vread = [&](int i) {  // step i of the stage: tile i / 16, step s = i % 16
+      const int tt = i >> 4, s = i & 15;
+      return *(const vrow_t*)(Vs + (32 * tt + 8 * (s >> 2) + (s & 3)) * ROWB);
+    };
+    // ---- S^T tiles (keys 32tt + 8*(v/4) + 4h + v%4, query l32): NT
+    // independent chains, K operands read one t ahead
+    f32x16 sc[NT];
+    f32x4 ka[2][NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) ka[0][tt] = kread(tt, 0);
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      if (t + 1 < KT) {
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) ka[(t + 1) & 1][tt] = kread(tt, t + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt)
+          sc[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[t & 1][tt][c], qf[t][c],
+                                                        (t == 0 && c == 0) ? f32x16{} : sc[tt], 0, 0, 0);
+    }
+    // ---- online softmax in the log2 domain (scale_log2 > 0); keys at or
+    // past seq_len (only in a block that crosses it) are excluded
+    if (key0 + HK > S) {
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          if (key0 + 32 * tt + 8 * (v >> 2) + 4 * h + (v & 3) >= S) sc[tt][v] = -INFINITY;
+    }
+    float mraw = sc[0][0];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) mraw = fmaxf(mraw, sc[tt][v]);
+    mraw = fmaxf(mraw, __shfl_xor(mraw, 32, 64));
+    mtrue = fmaxf(mtrue, mraw * scale_log2);
+    // P is taken relative to a reference max mref that only moves when the
+    // true running max exceeds it by more than RESCALE (log2 units), so
+    // P <= 2^RESCALE and o, l rarely need the multiply; o / l is the same
+    // quantity for any reference.
+    if (__builtin_amdgcn_ballot_w64(mtrue > mref + RESCALE) != 0) {
+      const bool move = mtrue > mref + RESCALE;
+      const float alpha = move ? (mref == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mref - mtrue)) : 1.f;
+      mref = move ? mtrue : mref;
+      lrun *= alpha;
+#pragma unroll
+      for (int u = 0; u < NU; ++u) o[u] *= alpha;
+    }
+    const float nmx = mref == -INFINITY ? 0.f : -mref;  // -inf scores give p = 0 either way
+    float lsum = 0.f;
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tt][v], scale_log2, nmx));
+        lsum += p;
+        sc[tt][v] = p;
+      }
+    lsum += __shfl_xor(lsum, 32, 64);
+    lrun += lsum;
+    // ---- O^T += V^T P^T, V operands read one step ahead
+    vrow_t vb[2];
+    vb[0] = vread(0);
+#pragma unroll
+    for (int i = 0; i < 16 * NT; ++i) {
+      if (i + 1 < 16 * NT) vb[(i + 1) & 1] = vread(i + 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < NU; ++u)
+        o[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[i & 1][u], sc[i >> 4][i & 15], o[u], 0, 0, 0);
+    }
+  };
+
+  if (nsteps > 0) issue(0);
+  for (int s = 0; s < nsteps; ++s) {
+    const int64_t key0 = first_key(s);
+    tsp::dma::wait_vm<0>();  // this wave's loads of stage s are done
+    tsp::dma::barrier();     // every wave's part is in LDS; stage (s+1) % NST is free
+    if (s + 1 < nsteps) issue(s + 1);
+    compute(lds + (s % NST) * STAGE, key0);
+  }
+
+  // ---- epilogue: element v of subtile u is O[q][NU*(8*(v/4) + 4h + v%4) + u]
+  // (o and l both relative to mref); the returned denominator is relative to
+  // the true max
+  const bool empty = nblk == 0;
+  const float lref = lrun > 1e-12f ? lrun : 1e-12f;
+  const float inv = empty ? 0.f : 1.f / lref;
+  const float ltrue = mref == -INFINITY ? lrun : lrun * __builtin_amdgcn_exp2f(mref - mtrue);
+  const float den = ltrue > 1e-12f ? ltrue : 1e-12f;
+  float* Oq = O + head * head_stride + q * D;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    float* dst = Oq + NU * (8 * a + 4 * h);  // 4*NU consecutive floats: index NU*c + u
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+      f32x4 t;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int idx = 4 * k + e;  // = NU*c + u
+        t[e] = o[idx % NU][4 * a + idx / NU] * inv;
+      }
+      *(f32x4*)(dst + 4 * k) = t;
+    }
+  }
+  if (h == 0 && rmax) {
+    const int64_t r = head * Mt * AB + q;
+    rmax[r] = empty ? 0.f : mtrue * 0.69314718055994531f;
+    rden[r] = empty ? 1e-12f : den;
+  }
+}
+
 template <typename T>
 int launch_generic(const void* Q, const void* K, const void* V, int64_t H, int64_t S, int64_t D, const int64_t* rp,
                    const int64_t* ci, int64_t b, int64_t Mt, double scale, void* O, void* rmax, void* rden,
@@ -589,6 +830,22 @@ extern "C" int tsp_bsa_fwd(const void* Q, const void* K, const void* V, int dtyp
                          (const uint16_t*)K, (const uint16_t*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs,
                          block_col_indices, Mt, sl2, (uint16_t*)O, (float*)row_max, (float*)row_denom);
     return tsp::check_launch("bsa_fwd_bf16_mfma launch");
+  }
+  if (dtype == TSP_F32 && block_size == AB && (head_dim == 64 || head_dim == 128) && scale > 0 &&
+      ((uintptr_t)Q % 16) == 0 && ((uintptr_t)K % 16) == 0 && ((uintptr_t)V % 16) == 0 && ((uintptr_t)O % 16) == 0 &&
+      (seq_len + AB) * head_dim * 4 <= (int64_t)UINT32_MAX) {
+    const int64_t grid = tsp::ceil_div(n_heads, 8) * Mt * 8;
+    if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_fwd: problem too large");
+    const float sl2 = (float)(scale * 1.4426950408889634);
+    if (head_dim == 128)
+      hipLaunchKernelGGL((bsa_fwd_f32_mfma<128>), dim3((unsigned)grid), dim3(256), 0, st, (const float*)Q,
+                         (const float*)K, (const float*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs,
+                         block_col_indices, Mt, sl2, (float*)O, (float*)row_max, (float*)row_denom);
+    else
+      hipLaunchKernelGGL((bsa_fwd_f32_mfma<64>), dim3((unsigned)grid), dim3(256), 0, st, (const float*)Q,
+                         (const float*)K, (const float*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs,
+                         block_col_indices, Mt, sl2, (float*)O, (float*)row_max, (float*)row_denom);
+    return tsp::check_launch("bsa_fwd_f32_mfma launch");
   }
   if (dtype == TSP_F64)
     return launch_generic<double>(Q, K, V, n_heads, seq_len, head_dim, block_row_ptrs, block_col_indices, block_size, Mt,

@@ -7,7 +7,9 @@ The oracle takes the same Q, K, V, dO and the GPU forward's O (an input of
 the backward: D = rowsum(dO * O)) and its own float64 row stats. Error
 measure per gradient element: |g - g_exact| / g_abs, with g_abs the oracle's
 absolute form (|dS| replaced by P (|dO V^T| + |D|), operands by their
-magnitudes). fp32 <= 1e-4, bf16 <= 2e-2, fp64 <= 1e-10.
+magnitudes). fp32 <= 1e-4, bf16 <= 2e-2, fp64 <= 1e-10. fp32 with b = 128
+and d in {64, 128} runs the fp32 MFMA kernels, bf16 with d = 128 the bf16
+MFMA kernels, everything else the generic kernels.
 """
 
 from __future__ import annotations
@@ -74,6 +76,11 @@ def _check_head(Q, K, V, dO, O, grads, mask_bsr, scale, tol, rows=None, cols=Non
         (300, 128, local_mask(3, 2), torch.bfloat16),     # MFMA, last key block crosses S
         (1024, 128, global_mask(8, 1, 1), torch.bfloat16),  # MFMA, global column split into 2 segments
         (256, 64, local_mask(2, 1), torch.bfloat16),      # generic bf16
+        (512, 128, local_mask(4, 1), torch.float32),      # fp32 MFMA kernels
+        (1024, 128, global_mask(8, 1, 1), torch.float32),  # fp32 MFMA, global column split into 2 segments
+        (300, 128, local_mask(3, 2), torch.float32),      # fp32 MFMA, last key block crosses S
+        (640, 64, W.cfg5_block_mask(5), torch.float32),   # fp32 MFMA d = 64, global columns split
+        (700, 64, torch.ones(6, 6, dtype=torch.bool), torch.float32),
     ],
 )
 def test_backward_matches_oracle(hip_backend, S, D, mask, dtype):
@@ -115,10 +122,41 @@ def test_backward_batched_heads_bf16(hip_backend):
                         D**-0.5, TOL[torch.bfloat16])
 
 
-def test_backward_deterministic(hip_backend):
+def test_backward_batched_heads_f32(hip_backend):
+    """fp32 MFMA kernels over 3 heads: the column pass's (item, head) grid."""
+    torch.manual_seed(15)
+    S, D = 512, 64
+    mask_bsr = W.bsr_from_block_mask(global_mask(4, 1, 1), 128)
+    Q, K, V, dO = (torch.randn(3, S, D) for _ in range(4))
+    O, dQ, dK, dV = _run(Q, K, V, dO, mask_bsr)
+    for hh in range(3):
+        _check_head(Q[hh], K[hh], V[hh], dO[hh], O[hh], (dQ[hh], dK[hh], dV[hh]), mask_bsr, D**-0.5,
+                    TOL[torch.float32])
+
+
+def test_backward_f32_long_row(hip_backend):
+    """A query block row with more than 64 stored blocks (the row pass reads
+    the row's block columns 64 at a time)."""
+    nb, D = 67, 64
+    S = nb * 128
+    mask = local_mask(nb, 0)
+    mask[1, :] = True
+    mask_bsr = W.bsr_from_block_mask(mask, 128)
+    g = torch.Generator().manual_seed(16)
+    Q, K, V, dO = (torch.randn(S, D, generator=g) for _ in range(4))
+    O, dQ, dK, dV = _run(Q, K, V, dO, mask_bsr)
+    rows, cols = [1, 2], [0, 1, 66]
+    sel_q = np.concatenate([np.arange(r * 128, (r + 1) * 128) for r in rows])
+    sel_k = np.concatenate([np.arange(c * 128, (c + 1) * 128) for c in cols])
+    _check_head(Q, K, V, dO, O, (dQ, dK, dV), mask_bsr, D**-0.5, TOL[torch.float32], rows=rows, cols=cols,
+                sel_q=sel_q, sel_k=sel_k)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_backward_deterministic(hip_backend, dtype):
     torch.manual_seed(13)
     mask_bsr = W.bsr_from_block_mask(global_mask(4, 1, 1), 128)
-    Q, K, V, dO = (torch.randn(2, 512, 128).to(torch.bfloat16) for _ in range(4))
+    Q, K, V, dO = (torch.randn(2, 512, 128).to(dtype) for _ in range(4))
     a = _run(Q, K, V, dO, mask_bsr)
     b = _run(Q, K, V, dO, mask_bsr)
     for x, y in zip(a, b):
@@ -146,3 +184,18 @@ def test_cfg5_backward_full_size(hip_backend):
     expect = dOd[:, live].sum(axis=1)
     bound = np.abs(dOd[:, live]).sum(axis=1) * 2e-2 / 8  # bf16 P and dV rounding, summed magnitudes
     assert (np.abs(got - expect) <= bound + 1e-3).all()
+
+
+def test_cfg5_backward_full_size_f32(hip_backend):
+    """cfg5's shapes and mask with fp32 Q, K, V, dO (the fp32 MFMA kernels):
+    sampled block rows of dQ and block columns of dK / dV against the oracle."""
+    Q, K, V, mask_bsr = W.cfg5_attention()
+    Q, K, V = Q.float(), K.float(), V.float()
+    dO = torch.randn(Q.shape, generator=torch.Generator().manual_seed(14))
+    O, dQ, dK, dV = _run(Q, K, V, dO, mask_bsr)
+    rows, cols = [0, 1, 5, 63], [0, 1, 2, 40, 63]
+    sel_q = np.concatenate([np.arange(r * 128, (r + 1) * 128) for r in rows])
+    sel_k = np.concatenate([np.arange(c * 128, (c + 1) * 128) for c in cols])
+    for hh in (0, 31):
+        _check_head(Q[hh], K[hh], V[hh], dO[hh], O[hh], (dQ[hh], dK[hh], dV[hh]), mask_bsr, 128**-0.5,
+                    TOL[torch.float32], rows=rows, cols=cols, sel_q=sel_q, sel_k=sel_k)

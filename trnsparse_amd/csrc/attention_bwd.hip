@@ -29,6 +29,9 @@
 //       rows in registers, then dV^T += dO^T P and dK^T += Q^T dS with Q and
 //       dO read through transpose reads. Q/dO halves and their stats stream
 //       through a 2-stage LDS ring.
+//   bsa_bwd_dq_f32<D> / bsa_bwd_dkdv_f32<D> / bsa_bwd_reduce_f32<D>  fp32,
+//       b = 128, D in {64, 128}: the same passes on v_mfma_f32_32x32x2_f32
+//       (operand forms at the kernels).
 //   bsa_bwd_dq_generic / bsa_bwd_dkdv_generic  any dtype / block size /
 //       head_dim: one thread per (row, 32-wide slice of head_dim).
 // Swizzle: K (row pass) and Q, dO (column pass) are read both as 16-byte rows
@@ -777,6 +780,460 @@ __global__ __launch_bounds__(256) void bsa_bwd_reduce(const int32_t* __restrict_
   }
 }
 
+// ------------------------------------------------------------- fp32 MFMA
+//
+// fp32, b = 128, head_dim D in {64, 128}, on v_mfma_f32_32x32x2_f32. Same
+// split as the bf16 kernels (a row pass for dQ that also leaves the query
+// stats, a column pass for dK / dV over the column plan, a reduce for split
+// columns), with one ring stage per 4096 / D rows (K and V rows in the row
+// pass, Q and dO rows plus their stats in the column pass) streamed by direct
+// buffer loads one stage ahead. Operand forms, as in the fp32 forward:
+//   * products over head_dim (S, dP): lane half h supplies d = 8t + 4h + c
+//     at step 4t + c, one b128 read per four MFMAs from 32 rows of a stage
+//     (chunk read) against the wave's own rows held in registers;
+//   * products over rows (dQ, dK, dV): the output's MFMA row r is head_dim
+//     NU*r + u, so one contiguous read of NU floats of a stage row (row
+//     read) feeds all NU subtiles, and the k index follows the accumulator
+//     row order of the S / dP tiles, whose elements are the B operand in
+//     place.
+// Stage rows are stored 16-byte chunk ^ (row % 16): chunk reads of one chunk
+// from 32 rows hit distinct banks, and a row read is a permutation of one
+// row.
+namespace abf {
+template <int D>
+struct Cfg {
+  static constexpr int BS = 128;
+  static constexpr int HR = 4096 / D;       // rows per ring stage
+  static constexpr int ROWB = D * 4;        // bytes per row
+  static constexpr int HBYTES = HR * ROWB;  // 16 KiB
+  static constexpr int NT = HR / 32;        // 32-row tiles per stage
+  static constexpr int NU = D / 32;         // head_dim subtiles of row products
+  static constexpr int KT = D / 8;          // b128 chunk reads per 32-row tile
+  static constexpr int SPB = BS / HR;       // stages per block
+};
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+template <int NU> struct VRow;
+template <> struct VRow<4> { typedef f32x4 type; };
+template <> struct VRow<2> { typedef f32x2 type; };
+
+// One wave's share of a stage: rows [row0, row0 + HR) of the buffer rs into
+// LDS dst, 16 instructions of 1 KiB, 4 per wave.
+template <int D>
+__device__ inline void dma_rows(tsp::dma::i32x4 rs, int64_t row0, uint32_t dst, int w, int lane) {
+  constexpr int LPR = D / 4, RPI = 64 / LPR, ROWB = D * 4;
+#pragma unroll
+  for (int qq = 0; qq < 4; ++qq) {
+    const int j = 4 * w + qq;
+    const int rr = RPI * j + lane / LPR;
+    const int p = lane % LPR;
+    tsp::dma::buffer16(rs, (uint32_t)((row0 + rr) * ROWB + ((p ^ (rr & 15)) << 4)), dst + j * 1024);
+  }
+}
+// chunk read: logical chunk c of stage row `row` (row % 16 == kx)
+template <int D>
+__device__ inline f32x4 chunk_read(const uint8_t* base, int row, int c, int kx) {
+  return *(const f32x4*)(base + row * (D * 4) + ((c ^ kx) << 4));
+}
+// row read: floats [NU * l32, NU * l32 + NU) of stage row `row`
+template <int D>
+__device__ inline typename VRow<D / 32>::type row_read(const uint8_t* base, int row, int l32) {
+  constexpr int NU = D / 32;
+  const int byte = NU * 4 * l32;
+  return *(const typename VRow<NU>::type*)(base + row * (D * 4) + ((((byte >> 4) ^ (row & 15))) << 4) + (byte & 15));
+}
+// Store a 32-row x D tile held as NU accumulators (element v of subtile u is
+// head_dim NU * (8 (v / 4) + 4 h + v % 4) + u of the lane's row) to dst, times f.
+template <int D>
+__device__ inline void store_rows(float* dst, const f32x16* acc, int h, float f) {
+  constexpr int NU = D / 32;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    float* d = dst + NU * (8 * a + 4 * h);
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+      f32x4 t;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int idx = 4 * k + e;
+        t[e] = acc[idx % NU][4 * a + idx / NU] * f;
+      }
+      *(f32x4*)(d + 4 * k) = t;
+    }
+  }
+}
+}  // namespace abf
+
+// Row pass: workgroup per (head, query block row m < Mt), XCD-aware order as
+// the forward; wavefront w owns queries m * 128 + 32 w + [0, 32) with their Q
+// and dO rows in registers. Per 32-key tile: S^T = K Q^T and dP^T = V dO^T
+// (K, V chunk reads), dS^T = P^T (dP^T - D) in place, dQ^T += K^T dS^T (K row
+// reads). Writes the column pass's query stats: plane 0 r = log2e * row_max
+// + log2 row_denom (P = exp2(log2e * scale * s - r)), plane 1 D.
+template <int D>
+__global__ __launch_bounds__(256, 1) void bsa_bwd_dq_f32(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V, const float* __restrict__ O,
+    const float* __restrict__ dO, int64_t S, int64_t H, const int64_t* __restrict__ rp,
+    const int64_t* __restrict__ ci, int64_t Mt, float scale_log2, float scale, const float* __restrict__ rmax,
+    const float* __restrict__ rden, float* __restrict__ qstat, float* __restrict__ dQ) {
+  typedef abf::Cfg<D> C;
+  constexpr int BS = C::BS, HR = C::HR, ROWB = C::ROWB, HBYTES = C::HBYTES, NT = C::NT, NU = C::NU, KT = C::KT;
+  constexpr int SPB = C::SPB, STAGE = 2 * HBYTES, NST = 2;
+  typedef typename abf::VRow<NU>::type vrow_t;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
+
+  const int64_t g = blockIdx.x;
+  const int64_t xcd = g & 7, slot = g >> 3;
+  const int64_t head = xcd + 8 * (slot / Mt);
+  const int64_t m = slot % Mt;
+  if (head >= H) return;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int64_t hs = head * S * D;
+  const int64_t q = m * BS + w * 32 + l32;  // < S since m < Mt
+
+  f32x4 qf[KT], dof[KT];
+  float dsum = 0.f;
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    qf[t] = *(const f32x4*)(Q + hs + q * D + 8 * t + 4 * h);
+    dof[t] = *(const f32x4*)(dO + hs + q * D + 8 * t + 4 * h);
+    const f32x4 of = *(const f32x4*)(O + hs + q * D + 8 * t + 4 * h);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) dsum += dof[t][c] * of[c];
+  }
+  const float Dq = dsum + __shfl_xor(dsum, 32, 64);
+  const float rq = rmax[head * Mt * BS + q] * LOG2E + __builtin_amdgcn_logf(rden[head * Mt * BS + q]);
+  const float nr = -rq;
+  if (h == 0) {
+    qstat[head * S + q] = rq;
+    qstat[H * S + head * S + q] = Dq;
+  }
+
+  f32x16 acc[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) acc[u] = f32x16{};
+
+  const int64_t start = rp[m];
+  const int nblk = (int)(rp[m + 1] - start);
+  const int nsteps = SPB * nblk;
+  const tsp::dma::i32x4 krs = tsp::dma::make_rsrc(K + hs, (uint32_t)(S * ROWB));
+  const tsp::dma::i32x4 vrs = tsp::dma::make_rsrc(V + hs, (uint32_t)(S * ROWB));
+  const uint32_t lds0 = tsp::dma::lds_addr(lds);
+
+  int cbase = 0, cv = 0;
+  auto load_cols = [&](int base) {
+    const int i = base + lane < nblk ? base + lane : nblk - 1;
+    return tsp::dma::load_lo32_sync(ci + start + i);
+  };
+  if (nblk > 0) cv = load_cols(0);
+  auto colblk = [&](int blk) {
+    if (blk - cbase >= 64) {
+      cbase = blk & ~63;
+      cv = load_cols(cbase);
+    }
+    return __builtin_amdgcn_readlane(cv, blk - cbase);
+  };
+  auto first_key = [&](int s) { return (int64_t)colblk(s / SPB) * BS + HR * (s % SPB); };
+  auto issue = [&](int s) {
+    const int64_t key0 = first_key(s);
+    const uint32_t st = lds0 + (s % NST) * STAGE;
+    abf::dma_rows<D>(krs, key0, st, w, lane);
+    abf::dma_rows<D>(vrs, key0, st + HBYTES, w, lane);
+  };
+
+  const int kx = l32 & 15;
+  auto compute = [&](const uint8_t* st, int64_t key0) {
+    const uint8_t* Ks = st;
+    const uint8_t* Vs = st + HBYTES;
+    f32x16 sc[NT], dp[NT];
+    f32x4 ka[2][NT], va[2][NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+      ka[0][tt] = abf::chunk_read<D>(Ks, 32 * tt + l32, h, kx);
+      va[0][tt] = abf::chunk_read<D>(Vs, 32 * tt + l32, h, kx);
+    }
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      if (t + 1 < KT) {
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) {
+          ka[(t + 1) & 1][tt] = abf::chunk_read<D>(Ks, 32 * tt + l32, 2 * (t + 1) + h, kx);
+          va[(t + 1) & 1][tt] = abf::chunk_read<D>(Vs, 32 * tt + l32, 2 * (t + 1) + h, kx);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) {
+          const bool first = t == 0 && c == 0;
+          sc[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[t & 1][tt][c], qf[t][c], first ? f32x16{} : sc[tt], 0, 0, 0);
+          dp[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(va[t & 1][tt][c], dof[t][c], first ? f32x16{} : dp[tt], 0, 0, 0);
+        }
+    }
+    // dS^T element v of tile tt: key key0 + 32 tt + 8 (v / 4) + 4 h + v % 4
+    const bool tail = key0 + HR > S;
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tt][v], scale_log2, nr));
+        if (tail && key0 + 32 * tt + 8 * (v >> 2) + 4 * h + (v & 3) >= S) p = 0.f;
+        sc[tt][v] = p * (dp[tt][v] - Dq);
+      }
+    // dQ^T += K^T dS^T
+    vrow_t kb[2];
+    auto krow = [&](int i) { return abf::row_read<D>(Ks, 32 * (i >> 4) + 8 * ((i & 15) >> 2) + 4 * h + (i & 3), l32); };
+    kb[0] = krow(0);
+#pragma unroll
+    for (int i = 0; i < 16 * NT; ++i) {
+      if (i + 1 < 16 * NT) kb[(i + 1) & 1] = krow(i + 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < NU; ++u)
+        acc[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(kb[i & 1][u], sc[i >> 4][i & 15], acc[u], 0, 0, 0);
+    }
+  };
+
+  if (nsteps > 0) issue(0);
+  for (int s = 0; s < nsteps; ++s) {
+    const int64_t key0 = first_key(s);
+    tsp::dma::wait_vm<0>();
+    tsp::dma::barrier();
+    if (s + 1 < nsteps) issue(s + 1);
+    compute(lds + (s % NST) * STAGE, key0);
+  }
+  abf::store_rows<D>(dQ + hs + q * D, acc, h, scale);
+}
+
+// Column pass: workgroup per (plan item, head), items heaviest first; an
+// item is (key block column, range [p0, p1) of its column view, partial slot
+// or -1). Wavefront w owns keys col * 128 + 32 w + [0, 32) with the K and V
+// rows in registers. Per 32-query tile of a stored block row m < Mt: S =
+// Q K^T and dP = dO V^T (Q, dO chunk reads), P and dS = P (dP - D) in place
+// with the stats staged beside the rows, dV^T += dO^T P and dK^T += Q^T dS
+// (dO, Q row reads). An item covering a whole column writes dK / dV, a
+// segment of a split column writes fp32 partials summed by the reduce.
+template <int D>
+__global__ __launch_bounds__(256, 1) void bsa_bwd_dkdv_f32(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ dO, int64_t S, int64_t H, const int64_t* __restrict__ crow,
+    const int32_t* __restrict__ items, int n_partials, int64_t Mt, float scale_log2, float scale,
+    const float* __restrict__ qstat, float* __restrict__ dK, float* __restrict__ dV, float* __restrict__ partial) {
+  typedef abf::Cfg<D> C;
+  constexpr int BS = C::BS, HR = C::HR, ROWB = C::ROWB, HBYTES = C::HBYTES, NT = C::NT, NU = C::NU, KT = C::KT;
+  constexpr int SPB = C::SPB, STAGE = 2 * HBYTES + 1024, NST = 2;  // Q rows, dO rows, stats (r[HR], D[HR])
+  typedef typename abf::VRow<NU>::type vrow_t;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
+
+  const int64_t it = blockIdx.x / H, head = blockIdx.x % H;
+  const int col = items[4 * it], p0 = items[4 * it + 1], p1 = items[4 * it + 2], pslot = items[4 * it + 3];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int64_t hs = head * S * D, HS = H * S;
+  const int64_t key = (int64_t)col * BS + w * 32 + l32;
+  const bool kvalid = key < S;
+
+  f32x4 kf[KT], vf[KT];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    kf[t] = kvalid ? *(const f32x4*)(K + hs + key * D + 8 * t + 4 * h) : f32x4{};
+    vf[t] = kvalid ? *(const f32x4*)(V + hs + key * D + 8 * t + 4 * h) : f32x4{};
+  }
+  f32x16 dk[NU], dv[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) dk[u] = dv[u] = f32x16{};
+
+  const int nblk = p1 - p0;
+  const int nsteps = SPB * nblk;
+  const tsp::dma::i32x4 qrs = tsp::dma::make_rsrc(Q + hs, (uint32_t)(S * ROWB));
+  const tsp::dma::i32x4 ors = tsp::dma::make_rsrc(dO + hs, (uint32_t)(S * ROWB));
+  const uint32_t lds0 = tsp::dma::lds_addr(lds);
+
+  // block rows of the item, 64 at a time in one VGPR, read with readlane
+  int rbase = 0, rv = 0;
+  auto load_rows = [&](int base) {
+    const int i = base + lane < nblk ? base + lane : nblk - 1;
+    return tsp::dma::load_lo32_sync(crow + p0 + i);
+  };
+  if (nblk > 0) rv = load_rows(0);
+  auto rowblk = [&](int i) {
+    if (i - rbase >= 64) {
+      rbase = i & ~63;
+      rv = load_rows(rbase);
+    }
+    return (int64_t)__builtin_amdgcn_readlane(rv, i - rbase);
+  };
+  // stage s: block row rowblk(s / SPB) (skipped when >= Mt: no forward
+  // queries), queries from m * 128 + HR * (s % SPB)
+  auto issue = [&](int s, int64_t mrow) {
+    if (mrow >= Mt) return;
+    const int64_t q0 = mrow * BS + HR * (s % SPB);
+    const uint32_t st = lds0 + (s % NST) * STAGE;
+    abf::dma_rows<D>(qrs, q0, st, w, lane);
+    abf::dma_rows<D>(ors, q0, st + HBYTES, w, lane);
+    if (w == 0) {  // lanes [0, HR/4): r, the rest D (the lanes past 2 HR / 4 repeat D)
+      constexpr int LPP = HR / 4;
+      const int plane = lane >= LPP ? 1 : 0;
+      tsp::dma::global16(qstat + plane * HS + head * S + q0 + 4 * (lane % LPP), st + 2 * HBYTES);
+    }
+  };
+
+  const int kx = l32 & 15;
+  auto compute = [&](const uint8_t* st) {
+    const uint8_t* Qs = st;
+    const uint8_t* Os = st + HBYTES;
+    const float* stats = (const float*)(st + 2 * HBYTES);
+    f32x16 sc[NT], dp[NT];
+    f32x4 qa[2][NT], oa[2][NT];
+#pragma unroll
+    for (int qt = 0; qt < NT; ++qt) {
+      qa[0][qt] = abf::chunk_read<D>(Qs, 32 * qt + l32, h, kx);
+      oa[0][qt] = abf::chunk_read<D>(Os, 32 * qt + l32, h, kx);
+    }
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      if (t + 1 < KT) {
+#pragma unroll
+        for (int qt = 0; qt < NT; ++qt) {
+          qa[(t + 1) & 1][qt] = abf::chunk_read<D>(Qs, 32 * qt + l32, 2 * (t + 1) + h, kx);
+          oa[(t + 1) & 1][qt] = abf::chunk_read<D>(Os, 32 * qt + l32, 2 * (t + 1) + h, kx);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int qt = 0; qt < NT; ++qt) {
+          const bool first = t == 0 && c == 0;
+          sc[qt] = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[t & 1][qt][c], kf[t][c], first ? f32x16{} : sc[qt], 0, 0, 0);
+          dp[qt] = __builtin_amdgcn_mfma_f32_32x32x2f32(oa[t & 1][qt][c], vf[t][c], first ? f32x16{} : dp[qt], 0, 0, 0);
+        }
+    }
+    // P and dS element v of tile qt: query 32 qt + 8 (v / 4) + 4 h + v % 4 of the stage
+#pragma unroll
+    for (int qt = 0; qt < NT; ++qt)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const f32x4 r4 = *(const f32x4*)(stats + 32 * qt + 8 * a + 4 * h);
+        const f32x4 d4 = *(const f32x4*)(stats + HR + 32 * qt + 8 * a + 4 * h);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int v = 4 * a + c;
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qt][v], scale_log2, -r4[c]));
+          sc[qt][v] = p;
+          dp[qt][v] = p * (dp[qt][v] - d4[c]);
+        }
+      }
+    // dV^T += dO^T P, dK^T += Q^T dS
+    vrow_t ob[2], qb[2];
+    auto rowof = [&](int i) { return 32 * (i >> 4) + 8 * ((i & 15) >> 2) + 4 * h + (i & 3); };
+    ob[0] = abf::row_read<D>(Os, rowof(0), l32);
+    qb[0] = abf::row_read<D>(Qs, rowof(0), l32);
+#pragma unroll
+    for (int i = 0; i < 16 * NT; ++i) {
+      if (i + 1 < 16 * NT) {
+        ob[(i + 1) & 1] = abf::row_read<D>(Os, rowof(i + 1), l32);
+        qb[(i + 1) & 1] = abf::row_read<D>(Qs, rowof(i + 1), l32);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        dv[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(ob[i & 1][u], sc[i >> 4][i & 15], dv[u], 0, 0, 0);
+        dk[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(qb[i & 1][u], dp[i >> 4][i & 15], dk[u], 0, 0, 0);
+      }
+    }
+  };
+
+  if (nsteps > 0) issue(0, rowblk(0));
+  for (int s = 0; s < nsteps; ++s) {
+    const int64_t mrow = rowblk(s / SPB);
+    tsp::dma::wait_vm<0>();
+    tsp::dma::barrier();
+    if (s + 1 < nsteps) issue(s + 1, rowblk((s + 1) / SPB));
+    if (mrow < Mt) compute(lds + (s % NST) * STAGE);
+  }
+
+  if (pslot < 0) {
+    if (kvalid) {
+      abf::store_rows<D>(dK + hs + key * D, dk, h, scale);
+      abf::store_rows<D>(dV + hs + key * D, dv, h, 1.f);
+    }
+  } else {
+    float* pk = partial + (((int64_t)head * n_partials + pslot) * 2) * (BS * D) + (w * 32 + l32) * D;
+    abf::store_rows<D>(pk, dk, h, scale);
+    abf::store_rows<D>(pk + BS * D, dv, h, 1.f);
+  }
+}
+
+// dK / dV of the split columns in fp32: sum of the segments' partials in
+// segment order (deterministic). Workgroup per (split, 16-key chunk, head);
+// thread per 4 consecutive head_dim values of one key of dK or dV.
+template <int D>
+__global__ __launch_bounds__(256) void bsa_bwd_reduce_f32(const int32_t* __restrict__ splits, int n_partials, int64_t S,
+                                                          const float* __restrict__ partial, float* __restrict__ dK,
+                                                          float* __restrict__ dV) {
+  constexpr int BS = 128;
+  const int sp = blockIdx.x >> 3, chunk = blockIdx.x & 7;
+  const int64_t head = blockIdx.y;
+  const int col = splits[4 * sp], slot0 = splits[4 * sp + 1], nseg = splits[4 * sp + 2];
+  const float* base = partial + (head * n_partials + slot0) * 2 * (BS * D);
+#pragma unroll
+  for (int e0 = 0; e0 < 2 * 16 * (D / 4); e0 += 256) {
+    const int e = e0 + threadIdx.x;
+    const int which = e / (16 * (D / 4));
+    const int r = chunk * 16 + (e / (D / 4)) % 16, d4 = e % (D / 4);
+    const int64_t key = (int64_t)col * BS + r;
+    if (key >= S) continue;
+    f32x4 sum = f32x4{};
+    for (int j = 0; j < nseg; ++j) sum += *(const f32x4*)(base + (j * 2 + which) * (BS * D) + r * D + 4 * d4);
+    *(f32x4*)((which ? dV : dK) + (head * S + key) * D + 4 * d4) = sum;
+  }
+}
+
+template <int D>
+int launch_f32(const void* Q, const void* K, const void* V, const void* O, const void* dO, int64_t H, int64_t S,
+               const int64_t* rp, const int64_t* ci, const int64_t* crow, int64_t Mt, double scale,
+               const void* rmax, const void* rden, void* dQ, void* dK, void* dV, const int32_t* plan, int64_t n_items,
+               int64_t n_splits, int64_t n_partials, void* workspace, hipStream_t st) {
+  const int64_t nh = tsp::ceil_div(H, 8);
+  const int64_t grid_a = nh * Mt * 8, grid_b = n_items * H;
+  if (grid_a > INT32_MAX || grid_b > INT32_MAX || 8 * n_splits > INT32_MAX || H > 65535)
+    return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_bwd: problem too large");
+  const float sl2 = (float)(scale * 1.4426950408889634);
+  float* qstat = (float*)workspace;
+  float* partial = (float*)((char*)workspace + 16 * H * S);
+  if (Mt * 128 < S) {  // rows without a block row: zero dQ
+    const int64_t tail = (S - Mt * 128) * D * 4;
+    for (int64_t hh = 0; hh < H; ++hh) {
+      int rc = tsp::zero_fill((char*)dQ + (hh * S + Mt * 128) * D * 4, tail, st);
+      if (rc) return rc;
+    }
+  }
+  if (grid_a > 0) {
+    hipLaunchKernelGGL((bsa_bwd_dq_f32<D>), dim3((unsigned)grid_a), dim3(256), 0, st, (const float*)Q, (const float*)K,
+                       (const float*)V, (const float*)O, (const float*)dO, S, H, rp, ci, Mt, sl2, (float)scale,
+                       (const float*)rmax, (const float*)rden, qstat, (float*)dQ);
+    int rc = tsp::check_launch("bsa_bwd_dq_f32 launch");
+    if (rc) return rc;
+  }
+  if (grid_b > 0) {
+    hipLaunchKernelGGL((bsa_bwd_dkdv_f32<D>), dim3((unsigned)grid_b), dim3(256), 0, st, (const float*)Q,
+                       (const float*)K, (const float*)V, (const float*)dO, S, H, crow, plan + 4, (int)n_partials, Mt,
+                       sl2, (float)scale, (const float*)qstat, (float*)dK, (float*)dV, partial);
+    int rc = tsp::check_launch("bsa_bwd_dkdv_f32 launch");
+    if (rc) return rc;
+  }
+  if (n_splits > 0) {
+    hipLaunchKernelGGL((bsa_bwd_reduce_f32<D>), dim3((unsigned)(8 * n_splits), (unsigned)H), dim3(256), 0, st,
+                       plan + 4 + 4 * n_items, (int)n_partials, S, (const float*)partial, (float*)dK, (float*)dV);
+    int rc = tsp::check_launch("bsa_bwd_reduce_f32 launch");
+    if (rc) return rc;
+  }
+  return TSP_OK;
+}
+
 }  // namespace
 
 // Host-side plan of the column pass. Items cover every key block column
@@ -923,6 +1380,20 @@ extern "C" int tsp_bsa_bwd(const void* Q, const void* K, const void* V, const vo
       if (rc) return rc;
     }
     return TSP_OK;
+  }
+
+  const bool aligned16 = aligned && ((uintptr_t)dQ % 16) == 0 && ((uintptr_t)dK % 16) == 0 && ((uintptr_t)dV % 16) == 0;
+  if (dtype == TSP_F32 && block_size == 128 && (head_dim == 64 || head_dim == 128) && scale > 0 && plan && aligned16 &&
+      (seq_len + 128) * head_dim * 4 <= (int64_t)UINT32_MAX) {
+    if (n_items < tsp::ceil_div(seq_len, block_size))
+      return tsp::fail(TSP_EINVAL, "tsp_bsa_bwd: plan has %lld items for %lld key block columns", (long long)n_items,
+                       (long long)tsp::ceil_div(seq_len, block_size));
+    if (head_dim == 128)
+      return launch_f32<128>(Q, K, V, O, dO, n_heads, seq_len, block_row_ptrs, block_col_indices, col_block_rows, Mt,
+                             scale, row_max, row_denom, dQ, dK, dV, plan, n_items, n_splits, n_partials, workspace,
+                             stream_);
+    return launch_f32<64>(Q, K, V, O, dO, n_heads, seq_len, block_row_ptrs, block_col_indices, col_block_rows, Mt, scale,
+                          row_max, row_denom, dQ, dK, dV, plan, n_items, n_splits, n_partials, workspace, stream_);
   }
 
   // D = rowsum(dO * O) into the workspace

@@ -54,7 +54,11 @@ def _check(A: ts.BSRMatrix, B: torch.Tensor, G: torch.Tensor, tol: float):
         ((300, 260), 128, 12, 1.0, torch.float32),     # unaligned m, n (padded blocks)
         ((300, 260), 128, 10, 1.0, torch.float32),     # N % 4 != 0: generic kernels
         ((40, 40), 8, 12, 0.4, torch.float64),         # any block size, fp64
-        ((256, 256), 128, 64, 0.5, torch.bfloat16),
+        ((256, 256), 128, 64, 0.5, torch.bfloat16),    # bf16 MFMA kernels
+        ((512, 384), 128, 256, 0.4, torch.bfloat16),
+        ((384, 256), 128, 200, 0.6, torch.bfloat16),   # N % 64 != 0: zero-filled k tail
+        ((300, 260), 128, 24, 1.0, torch.bfloat16),    # unaligned m, n
+        ((300, 260), 128, 12, 1.0, torch.bfloat16),    # N % 8 != 0: generic kernels
     ],
 )
 def test_backward_matches_oracle(hip_backend, shape, b, N, density, dtype):
@@ -79,6 +83,19 @@ def test_backward_empty_rows_and_columns(hip_backend):
     _check(bsr, B, G, TOL[torch.float32])
     _, dB = _grads(bsr, B, G)
     assert torch.count_nonzero(dB[128:256]).item() == 0  # block column 1 holds no blocks
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_backward_long_block_column(hip_backend, dtype):
+    """A block column with 65 stored blocks (the dB kernels read a column's
+    block ids 64 at a time)."""
+    g = torch.Generator().manual_seed(7)
+    A = torch.randn(65 * 128, 128, generator=g, dtype=torch.float64)
+    bsr = ts.BSRMatrix.from_dense(A.to(dtype), block_size=128)
+    assert bsr.n_blocks == 65
+    B = torch.randn(128, 64, generator=g, dtype=torch.float64).to(dtype)
+    G = torch.randn(65 * 128, 64, generator=g, dtype=torch.float64).to(dtype)
+    _check(bsr, B, G, TOL[dtype])
 
 
 def test_backward_deterministic(hip_backend):
@@ -118,3 +135,26 @@ def test_cfg3a_backward_full_size(hip_backend):
         exact = sum(blocks[k].T @ Gn[brow[k] * 128 : (brow[k] + 1) * 128] for k in ks)
         scale = sum(np.abs(blocks[k]).T @ np.abs(Gn[brow[k] * 128 : (brow[k] + 1) * 128]) for k in ks)
         assert ref.scaled_error(dB[j * 128 : (j + 1) * 128].cpu().numpy(), exact, scale) <= TOL[torch.float32]
+
+
+def test_cfg3b_backward_full_size(hip_backend):
+    """cfg3b (bf16, 1638 blocks, N = 512, the bf16 MFMA kernels): dA on a
+    sample of blocks and dB on a sample of block columns against float64."""
+    A, B = W.cfg3_bsr(dtype=torch.bfloat16)
+    G = torch.randn(A.shape[0], B.shape[1], generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    db, dB = _grads(A, B, G)
+    assert db.dtype == torch.bfloat16 and dB.dtype == torch.bfloat16
+    Gn, Bn = G.double().numpy(), B.double().numpy()
+    ptr, col = A.block_row_ptrs.numpy(), A.block_col_indices.numpy()
+    brow = np.repeat(np.arange(len(ptr) - 1), np.diff(ptr))
+    for k in (0, 1, 700, 1637):
+        i, j = brow[k], col[k]
+        exact = Gn[i * 128 : (i + 1) * 128] @ Bn[j * 128 : (j + 1) * 128].T
+        scale = np.abs(Gn[i * 128 : (i + 1) * 128]) @ np.abs(Bn[j * 128 : (j + 1) * 128]).T
+        assert ref.scaled_error(db[k].double().cpu().numpy(), exact, scale) <= TOL[torch.bfloat16]
+    blocks = A.blocks.double().numpy()
+    for j in (0, 64, 127):
+        ks = np.nonzero(col == j)[0]
+        exact = sum(blocks[k].T @ Gn[brow[k] * 128 : (brow[k] + 1) * 128] for k in ks)
+        scale = sum(np.abs(blocks[k]).T @ np.abs(Gn[brow[k] * 128 : (brow[k] + 1) * 128]) for k in ks)
+        assert ref.scaled_error(dB[j * 128 : (j + 1) * 128].double().cpu().numpy(), exact, scale) <= TOL[torch.bfloat16]

@@ -26,6 +26,9 @@
 //                        block row as the [k][n] operand. Scheduling as the
 //                        forward kernel (heaviest columns first, boustrophedon
 //                        over the XCDs, one workgroup per CU).
+//   bsr_sddmm_bf16_mfma / bsr_spmm_t_bf16_mfma   b == 128, bf16 (fp32
+//                        accumulation, bf16 results): the same two products on
+//                        v_mfma_f32_32x32x16_bf16 (operand forms at the kernels).
 //   bsr_sddmm_generic / bsr_spmm_t_generic   any block size, f32 / f64 / bf16
 //                        (accumulating in f32, f64 for f64): one thread per
 //                        output element.
@@ -282,6 +285,231 @@ __global__ __launch_bounds__(256) void bsr_spmm_t_f32_dma(
   }
 }
 
+// ------------------------------------------------------------ bf16 MFMA
+//
+// bf16 operands, fp32 accumulation, bf16 results, b == 128, on
+// v_mfma_f32_32x32x16_bf16 (lane half h supplies k = 8h .. 8h + 7 of each
+// 16-k step; A rows / B columns are lane % 32). One engine for both
+// products: 256 threads, 4 waves of 64x64 (2 x 2 accumulators), 64-wide
+// k-slabs of two operand tiles streamed through a 4-stage LDS ring by direct
+// loads issued three slabs ahead (4 + 4 wave instructions per slab). Each
+// operand tile is in one of two forms:
+//   ROW: [128 rows][64 k], rows of 128 B, k contiguous: a lane's 8 k values
+//        are one b128 read; chunk ^ ((row / 2) % 8) (16 consecutive rows of
+//        one chunk cover the 64 banks);
+//   TR:  [64 k][128 columns], rows of 256 B: the 8 k values come from two
+//        ds_read_b64_tr_b16 (4 consecutive k rows each); chunk ^ 4 (row % 4).
+// dA (SDDMM): both operands ROW (dC rows of the block row, B rows of the
+// block column, k = columns). dB = A^T dC: both operands TR (the block's
+// rows are k, its columns the output rows; dC rows of the block row).
+namespace bfb {
+constexpr int KC = 64;
+constexpr int NST = 4;
+constexpr int TILE = 16384;
+constexpr int STAGE = 2 * TILE;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// ROW tile: rows [row0, row0 + 128) x columns [k0, k0 + 64) of a bf16
+// row-major matrix (stride ld) behind rs; columns at or past kend read as
+// zero (kend % 8 == 0).
+__device__ inline void dma_row(i32x4 rs, int64_t row0, int64_t ld, int64_t k0, int64_t kend, uint32_t dst, int w,
+                               int lane) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int i = 4 * w + q;
+    const int r = 8 * i + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    const int64_t col = k0 + c * 8;
+    const uint32_t off = col < kend ? (uint32_t)(((row0 + r) * ld + col) * 2) : OOB;
+    tsp::dma::buffer16(rs, off, dst + i * 1024);
+  }
+}
+// TR tile: rows [row0, row0 + 64) x columns [c0, c0 + 128) of a bf16
+// row-major matrix (stride ld) behind rs.
+__device__ inline void dma_tr(i32x4 rs, int64_t row0, int64_t ld, int64_t c0, uint32_t dst, int w, int lane) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int j = 4 * w + q;
+    const int rr = 4 * j + (lane >> 4);
+    const int c = (lane & 15) ^ (4 * (rr & 3));
+    tsp::dma::buffer16(rs, (uint32_t)(((row0 + rr) * ld + c0 + c * 8) * 2), dst + j * 1024);
+  }
+}
+// The same TR tile from a 128-column block that is always in bounds.
+__device__ inline void dma_tr_block(const uint16_t* src, uint32_t dst, int w, int lane) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int j = 4 * w + q;
+    const int rr = 4 * j + (lane >> 4);
+    const int c = (lane & 15) ^ (4 * (rr & 3));
+    tsp::dma::global16(src + rr * BS + c * 8, dst + j * 1024);
+  }
+}
+// Operand of 16-k step ks for tile row / column `base` + lane % 32.
+__device__ inline bf16x8 op_row(const uint8_t* tile, int base, int ks, int lane) {
+  const int r = base + (lane & 31);
+  return *(const bf16x8*)(tile + r * 128 + (((2 * ks + (lane >> 5)) ^ ((r >> 1) & 7)) * 16));
+}
+__device__ inline bf16x8 op_tr(const uint8_t* tile, int base, int ks, int lane) {
+  const int gq = lane >> 4, jq = lane & 15;
+  const int col = base + 16 * (gq & 1) + 4 * (jq & 3);
+  s16x4 v[2];
+#pragma unroll
+  for (int kq = 0; kq < 2; ++kq) {
+    const int rr = 16 * ks + 8 * (gq >> 1) + (jq >> 2) + 4 * kq;
+    const uint8_t* p = tile + rr * 256 + (((col >> 3) ^ (4 * (jq >> 2))) * 16) + (col & 4) * 2;
+    v[kq] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
+  }
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// The slab loop shared by both kernels: issue(s) fills stage s % NST,
+// compute runs the 4 k-steps of a stage into acc.
+template <bool AROW, bool BROW, typename Issue>
+__device__ inline void run(Issue&& issue, int nsteps, const uint8_t* lds, f32x16 (&acc)[2][2], int wm, int wn,
+                           int lane) {
+  auto fetch = [&](const uint8_t* st, int ks, bf16x8 (&a)[2], bf16x8 (&b)[2]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      a[t] = AROW ? op_row(st, wm * 64 + 32 * t, ks, lane) : op_tr(st, wm * 64 + 32 * t, ks, lane);
+      b[t] = BROW ? op_row(st + TILE, wn * 64 + 32 * t, ks, lane) : op_tr(st + TILE, wn * 64 + 32 * t, ks, lane);
+    }
+  };
+  const int pre = nsteps < NST - 1 ? nsteps : NST - 1;
+  for (int s = 0; s < pre; ++s) issue(s);
+  for (int s = 0; s < nsteps; ++s) {
+    // this wave's loads of slab s are done when only later slabs' (8 each) are in flight
+    const int later = nsteps - 1 - s;
+    if (later >= 2)
+      tsp::dma::wait_vm<16>();
+    else if (later == 1)
+      tsp::dma::wait_vm<8>();
+    else
+      tsp::dma::wait_vm<0>();
+    tsp::dma::barrier();  // every wave's part of slab s is in LDS; stage (s - 1) % NST is free
+    if (s + NST - 1 < nsteps) issue(s + NST - 1);
+    const uint8_t* st = lds + (s % NST) * STAGE;
+    bf16x8 a[2][2], b[2][2];
+    fetch(st, 0, a[0], b[0]);
+#pragma unroll
+    for (int ks = 0; ks < KC / 16; ++ks) {
+      if (ks + 1 < KC / 16) fetch(st, ks + 1, a[(ks + 1) & 1], b[(ks + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks & 1][t], b[ks & 1][u], acc[t][u], 0, 0, 0);
+    }
+  }
+}
+}  // namespace bfb
+
+// dA (SDDMM), bf16: workgroup per stored block, XCD x takes a contiguous
+// range of blocks as in bsr_sddmm_f32_dma.
+__global__ __launch_bounds__(256) void bsr_sddmm_bf16_mfma(const uint16_t* __restrict__ G, int64_t ldg, int64_t m,
+                                                           const uint16_t* __restrict__ B, int64_t ldb, int64_t n,
+                                                           int64_t ncols, const int64_t* __restrict__ brow,
+                                                           const int64_t* __restrict__ ci, int64_t nnzb,
+                                                           uint16_t* __restrict__ out) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[bfb::NST * bfb::STAGE];
+  const int64_t g = blockIdx.x, xcd = g & 7, slot = g >> 3;
+  const int64_t per = tsp::ceil_div(nnzb, 8);
+  const int64_t kb = xcd * per + slot;
+  if (slot >= per || kb >= nnzb) return;
+  const int64_t i = brow[kb], j = ci[kb];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w & 1, wn = w >> 1, h = lane >> 5, l32 = lane & 31;
+  const i32x4 rsg = tsp::dma::make_rsrc(G, (uint32_t)(m * ldg * 2));
+  const i32x4 rsb = tsp::dma::make_rsrc(B, (uint32_t)(n * ldb * 2));
+  const uint32_t lds0 = tsp::dma::lds_addr(lds);
+  auto issue = [&](int s) {
+    const uint32_t st = lds0 + (s % bfb::NST) * bfb::STAGE;
+    bfb::dma_row(rsg, i * BS, ldg, (int64_t)s * bfb::KC, ncols, st, w, lane);
+    bfb::dma_row(rsb, j * BS, ldb, (int64_t)s * bfb::KC, ncols, st + bfb::TILE, w, lane);
+  };
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) acc[t][u] = f32x16{};
+  bfb::run<true, true>(issue, (int)tsp::ceil_div(ncols, bfb::KC), lds, acc, wm, wn, lane);
+  // dA block kb, row-major: lane holds column l32 and rows 8 (v / 4) + 4 h + v % 4
+  uint16_t* ob = out + kb * (BS * BS);
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = wm * 64 + 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
+        ob[r * BS + wn * 64 + 32 * u + l32] = tsp::f32_to_bf16_bits(acc[t][u][v]);
+      }
+}
+
+// dB = A^T dC, bf16: workgroup per (block column, 128-column tile) in the
+// forward's schedule, walking the column's blocks.
+__global__ __launch_bounds__(256) void bsr_spmm_t_bf16_mfma(
+    const uint16_t* __restrict__ blocks, const int64_t* __restrict__ cp, const int64_t* __restrict__ cbid,
+    const int64_t* __restrict__ crow, int64_t nbc, int nt, const uint16_t* __restrict__ X, int64_t ldx, int64_t m,
+    int64_t ncols, uint16_t* __restrict__ out, int64_t ldo, int64_t n, const int32_t* __restrict__ order) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[bfb::NST * bfb::STAGE];
+  int64_t col;
+  int ntile;
+  if (!T32::tile_item(blockIdx.x, nbc, nt, order, col, ntile)) return;
+  const int64_t n0 = (int64_t)ntile * BS;
+  const int64_t start = cp[col];
+  const int nblk = (int)(cp[col + 1] - start);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w & 1, wn = w >> 1, h = lane >> 5, l32 = lane & 31;
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) acc[t][u] = f32x16{};
+  if (nblk > 0) {
+    const i32x4 rsx = tsp::dma::make_rsrc(X, (uint32_t)(m * ldx * 2));
+    const uint32_t lds0 = tsp::dma::lds_addr(lds);
+    int cbase = 0, idv, rowv;
+    auto load_ids = [&](int base) {
+      const int64_t e = start + (base + lane < nblk ? base + lane : nblk - 1);
+      idv = tsp::dma::load_lo32_sync(cbid + e);
+      rowv = tsp::dma::load_lo32_sync(crow + e);
+    };
+    load_ids(0);
+    auto issue = [&](int s) {
+      const int b = s >> 1;
+      if (b - cbase >= 64) {
+        cbase = b & ~63;
+        load_ids(cbase);
+      }
+      const int64_t kb = __builtin_amdgcn_readlane(idv, b - cbase);
+      const int64_t ib = __builtin_amdgcn_readlane(rowv, b - cbase);
+      const int kk = (s & 1) * bfb::KC;
+      const uint32_t st = lds0 + (s % bfb::NST) * bfb::STAGE;
+      bfb::dma_tr_block(blocks + kb * (BS * BS) + kk * BS, st, w, lane);
+      bfb::dma_tr(rsx, ib * BS + kk, ldx, n0, st + bfb::TILE, w, lane);
+    };
+    bfb::run<false, false>(issue, nblk * (BS / bfb::KC), lds, acc, wm, wn, lane);
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int64_t r0 = col * BS + wm * 64 + 32 * t + 4 * h;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int64_t c = n0 + wn * 64 + 32 * u + l32;
+      if (c < ncols) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
+          if (r < n) out[r * ldo + c] = tsp::f32_to_bf16_bits(acc[t][u][v]);
+        }
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------ generic
 
 template <typename T> __device__ inline typename tsp::Acc<T>::type ldv(const T* p) { return (typename tsp::Acc<T>::type)*p; }
@@ -351,6 +579,15 @@ extern "C" int tsp_bsr_sddmm(const void* G, int64_t ldg, int64_t m, const void* 
                        (const float*)B, ldb, n, ncols, block_rows, block_col_indices, n_blocks, (float*)grad_blocks);
     return tsp::check_launch("bsr_sddmm_f32_dma launch");
   }
+  if (dtype == TSP_BF16 && block_size == BS && ncols % 8 == 0 && ldg % 8 == 0 && ldb % 8 == 0 && aligned16(G) &&
+      aligned16(B) && (m + BS) * ldg * 2 <= (int64_t)UINT32_MAX - 64 && (n + BS) * ldb * 2 <= (int64_t)UINT32_MAX - 64) {
+    const int64_t grid = tsp::ceil_div(n_blocks, 8) * 8;
+    if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_sddmm: too many blocks");
+    hipLaunchKernelGGL(bsr_sddmm_bf16_mfma, dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)G, ldg, m,
+                       (const uint16_t*)B, ldb, n, ncols, block_rows, block_col_indices, n_blocks,
+                       (uint16_t*)grad_blocks);
+    return tsp::check_launch("bsr_sddmm_bf16_mfma launch");
+  }
   const int64_t total = n_blocks * block_size * block_size;
   const int64_t grid = tsp::ceil_div(total, 256);
   if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_sddmm: too large for the generic kernel");
@@ -389,6 +626,16 @@ extern "C" int tsp_bsr_spmm_t(const void* blocks, int dtype, const int64_t* col_
                        col_block_ids, col_block_rows, n_block_cols, (int)nt, (const float*)X, ldx, m, ncols, (float*)out,
                        ldo, n, col_order);
     return tsp::check_launch("bsr_spmm_t_f32_dma launch");
+  }
+  if (dtype == TSP_BF16 && block_size == BS && ldx % 8 == 0 && aligned16(X) && aligned16(blocks) &&
+      (m + BS) * ldx * 2 + 2 * BS <= (int64_t)UINT32_MAX) {
+    const int64_t nt = tsp::ceil_div(ncols, BS);
+    const int64_t grid = tsp::ceil_div(n_block_cols, 8) * 8 * nt;
+    if (grid > INT32_MAX || nt > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm_t: problem too large");
+    hipLaunchKernelGGL(bsr_spmm_t_bf16_mfma, dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)blocks, col_ptrs,
+                       col_block_ids, col_block_rows, n_block_cols, (int)nt, (const uint16_t*)X, ldx, m, ncols,
+                       (uint16_t*)out, ldo, n, col_order);
+    return tsp::check_launch("bsr_spmm_t_bf16_mfma launch");
   }
   const int64_t grid = tsp::ceil_div(n * ncols, 256);
   if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm_t: too large for the generic kernel");

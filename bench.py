@@ -38,6 +38,7 @@ sys.path.insert(0, str(ROOT))
 
 FP32_MFMA_PEAK_TFLOPS = 157.3
 BF16_MFMA_PEAK_TFLOPS = 2500.0
+FP64_MFMA_PEAK_TFLOPS = 78.6
 HBM_PEAK_GBS = 8000.0
 
 
@@ -199,41 +200,61 @@ def bench_bsr_bf16(steps: int, warmup: int):
 
 
 def bench_bsr_backward(steps: int, warmup: int):
-    """Backward of bsr_spmm at config 3a (fp32): the two kernels the autograd
-    backward launches, each 27.48 GFLOP — tsp_bsr_sddmm (dA on the stored
-    pattern) and tsp_bsr_spmm_t (dB = A^T dC over the block-column view)."""
+    """Backward of bsr_spmm at config 3a (fp32) and 3b (bf16): the two
+    kernels the autograd backward launches, each 27.48 GFLOP — tsp_bsr_sddmm
+    (dA on the stored pattern) and tsp_bsr_spmm_t (dB = A^T dC over the
+    block-column view)."""
     import torch
 
     from trnsparse_amd import workloads as W
     from trnsparse_amd.hip import _lib
     from trnsparse_amd.hip import dispatch as D
 
-    A, B = W.cfg3_bsr(dtype=torch.float32)
-    m, n = A.shape
-    N = B.shape[1]
-    flops = 2.0 * A.n_blocks * 128 * 128 * N
-    dev = torch.device("cuda", torch.cuda.current_device())
-    blocks, Bd = A.blocks.to(dev), B.to(dev)
-    G = torch.randn(m, N, generator=torch.Generator().manual_seed(9)).to(dev)
-    rp = A.block_row_ptrs.to(dev)
-    ci = A.block_col_indices.to(dev)
-    brow, cp, cbid, crow, corder = D._bsr_bwd_plan(rp, ci, 128, 128, dev)
-    gb = torch.empty_like(blocks)
-    dB = torch.empty(n, N, device=dev)
-    st = _lib.stream_handle(dev)
-    code = _lib.dtype_code(torch.float32)
-    sddmm = lambda: _lib.call("tsp_bsr_sddmm", G.data_ptr(), N, m, Bd.data_ptr(), N, n, N, brow.data_ptr(),
-                              ci.data_ptr(), A.n_blocks, 128, code, gb.data_ptr(), st)
-    spmm_t = lambda: _lib.call("tsp_bsr_spmm_t", blocks.data_ptr(), code, cp.data_ptr(), cbid.data_ptr(),
-                               crow.data_ptr(), 128, 128, m, n, G.data_ptr(), N, N, dB.data_ptr(), N,
-                               corder.data_ptr(), st)
     out = []
-    for name, fn in (("bsr_spmm backward dA (sddmm) cfg3a fp32", sddmm), ("bsr_spmm backward dB (A^T dC) cfg3a fp32", spmm_t)):
-        _, ms = time_gpu(fn, steps, warmup)
-        tf = flops / (ms * 1e-3) / 1e12
-        out.append({"name": name, "value": round(tf * 1e3, 1), "unit": "GFLOP/s", "us": round(ms * 1e3, 1),
-                    "frac_fp32_mfma": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)})
+    for dt, cfg, peak, key in ((torch.float32, "cfg3a fp32", FP32_MFMA_PEAK_TFLOPS, "frac_fp32_mfma"),
+                               (torch.bfloat16, "cfg3b bf16", BF16_MFMA_PEAK_TFLOPS, "frac_bf16_mfma")):
+        A, B = W.cfg3_bsr(dtype=dt)
+        m, n = A.shape
+        N = B.shape[1]
+        flops = 2.0 * A.n_blocks * 128 * 128 * N
+        dev = torch.device("cuda", torch.cuda.current_device())
+        blocks, Bd = A.blocks.to(dev), B.to(dev)
+        G = torch.randn(m, N, generator=torch.Generator().manual_seed(9)).to(dt).to(dev)
+        rp = A.block_row_ptrs.to(dev)
+        ci = A.block_col_indices.to(dev)
+        brow, cp, cbid, crow, corder = D._bsr_bwd_plan(rp, ci, 128, 128, dev)
+        gb = torch.empty_like(blocks)
+        dB = torch.empty(n, N, device=dev, dtype=dt)
+        st = _lib.stream_handle(dev)
+        code = _lib.dtype_code(dt)
+        sddmm = lambda: _lib.call("tsp_bsr_sddmm", G.data_ptr(), N, m, Bd.data_ptr(), N, n, N, brow.data_ptr(),
+                                  ci.data_ptr(), A.n_blocks, 128, code, gb.data_ptr(), st)
+        spmm_t = lambda: _lib.call("tsp_bsr_spmm_t", blocks.data_ptr(), code, cp.data_ptr(), cbid.data_ptr(),
+                                   crow.data_ptr(), 128, 128, m, n, G.data_ptr(), N, N, dB.data_ptr(), N,
+                                   corder.data_ptr(), st)
+        for name, fn in ((f"bsr_spmm backward dA (sddmm) {cfg}", sddmm), (f"bsr_spmm backward dB (A^T dC) {cfg}", spmm_t)):
+            _, ms = time_gpu(fn, steps, warmup)
+            tf = flops / (ms * 1e-3) / 1e12
+            out.append({"name": name, "value": round(tf * 1e3, 1), "unit": "GFLOP/s", "us": round(ms * 1e3, 1),
+                        key: round(tf / peak, 4)})
     return out
+
+
+def bench_bsr_f64(steps: int, warmup: int):
+    """bsr_spmm on config 3a's pattern and sizes in fp64 (bsr_spmm_f64_dma)."""
+    import torch
+
+    import trnsparse_amd as ts
+    from trnsparse_amd import workloads as W
+
+    A, B = W.cfg3_bsr(dtype=torch.float64)
+    flops = 2.0 * A.n_blocks * 128 * 128 * B.shape[1]
+    Ad = ts.BSRMatrix(A.blocks.cuda(), A.block_col_indices, A.block_row_ptrs, A.shape, A.block_size)
+    Bd = B.cuda()
+    _, ms = time_gpu(lambda: ts.bsr_spmm(Ad, Bd), steps, warmup)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"name": "bsr_spmm cfg3a pattern fp64", "value": round(tf * 1e3, 1), "unit": "GFLOP/s",
+            "us": round(ms * 1e3, 1), "frac_fp64_mfma": round(tf / FP64_MFMA_PEAK_TFLOPS, 4)}
 
 
 def bench_bsr_spmv(steps: int, warmup: int, cpu: bool = False):
@@ -405,7 +426,13 @@ def bench_attention(steps: int, warmup: int, cpu: bool = False):
         secs = cb.time_call(lambda: cb.attention_head(Q[0], K[0], V[0], ptr, col, b, D**-0.5), reps=2, budget_s=20.0)
         res["cpu_baseline"] = {"value": round(flops / H / secs / 1e9, 2), "unit": "GFLOP/s", "cores": cb.threads(),
                                "kind": "port", "sample": "one head of cfg5 (bf16) through the reference's torch two-pass loops"}
-    return res
+    # the same workload with fp32 Q / K / V (bsa_fwd_f32_mfma)
+    Qf, Kf, Vf = (t.float() for t in (Qd, Kd, Vd))
+    _, ms32 = time_gpu(lambda: ts.block_sparse_attention_tiled(Qf, Kf, Vf, mask), steps, warmup)
+    tf32 = flops / (ms32 * 1e-3) / 1e12
+    res32 = {"name": "block_sparse_attention cfg5 32x8192x128 fp32", "value": round(tf32 * 1e3, 1), "unit": "GFLOP/s",
+             "us": round(ms32 * 1e3, 1), "frac_fp32_mfma": round(tf32 / FP32_MFMA_PEAK_TFLOPS, 4)}
+    return [res, res32]
 
 
 def bench_attention_backward(steps: int, warmup: int, cpu: bool = False):
@@ -425,24 +452,32 @@ def bench_attention_backward(steps: int, warmup: int, cpu: bool = False):
     H, S, D = Q.shape
     flops = 10.0 * mask.n_blocks * 128 * 128 * D * H
     dev = torch.device("cuda", torch.cuda.current_device())
-    Qd, Kd, Vd = Q.to(dev), K.to(dev), V.to(dev)
-    dO = torch.randn(Q.shape, generator=torch.Generator().manual_seed(14)).to(torch.bfloat16).to(dev)
-    O, rm, rd = Dp.hip_block_sparse_attention(Qd, Kd, Vd, mask, D**-0.5, return_stats=True)
     rp, ci, _ = Dp._bsr_plan(mask.block_col_indices, mask.block_row_ptrs, S // 128, dev, holder=mask)
     cp, crow, nbc, plan, (ni, ns, npart) = Dp._attn_bwd_plan(mask, H, S, dev)
-    dQ, dK, dV = (torch.empty_like(Qd) for _ in range(3))
-    ws = torch.empty(_lib.load().tsp_bsa_bwd_workspace_size(H, S, npart), dtype=torch.uint8, device=dev)
     st = _lib.stream_handle(dev)
-    code = _lib.dtype_code(torch.bfloat16)
-    call = lambda: _lib.call("tsp_bsa_bwd", Qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), O.data_ptr(), dO.data_ptr(),
-                             code, H, S, D, rp.data_ptr(), ci.data_ptr(), cp.data_ptr(), crow.data_ptr(), nbc, 128,
-                             D**-0.5, rm.data_ptr(), rd.data_ptr(), dQ.data_ptr(), dK.data_ptr(), dV.data_ptr(),
-                             plan.data_ptr(), ni, ns, npart, ws.data_ptr(), st)
-    _, ms = time_gpu(call, steps, warmup)
-    tf = flops / (ms * 1e-3) / 1e12
-    res = {"name": "block_sparse_attention backward cfg5 32x8192x128 bf16", "value": round(tf * 1e3, 1),
-           "unit": "GFLOP/s", "us": round(ms * 1e3, 1), "frac_bf16_mfma": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
-           "split_columns": ns, "items": ni}
+    ws = torch.empty(_lib.load().tsp_bsa_bwd_workspace_size(H, S, npart), dtype=torch.uint8, device=dev)
+    out = []
+    for dt in (torch.bfloat16, torch.float32):
+        Qd, Kd, Vd = Q.to(dt).to(dev), K.to(dt).to(dev), V.to(dt).to(dev)
+        dO = torch.randn(Q.shape, generator=torch.Generator().manual_seed(14)).to(torch.bfloat16).to(dt).to(dev)
+        O, rm, rd = Dp.hip_block_sparse_attention(Qd, Kd, Vd, mask, D**-0.5, return_stats=True)
+        dQ, dK, dV = (torch.empty_like(Qd) for _ in range(3))
+        code = _lib.dtype_code(dt)
+        call = lambda: _lib.call("tsp_bsa_bwd", Qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), O.data_ptr(), dO.data_ptr(),
+                                 code, H, S, D, rp.data_ptr(), ci.data_ptr(), cp.data_ptr(), crow.data_ptr(), nbc, 128,
+                                 D**-0.5, rm.data_ptr(), rd.data_ptr(), dQ.data_ptr(), dK.data_ptr(), dV.data_ptr(),
+                                 plan.data_ptr(), ni, ns, npart, ws.data_ptr(), st)
+        _, ms = time_gpu(call, steps, warmup)
+        tf = flops / (ms * 1e-3) / 1e12
+        peak, key, tag = ((BF16_MFMA_PEAK_TFLOPS, "frac_bf16_mfma", "bf16") if dt == torch.bfloat16 else
+                          (FP32_MFMA_PEAK_TFLOPS, "frac_fp32_mfma", "fp32"))
+        out.append({"name": f"block_sparse_attention backward cfg5 32x8192x128 {tag}", "value": round(tf * 1e3, 1),
+                    "unit": "GFLOP/s", "us": round(ms * 1e3, 1), key: round(tf / peak, 4),
+                    "split_columns": ns, "items": ni})
+        if dt == torch.bfloat16:
+            keep = (Qd, Kd, Vd, O, dO, rm, rd)
+    res = out[0]
+    Qd, Kd, Vd, O, dO, rm, rd = keep
     if cpu:
         from oracle import cpu_baseline as cb
 
@@ -453,7 +488,7 @@ def bench_attention_backward(steps: int, warmup: int, cpu: bool = False):
         res["cpu_baseline"] = {"value": round(flops / H / secs / 1e9, 2), "unit": "GFLOP/s", "cores": cb.threads(),
                                "kind": "port",
                                "sample": "one head of cfg5 (bf16) through the reference's torch backward loops"}
-    return res
+    return out
 
 
 def bench_formats(steps: int, warmup: int, cpu: bool = False):
@@ -646,6 +681,7 @@ def main(argv=None) -> int:
             ("spmv poisson int32", lambda: bench_spmv("poisson", 32, 20, 3)),
             ("spmv zipf int64", lambda: bench_spmv("zipf", 64, 10, 2)),
             ("bsr bf16", lambda: bench_bsr_bf16(max(5, args.steps // 2), 3)),
+            ("bsr f64", lambda: bench_bsr_f64(10, 2)),
             ("bsr backward", lambda: bench_bsr_backward(10, 2)),
             ("screened", lambda: bench_screened(10, 2, cpu=not args.no_cpu)),
             ("attention", lambda: bench_attention(10, 2, cpu=not args.no_cpu)),

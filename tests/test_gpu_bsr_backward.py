@@ -54,6 +54,10 @@ def _check(A: ts.BSRMatrix, B: torch.Tensor, G: torch.Tensor, tol: float):
         ((300, 260), 128, 12, 1.0, torch.float32),     # unaligned m, n (padded blocks)
         ((300, 260), 128, 10, 1.0, torch.float32),     # N % 4 != 0: generic kernels
         ((40, 40), 8, 12, 0.4, torch.float64),         # any block size, fp64
+        ((256, 384), 128, 64, 0.5, torch.float64),     # fp64 MFMA kernels
+        ((384, 256), 128, 200, 0.6, torch.float64),    # N % 32 != 0: zero-filled k tail
+        ((300, 260), 128, 12, 1.0, torch.float64),     # unaligned m, n
+        ((300, 260), 128, 11, 1.0, torch.float64),     # odd N: generic kernels
         ((256, 256), 128, 64, 0.5, torch.bfloat16),    # bf16 MFMA kernels
         ((512, 384), 128, 256, 0.4, torch.bfloat16),
         ((384, 256), 128, 200, 0.6, torch.bfloat16),   # N % 64 != 0: zero-filled k tail
@@ -85,7 +89,7 @@ def test_backward_empty_rows_and_columns(hip_backend):
     assert torch.count_nonzero(dB[128:256]).item() == 0  # block column 1 holds no blocks
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float64])
 def test_backward_long_block_column(hip_backend, dtype):
     """A block column with 65 stored blocks (the dB kernels read a column's
     block ids 64 at a time)."""

@@ -29,6 +29,8 @@
 //   bsr_sddmm_bf16_mfma / bsr_spmm_t_bf16_mfma   b == 128, bf16 (fp32
 //                        accumulation, bf16 results): the same two products on
 //                        v_mfma_f32_32x32x16_bf16 (operand forms at the kernels).
+//   bsr_sddmm_f64_mfma / bsr_spmm_t_f64_mfma   b == 128, fp64: the same two
+//                        products on v_mfma_f64_16x16x4_f64.
 //   bsr_sddmm_generic / bsr_spmm_t_generic   any block size, f32 / f64 / bf16
 //                        (accumulating in f32, f64 for f64): one thread per
 //                        output element.
@@ -510,6 +512,219 @@ __global__ __launch_bounds__(256) void bsr_spmm_t_bf16_mfma(
   }
 }
 
+// ------------------------------------------------------------ fp64 MFMA
+//
+// fp64, b == 128, on v_mfma_f64_16x16x4_f64 (A[i = lane % 16][k = lane / 16],
+// B[k = lane / 16][j = lane % 16]; accumulator element v of lane l is row
+// l / 16 + 4 v, column l % 16). The fp64 forward's structure: 4 waves of 64x64
+// as 4x4 accumulators, 32-wide k-slabs of two operand tiles through a 2-stage
+// direct-load ring, k permuted so that lane group g takes k = 8g + 2p + s at
+// k-step (p, s). Operand tile forms:
+//   ROW: [128 rows][32 k], rows of 256 B: a lane's k pair is one b128 read;
+//        chunk ^ (row % 16);
+//   COL: [32 k][128 columns], rows of 1 KiB: one b64 read per k-step;
+//        chunk ^ 8 ((k / 8) % 2).
+// dA (SDDMM): both operands ROW; dB = A^T dC: both COL.
+namespace f64b {
+constexpr int KC = 32;
+constexpr int NST = 2;
+constexpr int TILE = 32768;
+constexpr int STAGE = 2 * TILE;
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
+
+// ROW tile: rows [row0, row0 + 128) x columns [k0, k0 + 32) of a row-major
+// fp64 matrix (stride ld) behind rs; columns at or past kend read as zero
+// (kend even).
+__device__ inline void dma_row(i32x4 rs, int64_t row0, int64_t ld, int64_t k0, int64_t kend, uint32_t dst, int w,
+                               int lane) {
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int i = 8 * w + q;
+    const int r = 4 * i + (lane >> 4);
+    const int c = (lane & 15) ^ (r & 15);
+    const int64_t col = k0 + 2 * c;
+    const uint32_t off = col < kend ? (uint32_t)(((row0 + r) * ld + col) * 8) : OOB;
+    tsp::dma::buffer16(rs, off, dst + i * 1024);
+  }
+}
+// COL tile: rows [row0, row0 + 32) x columns [c0, c0 + 128) behind rs.
+__device__ inline void dma_col(i32x4 rs, int64_t row0, int64_t ld, int64_t c0, uint32_t dst, int w, int lane) {
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int j = 8 * w + q;
+    const int c = lane ^ (8 * ((j >> 3) & 1));
+    tsp::dma::buffer16(rs, (uint32_t)(((row0 + j) * ld + c0 + 2 * c) * 8), dst + j * 1024);
+  }
+}
+// The same COL tile from a 128-column block (always in bounds).
+__device__ inline void dma_col_block(const double* src, uint32_t dst, int w, int lane) {
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int j = 8 * w + q;
+    const int c = lane ^ (8 * ((j >> 3) & 1));
+    tsp::dma::global16(src + j * BS + 2 * c, dst + j * 1024);
+  }
+}
+
+// Operand values of k-steps (p, 0) and (p, 1) for tile rows / columns
+// base + 16 t + lane % 16, t = 0..3: v[t][s].
+template <bool ROWF>
+__device__ inline void fetch(const uint8_t* tile, int base, int p, int lane, double (&v)[4][2]) {
+  const int g = lane >> 4, l16 = lane & 15;
+  if (ROWF) {
+    const uint8_t* a = tile + (base + l16) * 256 + (((4 * g + p) ^ l16) * 16);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const f64x2 x = *(const f64x2*)(a + 16 * t * 256);
+      v[t][0] = x[0];
+      v[t][1] = x[1];
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int col = base + 16 * t + l16;
+      const int off = (((col >> 1) ^ (8 * (g & 1))) * 16) + (col & 1) * 8;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) v[t][s] = *(const double*)(tile + (8 * g + 2 * p + s) * 1024 + off);
+    }
+  }
+}
+
+template <bool AROW, bool BROW, typename Issue>
+__device__ inline void run(Issue&& issue, int nsteps, const uint8_t* lds, f64x4 (&acc)[4][4], int wm, int wn,
+                           int lane) {
+  struct Ops {
+    double a[4][2], b[4][2];
+  };
+  auto get = [&](const uint8_t* st, int p, Ops& o) {
+    fetch<AROW>(st, wm * 64, p, lane, o.a);
+    fetch<BROW>(st + TILE, wn * 64, p, lane, o.b);
+  };
+  if (nsteps > 0) issue(0);
+  for (int s = 0; s < nsteps; ++s) {
+    tsp::dma::wait_vm<0>();  // this wave's loads of slab s are done
+    tsp::dma::barrier();     // every wave's part is in LDS; stage (s + 1) % NST is free
+    if (s + 1 < nsteps) issue(s + 1);
+    const uint8_t* st = lds + (s % NST) * STAGE;
+    Ops o[2];
+    get(st, 0, o[0]);
+#pragma unroll
+    for (int p = 0; p < KC / 8; ++p) {
+      if (p + 1 < KC / 8) get(st, p + 1, o[(p + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            acc[t][u] = __builtin_amdgcn_mfma_f64_16x16x4f64(o[p & 1].a[t][k], o[p & 1].b[u][k], acc[t][u], 0, 0, 0);
+    }
+  }
+}
+}  // namespace f64b
+
+// dA (SDDMM), fp64: workgroup per stored block, XCD x takes a contiguous
+// range of blocks as in bsr_sddmm_f32_dma.
+__global__ __launch_bounds__(256) void bsr_sddmm_f64_mfma(const double* __restrict__ G, int64_t ldg, int64_t m,
+                                                          const double* __restrict__ B, int64_t ldb, int64_t n,
+                                                          int64_t ncols, const int64_t* __restrict__ brow,
+                                                          const int64_t* __restrict__ ci, int64_t nnzb,
+                                                          double* __restrict__ out) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[f64b::NST * f64b::STAGE];
+  const int64_t g = blockIdx.x, xcd = g & 7, slot = g >> 3;
+  const int64_t per = tsp::ceil_div(nnzb, 8);
+  const int64_t kb = xcd * per + slot;
+  if (slot >= per || kb >= nnzb) return;
+  const int64_t i = brow[kb], j = ci[kb];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w & 1, wn = w >> 1, gq = lane >> 4, l16 = lane & 15;
+  const i32x4 rsg = tsp::dma::make_rsrc(G, (uint32_t)(m * ldg * 8));
+  const i32x4 rsb = tsp::dma::make_rsrc(B, (uint32_t)(n * ldb * 8));
+  const uint32_t lds0 = tsp::dma::lds_addr(lds);
+  auto issue = [&](int s) {
+    const uint32_t st = lds0 + (s % f64b::NST) * f64b::STAGE;
+    f64b::dma_row(rsg, i * BS, ldg, (int64_t)s * f64b::KC, ncols, st, w, lane);
+    f64b::dma_row(rsb, j * BS, ldb, (int64_t)s * f64b::KC, ncols, st + f64b::TILE, w, lane);
+  };
+  f64b::f64x4 acc[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[t][u] = f64b::f64x4{};
+  f64b::run<true, true>(issue, (int)tsp::ceil_div(ncols, f64b::KC), lds, acc, wm, wn, lane);
+  double* ob = out + kb * (BS * BS);
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        ob[(wm * 64 + 16 * t + gq + 4 * v) * BS + wn * 64 + 16 * u + l16] = acc[t][u][v];
+}
+
+// dB = A^T dC, fp64: workgroup per (block column, 128-column tile) in the
+// forward's schedule, walking the column's blocks.
+__global__ __launch_bounds__(256) void bsr_spmm_t_f64_mfma(
+    const double* __restrict__ blocks, const int64_t* __restrict__ cp, const int64_t* __restrict__ cbid,
+    const int64_t* __restrict__ crow, int64_t nbc, int nt, const double* __restrict__ X, int64_t ldx, int64_t m,
+    int64_t ncols, double* __restrict__ out, int64_t ldo, int64_t n, const int32_t* __restrict__ order) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[f64b::NST * f64b::STAGE];
+  int64_t col;
+  int ntile;
+  if (!T32::tile_item(blockIdx.x, nbc, nt, order, col, ntile)) return;
+  const int64_t n0 = (int64_t)ntile * BS;
+  const int64_t start = cp[col];
+  const int nblk = (int)(cp[col + 1] - start);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w & 1, wn = w >> 1, gq = lane >> 4, l16 = lane & 15;
+  f64b::f64x4 acc[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[t][u] = f64b::f64x4{};
+  if (nblk > 0) {
+    constexpr int SPB = BS / f64b::KC;
+    const i32x4 rsx = tsp::dma::make_rsrc(X, (uint32_t)(m * ldx * 8));
+    const uint32_t lds0 = tsp::dma::lds_addr(lds);
+    int cbase = 0, idv, rowv;
+    auto load_ids = [&](int base) {
+      const int64_t e = start + (base + lane < nblk ? base + lane : nblk - 1);
+      idv = tsp::dma::load_lo32_sync(cbid + e);
+      rowv = tsp::dma::load_lo32_sync(crow + e);
+    };
+    load_ids(0);
+    auto issue = [&](int s) {
+      const int b = s / SPB;
+      if (b - cbase >= 64) {
+        cbase = b & ~63;
+        load_ids(cbase);
+      }
+      const int64_t kb = __builtin_amdgcn_readlane(idv, b - cbase);
+      const int64_t ib = __builtin_amdgcn_readlane(rowv, b - cbase);
+      const int kk = (s % SPB) * f64b::KC;
+      const uint32_t st = lds0 + (s % f64b::NST) * f64b::STAGE;
+      f64b::dma_col_block(blocks + kb * (BS * BS) + kk * BS, st, w, lane);
+      f64b::dma_col(rsx, ib * BS + kk, ldx, n0, st + f64b::TILE, w, lane);
+    };
+    f64b::run<false, false>(issue, nblk * SPB, lds, acc, wm, wn, lane);
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t c = n0 + wn * 64 + 16 * u + l16;
+      if (c < ncols) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int64_t r = col * BS + wm * 64 + 16 * t + gq + 4 * v;
+          if (r < n) out[r * ldo + c] = acc[t][u][v];
+        }
+      }
+    }
+}
+
 // ------------------------------------------------------------ generic
 
 template <typename T> __device__ inline typename tsp::Acc<T>::type ldv(const T* p) { return (typename tsp::Acc<T>::type)*p; }
@@ -588,6 +803,14 @@ extern "C" int tsp_bsr_sddmm(const void* G, int64_t ldg, int64_t m, const void* 
                        (uint16_t*)grad_blocks);
     return tsp::check_launch("bsr_sddmm_bf16_mfma launch");
   }
+  if (dtype == TSP_F64 && block_size == BS && ncols % 2 == 0 && ldg % 2 == 0 && ldb % 2 == 0 && aligned16(G) &&
+      aligned16(B) && (m + BS) * ldg * 8 <= (int64_t)UINT32_MAX - 64 && (n + BS) * ldb * 8 <= (int64_t)UINT32_MAX - 64) {
+    const int64_t grid = tsp::ceil_div(n_blocks, 8) * 8;
+    if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_sddmm: too many blocks");
+    hipLaunchKernelGGL(bsr_sddmm_f64_mfma, dim3((unsigned)grid), dim3(256), 0, st, (const double*)G, ldg, m,
+                       (const double*)B, ldb, n, ncols, block_rows, block_col_indices, n_blocks, (double*)grad_blocks);
+    return tsp::check_launch("bsr_sddmm_f64_mfma launch");
+  }
   const int64_t total = n_blocks * block_size * block_size;
   const int64_t grid = tsp::ceil_div(total, 256);
   if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_sddmm: too large for the generic kernel");
@@ -636,6 +859,16 @@ extern "C" int tsp_bsr_spmm_t(const void* blocks, int dtype, const int64_t* col_
                        col_block_ids, col_block_rows, n_block_cols, (int)nt, (const uint16_t*)X, ldx, m, ncols,
                        (uint16_t*)out, ldo, n, col_order);
     return tsp::check_launch("bsr_spmm_t_bf16_mfma launch");
+  }
+  if (dtype == TSP_F64 && block_size == BS && ldx % 2 == 0 && aligned16(X) && aligned16(blocks) &&
+      (m + BS) * ldx * 8 + 8 * BS <= (int64_t)UINT32_MAX) {
+    const int64_t nt = tsp::ceil_div(ncols, BS);
+    const int64_t grid = tsp::ceil_div(n_block_cols, 8) * 8 * nt;
+    if (grid > INT32_MAX || nt > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm_t: problem too large");
+    hipLaunchKernelGGL(bsr_spmm_t_f64_mfma, dim3((unsigned)grid), dim3(256), 0, st, (const double*)blocks, col_ptrs,
+                       col_block_ids, col_block_rows, n_block_cols, (int)nt, (const double*)X, ldx, m, ncols,
+                       (double*)out, ldo, n, col_order);
+    return tsp::check_launch("bsr_spmm_t_f64_mfma launch");
   }
   const int64_t grid = tsp::ceil_div(n * ncols, 256);
   if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm_t: too large for the generic kernel");

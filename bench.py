@@ -358,6 +358,31 @@ def bench_spmv(dist: str, index_bits: int, steps: int, warmup: int, cpu: bool = 
     return res
 
 
+def bench_spmm(steps: int, warmup: int):
+    """CSR SpMM (spmm) with config 2's matrix (poisson rows, int64 indices)
+    and dense B of N = 8 and 64 columns. Reported as GFLOP/s (2 nnz N) and as
+    the bytes the kernel requests: the stream (values, indices, row offsets),
+    one B row slice per nonzero and the output — B rows are re-read from
+    cache, so this is a request rate, not HBM traffic."""
+    import torch
+
+    import trnsparse_amd as ts
+    from trnsparse_amd import workloads as W
+
+    v, c, p, _, shape = W.cfg2_csr()
+    m, n = shape
+    nnz = len(v)
+    A = W.csr_matrix_from_arrays(v, c, p, shape, device="cuda")
+    out = []
+    for N in (8, 64):
+        B = torch.randn(n, N, generator=torch.Generator().manual_seed(N)).cuda()
+        _, ms = time_gpu(lambda: ts.spmm(A, B), steps, warmup)
+        req = nnz * 12 + (m + 1) * 8 + nnz * N * 4 + m * N * 4
+        out.append({"name": f"csr_spmm cfg2 poisson int64, B {n}x{N} fp32", "value": round(2.0 * nnz * N / (ms * 1e-3) / 1e9, 1),
+                    "unit": "GFLOP/s", "us": round(ms * 1e3, 1), "requested_GBps": round(req / (ms * 1e-3) / 1e9, 1)})
+    return out
+
+
 def bench_screened(steps: int, warmup: int, cpu: bool = False):
     """screened_spmm at config 4 (n=4096, threshold 1e-20): GFLOP/s counting
     the 128x128 A tiles that are not fully screened, and dense-equivalent."""
@@ -680,6 +705,7 @@ def main(argv=None) -> int:
             ("spmv poisson int64", lambda: bench_spmv("poisson", 64, 20, 3, cpu=not args.no_cpu)),
             ("spmv poisson int32", lambda: bench_spmv("poisson", 32, 20, 3)),
             ("spmv zipf int64", lambda: bench_spmv("zipf", 64, 10, 2)),
+            ("spmm", lambda: bench_spmm(10, 2)),
             ("bsr bf16", lambda: bench_bsr_bf16(max(5, args.steps // 2), 3)),
             ("bsr f64", lambda: bench_bsr_f64(10, 2)),
             ("bsr backward", lambda: bench_bsr_backward(10, 2)),

@@ -98,6 +98,24 @@ def test_spmm_reference_grid(hip_backend, M, K, N, density):
     assert ref.scaled_error(got.numpy(), exact, scale) <= TOL
 
 
+@pytest.mark.parametrize("N", [4, 8, 12, 16, 20, 32, 60, 64, 100, 128, 132, 260])
+@pytest.mark.parametrize("index_dtype", [np.int64, np.int32])
+def test_spmm_narrow_b(hip_backend, N, index_dtype):
+    """fp32 B with a multiple of 4 columns runs the narrow kernel (several
+    rows per wavefront, a row's nonzeros split over lane groups, 128-column
+    passes): rows of 0..300 nonzeros, alpha and beta with C."""
+    lens = list(np.random.default_rng(N).poisson(12, 3000).clip(0, 300)) + [0, 300, 1, 97]
+    A = _csr_from_lengths(lens, 2000, seed=N, index_dtype=index_dtype)
+    g = torch.Generator().manual_seed(N)
+    B = torch.randn(2000, N, generator=g)
+    C = torch.randn(len(lens), N, generator=g)
+    got = ts.spmm(A, B.cuda(), alpha=0.5, C=C.cuda(), beta=-2.0).cpu()
+    v, c, p, sh = _np(A)
+    exact = 0.5 * ref.csr_spmm(v, c, p, sh, B.numpy()) - 2.0 * C.numpy()
+    scale = 0.5 * ref.csr_spmm(v, c, p, sh, B.numpy(), absolute=True) + 2.0 * np.abs(C.numpy())
+    assert ref.scaled_error(got.numpy(), exact, scale) <= TOL
+
+
 # ---------------------------------------------------- partition edge cases
 
 

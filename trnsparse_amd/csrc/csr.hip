@@ -25,7 +25,9 @@
 //
 // SpMM: one wavefront per row, lanes across the columns of B (coalesced B
 // row reads), the row's (col, value) pairs loaded 64 at a time and broadcast
-// with shuffles.
+// with shuffles. fp32 B with a multiple of 4 columns takes the narrow
+// variant: several rows per wavefront, each row's nonzeros split over lane
+// groups, 16-byte B loads, 128-column passes.
 #include "common.h"
 
 namespace {
@@ -203,6 +205,95 @@ __global__ __launch_bounds__(256) void csr_spmm_kernel(
   }
 }
 
+// SpMM for fp32 B with ncols % 4 == 0 and 16-byte aligned rows: lanes =
+// (row slot, nonzero group, column quad). P lanes cover up to 128 columns
+// of a row as column quads (P a power of two; wider B takes several column
+// passes, each a work item of its own), G lane groups
+// take every G-th nonzero of the row, and R = 64 / (P G) rows run side by
+// side in a wavefront, so narrow B still fills the wavefront and every B
+// access is a 16-byte load. U nonzeros per group are fetched before their B
+// rows are loaded (U independent gathers in flight per lane). The groups'
+// float4 partial sums are added with xor shuffles at the end of the rows.
+template <typename IdxT, int P, int G>
+__global__ __launch_bounds__(256) void csr_spmm_narrow_kernel(
+    const float* __restrict__ vals, const IdxT* __restrict__ cols, const IdxT* __restrict__ ptr, int64_t m,
+    const float* __restrict__ B, int64_t ldb, int64_t ncols, float alpha, const float* __restrict__ Cin,
+    int64_t ldci, float beta, float* __restrict__ out, int64_t ldo) {
+  constexpr int R = 64 / (P * G);
+  constexpr int U = 4;
+  const int lane = threadIdx.x & 63;
+  const int cq = lane % P, gi = (lane / P) % G, rs = lane / (P * G);
+  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x / 64);
+  for (int64_t rc = wave; rc < tsp::ceil_div(m, R) * tsp::ceil_div(ncols, 4 * P); rc += nwaves) {
+    // item rc: rows r0 .. r0 + R, columns c0 .. c0 + 4P (wider B takes several column passes)
+    const int64_t npass = tsp::ceil_div(ncols, 4 * P);
+    const int64_t r0 = (rc / npass) * R, c0 = (rc % npass) * 4 * P + 4 * cq;
+    const bool cvalid = c0 < ncols;
+    const int64_t r = r0 + rs;
+    int64_t a = 0, e = 0;
+    if (r < m) {
+      a = (int64_t)ptr[r];
+      e = (int64_t)ptr[r + 1];
+    }
+    f32x4 acc = f32x4{};
+    for (int64_t j0 = a + gi; j0 < e; j0 += (int64_t)G * U) {
+      int64_t cj[U];
+      float vj[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t j = j0 + (int64_t)u * G;
+        cj[u] = j < e ? (int64_t)cols[j] : -1;
+        vj[u] = j < e ? vals[j] : 0.f;
+      }
+      f32x4 bv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        bv[u] = (cj[u] >= 0 && cvalid) ? *(const f32x4*)(B + cj[u] * ldb + c0) : f32x4{};
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc += vj[u] * bv[u];
+    }
+#pragma unroll
+    for (int o = P; o < P * G; o <<= 1) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] += __shfl_xor(acc[i], o, 64);
+    }
+    if (gi == 0 && r < m && cvalid) {
+      f32x4 res = alpha * acc;
+      if (Cin) res = res + beta * *(const f32x4*)(Cin + r * ldci + c0);
+      *(f32x4*)(out + r * ldo + c0) = res;
+    }
+  }
+}
+
+template <typename IdxT>
+int spmm_narrow_launch(const void* values, const void* col, const void* rp, int64_t m, const void* B, int64_t ldb,
+                       int64_t ncols, double alpha, const void* C, int64_t ldc, double beta, void* out, int64_t ldo,
+                       hipStream_t st) {
+  const float* cc = (C && beta != 0.0) ? (const float*)C : nullptr;
+  const int64_t quads = ncols / 4;
+  int P = 1;
+  while (P < quads && P < 32) P <<= 1;
+  const int G = P >= 16 ? 64 / P : 8;
+  const int64_t R = 64 / (P * G);
+  int64_t grid = tsp::ceil_div(tsp::ceil_div(m, R) * tsp::ceil_div(ncols, 4 * P), 4);
+  if (grid > 65536) grid = 65536;
+#define TSP_NARROW(PP, GG)                                                                                          \
+  hipLaunchKernelGGL((csr_spmm_narrow_kernel<IdxT, PP, GG>), dim3((unsigned)grid), dim3(256), 0, st,                \
+                     (const float*)values, (const IdxT*)col, (const IdxT*)rp, m, (const float*)B, ldb, ncols,       \
+                     (float)alpha, cc, ldc, (float)beta, (float*)out, ldo)
+  switch (P) {
+    case 1: TSP_NARROW(1, 8); break;
+    case 2: TSP_NARROW(2, 8); break;
+    case 4: TSP_NARROW(4, 8); break;
+    case 8: TSP_NARROW(8, 8); break;
+    case 16: TSP_NARROW(16, 4); break;
+    default: TSP_NARROW(32, 2); break;
+  }
+#undef TSP_NARROW
+  return tsp::check_launch("csr_spmm_narrow launch");
+}
+
 template <typename IdxT>
 int plan_launch(const void* row_ptrs, int64_t m, int64_t nwin, int64_t* win, hipStream_t st) {
   const int64_t grid = tsp::ceil_div(m + 1, 256);
@@ -295,6 +386,12 @@ extern "C" int tsp_csr_spmm(const void* values, int dtype, const void* col_indic
   if (!row_ptrs || !out || (nnz > 0 && (!values || !col_indices || !B)))
     return tsp::fail(TSP_EINVAL, "tsp_csr_spmm: null pointer");
   hipStream_t st = (hipStream_t)stream;
+  const bool a16 = ((uintptr_t)B % 16) == 0 && ((uintptr_t)out % 16) == 0 &&
+                   (!(C && beta != 0.0) || (((uintptr_t)C % 16) == 0 && ldc % 4 == 0));
+  if (dtype == TSP_F32 && ncols % 4 == 0 && ldb % 4 == 0 && ldo % 4 == 0 && a16)
+    return index_type == TSP_I64
+               ? spmm_narrow_launch<int64_t>(values, col_indices, row_ptrs, m, B, ldb, ncols, alpha, C, ldc, beta, out, ldo, st)
+               : spmm_narrow_launch<int32_t>(values, col_indices, row_ptrs, m, B, ldb, ncols, alpha, C, ldc, beta, out, ldo, st);
   if (index_type == TSP_I64)
     return dtype == TSP_F32 ? spmm_launch<int64_t, float>(values, col_indices, row_ptrs, m, B, ldb, ncols, alpha, C, ldc, beta, out, ldo, st)
                             : spmm_launch<int64_t, double>(values, col_indices, row_ptrs, m, B, ldb, ncols, alpha, C, ldc, beta, out, ldo, st);

@@ -174,6 +174,17 @@ int tsp_csr_spmm(const void* values, int dtype, const void* col_indices,
                  double alpha, const void* C, int64_t ldc, double beta,
                  void* out, int64_t ldo, void* stream);
 
+/* Values gradient of out = alpha * A @ X on A's own pattern (the reference's
+ * autograd for spmm, trnsparse/nki/dispatch.py:174-178, forms
+ * grad_out @ B^T densely and projects it onto the pattern):
+ *   out_values[p] = alpha * sum_c G[row p][c] * X[col p][c],
+ * G (m, ncols; stride ldg), X (n, ncols; stride ldx); ncols = 1 with unit
+ * strides for the SpMV case. No values argument: only the pattern is read. */
+int tsp_csr_sddmm(const void* col_indices, const void* row_ptrs, int index_type,
+                  int64_t m, int64_t n, int64_t nnz, const void* G, int64_t ldg,
+                  const void* X, int64_t ldx, int64_t ncols, int dtype,
+                  double alpha, void* out_values, void* stream);
+
 /* ======================================================================
  * Schwarz-screened dense SpMM:  C = (A * mask) @ B
  *   Q = sqrt(|diag|), mask[i,k] = Q[i]*Q[k] > threshold_sqrt, evaluated in

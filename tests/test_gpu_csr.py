@@ -116,6 +116,35 @@ def test_spmm_narrow_b(hip_backend, N, index_dtype):
     assert ref.scaled_error(got.numpy(), exact, scale) <= TOL
 
 
+@pytest.mark.parametrize("N", [0, 1, 3, 8, 64, 130])
+@pytest.mark.parametrize("index_dtype", [np.int64, np.int32])
+def test_csr_matmul_backward_on_device(hip_backend, N, index_dtype):
+    """Autograd of alpha * A @ X on the device (N = 0: the SpMV form): the
+    values gradient through tsp_csr_sddmm, dX through the device transpose
+    and SpMV / SpMM, both against float64 closed forms."""
+    lens = list(np.random.default_rng(5).poisson(6, 400).clip(0, 50)) + [0, 120]
+    A = _csr_from_lengths(lens, 300, seed=9, index_dtype=index_dtype)
+    g = torch.Generator().manual_seed(N)
+    vals = A.values.cuda().requires_grad_(True)
+    X = (torch.randn(300, N, generator=g) if N else torch.randn(300, generator=g)).cuda().requires_grad_(True)
+    Ad = ts.CSRMatrix(vals, A.col_indices.cuda(), A.row_ptrs.cuda(), A.shape)
+    out = ts.spmm(Ad, X, alpha=1.5) if N else ts.spmv(Ad, X, alpha=1.5)
+    G = torch.randn(out.shape, generator=g).cuda()
+    out.backward(G)
+    v, c, p, _ = _np(A)
+    rows = np.repeat(np.arange(len(lens)), np.diff(p))
+    Gn = G.double().cpu().numpy().reshape(len(lens), -1)
+    Xn = X.detach().double().cpu().numpy().reshape(300, -1)
+    exact_v = 1.5 * (Gn[rows] * Xn[c]).sum(axis=1)
+    scale_v = 1.5 * (np.abs(Gn[rows]) * np.abs(Xn[c])).sum(axis=1)
+    assert ref.scaled_error(vals.grad.double().cpu().numpy(), exact_v, scale_v) <= TOL
+    exact_x = np.zeros_like(Xn)
+    scale_x = np.zeros_like(Xn)
+    np.add.at(exact_x, c, 1.5 * v[:, None].astype(np.float64) * Gn[rows])
+    np.add.at(scale_x, c, 1.5 * np.abs(v[:, None].astype(np.float64) * Gn[rows]))
+    assert ref.scaled_error(X.grad.double().cpu().numpy().reshape(300, -1), exact_x, scale_x) <= TOL
+
+
 # ---------------------------------------------------- partition edge cases
 
 

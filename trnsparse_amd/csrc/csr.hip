@@ -23,6 +23,9 @@
 //   3. a last row longer than the LDS capacity is reduced by the whole
 //      workgroup (skewed / Zipf rows), wavefront shuffles + LDS across waves.
 //
+// SDDMM (values gradient of A X, tsp_csr_sddmm): per nonzero the dot product
+// of G's row and X's row over the dense columns, lanes as in the narrow SpMM.
+//
 // SpMM: one wavefront per row, lanes across the columns of B (coalesced B
 // row reads), the row's (col, value) pairs loaded 64 at a time and broadcast
 // with shuffles. fp32 B with a multiple of 4 columns takes the narrow
@@ -294,6 +297,114 @@ int spmm_narrow_launch(const void* values, const void* col, const void* rp, int6
   return tsp::check_launch("csr_spmm_narrow launch");
 }
 
+// CSR SDDMM on the matrix's own pattern (the values gradient of alpha A X):
+// dv[p] = alpha * sum_c G[row p][c] * X[col p][c] over ncols columns. Lanes as
+// in csr_spmm_narrow_kernel: P lanes per nonzero read V consecutive columns
+// each (P V columns per pass, more passes for wider operands), G groups take
+// every G-th nonzero of a row (U at a time), R rows per wavefront; the P
+// partial dot products of a nonzero are summed with xor shuffles within its
+// P lanes, which share every loop trip.
+template <typename T, int V>
+struct VecOf {
+  typedef T type __attribute__((ext_vector_type(V)));
+  __device__ static T hsum(type v) {
+    T s = v[0];
+#pragma unroll
+    for (int i = 1; i < V; ++i) s += v[i];
+    return s;
+  }
+};
+template <typename T>
+struct VecOf<T, 1> {
+  typedef T type;
+  __device__ static T hsum(T v) { return v; }
+};
+
+template <typename IdxT, typename T, int V, int P, int G>
+__global__ __launch_bounds__(256) void csr_sddmm_kernel(const IdxT* __restrict__ cols, const IdxT* __restrict__ ptr,
+                                                        int64_t m, const T* __restrict__ Gm, int64_t ldg,
+                                                        const T* __restrict__ X, int64_t ldx, int64_t ncols, T alpha,
+                                                        T* __restrict__ dv) {
+  constexpr int R = 64 / (P * G);
+  constexpr int U = 4;
+  typedef VecOf<T, V> VT;
+  typedef typename VT::type vt;
+  const int lane = threadIdx.x & 63;
+  const int cq = lane % P, gi = (lane / P) % G, rs = lane / (P * G);
+  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x / 64);
+  for (int64_t rc = wave; rc < tsp::ceil_div(m, R); rc += nwaves) {
+    const int64_t r = rc * R + rs;
+    int64_t a = 0, e = 0;
+    if (r < m) {
+      a = (int64_t)ptr[r];
+      e = (int64_t)ptr[r + 1];
+    }
+    for (int64_t j0 = a + gi; j0 < e; j0 += (int64_t)G * U) {
+      int64_t cj[U];
+      T dot[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t j = j0 + (int64_t)u * G;
+        cj[u] = j < e ? (int64_t)cols[j] : -1;
+        dot[u] = 0;
+      }
+      for (int64_t c0 = (int64_t)V * cq; c0 < ncols; c0 += (int64_t)V * P) {
+        const vt gv = *(const vt*)(Gm + r * ldg + c0);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (cj[u] >= 0) dot[u] += VT::hsum(gv * *(const vt*)(X + cj[u] * ldx + c0));
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int o = 1; o < P; o <<= 1) dot[u] += __shfl_xor(dot[u], o, 64);
+      if (cq == 0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int64_t j = j0 + (int64_t)u * G;
+          if (j < e) dv[j] = alpha * dot[u];
+        }
+      }
+    }
+  }
+}
+
+template <typename IdxT, typename T, int V>
+int sddmm_launch_v(const void* col, const void* rp, int64_t m, const void* Gm, int64_t ldg, const void* X, int64_t ldx,
+                   int64_t ncols, double alpha, void* dv, hipStream_t st) {
+  const int64_t units = tsp::ceil_div(ncols, V);
+  int P = 1;
+  while (P < units && P < 32) P <<= 1;
+  const int G = P >= 16 ? 64 / P : 8;
+  const int64_t R = 64 / (P * G);
+  int64_t grid = tsp::ceil_div(tsp::ceil_div(m, R), 4);
+  if (grid > 65536) grid = 65536;
+#define TSP_SDDMM(PP, GG)                                                                                           \
+  hipLaunchKernelGGL((csr_sddmm_kernel<IdxT, T, V, PP, GG>), dim3((unsigned)grid), dim3(256), 0, st,                \
+                     (const IdxT*)col, (const IdxT*)rp, m, (const T*)Gm, ldg, (const T*)X, ldx, ncols, (T)alpha,   \
+                     (T*)dv)
+  switch (P) {
+    case 1: TSP_SDDMM(1, 8); break;
+    case 2: TSP_SDDMM(2, 8); break;
+    case 4: TSP_SDDMM(4, 8); break;
+    case 8: TSP_SDDMM(8, 8); break;
+    case 16: TSP_SDDMM(16, 4); break;
+    default: TSP_SDDMM(32, 2); break;
+  }
+#undef TSP_SDDMM
+  return tsp::check_launch("csr_sddmm launch");
+}
+
+template <typename IdxT, typename T>
+int sddmm_launch(const void* col, const void* rp, int64_t m, const void* Gm, int64_t ldg, const void* X, int64_t ldx,
+                 int64_t ncols, double alpha, void* dv, hipStream_t st) {
+  constexpr int VW = 16 / (int)sizeof(T);
+  if (ncols % VW == 0 && ldg % VW == 0 && ldx % VW == 0 && ((uintptr_t)Gm % 16) == 0 && ((uintptr_t)X % 16) == 0)
+    return sddmm_launch_v<IdxT, T, VW>(col, rp, m, Gm, ldg, X, ldx, ncols, alpha, dv, st);
+  return sddmm_launch_v<IdxT, T, 1>(col, rp, m, Gm, ldg, X, ldx, ncols, alpha, dv, st);
+}
+
 template <typename IdxT>
 int plan_launch(const void* row_ptrs, int64_t m, int64_t nwin, int64_t* win, hipStream_t st) {
   const int64_t grid = tsp::ceil_div(m + 1, 256);
@@ -397,4 +508,25 @@ extern "C" int tsp_csr_spmm(const void* values, int dtype, const void* col_indic
                             : spmm_launch<int64_t, double>(values, col_indices, row_ptrs, m, B, ldb, ncols, alpha, C, ldc, beta, out, ldo, st);
   return dtype == TSP_F32 ? spmm_launch<int32_t, float>(values, col_indices, row_ptrs, m, B, ldb, ncols, alpha, C, ldc, beta, out, ldo, st)
                           : spmm_launch<int32_t, double>(values, col_indices, row_ptrs, m, B, ldb, ncols, alpha, C, ldc, beta, out, ldo, st);
+}
+
+extern "C" int tsp_csr_sddmm(const void* col_indices, const void* row_ptrs, int index_type, int64_t m, int64_t n,
+                             int64_t nnz, const void* G, int64_t ldg, const void* X, int64_t ldx, int64_t ncols,
+                             int dtype, double alpha, void* out_values, void* stream) {
+  int st0 = check_types("tsp_csr_sddmm", dtype, index_type);
+  if (st0) return st0;
+  if (m < 0 || n < 0 || nnz < 0 || ncols < 0) return tsp::fail(TSP_EINVAL, "tsp_csr_sddmm: negative size");
+  if (ldg < ncols || ldx < ncols) return tsp::fail(TSP_EINVAL, "tsp_csr_sddmm: leading dimension < ncols");
+  if (nnz == 0 || m == 0) return TSP_OK;
+  if (!col_indices || !row_ptrs || !out_values || (ncols > 0 && (!G || !X)))
+    return tsp::fail(TSP_EINVAL, "tsp_csr_sddmm: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  if (ncols == 0) {  // empty dot products
+    return tsp::zero_fill(out_values, nnz * (dtype == TSP_F64 ? 8 : 4), st);
+  }
+  if (index_type == TSP_I64)
+    return dtype == TSP_F32 ? sddmm_launch<int64_t, float>(col_indices, row_ptrs, m, G, ldg, X, ldx, ncols, alpha, out_values, st)
+                            : sddmm_launch<int64_t, double>(col_indices, row_ptrs, m, G, ldg, X, ldx, ncols, alpha, out_values, st);
+  return dtype == TSP_F32 ? sddmm_launch<int32_t, float>(col_indices, row_ptrs, m, G, ldg, X, ldx, ncols, alpha, out_values, st)
+                          : sddmm_launch<int32_t, double>(col_indices, row_ptrs, m, G, ldg, X, ldx, ncols, alpha, out_values, st);
 }

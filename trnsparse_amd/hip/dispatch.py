@@ -298,12 +298,21 @@ def _csr_forward(vals, cols, ptrs, win, shape, X, alpha, Y, beta, dev):
     return out
 
 
+def _csr_plan(ptrs: torch.Tensor, m: int, nnz: int, dev: torch.device) -> torch.Tensor:
+    """SpMV work-partition table of a device CSR pattern."""
+    size = _lib.load().tsp_csr_plan_size(m, nnz)
+    win = torch.empty(size, dtype=torch.int64, device=dev)
+    _lib.call("tsp_csr_plan", ptrs.data_ptr(), _lib.index_code(ptrs.dtype), m, nnz, win.data_ptr(), _lib.stream_handle(dev))
+    return win
+
+
 class _CSRMatMulFunction(torch.autograd.Function):
     """alpha * A @ X (+ beta * Y) for CSR A and dense X (vector or matrix).
 
-    Forward: the gfx950 SpMV / SpMM kernels. Backward (torch ops):
-      d values[p] = alpha * <dOut[row p], X[col p]>   (pattern fixed)
-      dX          = alpha * A^T @ dOut,   dY = beta * dOut
+    Forward: the gfx950 SpMV / SpMM kernels. Backward, on the device:
+      d values[p] = alpha * <dOut[row p], X[col p]>   (tsp_csr_sddmm, pattern fixed)
+      dX          = alpha * A^T @ dOut                (tsp_csr_transpose, then SpMV / SpMM)
+      dY          = beta * dOut
     """
 
     @staticmethod
@@ -323,20 +332,27 @@ class _CSRMatMulFunction(torch.autograd.Function):
         cols, ptrs = ctx.pattern
         dev = cols.device
         m, n = ctx.shape
-        gd = g.to(dev)
-        Xd = X.to(dev)
-        rows = torch.repeat_interleave(torch.arange(m, device=dev), (ptrs[1:] - ptrs[:-1]).long())
-        c = cols.long()
+        vdt = values.dtype
+        gd = g.to(dev, vdt).contiguous()
+        Xd = X.to(dev, vdt).contiguous()
+        nnz = cols.numel()
+        st = _lib.stream_handle(dev)
         gv = gx = gy = None
-        g2 = gd if gd.dim() == 2 else gd.unsqueeze(1)
-        X2 = Xd if Xd.dim() == 2 else Xd.unsqueeze(1)
-        if ctx.needs_input_grad[0]:
-            gv = (ctx.alpha * (g2[rows] * X2[c]).sum(dim=1)).to(values.device, values.dtype)
-        if ctx.needs_input_grad[4]:
-            vd = values.to(dev)
-            contrib = ctx.alpha * vd.unsqueeze(1) * g2[rows]
-            gx2 = torch.zeros(n, X2.shape[1], dtype=contrib.dtype, device=dev).index_add_(0, c, contrib)
-            gx = (gx2 if Xd.dim() == 2 else gx2.squeeze(1)).to(X.device, X.dtype)
+        with torch.cuda.device(dev):
+            if ctx.needs_input_grad[0]:
+                ncols = gd.shape[1] if gd.dim() == 2 else 1
+                gvd = torch.empty(nnz, dtype=vdt, device=dev)
+                _lib.call("tsp_csr_sddmm", cols.data_ptr(), ptrs.data_ptr(), _lib.index_code(cols.dtype), m, n, nnz,
+                          gd.data_ptr(), ncols, Xd.data_ptr(), ncols, ncols, _lib.dtype_code(vdt), float(ctx.alpha),
+                          gvd.data_ptr(), st)
+                gv = gvd.to(values.device)
+            if ctx.needs_input_grad[4]:
+                from . import formats as hf
+
+                tv, tc, tp = hf.csr_transpose(values.to(dev).contiguous(), cols, ptrs, (m, n))
+                win = _csr_plan(tp, n, nnz, dev) if gd.dim() == 1 else None
+                gxd = _csr_forward(tv, tc, tp, win, (n, m), gd, ctx.alpha, None, 0.0, dev)
+                gx = gxd.to(X.device, X.dtype)
         if ctx.needs_input_grad[6] and ctx.has_y:
             ydev, ydt, yshape = ctx.y_meta
             gy = (ctx.beta * gd).sum_to_size(yshape).to(ydev, ydt)

@@ -529,9 +529,17 @@ def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, 
 
     Q/K/V/O/dO (S, D) or (..., S, D) sharing one mask; row_max / row_denom
     as hip_block_sparse_attention returns them. Returns (dQ, dK, dV).
+
+    bf16 with 128-blocks and head_dim 64 runs on the fp32 MFMA kernels: the
+    operands are widened on the device (exact) and the gradients rounded to
+    bf16 once at the end; the bf16 MFMA kernels serve head_dim 128.
     """
     if not (Q.shape == K.shape == V.shape == O.shape == dO.shape):
         raise RuntimeError("Q, K, V, O, dO shapes differ")
+    if Q.dtype == torch.bfloat16 and Q.shape[-1] == 64 and mask_bsr.block_size == 128 and scale > 0:
+        grads = hip_block_sparse_attention_backward(*(t.float() for t in (Q, K, V, O, dO)), mask_bsr, scale,
+                                                    row_max, row_denom)
+        return tuple(gr.to(torch.bfloat16) for gr in grads)
     dt = Q.dtype
     code = _lib.dtype_code(dt)
     lead = Q.shape[:-2]

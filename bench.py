@@ -417,7 +417,13 @@ def bench_screened(steps: int, warmup: int, cpu: bool = False):
         secs = cb.time_call(lambda: cb.screened_spmm(A, diag, B, thr), reps=3, budget_s=20.0)
         res["cpu_baseline"] = {"value": round(flops / secs / 1e9, 2), "unit": "GFLOP/s", "cores": cb.threads(),
                                "kind": "port", "sample": "full cfg4 through the reference's torch path (mask, A*mask, MKL sgemm)"}
-    return res
+    # the same workload with fp64 A, diag and B (screened_f64_dma)
+    A64, d64, B64 = Ad.double(), dd.double(), Bd.double()
+    _, ms64 = time_gpu(lambda: ts.screened_spmm(A64, d64, B64, thr), max(2, steps // 2), warmup)
+    tf64 = flops / (ms64 * 1e-3) / 1e12
+    res64 = {"name": "screened_spmm cfg4 n=4096 fp64", "value": round(tf64 * 1e3, 1), "unit": "GFLOP/s",
+             "us": round(ms64 * 1e3, 1), "frac_fp64_mfma": round(tf64 / FP64_MFMA_PEAK_TFLOPS, 4)}
+    return [res, res64]
 
 
 def bench_attention(steps: int, warmup: int, cpu: bool = False):

@@ -117,9 +117,41 @@ def test_tile_skip_structured(hip_backend):
     _check(A, diag, B, 1e-12, got)
 
 
+@pytest.mark.parametrize("n,N,threshold,diag_dtype", [
+    (256, 64, 0.3, torch.float64), (300, 200, 1e-6, torch.float64), (512, 128, 1e-12, torch.float32),
+    (128, 8, 0.0, torch.float64),
+])
+def test_f64_mfma(hip_backend, n, N, threshold, diag_dtype):
+    """fp64 A and B (even n) run screened_f64_dma: against the float64 oracle
+    at 1e-12 of the dot-product scale; rows 128..255 (when present) have tiny
+    Q, so their tile pairs are skipped."""
+    g = torch.Generator().manual_seed(n + N)
+    diag = (torch.rand(n, generator=g, dtype=torch.float64) + 0.1).to(diag_dtype)
+    if n >= 256:
+        diag[128:256] = 1e-30
+    A = torch.randn(n, n, generator=g, dtype=torch.float64)
+    B = torch.randn(n, N, generator=g, dtype=torch.float64)
+    got = ts.screened_spmm(A.cuda(), diag.cuda(), B.cuda(), threshold=threshold).cpu()
+    assert got.dtype == torch.float64
+    mask = ref.screened_mask(diag.numpy(), threshold)
+    Am = np.where(mask, A.numpy(), 0.0)
+    err = ref.scaled_error(got.numpy(), Am @ B.numpy(), np.abs(Am) @ np.abs(B.numpy()))
+    assert err <= 1e-12, err
+
+
+def test_f64_mfma_mask_exact(hip_backend):
+    """(ones * mask) @ I in fp64 reproduces the mask exactly."""
+    n = 256
+    rng = np.random.default_rng(8)
+    diag = torch.from_numpy(10.0 ** rng.uniform(-16, 0, n))
+    got = ts.screened_spmm(torch.ones(n, n, dtype=torch.float64).cuda(), diag.cuda(),
+                           torch.eye(n, dtype=torch.float64).cuda(), threshold=1e-10).cpu().numpy()
+    assert np.array_equal(got, ref.screened_mask(diag.numpy(), 1e-10).astype(np.float64))
+
+
 def test_f64_generic_and_gradcheck(hip_backend):
     torch.manual_seed(7)
-    n = 40
+    n = 41  # odd: the generic kernel
     A = torch.randn(n, n, dtype=torch.float64, device="cuda", requires_grad=True)
     diag = (torch.abs(torch.randn(n, dtype=torch.float64)) * 4.0 + 0.01).cuda()
     B = torch.randn(n, 5, dtype=torch.float64, device="cuda", requires_grad=True)

@@ -38,6 +38,7 @@
 
 #include "lds_dma.h"
 #include "mfma_f32.h"
+#include "mfma_f64.h"
 
 namespace {
 
@@ -514,92 +515,25 @@ __global__ __launch_bounds__(256) void bsr_spmm_t_bf16_mfma(
 
 // ------------------------------------------------------------ fp64 MFMA
 //
-// fp64, b == 128, on v_mfma_f64_16x16x4_f64 (A[i = lane % 16][k = lane / 16],
-// B[k = lane / 16][j = lane % 16]; accumulator element v of lane l is row
-// l / 16 + 4 v, column l % 16). The fp64 forward's structure: 4 waves of 64x64
-// as 4x4 accumulators, 32-wide k-slabs of two operand tiles through a 2-stage
-// direct-load ring, k permuted so that lane group g takes k = 8g + 2p + s at
-// k-step (p, s). Operand tile forms:
-//   ROW: [128 rows][32 k], rows of 256 B: a lane's k pair is one b128 read;
-//        chunk ^ (row % 16);
-//   COL: [32 k][128 columns], rows of 1 KiB: one b64 read per k-step;
-//        chunk ^ 8 ((k / 8) % 2).
-// dA (SDDMM): both operands ROW; dB = A^T dC: both COL.
+// fp64, b == 128, on v_mfma_f64_16x16x4_f64 with the operand tiles of
+// mfma_f64.h: 4 waves of 64x64, 32-wide k-slabs of two operand tiles through
+// a 2-stage direct-load ring. dA (SDDMM): both operands ROW; dB = A^T dC:
+// both COL.
+namespace F64 = tsp::f64tile;
 namespace f64b {
-constexpr int KC = 32;
+namespace F = tsp::f64tile;
 constexpr int NST = 2;
-constexpr int TILE = 32768;
-constexpr int STAGE = 2 * TILE;
-typedef double f64x4 __attribute__((ext_vector_type(4)));
-typedef double f64x2 __attribute__((ext_vector_type(2)));
-
-// ROW tile: rows [row0, row0 + 128) x columns [k0, k0 + 32) of a row-major
-// fp64 matrix (stride ld) behind rs; columns at or past kend read as zero
-// (kend even).
-__device__ inline void dma_row(i32x4 rs, int64_t row0, int64_t ld, int64_t k0, int64_t kend, uint32_t dst, int w,
-                               int lane) {
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int i = 8 * w + q;
-    const int r = 4 * i + (lane >> 4);
-    const int c = (lane & 15) ^ (r & 15);
-    const int64_t col = k0 + 2 * c;
-    const uint32_t off = col < kend ? (uint32_t)(((row0 + r) * ld + col) * 8) : OOB;
-    tsp::dma::buffer16(rs, off, dst + i * 1024);
-  }
-}
-// COL tile: rows [row0, row0 + 32) x columns [c0, c0 + 128) behind rs.
-__device__ inline void dma_col(i32x4 rs, int64_t row0, int64_t ld, int64_t c0, uint32_t dst, int w, int lane) {
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int j = 8 * w + q;
-    const int c = lane ^ (8 * ((j >> 3) & 1));
-    tsp::dma::buffer16(rs, (uint32_t)(((row0 + j) * ld + c0 + 2 * c) * 8), dst + j * 1024);
-  }
-}
-// The same COL tile from a 128-column block (always in bounds).
-__device__ inline void dma_col_block(const double* src, uint32_t dst, int w, int lane) {
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int j = 8 * w + q;
-    const int c = lane ^ (8 * ((j >> 3) & 1));
-    tsp::dma::global16(src + j * BS + 2 * c, dst + j * 1024);
-  }
-}
-
-// Operand values of k-steps (p, 0) and (p, 1) for tile rows / columns
-// base + 16 t + lane % 16, t = 0..3: v[t][s].
-template <bool ROWF>
-__device__ inline void fetch(const uint8_t* tile, int base, int p, int lane, double (&v)[4][2]) {
-  const int g = lane >> 4, l16 = lane & 15;
-  if (ROWF) {
-    const uint8_t* a = tile + (base + l16) * 256 + (((4 * g + p) ^ l16) * 16);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const f64x2 x = *(const f64x2*)(a + 16 * t * 256);
-      v[t][0] = x[0];
-      v[t][1] = x[1];
-    }
-  } else {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int col = base + 16 * t + l16;
-      const int off = (((col >> 1) ^ (8 * (g & 1))) * 16) + (col & 1) * 8;
-#pragma unroll
-      for (int s = 0; s < 2; ++s) v[t][s] = *(const double*)(tile + (8 * g + 2 * p + s) * 1024 + off);
-    }
-  }
-}
+constexpr int STAGE = 2 * F::TILE;
 
 template <bool AROW, bool BROW, typename Issue>
-__device__ inline void run(Issue&& issue, int nsteps, const uint8_t* lds, f64x4 (&acc)[4][4], int wm, int wn,
+__device__ inline void run(Issue&& issue, int nsteps, const uint8_t* lds, F::f64x4 (&acc)[4][4], int wm, int wn,
                            int lane) {
   struct Ops {
     double a[4][2], b[4][2];
   };
   auto get = [&](const uint8_t* st, int p, Ops& o) {
-    fetch<AROW>(st, wm * 64, p, lane, o.a);
-    fetch<BROW>(st + TILE, wn * 64, p, lane, o.b);
+    F::fetch<AROW>(st, wm * 64, p, lane, o.a);
+    F::fetch<BROW>(st + F::TILE, wn * 64, p, lane, o.b);
   };
   if (nsteps > 0) issue(0);
   for (int s = 0; s < nsteps; ++s) {
@@ -610,16 +544,10 @@ __device__ inline void run(Issue&& issue, int nsteps, const uint8_t* lds, f64x4 
     Ops o[2];
     get(st, 0, o[0]);
 #pragma unroll
-    for (int p = 0; p < KC / 8; ++p) {
-      if (p + 1 < KC / 8) get(st, p + 1, o[(p + 1) & 1]);
+    for (int p = 0; p < F::KC / 8; ++p) {
+      if (p + 1 < F::KC / 8) get(st, p + 1, o[(p + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int k = 0; k < 2; ++k)
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int u = 0; u < 4; ++u)
-            acc[t][u] = __builtin_amdgcn_mfma_f64_16x16x4f64(o[p & 1].a[t][k], o[p & 1].b[u][k], acc[t][u], 0, 0, 0);
+      F::mma(o[p & 1].a, o[p & 1].b, acc);
     }
   }
 }
@@ -645,15 +573,15 @@ __global__ __launch_bounds__(256) void bsr_sddmm_f64_mfma(const double* __restri
   const uint32_t lds0 = tsp::dma::lds_addr(lds);
   auto issue = [&](int s) {
     const uint32_t st = lds0 + (s % f64b::NST) * f64b::STAGE;
-    f64b::dma_row(rsg, i * BS, ldg, (int64_t)s * f64b::KC, ncols, st, w, lane);
-    f64b::dma_row(rsb, j * BS, ldb, (int64_t)s * f64b::KC, ncols, st + f64b::TILE, w, lane);
+    F64::dma_row(rsg, i * BS, ldg, (int64_t)s * F64::KC, ncols, st, w, lane);
+    F64::dma_row(rsb, j * BS, ldb, (int64_t)s * F64::KC, ncols, st + F64::TILE, w, lane);
   };
-  f64b::f64x4 acc[4][4];
+  F64::f64x4 acc[4][4];
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc[t][u] = f64b::f64x4{};
-  f64b::run<true, true>(issue, (int)tsp::ceil_div(ncols, f64b::KC), lds, acc, wm, wn, lane);
+    for (int u = 0; u < 4; ++u) acc[t][u] = F64::f64x4{};
+  f64b::run<true, true>(issue, (int)tsp::ceil_div(ncols, F64::KC), lds, acc, wm, wn, lane);
   double* ob = out + kb * (BS * BS);
 #pragma unroll
   for (int t = 0; t < 4; ++t)
@@ -679,13 +607,13 @@ __global__ __launch_bounds__(256) void bsr_spmm_t_f64_mfma(
   const int nblk = (int)(cp[col + 1] - start);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wm = w & 1, wn = w >> 1, gq = lane >> 4, l16 = lane & 15;
-  f64b::f64x4 acc[4][4];
+  F64::f64x4 acc[4][4];
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc[t][u] = f64b::f64x4{};
+    for (int u = 0; u < 4; ++u) acc[t][u] = F64::f64x4{};
   if (nblk > 0) {
-    constexpr int SPB = BS / f64b::KC;
+    constexpr int SPB = BS / F64::KC;
     const i32x4 rsx = tsp::dma::make_rsrc(X, (uint32_t)(m * ldx * 8));
     const uint32_t lds0 = tsp::dma::lds_addr(lds);
     int cbase = 0, idv, rowv;
@@ -703,10 +631,10 @@ __global__ __launch_bounds__(256) void bsr_spmm_t_f64_mfma(
       }
       const int64_t kb = __builtin_amdgcn_readlane(idv, b - cbase);
       const int64_t ib = __builtin_amdgcn_readlane(rowv, b - cbase);
-      const int kk = (s % SPB) * f64b::KC;
+      const int kk = (s % SPB) * F64::KC;
       const uint32_t st = lds0 + (s % f64b::NST) * f64b::STAGE;
-      f64b::dma_col_block(blocks + kb * (BS * BS) + kk * BS, st, w, lane);
-      f64b::dma_col(rsx, ib * BS + kk, ldx, n0, st + f64b::TILE, w, lane);
+      F64::dma_col_block(blocks + kb * (BS * BS) + kk * BS, st, w, lane);
+      F64::dma_col(rsx, ib * BS + kk, ldx, n0, st + F64::TILE, w, lane);
     };
     f64b::run<false, false>(issue, nblk * SPB, lds, acc, wm, wn, lane);
   }

@@ -24,9 +24,12 @@
 //                       their LDS read; the K loop visits active k-tiles.
 //   screened_f32_mfma   the register-staged variant on the shared MFMA core
 //                       (mfma_f32.h), for operands past 4 GiB.
-//   screened_generic    f64 or unaligned operands: one thread per output.
+//   screened_f64_dma    fp64 (even m and strides): the same structure on
+//                       v_mfma_f64_16x16x4_f64 (mfma_f64.h operand tiles).
+//   screened_generic    other or unaligned operands: one thread per output.
 #include "lds_dma.h"
 #include "mfma_f32.h"
+#include "mfma_f64.h"
 
 namespace {
 
@@ -297,6 +300,112 @@ __global__ __launch_bounds__(256) void screened_f32_dma(
   }
 }
 
+// screened_f64_dma<QT>: fp64 A and B on v_mfma_f64_16x16x4_f64 with the
+// operand tiles of mfma_f64.h (4 waves of 64x64; A as a ROW tile [128][32]
+// of the C tile's rows, B as a COL tile [32][128]; 32-wide k-slabs through a
+// 2-stage direct-load ring, four per active k tile; A columns and B rows at
+// or past m read as zero). As in the fp32 kernel the mask multiplies the A
+// fragments after their LDS read, with Q_k of each slab staged in LDS.
+template <typename QT>
+__global__ __launch_bounds__(256) void screened_f64_dma(
+    const double* __restrict__ A, int64_t lda, const QT* __restrict__ Q, const QT* __restrict__ qmax, QT thr,
+    int64_t m, const double* __restrict__ B, int64_t ldb, int64_t ncols, double* __restrict__ C, int64_t ldc, int nmt,
+    int nnt) {
+  namespace F = tsp::f64tile;
+  constexpr int STAGE = 2 * F::TILE;
+  constexpr int SPT = TILE / F::KC;  // slabs per k tile
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
+  __shared__ __attribute__((aligned(16))) QT qs[2][F::KC];
+  int64_t mt64;
+  int ntile;
+  if (!T32::tile_item(blockIdx.x, nmt, nnt, nullptr, mt64, ntile)) return;
+  const int mt = (int)mt64;
+  const int64_t row0 = (int64_t)mt * TILE, n0 = (int64_t)ntile * TILE;
+  const QT qI = qmax[mt];
+  const int nkt = (int)tsp::ceil_div(m, TILE);
+  auto active = [&](int t) { return qI * qmax[t] > thr; };
+  int nact = 0;
+  for (int t = 0; t < nkt; ++t) nact += active(t) ? 1 : 0;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w & 1, wn = w >> 1, g = lane >> 4, l16 = lane & 15;
+  F::f64x4 acc[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[t][u] = F::f64x4{};
+
+  if (nact > 0) {
+    const tsp::dma::i32x4 rsa = tsp::dma::make_rsrc(A, (uint32_t)(m * lda * 8));
+    const tsp::dma::i32x4 rsb = tsp::dma::make_rsrc(B, (uint32_t)(m * ldb * 8));
+    const uint32_t lds0 = tsp::dma::lds_addr(lds);
+    QT qrow[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int64_t r = row0 + wm * 64 + 16 * t + l16;
+      qrow[t] = r < m ? Q[r] : (QT)0;
+    }
+    int kt_issue = -1;  // k tile of the slabs being issued (advanced in order)
+    QT qnext = 0;
+    auto issue = [&](int s) {
+      if ((s % SPT) == 0) {
+        ++kt_issue;
+        while (!active(kt_issue)) ++kt_issue;
+      }
+      const int64_t k0 = (int64_t)kt_issue * TILE + (s % SPT) * F::KC;
+      const uint32_t st = lds0 + (s & 1) * STAGE;
+      F::dma_row(rsa, row0, lda, k0, m, st, w, lane);
+      F::dma_col(rsb, k0, ldb, n0, st + F::TILE, w, lane);
+      if (w == 0 && lane < F::KC) qnext = k0 + lane < m ? Q[k0 + lane] : (QT)0;  // into qs before its barrier
+    };
+    const int nsteps = nact * SPT;
+    issue(0);
+    if (w == 0 && lane < F::KC) qs[0][lane] = qnext;
+    for (int s = 0; s < nsteps; ++s) {
+      tsp::dma::wait_vm<0>();  // this wave's loads of slab s are done
+      tsp::dma::barrier();     // slab s and its Q_k are visible; stage (s+1) % 2 is free
+      if (s + 1 < nsteps) issue(s + 1);
+      const uint8_t* st = lds + (s & 1) * STAGE;
+      const QT* qk = qs[s & 1];
+      struct Ops {
+        double a[4][2], b[4][2];
+      };
+      auto get = [&](int p, Ops& o) {
+        F::fetch<true>(st, wm * 64, p, lane, o.a);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const QT q = qk[8 * g + 2 * p + k];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) o.a[t][k] *= (qrow[t] * q > thr) ? 1.0 : 0.0;
+        }
+        F::fetch<false>(st + F::TILE, wn * 64, p, lane, o.b);
+      };
+      Ops o[2];
+      get(0, o[0]);
+#pragma unroll
+      for (int p = 0; p < F::KC / 8; ++p) {
+        if (p + 1 < F::KC / 8) get(p + 1, o[(p + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        F::mma(o[p & 1].a, o[p & 1].b, acc);
+      }
+      if (w == 0 && lane < F::KC && s + 1 < nsteps) qs[(s + 1) & 1][lane] = qnext;
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t c = n0 + wn * 64 + 16 * u + l16;
+      if (c < ncols) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int64_t r = row0 + wm * 64 + 16 * t + g + 4 * v;
+          if (r < m) C[r * ldc + c] = acc[t][u][v];
+        }
+      }
+    }
+}
+
 #ifndef SCREENED_KC
 #define SCREENED_KC 32
 #endif
@@ -348,6 +457,17 @@ int launch(const void* A, int dtype, int64_t lda, const void* diag, double thr_s
                        (const QT*)Q, (const QT*)qmax, thr, m, (const float*)B, ldb, ncols, (float*)C, ldc, (int)nmt,
                        (int)nnt);
     return tsp::check_launch("screened_f32_mfma launch");
+  }
+  if (dtype == TSP_F64 && (m % 2) == 0 && (lda % 2) == 0 && (ldb % 2) == 0 && ((uintptr_t)A % 16) == 0 &&
+      ((uintptr_t)B % 16) == 0 && (m + TILE) * lda * 8 + 8 * TILE <= (int64_t)UINT32_MAX &&
+      (m + TILE) * ldb * 8 + 8 * TILE <= (int64_t)UINT32_MAX) {
+    const int64_t nnt = tsp::ceil_div(ncols, TILE);
+    const int64_t grid = tsp::ceil_div(nmt, 8) * 8 * nnt;
+    if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_screened_spmm: problem too large");
+    hipLaunchKernelGGL((screened_f64_dma<QT>), dim3((unsigned)grid), dim3(256), 0, st, (const double*)A, lda,
+                       (const QT*)Q, (const QT*)qmax, thr, m, (const double*)B, ldb, ncols, (double*)C, ldc, (int)nmt,
+                       (int)nnt);
+    return tsp::check_launch("screened_f64_dma launch");
   }
   const int64_t grid = tsp::ceil_div(m * ncols, 256);
   if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_screened_spmm: problem too large for the generic kernel");

@@ -37,6 +37,7 @@
 
 #include "lds_dma.h"
 #include "mfma_f32.h"
+#include "mfma_f64.h"
 
 namespace {
 
@@ -282,41 +283,18 @@ __global__ __launch_bounds__(256) void bsr_spmm_f32_dma(
 //
 // bsr_spmm_f64_dma: b == 128, fp64. The tile, scheduling and slab ring of
 // bsr_spmm_f32_dma with v_mfma_f64_16x16x4_f64 (64 cycles per MFMA, the
-// same cadence per slab as the fp32 kernel's 32x32x2):
-//   * 4 waves, each a 64x64 sub-tile as 4x4 independent 16x16 accumulators;
-//   * 32-wide k-slabs: A [128][32] (256-byte rows) and B [32][128] (1 KiB
-//     rows) through a 2-stage direct-to-LDS ring (128 KiB), B through a
-//     buffer resource so rows past n read as zero;
-//   * k permuted within a slab: the MFMA's k slot g (lanes 16g..16g+15)
-//     takes k = 8g + s at k-step s, so a lane's A values for two k-steps
-//     are one 16-byte read;
-//   * swizzles: A chunk ^ (row % 16) (16 rows of one read cover all banks),
-//     B chunk ^ 8*((k / 8) % 2) (the four k slots' rows, 8 apart, in
-//     different bank halves).
-namespace f64k {
-constexpr int KC = 32;
-constexpr int A_ROWB = KC * 8;        // 256
-constexpr int B_ROWB = 128 * 8;       // 1024
-constexpr int A_BYTES = 128 * A_ROWB;  // 32 KiB
-constexpr int B_BYTES = KC * B_ROWB;   // 32 KiB
-constexpr int STAGE = A_BYTES + B_BYTES;
-constexpr int NST = 2;
-typedef double f64x4 __attribute__((ext_vector_type(4)));
-typedef double f64x2 __attribute__((ext_vector_type(2)));
-}  // namespace f64k
-
+// same cadence per slab as the fp32 kernel's 32x32x2) on the operand tiles
+// of mfma_f64.h: 4 waves of 64x64 (4x4 independent 16x16 accumulators),
+// 32-wide k-slabs of A as a ROW tile [128][32] (from the block, always in
+// bounds) and B as a COL tile [32][128] (through a buffer resource, rows
+// past n read as zero) in a 2-stage direct-to-LDS ring (128 KiB).
 __global__ __launch_bounds__(256) void bsr_spmm_f64_dma(
     const double* __restrict__ blocks, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci,
     int64_t mb, int nt, int64_t m, int64_t n, const double* __restrict__ B, int64_t ldb, int64_t ncols,
     double* __restrict__ C, int64_t ldc, const int32_t* __restrict__ order) {
-  using f64k::A_ROWB;
-  using f64k::B_ROWB;
-  using f64k::A_BYTES;
-  using f64k::NST;
-  using f64k::STAGE;
-  using f64k::f64x2;
-  using f64k::f64x4;
-  constexpr int FKC = f64k::KC;
+  namespace F = tsp::f64tile;
+  constexpr int NST = 2, STAGE = 2 * F::TILE;
+  constexpr int SPB = BS / F::KC;  // slabs per block
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
   int64_t row;
   int ntile;
@@ -328,11 +306,11 @@ __global__ __launch_bounds__(256) void bsr_spmm_f64_dma(
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wm = w & 1, wn = w >> 1, g = lane >> 4, l16 = lane & 15;
 
-  f64x4 acc[4][4];
+  F::f64x4 acc[4][4];
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc[t][u] = f64x4{};
+    for (int u = 0; u < 4; ++u) acc[t][u] = F::f64x4{};
 
   if (nblk > 0) {
     const tsp::dma::i32x4 brsrc = tsp::dma::make_rsrc(B, (uint32_t)(n * ldb * 8));
@@ -350,83 +328,36 @@ __global__ __launch_bounds__(256) void bsr_spmm_f64_dma(
       }
       return __builtin_amdgcn_readlane(cv, blk - cbase);
     };
-
     // ---- loads of slab s into stage s % NST: 8 A + 8 B wave instructions
-    constexpr int SPB = BS / FKC;  // slabs per block
     auto issue = [&](int s) {
       const int blk = s / SPB;
-      const int kk = (s % SPB) * FKC;
+      const int kk = (s % SPB) * F::KC;
       const uint32_t st = lds0 + (s % NST) * STAGE;
-      const double* ablk = blocks + (start + blk) * (BS * BS) + kk;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int i = 8 * w + q;                   // A rows [4i, 4i+4)
-        const int r = 4 * i + (lane >> 4);
-        const int c = (lane & 15) ^ (r & 15);      // logical chunk held at this lane's slot
-        tsp::dma::global16(ablk + r * BS + c * 2, st + i * 1024);
-      }
-      const int64_t brow0 = (int64_t)colblk(blk) * BS + kk;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int j = 8 * w + q;                   // B slab row j, 64 chunks of 16 bytes
-        const int c = lane ^ (8 * ((j >> 3) & 1));
-        const int64_t off = ((brow0 + j) * ldb + n0 + c * 2) * 8;
-        tsp::dma::buffer16(brsrc, (uint32_t)off, st + A_BYTES + j * 1024);
-      }
+      F::dma_row_block(blocks + (start + blk) * (BS * BS) + kk, st, w, lane);
+      F::dma_col(brsrc, (int64_t)colblk(blk) * BS + kk, ldb, n0, st + F::TILE, w, lane);
     };
-
-    // per-lane LDS byte offsets. A: rows wm*64 + 16t + l16 (row % 16 == l16);
-    // a pair p of k-steps (k = 8g + 2p, 8g + 2p + 1) is logical chunk 4g + p
-    const int abase = (wm * 64 + l16) * A_ROWB;
-    // B: k rows 8g + s, columns wn*64 + 16u + l16 -> chunk (col / 2) ^ 8*(g % 2), half col % 2
-    int bcoff[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int col = wn * 64 + 16 * u + l16;
-      bcoff[u] = (((col >> 1) ^ (8 * (g & 1))) * 16) + (col & 1) * 8;
-    }
     struct Ops {
-      f64x2 a[4];     // a[t] = k-steps 2p, 2p+1 of row tile t
-      double b[2][4]; // b[s][u]
+      double a[4][2], b[4][2];
     };
-    auto fetch = [&](const uint8_t* st, int p, Ops& o) {
-      const uint8_t* As = st + abase + (((4 * g + p) ^ l16) * 16);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) o.a[t] = *(const f64x2*)(As + 16 * t * A_ROWB);
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const uint8_t* Bs = st + A_BYTES + (8 * g + 2 * p + s2) * B_ROWB;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) o.b[s2][u] = *(const double*)(Bs + bcoff[u]);
-      }
+    auto get = [&](const uint8_t* st, int p, Ops& o) {
+      F::fetch<true>(st, wm * 64, p, lane, o.a);
+      F::fetch<false>(st + F::TILE, wn * 64, p, lane, o.b);
     };
-    auto mma = [&](const Ops& o) {
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int u = 0; u < 4; ++u)
-            acc[t][u] = __builtin_amdgcn_mfma_f64_16x16x4f64(o.a[t][s2], o.b[s2][u], acc[t][u], 0, 0, 0);
-    };
-    auto compute = [&](const uint8_t* st) {
-      Ops o[2];
-      fetch(st, 0, o[0]);
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        if (p + 1 < 4) fetch(st, p + 1, o[(p + 1) & 1]);
-        __builtin_amdgcn_sched_barrier(0);
-        mma(o[p & 1]);
-      }
-    };
-
     const int nsteps = nblk * SPB;
     issue(0);
     for (int s = 0; s < nsteps; ++s) {
       tsp::dma::wait_vm<0>();  // this wave's loads of slab s are done
       tsp::dma::barrier();     // every wave's part is in LDS; stage (s+1) % NST is free
       if (s + 1 < nsteps) issue(s + 1);
-      compute(lds + (s % NST) * STAGE);
+      const uint8_t* st = lds + (s % NST) * STAGE;
+      Ops o[2];
+      get(st, 0, o[0]);
+#pragma unroll
+      for (int p = 0; p < F::KC / 8; ++p) {
+        if (p + 1 < F::KC / 8) get(st, p + 1, o[(p + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        F::mma(o[p & 1].a, o[p & 1].b, acc);
+      }
     }
   }
   // accumulator layout of v_mfma_f64_16x16x4_f64 (checked on the device):

@@ -1,5 +1,5 @@
-// fp64 MFMA operand tiles shared by the fp64 BSR backward and the fp64
-// screened SpMM (v_mfma_f64_16x16x4_f64: A[i = lane % 16][k = lane / 16],
+// fp64 MFMA operand tiles shared by the fp64 BSR SpMM, its backward and the
+// fp64 screened SpMM (v_mfma_f64_16x16x4_f64: A[i = lane % 16][k = lane / 16],
 // B[k = lane / 16][j = lane % 16]; accumulator element v of lane l is row
 // l / 16 + 4 v, column l % 16).
 //
@@ -40,6 +40,17 @@ __device__ inline void dma_row(dma::i32x4 rs, int64_t row0, int64_t ld, int64_t 
     const int64_t col = k0 + 2 * c;
     const uint32_t off = col < kend ? (uint32_t)(((row0 + r) * ld + col) * 8) : OOB;
     dma::buffer16(rs, off, dst + i * 1024);
+  }
+}
+// The same ROW tile from a 128x128 block (k columns [0, 32) of src, row
+// stride BS; always in bounds).
+__device__ inline void dma_row_block(const double* src, uint32_t dst, int w, int lane) {
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int i = 8 * w + q;
+    const int r = 4 * i + (lane >> 4);
+    const int c = (lane & 15) ^ (r & 15);
+    dma::global16(src + r * BS + 2 * c, dst + i * 1024);
   }
 }
 // COL tile: rows [row0, row0 + 32) x columns [c0, c0 + 128) behind rs.

@@ -61,7 +61,8 @@ def _err(got, exact, sc):
 @pytest.mark.parametrize("S,D,mask", [
     (256, 32, local_mask(2, 1)), (256, 32, dilated_mask(2, 2)), (384, 32, global_mask(3, 1, 1)),
     (256, 32, torch.ones(2, 2, dtype=torch.bool)), (256, 256, local_mask(2, 1)), (256, 256, dilated_mask(2, 2)),
-    (512, 64, local_mask(4, 2)), (512, 64, global_mask(4, 2, 2)),
+    (512, 64, local_mask(4, 2)), (512, 64, global_mask(4, 2, 2)), (384, 100, global_mask(3, 1, 1)),
+    (300, 48, local_mask(3, 1)),
 ])
 def test_fp32_reference_cases(hip_backend, S, D, mask):
     torch.manual_seed(10)

@@ -10,7 +10,8 @@ absolute form (|dS| replaced by P (|dO V^T| + |D|), operands by their
 magnitudes). fp32 <= 1e-4, bf16 <= 2e-2, fp64 <= 1e-10. fp32 with b = 128
 and d in {64, 128} runs the fp32 MFMA kernels, bf16 with d = 128 the bf16
 MFMA kernels, bf16 with d = 64 the fp32 MFMA kernels on widened operands,
-everything else the generic kernels.
+other d below 128 zero-padded to 64 or 128 first; everything else (fp64,
+d > 128, other block sizes) the generic kernels.
 """
 
 from __future__ import annotations
@@ -78,7 +79,9 @@ def _check_head(Q, K, V, dO, O, grads, mask_bsr, scale, tol, rows=None, cols=Non
         (1024, 128, global_mask(8, 1, 1), torch.bfloat16),  # MFMA, global column split into 2 segments
         (256, 64, local_mask(2, 1), torch.bfloat16),      # bf16 d = 64: widened onto the fp32 MFMA kernels
         (640, 64, W.cfg5_block_mask(5), torch.bfloat16),
-        (256, 32, local_mask(2, 1), torch.bfloat16),      # generic bf16
+        (256, 32, local_mask(2, 1), torch.bfloat16),      # head_dim zero-padded to 64
+        (256, 100, global_mask(2, 0, 1), torch.float32),  # head_dim zero-padded to 128
+        (256, 160, local_mask(2, 1), torch.bfloat16),     # generic bf16
         (512, 128, local_mask(4, 1), torch.float32),      # fp32 MFMA kernels
         (1024, 128, global_mask(8, 1, 1), torch.float32),  # fp32 MFMA, global column split into 2 segments
         (300, 128, local_mask(3, 2), torch.float32),      # fp32 MFMA, last key block crosses S

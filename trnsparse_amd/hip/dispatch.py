@@ -7,9 +7,9 @@ and the result is returned on the caller's device, as the reference's
 `_to_xla` / `.to(orig_device)` round trip does, dispatch.py:88-94),
 prepares the cached per-pattern plan, allocates outputs and calls the C ABI
 on the current HIP stream. Autograd wrappers keep the reference's
-signatures; the BSR SpMM and attention backward passes call their own
-kernels through the C ABI, the screened SpMM backward (two dense masked
-products) runs as torch ops on the device.
+signatures; the BSR SpMM, CSR matmul and attention backward passes call
+their own kernels through the C ABI, the screened SpMM backward (two dense
+masked products) runs as torch ops on the device.
 
 Kernel failures raise RuntimeError; nothing falls back to another path.
 """
@@ -440,16 +440,39 @@ def hip_screened_spmm(A, diag_integrals, B, threshold: float):
 # --------------------------------------------------------------- attention
 
 
+def _mfma_head_dim(t: torch.Tensor, block_size: int) -> int | None:
+    """The head_dim an fp32 / bf16 operand of head_dim d < 128 (not 64) is
+    zero-padded to so that the MFMA attention kernels serve it (zero columns
+    change neither the scores nor the other columns of the results); None
+    when no padding applies."""
+    d = t.shape[-1]
+    if block_size != 128 or t.dtype not in (torch.float32, torch.bfloat16) or d in (64, 128) or d >= 128 or d == 0:
+        return None
+    return 64 if d < 64 else 128
+
+
+def _pad_head_dim(t: torch.Tensor, dp: int) -> torch.Tensor:
+    return torch.nn.functional.pad(t, (0, dp - t.shape[-1]))
+
+
 def hip_block_sparse_attention(Q, K, V, mask_bsr, scale: float, return_stats: bool = False):
     """Block-sparse attention forward (replaces nki_bsr_attn_tiled, reference
     dispatch.py:580-677). Q/K/V (S, D) or (..., S, D) sharing one mask.
     Honours `scale` (the reference NKI path used head_dim**-0.5 regardless).
     Stats come back as (..., S // b, b) in float32 (float64 for float64 input).
+    fp32 / bf16 with 128-blocks and head_dim below 128 other than 64 run the
+    MFMA kernels on operands zero-padded to head_dim 64 or 128.
     """
     if not (Q.shape == K.shape == V.shape):
         raise RuntimeError(f"Q, K, V shapes differ: {tuple(Q.shape)}, {tuple(K.shape)}, {tuple(V.shape)}")
     if not (Q.dtype == K.dtype == V.dtype):
         raise RuntimeError("Q, K, V dtypes differ")
+    dp = _mfma_head_dim(Q, mask_bsr.block_size)
+    if dp is not None and scale > 0:
+        res = hip_block_sparse_attention(*(_pad_head_dim(t, dp) for t in (Q, K, V)), mask_bsr, scale, return_stats)
+        if not return_stats:
+            return res[..., : Q.shape[-1]].contiguous()
+        return (res[0][..., : Q.shape[-1]].contiguous(),) + tuple(res[1:])
     code = _lib.dtype_code(Q.dtype)
     lead = Q.shape[:-2]
     S, D = Q.shape[-2:]
@@ -532,10 +555,16 @@ def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, 
 
     bf16 with 128-blocks and head_dim 64 runs on the fp32 MFMA kernels: the
     operands are widened on the device (exact) and the gradients rounded to
-    bf16 once at the end; the bf16 MFMA kernels serve head_dim 128.
+    bf16 once at the end; the bf16 MFMA kernels serve head_dim 128. Other
+    head_dims below 128 are zero-padded to 64 or 128 first, as in the forward.
     """
     if not (Q.shape == K.shape == V.shape == O.shape == dO.shape):
         raise RuntimeError("Q, K, V, O, dO shapes differ")
+    dp = _mfma_head_dim(Q, mask_bsr.block_size)
+    if dp is not None and scale > 0:
+        grads = hip_block_sparse_attention_backward(*(_pad_head_dim(t, dp) for t in (Q, K, V, O, dO)), mask_bsr, scale,
+                                                    row_max, row_denom)
+        return tuple(gr[..., : Q.shape[-1]].contiguous() for gr in grads)
     if Q.dtype == torch.bfloat16 and Q.shape[-1] == 64 and mask_bsr.block_size == 128 and scale > 0:
         grads = hip_block_sparse_attention_backward(*(t.float() for t in (Q, K, V, O, dO)), mask_bsr, scale,
                                                     row_max, row_denom)

@@ -42,8 +42,7 @@
 #include "common.h"
 
 #include "lds_dma.h"
-
-#include <utility>
+#include "slots.h"
 
 namespace {
 
@@ -270,13 +269,6 @@ __device__ inline u16x4 bf16x4_rne(f32x4 v) {
   return __builtin_bit_cast(u16x4, __builtin_convertvector(v, bf16x4));
 }
 
-// Keep a register operand that only MFMAs read in AGPRs (MFMA takes its A
-// and B operands from either file), leaving the VGPRs to values the VALU uses.
-__device__ inline void pin_agpr(bf16x8& v) {
-  u32x4 t = __builtin_bit_cast(u32x4, v);
-  asm volatile("" : "+a"(t));
-  v = __builtin_bit_cast(bf16x8, t);
-}
 
 typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
 __device__ inline bf16x8 lds_row(uint32_t rb, int ks, uint32_t off) {
@@ -298,16 +290,6 @@ __device__ inline bf16x8 lds_trp(uint32_t tb0, uint32_t tb1, int u, uint32_t off
 // the slots.
 constexpr int PF = 4;  // operand reads in flight
 
-// f(integral_constant<int, k>) for k = 0 .. N-1 in order, fully unrolled at
-// compile time (the slot loops are too long for the loop unroller).
-template <typename F, int... Ks>
-__device__ __attribute__((always_inline)) inline void static_for_impl(F&& f, std::integer_sequence<int, Ks...>) {
-  (f(std::integral_constant<int, Ks>{}), ...);
-}
-template <int N, typename F>
-__device__ __attribute__((always_inline)) inline void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
 
 // Row pass: workgroup per (head, query block row m < Mt), XCD-aware order as
 // the forward (XCD x walks heads x, x + 8, ...; block rows of one head side by
@@ -401,7 +383,7 @@ __global__ __launch_bounds__(256, 1) void bsa_bwd_dq_bf16_d128(
     float pd[2][16];
     bf16x8 db[2][2];
     bf16x8 ring[PF];
-    static_for<PF>([&](auto kc) __attribute__((always_inline)) { ring[decltype(kc)::value] = fetch(decltype(kc)::value); });
+    tsp::static_for<PF>([&](auto kc) __attribute__((always_inline)) { ring[decltype(kc)::value] = fetch(decltype(kc)::value); });
     // dS^T element v of tile tt (key 32 tt + 8 (v / 4) + 4 h + v % 4)
     auto ds_elem = [&](int tt, int v) {
       float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tt][v], scale_log2, nr));
@@ -415,7 +397,7 @@ __global__ __launch_bounds__(256, 1) void bsa_bwd_dq_bf16_d128(
         db[tt][v >> 3] = __builtin_convertvector(t, bf16x8);
       }
     };
-    static_for<48>([&](auto kc) __attribute__((always_inline)) {
+    tsp::static_for<48>([&](auto kc) __attribute__((always_inline)) {
       constexpr int k = decltype(kc)::value;
       const bf16x8 op = ring[k % PF];
       if constexpr (k + PF < 48) ring[k % PF] = fetch(k + PF);
@@ -455,8 +437,8 @@ __global__ __launch_bounds__(256, 1) void bsa_bwd_dq_bf16_d128(
   Dq = dsum + __shfl_xor(dsum, 32, 64);
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    pin_agpr(qf[s]);
-    pin_agpr(dof[s]);
+    tsp::pin_agpr(qf[s]);
+    tsp::pin_agpr(dof[s]);
   }
   rq = rmax[head * Mt * BS + q] * LOG2E + __builtin_amdgcn_logf(rden[head * Mt * BS + q]);
   nr = -rq;
@@ -557,7 +539,7 @@ __global__ __launch_bounds__(256, 1) void bsa_bwd_dkdv_bf16_d128(
     u32x4 pw[2][2], dw[2][2];  // bf16 pairs of P and dS, k order of the B operand
     f32x4 rc, dc, rn, dn;      // stats of the current / next group of 4 queries
     bf16x8 ring[PF];
-    static_for<PF>([&](auto kc) __attribute__((always_inline)) { ring[decltype(kc)::value] = fetch(decltype(kc)::value); });
+    tsp::static_for<PF>([&](auto kc) __attribute__((always_inline)) { ring[decltype(kc)::value] = fetch(decltype(kc)::value); });
     // stats (r, D) of the queries 32 qt + 8 g + 4 h + [0, 4)
     typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
     auto stats = [&](int qt, int gg) {
@@ -586,7 +568,7 @@ __global__ __launch_bounds__(256, 1) void bsa_bwd_dkdv_bf16_d128(
       pw[qt][v >> 3][(v & 7) >> 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(p, bf16x2));
       dw[qt][v >> 3][(v & 7) >> 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(d, bf16x2));
     };
-    static_for<64>([&](auto kc) __attribute__((always_inline)) {
+    tsp::static_for<64>([&](auto kc) __attribute__((always_inline)) {
       constexpr int k = decltype(kc)::value;
       const bf16x8 op = ring[k % PF];
       if constexpr (k + PF < 64) ring[k % PF] = fetch(k + PF);
@@ -692,8 +674,8 @@ __global__ __launch_bounds__(256, 1) void bsa_bwd_dkdv_bf16_d128(
       have_next = false;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        pin_agpr(kf[s]);
-        pin_agpr(vf[s]);
+        tsp::pin_agpr(kf[s]);
+        tsp::pin_agpr(vf[s]);
       }
 #pragma unroll
       for (int u = 0; u < NU; ++u) dk[u] = dv[u] = f32x16{};

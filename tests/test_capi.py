@@ -68,6 +68,12 @@ def test_argument_validation_is_host_side():
     assert lib.tsp_csr_sum(None, None, None, 2, None, None, None, 0, 0, 0, 4, None, None, None, None, 0, None) == -1
     assert lib.tsp_csr_transpose_workspace_size(10, 3, 4, 9) == -1 and lib.tsp_csr_sum_workspace_size(-1, 0, 3, 4, 0) == -1
     assert lib.tsp_csr_sum(None, None, None, 1, None, None, None, 1, 0, 2, 4, None, None, None, None, 0, None) == -1
+    # CSR SDDMM: bad dtype, bad index type, leading dimension below ncols, null pointers
+    assert lib.tsp_csr_sddmm(None, None, 1, 4, 4, 3, None, 8, None, 8, 8, 2, 1.0, None, None) == -2
+    assert lib.tsp_csr_sddmm(None, None, 7, 4, 4, 3, None, 8, None, 8, 8, 0, 1.0, None, None) == -1
+    assert lib.tsp_csr_sddmm(None, None, 1, 4, 4, 3, None, 4, None, 8, 8, 0, 1.0, None, None) == -1
+    assert lib.tsp_csr_sddmm(None, None, 1, 4, 4, 3, None, 8, None, 8, 8, 0, 1.0, None, None) == -1
+    assert lib.tsp_csr_sddmm(None, None, 1, 4, 4, 0, None, 8, None, 8, 8, 0, 1.0, None, None) == 0  # nothing to do
 
 
 def _plan(cp, H, S, b):

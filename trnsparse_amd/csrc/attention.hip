@@ -21,7 +21,9 @@
 //       held in registers), so a lane holds all scores of one query: the
 //       softmax needs one cross-lane shuffle. O^T = V^T P^T consumes P from
 //       registers (bf16) with V staged transposed in LDS. fp32 softmax with
-//       exp2, fp32 accumulation, bf16 output.
+//       exp2, fp32 accumulation, bf16 output. Kept for operands past 4 GiB.
+//   bsa_fwd_bf16_stream<D> the same work split with K/V streamed through an
+//       LDS ring by direct loads (D in {64, 128}).
 //   bsa_fwd_f32_mfma<D>   fp32, 128-blocks, D in {64, 128}: the same work
 //       split on v_mfma_f32_32x32x2_f32 with K/V streamed through an LDS ring.
 //   bsa_fwd_generic<T>    fp32/fp64/bf16, any block size and head_dim: one
@@ -278,41 +280,56 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_bf16_mfma(
   }
 }
 
-// ---------------------------------------------------------- bf16 MFMA, d=128
+// ------------------------------------------------- bf16 MFMA, d = 64 and 128
 //
-// bsa_fwd_bf16_d128: same work split and math as bsa_fwd_bf16_mfma (one
+// bsa_fwd_bf16_stream<D>: same work split and math as bsa_fwd_bf16_mfma (one
 // 256-thread workgroup per (head, 128-query block row), a wavefront per 32
 // queries, S^T = K Q^T with the wave's Q rows in registers, online softmax in
 // the exp2 domain, O^T += V^T P^T with P from registers), restructured so the
 // key blocks stream while the MFMAs run:
 //   * keys are consumed in 64-key halves that go through a 2-stage LDS ring
-//     (K half 16 KiB + V half 16 KiB per stage, 64 KiB per workgroup, two
-//     workgroups per CU), filled by direct global->LDS buffer loads issued one
-//     half ahead; rows at or past seq_len read as zero;
+//     (K half + V half per stage: 64 KiB per workgroup at D = 128, 32 KiB at
+//     D = 64), filled by direct global->LDS buffer loads issued one half
+//     ahead; rows at or past seq_len read as zero;
 //   * V stays [key][d] in LDS and the A operand of O^T += V^T P^T (8 keys of
 //     one d column per lane) comes from ds_read_b64_tr_b16;
 //   * 16-byte chunks are XOR-swizzled for conflict-free reads on the 64-bank
-//     LDS: K rows (b128 reads of 16 consecutive keys) chunk ^ (key % 16),
-//     V rows (transpose reads of 4 consecutive keys) chunk ^ 4*(key % 4);
+//     LDS (att::Geo: K rows for b128 reads of 16 consecutive keys, V rows for
+//     transpose reads of 4 consecutive keys);
 //   * each MFMA's LDS operand is read one step ahead.
 namespace att {
-constexpr int D = 128;
 constexpr int HK = 64;                 // keys per ring stage
-constexpr int ROWB = D * 2;            // bytes per K/V row
-constexpr int HBYTES = HK * ROWB;      // 16 KiB
-constexpr int STAGE = 2 * HBYTES;      // K half, then V half
 constexpr int NST = 2;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+// Row geometry and swizzles per head_dim: K rows are read as 16-byte pieces
+// of 16 consecutive keys (one chunk), V rows through transpose reads of 4
+// consecutive keys. D = 128 (256-byte rows, 16 chunks): K chunk ^ (key % 16),
+// V chunk ^ 4 (key % 4). D = 64 (128-byte rows, where keys k and k + 2 share
+// banks): K chunk ^ ((key / 2) % 8), V chunk ^ 4 ((key / 2) % 2).
+template <int D>
+struct Geo {
+  static constexpr int ROWB = D * 2;           // bytes per K/V row
+  static constexpr int HBYTES = HK * ROWB;     // bytes per K (or V) half
+  static constexpr int STAGE = 2 * HBYTES;
+  static constexpr int KS = D / 16;            // k-steps of S^T
+  static constexpr int NU = D / 32;            // 32-wide d subtiles of O^T
+  static constexpr int LPR = ROWB / 16;        // lanes per row in a 1 KiB load
+  static constexpr int RPI = 64 / LPR;         // rows per load instruction
+  __host__ __device__ static constexpr int kswz(int key) { return D == 128 ? (key & 15) : ((key >> 1) & 7); }
+  __host__ __device__ static constexpr int vswz(int key) { return D == 128 ? (key & 3) : ((key >> 1) & 1); }
+};
 }  // namespace att
 
-__global__ __launch_bounds__(256, 2) void bsa_fwd_bf16_d128(
+// D = 64 fits three wavefronts per SIMD (136 registers, 32 KiB of LDS per workgroup)
+template <int D>
+__global__ __launch_bounds__(256, D == 64 ? 3 : 2) void bsa_fwd_bf16_stream(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int64_t S,
     int64_t head_stride, int64_t H, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci, int64_t Mt,
     float scale_log2, uint16_t* __restrict__ O, float* __restrict__ rmax, float* __restrict__ rden) {
   using namespace att;
-  constexpr int KS = D / 16;  // k-steps of S^T = K Q^T
-  constexpr int NU = D / 32;  // 32-wide d subtiles of O^T
+  typedef Geo<D> G;
+  constexpr int ROWB = G::ROWB, HBYTES = G::HBYTES, STAGE = G::STAGE, KS = G::KS, NU = G::NU;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
 
   // XCD-aware order: XCD x walks heads x, x+8, ...; the block rows of one
@@ -367,40 +384,39 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_bf16_d128(
   };
   auto first_key = [&](int s) { return (int64_t)colblk(s >> 1) * AB + HK * (s & 1); };
 
-  // ---- loads of half s into stage s % NST: 4 K + 4 V wave instructions
+  // ---- loads of half s into stage s % NST: per wave HBYTES / 4 KiB K and V instructions
   auto issue = [&](int s) {
     const int64_t key0 = first_key(s);
     const uint32_t st = lds0 + (s % NST) * STAGE;
+    constexpr int NI = HBYTES / 4096;
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-      const int j = 4 * w + qq;                 // rows [4j, 4j+4) of the half
-      const int rr = 4 * j + (lane >> 4);
-      const int p = lane & 15;                  // this lane's 16-byte slot in the row
+    for (int qq = 0; qq < NI; ++qq) {
+      const int j = NI * w + qq;                // rows [RPI j, RPI j + RPI) of the half
+      const int rr = G::RPI * j + lane / G::LPR;
+      const int p = lane % G::LPR;              // this lane's 16-byte slot in the row
       const int64_t rowoff = (key0 + rr) * ROWB;
-      tsp::dma::buffer16(krs, (uint32_t)(rowoff + ((p ^ (rr & 15)) * 16)), st + j * 1024);
-      tsp::dma::buffer16(vrs, (uint32_t)(rowoff + ((p ^ (4 * (rr & 3))) * 16)), st + HBYTES + j * 1024);
+      tsp::dma::buffer16(krs, (uint32_t)(rowoff + ((p ^ G::kswz(rr)) * 16)), st + j * 1024);
+      tsp::dma::buffer16(vrs, (uint32_t)(rowoff + ((p ^ (4 * G::vswz(rr))) * 16)), st + HBYTES + j * 1024);
     }
   };
 
   // per-lane LDS offsets
-  // S^T A operand (K rows 32*tt + l32, d chunk 2*ks + h): chunk ^ (row % 16)
-  const int krow0 = l32, krow1 = 32 + l32;
   // O^T A operand via transpose reads: lane j of 16-lane group gq points at
   // key row kb + 8*r + 4*(gq>>1) + j/4 (r: which 4-key read), d column
-  // 32u + 16*(gq&1) + 4*(j%4); the swizzle term is 4*(j/4).
+  // 32u + 16*(gq&1) + 4*(j%4); the swizzle term is 4*vswz(row).
   const int vrow = 4 * (gq >> 1) + (jq >> 2);
-  const int vsw = 4 * (jq >> 2);
+  const int vsw = 4 * G::vswz(vrow);  // rows read are vrow + multiples of 8, same swizzle
   const int vcol = 16 * (gq & 1) + 4 * (jq & 3);  // plus 32u
 
-  // per-lane byte offsets of the d chunk of K reads: chunk (2ks + h) ^ (row % 16)
-  // with row % 16 == l32 % 16 for both 32-key tiles
-  const int kx = (l32 & 15) ^ h;
+  // K reads: logical chunk 2ks + h of row 32tt + l32 sits in slot
+  // (2ks + h) ^ kswz(row), the same for both 32-key tiles
+  const int kx = G::kswz(l32) ^ h;
   // V transpose reads: byte offset within a row for d subtile u is
   // ((4u + c0) ^ vsw) * 16 + (col & 4) * 2 = ((u ^ (vsw/4)) << 6) + c0 * 16 + ...
   const int vlane = vrow * ROWB + ((vcol >> 3) & 3) * 16 + (vcol & 4) * 2;
 
   auto compute = [&](const uint8_t* st, int64_t key0) {
-    const uint8_t* Ks = st + krow0 * ROWB;
+    const uint8_t* Ks = st + l32 * ROWB;
     const uint8_t* Vs = st + HBYTES + vlane;
     auto kread = [&](int ks, int tile) {
       return *(const bf16x8*)(Ks + tile * 32 * ROWB + (((2 * ks) ^ kx) * 16));
@@ -817,8 +833,13 @@ extern "C" int tsp_bsa_fwd(const void* Q, const void* K, const void* V, int dtyp
     const int64_t grid = tsp::ceil_div(n_heads, 8) * Mt * 8;
     if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_fwd: problem too large");
     const float sl2 = (float)(scale * 1.4426950408889634);
-    if (head_dim == 128 && scale > 0 && (seq_len + AB) * head_dim * 2 <= (int64_t)UINT32_MAX)
-      hipLaunchKernelGGL(bsa_fwd_bf16_d128, dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)Q,
+    const bool streamed = scale > 0 && (seq_len + AB) * head_dim * 2 <= (int64_t)UINT32_MAX;
+    if (streamed && head_dim == 128)
+      hipLaunchKernelGGL((bsa_fwd_bf16_stream<128>), dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)Q,
+                         (const uint16_t*)K, (const uint16_t*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs,
+                         block_col_indices, Mt, sl2, (uint16_t*)O, (float*)row_max, (float*)row_denom);
+    else if (streamed)
+      hipLaunchKernelGGL((bsa_fwd_bf16_stream<64>), dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)Q,
                          (const uint16_t*)K, (const uint16_t*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs,
                          block_col_indices, Mt, sl2, (uint16_t*)O, (float*)row_max, (float*)row_denom);
     else if (head_dim == 128)

@@ -149,6 +149,26 @@ def test_f64_mfma_mask_exact(hip_backend):
     assert np.array_equal(got, ref.screened_mask(diag.numpy(), 1e-10).astype(np.float64))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_16bit_operands(hip_backend, dtype):
+    """bf16 / fp16 A and B (fp32 diag): C in A's dtype within the 16-bit
+    tolerance of the dot-product scale; the mask is the fp32 one."""
+    n, N = 384, 96
+    g = torch.Generator().manual_seed(9)
+    diag = torch.rand(n, generator=g) + 0.05
+    diag[128:256] = 1e-30
+    A = torch.randn(n, n, generator=g).to(dtype)
+    B = torch.randn(n, N, generator=g).to(dtype)
+    got = ts.screened_spmm(A.cuda(), diag.cuda(), B.cuda(), threshold=1e-8).cpu()
+    assert got.dtype == dtype
+    mask = ref.screened_mask(diag.numpy(), 1e-8)
+    Am = np.where(mask, A.double().numpy(), 0.0)
+    Bn = B.double().numpy()
+    err = ref.scaled_error(got.double().numpy(), Am @ Bn, np.abs(Am) @ np.abs(Bn))
+    assert err <= 2e-2, err
+    assert torch.count_nonzero(got[128:256]).item() == 0
+
+
 def test_f64_generic_and_gradcheck(hip_backend):
     torch.manual_seed(7)
     n = 41  # odd: the generic kernel

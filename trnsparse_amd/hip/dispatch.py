@@ -385,8 +385,13 @@ def _screened_forward(A, diag, threshold, B, dev):
     M, K = A.shape
     if A.dtype != B.dtype:
         raise RuntimeError(f"screened_spmm: A dtype {A.dtype} and B dtype {B.dtype} differ")
+    if A.dtype in (torch.bfloat16, torch.float16):
+        # 16-bit A and B: widened on the device (exact), the fp32 kernel, one
+        # rounding of C back to A's dtype; the mask stays in diag's precision
+        return _screened_forward(_on(A, dev, torch.float32), diag, threshold, _on(B, dev, torch.float32),
+                                 dev).to(A.dtype)
     if A.dtype not in (torch.float32, torch.float64):
-        raise RuntimeError(f"HIP screened_spmm supports float32 and float64, got {A.dtype}")
+        raise RuntimeError(f"HIP screened_spmm supports float32, float64, bfloat16 and float16, got {A.dtype}")
     if diag.dtype not in (torch.float32, torch.float64):
         raise RuntimeError(f"HIP screened_spmm needs float32 or float64 diag_integrals, got {diag.dtype}")
     if B.dim() != 2 or B.shape[0] != K:

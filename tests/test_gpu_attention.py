@@ -197,3 +197,19 @@ def test_cfg5_full_size_sampled(hip_backend):
         out, _, _, sc = _oracle(Q[hh], K[hh], V[hh], mask_bsr, 128**-0.5, rows=rows)
         sel = np.concatenate([np.arange(r * 128, (r + 1) * 128) for r in rows])
         assert _err(got[hh].float().cpu().numpy()[sel], out[sel], sc[sel]) <= TOL_BF16
+
+
+def test_fp16_widened(hip_backend):
+    """fp16 Q/K/V run the fp32 kernels on widened operands: O comes back in
+    fp16 within the 16-bit tolerance, and the backward gives fp16 gradients."""
+    S, D = 512, 64
+    g = torch.Generator().manual_seed(17)
+    mask_bsr = W.bsr_from_block_mask(global_mask(4, 1, 1), 128)
+    Q, K, V = (torch.randn(S, D, generator=g).half() for _ in range(3))
+    got = ts.block_sparse_attention_tiled(Q.cuda(), K.cuda(), V.cuda(), mask_bsr)
+    assert got.dtype == torch.float16
+    out, _, _, sc = _oracle(Q, K, V, mask_bsr, D**-0.5)
+    assert _err(got.float().cpu().numpy(), out, sc) <= TOL_BF16
+    q, k, v = (t.cuda().requires_grad_(True) for t in (Q, K, V))
+    ts.block_sparse_attention_tiled(q, k, v, mask_bsr).float().sum().backward()
+    assert q.grad.dtype == torch.float16 and torch.isfinite(q.grad.float()).all()

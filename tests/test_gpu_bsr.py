@@ -226,3 +226,21 @@ def test_cfg3b_bf16_full_size(hip_backend):
     exact, scale = _oracle(A, B, rows=rows)
     got = torch.cat([C[r * 128 : (r + 1) * 128] for r in rows]).cpu().numpy()
     assert ref.scaled_error(got, exact, scale) <= TOL_F32
+
+
+def test_fp16_widened(hip_backend):
+    """fp16 blocks and B run the fp32 kernel on widened operands; the result
+    and the autograd gradients come back in fp16."""
+    g = torch.Generator().manual_seed(21)
+    A = torch.randn(256, 384, generator=g) * (torch.rand(256, 384, generator=g) < 0.5)
+    bsr = ts.BSRMatrix.from_dense(A.half(), block_size=128)
+    B = torch.randn(384, 96, generator=g).half()
+    C = ts.bsr_spmm(bsr, B.cuda())
+    assert C.dtype == torch.float16
+    exact = A.half().double() @ B.double()
+    scale = A.half().double().abs() @ B.double().abs()
+    assert ((C.double().cpu() - exact).abs() / scale.clamp_min(1e-30)).max().item() <= 2e-2
+    blocks = bsr.blocks.cuda().requires_grad_(True)
+    Bd = B.cuda().requires_grad_(True)
+    ts.bsr_spmm(ts.BSRMatrix(blocks, bsr.block_col_indices, bsr.block_row_ptrs, bsr.shape, 128), Bd).float().sum().backward()
+    assert blocks.grad.dtype == torch.float16 and Bd.grad.dtype == torch.float16

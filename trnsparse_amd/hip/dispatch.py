@@ -224,12 +224,19 @@ def _bsr_blocks_on(A, dev):
 
 
 def hip_bsr_spmm(A, B: torch.Tensor, out_dtype: torch.dtype | None = None) -> torch.Tensor:
-    """BSR SpMM entry point (replaces nki_bsr_spmm, reference dispatch.py:372-381)."""
+    """BSR SpMM entry point (replaces nki_bsr_spmm, reference dispatch.py:372-381).
+
+    fp16 blocks and B are widened to fp32 (exact; the casts carry autograd)
+    and the result rounded to the output dtype once."""
     m, _ = A.shape
     b = A.block_size
     dev = _target_device(B, A.blocks)
     with torch.cuda.device(dev):
         plan = _bsr_plan(A.block_col_indices, A.block_row_ptrs, (m + b - 1) // b, dev, holder=A)
+    if A.blocks.dtype == torch.float16 and B.dtype == torch.float16:
+        C = _BSRSpMMFunction.apply(A.blocks.float(), A.block_col_indices, A.block_row_ptrs, A.shape, A.block_size,
+                                   B.float(), torch.float32, plan)
+        return C.to(out_dtype or torch.float16)
     return _BSRSpMMFunction.apply(
         A.blocks, A.block_col_indices, A.block_row_ptrs, A.shape, A.block_size, B, out_dtype, plan
     )
@@ -466,12 +473,16 @@ def hip_block_sparse_attention(Q, K, V, mask_bsr, scale: float, return_stats: bo
     Honours `scale` (the reference NKI path used head_dim**-0.5 regardless).
     Stats come back as (..., S // b, b) in float32 (float64 for float64 input).
     fp32 / bf16 with 128-blocks and head_dim below 128 other than 64 run the
-    MFMA kernels on operands zero-padded to head_dim 64 or 128.
+    MFMA kernels on operands zero-padded to head_dim 64 or 128; fp16 runs in
+    fp32 (widened operands, O rounded back once).
     """
     if not (Q.shape == K.shape == V.shape):
         raise RuntimeError(f"Q, K, V shapes differ: {tuple(Q.shape)}, {tuple(K.shape)}, {tuple(V.shape)}")
     if not (Q.dtype == K.dtype == V.dtype):
         raise RuntimeError("Q, K, V dtypes differ")
+    if Q.dtype == torch.float16:  # widened to fp32 (exact), O rounded back once
+        res = hip_block_sparse_attention(Q.float(), K.float(), V.float(), mask_bsr, scale, return_stats)
+        return res.half() if not return_stats else (res[0].half(),) + tuple(res[1:])
     dp = _mfma_head_dim(Q, mask_bsr.block_size)
     if dp is not None and scale > 0:
         res = hip_block_sparse_attention(*(_pad_head_dim(t, dp) for t in (Q, K, V)), mask_bsr, scale, return_stats)
@@ -565,6 +576,10 @@ def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, 
     """
     if not (Q.shape == K.shape == V.shape == O.shape == dO.shape):
         raise RuntimeError("Q, K, V, O, dO shapes differ")
+    if Q.dtype == torch.float16:  # widened to fp32 (exact), gradients rounded back once
+        grads = hip_block_sparse_attention_backward(*(t.float() for t in (Q, K, V, O, dO)), mask_bsr, scale,
+                                                    row_max, row_denom)
+        return tuple(gr.half() for gr in grads)
     dp = _mfma_head_dim(Q, mask_bsr.block_size)
     if dp is not None and scale > 0:
         grads = hip_block_sparse_attention_backward(*(_pad_head_dim(t, dp) for t in (Q, K, V, O, dO)), mask_bsr, scale,

@@ -660,6 +660,9 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="headline only")
+    ap.add_argument("--only", metavar="JOB", default=None,
+                    help="run only the named secondary job (e.g. 'spmv poisson int64') and print its result; for "
+                    "profiling one kernel")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 256 MiB device copy (known bytes) to calibrate PMC byte counters")
     ap.add_argument("--calibrate-peaks", action="store_true",
@@ -704,8 +707,9 @@ def main(argv=None) -> int:
         print(json.dumps(calibrate_gather()), flush=True)
         return 0
 
-    head = bench_bsr_fp32(args.steps, args.warmup, cpu=not args.no_cpu)
     secondary = []
+    if args.only is None:
+        head = bench_bsr_fp32(args.steps, args.warmup, cpu=not args.no_cpu)
     if not args.no_secondary:
         jobs = [
             ("spmv poisson int64", lambda: bench_spmv("poisson", 64, 20, 3, cpu=not args.no_cpu)),
@@ -722,6 +726,13 @@ def main(argv=None) -> int:
             ("bsr spmv", lambda: bench_bsr_spmv(20, 3, cpu=not args.no_cpu)),
             ("csr ops", lambda: bench_csr_ops(5, 1)),
         ]
+        if args.only is not None:
+            chosen = [j for j in jobs if j[0] == args.only]
+            if not chosen:
+                print(f"--only: no job named {args.only!r}; jobs: {[j[0] for j in jobs]}", file=sys.stderr)
+                return 2
+            print(json.dumps(chosen[0][1]()), flush=True)
+            return 0
         for name, fn in jobs:
             try:
                 r = fn()

@@ -152,11 +152,22 @@ def test_csr_to_dense_and_to_coo(hip_backend, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-def test_coo_to_csr_matches_cpu_and_oracle(hip_backend, dtype):
+@pytest.mark.parametrize(
+    "m,n",
+    [
+        (500, 700),        # 32-bit sort keys; duplicates likely
+        (65535, 65537),    # m * n = 2^32 - 1: the largest shape on 32-bit keys
+        (65536, 65536),    # m * n = 2^32: 64-bit keys
+        (100000, 50000),   # 64-bit keys
+    ],
+)
+def test_coo_to_csr_matches_cpu_and_oracle(hip_backend, dtype, m, n):
     g = torch.Generator().manual_seed(21)
-    m, n, nnz = 500, 700, 20000  # duplicates likely
+    nnz = 20000
     rows = torch.randint(0, m, (nnz,), generator=g)
     cols = torch.randint(0, n, (nnz,), generator=g)
+    rows[:3] = torch.tensor([m - 1, m - 1, 0])  # the largest and smallest keys
+    cols[:3] = torch.tensor([n - 1, n - 2, 0])
     vals = torch.randn(nnz, generator=g).to(dtype)
     got = ts.COOMatrix(vals.cuda(), rows.cuda(), cols.cuda(), (m, n)).to_csr()
     want = ts.COOMatrix(vals, rows, cols, (m, n)).to_csr()

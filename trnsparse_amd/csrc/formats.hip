@@ -418,28 +418,33 @@ int launch_entry_rows(const int64_t* row_ptrs, int64_t m, int64_t nnz, Fn fn, hi
 
 // ------------------------------------------------------------- COO -> CSR
 
+// K is uint32_t when every key, row_ptrs' bound m * n included, fits in 32
+// bits: the radix sort then moves half the key bytes per pass.
+template <typename K>
 __global__ __launch_bounds__(256) void coo_keys_kernel(const int64_t* __restrict__ rows,
                                                        const int64_t* __restrict__ cols, int64_t nnz, int64_t n,
-                                                       uint64_t* __restrict__ keys) {
+                                                       K* __restrict__ keys) {
   const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (k >= nnz) return;
-  keys[k] = (uint64_t)(rows[k] * n + cols[k]);
+  keys[k] = (K)(rows[k] * n + cols[k]);
 }
 
 // column of each sorted key (key = row * n + col)
-__global__ __launch_bounds__(256) void key_cols_kernel(const uint64_t* __restrict__ keys, int64_t nnz, int64_t n,
+template <typename K>
+__global__ __launch_bounds__(256) void key_cols_kernel(const K* __restrict__ keys, int64_t nnz, int64_t n,
                                                        int64_t* __restrict__ cols_out) {
   const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (k >= nnz) return;
-  cols_out[k] = (int64_t)(keys[k] % (uint64_t)n);
+  cols_out[k] = (int64_t)(keys[k] % (K)n);
 }
 
 // row_ptrs[r] = first k with sorted key >= r * n (r = 0 .. m).
-__global__ __launch_bounds__(256) void coo_row_ptrs_kernel(const uint64_t* __restrict__ keys, int64_t nnz, int64_t m,
+template <typename K>
+__global__ __launch_bounds__(256) void coo_row_ptrs_kernel(const K* __restrict__ keys, int64_t nnz, int64_t m,
                                                            int64_t n, int64_t* __restrict__ row_ptrs) {
   const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (r > m) return;
-  const uint64_t key = (uint64_t)(r * n);
+  const K key = (K)(r * n);
   int64_t lo = 0, hi = nnz;
   while (lo < hi) {
     const int64_t mid = (lo + hi) >> 1;
@@ -1165,20 +1170,51 @@ hipError_t sort_pairs_dtype(int dtype, void* tmp, size_t& tmp_bytes, const K* ki
   return sort_pairs(tmp, tmp_bytes, kin, kout, (const uint16_t*)vin, (uint16_t*)vout, nnz, bits, st);
 }
 
+template <typename K = uint64_t>
 int64_t coo_sort_tmp(int dtype, int64_t nnz, int bits) {
   size_t tmp = 0;
-  if (nnz > 0 && sort_pairs_dtype<uint64_t, float>(dtype, nullptr, tmp, (const uint64_t*)nullptr, (uint64_t*)nullptr,
-                                                   nullptr, nullptr, nnz, bits, 0) != hipSuccess)
+  if (nnz > 0 && sort_pairs_dtype<K, float>(dtype, nullptr, tmp, (const K*)nullptr, (K*)nullptr, nullptr, nullptr, nnz,
+                                            bits, 0) != hipSuccess)
     return -1;
   return (int64_t)tmp;
+}
+
+// keys fit in 32 bits: every key and the bound m * n are <= UINT32_MAX
+bool narrow_keys(int64_t m, int64_t n) { return m == 0 || n <= (int64_t)UINT32_MAX / m; }
+
+template <typename K>
+int coo_to_csr_keys(const void* values, int dtype, const int64_t* row_indices, const int64_t* col_indices, int64_t nnz,
+                    int64_t m, int64_t n, int64_t* row_ptrs, int64_t* col_out, void* values_out, char* w,
+                    int64_t workspace_bytes, hipStream_t st) {
+  const int64_t g = tsp::ceil_div(nnz, 256);
+  K* keys = (K*)w;
+  K* keys_s = (K*)(w + align256(8 * nnz));
+  void* tmp = w + 2 * align256(8 * nnz);
+  size_t tmp_bytes = (size_t)(workspace_bytes - 2 * align256(8 * nnz));
+  hipLaunchKernelGGL(coo_keys_kernel<K>, dim3((unsigned)g), dim3(256), 0, st, row_indices, col_indices, nnz, n, keys);
+  int rc = tsp::check_launch("coo_keys launch");
+  if (rc) return rc;
+  if (sort_pairs_dtype<K, float>(dtype, tmp, tmp_bytes, keys, keys_s, values, values_out, nnz, key_bits(m, n), st) !=
+      hipSuccess)
+    return tsp::check_hip(hipGetLastError(), "radix_sort_pairs");
+  rc = tsp::check_launch("radix_sort_pairs");
+  if (rc) return rc;
+  hipLaunchKernelGGL(key_cols_kernel<K>, dim3((unsigned)g), dim3(256), 0, st, keys_s, nnz, n, col_out);
+  rc = tsp::check_launch("key_cols launch");
+  if (rc) return rc;
+  hipLaunchKernelGGL(coo_row_ptrs_kernel<K>, dim3((unsigned)tsp::ceil_div(m + 1, 256)), dim3(256), 0, st, keys_s, nnz,
+                     m, n, row_ptrs);
+  return tsp::check_launch("coo_row_ptrs launch");
 }
 
 }  // namespace
 
 extern "C" int64_t tsp_coo_to_csr_workspace_size(int64_t nnz, int64_t m, int64_t n) {
   if (nnz < 0 || m < 0 || n < 0) return -1;
-  // sized for the widest value type (fp64), which also covers fp32 / bf16
-  const int64_t tmp = coo_sort_tmp(TSP_F64, nnz, nnz > 0 ? key_bits(m, n) : 1);
+  // sized for the widest value type (fp64), which also covers fp32 / bf16;
+  // the two key arrays get 8 bytes an entry whichever key width runs
+  const int bits = nnz > 0 ? key_bits(m, n) : 1;
+  const int64_t tmp = narrow_keys(m, n) ? coo_sort_tmp<uint32_t>(TSP_F64, nnz, bits) : coo_sort_tmp(TSP_F64, nnz, bits);
   if (tmp < 0) return -1;
   return 2 * align256(8 * nnz) + align256(tmp);
 }
@@ -1201,25 +1237,11 @@ extern "C" int tsp_coo_to_csr(const void* values, int dtype, const int64_t* row_
     return tsp::fail(TSP_EINVAL, "tsp_coo_to_csr: workspace too small");
   const int64_t g = tsp::ceil_div(nnz, 256);
   if (g > INT32_MAX || tsp::ceil_div(m + 1, 256) > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_coo_to_csr: too large");
-  char* w = (char*)workspace;
-  uint64_t* keys = (uint64_t*)w;
-  uint64_t* keys_s = (uint64_t*)(w + align256(8 * nnz));
-  void* tmp = w + 2 * align256(8 * nnz);
-  size_t tmp_bytes = (size_t)(workspace_bytes - 2 * align256(8 * nnz));
-  hipLaunchKernelGGL(coo_keys_kernel, dim3((unsigned)g), dim3(256), 0, st, row_indices, col_indices, nnz, n, keys);
-  int rc = tsp::check_launch("coo_keys launch");
-  if (rc) return rc;
-  if (sort_pairs_dtype<uint64_t, float>(dtype, tmp, tmp_bytes, keys, keys_s, values, values_out, nnz, key_bits(m, n),
-                                        st) != hipSuccess)
-    return tsp::check_hip(hipGetLastError(), "radix_sort_pairs");
-  rc = tsp::check_launch("radix_sort_pairs");
-  if (rc) return rc;
-  hipLaunchKernelGGL(key_cols_kernel, dim3((unsigned)g), dim3(256), 0, st, keys_s, nnz, n, col_out);
-  rc = tsp::check_launch("key_cols launch");
-  if (rc) return rc;
-  hipLaunchKernelGGL(coo_row_ptrs_kernel, dim3((unsigned)tsp::ceil_div(m + 1, 256)), dim3(256), 0, st, keys_s, nnz, m,
-                     n, row_ptrs);
-  return tsp::check_launch("coo_row_ptrs launch");
+  if (narrow_keys(m, n))
+    return coo_to_csr_keys<uint32_t>(values, dtype, row_indices, col_indices, nnz, m, n, row_ptrs, col_out, values_out,
+                                     (char*)workspace, workspace_bytes, st);
+  return coo_to_csr_keys<uint64_t>(values, dtype, row_indices, col_indices, nnz, m, n, row_ptrs, col_out, values_out,
+                                   (char*)workspace, workspace_bytes, st);
 }
 
 extern "C" int64_t tsp_coo_sum_to_csr_workspace_size(int64_t nnz, int64_t m, int64_t n) {
@@ -1260,7 +1282,7 @@ extern "C" int tsp_coo_sum_to_csr(const void* values, int dtype, const int64_t* 
   uint64_t* ukeys = (uint64_t*)(w + 5 * a);
   void* tmp = w + 6 * a;
   size_t tmp_bytes = (size_t)(workspace_bytes - 6 * a);
-  hipLaunchKernelGGL(coo_keys_kernel, dim3((unsigned)g), dim3(256), 0, st, row_indices, col_indices, nnz, n, keys);
+  hipLaunchKernelGGL(coo_keys_kernel<uint64_t>, dim3((unsigned)g), dim3(256), 0, st, row_indices, col_indices, nnz, n, keys);
   int rc = tsp::check_launch("coo_keys launch");
   if (rc) return rc;
   if (sort_pairs_dtype<uint64_t, float>(dtype, tmp, tmp_bytes, keys, keys_s, values, vals_s, nnz, key_bits(m, n),

@@ -107,7 +107,10 @@ __global__ __launch_bounds__(T32::NTHR) void bsr_spmm_f32_mfma(
 // restructured for issue efficiency:
 //   * 4 waves, each a 64x64 sub-tile as four independent 32x32
 //     v_mfma_f32_32x32x2_f32 accumulators: per 8 k a wave reads two 16-byte
-//     A fragments and eight 4-byte B values for 16 MFMAs;
+//     A fragments and four 8-byte B pairs for 16 MFMAs. The two column
+//     subtiles of a wave interleave (subtile u holds columns wn*64 + 2j + u,
+//     j = lane % 32), so one 8-byte read of a B row feeds both, and the
+//     epilogue stores the two subtiles' values as one 8-byte pair;
 //   * KC-wide k-slabs of A (128 x KC) and B (KC x 128) stream through a
 //     2-stage LDS ring by direct global->LDS loads issued one slab ahead
 //     (a slab is ~KC*128 MFMA cycles per SIMD, ample time for the loads);
@@ -118,11 +121,12 @@ __global__ __launch_bounds__(T32::NTHR) void bsr_spmm_f32_mfma(
 //   * swizzles for the 64-bank LDS: A rows of KC*4 bytes, chunk ^ (row % 16)
 //     for 256-byte rows or chunk ^ ((row / 2) % 8) for 128-byte rows, so 16
 //     consecutive rows of one b128 read cover all banks; B rows (512 B)
-//     chunk ^ 8*((k / 4) % 2), so the two lane halves (k rows 4 apart) of a
-//     4-byte read land in different bank halves.
+//     chunk ^ 8*((k / 4) % 2), so the two lane halves (k rows 4 apart) of an
+//     8-byte read land in different bank halves.
 // KC = 64 (128 KiB ring, one workgroup per CU, so the in-order dispatcher
 // list-schedules the ranked rows) measured faster on cfg3a than KC = 32
-// (64 KiB, two workgroups per CU): 237 us vs 263 us.
+// (64 KiB, two workgroups per CU): 237 us vs 263 us. The paired B reads took
+// cfg3a from 238.6 to 235.3 us.
 template <int KC_>
 struct F32S {
   static constexpr int KC = KC_;
@@ -207,13 +211,11 @@ __global__ __launch_bounds__(256) void bsr_spmm_f32_dma(
     };
 
     // per-lane LDS offsets: A rows wm*64 + 32t + l32 (the swizzle term is the
-    // same for both t); B columns wn*64 + 32u + l32, rows 8g + 4h + s
+    // same for both t); B columns wn*64 + 2*l32 + u, rows 8g + 4h + s
     const int arow = wm * 64 + l32;
-    const int bcol = wn * 64 + l32;
-    int boff[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-      boff[u] = ((((bcol + 32 * u) >> 2) ^ (8 * h)) * 16) + (bcol & 3) * 4 + 4 * h * G::B_ROWB;
+    // subtile u holds columns wn*64 + 2*l32 + u: one b64 read serves both
+    const int bc2 = wn * 64 + 2 * l32;
+    const int boff2 = (((bc2 >> 2) ^ (8 * h)) * 16) + (bc2 & 3) * 4 + 4 * h * G::B_ROWB;
     struct Ops {
       f32x4 a[2];
       float b[2][4];
@@ -224,9 +226,11 @@ __global__ __launch_bounds__(256) void bsr_spmm_f32_dma(
       o.a[1] = *(const f32x4*)(As + 32 * G::A_ROWB);
       const uint8_t* Bs = st + G::A_BYTES + 8 * g * G::B_ROWB;
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int s = 0; s < 4; ++s) o.b[u][s] = *(const float*)(Bs + s * G::B_ROWB + boff[u]);
+      for (int s = 0; s < 4; ++s) {
+        const f32x2 bb = *(const f32x2*)(Bs + s * G::B_ROWB + boff2);
+        o.b[0][s] = bb[0];
+        o.b[1][s] = bb[1];
+      }
     };
     auto mma = [&](const Ops& o) {
 #pragma unroll
@@ -257,18 +261,22 @@ __global__ __launch_bounds__(256) void bsr_spmm_f32_dma(
       compute(lds + (s % G::NST) * G::STAGE);
     }
   }
-  // accumulator layout: lane holds column l32 and rows 8*(v/4) + 4*h + v%4
+  // accumulator layout: lane holds rows 8*(v/4) + 4*h + v%4 of columns
+  // wn*64 + 2*l32 + u (subtile u)
+  const int64_t c = n0 + wn * 64 + 2 * l32;
+  const bool pair = c + 1 < ncols && (ldc & 1) == 0 && ((uintptr_t)C & 7) == 0;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int64_t r0 = row * BS + wm * 64 + 32 * t + 4 * h;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int64_t c = n0 + wn * 64 + 32 * u + l32;
-      if (c < ncols) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
-          if (r < m) C[r * ldc + c] = acc[t][u][v];
+    for (int v = 0; v < 16; ++v) {
+      const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
+      if (r < m) {
+        if (pair) {
+          *(f32x2*)(C + r * ldc + c) = f32x2{acc[t][0][v], acc[t][1][v]};
+        } else {
+          if (c < ncols) C[r * ldc + c] = acc[t][0][v];
+          if (c + 1 < ncols) C[r * ldc + c + 1] = acc[t][1][v];
         }
       }
     }

@@ -149,6 +149,8 @@ __global__ __launch_bounds__(T32::NTHR) void screened_f32_mfma(
 // m read as zero). The mask cannot be applied while staging, so it is
 // applied to the A fragments after their LDS read: a * (Q_i*Q_k > thr ? 1 : 0)
 // in diag's precision, with Q_k of the slab staged in LDS next to the ring.
+// As there, a wave's two column subtiles interleave (columns 2j + u) so one
+// 8-byte B read feeds both and C is stored in 8-byte pairs.
 namespace sdma {
 constexpr int KROWB = TILE * 4;        // B tile rows: 512 B
 constexpr uint32_t OOB = 0xFFFFFFF0u;
@@ -227,11 +229,10 @@ __global__ __launch_bounds__(256) void screened_f32_dma(
       }
       if (w == 0 && lane < SKC) qnext = k0 + lane < m ? Q[k0 + lane] : (QT)0;  // into qs before its barrier
     };
-    const int bcol = wn * 64 + l32;
-    int boff[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-      boff[u] = ((((bcol + 32 * u) >> 2) ^ (8 * h)) * 16) + (bcol & 3) * 4 + 4 * h * KROWB;
+    // column subtile u holds columns wn*64 + 2*l32 + u: one 8-byte read of a
+    // B row feeds both subtiles
+    const int bc2 = wn * 64 + 2 * l32;
+    const int boff2 = (((bc2 >> 2) ^ (8 * h)) * 16) + (bc2 & 3) * 4 + 4 * h * KROWB;
     struct Ops {
       float a[2][4];
       float b[2][4];
@@ -249,9 +250,11 @@ __global__ __launch_bounds__(256) void screened_f32_dma(
       }
       const uint8_t* Bs = st + TBYTES + 8 * g * KROWB;
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int s = 0; s < 4; ++s) o.b[u][s] = *(const float*)(Bs + s * KROWB + boff[u]);
+      for (int s = 0; s < 4; ++s) {
+        const f32x2 bb = *(const f32x2*)(Bs + s * KROWB + boff2);
+        o.b[0][s] = bb[0];
+        o.b[1][s] = bb[1];
+      }
     };
     auto mma = [&](const Ops& o) {
 #pragma unroll
@@ -283,17 +286,21 @@ __global__ __launch_bounds__(256) void screened_f32_dma(
       if (w == 0 && lane < SKC && s + 1 < nsteps) qs[(s + 1) & 1][lane] = qnext;
     }
   }
+  // lane holds rows 8*(v/4) + 4*h + v%4 of columns wn*64 + 2*l32 + u
+  const int64_t c = n0 + wn * 64 + 2 * l32;
+  const bool pair = c + 1 < ncols && (ldc & 1) == 0 && ((uintptr_t)C & 7) == 0;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int64_t r0 = row0 + wm * 64 + 32 * t + 4 * h;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int64_t c = n0 + wn * 64 + 32 * u + l32;
-      if (c < ncols) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
-          if (r < m) C[r * ldc + c] = acc[t][u][v];
+    for (int v = 0; v < 16; ++v) {
+      const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
+      if (r < m) {
+        if (pair) {
+          *(f32x2*)(C + r * ldc + c) = f32x2{acc[t][0][v], acc[t][1][v]};
+        } else {
+          if (c < ncols) C[r * ldc + c] = acc[t][0][v];
+          if (c + 1 < ncols) C[r * ldc + c + 1] = acc[t][1][v];
         }
       }
     }

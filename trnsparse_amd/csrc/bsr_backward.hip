@@ -97,11 +97,17 @@ __device__ inline void dma_k_tile_global(const float* src, int64_t ld, uint32_t 
 __device__ inline f32x4 frag_row(const uint8_t* tile, int r, int g, int h) {
   return *(const f32x4*)(tile + r * TROWB + (((2 * g + h) ^ (r & 15)) * 16));
 }
-// From a k tile: column c -> 4 values from rows 8g + 4h + s.
-__device__ inline void frag_k(const uint8_t* tile, int c, int g, int h, float (&v)[4]) {
-  const uint8_t* p = tile + (8 * g + 4 * h) * KROWB + ((((c >> 2) ^ (8 * h))) * 16) + (c & 3) * 4;
+// From a k tile: the column pair c2, c2 + 1 (c2 even) -> 4 values each from
+// rows 8g + 4h + s, one 8-byte read per row; v[i] feeds the subtile whose
+// columns are the ones of parity i.
+__device__ inline void frag_k2(const uint8_t* tile, int c2, int g, int h, float (&v)[2][4]) {
+  const uint8_t* p = tile + (8 * g + 4 * h) * KROWB + ((((c2 >> 2) ^ (8 * h))) * 16) + (c2 & 3) * 4;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) v[s] = *(const float*)(p + s * KROWB);
+  for (int s = 0; s < 4; ++s) {
+    const f32x2 x = *(const f32x2*)(p + s * KROWB);
+    v[0][s] = x[0];
+    v[1][s] = x[1];
+  }
 }
 
 struct Acc4 {
@@ -243,16 +249,16 @@ __global__ __launch_bounds__(256) void bsr_spmm_t_f32_dma(
       // dC rows ib*128 + kk .. +64 (past m: zero), columns n0 .. n0+128
       dma_k_tile(rsx, ib * BS + kk, ldx, n0, st + TILE, w, lane);
     };
-    const int ac = wm * 64 + l32, bc = wn * 64 + l32;
+    // subtiles interleave: row subtile t holds output rows wm*64 + 2i + t,
+    // column subtile u holds columns wn*64 + 2j + u, so one 8-byte read per
+    // k row feeds both subtiles of an operand
+    const int ac2 = wm * 64 + 2 * l32, bc2 = wn * 64 + 2 * l32;
     struct Ops {
       float x[2][4], y[2][4];
     };
     auto fetch = [&](const uint8_t* st, int gg, Ops& o) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        frag_k(st, ac + 32 * t, gg, h, o.x[t]);
-        frag_k(st + TILE, bc + 32 * t, gg, h, o.y[t]);
-      }
+      frag_k2(st, ac2, gg, h, o.x);
+      frag_k2(st + TILE, bc2, gg, h, o.y);
     };
     const int nsteps = nblk * (BS / KC);
     issue(0);
@@ -271,17 +277,23 @@ __global__ __launch_bounds__(256) void bsr_spmm_t_f32_dma(
       }
     }
   }
+  // accumulator (t, u) element v of lane (h, l32): MFMA row i = 8(v/4) + 4h +
+  // v%4 and column j = l32, i.e. output row wm*64 + 2i + t, column
+  // wn*64 + 2j + u; the (u = 0, 1) pair is one 8-byte store
+  const int64_t c = n0 + wn * 64 + 2 * l32;
+  const bool pair = c + 1 < ncols && (ldo & 1) == 0 && ((uintptr_t)out & 7) == 0;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int64_t r0 = col * BS + wm * 64 + 32 * t + 4 * h;
+  for (int v = 0; v < 16; ++v) {
+    const int64_t rb = col * BS + wm * 64 + 2 * (8 * (v >> 2) + 4 * h + (v & 3));
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int64_t c = n0 + wn * 64 + 32 * u + l32;
-      if (c < ncols) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
-          if (r < n) out[r * ldo + c] = acc.a[t][u][v];
+    for (int t = 0; t < 2; ++t) {
+      const int64_t r = rb + t;
+      if (r < n) {
+        if (pair) {
+          *(f32x2*)(out + r * ldo + c) = f32x2{acc.a[t][0][v], acc.a[t][1][v]};
+        } else {
+          if (c < ncols) out[r * ldo + c] = acc.a[t][0][v];
+          if (c + 1 < ncols) out[r * ldo + c + 1] = acc.a[t][1][v];
         }
       }
     }

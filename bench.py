@@ -161,14 +161,14 @@ def bench_bsr_fp32(steps: int, warmup: int, cpu: bool):
 
         nthr = cb.threads()
         torch.set_num_threads(nthr)
-        secs = cb.time_call(lambda: cb.bsr_spmm(A.blocks, A.block_col_indices, A.block_row_ptrs, A.shape, 128, B), reps=3)
+        secs, reps = cb.time_call(lambda: cb.bsr_spmm(A.blocks, A.block_col_indices, A.block_row_ptrs, A.shape, 128, B), reps=5)
         res["cpu_baseline"] = {
             "value": round(flops / secs / 1e9, 2),
             "unit": "GFLOP/s",
             "cores": nthr,
             "kind": "port",
             "sample": "full cfg3a (1638 blocks, N=512, fp32) through the reference's torch loop "
-            "(one MKL sgemm per stored block), median of up to 3 reps after a warmup",
+            f"(one MKL sgemm per stored block), median of {reps} reps after a warmup, torch threads = {nthr}",
         }
     return res
 
@@ -286,9 +286,10 @@ def bench_bsr_spmv(steps: int, warmup: int, cpu: bool = False):
 
         xc = x.cpu()
         ptr, col = A.block_row_ptrs, A.block_col_indices
-        secs = cb.time_call(lambda: cb.bsr_spmm(A.blocks, col, ptr, A.shape, 128, xc), reps=3, budget_s=10.0)
+        secs, reps = cb.time_call(lambda: cb.bsr_spmm(A.blocks, col, ptr, A.shape, 128, xc), reps=5, budget_s=10.0)
         res["cpu_baseline"] = {"value": round(byts / secs / 1e9, 2), "unit": "GB/s", "cores": cb.threads(),
-                               "kind": "port", "sample": "the full cfg3 matvec through the reference's torch loop"}
+                               "kind": "port", "sample": f"the full cfg3 matvec through the reference's torch loop, "
+                                                         f"median of {reps} reps after a warmup"}
     out.append(res)
     S, lo, hi = W.spd_bsr(nb=128, b=128, band=2, n_pairs=502)
     Sd = ts.BSRMatrix(S.blocks.to(dev), S.block_col_indices.to(dev), S.block_row_ptrs.to(dev), S.shape, 128)
@@ -312,21 +313,32 @@ def bench_bsr_spmv(steps: int, warmup: int, cpu: bool = False):
                 xx = xx + (2.0 / (lo + hi)) * (rc - cb.bsr_spmm(S.blocks, col, ptr, S.shape, 128, xx[:, None])[:, 0])
             return xx
 
-        secs = cb.time_call(ref_steps, reps=2, budget_s=10.0) / 3
+        secs, reps = cb.time_call(ref_steps, reps=5, budget_s=10.0)
+        secs /= 3
         res["cpu_baseline"] = {"value": round(byts / secs / 1e9, 2), "unit": "GB/s", "cores": cb.threads(),
-                               "kind": "port", "sample": "3 Richardson steps through the reference's torch loop"}
+                               "kind": "port", "sample": f"3 Richardson steps through the reference's torch loop, "
+                                                         f"median of {reps} reps after a warmup"}
     out.append(res)
     return out
 
 
-def bench_spmv(dist: str, index_bits: int, steps: int, warmup: int, cpu: bool = False):
+def bench_spmv(dist: str, index_bits: int, steps: int, warmup: int, cpu: bool = False, plan: str = "always"):
     """CSR SpMV at config 2: algorithmic HBM bytes / kernel time, L2+MALL
-    flushed before every timed launch (the working set fits in the MALL)."""
+    flushed before every timed launch (the working set fits in the MALL).
+
+    plan "always": the column-sorted plan (tsp_csr_colplan_spmv; built once
+    per matrix outside the timed region, its build time reported beside);
+    plan "never": the windowed kernel over the caller's CSR arrays
+    (tsp_csr_spmv, deterministic). `algorithmic_bytes` is the reference
+    layout's traffic (nnz*(4+idx) + (m+1)*idx + 4n + 4m) and defines `value`
+    and `frac_hbm`; `kernel_bytes` is what the kernel itself has to move (the
+    plan's 8-byte entries, x, y and the column groups' partial sums)."""
     import numpy as np
     import torch
 
     import trnsparse_amd as ts
     from trnsparse_amd import workloads as W
+    from trnsparse_amd.hip import dispatch as D
 
     idt = np.int64 if index_bits == 64 else np.int32
     v, c, p, x, shape = W.cfg2_csr(dist=dist, index_dtype=idt)
@@ -336,25 +348,58 @@ def bench_spmv(dist: str, index_bits: int, steps: int, warmup: int, cpu: bool = 
     xd = torch.from_numpy(x).cuda()
     ib = index_bits // 8
     byts = nnz * (4 + ib) + (m + 1) * ib + n * 4 + m * 4
-    flush = make_flush()
-    _, ev_ms = time_gpu(lambda: ts.spmv(A, xd), steps, warmup, flush=flush)
+    prev = D.get_spmv_plan()
+    D.set_spmv_plan(plan)
+    try:
+        build_ms = None
+        kbytes = byts
+        if plan == "always":
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            ts.spmv(A, xd)  # builds the plan
+            torch.cuda.synchronize()
+            build_ms = (time.perf_counter() - t0) * 1e3
+            geom = A._hip_colplan[2]
+            G = int(geom[3])
+            kbytes = nnz * 8 + n * 4 + m * 4 + (2 * G * m * 4 if G > 1 else 0)
+        flush = make_flush()
+        _, ev_ms = time_gpu(lambda: ts.spmv(A, xd), steps, warmup, flush=flush)
+    finally:
+        D.set_spmv_plan(prev)
     gbs = byts / (ev_ms * 1e-3) / 1e9
+    kind = "column-sorted plan" if plan == "always" else "windowed"
     res = {
-        "name": f"csr_spmv cfg2 {dist} int{index_bits}",
+        "name": f"csr_spmv cfg2 {dist} int{index_bits} ({kind})",
         "value": round(gbs, 1),
         "unit": "GB/s",
         "us": round(ev_ms * 1e3, 2),
         "nnz": nnz,
         "algorithmic_bytes": byts,
         "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+        "timing": f"median of {steps} launches, each after a 1 GiB read flush of L2 and MALL",
     }
+    if plan == "always":
+        res["kernel_bytes"] = kbytes
+        res["frac_hbm_kernel_bytes"] = round(kbytes / (ev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        res["plan_build_ms"] = round(build_ms, 2)
+        res["plan_geometry"] = {"rows_per_tile": 1 << int(geom[0]), "cols_per_group": 1 << int(geom[2]),
+                                "groups": G, "tiles": int(geom[4])}
     if cpu:
         from oracle import build as oracle_c
         from oracle import cpu_baseline as cb
 
-        secs = cb.time_call(lambda: oracle_c.csr_spmv_f32(v, c, p, m, x), reps=5, budget_s=10.0)
-        res["cpu_baseline"] = {"value": round(byts / secs / 1e9, 2), "unit": "GB/s", "cores": cb.threads(),
-                               "kind": "port", "sample": "full cfg2 matrix, oracle/csr_spmv.c fp32 OpenMP over rows"}
+        nthr = cb.threads()
+        torch.set_num_threads(nthr)
+        vt, ct, pt, xt = (torch.from_numpy(a) for a in (v, c, p, x))
+        secs, reps = cb.time_call(lambda: cb.spmv(vt, ct, pt, shape, xt), reps=5, budget_s=15.0)
+        res["cpu_baseline"] = {"value": round(byts / secs / 1e9, 2), "unit": "GB/s", "cores": nthr,
+                               "kind": "port",
+                               "sample": f"full cfg2 matrix through the reference's CPU path "
+                                         f"(torch.sparse_csr_tensor @ x, ops.py:25-45), median of {reps} reps "
+                                         f"after a warmup, torch threads = {nthr}"}
+        csecs, creps = cb.time_call(lambda: oracle_c.csr_spmv_f32(v, c, p, m, x), reps=5, budget_s=10.0)
+        res["cpu_c_loop"] = {"value": round(byts / csecs / 1e9, 2), "unit": "GB/s", "cores": nthr,
+                             "sample": f"oracle/csr_spmv.c fp32 OpenMP over rows, median of {creps} reps"}
     return res
 
 
@@ -414,9 +459,10 @@ def bench_screened(steps: int, warmup: int, cpu: bool = False):
     if cpu:
         from oracle import cpu_baseline as cb
 
-        secs = cb.time_call(lambda: cb.screened_spmm(A, diag, B, thr), reps=3, budget_s=20.0)
+        secs, reps = cb.time_call(lambda: cb.screened_spmm(A, diag, B, thr), reps=5, budget_s=20.0)
         res["cpu_baseline"] = {"value": round(flops / secs / 1e9, 2), "unit": "GFLOP/s", "cores": cb.threads(),
-                               "kind": "port", "sample": "full cfg4 through the reference's torch path (mask, A*mask, MKL sgemm)"}
+                               "kind": "port", "sample": f"full cfg4 through the reference's torch path (mask, A*mask, "
+                                                         f"MKL sgemm), median of {reps} reps after a warmup"}
     # the same workload with fp64 A, diag and B (screened_f64_dma)
     A64, d64, B64 = Ad.double(), dd.double(), Bd.double()
     _, ms64 = time_gpu(lambda: ts.screened_spmm(A64, d64, B64, thr), max(2, steps // 2), warmup)
@@ -454,9 +500,11 @@ def bench_attention(steps: int, warmup: int, cpu: bool = False):
 
         b = 128
         ptr, col = mask.block_row_ptrs, mask.block_col_indices
-        secs = cb.time_call(lambda: cb.attention_head(Q[0], K[0], V[0], ptr, col, b, D**-0.5), reps=2, budget_s=20.0)
+        secs, reps = cb.time_call(lambda: cb.attention_head(Q[0], K[0], V[0], ptr, col, b, D**-0.5), reps=5,
+                                  budget_s=20.0)
         res["cpu_baseline"] = {"value": round(flops / H / secs / 1e9, 2), "unit": "GFLOP/s", "cores": cb.threads(),
-                               "kind": "port", "sample": "one head of cfg5 (bf16) through the reference's torch two-pass loops"}
+                               "kind": "port", "sample": f"one head of cfg5 (bf16) through the reference's torch "
+                                                         f"two-pass loops, median of {reps} reps after a warmup"}
     # the same workload with fp32 Q / K / V (bsa_fwd_f32_mfma)
     Qf, Kf, Vf = (t.float() for t in (Qd, Kd, Vd))
     _, ms32 = time_gpu(lambda: ts.block_sparse_attention_tiled(Qf, Kf, Vf, mask), steps, warmup)
@@ -514,11 +562,12 @@ def bench_attention_backward(steps: int, warmup: int, cpu: bool = False):
 
         args = [t[0].cpu() for t in (Qd, Kd, Vd, O, dO)]
         r0, d0 = rm[0].reshape(-1).cpu().to(torch.bfloat16), rd[0].reshape(-1).cpu().to(torch.bfloat16)
-        secs = cb.time_call(lambda: cb.attention_backward_head(*args, mask.block_row_ptrs, mask.block_col_indices, 128,
-                                                               D**-0.5, r0, d0), reps=2, budget_s=20.0)
+        secs, reps = cb.time_call(lambda: cb.attention_backward_head(*args, mask.block_row_ptrs, mask.block_col_indices,
+                                                                     128, D**-0.5, r0, d0), reps=5, budget_s=20.0)
         res["cpu_baseline"] = {"value": round(flops / H / secs / 1e9, 2), "unit": "GFLOP/s", "cores": cb.threads(),
                                "kind": "port",
-                               "sample": "one head of cfg5 (bf16) through the reference's torch backward loops"}
+                               "sample": f"one head of cfg5 (bf16) through the reference's torch backward loops, "
+                                         f"median of {reps} reps after a warmup"}
     return out
 
 
@@ -549,9 +598,10 @@ def bench_formats(steps: int, warmup: int, cpu: bool = False):
         from oracle import cpu_baseline as cb
 
         Dc = D.cpu()
-        secs = cb.time_call(lambda: cb.bsr_from_dense(Dc, 128), reps=2, budget_s=20.0)
+        secs, reps = cb.time_call(lambda: cb.bsr_from_dense(Dc, 128), reps=5, budget_s=20.0)
         res["cpu_baseline"] = {"value": round(byts / secs / 1e9, 2), "unit": "GB/s", "cores": cb.threads(),
-                               "kind": "port", "sample": "the full cfg3 dense matrix through the reference's torch ops"}
+                               "kind": "port", "sample": f"the full cfg3 dense matrix through the reference's torch "
+                                                         f"ops, median of {reps} reps after a warmup"}
     out.append(res)
     csr = ts.from_dense(D)
     nnz = csr.nnz
@@ -715,6 +765,9 @@ def main(argv=None) -> int:
             ("spmv poisson int64", lambda: bench_spmv("poisson", 64, 20, 3, cpu=not args.no_cpu)),
             ("spmv poisson int32", lambda: bench_spmv("poisson", 32, 20, 3)),
             ("spmv zipf int64", lambda: bench_spmv("zipf", 64, 10, 2)),
+            ("spmv windowed poisson int64", lambda: bench_spmv("poisson", 64, 20, 3, plan="never")),
+            ("spmv windowed poisson int32", lambda: bench_spmv("poisson", 32, 20, 3, plan="never")),
+            ("spmv windowed zipf int64", lambda: bench_spmv("zipf", 64, 10, 2, plan="never")),
             ("spmm", lambda: bench_spmm(10, 2)),
             ("bsr bf16", lambda: bench_bsr_bf16(max(5, args.steps // 2), 3)),
             ("bsr f64", lambda: bench_bsr_f64(10, 2)),

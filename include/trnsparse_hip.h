@@ -166,6 +166,47 @@ int tsp_csr_spmv(const void* values, int dtype, const void* col_indices,
                  double alpha, const void* y, double beta, void* out,
                  void* stream);
 
+/* ---- SpMV over a cached column-sorted plan (fp32 values) -------------
+ * Same result as tsp_csr_spmv (reference trnsparse/ops.py:30-48, the
+ * torch.sparse_csr @ x call at :45), computed from a reordered copy of the
+ * matrix built once per pattern: tiles of 2^rbits rows x 2^cbits columns,
+ * each tile's entries sorted by column, 8 bytes per entry (packed row /
+ * column within the tile and the fp32 value), so the x gathers of one
+ * wavefront instruction share cache lines. Row sums of one tile are added
+ * in LDS in a run-dependent order (results may differ between runs in the
+ * last bits; tsp_csr_spmv is the deterministic path).
+ *
+ * geometry (10 int64, host memory), filled by tsp_csr_colplan_geometry:
+ *   [0] rbits   [1] row blocks   [2] cbits   [3] column groups G
+ *   [4] tiles   [5] sort key bits [6] plan bytes  [7] build workspace bytes
+ *   [8] SpMV workspace bytes (G * m * 4; 0 when G == 1)  [9] reserved
+ * rows_per_block_log2 (12..14) and tiles_hint tune the tiling; 0 = auto.
+ * TSP_EUNSUPPORTED when nnz > 2^32 - 1. The plan holds entry positions as
+ * uint32: row_ptrs[m] must be below 2^32. */
+int tsp_csr_colplan_geometry(int64_t m, int64_t n, int64_t nnz,
+                             int rows_per_block_log2, int64_t tiles_hint,
+                             int64_t* geometry);
+
+/* Build the plan (geometry[6] bytes at `plan`, device) from the CSR arrays;
+ * `workspace` (geometry[7] bytes, device) is scratch for the build only. */
+int tsp_csr_colplan_build(const void* values, int dtype,
+                          const void* col_indices, const void* row_ptrs,
+                          int index_type, int64_t m, int64_t n, int64_t nnz,
+                          const int64_t* geometry, void* plan,
+                          void* workspace, void* stream);
+
+/* Copy new values of the same pattern into the plan (one gather pass). */
+int tsp_csr_colplan_refresh(const void* values, int dtype, int64_t m,
+                            int64_t n, int64_t nnz, const int64_t* geometry,
+                            void* plan, void* stream);
+
+/* out (m,) = alpha * A @ x (+ beta * y) over the plan; x (n,), y (m,) or
+ * NULL; workspace: geometry[8] bytes of device memory (NULL if 0). */
+int tsp_csr_colplan_spmv(const void* plan, int dtype, int64_t m, int64_t n,
+                         int64_t nnz, const int64_t* geometry, const void* x,
+                         double alpha, const void* y, double beta, void* out,
+                         void* workspace, void* stream);
+
 /* out (m, ncols; row stride ldo) = alpha * A @ B (+ beta * C);
  * B (n, ncols; stride ldb), C (m, ncols; stride ldc) or NULL. */
 int tsp_csr_spmm(const void* values, int dtype, const void* col_indices,

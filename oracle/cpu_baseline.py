@@ -137,8 +137,9 @@ def bsr_from_dense(A, b, threshold=0.0):
     return grid[keep].contiguous(), cols, ptrs
 
 
-def time_call(fn, reps: int = 3, budget_s: float = 30.0) -> float:
-    """Median wall time (s) of `fn()` after one warmup, within a time budget."""
+def time_call(fn, reps: int = 5, budget_s: float = 30.0) -> tuple[float, int]:
+    """(median wall time in s, number of timed reps) of `fn()` after one
+    untimed warmup call; the rep count is cut so the reps fit `budget_s`."""
     t0 = time.perf_counter()
     fn()
     first = time.perf_counter() - t0
@@ -149,4 +150,4 @@ def time_call(fn, reps: int = 3, budget_s: float = 30.0) -> float:
         fn()
         ts.append(time.perf_counter() - t0)
     ts.sort()
-    return ts[len(ts) // 2]
+    return ts[len(ts) // 2], reps

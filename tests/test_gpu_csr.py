@@ -210,6 +210,19 @@ def test_spmm_gradcheck_f64(hip_backend):
 @pytest.mark.parametrize("dist", ["poisson", "zipf"])
 @pytest.mark.parametrize("index_dtype", [np.int64, np.int32])
 def test_cfg2_full_size(hip_backend, dist, index_dtype):
+    """The windowed kernel (deterministic: a repeat call is bit-identical);
+    the column-sorted plan path has its own tests (test_gpu_csr_colplan.py)."""
+    from trnsparse_amd.hip import dispatch as D
+
+    prev = D.get_spmv_plan()
+    D.set_spmv_plan("never")
+    try:
+        _cfg2_windowed(dist, index_dtype)
+    finally:
+        D.set_spmv_plan(prev)
+
+
+def _cfg2_windowed(dist, index_dtype):
     v, c, p, x, shape = W.cfg2_csr(dist=dist, index_dtype=index_dtype)
     A = W.csr_matrix_from_arrays(v, c, p, shape, device="cuda")
     xd = torch.from_numpy(x).cuda()

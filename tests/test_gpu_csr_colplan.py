@@ -1,0 +1,174 @@
+"""GPU parity of the column-sorted SpMV plan (tsp_csr_colplan_*) against the oracle.
+
+The plan path computes the reference's spmv (trnsparse/ops.py:30-48) from a
+reordered copy of the matrix; these tests drive it through the public
+`spmv` with the plan forced on, and through the C ABI for the tiling hints.
+Cases: tile edges (m, n not multiples of the tile), empty rows and empty
+tiles, one row / one column, int32 and int64 indices, alpha / beta / y,
+new values on a cached pattern (refresh), NaN in x at unreferenced
+columns (lanes past a tile's end must not leak into a row), and the
+full-size BASELINE config 2 (Poisson and Zipf rows) against the C oracle
+with a float64 accumulator plus the checksum property sum(y) = colsum(A).x.
+fp32 tolerance: max error <= 1e-4 relative to the (|A|.|x|)_i scale.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import trnsparse_amd as ts
+from oracle import build as oracle_c
+from oracle import ref
+from trnsparse_amd import workloads as W
+from trnsparse_amd.hip import _lib
+from trnsparse_amd.hip import dispatch as D
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+@pytest.fixture
+def plan_always(hip_backend):
+    prev = D.get_spmv_plan()
+    D.set_spmv_plan("always")
+    yield
+    D.set_spmv_plan(prev)
+
+
+def _random(m, n, lens, seed, index_dtype=np.int64):
+    rng = np.random.default_rng(seed)
+    v, c, p = W.random_csr(lens, n, rng)
+    return v, c.astype(index_dtype), p.astype(index_dtype), rng
+
+
+def _check(v, c, p, shape, x, got, alpha=1.0, y=None, beta=0.0):
+    exact = ref.csr_spmv(v, c.astype(np.int64), p.astype(np.int64), shape, x, alpha, y, beta)
+    scale = ref.csr_spmv(v, c.astype(np.int64), p.astype(np.int64), shape, x, alpha, y, beta, absolute=True)
+    err = ref.scaled_error(got, exact, scale)
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize(
+    "m,n,mean,seed",
+    [
+        (5000, 7000, 9, 0),        # one row block, several column groups
+        (40000, 33333, 12, 1),     # m, n not multiples of the tile
+        (17000, 1, 1, 2),          # a single column
+        (1, 50000, 3000, 3),       # a single long row
+        (70000, 200000, 2, 4),     # sparse: tiles with few or no entries
+    ],
+)
+@pytest.mark.parametrize("index_dtype", [np.int64, np.int32])
+def test_colplan_spmv_shapes(plan_always, m, n, mean, seed, index_dtype):
+    rng0 = np.random.default_rng(100 + seed)
+    lens = np.minimum(rng0.poisson(mean, m), n)
+    lens[rng0.random(m) < 0.1] = 0                    # empty rows
+    v, c, p, rng = _random(m, n, lens, seed, index_dtype)
+    A = W.csr_matrix_from_arrays(v, c, p, (m, n), device="cuda")
+    x = rng.standard_normal(n).astype(np.float32)
+    got = ts.spmv(A, torch.from_numpy(x).cuda())
+    assert getattr(A, "_hip_colplan", None) is not None or len(v) == 0
+    _check(v, c, p, (m, n), x, got.cpu().numpy())
+    y = rng.standard_normal(m).astype(np.float32)
+    got = ts.spmv(A, torch.from_numpy(x).cuda(), alpha=-1.5, y=torch.from_numpy(y).cuda(), beta=0.25)
+    _check(v, c, p, (m, n), x, got.cpu().numpy(), -1.5, y, 0.25)
+
+
+@pytest.mark.parametrize("rbits,tiles", [(12, 0), (13, 7), (14, 1), (14, 600), (12, 4096)])
+def test_colplan_tiling_hints_via_c_abi(hip_backend, rbits, tiles):
+    """Every tiling the geometry allows gives the oracle's result; G == 1
+    (no partial vectors) and G > 1 (partials summed by the second kernel)."""
+    m, n = 30000, 90000
+    rng0 = np.random.default_rng(rbits * 1000 + tiles)
+    v, c, p, rng = _random(m, n, rng0.poisson(11, m), rbits + tiles)
+    A = W.csr_matrix_from_arrays(v, c, p, (m, n), device="cuda")
+    vals, cols, ptrs, _ = D._csr_device(A, torch.device("cuda"))
+    prev = D.get_spmv_plan()
+    D.set_spmv_plan("always")
+    try:
+        geom, plan = D._csr_colplan(A, vals, cols, ptrs, torch.device("cuda"), rbits, tiles)
+    finally:
+        D.set_spmv_plan(prev)
+    assert geom[0] == rbits and geom[4] == geom[1] * geom[3]
+    assert geom[3] == -(-n // (1 << int(geom[2])))
+    x = rng.standard_normal(n).astype(np.float32)
+    y = rng.standard_normal(m).astype(np.float32)
+    xd, yd = torch.from_numpy(x).cuda(), torch.from_numpy(y).cuda()
+    out = torch.empty(m, device="cuda")
+    work = torch.empty(max(1, int(geom[8])), dtype=torch.uint8, device="cuda")
+    _lib.call("tsp_csr_colplan_spmv", plan.data_ptr(), _lib.TSP_F32, m, n, len(v), geom.ctypes.data, xd.data_ptr(),
+              0.5, yd.data_ptr(), -2.0, out.data_ptr(), work.data_ptr(), _lib.stream_handle(torch.device("cuda")))
+    _check(v, c, p, (m, n), x, out.cpu().numpy(), 0.5, y, -2.0)
+    # a geometry that does not belong to the shape is refused on the host
+    bad = geom.copy()
+    bad[3] += 1
+    with pytest.raises(RuntimeError, match="geometry"):
+        _lib.call("tsp_csr_colplan_spmv", plan.data_ptr(), _lib.TSP_F32, m, n, len(v), bad.ctypes.data,
+                  xd.data_ptr(), 1.0, None, 0.0, out.data_ptr(), work.data_ptr(), 0)
+
+
+def test_colplan_refresh_follows_new_values(plan_always):
+    m, n = 20000, 20000
+    v, c, p, rng = _random(m, n, np.full(m, 16), 7)
+    A = W.csr_matrix_from_arrays(v, c, p, (m, n), device="cuda")
+    x = rng.standard_normal(n).astype(np.float32)
+    xd = torch.from_numpy(x).cuda()
+    _check(v, c, p, (m, n), x, ts.spmv(A, xd).cpu().numpy())
+    plan_before = A._hip_colplan[3]
+    v2 = rng.standard_normal(len(v)).astype(np.float32)
+    A.values.copy_(torch.from_numpy(v2))           # in place: same pattern, new values
+    _check(v2, c, p, (m, n), x, ts.spmv(A, xd).cpu().numpy())
+    assert A._hip_colplan[3] is plan_before        # regathered, not rebuilt
+
+
+def test_colplan_nan_at_unreferenced_columns(plan_always):
+    """x holds NaN / inf at every column no entry references; lanes past a
+    tile's end (which read padding or the next tile) must not reach a row."""
+    m, n = 9000, 40000
+    v, c, p, rng = _random(m, n, np.full(m, 5), 8)
+    x = np.full(n, np.nan, np.float32)
+    x[1::3] = np.inf
+    used = np.unique(c)
+    x[used] = rng.standard_normal(len(used)).astype(np.float32)
+    A = W.csr_matrix_from_arrays(v, c, p, (m, n), device="cuda")
+    got = ts.spmv(A, torch.from_numpy(x).cuda()).cpu().numpy()
+    assert np.isfinite(got).all()
+    _check(v, c, p, (m, n), x, got)
+
+
+def test_colplan_auto_mode_builds_on_reuse(hip_backend):
+    prev = D.get_spmv_plan()
+    D.set_spmv_plan("auto")
+    try:
+        m = n = 1 << 15
+        v, c, p, rng = _random(m, n, np.full(m, 12), 9)
+        A = W.csr_matrix_from_arrays(v, c, p, (m, n), device="cuda")
+        xd = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).cuda()
+        first = ts.spmv(A, xd)
+        assert getattr(A, "_hip_colplan", None) is None      # one-off use: windowed kernel
+        second = ts.spmv(A, xd)
+        assert getattr(A, "_hip_colplan", None) is not None  # reused unchanged: plan built
+        _check(v, c, p, (m, n), xd.cpu().numpy(), second.cpu().numpy())
+        torch.testing.assert_close(first, second, rtol=1e-5, atol=1e-4)
+    finally:
+        D.set_spmv_plan(prev)
+
+
+@pytest.mark.parametrize("dist", ["poisson", "zipf"])
+@pytest.mark.parametrize("index_dtype", [np.int64, np.int32])
+def test_colplan_cfg2_full_size(plan_always, dist, index_dtype):
+    v, c, p, x, shape = W.cfg2_csr(dist=dist, index_dtype=index_dtype)
+    A = W.csr_matrix_from_arrays(v, c, p, shape, device="cuda")
+    xd = torch.from_numpy(x).cuda()
+    got = ts.spmv(A, xd).cpu().numpy()
+    assert A._hip_colplan is not None
+    exact = oracle_c.csr_spmv_f64(v, c, p, shape[0], x)
+    scale = oracle_c.csr_spmv_f64(v, c, p, shape[0], x, absolute=True)
+    assert ref.scaled_error(got, exact, scale) <= TOL
+    colsum = np.bincount(c.astype(np.int64), weights=v.astype(np.float64), minlength=shape[1])
+    assert abs(got.astype(np.float64).sum() - colsum @ x) <= TOL * float(np.abs(v).astype(np.float64) @ np.abs(x[c]))
+    again = ts.spmv(A, xd).cpu().numpy()
+    assert ref.scaled_error(again, exact, scale) <= TOL

@@ -229,6 +229,47 @@ def test_spmv_vs_scipy_with_empty_rows():
     np.testing.assert_allclose(ref.csr_spmv(v, c, p, sh, x), sp.csr_matrix(A) @ x, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("idx", [np.int64, np.int32])
+def test_c_oracle_spmv_vs_ref(idx):
+    """oracle/csr_spmv.c (the full-size cfg2 oracle) against ref.csr_spmv and
+    scipy: int32 and int64 indices, alpha / beta / y, absolute=True, empty
+    rows (first, middle, last) and a row longer than 4096 entries."""
+    from oracle import build as oracle_c
+
+    rng = np.random.default_rng(11)
+    m, n = 700, 9000
+    lens = rng.integers(0, 40, m)
+    lens[[0, 350, m - 1]] = 0
+    lens[123] = 5000
+    lens[124] = 4097
+    ptr = np.zeros(m + 1, np.int64)
+    np.cumsum(lens, out=ptr[1:])
+    cols = np.concatenate([np.sort(rng.choice(n, size=k, replace=False)) for k in lens]).astype(np.int64)
+    vals = rng.standard_normal(len(cols)).astype(np.float32)
+    x = rng.standard_normal(n).astype(np.float32)
+    y = rng.standard_normal(m).astype(np.float32)
+    c, p = cols.astype(idx), ptr.astype(idx)
+    dense = sp.csr_matrix((vals.astype(np.float64), cols, ptr), shape=(m, n))
+    for alpha, yy, beta in ((1.0, None, 0.0), (-2.5, y, 0.75), (0.5, y, 0.0)):
+        exact = ref.csr_spmv(vals, cols, ptr, (m, n), x, alpha=alpha, y=yy, beta=beta)
+        got64 = oracle_c.csr_spmv_f64(vals, c, p, m, x, alpha=alpha, y=yy, beta=beta)
+        np.testing.assert_allclose(got64, exact, rtol=1e-12, atol=1e-12)
+        expect = alpha * (dense @ x.astype(np.float64))
+        if yy is not None and beta != 0.0:
+            expect = expect + beta * yy.astype(np.float64)
+        np.testing.assert_allclose(got64, expect, rtol=1e-12, atol=1e-12)
+        scale = ref.csr_spmv(vals, cols, ptr, (m, n), x, alpha=alpha, y=yy, beta=beta, absolute=True)
+        np.testing.assert_allclose(oracle_c.csr_spmv_f64(vals, c, p, m, x, alpha=alpha, y=yy, beta=beta,
+                                                         absolute=True), scale, rtol=1e-12, atol=1e-12)
+        got32 = oracle_c.csr_spmv_f32(vals, c, p, m, x, alpha=alpha, y=yy, beta=beta)
+        assert got32.dtype == np.float32
+        assert ref.scaled_error(got32, exact, scale) < 1e-5
+        for r in (0, 350, m - 1):  # empty rows: beta * y, or exactly zero
+            assert got32[r] == (np.float32(beta) * y[r] if yy is not None and beta else 0.0)
+    # the long rows reach the C loop's end: a wrong bound drops their tails
+    assert abs(got64[123] - exact[123]) <= 1e-9 * scale[123]
+
+
 def test_spmm_known_answer_and_scipy():
     # reference tests/test_ops.py:61-67: 2*I@ones + 0.5*10 = 7
     v, c, p, sh = _csr(np.eye(2))

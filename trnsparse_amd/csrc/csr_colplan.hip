@@ -1,0 +1,673 @@
+// CSR SpMV over a cached column-sorted plan ("colplan") for gfx950.
+//
+// Semantics are the reference's spmv (trnsparse/ops.py:30-48):
+//   out = alpha * (A @ x)   then  + beta * y   only if y and beta != 0.
+//
+// Why a plan. With the reference's CSR layout every nonzero gathers one
+// 4-byte x value from a random column; on cfg2 (1 M x 1 M, 16 per row,
+// uniform columns) each gather is its own L1->L2 request (18.8 M requests
+// per SpMV, L2 hit rate 82 %, the misses refetching x lines from the MALL).
+// The plan reorders the nonzeros once per pattern so that the gathers of
+// one wavefront instruction fall on a few x lines:
+//
+//   tile (rb, g) = rows [rb*R, rb*R + R) x columns [g*Cg, g*Cg + Cg)
+//   a tile's entries sorted by column (ties in row order), cut into epochs
+//   of E = 4096 entries (the last one padded)
+//
+// A 64-lane instruction then covers 64 consecutive nonzeros in column
+// order of R rows: at cfg2 density (R = 8192 rows, 0.125 nonzeros per
+// column) about 512 columns, 16 lines of 128 bytes, coalesced by the address
+// unit into 16 requests instead of 64 (measured: 3.9 M L1->L2 requests per
+// SpMV instead of 18.8 M). Tiles of 8192 rows keep a workgroup's LDS at
+// 64 KiB, so two workgroups share a CU and one's barriers overlap the
+// other's work (77.5 us on cfg2 against 85-89 us for 16384-row tiles with
+// one 1024-thread workgroup per CU).
+//
+// Row sums without atomics. Float add atomics in LDS (ds_add_f32) run at a
+// small fraction of the rate of other LDS operations on gfx950 (measured:
+// they made this kernel 2.2x slower than plain LDS read-modify-write, with
+// or without bank conflicts), so each epoch runs in two phases separated by
+// a barrier:
+//   phase 1  wavefronts take 64-entry chunks round robin, gather x, and
+//            store product and row into LDS at the entry's position in row
+//            order (the plan's per-epoch inverse permutation, 16 bits per
+//            entry);
+//   phase 2  wavefront w reads positions w*E/W .. (w+1)*E/W - 1 of the
+//            epoch (consecutive: no bank conflicts), adds runs of equal rows
+//            with a segmented scan across lanes, and adds each run into the
+//            tile's LDS row sum with a plain read-modify-write: a row's run
+//            belongs to one wavefront, except its first run, which goes to a
+//            carry slot that wavefront 0 adds after the epoch's closing
+//            barrier, in wavefront order.
+// Every sum is taken in a fixed order, so results are deterministic.
+// With G > 1 column groups each tile writes its row sums to a partial
+// vector and a second kernel adds the G partials per row in group order
+// and applies alpha / beta.
+//
+// Plan buffer (device): toff (T+1 int64, first sorted entry of each tile),
+// eoff (T+1 int64, first epoch of each tile), ent (8 bytes per padded entry:
+// value bits << 32 | row_in_tile << cbits | column_in_group), pinv (uint16
+// per padded entry: the entry's position in the epoch's row order, stored in
+// the SpMV kernel's lane order), pos (uint32 per padded entry: position in
+// the caller's CSR arrays, for new values on the same pattern; 0xffffffff
+// for padding). The three per-entry arrays hold one more epoch of zeros
+// past the last tile's, which the SpMV kernel's prefetch reads when a tile
+// has no epoch left to prefetch.
+#include "common.h"
+
+#include <rocprim/device/device_radix_sort.hpp>
+
+namespace {
+
+constexpr int GEOM_RBITS = 0, GEOM_NRB = 1, GEOM_CBITS = 2, GEOM_G = 3, GEOM_T = 4, GEOM_KEYBITS = 5,
+              GEOM_PLAN_BYTES = 6, GEOM_BUILD_BYTES = 7, GEOM_SPMV_BYTES = 8, GEOM_PMAX = 9;
+
+constexpr int EBITS = 12;
+constexpr int E = 1 << EBITS;  // entries per epoch
+constexpr uint32_t POS_PAD = 0xffffffffu;
+constexpr int SPMV_NT = 512;                   // threads of the SpMV workgroup
+constexpr int SPMV_W = SPMV_NT / 64;           // wavefronts of the SpMV workgroup
+
+int ilog2_ceil(int64_t v) {
+  int b = 0;
+  while (((int64_t)1 << b) < v) ++b;
+  return b;
+}
+
+int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+
+__device__ inline int64_t upper_bound_i64(const int64_t* __restrict__ a, int64_t n, int64_t v) {
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (a[mid] <= v)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+// ------------------------------------------------------------ plan build
+
+// One thread per row: sort key (tile, column in group) and payload
+// (row in tile, CSR position) of each of the row's entries.
+template <typename IdxT, typename K>
+__global__ __launch_bounds__(256) void colplan_keys_kernel(const IdxT* __restrict__ col, const IdxT* __restrict__ ptr,
+                                                           int64_t m, int rbits, int cbits, int64_t G,
+                                                           K* __restrict__ keys, uint64_t* __restrict__ payload) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= m) return;
+  const int64_t base = (int64_t)ptr[0];
+  const int64_t a = (int64_t)ptr[r], e = (int64_t)ptr[r + 1];
+  const int64_t rb = r >> rbits;
+  const uint64_t rl = (uint64_t)(r & (((int64_t)1 << rbits) - 1)) << 32;
+  const int64_t cmask = ((int64_t)1 << cbits) - 1;
+  for (int64_t p = a; p < e; ++p) {  // p: position in the caller's arrays; p - base: position in the sort
+    const int64_t c = (int64_t)col[p];
+    const int64_t tile = rb * G + (c >> cbits);
+    keys[p - base] = (K)((tile << cbits) | (c & cmask));
+    payload[p - base] = rl | (uint64_t)p;
+  }
+}
+
+// toff[t] = first sorted entry of tile t (lower bound of t << cbits).
+template <typename K>
+__global__ __launch_bounds__(256) void colplan_offsets_kernel(const K* __restrict__ keys, int64_t nnz, int cbits,
+                                                              int64_t T, int64_t* __restrict__ toff) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t > T) return;
+  const K target = (K)t << cbits;
+  int64_t lo = 0, hi = nnz;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (keys[mid] < target)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  toff[t] = lo;
+}
+
+// eoff = exclusive scan of the tiles' epoch counts (one workgroup).
+__global__ __launch_bounds__(1024) void colplan_epochs_kernel(const int64_t* __restrict__ toff, int64_t T,
+                                                              int64_t* __restrict__ eoff) {
+  __shared__ int64_t part[1024];
+  const int tid = threadIdx.x;
+  const int64_t per = (T + 1023) / 1024;
+  const int64_t t0 = tid * per, t1 = t0 + per < T ? t0 + per : T;
+  int64_t s = 0;
+  for (int64_t t = t0; t < t1; ++t) s += (toff[t + 1] - toff[t] + E - 1) >> EBITS;
+  part[tid] = s;
+  __syncthreads();
+  if (tid == 0) {
+    int64_t run = 0;
+    for (int i = 0; i < 1024; ++i) {
+      const int64_t v = part[i];
+      part[i] = run;
+      run += v;
+    }
+  }
+  __syncthreads();
+  s = part[tid];
+  for (int64_t t = t0; t < t1; ++t) {
+    eoff[t] = s;
+    s += (toff[t + 1] - toff[t] + E - 1) >> EBITS;
+  }
+  if (tid == 1023) eoff[T] = s;
+}
+
+__global__ __launch_bounds__(256) void colplan_fill_kernel(uint64_t* __restrict__ ent, uint16_t* __restrict__ pinv,
+                                                           uint32_t* __restrict__ pos, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  ent[i] = 0;
+  pinv[i] = 0;
+  pos[i] = POS_PAD;
+}
+
+// Sorted entry i of tile t goes to padded position (eoff[t] + j / E) * E + j % E,
+// j = i - toff[t].
+template <typename K>
+__global__ __launch_bounds__(256) void colplan_scatter_kernel(const K* __restrict__ keys,
+                                                              const uint64_t* __restrict__ payload,
+                                                              const float* __restrict__ vals, int64_t nnz, int cbits,
+                                                              const int64_t* __restrict__ toff,
+                                                              const int64_t* __restrict__ eoff, int64_t T,
+                                                              uint64_t* __restrict__ ent, uint32_t* __restrict__ pos) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nnz) return;
+  const int64_t t = upper_bound_i64(toff, T + 1, i) - 1;
+  const int64_t j = i - toff[t];
+  const int64_t P = ((eoff[t] + (j >> EBITS)) << EBITS) + (j & (E - 1));
+  const uint64_t pl = payload[i];
+  const uint32_t p = (uint32_t)pl;
+  const uint32_t rl = (uint32_t)(pl >> 32);
+  const uint32_t cin = (uint32_t)(keys[i] & (((K)1 << cbits) - 1));
+  ent[P] = ((uint64_t)__builtin_bit_cast(uint32_t, vals[p]) << 32) | (uint64_t)((rl << cbits) | cin);
+  pos[P] = p;
+}
+
+// One workgroup per epoch: each entry's position in the epoch's (row,
+// position) order, by a bitonic sort of the E keys row << EBITS | position
+// in LDS. Padding positions take row 2^rbits and sort last. Entry i =
+// (j * W + w) * 64 + l (chunk j of wavefront w, lane l in the SpMV kernel's
+// phase 1) stores its position in the 32-bit word ((j / 2) * W + w) * 64 +
+// l, low half for even j, high half for odd j: a lane loads the positions
+// of two of its entries with one dword.
+__global__ __launch_bounds__(1024) void colplan_perm_kernel(const uint64_t* __restrict__ ent,
+                                                            const int64_t* __restrict__ toff,
+                                                            const int64_t* __restrict__ eoff, int64_t T, int rbits,
+                                                            int cbits, uint16_t* __restrict__ pinv) {
+  __shared__ uint32_t key[E];
+  const int tid = threadIdx.x;
+  const int64_t ep = blockIdx.x;
+  if (ep >= eoff[T]) return;  // the grid covers the epoch count's upper bound
+  const int64_t t = upper_bound_i64(eoff, T + 1, ep) - 1;
+  const int64_t left = (toff[t + 1] - toff[t]) - ((ep - eoff[t]) << EBITS);
+  const int cnt = left < E ? (int)left : E;
+  const uint64_t* __restrict__ e = ent + (ep << EBITS);
+  for (int i = tid; i < E; i += 1024) {
+    const uint32_t row = i < cnt ? (uint32_t)e[i] >> cbits : (1u << rbits);
+    key[i] = (row << EBITS) | (uint32_t)i;
+  }
+  __syncthreads();
+  for (int k = 2; k <= E; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = tid; i < E; i += 1024) {
+        const int l = i ^ j;
+        if (l > i) {
+          const uint32_t a = key[i], b = key[l];
+          if ((a > b) == ((i & k) == 0)) {
+            key[i] = b;
+            key[l] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  uint16_t* __restrict__ out = pinv + (ep << EBITS);
+  for (int s = tid; s < E; s += 1024) {
+    const int i = (int)(key[s] & (E - 1));
+    const int c = i >> 6, j = c / SPMV_W, w = c % SPMV_W, l = i & 63;
+    out[2 * (((j >> 1) * SPMV_W + w) * 64 + l) + (j & 1)] = (uint16_t)s;
+  }
+}
+
+__global__ __launch_bounds__(256) void colplan_refresh_kernel(const float* __restrict__ vals,
+                                                              const uint32_t* __restrict__ pos, int64_t n,
+                                                              uint64_t* __restrict__ ent) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t p = pos[i];
+  const uint32_t bits = p == POS_PAD ? 0u : __builtin_bit_cast(uint32_t, vals[p]);
+  ent[i] = ((uint64_t)bits << 32) | (ent[i] & 0xffffffffull);
+}
+
+// ----------------------------------------------------------------- SpMV
+
+// One step of a segmented inclusive scan with DPP: add the value of the
+// lane the DPP control names when it holds the same row (rows ascend
+// across the lanes, so equal rows mean every lane between is in the run).
+template <int CTRL, int ROW_MASK>
+__device__ inline float seg_step(float s, uint32_t r) {
+  const uint32_t ro = (uint32_t)__builtin_amdgcn_update_dpp((int)0xffffffffu, (int)r, CTRL, ROW_MASK, 0xf, false);
+  const float so = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), CTRL, ROW_MASK,
+                                                                         0xf, false));
+  return ro == r ? s + so : s;
+}
+
+// Inclusive sums of runs of equal r over the 64 lanes, without LDS: shifts
+// by 1, 2, 4, 8 inside each 16-lane row, then lane 15 of each row into the
+// next row and lane 31 into the upper half (row_bcast:15 / :31).
+__device__ inline float seg_scan(float s, uint32_t r) {
+  s = seg_step<0x111, 0xf>(s, r);  // row_shr:1
+  s = seg_step<0x112, 0xf>(s, r);  // row_shr:2
+  s = seg_step<0x114, 0xf>(s, r);  // row_shr:4
+  s = seg_step<0x118, 0xf>(s, r);  // row_shr:8
+  s = seg_step<0x142, 0xa>(s, r);  // row_bcast:15 -> rows 1 and 3
+  s = seg_step<0x143, 0xc>(s, r);  // row_bcast:31 -> rows 2 and 3
+  return s;
+}
+
+template <int RBITS, int NT>
+__global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restrict__ ent,
+                                                       const uint16_t* __restrict__ pinv,
+                                                       const int64_t* __restrict__ toff,
+                                                       const int64_t* __restrict__ eoff, const float* __restrict__ x,
+                                                       int64_t m, int cbits, int64_t G, int64_t nrb, int64_t pmax,
+                                                       int xcd_map,
+                                                       float alpha, const float* __restrict__ y, float beta,
+                                                       float* __restrict__ out, float* __restrict__ partial) {
+  constexpr int R = 1 << RBITS;
+  constexpr int W = NT / 64;
+  constexpr int K = E / 64 / W;  // chunks per wavefront in each phase
+  constexpr int SPAN = E / W;    // phase-2 positions per wavefront
+  static_assert(W == SPMV_W, "the plan's position layout is made for this workgroup size");
+  constexpr uint32_t NONE = 0xffffffffu;
+  __shared__ float acc[R + 1];  // acc[R]: the padding positions' row
+  __shared__ u32x2 slot[E];     // (product bits, row) of each epoch position
+  __shared__ uint32_t crow[W];
+  __shared__ float cval[W];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t T = nrb * G;
+  // q runs over tiles group-major; with xcd_map, XCD k (= blockIdx % 8)
+  // takes the k-th eighth of that order, so an XCD works on one column
+  // group (or a run of consecutive groups) and keeps its x slice in L2.
+  const int64_t q = xcd_map ? (int64_t)(blockIdx.x & 7) * (T >> 3) + (blockIdx.x >> 3) : (int64_t)blockIdx.x;
+  const int64_t g = q / nrb, rb = q - g * nrb;
+  const int64_t t = rb * G + g;
+
+  for (int i = tid; i <= R; i += NT) acc[i] = 0.f;
+  if (tid < W) crow[tid] = NONE;
+
+  const int64_t cnt_t = toff[t + 1] - toff[t];
+  const int64_t ep0 = eoff[t], nep = eoff[t + 1] - ep0;
+  const float* __restrict__ xg = x + (g << cbits);
+  const uint32_t cmask = (1u << cbits) - 1u;
+
+  // Entries and the epoch's row-order positions stream two epochs ahead:
+  // epoch k's registers (set A for even k, set B for odd k) are refilled
+  // with epoch k + 2 as soon as phase 1 of epoch k has consumed them. Loads
+  // issue in the order gathers(k), prefetch(k + 2), and vector memory loads
+  // complete in order, so the waits of both phases (for the gathers, for
+  // the prefetch of two epochs back) never cover the newest stream loads.
+  uint64_t evA[K], evB[K];
+  uint32_t pwA[K / 2], pwB[K / 2];
+  // k past the tile's last epoch: the plan's zero epoch after all tiles
+  auto load_epoch = [&](uint64_t (&ev)[K], uint32_t (&pw)[K / 2], int64_t k) {
+    const int64_t eb = k < nep ? (ep0 + k) << EBITS : pmax;  // past the tile's end: the zero epoch
+    const uint64_t* __restrict__ pe = ent + eb + w * 64 + lane;
+#pragma unroll
+    for (int j = 0; j < K; ++j) ev[j] = __builtin_nontemporal_load(pe + j * W * 64);
+    const uint32_t* __restrict__ pp = (const uint32_t*)(pinv + eb) + w * 64 + lane;
+#pragma unroll
+    for (int j = 0; j < K / 2; ++j) pw[j] = __builtin_nontemporal_load(pp + j * W * 64);
+  };
+  if (nep > 0) {
+    load_epoch(evA, pwA, 0);
+    load_epoch(evB, pwB, 1);
+  }
+  __syncthreads();
+
+  auto epoch = [&](uint64_t (&ev)[K], uint32_t (&pw)[K / 2], int64_t k) {
+    const int64_t left = cnt_t - (k << EBITS);
+    const int cnt = left < E ? (int)left : E;
+    // ---- phase 1: products and rows in column order
+    float xv[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) xv[j] = xg[(uint32_t)ev[j] & cmask];
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const int i = (j * W + w) * 64 + lane;
+      const float pr = __builtin_bit_cast(float, (uint32_t)(ev[j] >> 32)) * xv[j];
+      slot[(pw[j >> 1] >> (16 * (j & 1))) & 0xffffu] =
+          u32x2{__builtin_bit_cast(uint32_t, pr), i < cnt ? (uint32_t)ev[j] >> cbits : (uint32_t)R};
+    }
+    // unconditional (past the tile's end it reads the zero epoch), so no
+    // path without these loads makes the compiler wait for them early
+    load_epoch(ev, pw, k + 2);
+    __syncthreads();
+    // ---- phase 2: runs of equal rows in row order
+    // All LDS reads first: the K positions' (product, row), then the row
+    // sums of those rows (each row of the span is written by this
+    // wavefront at most once per epoch, so the values read here are the
+    // ones to add to). Then per chunk: segmented scan, and run tails write
+    // sum + old value. A run still open at the chunk's end is pending:
+    // (row, partial sum, old row sum) carried in scalars into the next
+    // chunk. A wavefront's first run (w > 0) goes to its carry slot, whether
+    // or not the previous wavefront's span ends in the same row; wavefront 0
+    // adds the carries after the epoch's barrier.
+    u32x2 sl[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) sl[j] = slot[w * SPAN + j * 64 + lane];
+    float av[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) av[j] = acc[sl[j].y];
+    uint32_t pend_row = NONE, carry_row = NONE;
+    float pend = 0.f, pend_acc = 0.f, carry_val = 0.f;
+    bool pend_carry = false;
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const uint32_t r = sl[j].y;
+      float s = seg_scan(__builtin_bit_cast(float, sl[j].x), r);
+      // run heads: lane 0 and every lane whose left neighbour (wave_shr:1)
+      // holds another row; tails: the lane before a head, and lane 63
+      const uint32_t rp = (uint32_t)__builtin_amdgcn_update_dpp((int)NONE, (int)r, 0x138, 0xf, 0xf, false);
+      const uint64_t tails = (__ballot(rp != r) >> 1) | (1ull << 63);
+      const int ft = (int)__builtin_ctzll(tails);  // tail lane of the chunk's first run
+      const uint32_t r0 = __builtin_amdgcn_readfirstlane(r);
+      const bool merge = pend_row == r0;  // the chunk's first run continues the pending run
+      if (!merge && pend_row != NONE) {   // the pending run ended with the previous chunk
+        if (pend_carry) {
+          carry_row = pend_row;
+          carry_val = pend;
+        } else if (lane == 0) {
+          acc[pend_row] = pend_acc + pend;
+        }
+      }
+      if (merge && r == r0) s += pend;
+      const bool carry_first = j == 0 ? w > 0 : (merge && pend_carry);
+      if (carry_first && ft < 63) {
+        carry_row = r0;
+        carry_val = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), ft));
+      }
+      if (((tails >> lane) & 1ull) && lane < 63 && !(carry_first && r == r0)) acc[r] = av[j] + s;
+      const uint32_t r63 = __builtin_amdgcn_readlane(r, 63);
+      pend_carry = r63 == r0 && carry_first;
+      pend_row = r63;
+      pend = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), 63));
+      pend_acc = merge && r63 == r0 ? pend_acc
+                                   : __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, av[j]), 63));
+    }
+    if (pend_carry) {
+      carry_row = pend_row;
+      carry_val = pend;
+    } else if (lane == 0) {
+      acc[pend_row] = pend_acc + pend;
+    }
+    if (lane == 0) {
+      crow[w] = carry_row;
+      cval[w] = carry_val;
+    }
+    __syncthreads();
+    if (w == 0) {  // the carries, in wavefront order: rows ascend with w
+      const uint32_t cr = lane < W ? crow[lane] : NONE;
+      const float cs = seg_scan(lane < W ? cval[lane] : 0.f, cr);
+      const uint32_t crn = (uint32_t)__builtin_amdgcn_update_dpp((int)NONE, (int)cr, 0x130, 0xf, 0xf, false);
+      if (cr != NONE && (lane == 63 || crn != cr)) acc[cr] += cs;
+    }
+  };
+
+  for (int64_t k = 0; k < nep; k += 2) {
+    epoch(evA, pwA, k);
+    if (k + 1 < nep) epoch(evB, pwB, k + 1);
+  }
+  __syncthreads();
+
+  const int64_t r0 = rb << RBITS;
+  if (G == 1) {
+    for (int i = tid; i < R; i += NT) {
+      const int64_t r = r0 + i;
+      if (r < m) {
+        float res = alpha * acc[i];
+        if (y) res = res + beta * y[r];
+        out[r] = res;
+      }
+    }
+  } else {
+    float* __restrict__ pg = partial + g * m;
+    for (int i = tid; i < R; i += NT) {
+      const int64_t r = r0 + i;
+      if (r < m) pg[r] = acc[i];
+    }
+  }
+}
+
+// out[r] = alpha * (partial[0][r] + ... + partial[G-1][r]) (+ beta * y[r]),
+// the groups added in increasing order.
+__global__ __launch_bounds__(256) void colplan_finish_f32(const float* __restrict__ partial, int64_t m, int64_t G,
+                                                          float alpha, const float* __restrict__ y, float beta,
+                                                          float* __restrict__ out) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= m) return;
+  float s = partial[r];
+  for (int64_t g = 1; g < G; ++g) s += partial[g * m + r];
+  float res = alpha * s;
+  if (y) res = res + beta * y[r];
+  out[r] = res;
+}
+
+// ------------------------------------------------------------- geometry
+
+constexpr int RBITS_MAX = 14;          // 16384 rows: 64 KiB of fp32 row sums per workgroup
+constexpr int RBITS_DEFAULT = 13;      // 8192 rows: 32 KiB, so two workgroups share a CU
+constexpr int64_t TILES_TARGET = 512;  // two workgroups per CU
+
+int geometry(int64_t m, int64_t n, int64_t nnz, int rbits_hint, int64_t tiles_hint, int64_t* g) {
+  if (m <= 0 || n <= 0 || nnz < 0) return tsp::fail(TSP_EINVAL, "tsp_csr_colplan_geometry: bad size");
+  if (nnz > (int64_t)UINT32_MAX - 1) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_colplan: more than 2^32-2 entries");
+  const int rbits = rbits_hint > 0 ? rbits_hint : RBITS_DEFAULT;
+  if (rbits < 12 || rbits > RBITS_MAX)
+    return tsp::fail(TSP_EINVAL, "tsp_csr_colplan: rows per tile 2^%d outside 2^12..2^14", rbits);
+  const int64_t nrb = tsp::ceil_div(m, (int64_t)1 << rbits);
+  const int64_t target = tiles_hint > 0 ? tiles_hint : TILES_TARGET;
+  int64_t gw = tsp::ceil_div(target, nrb);
+  if (gw < 1) gw = 1;
+  int cbits = ilog2_ceil(tsp::ceil_div(n, gw));
+  if (cbits < 6) cbits = 6;
+  if (rbits + cbits > 32) cbits = 32 - rbits;
+  const int64_t G = tsp::ceil_div(n, (int64_t)1 << cbits);
+  const int64_t T = nrb * G;
+  if (T > INT32_MAX / 2) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_colplan: too many tiles");
+  const int keybits = ilog2_ceil(T + 1) + cbits;
+  if (keybits > 63) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_colplan: key wider than 63 bits");
+  const int64_t pmax = nnz + T * (int64_t)E;  // padded entries, at most
+  if ((pmax >> EBITS) > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_colplan: too many epochs");
+  const int64_t ksz = keybits <= 32 ? 4 : 8;
+  size_t tmp = 0;
+  hipError_t e = keybits <= 32
+                     ? rocprim::radix_sort_pairs(nullptr, tmp, (const uint32_t*)nullptr, (uint32_t*)nullptr,
+                                                 (const uint64_t*)nullptr, (uint64_t*)nullptr, (size_t)nnz, 0, keybits)
+                     : rocprim::radix_sort_pairs(nullptr, tmp, (const uint64_t*)nullptr, (uint64_t*)nullptr,
+                                                 (const uint64_t*)nullptr, (uint64_t*)nullptr, (size_t)nnz, 0, keybits);
+  if (e != hipSuccess) return tsp::check_hip(e, "tsp_csr_colplan: sort size query");
+  g[GEOM_RBITS] = rbits;
+  g[GEOM_NRB] = nrb;
+  g[GEOM_CBITS] = cbits;
+  g[GEOM_G] = G;
+  g[GEOM_T] = T;
+  g[GEOM_KEYBITS] = keybits;
+  g[GEOM_PLAN_BYTES] =
+      2 * align256((T + 1) * 8) + align256((pmax + E) * 8) + align256((pmax + E) * 2) + align256((pmax + E) * 4);
+  g[GEOM_BUILD_BYTES] = 2 * align256(nnz * ksz) + 2 * align256(nnz * 8) + align256((int64_t)tmp);
+  g[GEOM_SPMV_BYTES] = G > 1 ? G * m * 4 : 0;
+  g[GEOM_PMAX] = pmax;
+  return TSP_OK;
+}
+
+struct PlanView {
+  int64_t* toff;
+  int64_t* eoff;
+  uint64_t* ent;
+  uint16_t* pinv;
+  uint32_t* pos;
+  int64_t pmax;
+};
+
+PlanView plan_view(void* plan, const int64_t* g) {
+  uint8_t* p = (uint8_t*)plan;
+  const int64_t T = g[GEOM_T];
+  PlanView v;
+  v.pmax = g[GEOM_PMAX];
+  v.toff = (int64_t*)p;
+  p += align256((T + 1) * 8);
+  v.eoff = (int64_t*)p;
+  p += align256((T + 1) * 8);
+  v.ent = (uint64_t*)p;
+  p += align256((v.pmax + E) * 8);
+  v.pinv = (uint16_t*)p;
+  p += align256((v.pmax + E) * 2);
+  v.pos = (uint32_t*)p;
+  return v;
+}
+
+// The geometry comes back from the caller: everything the kernels index
+// with must follow from (m, n, nnz) and the two tiling choices.
+int check_geom(const char* who, int64_t m, int64_t n, int64_t nnz, const int64_t* geom) {
+  if (!geom) return tsp::fail(TSP_EINVAL, "%s: null geometry", who);
+  if (m <= 0 || n <= 0 || nnz < 0) return tsp::fail(TSP_EINVAL, "%s: bad size", who);
+  const int64_t rbits = geom[GEOM_RBITS], cbits = geom[GEOM_CBITS];
+  if (rbits < 12 || rbits > RBITS_MAX || cbits < 6 || rbits + cbits > 32 ||
+      geom[GEOM_NRB] != tsp::ceil_div(m, (int64_t)1 << rbits) ||
+      geom[GEOM_G] != tsp::ceil_div(n, (int64_t)1 << cbits) || geom[GEOM_T] != geom[GEOM_NRB] * geom[GEOM_G] ||
+      geom[GEOM_KEYBITS] != ilog2_ceil(geom[GEOM_T] + 1) + cbits || geom[GEOM_PMAX] != nnz + geom[GEOM_T] * (int64_t)E)
+    return tsp::fail(TSP_EINVAL, "%s: geometry does not belong to a %lld x %lld matrix with %lld entries", who,
+                     (long long)m, (long long)n, (long long)nnz);
+  return TSP_OK;
+}
+
+template <typename IdxT, typename K>
+int build_typed(const float* vals, const void* col, const void* ptr, int64_t m, int64_t nnz, const int64_t* g,
+                void* plan, void* work, hipStream_t st) {
+  const int rbits = (int)g[GEOM_RBITS], cbits = (int)g[GEOM_CBITS];
+  const int64_t G = g[GEOM_G], T = g[GEOM_T];
+  uint8_t* w = (uint8_t*)work;
+  K* kin = (K*)w;
+  w += align256(nnz * (int64_t)sizeof(K));
+  K* kout = (K*)w;
+  w += align256(nnz * (int64_t)sizeof(K));
+  uint64_t* pin = (uint64_t*)w;
+  w += align256(nnz * 8);
+  uint64_t* pout = (uint64_t*)w;
+  w += align256(nnz * 8);
+  void* tmp = w;
+  size_t tmp_bytes = 0;
+  hipError_t e = rocprim::radix_sort_pairs(nullptr, tmp_bytes, kin, kout, pin, pout, (size_t)nnz, 0,
+                                           (int)g[GEOM_KEYBITS], st);
+  if (e != hipSuccess) return tsp::check_hip(e, "tsp_csr_colplan_build: sort size query");
+  PlanView v = plan_view(plan, g);
+  hipLaunchKernelGGL(colplan_fill_kernel, dim3((unsigned)tsp::ceil_div(v.pmax + E, 256)), dim3(256), 0, st, v.ent,
+                     v.pinv, v.pos, v.pmax + E);
+  int rc = tsp::check_launch("colplan_fill launch");
+  if (rc) return rc;
+  if (nnz > 0) {
+    hipLaunchKernelGGL((colplan_keys_kernel<IdxT, K>), dim3((unsigned)tsp::ceil_div(m, 256)), dim3(256), 0, st,
+                       (const IdxT*)col, (const IdxT*)ptr, m, rbits, cbits, G, kin, pin);
+    rc = tsp::check_launch("colplan_keys launch");
+    if (rc) return rc;
+    e = rocprim::radix_sort_pairs(tmp, tmp_bytes, kin, kout, pin, pout, (size_t)nnz, 0, (int)g[GEOM_KEYBITS], st);
+    if (e != hipSuccess) return tsp::check_hip(e, "tsp_csr_colplan_build: radix sort");
+  }
+  hipLaunchKernelGGL((colplan_offsets_kernel<K>), dim3((unsigned)tsp::ceil_div(T + 1, 256)), dim3(256), 0, st,
+                     kout, nnz, cbits, T, v.toff);
+  rc = tsp::check_launch("colplan_offsets launch");
+  if (rc) return rc;
+  hipLaunchKernelGGL(colplan_epochs_kernel, dim3(1), dim3(1024), 0, st, v.toff, T, v.eoff);
+  rc = tsp::check_launch("colplan_epochs launch");
+  if (rc || nnz == 0) return rc;
+  hipLaunchKernelGGL((colplan_scatter_kernel<K>), dim3((unsigned)tsp::ceil_div(nnz, 256)), dim3(256), 0, st, kout,
+                     pout, vals, nnz, cbits, v.toff, v.eoff, T, v.ent, v.pos);
+  rc = tsp::check_launch("colplan_scatter launch");
+  if (rc) return rc;
+  // one workgroup per epoch; the grid covers the upper bound pmax / E
+  hipLaunchKernelGGL(colplan_perm_kernel, dim3((unsigned)(v.pmax >> EBITS)), dim3(1024), 0, st, v.ent, v.toff,
+                     v.eoff, T, rbits, cbits, v.pinv);
+  return tsp::check_launch("colplan_perm launch");
+}
+
+template <int RBITS>
+void launch_spmv(const PlanView& v, const float* x, int64_t m, const int64_t* g, float alpha, const float* y,
+                 float beta, float* out, float* partial, hipStream_t st) {
+  const int64_t T = g[GEOM_T];
+  const int xcd_map = (T % 8) == 0 ? 1 : 0;
+  hipLaunchKernelGGL((colplan_spmv_f32<RBITS, SPMV_NT>), dim3((unsigned)T), dim3(SPMV_NT), 0, st, v.ent, v.pinv, v.toff,
+                     v.eoff, x, m, (int)g[GEOM_CBITS], g[GEOM_G], g[GEOM_NRB], v.pmax, xcd_map, alpha, y, beta, out,
+                     partial);
+}
+
+}  // namespace
+
+extern "C" int tsp_csr_colplan_geometry(int64_t m, int64_t n, int64_t nnz, int rows_per_block_log2,
+                                        int64_t tiles_hint, int64_t* geometry_out) {
+  if (!geometry_out) return tsp::fail(TSP_EINVAL, "tsp_csr_colplan_geometry: null output");
+  if (tiles_hint < 0 || rows_per_block_log2 < 0) return tsp::fail(TSP_EINVAL, "tsp_csr_colplan_geometry: negative hint");
+  return geometry(m, n, nnz, rows_per_block_log2, tiles_hint, geometry_out);
+}
+
+extern "C" int tsp_csr_colplan_build(const void* values, int dtype, const void* col_indices, const void* row_ptrs,
+                                     int index_type, int64_t m, int64_t n, int64_t nnz, const int64_t* geometry,
+                                     void* plan, void* workspace, void* stream) {
+  if (dtype != TSP_F32) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_colplan_build: dtype %d (the plan holds fp32 values)", dtype);
+  if (index_type != TSP_I32 && index_type != TSP_I64) return tsp::fail(TSP_EINVAL, "tsp_csr_colplan_build: bad index_type");
+  int rc = check_geom("tsp_csr_colplan_build", m, n, nnz, geometry);
+  if (rc) return rc;
+  if (!row_ptrs || !plan || !workspace || (nnz > 0 && (!values || !col_indices)))
+    return tsp::fail(TSP_EINVAL, "tsp_csr_colplan_build: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  const bool k32 = geometry[GEOM_KEYBITS] <= 32;
+  if (index_type == TSP_I64)
+    return k32 ? build_typed<int64_t, uint32_t>((const float*)values, col_indices, row_ptrs, m, nnz, geometry, plan, workspace, st)
+               : build_typed<int64_t, uint64_t>((const float*)values, col_indices, row_ptrs, m, nnz, geometry, plan, workspace, st);
+  return k32 ? build_typed<int32_t, uint32_t>((const float*)values, col_indices, row_ptrs, m, nnz, geometry, plan, workspace, st)
+             : build_typed<int32_t, uint64_t>((const float*)values, col_indices, row_ptrs, m, nnz, geometry, plan, workspace, st);
+}
+
+extern "C" int tsp_csr_colplan_refresh(const void* values, int dtype, int64_t m, int64_t n, int64_t nnz,
+                                       const int64_t* geometry, void* plan, void* stream) {
+  if (dtype != TSP_F32) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_colplan_refresh: dtype %d (the plan holds fp32 values)", dtype);
+  int rc = check_geom("tsp_csr_colplan_refresh", m, n, nnz, geometry);
+  if (rc) return rc;
+  if (nnz == 0) return TSP_OK;
+  if (!values || !plan) return tsp::fail(TSP_EINVAL, "tsp_csr_colplan_refresh: null pointer");
+  PlanView v = plan_view(plan, geometry);
+  hipLaunchKernelGGL(colplan_refresh_kernel, dim3((unsigned)tsp::ceil_div(v.pmax, 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const float*)values, v.pos, v.pmax, v.ent);
+  return tsp::check_launch("colplan_refresh launch");
+}
+
+extern "C" int tsp_csr_colplan_spmv(const void* plan, int dtype, int64_t m, int64_t n, int64_t nnz,
+                                    const int64_t* geometry, const void* x, double alpha, const void* y, double beta,
+                                    void* out, void* workspace, void* stream) {
+  if (dtype != TSP_F32) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_colplan_spmv: dtype %d (the plan holds fp32 values)", dtype);
+  int rc = check_geom("tsp_csr_colplan_spmv", m, n, nnz, geometry);
+  if (rc) return rc;
+  if (!plan || !x || !out) return tsp::fail(TSP_EINVAL, "tsp_csr_colplan_spmv: null pointer");
+  const int64_t G = geometry[GEOM_G];
+  if (G > 1 && !workspace) return tsp::fail(TSP_EINVAL, "tsp_csr_colplan_spmv: null workspace (%lld column groups)", (long long)G);
+  hipStream_t st = (hipStream_t)stream;
+  const float* yy = (y && beta != 0.0) ? (const float*)y : nullptr;
+  PlanView v = plan_view((void*)plan, geometry);
+  switch (geometry[GEOM_RBITS]) {
+    case 12: launch_spmv<12>(v, (const float*)x, m, geometry, (float)alpha, yy, (float)beta, (float*)out, (float*)workspace, st); break;
+    case 13: launch_spmv<13>(v, (const float*)x, m, geometry, (float)alpha, yy, (float)beta, (float*)out, (float*)workspace, st); break;
+    default: launch_spmv<14>(v, (const float*)x, m, geometry, (float)alpha, yy, (float)beta, (float*)out, (float*)workspace, st); break;
+  }
+  rc = tsp::check_launch("colplan_spmv launch");
+  if (rc || G == 1) return rc;
+  hipLaunchKernelGGL(colplan_finish_f32, dim3((unsigned)tsp::ceil_div(m, 256)), dim3(256), 0, st,
+                     (const float*)workspace, m, G, (float)alpha, yy, (float)beta, (float*)out);
+  return tsp::check_launch("colplan_finish launch");
+}

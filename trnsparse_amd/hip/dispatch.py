@@ -277,7 +277,7 @@ def _csr_device(A, dev: torch.device):
     return res
 
 
-def _csr_forward(vals, cols, ptrs, win, shape, X, alpha, Y, beta, dev):
+def _csr_forward(vals, cols, ptrs, win, shape, X, alpha, Y, beta, dev, colplan=None):
     m, n = shape
     if vals.dtype != X.dtype:
         raise RuntimeError(f"CSR values dtype {vals.dtype} and dense operand dtype {X.dtype} differ")
@@ -293,6 +293,12 @@ def _csr_forward(vals, cols, ptrs, win, shape, X, alpha, Y, beta, dev):
         out = torch.empty(m, dtype=vals.dtype, device=dev)
         if use_y and Yd.shape != (m,):
             Yd = Yd.expand(m).contiguous()
+        if colplan is not None:
+            geom, plan = colplan
+            work = torch.empty(max(1, int(geom[8])) // 4, dtype=torch.float32, device=dev) if geom[8] else None
+            _lib.call("tsp_csr_colplan_spmv", plan.data_ptr(), code, m, n, vals.numel(), geom.ctypes.data,
+                      Xd.data_ptr(), float(alpha), _lib.ptr(Yd), float(beta), out.data_ptr(), _lib.ptr(work), st)
+            return out
         _lib.call("tsp_csr_spmv", vals.data_ptr(), code, cols.data_ptr(), ptrs.data_ptr(), icode, m, n, vals.numel(),
                   win.data_ptr(), Xd.data_ptr(), float(alpha), _lib.ptr(Yd), float(beta), out.data_ptr(), st)
         return out
@@ -303,6 +309,71 @@ def _csr_forward(vals, cols, ptrs, win, shape, X, alpha, Y, beta, dev):
     _lib.call("tsp_csr_spmm", vals.data_ptr(), code, cols.data_ptr(), ptrs.data_ptr(), icode, m, n, vals.numel(),
               Xd.data_ptr(), ncols, ncols, float(alpha), _lib.ptr(Yd), ncols, float(beta), out.data_ptr(), ncols, st)
     return out
+
+
+# SpMV over the column-sorted plan (tsp_csr_colplan_*): "auto" builds the
+# plan the second time an unchanged fp32 matrix with at least
+# COLPLAN_MIN_NNZ entries meets a vector (a one-off matrix keeps the
+# windowed kernel, which needs no reordered copy), "always" on first use,
+# "never" not at all. New values on a cached pattern are regathered into
+# the plan without sorting again.
+_SPMV_PLAN_MODES = ("auto", "always", "never")
+_spmv_plan_mode = "auto"
+COLPLAN_MIN_NNZ = 1 << 18
+
+
+def set_spmv_plan(mode: str) -> None:
+    """Select when spmv uses the column-sorted plan: "auto", "always", "never"."""
+    global _spmv_plan_mode
+    if mode not in _SPMV_PLAN_MODES:
+        raise AssertionError(f"spmv plan mode must be one of {_SPMV_PLAN_MODES}, got {mode!r}")
+    _spmv_plan_mode = mode
+
+
+def get_spmv_plan() -> str:
+    return _spmv_plan_mode
+
+
+def _csr_colplan(A, vals, cols, ptrs, dev, rows_per_block_log2: int = 0, tiles_hint: int = 0):
+    """The column-sorted SpMV plan of A, cached on the matrix, or None when
+    the plan does not apply (mode, dtype, size) or is not due yet."""
+    mode = _spmv_plan_mode
+    nnz = vals.numel()
+    if mode == "never" or vals.dtype != torch.float32 or nnz == 0:
+        return None
+    if mode == "auto" and nnz < COLPLAN_MIN_NNZ:
+        return None
+    m, n = A.shape
+    skey = (str(dev), rows_per_block_log2, tiles_hint) + _key(A.col_indices, A.row_ptrs)
+    vkey = _key(A.values)
+    cached = getattr(A, "_hip_colplan", None)
+    if cached is not None and cached[0] == skey:
+        _, ckey, geom, plan, uses = cached
+        if ckey != vkey:
+            _lib.call("tsp_csr_colplan_refresh", vals.data_ptr(), _lib.TSP_F32, m, n, nnz, geom.ctypes.data,
+                      plan.data_ptr(), _lib.stream_handle(dev))
+        A._hip_colplan = (skey, vkey, geom, plan, uses + 1)
+        return geom, plan
+    if mode == "auto":
+        seen = getattr(A, "_hip_colplan_seen", None)
+        if seen != (skey, vkey):
+            try:
+                A._hip_colplan_seen = (skey, vkey)
+            except AttributeError:
+                pass
+            return None
+    geom = np.zeros(10, dtype=np.int64)
+    _lib.call("tsp_csr_colplan_geometry", m, n, nnz, rows_per_block_log2, tiles_hint, geom.ctypes.data)
+    plan = torch.empty(int(geom[6]), dtype=torch.uint8, device=dev)
+    work = torch.empty(int(geom[7]), dtype=torch.uint8, device=dev)
+    _lib.call("tsp_csr_colplan_build", vals.data_ptr(), _lib.TSP_F32, cols.data_ptr(), ptrs.data_ptr(),
+              _lib.index_code(cols.dtype), m, n, nnz, geom.ctypes.data, plan.data_ptr(), work.data_ptr(),
+              _lib.stream_handle(dev))
+    try:
+        A._hip_colplan = (skey, vkey, geom, plan, 1)
+    except AttributeError:
+        pass
+    return geom, plan
 
 
 def _csr_plan(ptrs: torch.Tensor, m: int, nnz: int, dev: torch.device) -> torch.Tensor:
@@ -324,9 +395,9 @@ class _CSRMatMulFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, values, col_indices, row_ptrs, shape, X, alpha, Y, beta, prepared):
-        vals, cols, ptrs, win = prepared
+        vals, cols, ptrs, win, colplan = prepared
         dev = vals.device
-        out = _csr_forward(vals, cols, ptrs, win, shape, X, alpha, Y, beta, dev)
+        out = _csr_forward(vals, cols, ptrs, win, shape, X, alpha, Y, beta, dev, colplan)
         ctx.save_for_backward(values, X)
         ctx.pattern = (cols, ptrs)
         ctx.shape, ctx.alpha, ctx.beta, ctx.has_y = shape, alpha, beta, Y is not None and beta != 0.0
@@ -370,6 +441,8 @@ def _csr_apply(A, X, alpha, Y, beta):
     dev = _target_device(X, A.values)
     with torch.cuda.device(dev):
         prepared = _csr_device(A, dev)
+        colplan = _csr_colplan(A, *prepared[:3], dev) if X.dim() == 1 else None
+        prepared = prepared + (colplan,)
         return _CSRMatMulFunction.apply(A.values, A.col_indices, A.row_ptrs, tuple(A.shape), X, alpha, Y, beta, prepared)
 
 

@@ -246,6 +246,23 @@ int tsp_screened_spmm(const void* A, int dtype, int64_t lda, const void* diag,
                       const void* B, int64_t ldb, int64_t ncols, void* C,
                       int64_t ldc, void* workspace, void* stream);
 
+/* tsp_screened_spmm without the workspace argument: no counterpart in the
+ * reference. For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): the
+ * workspace lives in a 1 MiB device array of the library, one per GPU, kept
+ * until the process ends. m is limited to
+ * tsp_screened_spmm_noalloc_max_rows(diag_dtype) rows (a larger m returns
+ * TSP_EINVAL). The call allocates and frees nothing. Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams or
+ * threads) race; serialize them. Same results as tsp_screened_spmm. */
+int64_t tsp_screened_spmm_noalloc_max_rows(int diag_dtype);
+
+int tsp_screened_spmm_noalloc(const void* A, int dtype, int64_t lda,
+                              const void* diag, int diag_dtype,
+                              double threshold_sqrt, int64_t m,
+                              const void* B, int64_t ldb, int64_t ncols,
+                              void* C, int64_t ldc, void* stream);
+
 /* ======================================================================
  * Block-sparse attention forward, per head h < n_heads:
  *   O[h] = softmax_rows(scale * Q[h] K[h]^T restricted to the stored mask

@@ -76,6 +76,24 @@ def test_argument_validation_is_host_side():
     assert lib.tsp_csr_sddmm(None, None, 1, 4, 4, 0, None, 8, None, 8, 8, 0, 1.0, None, None) == 0  # nothing to do
 
 
+@pytest.mark.skipif(not LIB.exists(), reason="library not built (run __graft_entry__.build())")
+def test_screened_noalloc_size_limit_is_host_side():
+    """The allocation-free screened SpMM refuses m past its scratch before any
+    device work (dummy non-null pointers: nothing is dereferenced)."""
+    from trnsparse_amd.hip import _lib
+
+    lib = _lib.load()
+    dummy = ctypes.c_void_p(256)
+    for code in (_lib.TSP_F32, _lib.TSP_F64):
+        mmax = lib.tsp_screened_spmm_noalloc_max_rows(code)
+        assert mmax >= 4096  # BASELINE config 4 fits
+        st = lib.tsp_screened_spmm_noalloc(dummy, 0, mmax + 128, dummy, code, 1e-5, mmax + 128, dummy, 8, 8, dummy, 8,
+                                           None)
+        assert st == -1 and b"scratch" in lib.tsp_last_error()
+    assert lib.tsp_screened_spmm_noalloc_max_rows(7) == -1
+    assert lib.tsp_screened_spmm_noalloc(None, 0, 4, None, 0, 0.0, 4, None, 0, 0, None, 0, None) == 0  # no columns
+
+
 def _plan(cp, H, S, b):
     import numpy as np
 

@@ -27,6 +27,8 @@
 //   screened_f64_dma    fp64 (even m and strides): the same structure on
 //                       v_mfma_f64_16x16x4_f64 (mfma_f64.h operand tiles).
 //   screened_generic    other or unaligned operands: one thread per output.
+#include <atomic>
+
 #include "lds_dma.h"
 #include "mfma_f32.h"
 #include "mfma_f64.h"
@@ -50,10 +52,8 @@ __global__ __launch_bounds__(TILE) void screened_q(const QT* __restrict__ diag, 
   __shared__ QT red[TILE / 64];
   const int64_t i = (int64_t)blockIdx.x * TILE + threadIdx.x;
   QT q = 0;
-  if (i < m) {
-    q = qsqrt<QT>(diag[i]);
-    Q[i] = q;
-  }
+  if (i < m) q = qsqrt<QT>(diag[i]);
+  Q[i] = q;  // rows past m (the last tile's tail) hold 0: every workspace word is written
   // max ignoring NaN (a NaN Q never passes the compare)
   QT mx = q == q ? q : (QT)0;
   for (int o = 32; o > 0; o >>= 1) {
@@ -487,12 +487,83 @@ int launch(const void* A, int dtype, int64_t lda, const void* diag, double thr_s
   return tsp::check_launch("screened_generic launch");
 }
 
+// ------------------------------------------------ allocation-free variant
+//
+// tsp_screened_spmm_noalloc keeps the workspace (Q and the per-tile maxima)
+// in this file-scope device array instead of caller memory. Each GPU holds
+// its own copy for the life of the process; its device address is looked up
+// once per device with hipGetSymbolAddress (the array's name is only a
+// host-side stand-in) and cached. Every call on a GPU shares that GPU's
+// array: calls that overlap on one GPU (other streams, other threads) race.
+// screened_q rewrites every word the kernels read, so nothing needs
+// clearing between calls.
+constexpr int64_t SCREENED_SCRATCH_BYTES = 1 << 20;
+constexpr int SCRATCH_MAX_DEVICES = 64;
+static __device__ __align__(256) uint8_t scratch[SCREENED_SCRATCH_BYTES];
+static std::atomic<void*> g_scratch_ptr[SCRATCH_MAX_DEVICES];
+
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  int rc = tsp::check_hip(hipGetDevice(&dev), "tsp_screened_spmm_noalloc: hipGetDevice");
+  if (rc) return rc;
+  if (dev < 0 || dev >= SCRATCH_MAX_DEVICES)
+    return tsp::fail(TSP_EUNSUPPORTED, "tsp_screened_spmm_noalloc: device %d past the %d supported", dev,
+                     SCRATCH_MAX_DEVICES);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {  // first call on this device (a racing thread stores the same address)
+    rc = tsp::check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "tsp_screened_spmm_noalloc: hipGetSymbolAddress");
+    if (rc) return rc;
+    if (!p) return tsp::fail(TSP_EHIP, "tsp_screened_spmm_noalloc: null scratch address");
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return TSP_OK;
+}
+
+int64_t workspace_bytes(int64_t m, int diag_dtype) {
+  const int64_t nmt = tsp::ceil_div(m, TILE);
+  return (nmt * TILE + nmt) * (diag_dtype == TSP_F64 ? 8 : 4);
+}
+
+int check_args(const char* who, const void* A, int dtype, int64_t lda, const void* diag, int diag_dtype, int64_t m,
+               const void* B, int64_t ldb, int64_t ncols, const void* C, int64_t ldc) {
+  if (dtype != TSP_F32 && dtype != TSP_F64) return tsp::fail(TSP_EUNSUPPORTED, "%s: dtype %d not supported", who, dtype);
+  if (diag_dtype != TSP_F32 && diag_dtype != TSP_F64)
+    return tsp::fail(TSP_EUNSUPPORTED, "%s: diag dtype %d not supported", who, diag_dtype);
+  if (m < 0 || ncols < 0) return tsp::fail(TSP_EINVAL, "%s: negative size", who);
+  if (lda < m || ldb < ncols || ldc < ncols) return tsp::fail(TSP_EINVAL, "%s: leading dimension too small", who);
+  if (m > 0 && ncols > 0 && (!A || !diag || !B || !C)) return tsp::fail(TSP_EINVAL, "%s: null pointer", who);
+  return TSP_OK;
+}
+
 }  // namespace
+
+extern "C" int64_t tsp_screened_spmm_noalloc_max_rows(int diag_dtype) {
+  if (diag_dtype != TSP_F32 && diag_dtype != TSP_F64) return -1;
+  const int64_t per_tile = (TILE + 1) * (diag_dtype == TSP_F64 ? 8 : 4);
+  return (SCREENED_SCRATCH_BYTES / per_tile) * TILE;
+}
+
+extern "C" int tsp_screened_spmm_noalloc(const void* A, int dtype, int64_t lda, const void* diag, int diag_dtype,
+                                         double threshold_sqrt, int64_t m, const void* B, int64_t ldb, int64_t ncols,
+                                         void* C, int64_t ldc, void* stream) {
+  int rc = check_args("tsp_screened_spmm_noalloc", A, dtype, lda, diag, diag_dtype, m, B, ldb, ncols, C, ldc);
+  if (rc) return rc;
+  if (m == 0 || ncols == 0) return TSP_OK;
+  if (workspace_bytes(m, diag_dtype) > SCREENED_SCRATCH_BYTES)
+    return tsp::fail(TSP_EINVAL, "tsp_screened_spmm_noalloc: m = %lld needs %lld bytes of scratch, more than its %lld",
+                     (long long)m, (long long)workspace_bytes(m, diag_dtype), (long long)SCREENED_SCRATCH_BYTES);
+  void* ws = nullptr;
+  rc = scratch_on_current_device(&ws);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  return diag_dtype == TSP_F32 ? launch<float>(A, dtype, lda, diag, threshold_sqrt, m, B, ldb, ncols, C, ldc, ws, st)
+                               : launch<double>(A, dtype, lda, diag, threshold_sqrt, m, B, ldb, ncols, C, ldc, ws, st);
+}
 
 extern "C" int64_t tsp_screened_workspace_size(int64_t m, int diag_dtype) {
   if (m < 0 || (diag_dtype != TSP_F32 && diag_dtype != TSP_F64)) return -1;
-  const int64_t nmt = tsp::ceil_div(m, TILE);
-  return (nmt * TILE + nmt) * (diag_dtype == TSP_F64 ? 8 : 4);
+  return workspace_bytes(m, diag_dtype);
 }
 
 extern "C" int tsp_screened_spmm(const void* A, int dtype, int64_t lda, const void* diag, int diag_dtype,

@@ -72,6 +72,8 @@ def test_reference_grid(hip_backend, m_blocks, n_blocks, N, density):
         ((40, 40), 8, 12, 0.1),  # sparse, :85-93
         ((200, 137), 128, 64, 1.0),  # unaligned 128-blocks (MFMA kernel bounds)
         ((300, 260), 128, 10, 1.0),  # N not a multiple of 4 (padded B panels)
+        ((300, 260), 128, 11, 1.0),  # odd N: the fp32 kernel's unpaired last-column stores
+        ((256, 384), 128, 129, 0.7),  # odd N past one column tile
         ((384, 256), 128, 200, 0.6),  # partial column tile
         ((256, 256), 64, 96, 0.7),  # block size 64 (generic kernel)
     ],
@@ -226,6 +228,15 @@ def test_cfg3b_bf16_full_size(hip_backend):
     exact, scale = _oracle(A, B, rows=rows)
     got = torch.cat([C[r * 128 : (r + 1) * 128] for r in rows]).cpu().numpy()
     assert ref.scaled_error(got, exact, scale) <= TOL_F32
+    # linearity over every row at full size: C @ 1 = A @ (B @ 1), the right
+    # side through the fp32 kernel on the exactly widened blocks
+    ones = torch.ones(B.shape[1], 1, dtype=torch.float64)
+    lhs = C.double().cpu() @ ones
+    A32 = ts.BSRMatrix(A.blocks.float(), A.block_col_indices, A.block_row_ptrs, A.shape, 128)
+    rhs = ts.bsr_spmm(A32, (B.double() @ ones).float().cuda()).double().cpu()
+    sc = torch.from_numpy(ref.bsr_spmm(A32.blocks.numpy(), A.block_col_indices.numpy(), A.block_row_ptrs.numpy(),
+                                       A.shape, 128, np.abs(B.float().numpy()).sum(1, keepdims=True), absolute=True))
+    assert ((lhs - rhs).abs() / sc.clamp_min(1e-30)).max().item() <= TOL_F32
 
 
 def test_fp16_widened(hip_backend):

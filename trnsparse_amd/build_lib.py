@@ -48,6 +48,52 @@ def _sources() -> list[pathlib.Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
+# The direct-to-LDS load helpers (csrc/lds_dma.h) set M0 inside inline asm,
+# which the compiler does not track (M0 is a reserved register: its clobber
+# is ignored). That is only safe while no instruction the compiler generates
+# for those kernels keeps a value in M0, so every build emits their gfx950
+# assembly and fails if an instruction outside the asm blocks names m0.
+# (The compiler's own LDS-load builtins track M0 but also make it wait for
+# every outstanding load before each LDS read: measured +31 % on the bf16
+# BSR kernel at cfg3b.)
+DMA_HEADER = "lds_dma.h"
+
+
+def m0_uses_outside_asm(asm_text: str) -> list[str]:
+    """Instructions outside ;;#ASMSTART / ;;#ASMEND that read or write M0."""
+    import re
+
+    bad, in_asm = [], False
+    for line in asm_text.splitlines():
+        t = line.strip()
+        if t.startswith(";;#ASMSTART"):
+            in_asm = True
+            continue
+        if t.startswith(";;#ASMEND"):
+            in_asm = False
+            continue
+        if in_asm or not t or t.startswith((";", ".", "//")) or t.endswith(":"):
+            continue
+        code = t.split(";", 1)[0]
+        if re.search(r"\bm0\b", code):
+            bad.append(t)
+    return bad
+
+
+def _check_m0(src: pathlib.Path, verbose: bool) -> None:
+    asm = BUILD / (src.stem + ".s")
+    cmd = [HIPCC, *CFLAGS, *EXTRA.get(src.name, []), "--cuda-device-only", "-S", str(src), "-o", str(asm)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed on {src.name}:\n{r.stdout}{r.stderr}")
+    bad = m0_uses_outside_asm(asm.read_text())
+    if bad:
+        raise RuntimeError(f"{src.name}: compiler-generated code uses M0, which the inline-asm LDS loads of "
+                           f"{DMA_HEADER} overwrite:\n" + "\n".join(bad[:10]))
+
+
 def _compile(src: pathlib.Path, verbose: bool) -> pathlib.Path:
     obj = BUILD / (src.stem + ".o")
     cmd = [HIPCC, *CFLAGS, *EXTRA.get(src.name, []), "-c", str(src), "-o", str(obj)]
@@ -69,8 +115,12 @@ def build(verbose: bool = False, jobs: int | None = None) -> pathlib.Path:
     BUILD.mkdir(exist_ok=True)
     srcs = _sources()
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2)))
+    dma = [s for s in srcs if DMA_HEADER in s.read_text()]
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
+        checks = [ex.submit(_check_m0, s, verbose) for s in dma]
         objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
+        for c in checks:
+            c.result()
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *map(str, objs)]
     if verbose:

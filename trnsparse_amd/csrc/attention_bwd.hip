@@ -39,6 +39,8 @@
 // consecutive keys, 4 chunks); slot = chunk ^ (((key % 4) << 2) | ((key / 4) %
 // 4)) is conflict-free for both on the 64-bank LDS. V in the row pass is only
 // read as rows: slot = chunk ^ (key % 16).
+#include <new>
+
 #include "common.h"
 
 #include "lds_dma.h"
@@ -1243,8 +1245,15 @@ extern "C" int64_t tsp_bsa_bwd_plan(const int64_t* col_ptrs, int64_t n_block_col
   int64_t L = (int64_t)((double)n_heads * (double)nnzb / 256.0 / 2.0 + 0.999);
   L = L < 4 ? 4 : (L > abw::SEG_MAX ? abw::SEG_MAX : L);
   struct Item { int32_t col, p0, p1, slot, weight; };
-  Item* items = new Item[ncols + nnzb / L + 1];
-  int32_t* splits = new int32_t[4 * (nnzb / (L + 1) + 1)];
+  // no exception crosses the C ABI: allocation failure is a status
+  Item* items = new (std::nothrow) Item[ncols + nnzb / L + 1];
+  int32_t* splits = new (std::nothrow) int32_t[4 * (nnzb / (L + 1) + 1)];
+  if (!items || !splits) {
+    delete[] items;
+    delete[] splits;
+    tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_bwd_plan: host memory for %lld items", (long long)(ncols + nnzb / L + 1));
+    return -1;
+  }
   int64_t ni = 0, ns = 0, np = 0;
   for (int64_t c = 0; c < ncols; ++c) {
     const int64_t b0 = c < n_block_cols ? col_ptrs[c] : 0;

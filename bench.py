@@ -534,7 +534,7 @@ def bench_attention_backward(steps: int, warmup: int, cpu: bool = False):
     rp, ci, _ = Dp._bsr_plan(mask.block_col_indices, mask.block_row_ptrs, S // 128, dev, holder=mask)
     cp, crow, nbc, plan, (ni, ns, npart) = Dp._attn_bwd_plan(mask, H, S, dev)
     st = _lib.stream_handle(dev)
-    ws = torch.empty(_lib.load().tsp_bsa_bwd_workspace_size(H, S, npart), dtype=torch.uint8, device=dev)
+    ws = torch.empty(_lib.load().tsp_bsa_bwd_workspace_size(H, S, D, npart), dtype=torch.uint8, device=dev)
     out = []
     for dt in (torch.bfloat16, torch.float32):
         Qd, Kd, Vd = Q.to(dt).to(dev), K.to(dt).to(dev), V.to(dt).to(dev)

@@ -267,9 +267,9 @@ int tsp_screened_spmm_noalloc(const void* A, int dtype, int64_t lda,
  * Block-sparse attention forward, per head h < n_heads:
  *   O[h] = softmax_rows(scale * Q[h] K[h]^T restricted to the stored mask
  *          blocks) V[h]
- * Q, K, V, O (n_heads, seq_len, head_dim) contiguous, `dtype` (TSP_BF16 on
- * the MFMA path for block_size 128 and head_dim 64/128; TSP_F32, TSP_F64
- * and other shapes on the generic path). The mask (block_row_ptrs with at
+ * Q, K, V, O (n_heads, seq_len, head_dim) contiguous, `dtype` (TSP_BF16 and
+ * TSP_F32 on the MFMA path for block_size 128, scale > 0 and head_dim 64,
+ * 128 or 256; TSP_F64 and other shapes on the generic path). The mask (block_row_ptrs with at
  * least seq_len/block_size + 1 entries, block_col_indices) is shared by all
  * heads; only its pattern is used. Rows of an empty block row, and rows past
  * (seq_len/block_size)*block_size, are zero.
@@ -306,9 +306,10 @@ int tsp_bsa_fwd(const void* Q, const void* K, const void* V, int dtype,
  * (int32 entries), then again with a buffer of that length. Its header
  * holds n_items, n_splits, n_partials; `plan` of tsp_bsa_bwd is a device
  * copy of the whole plan. `workspace` holds
- * tsp_bsa_bwd_workspace_size(n_heads, seq_len, n_partials) bytes.
- * bf16 with block_size 128 and head_dim 128 runs on the MFMA kernels; other
- * shapes and fp32/fp64 on the generic kernels (which ignore the plan).
+ * tsp_bsa_bwd_workspace_size(n_heads, seq_len, head_dim, n_partials) bytes.
+ * block_size 128 with scale > 0 runs on the MFMA kernels for bf16 at
+ * head_dim 128 and fp32 at head_dim 64, 128 and 256; other shapes and fp64
+ * run on the generic kernels (which ignore the plan).
  * Replaces nki_bsr_attn_bwd (trnsparse/nki/dispatch.py:813-929; its host
  * gathers _attn_bwd_gather, dispatch.py:680-810) and the torch backward
  * _block_sparse_attn_backward (trnsparse/ops.py:360-473).
@@ -317,7 +318,7 @@ int64_t tsp_bsa_bwd_plan(const int64_t* col_ptrs, int64_t n_block_cols,
                          int64_t n_heads, int64_t seq_len, int64_t block_size,
                          int32_t* plan, int64_t capacity);
 int64_t tsp_bsa_bwd_workspace_size(int64_t n_heads, int64_t seq_len,
-                                   int64_t n_partials);
+                                   int64_t head_dim, int64_t n_partials);
 int tsp_bsa_bwd(const void* Q, const void* K, const void* V, const void* O,
                 const void* dO, int dtype, int64_t n_heads, int64_t seq_len,
                 int64_t head_dim, const int64_t* block_row_ptrs,

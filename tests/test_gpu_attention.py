@@ -4,8 +4,9 @@ Masks follow the reference's builders (local window, dilated, global tokens;
 examples/block_sparse_attention.py:49-109) and the BASELINE config-5 mask.
 Error measure: |O - O_exact| / (P |V|)_ij with the float64 oracle's softmax
 weights P — fp32 inputs <= 1e-4 (fp32 MFMA kernel for b = 128 and D in
-{64, 128}, generic kernel otherwise), bf16 inputs <= 2e-2 (MFMA kernel,
-oracle run on the exact bf16 values). The reference's hardware test
+{64, 128, 256}, other D below 256 zero-padded to those, generic kernel
+otherwise), bf16 inputs <= 2e-2 (MFMA kernel, oracle run on the exact bf16
+values). The reference's hardware test
 tolerance (tests/test_nki_attn.py:63-67, atol 1e-3 / rtol 1e-4 against the
 torch path) is checked for fp32 as well.
 """
@@ -80,6 +81,8 @@ def test_fp32_reference_cases(hip_backend, S, D, mask):
 @pytest.mark.parametrize("S,D,mask", [
     (512, 128, local_mask(4, 2)), (512, 64, dilated_mask(4, 2)), (1024, 128, global_mask(8, 1, 2)),
     (1024, 128, torch.ones(8, 8, dtype=torch.bool)), (640, 64, W.cfg5_block_mask(5)),
+    (512, 256, local_mask(4, 2)), (1024, 256, global_mask(8, 1, 2)), (700, 256, torch.ones(6, 6, dtype=torch.bool)),
+    (640, 200, W.cfg5_block_mask(5)),  # head_dim zero-padded to 256
 ])
 def test_bf16_mfma(hip_backend, S, D, mask):
     g = torch.Generator().manual_seed(11)
@@ -97,9 +100,11 @@ def test_bf16_mfma(hip_backend, S, D, mask):
     (512, 128, local_mask(4, 2), 1), (1024, 128, global_mask(8, 1, 2), 9),
     (700, 128, torch.ones(6, 6, dtype=torch.bool), 2), (640, 64, W.cfg5_block_mask(5), 3),
     (300, 64, local_mask(3, 1), 1), (512, 64, torch.ones(4, 4, dtype=torch.bool), 8),
+    (512, 256, local_mask(4, 2), 1), (700, 256, global_mask(6, 1, 2), 9), (640, 256, W.cfg5_block_mask(5), 2),
+    (384, 136, global_mask(3, 1, 1), 1),  # head_dim zero-padded to 256
 ])
 def test_fp32_mfma(hip_backend, S, D, mask, H):
-    """fp32, b = 128, D in {64, 128} runs bsa_fwd_f32_mfma: ragged S (keys
+    """fp32, b = 128, D in {64, 128, 256} runs bsa_fwd_f32_mfma: ragged S (keys
     past S inside a stored block), more heads than a multiple of 8, and
     queries with wide score ranges (the running max moves by more than the
     lazy-rescale threshold)."""
@@ -116,10 +121,11 @@ def test_fp32_mfma(hip_backend, S, D, mask, H):
         np.testing.assert_allclose(rden[hh].cpu().numpy(), ed, rtol=1e-4)
 
 
-def test_fp32_mfma_long_row(hip_backend):
+@pytest.mark.parametrize("D", [64, 256])
+def test_fp32_mfma_long_row(hip_backend, D):
     """A block row with more than 64 stored blocks (the kernel reads the
     row's block columns 64 at a time)."""
-    nb, D = 67, 64
+    nb = 67
     S = nb * 128
     mask = local_mask(nb, 0)
     mask[1, :] = True
@@ -243,3 +249,37 @@ def test_fp16_widened(hip_backend):
     q, k, v = (t.cuda().requires_grad_(True) for t in (Q, K, V))
     ts.block_sparse_attention_tiled(q, k, v, mask_bsr).float().sum().backward()
     assert q.grad.dtype == torch.float16 and torch.isfinite(q.grad.float()).all()
+
+
+@pytest.mark.parametrize("mask,seed", [(local_mask(4, 2), 50), (dilated_mask(4, 2), 51)])
+def test_reference_head_dim_256_case(hip_backend, mask, seed):
+    """The reference's head_dim-256 hardware case (tests/test_nki_attn.py:
+    153-201): fp32, seq 512, 128-blocks, local window 2 and dilated stride 2,
+    forward and backward against the torch path at atol 1e-3 / rtol 1e-4,
+    and against the float64 oracle."""
+    from oracle import ref as R
+
+    torch.manual_seed(seed)
+    S, D = 512, 256
+    Q, K, V = (torch.randn(S, D) for _ in range(3))
+    mask_bsr = W.bsr_from_block_mask(mask, 128)
+    ts.set_backend("pytorch")
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (Q, K, V))
+    expect = ts.block_sparse_attention_tiled(qr, kr, vr, mask_bsr)
+    dO = torch.randn_like(expect)
+    expect.backward(dO)
+    ts.set_backend("hip")
+    qg, kg, vg = (t.cuda().requires_grad_(True) for t in (Q, K, V))
+    got = ts.block_sparse_attention_tiled(qg, kg, vg, mask_bsr)
+    got.backward(dO.cuda())
+    torch.testing.assert_close(got.detach().cpu(), expect.detach(), atol=1e-3, rtol=1e-4)
+    for a, b in ((qg, qr), (kg, kr), (vg, vr)):
+        torch.testing.assert_close(a.grad.cpu(), b.grad, atol=1e-3, rtol=1e-4)
+    out, _, _, sc = _oracle(Q, K, V, mask_bsr, D**-0.5)
+    assert _err(got.detach().cpu().numpy(), out, sc) <= TOL_F32
+    args = (Q.double().numpy(), K.double().numpy(), V.double().numpy(), got.detach().cpu().double().numpy(),
+            dO.double().numpy(), mask_bsr.block_row_ptrs.numpy(), mask_bsr.block_col_indices.numpy(), 128, D**-0.5)
+    exact = R.block_sparse_attention_backward(*args)
+    bound = R.block_sparse_attention_backward(*args, absolute=True)
+    for gr, e, a in zip((qg.grad, kg.grad, vg.grad), exact, bound):
+        assert R.scaled_error(gr.cpu().double().numpy(), e, np.maximum(a, 1e-30)) <= TOL_F32

@@ -8,10 +8,11 @@ the backward: D = rowsum(dO * O)) and its own float64 row stats. Error
 measure per gradient element: |g - g_exact| / g_abs, with g_abs the oracle's
 absolute form (|dS| replaced by P (|dO V^T| + |D|), operands by their
 magnitudes). fp32 <= 1e-4, bf16 <= 2e-2, fp64 <= 1e-10. fp32 with b = 128
-and d in {64, 128} runs the fp32 MFMA kernels, bf16 with d = 128 the bf16
-MFMA kernels, bf16 with d = 64 the fp32 MFMA kernels on widened operands,
-other d below 128 zero-padded to 64 or 128 first; everything else (fp64,
-d > 128, other block sizes) the generic kernels.
+and d in {64, 128, 256} runs the fp32 MFMA kernels (16-row tiles at
+d = 256), bf16 with d = 128 the bf16 MFMA kernels, bf16 with d = 64 or 256
+the fp32 MFMA kernels on widened operands, other d below 256 zero-padded to
+64, 128 or 256 first; everything else (fp64, d > 256, other block sizes)
+the generic kernels.
 """
 
 from __future__ import annotations
@@ -81,7 +82,13 @@ def _check_head(Q, K, V, dO, O, grads, mask_bsr, scale, tol, rows=None, cols=Non
         (640, 64, W.cfg5_block_mask(5), torch.bfloat16),
         (256, 32, local_mask(2, 1), torch.bfloat16),      # head_dim zero-padded to 64
         (256, 100, global_mask(2, 0, 1), torch.float32),  # head_dim zero-padded to 128
-        (256, 160, local_mask(2, 1), torch.bfloat16),     # generic bf16
+        (256, 160, local_mask(2, 1), torch.bfloat16),     # head_dim zero-padded to 256, widened
+        (256, 320, local_mask(2, 1), torch.bfloat16),     # generic bf16
+        (512, 256, local_mask(4, 2), torch.float32),      # fp32 MFMA d = 256
+        (700, 256, global_mask(6, 1, 1), torch.float32),  # d = 256, ragged S, global column split
+        (640, 256, W.cfg5_block_mask(5), torch.float32),
+        (300, 200, local_mask(3, 2), torch.float32),      # zero-padded to 256, last key block crosses S
+        (512, 256, local_mask(4, 1), torch.bfloat16),     # bf16 d = 256: widened onto the fp32 d = 256 kernels
         (512, 128, local_mask(4, 1), torch.float32),      # fp32 MFMA kernels
         (1024, 128, global_mask(8, 1, 1), torch.float32),  # fp32 MFMA, global column split into 2 segments
         (300, 128, local_mask(3, 2), torch.float32),      # fp32 MFMA, last key block crosses S
@@ -98,11 +105,11 @@ def test_backward_matches_oracle(hip_backend, S, D, mask, dtype):
     _check_head(Q, K, V, dO, O, (dQ, dK, dV), mask_bsr, D**-0.5, TOL[dtype])
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_backward_empty_rows_and_ragged(hip_backend, dtype):
+@pytest.mark.parametrize("dtype,D", [(torch.float32, 128), (torch.bfloat16, 128), (torch.float32, 256)])
+def test_backward_empty_rows_and_ragged(hip_backend, dtype, D):
     """Block row 1 stores nothing, block column 2 is never stored, rows past
     (S // b) b have no block row: their gradients are exactly zero."""
-    S, D = 440, 128
+    S = 440
     mask = torch.tensor([[True, False, False, True], [False, False, False, False],
                          [True, True, False, False], [False, False, False, True]])
     mask_bsr = W.bsr_from_block_mask(mask, 128)
@@ -128,10 +135,11 @@ def test_backward_batched_heads_bf16(hip_backend):
                         D**-0.5, TOL[torch.bfloat16])
 
 
-def test_backward_batched_heads_f32(hip_backend):
+@pytest.mark.parametrize("D", [64, 256])
+def test_backward_batched_heads_f32(hip_backend, D):
     """fp32 MFMA kernels over 3 heads: the column pass's (item, head) grid."""
     torch.manual_seed(15)
-    S, D = 512, 64
+    S = 512
     mask_bsr = W.bsr_from_block_mask(global_mask(4, 1, 1), 128)
     Q, K, V, dO = (torch.randn(3, S, D) for _ in range(4))
     O, dQ, dK, dV = _run(Q, K, V, dO, mask_bsr)

@@ -23,9 +23,13 @@
 //       registers (bf16) with V staged transposed in LDS. fp32 softmax with
 //       exp2, fp32 accumulation, bf16 output. Kept for operands past 4 GiB.
 //   bsa_fwd_bf16_stream<D> the same work split with K/V streamed through an
-//       LDS ring by direct loads (D in {64, 128}).
-//   bsa_fwd_f32_mfma<D>   fp32, 128-blocks, D in {64, 128}: the same work
-//       split on v_mfma_f32_32x32x2_f32 with K/V streamed through an LDS ring.
+//       LDS ring by direct loads (D in {64, 128, 256}).
+//   bsa_fwd_f32_mfma<D>   fp32, 128-blocks, D in {64, 128, 256}: the same
+//       work split on v_mfma_f32_32x32x2_f32 with K/V streamed through an
+//       LDS ring.
+// head_dim 256 keeps the whole score product in one workgroup (64 k-steps
+// of 16 bf16 / 128 of 2 fp32 per 32-key tile) with one workgroup per CU;
+// other head_dims are padded with zero columns by the caller.
 //   bsa_fwd_generic<T>    fp32/fp64/bf16, any block size and head_dim: one
 //       thread per (query, 32-wide slice of head_dim), online softmax in
 //       the accumulation type (double for fp64).
@@ -280,7 +284,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_bf16_mfma(
   }
 }
 
-// ------------------------------------------------- bf16 MFMA, d = 64 and 128
+// ------------------------------------------- bf16 MFMA, d = 64, 128 and 256
 //
 // bsa_fwd_bf16_stream<D>: same work split and math as bsa_fwd_bf16_mfma (one
 // 256-thread workgroup per (head, 128-query block row), a wavefront per 32
@@ -288,8 +292,8 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_bf16_mfma(
 // the exp2 domain, O^T += V^T P^T with P from registers), restructured so the
 // key blocks stream while the MFMAs run:
 //   * keys are consumed in 64-key halves that go through a 2-stage LDS ring
-//     (K half + V half per stage: 64 KiB per workgroup at D = 128, 32 KiB at
-//     D = 64), filled by direct global->LDS buffer loads issued one half
+//     (K half + V half per stage: 128 KiB per workgroup at D = 256, 64 KiB
+//     at D = 128, 32 KiB at D = 64), filled by direct global->LDS buffer loads issued one half
 //     ahead; rows at or past seq_len read as zero;
 //   * V stays [key][d] in LDS and the A operand of O^T += V^T P^T (8 keys of
 //     one d column per lane) comes from ds_read_b64_tr_b16;
@@ -305,8 +309,10 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 // Row geometry and swizzles per head_dim: K rows are read as 16-byte pieces
 // of 16 consecutive keys (one chunk), V rows through transpose reads of 4
 // consecutive keys. D = 128 (256-byte rows, 16 chunks): K chunk ^ (key % 16),
-// V chunk ^ 4 (key % 4). D = 64 (128-byte rows, where keys k and k + 2 share
-// banks): K chunk ^ ((key / 2) % 8), V chunk ^ 4 ((key / 2) % 2).
+// V chunk ^ 4 (key % 4); D = 256 (512-byte rows, 32 chunks, again starting
+// at bank 0) uses the same terms on the low chunk bits. D = 64 (128-byte
+// rows, where keys k and k + 2 share banks): K chunk ^ ((key / 2) % 8), V
+// chunk ^ 4 ((key / 2) % 2).
 template <int D>
 struct Geo {
   static constexpr int ROWB = D * 2;           // bytes per K/V row
@@ -316,14 +322,16 @@ struct Geo {
   static constexpr int NU = D / 32;            // 32-wide d subtiles of O^T
   static constexpr int LPR = ROWB / 16;        // lanes per row in a 1 KiB load
   static constexpr int RPI = 64 / LPR;         // rows per load instruction
-  __host__ __device__ static constexpr int kswz(int key) { return D == 128 ? (key & 15) : ((key >> 1) & 7); }
-  __host__ __device__ static constexpr int vswz(int key) { return D == 128 ? (key & 3) : ((key >> 1) & 1); }
+  __host__ __device__ static constexpr int kswz(int key) { return D >= 128 ? (key & 15) : ((key >> 1) & 7); }
+  __host__ __device__ static constexpr int vswz(int key) { return D >= 128 ? (key & 3) : ((key >> 1) & 1); }
 };
 }  // namespace att
 
-// D = 64 fits three wavefronts per SIMD (136 registers, 32 KiB of LDS per workgroup)
+// D = 64 fits three wavefronts per SIMD (136 registers, 32 KiB of LDS per
+// workgroup); D = 256 holds 128 KiB of ring and 64 + 128 registers of Q and O
+// per lane, one workgroup per CU
 template <int D>
-__global__ __launch_bounds__(256, D == 64 ? 3 : 2) void bsa_fwd_bf16_stream(
+__global__ __launch_bounds__(256, D == 64 ? 3 : (D == 128 ? 2 : 1)) void bsa_fwd_bf16_stream(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int64_t S,
     int64_t head_stride, int64_t H, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci, int64_t Mt,
     float scale_log2, uint16_t* __restrict__ O, float* __restrict__ rmax, float* __restrict__ rden) {
@@ -556,37 +564,43 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void bsa_fwd_bf16_stream(
 
 // ---------------------------------------------------------------- fp32 MFMA
 //
-// bsa_fwd_f32_mfma<D>: fp32, 128-blocks, D in {64, 128}. The work split and
+// bsa_fwd_f32_mfma<D>: fp32, 128-blocks, D in {64, 128, 256}. The work split and
 // math of the bf16 kernels (one 256-thread workgroup per (head, 128-query
 // block row), a wavefront per 32 queries, S^T = K Q^T with the wave's Q rows
 // in registers, online softmax in the exp2 domain with lazy rescaling,
 // O^T += V^T P^T with P from registers) on v_mfma_f32_32x32x2_f32:
-//   * keys stream through a 2-stage LDS ring of HK = 4096 / D keys per stage
-//     (K rows then V rows, 32 KiB per stage, 64 KiB per workgroup, two
-//     workgroups per CU), filled by direct global->LDS buffer loads issued
-//     one stage ahead; rows at or past seq_len read as zero;
+//   * keys stream through a 2-stage LDS ring of HK = max(32, 4096 / D) keys
+//     per stage (K rows then V rows: 32 KiB per stage and two workgroups per
+//     CU for D <= 128, 64 KiB per stage and one workgroup per CU for
+//     D = 256), filled by direct global->LDS buffer loads issued one stage
+//     ahead; rows at or past seq_len read as zero;
 //   * S^T: the MFMA k index is the head dimension; at step 4t + c lane half h
 //     supplies d = 8t + 4h + c, so one b128 LDS read of a K row feeds four
 //     MFMAs and Q[q][8t + 4h .. +3] is the matching register fragment. K
 //     rows are stored 16-byte chunk ^ (key % 16) (conflict-free reads of one
 //     chunk from 32 rows);
-//   * O^T: row r of d subtile u is d = NU*r + u, so a lane's A operands for
-//     all NU subtiles are one contiguous read V[key][NU*l32 .. +NU) and its
-//     outputs cover 4*NU consecutive d; the k index is the key: at step s
+//   * O^T: with NUH = min(NU, 4) subtiles per 128 columns, row r of d
+//     subtile u is d = 128*(u / NUH) + NUH*r + u % NUH, so a lane's A
+//     operands are one contiguous read V[key][NUH*l32 .. +NUH) per 128
+//     columns (conflict-free b128 reads at D = 256) and its outputs cover
+//     4*NUH consecutive d per 128 columns; the k index is the key: at step s
 //     lane half h supplies key 8*(s/4) + 4h + s%4 of the 32-key tile, which
 //     is its own S^T element s, so P is consumed where it was computed.
 namespace attf {
 template <int D>
 struct Cfg {
-  static constexpr int HK = 4096 / D;       // keys per ring stage
+  static constexpr int HK = D > 128 ? 32 : 4096 / D;  // keys per ring stage
   static constexpr int ROWB = D * 4;        // bytes per K/V row
-  static constexpr int HBYTES = HK * ROWB;  // 16 KiB of K (or V) per stage
+  static constexpr int HBYTES = HK * ROWB;  // K (or V) bytes per stage: 16 KiB, 32 KiB at D = 256
   static constexpr int STAGE = 2 * HBYTES;
   static constexpr int NST = 2;
   static constexpr int NT = HK / 32;        // 32-key S^T tiles per stage
   static constexpr int NU = D / 32;         // d subtiles of O^T
+  static constexpr int NUH = NU < 4 ? NU : 4;  // subtiles per 128 columns
+  static constexpr int NB = NU / NUH;       // 128-column groups
   static constexpr int KT = D / 8;          // b128 K reads per S^T tile
   static constexpr int SPB = AB / HK;       // stages per key block
+  static constexpr int NI = HBYTES / 4096;  // 1 KiB K (and V) loads per wave per stage
 };
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 template <int NU> struct VRow;
@@ -595,14 +609,14 @@ template <> struct VRow<2> { typedef f32x2 type; };
 }  // namespace attf
 
 template <int D>
-__global__ __launch_bounds__(256, 2) void bsa_fwd_f32_mfma(
+__global__ __launch_bounds__(256, D > 128 ? 1 : 2) void bsa_fwd_f32_mfma(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V, int64_t S,
     int64_t head_stride, int64_t H, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci, int64_t Mt,
     float scale_log2, float* __restrict__ O, float* __restrict__ rmax, float* __restrict__ rden) {
   typedef attf::Cfg<D> C;
   constexpr int HK = C::HK, ROWB = C::ROWB, HBYTES = C::HBYTES, STAGE = C::STAGE, NST = C::NST;
-  constexpr int NT = C::NT, NU = C::NU, KT = C::KT, SPB = C::SPB;
-  typedef typename attf::VRow<NU>::type vrow_t;
+  constexpr int NT = C::NT, NU = C::NU, NUH = C::NUH, NB = C::NB, KT = C::KT, SPB = C::SPB, NI = C::NI;
+  typedef typename attf::VRow<NUH>::type vrow_t;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
 
   // XCD-aware order: XCD x walks heads x, x+8, ...; the block rows of one
@@ -656,14 +670,14 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_f32_mfma(
   };
   auto first_key = [&](int s) { return (int64_t)colblk(s / SPB) * AB + HK * (s % SPB); };
 
-  // ---- loads of stage s: 16 K + 16 V instructions of 1 KiB, 4 + 4 per wave
+  // ---- loads of stage s: K and V instructions of 1 KiB, NI + NI per wave
   auto issue = [&](int s) {
     constexpr int LPR = D / 4, RPI = 64 / LPR;  // lanes per row, rows per instruction
     const int64_t key0 = first_key(s);
     const uint32_t st = lds0 + (s % NST) * STAGE;
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-      const int j = 4 * w + qq;
+    for (int qq = 0; qq < NI; ++qq) {
+      const int j = NI * w + qq;
       const int rr = RPI * j + lane / LPR;  // row of the stage
       const int p = lane % LPR;             // this lane's 16-byte slot in the row
       const uint32_t rowoff = (uint32_t)((key0 + rr) * ROWB);
@@ -675,11 +689,15 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_f32_mfma(
   const int kx = l32 & 15;  // K swizzle term: row % 16 for rows 32tt + l32
   auto compute = [&](const uint8_t* st, int64_t key0) {
     const uint8_t* Ks = st + l32 * ROWB;
-    const uint8_t* Vs = st + HBYTES + 4 * h * ROWB + l32 * NU * 4;
+    const uint8_t* Vs = st + HBYTES + 4 * h * ROWB + l32 * NUH * 4;
     auto kread = [&](int tt, int t) { return *(const f32x4*)(Ks + tt * 32 * ROWB + (((2 * t + h) ^ kx) * 16)); };
+    struct vrows { vrow_t b[NB]; };
     auto vread = [&](int i) {  // step i of the stage: tile i / 16, step s = i % 16
       const int tt = i >> 4, s = i & 15;
-      return *(const vrow_t*)(Vs + (32 * tt + 8 * (s >> 2) + (s & 3)) * ROWB);
+      vrows r;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) r.b[b] = *(const vrow_t*)(Vs + (32 * tt + 8 * (s >> 2) + (s & 3)) * ROWB + 512 * b);
+      return r;
     };
     // ---- S^T tiles (keys 32tt + 8*(v/4) + 4h + v%4, query l32): NT
     // independent chains, K operands read one t ahead
@@ -742,7 +760,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_f32_mfma(
     lsum += __shfl_xor(lsum, 32, 64);
     lrun += lsum;
     // ---- O^T += V^T P^T, V operands read one step ahead
-    vrow_t vb[2];
+    vrows vb[2];
     vb[0] = vread(0);
 #pragma unroll
     for (int i = 0; i < 16 * NT; ++i) {
@@ -750,7 +768,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_f32_mfma(
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < NU; ++u)
-        o[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[i & 1][u], sc[i >> 4][i & 15], o[u], 0, 0, 0);
+        o[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[i & 1].b[u / NUH][u % NUH], sc[i >> 4][i & 15], o[u], 0, 0, 0);
     }
   };
 
@@ -763,9 +781,9 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_f32_mfma(
     compute(lds + (s % NST) * STAGE, key0);
   }
 
-  // ---- epilogue: element v of subtile u is O[q][NU*(8*(v/4) + 4h + v%4) + u]
-  // (o and l both relative to mref); the returned denominator is relative to
-  // the true max
+  // ---- epilogue: element v of subtile u is
+  // O[q][128*(u/NUH) + NUH*(8*(v/4) + 4h + v%4) + u%NUH] (o and l both
+  // relative to mref); the returned denominator is relative to the true max
   const bool empty = nblk == 0;
   const float lref = lrun > 1e-12f ? lrun : 1e-12f;
   const float inv = empty ? 0.f : 1.f / lref;
@@ -773,19 +791,21 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_f32_mfma(
   const float den = ltrue > 1e-12f ? ltrue : 1e-12f;
   float* Oq = O + head * head_stride + q * D;
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    float* dst = Oq + NU * (8 * a + 4 * h);  // 4*NU consecutive floats: index NU*c + u
+  for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int k = 0; k < NU; ++k) {
-      f32x4 t;
+    for (int a = 0; a < 4; ++a) {
+      float* dst = Oq + 128 * b + NUH * (8 * a + 4 * h);  // 4*NUH consecutive floats: index NUH*c + u
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int idx = 4 * k + e;  // = NU*c + u
-        t[e] = o[idx % NU][4 * a + idx / NU] * inv;
+      for (int k = 0; k < NUH; ++k) {
+        f32x4 t;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int idx = 4 * k + e;  // = NUH*c + u
+          t[e] = o[NUH * b + idx % NUH][4 * a + idx / NUH] * inv;
+        }
+        *(f32x4*)(dst + 4 * k) = t;
       }
-      *(f32x4*)(dst + 4 * k) = t;
     }
-  }
   if (h == 0 && rmax) {
     const int64_t r = head * Mt * AB + q;
     rmax[r] = empty ? 0.f : mtrue * 0.69314718055994531f;
@@ -828,44 +848,47 @@ extern "C" int tsp_bsa_fwd(const void* Q, const void* K, const void* V, int dtyp
     }
   }
   if (Mt == 0) return TSP_OK;
-  if (dtype == TSP_BF16 && block_size == AB && (head_dim == 64 || head_dim == 128) && ((uintptr_t)Q % 16) == 0 &&
+  const bool bf16_streamed = scale > 0 && (seq_len + AB) * head_dim * 2 <= (int64_t)UINT32_MAX;
+  if (dtype == TSP_BF16 && block_size == AB &&
+      (head_dim == 64 || head_dim == 128 || (head_dim == 256 && bf16_streamed)) && ((uintptr_t)Q % 16) == 0 &&
       ((uintptr_t)K % 16) == 0 && ((uintptr_t)V % 16) == 0 && ((uintptr_t)O % 8) == 0) {
     const int64_t grid = tsp::ceil_div(n_heads, 8) * Mt * 8;
     if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_fwd: problem too large");
     const float sl2 = (float)(scale * 1.4426950408889634);
-    const bool streamed = scale > 0 && (seq_len + AB) * head_dim * 2 <= (int64_t)UINT32_MAX;
-    if (streamed && head_dim == 128)
-      hipLaunchKernelGGL((bsa_fwd_bf16_stream<128>), dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)Q,
-                         (const uint16_t*)K, (const uint16_t*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs,
-                         block_col_indices, Mt, sl2, (uint16_t*)O, (float*)row_max, (float*)row_denom);
-    else if (streamed)
-      hipLaunchKernelGGL((bsa_fwd_bf16_stream<64>), dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)Q,
-                         (const uint16_t*)K, (const uint16_t*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs,
-                         block_col_indices, Mt, sl2, (uint16_t*)O, (float*)row_max, (float*)row_denom);
+#define TSP_FWD_BF16(KERNEL)                                                                                        \
+  hipLaunchKernelGGL((KERNEL), dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)Q, (const uint16_t*)K,       \
+                     (const uint16_t*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs, block_col_indices, Mt, \
+                     sl2, (uint16_t*)O, (float*)row_max, (float*)row_denom)
+    if (bf16_streamed && head_dim == 256)
+      TSP_FWD_BF16(bsa_fwd_bf16_stream<256>);
+    else if (bf16_streamed && head_dim == 128)
+      TSP_FWD_BF16(bsa_fwd_bf16_stream<128>);
+    else if (bf16_streamed)
+      TSP_FWD_BF16(bsa_fwd_bf16_stream<64>);
     else if (head_dim == 128)
-      hipLaunchKernelGGL((bsa_fwd_bf16_mfma<128>), dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)Q,
-                         (const uint16_t*)K, (const uint16_t*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs,
-                         block_col_indices, Mt, sl2, (uint16_t*)O, (float*)row_max, (float*)row_denom);
+      TSP_FWD_BF16(bsa_fwd_bf16_mfma<128>);
     else
-      hipLaunchKernelGGL((bsa_fwd_bf16_mfma<64>), dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)Q,
-                         (const uint16_t*)K, (const uint16_t*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs,
-                         block_col_indices, Mt, sl2, (uint16_t*)O, (float*)row_max, (float*)row_denom);
+      TSP_FWD_BF16(bsa_fwd_bf16_mfma<64>);
+#undef TSP_FWD_BF16
     return tsp::check_launch("bsa_fwd_bf16_mfma launch");
   }
-  if (dtype == TSP_F32 && block_size == AB && (head_dim == 64 || head_dim == 128) && scale > 0 &&
+  if (dtype == TSP_F32 && block_size == AB && (head_dim == 64 || head_dim == 128 || head_dim == 256) && scale > 0 &&
       ((uintptr_t)Q % 16) == 0 && ((uintptr_t)K % 16) == 0 && ((uintptr_t)V % 16) == 0 && ((uintptr_t)O % 16) == 0 &&
       (seq_len + AB) * head_dim * 4 <= (int64_t)UINT32_MAX) {
     const int64_t grid = tsp::ceil_div(n_heads, 8) * Mt * 8;
     if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_fwd: problem too large");
     const float sl2 = (float)(scale * 1.4426950408889634);
-    if (head_dim == 128)
-      hipLaunchKernelGGL((bsa_fwd_f32_mfma<128>), dim3((unsigned)grid), dim3(256), 0, st, (const float*)Q,
-                         (const float*)K, (const float*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs,
-                         block_col_indices, Mt, sl2, (float*)O, (float*)row_max, (float*)row_denom);
+#define TSP_FWD_F32(KERNEL)                                                                                       \
+  hipLaunchKernelGGL((KERNEL), dim3((unsigned)grid), dim3(256), 0, st, (const float*)Q, (const float*)K,           \
+                     (const float*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs, block_col_indices, Mt, \
+                     sl2, (float*)O, (float*)row_max, (float*)row_denom)
+    if (head_dim == 256)
+      TSP_FWD_F32(bsa_fwd_f32_mfma<256>);
+    else if (head_dim == 128)
+      TSP_FWD_F32(bsa_fwd_f32_mfma<128>);
     else
-      hipLaunchKernelGGL((bsa_fwd_f32_mfma<64>), dim3((unsigned)grid), dim3(256), 0, st, (const float*)Q,
-                         (const float*)K, (const float*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs,
-                         block_col_indices, Mt, sl2, (float*)O, (float*)row_max, (float*)row_denom);
+      TSP_FWD_F32(bsa_fwd_f32_mfma<64>);
+#undef TSP_FWD_F32
     return tsp::check_launch("bsa_fwd_f32_mfma launch");
   }
   if (dtype == TSP_F64)

@@ -31,7 +31,8 @@
 //       through a 2-stage LDS ring.
 //   bsa_bwd_dq_f32<D> / bsa_bwd_dkdv_f32<D> / bsa_bwd_reduce_f32<D>  fp32,
 //       b = 128, D in {64, 128}: the same passes on v_mfma_f32_32x32x2_f32
-//       (operand forms at the kernels).
+//       (operand forms at the kernels); D = 256 runs the row and column
+//       passes of attention_bwd_d256.hip (16-row tiles) and the reduce here.
 //   bsa_bwd_dq_generic / bsa_bwd_dkdv_generic  any dtype / block size /
 //       head_dim: one thread per (row, 32-wide slice of head_dim).
 // Swizzle: K (row pass) and Q, dO (column pass) are read both as 16-byte rows
@@ -45,6 +46,17 @@
 
 #include "lds_dma.h"
 #include "slots.h"
+
+namespace tsp {
+// attention_bwd_d256.hip: the fp32 head_dim-256 row and column passes
+int bsa_bwd_f32_d256_rows(const float* Q, const float* K, const float* V, const float* O, const float* dO, int64_t S,
+                        int64_t H, const int64_t* rp, const int64_t* ci, int64_t Mt, float scale_log2, float scale,
+                        const float* rmax, const float* rden, float* qstat, float* dQ, hipStream_t st);
+int bsa_bwd_f32_d256_cols(const float* Q, const float* K, const float* V, const float* dO, int64_t S, int64_t H,
+                          const int64_t* crow, const int32_t* items, int64_t n_items, int n_partials, int64_t Mt,
+                          float scale_log2, float scale, const float* qstat, float* dK, float* dV, float* partial,
+                          hipStream_t st);
+}  // namespace tsp
 
 namespace {
 
@@ -1182,7 +1194,7 @@ int launch_f32(const void* Q, const void* K, const void* V, const void* O, const
                const void* rmax, const void* rden, void* dQ, void* dK, void* dV, const int32_t* plan, int64_t n_items,
                int64_t n_splits, int64_t n_partials, void* workspace, hipStream_t st) {
   const int64_t nh = tsp::ceil_div(H, 8);
-  const int64_t grid_a = nh * Mt * 8, grid_b = n_items * H;
+  const int64_t grid_a = nh * Mt * 8 * (D == 256 ? 2 : 1), grid_b = n_items * H * (D == 256 ? 2 : 1);
   if (grid_a > INT32_MAX || grid_b > INT32_MAX || 8 * n_splits > INT32_MAX || H > 65535)
     return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_bwd: problem too large");
   const float sl2 = (float)(scale * 1.4426950408889634);
@@ -1195,19 +1207,30 @@ int launch_f32(const void* Q, const void* K, const void* V, const void* O, const
       if (rc) return rc;
     }
   }
-  if (grid_a > 0) {
-    hipLaunchKernelGGL((bsa_bwd_dq_f32<D>), dim3((unsigned)grid_a), dim3(256), 0, st, (const float*)Q, (const float*)K,
-                       (const float*)V, (const float*)O, (const float*)dO, S, H, rp, ci, Mt, sl2, (float)scale,
-                       (const float*)rmax, (const float*)rden, qstat, (float*)dQ);
-    int rc = tsp::check_launch("bsa_bwd_dq_f32 launch");
+  if constexpr (D == 256) {  // 16-row tiles, half a block per workgroup (attention_bwd_d256.hip)
+    int rc = tsp::bsa_bwd_f32_d256_rows((const float*)Q, (const float*)K, (const float*)V, (const float*)O,
+                                      (const float*)dO, S, H, rp, ci, Mt, sl2, (float)scale, (const float*)rmax,
+                                      (const float*)rden, qstat, (float*)dQ, st);
     if (rc) return rc;
-  }
-  if (grid_b > 0) {
-    hipLaunchKernelGGL((bsa_bwd_dkdv_f32<D>), dim3((unsigned)grid_b), dim3(256), 0, st, (const float*)Q,
-                       (const float*)K, (const float*)V, (const float*)dO, S, H, crow, plan + 4, (int)n_partials, Mt,
-                       sl2, (float)scale, (const float*)qstat, (float*)dK, (float*)dV, partial);
-    int rc = tsp::check_launch("bsa_bwd_dkdv_f32 launch");
+    rc = tsp::bsa_bwd_f32_d256_cols((const float*)Q, (const float*)K, (const float*)V, (const float*)dO, S, H, crow,
+                                    plan + 4, n_items, (int)n_partials, Mt, sl2, (float)scale, (const float*)qstat,
+                                    (float*)dK, (float*)dV, partial, st);
     if (rc) return rc;
+  } else {
+    if (grid_a > 0) {
+      hipLaunchKernelGGL((bsa_bwd_dq_f32<D>), dim3((unsigned)grid_a), dim3(256), 0, st, (const float*)Q,
+                         (const float*)K, (const float*)V, (const float*)O, (const float*)dO, S, H, rp, ci, Mt, sl2,
+                         (float)scale, (const float*)rmax, (const float*)rden, qstat, (float*)dQ);
+      int rc = tsp::check_launch("bsa_bwd_dq_f32 launch");
+      if (rc) return rc;
+    }
+    if (grid_b > 0) {
+      hipLaunchKernelGGL((bsa_bwd_dkdv_f32<D>), dim3((unsigned)grid_b), dim3(256), 0, st, (const float*)Q,
+                         (const float*)K, (const float*)V, (const float*)dO, S, H, crow, plan + 4, (int)n_partials, Mt,
+                         sl2, (float)scale, (const float*)qstat, (float*)dK, (float*)dV, partial);
+      int rc = tsp::check_launch("bsa_bwd_dkdv_f32 launch");
+      if (rc) return rc;
+    }
   }
   if (n_splits > 0) {
     hipLaunchKernelGGL((bsa_bwd_reduce_f32<D>), dim3((unsigned)(8 * n_splits), (unsigned)H), dim3(256), 0, st,
@@ -1299,9 +1322,10 @@ extern "C" int64_t tsp_bsa_bwd_plan(const int64_t* col_ptrs, int64_t n_block_col
   return need;
 }
 
-extern "C" int64_t tsp_bsa_bwd_workspace_size(int64_t n_heads, int64_t seq_len, int64_t n_partials) {
-  if (n_heads < 0 || seq_len < 0 || n_partials < 0) return -1;
-  return 16 * n_heads * seq_len + n_heads * n_partials * 2 * abw::BS * abw::D * 4;
+extern "C" int64_t tsp_bsa_bwd_workspace_size(int64_t n_heads, int64_t seq_len, int64_t head_dim, int64_t n_partials) {
+  if (n_heads < 0 || seq_len < 0 || head_dim < 0 || n_partials < 0) return -1;
+  const int64_t pd = head_dim > abw::D ? head_dim : abw::D;  // fp32 partial rows of dK and dV
+  return 16 * n_heads * seq_len + n_heads * n_partials * 2 * abw::BS * pd * 4;
 }
 
 extern "C" int tsp_bsa_bwd(const void* Q, const void* K, const void* V, const void* O, const void* dO, int dtype,
@@ -1374,11 +1398,16 @@ extern "C" int tsp_bsa_bwd(const void* Q, const void* K, const void* V, const vo
   }
 
   const bool aligned16 = aligned && ((uintptr_t)dQ % 16) == 0 && ((uintptr_t)dK % 16) == 0 && ((uintptr_t)dV % 16) == 0;
-  if (dtype == TSP_F32 && block_size == 128 && (head_dim == 64 || head_dim == 128) && scale > 0 && plan && aligned16 &&
+  if (dtype == TSP_F32 && block_size == 128 && (head_dim == 64 || head_dim == 128 || head_dim == 256) && scale > 0 &&
+      plan && aligned16 &&
       (seq_len + 128) * head_dim * 4 <= (int64_t)UINT32_MAX) {
     if (n_items < tsp::ceil_div(seq_len, block_size))
       return tsp::fail(TSP_EINVAL, "tsp_bsa_bwd: plan has %lld items for %lld key block columns", (long long)n_items,
                        (long long)tsp::ceil_div(seq_len, block_size));
+    if (head_dim == 256)
+      return launch_f32<256>(Q, K, V, O, dO, n_heads, seq_len, block_row_ptrs, block_col_indices, col_block_rows, Mt,
+                             scale, row_max, row_denom, dQ, dK, dV, plan, n_items, n_splits, n_partials, workspace,
+                             stream_);
     if (head_dim == 128)
       return launch_f32<128>(Q, K, V, O, dO, n_heads, seq_len, block_row_ptrs, block_col_indices, col_block_rows, Mt,
                              scale, row_max, row_denom, dQ, dK, dV, plan, n_items, n_splits, n_partials, workspace,

@@ -76,7 +76,7 @@ SIGNATURES: dict[str, tuple] = {
     "tsp_csr_sum": (_INT, [_P, _P, _P, _I64, _P, _P, _P, _I64, _INT, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "tsp_csr_transpose": (_INT, [_P, _INT, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "tsp_bsa_bwd_plan": (_I64, [_P, _I64, _I64, _I64, _I64, _P, _I64]),
-    "tsp_bsa_bwd_workspace_size": (_I64, [_I64, _I64, _I64]),
+    "tsp_bsa_bwd_workspace_size": (_I64, [_I64, _I64, _I64, _I64]),
     "tsp_bsa_bwd": (
         _INT,
         [_P, _P, _P, _P, _P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _DBL, _P, _P, _P, _P, _P,

@@ -526,14 +526,14 @@ def hip_screened_spmm(A, diag_integrals, B, threshold: float):
 
 
 def _mfma_head_dim(t: torch.Tensor, block_size: int) -> int | None:
-    """The head_dim an fp32 / bf16 operand of head_dim d < 128 (not 64) is
-    zero-padded to so that the MFMA attention kernels serve it (zero columns
-    change neither the scores nor the other columns of the results); None
-    when no padding applies."""
+    """The head_dim an fp32 / bf16 operand of head_dim d < 256 other than 64
+    and 128 is zero-padded to (64, 128 or 256) so that the MFMA attention
+    kernels serve it (zero columns change neither the scores nor the other
+    columns of the results); None when no padding applies."""
     d = t.shape[-1]
-    if block_size != 128 or t.dtype not in (torch.float32, torch.bfloat16) or d in (64, 128) or d >= 128 or d == 0:
+    if block_size != 128 or t.dtype not in (torch.float32, torch.bfloat16) or d in (64, 128, 256) or d > 256 or d == 0:
         return None
-    return 64 if d < 64 else 128
+    return 64 if d < 64 else (128 if d < 128 else 256)
 
 
 def _pad_head_dim(t: torch.Tensor, dp: int) -> torch.Tensor:
@@ -545,9 +545,9 @@ def hip_block_sparse_attention(Q, K, V, mask_bsr, scale: float, return_stats: bo
     dispatch.py:580-677). Q/K/V (S, D) or (..., S, D) sharing one mask.
     Honours `scale` (the reference NKI path used head_dim**-0.5 regardless).
     Stats come back as (..., S // b, b) in float32 (float64 for float64 input).
-    fp32 / bf16 with 128-blocks and head_dim below 128 other than 64 run the
-    MFMA kernels on operands zero-padded to head_dim 64 or 128; fp16 runs in
-    fp32 (widened operands, O rounded back once).
+    fp32 / bf16 with 128-blocks run the MFMA kernels at head_dim 64, 128 and
+    256, and on operands zero-padded to the next of those below 256; fp16
+    runs in fp32 (widened operands, O rounded back once).
     """
     if not (Q.shape == K.shape == V.shape):
         raise RuntimeError(f"Q, K, V shapes differ: {tuple(Q.shape)}, {tuple(K.shape)}, {tuple(V.shape)}")
@@ -642,10 +642,11 @@ def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, 
     Q/K/V/O/dO (S, D) or (..., S, D) sharing one mask; row_max / row_denom
     as hip_block_sparse_attention returns them. Returns (dQ, dK, dV).
 
-    bf16 with 128-blocks and head_dim 64 runs on the fp32 MFMA kernels: the
-    operands are widened on the device (exact) and the gradients rounded to
-    bf16 once at the end; the bf16 MFMA kernels serve head_dim 128. Other
-    head_dims below 128 are zero-padded to 64 or 128 first, as in the forward.
+    bf16 with 128-blocks and head_dim 64 or 256 runs on the fp32 MFMA
+    kernels: the operands are widened on the device (exact) and the gradients
+    rounded to bf16 once at the end; the bf16 MFMA kernels serve head_dim
+    128. Other head_dims below 256 are zero-padded to 64, 128 or 256 first,
+    as in the forward.
     """
     if not (Q.shape == K.shape == V.shape == O.shape == dO.shape):
         raise RuntimeError("Q, K, V, O, dO shapes differ")
@@ -658,7 +659,7 @@ def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, 
         grads = hip_block_sparse_attention_backward(*(_pad_head_dim(t, dp) for t in (Q, K, V, O, dO)), mask_bsr, scale,
                                                     row_max, row_denom)
         return tuple(gr[..., : Q.shape[-1]].contiguous() for gr in grads)
-    if Q.dtype == torch.bfloat16 and Q.shape[-1] == 64 and mask_bsr.block_size == 128 and scale > 0:
+    if Q.dtype == torch.bfloat16 and Q.shape[-1] in (64, 256) and mask_bsr.block_size == 128 and scale > 0:
         grads = hip_block_sparse_attention_backward(*(t.float() for t in (Q, K, V, O, dO)), mask_bsr, scale,
                                                     row_max, row_denom)
         return tuple(gr.to(torch.bfloat16) for gr in grads)
@@ -682,7 +683,7 @@ def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, 
         rm = _on(row_max, dev, sdt).reshape(H, Mt * b)
         rd = _on(row_denom, dev, sdt).reshape(H, Mt * b)
         dQ, dK, dV = (torch.empty_like(q) for _ in range(3))
-        ws = torch.empty(max(1, _lib.load().tsp_bsa_bwd_workspace_size(H, S, n_partials)), dtype=torch.uint8,
+        ws = torch.empty(max(1, _lib.load().tsp_bsa_bwd_workspace_size(H, S, D, n_partials)), dtype=torch.uint8,
                          device=dev)
         _lib.call("tsp_bsa_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), code, H, S, D,
                   rp.data_ptr(), ci.data_ptr(), cp.data_ptr(), crow.data_ptr(), nbc, b, float(scale), rm.data_ptr(),

@@ -514,6 +514,51 @@ def bench_attention(steps: int, warmup: int, cpu: bool = False):
     return [res, res32]
 
 
+def bench_attention_d256(steps: int, warmup: int):
+    """Config 5's mask and shape at head_dim 256 (32 heads x 8192 x 256):
+    forward in bf16 (bsa_fwd_bf16_stream<256>) and fp32
+    (bsa_fwd_f32_mfma<256>), backward in fp32 (the 16-row-tile row and
+    column passes). FLOPs as the head_dim-128 lines: 4 (forward) and 10
+    (backward) x nnzb x 128^2 x d x heads."""
+    import torch
+
+    import trnsparse_amd as ts
+    from trnsparse_amd import workloads as W
+    from trnsparse_amd.hip import _lib
+    from trnsparse_amd.hip import dispatch as Dp
+
+    Q, K, V, mask = W.cfg5_attention(d=256)
+    H, S, D = Q.shape
+    out = []
+    dev = torch.device("cuda", torch.cuda.current_device())
+    for dt in (torch.bfloat16, torch.float32):
+        Qd, Kd, Vd = (t.to(dt).to(dev) for t in (Q, K, V))
+        _, ms = time_gpu(lambda: ts.block_sparse_attention_tiled(Qd, Kd, Vd, mask), steps, warmup)
+        tf = 4.0 * mask.n_blocks * 128 * 128 * D * H / (ms * 1e-3) / 1e12
+        peak, key, tag = ((BF16_MFMA_PEAK_TFLOPS, "frac_bf16_mfma", "bf16") if dt == torch.bfloat16 else
+                          (FP32_MFMA_PEAK_TFLOPS, "frac_fp32_mfma", "fp32"))
+        out.append({"name": f"block_sparse_attention cfg5 mask 32x8192x256 {tag}", "value": round(tf * 1e3, 1),
+                    "unit": "GFLOP/s", "us": round(ms * 1e3, 1), key: round(tf / peak, 4)})
+        del Qd, Kd, Vd
+    rp, ci, _ = Dp._bsr_plan(mask.block_col_indices, mask.block_row_ptrs, S // 128, dev, holder=mask)
+    cp, crow, nbc, plan, (ni, ns, npart) = Dp._attn_bwd_plan(mask, H, S, dev)
+    ws = torch.empty(_lib.load().tsp_bsa_bwd_workspace_size(H, S, D, npart), dtype=torch.uint8, device=dev)
+    Qd, Kd, Vd = (t.float().to(dev) for t in (Q, K, V))
+    dO = torch.randn(Q.shape, generator=torch.Generator().manual_seed(14)).to(dev)
+    O, rm, rd = Dp.hip_block_sparse_attention(Qd, Kd, Vd, mask, D**-0.5, return_stats=True)
+    dQ, dK, dV = (torch.empty_like(Qd) for _ in range(3))
+    st = _lib.stream_handle(dev)
+    call = lambda: _lib.call("tsp_bsa_bwd", Qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), O.data_ptr(), dO.data_ptr(),
+                             _lib.TSP_F32, H, S, D, rp.data_ptr(), ci.data_ptr(), cp.data_ptr(), crow.data_ptr(), nbc,
+                             128, D**-0.5, rm.data_ptr(), rd.data_ptr(), dQ.data_ptr(), dK.data_ptr(), dV.data_ptr(),
+                             plan.data_ptr(), ni, ns, npart, ws.data_ptr(), st)
+    _, ms = time_gpu(call, steps, warmup)
+    tf = 10.0 * mask.n_blocks * 128 * 128 * D * H / (ms * 1e-3) / 1e12
+    out.append({"name": "block_sparse_attention backward cfg5 mask 32x8192x256 fp32", "value": round(tf * 1e3, 1),
+                "unit": "GFLOP/s", "us": round(ms * 1e3, 1), "frac_fp32_mfma": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)})
+    return out
+
+
 def bench_attention_backward(steps: int, warmup: int, cpu: bool = False):
     """Backward of block_sparse_attention_tiled at config 5 (tsp_bsa_bwd: the
     row pass for dQ, the column pass for dK / dV and the reduce of split
@@ -775,6 +820,7 @@ def main(argv=None) -> int:
             ("screened", lambda: bench_screened(10, 2, cpu=not args.no_cpu)),
             ("attention", lambda: bench_attention(10, 2, cpu=not args.no_cpu)),
             ("attention backward", lambda: bench_attention_backward(10, 2, cpu=not args.no_cpu)),
+            ("attention d256", lambda: bench_attention_d256(5, 2)),
             ("formats", lambda: bench_formats(5, 1, cpu=not args.no_cpu)),
             ("bsr spmv", lambda: bench_bsr_spmv(20, 3, cpu=not args.no_cpu)),
             ("csr ops", lambda: bench_csr_ops(5, 1)),

@@ -325,6 +325,17 @@ struct Geo {
   __host__ __device__ static constexpr int kswz(int key) { return D >= 128 ? (key & 15) : ((key >> 1) & 7); }
   __host__ __device__ static constexpr int vswz(int key) { return D >= 128 ? (key & 3) : ((key >> 1) & 1); }
 };
+// max / sum of v over lanes l and l ^ 32 (the two halves of a 64-lane wave)
+// with one v_permlane32_swap: with both operands v, the pair it returns holds
+// v[l] and v[l ^ 32] in every lane
+__device__ inline float halves_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float halves_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 }  // namespace att
 
 // D = 64 fits three wavefronts per SIMD (136 registers, 32 KiB of LDS per
@@ -465,7 +476,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : (D == 128 ? 2 : 1)) void bsa_fwd
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) mraw = fmaxf(mraw, sc[tt][v]);
-    mraw = fmaxf(mraw, __shfl_xor(mraw, 32, 64));
+    mraw = att::halves_max(mraw);
     mtrue = fmaxf(mtrue, mraw * scale_log2);
     // Lazy rescaling: P is taken relative to a reference max mref that only
     // moves when the true running max exceeds it by more than RESCALE (log2
@@ -497,8 +508,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : (D == 128 ? 2 : 1)) void bsa_fwd
         pb[tt][a] = __builtin_convertvector(pv, bf16x8);
       }
     }
-    lsum += __shfl_xor(lsum, 32, 64);
-    lrun += lsum;
+    lrun += lsum;  // this lane half's part; the halves are combined at the end
     // ---- O^T += V^T P^T. k-step (tt, a) covers keys 32tt + 16a + [0,16):
     // MFMA k index i < 4 is key 32tt + 16a + 4h + i, i >= 4 is key
     // 32tt + 16a + 8 + 4h + (i-4) — the lane's own S^T rows, so pb[tt][a]
@@ -538,6 +548,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : (D == 128 ? 2 : 1)) void bsa_fwd
 
   // ---- epilogue: O[q][32u + 8*(v/4) + 4h + v%4] = o / l (both relative to
   // mref); the returned denominator is relative to the true max
+  lrun = att::halves_sum(lrun);
   const bool empty = nblk == 0;
   const float lref = lrun > 1e-12f ? lrun : 1e-12f;
   const float inv = empty ? 0.f : 1.f / lref;

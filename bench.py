@@ -467,9 +467,21 @@ def bench_screened(steps: int, warmup: int, cpu: bool = False):
     A64, d64, B64 = Ad.double(), dd.double(), Bd.double()
     _, ms64 = time_gpu(lambda: ts.screened_spmm(A64, d64, B64, thr), max(2, steps // 2), warmup)
     tf64 = flops / (ms64 * 1e-3) / 1e12
-    res64 = {"name": "screened_spmm cfg4 n=4096 fp64", "value": round(tf64 * 1e3, 1), "unit": "GFLOP/s",
-             "us": round(ms64 * 1e3, 1), "frac_fp64_mfma": round(tf64 / FP64_MFMA_PEAK_TFLOPS, 4)}
-    return [res, res64]
+    res64 = {"name": "screened_spmm cfg4 n=4096 fp64", "value": round(tf64 * 1e3, 1),
+             "unit": "GFLOP/s", "us": round(ms64 * 1e3, 1), "frac_fp64_mfma": round(tf64 / FP64_MFMA_PEAK_TFLOPS, 4)}
+    del A64, d64, B64
+    # backward in fp32 (tsp_screened_spmm_backward: dA and dB, each a product
+    # over the active tile pairs with the same flop count as the forward)
+    from trnsparse_amd.hip import dispatch as Dp
+
+    G = torch.randn(B.shape, generator=torch.Generator().manual_seed(9)).cuda()
+    dev = Ad.device
+    _, msb = time_gpu(lambda: Dp._screened_backward(Ad, dd, thr, Bd, G, True, True, dev), max(2, steps // 2), warmup)
+    tfb = 2 * flops / (msb * 1e-3) / 1e12
+    resb = {"name": "screened_spmm backward cfg4 n=4096 fp32 (dA and dB)", "value": round(tfb * 1e3, 1),
+            "unit": "GFLOP/s", "us": round(msb * 1e3, 1), "frac_fp32_mfma": round(tfb / FP32_MFMA_PEAK_TFLOPS, 4),
+            "dense_equiv_gflops": round(2 * dense_flops / (msb * 1e-3) / 1e9, 1)}
+    return [res, res64, resb]
 
 
 def bench_attention(steps: int, warmup: int, cpu: bool = False):

@@ -263,6 +263,24 @@ int tsp_screened_spmm_noalloc(const void* A, int dtype, int64_t lda,
                               const void* B, int64_t ldb, int64_t ncols,
                               void* C, int64_t ldc, void* stream);
 
+/* Gradients of C = (A * mask) @ B with the same mask:
+ *   dA = (dC @ B^T) * mask   (m, m; stride ldda), written when dA != NULL
+ *   dB = (A * mask)^T @ dC   (m, ncols; stride lddb), written when dB != NULL
+ * dC (m, ncols; stride lddc) in `dtype`; no gradient for diag or the
+ * threshold (the mask is discrete). The mask is not materialised: 128x128
+ * tile pairs whose largest Q product is at or below the threshold are
+ * skipped (dA tiles written as zeros). `workspace` as for
+ * tsp_screened_spmm. TSP_F32 runs the MFMA kernels, TSP_F64 the generic
+ * ones. Replaces _ScreenedSpMMFunction.backward
+ * (trnsparse/nki/dispatch.py:478-484). */
+int tsp_screened_spmm_backward(const void* A, int dtype, int64_t lda,
+                               const void* diag, int diag_dtype,
+                               double threshold_sqrt, int64_t m,
+                               const void* B, int64_t ldb, int64_t ncols,
+                               const void* dC, int64_t lddc, void* dA,
+                               int64_t ldda, void* dB, int64_t lddb,
+                               void* workspace, void* stream);
+
 /* ======================================================================
  * Block-sparse attention forward, per head h < n_heads:
  *   O[h] = softmax_rows(scale * Q[h] K[h]^T restricted to the stored mask

@@ -270,6 +270,20 @@ def screened_spmm(A, diag, B, threshold, absolute=False):
     return Am @ Bv
 
 
+def screened_spmm_backward(A, diag, B, threshold, dC, absolute=False):
+    """(dA, dB) of C = (A * mask) @ B in float64 (reference
+    nki/dispatch.py:478-484: grad_A = (grad_out @ B.T) * mask, grad_B =
+    (A * mask).T @ grad_out; no gradient to diag or threshold). `absolute`
+    gives the same products over |A|, |B|, |dC| (the error scale)."""
+    mask = screened_mask(diag, threshold)
+    Av, Bv, Gv = (x.astype(np.float64) for x in (A, B, dC))
+    if absolute:
+        Av, Bv, Gv = np.abs(Av), np.abs(Bv), np.abs(Gv)
+    dA = np.where(mask, Gv @ Bv.T, 0.0)
+    dB = np.where(mask, Av, 0.0).T @ Gv
+    return dA, dB
+
+
 # ------------------------------------------------------------ attention
 
 

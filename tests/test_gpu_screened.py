@@ -194,3 +194,112 @@ def test_cfg4_full_size(hip_backend):
     mask = torch.from_numpy(ref.screened_mask(diag.numpy(), thr))
     sc = (A.abs().double() * mask) @ (B.abs().double() @ ones)
     assert ((lhs - rhs).abs() / sc).max().item() <= TOL
+
+
+# ------------------------------------------------------------------ backward
+
+
+def _check_backward(A, diag, B, thr, G, dA, dB, tol, rows=None):
+    """dA, dB against ref.screened_spmm_backward with the |.| error scale;
+    `rows` restricts the dA check and the dB check to those rows."""
+    An, Bn, Gn = (t.double().cpu().numpy() for t in (A, B, G))
+    dn = diag.cpu().numpy()
+    if rows is None:
+        eA, eB = ref.screened_spmm_backward(An, dn, Bn, thr, Gn)
+        sA, sB = ref.screened_spmm_backward(An, dn, Bn, thr, Gn, absolute=True)
+    else:
+        mask = ref.screened_mask(dn, thr)
+        eA = np.where(mask[rows], Gn[rows] @ Bn.T, 0.0)
+        sA = np.where(mask[rows], np.abs(Gn[rows]) @ np.abs(Bn).T, 0.0)
+        eB = np.where(mask[:, rows], An[:, rows], 0.0).T @ Gn
+        sB = np.where(mask[:, rows], np.abs(An[:, rows]), 0.0).T @ np.abs(Gn)
+    if dA is not None:
+        gA = dA.double().cpu().numpy()
+        gA = gA if rows is None else gA[rows]
+        assert ref.scaled_error(gA, eA, np.maximum(sA, 1e-300)) <= tol
+        # masked pairs are exact zeros
+        assert (gA[sA == 0] == 0).all()
+    if dB is not None:
+        gB = dB.double().cpu().numpy()
+        gB = gB if rows is None else gB[rows]
+        assert ref.scaled_error(gB, eB, np.maximum(sB, 1e-300)) <= tol
+
+
+@pytest.mark.parametrize("n,N,thr", [
+    (200, 70, 1e-6),      # partial tiles on both sides, some tile pairs skipped
+    (384, 128, 1e-3),     # whole tiles
+    (257, 1, 1e-9),       # one column
+    (128, 300, 0.0),      # nothing masked
+    (150, 20, 1e30),      # everything masked: exact zeros
+])
+def test_backward_f32_vs_oracle(hip_backend, n, N, thr):
+    g = torch.Generator().manual_seed(n + N)
+    diag = torch.pow(10.0, torch.empty(n).uniform_(-8.0, 0.0, generator=g))
+    diag[: n // 3] *= 1e-6                               # rows whose tiles drop out
+    A = torch.randn(n, n, generator=g)
+    B = torch.randn(n, N, generator=g)
+    G = torch.randn(n, N, generator=g)
+    Ad, Bd = A.cuda().requires_grad_(True), B.cuda().requires_grad_(True)
+    out = ts.screened_spmm(Ad, diag.cuda(), Bd, threshold=thr)
+    out.backward(G.cuda())
+    assert Ad.grad.dtype == torch.float32 and Bd.grad.shape == B.shape
+    _check_backward(A, diag, B, thr, G, Ad.grad, Bd.grad, TOL)
+
+
+def test_backward_one_input_grad(hip_backend):
+    """Only A (then only B) requires grad: the other product is not run."""
+    g = torch.Generator().manual_seed(4)
+    n, N, thr = 160, 33, 1e-5
+    diag = torch.pow(10.0, torch.empty(n).uniform_(-8.0, 0.0, generator=g))
+    A, B, G = torch.randn(n, n, generator=g), torch.randn(n, N, generator=g), torch.randn(n, N, generator=g)
+    Ad = A.cuda().requires_grad_(True)
+    ts.screened_spmm(Ad, diag.cuda(), B.cuda(), threshold=thr).backward(G.cuda())
+    _check_backward(A, diag, B, thr, G, Ad.grad, None, TOL)
+    Bd = B.cuda().requires_grad_(True)
+    ts.screened_spmm(A.cuda(), diag.cuda(), Bd, threshold=thr).backward(G.cuda())
+    _check_backward(A, diag, B, thr, G, None, Bd.grad, TOL)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float64, 1e-12), (torch.bfloat16, 2e-2)])
+def test_backward_f64_and_bf16(hip_backend, dtype, tol):
+    """fp64 runs the generic backward kernels (f64 diag too), bf16 the fp32
+    MFMA kernels on widened operands with one rounding of the gradients."""
+    g = torch.Generator().manual_seed(5)
+    n, N, thr = 140, 24, 1e-6
+    diag = torch.pow(10.0, torch.empty(n, dtype=torch.float64).uniform_(-8.0, 0.0, generator=g))
+    if dtype != torch.float64:
+        diag = diag.float()
+    A, B, G = (torch.randn(n, k, generator=g, dtype=torch.float64).to(dtype) for k in (n, N, N))
+    Ad, Bd = A.cuda().requires_grad_(True), B.cuda().requires_grad_(True)
+    ts.screened_spmm(Ad, diag.cuda(), Bd, threshold=thr).backward(G.cuda())
+    assert Ad.grad.dtype == dtype and Bd.grad.dtype == dtype
+    _check_backward(A, diag, B, thr, G, Ad.grad, Bd.grad, tol)
+
+
+def test_backward_cfg4_full_size(hip_backend):
+    """cfg4 (4096 x 4096, N = 4096): sampled rows of dA and dB against the
+    oracle, and at full size dA @ 1 = ((dC B^T) * mask) @ 1 checked through
+    the forward kernel: the row sums of dA equal screened_spmm of dC B^T
+    with a ones vector (both apply the same mask)."""
+    A, diag, B, thr = W.cfg4_screened()
+    g = torch.Generator().manual_seed(6)
+    G = torch.randn(B.shape, generator=g)
+    Ad, Bd = A.cuda().requires_grad_(True), B.cuda().requires_grad_(True)
+    ts.screened_spmm(Ad, diag.cuda(), Bd, threshold=thr).backward(G.cuda())
+    rows = np.r_[0:64, 2000:2048, 4032:4096]
+    _check_backward(A, diag, B, thr, G, Ad.grad, Bd.grad, TOL, rows=rows)
+    # full size: dA @ 1 == (X * mask) @ 1 with X = dC B^T, via the forward kernel
+    X = (G.cuda().double() @ B.cuda().double().T).float()
+    ones = torch.ones(A.shape[0], 1, device="cuda")
+    lhs = (Ad.grad.double() @ ones.double()).cpu()
+    rhs = ts.screened_spmm(X, diag.cuda(), ones, threshold=thr).double().cpu()
+    mask = torch.from_numpy(ref.screened_mask(diag.numpy(), thr)).cuda()
+    sc = ((X.abs().double() * mask) @ ones.double()).cpu() + 1e-30
+    assert ((lhs - rhs).abs() / sc).max().item() <= 1e-4
+    # dB column sums: 1^T dB = 1^T (A * mask)^T dC = ((A * mask) @ 1)^T dC
+    am1 = ts.screened_spmm(A.cuda(), diag.cuda(), torch.ones(A.shape[0], 1, device="cuda"), threshold=thr)
+    lhs = Bd.grad.double().sum(0).cpu()
+    rhs = (am1.double().T @ G.cuda().double()).squeeze(0).cpu()
+    scb = (ts.screened_spmm(A.abs().cuda(), diag.cuda(), torch.ones(A.shape[0], 1, device="cuda"),
+                            threshold=thr).double().T @ G.abs().cuda().double()).squeeze(0).cpu() + 1e-30
+    assert ((lhs - rhs).abs() / scb).max().item() <= 1e-4

@@ -327,6 +327,44 @@ def test_screened_mask_matches_torch_semantics():
         np.testing.assert_array_equal(ref.screened_mask(d, thr), tmask)
 
 
+def test_screened_backward_vs_torch_autograd():
+    """ref.screened_spmm_backward against float64 torch autograd of
+    (A * mask) @ B with the mask built by torch (a different route to the
+    same gradients), on a mask that keeps part of the pairs."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(9)
+    n, N = 48, 7
+    d = (10.0 ** rng.uniform(-6, 0, n)).astype(np.float32)
+    A, B, G = rng.standard_normal((n, n)), rng.standard_normal((n, N)), rng.standard_normal((n, N))
+    thr = 1e-4
+    At = torch.tensor(A, requires_grad=True)
+    Bt = torch.tensor(B, requires_grad=True)
+    Q = torch.sqrt(torch.abs(torch.from_numpy(d)))
+    mask = ((Q.unsqueeze(-1) * Q.unsqueeze(0)) > math.sqrt(thr)).double()
+    assert 0 < mask.sum() < n * n
+    ((At * mask) @ Bt).backward(torch.from_numpy(G))
+    dA, dB = ref.screened_spmm_backward(A, d, B, thr, G)
+    np.testing.assert_allclose(dA, At.grad.numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(dB, Bt.grad.numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_screened_backward_closed_forms():
+    """Threshold 0 (every pair kept): dA = dC B^T, dB = A^T dC; a threshold
+    above every pair: both zero; the absolute form bounds the signed one."""
+    rng = np.random.default_rng(10)
+    n, N = 33, 5
+    d = np.abs(rng.standard_normal(n)).astype(np.float32) + 0.1
+    A, B, G = rng.standard_normal((n, n)), rng.standard_normal((n, N)), rng.standard_normal((n, N))
+    dA, dB = ref.screened_spmm_backward(A, d, B, 0.0, G)
+    np.testing.assert_allclose(dA, G @ B.T, rtol=1e-12)
+    np.testing.assert_allclose(dB, A.T @ G, rtol=1e-12)
+    dA, dB = ref.screened_spmm_backward(A, d, B, 1e30, G)
+    assert not dA.any() and not dB.any()
+    sA, sB = ref.screened_spmm_backward(A, d, B, 0.05, G, absolute=True)
+    dA, dB = ref.screened_spmm_backward(A, d, B, 0.05, G)
+    assert (np.abs(dA) <= sA + 1e-12).all() and (np.abs(dB) <= sB + 1e-12).all()
+
+
 # ------------------------------------------------------------- attention
 
 

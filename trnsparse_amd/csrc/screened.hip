@@ -27,11 +27,14 @@
 //   screened_f64_dma    fp64 (even m and strides): the same structure on
 //                       v_mfma_f64_16x16x4_f64 (mfma_f64.h operand tiles).
 //   screened_generic    other or unaligned operands: one thread per output.
+//   screened_bwd_a_f32 / screened_bwd_b_f32 / screened_bwd_*_generic
+//                       the backward (below).
 #include <atomic>
 
 #include "lds_dma.h"
 #include "mfma_f32.h"
 #include "mfma_f64.h"
+#include "f32_pair_tiles.h"
 
 namespace {
 
@@ -434,6 +437,329 @@ __global__ __launch_bounds__(256) void screened_generic(const T* __restrict__ A,
   C[i * ldc + c] = (T)acc;
 }
 
+// ---------------------------------------------------------------- backward
+//
+// The reference backward (trnsparse/nki/dispatch.py:478-484) materialises
+// the mask and runs two dense products:
+//   dA = (dC @ B^T) * mask            dB = (A * mask)^T @ dC
+// Neither the mask nor A * mask is formed here; both products skip the
+// 128x128 tile pairs (I, J) with fl(Qmax_I * Qmax_J) <= thr, where every
+// pair is masked (the forward's tile skip, with the same caveat for
+// non-finite entries inside such a tile):
+//   screened_bwd_a_f32   dA tile (I, J) per workgroup. A masked pair writes
+//       zeros; the others run the BSR backward's SDDMM engine (row tiles of
+//       dC and B, k = the N columns, f32_pair_tiles.h) and the mask
+//       multiplies each result in the epilogue (v * 1 or v * 0, the
+//       reference's product with the float mask).
+//   screened_bwd_b_f32   dB tile (rows J = columns of A, a 128-column tile
+//       of N) per workgroup, walking the row tiles I of A active with J: the
+//       A tile [k = rows i][columns] is the A^T operand (k tile reads),
+//       masked after its LDS read with Q_i of the slab staged beside the
+//       ring; dC rows of I are the [k][n] operand.
+//   screened_bwd_a_generic / screened_bwd_b_generic   fp64 and operands the
+//       streamed kernels do not take: one thread per output.
+namespace P = tsp::f32pair;
+
+template <typename QT>
+__global__ __launch_bounds__(256) void screened_bwd_a_f32(const float* __restrict__ G, int64_t ldg,
+                                                          const float* __restrict__ B, int64_t ldb, int64_t ncols,
+                                                          const QT* __restrict__ Q, const QT* __restrict__ qmax,
+                                                          QT thr, int64_t m, int nmt, float* __restrict__ dA,
+                                                          int64_t ldda) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[P::NST * P::STAGE];
+  // XCD-aware: XCD x takes a contiguous range of tiles, so the tiles of one
+  // row tile I share its dC panel in that XCD's L2
+  const int64_t ntiles = (int64_t)nmt * nmt;
+  const int64_t gid = blockIdx.x, xcd = gid & 7, slot = gid >> 3;
+  const int64_t per = tsp::ceil_div(ntiles, 8);
+  const int64_t tix = xcd * per + slot;
+  if (slot >= per || tix >= ntiles) return;
+  const int I = (int)(tix / nmt), J = (int)(tix % nmt);
+  const int64_t r0 = (int64_t)I * TILE, c0 = (int64_t)J * TILE;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+
+  if (!(qmax[I] * qmax[J] > thr)) {
+    // every pair of the tile is masked: zeros, 4 columns per thread, 8 rows per pass
+    const int64_t c = c0 + 4 * (tid & 31);
+    for (int rr = tid >> 5; rr < TILE; rr += 8) {
+      const int64_t r = r0 + rr;
+      if (r >= m) break;
+      float* p = dA + r * ldda + c;
+      if (c + 3 < m && ((uintptr_t)p & 15) == 0) {
+        *(f32x4*)p = f32x4{};
+      } else {
+        for (int e = 0; e < 4; ++e)
+          if (c + e < m) p[e] = 0.f;
+      }
+    }
+    return;
+  }
+
+  const int wm = w & 1, wn = w >> 1, h = lane >> 5, l32 = lane & 31;
+  const P::i32x4 rsg = tsp::dma::make_rsrc(G, (uint32_t)(m * ldg * 4));
+  const P::i32x4 rsb = tsp::dma::make_rsrc(B, (uint32_t)(m * ldb * 4));
+  const uint32_t lds0 = tsp::dma::lds_addr(lds);
+  auto issue = [&](int s) {
+    const uint32_t st = lds0 + (s % P::NST) * P::STAGE;
+    P::dma_row_tile(rsg, r0, ldg, (int64_t)s * P::KC, ncols, st, w, lane);
+    P::dma_row_tile(rsb, c0, ldb, (int64_t)s * P::KC, ncols, st + P::TILE, w, lane);
+  };
+  P::Acc4 acc;
+  acc.zero();
+  const int ar = wm * 64 + l32, br = wn * 64 + l32;
+  struct Ops {
+    float x[2][4], y[2][4];
+  };
+  auto fetch = [&](const uint8_t* st, int gg, Ops& o) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const f32x4 a = P::frag_row(st, ar + 32 * t, gg, h);
+      const f32x4 b = P::frag_row(st + P::TILE, br + 32 * t, gg, h);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        o.x[t][s] = a[s];
+        o.y[t][s] = b[s];
+      }
+    }
+  };
+  const int nsteps = (int)tsp::ceil_div(ncols, P::KC);
+  if (nsteps > 0) issue(0);
+  for (int s = 0; s < nsteps; ++s) {
+    tsp::dma::wait_vm<0>();
+    tsp::dma::barrier();
+    if (s + 1 < nsteps) issue(s + 1);
+    const uint8_t* st = lds + (s % P::NST) * P::STAGE;
+    Ops o[2];
+    fetch(st, 0, o[0]);
+#pragma unroll
+    for (int gg = 0; gg < P::KC / 8; ++gg) {
+      if (gg + 1 < P::KC / 8) fetch(st, gg + 1, o[(gg + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      acc.mma(o[gg & 1].x, o[gg & 1].y);
+    }
+  }
+  // lane holds column l32 of subtile u and rows 8*(v/4) + 4h + v%4 of subtile t;
+  // Q is padded with zeros to whole tiles
+  QT qc[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) qc[u] = Q[c0 + wn * 64 + 32 * u + l32];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t r = r0 + wm * 64 + 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
+      if (r >= m) continue;
+      const QT qr = Q[r];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int64_t c = c0 + wn * 64 + 32 * u + l32;
+        if (c < m) dA[r * ldda + c] = acc.a[t][u][v] * ((qr * qc[u] > thr) ? 1.0f : 0.0f);
+      }
+    }
+}
+
+template <typename QT>
+__global__ __launch_bounds__(256) void screened_bwd_b_f32(const float* __restrict__ A, int64_t lda,
+                                                          const float* __restrict__ G, int64_t ldg, int64_t ncols,
+                                                          const QT* __restrict__ Q, const QT* __restrict__ qmax,
+                                                          QT thr, int64_t m, int nmt, int nnt, float* __restrict__ dB,
+                                                          int64_t lddb) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[P::NST * P::STAGE];
+  __shared__ __attribute__((aligned(16))) QT qs[2][P::KC];
+  // XCD-aware: the column tiles of one row tile J share an XCD (and A's panel in its L2)
+  int64_t jt64;
+  int ntile;
+  if (!T32::tile_item(blockIdx.x, nmt, nnt, nullptr, jt64, ntile)) return;
+  const int J = (int)jt64;
+  const int64_t k0 = (int64_t)J * TILE, n0 = (int64_t)ntile * TILE;
+  const QT qJ = qmax[J];
+  auto active = [&](int t) { return qmax[t] * qJ > thr; };
+  int nact = 0;
+  for (int t = 0; t < nmt; ++t) nact += active(t) ? 1 : 0;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w & 1, wn = w >> 1, h = lane >> 5, l32 = lane & 31;
+  P::Acc4 acc;
+  acc.zero();
+  // A^T operand: output rows (columns of A) ac2 + t; row subtile t holds rows wm*64 + 2i + t
+  const int ac2 = wm * 64 + 2 * l32, bc2 = wn * 64 + 2 * l32;
+  if (nact > 0) {
+    const P::i32x4 rsa = tsp::dma::make_rsrc(A, (uint32_t)(m * lda * 4));
+    const P::i32x4 rsg = tsp::dma::make_rsrc(G, (uint32_t)(m * ldg * 4));
+    const uint32_t lds0 = tsp::dma::lds_addr(lds);
+    QT qk[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) qk[t] = Q[k0 + ac2 + t];  // padded with zeros to whole tiles
+    constexpr int SPT = TILE / P::KC;  // slabs per row tile
+    int it_issue = -1;                 // row tile of the slabs being issued (advanced in order)
+    QT qnext = 0;
+    auto issue = [&](int s) {
+      if ((s % SPT) == 0) {
+        ++it_issue;
+        while (!active(it_issue)) ++it_issue;
+      }
+      const int64_t i0 = (int64_t)it_issue * TILE + (s % SPT) * P::KC;
+      const uint32_t st = lds0 + (s % P::NST) * P::STAGE;
+      // rows i0 .. i0+64 of A (past m: zero) as [k][columns k0 .. k0+128]
+      P::dma_k_tile(rsa, i0, lda, k0, st, w, lane);
+      P::dma_k_tile(rsg, i0, ldg, n0, st + P::TILE, w, lane);
+      if (w == 0) qnext = Q[i0 + lane];  // into qs before its barrier
+    };
+    struct Ops {
+      float x[2][4], y[2][4];
+    };
+    auto fetch = [&](const uint8_t* st, const QT* qi, int gg, Ops& o) {
+      P::frag_k2(st, ac2, gg, h, o.x);
+      P::frag_k2(st + P::TILE, bc2, gg, h, o.y);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const QT q = qi[8 * gg + 4 * h + s];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) o.x[t][s] *= (q * qk[t] > thr) ? 1.0f : 0.0f;
+      }
+    };
+    const int nsteps = nact * SPT;
+    issue(0);
+    if (w == 0) qs[0][lane] = qnext;
+    for (int s = 0; s < nsteps; ++s) {
+      tsp::dma::wait_vm<0>();  // this wave's loads of slab s are done
+      tsp::dma::barrier();     // slab s and its Q_i are visible; stage (s+1) % 2 is free
+      if (s + 1 < nsteps) issue(s + 1);
+      const uint8_t* st = lds + (s % P::NST) * P::STAGE;
+      const QT* qi = qs[s & 1];
+      Ops o[2];
+      fetch(st, qi, 0, o[0]);
+#pragma unroll
+      for (int gg = 0; gg < P::KC / 8; ++gg) {
+        if (gg + 1 < P::KC / 8) fetch(st, qi, gg + 1, o[(gg + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        acc.mma(o[gg & 1].x, o[gg & 1].y);
+      }
+      if (w == 0 && s + 1 < nsteps) qs[(s + 1) & 1][lane] = qnext;
+    }
+  }
+  // accumulator (t, u) element v of lane (h, l32): output row k0 + wm*64 +
+  // 2(8(v/4) + 4h + v%4) + t, column n0 + wn*64 + 2 l32 + u; (u = 0, 1) is
+  // one 8-byte store
+  const int64_t c = n0 + bc2;
+  const bool pair = c + 1 < ncols && (lddb & 1) == 0 && ((uintptr_t)dB & 7) == 0;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int64_t rb = k0 + wm * 64 + 2 * (8 * (v >> 2) + 4 * h + (v & 3));
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int64_t r = rb + t;
+      if (r < m) {
+        if (pair) {
+          *(f32x2*)(dB + r * lddb + c) = f32x2{acc.a[t][0][v], acc.a[t][1][v]};
+        } else {
+          if (c < ncols) dB[r * lddb + c] = acc.a[t][0][v];
+          if (c + 1 < ncols) dB[r * lddb + c + 1] = acc.a[t][1][v];
+        }
+      }
+    }
+  }
+}
+
+// dA[r][c] = (sum_n G[r][n] B[c][n]) * mask(r, c)
+template <typename T, typename QT>
+__global__ __launch_bounds__(256) void screened_bwd_a_generic(const T* __restrict__ G, int64_t ldg,
+                                                              const T* __restrict__ B, int64_t ldb, int64_t ncols,
+                                                              const QT* __restrict__ Q, QT thr, int64_t m,
+                                                              T* __restrict__ dA, int64_t ldda) {
+  typedef typename tsp::Acc<T>::type AccT;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= m * m) return;
+  const int64_t r = t / m, c = t - r * m;
+  AccT acc = 0;
+  for (int64_t k = 0; k < ncols; ++k) acc += (AccT)G[r * ldg + k] * (AccT)B[c * ldb + k];
+  dA[r * ldda + c] = (T)acc * ((Q[r] * Q[c] > thr) ? (T)1 : (T)0);
+}
+
+// dB[k][n] = sum_i (A[i][k] * mask(i, k)) G[i][n]
+template <typename T, typename QT>
+__global__ __launch_bounds__(256) void screened_bwd_b_generic(const T* __restrict__ A, int64_t lda,
+                                                              const T* __restrict__ G, int64_t ldg, int64_t ncols,
+                                                              const QT* __restrict__ Q, QT thr, int64_t m,
+                                                              T* __restrict__ dB, int64_t lddb) {
+  typedef typename tsp::Acc<T>::type AccT;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= m * ncols) return;
+  const int64_t k = t / ncols, n = t - k * ncols;
+  const QT qk = Q[k];
+  AccT acc = 0;
+  for (int64_t i = 0; i < m; ++i) {
+    const T a = A[i * lda + k] * ((Q[i] * qk > thr) ? (T)1 : (T)0);
+    acc += (AccT)a * (AccT)G[i * ldg + n];
+  }
+  dB[k * lddb + n] = (T)acc;
+}
+
+template <typename QT>
+int launch_backward(const void* A, int dtype, int64_t lda, const void* diag, double thr_sqrt, int64_t m, const void* B,
+                    int64_t ldb, int64_t ncols, const void* G, int64_t ldg, void* dA, int64_t ldda, void* dB,
+                    int64_t lddb, void* ws, hipStream_t st) {
+  const int64_t nmt = tsp::ceil_div(m, TILE);
+  QT* Q = (QT*)ws;
+  QT* qmax = Q + nmt * TILE;
+  const QT thr = (QT)thr_sqrt;
+  if (nmt > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_screened_spmm_backward: too many rows");
+  hipLaunchKernelGGL((screened_q<QT>), dim3((unsigned)nmt), dim3(TILE), 0, st, (const QT*)diag, m, Q, qmax);
+  int rc = tsp::check_launch("screened_q launch");
+  if (rc) return rc;
+  // streamed fp32 kernels: 16-byte aligned rows, buffer offsets within 32 bits
+  auto fits = [&](const void* p, int64_t ld) {
+    return (ld % 4) == 0 && ((uintptr_t)p % 16) == 0 && (m + TILE) * ld * 4 + 4 * TILE <= (int64_t)UINT32_MAX;
+  };
+  const bool f32 = dtype == TSP_F32 && fits(G, ldg);
+  if (dA) {
+    if (f32 && fits(B, ldb)) {
+      const int64_t grid = tsp::ceil_div(nmt * nmt, 8) * 8;
+      if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_screened_spmm_backward: problem too large");
+      hipLaunchKernelGGL((screened_bwd_a_f32<QT>), dim3((unsigned)grid), dim3(256), 0, st, (const float*)G, ldg,
+                         (const float*)B, ldb, ncols, (const QT*)Q, (const QT*)qmax, thr, m, (int)nmt, (float*)dA,
+                         ldda);
+      rc = tsp::check_launch("screened_bwd_a_f32 launch");
+    } else {
+      const int64_t grid = tsp::ceil_div(m * m, 256);
+      if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_screened_spmm_backward: problem too large");
+      if (dtype == TSP_F32)
+        hipLaunchKernelGGL((screened_bwd_a_generic<float, QT>), dim3((unsigned)grid), dim3(256), 0, st,
+                           (const float*)G, ldg, (const float*)B, ldb, ncols, (const QT*)Q, thr, m, (float*)dA, ldda);
+      else
+        hipLaunchKernelGGL((screened_bwd_a_generic<double, QT>), dim3((unsigned)grid), dim3(256), 0, st,
+                           (const double*)G, ldg, (const double*)B, ldb, ncols, (const QT*)Q, thr, m, (double*)dA,
+                           ldda);
+      rc = tsp::check_launch("screened_bwd_a_generic launch");
+    }
+    if (rc) return rc;
+  }
+  if (dB) {
+    if (f32 && fits(A, lda)) {
+      const int64_t nnt = tsp::ceil_div(ncols, TILE);
+      const int64_t grid = tsp::ceil_div(nmt, 8) * 8 * nnt;
+      if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_screened_spmm_backward: problem too large");
+      hipLaunchKernelGGL((screened_bwd_b_f32<QT>), dim3((unsigned)grid), dim3(256), 0, st, (const float*)A, lda,
+                         (const float*)G, ldg, ncols, (const QT*)Q, (const QT*)qmax, thr, m, (int)nmt, (int)nnt,
+                         (float*)dB, lddb);
+      rc = tsp::check_launch("screened_bwd_b_f32 launch");
+    } else {
+      const int64_t grid = tsp::ceil_div(m * ncols, 256);
+      if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_screened_spmm_backward: problem too large");
+      if (dtype == TSP_F32)
+        hipLaunchKernelGGL((screened_bwd_b_generic<float, QT>), dim3((unsigned)grid), dim3(256), 0, st,
+                           (const float*)A, lda, (const float*)G, ldg, ncols, (const QT*)Q, thr, m, (float*)dB, lddb);
+      else
+        hipLaunchKernelGGL((screened_bwd_b_generic<double, QT>), dim3((unsigned)grid), dim3(256), 0, st,
+                           (const double*)A, lda, (const double*)G, ldg, ncols, (const QT*)Q, thr, m, (double*)dB,
+                           lddb);
+      rc = tsp::check_launch("screened_bwd_b_generic launch");
+    }
+    if (rc) return rc;
+  }
+  return TSP_OK;
+}
+
 template <typename QT>
 int launch(const void* A, int dtype, int64_t lda, const void* diag, double thr_sqrt, int64_t m, const void* B,
            int64_t ldb, int64_t ncols, void* C, int64_t ldc, void* ws, hipStream_t st) {
@@ -580,4 +906,35 @@ extern "C" int tsp_screened_spmm(const void* A, int dtype, int64_t lda, const vo
   return diag_dtype == TSP_F32
              ? launch<float>(A, dtype, lda, diag, threshold_sqrt, m, B, ldb, ncols, C, ldc, workspace, st)
              : launch<double>(A, dtype, lda, diag, threshold_sqrt, m, B, ldb, ncols, C, ldc, workspace, st);
+}
+
+extern "C" int tsp_screened_spmm_backward(const void* A, int dtype, int64_t lda, const void* diag, int diag_dtype,
+                                          double threshold_sqrt, int64_t m, const void* B, int64_t ldb, int64_t ncols,
+                                          const void* dC, int64_t lddc, void* dA, int64_t ldda, void* dB,
+                                          int64_t lddb, void* workspace, void* stream) {
+  if (dtype != TSP_F32 && dtype != TSP_F64)
+    return tsp::fail(TSP_EUNSUPPORTED, "tsp_screened_spmm_backward: dtype %d not supported", dtype);
+  if (diag_dtype != TSP_F32 && diag_dtype != TSP_F64)
+    return tsp::fail(TSP_EUNSUPPORTED, "tsp_screened_spmm_backward: diag dtype %d not supported", diag_dtype);
+  if (m < 0 || ncols < 0) return tsp::fail(TSP_EINVAL, "tsp_screened_spmm_backward: negative size");
+  if (lddc < ncols || (dA && (ldb < ncols || ldda < m)) || (dB && (lda < m || lddb < ncols)))
+    return tsp::fail(TSP_EINVAL, "tsp_screened_spmm_backward: leading dimension too small");
+  if (m == 0 || (!dA && !dB)) return TSP_OK;
+  if (!diag || !dC || !workspace || (dA && !B) || (dB && !A))
+    return tsp::fail(TSP_EINVAL, "tsp_screened_spmm_backward: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  if (ncols == 0) {  // dA = 0 (an empty sum); dB has no columns
+    if (!dA) return TSP_OK;
+    const int64_t es = dtype == TSP_F64 ? 8 : 4;
+    for (int64_t r = 0; r < m; ++r) {
+      int rc = tsp::zero_fill((char*)dA + r * ldda * es, m * es, st);
+      if (rc) return rc;
+    }
+    return TSP_OK;
+  }
+  return diag_dtype == TSP_F32
+             ? launch_backward<float>(A, dtype, lda, diag, threshold_sqrt, m, B, ldb, ncols, dC, lddc, dA, ldda, dB,
+                                      lddb, workspace, st)
+             : launch_backward<double>(A, dtype, lda, diag, threshold_sqrt, m, B, ldb, ncols, dC, lddc, dA, ldda, dB,
+                                       lddb, workspace, st);
 }

@@ -58,6 +58,8 @@ SIGNATURES: dict[str, tuple] = {
     "tsp_screened_spmm": (_INT, [_P, _INT, _I64, _P, _INT, _DBL, _I64, _P, _I64, _I64, _P, _I64, _P, _P]),
     "tsp_screened_spmm_noalloc_max_rows": (_I64, [_INT]),
     "tsp_screened_spmm_noalloc": (_INT, [_P, _INT, _I64, _P, _INT, _DBL, _I64, _P, _I64, _I64, _P, _I64, _P]),
+    "tsp_screened_spmm_backward": (_INT, [_P, _INT, _I64, _P, _INT, _DBL, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P,
+                                          _I64, _P, _P]),
     "tsp_bsa_fwd": (_INT, [_P, _P, _P, _INT, _I64, _I64, _I64, _P, _P, _I64, _DBL, _P, _P, _P, _P]),
     "tsp_format_workspace_size": (_I64, [_I64]),
     "tsp_bsr_from_dense_pattern": (_INT, [_P, _INT, _I64, _I64, _I64, _I64, _DBL, _P, _P, _P, _P]),

@@ -487,12 +487,37 @@ def _screened_forward(A, diag, threshold, B, dev):
     return C
 
 
+def _screened_backward(A, diag, threshold, B, G, need_a: bool, need_b: bool, dev):
+    """(dA, dB) of C = (A * mask) @ B through tsp_screened_spmm_backward: dA =
+    (dC @ B^T) * mask, dB = (A * mask)^T @ dC, the mask never formed (reference
+    dispatch.py:478-484 builds it). 16-bit operands are widened to fp32 on the
+    device and the gradients rounded back once, as in the forward."""
+    import math
+
+    if A.dtype in (torch.bfloat16, torch.float16):
+        dA, dB = _screened_backward(_on(A, dev, torch.float32), diag, threshold, _on(B, dev, torch.float32),
+                                    _on(G, dev, torch.float32), need_a, need_b, dev)
+        return (dA.to(A.dtype) if dA is not None else None, dB.to(A.dtype) if dB is not None else None)
+    M = A.shape[0]
+    Ad, Bd, Gd, dd = _on(A, dev), _on(B, dev), _on(G, dev, A.dtype), _on(diag, dev)
+    ncols = Gd.shape[1]
+    dA = torch.empty(M, M, dtype=A.dtype, device=dev) if need_a else None
+    dB = torch.empty(M, ncols, dtype=A.dtype, device=dev) if need_b else None
+    dcode = _lib.dtype_code(dd.dtype)
+    ws = torch.empty(max(1, _lib.load().tsp_screened_workspace_size(M, dcode)), dtype=torch.uint8, device=dev)
+    _lib.call("tsp_screened_spmm_backward", Ad.data_ptr(), _lib.dtype_code(Ad.dtype), M, dd.data_ptr(), dcode,
+              math.sqrt(threshold), M, Bd.data_ptr(), ncols, ncols, Gd.data_ptr(), ncols, _lib.ptr(dA), M,
+              _lib.ptr(dB), ncols, ws.data_ptr(), _lib.stream_handle(dev))
+    return dA, dB
+
+
 class _ScreenedSpMMFunction(torch.autograd.Function):
     """Autograd wrapper of the fused screened SpMM (reference dispatch.py:447-484).
 
     Forward: the gfx950 kernel (mask applied while staging A tiles).
-    Backward (torch ops): dA = (dC @ B^T) * mask, dB = (A * mask)^T @ dC; no
-    gradient to diag_integrals or threshold (the mask is discrete).
+    Backward: tsp_screened_spmm_backward, dA = (dC @ B^T) * mask and dB =
+    (A * mask)^T @ dC with fully masked tile pairs skipped; no gradient to
+    diag_integrals or threshold (the mask is discrete).
     """
 
     @staticmethod
@@ -506,15 +531,15 @@ class _ScreenedSpMMFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out):
-        import math
-
         A, diag, B = ctx.saved_tensors
-        Q = torch.sqrt(torch.abs(diag))
-        mask = ((Q.unsqueeze(-1) * Q.unsqueeze(0)) > math.sqrt(ctx.threshold)).to(A.dtype)
-        g = grad_out.to(A.device)
-        grad_A = (g @ B.to(A.device).T) * mask if ctx.needs_input_grad[0] else None
-        grad_B = ((A * mask).T @ g).to(B.device) if ctx.needs_input_grad[3] else None
-        return grad_A, None, None, grad_B
+        need_a, need_b = ctx.needs_input_grad[0], ctx.needs_input_grad[3]
+        if not (need_a or need_b):
+            return None, None, None, None
+        dev = _target_device(B, A, diag)
+        with torch.cuda.device(dev):
+            dA, dB = _screened_backward(A, diag, ctx.threshold, B, grad_out, need_a, need_b, dev)
+        return (dA.to(A.device) if dA is not None else None, None, None,
+                dB.to(B.device) if dB is not None else None)
 
 
 def hip_screened_spmm(A, diag_integrals, B, threshold: float):

@@ -176,6 +176,33 @@ def bench_bsr_fp32(steps: int, warmup: int, cpu: bool):
 # ------------------------------------------------------------ secondary
 
 
+def bench_bsr_small(steps: int, warmup: int):
+    """bsr_spmm with block sizes 16, 32 and 64 (bsr_spmm_small) on cfg3's
+    dense size (16384 x 16384, N = 512) and block density (10 %, banded plus
+    uniform), fp32: GFLOP/s over the stored blocks."""
+    import torch
+
+    import trnsparse_amd as ts
+    from trnsparse_amd import workloads as W
+
+    out = []
+    n, N = 16384, 512
+    g = torch.Generator().manual_seed(21)
+    B = torch.randn(n, N, generator=g).cuda()
+    for b in (16, 32, 64):
+        nb = n // b
+        mask = W.cfg3_block_mask(nb, half_band=3 * 128 // b, density=0.10, seed=22)
+        blocks = torch.randn(int(mask.sum()), b, b, generator=g)
+        A = W.bsr_from_block_mask(mask, b, blocks=blocks)
+        A = ts.BSRMatrix(A.blocks.cuda(), A.block_col_indices.cuda(), A.block_row_ptrs.cuda(), A.shape, b)
+        flops = 2.0 * A.n_blocks * b * b * N
+        _, ms = time_gpu(lambda: ts.bsr_spmm(A, B), steps, warmup)
+        tf = flops / (ms * 1e-3) / 1e12
+        out.append({"name": f"bsr_spmm b={b} 16384^2 10% blocks N=512 fp32", "value": round(tf * 1e3, 1),
+                    "unit": "GFLOP/s", "us": round(ms * 1e3, 1), "frac_fp32_mfma": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)})
+    return out
+
+
 def bench_bsr_bf16(steps: int, warmup: int):
     import torch
 
@@ -828,6 +855,7 @@ def main(argv=None) -> int:
             ("spmm", lambda: bench_spmm(10, 2)),
             ("bsr bf16", lambda: bench_bsr_bf16(max(5, args.steps // 2), 3)),
             ("bsr f64", lambda: bench_bsr_f64(10, 2)),
+            ("bsr small", lambda: bench_bsr_small(10, 2)),
             ("bsr backward", lambda: bench_bsr_backward(10, 2)),
             ("screened", lambda: bench_screened(10, 2, cpu=not args.no_cpu)),
             ("attention", lambda: bench_attention(10, 2, cpu=not args.no_cpu)),

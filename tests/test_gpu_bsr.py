@@ -75,7 +75,7 @@ def test_reference_grid(hip_backend, m_blocks, n_blocks, N, density):
         ((300, 260), 128, 11, 1.0),  # odd N: the fp32 kernel's unpaired last-column stores
         ((256, 384), 128, 129, 0.7),  # odd N past one column tile
         ((384, 256), 128, 200, 0.6),  # partial column tile
-        ((256, 256), 64, 96, 0.7),  # block size 64 (generic kernel)
+        ((256, 256), 64, 96, 0.7),  # block size 64 (small-block MFMA kernel)
     ],
 )
 def test_shapes(hip_backend, shape, b, N, density):
@@ -87,6 +87,39 @@ def test_shapes(hip_backend, shape, b, N, density):
     exact, scale = _oracle(bsr, B)
     assert got.shape == (shape[0], N)
     assert ref.scaled_error(got.numpy(), exact, scale) <= TOL_F32
+
+
+@pytest.mark.parametrize(
+    "shape,b,N,density",
+    [
+        ((64, 64), 16, 64, 0.6),      # whole tiles
+        ((200, 150), 16, 37, 0.5),    # ragged m, n (B rows past n read as zero), partial column tile
+        ((96, 96), 32, 130, 0.4),     # three column tiles, the last partial
+        ((150, 301), 32, 5, 0.8),     # narrow N
+        ((320, 200), 64, 200, 0.3),   # ragged n inside a block column
+        ((128, 2048), 64, 64, 0.9),   # long block rows (32 blocks)
+    ],
+)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_small_block_mfma(hip_backend, shape, b, N, density, dtype):
+    """b in {16, 32, 64} runs bsr_spmm_small (fp32 MFMA; bf16 widened at the
+    load), with empty block rows mixed in; fp32 out for fp32, bf16 in -> fp32
+    and bf16 out."""
+    g = torch.Generator().manual_seed(b + N)
+    A = torch.randn(*shape, generator=g) * (torch.rand(*shape, generator=g) < density)
+    A[b : 2 * b] = 0.0                                  # an empty block row
+    A = A.to(dtype).float()
+    bsr = ts.BSRMatrix.from_dense(A.to(dtype), block_size=b)
+    B = torch.randn(shape[1], N, generator=g).to(dtype)
+    exact, scale = _oracle(ts.BSRMatrix.from_dense(A, block_size=b), B.float())
+    got = ts.bsr_spmm(bsr, B.cuda(), out_dtype=torch.float32).cpu()
+    assert got.dtype == torch.float32 and got.shape == (shape[0], N)
+    assert ref.scaled_error(got.numpy(), exact, scale) <= TOL_F32
+    assert torch.count_nonzero(got[b : 2 * b]).item() == 0
+    if dtype == torch.bfloat16:
+        got16 = ts.bsr_spmm(bsr, B.cuda()).cpu()
+        assert got16.dtype == torch.bfloat16
+        assert ref.scaled_error(got16.float().numpy(), exact, scale) <= 1e-2
 
 
 def test_empty_pattern_is_zero(hip_backend):

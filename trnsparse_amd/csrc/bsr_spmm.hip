@@ -24,6 +24,10 @@
 //                      transpose reads).
 //   bsr_spmm_f64_dma   b == 128, fp64 (v_mfma_f64_16x16x4_f64, the streamed
 //                      structure of bsr_spmm_f32_dma).
+//   bsr_spmm_small<b>  b in {16, 32, 64}, fp32 or bf16 in (fp32 MFMA, bf16
+//                      widened exactly at the load), fp32 / bf16 out: a
+//                      wavefront per (block row, 64 columns of C), operands
+//                      straight from memory into MFMA registers.
 //   bsr_spmm_generic   any block size / dtype (f32, f64, bf16): one thread per
 //                      output element, a plain dot product over stored blocks.
 //
@@ -560,6 +564,141 @@ __global__ __launch_bounds__(512) void bsr_spmm_bf16_mfma(
   }
 }
 
+// ------------------------------------------------------ small block sizes
+//
+// bsr_spmm_small<BSZ>: b = 16, 32 or 64. A block row of C is only b rows, so
+// a wavefront owns one (block row, 64-column) tile of C and walks the row's
+// stored blocks with its operands loaded directly into registers (4 waves
+// per workgroup take consecutive column tiles of one block row and share
+// its A blocks through L1):
+//   b = 32, 64: v_mfma_f32_32x32x2_f32, b/32 row subtiles x 2 column
+//     subtiles; at step 4g + c lane half h supplies k = 8g + 4h + c, so the
+//     lane's A values for four MFMAs are one 16-byte read of its block row
+//     (8 bytes for bf16) and its B values four loads of rows 8g + 4h + c,
+//     coalesced over the 32 columns of the subtile;
+//   b = 16: v_mfma_f32_16x16x4_f32, 4 column subtiles; lane group q = lane/16
+//     supplies k = 4q + c at step c, one 16-byte A read per block.
+// B rows at or past n read as zero, C rows past m and columns past ncols are
+// not written.
+template <typename T>
+__device__ inline f32x4 load4_acc(const T* p);
+template <>
+__device__ inline f32x4 load4_acc<float>(const float* p) { return *(const f32x4*)p; }
+template <>
+__device__ inline f32x4 load4_acc<uint16_t>(const uint16_t* p) {
+  typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+  const u16x4 v = *(const u16x4*)p;
+  return f32x4{tsp::bf16_bits_to_f32(v[0]), tsp::bf16_bits_to_f32(v[1]), tsp::bf16_bits_to_f32(v[2]),
+               tsp::bf16_bits_to_f32(v[3])};
+}
+
+template <int BSZ, typename T, typename OutT>
+__global__ __launch_bounds__(256) void bsr_spmm_small(const T* __restrict__ blocks, const int64_t* __restrict__ rp,
+                                                      const int64_t* __restrict__ ci, int64_t mb, int64_t m, int64_t n,
+                                                      const T* __restrict__ B, int64_t ldb, int64_t ncols,
+                                                      OutT* __restrict__ C, int64_t ldc, int64_t nct) {
+  static_assert(BSZ == 16 || BSZ == 32 || BSZ == 64, "block size");
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t item = (int64_t)blockIdx.x * 4 + w;  // (block row, 64-column tile)
+  const int64_t row = item / nct;
+  if (row >= mb) return;
+  const int64_t n0 = (item - row * nct) * 64;
+  const int64_t start = rp[row], end = rp[row + 1];
+  auto bval = [&](int64_t k, int64_t c) {
+    return k < n && c < ncols ? tsp::to_acc<T>(B[k * ldb + c]) : 0.f;
+  };
+  if constexpr (BSZ == 16) {
+    const int l16 = lane & 15, q = lane >> 4;
+    f32x4 acc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u] = f32x4{};
+    for (int64_t idx = start; idx < end; ++idx) {
+      const int64_t kb = ci[idx] * BSZ + 4 * q;
+      const f32x4 a = load4_acc<T>(blocks + idx * (BSZ * BSZ) + l16 * BSZ + 4 * q);
+      float bv[4][4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) bv[u][c] = bval(kb + c, n0 + 16 * u + l16);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c], bv[u][c], acc[u], 0, 0, 0);
+    }
+    // element r of subtile u: row 4q + r, column 16u + l16
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t c = n0 + 16 * u + l16;
+      if (c >= ncols) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t rr = row * BSZ + 4 * q + r;
+        if (rr < m) C[rr * ldc + c] = tsp::from_acc<OutT>(acc[u][r]);
+      }
+    }
+  } else {
+    constexpr int RT = BSZ / 32;
+    const int h = lane >> 5, l32 = lane & 31;
+    f32x16 acc[RT][2];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) acc[t][0] = acc[t][1] = f32x16{};
+    for (int64_t idx = start; idx < end; ++idx) {
+      const int64_t kb = ci[idx] * BSZ;
+      const T* Ab = blocks + idx * (BSZ * BSZ);
+#pragma unroll
+      for (int g = 0; g < BSZ / 8; ++g) {
+        f32x4 a[RT];
+#pragma unroll
+        for (int t = 0; t < RT; ++t) a[t] = load4_acc<T>(Ab + (32 * t + l32) * BSZ + 8 * g + 4 * h);
+        float bv[2][4];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) bv[u][c] = bval(kb + 8 * g + 4 * h + c, n0 + 32 * u + l32);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int t = 0; t < RT; ++t)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+              acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t][c], bv[u][c], acc[t][u], 0, 0, 0);
+      }
+    }
+    // element v of subtile (t, u): row 32t + 8(v/4) + 4h + v%4, column 32u + l32
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int64_t c = n0 + 32 * u + l32;
+      if (c >= ncols) continue;
+#pragma unroll
+      for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t rr = row * BSZ + 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
+          if (rr < m) C[rr * ldc + c] = tsp::from_acc<OutT>(acc[t][u][v]);
+        }
+    }
+  }
+}
+
+template <typename T, typename OutT>
+int launch_small(int64_t bs, const void* blocks, const int64_t* rp, const int64_t* ci, int64_t mb, int64_t m, int64_t n,
+                 const void* B, int64_t ldb, int64_t ncols, void* C, int64_t ldc, hipStream_t st) {
+  const int64_t nct = tsp::ceil_div(ncols, 64);
+  const int64_t grid = tsp::ceil_div(mb * nct, 4);
+  if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm: problem too large");
+#define TSP_SMALL(BSZ)                                                                                              \
+  hipLaunchKernelGGL((bsr_spmm_small<BSZ, T, OutT>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)blocks, rp, ci, \
+                     mb, m, n, (const T*)B, ldb, ncols, (OutT*)C, ldc, nct)
+  if (bs == 16)
+    TSP_SMALL(16);
+  else if (bs == 32)
+    TSP_SMALL(32);
+  else
+    TSP_SMALL(64);
+#undef TSP_SMALL
+  return tsp::check_launch("bsr_spmm_small launch");
+}
+
 template <typename T, typename OutT>
 __global__ __launch_bounds__(256) void bsr_spmm_generic(
     const T* __restrict__ blocks, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci,
@@ -701,6 +840,17 @@ extern "C" int tsp_bsr_spmm(const void* blocks, int dtype, const int64_t* block_
     hipLaunchKernelGGL(bsr_spmm_f64_dma, dim3((unsigned)grid), dim3(256), 0, st, (const double*)blocks, block_row_ptrs,
                        block_col_indices, mb, (int)nt, m, n, (const double*)B, ldb, ncols, (double*)C, ldc, row_order);
     return tsp::check_launch("bsr_spmm_f64_dma launch");
+  }
+  if ((block_size == 16 || block_size == 32 || block_size == 64) && ((uintptr_t)blocks % 16) == 0) {
+    if (dtype == TSP_F32)
+      return launch_small<float, float>(block_size, blocks, block_row_ptrs, block_col_indices, mb, m, n, B, ldb, ncols,
+                                        C, ldc, st);
+    if (dtype == TSP_BF16 && out_dtype == TSP_F32)
+      return launch_small<uint16_t, float>(block_size, blocks, block_row_ptrs, block_col_indices, mb, m, n, B, ldb,
+                                           ncols, C, ldc, st);
+    if (dtype == TSP_BF16)
+      return launch_small<uint16_t, uint16_t>(block_size, blocks, block_row_ptrs, block_col_indices, mb, m, n, B, ldb,
+                                              ncols, C, ldc, st);
   }
   if (dtype == TSP_F32) return launch_generic<float, float>(blocks, block_row_ptrs, block_col_indices, block_size, m, n, B, ldb, ncols, C, ldc, st);
   if (dtype == TSP_F64) return launch_generic<double, double>(blocks, block_row_ptrs, block_col_indices, block_size, m, n, B, ldb, ncols, C, ldc, st);

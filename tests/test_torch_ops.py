@@ -1,0 +1,120 @@
+"""The registered operator layer (torch.ops.trnsparse_hip, csrc/torch_ops.cpp).
+
+CPU: the operator library loads next to the C library, every operator has
+its schema, and the Meta implementations give the output shapes and dtypes
+(what torch.compile traces with). GPU: operators called directly agree with
+the public API, a torch.compile(fullgraph=True) region traces through them,
+and a HIP graph replays them.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from trnsparse_amd.hip import _lib
+
+OPS = {
+    "bsr_spmm": "(Tensor blocks, Tensor block_row_ptrs, Tensor block_col_indices, Tensor? row_order, int m, int n, "
+                "int block_size, Tensor B, ScalarType out_dtype) -> Tensor",
+    "bsr_sddmm": "(Tensor grad_out, Tensor B, Tensor block_rows, Tensor block_col_indices, int m, int n, "
+                 "int block_size) -> Tensor",
+    "bsr_spmm_t": "(Tensor blocks, Tensor col_ptrs, Tensor col_block_ids, Tensor col_block_rows, Tensor col_order, "
+                  "int m, int n, int block_size, Tensor grad_out) -> Tensor",
+    "csr_spmv": "(Tensor values, Tensor col_indices, Tensor row_ptrs, Tensor windows, int m, int n, Tensor x, "
+                "float alpha, Tensor? y, float beta) -> Tensor",
+    "csr_colplan_spmv": "(Tensor plan, Tensor geometry, int m, int n, int nnz, Tensor x, float alpha, Tensor? y, "
+                        "float beta) -> Tensor",
+    "csr_spmm": "(Tensor values, Tensor col_indices, Tensor row_ptrs, int m, int n, Tensor X, float alpha, "
+                "Tensor? Y, float beta) -> Tensor",
+    "screened_spmm": "(Tensor A, Tensor diag_integrals, Tensor B, float threshold_sqrt) -> Tensor",
+    "screened_spmm_backward": "(Tensor A, Tensor diag_integrals, Tensor B, float threshold_sqrt, Tensor grad_out, "
+                              "bool need_a, bool need_b) -> (Tensor, Tensor)",
+    "bsa_fwd": "(Tensor Q, Tensor K, Tensor V, Tensor block_row_ptrs, Tensor block_col_indices, int block_size, "
+               "float scale, bool return_stats) -> (Tensor, Tensor, Tensor)",
+    "bsa_bwd": "(Tensor Q, Tensor K, Tensor V, Tensor O, Tensor dO, Tensor block_row_ptrs, Tensor block_col_indices, "
+               "Tensor col_ptrs, Tensor col_block_rows, int n_block_cols, int block_size, float scale, "
+               "Tensor row_max, Tensor row_denom, Tensor plan, int n_items, int n_splits, int n_partials) -> "
+               "(Tensor, Tensor, Tensor)",
+}
+
+
+def test_operator_library_in_tree_and_schemas():
+    ops = _lib.ops()
+    assert _lib.OPS_PATH.parent == _lib.LIB_PATH.parent  # in-tree, next to the C library
+    for name, sig in OPS.items():
+        assert str(getattr(ops, name).default._schema) == f"trnsparse_hip::{name}{sig}"
+
+
+def _meta(*shape, dtype=torch.float32):
+    return torch.empty(*shape, dtype=dtype, device="meta")
+
+
+def test_meta_shapes():
+    ops = _lib.ops()
+    i64 = torch.int64
+    rp, ci = _meta(4, dtype=i64), _meta(6, dtype=i64)
+    assert ops.bsr_spmm(_meta(6, 128, 128), rp, ci, None, 300, 512, 128, _meta(512, 70), torch.float32).shape == (300, 70)
+    c = ops.bsr_spmm(_meta(6, 32, 32, dtype=torch.bfloat16), rp, ci, None, 96, 96, 32,
+                     _meta(96, 8, dtype=torch.bfloat16), torch.bfloat16)
+    assert c.shape == (96, 8) and c.dtype == torch.bfloat16
+    assert ops.bsr_sddmm(_meta(300, 70), _meta(512, 70), ci, ci, 300, 512, 128).shape == (6, 128, 128)
+    assert ops.bsr_spmm_t(_meta(6, 128, 128), _meta(5, dtype=i64), ci, ci, _meta(4, dtype=torch.int32), 300, 512, 128,
+                          _meta(300, 70)).shape == (512, 70)
+    v, cols, ptrs = _meta(50), _meta(50, dtype=torch.int32), _meta(11, dtype=torch.int32)
+    assert ops.csr_spmv(v, cols, ptrs, _meta(3, dtype=i64), 10, 20, _meta(20), 1.0, None, 0.0).shape == (10,)
+    geom = torch.zeros(10, dtype=i64)
+    assert ops.csr_colplan_spmv(_meta(100, dtype=torch.uint8), geom, 10, 20, 50, _meta(20), 1.0, None, 0.0).shape == (10,)
+    assert ops.csr_spmm(v, cols, ptrs, 10, 20, _meta(20, 3), 1.0, None, 0.0).shape == (10, 3)
+    assert ops.screened_spmm(_meta(64, 64), _meta(64), _meta(64, 9), 1e-5).shape == (64, 9)
+    dA, dB = ops.screened_spmm_backward(_meta(64, 64), _meta(64), _meta(64, 9), 1e-5, _meta(64, 9), True, False)
+    assert dA.shape == (64, 64) and dB.numel() == 0
+    Q = _meta(3, 512, 64, dtype=torch.bfloat16)
+    O, rm, rd = ops.bsa_fwd(Q, Q, Q, rp, ci, 128, 0.125, True)
+    assert O.shape == Q.shape and O.dtype == torch.bfloat16 and rm.shape == (3, 4, 128) and rm.dtype == torch.float32
+    O, rm, _ = ops.bsa_fwd(_meta(2, 300, 32, dtype=torch.float64), _meta(2, 300, 32, dtype=torch.float64),
+                           _meta(2, 300, 32, dtype=torch.float64), rp, ci, 128, 0.2, True)
+    assert rm.shape == (2, 2, 128) and rm.dtype == torch.float64
+    g = ops.bsa_bwd(Q, Q, Q, Q, Q, rp, ci, rp, ci, 4, 128, 0.125, _meta(3, 512), _meta(3, 512),
+                    _meta(20, dtype=torch.int32), 4, 0, 0)
+    assert all(t.shape == Q.shape and t.dtype == Q.dtype for t in g)
+
+
+@pytest.mark.gpu
+def test_ops_match_api_compile_and_graph(hip_backend):
+    import trnsparse_amd as ts
+    from trnsparse_amd.hip import dispatch as D
+
+    ops = _lib.ops()
+    g = torch.Generator().manual_seed(3)
+    A = torch.randn(384, 256, generator=g) * (torch.rand(384, 256, generator=g) < 0.5)
+    bsr = ts.BSRMatrix.from_dense(A, block_size=128)
+    B = torch.randn(256, 96, generator=g).cuda()
+    want = ts.bsr_spmm(bsr, B)
+    rp, ci, order = D._bsr_plan(bsr.block_col_indices, bsr.block_row_ptrs, 3, B.device, holder=bsr)
+    blocks = bsr.blocks.cuda()
+    got = ops.bsr_spmm(blocks, rp, ci, order, 384, 256, 128, B, torch.float32)
+    torch.testing.assert_close(got, want, rtol=0, atol=0)
+
+    @torch.compile(fullgraph=True, backend="aot_eager")
+    def f(blocks, rp, ci, B):
+        return ops.bsr_spmm(blocks, rp, ci, None, 384, 256, 128, B * 2.0, torch.float32) + 1.0
+
+    torch.testing.assert_close(f(blocks, rp, ci, B), 2.0 * want + 1.0, rtol=1e-6, atol=1e-5)
+
+    # HIP graph: capture once, replay with new B contents, eager work between replays
+    static_B = B.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.bsr_spmm(blocks, rp, ci, order, 384, 256, 128, static_B, torch.float32)  # warm up on the side stream
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_C = ops.bsr_spmm(blocks, rp, ci, order, 384, 256, 128, static_B, torch.float32)
+    for rep in range(3):
+        newB = torch.randn(256, 96, generator=torch.Generator().manual_seed(10 + rep)).cuda()
+        static_B.copy_(newB)
+        graph.replay()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(static_C, ts.bsr_spmm(bsr, newB), rtol=0, atol=0)

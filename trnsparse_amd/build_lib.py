@@ -110,8 +110,37 @@ def _compile(src: pathlib.Path, verbose: bool) -> pathlib.Path:
     return obj
 
 
+# The PyTorch operator library (csrc/torch_ops.cpp, torch.ops.trnsparse_hip):
+# host code only, compiled against torch's headers and linked to
+# libtrnsparse_hip.so (found next to it through $ORIGIN).
+OPS_SRC = CSRC / "torch_ops.cpp"
+OPS_LIB = PKG / "libtrnsparse_torch_ops.so"
+
+
+def build_ops(verbose: bool = False) -> pathlib.Path:
+    """Compile and link the operator library (needs libtrnsparse_hip.so built)."""
+    import torch
+    import torch.utils.cpp_extension as ce
+
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = OPS_LIB.with_suffix(".so.tmp")
+    tlib = ce.library_paths()[0]
+    cmd = ["g++", "-std=c++17", "-O2", "-fPIC", "-shared", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM", *(f"-I{p}" for p in ce.include_paths()), "-I/opt/rocm/include",
+           f"-I{ROOT / 'include'}", str(OPS_SRC), "-o", str(tmp), f"-L{tlib}", "-lc10", "-lc10_hip", "-ltorch",
+           "-ltorch_cpu", f"-L{PKG}", "-ltrnsparse_hip", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{tlib}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"operator library build failed:\n{r.stdout}{r.stderr}")
+    os.replace(tmp, OPS_LIB)
+    return OPS_LIB
+
+
 def build(verbose: bool = False, jobs: int | None = None) -> pathlib.Path:
-    """Compile every `csrc/*.hip` and link the shared library. Always rebuilds."""
+    """Compile every `csrc/*.hip`, link the shared library, then build the
+    operator library over it. Always rebuilds."""
     BUILD.mkdir(exist_ok=True)
     srcs = _sources()
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2)))
@@ -129,6 +158,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> pathlib.Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}{r.stderr}")
     os.replace(tmp, LIB)
+    build_ops(verbose)
     return LIB
 
 

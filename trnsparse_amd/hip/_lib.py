@@ -111,6 +111,29 @@ def load() -> ctypes.CDLL:
     return _lib
 
 
+OPS_PATH = pathlib.Path(__file__).resolve().parent.parent / "libtrnsparse_torch_ops.so"
+_ops = None
+
+
+def ops():
+    """`torch.ops.trnsparse_hip` (csrc/torch_ops.cpp) after loading the
+    operator library once; raise RuntimeError if it is not built."""
+    global _ops
+    if _ops is not None:
+        return _ops
+    load()  # the operator library links against the C library
+    with _lock:
+        if _ops is None:
+            if not OPS_PATH.exists():
+                raise RuntimeError(
+                    f"{OPS_PATH.name} is not built; run `python -m trnsparse_amd.build_lib` "
+                    "(the HIP backend has no fallback)"
+                )
+            torch.ops.load_library(str(OPS_PATH))
+            _ops = torch.ops.trnsparse_hip
+    return _ops
+
+
 def last_error() -> str:
     return load().tsp_last_error().decode(errors="replace")
 

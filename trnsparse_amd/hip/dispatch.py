@@ -91,27 +91,8 @@ def _bsr_spmm_launch(blocks, rp, ci, order, shape, b, B, out_dtype, dev) -> torc
         # Row stride a multiple of 16 bytes for the vectorised B panel loads.
         B_d = F.pad(B_d, (0, vec - ncols % vec))
         ldb = B_d.shape[1]
-    C = torch.empty((m, ncols), dtype=out_dtype, device=dev)
-    _lib.call(
-        "tsp_bsr_spmm",
-        blocks_d.data_ptr(),
-        _lib.dtype_code(blocks_d.dtype),
-        rp.data_ptr(),
-        ci.data_ptr(),
-        blocks_d.shape[0],
-        b,
-        m,
-        n,
-        B_d.data_ptr(),
-        ldb,
-        ncols,
-        C.data_ptr(),
-        ncols,
-        _lib.dtype_code(out_dtype),
-        order.data_ptr() if order is not None else None,
-        _lib.stream_handle(dev),
-    )
-    return C
+    # (a padded B is passed as its first ncols columns: the row stride stays ldb)
+    return _lib.ops().bsr_spmm(blocks_d, rp, ci, order, m, n, b, B_d[:, :ncols], out_dtype)
 
 
 class _BSRSpMMFunction(torch.autograd.Function):
@@ -152,8 +133,7 @@ class _BSRSpMMFunction(torch.autograd.Function):
         nbc = (n + b - 1) // b
         ncols = grad_out.shape[1]
         dt = A_blocks.dtype
-        code = _lib.dtype_code(dt)
-        st = _lib.stream_handle(dev)
+        _lib.dtype_code(dt)  # raises for a dtype the kernels do not take
         with torch.cuda.device(dev):
             blocks = _on(A_blocks, dev)
             G = _on(grad_out, dev, dt)
@@ -161,14 +141,10 @@ class _BSRSpMMFunction(torch.autograd.Function):
             grad_blocks = grad_B = None
             if ctx.needs_input_grad[0]:
                 Bd = _on(B, dev, dt)
-                gb = torch.empty_like(blocks)
-                _lib.call("tsp_bsr_sddmm", G.data_ptr(), ncols, m, Bd.data_ptr(), ncols, n, ncols, brow.data_ptr(),
-                          ci.data_ptr(), blocks.shape[0], b, code, gb.data_ptr(), st)
+                gb = _lib.ops().bsr_sddmm(G, Bd, brow, ci, m, n, b)
                 grad_blocks = gb.to(A_blocks.device)
             if ctx.needs_input_grad[5]:
-                dB = torch.empty(n, ncols, dtype=dt, device=dev)
-                _lib.call("tsp_bsr_spmm_t", blocks.data_ptr(), code, cp.data_ptr(), cbid.data_ptr(), crow.data_ptr(),
-                          nbc, b, m, n, G.data_ptr(), ncols, ncols, dB.data_ptr(), ncols, corder.data_ptr(), st)
+                dB = _lib.ops().bsr_spmm_t(blocks, cp, cbid, crow, corder, m, n, b, G)
                 grad_B = dB.to(B.device, B.dtype)
         return grad_blocks, None, None, None, None, grad_B, None, None
 
@@ -284,31 +260,28 @@ def _csr_forward(vals, cols, ptrs, win, shape, X, alpha, Y, beta, dev, colplan=N
     code = _lib.dtype_code(vals.dtype)
     if code == _lib.TSP_BF16:
         raise RuntimeError("HIP CSR kernels support float32 and float64 values")
-    icode = _lib.index_code(cols.dtype)
+    _lib.index_code(cols.dtype)  # raises for an index dtype the kernels do not take
     Xd = _on(X, dev)
     use_y = Y is not None and beta != 0.0
     Yd = _on(Y, dev, vals.dtype) if use_y else None
-    st = _lib.stream_handle(dev)
     if Xd.dim() == 1:
-        out = torch.empty(m, dtype=vals.dtype, device=dev)
         if use_y and Yd.shape != (m,):
             Yd = Yd.expand(m).contiguous()
         if colplan is not None:
             geom, plan = colplan
-            work = torch.empty(max(1, int(geom[8])) // 4, dtype=torch.float32, device=dev) if geom[8] else None
-            _lib.call("tsp_csr_colplan_spmv", plan.data_ptr(), code, m, n, vals.numel(), geom.ctypes.data,
-                      Xd.data_ptr(), float(alpha), _lib.ptr(Yd), float(beta), out.data_ptr(), _lib.ptr(work), st)
-            return out
-        _lib.call("tsp_csr_spmv", vals.data_ptr(), code, cols.data_ptr(), ptrs.data_ptr(), icode, m, n, vals.numel(),
-                  win.data_ptr(), Xd.data_ptr(), float(alpha), _lib.ptr(Yd), float(beta), out.data_ptr(), st)
-        return out
+            return _lib.ops().csr_colplan_spmv(plan, _geometry_tensor(geom), m, n, vals.numel(), Xd, float(alpha), Yd,
+                                               float(beta))
+        return _lib.ops().csr_spmv(vals, cols, ptrs, win, m, n, Xd, float(alpha), Yd, float(beta))
     ncols = Xd.shape[1]
-    out = torch.empty(m, ncols, dtype=vals.dtype, device=dev)
     if use_y and Yd.shape != (m, ncols):
         Yd = Yd.expand(m, ncols).contiguous()
-    _lib.call("tsp_csr_spmm", vals.data_ptr(), code, cols.data_ptr(), ptrs.data_ptr(), icode, m, n, vals.numel(),
-              Xd.data_ptr(), ncols, ncols, float(alpha), _lib.ptr(Yd), ncols, float(beta), out.data_ptr(), ncols, st)
-    return out
+    return _lib.ops().csr_spmm(vals, cols, ptrs, m, n, Xd, float(alpha), Yd, float(beta))
+
+
+def _geometry_tensor(geom) -> torch.Tensor:
+    """The column plan's 10 host int64 geometry values as a CPU tensor (the
+    operator's argument form), sharing memory with the numpy array."""
+    return torch.from_numpy(geom)
 
 
 # SpMV over the column-sorted plan (tsp_csr_colplan_*): "auto" builds the
@@ -478,13 +451,7 @@ def _screened_forward(A, diag, threshold, B, dev):
         raise RuntimeError(f"screened_spmm: B shape {tuple(B.shape)} does not match A {tuple(A.shape)}")
     Ad, Bd, dd = _on(A, dev), _on(B, dev), _on(diag, dev)
     ncols = Bd.shape[1]
-    C = torch.empty(M, ncols, dtype=A.dtype, device=dev)
-    dcode = _lib.dtype_code(dd.dtype)
-    ws = torch.empty(max(1, _lib.load().tsp_screened_workspace_size(M, dcode)), dtype=torch.uint8, device=dev)
-    _lib.call("tsp_screened_spmm", Ad.data_ptr(), _lib.dtype_code(Ad.dtype), M, dd.data_ptr(), dcode,
-              math.sqrt(threshold), M, Bd.data_ptr(), ncols, ncols, C.data_ptr(), ncols, ws.data_ptr(),
-              _lib.stream_handle(dev))
-    return C
+    return _lib.ops().screened_spmm(Ad, dd, Bd, math.sqrt(threshold))
 
 
 def _screened_backward(A, diag, threshold, B, G, need_a: bool, need_b: bool, dev):
@@ -498,17 +465,9 @@ def _screened_backward(A, diag, threshold, B, G, need_a: bool, need_b: bool, dev
         dA, dB = _screened_backward(_on(A, dev, torch.float32), diag, threshold, _on(B, dev, torch.float32),
                                     _on(G, dev, torch.float32), need_a, need_b, dev)
         return (dA.to(A.dtype) if dA is not None else None, dB.to(A.dtype) if dB is not None else None)
-    M = A.shape[0]
     Ad, Bd, Gd, dd = _on(A, dev), _on(B, dev), _on(G, dev, A.dtype), _on(diag, dev)
-    ncols = Gd.shape[1]
-    dA = torch.empty(M, M, dtype=A.dtype, device=dev) if need_a else None
-    dB = torch.empty(M, ncols, dtype=A.dtype, device=dev) if need_b else None
-    dcode = _lib.dtype_code(dd.dtype)
-    ws = torch.empty(max(1, _lib.load().tsp_screened_workspace_size(M, dcode)), dtype=torch.uint8, device=dev)
-    _lib.call("tsp_screened_spmm_backward", Ad.data_ptr(), _lib.dtype_code(Ad.dtype), M, dd.data_ptr(), dcode,
-              math.sqrt(threshold), M, Bd.data_ptr(), ncols, ncols, Gd.data_ptr(), ncols, _lib.ptr(dA), M,
-              _lib.ptr(dB), ncols, ws.data_ptr(), _lib.stream_handle(dev))
-    return dA, dB
+    dA, dB = _lib.ops().screened_spmm_backward(Ad, dd, Bd, math.sqrt(threshold), Gd, bool(need_a), bool(need_b))
+    return (dA if need_a else None, dB if need_b else None)
 
 
 class _ScreenedSpMMFunction(torch.autograd.Function):
@@ -587,7 +546,7 @@ def hip_block_sparse_attention(Q, K, V, mask_bsr, scale: float, return_stats: bo
         if not return_stats:
             return res[..., : Q.shape[-1]].contiguous()
         return (res[0][..., : Q.shape[-1]].contiguous(),) + tuple(res[1:])
-    code = _lib.dtype_code(Q.dtype)
+    _lib.dtype_code(Q.dtype)  # raises for a dtype the kernels do not take
     lead = Q.shape[:-2]
     S, D = Q.shape[-2:]
     b = mask_bsr.block_size
@@ -601,12 +560,7 @@ def hip_block_sparse_attention(Q, K, V, mask_bsr, scale: float, return_stats: bo
             raise IndexError(f"mask has {rp.numel() - 1} block rows, attention needs {Mt}")
         Qd, Kd, Vd = (_on(t, dev).reshape(-1, S, D) for t in (Q, K, V))
         H = Qd.shape[0]
-        O = torch.empty_like(Qd)
-        sdt = torch.float64 if Q.dtype == torch.float64 else torch.float32
-        rmax = torch.empty(H, Mt, b, dtype=sdt, device=dev) if return_stats else None
-        rden = torch.empty(H, Mt, b, dtype=sdt, device=dev) if return_stats else None
-        _lib.call("tsp_bsa_fwd", Qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), code, H, S, D, rp.data_ptr(),
-                  ci.data_ptr(), b, float(scale), O.data_ptr(), _lib.ptr(rmax), _lib.ptr(rden), _lib.stream_handle(dev))
+        O, rmax, rden = _lib.ops().bsa_fwd(Qd, Kd, Vd, rp, ci, b, float(scale), bool(return_stats))
     out = O.reshape(*lead, S, D).to(orig)
     if not return_stats:
         return out
@@ -689,7 +643,7 @@ def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, 
                                                     row_max, row_denom)
         return tuple(gr.to(torch.bfloat16) for gr in grads)
     dt = Q.dtype
-    code = _lib.dtype_code(dt)
+    _lib.dtype_code(dt)  # raises for a dtype the kernels do not take
     lead = Q.shape[:-2]
     S, D = Q.shape[-2:]
     b = mask_bsr.block_size
@@ -707,11 +661,6 @@ def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, 
         cp, crow, nbc, plan, (n_items, n_splits, n_partials) = _attn_bwd_plan(mask_bsr, H, S, dev)
         rm = _on(row_max, dev, sdt).reshape(H, Mt * b)
         rd = _on(row_denom, dev, sdt).reshape(H, Mt * b)
-        dQ, dK, dV = (torch.empty_like(q) for _ in range(3))
-        ws = torch.empty(max(1, _lib.load().tsp_bsa_bwd_workspace_size(H, S, D, n_partials)), dtype=torch.uint8,
-                         device=dev)
-        _lib.call("tsp_bsa_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), code, H, S, D,
-                  rp.data_ptr(), ci.data_ptr(), cp.data_ptr(), crow.data_ptr(), nbc, b, float(scale), rm.data_ptr(),
-                  rd.data_ptr(), dQ.data_ptr(), dK.data_ptr(), dV.data_ptr(), plan.data_ptr(), n_items, n_splits,
-                  n_partials, ws.data_ptr(), _lib.stream_handle(dev))
+        dQ, dK, dV = _lib.ops().bsa_bwd(q, k, v, o, do, rp, ci, cp, crow, nbc, b, float(scale), rm, rd, plan, n_items,
+                                        n_splits, n_partials)
     return tuple(g.reshape(*lead, S, D).to(orig) for g in (dQ, dK, dV))

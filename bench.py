@@ -356,7 +356,9 @@ def bench_spmv(dist: str, index_bits: int, steps: int, warmup: int, cpu: bool = 
     plan "always": the column-sorted plan (tsp_csr_colplan_spmv; built once
     per matrix outside the timed region, its build time reported beside);
     plan "never": the windowed kernel over the caller's CSR arrays
-    (tsp_csr_spmv, deterministic). `algorithmic_bytes` is the reference
+    (tsp_csr_spmv, deterministic); plan "bucketed": the row-per-wavefront
+    kernels with long rows split out by length (tsp_csr_bucketed_spmv, plan
+    built outside the timed region). `algorithmic_bytes` is the reference
     layout's traffic (nnz*(4+idx) + (m+1)*idx + 4n + 4m) and defines `value`
     and `frac_hbm`; `kernel_bytes` is what the kernel itself has to move (the
     plan's 8-byte entries, x, y and the column groups' partial sums)."""
@@ -389,12 +391,15 @@ def bench_spmv(dist: str, index_bits: int, steps: int, warmup: int, cpu: bool = 
             geom = A._hip_colplan[2]
             G = int(geom[3])
             kbytes = nnz * 8 + n * 4 + m * 4 + (2 * G * m * 4 if G > 1 else 0)
+        if plan == "bucketed":
+            ts.spmv(A, xd)  # builds the bucket plan
         flush = make_flush()
         _, ev_ms = time_gpu(lambda: ts.spmv(A, xd), steps, warmup, flush=flush)
+        buckets = A._hip_bucket_plan[1][1:] if plan == "bucketed" else None
     finally:
         D.set_spmv_plan(prev)
     gbs = byts / (ev_ms * 1e-3) / 1e9
-    kind = "column-sorted plan" if plan == "always" else "windowed"
+    kind = {"always": "column-sorted plan", "bucketed": "length-bucketed rows"}.get(plan, "windowed")
     res = {
         "name": f"csr_spmv cfg2 {dist} int{index_bits} ({kind})",
         "value": round(gbs, 1),
@@ -405,6 +410,8 @@ def bench_spmv(dist: str, index_bits: int, steps: int, warmup: int, cpu: bool = 
         "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
         "timing": f"median of {steps} launches, each after a 1 GiB read flush of L2 and MALL",
     }
+    if buckets is not None:
+        res["rows_medium_long"] = list(buckets)
     if plan == "always":
         res["kernel_bytes"] = kbytes
         res["frac_hbm_kernel_bytes"] = round(kbytes / (ev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
@@ -852,6 +859,8 @@ def main(argv=None) -> int:
             ("spmv windowed poisson int64", lambda: bench_spmv("poisson", 64, 20, 3, plan="never")),
             ("spmv windowed poisson int32", lambda: bench_spmv("poisson", 32, 20, 3, plan="never")),
             ("spmv windowed zipf int64", lambda: bench_spmv("zipf", 64, 10, 2, plan="never")),
+            ("spmv bucketed poisson int64", lambda: bench_spmv("poisson", 64, 20, 3, plan="bucketed")),
+            ("spmv bucketed zipf int64", lambda: bench_spmv("zipf", 64, 10, 2, plan="bucketed")),
             ("spmm", lambda: bench_spmm(10, 2)),
             ("bsr bf16", lambda: bench_bsr_bf16(max(5, args.steps // 2), 3)),
             ("bsr f64", lambda: bench_bsr_f64(10, 2)),

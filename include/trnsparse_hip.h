@@ -159,6 +159,27 @@ int64_t tsp_csr_plan_size(int64_t m, int64_t nnz);
 int tsp_csr_plan(const void* row_ptrs, int index_type, int64_t m, int64_t nnz,
                  int64_t* windows, void* stream);
 
+/* ---- length-bucketed SpMV (the same result as tsp_csr_spmv) ----------
+ * Row-per-wavefront kernels with the skewed rows split out: rows with at
+ * most 32 entries take 8 lanes each in natural order, rows with up to 2048
+ * one wavefront each, longer rows one 512-thread workgroup each (lists in
+ * the plan). tsp_csr_bucket_plan_size(m) bytes of plan (int32: the medium
+ * and long row counts at [0] and [1], the lists from [4] and [4 + m]),
+ * built by tsp_csr_bucket_plan from the pattern; the caller reads the two
+ * counts back once and passes them to tsp_csr_bucketed_spmv. Same
+ * reference interface as tsp_csr_spmv (trnsparse/ops.py:30-48). */
+int64_t tsp_csr_bucket_plan_size(int64_t m);
+
+int tsp_csr_bucket_plan(const void* row_ptrs, int index_type, int64_t m,
+                        void* plan, void* stream);
+
+int tsp_csr_bucketed_spmv(const void* values, int dtype,
+                          const void* col_indices, const void* row_ptrs,
+                          int index_type, int64_t m, int64_t n, int64_t nnz,
+                          const void* plan, int64_t n_medium, int64_t n_long,
+                          const void* x, double alpha, const void* y,
+                          double beta, void* out, void* stream);
+
 /* out (m,) = alpha * A @ x (+ beta * y); x (n,), y (m,) or NULL. */
 int tsp_csr_spmv(const void* values, int dtype, const void* col_indices,
                  const void* row_ptrs, int index_type, int64_t m, int64_t n,

@@ -172,3 +172,66 @@ def test_colplan_cfg2_full_size(plan_always, dist, index_dtype):
     assert abs(got.astype(np.float64).sum() - colsum @ x) <= TOL * float(np.abs(v).astype(np.float64) @ np.abs(x[c]))
     again = ts.spmv(A, xd).cpu().numpy()
     assert ref.scaled_error(again, exact, scale) <= TOL
+
+
+# ----------------------------------------------------- length-bucketed rows
+
+
+@pytest.fixture
+def plan_bucketed(hip_backend):
+    prev = D.get_spmv_plan()
+    D.set_spmv_plan("bucketed")
+    yield
+    D.set_spmv_plan(prev)
+
+
+@pytest.mark.parametrize("index_dtype", [np.int64, np.int32])
+def test_bucketed_spmv_every_bucket(plan_bucketed, index_dtype):
+    """Rows of every class (empty, <= 32, the 32 / 33 and 2048 / 2049 edges,
+    a 100000-entry row) against the oracle, with alpha / beta / y; the plan
+    holds exactly the rows above 32 and above 2048 entries."""
+    m, n = 6000, 150000
+    rng0 = np.random.default_rng(11)
+    lens = np.minimum(rng0.poisson(9, m), n)
+    lens[rng0.random(m) < 0.1] = 0
+    lens[[5, 6, 7, 8, 9]] = [32, 33, 2048, 2049, 100000]
+    lens[rng0.choice(m, 200, replace=False)] = rng0.integers(34, 3000, 200)
+    v, c, p, rng = _random(m, n, lens, 12, index_dtype)
+    A = W.csr_matrix_from_arrays(v, c, p, (m, n), device="cuda")
+    x = rng.standard_normal(n).astype(np.float32)
+    got = ts.spmv(A, torch.from_numpy(x).cuda())
+    _check(v, c, p, (m, n), x, got.cpu().numpy())
+    plan, n_med, n_long = A._hip_bucket_plan[1]
+    assert n_med == int(((lens > 32) & (lens <= 2048)).sum()) and n_long == int((lens > 2048).sum())
+    assert sorted(plan[4:4 + n_med].cpu().tolist()) == np.flatnonzero((lens > 32) & (lens <= 2048)).tolist()
+    assert sorted(plan[4 + m:4 + m + n_long].cpu().tolist()) == np.flatnonzero(lens > 2048).tolist()
+    y = rng.standard_normal(m).astype(np.float32)
+    got = ts.spmv(A, torch.from_numpy(x).cuda(), alpha=0.5, y=torch.from_numpy(y).cuda(), beta=-2.0)
+    _check(v, c, p, (m, n), x, got.cpu().numpy(), 0.5, y, -2.0)
+
+
+def test_bucketed_spmv_f64_and_empty(plan_bucketed):
+    m, n = 3000, 5000
+    rng0 = np.random.default_rng(13)
+    lens = np.minimum(rng0.poisson(40, m), n)
+    v, c, p, rng = _random(m, n, lens, 14)
+    v = v.astype(np.float64)
+    A = W.csr_matrix_from_arrays(v, c, p, (m, n), device="cuda")
+    x = rng.standard_normal(n)
+    got = ts.spmv(A, torch.from_numpy(x).cuda()).cpu().numpy()
+    exact = ref.csr_spmv(v, c, p, (m, n), x)
+    scale = ref.csr_spmv(v, c, p, (m, n), x, absolute=True)
+    assert ref.scaled_error(got, exact, scale) <= 1e-12
+    E = W.csr_matrix_from_arrays(np.zeros(0, np.float32), np.zeros(0, np.int64), np.zeros(m + 1, np.int64), (m, n),
+                                 device="cuda")
+    assert torch.count_nonzero(ts.spmv(E, torch.ones(n, device="cuda"))).item() == 0
+
+
+@pytest.mark.parametrize("dist", ["poisson", "zipf"])
+def test_bucketed_cfg2_full_size(plan_bucketed, dist):
+    v, c, p, x, shape = W.cfg2_csr(dist=dist, index_dtype=np.int64)
+    A = W.csr_matrix_from_arrays(v, c, p, shape, device="cuda")
+    got = ts.spmv(A, torch.from_numpy(x).cuda()).cpu().numpy()
+    exact = oracle_c.csr_spmv_f64(v, c, p, shape[0], x)
+    scale = oracle_c.csr_spmv_f64(v, c, p, shape[0], x, absolute=True)
+    assert ref.scaled_error(got, exact, scale) <= TOL

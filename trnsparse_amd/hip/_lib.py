@@ -54,6 +54,10 @@ SIGNATURES: dict[str, tuple] = {
         [_P, _INT, _P, _P, _INT, _I64, _I64, _I64, _P, _I64, _I64, _DBL, _P, _I64, _DBL, _P, _I64, _P],
     ),
     "tsp_csr_sddmm": (_INT, [_P, _P, _INT, _I64, _I64, _I64, _P, _I64, _P, _I64, _I64, _INT, _DBL, _P, _P]),
+    "tsp_csr_bucket_plan_size": (_I64, [_I64]),
+    "tsp_csr_bucket_plan": (_INT, [_P, _INT, _I64, _P, _P]),
+    "tsp_csr_bucketed_spmv": (_INT, [_P, _INT, _P, _P, _INT, _I64, _I64, _I64, _P, _I64, _I64, _P, _DBL, _P, _DBL, _P,
+                                     _P]),
     "tsp_screened_workspace_size": (_I64, [_I64, _INT]),
     "tsp_screened_spmm": (_INT, [_P, _INT, _I64, _P, _INT, _DBL, _I64, _P, _I64, _I64, _P, _I64, _P, _P]),
     "tsp_screened_spmm_noalloc_max_rows": (_I64, [_INT]),

@@ -254,6 +254,9 @@ def _csr_device(A, dev: torch.device):
 
 
 def _csr_forward(vals, cols, ptrs, win, shape, X, alpha, Y, beta, dev, colplan=None):
+    """out = alpha * A @ X (+ beta * Y). `colplan` is None (windowed kernel),
+    ("colplan", geometry, plan) or ("bucketed", plan, n_medium, n_long) for a
+    vector X."""
     m, n = shape
     if vals.dtype != X.dtype:
         raise RuntimeError(f"CSR values dtype {vals.dtype} and dense operand dtype {X.dtype} differ")
@@ -267,8 +270,15 @@ def _csr_forward(vals, cols, ptrs, win, shape, X, alpha, Y, beta, dev, colplan=N
     if Xd.dim() == 1:
         if use_y and Yd.shape != (m,):
             Yd = Yd.expand(m).contiguous()
+        if colplan is not None and colplan[0] == "bucketed":
+            _, plan, n_med, n_long = colplan
+            out = torch.empty(m, dtype=vals.dtype, device=dev)
+            _lib.call("tsp_csr_bucketed_spmv", vals.data_ptr(), code, cols.data_ptr(), ptrs.data_ptr(),
+                      _lib.index_code(cols.dtype), m, n, vals.numel(), plan.data_ptr(), n_med, n_long, Xd.data_ptr(),
+                      float(alpha), _lib.ptr(Yd), float(beta), out.data_ptr(), _lib.stream_handle(dev))
+            return out
         if colplan is not None:
-            geom, plan = colplan
+            _, geom, plan = colplan
             return _lib.ops().csr_colplan_spmv(plan, _geometry_tensor(geom), m, n, vals.numel(), Xd, float(alpha), Yd,
                                                float(beta))
         return _lib.ops().csr_spmv(vals, cols, ptrs, win, m, n, Xd, float(alpha), Yd, float(beta))
@@ -289,14 +299,17 @@ def _geometry_tensor(geom) -> torch.Tensor:
 # COLPLAN_MIN_NNZ entries meets a vector (a one-off matrix keeps the
 # windowed kernel, which needs no reordered copy), "always" on first use,
 # "never" not at all. New values on a cached pattern are regathered into
-# the plan without sorting again.
-_SPMV_PLAN_MODES = ("auto", "always", "never")
+# the plan without sorting again. "bucketed" runs the row-per-wavefront
+# kernels with long rows split out by length (tsp_csr_bucketed_spmv)
+# instead of either.
+_SPMV_PLAN_MODES = ("auto", "always", "never", "bucketed")
 _spmv_plan_mode = "auto"
 COLPLAN_MIN_NNZ = 1 << 18
 
 
 def set_spmv_plan(mode: str) -> None:
-    """Select when spmv uses the column-sorted plan: "auto", "always", "never"."""
+    """Select when spmv uses the column-sorted plan: "auto", "always",
+    "never"; or "bucketed" for the length-bucketed row kernels."""
     global _spmv_plan_mode
     if mode not in _SPMV_PLAN_MODES:
         raise AssertionError(f"spmv plan mode must be one of {_SPMV_PLAN_MODES}, got {mode!r}")
@@ -307,12 +320,33 @@ def get_spmv_plan() -> str:
     return _spmv_plan_mode
 
 
+def _csr_bucket_plan(A, ptrs: torch.Tensor, dev: torch.device):
+    """(plan, n_medium, n_long) of the length-bucketed SpMV, cached on A by
+    pattern: the lists of rows with more than 32 and more than 2048 entries
+    (tsp_csr_bucket_plan) and their counts, read back once."""
+    m = A.shape[0]
+    key = (str(dev),) + _key(A.row_ptrs)
+    cached = getattr(A, "_hip_bucket_plan", None)
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    plan = torch.empty(_lib.load().tsp_csr_bucket_plan_size(m) // 4, dtype=torch.int32, device=dev)
+    _lib.call("tsp_csr_bucket_plan", ptrs.data_ptr(), _lib.index_code(ptrs.dtype), m, plan.data_ptr(),
+              _lib.stream_handle(dev))
+    n_med, n_long = (int(v) for v in plan[:2].cpu())
+    out = (plan, n_med, n_long)
+    try:
+        A._hip_bucket_plan = (key, out)
+    except AttributeError:
+        pass
+    return out
+
+
 def _csr_colplan(A, vals, cols, ptrs, dev, rows_per_block_log2: int = 0, tiles_hint: int = 0):
     """The column-sorted SpMV plan of A, cached on the matrix, or None when
     the plan does not apply (mode, dtype, size) or is not due yet."""
     mode = _spmv_plan_mode
     nnz = vals.numel()
-    if mode == "never" or vals.dtype != torch.float32 or nnz == 0:
+    if mode in ("never", "bucketed") or vals.dtype != torch.float32 or nnz == 0:
         return None
     if mode == "auto" and nnz < COLPLAN_MIN_NNZ:
         return None
@@ -414,7 +448,12 @@ def _csr_apply(A, X, alpha, Y, beta):
     dev = _target_device(X, A.values)
     with torch.cuda.device(dev):
         prepared = _csr_device(A, dev)
-        colplan = _csr_colplan(A, *prepared[:3], dev) if X.dim() == 1 else None
+        colplan = None
+        if X.dim() == 1 and _spmv_plan_mode == "bucketed":
+            colplan = ("bucketed",) + _csr_bucket_plan(A, prepared[2], dev)
+        elif X.dim() == 1:
+            cp = _csr_colplan(A, *prepared[:3], dev)
+            colplan = ("colplan",) + cp if cp is not None else None
         prepared = prepared + (colplan,)
         return _CSRMatMulFunction.apply(A.values, A.col_indices, A.row_ptrs, tuple(A.shape), X, alpha, Y, beta, prepared)
 

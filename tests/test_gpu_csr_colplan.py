@@ -110,6 +110,41 @@ def test_colplan_tiling_hints_via_c_abi(hip_backend, rbits, tiles):
                   xd.data_ptr(), 1.0, None, 0.0, out.data_ptr(), work.data_ptr(), 0)
 
 
+@pytest.mark.parametrize("rbits,tiles", [(13, 1), (12, 0)])
+def test_colplan_runs_across_lanes_and_wavefronts(hip_backend, rbits, tiles):
+    """Rows whose entries in one epoch fill whole lanes (8 positions), cross
+    lane boundaries, and span several wavefronts (the carry slots, added in
+    wavefront order after the epoch), next to rows of one or two entries.
+    With tiles=1 a tile holds all columns, so a row of 30000 entries takes
+    most positions of its epochs. Two calls must agree bit for bit."""
+    m, n = 8192, 60000
+    rng0 = np.random.default_rng(21)
+    lens = rng0.poisson(2, m)
+    heavy = rng0.choice(m, 12, replace=False)
+    lens[heavy] = [8, 9, 16, 63, 512, 513, 1500, 4096, 9000, 20000, 30000, 59000]
+    v, c, p, rng = _random(m, n, lens, 22)
+    A = W.csr_matrix_from_arrays(v, c, p, (m, n), device="cuda")
+    vals, cols, ptrs, _ = D._csr_device(A, torch.device("cuda"))
+    prev = D.get_spmv_plan()
+    D.set_spmv_plan("always")
+    try:
+        geom, plan = D._csr_colplan(A, vals, cols, ptrs, torch.device("cuda"), rbits, tiles)
+    finally:
+        D.set_spmv_plan(prev)
+    x = rng.standard_normal(n).astype(np.float32)
+    xd = torch.from_numpy(x).cuda()
+    outs = []
+    for _ in range(2):
+        out = torch.empty(m, device="cuda")
+        work = torch.empty(max(1, int(geom[8])), dtype=torch.uint8, device="cuda")
+        _lib.call("tsp_csr_colplan_spmv", plan.data_ptr(), _lib.TSP_F32, m, n, len(v), geom.ctypes.data,
+                  xd.data_ptr(), 1.0, None, 0.0, out.data_ptr(), work.data_ptr(),
+                  _lib.stream_handle(torch.device("cuda")))
+        outs.append(out.cpu().numpy())
+    _check(v, c, p, (m, n), x, outs[0])
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
 def test_colplan_refresh_follows_new_values(plan_always):
     m, n = 20000, 20000
     v, c, p, rng = _random(m, n, np.full(m, 16), 7)

@@ -32,13 +32,18 @@
 //            store product and row into LDS at the entry's position in row
 //            order (the plan's per-epoch inverse permutation, 16 bits per
 //            entry);
-//   phase 2  wavefront w reads positions w*E/W .. (w+1)*E/W - 1 of the
-//            epoch (consecutive: no bank conflicts), adds runs of equal rows
-//            with a segmented scan across lanes, and adds each run into the
-//            tile's LDS row sum with a plain read-modify-write: a row's run
-//            belongs to one wavefront, except its first run, which goes to a
+//   phase 2  wavefront w owns positions w*E/W .. (w+1)*E/W - 1 of the
+//            epoch and lane l of it the 8 consecutive positions from
+//            w*E/W + 8l (four 16-byte LDS reads). The lane adds its runs of
+//            equal rows in order; a run that ends inside the lane is added
+//            to the tile's LDS row sum by a plain read-modify-write. Runs
+//            that cross lanes are joined by one segmented scan of the lanes'
+//            last runs (key: row), so each row is written by exactly one
+//            lane, except the wavefront's first row, whose sum goes to a
 //            carry slot that wavefront 0 adds after the epoch's closing
-//            barrier, in wavefront order.
+//            barrier, in wavefront order. (The first form of this phase
+//            scanned every 64-position chunk across lanes: about 5x the VALU
+//            work, 82 us against 67 us on cfg2.)
 // Every sum is taken in a fixed order, so results are deterministic.
 // With G > 1 column groups each tile writes its row sums to a partial
 // vector and a second kernel adds the G partials per row in group order
@@ -47,10 +52,13 @@
 // Plan buffer (device): toff (T+1 int64, first sorted entry of each tile),
 // eoff (T+1 int64, first epoch of each tile), ent (8 bytes per padded entry:
 // value bits << 32 | row_in_tile << cbits | column_in_group), pinv (uint16
-// per padded entry: the entry's position in the epoch's row order, stored in
-// the SpMV kernel's lane order), pos (uint32 per padded entry: position in
+// per padded entry: the entry's position in the epoch's row order, swizzled
+// for phase 2's 16-byte reads), pos (uint32 per padded entry: position in
 // the caller's CSR arrays, for new values on the same pattern; 0xffffffff
-// for padding). The three per-entry arrays hold one more epoch of zeros
+// for padding). Inside an epoch, ent and pos are stored in the SpMV
+// kernel's lane order (entry_slot below): one 16-byte load gives a lane two
+// of its chunks' entries, and pinv holds a lane's 8 positions in 16
+// consecutive bytes. The three per-entry arrays hold one more epoch of zeros
 // past the last tile's, which the SpMV kernel's prefetch reads when a tile
 // has no epoch left to prefetch.
 #include "common.h"
@@ -67,6 +75,25 @@ constexpr int E = 1 << EBITS;  // entries per epoch
 constexpr uint32_t POS_PAD = 0xffffffffu;
 constexpr int SPMV_NT = 512;                   // threads of the SpMV workgroup
 constexpr int SPMV_W = SPMV_NT / 64;           // wavefronts of the SpMV workgroup
+
+constexpr int SPMV_K = E / 64 / SPMV_W;       // 64-entry chunks per wavefront and epoch
+static_assert(SPMV_K == 8, "a lane loads its chunks' entries and positions in 16-byte pieces");
+
+// Where column-order entry li = (j * W + w) * 64 + l of an epoch (chunk j of
+// wavefront w, lane l) is stored: wavefront w's entries are one contiguous
+// E/W block, in which 16-byte piece q of lane l holds its chunks 2q and
+// 2q + 1, so the four loads of a wavefront each read 1 KiB contiguously.
+__host__ __device__ constexpr int entry_slot(int li) {
+  return ((li >> 6) % SPMV_W) * (E / SPMV_W) + (((li >> 6) / SPMV_W) >> 1) * 128 + 2 * (li & 63) +
+         (((li >> 6) / SPMV_W) & 1);
+}
+
+// LDS slot of row-order position s: position pairs P = s/2 are XOR-swizzled
+// (P ^ ((P >> 3) & 3)) so that phase 2's 16-byte reads, lane l at pairs
+// 4l .. 4l + 3, put 8 consecutive lanes on 8 different 16-byte bank groups.
+__host__ __device__ constexpr int pos_slot(int s) {
+  return ((((s >> 1) ^ ((s >> 4) & 3))) << 1) | (s & 1);
+}
 
 int ilog2_ceil(int64_t v) {
   int b = 0;
@@ -166,8 +193,8 @@ __global__ __launch_bounds__(256) void colplan_fill_kernel(uint64_t* __restrict_
   pos[i] = POS_PAD;
 }
 
-// Sorted entry i of tile t goes to padded position (eoff[t] + j / E) * E + j % E,
-// j = i - toff[t].
+// Sorted entry i of tile t is column-order entry j % E of epoch eoff[t] + j / E
+// (j = i - toff[t]), stored at entry_slot(j % E) of that epoch.
 template <typename K>
 __global__ __launch_bounds__(256) void colplan_scatter_kernel(const K* __restrict__ keys,
                                                               const uint64_t* __restrict__ payload,
@@ -179,7 +206,7 @@ __global__ __launch_bounds__(256) void colplan_scatter_kernel(const K* __restric
   if (i >= nnz) return;
   const int64_t t = upper_bound_i64(toff, T + 1, i) - 1;
   const int64_t j = i - toff[t];
-  const int64_t P = ((eoff[t] + (j >> EBITS)) << EBITS) + (j & (E - 1));
+  const int64_t P = ((eoff[t] + (j >> EBITS)) << EBITS) + entry_slot((int)(j & (E - 1)));
   const uint64_t pl = payload[i];
   const uint32_t p = (uint32_t)pl;
   const uint32_t rl = (uint32_t)(pl >> 32);
@@ -189,12 +216,11 @@ __global__ __launch_bounds__(256) void colplan_scatter_kernel(const K* __restric
 }
 
 // One workgroup per epoch: each entry's position in the epoch's (row,
-// position) order, by a bitonic sort of the E keys row << EBITS | position
-// in LDS. Padding positions take row 2^rbits and sort last. Entry i =
-// (j * W + w) * 64 + l (chunk j of wavefront w, lane l in the SpMV kernel's
-// phase 1) stores its position in the 32-bit word ((j / 2) * W + w) * 64 +
-// l, low half for even j, high half for odd j: a lane loads the positions
-// of two of its entries with one dword.
+// column order) order, by a bitonic sort of the E keys row << EBITS | li in
+// LDS. Padding entries take row 2^rbits and sort last. Column-order entry
+// li = (j * W + w) * 64 + l (chunk j of wavefront w, lane l in the SpMV
+// kernel's phase 1) stores pos_slot(its position) in uint16 (w * 64 + l) * K
+// + j: a lane loads the positions of its K entries with one 16-byte load.
 __global__ __launch_bounds__(1024) void colplan_perm_kernel(const uint64_t* __restrict__ ent,
                                                             const int64_t* __restrict__ toff,
                                                             const int64_t* __restrict__ eoff, int64_t T, int rbits,
@@ -208,7 +234,7 @@ __global__ __launch_bounds__(1024) void colplan_perm_kernel(const uint64_t* __re
   const int cnt = left < E ? (int)left : E;
   const uint64_t* __restrict__ e = ent + (ep << EBITS);
   for (int i = tid; i < E; i += 1024) {
-    const uint32_t row = i < cnt ? (uint32_t)e[i] >> cbits : (1u << rbits);
+    const uint32_t row = i < cnt ? (uint32_t)e[entry_slot(i)] >> cbits : (1u << rbits);
     key[i] = (row << EBITS) | (uint32_t)i;
   }
   __syncthreads();
@@ -231,7 +257,7 @@ __global__ __launch_bounds__(1024) void colplan_perm_kernel(const uint64_t* __re
   for (int s = tid; s < E; s += 1024) {
     const int i = (int)(key[s] & (E - 1));
     const int c = i >> 6, j = c / SPMV_W, w = c % SPMV_W, l = i & 63;
-    out[2 * (((j >> 1) * SPMV_W + w) * 64 + l) + (j & 1)] = (uint16_t)s;
+    out[(w * 64 + l) * SPMV_K + j] = (uint16_t)pos_slot(s);
   }
 }
 
@@ -282,12 +308,14 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
                                                        float* __restrict__ out, float* __restrict__ partial) {
   constexpr int R = 1 << RBITS;
   constexpr int W = NT / 64;
-  constexpr int K = E / 64 / W;  // chunks per wavefront in each phase
+  constexpr int K = E / 64 / W;  // chunks per wavefront in phase 1
   constexpr int SPAN = E / W;    // phase-2 positions per wavefront
-  static_assert(W == SPMV_W, "the plan's position layout is made for this workgroup size");
+  static_assert(W == SPMV_W && K == SPMV_K, "the plan's layout is made for this workgroup size");
+  static_assert(SPAN == 8 * 64, "phase 2 gives each lane 8 positions");
   constexpr uint32_t NONE = 0xffffffffu;
-  __shared__ float acc[R + 1];  // acc[R]: the padding positions' row
-  __shared__ u32x2 slot[E];     // (product bits, row) of each epoch position
+  typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
+  __shared__ float acc[R + 1];                          // acc[R]: the padding positions' row
+  __shared__ __attribute__((aligned(16))) u32x2 slot[E];  // (product bits, row) at pos_slot(position)
   __shared__ uint32_t crow[W];
   __shared__ float cval[W];
 
@@ -301,7 +329,6 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
   const int64_t t = rb * G + g;
 
   for (int i = tid; i <= R; i += NT) acc[i] = 0.f;
-  if (tid < W) crow[tid] = NONE;
 
   const int64_t cnt_t = toff[t + 1] - toff[t];
   const int64_t ep0 = eoff[t], nep = eoff[t + 1] - ep0;
@@ -310,21 +337,27 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
 
   // Entries and the epoch's row-order positions stream two epochs ahead:
   // epoch k's registers (set A for even k, set B for odd k) are refilled
-  // with epoch k + 2 as soon as phase 1 of epoch k has consumed them. Loads
-  // issue in the order gathers(k), prefetch(k + 2), and vector memory loads
-  // complete in order, so the waits of both phases (for the gathers, for
-  // the prefetch of two epochs back) never cover the newest stream loads.
+  // with epoch k + 2 as soon as phase 1 of epoch k has consumed them.
+  // Vector memory loads complete in order, so the wait for epoch k's
+  // gathers also covers epoch k + 1's stream (issued one epoch earlier),
+  // never the newest one.
   uint64_t evA[K], evB[K];
   uint32_t pwA[K / 2], pwB[K / 2];
   // k past the tile's last epoch: the plan's zero epoch after all tiles
   auto load_epoch = [&](uint64_t (&ev)[K], uint32_t (&pw)[K / 2], int64_t k) {
     const int64_t eb = k < nep ? (ep0 + k) << EBITS : pmax;  // past the tile's end: the zero epoch
-    const uint64_t* __restrict__ pe = ent + eb + w * 64 + lane;
+    const u64x2* __restrict__ pe = reinterpret_cast<const u64x2*>(ent + eb + w * SPAN) + lane;
 #pragma unroll
-    for (int j = 0; j < K; ++j) ev[j] = __builtin_nontemporal_load(pe + j * W * 64);
-    const uint32_t* __restrict__ pp = (const uint32_t*)(pinv + eb) + w * 64 + lane;
-#pragma unroll
-    for (int j = 0; j < K / 2; ++j) pw[j] = __builtin_nontemporal_load(pp + j * W * 64);
+    for (int h = 0; h < K / 2; ++h) {
+      const u64x2 v = __builtin_nontemporal_load(pe + h * 64);
+      ev[2 * h] = v.x;
+      ev[2 * h + 1] = v.y;
+    }
+    const u32x4 pv = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(pinv + eb) + w * 64 + lane);
+    pw[0] = pv.x;
+    pw[1] = pv.y;
+    pw[2] = pv.z;
+    pw[3] = pv.w;
   };
   if (nep > 0) {
     load_epoch(evA, pwA, 0);
@@ -341,76 +374,80 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
     for (int j = 0; j < K; ++j) xv[j] = xg[(uint32_t)ev[j] & cmask];
 #pragma unroll
     for (int j = 0; j < K; ++j) {
-      const int i = (j * W + w) * 64 + lane;
+      // column-order index (j * W + w) * 64 + lane < cnt, with the chunk
+      // offset moved to the (uniform) right-hand side
+      const bool real = w * 64 + lane < cnt - j * W * 64;
       const float pr = __builtin_bit_cast(float, (uint32_t)(ev[j] >> 32)) * xv[j];
       slot[(pw[j >> 1] >> (16 * (j & 1))) & 0xffffu] =
-          u32x2{__builtin_bit_cast(uint32_t, pr), i < cnt ? (uint32_t)ev[j] >> cbits : (uint32_t)R};
+          u32x2{__builtin_bit_cast(uint32_t, pr), real ? (uint32_t)ev[j] >> cbits : (uint32_t)R};
     }
     // unconditional (past the tile's end it reads the zero epoch), so no
     // path without these loads makes the compiler wait for them early
     load_epoch(ev, pw, k + 2);
     __syncthreads();
-    // ---- phase 2: runs of equal rows in row order
-    // All LDS reads first: the K positions' (product, row), then the row
-    // sums of those rows (each row of the span is written by this
-    // wavefront at most once per epoch, so the values read here are the
-    // ones to add to). Then per chunk: segmented scan, and run tails write
-    // sum + old value. A run still open at the chunk's end is pending:
-    // (row, partial sum, old row sum) carried in scalars into the next
-    // chunk. A wavefront's first run (w > 0) goes to its carry slot, whether
-    // or not the previous wavefront's span ends in the same row; wavefront 0
-    // adds the carries after the epoch's barrier.
-    u32x2 sl[K];
+    // ---- phase 2: lane l adds positions pb .. pb + 7 in row order
+    const int pb = w * SPAN + 8 * lane;
+    uint32_t rr[8];
+    float sm[8];
+    const u32x4* __restrict__ s2 = reinterpret_cast<const u32x4*>(slot);
 #pragma unroll
-    for (int j = 0; j < K; ++j) sl[j] = slot[w * SPAN + j * 64 + lane];
-    float av[K];
+    for (int h = 0; h < 4; ++h) {
+      const int P = (pb >> 1) + h;
+      const u32x4 v = s2[P ^ ((P >> 3) & 3)];  // pos_slot of positions 2P, 2P + 1
+      // (component by component: __builtin_bit_cast of a vector component
+      // reads component 0 with this compiler, so __uint_as_float)
+      sm[2 * h] = __uint_as_float(v.x);
+      rr[2 * h] = v.y;
+      sm[2 * h + 1] = __uint_as_float(v.z);
+      rr[2 * h + 1] = v.w;
+    }
+    float old[8];  // the rows' sums before this epoch (only this lane writes a row it ends)
 #pragma unroll
-    for (int j = 0; j < K; ++j) av[j] = acc[sl[j].y];
-    uint32_t pend_row = NONE, carry_row = NONE;
-    float pend = 0.f, pend_acc = 0.f, carry_val = 0.f;
-    bool pend_carry = false;
+    for (int i = 0; i < 8; ++i) old[i] = acc[rr[i]];
 #pragma unroll
-    for (int j = 0; j < K; ++j) {
-      const uint32_t r = sl[j].y;
-      float s = seg_scan(__builtin_bit_cast(float, sl[j].x), r);
-      // run heads: lane 0 and every lane whose left neighbour (wave_shr:1)
-      // holds another row; tails: the lane before a head, and lane 63
-      const uint32_t rp = (uint32_t)__builtin_amdgcn_update_dpp((int)NONE, (int)r, 0x138, 0xf, 0xf, false);
-      const uint64_t tails = (__ballot(rp != r) >> 1) | (1ull << 63);
-      const int ft = (int)__builtin_ctzll(tails);  // tail lane of the chunk's first run
-      const uint32_t r0 = __builtin_amdgcn_readfirstlane(r);
-      const bool merge = pend_row == r0;  // the chunk's first run continues the pending run
-      if (!merge && pend_row != NONE) {   // the pending run ended with the previous chunk
-        if (pend_carry) {
-          carry_row = pend_row;
-          carry_val = pend;
-        } else if (lane == 0) {
-          acc[pend_row] = pend_acc + pend;
+    for (int i = 1; i < 8; ++i) sm[i] = rr[i] == rr[i - 1] ? sm[i - 1] + sm[i] : sm[i];
+    // sm[i]: sum of the lane's run through position i
+    const uint32_t r0 = rr[0], r7 = rr[7];
+    // Tl: the lane's last run plus the same row's runs in the lanes before
+    // (a lane whose 8 positions hold one row passes its whole sum on)
+    const float Tl = seg_scan(sm[7], r7);
+    const uint32_t next_r0 = (uint32_t)__builtin_amdgcn_update_dpp((int)NONE, (int)r0, 0x130, 0xf, 0xf, false);  // wave_shl:1
+    const uint32_t prev_r7 = (uint32_t)__builtin_amdgcn_update_dpp((int)NONE, (int)r7, 0x138, 0xf, 0xf, false);  // wave_shr:1
+    const float prev_T =
+        __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, Tl), 0x138, 0xf, 0xf, false));
+    const float inc = r0 == prev_r7 ? prev_T : 0.f;  // what flows into the lane's first run
+    const uint32_t first = __builtin_amdgcn_readfirstlane(r0);
+    // the wavefront's first row may continue the previous wavefront's last
+    // one: its sum goes to the carry slot (w > 0)
+    const bool to_carry = w > 0;
+    bool cf = false;
+    float cv = 0.f;
+#pragma unroll
+    for (int i = 0; i < 7; ++i) {
+      if (rr[i] != rr[i + 1]) {  // a run ends inside the lane
+        const float v = sm[i] + (rr[i] == r0 ? inc : 0.f);
+        if (to_carry && rr[i] == first) {
+          cf = true;
+          cv = v;
+        } else {
+          acc[rr[i]] = old[i] + v;
         }
       }
-      if (merge && r == r0) s += pend;
-      const bool carry_first = j == 0 ? w > 0 : (merge && pend_carry);
-      if (carry_first && ft < 63) {
-        carry_row = r0;
-        carry_val = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), ft));
+    }
+    if (next_r0 != r7) {  // the lane's last run ends here (lane 63: always)
+      if (to_carry && r7 == first) {
+        cf = true;
+        cv = Tl;
+      } else {
+        acc[r7] = old[7] + Tl;
       }
-      if (((tails >> lane) & 1ull) && lane < 63 && !(carry_first && r == r0)) acc[r] = av[j] + s;
-      const uint32_t r63 = __builtin_amdgcn_readlane(r, 63);
-      pend_carry = r63 == r0 && carry_first;
-      pend_row = r63;
-      pend = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), 63));
-      pend_acc = merge && r63 == r0 ? pend_acc
-                                   : __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, av[j]), 63));
     }
-    if (pend_carry) {
-      carry_row = pend_row;
-      carry_val = pend;
-    } else if (lane == 0) {
-      acc[pend_row] = pend_acc + pend;
-    }
+    const uint64_t cm = __ballot(cf);  // at most one lane: the lane that ends the first row
     if (lane == 0) {
-      crow[w] = carry_row;
-      cval[w] = carry_val;
+      crow[w] = cm ? first : NONE;
+      cval[w] = cm ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv),
+                                                                          (int)__builtin_ctzll(cm)))
+                   : 0.f;
     }
     __syncthreads();
     if (w == 0) {  // the carries, in wavefront order: rows ascend with w
@@ -421,10 +458,15 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
     }
   };
 
-  for (int64_t k = 0; k < nep; k += 2) {
+  // Pairs of epochs in the loop and an odd last one after it: with the
+  // second epoch of a pair conditional, the compiler's wait analysis
+  // assumes the path that skips it and waits for the newest stream loads.
+  int64_t k = 0;
+  for (; k + 1 < nep; k += 2) {
     epoch(evA, pwA, k);
-    if (k + 1 < nep) epoch(evB, pwB, k + 1);
+    epoch(evB, pwB, k + 1);
   }
+  if (k < nep) epoch(evA, pwA, k);
   __syncthreads();
 
   const int64_t r0 = rb << RBITS;

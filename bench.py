@@ -361,7 +361,8 @@ def bench_spmv(dist: str, index_bits: int, steps: int, warmup: int, cpu: bool = 
     built outside the timed region). `algorithmic_bytes` is the reference
     layout's traffic (nnz*(4+idx) + (m+1)*idx + 4n + 4m) and defines `value`
     and `frac_hbm`; `kernel_bytes` is what the kernel itself has to move (the
-    plan's 8-byte entries, x, y and the column groups' partial sums)."""
+    plan's 8-byte entries and 2-byte positions, x, y and the column groups'
+    partial sums)."""
     import numpy as np
     import torch
 
@@ -383,14 +384,20 @@ def bench_spmv(dist: str, index_bits: int, steps: int, warmup: int, cpu: bool = 
         build_ms = None
         kbytes = byts
         if plan == "always":
+            ts.spmv(A, xd)  # builds the plan (the first use also loads the kernels)
+            # build time on a second matrix object of the same pattern, after
+            # the one-time kernel loading
+            A2 = W.csr_matrix_from_arrays(v, c, p, shape, device="cuda")
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            ts.spmv(A, xd)  # builds the plan
+            ts.spmv(A2, xd)
             torch.cuda.synchronize()
             build_ms = (time.perf_counter() - t0) * 1e3
+            del A2
             geom = A._hip_colplan[2]
             G = int(geom[3])
-            kbytes = nnz * 8 + n * 4 + m * 4 + (2 * G * m * 4 if G > 1 else 0)
+            # 8-byte entry + 16-bit row-order position per nonzero, x, y, partials
+            kbytes = nnz * 10 + n * 4 + m * 4 + (2 * G * m * 4 if G > 1 else 0)
         if plan == "bucketed":
             ts.spmv(A, xd)  # builds the bucket plan
         flush = make_flush()

@@ -15,13 +15,13 @@
 //   of E = 4096 entries (the last one padded)
 //
 // A 64-lane instruction then covers 64 consecutive nonzeros in column
-// order of R rows: at cfg2 density (R = 8192 rows, 0.125 nonzeros per
-// column) about 512 columns, 16 lines of 128 bytes, coalesced by the address
-// unit into 16 requests instead of 64 (measured: 3.9 M L1->L2 requests per
-// SpMV instead of 18.8 M). Tiles of 8192 rows keep a workgroup's LDS at
-// 64 KiB, so two workgroups share a CU and one's barriers overlap the
-// other's work (77.5 us on cfg2 against 85-89 us for 16384-row tiles with
-// one 1024-thread workgroup per CU).
+// order of R rows: at cfg2 density (R = 16384 rows, 0.25 nonzeros per
+// column) about 256 columns, 8 lines of 128 bytes, coalesced by the address
+// unit into 8 requests instead of 64. Each tile still reads its whole x
+// slice through L1 once, so the x traffic is (m / R) x n x 4 bytes: 16384-
+// row tiles (64 KiB of LDS row sums, one 1024-thread workgroup per CU) read
+// half what 8192-row tiles (two 512-thread workgroups per CU) read, and
+// were measured faster on cfg2 (61.6 us against 66.8 us).
 //
 // Row sums without atomics. Float add atomics in LDS (ds_add_f32) run at a
 // small fraction of the rate of other LDS operations on gfx950 (measured:
@@ -33,8 +33,8 @@
 //            order (the plan's per-epoch inverse permutation, 16 bits per
 //            entry);
 //   phase 2  wavefront w owns positions w*E/W .. (w+1)*E/W - 1 of the
-//            epoch and lane l of it the 8 consecutive positions from
-//            w*E/W + 8l (four 16-byte LDS reads). The lane adds its runs of
+//            epoch and lane l of it the 4 consecutive positions from
+//            w*E/W + 4l (two 16-byte LDS reads). The lane adds its runs of
 //            equal rows in order; a run that ends inside the lane is added
 //            to the tile's LDS row sum by a plain read-modify-write. Runs
 //            that cross lanes are joined by one segmented scan of the lanes'
@@ -42,8 +42,8 @@
 //            lane, except the wavefront's first row, whose sum goes to a
 //            carry slot that wavefront 0 adds after the epoch's closing
 //            barrier, in wavefront order. (The first form of this phase
-//            scanned every 64-position chunk across lanes: about 5x the VALU
-//            work, 82 us against 67 us on cfg2.)
+//            scanned every 64-position chunk across lanes: several times
+//            the VALU work, 82 us against 67 us on cfg2.)
 // Every sum is taken in a fixed order, so results are deterministic.
 // With G > 1 column groups each tile writes its row sums to a partial
 // vector and a second kernel adds the G partials per row in group order
@@ -57,7 +57,7 @@
 // the caller's CSR arrays, for new values on the same pattern; 0xffffffff
 // for padding). Inside an epoch, ent and pos are stored in the SpMV
 // kernel's lane order (entry_slot below): one 16-byte load gives a lane two
-// of its chunks' entries, and pinv holds a lane's 8 positions in 16
+// of its chunks' entries, and pinv holds a lane's 4 positions in 8
 // consecutive bytes. The three per-entry arrays hold one more epoch of zeros
 // past the last tile's, which the SpMV kernel's prefetch reads when a tile
 // has no epoch left to prefetch.
@@ -73,26 +73,27 @@ constexpr int GEOM_RBITS = 0, GEOM_NRB = 1, GEOM_CBITS = 2, GEOM_G = 3, GEOM_T =
 constexpr int EBITS = 12;
 constexpr int E = 1 << EBITS;  // entries per epoch
 constexpr uint32_t POS_PAD = 0xffffffffu;
-constexpr int SPMV_NT = 512;                   // threads of the SpMV workgroup
+constexpr int SPMV_NT = 1024;                  // threads of the SpMV workgroup
 constexpr int SPMV_W = SPMV_NT / 64;           // wavefronts of the SpMV workgroup
 
 constexpr int SPMV_K = E / 64 / SPMV_W;       // 64-entry chunks per wavefront and epoch
-static_assert(SPMV_K == 8, "a lane loads its chunks' entries and positions in 16-byte pieces");
+constexpr int SPMV_PL = E / SPMV_W / 64;      // phase-2 row-order positions per lane
+static_assert(SPMV_K == 4 && SPMV_PL == 4, "a lane's entries and positions are loaded in 16- and 8-byte pieces");
 
 // Where column-order entry li = (j * W + w) * 64 + l of an epoch (chunk j of
 // wavefront w, lane l) is stored: wavefront w's entries are one contiguous
 // E/W block, in which 16-byte piece q of lane l holds its chunks 2q and
-// 2q + 1, so the four loads of a wavefront each read 1 KiB contiguously.
+// 2q + 1, so each load of a wavefront reads 1 KiB contiguously.
 __host__ __device__ constexpr int entry_slot(int li) {
   return ((li >> 6) % SPMV_W) * (E / SPMV_W) + (((li >> 6) / SPMV_W) >> 1) * 128 + 2 * (li & 63) +
          (((li >> 6) / SPMV_W) & 1);
 }
 
 // LDS slot of row-order position s: position pairs P = s/2 are XOR-swizzled
-// (P ^ ((P >> 3) & 3)) so that phase 2's 16-byte reads, lane l at pairs
-// 4l .. 4l + 3, put 8 consecutive lanes on 8 different 16-byte bank groups.
+// (P ^ ((P >> 3) & 1)) so that phase 2's 16-byte reads, lane l at pairs
+// 2l and 2l + 1, put 8 consecutive lanes on 8 different 16-byte bank groups.
 __host__ __device__ constexpr int pos_slot(int s) {
-  return ((((s >> 1) ^ ((s >> 4) & 3))) << 1) | (s & 1);
+  return ((((s >> 1) ^ ((s >> 4) & 1))) << 1) | (s & 1);
 }
 
 int ilog2_ceil(int64_t v) {
@@ -310,8 +311,8 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
   constexpr int W = NT / 64;
   constexpr int K = E / 64 / W;  // chunks per wavefront in phase 1
   constexpr int SPAN = E / W;    // phase-2 positions per wavefront
-  static_assert(W == SPMV_W && K == SPMV_K, "the plan's layout is made for this workgroup size");
-  static_assert(SPAN == 8 * 64, "phase 2 gives each lane 8 positions");
+  constexpr int PL = SPAN / 64;  // phase-2 positions per lane
+  static_assert(W == SPMV_W && K == SPMV_K && PL == SPMV_PL, "the plan's layout is made for this workgroup size");
   constexpr uint32_t NONE = 0xffffffffu;
   typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
   __shared__ float acc[R + 1];                          // acc[R]: the padding positions' row
@@ -335,14 +336,17 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
   const float* __restrict__ xg = x + (g << cbits);
   const uint32_t cmask = (1u << cbits) - 1u;
 
-  // Entries and the epoch's row-order positions stream two epochs ahead:
-  // epoch k's registers (set A for even k, set B for odd k) are refilled
-  // with epoch k + 2 as soon as phase 1 of epoch k has consumed them.
-  // Vector memory loads complete in order, so the wait for epoch k's
-  // gathers also covers epoch k + 1's stream (issued one epoch earlier),
-  // never the newest one.
-  uint64_t evA[K], evB[K];
-  uint32_t pwA[K / 2], pwB[K / 2];
+  // Software pipeline over epochs, with three register sets for the
+  // entries and positions and two for the gathered x values. In epoch k a
+  // wavefront issues the x gathers of epoch k + 1, multiplies epoch k's
+  // entries by its x values (gathered one epoch earlier), and refills
+  // epoch k's entry set with epoch k + 3. Vector memory loads complete in
+  // order, so waiting for epoch k's x covers the stream of epoch k + 1
+  // (issued two epochs earlier) but never the newer loads: the stream gets
+  // two epochs of lead and the gathers one.
+  uint64_t evA[K], evB[K], evC[K];
+  uint32_t pwA[K / 2], pwB[K / 2], pwC[K / 2];
+  float xa[K], xb[K];
   // k past the tile's last epoch: the plan's zero epoch after all tiles
   auto load_epoch = [&](uint64_t (&ev)[K], uint32_t (&pw)[K / 2], int64_t k) {
     const int64_t eb = k < nep ? (ep0 + k) << EBITS : pmax;  // past the tile's end: the zero epoch
@@ -353,25 +357,29 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
       ev[2 * h] = v.x;
       ev[2 * h + 1] = v.y;
     }
-    const u32x4 pv = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(pinv + eb) + w * 64 + lane);
+    const u32x2 pv = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(pinv + eb) + w * 64 + lane);
     pw[0] = pv.x;
     pw[1] = pv.y;
-    pw[2] = pv.z;
-    pw[3] = pv.w;
+  };
+  // gathers of an epoch's x (past the tile's end the zero epoch's column 0,
+  // which is inside x)
+  auto gather = [&](float (&xv)[K], const uint64_t (&ev)[K]) {
+#pragma unroll
+    for (int j = 0; j < K; ++j) xv[j] = xg[(uint32_t)ev[j] & cmask];
   };
   if (nep > 0) {
     load_epoch(evA, pwA, 0);
     load_epoch(evB, pwB, 1);
+    load_epoch(evC, pwC, 2);
   }
   __syncthreads();
 
-  auto epoch = [&](uint64_t (&ev)[K], uint32_t (&pw)[K / 2], int64_t k) {
+  auto epoch = [&](uint64_t (&ev)[K], uint32_t (&pw)[K / 2], const float (&xv)[K], const uint64_t (&evn)[K],
+                   float (&xvn)[K], int64_t k) {
     const int64_t left = cnt_t - (k << EBITS);
     const int cnt = left < E ? (int)left : E;
+    gather(xvn, evn);
     // ---- phase 1: products and rows in column order
-    float xv[K];
-#pragma unroll
-    for (int j = 0; j < K; ++j) xv[j] = xg[(uint32_t)ev[j] & cmask];
 #pragma unroll
     for (int j = 0; j < K; ++j) {
       // column-order index (j * W + w) * 64 + lane < cnt, with the chunk
@@ -383,17 +391,17 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
     }
     // unconditional (past the tile's end it reads the zero epoch), so no
     // path without these loads makes the compiler wait for them early
-    load_epoch(ev, pw, k + 2);
+    load_epoch(ev, pw, k + 3);
     __syncthreads();
-    // ---- phase 2: lane l adds positions pb .. pb + 7 in row order
-    const int pb = w * SPAN + 8 * lane;
-    uint32_t rr[8];
-    float sm[8];
+    // ---- phase 2: lane l adds positions pb .. pb + PL - 1 in row order
+    const int pb = w * SPAN + PL * lane;
+    uint32_t rr[PL];
+    float sm[PL];
     const u32x4* __restrict__ s2 = reinterpret_cast<const u32x4*>(slot);
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
+    for (int h = 0; h < PL / 2; ++h) {
       const int P = (pb >> 1) + h;
-      const u32x4 v = s2[P ^ ((P >> 3) & 3)];  // pos_slot of positions 2P, 2P + 1
+      const u32x4 v = s2[P ^ ((P >> 3) & 1)];  // pos_slot of positions 2P, 2P + 1
       // (component by component: __builtin_bit_cast of a vector component
       // reads component 0 with this compiler, so __uint_as_float)
       sm[2 * h] = __uint_as_float(v.x);
@@ -401,21 +409,21 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
       sm[2 * h + 1] = __uint_as_float(v.z);
       rr[2 * h + 1] = v.w;
     }
-    float old[8];  // the rows' sums before this epoch (only this lane writes a row it ends)
+    float old[PL];  // the rows' sums before this epoch (only this lane writes a row it ends)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) old[i] = acc[rr[i]];
+    for (int i = 0; i < PL; ++i) old[i] = acc[rr[i]];
 #pragma unroll
-    for (int i = 1; i < 8; ++i) sm[i] = rr[i] == rr[i - 1] ? sm[i - 1] + sm[i] : sm[i];
+    for (int i = 1; i < PL; ++i) sm[i] = rr[i] == rr[i - 1] ? sm[i - 1] + sm[i] : sm[i];
     // sm[i]: sum of the lane's run through position i
-    const uint32_t r0 = rr[0], r7 = rr[7];
+    const uint32_t r0 = rr[0], rl = rr[PL - 1];
     // Tl: the lane's last run plus the same row's runs in the lanes before
-    // (a lane whose 8 positions hold one row passes its whole sum on)
-    const float Tl = seg_scan(sm[7], r7);
+    // (a lane whose positions hold one row passes its whole sum on)
+    const float Tl = seg_scan(sm[PL - 1], rl);
     const uint32_t next_r0 = (uint32_t)__builtin_amdgcn_update_dpp((int)NONE, (int)r0, 0x130, 0xf, 0xf, false);  // wave_shl:1
-    const uint32_t prev_r7 = (uint32_t)__builtin_amdgcn_update_dpp((int)NONE, (int)r7, 0x138, 0xf, 0xf, false);  // wave_shr:1
+    const uint32_t prev_rl = (uint32_t)__builtin_amdgcn_update_dpp((int)NONE, (int)rl, 0x138, 0xf, 0xf, false);  // wave_shr:1
     const float prev_T =
         __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, Tl), 0x138, 0xf, 0xf, false));
-    const float inc = r0 == prev_r7 ? prev_T : 0.f;  // what flows into the lane's first run
+    const float inc = r0 == prev_rl ? prev_T : 0.f;  // what flows into the lane's first run
     const uint32_t first = __builtin_amdgcn_readfirstlane(r0);
     // the wavefront's first row may continue the previous wavefront's last
     // one: its sum goes to the carry slot (w > 0)
@@ -423,7 +431,7 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
     bool cf = false;
     float cv = 0.f;
 #pragma unroll
-    for (int i = 0; i < 7; ++i) {
+    for (int i = 0; i < PL - 1; ++i) {
       if (rr[i] != rr[i + 1]) {  // a run ends inside the lane
         const float v = sm[i] + (rr[i] == r0 ? inc : 0.f);
         if (to_carry && rr[i] == first) {
@@ -434,12 +442,12 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
         }
       }
     }
-    if (next_r0 != r7) {  // the lane's last run ends here (lane 63: always)
-      if (to_carry && r7 == first) {
+    if (next_r0 != rl) {  // the lane's last run ends here (lane 63: always)
+      if (to_carry && rl == first) {
         cf = true;
         cv = Tl;
       } else {
-        acc[r7] = old[7] + Tl;
+        acc[rl] = old[PL - 1] + Tl;
       }
     }
     const uint64_t cm = __ballot(cf);  // at most one lane: the lane that ends the first row
@@ -458,15 +466,25 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
     }
   };
 
-  // Pairs of epochs in the loop and an odd last one after it: with the
-  // second epoch of a pair conditional, the compiler's wait analysis
-  // assumes the path that skips it and waits for the newest stream loads.
+  // Six epochs per trip (the period of three entry sets and two x sets),
+  // the rest after the loop: with later epochs of a trip conditional, the
+  // compiler's wait analysis assumes the paths that skip them and waits for
+  // the newest stream loads.
+  if (nep > 0) gather(xa, evA);
   int64_t k = 0;
-  for (; k + 1 < nep; k += 2) {
-    epoch(evA, pwA, k);
-    epoch(evB, pwB, k + 1);
+  for (; k + 5 < nep; k += 6) {
+    epoch(evA, pwA, xa, evB, xb, k);
+    epoch(evB, pwB, xb, evC, xa, k + 1);
+    epoch(evC, pwC, xa, evA, xb, k + 2);
+    epoch(evA, pwA, xb, evB, xa, k + 3);
+    epoch(evB, pwB, xa, evC, xb, k + 4);
+    epoch(evC, pwC, xb, evA, xa, k + 5);
   }
-  if (k < nep) epoch(evA, pwA, k);
+  if (k < nep) epoch(evA, pwA, xa, evB, xb, k);
+  if (k + 1 < nep) epoch(evB, pwB, xb, evC, xa, k + 1);
+  if (k + 2 < nep) epoch(evC, pwC, xa, evA, xb, k + 2);
+  if (k + 3 < nep) epoch(evA, pwA, xb, evB, xa, k + 3);
+  if (k + 4 < nep) epoch(evB, pwB, xa, evC, xb, k + 4);
   __syncthreads();
 
   const int64_t r0 = rb << RBITS;
@@ -505,8 +523,8 @@ __global__ __launch_bounds__(256) void colplan_finish_f32(const float* __restric
 // ------------------------------------------------------------- geometry
 
 constexpr int RBITS_MAX = 14;          // 16384 rows: 64 KiB of fp32 row sums per workgroup
-constexpr int RBITS_DEFAULT = 13;      // 8192 rows: 32 KiB, so two workgroups share a CU
-constexpr int64_t TILES_TARGET = 512;  // two workgroups per CU
+constexpr int RBITS_DEFAULT = 14;      // one x-slice read per 16384 rows (the gathers' L1 fill halves against 8192)
+constexpr int64_t TILES_TARGET = 256;  // one 1024-thread workgroup per CU
 
 int geometry(int64_t m, int64_t n, int64_t nnz, int rbits_hint, int64_t tiles_hint, int64_t* g) {
   if (m <= 0 || n <= 0 || nnz < 0) return tsp::fail(TSP_EINVAL, "tsp_csr_colplan_geometry: bad size");

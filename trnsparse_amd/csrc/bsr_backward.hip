@@ -225,8 +225,12 @@ __global__ __launch_bounds__(256) void bsr_spmm_t_f32_dma(
 // v_mfma_f32_32x32x16_bf16 (lane half h supplies k = 8h .. 8h + 7 of each
 // 16-k step; A rows / B columns are lane % 32). One engine for both
 // products: 256 threads, 4 waves of 64x64 (2 x 2 accumulators), 64-wide
-// k-slabs of two operand tiles streamed through a 4-stage LDS ring by direct
-// loads issued three slabs ahead (4 + 4 wave instructions per slab). Each
+// k-slabs of two operand tiles streamed through a 2-stage LDS ring by direct
+// loads issued one slab ahead (4 + 4 wave instructions per slab). 64 KiB of
+// LDS lets two workgroups share a CU, so each SIMD runs one wavefront of
+// each and one's operand reads overlap the other's MFMAs: with a 4-stage
+// ring (one workgroup, one wavefront per SIMD) the LDS read latency was
+// exposed in every 16-k step and both kernels took 23-31 % longer. Each
 // operand tile is in one of two forms:
 //   ROW: [128 rows][64 k], rows of 128 B, k contiguous: a lane's 8 k values
 //        are one b128 read; chunk ^ ((row / 2) % 8) (16 consecutive rows of
@@ -238,7 +242,7 @@ __global__ __launch_bounds__(256) void bsr_spmm_t_f32_dma(
 // rows are k, its columns the output rows; dC rows of the block row).
 namespace bfb {
 constexpr int KC = 64;
-constexpr int NST = 4;
+constexpr int NST = 2;
 constexpr int TILE = 16384;
 constexpr int STAGE = 2 * TILE;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -247,18 +251,31 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 // ROW tile: rows [row0, row0 + 128) x columns [k0, k0 + 64) of a bf16
 // row-major matrix (stride ld) behind rs; columns at or past kend read as
 // zero (kend % 8 == 0).
-__device__ inline void dma_row(i32x4 rs, int64_t row0, int64_t ld, int64_t k0, int64_t kend, uint32_t dst, int w,
-                               int lane) {
+// The ROW tile stream of one operand with the per-lane offsets computed
+// once: slab s adds s * KC columns (2 bytes each) and compares with kend.
+struct RowStream {
+  uint32_t base[4];
+  int col[4];
+  __device__ RowStream(int64_t row0, int64_t ld, int w, int lane) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int i = 4 * w + q;
-    const int r = 8 * i + (lane >> 3);
-    const int c = (lane & 7) ^ ((r >> 1) & 7);
-    const int64_t col = k0 + c * 8;
-    const uint32_t off = col < kend ? (uint32_t)(((row0 + r) * ld + col) * 2) : OOB;
-    tsp::dma::buffer16(rs, off, dst + i * 1024);
+    for (int q = 0; q < 4; ++q) {
+      const int i = 4 * w + q;
+      const int r = 8 * i + (lane >> 3);
+      const int c = (lane & 7) ^ ((r >> 1) & 7);
+      col[q] = c * 8;
+      base[q] = (uint32_t)(((row0 + r) * ld + c * 8) * 2);
+    }
   }
-}
+  __device__ inline void issue(i32x4 rs, int s, int64_t kend, uint32_t dst, int w) const {
+    const int k0 = s * KC;
+    const int lim = (int)(kend - k0);  // columns k0 + col < kend  <=>  col < lim
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t off = col[q] < lim ? base[q] + (uint32_t)(k0 * 2) : OOB;
+      tsp::dma::buffer16(rs, off, dst + (4 * w + q) * 1024);
+    }
+  }
+};
 // TR tile: rows [row0, row0 + 64) x columns [c0, c0 + 128) of a bf16
 // row-major matrix (stride ld) behind rs.
 __device__ inline void dma_tr(i32x4 rs, int64_t row0, int64_t ld, int64_t c0, uint32_t dst, int w, int lane) {
@@ -313,8 +330,10 @@ __device__ inline void run(Issue&& issue, int nsteps, const uint8_t* lds, f32x16
   const int pre = nsteps < NST - 1 ? nsteps : NST - 1;
   for (int s = 0; s < pre; ++s) issue(s);
   for (int s = 0; s < nsteps; ++s) {
-    // this wave's loads of slab s are done when only later slabs' (8 each) are in flight
-    const int later = nsteps - 1 - s;
+    // this wave's loads of slab s are done when only the later slabs already
+    // issued (8 loads each, at most NST - 2 of them) are in flight
+    const int later0 = nsteps - 1 - s;
+    const int later = later0 < NST - 2 ? later0 : NST - 2;
     if (later >= 2)
       tsp::dma::wait_vm<16>();
     else if (later == 1)
@@ -358,10 +377,11 @@ __global__ __launch_bounds__(256) void bsr_sddmm_bf16_mfma(const uint16_t* __res
   const i32x4 rsg = tsp::dma::make_rsrc(G, (uint32_t)(m * ldg * 2));
   const i32x4 rsb = tsp::dma::make_rsrc(B, (uint32_t)(n * ldb * 2));
   const uint32_t lds0 = tsp::dma::lds_addr(lds);
+  const bfb::RowStream sg(i * BS, ldg, w, lane), sb(j * BS, ldb, w, lane);
   auto issue = [&](int s) {
     const uint32_t st = lds0 + (s % bfb::NST) * bfb::STAGE;
-    bfb::dma_row(rsg, i * BS, ldg, (int64_t)s * bfb::KC, ncols, st, w, lane);
-    bfb::dma_row(rsb, j * BS, ldb, (int64_t)s * bfb::KC, ncols, st + bfb::TILE, w, lane);
+    sg.issue(rsg, s, ncols, st, w);
+    sb.issue(rsb, s, ncols, st + bfb::TILE, w);
   };
   f32x16 acc[2][2];
 #pragma unroll

@@ -63,7 +63,7 @@
 // has no epoch left to prefetch.
 #include "common.h"
 
-#include <rocprim/device/device_radix_sort.hpp>
+#include "radix_sort.h"
 
 namespace {
 
@@ -549,10 +549,10 @@ int geometry(int64_t m, int64_t n, int64_t nnz, int rbits_hint, int64_t tiles_hi
   const int64_t ksz = keybits <= 32 ? 4 : 8;
   size_t tmp = 0;
   hipError_t e = keybits <= 32
-                     ? rocprim::radix_sort_pairs(nullptr, tmp, (const uint32_t*)nullptr, (uint32_t*)nullptr,
-                                                 (const uint64_t*)nullptr, (uint64_t*)nullptr, (size_t)nnz, 0, keybits)
-                     : rocprim::radix_sort_pairs(nullptr, tmp, (const uint64_t*)nullptr, (uint64_t*)nullptr,
-                                                 (const uint64_t*)nullptr, (uint64_t*)nullptr, (size_t)nnz, 0, keybits);
+                     ? tsp::rsort::radix_sort_pairs(nullptr, tmp, (const uint32_t*)nullptr, (uint32_t*)nullptr,
+                                                    (const uint64_t*)nullptr, (uint64_t*)nullptr, nnz, 0, keybits)
+                     : tsp::rsort::radix_sort_pairs(nullptr, tmp, (const uint64_t*)nullptr, (uint64_t*)nullptr,
+                                                    (const uint64_t*)nullptr, (uint64_t*)nullptr, nnz, 0, keybits);
   if (e != hipSuccess) return tsp::check_hip(e, "tsp_csr_colplan: sort size query");
   g[GEOM_RBITS] = rbits;
   g[GEOM_NRB] = nrb;
@@ -625,8 +625,8 @@ int build_typed(const float* vals, const void* col, const void* ptr, int64_t m, 
   w += align256(nnz * 8);
   void* tmp = w;
   size_t tmp_bytes = 0;
-  hipError_t e = rocprim::radix_sort_pairs(nullptr, tmp_bytes, kin, kout, pin, pout, (size_t)nnz, 0,
-                                           (int)g[GEOM_KEYBITS], st);
+  hipError_t e = tsp::rsort::radix_sort_pairs(nullptr, tmp_bytes, (const K*)kin, kout, (const uint64_t*)pin, pout, nnz,
+                                              0, (int)g[GEOM_KEYBITS], st);
   if (e != hipSuccess) return tsp::check_hip(e, "tsp_csr_colplan_build: sort size query");
   PlanView v = plan_view(plan, g);
   hipLaunchKernelGGL(colplan_fill_kernel, dim3((unsigned)tsp::ceil_div(v.pmax + E, 256)), dim3(256), 0, st, v.ent,
@@ -638,7 +638,8 @@ int build_typed(const float* vals, const void* col, const void* ptr, int64_t m, 
                        (const IdxT*)col, (const IdxT*)ptr, m, rbits, cbits, G, kin, pin);
     rc = tsp::check_launch("colplan_keys launch");
     if (rc) return rc;
-    e = rocprim::radix_sort_pairs(tmp, tmp_bytes, kin, kout, pin, pout, (size_t)nnz, 0, (int)g[GEOM_KEYBITS], st);
+    e = tsp::rsort::radix_sort_pairs(tmp, tmp_bytes, (const K*)kin, kout, (const uint64_t*)pin, pout, nnz, 0,
+                                     (int)g[GEOM_KEYBITS], st);
     if (e != hipSuccess) return tsp::check_hip(e, "tsp_csr_colplan_build: radix sort");
   }
   hipLaunchKernelGGL((colplan_offsets_kernel<K>), dim3((unsigned)tsp::ceil_div(T + 1, 256)), dim3(256), 0, st,

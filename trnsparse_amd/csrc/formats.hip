@@ -28,8 +28,7 @@
 // dense matrix with 16-byte loads where the row stride and base allow.
 #include "common.h"
 
-#include <rocprim/device/device_radix_sort.hpp>
-#include <rocprim/device/device_scan.hpp>
+#include "radix_sort.h"
 
 namespace {
 
@@ -1157,7 +1156,7 @@ namespace {
 template <typename K, typename V>
 hipError_t sort_pairs(void* tmp, size_t& tmp_bytes, const K* kin, K* kout, const V* vin, V* vout, int64_t nnz,
                       int bits, hipStream_t st) {
-  return rocprim::radix_sort_pairs(tmp, tmp_bytes, kin, kout, vin, vout, (size_t)nnz, 0, bits, st);
+  return tsp::rsort::radix_sort_pairs(tmp, tmp_bytes, kin, kout, vin, vout, nnz, 0, bits, st);
 }
 
 template <typename K, typename F>
@@ -1194,9 +1193,9 @@ int coo_to_csr_keys(const void* values, int dtype, const int64_t* row_indices, c
   hipLaunchKernelGGL(coo_keys_kernel<K>, dim3((unsigned)g), dim3(256), 0, st, row_indices, col_indices, nnz, n, keys);
   int rc = tsp::check_launch("coo_keys launch");
   if (rc) return rc;
-  if (sort_pairs_dtype<K, float>(dtype, tmp, tmp_bytes, keys, keys_s, values, values_out, nnz, key_bits(m, n), st) !=
-      hipSuccess)
-    return tsp::check_hip(hipGetLastError(), "radix_sort_pairs");
+  const hipError_t se =
+      sort_pairs_dtype<K, float>(dtype, tmp, tmp_bytes, keys, keys_s, values, values_out, nnz, key_bits(m, n), st);
+  if (se != hipSuccess) return tsp::check_hip(se, "radix_sort_pairs");
   rc = tsp::check_launch("radix_sort_pairs");
   if (rc) return rc;
   hipLaunchKernelGGL(key_cols_kernel<K>, dim3((unsigned)g), dim3(256), 0, st, keys_s, nnz, n, col_out);
@@ -1249,9 +1248,7 @@ extern "C" int64_t tsp_coo_sum_to_csr_workspace_size(int64_t nnz, int64_t m, int
   const int64_t sort_b = coo_sort_tmp(TSP_F64, nnz, nnz > 0 ? key_bits(m, n) : 1);
   if (sort_b < 0) return -1;
   size_t scan_b = 0;
-  if (nnz > 0 && rocprim::inclusive_scan(nullptr, scan_b, (int64_t*)nullptr, (int64_t*)nullptr, (size_t)nnz,
-                                         rocprim::plus<int64_t>()) != hipSuccess)
-    return -1;
+  if (nnz > 0 && tsp::rsort::inclusive_scan<int64_t>(nullptr, scan_b, nullptr, nullptr, nnz) != hipSuccess) return -1;
   const int64_t tmp = sort_b > (int64_t)scan_b ? sort_b : (int64_t)scan_b;
   return 6 * align256(8 * nnz) + align256(tmp);
 }
@@ -1285,15 +1282,15 @@ extern "C" int tsp_coo_sum_to_csr(const void* values, int dtype, const int64_t* 
   hipLaunchKernelGGL(coo_keys_kernel<uint64_t>, dim3((unsigned)g), dim3(256), 0, st, row_indices, col_indices, nnz, n, keys);
   int rc = tsp::check_launch("coo_keys launch");
   if (rc) return rc;
-  if (sort_pairs_dtype<uint64_t, float>(dtype, tmp, tmp_bytes, keys, keys_s, values, vals_s, nnz, key_bits(m, n),
-                                        st) != hipSuccess)
-    return tsp::check_hip(hipGetLastError(), "radix_sort_pairs");
+  const hipError_t sse =
+      sort_pairs_dtype<uint64_t, float>(dtype, tmp, tmp_bytes, keys, keys_s, values, vals_s, nnz, key_bits(m, n), st);
+  if (sse != hipSuccess) return tsp::check_hip(sse, "radix_sort_pairs");
   hipLaunchKernelGGL(run_heads_kernel, dim3((unsigned)g), dim3(256), 0, st, keys_s, nnz, head);
   rc = tsp::check_launch("run_heads launch");
   if (rc) return rc;
   tmp_bytes = (size_t)(workspace_bytes - 6 * a);
-  if (rocprim::inclusive_scan(tmp, tmp_bytes, head, seg, (size_t)nnz, rocprim::plus<int64_t>(), st) != hipSuccess)
-    return tsp::check_hip(hipGetLastError(), "inclusive_scan");
+  hipError_t se = tsp::rsort::inclusive_scan(tmp, tmp_bytes, (const int64_t*)head, seg, nnz, st);
+  if (se != hipSuccess) return tsp::check_hip(se, "inclusive_scan");
   if (dtype == TSP_F32)
     hipLaunchKernelGGL(run_sum_kernel<float>, dim3((unsigned)g), dim3(256), 0, st, keys_s, seg, head,
                        (const float*)vals_s, nnz, n, ukeys, col_out, (float*)values_out);
@@ -1341,9 +1338,9 @@ int csr_transpose_t(const T* values, const int64_t* col_indices, const int64_t* 
   size_t tmp_bytes = (size_t)(workspace_bytes - (2 * ka + 2 * pa));
   int rc = launch_entry_rows(row_ptrs, m, nnz, TrKeys<T>{col_indices, values, keys, pay}, st, "tr_keys launch");
   if (rc) return rc;
-  if (sort_pairs(tmp, tmp_bytes, (const uint32_t*)keys, keys_s, (const RowVal<T>*)pay, pay_s, nnz, col_bits(n), st) !=
-      hipSuccess)
-    return tsp::check_hip(hipGetLastError(), "radix_sort_pairs");
+  const hipError_t se =
+      sort_pairs(tmp, tmp_bytes, (const uint32_t*)keys, keys_s, (const RowVal<T>*)pay, pay_s, nnz, col_bits(n), st);
+  if (se != hipSuccess) return tsp::check_hip(se, "radix_sort_pairs");
   hipLaunchKernelGGL(tr_unpack_kernel<T>, dim3((unsigned)g), dim3(256), 0, st, (const RowVal<T>*)pay_s, nnz, out_col,
                      out_values);
   rc = tsp::check_launch("tr_unpack launch");
@@ -1404,9 +1401,7 @@ namespace {
 
 int64_t sum_scan_tmp(int64_t m) {
   size_t b = 0;
-  if (rocprim::exclusive_scan(nullptr, b, (int64_t*)nullptr, (int64_t*)nullptr, (int64_t)0, (size_t)(m + 1),
-                              rocprim::plus<int64_t>()) != hipSuccess)
-    return -1;
+  if (tsp::rsort::exclusive_scan<int64_t>(nullptr, b, nullptr, nullptr, 0, m + 1) != hipSuccess) return -1;
   return (int64_t)b;
 }
 
@@ -1439,9 +1434,8 @@ int csr_sum_t(const T* av, const int64_t* ac, const int64_t* ar, const T* bv, co
                      ucount, (const int64_t*)nullptr, (int64_t*)nullptr, (T*)nullptr);
   rc = tsp::check_launch("csr_sum_long (count) launch");
   if (rc) return rc;
-  if (rocprim::exclusive_scan(tmp, tb, ucount, row_ptrs, (int64_t)0, (size_t)(m + 1), rocprim::plus<int64_t>(), st) !=
-      hipSuccess)
-    return tsp::check_hip(hipGetLastError(), "exclusive_scan");
+  hipError_t se = tsp::rsort::exclusive_scan(tmp, tb, (const int64_t*)ucount, row_ptrs, (int64_t)0, m + 1, st);
+  if (se != hipSuccess) return tsp::check_hip(se, "exclusive_scan");
   if (key32)
     hipLaunchKernelGGL((csr_sum_wave_kernel<T, true, uint32_t>), dim3(gw), dim3(256), 0, st, av, ac, ar, bv, bc, br, m,
                        (int64_t*)nullptr, (const int64_t*)row_ptrs, col_out, values_out);

@@ -1,0 +1,325 @@
+// Device-wide prefix sums and a stable LSD radix sort of (key, value) pairs,
+// hand-written for gfx950 (wave64). Used by the format constructors (COO ->
+// CSR, the CSR transpose, duplicate summation) and the SpMV column-plan
+// build.
+//
+// Scan: blocks of 256 threads x 16 consecutive elements; a three-phase
+// reduce / scan-of-block-sums / apply, the block sums scanned recursively.
+//
+// Sort: 8-bit digits over bits [begin_bit, end_bit), tiles of 2048 keys
+// (256 threads x 8 keys, striped, so round i of thread t is key i*256 + t).
+// Per pass:
+//   rs_count    per-tile digit counts into a digit-major table
+//               counts[d * ntiles + tile];
+//   scan        exclusive scan of the table: the output start of digit d's
+//               keys from each tile, tiles in order;
+//   rs_scatter  each key's rank among equal digits of its tile: lanes of a
+//               wavefront with the same digit found by 8 ballots, counts per
+//               (round, wavefront, digit) in LDS prefixed in key order; the
+//               tile is reordered by digit in LDS and written as runs, so
+//               consecutive lanes write consecutive addresses.
+// Equal digits keep their input order within and across tiles, so every
+// pass and the sort are stable. Passes alternate between the output and a
+// temporary buffer so the last one lands in the output.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace tsp {
+namespace rsort {
+
+constexpr int NT = 256;             // threads per block
+constexpr int NW = NT / 64;         // wavefronts per block
+constexpr int SCAN_IPT = 16;        // scan elements per thread
+constexpr int SCAN_TILE = NT * SCAN_IPT;
+constexpr int IPT = 8;              // sort keys per thread
+constexpr int TILE = NT * IPT;      // sort keys per tile
+constexpr int RADIX = 256;
+
+inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// ------------------------------------------------------------------ scan
+
+// Exclusive scan of one value per thread over the 256 threads of a block;
+// `total` receives the block's sum. Every thread must call it.
+template <typename T>
+__device__ inline T block_exclusive_scan(T v, T& total) {
+  __shared__ T wsum[NW];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  T x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const T y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) wsum[w] = x;
+  __syncthreads();
+  T before = 0, all = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const T s = wsum[i];
+    if (i < w) before += s;
+    all += s;
+  }
+  __syncthreads();  // wsum may be reused by a later call
+  total = all;
+  return before + x - v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(NT) void scan_reduce_kernel(const T* __restrict__ in, int64_t n, T* __restrict__ sums) {
+  const int64_t base = (int64_t)blockIdx.x * SCAN_TILE + (int64_t)threadIdx.x * SCAN_IPT;
+  T s = 0;
+#pragma unroll
+  for (int i = 0; i < SCAN_IPT; ++i)
+    if (base + i < n) s += in[base + i];
+  T total;
+  block_exclusive_scan(s, total);
+  if (threadIdx.x == 0) sums[blockIdx.x] = total;
+}
+
+// out[i] = init + offs[block] + (sum of in[block start .. i), or .. i] when inclusive).
+// in == out is allowed: each thread reads its elements before writing them.
+template <typename T>
+__global__ __launch_bounds__(NT) void scan_apply_kernel(const T* in, T* out, int64_t n, const T* __restrict__ offs,
+                                                        int inclusive, T init) {
+  const int64_t base = (int64_t)blockIdx.x * SCAN_TILE + (int64_t)threadIdx.x * SCAN_IPT;
+  T v[SCAN_IPT];
+  T s = 0;
+#pragma unroll
+  for (int i = 0; i < SCAN_IPT; ++i) {
+    v[i] = base + i < n ? in[base + i] : T(0);
+    s += v[i];
+  }
+  T total;
+  T run = block_exclusive_scan(s, total) + init + (offs ? offs[blockIdx.x] : T(0));
+#pragma unroll
+  for (int i = 0; i < SCAN_IPT; ++i) {
+    if (base + i < n) out[base + i] = inclusive ? run + v[i] : run;
+    run += v[i];
+  }
+}
+
+// Temporary bytes for scan() over n elements: the block sums of every level.
+inline size_t scan_tmp_bytes(int64_t n, size_t elem) {
+  size_t b = 0;
+  int64_t nb = (n + SCAN_TILE - 1) / SCAN_TILE;
+  while (nb > 1) {
+    b += 2 * align256((size_t)nb * elem);
+    nb = (nb + SCAN_TILE - 1) / SCAN_TILE;
+  }
+  return b + 256;
+}
+
+// Prefix sums of in[0, n) into out (in place allowed), plus init.
+template <typename T>
+hipError_t scan(void* tmp, const T* in, T* out, int64_t n, bool inclusive, T init, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  const int64_t nb = (n + SCAN_TILE - 1) / SCAN_TILE;
+  if (nb > INT32_MAX) return hipErrorInvalidValue;
+  if (nb == 1) {
+    hipLaunchKernelGGL(scan_apply_kernel<T>, dim3(1), dim3(NT), 0, st, in, out, n, (const T*)nullptr,
+                       inclusive ? 1 : 0, init);
+    return hipGetLastError();
+  }
+  T* sums = (T*)tmp;
+  T* offs = (T*)((char*)tmp + align256((size_t)nb * sizeof(T)));
+  void* next = (char*)tmp + 2 * align256((size_t)nb * sizeof(T));
+  hipLaunchKernelGGL(scan_reduce_kernel<T>, dim3((unsigned)nb), dim3(NT), 0, st, in, n, sums);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  e = scan(next, (const T*)sums, offs, nb, false, T(0), st);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(scan_apply_kernel<T>, dim3((unsigned)nb), dim3(NT), 0, st, in, out, n, (const T*)offs,
+                     inclusive ? 1 : 0, init);
+  return hipGetLastError();
+}
+
+// rocPRIM-style entry points: tmp == nullptr stores the temporary size.
+template <typename T>
+hipError_t inclusive_scan(void* tmp, size_t& tmp_bytes, const T* in, T* out, int64_t n, hipStream_t st = 0) {
+  if (!tmp) {
+    tmp_bytes = scan_tmp_bytes(n, sizeof(T));
+    return hipSuccess;
+  }
+  return scan(tmp, in, out, n, true, T(0), st);
+}
+template <typename T>
+hipError_t exclusive_scan(void* tmp, size_t& tmp_bytes, const T* in, T* out, T init, int64_t n,
+                          hipStream_t st = 0) {
+  if (!tmp) {
+    tmp_bytes = scan_tmp_bytes(n, sizeof(T));
+    return hipSuccess;
+  }
+  return scan(tmp, in, out, n, false, init, st);
+}
+
+// ------------------------------------------------------------------ sort
+
+template <typename K>
+__device__ inline uint32_t digit_of(K k, int shift, uint32_t mask) {
+  return (uint32_t)(k >> shift) & mask;
+}
+
+template <typename K>
+__global__ __launch_bounds__(NT) void rs_count_kernel(const K* __restrict__ keys, int64_t n, int shift,
+                                                      uint32_t mask, int64_t ntiles, uint32_t* __restrict__ counts) {
+  __shared__ uint32_t h[NW][RADIX];
+  const int tid = threadIdx.x, w = tid >> 6;
+  for (int i = tid; i < NW * RADIX; i += NT) (&h[0][0])[i] = 0;
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * TILE;
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const int64_t idx = base + i * NT + tid;
+    if (idx < n) atomicAdd(&h[w][digit_of(keys[idx], shift, mask)], 1u);
+  }
+  __syncthreads();
+  uint32_t s = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) s += h[i][tid];
+  counts[(int64_t)tid * ntiles + blockIdx.x] = s;
+}
+
+template <typename K, typename V>
+__global__ __launch_bounds__(NT) void rs_scatter_kernel(const K* __restrict__ kin, const V* __restrict__ vin,
+                                                        K* __restrict__ kout, V* __restrict__ vout, int64_t n,
+                                                        int shift, uint32_t mask, int64_t ntiles,
+                                                        const uint32_t* __restrict__ offs) {
+  __shared__ uint16_t cnt[IPT][NW][RADIX];  // per (round, wavefront, digit): count, then start (< TILE)
+  __shared__ uint32_t gbase[RADIX];         // output start of digit d's keys from this tile
+  __shared__ uint32_t lbase[RADIX];         // start of digit d in the tile reordered by digit
+  __shared__ K sk[TILE];
+  __shared__ V sv[TILE];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int i = tid; i < IPT * NW * RADIX / 2; i += NT) ((uint32_t*)&cnt[0][0][0])[i] = 0;
+  gbase[tid] = offs[(int64_t)tid * ntiles + blockIdx.x];
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * TILE;
+  const uint64_t lt = (1ull << lane) - 1;
+  K k[IPT];
+  V val[IPT];
+  uint32_t dg[IPT], rk[IPT];
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const int64_t idx = base + i * NT + tid;
+    if (idx < n) {
+      k[i] = kin[idx];
+      val[i] = vin[idx];
+    } else {
+      k[i] = K(0);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const int64_t idx = base + i * NT + tid;
+    const bool valid = idx < n;
+    dg[i] = digit_of(k[i], shift, mask);
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const bool bit = (dg[i] >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    rk[i] = (uint32_t)__popcll(peers & lt);
+    if (valid && rk[i] == 0) cnt[i][w][dg[i]] = (uint16_t)__popcll(peers);
+  }
+  __syncthreads();
+  // digit tid: starts of its (round, wavefront) groups in key order, and its tile total
+  uint32_t run = 0;
+#pragma unroll
+  for (int i = 0; i < IPT; ++i)
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      const uint32_t c = cnt[i][v][tid];
+      cnt[i][v][tid] = (uint16_t)run;
+      run += c;
+    }
+  uint32_t total;
+  lbase[tid] = block_exclusive_scan(run, total);
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const int64_t idx = base + i * NT + tid;
+    if (idx < n) {
+      const uint32_t p = lbase[dg[i]] + cnt[i][w][dg[i]] + rk[i];
+      if (p < (uint32_t)TILE) {  // always true; keeps a miscount from writing outside the tile
+        sk[p] = k[i];
+        sv[p] = val[i];
+      }
+    }
+  }
+  __syncthreads();
+  const int cnt_tile = (int)(n - base < TILE ? n - base : TILE);
+  for (int j = tid; j < cnt_tile; j += NT) {
+    const K kk = sk[j];
+    const uint32_t d = digit_of(kk, shift, mask);
+    const int64_t pos = (int64_t)gbase[d] + (j - (int64_t)lbase[d]);
+    if (pos >= 0 && pos < n) {  // always true; keeps a miscount from writing outside the output
+      kout[pos] = kk;
+      vout[pos] = sv[j];
+    }
+  }
+}
+
+// Stable sort of (kin, vin)[0, n) by key bits [begin_bit, end_bit) into (kout, vout);
+// the inputs are left unchanged. tmp == nullptr stores the temporary size.
+// Keys must be unsigned; n < 2^32.
+template <typename K, typename V>
+hipError_t radix_sort_pairs(void* tmp, size_t& tmp_bytes, const K* kin, K* kout, const V* vin, V* vout, int64_t n,
+                            int begin_bit, int end_bit, hipStream_t st = 0) {
+  if (n < 0 || n > (int64_t)UINT32_MAX || begin_bit < 0 || end_bit > (int)(8 * sizeof(K)) || end_bit < begin_bit)
+    return hipErrorInvalidValue;
+  const int64_t ntiles = (n + TILE - 1) / TILE;
+  const int64_t table = (int64_t)RADIX * (ntiles > 0 ? ntiles : 1);
+  const size_t kb = align256((size_t)n * sizeof(K)), vb = align256((size_t)n * sizeof(V));
+  const size_t cb = align256((size_t)table * sizeof(uint32_t));
+  const size_t need = kb + vb + cb + scan_tmp_bytes(table, sizeof(uint32_t));
+  if (!tmp) {
+    tmp_bytes = need;
+    return hipSuccess;
+  }
+  if (tmp_bytes < need) return hipErrorInvalidValue;
+  if (n == 0) return hipSuccess;
+  K* tk = (K*)tmp;
+  V* tv = (V*)((char*)tmp + kb);
+  uint32_t* counts = (uint32_t*)((char*)tmp + kb + vb);
+  void* stmp = (char*)tmp + kb + vb + cb;
+  const int passes = (end_bit - begin_bit + 7) / 8;
+  if (passes == 0) {
+    hipError_t e = hipMemcpyAsync(kout, kin, (size_t)n * sizeof(K), hipMemcpyDeviceToDevice, st);
+    if (e != hipSuccess) return e;
+    return hipMemcpyAsync(vout, vin, (size_t)n * sizeof(V), hipMemcpyDeviceToDevice, st);
+  }
+  const K* sk = kin;
+  const V* sv = vin;
+  for (int p = 0; p < passes; ++p) {
+    // the last pass writes the output: an odd count starts there, an even one in tmp
+    const bool to_out = ((passes - 1 - p) & 1) == 0;
+    K* dk = to_out ? kout : tk;
+    V* dv = to_out ? vout : tv;
+    const int shift = begin_bit + 8 * p;
+    const int bits = end_bit - shift < 8 ? end_bit - shift : 8;
+    const uint32_t mask = (1u << bits) - 1;
+    hipLaunchKernelGGL(rs_count_kernel<K>, dim3((unsigned)ntiles), dim3(NT), 0, st, sk, n, shift, mask, ntiles,
+                       counts);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    e = scan(stmp, (const uint32_t*)counts, counts, table, false, 0u, st);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((rs_scatter_kernel<K, V>), dim3((unsigned)ntiles), dim3(NT), 0, st, sk, sv, dk, dv, n, shift,
+                       mask, ntiles, (const uint32_t*)counts);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    sk = dk;
+    sv = dv;
+  }
+  return hipSuccess;
+}
+
+}  // namespace rsort
+}  // namespace tsp

@@ -172,10 +172,26 @@ __global__ __launch_bounds__(NT) void rs_count_kernel(const K* __restrict__ keys
   for (int i = tid; i < NW * RADIX; i += NT) (&h[0][0])[i] = 0;
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * TILE;
+  if (base + TILE <= n && ((uintptr_t)keys & 15) == 0) {
+    // full tile: counting ignores order, so each thread takes IPT consecutive keys in 16-byte loads
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    constexpr int PER = 16 / (int)sizeof(K), NV = IPT / PER;
+    const u32x4* p = (const u32x4*)(keys + base + (int64_t)tid * IPT);
+    u32x4 v[NV];
 #pragma unroll
-  for (int i = 0; i < IPT; ++i) {
-    const int64_t idx = base + i * NT + tid;
-    if (idx < n) atomicAdd(&h[w][digit_of(keys[idx], shift, mask)], 1u);
+    for (int j = 0; j < NV; ++j) v[j] = p[j];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const K* kk = (const K*)&v[j];
+#pragma unroll
+      for (int e = 0; e < PER; ++e) atomicAdd(&h[w][digit_of(kk[e], shift, mask)], 1u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) {
+      const int64_t idx = base + i * NT + tid;
+      if (idx < n) atomicAdd(&h[w][digit_of(keys[idx], shift, mask)], 1u);
+    }
   }
   __syncthreads();
   uint32_t s = 0;

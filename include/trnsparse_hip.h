@@ -125,6 +125,23 @@ int tsp_bsr_spmv(const void* blocks, int dtype, const int64_t* block_row_ptrs,
  *   element written. col_order: optional heaviest-first permutation of the
  *   block columns (tsp_bsr_row_order on col_ptrs), scheduling only.
  * ==================================================================== */
+/* tsp_bsr_col_view: the pattern views the two backward kernels take, built
+ *   on the device from the block CSR (block_row_ptrs (n_block_rows+1,),
+ *   block_col_indices (nnzb,), int64): block_rows (nnzb,) the block row of
+ *   every stored block; col_ptrs (n_block_cols+1,); col_block_ids /
+ *   col_block_rows (nnzb,), per block column in increasing block-row order,
+ *   the stored block index and its block row (a stable sort of the blocks
+ *   by column). The reference backward gathers dense panels on the host
+ *   instead (trnsparse/nki/dispatch.py:348-369); this view replaces that
+ *   gather. nnzb, n_block_rows <= 2^32. workspace:
+ *   tsp_bsr_col_view_workspace_size(nnzb, n_block_cols) bytes. */
+int64_t tsp_bsr_col_view_workspace_size(int64_t nnzb, int64_t n_block_cols);
+int tsp_bsr_col_view(const int64_t* block_row_ptrs,
+                     const int64_t* block_col_indices, int64_t n_block_rows,
+                     int64_t n_block_cols, int64_t nnzb, int64_t* block_rows,
+                     int64_t* col_ptrs, int64_t* col_block_ids,
+                     int64_t* col_block_rows, void* workspace,
+                     int64_t workspace_bytes, void* stream);
 int tsp_bsr_sddmm(const void* G, int64_t ldg, int64_t m,
                   const void* B, int64_t ldb, int64_t n, int64_t ncols,
                   const int64_t* block_rows, const int64_t* block_col_indices,

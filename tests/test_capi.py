@@ -67,6 +67,10 @@ def test_argument_validation_is_host_side():
     assert lib.tsp_csr_transpose(None, 9, None, None, 3, 4, 5, None, None, None, None, 0, None) == -2
     assert lib.tsp_csr_sum(None, None, None, 2, None, None, None, 0, 0, 0, 4, None, None, None, None, 0, None) == -1
     assert lib.tsp_csr_transpose_workspace_size(10, 3, 4, 9) == -1 and lib.tsp_csr_sum_workspace_size(-1, 0, 3, 4, 0) == -1
+    # BSR block-column view: blocks without block rows, null outputs, bad sizes
+    assert lib.tsp_bsr_col_view(None, None, 0, 4, 3, None, None, None, None, None, 0, None) == -1
+    assert lib.tsp_bsr_col_view(None, None, 2, 4, 3, None, None, None, None, None, 0, None) == -1
+    assert lib.tsp_bsr_col_view_workspace_size(-1, 4) == -1 and lib.tsp_bsr_col_view_workspace_size(10, 4) > 0
     assert lib.tsp_csr_sum(None, None, None, 1, None, None, None, 1, 0, 2, 4, None, None, None, None, 0, None) == -1
     # CSR SDDMM: bad dtype, bad index type, leading dimension below ncols, null pointers
     assert lib.tsp_csr_sddmm(None, None, 1, 4, 4, 3, None, 8, None, 8, 8, 2, 1.0, None, None) == -2

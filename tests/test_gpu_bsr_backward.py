@@ -162,3 +162,26 @@ def test_cfg3b_backward_full_size(hip_backend):
         exact = sum(blocks[k].T @ Gn[brow[k] * 128 : (brow[k] + 1) * 128] for k in ks)
         scale = sum(np.abs(blocks[k]).T @ np.abs(Gn[brow[k] * 128 : (brow[k] + 1) * 128]) for k in ks)
         assert ref.scaled_error(dB[j * 128 : (j + 1) * 128].double().cpu().numpy(), exact, scale) <= TOL[torch.bfloat16]
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mb,nbc,p", [(1, 1, 1.0), (7, 300, 0.2), (40, 3, 0.9), (5, 5, 0.0)])
+def test_block_column_view(mb, nbc, p):
+    """tsp_bsr_col_view against a stable numpy sort of the blocks by column."""
+    from trnsparse_amd.hip import dispatch as D
+
+    g = torch.Generator().manual_seed(mb * 1000 + nbc)
+    mask = torch.rand(mb, nbc, generator=g) < p
+    A = W.bsr_from_block_mask(mask, 128)
+    rp_h = A.block_row_ptrs.numpy()
+    ci_h = A.block_col_indices.numpy()
+    dev = torch.device("cuda")
+    brow, cp, cbid, crow, corder = D._bsr_bwd_plan(A.block_row_ptrs.to(dev), A.block_col_indices.to(dev), mb, nbc, dev)
+    want_brow = np.repeat(np.arange(mb), np.diff(rp_h))
+    order = np.argsort(ci_h, kind="stable")
+    want_cp = np.zeros(nbc + 1, dtype=np.int64)
+    want_cp[1:] = np.cumsum(np.bincount(ci_h, minlength=nbc))
+    assert np.array_equal(brow.cpu().numpy(), want_brow)
+    assert np.array_equal(cp.cpu().numpy(), want_cp)
+    assert np.array_equal(cbid.cpu().numpy(), order)
+    assert np.array_equal(crow.cpu().numpy(), want_brow[order])
+    assert sorted(corder.cpu().numpy().tolist()[:nbc]) == list(range(nbc))

@@ -1397,6 +1397,86 @@ extern "C" int tsp_csr_transpose(const void* values, int dtype, const int64_t* c
                          (uint16_t*)out_values, w, workspace_bytes, st);
 }
 
+// ------------------------------------------------ BSR block-column view
+
+namespace {
+
+// entry k (block k of block row r): sort key = its block column; payload = (r, k)
+struct BlkKeys {
+  const int64_t* cols;
+  uint32_t* keys;
+  RowVal<uint32_t>* payload;
+  int64_t* block_rows;
+  __device__ void operator()(int64_t k, int64_t r) const {
+    keys[k] = (uint32_t)cols[k];
+    payload[k] = RowVal<uint32_t>{(uint32_t)r, (uint32_t)k};
+    block_rows[k] = r;
+  }
+};
+
+__global__ __launch_bounds__(256) void blk_unpack_kernel(const RowVal<uint32_t>* __restrict__ payload, int64_t nnzb,
+                                                         int64_t* __restrict__ col_block_rows,
+                                                         int64_t* __restrict__ col_block_ids) {
+  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (k >= nnzb) return;
+  const RowVal<uint32_t> p = payload[k];
+  col_block_rows[k] = (int64_t)p.row;
+  col_block_ids[k] = (int64_t)p.val;
+}
+
+}  // namespace
+
+extern "C" int64_t tsp_bsr_col_view_workspace_size(int64_t nnzb, int64_t n_block_cols) {
+  if (nnzb < 0 || n_block_cols < 0) return -1;
+  size_t tmp = 0;
+  if (nnzb > 0 && tsp::rsort::radix_sort_pairs(nullptr, tmp, (const uint32_t*)nullptr, (uint32_t*)nullptr,
+                                               (const RowVal<uint32_t>*)nullptr, (RowVal<uint32_t>*)nullptr, nnzb, 0,
+                                               col_bits(n_block_cols)) != hipSuccess)
+    return -1;
+  return 2 * align256(4 * nnzb) + 2 * align256(8 * nnzb) + align256((int64_t)tmp);
+}
+
+extern "C" int tsp_bsr_col_view(const int64_t* block_row_ptrs, const int64_t* block_col_indices, int64_t n_block_rows,
+                                int64_t n_block_cols, int64_t nnzb, int64_t* block_rows, int64_t* col_ptrs,
+                                int64_t* col_block_ids, int64_t* col_block_rows, void* workspace,
+                                int64_t workspace_bytes, void* stream) {
+  if (nnzb < 0 || n_block_rows < 0 || n_block_cols < 0 || (n_block_rows == 0 && nnzb > 0))
+    return tsp::fail(TSP_EINVAL, "tsp_bsr_col_view: bad size");
+  if (nnzb > UINT32_MAX || n_block_rows > UINT32_MAX || n_block_cols > (int64_t)UINT32_MAX + 1)
+    return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_col_view: sizes past 2^32");
+  if (!col_ptrs) return tsp::fail(TSP_EINVAL, "tsp_bsr_col_view: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  if (nnzb == 0) return tsp::zero_fill(col_ptrs, 8 * (n_block_cols + 1), st);
+  if (!block_row_ptrs || !block_col_indices || !block_rows || !col_block_ids || !col_block_rows || !workspace)
+    return tsp::fail(TSP_EINVAL, "tsp_bsr_col_view: null pointer");
+  if (workspace_bytes < tsp_bsr_col_view_workspace_size(nnzb, n_block_cols))
+    return tsp::fail(TSP_EINVAL, "tsp_bsr_col_view: workspace too small");
+  if (tsp::ceil_div(n_block_cols + 1, 256) > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_col_view: too large");
+  char* w = (char*)workspace;
+  const int64_t ka = align256(4 * nnzb), pa = align256(8 * nnzb);
+  uint32_t* keys = (uint32_t*)w;
+  uint32_t* keys_s = (uint32_t*)(w + ka);
+  RowVal<uint32_t>* pay = (RowVal<uint32_t>*)(w + 2 * ka);
+  RowVal<uint32_t>* pay_s = (RowVal<uint32_t>*)(w + 2 * ka + pa);
+  void* tmp = w + 2 * ka + 2 * pa;
+  size_t tmp_bytes = (size_t)(workspace_bytes - (2 * ka + 2 * pa));
+  int rc = launch_entry_rows(block_row_ptrs, n_block_rows, nnzb, BlkKeys{block_col_indices, keys, pay, block_rows}, st,
+                             "bsr_col_view keys launch");
+  if (rc) return rc;
+  // stable: within a block column, blocks keep their CSR order, i.e. increasing block row
+  const hipError_t se = tsp::rsort::radix_sort_pairs(tmp, tmp_bytes, (const uint32_t*)keys, keys_s,
+                                                     (const RowVal<uint32_t>*)pay, pay_s, nnzb, 0,
+                                                     col_bits(n_block_cols), st);
+  if (se != hipSuccess) return tsp::check_hip(se, "radix_sort_pairs");
+  hipLaunchKernelGGL(blk_unpack_kernel, dim3((unsigned)tsp::ceil_div(nnzb, 256)), dim3(256), 0, st,
+                     (const RowVal<uint32_t>*)pay_s, nnzb, col_block_rows, col_block_ids);
+  rc = tsp::check_launch("bsr_col_view unpack launch");
+  if (rc) return rc;
+  hipLaunchKernelGGL(tr_row_ptrs_kernel, dim3((unsigned)tsp::ceil_div(n_block_cols + 1, 256)), dim3(256), 0, st,
+                     (const uint32_t*)keys_s, nnzb, n_block_cols, col_ptrs);
+  return tsp::check_launch("bsr_col_view col_ptrs launch");
+}
+
 namespace {
 
 int64_t sum_scan_tmp(int64_t m) {

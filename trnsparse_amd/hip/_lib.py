@@ -36,6 +36,8 @@ SIGNATURES: dict[str, tuple] = {
         [_P, _INT, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _INT, _P, _P],
     ),
     "tsp_bsr_row_order": (_INT, [_P, _I64, _P, _P]),
+    "tsp_bsr_col_view_workspace_size": (_I64, [_I64, _I64]),
+    "tsp_bsr_col_view": (_INT, [_P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P]),
     "tsp_bsr_spmv": (
         _INT,
         [_P, _INT, _P, _P, _I64, _I64, _I64, _I64, _P, _DBL, _P, _DBL, _P, _DBL, _P, _DBL, _P, _P, _P],

@@ -150,23 +150,29 @@ class _BSRSpMMFunction(torch.autograd.Function):
 
 
 def _bsr_bwd_plan(rp: torch.Tensor, ci: torch.Tensor, mb: int, nbc: int, dev: torch.device):
-    """Pattern views for the backward kernels, on the device: the block row of
-    every stored block, and the block-column view (col_ptrs; per column, in
-    increasing block-row order, the stored block index and its block row),
-    plus the heaviest-first order of the block columns."""
-    counts = rp[1:] - rp[:-1]
-    brow = torch.repeat_interleave(torch.arange(mb, device=dev, dtype=torch.int64), counts)
+    """Pattern views for the backward kernels, built on the device by
+    tsp_bsr_col_view: the block row of every stored block, and the
+    block-column view (col_ptrs; per column, in increasing block-row order,
+    the stored block index and its block row), plus the heaviest-first order
+    of the block columns (tsp_bsr_row_order on col_ptrs)."""
     nnzb = ci.numel()
-    key = ci * max(mb, 1) + brow
-    cbid = torch.sort(key, stable=True).indices.to(torch.int64)
-    crow = brow[cbid].contiguous()
-    cp = torch.zeros(nbc + 1, dtype=torch.int64, device=dev)
-    if nnzb:
-        cp[1:] = torch.cumsum(torch.bincount(ci, minlength=nbc), 0)
+    i64 = dict(dtype=torch.int64, device=dev)
+    brow = torch.empty(max(nnzb, 1), **i64)
+    cp = torch.empty(nbc + 1, **i64)
+    cbid = torch.empty(max(nnzb, 1), **i64)
+    crow = torch.empty(max(nnzb, 1), **i64)
+    lib = _lib.load()
+    wsz = lib.tsp_bsr_col_view_workspace_size(nnzb, nbc)
+    if wsz < 0:
+        raise RuntimeError(f"tsp_bsr_col_view_workspace_size failed for {nnzb} blocks, {nbc} block columns")
+    ws = torch.empty(max(int(wsz), 1), dtype=torch.uint8, device=dev)
+    st = _lib.stream_handle(dev)
+    _lib.call("tsp_bsr_col_view", rp.data_ptr(), ci.data_ptr(), mb, nbc, nnzb, brow.data_ptr(), cp.data_ptr(),
+              cbid.data_ptr(), crow.data_ptr(), ws.data_ptr(), int(wsz), st)
     corder = torch.empty(max(nbc, 1), dtype=torch.int32, device=dev)
     if nbc:
-        _lib.call("tsp_bsr_row_order", cp.data_ptr(), nbc, corder.data_ptr(), _lib.stream_handle(dev))
-    return brow.contiguous(), cp, cbid.contiguous(), crow, corder
+        _lib.call("tsp_bsr_row_order", cp.data_ptr(), nbc, corder.data_ptr(), st)
+    return brow[:nnzb], cp, cbid[:nnzb], crow[:nnzb], corder
 
 
 def hip_bsr_matvec_update(A, x: torch.Tensor, alpha: float, out: torch.Tensor, u=None, beta: float = 0.0, v=None,

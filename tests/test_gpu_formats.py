@@ -182,6 +182,40 @@ def test_coo_to_csr_matches_cpu_and_oracle(hip_backend, dtype, m, n):
     assert empty.row_ptrs.cpu().tolist() == [0] * 5 and empty.nnz == 0
 
 
+def test_coo_large_sort_and_multi_level_scans(hip_backend):
+    """17 M entries on a 4096 x 4096 grid (about one duplicate per cell):
+    COO -> CSR sorts 8301 tiles (a two-level scan of the digit-count table)
+    and the duplicate sum scans 17 M run heads (three scan levels). Integer
+    values make every sum exact, so both are compared bit for bit with a
+    stable numpy sort."""
+    from trnsparse_amd.hip import formats as HF
+
+    g = torch.Generator().manual_seed(31)
+    m = n = 4096
+    nnz = 17_000_000
+    rows = torch.randint(0, m, (nnz,), generator=g)
+    cols = torch.randint(0, n, (nnz,), generator=g)
+    vals = torch.randint(-1000, 1001, (nnz,), generator=g).to(torch.float32)
+    key = rows.numpy() * n + cols.numpy()
+    order = np.argsort(key, kind="stable")
+    ks = key[order]
+    # COO -> CSR: the stable permutation
+    v, c, p = HF.coo_to_csr(vals.cuda(), rows.cuda(), cols.cuda(), (m, n))
+    np.testing.assert_array_equal(v.cpu().numpy(), vals.numpy()[order])
+    np.testing.assert_array_equal(c.cpu().numpy(), ks % n)
+    np.testing.assert_array_equal(p.cpu().numpy(), np.searchsorted(ks, np.arange(m + 1) * n))
+    # duplicates summed: one entry per distinct key
+    heads = np.ones(nnz, dtype=bool)
+    heads[1:] = ks[1:] != ks[:-1]
+    starts = np.flatnonzero(heads)
+    want_v = np.add.reduceat(vals.numpy()[order].astype(np.float64), starts).astype(np.float32)
+    uk = ks[starts]
+    sv, sc, sp = HF.coo_sum_to_csr(vals.cuda(), rows.cuda(), cols.cuda(), (m, n))
+    np.testing.assert_array_equal(sv.cpu().numpy(), want_v)
+    np.testing.assert_array_equal(sc.cpu().numpy(), uk % n)
+    np.testing.assert_array_equal(sp.cpu().numpy(), np.searchsorted(uk, np.arange(m + 1) * n))
+
+
 def test_cfg3_round_trip_full_size(hip_backend):
     """cfg3 (16384^2, 1638 stored 128x128 blocks, fp32): to_dense then
     from_dense on the device gives back the same structure and blocks

@@ -118,24 +118,68 @@ __device__ inline int64_t upper_bound_i64(const int64_t* __restrict__ a, int64_t
 
 // ------------------------------------------------------------ plan build
 
-// One thread per row: sort key (tile, column in group) and payload
-// (row in tile, CSR position) of each of the row's entries.
+// Sort key (tile, column in group) and payload (row in tile, CSR position)
+// of every entry, entry-parallel: a workgroup takes KTILE consecutive
+// entries, finds the rows they span by binary search of row_ptrs, stages
+// those row pointers in LDS when there are at most KSPAN of them, and gives
+// each entry its row by a search of the staged span (one thread per row
+// would read the column indices uncoalesced and stall on a long row).
+constexpr int KTILE = 4096;
+constexpr int KSPAN = 2048;
+
+template <typename IdxT>
+__device__ inline int64_t row_of(const IdxT* __restrict__ ptr, int64_t m, int64_t p) {
+  int64_t lo = 0, hi = m;  // ptr[lo] <= p < ptr[hi]: the last row starting at or before p
+  while (hi - lo > 1) {
+    const int64_t mid = (lo + hi) >> 1;
+    if ((int64_t)ptr[mid] <= p)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
 template <typename IdxT, typename K>
 __global__ __launch_bounds__(256) void colplan_keys_kernel(const IdxT* __restrict__ col, const IdxT* __restrict__ ptr,
-                                                           int64_t m, int rbits, int cbits, int64_t G,
+                                                           int64_t m, int64_t nnz, int rbits, int cbits, int64_t G,
                                                            K* __restrict__ keys, uint64_t* __restrict__ payload) {
-  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= m) return;
-  const int64_t base = (int64_t)ptr[0];
-  const int64_t a = (int64_t)ptr[r], e = (int64_t)ptr[r + 1];
-  const int64_t rb = r >> rbits;
-  const uint64_t rl = (uint64_t)(r & (((int64_t)1 << rbits) - 1)) << 32;
-  const int64_t cmask = ((int64_t)1 << cbits) - 1;
-  for (int64_t p = a; p < e; ++p) {  // p: position in the caller's arrays; p - base: position in the sort
+  __shared__ int64_t srp[KSPAN + 1];
+  __shared__ int64_t span[2];
+  const int64_t base = (int64_t)ptr[0];  // p: position in the caller's arrays; p - base: position in the sort
+  const int64_t e0 = (int64_t)blockIdx.x * KTILE;
+  const int64_t e1 = e0 + KTILE < nnz ? e0 + KTILE : nnz;
+  if (threadIdx.x == 0) {
+    span[0] = row_of(ptr, m, base + e0);
+    span[1] = row_of(ptr, m, base + e1 - 1);
+  }
+  __syncthreads();
+  const int64_t rlo = span[0], nr = span[1] - rlo + 1;
+  const bool staged = nr <= KSPAN;
+  if (staged)
+    for (int64_t i = threadIdx.x; i <= nr; i += 256) srp[i] = (int64_t)ptr[rlo + i];
+  __syncthreads();
+  const int64_t rmask = ((int64_t)1 << rbits) - 1, cmask = ((int64_t)1 << cbits) - 1;
+  for (int64_t k = e0 + threadIdx.x; k < e1; k += 256) {
+    const int64_t p = base + k;
+    int64_t r;
+    if (staged) {
+      int lo = 0, hi = (int)nr;  // srp[lo] <= p < srp[hi]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (srp[mid] <= p)
+          lo = mid;
+        else
+          hi = mid;
+      }
+      r = rlo + lo;
+    } else {
+      r = row_of(ptr, m, p);
+    }
     const int64_t c = (int64_t)col[p];
-    const int64_t tile = rb * G + (c >> cbits);
-    keys[p - base] = (K)((tile << cbits) | (c & cmask));
-    payload[p - base] = rl | (uint64_t)p;
+    const int64_t tile = (r >> rbits) * G + (c >> cbits);
+    keys[k] = (K)((tile << cbits) | (c & cmask));
+    payload[k] = ((uint64_t)(r & rmask) << 32) | (uint64_t)p;
   }
 }
 
@@ -634,8 +678,9 @@ int build_typed(const float* vals, const void* col, const void* ptr, int64_t m, 
   int rc = tsp::check_launch("colplan_fill launch");
   if (rc) return rc;
   if (nnz > 0) {
-    hipLaunchKernelGGL((colplan_keys_kernel<IdxT, K>), dim3((unsigned)tsp::ceil_div(m, 256)), dim3(256), 0, st,
-                       (const IdxT*)col, (const IdxT*)ptr, m, rbits, cbits, G, kin, pin);
+    if (tsp::ceil_div(nnz, KTILE) > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_colplan_build: too many entries");
+    hipLaunchKernelGGL((colplan_keys_kernel<IdxT, K>), dim3((unsigned)tsp::ceil_div(nnz, KTILE)), dim3(256), 0, st,
+                       (const IdxT*)col, (const IdxT*)ptr, m, nnz, rbits, cbits, G, kin, pin);
     rc = tsp::check_launch("colplan_keys launch");
     if (rc) return rc;
     e = tsp::rsort::radix_sort_pairs(tmp, tmp_bytes, (const K*)kin, kout, (const uint64_t*)pin, pout, nnz, 0,

@@ -182,6 +182,35 @@ def test_coo_to_csr_matches_cpu_and_oracle(hip_backend, dtype, m, n):
     assert empty.row_ptrs.cpu().tolist() == [0] * 5 and empty.nnz == 0
 
 
+@pytest.mark.parametrize("nnz", [1, 2, 2047, 2048, 2049, 4095, 4096, 4097, 12289])
+@pytest.mark.parametrize("kind", ["random", "equal", "two"])
+def test_coo_to_csr_tile_edges_and_stability(hip_backend, nnz, kind):
+    """The device radix sort at its tile boundaries (2048- and 4096-key
+    tiles), a single entry, and all-equal or two-valued keys, where only
+    stability fixes the order: compared bit for bit with a stable numpy sort."""
+    from trnsparse_amd.hip import formats as HF
+
+    g = torch.Generator().manual_seed(nnz)
+    m, n = 300, 257
+    if kind == "random":
+        rows = torch.randint(0, m, (nnz,), generator=g)
+        cols = torch.randint(0, n, (nnz,), generator=g)
+    elif kind == "equal":
+        rows = torch.full((nnz,), 7)
+        cols = torch.full((nnz,), 255)
+    else:
+        pick = torch.randint(0, 2, (nnz,), generator=g)
+        rows = torch.where(pick == 1, torch.tensor(m - 1), torch.tensor(0))
+        cols = torch.where(pick == 1, torch.tensor(0), torch.tensor(n - 1))
+    vals = torch.arange(nnz, dtype=torch.float32)  # the value is the input position
+    key = rows.numpy() * n + cols.numpy()
+    order = np.argsort(key, kind="stable")
+    v, c, p = HF.coo_to_csr(vals.cuda(), rows.cuda(), cols.cuda(), (m, n))
+    np.testing.assert_array_equal(v.cpu().numpy(), vals.numpy()[order])
+    np.testing.assert_array_equal(c.cpu().numpy(), key[order] % n)
+    np.testing.assert_array_equal(p.cpu().numpy(), np.searchsorted(key[order], np.arange(m + 1) * n))
+
+
 def test_coo_large_sort_and_multi_level_scans(hip_backend):
     """17 M entries on a 4096 x 4096 grid (about one duplicate per cell):
     COO -> CSR sorts 8301 tiles (a two-level scan of the digit-count table)

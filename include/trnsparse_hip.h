@@ -415,7 +415,8 @@ int tsp_bsa_bwd(const void* Q, const void* K, const void* V, const void* O,
  * tsp_csr_row_indices (replaces the row expansion of CSRMatrix.to_coo,
  *   formats.py:54-65): rows[k] = row of entry k.
  * tsp_coo_to_csr (replaces COOMatrix.to_csr, formats.py:104-124): entries
- *   sorted by row*n + col (stable), row_ptrs (m+1); workspace:
+ *   sorted by row*n + col (stable), row_ptrs (m+1); nnz < 2^32 (the device
+ *   sort's positions are 32-bit; TSP_EUNSUPPORTED past it); workspace:
  *   tsp_coo_to_csr_workspace_size(nnz, m, n) bytes.
  * ==================================================================== */
 int64_t tsp_format_workspace_size(int64_t rows);
@@ -465,7 +466,7 @@ int tsp_coo_to_csr(const void* values, int dtype, const int64_t* row_indices,
  * sorted by column, so rows ascend within each output row and duplicates
  * keep their input order: the reference's structure and values, bit for
  * bit. out_row_ptrs (n+1,) int64, out_col / out_values (nnz,) (out_col
- * int64 = the original rows). m, n <= 2^32. workspace:
+ * int64 = the original rows). m, n <= 2^32, nnz < 2^32. workspace:
  * tsp_csr_transpose_workspace_size(nnz, m, n, dtype) bytes. */
 int64_t tsp_csr_transpose_workspace_size(int64_t nnz, int64_t m, int64_t n,
                                          int dtype);

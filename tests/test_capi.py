@@ -71,6 +71,9 @@ def test_argument_validation_is_host_side():
     assert lib.tsp_bsr_col_view(None, None, 0, 4, 3, None, None, None, None, None, 0, None) == -1
     assert lib.tsp_bsr_col_view(None, None, 2, 4, 3, None, None, None, None, None, 0, None) == -1
     assert lib.tsp_bsr_col_view_workspace_size(-1, 4) == -1 and lib.tsp_bsr_col_view_workspace_size(10, 4) > 0
+    # the device sort's 32-bit positions: more than 2^32 - 1 entries are refused with a message
+    assert lib.tsp_coo_to_csr_workspace_size(1 << 33, 10, 10) == -1 and b"2^32" in lib.tsp_last_error()
+    assert lib.tsp_csr_transpose(None, 0, None, None, 4, 4, 1 << 33, None, None, None, None, 0, None) == -2
     assert lib.tsp_csr_sum(None, None, None, 1, None, None, None, 1, 0, 2, 4, None, None, None, None, 0, None) == -1
     # CSR SDDMM: bad dtype, bad index type, leading dimension below ncols, null pointers
     assert lib.tsp_csr_sddmm(None, None, 1, 4, 4, 3, None, 8, None, 8, 8, 2, 1.0, None, None) == -2

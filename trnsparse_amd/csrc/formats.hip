@@ -1210,6 +1210,7 @@ int coo_to_csr_keys(const void* values, int dtype, const int64_t* row_indices, c
 
 extern "C" int64_t tsp_coo_to_csr_workspace_size(int64_t nnz, int64_t m, int64_t n) {
   if (nnz < 0 || m < 0 || n < 0) return -1;
+  if (nnz > UINT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_coo_to_csr: more than 2^32 - 1 entries"), -1;
   // sized for the widest value type (fp64), which also covers fp32 / bf16;
   // the two key arrays get 8 bytes an entry whichever key width runs
   const int bits = nnz > 0 ? key_bits(m, n) : 1;
@@ -1223,6 +1224,7 @@ extern "C" int tsp_coo_to_csr(const void* values, int dtype, const int64_t* row_
                               void* workspace, int64_t workspace_bytes, void* stream) {
   if (!dtype_ok(dtype)) return tsp::fail(TSP_EUNSUPPORTED, "tsp_coo_to_csr: dtype %d", dtype);
   if (nnz < 0 || m < 0 || n < 0) return tsp::fail(TSP_EINVAL, "tsp_coo_to_csr: bad size");
+  if (nnz > UINT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_coo_to_csr: more than 2^32 - 1 entries");
   if (m > 0 && n > 0 && m > INT64_MAX / n) return tsp::fail(TSP_EUNSUPPORTED, "tsp_coo_to_csr: m * n overflows");
   if (!row_ptrs) return tsp::fail(TSP_EINVAL, "tsp_coo_to_csr: null pointer");
   hipStream_t st = (hipStream_t)stream;
@@ -1245,6 +1247,7 @@ extern "C" int tsp_coo_to_csr(const void* values, int dtype, const int64_t* row_
 
 extern "C" int64_t tsp_coo_sum_to_csr_workspace_size(int64_t nnz, int64_t m, int64_t n) {
   if (nnz < 0 || m < 0 || n < 0) return -1;
+  if (nnz > UINT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_coo_sum_to_csr: more than 2^32 - 1 entries"), -1;
   const int64_t sort_b = coo_sort_tmp(TSP_F64, nnz, nnz > 0 ? key_bits(m, n) : 1);
   if (sort_b < 0) return -1;
   size_t scan_b = 0;
@@ -1259,6 +1262,7 @@ extern "C" int tsp_coo_sum_to_csr(const void* values, int dtype, const int64_t* 
                                   void* stream) {
   if (!dtype_ok(dtype)) return tsp::fail(TSP_EUNSUPPORTED, "tsp_coo_sum_to_csr: dtype %d", dtype);
   if (nnz < 0 || m < 0 || n < 0) return tsp::fail(TSP_EINVAL, "tsp_coo_sum_to_csr: bad size");
+  if (nnz > UINT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_coo_sum_to_csr: more than 2^32 - 1 entries");
   if (m > 0 && n > 0 && m > INT64_MAX / n) return tsp::fail(TSP_EUNSUPPORTED, "tsp_coo_sum_to_csr: m * n overflows");
   if (!row_ptrs) return tsp::fail(TSP_EINVAL, "tsp_coo_sum_to_csr: null pointer");
   hipStream_t st = (hipStream_t)stream;
@@ -1354,6 +1358,7 @@ int csr_transpose_t(const T* values, const int64_t* col_indices, const int64_t* 
 
 extern "C" int64_t tsp_csr_transpose_workspace_size(int64_t nnz, int64_t m, int64_t n, int dtype) {
   if (nnz < 0 || m < 0 || n < 0 || !dtype_ok(dtype)) return -1;
+  if (nnz > UINT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_transpose: more than 2^32 - 1 entries"), -1;
   const int bits = col_bits(n);
   int64_t tmp, pay;
   if (dtype == TSP_F32) {
@@ -1375,8 +1380,8 @@ extern "C" int tsp_csr_transpose(const void* values, int dtype, const int64_t* c
                                  void* out_values, void* workspace, int64_t workspace_bytes, void* stream) {
   if (!dtype_ok(dtype)) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_transpose: dtype %d", dtype);
   if (nnz < 0 || m < 0 || n < 0 || (m == 0 && nnz > 0)) return tsp::fail(TSP_EINVAL, "tsp_csr_transpose: bad size");
-  if (m > UINT32_MAX || n > (int64_t)UINT32_MAX + 1)
-    return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_transpose: dimensions past 2^32");
+  if (m > UINT32_MAX || n > (int64_t)UINT32_MAX + 1 || nnz > UINT32_MAX)
+    return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_transpose: dimensions or entries past 2^32");
   if (!out_row_ptrs) return tsp::fail(TSP_EINVAL, "tsp_csr_transpose: null pointer");
   hipStream_t st = (hipStream_t)stream;
   if (nnz == 0) return tsp::zero_fill(out_row_ptrs, 8 * (n + 1), st);
@@ -1428,6 +1433,7 @@ __global__ __launch_bounds__(256) void blk_unpack_kernel(const RowVal<uint32_t>*
 
 extern "C" int64_t tsp_bsr_col_view_workspace_size(int64_t nnzb, int64_t n_block_cols) {
   if (nnzb < 0 || n_block_cols < 0) return -1;
+  if (nnzb > UINT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_col_view: more than 2^32 - 1 blocks"), -1;
   size_t tmp = 0;
   if (nnzb > 0 && tsp::rsort::radix_sort_pairs(nullptr, tmp, (const uint32_t*)nullptr, (uint32_t*)nullptr,
                                                (const RowVal<uint32_t>*)nullptr, (RowVal<uint32_t>*)nullptr, nnzb, 0,

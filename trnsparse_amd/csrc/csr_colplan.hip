@@ -261,48 +261,93 @@ __global__ __launch_bounds__(256) void colplan_scatter_kernel(const K* __restric
 }
 
 // One workgroup per epoch: each entry's position in the epoch's (row,
-// column order) order, by a bitonic sort of the E keys row << EBITS | li in
-// LDS. Padding entries take row 2^rbits and sort last. Column-order entry
-// li = (j * W + w) * 64 + l (chunk j of wavefront w, lane l in the SpMV
-// kernel's phase 1) stores pos_slot(its position) in uint16 (w * 64 + l) * K
-// + j: a lane loads the positions of its K entries with one 16-byte load.
+// column order) order, by a stable LSD radix sort in LDS of the E keys
+// row << EBITS | li on the row bits (two 8-bit passes; padding entries take
+// row 2^rbits and sort last). A pass ranks each key among equal digits: the
+// lanes of a wavefront holding the same digit come from 8 ballots, and the
+// counts per (round, wavefront, digit) are prefixed in key order, so equal
+// rows keep their column order. Column-order entry li = (j * W + w) * 64 + l
+// (chunk j of wavefront w, lane l in the SpMV kernel's phase 1) stores
+// pos_slot(its position) in uint16 (w * 64 + l) * K + j: a lane loads the
+// positions of its K entries with one 16-byte load.
 __global__ __launch_bounds__(1024) void colplan_perm_kernel(const uint64_t* __restrict__ ent,
                                                             const int64_t* __restrict__ toff,
                                                             const int64_t* __restrict__ eoff, int64_t T, int rbits,
                                                             int cbits, uint16_t* __restrict__ pinv) {
-  __shared__ uint32_t key[E];
-  const int tid = threadIdx.x;
+  constexpr int NR = E / 1024;  // keys per thread (rounds)
+  __shared__ uint32_t key[2][E];
+  __shared__ uint16_t cnt[NR][16][256];  // per (round, wavefront, digit): count, then start (< E)
+  __shared__ uint32_t dbase[256];
+  __shared__ uint32_t wtot[4];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t ep = blockIdx.x;
   if (ep >= eoff[T]) return;  // the grid covers the epoch count's upper bound
   const int64_t t = upper_bound_i64(eoff, T + 1, ep) - 1;
   const int64_t left = (toff[t + 1] - toff[t]) - ((ep - eoff[t]) << EBITS);
-  const int cnt = left < E ? (int)left : E;
+  const int count = left < E ? (int)left : E;
   const uint64_t* __restrict__ e = ent + (ep << EBITS);
   for (int i = tid; i < E; i += 1024) {
-    const uint32_t row = i < cnt ? (uint32_t)e[entry_slot(i)] >> cbits : (1u << rbits);
-    key[i] = (row << EBITS) | (uint32_t)i;
+    const uint32_t row = i < count ? (uint32_t)e[entry_slot(i)] >> cbits : (1u << rbits);
+    key[0][i] = (row << EBITS) | (uint32_t)i;
   }
-  __syncthreads();
-  for (int k = 2; k <= E; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = tid; i < E; i += 1024) {
-        const int l = i ^ j;
-        if (l > i) {
-          const uint32_t a = key[i], b = key[l];
-          if ((a > b) == ((i & k) == 0)) {
-            key[i] = b;
-            key[l] = a;
-          }
-        }
+  const uint64_t lt = (1ull << lane) - 1;
+#pragma unroll 1
+  for (int pass = 0; pass < 2; ++pass) {  // rows < 2^15: bits EBITS .. EBITS + 15
+    const uint32_t* src = key[pass];
+    uint32_t* dst = key[pass ^ 1];
+    const int shift = EBITS + 8 * pass;
+    for (int i = tid; i < NR * 16 * 256 / 2; i += 1024) ((uint32_t*)&cnt[0][0][0])[i] = 0;
+    __syncthreads();
+    uint32_t kv[NR], dg[NR], rk[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      kv[r] = src[r * 1024 + tid];
+      dg[r] = (kv[r] >> shift) & 255u;
+      uint64_t peers = ~0ull;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const bool bit = (dg[r] >> b) & 1;
+        const uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
       }
-      __syncthreads();
+      rk[r] = (uint32_t)__popcll(peers & lt);
+      if (rk[r] == 0) cnt[r][w][dg[r]] = (uint16_t)__popcll(peers);
     }
+    __syncthreads();
+    // digit tid (< 256): starts of its (round, wavefront) groups, then its start in the epoch
+    uint32_t tot = 0;
+    if (tid < 256)
+#pragma unroll
+      for (int r = 0; r < NR; ++r)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const uint32_t c = cnt[r][v][tid];
+          cnt[r][v][tid] = (uint16_t)tot;
+          tot += c;
+        }
+    uint32_t x = tot;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t y = __shfl_up(x, d, 64);
+      if (lane >= d) x += y;
+    }
+    if (tid < 256 && lane == 63) wtot[w] = x;
+    __syncthreads();
+    if (tid < 256) {
+      uint32_t before = 0;
+      for (int i = 0; i < w; ++i) before += wtot[i];
+      dbase[tid] = before + x - tot;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < NR; ++r) dst[dbase[dg[r]] + cnt[r][w][dg[r]] + rk[r]] = kv[r];
+    __syncthreads();
   }
   uint16_t* __restrict__ out = pinv + (ep << EBITS);
   for (int s = tid; s < E; s += 1024) {
-    const int i = (int)(key[s] & (E - 1));
-    const int c = i >> 6, j = c / SPMV_W, w = c % SPMV_W, l = i & 63;
-    out[(w * 64 + l) * SPMV_K + j] = (uint16_t)pos_slot(s);
+    const int i = (int)(key[0][s] & (E - 1));
+    const int c = i >> 6, j = c / SPMV_W, w2 = c % SPMV_W, l = i & 63;
+    out[(w2 * 64 + l) * SPMV_K + j] = (uint16_t)pos_slot(s);
   }
 }
 

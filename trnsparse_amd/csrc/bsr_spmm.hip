@@ -612,18 +612,36 @@ __global__ __launch_bounds__(256) void bsr_spmm_small(const T* __restrict__ bloc
     f32x4 acc[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) acc[u] = f32x4{};
-    for (int64_t idx = start; idx < end; ++idx) {
+    // one step per stored block; the next block's operands load while this one's MFMAs run
+    // (the last block is loaded again past the end, so the loop has no conditional loads)
+    const int64_t nst = end - start;
+    auto load = [&](int64_t st_, f32x4& a, float (&bv)[4][4]) {
+      const int64_t idx = start + (st_ < nst ? st_ : nst - 1);
       const int64_t kb = ci[idx] * BSZ + 4 * q;
-      const f32x4 a = load4_acc<T>(blocks + idx * (BSZ * BSZ) + l16 * BSZ + 4 * q);
-      float bv[4][4];
+      a = load4_acc<T>(blocks + idx * (BSZ * BSZ) + l16 * BSZ + 4 * q);
 #pragma unroll
       for (int u = 0; u < 4; ++u)
 #pragma unroll
         for (int c = 0; c < 4; ++c) bv[u][c] = bval(kb + c, n0 + 16 * u + l16);
+    };
+    auto mma = [&](const f32x4& a, const float (&bv)[4][4]) {
 #pragma unroll
       for (int c = 0; c < 4; ++c)
 #pragma unroll
         for (int u = 0; u < 4; ++u) acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c], bv[u][c], acc[u], 0, 0, 0);
+    };
+    if (nst > 0) {
+      f32x4 a0, a1;
+      float b0[4][4], b1[4][4];
+      load(0, a0, b0);
+      int64_t st_ = 0;
+      for (; st_ + 1 < nst; st_ += 2) {
+        load(st_ + 1, a1, b1);
+        mma(a0, b0);
+        load(st_ + 2, a0, b0);
+        mma(a1, b1);
+      }
+      if (st_ < nst) mma(a0, b0);
     }
     // element r of subtile u: row 4q + r, column 16u + l16
 #pragma unroll

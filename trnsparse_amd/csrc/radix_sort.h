@@ -43,6 +43,7 @@ constexpr int sort_ipt() {
   return sizeof(K) + sizeof(V) <= 8 ? 16 : 8;
 }
 constexpr int RADIX = 256;
+static_assert(NT == RADIX, "the sort kernels give each thread one digit's table entry");
 
 inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 

@@ -192,6 +192,33 @@ def test_colplan_auto_mode_builds_on_reuse(hip_backend):
         D.set_spmv_plan(prev)
 
 
+def test_colplan_auto_mode_regathers_reused_values_only(hip_backend):
+    """Under "auto", new values on a planned pattern run the windowed kernel
+    once; the plan takes them (one regather) when they come back, and
+    values that change on every call never pay the regather."""
+    prev = D.get_spmv_plan()
+    D.set_spmv_plan("auto")
+    try:
+        m = n = 1 << 15
+        v, c, p, rng = _random(m, n, np.full(m, 12), 10)
+        A = W.csr_matrix_from_arrays(v, c, p, (m, n), device="cuda")
+        x = rng.standard_normal(n).astype(np.float32)
+        xd = torch.from_numpy(x).cuda()
+        ts.spmv(A, xd)
+        ts.spmv(A, xd)                                   # plan built on reuse
+        key0 = A._hip_colplan[1]
+        for _ in range(2):                               # new values every call
+            v = rng.standard_normal(len(v)).astype(np.float32)
+            A.values.copy_(torch.from_numpy(v))
+            _check(v, c, p, (m, n), x, ts.spmv(A, xd).cpu().numpy())
+            assert A._hip_colplan[1] == key0             # not regathered
+        _check(v, c, p, (m, n), x, ts.spmv(A, xd).cpu().numpy())  # the same values again
+        assert A._hip_colplan[1] != key0                 # regathered once
+        _check(v, c, p, (m, n), x, ts.spmv(A, xd).cpu().numpy())
+    finally:
+        D.set_spmv_plan(prev)
+
+
 @pytest.mark.parametrize("dist", ["poisson", "zipf"])
 @pytest.mark.parametrize("index_dtype", [np.int64, np.int32])
 def test_colplan_cfg2_full_size(plan_always, dist, index_dtype):

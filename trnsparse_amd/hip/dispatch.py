@@ -363,6 +363,15 @@ def _csr_colplan(A, vals, cols, ptrs, dev, rows_per_block_log2: int = 0, tiles_h
     if cached is not None and cached[0] == skey:
         _, ckey, geom, plan, uses = cached
         if ckey != vkey:
+            # New values on the cached pattern: regathering them into the plan
+            # costs about three plan SpMVs, more than one windowed SpMV, so under
+            # "auto" they are regathered only when the same values come back.
+            if mode == "auto" and getattr(A, "_hip_colplan_pending", None) != vkey:
+                try:
+                    A._hip_colplan_pending = vkey
+                except AttributeError:
+                    pass
+                return None
             _lib.call("tsp_csr_colplan_refresh", vals.data_ptr(), _lib.TSP_F32, m, n, nnz, geom.ctypes.data,
                       plan.data_ptr(), _lib.stream_handle(dev))
         A._hip_colplan = (skey, vkey, geom, plan, uses + 1)

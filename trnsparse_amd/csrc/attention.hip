@@ -27,9 +27,9 @@
 //   bsa_fwd_f32_mfma<D>   fp32, 128-blocks, D in {64, 128, 256}: the same
 //       work split on v_mfma_f32_32x32x2_f32 with K/V streamed through an
 //       LDS ring.
-// head_dim 256 keeps the whole score product in one workgroup (64 k-steps
-// of 16 bf16 / 128 of 2 fp32 per 32-key tile) with one workgroup per CU;
-// other head_dims are padded with zero columns by the caller.
+// head_dim 256 keeps the whole score product in one workgroup (16 k-steps
+// of 16 bf16 / 128 of 2 fp32 per 32-key tile); other head_dims are padded
+// with zero columns by the caller.
 //   bsa_fwd_generic<T>    fp32/fp64/bf16, any block size and head_dim: one
 //       thread per (query, 32-wide slice of head_dim), online softmax in
 //       the accumulation type (double for fp64).
@@ -291,10 +291,11 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_bf16_mfma(
 // queries, S^T = K Q^T with the wave's Q rows in registers, online softmax in
 // the exp2 domain, O^T += V^T P^T with P from registers), restructured so the
 // key blocks stream while the MFMAs run:
-//   * keys are consumed in 64-key halves that go through a 2-stage LDS ring
-//     (K half + V half per stage: 128 KiB per workgroup at D = 256, 64 KiB
-//     at D = 128, 32 KiB at D = 64), filled by direct global->LDS buffer loads issued one half
-//     ahead; rows at or past seq_len read as zero;
+//   * keys are consumed in stages of HK keys (64 at D <= 128, 32 at D = 256)
+//     that go through a 2-stage LDS ring (K part + V part per stage: 64 KiB
+//     per workgroup at D = 128 and 256, 32 KiB at D = 64), filled by direct
+//     global->LDS buffer loads issued one stage ahead; rows at or past
+//     seq_len read as zero;
 //   * V stays [key][d] in LDS and the A operand of O^T += V^T P^T (8 keys of
 //     one d column per lane) comes from ds_read_b64_tr_b16;
 //   * 16-byte chunks are XOR-swizzled for conflict-free reads on the 64-bank
@@ -302,7 +303,6 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_bf16_mfma(
 //     transpose reads of 4 consecutive keys);
 //   * each MFMA's LDS operand is read one step ahead.
 namespace att {
-constexpr int HK = 64;                 // keys per ring stage
 constexpr int NST = 2;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -315,6 +315,9 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 // chunk ^ 4 ((key / 2) % 2).
 template <int D>
 struct Geo {
+  static constexpr int HK = D > 128 ? 32 : 64; // keys per ring stage
+  static constexpr int NT = HK / 32;           // 32-key S^T tiles per stage
+  static constexpr int SPB = AB / HK;          // stages per key block
   static constexpr int ROWB = D * 2;           // bytes per K/V row
   static constexpr int HBYTES = HK * ROWB;     // bytes per K (or V) half
   static constexpr int STAGE = 2 * HBYTES;
@@ -339,16 +342,20 @@ __device__ inline float halves_sum(float v) {
 }  // namespace att
 
 // D = 64 fits three wavefronts per SIMD (136 registers, 32 KiB of LDS per
-// workgroup); D = 256 holds 128 KiB of ring and 64 + 128 registers of Q and O
-// per lane, one workgroup per CU
+// workgroup). D = 256 takes 32-key stages so that two workgroups fit per CU
+// (64 KiB of ring each): its 64 + 128 registers of Q and O per lane leave
+// room for one 32-key score tile, and the loop body stays within the 256
+// registers of two wavefronts per SIMD (a few values live across the loop
+// are spilled outside it). Per stage that is 32 MFMAs, as at D = 128.
 template <int D>
-__global__ __launch_bounds__(256, D == 64 ? 3 : (D == 128 ? 2 : 1)) void bsa_fwd_bf16_stream(
+__global__ __launch_bounds__(256, D == 64 ? 3 : 2) void bsa_fwd_bf16_stream(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int64_t S,
     int64_t head_stride, int64_t H, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci, int64_t Mt,
     float scale_log2, uint16_t* __restrict__ O, float* __restrict__ rmax, float* __restrict__ rden) {
   using namespace att;
   typedef Geo<D> G;
   constexpr int ROWB = G::ROWB, HBYTES = G::HBYTES, STAGE = G::STAGE, KS = G::KS, NU = G::NU;
+  constexpr int HK = G::HK, NT = G::NT, SPB = G::SPB;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
 
   // XCD-aware order: XCD x walks heads x, x+8, ...; the block rows of one
@@ -382,7 +389,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : (D == 128 ? 2 : 1)) void bsa_fwd
 
   const int64_t start = rp[m];
   const int nblk = (int)(rp[m + 1] - start);
-  const int nsteps = 2 * nblk;
+  const int nsteps = SPB * nblk;
   const tsp::dma::i32x4 krs = tsp::dma::make_rsrc(Kh, (uint32_t)(S * D * 2));
   const tsp::dma::i32x4 vrs = tsp::dma::make_rsrc(Vh, (uint32_t)(S * D * 2));
   const uint32_t lds0 = tsp::dma::lds_addr(lds);
@@ -401,16 +408,16 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : (D == 128 ? 2 : 1)) void bsa_fwd
     }
     return __builtin_amdgcn_readlane(cv, blk - cbase);
   };
-  auto first_key = [&](int s) { return (int64_t)colblk(s >> 1) * AB + HK * (s & 1); };
+  auto first_key = [&](int s) { return (int64_t)colblk(s / SPB) * AB + HK * (s % SPB); };
 
-  // ---- loads of half s into stage s % NST: per wave HBYTES / 4 KiB K and V instructions
+  // ---- loads of stage s into ring slot s % NST: per wave HBYTES / 4 KiB K and V instructions
   auto issue = [&](int s) {
     const int64_t key0 = first_key(s);
     const uint32_t st = lds0 + (s % NST) * STAGE;
     constexpr int NI = HBYTES / 4096;
 #pragma unroll
     for (int qq = 0; qq < NI; ++qq) {
-      const int j = NI * w + qq;                // rows [RPI j, RPI j + RPI) of the half
+      const int j = NI * w + qq;                // rows [RPI j, RPI j + RPI) of the stage
       const int rr = G::RPI * j + lane / G::LPR;
       const int p = lane % G::LPR;              // this lane's 16-byte slot in the row
       const int64_t rowoff = (key0 + rr) * ROWB;
@@ -442,38 +449,34 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : (D == 128 ? 2 : 1)) void bsa_fwd
     };
     // ---- S^T tiles (keys 32*tt + 8*(v/4) + 4h + v%4, query l32): two
     // independent accumulator chains, operands read one k-step ahead
-    f32x16 sc[2];
-    bf16x8 ka[2][2];
-    ka[0][0] = kread(0, 0);
-    ka[0][1] = kread(0, 1);
+    f32x16 sc[NT];
+    bf16x8 ka[2][NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) ka[0][tt] = kread(0, tt);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       if (ks + 1 < KS) {
-        ka[(ks + 1) & 1][0] = kread(ks + 1, 0);
-        ka[(ks + 1) & 1][1] = kread(ks + 1, 1);
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) ka[(ks + 1) & 1][tt] = kread(ks + 1, tt);
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (ks == 0) {
-        sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[0][0], qf[0], f32x16{}, 0, 0, 0);
-        sc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[0][1], qf[0], f32x16{}, 0, 0, 0);
-      } else {
-        sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[ks & 1][0], qf[ks], sc[0], 0, 0, 0);
-        sc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[ks & 1][1], qf[ks], sc[1], 0, 0, 0);
-      }
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt)
+        sc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[ks & 1][tt], qf[ks], ks == 0 ? f32x16{} : sc[tt], 0, 0, 0);
     }
     // ---- online softmax in the log2 domain (scale_log2 > 0, so the max of
     // the raw scores scales to the max of the scaled ones); keys at or past
     // seq_len (only in a block that crosses it) are excluded
     if (key0 + HK > S) {
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
+      for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
         for (int v = 0; v < 16; ++v)
           if (key0 + 32 * tt + 8 * (v >> 2) + 4 * h + (v & 3) >= S) sc[tt][v] = -INFINITY;
     }
     float mraw = sc[0][0];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+    for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) mraw = fmaxf(mraw, sc[tt][v]);
     mraw = att::halves_max(mraw);
@@ -492,9 +495,9 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : (D == 128 ? 2 : 1)) void bsa_fwd
     }
     const float nmx = mref == -INFINITY ? 0.f : -mref;  // -inf scores give p = 0 either way
     float lsum = 0.f;
-    bf16x8 pb[2][2];
+    bf16x8 pb[NT][2];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
+    for (int tt = 0; tt < NT; ++tt) {
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
         typedef float f32x8 __attribute__((ext_vector_type(8)));
@@ -526,9 +529,9 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : (D == 128 ? 2 : 1)) void bsa_fwd
     bf16x8 vb[2];
     vb[0] = vread(0, 0, 0);
 #pragma unroll
-    for (int step = 0; step < 4 * NU; ++step) {
+    for (int step = 0; step < 2 * NT * NU; ++step) {
       const int tt = step / (2 * NU), a = (step / NU) % 2, u = step % NU;
-      if (step + 1 < 4 * NU) {
+      if (step + 1 < 2 * NT * NU) {
         const int s1 = step + 1;
         vb[s1 & 1] = vread(s1 / (2 * NU), (s1 / NU) % 2, s1 % NU);
       }
@@ -540,7 +543,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : (D == 128 ? 2 : 1)) void bsa_fwd
   if (nsteps > 0) issue(0);
   for (int s = 0; s < nsteps; ++s) {
     const int64_t key0 = first_key(s);
-    tsp::dma::wait_vm<0>();  // this wave's loads of half s are done
+    tsp::dma::wait_vm<0>();  // this wave's loads of stage s are done
     tsp::dma::barrier();     // every wave's part is in LDS; stage (s+1) % NST is free
     if (s + 1 < nsteps) issue(s + 1);
     compute(lds + (s % NST) * STAGE, key0);

@@ -9,10 +9,10 @@ measure per gradient element: |g - g_exact| / g_abs, with g_abs the oracle's
 absolute form (|dS| replaced by P (|dO V^T| + |D|), operands by their
 magnitudes). fp32 <= 1e-4, bf16 <= 2e-2, fp64 <= 1e-10. fp32 with b = 128
 and d in {64, 128, 256} runs the fp32 MFMA kernels (16-row tiles at
-d = 256), bf16 with d = 128 the bf16 MFMA kernels, bf16 with d = 64 or 256
-the fp32 MFMA kernels on widened operands, other d below 256 zero-padded to
-64, 128 or 256 first; everything else (fp64, d > 256, other block sizes)
-the generic kernels.
+d = 256), bf16 with d <= 128 the bf16 MFMA kernels of d = 128 (d below 128
+zero-padded to 128), bf16 with d = 256 the fp32 MFMA kernels on widened
+operands, other d below 256 zero-padded to 64, 128 or 256 first;
+everything else (fp64, d > 256, other block sizes) the generic kernels.
 """
 
 from __future__ import annotations
@@ -78,9 +78,10 @@ def _check_head(Q, K, V, dO, O, grads, mask_bsr, scale, tol, rows=None, cols=Non
         (512, 128, global_mask(4, 1, 1), torch.bfloat16),
         (300, 128, local_mask(3, 2), torch.bfloat16),     # MFMA, last key block crosses S
         (1024, 128, global_mask(8, 1, 1), torch.bfloat16),  # MFMA, global column split into 2 segments
-        (256, 64, local_mask(2, 1), torch.bfloat16),      # bf16 d = 64: widened onto the fp32 MFMA kernels
+        (256, 64, local_mask(2, 1), torch.bfloat16),      # bf16 d = 64: zero-padded to 128, bf16 MFMA kernels
         (640, 64, W.cfg5_block_mask(5), torch.bfloat16),
-        (256, 32, local_mask(2, 1), torch.bfloat16),      # head_dim zero-padded to 64
+        (256, 32, local_mask(2, 1), torch.bfloat16),      # head_dim zero-padded to 128
+        (300, 96, local_mask(3, 1), torch.bfloat16),      # zero-padded to 128, last key block crosses S
         (256, 100, global_mask(2, 0, 1), torch.float32),  # head_dim zero-padded to 128
         (256, 160, local_mask(2, 1), torch.bfloat16),     # head_dim zero-padded to 256, widened
         (256, 320, local_mask(2, 1), torch.bfloat16),     # generic bf16

@@ -675,11 +675,14 @@ def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, 
     Q/K/V/O/dO (S, D) or (..., S, D) sharing one mask; row_max / row_denom
     as hip_block_sparse_attention returns them. Returns (dQ, dK, dV).
 
-    bf16 with 128-blocks and head_dim 64 or 256 runs on the fp32 MFMA
-    kernels: the operands are widened on the device (exact) and the gradients
-    rounded to bf16 once at the end; the bf16 MFMA kernels serve head_dim
-    128. Other head_dims below 256 are zero-padded to 64, 128 or 256 first,
-    as in the forward.
+    bf16 with 128-blocks: head_dims below 128 are zero-padded to 128 and
+    run the bf16 MFMA kernels of head_dim 128 (zero columns change neither
+    the scores nor the other gradient columns, and those kernels run at
+    several times the rate of the fp32 ones on widened operands); head_dim
+    256 runs on the fp32 MFMA kernels, its operands widened on the device
+    (exact) and the gradients rounded to bf16 once at the end. Other
+    head_dims below 256 are zero-padded to 64, 128 or 256 first, as in the
+    forward.
     """
     if not (Q.shape == K.shape == V.shape == O.shape == dO.shape):
         raise RuntimeError("Q, K, V, O, dO shapes differ")
@@ -687,12 +690,16 @@ def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, 
         grads = hip_block_sparse_attention_backward(*(t.float() for t in (Q, K, V, O, dO)), mask_bsr, scale,
                                                     row_max, row_denom)
         return tuple(gr.half() for gr in grads)
+    if Q.dtype == torch.bfloat16 and 0 < Q.shape[-1] < 128 and mask_bsr.block_size == 128 and scale > 0:
+        grads = hip_block_sparse_attention_backward(*(_pad_head_dim(t, 128) for t in (Q, K, V, O, dO)), mask_bsr,
+                                                    scale, row_max, row_denom)
+        return tuple(gr[..., : Q.shape[-1]].contiguous() for gr in grads)
     dp = _mfma_head_dim(Q, mask_bsr.block_size)
     if dp is not None and scale > 0:
         grads = hip_block_sparse_attention_backward(*(_pad_head_dim(t, dp) for t in (Q, K, V, O, dO)), mask_bsr, scale,
                                                     row_max, row_denom)
         return tuple(gr[..., : Q.shape[-1]].contiguous() for gr in grads)
-    if Q.dtype == torch.bfloat16 and Q.shape[-1] in (64, 256) and mask_bsr.block_size == 128 and scale > 0:
+    if Q.dtype == torch.bfloat16 and Q.shape[-1] == 256 and mask_bsr.block_size == 128 and scale > 0:
         grads = hip_block_sparse_attention_backward(*(t.float() for t in (Q, K, V, O, dO)), mask_bsr, scale,
                                                     row_max, row_denom)
         return tuple(gr.to(torch.bfloat16) for gr in grads)

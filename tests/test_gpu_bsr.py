@@ -98,6 +98,9 @@ def test_shapes(hip_backend, shape, b, N, density):
         ((150, 301), 32, 5, 0.8),     # narrow N
         ((320, 200), 64, 200, 0.3),   # ragged n inside a block column
         ((128, 2048), 64, 64, 0.9),   # long block rows (32 blocks)
+        ((200, 150), 16, 512, 0.5),   # 8 column tiles, 13 block rows
+        ((330, 260), 32, 1000, 0.4),  # 16 column tiles, the last partial
+        ((256, 512), 64, 512, 0.3),
     ],
 )
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

@@ -123,9 +123,12 @@ def test_backward_empty_rows_and_ragged(hip_backend, dtype, D):
     _check_head(Q, K, V, dO, O, (dQ, dK, dV), mask_bsr, 0.1, TOL[dtype])
 
 
-def test_backward_batched_heads_bf16(hip_backend):
+@pytest.mark.parametrize("D", [128, 64])
+def test_backward_batched_heads_bf16(hip_backend, D):
+    """Leading (batch, head) dims; at D = 64 the operands are zero-padded to
+    128 and the gradients cut back to 64 columns."""
     torch.manual_seed(12)
-    S, D = 512, 128
+    S = 512
     mask_bsr = W.bsr_from_block_mask(global_mask(4, 1, 1), 128)
     Q, K, V, dO = (torch.randn(2, 2, S, D).to(torch.bfloat16) for _ in range(4))
     O, dQ, dK, dV = _run(Q, K, V, dO, mask_bsr)

@@ -11,13 +11,17 @@
 // second pass.
 //
 // N = 1 is HBM-bound (2 flops per 4-byte block element): no MFMA. The fast
-// kernel (block size 128) gives one wavefront an 8-row slice of a block
-// row: per stored block it reads the slice's 8 x 128 elements as one
-// contiguous 4 KiB run with 16-byte loads (lane l always covers the same
-// 16 bytes of a block row, so its x piece is one 16-byte load per block),
-// accumulates a partial per row and reduces each row over the lanes that
-// share it at the end. Slices of heavy block rows are dispatched first.
-// Other block sizes use a thread-per-row kernel.
+// kernel (block size 128) gives one workgroup an 8-row slice of a block
+// row and its 4 wavefronts every 4th stored block of the row each: per
+// block a wavefront reads the slice's 8 x 128 elements as one contiguous
+// 4 KiB run with 16-byte loads (lane l always covers the same 16 bytes of a
+// block row, so its x piece is one 16-byte load per block), accumulates a
+// partial per row and reduces each row over the lanes that share it; the
+// 4 wavefronts' row sums are then added in wavefront order through LDS.
+// Splitting a block row's blocks over 4 wavefronts keeps the longest rows
+// from setting the kernel's length (cfg3's rows hold 8 to 20 blocks).
+// Slices of heavy block rows are dispatched first. Other block sizes use a
+// thread-per-row kernel.
 #include "common.h"
 
 namespace {
@@ -46,16 +50,17 @@ __device__ inline void finish(int64_t r, typename SAcc<T>::type ax, typename SAc
   out[r] = from_a<T>(y);
 }
 
-// Fast kernel: wavefront per (block row, 8-row slice); 4 wavefronts per
-// workgroup. V elements per 16-byte load; LPR = SB / V lanes share a row,
-// RPI = 64 / LPR rows per load instruction, NI = SLICE / RPI loads per block.
+// Fast kernel: workgroup per (block row, 8-row slice), wavefront w takes the
+// row's stored blocks w, w + 4, ... V elements per 16-byte load; LPR = SB / V
+// lanes share a row, RPI = 64 / LPR rows per load instruction, NI = SLICE /
+// RPI loads per block.
 template <typename T>
 __global__ __launch_bounds__(256) void bsr_spmv_b128(const T* __restrict__ blocks, const int64_t* __restrict__ rp,
                                                      const int64_t* __restrict__ ci, int64_t mb, int64_t m, int64_t n,
                                                      const T* __restrict__ x, typename SAcc<T>::type alpha,
                                                      const T* __restrict__ u, typename SAcc<T>::type beta,
                                                      const T* __restrict__ v, typename SAcc<T>::type gamma,
-                                                     const T* __restrict__ w, typename SAcc<T>::type delta,
+                                                     const T* __restrict__ w_vec, typename SAcc<T>::type delta,
                                                      T* __restrict__ out, const int32_t* __restrict__ order) {
   typedef typename SAcc<T>::type AccT;
   constexpr int V = 16 / sizeof(T);
@@ -63,8 +68,10 @@ __global__ __launch_bounds__(256) void bsr_spmv_b128(const T* __restrict__ block
   constexpr int RPI = 64 / LPR;
   constexpr int NI = SLICE / RPI;
   constexpr int NSL = SB / SLICE;  // slices per block row
-  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  __shared__ typename SAcc<T>::type part[4][SLICE];
+  const int64_t unit = blockIdx.x;
   if (unit >= mb * NSL) return;
+  const int w = threadIdx.x >> 6;
   const int64_t i = order ? order[unit / NSL] : unit / NSL;
   const int sl = (int)(unit % NSL);
   const int lane = threadIdx.x & 63;
@@ -81,12 +88,13 @@ __global__ __launch_bounds__(256) void bsr_spmv_b128(const T* __restrict__ block
   for (int64_t base = s; base < e; base += 64) {
     const int cnt = (int)(e - base < 64 ? e - base : 64);
     const int myc = lane < cnt ? (int)ci[base + lane] : 0;
-    for (int kk = 0; kk < cnt; kk += UNR) {
+    for (int k0 = w; k0 < cnt; k0 += 4 * UNR) {
       Vec<T, V> xv[UNR], a[UNR][NI];
 #pragma unroll
       for (int j = 0; j < UNR; ++j) {
-        if (kk + j < cnt) {
-          const int64_t c0 = (int64_t)__builtin_amdgcn_readlane(myc, kk + j) * SB + cl * V;
+        const int kk = k0 + 4 * j;
+        if (kk < cnt) {
+          const int64_t c0 = (int64_t)__builtin_amdgcn_readlane(myc, kk) * SB + cl * V;
           // x piece (zero past n: the reference pads B's rows)
           if (c0 + V <= n) {
             xv[j] = *(const Vec<T, V>*)(x + c0);
@@ -94,14 +102,14 @@ __global__ __launch_bounds__(256) void bsr_spmv_b128(const T* __restrict__ block
 #pragma unroll
             for (int t = 0; t < V; ++t) xv[j].e[t] = c0 + t < n ? x[c0 + t] : T(0);
           }
-          const T* blk = blocks + (base + kk + j) * SB * SB + r0 * SB;
+          const T* blk = blocks + (base + kk) * SB * SB + r0 * SB;
 #pragma unroll
           for (int q = 0; q < NI; ++q) a[j][q] = *(const Vec<T, V>*)(blk + (q * 64 + lane) * V);
         }
       }
 #pragma unroll
       for (int j = 0; j < UNR; ++j) {
-        if (kk + j < cnt) {
+        if (k0 + 4 * j < cnt) {
 #pragma unroll
           for (int q = 0; q < NI; ++q)
 #pragma unroll
@@ -110,14 +118,21 @@ __global__ __launch_bounds__(256) void bsr_spmv_b128(const T* __restrict__ block
       }
     }
   }
-  // row (r0 + q * RPI + rl): sum over its LPR lanes
+  // row (r0 + q * RPI + rl): sum over its LPR lanes, then over the 4
+  // wavefronts in wavefront order
 #pragma unroll
   for (int q = 0; q < NI; ++q) {
     AccT t = acc[q];
 #pragma unroll
     for (int o = LPR / 2; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
-    const int64_t r = i * SB + r0 + q * RPI + rl;
-    if (cl == 0 && r < m) finish<T>(r, t, alpha, u, beta, v, gamma, w, delta, out);
+    if (cl == 0) part[w][q * RPI + rl] = t;
+  }
+  __syncthreads();
+  if (threadIdx.x < SLICE) {
+    const int rr = threadIdx.x;
+    const AccT t = ((part[0][rr] + part[1][rr]) + part[2][rr]) + part[3][rr];
+    const int64_t r = i * SB + r0 + rr;
+    if (r < m) finish<T>(r, t, alpha, u, beta, v, gamma, w_vec, delta, out);
   }
 }
 
@@ -151,8 +166,7 @@ int launch(const void* blocks, const int64_t* rp, const int64_t* ci, int64_t b, 
   const int64_t mb = tsp::ceil_div(m, b);
   const bool aligned = ((uintptr_t)blocks % 16) == 0 && ((uintptr_t)x % 16) == 0;
   if (b == SB && aligned) {
-    const int64_t units = mb * (SB / SLICE);
-    const int64_t g = tsp::ceil_div(units, 4);
+    const int64_t g = mb * (SB / SLICE);  // one workgroup per (block row, slice)
     if (g > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmv: too many block rows");
     hipLaunchKernelGGL(bsr_spmv_b128<T>, dim3((unsigned)g), dim3(256), 0, st, (const T*)blocks, rp, ci, mb, m, n,
                        (const T*)x, (AccT)alpha, (const T*)u, (AccT)beta, (const T*)v, (AccT)gamma, (const T*)w,

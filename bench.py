@@ -97,6 +97,57 @@ def time_gpu(fn, steps: int, warmup: int, flush=None, prewarm_s: float = 0.25):
     return wall, times[len(times) // 2]
 
 
+def time_gpu_spread(fn, steps: int, warmup: int, segments: int = 5, prewarm_s: float = 0.25):
+    """Per-launch event times of `segments` back-to-back timed segments of
+    `steps` launches each (same pre-warm and warmup as time_gpu), as
+    (median, min, max) in ms: the spread of a line across segments of one
+    run, next to its median."""
+    import torch
+
+    if prewarm_s > 0:
+        prewarm(fn, prewarm_s)
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    seg = []
+    for _ in range(segments):
+        s, e = _events()
+        s.record()
+        for _ in range(steps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        seg.append(s.elapsed_time(e) / steps)
+    seg.sort()
+    return seg[len(seg) // 2], seg[0], seg[-1]
+
+
+def host_cpu() -> dict:
+    """The GPU box's host CPU as the CPU baselines see it: model name,
+    sockets (distinct physical ids), logical CPUs in the machine and in this
+    process's affinity mask, and the thread count the baselines use."""
+    from oracle import cpu_baseline as cb
+
+    model, phys = None, set()
+    try:
+        for ln in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+            k, _, v = ln.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "model name" and model is None:
+                model = v
+            elif k == "physical id":
+                phys.add(v)
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    return {"model": model, "sockets": len(phys) or None, "logical_cpus": os.cpu_count(),
+            "affinity_cpus": affinity, "baseline_threads": cb.threads(),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
 def make_flush():
     """Read 1 GiB to evict L2 and the 256 MiB MALL between timed reps.
 
@@ -203,7 +254,9 @@ def bench_bsr_small(steps: int, warmup: int):
     return out
 
 
-def bench_bsr_bf16(steps: int, warmup: int):
+def bench_bsr_bf16(steps: int, warmup: int, cpu: bool = False):
+    """bsr_spmm at config 3b: bf16 A and B, fp32 accumulation and output.
+    `us` is the median of 5 timed segments, `us_spread` their min and max."""
     import torch
 
     import trnsparse_amd as ts
@@ -213,17 +266,35 @@ def bench_bsr_bf16(steps: int, warmup: int):
     flops = 2.0 * A.n_blocks * 128 * 128 * B.shape[1]
     Ad = ts.BSRMatrix(A.blocks.cuda(), A.block_col_indices, A.block_row_ptrs, A.shape, A.block_size)
     Bd = B.cuda()
-    _, ev_ms = time_gpu(lambda: ts.bsr_spmm(Ad, Bd, out_dtype=torch.float32), steps, warmup)
+    ev_ms, lo, hi = time_gpu_spread(lambda: ts.bsr_spmm(Ad, Bd, out_dtype=torch.float32), steps, warmup)
     tf = flops / (ev_ms * 1e-3) / 1e12
     byts = A.n_blocks * 128 * 128 * 2 + B.numel() * 2 + B.numel() * 4
-    return {
+    res = {
         "name": "bsr_spmm cfg3b bf16->fp32",
         "value": round(tf * 1e3, 1),
         "unit": "GFLOP/s",
         "us": round(ev_ms * 1e3, 1),
+        "us_spread": [round(lo * 1e3, 1), round(hi * 1e3, 1)],
         "frac_bf16_mfma": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
         "frac_hbm_min_bytes": round(byts / (ev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
     }
+    if cpu:
+        from oracle import cpu_baseline as cb
+
+        nthr = cb.threads()
+        torch.set_num_threads(nthr)
+        secs, reps = cb.time_call(lambda: cb.bsr_spmm(A.blocks, A.block_col_indices, A.block_row_ptrs, A.shape, 128, B),
+                                  reps=5, budget_s=20.0)
+        res["cpu_baseline"] = {
+            "value": round(flops / secs / 1e9, 2),
+            "unit": "GFLOP/s",
+            "cores": nthr,
+            "kind": "port",
+            "sample": "full cfg3b (1638 blocks, N=512) through the reference's torch loop in the input dtype "
+            f"(bf16 blocks and B, one torch bf16 matmul per stored block, `+=` into a bf16 output, ops.py:162-192), "
+            f"median of {reps} reps after a warmup, torch threads = {nthr}",
+        }
+    return res
 
 
 def bench_bsr_backward(steps: int, warmup: int):
@@ -260,10 +331,10 @@ def bench_bsr_backward(steps: int, warmup: int):
                                    crow.data_ptr(), 128, 128, m, n, G.data_ptr(), N, N, dB.data_ptr(), N,
                                    corder.data_ptr(), st)
         for name, fn in ((f"bsr_spmm backward dA (sddmm) {cfg}", sddmm), (f"bsr_spmm backward dB (A^T dC) {cfg}", spmm_t)):
-            _, ms = time_gpu(fn, steps, warmup)
+            ms, lo, hi = time_gpu_spread(fn, steps, warmup)
             tf = flops / (ms * 1e-3) / 1e12
             out.append({"name": name, "value": round(tf * 1e3, 1), "unit": "GFLOP/s", "us": round(ms * 1e3, 1),
-                        key: round(tf / peak, 4)})
+                        "us_spread": [round(lo * 1e3, 1), round(hi * 1e3, 1)], key: round(tf / peak, 4)})
     return out
 
 
@@ -538,13 +609,14 @@ def bench_attention(steps: int, warmup: int, cpu: bool = False):
     flops = 4.0 * mask.n_blocks * 128 * 128 * D * H
     byts = 4 * H * S * D * 2
     Qd, Kd, Vd = Q.cuda(), K.cuda(), V.cuda()
-    _, ev_ms = time_gpu(lambda: ts.block_sparse_attention_tiled(Qd, Kd, Vd, mask), steps, warmup)
+    ev_ms, lo, hi = time_gpu_spread(lambda: ts.block_sparse_attention_tiled(Qd, Kd, Vd, mask), steps, warmup)
     tf = flops / (ev_ms * 1e-3) / 1e12
     res = {
         "name": "block_sparse_attention cfg5 32x8192x128 bf16",
         "value": round(tf * 1e3, 1),
         "unit": "GFLOP/s",
         "us": round(ev_ms * 1e3, 1),
+        "us_spread": [round(lo * 1e3, 1), round(hi * 1e3, 1)],
         "frac_bf16_mfma": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
         "frac_hbm_min_bytes": round(byts / (ev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
     }
@@ -644,13 +716,13 @@ def bench_attention_backward(steps: int, warmup: int, cpu: bool = False):
                                  code, H, S, D, rp.data_ptr(), ci.data_ptr(), cp.data_ptr(), crow.data_ptr(), nbc, 128,
                                  D**-0.5, rm.data_ptr(), rd.data_ptr(), dQ.data_ptr(), dK.data_ptr(), dV.data_ptr(),
                                  plan.data_ptr(), ni, ns, npart, ws.data_ptr(), st)
-        _, ms = time_gpu(call, steps, warmup)
+        ms, lo, hi = time_gpu_spread(call, steps, warmup)
         tf = flops / (ms * 1e-3) / 1e12
         peak, key, tag = ((BF16_MFMA_PEAK_TFLOPS, "frac_bf16_mfma", "bf16") if dt == torch.bfloat16 else
                           (FP32_MFMA_PEAK_TFLOPS, "frac_fp32_mfma", "fp32"))
         out.append({"name": f"block_sparse_attention backward cfg5 32x8192x128 {tag}", "value": round(tf * 1e3, 1),
-                    "unit": "GFLOP/s", "us": round(ms * 1e3, 1), key: round(tf / peak, 4),
-                    "split_columns": ns, "items": ni})
+                    "unit": "GFLOP/s", "us": round(ms * 1e3, 1), "us_spread": [round(lo * 1e3, 1), round(hi * 1e3, 1)],
+                    key: round(tf / peak, 4), "split_columns": ns, "items": ni})
         if dt == torch.bfloat16:
             keep = (Qd, Kd, Vd, O, dO, rm, rd)
     res = out[0]
@@ -869,7 +941,7 @@ def main(argv=None) -> int:
             ("spmv bucketed poisson int64", lambda: bench_spmv("poisson", 64, 20, 3, plan="bucketed")),
             ("spmv bucketed zipf int64", lambda: bench_spmv("zipf", 64, 10, 2, plan="bucketed")),
             ("spmm", lambda: bench_spmm(10, 2)),
-            ("bsr bf16", lambda: bench_bsr_bf16(max(5, args.steps // 2), 3)),
+            ("bsr bf16", lambda: bench_bsr_bf16(max(5, args.steps // 2), 3, cpu=not args.no_cpu)),
             ("bsr f64", lambda: bench_bsr_f64(10, 2)),
             ("bsr small", lambda: bench_bsr_small(10, 2)),
             ("bsr backward", lambda: bench_bsr_backward(10, 2)),
@@ -919,6 +991,7 @@ def main(argv=None) -> int:
         },
         "roofline": head["roofline"],
         "cpu_baseline": head.get("cpu_baseline"),
+        "host_cpu": host_cpu(),
         "secondary": secondary,
         "timing": "HIP events on the launch stream; untimed 0.25 s clock pre-warm of the same op, then the W warmup steps",
     }

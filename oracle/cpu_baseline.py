@@ -28,7 +28,12 @@ import torch
 
 
 def threads() -> int:
-    n = os.cpu_count() or 1
+    """Threads the CPU baselines run on: the CPUs this process may use (its
+    affinity mask, else the machine's count), capped by OMP_NUM_THREADS."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
     env = os.environ.get("OMP_NUM_THREADS")
     if env and env.isdigit():
         n = min(n, int(env))

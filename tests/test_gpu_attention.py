@@ -206,10 +206,11 @@ def test_cfg5_full_size_sampled(hip_backend):
 
 
 def test_cfg5_full_size_every_row(hip_backend):
-    """Whole-output checks at full size, every (head, row): V = 1 gives O = 1
-    on every row (all of cfg5's block rows hold blocks), and the saved
-    row_max / row_denom of all 32 heads match a float64 pass over the stored
-    blocks' scores on the CPU."""
+    """Whole-output check at full size, every (head, row, column): O of all
+    32 heads against a float64 P.V over each block row's stored blocks on
+    the CPU (bf16 bar, relative to P.|V|), the saved row_max / row_denom of
+    all heads against the same pass, and V = 1 giving O = 1 on every row
+    (all of cfg5's block rows hold blocks)."""
     from trnsparse_amd.hip.dispatch import hip_block_sparse_attention
 
     Q, K, V, mask_bsr = W.cfg5_attention()
@@ -218,21 +219,32 @@ def test_cfg5_full_size_every_row(hip_backend):
     ones = torch.ones_like(V).cuda()
     O1 = ts.block_sparse_attention_tiled(Q.cuda(), K.cuda(), ones, mask_bsr)
     assert (O1.float() - 1.0).abs().max().item() <= TOL_BF16
-    _, rm, rd = hip_block_sparse_attention(Q.cuda(), K.cuda(), V.cuda(), mask_bsr, scale, return_stats=True)
+    del O1, ones
+    O, rm, rd = hip_block_sparse_attention(Q.cuda(), K.cuda(), V.cuda(), mask_bsr, scale, return_stats=True)
+    O = O.double().cpu()
     rm = rm.double().cpu().reshape(H, S)
     rd = rd.double().cpu().reshape(H, S)
     ptr, col = mask_bsr.block_row_ptrs.tolist(), mask_bsr.block_col_indices.tolist()
-    q64, k64 = Q.double(), K.double()
-    torch.set_num_threads(max(1, torch.get_num_threads()))
+    q64, k64, v64 = Q.double(), K.double(), V.double()
+    worst = 0.0
     for i in range(S // 128):
         cols = col[ptr[i]:ptr[i + 1]]
         keys = torch.cat([k64[:, c * 128:(c + 1) * 128] for c in cols], dim=1)   # (H, nb*128, D)
+        vals = torch.cat([v64[:, c * 128:(c + 1) * 128] for c in cols], dim=1)   # (H, nb*128, D)
         s = scale * torch.bmm(q64[:, i * 128:(i + 1) * 128], keys.transpose(1, 2).contiguous())
         mx = s.max(dim=2).values
-        den = torch.exp(s - mx[..., None]).sum(dim=2)
+        e = torch.exp(s - mx[..., None])
+        den = e.sum(dim=2)
         sl = slice(i * 128, (i + 1) * 128)
         assert (rm[:, sl] - mx).abs().max().item() <= 1e-4 * (1.0 + mx.abs().max().item()), i
         assert ((rd[:, sl] - den).abs() / den).max().item() <= 1e-4, i
+        P = e / den[..., None]
+        exact = torch.bmm(P, vals)                     # (H, 128, D)
+        bound = torch.bmm(P, vals.abs()).clamp_min(1e-30)
+        err = ((O[:, sl] - exact).abs() / bound).max().item()
+        worst = max(worst, err)
+        assert err <= TOL_BF16, (i, err)
+    assert worst > 0.0  # the check compared real values
 
 
 def test_fp16_widened(hip_backend):

@@ -182,8 +182,8 @@ def test_backward_deterministic(hip_backend, dtype):
 
 
 def test_cfg5_backward_full_size(hip_backend):
-    """cfg5 (32 heads, S 8192, d 128, 370 mask blocks): sampled block rows of
-    dQ and block columns of dK / dV against the oracle, and the identity
+    """cfg5 (32 heads, S 8192, d 128, 370 mask blocks): on every head, sampled
+    block rows of dQ and block columns of dK / dV against the oracle, and the identity
     sum_k dV[k] = sum over queries of non-empty block rows of dO[q] (each
     softmax row sums to one) on every head."""
     Q, K, V, mask_bsr = W.cfg5_attention()
@@ -193,7 +193,7 @@ def test_cfg5_backward_full_size(hip_backend):
     rows, cols = [0, 1, 5, 63], [0, 2, 40, 63]
     sel_q = np.concatenate([np.arange(r * 128, (r + 1) * 128) for r in rows])
     sel_k = np.concatenate([np.arange(c * 128, (c + 1) * 128) for c in cols])
-    for hh in (0, 31):
+    for hh in range(Q.shape[0]):  # all 32 heads
         _check_head(Q[hh], K[hh], V[hh], dO[hh], O[hh], (dQ[hh], dK[hh], dV[hh]), mask_bsr, 128**-0.5,
                     TOL[torch.bfloat16], rows=rows, cols=cols, sel_q=sel_q, sel_k=sel_k)
     live = np.repeat(np.diff(ptr)[: 8192 // 128] > 0, 128)
@@ -206,7 +206,8 @@ def test_cfg5_backward_full_size(hip_backend):
 
 def test_cfg5_backward_full_size_f32(hip_backend):
     """cfg5's shapes and mask with fp32 Q, K, V, dO (the fp32 MFMA kernels):
-    sampled block rows of dQ and block columns of dK / dV against the oracle."""
+    on every head, sampled block rows of dQ and block columns of dK / dV
+    against the oracle."""
     Q, K, V, mask_bsr = W.cfg5_attention()
     Q, K, V = Q.float(), K.float(), V.float()
     dO = torch.randn(Q.shape, generator=torch.Generator().manual_seed(14))
@@ -214,6 +215,6 @@ def test_cfg5_backward_full_size_f32(hip_backend):
     rows, cols = [0, 1, 5, 63], [0, 1, 2, 40, 63]
     sel_q = np.concatenate([np.arange(r * 128, (r + 1) * 128) for r in rows])
     sel_k = np.concatenate([np.arange(c * 128, (c + 1) * 128) for c in cols])
-    for hh in (0, 31):
+    for hh in range(Q.shape[0]):  # all 32 heads
         _check_head(Q[hh], K[hh], V[hh], dO[hh], O[hh], (dQ[hh], dK[hh], dV[hh]), mask_bsr, 128**-0.5,
                     TOL[torch.float32], rows=rows, cols=cols, sel_q=sel_q, sel_k=sel_k)

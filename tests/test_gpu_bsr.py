@@ -201,6 +201,34 @@ def test_dtype_mismatch_raises(hip_backend):
         ts.bsr_spmm(bsr, torch.randn(64, 8).cuda())
 
 
+def _f64_pass(A: ts.BSRMatrix, B: torch.Tensor):
+    """(exact, scale) = (A @ B, |A| @ |B|) over every block row in float64
+    on the CPU: per block row, its stored blocks side by side times the
+    matching B row panels stacked (torch float64 matmuls, independent of
+    the numpy oracle's loop)."""
+    b = A.block_size
+    blocks = A.blocks.double()
+    B64 = B.double()
+    ptr, col = A.block_row_ptrs.tolist(), A.block_col_indices.tolist()
+    m = A.shape[0]
+    exact = torch.zeros(m, B.shape[1], dtype=torch.float64)
+    scale = torch.zeros(m, B.shape[1], dtype=torch.float64)
+    for i in range(len(ptr) - 1):
+        k0, k1 = ptr[i], ptr[i + 1]
+        if k0 == k1:
+            continue
+        arow = blocks[k0:k1].permute(1, 0, 2).reshape(b, (k1 - k0) * b)          # [A_i,c0 | A_i,c1 | ...]
+        panels = torch.cat([B64[c * b:(c + 1) * b] for c in col[k0:k1]], dim=0)  # [B_c0; B_c1; ...]
+        r1 = min(m, (i + 1) * b)
+        exact[i * b:r1] = (arow @ panels)[: r1 - i * b]
+        scale[i * b:r1] = (arow.abs() @ panels.abs())[: r1 - i * b]
+    return exact, scale
+
+
+def _whole_output_error(got: torch.Tensor, exact: torch.Tensor, scale: torch.Tensor) -> float:
+    return ((got.double().cpu() - exact).abs() / scale.clamp_min(1e-30)).max().item()
+
+
 def test_cfg1_plumbing(hip_backend):
     A, B, Ad = W.cfg1_bsr_plumbing()
     assert A.n_blocks == 24
@@ -210,10 +238,14 @@ def test_cfg1_plumbing(hip_backend):
 
 
 def test_cfg3_fp32_full_size(hip_backend):
-    """16384^2, 10% block density, N=512: every 16th block row vs the oracle,
-    plus the full-size checksum property sum(C) = colsum(A) . rowsum(B)."""
+    """16384^2, 10% block density, N=512: every element of C against a
+    float64 pass over all 128 block rows, plus 16 block rows against the
+    numpy oracle and the full-size checksum property
+    sum(C) = colsum(A) . rowsum(B)."""
     A, B = W.cfg3_bsr()
     C = ts.bsr_spmm(A, B.cuda())
+    exact64, scale64 = _f64_pass(A, B)
+    assert _whole_output_error(C, exact64, scale64) <= TOL_F32
     rows = list(range(0, 128, 16)) + [1, 126, 127]
     exact, scale = _oracle(A, B, rows=rows)
     got = torch.cat([C[r * 128 : (r + 1) * 128] for r in rows]).cpu().numpy()
@@ -260,6 +292,10 @@ def test_cfg3b_bf16_full_size(hip_backend):
     A, B = W.cfg3_bsr(dtype=torch.bfloat16)
     C = ts.bsr_spmm(A, B.cuda(), out_dtype=torch.float32)
     assert C.dtype == torch.float32 and C.shape == (16384, 512)
+    # every element against a float64 pass over the exact bf16 values: fp32
+    # accumulation of exact bf16 products holds the fp32 bar
+    exact64, scale64 = _f64_pass(A, B)
+    assert _whole_output_error(C, exact64, scale64) <= TOL_F32
     rows = list(range(3, 128, 16)) + [0, 127]
     exact, scale = _oracle(A, B, rows=rows)
     got = torch.cat([C[r * 128 : (r + 1) * 128] for r in rows]).cpu().numpy()

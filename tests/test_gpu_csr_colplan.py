@@ -187,7 +187,13 @@ def test_colplan_auto_mode_builds_on_reuse(hip_backend):
         second = ts.spmv(A, xd)
         assert getattr(A, "_hip_colplan", None) is not None  # reused unchanged: plan built
         _check(v, c, p, (m, n), xd.cpu().numpy(), second.cpu().numpy())
+        # the two kernels add a row's products in different orders: the first
+        # two auto-mode calls agree to tolerance, not bit for bit; from the
+        # second call on the plan runs and repeats exactly
         torch.testing.assert_close(first, second, rtol=1e-5, atol=1e-4)
+        assert torch.equal(ts.spmv(A, xd), second)
+        D.set_spmv_plan("never")
+        assert torch.equal(ts.spmv(A, xd), first)  # "never": always the windowed kernel, bit-stable
     finally:
         D.set_spmv_plan(prev)
 

@@ -187,6 +187,13 @@ def test_cfg4_full_size(hip_backend):
     got = ts.screened_spmm(A.cuda(), diag.cuda(), B.cuda(), threshold=thr).cpu()
     rows = np.r_[0:128, 1000:1040, 2048:2176, 3968:4096]
     _check(A, diag, B, thr, got, rows=rows)
+    # every row: (A*mask) @ B and its |.| scale in float64 on the CPU, the
+    # mask from the oracle's rule
+    Am = A.double() * torch.from_numpy(ref.screened_mask(diag.numpy(), thr))
+    exact = Am @ B.double()
+    scale = Am.abs() @ B.double().abs()
+    assert ((got.double() - exact).abs() / scale.clamp_min(1e-30)).max().item() <= TOL
+    del Am, exact, scale
     # linearity at full size: C @ 1 = (A*mask) @ (B @ 1)
     ones = torch.ones(B.shape[1], 1, dtype=torch.float64)
     lhs = got.double() @ ones

@@ -118,3 +118,79 @@ def test_ops_match_api_compile_and_graph(hip_backend):
         graph.replay()
         torch.cuda.synchronize()
         torch.testing.assert_close(static_C, ts.bsr_spmm(bsr, newB), rtol=0, atol=0)
+
+
+@pytest.mark.gpu
+def test_ops_reject_mismatched_arguments(hip_backend):
+    """Every operator checks its tensors against the sizes and dtypes it
+    passes to the kernels: a mismatched call raises before any launch."""
+    import trnsparse_amd as ts
+    from trnsparse_amd.hip import dispatch as D
+
+    ops = _lib.ops()
+    dev = torch.device("cuda")
+    i64 = dict(dtype=torch.int64, device=dev)
+    # BSR: a 256 x 256 matrix in 128-blocks, three stored blocks
+    rp = torch.tensor([0, 2, 3], **i64)
+    ci = torch.tensor([0, 1, 1], **i64)
+    blocks = torch.randn(3, 128, 128, device=dev)
+    B = torch.randn(256, 16, device=dev)
+    ops.bsr_spmm(blocks, rp, ci, None, 256, 256, 128, B, torch.float32)  # the well-formed call runs
+    bad_bsr = [
+        lambda: ops.bsr_spmm(blocks, rp, ci, None, 256, 256, 128, B[:200], torch.float32),  # B shorter than n
+        lambda: ops.bsr_spmm(blocks, rp, ci, None, 384, 256, 128, B, torch.float32),  # row_ptrs vs m
+        lambda: ops.bsr_spmm(blocks, rp, ci[:2], None, 256, 256, 128, B, torch.float32),  # indices vs blocks
+        lambda: ops.bsr_spmm(blocks, rp, ci, None, 256, 256, 64, B, torch.float32),  # block size vs blocks
+        lambda: ops.bsr_spmm(blocks.double(), rp, ci, None, 256, 256, 128, B, torch.float32),  # dtypes differ
+        lambda: ops.bsr_spmm(blocks, rp.int(), ci, None, 256, 256, 128, B, torch.float32),  # int32 pointers
+        lambda: ops.bsr_spmm(blocks, rp, ci, torch.zeros(1, dtype=torch.int32, device=dev), 256, 256, 128, B,
+                             torch.float32),  # row order of the wrong length
+        lambda: ops.bsr_sddmm(B, B[:, :8].contiguous(), torch.zeros(3, **i64), ci, 256, 256, 128),  # N differs
+        lambda: ops.bsr_spmm_t(blocks, torch.zeros(2, **i64), ci, ci, torch.empty(0, dtype=torch.int32, device=dev),
+                               256, 256, 128, B),  # col_ptrs vs n
+    ]
+    # CSR: 10 x 20, 30 entries
+    g = torch.Generator().manual_seed(0)
+    dense = torch.randn(10, 20, generator=g) * (torch.rand(10, 20, generator=g) < 0.15)
+    A = ts.CSRMatrix.from_dense(dense)
+    vals, cols, ptrs, win = D._csr_device(A, dev)
+    x = torch.randn(20, device=dev)
+    ops.csr_spmv(vals, cols, ptrs, win, 10, 20, x, 1.0, None, 0.0)
+    X = torch.randn(20, 4, device=dev)
+    bad_csr = [
+        lambda: ops.csr_spmv(vals.double(), cols, ptrs, win, 10, 20, x, 1.0, None, 0.0),  # fp64 values, fp32 x
+        lambda: ops.csr_spmv(vals, cols, ptrs, win, 10, 20, x[:15], 1.0, None, 0.0),  # x shorter than n
+        lambda: ops.csr_spmv(vals, cols, ptrs, win, 10, 20, x, 1.0, torch.ones(7, device=dev), 1.0),  # y vs m
+        lambda: ops.csr_spmv(vals, cols.int(), ptrs, win, 10, 20, x, 1.0, None, 0.0),  # index widths differ
+        lambda: ops.csr_spmv(vals, cols, ptrs, win, 12, 20, x, 1.0, None, 0.0),  # row_ptrs vs m
+        lambda: ops.csr_spmm(vals, cols, ptrs, 10, 20, X[:12], 1.0, None, 0.0),  # X rows vs n
+        lambda: ops.csr_spmm(vals, cols, ptrs, 10, 20, X, 1.0, torch.ones(10, 3, device=dev), 1.0),  # Y shape
+    ]
+    # screened: A must be square, diag and B must match it
+    As = torch.randn(64, 64, device=dev)
+    diag = torch.rand(64, device=dev)
+    Bs = torch.randn(64, 8, device=dev)
+    ops.screened_spmm(As, diag, Bs, 1e-3)
+    bad_scr = [
+        lambda: ops.screened_spmm(As[:, :32].contiguous(), diag, Bs, 1e-3),
+        lambda: ops.screened_spmm(As, diag[:32], Bs, 1e-3),
+        lambda: ops.screened_spmm(As, diag, Bs[:32], 1e-3),
+        lambda: ops.screened_spmm_backward(As[:32].contiguous(), diag, Bs, 1e-3, Bs, True, True),
+        lambda: ops.screened_spmm_backward(As, diag, Bs, 1e-3, Bs[:, :4].contiguous(), True, True),
+    ]
+    # attention: one shape and dtype for Q, K, V
+    Q = torch.randn(2, 256, 64, device=dev)
+    bad_attn = [
+        lambda: ops.bsa_fwd(Q, Q.double(), Q, rp, ci, 128, 0.125, False),
+        lambda: ops.bsa_fwd(Q, Q, Q, rp[:2], ci, 128, 0.125, False),
+        lambda: ops.bsa_bwd(Q, Q, Q, Q, Q[:1], rp, ci, rp, ci, 2, 128, 0.125, torch.zeros(2, 256, device=dev),
+                            torch.ones(2, 256, device=dev), torch.zeros(4, dtype=torch.int32, device=dev), 0, 0, 0),
+        lambda: ops.bsa_bwd(Q, Q, Q, Q, Q, rp, ci, rp, ci, 2, 128, 0.125, torch.zeros(2, 100, device=dev),
+                            torch.ones(2, 256, device=dev), torch.zeros(4, dtype=torch.int32, device=dev), 0, 0, 0),
+        lambda: ops.bsa_bwd(Q, Q, Q, Q, Q, rp, ci, rp, ci, 2, 128, 0.125, torch.zeros(2, 256, device=dev),
+                            torch.ones(2, 256, device=dev), torch.zeros(4, dtype=torch.int32, device=dev), 5, 0, 0),
+    ]
+    for i, call in enumerate(bad_bsr + bad_csr + bad_scr + bad_attn):
+        with pytest.raises(RuntimeError):
+            call()
+    torch.cuda.synchronize()

@@ -46,13 +46,15 @@ def _run(name, A, diag, B, thr, with_ws):
     return C.cpu()
 
 
+@pytest.mark.parametrize("diag_dtype", [torch.float32, torch.float64])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
-def test_noalloc_matches_workspace_entry_point(dtype):
+def test_noalloc_matches_workspace_entry_point(dtype, diag_dtype):
     thr = 1e-6
     # two calls in a row, the second smaller: the scratch keeps the first
     # call's Q values past the second call's rows, which must not leak in
+    # (an fp64 diag stores 8-byte Q entries in the scratch, a smaller row limit)
     for n, ncols, seed in ((1000, 96, 1), (300, 40, 2)):
-        A, diag, B = _case(n, ncols, seed, dtype)
+        A, diag, B = _case(n, ncols, seed, dtype, diag_dtype)
         got = _run("noalloc", A, diag, B, thr, with_ws=False)
         want = _run("ws", A, diag, B, thr, with_ws=True)
         assert torch.equal(got, want)

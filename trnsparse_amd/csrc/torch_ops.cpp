@@ -18,6 +18,7 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include <algorithm>
 #include <string>
 #include <tuple>
 
@@ -57,6 +58,39 @@ void need(const at::Tensor& t, const at::Tensor& like, const char* name) {
 
 const void* opt_ptr(const c10::optional<at::Tensor>& t) { return t.has_value() ? t->data_ptr() : nullptr; }
 
+// The operators are public (C++ callers and torch.ops users reach them
+// without the Python layer), and the kernels trust every size they are
+// given: each operator checks that its tensors match the sizes, dtypes and
+// index widths it passes on, so a mismatched call raises here instead of
+// launching a kernel that reads or writes past a buffer.
+void need_dtype(const at::Tensor& t, at::ScalarType dt, const char* op, const char* name) {
+  TORCH_CHECK(t.scalar_type() == dt, op, ": ", name, " has dtype ", t.scalar_type(), ", expected ", dt);
+}
+
+void need_numel(const at::Tensor& t, int64_t n, const char* op, const char* name) {
+  TORCH_CHECK(t.numel() == n, op, ": ", name, " has ", t.numel(), " elements, expected ", n);
+}
+
+void need_2d(const at::Tensor& t, int64_t rows, int64_t cols, const char* op, const char* name) {
+  TORCH_CHECK(t.dim() == 2 && t.size(0) == rows && t.size(1) == cols, op, ": ", name, " has shape ", t.sizes(),
+              ", expected [", rows, ", ", cols, "]");
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// A BSR pattern of an m x n matrix in b x b blocks: int64 row pointers over
+// the block rows, int64 column indices and (nnzb, b, b) blocks.
+void need_bsr(const at::Tensor& blocks, const at::Tensor& rp, const at::Tensor& ci, int64_t m, int64_t n,
+              int64_t b, const char* op) {
+  TORCH_CHECK(m >= 0 && n >= 0 && b > 0, op, ": bad sizes m=", m, " n=", n, " block_size=", b);
+  need_dtype(rp, at::kLong, op, "block_row_ptrs");
+  need_dtype(ci, at::kLong, op, "block_col_indices");
+  need_numel(rp, cdiv(m, b) + 1, op, "block_row_ptrs");
+  TORCH_CHECK(blocks.dim() == 3 && blocks.size(1) == b && blocks.size(2) == b, op, ": blocks has shape ",
+              blocks.sizes(), ", expected [nnzb, ", b, ", ", b, "]");
+  need_numel(ci, blocks.size(0), op, "block_col_indices");
+}
+
 // ------------------------------------------------------------------- BSR
 
 at::Tensor bsr_spmm(const at::Tensor& blocks, const at::Tensor& rp, const at::Tensor& ci,
@@ -65,6 +99,17 @@ at::Tensor bsr_spmm(const at::Tensor& blocks, const at::Tensor& rp, const at::Te
   for (auto* p : {&rp, &ci}) need(*p, B, "pattern");
   need(blocks, B, "blocks");
   TORCH_CHECK(B.dim() == 2 && B.stride(1) == 1, "bsr_spmm: B must be 2-D with unit column stride");
+  need_bsr(blocks, rp, ci, m, n, block_size, "bsr_spmm");
+  need_dtype(blocks, B.scalar_type(), "bsr_spmm", "blocks (the dtype of B)");
+  TORCH_CHECK(B.size(0) >= n, "bsr_spmm: B has ", B.size(0), " rows, expected at least n = ", n);
+  TORCH_CHECK(B.stride(0) >= B.size(1), "bsr_spmm: B's row stride ", B.stride(0), " is below its ", B.size(1),
+              " columns");
+  if (row_order.has_value() && row_order->numel()) {
+    need(*row_order, B, "row_order");
+    need_dtype(*row_order, at::kInt, "bsr_spmm", "row_order");
+    TORCH_CHECK(row_order->numel() >= cdiv(m, block_size), "bsr_spmm: row_order has ", row_order->numel(),
+                " entries for ", cdiv(m, block_size), " block rows");
+  }
   const int64_t ncols = B.size(1);
   auto C = at::empty({m, ncols}, B.options().dtype(out_dtype));
   const int32_t* order = row_order.has_value() && row_order->numel() ? row_order->data_ptr<int32_t>() : nullptr;
@@ -87,6 +132,14 @@ at::Tensor bsr_sddmm(const at::Tensor& G, const at::Tensor& B, const at::Tensor&
   need(B, G, "B");
   need(block_rows, G, "block_rows");
   need(block_col_indices, G, "block_col_indices");
+  TORCH_CHECK(m >= 0 && n >= 0 && block_size > 0, "bsr_sddmm: bad sizes");
+  TORCH_CHECK(G.dim() == 2 && G.size(0) == m, "bsr_sddmm: grad_out has shape ", G.sizes(), ", expected [", m,
+              ", N]");
+  need_2d(B, n, G.size(1), "bsr_sddmm", "B");
+  need_dtype(B, G.scalar_type(), "bsr_sddmm", "B (the dtype of grad_out)");
+  need_dtype(block_rows, at::kLong, "bsr_sddmm", "block_rows");
+  need_dtype(block_col_indices, at::kLong, "bsr_sddmm", "block_col_indices");
+  need_numel(block_rows, block_col_indices.numel(), "bsr_sddmm", "block_rows");
   const int64_t nnzb = block_col_indices.numel(), ncols = G.size(1);
   auto out = at::empty({nnzb, block_size, block_size}, G.options());
   check(tsp_bsr_sddmm(G.data_ptr(), ncols, m, B.data_ptr(), ncols, n, ncols, block_rows.data_ptr<int64_t>(),
@@ -105,6 +158,21 @@ at::Tensor bsr_spmm_t(const at::Tensor& blocks, const at::Tensor& cp, const at::
                       const at::Tensor& col_order, int64_t m, int64_t n, int64_t block_size, const at::Tensor& G) {
   for (auto* p : {&blocks, &cp, &cbid, &crow, &col_order}) need(*p, G, "pattern");
   need(G, G, "dC");
+  TORCH_CHECK(m >= 0 && n >= 0 && block_size > 0, "bsr_spmm_t: bad sizes");
+  TORCH_CHECK(G.dim() == 2 && G.size(0) == m, "bsr_spmm_t: grad_out has shape ", G.sizes(), ", expected [", m,
+              ", N]");
+  TORCH_CHECK(blocks.dim() == 3 && blocks.size(1) == block_size && blocks.size(2) == block_size,
+              "bsr_spmm_t: blocks has shape ", blocks.sizes());
+  need_dtype(blocks, G.scalar_type(), "bsr_spmm_t", "blocks (the dtype of grad_out)");
+  for (auto* p : {&cp, &cbid, &crow}) need_dtype(*p, at::kLong, "bsr_spmm_t", "column view");
+  need_numel(cp, cdiv(n, block_size) + 1, "bsr_spmm_t", "col_ptrs");
+  need_numel(cbid, blocks.size(0), "bsr_spmm_t", "col_block_ids");
+  need_numel(crow, blocks.size(0), "bsr_spmm_t", "col_block_rows");
+  if (col_order.numel()) {
+    need_dtype(col_order, at::kInt, "bsr_spmm_t", "col_order");
+    TORCH_CHECK(col_order.numel() >= cdiv(n, block_size), "bsr_spmm_t: col_order has ", col_order.numel(),
+                " entries for ", cdiv(n, block_size), " block columns");
+  }
   const int64_t ncols = G.size(1), nbc = cp.numel() - 1;
   auto out = at::empty({n, ncols}, G.options());
   check(tsp_bsr_spmm_t(blocks.data_ptr(), dtype_code(blocks.scalar_type()), cp.data_ptr<int64_t>(),
@@ -122,12 +190,33 @@ at::Tensor bsr_spmm_t_meta(const at::Tensor&, const at::Tensor&, const at::Tenso
 
 // ------------------------------------------------------------------- CSR
 
+// A CSR matrix of m rows and n columns whose values share the dense
+// operand's dtype, with one index dtype for both index arrays.
+void need_csr(const at::Tensor& values, const at::Tensor& cols, const at::Tensor& ptrs, int64_t m, int64_t n,
+              const at::Tensor& dense, const char* op) {
+  TORCH_CHECK(m >= 0 && n >= 0, op, ": bad sizes m=", m, " n=", n);
+  need_dtype(values, dense.scalar_type(), op, "values (the dtype of the dense operand)");
+  index_code(cols.scalar_type());
+  need_dtype(ptrs, cols.scalar_type(), op, "row_ptrs (the dtype of col_indices)");
+  need_numel(ptrs, m + 1, op, "row_ptrs");
+  need_numel(cols, values.numel(), op, "col_indices");
+}
+
 at::Tensor csr_spmv(const at::Tensor& values, const at::Tensor& cols, const at::Tensor& ptrs,
                     const at::Tensor& windows, int64_t m, int64_t n, const at::Tensor& x, double alpha,
                     const c10::optional<at::Tensor>& y, double beta) {
   for (auto* p : {&values, &cols, &ptrs, &windows}) need(*p, x, "matrix");
   need(x, x, "x");
   if (y.has_value()) need(*y, x, "y");
+  need_csr(values, cols, ptrs, m, n, x, "csr_spmv");
+  need_numel(x, n, "csr_spmv", "x");
+  if (y.has_value()) {
+    need_dtype(*y, x.scalar_type(), "csr_spmv", "y (the dtype of x)");
+    need_numel(*y, m, "csr_spmv", "y");
+  }
+  need_dtype(windows, at::kLong, "csr_spmv", "windows");
+  TORCH_CHECK(windows.numel() >= tsp_csr_plan_size(m, values.numel()), "csr_spmv: windows has ", windows.numel(),
+              " entries, tsp_csr_plan_size gives ", tsp_csr_plan_size(m, values.numel()));
   auto out = at::empty({m}, x.options());
   check(tsp_csr_spmv(values.data_ptr(), dtype_code(values.scalar_type()), cols.data_ptr(), ptrs.data_ptr(),
                      index_code(cols.scalar_type()), m, n, values.numel(), windows.data_ptr<int64_t>(), x.data_ptr(),
@@ -150,6 +239,14 @@ at::Tensor csr_colplan_spmv(const at::Tensor& plan, const at::Tensor& geometry, 
                   geometry.is_contiguous(),
               "csr_colplan_spmv: geometry must be the 10 int64 host values of tsp_csr_colplan_geometry");
   const int64_t* geom = geometry.data_ptr<int64_t>();
+  need_dtype(x, at::kFloat, "csr_colplan_spmv", "x");
+  need_numel(x, n, "csr_colplan_spmv", "x");
+  if (y.has_value()) {
+    need_dtype(*y, at::kFloat, "csr_colplan_spmv", "y");
+    need_numel(*y, m, "csr_colplan_spmv", "y");
+  }
+  TORCH_CHECK(plan.nbytes() >= (size_t)geom[6], "csr_colplan_spmv: plan holds ", plan.nbytes(),
+              " bytes, the geometry needs ", geom[6]);
   auto out = at::empty({m}, x.options());
   at::Tensor work;
   if (geom[8] > 0) work = at::empty({geom[8]}, x.options().dtype(at::kByte));
@@ -170,7 +267,13 @@ at::Tensor csr_spmm(const at::Tensor& values, const at::Tensor& cols, const at::
   for (auto* p : {&values, &cols, &ptrs}) need(*p, X, "matrix");
   need(X, X, "X");
   if (Y.has_value()) need(*Y, X, "Y");
+  need_csr(values, cols, ptrs, m, n, X, "csr_spmm");
+  TORCH_CHECK(X.dim() == 2 && X.size(0) == n, "csr_spmm: X has shape ", X.sizes(), ", expected [", n, ", N]");
   const int64_t ncols = X.size(1);
+  if (Y.has_value()) {
+    need_dtype(*Y, X.scalar_type(), "csr_spmm", "Y (the dtype of X)");
+    need_2d(*Y, m, ncols, "csr_spmm", "Y");
+  }
   auto out = at::empty({m, ncols}, X.options());
   check(tsp_csr_spmm(values.data_ptr(), dtype_code(values.scalar_type()), cols.data_ptr(), ptrs.data_ptr(),
                      index_code(cols.scalar_type()), m, n, values.numel(), X.data_ptr(), ncols, ncols, alpha,
@@ -196,7 +299,13 @@ at::Tensor screened_spmm(const at::Tensor& A, const at::Tensor& diag, const at::
   need(A, B, "A");
   need(diag, B, "diag_integrals");
   need(B, B, "B");
-  const int64_t m = A.size(0), ncols = B.size(1);
+  TORCH_CHECK(A.dim() == 2 && A.size(0) == A.size(1), "screened_spmm: A has shape ", A.sizes(), ", expected square");
+  const int64_t m = A.size(0);
+  TORCH_CHECK(B.dim() == 2 && B.size(0) == m, "screened_spmm: B has shape ", B.sizes(), ", expected [", m, ", N]");
+  need_dtype(A, B.scalar_type(), "screened_spmm", "A (the dtype of B)");
+  TORCH_CHECK(diag.dim() == 1, "screened_spmm: diag_integrals must be 1-D");
+  need_numel(diag, m, "screened_spmm", "diag_integrals");
+  const int64_t ncols = B.size(1);
   auto C = at::empty({m, ncols}, B.options());
   auto ws = screened_workspace(diag, m);
   check(tsp_screened_spmm(A.data_ptr(), dtype_code(A.scalar_type()), A.size(1), diag.data_ptr(),
@@ -217,7 +326,17 @@ std::tuple<at::Tensor, at::Tensor> screened_spmm_backward(const at::Tensor& A, c
   need(diag, dC, "diag_integrals");
   need(B, dC, "B");
   need(dC, dC, "grad_out");
-  const int64_t m = A.size(0), ncols = dC.size(1);
+  TORCH_CHECK(A.dim() == 2 && A.size(0) == A.size(1), "screened_spmm_backward: A has shape ", A.sizes(),
+              ", expected square");
+  const int64_t m = A.size(0);
+  TORCH_CHECK(dC.dim() == 2 && dC.size(0) == m, "screened_spmm_backward: grad_out has shape ", dC.sizes(),
+              ", expected [", m, ", N]");
+  need_2d(B, m, dC.size(1), "screened_spmm_backward", "B");
+  need_dtype(A, dC.scalar_type(), "screened_spmm_backward", "A (the dtype of grad_out)");
+  need_dtype(B, dC.scalar_type(), "screened_spmm_backward", "B (the dtype of grad_out)");
+  TORCH_CHECK(diag.dim() == 1, "screened_spmm_backward: diag_integrals must be 1-D");
+  need_numel(diag, m, "screened_spmm_backward", "diag_integrals");
+  const int64_t ncols = dC.size(1);
   // a gradient that is not asked for comes back empty (no kernel runs for it)
   auto dA = need_a ? at::empty({m, m}, A.options()) : at::empty({0}, A.options());
   auto dB = need_b ? at::empty({m, ncols}, B.options()) : at::empty({0}, B.options());
@@ -249,7 +368,13 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> bsa_fwd(const at::Tensor& Q, cons
   need(Q, Q, "Q");
   TORCH_CHECK(Q.dim() == 3 && K.sizes() == Q.sizes() && V.sizes() == Q.sizes(),
               "bsa_fwd: Q, K, V must be (heads, seq, head_dim) of one shape");
+  TORCH_CHECK(block_size > 0, "bsa_fwd: block_size must be positive");
+  for (auto* p : {&K, &V}) need_dtype(*p, Q.scalar_type(), "bsa_fwd", "K and V (the dtype of Q)");
   const int64_t H = Q.size(0), S = Q.size(1), D = Q.size(2), Mt = S / block_size;
+  need_dtype(rp, at::kLong, "bsa_fwd", "block_row_ptrs");
+  need_dtype(ci, at::kLong, "bsa_fwd", "block_col_indices");
+  TORCH_CHECK(rp.numel() >= Mt + 1, "bsa_fwd: block_row_ptrs has ", rp.numel(), " entries, expected at least ",
+              Mt + 1);
   auto O = at::empty_like(Q);
   at::Tensor rmax, rden;
   if (return_stats) {
@@ -283,7 +408,28 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> bsa_bwd(
   for (auto* p : {&K, &V, &O, &dO, &rp, &ci, &cp, &crow, &row_max, &row_denom, &plan}) need(*p, Q, "operand");
   need(Q, Q, "Q");
   TORCH_CHECK(Q.dim() == 3, "bsa_bwd: operands must be (heads, seq, head_dim)");
-  const int64_t H = Q.size(0), S = Q.size(1), D = Q.size(2);
+  TORCH_CHECK(block_size > 0, "bsa_bwd: block_size must be positive");
+  for (auto* p : {&K, &V, &O, &dO}) {
+    TORCH_CHECK(p->sizes() == Q.sizes(), "bsa_bwd: K, V, O and grad_out must have Q's shape ", Q.sizes());
+    need_dtype(*p, Q.scalar_type(), "bsa_bwd", "K, V, O and grad_out (the dtype of Q)");
+  }
+  const int64_t H = Q.size(0), S = Q.size(1), D = Q.size(2), Mt = S / block_size;
+  for (auto* p : {&rp, &ci, &cp, &crow}) need_dtype(*p, at::kLong, "bsa_bwd", "mask views");
+  TORCH_CHECK(rp.numel() >= Mt + 1, "bsa_bwd: block_row_ptrs has ", rp.numel(), " entries, expected at least ",
+              Mt + 1);
+  TORCH_CHECK(n_block_cols >= 0, "bsa_bwd: negative n_block_cols");
+  need_numel(cp, n_block_cols + 1, "bsa_bwd", "col_ptrs");
+  // the column view covers the stored blocks of the block rows below Mt
+  TORCH_CHECK(crow.numel() <= std::max<int64_t>(ci.numel(), 1), "bsa_bwd: col_block_rows has ", crow.numel(),
+              " entries, more than the mask's ", ci.numel(), " blocks");
+  for (auto* p : {&row_max, &row_denom}) {
+    need_dtype(*p, stat_dtype(Q), "bsa_bwd", "row_max and row_denom");
+    need_numel(*p, H * Mt * block_size, "bsa_bwd", "row_max and row_denom");
+  }
+  need_dtype(plan, at::kInt, "bsa_bwd", "plan");
+  TORCH_CHECK(n_items >= 0 && n_splits >= 0 && n_partials >= 0, "bsa_bwd: negative plan counts");
+  TORCH_CHECK(plan.numel() >= 4 + 4 * n_items + 4 * n_splits, "bsa_bwd: plan has ", plan.numel(),
+              " entries, its header counts need ", 4 + 4 * n_items + 4 * n_splits);
   auto dQ = at::empty_like(Q), dK = at::empty_like(Q), dV = at::empty_like(Q);
   const int64_t wsb = tsp_bsa_bwd_workspace_size(H, S, D, n_partials);
   TORCH_CHECK(wsb >= 0, "tsp_bsa_bwd_workspace_size failed: ", tsp_last_error());

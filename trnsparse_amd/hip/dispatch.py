@@ -315,7 +315,13 @@ COLPLAN_MIN_NNZ = 1 << 18
 
 def set_spmv_plan(mode: str) -> None:
     """Select when spmv uses the column-sorted plan: "auto", "always",
-    "never"; or "bucketed" for the length-bucketed row kernels."""
+    "never"; or "bucketed" for the length-bucketed row kernels.
+
+    Each kernel is deterministic, but the windowed kernel and the plan add a
+    row's products in different orders, so under "auto" (windowed kernel on
+    a matrix's first product, the plan from the second) two identical
+    spmv(A, x) calls can differ in the last bits. "never" or "always" give
+    bit-identical repeated calls."""
     global _spmv_plan_mode
     if mode not in _SPMV_PLAN_MODES:
         raise AssertionError(f"spmv plan mode must be one of {_SPMV_PLAN_MODES}, got {mode!r}")

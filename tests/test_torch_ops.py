@@ -152,7 +152,7 @@ def test_ops_reject_mismatched_arguments(hip_backend):
     # CSR: 10 x 20, 30 entries
     g = torch.Generator().manual_seed(0)
     dense = torch.randn(10, 20, generator=g) * (torch.rand(10, 20, generator=g) < 0.15)
-    A = ts.CSRMatrix.from_dense(dense)
+    A = ts.from_dense(dense)
     vals, cols, ptrs, win = D._csr_device(A, dev)
     x = torch.randn(20, device=dev)
     ops.csr_spmv(vals, cols, ptrs, win, 10, 20, x, 1.0, None, 0.0)

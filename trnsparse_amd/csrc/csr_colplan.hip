@@ -437,16 +437,23 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
   uint32_t pwA[K / 2], pwB[K / 2], pwC[K / 2];
   float xa[K], xb[K];
   // k past the tile's last epoch: the plan's zero epoch after all tiles
+  // A chunk pair (or a lane's positions) holding no entry of the epoch (the
+  // padding of a tile's last epoch, every chunk past the tile's end) reads
+  // the plan's zero epoch instead: the load stays unconditional, and the
+  // padding is never fetched from HBM (about 6 % of the plan on cfg2).
   auto load_epoch = [&](uint64_t (&ev)[K], uint32_t (&pw)[K / 2], int64_t k) {
-    const int64_t eb = k < nep ? (ep0 + k) << EBITS : pmax;  // past the tile's end: the zero epoch
-    const u64x2* __restrict__ pe = reinterpret_cast<const u64x2*>(ent + eb + w * SPAN) + lane;
+    const int64_t left = cnt_t - (k << EBITS);  // entries of epoch k (<= 0 past the tile's end)
+    const int64_t eb = (ep0 + k) << EBITS;
 #pragma unroll
     for (int h = 0; h < K / 2; ++h) {
-      const u64x2 v = __builtin_nontemporal_load(pe + h * 64);
+      // the pair's first chunk 2h starts at column-order entry (2h * W + w) * 64
+      const int64_t src = (int64_t)((2 * h * W + w) * 64) < left ? eb : pmax;
+      const u64x2 v = __builtin_nontemporal_load(reinterpret_cast<const u64x2*>(ent + src + w * SPAN) + h * 64 + lane);
       ev[2 * h] = v.x;
       ev[2 * h + 1] = v.y;
     }
-    const u32x2 pv = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(pinv + eb) + w * 64 + lane);
+    const int64_t psrc = (int64_t)(w * 64) < left ? eb : pmax;
+    const u32x2 pv = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(pinv + psrc) + w * 64 + lane);
     pw[0] = pv.x;
     pw[1] = pv.y;
   };
@@ -475,8 +482,8 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
       // offset moved to the (uniform) right-hand side
       const bool real = w * 64 + lane < cnt - j * W * 64;
       const float pr = __builtin_bit_cast(float, (uint32_t)(ev[j] >> 32)) * xv[j];
-      slot[(pw[j >> 1] >> (16 * (j & 1))) & 0xffffu] =
-          u32x2{__builtin_bit_cast(uint32_t, pr), real ? (uint32_t)ev[j] >> cbits : (uint32_t)R};
+      if (real)  // the padding's positions (cnt .. E - 1 in row order) are never read
+        slot[(pw[j >> 1] >> (16 * (j & 1))) & 0xffffu] = u32x2{__builtin_bit_cast(uint32_t, pr), (uint32_t)ev[j] >> cbits};
     }
     // unconditional (past the tile's end it reads the zero epoch), so no
     // path without these loads makes the compiler wait for them early
@@ -493,10 +500,13 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
       const u32x4 v = s2[P ^ ((P >> 3) & 1)];  // pos_slot of positions 2P, 2P + 1
       // (component by component: __builtin_bit_cast of a vector component
       // reads component 0 with this compiler, so __uint_as_float)
-      sm[2 * h] = __uint_as_float(v.x);
-      rr[2 * h] = v.y;
-      sm[2 * h + 1] = __uint_as_float(v.z);
-      rr[2 * h + 1] = v.w;
+      // padding sorts after every row: positions cnt .. E - 1 (not written in
+      // phase 1) are the padding row R with nothing to add
+      const bool p0 = pb + 2 * h < cnt, p1 = pb + 2 * h + 1 < cnt;
+      sm[2 * h] = p0 ? __uint_as_float(v.x) : 0.f;
+      rr[2 * h] = p0 ? v.y : (uint32_t)R;
+      sm[2 * h + 1] = p1 ? __uint_as_float(v.z) : 0.f;
+      rr[2 * h + 1] = p1 ? v.w : (uint32_t)R;
     }
     float old[PL];  // the rows' sums before this epoch (only this lane writes a row it ends)
 #pragma unroll
@@ -540,11 +550,14 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
       }
     }
     const uint64_t cm = __ballot(cf);  // at most one lane: the lane that ends the first row
+    // read that lane with the whole wavefront active: inside the lane-0 branch
+    // the compiler may compute cv for lane 0 only (a readlane of an inactive
+    // lane returns a stale register)
+    const float cvl = __builtin_bit_cast(
+        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv), cm ? (int)__builtin_ctzll(cm) : 0));
     if (lane == 0) {
       crow[w] = cm ? first : NONE;
-      cval[w] = cm ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv),
-                                                                          (int)__builtin_ctzll(cm)))
-                   : 0.f;
+      cval[w] = cm ? cvl : 0.f;
     }
     __syncthreads();
     if (w == 0) {  // the carries, in wavefront order: rows ascend with w
@@ -607,6 +620,20 @@ __global__ __launch_bounds__(256) void colplan_finish_f32(const float* __restric
   float res = alpha * s;
   if (y) res = res + beta * y[r];
   out[r] = res;
+}
+
+// The same for m a multiple of 4 with 16-byte aligned y and out: four rows
+// per thread, 16-byte loads and stores (the same additions in the same order).
+__global__ __launch_bounds__(256) void colplan_finish4_f32(const float* __restrict__ partial, int64_t m, int64_t G,
+                                                           float alpha, const float* __restrict__ y, float beta,
+                                                           float* __restrict__ out) {
+  const int64_t r = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+  if (r >= m) return;
+  f32x4 s = *reinterpret_cast<const f32x4*>(partial + r);
+  for (int64_t g = 1; g < G; ++g) s += *reinterpret_cast<const f32x4*>(partial + g * m + r);
+  f32x4 res = alpha * s;
+  if (y) res = res + beta * *reinterpret_cast<const f32x4*>(y + r);
+  *reinterpret_cast<f32x4*>(out + r) = res;
 }
 
 // ------------------------------------------------------------- geometry
@@ -818,7 +845,13 @@ extern "C" int tsp_csr_colplan_spmv(const void* plan, int dtype, int64_t m, int6
   }
   rc = tsp::check_launch("colplan_spmv launch");
   if (rc || G == 1) return rc;
-  hipLaunchKernelGGL(colplan_finish_f32, dim3((unsigned)tsp::ceil_div(m, 256)), dim3(256), 0, st,
-                     (const float*)workspace, m, G, (float)alpha, yy, (float)beta, (float*)out);
+  const bool vec4 = m % 4 == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)yy & 15) == 0 &&
+                    ((uintptr_t)workspace & 15) == 0;
+  if (vec4)
+    hipLaunchKernelGGL(colplan_finish4_f32, dim3((unsigned)tsp::ceil_div(m / 4, 256)), dim3(256), 0, st,
+                       (const float*)workspace, m, G, (float)alpha, yy, (float)beta, (float*)out);
+  else
+    hipLaunchKernelGGL(colplan_finish_f32, dim3((unsigned)tsp::ceil_div(m, 256)), dim3(256), 0, st,
+                       (const float*)workspace, m, G, (float)alpha, yy, (float)beta, (float*)out);
   return tsp::check_launch("colplan_finish launch");
 }

@@ -684,6 +684,48 @@ def bench_attention_d256(steps: int, warmup: int):
     return out
 
 
+def bench_attention_blocks(steps: int, warmup: int):
+    """Config 5's mask and shape (32 heads x 8192) on the block-product path:
+    bf16 backward at head_dim 256, and forward and backward at head_dim 512 in
+    bf16 and fp32 (SDDMM scores, block softmax / gradient, BSR SpMMs over the
+    mask stacked over heads). FLOPs as the other attention lines: 4 (forward)
+    and 10 (backward) x nnzb x 128^2 x d x heads. Each step is the whole
+    sequence of launches; `us` is the median of 5 timed segments."""
+    import torch
+
+    from trnsparse_amd import workloads as W
+    from trnsparse_amd.hip import dispatch as Dp
+
+    out = []
+    dev = torch.device("cuda", torch.cuda.current_device())
+    for d, dt, fwd in ((256, torch.bfloat16, False), (512, torch.bfloat16, True), (512, torch.float32, True)):
+        Q, K, V, mask = W.cfg5_attention(d=d)
+        H, S, D = Q.shape
+        Qd, Kd, Vd = (t.to(dt).to(dev) for t in (Q, K, V))
+        del Q, K, V
+        tag = "bf16" if dt == torch.bfloat16 else "fp32"
+        peak, key = ((BF16_MFMA_PEAK_TFLOPS, "frac_bf16_mfma") if dt == torch.bfloat16 else
+                     (FP32_MFMA_PEAK_TFLOPS, "frac_fp32_mfma"))
+        O, rm, rd = Dp.hip_block_sparse_attention(Qd, Kd, Vd, mask, D**-0.5, return_stats=True)
+        if fwd:
+            ms, lo, hi = time_gpu_spread(lambda: Dp._attention_blocks_fwd(Qd, Kd, Vd, mask, D**-0.5, dev), steps, warmup)
+            tf = 4.0 * mask.n_blocks * 128 * 128 * D * H / (ms * 1e-3) / 1e12
+            out.append({"name": f"block_sparse_attention cfg5 mask 32x8192x{D} {tag} (block products)",
+                        "value": round(tf * 1e3, 1), "unit": "GFLOP/s", "us": round(ms * 1e3, 1),
+                        "us_spread": [round(lo * 1e3, 1), round(hi * 1e3, 1)], key: round(tf / peak, 4)})
+        dO = torch.randn(Qd.shape, generator=torch.Generator().manual_seed(14)).to(dt).to(dev)
+        rmf, rdf = rm.reshape(H, S), rd.reshape(H, S)
+        ms, lo, hi = time_gpu_spread(lambda: Dp._attention_blocks_bwd(Qd, Kd, Vd, O, dO, mask, D**-0.5, rmf, rdf, dev),
+                                     steps, warmup)
+        tf = 10.0 * mask.n_blocks * 128 * 128 * D * H / (ms * 1e-3) / 1e12
+        out.append({"name": f"block_sparse_attention backward cfg5 mask 32x8192x{D} {tag} (block products)",
+                    "value": round(tf * 1e3, 1), "unit": "GFLOP/s", "us": round(ms * 1e3, 1),
+                    "us_spread": [round(lo * 1e3, 1), round(hi * 1e3, 1)], key: round(tf / peak, 4)})
+        del Qd, Kd, Vd, O, dO, rm, rd
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_attention_backward(steps: int, warmup: int, cpu: bool = False):
     """Backward of block_sparse_attention_tiled at config 5 (tsp_bsa_bwd: the
     row pass for dQ, the column pass for dK / dV and the reduce of split
@@ -949,6 +991,7 @@ def main(argv=None) -> int:
             ("attention", lambda: bench_attention(10, 2, cpu=not args.no_cpu)),
             ("attention backward", lambda: bench_attention_backward(10, 2, cpu=not args.no_cpu)),
             ("attention d256", lambda: bench_attention_d256(5, 2)),
+            ("attention blocks", lambda: bench_attention_blocks(3, 1)),
             ("formats", lambda: bench_formats(5, 1, cpu=not args.no_cpu)),
             ("bsr spmv", lambda: bench_bsr_spmv(20, 3, cpu=not args.no_cpu)),
             ("csr ops", lambda: bench_csr_ops(5, 1)),

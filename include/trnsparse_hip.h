@@ -148,6 +148,21 @@ int tsp_bsr_sddmm(const void* G, int64_t ldg, int64_t m,
                   int64_t n_blocks, int64_t block_size, int dtype,
                   void* grad_blocks, void* stream);
 
+/* tsp_bsr_sddmm_ex: tsp_bsr_sddmm with the blocks written in out_dtype:
+ *   out_dtype == dtype is tsp_bsr_sddmm itself; dtype TSP_BF16 with
+ *   out_dtype TSP_F32 keeps the fp32 accumulators (block_size 128, ncols,
+ *   ldg, ldb multiples of 8, 16-byte aligned G and B). The block scores of
+ *   the block-sparse attention path (S = Q K^T, dP = dO V^T on the mask
+ *   pattern) are formed this way before their fp32 softmax; the reference
+ *   forms them per block inside its attention loops
+ *   (trnsparse/ops.py:311, 349, 462, 466). */
+int tsp_bsr_sddmm_ex(const void* G, int64_t ldg, int64_t m,
+                     const void* B, int64_t ldb, int64_t n, int64_t ncols,
+                     const int64_t* block_rows,
+                     const int64_t* block_col_indices, int64_t n_blocks,
+                     int64_t block_size, int dtype, void* out_blocks,
+                     int out_dtype, void* stream);
+
 int tsp_bsr_spmm_t(const void* blocks, int dtype,
                    const int64_t* col_ptrs, const int64_t* col_block_ids,
                    const int64_t* col_block_rows, int64_t n_block_cols,
@@ -341,6 +356,65 @@ int tsp_bsa_fwd(const void* Q, const void* K, const void* V, int dtype,
                 const int64_t* block_row_ptrs, const int64_t* block_col_indices,
                 int64_t block_size, double scale, void* O, void* row_max,
                 void* row_denom, void* stream);
+
+/* ====================================================================
+ * Block-sparse attention as block-sparse products (any head_dim).
+ *
+ * For the head_dims the one-pass kernels above do not serve (head_dim over
+ * 256; bf16 gradients at head_dim 256), attention runs as block-sparse
+ * products over the mask stacked over heads: the pattern whose block row
+ * h * Mt + i holds the mask blocks of block row i shifted by h * Mt block
+ * columns, so Q, K, V (n_heads, seq_len, head_dim) contiguous are its
+ * (n_heads * seq_len, head_dim) operands. Block scores S = Q K^T come from
+ * tsp_bsr_sddmm_ex (fp32), the softmax below turns them into P, O = P V is
+ * tsp_bsr_spmm; the backward forms S and dP = dO V^T the same way, P and
+ * dS below, and dV = P^T dO, dK = dS^T Q (tsp_bsr_spmm_t), dQ = dS K
+ * (tsp_bsr_spmm). Blocks are (nnzb, 128, 128) fp32 row-major in the stacked
+ * pattern's order. Semantics as tsp_bsa_fwd / tsp_bsa_bwd.
+ *
+ * tsp_bsa_block_softmax: per row r of stacked block row R (row R * 128 + r
+ *   of the stacked operands), over the row's entries in blocks
+ *   block_row_ptrs[R] .. block_row_ptrs[R + 1] - 1:
+ *     row_max[row]   = max scale * S,  row_denom[row] = max(sum exp(scale *
+ *     S - row_max), 1e-12)  (0 and 1e-12 for a row with no block)
+ *     P              = exp(scale * S - row_max) / row_denom, written in
+ *                      out_dtype (TSP_F32 may alias S, TSP_BF16)
+ *   Replaces the reference's tile stats, row reduction and weighting
+ *   (trnsparse/ops.py:302-351; trnsparse/nki/dispatch.py:562-577).
+ * tsp_bsa_block_grad: per stored block k (block row block_rows[k]), with
+ *   the forward's stats and Drow[row] = sum_d dO[row][d] O[row][d]:
+ *     P  = exp(scale * S - row_max) / row_denom
+ *     dS = scale * P * (dP - Drow)
+ *   written in out_dtype (TSP_F32 may alias S and dP; TSP_BF16).
+ *   Replaces the per-block P and dS of trnsparse/ops.py:461-467.
+ * tsp_bsa_rowdot: Drow[r] = sum_d dO[r][d] O[r][d] in fp32 for rows r <
+ *   rows of (rows, head_dim) contiguous O and dO in `dtype` (TSP_F32,
+ *   TSP_BF16). Replaces trnsparse/ops.py:395.
+ * ==================================================================== */
+int tsp_bsa_block_softmax(const float* S, const int64_t* block_row_ptrs,
+                          int64_t n_block_rows, int64_t block_size,
+                          double scale, void* P, int out_dtype,
+                          float* row_max, float* row_denom, void* stream);
+int tsp_bsa_block_grad(const float* S, const float* dP,
+                       const int64_t* block_rows, int64_t n_blocks,
+                       int64_t block_size, double scale,
+                       const float* row_max, const float* row_denom,
+                       const float* Drow, void* P, void* dS, int out_dtype,
+                       void* stream);
+int tsp_bsa_rowdot(const void* O, const void* dO, int dtype, int64_t rows,
+                   int64_t head_dim, float* Drow, void* stream);
+/* tsp_bsa_block_pgrad: tsp_bsr_sddmm_ex for S = Q K^T and dP = dO V^T and
+ *   tsp_bsa_block_grad in one kernel for bf16 (the fp32 scores stay in
+ *   registers): Q, K, V, dO (rows, head_dim) bf16 contiguous, head_dim a
+ *   multiple of 8; P and dS written as bf16 blocks. Replaces the per-block
+ *   products and P / dS of trnsparse/ops.py:461-467. */
+int tsp_bsa_block_pgrad(const void* Q, const void* K, const void* V,
+                        const void* dO, int dtype, int64_t rows,
+                        int64_t head_dim, const int64_t* block_rows,
+                        const int64_t* block_col_indices, int64_t n_blocks,
+                        int64_t block_size, double scale,
+                        const float* row_max, const float* row_denom,
+                        const float* Drow, void* P, void* dS, void* stream);
 
 /* ====================================================================
  * Block-sparse attention backward, per head h < n_heads, from the forward's

@@ -295,3 +295,77 @@ def test_reference_head_dim_256_case(hip_backend, mask, seed):
     bound = R.block_sparse_attention_backward(*args, absolute=True)
     for gr, e, a in zip((qg.grad, kg.grad, vg.grad), exact, bound):
         assert R.scaled_error(gr.cpu().double().numpy(), e, np.maximum(a, 1e-30)) <= TOL_F32
+
+
+# ------------------------------------------- head_dim over 256: block products
+
+
+@pytest.mark.parametrize("S,D,mask,H,dt", [
+    (512, 512, local_mask(4, 2), 1, torch.float32),
+    (512, 512, dilated_mask(4, 2), 2, torch.float32),
+    (640, 512, W.cfg5_block_mask(5), 3, torch.bfloat16),
+    (512, 384, global_mask(4, 1, 1), 2, torch.bfloat16),
+    (256, 300, local_mask(2, 1), 1, torch.float32),   # head_dim zero-padded to 304
+    (384, 1024, torch.ones(3, 3, dtype=torch.bool), 1, torch.float32),
+])
+def test_block_products_forward(hip_backend, S, D, mask, H, dt):
+    """head_dim over 256 (fp32 and bf16, 128-blocks, whole blocks) runs as
+    SDDMM scores, the block softmax and a BSR SpMM with V over the mask
+    stacked over heads: O and the stats of every head against the oracle."""
+    g = torch.Generator().manual_seed(60)
+    Q, K, V = (torch.randn(H, S, D, generator=g).to(dt) for _ in range(3))
+    Q[:, ::5] *= 6  # wide score ranges
+    mask_bsr = W.bsr_from_block_mask(mask, 128)
+    got, rmax, rden = hip_block_sparse_attention(Q.cuda(), K.cuda(), V.cuda(), mask_bsr, D**-0.5, return_stats=True)
+    assert got.dtype == dt and got.shape == (H, S, D)
+    tol = TOL_F32 if dt == torch.float32 else TOL_BF16
+    for hh in range(H):
+        out, em, ed, sc = _oracle(Q[hh], K[hh], V[hh], mask_bsr, D**-0.5)
+        assert _err(got[hh].float().cpu().numpy(), out, sc) <= tol
+        np.testing.assert_allclose(rmax[hh].cpu().numpy(), em, rtol=1e-4, atol=1e-4 if dt == torch.float32 else 2e-2)
+        np.testing.assert_allclose(rden[hh].cpu().numpy(), ed, rtol=1e-4 if dt == torch.float32 else 3e-2)
+
+
+def test_block_products_empty_rows_and_columns_past_seq(hip_backend):
+    """Block products with an empty block row (zeros, stats 0 and 1e-12)
+    and a mask wider than the sequence (its block columns past S hold no
+    keys)."""
+    S, D = 384, 320
+    mask = torch.tensor([[True, False, False, True], [False, False, False, False], [True, True, True, True],
+                         [True, True, True, True]])
+    mask_bsr = W.bsr_from_block_mask(mask, 128)
+    g = torch.Generator().manual_seed(61)
+    Q, K, V = (torch.randn(S, D, generator=g) for _ in range(3))
+    got, rmax, rden = hip_block_sparse_attention(Q.cuda(), K.cuda(), V.cuda(), mask_bsr, 0.05, return_stats=True)
+    got = got.cpu()
+    assert torch.count_nonzero(got[128:256]).item() == 0
+    assert torch.all(rmax[1] == 0) and torch.all(rden[1] == 1e-12)
+    # the oracle on the mask cut to the sequence's 3 block columns
+    cut = W.bsr_from_block_mask(mask[:3, :3], 128)
+    out, em, ed, sc = _oracle(Q, K, V, cut, 0.05)
+    assert _err(got.numpy(), out, sc) <= TOL_F32
+    np.testing.assert_allclose(rmax.cpu().numpy(), em, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("mask,seed", [(local_mask(4, 2), 52), (dilated_mask(4, 2), 53)])
+def test_reference_large_head_dim_case_512(hip_backend, mask, seed):
+    """The reference's large-head_dim hardware case (tests/test_nki_attn.py:
+    153-201, K-tiled head_dim; the reference supports 256 and 512,
+    trnsparse/nki/dispatch.py:515-518) at head_dim 512: fp32, seq 512,
+    forward and backward against the torch path at atol 1e-3 / rtol 1e-4."""
+    torch.manual_seed(seed)
+    S, D = 512, 512
+    Q, K, V = (torch.randn(S, D) for _ in range(3))
+    mask_bsr = W.bsr_from_block_mask(mask, 128)
+    ts.set_backend("pytorch")
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (Q, K, V))
+    ref_out = ts.block_sparse_attention_tiled(qr, kr, vr, mask_bsr)
+    dO = torch.randn_like(ref_out)
+    ref_out.backward(dO)
+    ts.set_backend("hip")
+    q, k, v = (t.cuda().requires_grad_(True) for t in (Q, K, V))
+    out = ts.block_sparse_attention_tiled(q, k, v, mask_bsr)
+    out.backward(dO.cuda())
+    torch.testing.assert_close(out.detach().cpu(), ref_out.detach(), atol=1e-3, rtol=1e-4)
+    for got, want in ((q.grad, qr.grad), (k.grad, kr.grad), (v.grad, vr.grad)):
+        torch.testing.assert_close(got.cpu(), want, atol=1e-3, rtol=1e-4)

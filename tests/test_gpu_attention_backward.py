@@ -10,9 +10,11 @@ absolute form (|dS| replaced by P (|dO V^T| + |D|), operands by their
 magnitudes). fp32 <= 1e-4, bf16 <= 2e-2, fp64 <= 1e-10. fp32 with b = 128
 and d in {64, 128, 256} runs the fp32 MFMA kernels (16-row tiles at
 d = 256), bf16 with d <= 128 the bf16 MFMA kernels of d = 128 (d below 128
-zero-padded to 128), bf16 with d = 256 the fp32 MFMA kernels on widened
-operands, other d below 256 zero-padded to 64, 128 or 256 first;
-everything else (fp64, d > 256, other block sizes) the generic kernels.
+zero-padded to 128), bf16 with d = 256 and fp32 / bf16 with d > 256
+block products over the mask stacked over heads (SDDMM, elementwise softmax
+gradient, BSR SpMMs) when S is a whole number of blocks, other d below 256
+zero-padded to 64, 128 or 256 first; everything else (fp64, ragged S at
+large d, other block sizes) the generic kernels.
 """
 
 from __future__ import annotations
@@ -83,13 +85,17 @@ def _check_head(Q, K, V, dO, O, grads, mask_bsr, scale, tol, rows=None, cols=Non
         (256, 32, local_mask(2, 1), torch.bfloat16),      # head_dim zero-padded to 128
         (300, 96, local_mask(3, 1), torch.bfloat16),      # zero-padded to 128, last key block crosses S
         (256, 100, global_mask(2, 0, 1), torch.float32),  # head_dim zero-padded to 128
-        (256, 160, local_mask(2, 1), torch.bfloat16),     # head_dim zero-padded to 256, widened
-        (256, 320, local_mask(2, 1), torch.bfloat16),     # generic bf16
+        (256, 160, local_mask(2, 1), torch.bfloat16),     # head_dim zero-padded to 256: block products
+        (256, 320, local_mask(2, 1), torch.bfloat16),     # block products (head_dim over 256)
+        (300, 320, local_mask(3, 1), torch.bfloat16),     # generic bf16 (S not whole blocks)
+        (512, 512, local_mask(4, 2), torch.float32),      # block products, fp32
+        (640, 512, W.cfg5_block_mask(5), torch.bfloat16),  # block products, bf16
+        (512, 384, global_mask(4, 1, 1), torch.float32),
         (512, 256, local_mask(4, 2), torch.float32),      # fp32 MFMA d = 256
         (700, 256, global_mask(6, 1, 1), torch.float32),  # d = 256, ragged S, global column split
         (640, 256, W.cfg5_block_mask(5), torch.float32),
         (300, 200, local_mask(3, 2), torch.float32),      # zero-padded to 256, last key block crosses S
-        (512, 256, local_mask(4, 1), torch.bfloat16),     # bf16 d = 256: widened onto the fp32 d = 256 kernels
+        (512, 256, local_mask(4, 1), torch.bfloat16),     # bf16 d = 256: block products on bf16 MFMA
         (512, 128, local_mask(4, 1), torch.float32),      # fp32 MFMA kernels
         (1024, 128, global_mask(8, 1, 1), torch.float32),  # fp32 MFMA, global column split into 2 segments
         (300, 128, local_mask(3, 2), torch.float32),      # fp32 MFMA, last key block crosses S
@@ -218,3 +224,19 @@ def test_cfg5_backward_full_size_f32(hip_backend):
     for hh in range(Q.shape[0]):  # all 32 heads
         _check_head(Q[hh], K[hh], V[hh], dO[hh], O[hh], (dQ[hh], dK[hh], dV[hh]), mask_bsr, 128**-0.5,
                     TOL[torch.float32], rows=rows, cols=cols, sel_q=sel_q, sel_k=sel_k)
+
+
+@pytest.mark.parametrize("D,dtype", [(256, torch.bfloat16), (512, torch.float32), (512, torch.bfloat16)])
+def test_backward_block_products_batched_heads(hip_backend, D, dtype):
+    """Block-product backward over 4 heads (the stacked pattern), with an
+    empty block row: every head's gradients against the oracle."""
+    torch.manual_seed(70)
+    H, S = 4, 512
+    mask = global_mask(4, 1, 1)
+    mask[2, :] = False
+    mask_bsr = W.bsr_from_block_mask(mask, 128)
+    Q, K, V, dO = (torch.randn(H, S, D).to(dtype) for _ in range(4))
+    O, dQ, dK, dV = _run(Q, K, V, dO, mask_bsr)
+    assert torch.count_nonzero(dQ[:, 256:384]).item() == 0
+    for hh in range(H):
+        _check_head(Q[hh], K[hh], V[hh], dO[hh], O[hh], (dQ[hh], dK[hh], dV[hh]), mask_bsr, D**-0.5, TOL[dtype])

@@ -360,12 +360,18 @@ __device__ inline void run(Issue&& issue, int nsteps, const uint8_t* lds, f32x16
 }  // namespace bfb
 
 // dA (SDDMM), bf16: workgroup per stored block, XCD x takes a contiguous
-// range of blocks as in bsr_sddmm_f32_dma.
+// range of blocks as in bsr_sddmm_f32_dma. OutT uint16_t: bf16 blocks (the
+// gradient of bf16 blocks); float: the fp32 accumulators as they are (block
+// scores that a softmax reads next).
+__device__ inline void store_out(uint16_t* p, float v) { *p = tsp::f32_to_bf16_bits(v); }
+__device__ inline void store_out(float* p, float v) { *p = v; }
+
+template <typename OutT>
 __global__ __launch_bounds__(256) void bsr_sddmm_bf16_mfma(const uint16_t* __restrict__ G, int64_t ldg, int64_t m,
                                                            const uint16_t* __restrict__ B, int64_t ldb, int64_t n,
                                                            int64_t ncols, const int64_t* __restrict__ brow,
                                                            const int64_t* __restrict__ ci, int64_t nnzb,
-                                                           uint16_t* __restrict__ out) {
+                                                           OutT* __restrict__ out) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[bfb::NST * bfb::STAGE];
   const int64_t g = blockIdx.x, xcd = g & 7, slot = g >> 3;
   const int64_t per = tsp::ceil_div(nnzb, 8);
@@ -390,7 +396,7 @@ __global__ __launch_bounds__(256) void bsr_sddmm_bf16_mfma(const uint16_t* __res
     for (int u = 0; u < 2; ++u) acc[t][u] = f32x16{};
   bfb::run<true, true>(issue, (int)tsp::ceil_div(ncols, bfb::KC), lds, acc, wm, wn, lane);
   // dA block kb, row-major: lane holds column l32 and rows 8 (v / 4) + 4 h + v % 4
-  uint16_t* ob = out + kb * (BS * BS);
+  OutT* ob = out + kb * (BS * BS);
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -398,7 +404,80 @@ __global__ __launch_bounds__(256) void bsr_sddmm_bf16_mfma(const uint16_t* __res
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int r = wm * 64 + 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
-        ob[r * BS + wn * 64 + 32 * u + l32] = tsp::f32_to_bf16_bits(acc[t][u][v]);
+        store_out(ob + r * BS + wn * 64 + 32 * u + l32, acc[t][u][v]);
+      }
+}
+
+// Block gradient of block-sparse attention, bf16 (the block-product path for
+// head_dims the one-pass backward kernels do not hold): per stored block kb
+// = (block row i, block column j) of the mask stacked over heads, S = Q_i
+// K_j^T and dP = dO_i V_j^T run through the SDDMM engine one after the other
+// (both accumulators stay in registers), then
+//   P  = exp(scale S - row_max) / row_denom,   dS = scale P (dP - Drow)
+// are written as bf16 blocks (reference trnsparse/ops.py:461-467). The fp32
+// scores never leave the workgroup.
+__global__ __launch_bounds__(256) void bsa_block_pgrad_bf16(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+    const uint16_t* __restrict__ dO, int64_t rows, int64_t D, const int64_t* __restrict__ brow,
+    const int64_t* __restrict__ ci, int64_t nnzb, float scale, const float* __restrict__ rmax,
+    const float* __restrict__ rden, const float* __restrict__ Drow, uint16_t* __restrict__ P,
+    uint16_t* __restrict__ dS) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[bfb::NST * bfb::STAGE];
+  __shared__ float rstat[3][BS];
+  const int64_t g = blockIdx.x, xcd = g & 7, slot = g >> 3;
+  const int64_t per = tsp::ceil_div(nnzb, 8);
+  const int64_t kb = xcd * per + slot;
+  if (slot >= per || kb >= nnzb) return;
+  const int64_t i = brow[kb], j = ci[kb];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wm = w & 1, wn = w >> 1, h = lane >> 5, l32 = lane & 31;
+  if (tid < BS) {
+    rstat[0][tid] = rmax[i * BS + tid];
+    rstat[1][tid] = rden[i * BS + tid];
+    rstat[2][tid] = Drow[i * BS + tid];
+  }
+  const uint32_t bytes = (uint32_t)(rows * D * 2);
+  const i32x4 rq = tsp::dma::make_rsrc(Q, bytes), rk = tsp::dma::make_rsrc(K, bytes);
+  const i32x4 rv = tsp::dma::make_rsrc(V, bytes), rdo = tsp::dma::make_rsrc(dO, bytes);
+  const uint32_t lds0 = tsp::dma::lds_addr(lds);
+  const bfb::RowStream sq(i * BS, D, w, lane), sk(j * BS, D, w, lane);
+  const bfb::RowStream sdo(i * BS, D, w, lane), sv(j * BS, D, w, lane);
+  const int nsteps = (int)tsp::ceil_div(D, bfb::KC);
+  f32x16 as[2][2], ap[2][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      as[t][u] = f32x16{};
+      ap[t][u] = f32x16{};
+    }
+  auto issue_s = [&](int s) {
+    const uint32_t st = lds0 + (s % bfb::NST) * bfb::STAGE;
+    sq.issue(rq, s, D, st, w);
+    sk.issue(rk, s, D, st + bfb::TILE, w);
+  };
+  bfb::run<true, true>(issue_s, nsteps, lds, as, wm, wn, lane);
+  tsp::dma::barrier();  // every wave has read its last stage before the ring refills
+  auto issue_p = [&](int s) {
+    const uint32_t st = lds0 + (s % bfb::NST) * bfb::STAGE;
+    sdo.issue(rdo, s, D, st, w);
+    sv.issue(rv, s, D, st + bfb::TILE, w);
+  };
+  bfb::run<true, true>(issue_p, nsteps, lds, ap, wm, wn, lane);
+  // lane holds column l32 of each 32-column tile and rows 8 (v / 4) + 4 h + v % 4
+  uint16_t* pb = P + kb * (BS * BS);
+  uint16_t* db = dS + kb * (BS * BS);
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = wm * 64 + 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
+        const int c = wn * 64 + 32 * u + l32;
+        const float pr = __expf(scale * as[t][u][v] - rstat[0][r]) / rstat[1][r];
+        pb[r * BS + c] = tsp::f32_to_bf16_bits(pr);
+        db[r * BS + c] = tsp::f32_to_bf16_bits(scale * (pr * (ap[t][u][v] - rstat[2][r])));
       }
 }
 
@@ -677,8 +756,8 @@ extern "C" int tsp_bsr_sddmm(const void* G, int64_t ldg, int64_t m, const void* 
       aligned16(B) && (m + BS) * ldg * 2 <= (int64_t)UINT32_MAX - 64 && (n + BS) * ldb * 2 <= (int64_t)UINT32_MAX - 64) {
     const int64_t grid = tsp::ceil_div(n_blocks, 8) * 8;
     if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_sddmm: too many blocks");
-    hipLaunchKernelGGL(bsr_sddmm_bf16_mfma, dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)G, ldg, m,
-                       (const uint16_t*)B, ldb, n, ncols, block_rows, block_col_indices, n_blocks,
+    hipLaunchKernelGGL((bsr_sddmm_bf16_mfma<uint16_t>), dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)G,
+                       ldg, m, (const uint16_t*)B, ldb, n, ncols, block_rows, block_col_indices, n_blocks,
                        (uint16_t*)grad_blocks);
     return tsp::check_launch("bsr_sddmm_bf16_mfma launch");
   }
@@ -704,6 +783,57 @@ extern "C" int tsp_bsr_sddmm(const void* G, int64_t ldg, int64_t m, const void* 
     SDDMM_GEN(uint16_t);
 #undef SDDMM_GEN
   return tsp::check_launch("bsr_sddmm_generic launch");
+}
+
+extern "C" int tsp_bsr_sddmm_ex(const void* G, int64_t ldg, int64_t m, const void* B, int64_t ldb, int64_t n,
+                                int64_t ncols, const int64_t* block_rows, const int64_t* block_col_indices,
+                                int64_t n_blocks, int64_t block_size, int dtype, void* out_blocks, int out_dtype,
+                                void* stream) {
+  if (out_dtype == dtype)
+    return tsp_bsr_sddmm(G, ldg, m, B, ldb, n, ncols, block_rows, block_col_indices, n_blocks, block_size, dtype,
+                         out_blocks, stream);
+  if (dtype != TSP_BF16 || out_dtype != TSP_F32)
+    return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_sddmm_ex: dtype %d with out_dtype %d (bf16 -> f32 or equal dtypes)",
+                     dtype, out_dtype);
+  if (block_size <= 0 || m < 0 || n < 0 || ncols < 0 || n_blocks < 0) return tsp::fail(TSP_EINVAL, "tsp_bsr_sddmm_ex: bad size");
+  if (ldg < ncols || ldb < ncols) return tsp::fail(TSP_EINVAL, "tsp_bsr_sddmm_ex: leading dimension < ncols");
+  if (n_blocks == 0) return TSP_OK;
+  if (!G || !B || !block_rows || !block_col_indices || !out_blocks) return tsp::fail(TSP_EINVAL, "tsp_bsr_sddmm_ex: null pointer");
+  if (!(block_size == BS && ncols % 8 == 0 && ldg % 8 == 0 && ldb % 8 == 0 && aligned16(G) && aligned16(B) &&
+        (m + BS) * ldg * 2 <= (int64_t)UINT32_MAX - 64 && (n + BS) * ldb * 2 <= (int64_t)UINT32_MAX - 64))
+    return tsp::fail(TSP_EUNSUPPORTED,
+                     "tsp_bsr_sddmm_ex: bf16 -> f32 needs block_size 128, ncols / ldg / ldb multiples of 8, 16-byte "
+                     "aligned operands under 4 GiB");
+  const int64_t grid = tsp::ceil_div(n_blocks, 8) * 8;
+  if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_sddmm_ex: too many blocks");
+  hipLaunchKernelGGL((bsr_sddmm_bf16_mfma<float>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)G, ldg, m, (const uint16_t*)B, ldb, n, ncols, block_rows, block_col_indices,
+                     n_blocks, (float*)out_blocks);
+  return tsp::check_launch("bsr_sddmm_bf16_mfma<float> launch");
+}
+
+extern "C" int tsp_bsa_block_pgrad(const void* Q, const void* K, const void* V, const void* dO, int dtype,
+                                   int64_t rows, int64_t head_dim, const int64_t* block_rows,
+                                   const int64_t* block_col_indices, int64_t n_blocks, int64_t block_size,
+                                   double scale, const float* row_max, const float* row_denom, const float* Drow,
+                                   void* P, void* dS, void* stream) {
+  if (dtype != TSP_BF16) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_block_pgrad: dtype %d (bf16 only)", dtype);
+  if (block_size != BS) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_block_pgrad: block_size %lld (128 only)", (long long)block_size);
+  if (rows < 0 || head_dim <= 0 || n_blocks < 0) return tsp::fail(TSP_EINVAL, "tsp_bsa_block_pgrad: bad size");
+  if (n_blocks == 0) return TSP_OK;
+  if (!Q || !K || !V || !dO || !block_rows || !block_col_indices || !row_max || !row_denom || !Drow || !P || !dS)
+    return tsp::fail(TSP_EINVAL, "tsp_bsa_block_pgrad: null pointer");
+  if (head_dim % 8 || !aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(dO) ||
+      rows * head_dim * 2 > (int64_t)UINT32_MAX - 64)
+    return tsp::fail(TSP_EUNSUPPORTED,
+                     "tsp_bsa_block_pgrad: head_dim a multiple of 8, 16-byte aligned operands under 4 GiB");
+  const int64_t grid = tsp::ceil_div(n_blocks, 8) * 8;
+  if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_block_pgrad: too many blocks");
+  hipLaunchKernelGGL(bsa_block_pgrad_bf16, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)Q,
+                     (const uint16_t*)K, (const uint16_t*)V, (const uint16_t*)dO, rows, head_dim, block_rows,
+                     block_col_indices, n_blocks, (float)scale, row_max, row_denom, Drow, (uint16_t*)P,
+                     (uint16_t*)dS);
+  return tsp::check_launch("bsa_block_pgrad_bf16 launch");
 }
 
 extern "C" int tsp_bsr_spmm_t(const void* blocks, int dtype, const int64_t* col_ptrs, const int64_t* col_block_ids,

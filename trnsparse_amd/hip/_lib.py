@@ -44,6 +44,12 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "tsp_bsr_sddmm": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _INT, _P, _P]),
     "tsp_bsr_spmm_t": (_INT, [_P, _INT, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _P]),
+    "tsp_bsr_sddmm_ex": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _INT, _P, _INT, _P]),
+    "tsp_bsa_block_softmax": (_INT, [_P, _P, _I64, _I64, _DBL, _P, _INT, _P, _P, _P]),
+    "tsp_bsa_block_grad": (_INT, [_P, _P, _P, _I64, _I64, _DBL, _P, _P, _P, _P, _P, _INT, _P]),
+    "tsp_bsa_rowdot": (_INT, [_P, _P, _INT, _I64, _I64, _P, _P]),
+    "tsp_bsa_block_pgrad": (_INT, [_P, _P, _P, _P, _INT, _I64, _I64, _P, _P, _I64, _I64, _DBL, _P, _P, _P, _P, _P,
+                                   _P]),
     "tsp_csr_plan_size": (_I64, [_I64, _I64]),
     "tsp_csr_plan": (_INT, [_P, _INT, _I64, _I64, _P, _P]),
     "tsp_csr_spmv": (_INT, [_P, _INT, _P, _P, _INT, _I64, _I64, _I64, _P, _P, _DBL, _P, _DBL, _P, _P]),

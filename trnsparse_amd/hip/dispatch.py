@@ -590,8 +590,11 @@ def hip_block_sparse_attention(Q, K, V, mask_bsr, scale: float, return_stats: bo
     Honours `scale` (the reference NKI path used head_dim**-0.5 regardless).
     Stats come back as (..., S // b, b) in float32 (float64 for float64 input).
     fp32 / bf16 with 128-blocks run the MFMA kernels at head_dim 64, 128 and
-    256, and on operands zero-padded to the next of those below 256; fp16
-    runs in fp32 (widened operands, O rounded back once).
+    256, and on operands zero-padded to the next of those below 256; head_dims
+    over 256 run as block products over the mask stacked over heads (SDDMM
+    scores, an elementwise block softmax, a BSR SpMM with V) when the
+    sequence is a whole number of 128-blocks; fp16 runs in fp32 (widened
+    operands, O rounded back once).
     """
     if not (Q.shape == K.shape == V.shape):
         raise RuntimeError(f"Q, K, V shapes differ: {tuple(Q.shape)}, {tuple(K.shape)}, {tuple(V.shape)}")
@@ -606,6 +609,20 @@ def hip_block_sparse_attention(Q, K, V, mask_bsr, scale: float, return_stats: bo
         if not return_stats:
             return res[..., : Q.shape[-1]].contiguous()
         return (res[0][..., : Q.shape[-1]].contiguous(),) + tuple(res[1:])
+    bd = _blocks_head_dim(Q, mask_bsr.block_size) if Q.shape[-1] > 256 else None
+    if bd is not None:
+        # head_dim over 256: block products over the mask stacked over heads
+        d = Q.shape[-1]
+        lead, S = Q.shape[:-2], Q.shape[-2]
+        orig = Q.device
+        dev = _target_device(Q, K, V)
+        with torch.cuda.device(dev):
+            Qd, Kd, Vd = (_pad_head_dim(_on(t, dev).reshape(-1, S, d), bd).contiguous() for t in (Q, K, V))
+            O, rmax, rden = _attention_blocks_fwd(Qd, Kd, Vd, mask_bsr, scale, dev)
+        out = O[..., :d].reshape(*lead, S, d).to(orig)
+        if not return_stats:
+            return out
+        return out, rmax.reshape(*lead, S // 128, 128).to(orig), rden.reshape(*lead, S // 128, 128).to(orig)
     _lib.dtype_code(Q.dtype)  # raises for a dtype the kernels do not take
     lead = Q.shape[:-2]
     S, D = Q.shape[-2:]
@@ -674,6 +691,133 @@ def _attn_bwd_plan(mask_bsr, H: int, S: int, dev: torch.device):
     return out
 
 
+# ------------------------------------------- attention as block products
+#
+# Head_dims the one-pass kernels do not hold in registers (over 256; bf16
+# gradients at 256) run as block-sparse products over the mask stacked over
+# heads: stacked block row h * Mt + i holds mask block row i shifted by h * Mt
+# block columns, so (H, S, D) operands are its (H * S, D) dense operands.
+# Scores and score gradients are SDDMMs on that pattern (tsp_bsr_sddmm_ex,
+# fp32 blocks), the softmax and its gradient are elementwise passes over the
+# blocks (tsp_bsa_block_softmax, tsp_bsa_block_grad), and O, dQ, dK, dV are
+# BSR SpMMs (tsp_bsr_spmm, tsp_bsr_spmm_t): every product on MFMA.
+
+
+def _blocks_head_dim(t: torch.Tensor, block_size: int) -> int | None:
+    """Head_dim the block-product path runs a (..., S, D) fp32 / bf16 operand
+    at (D rounded up to a multiple of 8, the SDDMM's vector width), or None
+    when the path does not apply (block size other than 128, a sequence that
+    is not a whole number of blocks)."""
+    S, d = t.shape[-2:]
+    if block_size != 128 or t.dtype not in (torch.float32, torch.bfloat16) or S == 0 or S % 128 or d == 0:
+        return None
+    return (d + 7) // 8 * 8
+
+
+def _attn_stack_plan(mask_bsr, H: int, S: int, dev: torch.device):
+    """The mask's block rows below Mt = S // 128 and block columns below Mt
+    (keys at or past S do not exist), stacked over H heads: (rp, ci, order,
+    brow, cp, cbid, crow, corder, nnzb). Built on the host from the pattern
+    and cached on the mask's column-index tensor, keyed by the pattern's
+    identity and version and (H, S, device)."""
+    b = mask_bsr.block_size
+    Mt = S // b
+    ci_t, rp_t = mask_bsr.block_col_indices, mask_bsr.block_row_ptrs
+    key = (rp_t.data_ptr(), rp_t._version, rp_t.numel(), ci_t.data_ptr(), ci_t._version, ci_t.numel(), H, S,
+           str(dev))
+    hit = getattr(ci_t, "_tsp_attn_stack_plan", None)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    rp = rp_t.detach().to("cpu", torch.int64).numpy()
+    ci = ci_t.detach().to("cpu", torch.int64).numpy()
+    if rp.size < Mt + 1:
+        raise IndexError(f"mask has {rp.size - 1} block rows, attention needs {Mt}")
+    brow0 = np.repeat(np.arange(Mt, dtype=np.int64), np.diff(rp[: Mt + 1]))
+    col0 = ci[: int(rp[Mt])]
+    keep = col0 < Mt
+    brow0, col0 = brow0[keep], col0[keep]
+    counts = np.bincount(brow0, minlength=Mt).astype(np.int64)
+    shift = (Mt * np.arange(H, dtype=np.int64))[:, None]
+    col = (col0[None, :] + shift).reshape(-1)
+    rps = np.zeros(H * Mt + 1, dtype=np.int64)
+    rps[1:] = np.cumsum(np.tile(counts, H))
+    nbr = H * Mt
+    rp_d = torch.from_numpy(rps).to(dev)
+    ci_d = torch.from_numpy(col if col.size else np.zeros(0, np.int64)).to(dev)
+    order = torch.empty(max(nbr, 1), dtype=torch.int32, device=dev)
+    _lib.call("tsp_bsr_row_order", rp_d.data_ptr(), nbr, order.data_ptr(), _lib.stream_handle(dev))
+    brow, cp, cbid, crow, corder = _bsr_bwd_plan(rp_d, ci_d, nbr, nbr, dev)
+    out = (rp_d, ci_d, order, brow, cp, cbid, crow, corder, int(col.size))
+    try:
+        ci_t._tsp_attn_stack_plan = (key, out)
+    except AttributeError:
+        pass
+    return out
+
+
+def _block_scores(A: torch.Tensor, B: torch.Tensor, plan, dev) -> torch.Tensor:
+    """fp32 blocks A B^T on the stacked pattern (A, B (rows, D) in fp32 / bf16)."""
+    rp, ci, _, brow, _, _, _, _, nnzb = plan
+    rows, D = A.shape
+    out = torch.empty((max(nnzb, 1), 128, 128), dtype=torch.float32, device=dev)
+    _lib.call("tsp_bsr_sddmm_ex", A.data_ptr(), D, rows, B.data_ptr(), D, rows, D, brow.data_ptr(), ci.data_ptr(), nnzb,
+              128, _lib.dtype_code(A.dtype), out.data_ptr(), _lib.TSP_F32, _lib.stream_handle(dev))
+    return out
+
+
+def _attention_blocks_fwd(Qd, Kd, Vd, mask_bsr, scale: float, dev):
+    """(O, row_max, row_denom) of (H, S, D) fp32 / bf16 operands on the
+    block-product path; stats (H, S // 128, 128) fp32."""
+    H, S, D = Qd.shape
+    rows = H * S
+    dt = Qd.dtype
+    plan = _attn_stack_plan(mask_bsr, H, S, dev)
+    rp, ci, order, _, _, _, _, _, nnzb = plan
+    Sb = _block_scores(Qd.reshape(rows, D), Kd.reshape(rows, D), plan, dev)
+    P = Sb if dt == torch.float32 else torch.empty(Sb.shape, dtype=dt, device=dev)
+    rmax = torch.empty(rows, dtype=torch.float32, device=dev)
+    rden = torch.empty(rows, dtype=torch.float32, device=dev)
+    _lib.call("tsp_bsa_block_softmax", Sb.data_ptr(), rp.data_ptr(), rp.numel() - 1, 128, float(scale), P.data_ptr(),
+              _lib.dtype_code(dt), rmax.data_ptr(), rden.data_ptr(), _lib.stream_handle(dev))
+    del Sb
+    O = _lib.ops().bsr_spmm(P[:nnzb], rp, ci, order, rows, rows, 128, Vd.reshape(rows, D), dt)
+    Mt = S // 128
+    return O.reshape(H, S, D), rmax.reshape(H, Mt, 128), rden.reshape(H, Mt, 128)
+
+
+def _attention_blocks_bwd(q, k, v, o, do, mask_bsr, scale: float, rm, rd, dev):
+    """(dQ, dK, dV) of (H, S, D) fp32 / bf16 operands on the block-product
+    path, from the forward's O and fp32 stats."""
+    H, S, D = q.shape
+    rows = H * S
+    dt = q.dtype
+    plan = _attn_stack_plan(mask_bsr, H, S, dev)
+    rp, ci, order, brow, cp, cbid, crow, corder, nnzb = plan
+    q2, k2, v2, o2, do2 = (t.reshape(rows, D) for t in (q, k, v, o, do))
+    st = _lib.stream_handle(dev)
+    Drow = torch.empty(rows, dtype=torch.float32, device=dev)
+    _lib.call("tsp_bsa_rowdot", o2.data_ptr(), do2.data_ptr(), _lib.dtype_code(dt), rows, D, Drow.data_ptr(), st)
+    if dt == torch.float32:
+        # fp32 scores as blocks, P and dS written over them
+        Sb = _block_scores(q2, k2, plan, dev)
+        dPb = _block_scores(do2, v2, plan, dev)
+        _lib.call("tsp_bsa_block_grad", Sb.data_ptr(), dPb.data_ptr(), brow.data_ptr(), nnzb, 128, float(scale),
+                  rm.data_ptr(), rd.data_ptr(), Drow.data_ptr(), Sb.data_ptr(), dPb.data_ptr(), _lib.TSP_F32, st)
+        P, dS = Sb, dPb
+    else:
+        # bf16: both score products and the gradient in one kernel
+        P = torch.empty((max(nnzb, 1), 128, 128), dtype=dt, device=dev)
+        dS = torch.empty_like(P)
+        _lib.call("tsp_bsa_block_pgrad", q2.data_ptr(), k2.data_ptr(), v2.data_ptr(), do2.data_ptr(),
+                  _lib.dtype_code(dt), rows, D, brow.data_ptr(), ci.data_ptr(), nnzb, 128, float(scale), rm.data_ptr(),
+                  rd.data_ptr(), Drow.data_ptr(), P.data_ptr(), dS.data_ptr(), st)
+    ops = _lib.ops()
+    dV = ops.bsr_spmm_t(P[:nnzb], cp, cbid, crow, corder, rows, rows, 128, do2)
+    dK = ops.bsr_spmm_t(dS[:nnzb], cp, cbid, crow, corder, rows, rows, 128, q2)
+    dQ = ops.bsr_spmm(dS[:nnzb], rp, ci, order, rows, rows, 128, k2, dt)
+    return dQ.reshape(H, S, D), dK.reshape(H, S, D), dV.reshape(H, S, D)
+
+
 def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, row_max, row_denom):
     """Block-sparse attention backward (replaces nki_bsr_attn_bwd, reference
     dispatch.py:813-929, and the torch backward ops.py:360-473).
@@ -684,11 +828,12 @@ def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, 
     bf16 with 128-blocks: head_dims below 128 are zero-padded to 128 and
     run the bf16 MFMA kernels of head_dim 128 (zero columns change neither
     the scores nor the other gradient columns, and those kernels run at
-    several times the rate of the fp32 ones on widened operands); head_dim
-    256 runs on the fp32 MFMA kernels, its operands widened on the device
-    (exact) and the gradients rounded to bf16 once at the end. Other
-    head_dims below 256 are zero-padded to 64, 128 or 256 first, as in the
-    forward.
+    several times the rate of the fp32 ones on widened operands). bf16 at
+    head_dim 256, and fp32 / bf16 at head_dims over 256, run as block
+    products over the mask stacked over heads (SDDMMs for S and dP, the
+    elementwise softmax gradient, BSR SpMMs for dQ, dK, dV) when the
+    sequence is a whole number of 128-blocks. Other head_dims below 256 are
+    zero-padded to 64, 128 or 256 first, as in the forward.
     """
     if not (Q.shape == K.shape == V.shape == O.shape == dO.shape):
         raise RuntimeError("Q, K, V, O, dO shapes differ")
@@ -705,10 +850,22 @@ def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, 
         grads = hip_block_sparse_attention_backward(*(_pad_head_dim(t, dp) for t in (Q, K, V, O, dO)), mask_bsr, scale,
                                                     row_max, row_denom)
         return tuple(gr[..., : Q.shape[-1]].contiguous() for gr in grads)
-    if Q.dtype == torch.bfloat16 and Q.shape[-1] == 256 and mask_bsr.block_size == 128 and scale > 0:
-        grads = hip_block_sparse_attention_backward(*(t.float() for t in (Q, K, V, O, dO)), mask_bsr, scale,
-                                                    row_max, row_denom)
-        return tuple(gr.to(torch.bfloat16) for gr in grads)
+    d = Q.shape[-1]
+    bd = _blocks_head_dim(Q, mask_bsr.block_size) if (d > 256 or (d == 256 and Q.dtype == torch.bfloat16)) else None
+    if bd is not None:
+        # block products over the mask stacked over heads (bf16 at 256: on the
+        # bf16 MFMA kernels instead of the fp32 ones on widened operands)
+        lead, S = Q.shape[:-2], Q.shape[-2]
+        orig = Q.device
+        dev = _target_device(Q, K, V, O, dO)
+        with torch.cuda.device(dev):
+            q, k, v, o, do = (_pad_head_dim(_on(t, dev, Q.dtype).reshape(-1, S, d), bd).contiguous()
+                              for t in (Q, K, V, O, dO))
+            H = q.shape[0]
+            rm = _on(row_max, dev, torch.float32).reshape(H, S)
+            rd = _on(row_denom, dev, torch.float32).reshape(H, S)
+            grads = _attention_blocks_bwd(q, k, v, o, do, mask_bsr, scale, rm, rd, dev)
+        return tuple(g[..., :d].reshape(*lead, S, d).to(orig) for g in grads)
     dt = Q.dtype
     _lib.dtype_code(dt)  # raises for a dtype the kernels do not take
     lead = Q.shape[:-2]

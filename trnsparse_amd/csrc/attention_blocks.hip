@@ -99,16 +99,34 @@ __global__ __launch_bounds__(256) void bsa_block_grad_kernel(const float* __rest
 
 template <typename T> __device__ inline float ldf(const T* p) { return (float)*p; }
 template <> __device__ inline float ldf<uint16_t>(const uint16_t* p) { return tsp::bf16_bits_to_f32(*p); }
+__device__ inline float cvf(float v) { return v; }
+__device__ inline float cvf(uint16_t v) { return tsp::bf16_bits_to_f32(v); }
 
-// Drow[r] = sum_d dO[r][d] O[r][d], one wavefront per row.
-template <typename T>
+// Drow[r] = sum_d dO[r][d] O[r][d], one wavefront per row; VEC: head_dim a
+// multiple of 4 with 8-byte (bf16) / 16-byte (fp32) aligned rows, four
+// elements per lane and load.
+template <typename T> struct Vec4;
+template <> struct Vec4<float> { typedef f32x4 type; };
+template <> struct Vec4<uint16_t> { typedef uint16_t type __attribute__((ext_vector_type(4))); };
+
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void bsa_rowdot_kernel(const T* __restrict__ O, const T* __restrict__ dO,
                                                          int64_t rows, int64_t D, float* __restrict__ Drow) {
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (r >= rows) return;
   float s = 0.f;
-  for (int64_t d = lane; d < D; d += 64) s += ldf(O + r * D + d) * ldf(dO + r * D + d);
+  if (VEC) {
+    typedef typename Vec4<T>::type V4;
+    const V4* o4 = reinterpret_cast<const V4*>(O + r * D);
+    const V4* g4 = reinterpret_cast<const V4*>(dO + r * D);
+    for (int64_t d = lane; d < D / 4; d += 64) {
+      const V4 a = o4[d], b = g4[d];
+      s += cvf((T)a.x) * cvf((T)b.x) + cvf((T)a.y) * cvf((T)b.y) + cvf((T)a.z) * cvf((T)b.z) + cvf((T)a.w) * cvf((T)b.w);
+    }
+  } else {
+    for (int64_t d = lane; d < D; d += 64) s += ldf(O + r * D + d) * ldf(dO + r * D + d);
+  }
   s = tsp::wave_sum(s);
   if (lane == 0) Drow[r] = s;
 }
@@ -169,11 +187,22 @@ extern "C" int tsp_bsa_rowdot(const void* O, const void* dO, int dtype, int64_t 
   const int64_t grid = tsp::ceil_div(rows, 4);
   if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_rowdot: too many rows");
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == TSP_F32)
-    hipLaunchKernelGGL(bsa_rowdot_kernel<float>, dim3((unsigned)grid), dim3(256), 0, st, (const float*)O,
-                       (const float*)dO, rows, head_dim, Drow);
-  else
-    hipLaunchKernelGGL(bsa_rowdot_kernel<uint16_t>, dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)O,
-                       (const uint16_t*)dO, rows, head_dim, Drow);
+  const int64_t esz = dtype == TSP_F32 ? 4 : 2;
+  const bool vec = head_dim % 4 == 0 && ((uintptr_t)O % (4 * esz)) == 0 && ((uintptr_t)dO % (4 * esz)) == 0;
+  if (dtype == TSP_F32) {
+    if (vec)
+      hipLaunchKernelGGL((bsa_rowdot_kernel<float, true>), dim3((unsigned)grid), dim3(256), 0, st, (const float*)O,
+                         (const float*)dO, rows, head_dim, Drow);
+    else
+      hipLaunchKernelGGL((bsa_rowdot_kernel<float, false>), dim3((unsigned)grid), dim3(256), 0, st, (const float*)O,
+                         (const float*)dO, rows, head_dim, Drow);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((bsa_rowdot_kernel<uint16_t, true>), dim3((unsigned)grid), dim3(256), 0, st,
+                         (const uint16_t*)O, (const uint16_t*)dO, rows, head_dim, Drow);
+    else
+      hipLaunchKernelGGL((bsa_rowdot_kernel<uint16_t, false>), dim3((unsigned)grid), dim3(256), 0, st,
+                         (const uint16_t*)O, (const uint16_t*)dO, rows, head_dim, Drow);
+  }
   return tsp::check_launch("bsa_rowdot launch");
 }

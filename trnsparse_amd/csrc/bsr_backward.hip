@@ -464,20 +464,35 @@ __global__ __launch_bounds__(256) void bsa_block_pgrad_bf16(
     sv.issue(rv, s, D, st + bfb::TILE, w);
   };
   bfb::run<true, true>(issue_p, nsteps, lds, ap, wm, wn, lane);
-  // lane holds column l32 of each 32-column tile and rows 8 (v / 4) + 4 h + v % 4
-  uint16_t* pb = P + kb * (BS * BS);
-  uint16_t* db = dS + kb * (BS * BS);
+  // lane holds column l32 of each 32-column tile and rows 8 (v / 4) + 4 h + v % 4.
+  // Rows v and v + 1 (v even) are adjacent: neighbouring lanes swap one value
+  // (DPP quad_perm [1,0,3,2]) so that the even lane stores row v's two
+  // columns c, c + 1 and the odd lane row v + 1's columns c - 1, c, each as
+  // one 4-byte store.
+  uint32_t* pb = reinterpret_cast<uint32_t*>(P + kb * (BS * BS));
+  uint32_t* db = reinterpret_cast<uint32_t*>(dS + kb * (BS * BS));
+  const bool even = (lane & 1) == 0;
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = wm * 64 + 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
+      for (int v = 0; v < 16; v += 2) {
+        const int r0 = wm * 64 + 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
         const int c = wn * 64 + 32 * u + l32;
-        const float pr = __expf(scale * as[t][u][v] - rstat[0][r]) / rstat[1][r];
-        pb[r * BS + c] = tsp::f32_to_bf16_bits(pr);
-        db[r * BS + c] = tsp::f32_to_bf16_bits(scale * (pr * (ap[t][u][v] - rstat[2][r])));
+        uint32_t pw[2], dw[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int r = r0 + e;
+          const float pr = __expf(scale * as[t][u][v + e] - rstat[0][r]) / rstat[1][r];
+          pw[e] = tsp::f32_to_bf16_bits(pr);
+          dw[e] = tsp::f32_to_bf16_bits(scale * (pr * (ap[t][u][v + e] - rstat[2][r])));
+        }
+        const uint32_t py = (uint32_t)__builtin_amdgcn_mov_dpp((int)(even ? pw[1] : pw[0]), 0xB1, 0xF, 0xF, false);
+        const uint32_t dy = (uint32_t)__builtin_amdgcn_mov_dpp((int)(even ? dw[1] : dw[0]), 0xB1, 0xF, 0xF, false);
+        const int o = even ? (r0 * BS + c) >> 1 : ((r0 + 1) * BS + c - 1) >> 1;
+        pb[o] = even ? (pw[0] | (py << 16)) : (py | (pw[1] << 16));
+        db[o] = even ? (dw[0] | (dy << 16)) : (dy | (dw[1] << 16));
       }
 }
 

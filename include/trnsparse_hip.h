@@ -225,17 +225,18 @@ int tsp_csr_spmv(const void* values, int dtype, const void* col_indices,
  * matrix built once per pattern: tiles of 2^rbits rows x 2^cbits columns,
  * each tile's entries sorted by column, 8 bytes per entry (packed row /
  * column within the tile and the fp32 value), so the x gathers of one
- * wavefront instruction share cache lines. Row sums of one tile are added
- * in LDS in a run-dependent order (results may differ between runs in the
- * last bits; tsp_csr_spmv is the deterministic path).
+ * wavefront instruction share cache lines. Every sum runs in a fixed order
+ * (repeated calls are bit-identical), but not in the order of tsp_csr_spmv:
+ * the two paths can differ in the last bits.
  *
  * geometry (10 int64, host memory), filled by tsp_csr_colplan_geometry:
  *   [0] rbits   [1] row blocks   [2] cbits   [3] column groups G
  *   [4] tiles   [5] sort key bits [6] plan bytes  [7] build workspace bytes
  *   [8] SpMV workspace bytes (G * m * 4; 0 when G == 1)  [9] reserved
  * rows_per_block_log2 (12..14) and tiles_hint tune the tiling; 0 = auto.
- * TSP_EUNSUPPORTED when nnz > 2^32 - 1. The plan holds entry positions as
- * uint32: row_ptrs[m] must be below 2^32. */
+ * TSP_EUNSUPPORTED when nnz > 2^32 - 2. The plan holds each entry's
+ * position k in the pattern (uint32) and row_ptrs[0] (any value) beside
+ * them; tsp_csr_colplan_refresh reads values[row_ptrs[0] + k]. */
 int tsp_csr_colplan_geometry(int64_t m, int64_t n, int64_t nnz,
                              int rows_per_block_log2, int64_t tiles_hint,
                              int64_t* geometry);

@@ -145,6 +145,46 @@ def test_colplan_runs_across_lanes_and_wavefronts(hip_backend, rbits, tiles):
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
 
 
+@pytest.mark.parametrize("index_dtype", [np.int64, np.int32])
+def test_colplan_view_with_nonzero_first_row_pointer(hip_backend, index_dtype):
+    """A CSR view whose row_ptrs[0] is not zero (the pattern's entries start
+    `base` entries into the arrays): the plan keeps each entry's position
+    relative to row_ptrs[0], so the build, the SpMV and a refresh with new
+    values all read values[row_ptrs[0] + k], whatever base is."""
+    m, n, base = 12000, 15000, 777
+    v, c, p, rng = _random(m, n, np.random.default_rng(5).poisson(9, m), 31, index_dtype)
+    junk_v = rng.standard_normal(base).astype(np.float32) * 1e6
+    junk_c = rng.integers(0, n, base).astype(index_dtype)
+    dev = torch.device("cuda")
+    vals = torch.from_numpy(np.concatenate([junk_v, v])).to(dev)
+    cols = torch.from_numpy(np.concatenate([junk_c, c])).to(dev)
+    ptrs = torch.from_numpy((p + base).astype(index_dtype)).to(dev)
+    nnz = len(v)
+    geom = np.zeros(10, dtype=np.int64)
+    _lib.call("tsp_csr_colplan_geometry", m, n, nnz, 0, 0, geom.ctypes.data)
+    plan = torch.empty(int(geom[6]), dtype=torch.uint8, device=dev)
+    work = torch.empty(int(geom[7]), dtype=torch.uint8, device=dev)
+    st = _lib.stream_handle(dev)
+    _lib.call("tsp_csr_colplan_build", vals.data_ptr(), _lib.TSP_F32, cols.data_ptr(), ptrs.data_ptr(),
+              _lib.index_code(cols.dtype), m, n, nnz, geom.ctypes.data, plan.data_ptr(), work.data_ptr(), st)
+    x = rng.standard_normal(n).astype(np.float32)
+    xd = torch.from_numpy(x).to(dev)
+    out = torch.empty(m, device=dev)
+    ws = torch.empty(max(1, int(geom[8])), dtype=torch.uint8, device=dev)
+
+    def run():
+        _lib.call("tsp_csr_colplan_spmv", plan.data_ptr(), _lib.TSP_F32, m, n, nnz, geom.ctypes.data, xd.data_ptr(),
+                  1.0, None, 0.0, out.data_ptr(), ws.data_ptr(), st)
+        return out.cpu().numpy()
+
+    _check(v, c, p, (m, n), x, run())
+    v2 = rng.standard_normal(nnz).astype(np.float32)
+    vals[base:] = torch.from_numpy(v2).to(dev)
+    _lib.call("tsp_csr_colplan_refresh", vals.data_ptr(), _lib.TSP_F32, m, n, nnz, geom.ctypes.data, plan.data_ptr(),
+              st)
+    _check(v2, c, p, (m, n), x, run())
+
+
 def test_colplan_refresh_follows_new_values(plan_always):
     m, n = 20000, 20000
     v, c, p, rng = _random(m, n, np.full(m, 16), 7)

@@ -53,9 +53,10 @@
 // eoff (T+1 int64, first epoch of each tile), ent (8 bytes per padded entry:
 // value bits << 32 | row_in_tile << cbits | column_in_group), pinv (uint16
 // per padded entry: the entry's position in the epoch's row order, swizzled
-// for phase 2's 16-byte reads), pos (uint32 per padded entry: position in
-// the caller's CSR arrays, for new values on the same pattern; 0xffffffff
-// for padding). Inside an epoch, ent and pos are stored in the SpMV
+// for phase 2's 16-byte reads), pos (uint32 per padded entry: position k in
+// the pattern's entries, for new values on the same pattern, read at
+// values[row_ptrs[0] + k]; 0xffffffff for padding), and a 256-byte header
+// holding row_ptrs[0] (int64). Inside an epoch, ent and pos are stored in the SpMV
 // kernel's lane order (entry_slot below): one 16-byte load gives a lane two
 // of its chunks' entries, and pinv holds a lane's 4 positions in 8
 // consecutive bytes. The three per-entry arrays hold one more epoch of zeros
@@ -143,10 +144,14 @@ __device__ inline int64_t row_of(const IdxT* __restrict__ ptr, int64_t m, int64_
 template <typename IdxT, typename K>
 __global__ __launch_bounds__(256) void colplan_keys_kernel(const IdxT* __restrict__ col, const IdxT* __restrict__ ptr,
                                                            int64_t m, int64_t nnz, int rbits, int cbits, int64_t G,
-                                                           K* __restrict__ keys, uint64_t* __restrict__ payload) {
+                                                           K* __restrict__ keys, uint64_t* __restrict__ payload,
+                                                           int64_t* __restrict__ plan_base) {
   __shared__ int64_t srp[KSPAN + 1];
   __shared__ int64_t span[2];
-  const int64_t base = (int64_t)ptr[0];  // p: position in the caller's arrays; p - base: position in the sort
+  // p = base + k: position in the caller's arrays; k < nnz: position in the
+  // sort, the one the plan keeps (base may be any row_ptrs[0])
+  const int64_t base = (int64_t)ptr[0];
+  if (blockIdx.x == 0 && threadIdx.x == 0) plan_base[0] = base;
   const int64_t e0 = (int64_t)blockIdx.x * KTILE;
   const int64_t e1 = e0 + KTILE < nnz ? e0 + KTILE : nnz;
   if (threadIdx.x == 0) {
@@ -179,7 +184,7 @@ __global__ __launch_bounds__(256) void colplan_keys_kernel(const IdxT* __restric
     const int64_t c = (int64_t)col[p];
     const int64_t tile = (r >> rbits) * G + (c >> cbits);
     keys[k] = (K)((tile << cbits) | (c & cmask));
-    payload[k] = ((uint64_t)(r & rmask) << 32) | (uint64_t)p;
+    payload[k] = ((uint64_t)(r & rmask) << 32) | (uint64_t)k;
   }
 }
 
@@ -246,6 +251,7 @@ __global__ __launch_bounds__(256) void colplan_scatter_kernel(const K* __restric
                                                               const float* __restrict__ vals, int64_t nnz, int cbits,
                                                               const int64_t* __restrict__ toff,
                                                               const int64_t* __restrict__ eoff, int64_t T,
+                                                              const int64_t* __restrict__ plan_base,
                                                               uint64_t* __restrict__ ent, uint32_t* __restrict__ pos) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= nnz) return;
@@ -253,10 +259,10 @@ __global__ __launch_bounds__(256) void colplan_scatter_kernel(const K* __restric
   const int64_t j = i - toff[t];
   const int64_t P = ((eoff[t] + (j >> EBITS)) << EBITS) + entry_slot((int)(j & (E - 1)));
   const uint64_t pl = payload[i];
-  const uint32_t p = (uint32_t)pl;
+  const uint32_t p = (uint32_t)pl;  // position k in the sort; the value sits at base + k
   const uint32_t rl = (uint32_t)(pl >> 32);
   const uint32_t cin = (uint32_t)(keys[i] & (((K)1 << cbits) - 1));
-  ent[P] = ((uint64_t)__builtin_bit_cast(uint32_t, vals[p]) << 32) | (uint64_t)((rl << cbits) | cin);
+  ent[P] = ((uint64_t)__builtin_bit_cast(uint32_t, vals[plan_base[0] + p]) << 32) | (uint64_t)((rl << cbits) | cin);
   pos[P] = p;
 }
 
@@ -353,11 +359,12 @@ __global__ __launch_bounds__(1024) void colplan_perm_kernel(const uint64_t* __re
 
 __global__ __launch_bounds__(256) void colplan_refresh_kernel(const float* __restrict__ vals,
                                                               const uint32_t* __restrict__ pos, int64_t n,
+                                                              const int64_t* __restrict__ plan_base,
                                                               uint64_t* __restrict__ ent) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const uint32_t p = pos[i];
-  const uint32_t bits = p == POS_PAD ? 0u : __builtin_bit_cast(uint32_t, vals[p]);
+  const uint32_t bits = p == POS_PAD ? 0u : __builtin_bit_cast(uint32_t, vals[plan_base[0] + p]);
   ent[i] = ((uint64_t)bits << 32) | (ent[i] & 0xffffffffull);
 }
 
@@ -676,8 +683,8 @@ int geometry(int64_t m, int64_t n, int64_t nnz, int rbits_hint, int64_t tiles_hi
   g[GEOM_G] = G;
   g[GEOM_T] = T;
   g[GEOM_KEYBITS] = keybits;
-  g[GEOM_PLAN_BYTES] =
-      2 * align256((T + 1) * 8) + align256((pmax + E) * 8) + align256((pmax + E) * 2) + align256((pmax + E) * 4);
+  g[GEOM_PLAN_BYTES] = 2 * align256((T + 1) * 8) + align256((pmax + E) * 8) + align256((pmax + E) * 2) +
+                        align256((pmax + E) * 4) + 256;  // + the header (row_ptrs[0] of the built pattern)
   g[GEOM_BUILD_BYTES] = 2 * align256(nnz * ksz) + 2 * align256(nnz * 8) + align256((int64_t)tmp);
   g[GEOM_SPMV_BYTES] = G > 1 ? G * m * 4 : 0;
   g[GEOM_PMAX] = pmax;
@@ -690,6 +697,7 @@ struct PlanView {
   uint64_t* ent;
   uint16_t* pinv;
   uint32_t* pos;
+  int64_t* base;  // row_ptrs[0] of the pattern the plan was built from
   int64_t pmax;
 };
 
@@ -707,6 +715,8 @@ PlanView plan_view(void* plan, const int64_t* g) {
   v.pinv = (uint16_t*)p;
   p += align256((v.pmax + E) * 2);
   v.pos = (uint32_t*)p;
+  p += align256((v.pmax + E) * 4);
+  v.base = (int64_t*)p;
   return v;
 }
 
@@ -752,7 +762,7 @@ int build_typed(const float* vals, const void* col, const void* ptr, int64_t m, 
   if (nnz > 0) {
     if (tsp::ceil_div(nnz, KTILE) > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_colplan_build: too many entries");
     hipLaunchKernelGGL((colplan_keys_kernel<IdxT, K>), dim3((unsigned)tsp::ceil_div(nnz, KTILE)), dim3(256), 0, st,
-                       (const IdxT*)col, (const IdxT*)ptr, m, nnz, rbits, cbits, G, kin, pin);
+                       (const IdxT*)col, (const IdxT*)ptr, m, nnz, rbits, cbits, G, kin, pin, v.base);
     rc = tsp::check_launch("colplan_keys launch");
     if (rc) return rc;
     e = tsp::rsort::radix_sort_pairs(tmp, tmp_bytes, (const K*)kin, kout, (const uint64_t*)pin, pout, nnz, 0,
@@ -767,7 +777,7 @@ int build_typed(const float* vals, const void* col, const void* ptr, int64_t m, 
   rc = tsp::check_launch("colplan_epochs launch");
   if (rc || nnz == 0) return rc;
   hipLaunchKernelGGL((colplan_scatter_kernel<K>), dim3((unsigned)tsp::ceil_div(nnz, 256)), dim3(256), 0, st, kout,
-                     pout, vals, nnz, cbits, v.toff, v.eoff, T, v.ent, v.pos);
+                     pout, vals, nnz, cbits, v.toff, v.eoff, T, v.base, v.ent, v.pos);
   rc = tsp::check_launch("colplan_scatter launch");
   if (rc) return rc;
   // one workgroup per epoch; the grid covers the upper bound pmax / E
@@ -822,7 +832,7 @@ extern "C" int tsp_csr_colplan_refresh(const void* values, int dtype, int64_t m,
   if (!values || !plan) return tsp::fail(TSP_EINVAL, "tsp_csr_colplan_refresh: null pointer");
   PlanView v = plan_view(plan, geometry);
   hipLaunchKernelGGL(colplan_refresh_kernel, dim3((unsigned)tsp::ceil_div(v.pmax, 256)), dim3(256), 0,
-                     (hipStream_t)stream, (const float*)values, v.pos, v.pmax, v.ent);
+                     (hipStream_t)stream, (const float*)values, v.pos, v.pmax, v.base, v.ent);
   return tsp::check_launch("colplan_refresh launch");
 }
 

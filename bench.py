@@ -122,6 +122,53 @@ def time_gpu_spread(fn, steps: int, warmup: int, segments: int = 5, prewarm_s: f
     return seg[len(seg) // 2], seg[0], seg[-1]
 
 
+_CLOCK_LIB = None
+
+
+def shader_clock_ghz(fn, per_call_ms: float, window_ms: float = 1.0):
+    """Shader clock (GHz) while `fn` runs back to back, or None when the probe
+    library (trnsparse_amd/libtrnsparse_clock.so) is not built.
+
+    A one-wave probe on a side stream counts shader-clock cycles over
+    `window_ms` of the 100 MHz real-time counter; it starts once a few
+    launches of `fn` have finished (an event wait) and the train continues
+    for twice the window behind it. The MFMA kernels here run at a clock the
+    power manager sets by load and by board: the same bf16 kernel costs a
+    fixed number of shader cycles, so its time moves with this figure."""
+    import ctypes
+    import math
+
+    import torch
+
+    global _CLOCK_LIB
+    if _CLOCK_LIB is None:
+        path = ROOT / "trnsparse_amd" / "libtrnsparse_clock.so"
+        if not path.exists():
+            return None
+        lib = ctypes.CDLL(str(path))
+        lib.tsp_probe_shader_clock.argtypes = [ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
+        lib.tsp_probe_shader_clock.restype = ctypes.c_int
+        _CLOCK_LIB = lib
+    dev = torch.device("cuda", torch.cuda.current_device())
+    out = torch.zeros(2, dtype=torch.int64, device=dev)
+    side = torch.cuda.Stream(device=dev)
+    lead = max(2, int(math.ceil(0.2 * window_ms / per_call_ms)))
+    tail = max(4, int(math.ceil(2.0 * window_ms / per_call_ms)))
+    torch.cuda.synchronize()
+    for _ in range(lead):
+        fn()
+    started = torch.cuda.Event()
+    started.record()
+    side.wait_event(started)
+    if _CLOCK_LIB.tsp_probe_shader_clock(int(window_ms * 1e5), out.data_ptr(), side.cuda_stream) != 0:
+        raise RuntimeError("tsp_probe_shader_clock failed")
+    for _ in range(tail):
+        fn()
+    torch.cuda.synchronize()
+    cycles, ticks = out.cpu().tolist()
+    return round(cycles / ticks * 0.1, 3) if ticks else None
+
+
 def host_cpu() -> dict:
     """The GPU box's host CPU as the CPU baselines see it: model name,
     sockets (distinct physical ids), logical CPUs in the machine and in this
@@ -198,6 +245,7 @@ def bench_bsr_fp32(steps: int, warmup: int, cpu: bool):
         "ms_per_step": wall_ms,
         "event_ms": ev_ms,
         "flops": flops,
+        "shader_ghz": shader_clock_ghz(lambda: ts.bsr_spmm(Ad, Bd), ev_ms),
         "roofline": {
             "bound": "mfma",
             "achieved": round(achieved, 2),
@@ -266,7 +314,8 @@ def bench_bsr_bf16(steps: int, warmup: int, cpu: bool = False):
     flops = 2.0 * A.n_blocks * 128 * 128 * B.shape[1]
     Ad = ts.BSRMatrix(A.blocks.cuda(), A.block_col_indices, A.block_row_ptrs, A.shape, A.block_size)
     Bd = B.cuda()
-    ev_ms, lo, hi = time_gpu_spread(lambda: ts.bsr_spmm(Ad, Bd, out_dtype=torch.float32), steps, warmup)
+    fwd = lambda: ts.bsr_spmm(Ad, Bd, out_dtype=torch.float32)
+    ev_ms, lo, hi = time_gpu_spread(fwd, steps, warmup)
     tf = flops / (ev_ms * 1e-3) / 1e12
     byts = A.n_blocks * 128 * 128 * 2 + B.numel() * 2 + B.numel() * 4
     res = {
@@ -275,6 +324,7 @@ def bench_bsr_bf16(steps: int, warmup: int, cpu: bool = False):
         "unit": "GFLOP/s",
         "us": round(ev_ms * 1e3, 1),
         "us_spread": [round(lo * 1e3, 1), round(hi * 1e3, 1)],
+        "shader_ghz": shader_clock_ghz(fwd, ev_ms),
         "frac_bf16_mfma": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
         "frac_hbm_min_bytes": round(byts / (ev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
     }
@@ -334,7 +384,8 @@ def bench_bsr_backward(steps: int, warmup: int):
             ms, lo, hi = time_gpu_spread(fn, steps, warmup)
             tf = flops / (ms * 1e-3) / 1e12
             out.append({"name": name, "value": round(tf * 1e3, 1), "unit": "GFLOP/s", "us": round(ms * 1e3, 1),
-                        "us_spread": [round(lo * 1e3, 1), round(hi * 1e3, 1)], key: round(tf / peak, 4)})
+                        "us_spread": [round(lo * 1e3, 1), round(hi * 1e3, 1)], key: round(tf / peak, 4),
+                        "shader_ghz": shader_clock_ghz(fn, ms)})
     return out
 
 
@@ -609,7 +660,8 @@ def bench_attention(steps: int, warmup: int, cpu: bool = False):
     flops = 4.0 * mask.n_blocks * 128 * 128 * D * H
     byts = 4 * H * S * D * 2
     Qd, Kd, Vd = Q.cuda(), K.cuda(), V.cuda()
-    ev_ms, lo, hi = time_gpu_spread(lambda: ts.block_sparse_attention_tiled(Qd, Kd, Vd, mask), steps, warmup)
+    fwd = lambda: ts.block_sparse_attention_tiled(Qd, Kd, Vd, mask)
+    ev_ms, lo, hi = time_gpu_spread(fwd, steps, warmup)
     tf = flops / (ev_ms * 1e-3) / 1e12
     res = {
         "name": "block_sparse_attention cfg5 32x8192x128 bf16",
@@ -617,6 +669,7 @@ def bench_attention(steps: int, warmup: int, cpu: bool = False):
         "unit": "GFLOP/s",
         "us": round(ev_ms * 1e3, 1),
         "us_spread": [round(lo * 1e3, 1), round(hi * 1e3, 1)],
+        "shader_ghz": shader_clock_ghz(fwd, ev_ms),
         "frac_bf16_mfma": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
         "frac_hbm_min_bytes": round(byts / (ev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
     }
@@ -764,7 +817,7 @@ def bench_attention_backward(steps: int, warmup: int, cpu: bool = False):
                           (FP32_MFMA_PEAK_TFLOPS, "frac_fp32_mfma", "fp32"))
         out.append({"name": f"block_sparse_attention backward cfg5 32x8192x128 {tag}", "value": round(tf * 1e3, 1),
                     "unit": "GFLOP/s", "us": round(ms * 1e3, 1), "us_spread": [round(lo * 1e3, 1), round(hi * 1e3, 1)],
-                    key: round(tf / peak, 4), "split_columns": ns, "items": ni})
+                    key: round(tf / peak, 4), "split_columns": ns, "items": ni, "shader_ghz": shader_clock_ghz(call, ms)})
         if dt == torch.bfloat16:
             keep = (Qd, Kd, Vd, O, dO, rm, rd)
     res = out[0]
@@ -1033,10 +1086,13 @@ def main(argv=None) -> int:
             "flops_per_step": head["flops"],
         },
         "roofline": head["roofline"],
+        "shader_ghz": head.get("shader_ghz"),
         "cpu_baseline": head.get("cpu_baseline"),
         "host_cpu": host_cpu(),
         "secondary": secondary,
-        "timing": "HIP events on the launch stream; untimed 0.25 s clock pre-warm of the same op, then the W warmup steps",
+        "timing": "HIP events on the launch stream; untimed 0.25 s clock pre-warm of the same op, then the W warmup steps; "
+        "shader_ghz: shader clock during a separate back-to-back train of the same op (s_memtime against the 100 MHz "
+        "s_memrealtime, one probe wave on a side stream)",
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -138,9 +138,28 @@ def build_ops(verbose: bool = False) -> pathlib.Path:
     return OPS_LIB
 
 
+# The benchmark's shader-clock probe (csrc/probe/shader_clock.hip): a library
+# of its own, outside the C ABI, loaded only by bench.py.
+CLOCK_SRC = CSRC / "probe" / "shader_clock.hip"
+CLOCK_LIB = PKG / "libtrnsparse_clock.so"
+
+
+def build_clock(verbose: bool = False) -> pathlib.Path:
+    tmp = CLOCK_LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, *CFLAGS, "-shared", str(CLOCK_SRC), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {CLOCK_SRC.name}:\n{r.stdout}{r.stderr}")
+    os.replace(tmp, CLOCK_LIB)
+    return CLOCK_LIB
+
+
 def build(verbose: bool = False, jobs: int | None = None) -> pathlib.Path:
     """Compile every `csrc/*.hip`, link the shared library, then build the
-    operator library over it. Always rebuilds."""
+    operator library over it and the benchmark's clock probe. Always
+    rebuilds."""
     BUILD.mkdir(exist_ok=True)
     srcs = _sources()
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2)))
@@ -159,6 +178,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> pathlib.Path:
         raise RuntimeError(f"link failed:\n{r.stdout}{r.stderr}")
     os.replace(tmp, LIB)
     build_ops(verbose)
+    build_clock(verbose)
     return LIB
 
 

@@ -223,45 +223,60 @@ __global__ __launch_bounds__(256) void bsr_spmm_t_f32_dma(
 //
 // bf16 operands, fp32 accumulation, bf16 results, b == 128, on
 // v_mfma_f32_32x32x16_bf16 (lane half h supplies k = 8h .. 8h + 7 of each
-// 16-k step; A rows / B columns are lane % 32). One engine for both
-// products: 256 threads, 4 waves of 64x64 (2 x 2 accumulators), 64-wide
-// k-slabs of two operand tiles streamed through a 2-stage LDS ring by direct
-// loads issued one slab ahead (4 + 4 wave instructions per slab). 64 KiB of
-// LDS lets two workgroups share a CU, so each SIMD runs one wavefront of
-// each and one's operand reads overlap the other's MFMAs: with a 4-stage
-// ring (one workgroup, one wavefront per SIMD) the LDS read latency was
-// exposed in every 16-k step and both kernels took 23-31 % longer. Each
-// operand tile is in one of two forms:
-//   ROW: [128 rows][64 k], rows of 128 B, k contiguous: a lane's 8 k values
-//        are one b128 read; chunk ^ ((row / 2) % 8) (16 consecutive rows of
-//        one chunk cover the 64 banks);
-//   TR:  [64 k][128 columns], rows of 256 B: the 8 k values come from two
+// 16-k step; A rows / B columns are lane % 32). One engine for the products:
+// 256 threads, 4 waves of 64x64 (2 x 2 accumulators), KC-wide k-slabs of two
+// operand tiles streamed through an NST-stage LDS ring by direct loads
+// issued NST - 1 slabs ahead (LPW + LPW wave instructions per slab). Each
+// kernel picks its (KC, NST): the ring is sized so that several workgroups
+// share a CU and one's operand reads and load waits overlap another's MFMAs
+// (with one workgroup and a 4-stage ring the LDS read latency was exposed in
+// every 16-k step: 23-31 % slower). Measured on cfg3b dA: KC = 64 with a
+// 2-stage ring (64 KiB, two workgroups per CU) 53-54 us; KC = 32 with a
+// 3-stage ring (48 KiB, three per CU) 44 us, with 4 or 5 stages (two per
+// CU) 49 us, KC = 64 with 3 stages (one per CU) 60 us. Each operand tile is
+// in one of two forms, TILE = 128 x KC x 2 bytes:
+//   ROW: [128 rows][KC k], rows of 2 KC bytes, k contiguous: a lane's 8 k
+//        values are one b128 read; the 16-byte chunk c of row r sits in slot
+//        c ^ sw(r) so that 16 consecutive rows of one chunk cover the 64
+//        banks (KC = 64: (r / 2) % 8; KC = 32: (r / 4) % 4);
+//   TR:  [KC k][128 columns], rows of 256 B: the 8 k values come from two
 //        ds_read_b64_tr_b16 (4 consecutive k rows each); chunk ^ 4 (row % 4).
 // dA (SDDMM): both operands ROW (dC rows of the block row, B rows of the
 // block column, k = columns). dB = A^T dC: both operands TR (the block's
 // rows are k, its columns the output rows; dC rows of the block row).
 namespace bfb {
-constexpr int KC = 64;
-constexpr int NST = 2;
-constexpr int TILE = 16384;
-constexpr int STAGE = 2 * TILE;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-// ROW tile: rows [row0, row0 + 128) x columns [k0, k0 + 64) of a bf16
+template <int KC_>
+struct Slab {
+  static constexpr int KC = KC_;
+  static_assert(KC == 32 || KC == 64, "slab widths with a conflict-free ROW swizzle");
+  static constexpr int RB = 2 * KC;            // bytes per ROW-tile row
+  static constexpr int LPR = RB / 16;          // lanes per ROW-tile row in a 1 KiB piece
+  static constexpr int RPP = 64 / LPR;         // ROW-tile rows per 1 KiB piece
+  static constexpr int TILE = 128 * RB;        // bytes per operand tile
+  static constexpr int STAGE = 2 * TILE;
+  static constexpr int LPW = TILE / 4096;      // 1 KiB pieces per wave and tile
+  __device__ static constexpr int sw(int r) { return KC == 64 ? ((r >> 1) & 7) : ((r >> 2) & 3); }
+};
+
+// ROW tile: rows [row0, row0 + 128) x columns [k0, k0 + KC) of a bf16
 // row-major matrix (stride ld) behind rs; columns at or past kend read as
 // zero (kend % 8 == 0).
 // The ROW tile stream of one operand with the per-lane offsets computed
 // once: slab s adds s * KC columns (2 bytes each) and compares with kend.
+template <int KC>
 struct RowStream {
-  uint32_t base[4];
-  int col[4];
+  using S = Slab<KC>;
+  uint32_t base[S::LPW];
+  int col[S::LPW];
   __device__ RowStream(int64_t row0, int64_t ld, int w, int lane) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int i = 4 * w + q;
-      const int r = 8 * i + (lane >> 3);
-      const int c = (lane & 7) ^ ((r >> 1) & 7);
+    for (int q = 0; q < S::LPW; ++q) {
+      const int i = S::LPW * w + q;
+      const int r = S::RPP * i + lane / S::LPR;
+      const int c = (lane % S::LPR) ^ S::sw(r);
       col[q] = c * 8;
       base[q] = (uint32_t)(((row0 + r) * ld + c * 8) * 2);
     }
@@ -270,37 +285,43 @@ struct RowStream {
     const int k0 = s * KC;
     const int lim = (int)(kend - k0);  // columns k0 + col < kend  <=>  col < lim
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < S::LPW; ++q) {
       const uint32_t off = col[q] < lim ? base[q] + (uint32_t)(k0 * 2) : OOB;
-      tsp::dma::buffer16(rs, off, dst + (4 * w + q) * 1024);
+      tsp::dma::buffer16(rs, off, dst + (S::LPW * w + q) * 1024);
     }
   }
 };
-// TR tile: rows [row0, row0 + 64) x columns [c0, c0 + 128) of a bf16
+// TR tile: rows [row0, row0 + KC) x columns [c0, c0 + 128) of a bf16
 // row-major matrix (stride ld) behind rs.
+template <int KC>
 __device__ inline void dma_tr(i32x4 rs, int64_t row0, int64_t ld, int64_t c0, uint32_t dst, int w, int lane) {
+  constexpr int LPW = Slab<KC>::LPW;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int j = 4 * w + q;
+  for (int q = 0; q < LPW; ++q) {
+    const int j = LPW * w + q;
     const int rr = 4 * j + (lane >> 4);
     const int c = (lane & 15) ^ (4 * (rr & 3));
     tsp::dma::buffer16(rs, (uint32_t)(((row0 + rr) * ld + c0 + c * 8) * 2), dst + j * 1024);
   }
 }
 // The same TR tile from a 128-column block that is always in bounds.
+template <int KC>
 __device__ inline void dma_tr_block(const uint16_t* src, uint32_t dst, int w, int lane) {
+  constexpr int LPW = Slab<KC>::LPW;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int j = 4 * w + q;
+  for (int q = 0; q < LPW; ++q) {
+    const int j = LPW * w + q;
     const int rr = 4 * j + (lane >> 4);
     const int c = (lane & 15) ^ (4 * (rr & 3));
     tsp::dma::global16(src + rr * BS + c * 8, dst + j * 1024);
   }
 }
 // Operand of 16-k step ks for tile row / column `base` + lane % 32.
+template <int KC>
 __device__ inline bf16x8 op_row(const uint8_t* tile, int base, int ks, int lane) {
+  using S = Slab<KC>;
   const int r = base + (lane & 31);
-  return *(const bf16x8*)(tile + r * 128 + (((2 * ks + (lane >> 5)) ^ ((r >> 1) & 7)) * 16));
+  return *(const bf16x8*)(tile + r * S::RB + (((2 * ks + (lane >> 5)) ^ S::sw(r)) * 16));
 }
 __device__ inline bf16x8 op_tr(const uint8_t* tile, int base, int ks, int lane) {
   const int gq = lane >> 4, jq = lane & 15;
@@ -315,34 +336,49 @@ __device__ inline bf16x8 op_tr(const uint8_t* tile, int base, int ks, int lane) 
   return __builtin_bit_cast(bf16x8, __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-// The slab loop shared by both kernels: issue(s) fills stage s % NST,
-// compute runs the 4 k-steps of a stage into acc.
-template <bool AROW, bool BROW, typename Issue>
+// Wait until this wave's loads of a slab are done while the `later` slabs
+// issued after it (LPS loads each) may still be in flight.
+template <int LPS, int NST>
+__device__ inline void wait_slab(int later) {
+  if constexpr (NST >= 4) {
+    if (later >= 2) {
+      tsp::dma::wait_vm<2 * LPS>();
+      return;
+    }
+  }
+  if constexpr (NST >= 3) {
+    if (later >= 1) {
+      tsp::dma::wait_vm<LPS>();
+      return;
+    }
+  }
+  tsp::dma::wait_vm<0>();
+}
+
+// The slab loop shared by the kernels: issue(s) fills stage s % NST,
+// compute runs the KC / 16 k-steps of a stage into acc.
+template <bool AROW, bool BROW, int KC, int NST, typename Issue>
 __device__ inline void run(Issue&& issue, int nsteps, const uint8_t* lds, f32x16 (&acc)[2][2], int wm, int wn,
                            int lane) {
+  using S = Slab<KC>;
+  static_assert(NST >= 2 && NST <= 4, "ring depths with a vmcnt schedule");
   auto fetch = [&](const uint8_t* st, int ks, bf16x8 (&a)[2], bf16x8 (&b)[2]) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      a[t] = AROW ? op_row(st, wm * 64 + 32 * t, ks, lane) : op_tr(st, wm * 64 + 32 * t, ks, lane);
-      b[t] = BROW ? op_row(st + TILE, wn * 64 + 32 * t, ks, lane) : op_tr(st + TILE, wn * 64 + 32 * t, ks, lane);
+      a[t] = AROW ? op_row<KC>(st, wm * 64 + 32 * t, ks, lane) : op_tr(st, wm * 64 + 32 * t, ks, lane);
+      b[t] = BROW ? op_row<KC>(st + S::TILE, wn * 64 + 32 * t, ks, lane) : op_tr(st + S::TILE, wn * 64 + 32 * t, ks, lane);
     }
   };
   const int pre = nsteps < NST - 1 ? nsteps : NST - 1;
   for (int s = 0; s < pre; ++s) issue(s);
   for (int s = 0; s < nsteps; ++s) {
     // this wave's loads of slab s are done when only the later slabs already
-    // issued (8 loads each, at most NST - 2 of them) are in flight
+    // issued (2 LPW loads each, at most NST - 2 of them) are in flight
     const int later0 = nsteps - 1 - s;
-    const int later = later0 < NST - 2 ? later0 : NST - 2;
-    if (later >= 2)
-      tsp::dma::wait_vm<16>();
-    else if (later == 1)
-      tsp::dma::wait_vm<8>();
-    else
-      tsp::dma::wait_vm<0>();
+    wait_slab<2 * S::LPW, NST>(later0 < NST - 2 ? later0 : NST - 2);
     tsp::dma::barrier();  // every wave's part of slab s is in LDS; stage (s - 1) % NST is free
     if (s + NST - 1 < nsteps) issue(s + NST - 1);
-    const uint8_t* st = lds + (s % NST) * STAGE;
+    const uint8_t* st = lds + (s % NST) * S::STAGE;
     bf16x8 a[2][2], b[2][2];
     fetch(st, 0, a[0], b[0]);
 #pragma unroll
@@ -359,6 +395,19 @@ __device__ inline void run(Issue&& issue, int nsteps, const uint8_t* lds, f32x16
 }
 }  // namespace bfb
 
+// Slab width and ring depth of each bf16 kernel. dA with bf16 blocks: the
+// forms listed at the engine ran 43.5-43.7 us alike on a box whose loads
+// return quickly, and 32/3 was 15-19 % faster on boxes where the same kernel
+// at 64/2 took 53-54 us at the same shader clock (more loads in flight and
+// three workgroups per CU hide the longer memory latency). Block scores with
+// fp32 output (attention at d = 512 over the stacked mask: 331 us against
+// 345 at 32/3), dB and the attention block gradient keep 64/2 (dB 44.4 us
+// against 48.0, the block gradient at d = 256 555 us against 590).
+constexpr int SDDMM_KC = 32, SDDMM_NST = 3;
+constexpr int SCORES_KC = 64, SCORES_NST = 2;
+constexpr int PGRAD_KC = 64, PGRAD_NST = 2;
+constexpr int SPMMT_KC = 64, SPMMT_NST = 2;
+
 // dA (SDDMM), bf16: workgroup per stored block, XCD x takes a contiguous
 // range of blocks as in bsr_sddmm_f32_dma. OutT uint16_t: bf16 blocks (the
 // gradient of bf16 blocks); float: the fp32 accumulators as they are (block
@@ -366,13 +415,14 @@ __device__ inline void run(Issue&& issue, int nsteps, const uint8_t* lds, f32x16
 __device__ inline void store_out(uint16_t* p, float v) { *p = tsp::f32_to_bf16_bits(v); }
 __device__ inline void store_out(float* p, float v) { *p = v; }
 
-template <typename OutT>
+template <typename OutT, int KC = SDDMM_KC, int NST = SDDMM_NST>
 __global__ __launch_bounds__(256) void bsr_sddmm_bf16_mfma(const uint16_t* __restrict__ G, int64_t ldg, int64_t m,
                                                            const uint16_t* __restrict__ B, int64_t ldb, int64_t n,
                                                            int64_t ncols, const int64_t* __restrict__ brow,
                                                            const int64_t* __restrict__ ci, int64_t nnzb,
                                                            OutT* __restrict__ out) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[bfb::NST * bfb::STAGE];
+  using S = bfb::Slab<KC>;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * S::STAGE];
   const int64_t g = blockIdx.x, xcd = g & 7, slot = g >> 3;
   const int64_t per = tsp::ceil_div(nnzb, 8);
   const int64_t kb = xcd * per + slot;
@@ -383,18 +433,18 @@ __global__ __launch_bounds__(256) void bsr_sddmm_bf16_mfma(const uint16_t* __res
   const i32x4 rsg = tsp::dma::make_rsrc(G, (uint32_t)(m * ldg * 2));
   const i32x4 rsb = tsp::dma::make_rsrc(B, (uint32_t)(n * ldb * 2));
   const uint32_t lds0 = tsp::dma::lds_addr(lds);
-  const bfb::RowStream sg(i * BS, ldg, w, lane), sb(j * BS, ldb, w, lane);
+  const bfb::RowStream<KC> sg(i * BS, ldg, w, lane), sb(j * BS, ldb, w, lane);
   auto issue = [&](int s) {
-    const uint32_t st = lds0 + (s % bfb::NST) * bfb::STAGE;
+    const uint32_t st = lds0 + (s % NST) * S::STAGE;
     sg.issue(rsg, s, ncols, st, w);
-    sb.issue(rsb, s, ncols, st + bfb::TILE, w);
+    sb.issue(rsb, s, ncols, st + S::TILE, w);
   };
   f32x16 acc[2][2];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int u = 0; u < 2; ++u) acc[t][u] = f32x16{};
-  bfb::run<true, true>(issue, (int)tsp::ceil_div(ncols, bfb::KC), lds, acc, wm, wn, lane);
+  bfb::run<true, true, KC, NST>(issue, (int)tsp::ceil_div(ncols, KC), lds, acc, wm, wn, lane);
   // dA block kb, row-major: lane holds column l32 and rows 8 (v / 4) + 4 h + v % 4
   OutT* ob = out + kb * (BS * BS);
 #pragma unroll
@@ -416,13 +466,15 @@ __global__ __launch_bounds__(256) void bsr_sddmm_bf16_mfma(const uint16_t* __res
 //   P  = exp(scale S - row_max) / row_denom,   dS = scale P (dP - Drow)
 // are written as bf16 blocks (reference trnsparse/ops.py:461-467). The fp32
 // scores never leave the workgroup.
+template <int KC = PGRAD_KC, int NST = PGRAD_NST>
 __global__ __launch_bounds__(256) void bsa_block_pgrad_bf16(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     const uint16_t* __restrict__ dO, int64_t rows, int64_t D, const int64_t* __restrict__ brow,
     const int64_t* __restrict__ ci, int64_t nnzb, float scale, const float* __restrict__ rmax,
     const float* __restrict__ rden, const float* __restrict__ Drow, uint16_t* __restrict__ P,
     uint16_t* __restrict__ dS) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[bfb::NST * bfb::STAGE];
+  using S = bfb::Slab<KC>;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * S::STAGE];
   __shared__ float rstat[3][BS];
   const int64_t g = blockIdx.x, xcd = g & 7, slot = g >> 3;
   const int64_t per = tsp::ceil_div(nnzb, 8);
@@ -440,9 +492,9 @@ __global__ __launch_bounds__(256) void bsa_block_pgrad_bf16(
   const i32x4 rq = tsp::dma::make_rsrc(Q, bytes), rk = tsp::dma::make_rsrc(K, bytes);
   const i32x4 rv = tsp::dma::make_rsrc(V, bytes), rdo = tsp::dma::make_rsrc(dO, bytes);
   const uint32_t lds0 = tsp::dma::lds_addr(lds);
-  const bfb::RowStream sq(i * BS, D, w, lane), sk(j * BS, D, w, lane);
-  const bfb::RowStream sdo(i * BS, D, w, lane), sv(j * BS, D, w, lane);
-  const int nsteps = (int)tsp::ceil_div(D, bfb::KC);
+  const bfb::RowStream<KC> sq(i * BS, D, w, lane), sk(j * BS, D, w, lane);
+  const bfb::RowStream<KC> sdo(i * BS, D, w, lane), sv(j * BS, D, w, lane);
+  const int nsteps = (int)tsp::ceil_div(D, KC);
   f32x16 as[2][2], ap[2][2];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
@@ -452,18 +504,18 @@ __global__ __launch_bounds__(256) void bsa_block_pgrad_bf16(
       ap[t][u] = f32x16{};
     }
   auto issue_s = [&](int s) {
-    const uint32_t st = lds0 + (s % bfb::NST) * bfb::STAGE;
+    const uint32_t st = lds0 + (s % NST) * S::STAGE;
     sq.issue(rq, s, D, st, w);
-    sk.issue(rk, s, D, st + bfb::TILE, w);
+    sk.issue(rk, s, D, st + S::TILE, w);
   };
-  bfb::run<true, true>(issue_s, nsteps, lds, as, wm, wn, lane);
+  bfb::run<true, true, KC, NST>(issue_s, nsteps, lds, as, wm, wn, lane);
   tsp::dma::barrier();  // every wave has read its last stage before the ring refills
   auto issue_p = [&](int s) {
-    const uint32_t st = lds0 + (s % bfb::NST) * bfb::STAGE;
+    const uint32_t st = lds0 + (s % NST) * S::STAGE;
     sdo.issue(rdo, s, D, st, w);
-    sv.issue(rv, s, D, st + bfb::TILE, w);
+    sv.issue(rv, s, D, st + S::TILE, w);
   };
-  bfb::run<true, true>(issue_p, nsteps, lds, ap, wm, wn, lane);
+  bfb::run<true, true, KC, NST>(issue_p, nsteps, lds, ap, wm, wn, lane);
   // lane holds column l32 of each 32-column tile and rows 8 (v / 4) + 4 h + v % 4.
   // Rows v and v + 1 (v even) are adjacent: neighbouring lanes swap one value
   // (DPP quad_perm [1,0,3,2]) so that the even lane stores row v's two
@@ -498,11 +550,14 @@ __global__ __launch_bounds__(256) void bsa_block_pgrad_bf16(
 
 // dB = A^T dC, bf16: workgroup per (block column, 128-column tile) in the
 // forward's schedule, walking the column's blocks.
+template <int KC = SPMMT_KC, int NST = SPMMT_NST>
 __global__ __launch_bounds__(256) void bsr_spmm_t_bf16_mfma(
     const uint16_t* __restrict__ blocks, const int64_t* __restrict__ cp, const int64_t* __restrict__ cbid,
     const int64_t* __restrict__ crow, int64_t nbc, int nt, const uint16_t* __restrict__ X, int64_t ldx, int64_t m,
     int64_t ncols, uint16_t* __restrict__ out, int64_t ldo, int64_t n, const int32_t* __restrict__ order) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[bfb::NST * bfb::STAGE];
+  using S = bfb::Slab<KC>;
+  constexpr int SPB = BS / KC;  // slabs per block
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * S::STAGE];
   int64_t col;
   int ntile;
   if (!T32::tile_item(blockIdx.x, nbc, nt, order, col, ntile)) return;
@@ -527,19 +582,19 @@ __global__ __launch_bounds__(256) void bsr_spmm_t_bf16_mfma(
     };
     load_ids(0);
     auto issue = [&](int s) {
-      const int b = s >> 1;
+      const int b = s / SPB;
       if (b - cbase >= 64) {
         cbase = b & ~63;
         load_ids(cbase);
       }
       const int64_t kb = __builtin_amdgcn_readlane(idv, b - cbase);
       const int64_t ib = __builtin_amdgcn_readlane(rowv, b - cbase);
-      const int kk = (s & 1) * bfb::KC;
-      const uint32_t st = lds0 + (s % bfb::NST) * bfb::STAGE;
-      bfb::dma_tr_block(blocks + kb * (BS * BS) + kk * BS, st, w, lane);
-      bfb::dma_tr(rsx, ib * BS + kk, ldx, n0, st + bfb::TILE, w, lane);
+      const int kk = (s % SPB) * KC;
+      const uint32_t st = lds0 + (s % NST) * S::STAGE;
+      bfb::dma_tr_block<KC>(blocks + kb * (BS * BS) + kk * BS, st, w, lane);
+      bfb::dma_tr<KC>(rsx, ib * BS + kk, ldx, n0, st + S::TILE, w, lane);
     };
-    bfb::run<false, false>(issue, nblk * (BS / bfb::KC), lds, acc, wm, wn, lane);
+    bfb::run<false, false, KC, NST>(issue, nblk * SPB, lds, acc, wm, wn, lane);
   }
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -821,7 +876,7 @@ extern "C" int tsp_bsr_sddmm_ex(const void* G, int64_t ldg, int64_t m, const voi
                      "aligned operands under 4 GiB");
   const int64_t grid = tsp::ceil_div(n_blocks, 8) * 8;
   if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_sddmm_ex: too many blocks");
-  hipLaunchKernelGGL((bsr_sddmm_bf16_mfma<float>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL((bsr_sddmm_bf16_mfma<float, SCORES_KC, SCORES_NST>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)G, ldg, m, (const uint16_t*)B, ldb, n, ncols, block_rows, block_col_indices,
                      n_blocks, (float*)out_blocks);
   return tsp::check_launch("bsr_sddmm_bf16_mfma<float> launch");
@@ -844,7 +899,7 @@ extern "C" int tsp_bsa_block_pgrad(const void* Q, const void* K, const void* V, 
                      "tsp_bsa_block_pgrad: head_dim a multiple of 8, 16-byte aligned operands under 4 GiB");
   const int64_t grid = tsp::ceil_div(n_blocks, 8) * 8;
   if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_block_pgrad: too many blocks");
-  hipLaunchKernelGGL(bsa_block_pgrad_bf16, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)Q,
+  hipLaunchKernelGGL((bsa_block_pgrad_bf16<>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)Q,
                      (const uint16_t*)K, (const uint16_t*)V, (const uint16_t*)dO, rows, head_dim, block_rows,
                      block_col_indices, n_blocks, (float)scale, row_max, row_denom, Drow, (uint16_t*)P,
                      (uint16_t*)dS);
@@ -879,7 +934,7 @@ extern "C" int tsp_bsr_spmm_t(const void* blocks, int dtype, const int64_t* col_
     const int64_t nt = tsp::ceil_div(ncols, BS);
     const int64_t grid = tsp::ceil_div(n_block_cols, 8) * 8 * nt;
     if (grid > INT32_MAX || nt > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm_t: problem too large");
-    hipLaunchKernelGGL(bsr_spmm_t_bf16_mfma, dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)blocks, col_ptrs,
+    hipLaunchKernelGGL((bsr_spmm_t_bf16_mfma<>), dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)blocks, col_ptrs,
                        col_block_ids, col_block_rows, n_block_cols, (int)nt, (const uint16_t*)X, ldx, m, ncols,
                        (uint16_t*)out, ldo, n, col_order);
     return tsp::check_launch("bsr_spmm_t_bf16_mfma launch");

@@ -276,7 +276,7 @@ def bench_bsr_fp32(steps: int, warmup: int, cpu: bool):
 
 
 def bench_bsr_small(steps: int, warmup: int):
-    """bsr_spmm with block sizes 16, 32 and 64 (bsr_spmm_small) on cfg3's
+    """bsr_spmm with block sizes 8, 16, 32 and 64 (bsr_spmm_small) on cfg3's
     dense size (16384 x 16384, N = 512) and block density (10 %, banded plus
     uniform), fp32: GFLOP/s over the stored blocks."""
     import torch
@@ -288,7 +288,7 @@ def bench_bsr_small(steps: int, warmup: int):
     n, N = 16384, 512
     g = torch.Generator().manual_seed(21)
     B = torch.randn(n, N, generator=g).cuda()
-    for b in (16, 32, 64):
+    for b in (8, 16, 32, 64):
         nb = n // b
         mask = W.cfg3_block_mask(nb, half_band=3 * 128 // b, density=0.10, seed=22)
         blocks = torch.randn(int(mask.sum()), b, b, generator=g)

@@ -67,7 +67,7 @@ def test_reference_grid(hip_backend, m_blocks, n_blocks, N, density):
 @pytest.mark.parametrize(
     "shape,b,N,density",
     [
-        ((24, 24), 8, 16, 0.5),  # reference tests/test_bsr.py:68-74 (generic kernel)
+        ((24, 24), 8, 16, 0.5),  # reference tests/test_bsr.py:68-74 (b = 8: 4x4x1 MFMA kernel)
         ((20, 14), 8, 10, 1.0),  # unaligned, :76-83
         ((40, 40), 8, 12, 0.1),  # sparse, :85-93
         ((200, 137), 128, 64, 1.0),  # unaligned 128-blocks (MFMA kernel bounds)
@@ -92,6 +92,13 @@ def test_shapes(hip_backend, shape, b, N, density):
 @pytest.mark.parametrize(
     "shape,b,N,density",
     [
+        ((64, 64), 8, 64, 0.6),       # b = 8: whole tiles
+        ((200, 150), 8, 37, 0.5),     # b = 8: ragged m, n, partial column tile
+        ((96, 96), 8, 130, 0.4),      # b = 8: three column tiles, the last partial
+        ((330, 260), 8, 1000, 0.4),   # b = 8: 16 column tiles
+        ((64, 1024), 8, 96, 0.9),     # b = 8: long block rows (over 100 blocks)
+        ((200, 150), 8, 256, 0.5),    # b = 8: 16-byte B rows, the last block column past n element-wise
+        ((136, 136), 8, 384, 0.7),    # b = 8: three full 128-column tiles
         ((64, 64), 16, 64, 0.6),      # whole tiles
         ((200, 150), 16, 37, 0.5),    # ragged m, n (B rows past n read as zero), partial column tile
         ((96, 96), 32, 130, 0.4),     # three column tiles, the last partial
@@ -105,7 +112,7 @@ def test_shapes(hip_backend, shape, b, N, density):
 )
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_small_block_mfma(hip_backend, shape, b, N, density, dtype):
-    """b in {16, 32, 64} runs bsr_spmm_small (fp32 MFMA; bf16 widened at the
+    """b in {8, 16, 32, 64} runs bsr_spmm_small (fp32 MFMA; bf16 widened at the
     load), with empty block rows mixed in; fp32 out for fp32, bf16 in -> fp32
     and bf16 out."""
     g = torch.Generator().manual_seed(b + N)

@@ -24,10 +24,11 @@
 //                      transpose reads).
 //   bsr_spmm_f64_dma   b == 128, fp64 (v_mfma_f64_16x16x4_f64, the streamed
 //                      structure of bsr_spmm_f32_dma).
-//   bsr_spmm_small<b>  b in {16, 32, 64}, fp32 or bf16 in (fp32 MFMA, bf16
-//                      widened exactly at the load), fp32 / bf16 out: a
+//   bsr_spmm_small<b>  b in {8, 16, 32, 64}, fp32 or bf16 in (fp32 MFMA,
+//                      bf16 widened exactly at the load), fp32 / bf16 out: a
 //                      wavefront per (block row, 64 columns of C), operands
-//                      straight from memory into MFMA registers.
+//                      straight from memory into MFMA registers (b = 8 on
+//                      the 16-product 4x4x1 form).
 //   bsr_spmm_generic   any block size / dtype (f32, f64, bf16): one thread per
 //                      output element, a plain dot product over stored blocks.
 //
@@ -566,7 +567,7 @@ __global__ __launch_bounds__(512) void bsr_spmm_bf16_mfma(
 
 // ------------------------------------------------------ small block sizes
 //
-// bsr_spmm_small<BSZ>: b = 16, 32 or 64. A block row of C is only b rows, so
+// bsr_spmm_small<BSZ>: b = 8, 16, 32 or 64. A block row of C is only b rows, so
 // a wavefront owns one (block row, 64-column) tile of C and walks the row's
 // stored blocks with its operands loaded directly into registers (4 waves
 // per workgroup take consecutive column tiles of one block row and share
@@ -576,6 +577,9 @@ __global__ __launch_bounds__(512) void bsr_spmm_bf16_mfma(
 //     lane's A values for four MFMAs are one 16-byte read of its block row
 //     (8 bytes for bf16) and its B values four loads of rows 8g + 4h + c,
 //     coalesced over the 32 columns of the subtile;
+//   b = 8: v_mfma_f32_4x4x1_16b_f32 (16 products of 4x4 per instruction
+//     as 2 row groups x 8 column groups, two instructions per k for the 64
+//     columns), 8 k-steps per block;
 //   b = 16: v_mfma_f32_16x16x4_f32, 4 column subtiles; lane group q = lane/16
 //     supplies k = 4q + c at step c, one 16-byte A read per block.
 // B rows at or past n read as zero, C rows past m and columns past ncols are
@@ -592,22 +596,113 @@ __device__ inline f32x4 load4_acc<uint16_t>(const uint16_t* p) {
                tsp::bf16_bits_to_f32(v[3])};
 }
 
+// 4 consecutive outputs of one row as one store (16 bytes fp32, 8 bytes bf16)
+__device__ inline void store4_out(float* p, f32x4 v) { *(f32x4*)p = v; }
+__device__ inline void store4_out(uint16_t* p, f32x4 v) {
+  typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+  *(u16x4*)p = u16x4{tsp::f32_to_bf16_bits(v[0]), tsp::f32_to_bf16_bits(v[1]), tsp::f32_to_bf16_bits(v[2]),
+                     tsp::f32_to_bf16_bits(v[3])};
+}
+
 template <int BSZ, typename T, typename OutT>
 __global__ __launch_bounds__(256) void bsr_spmm_small(const T* __restrict__ blocks, const int64_t* __restrict__ rp,
                                                       const int64_t* __restrict__ ci, int64_t mb, int64_t m, int64_t n,
                                                       const T* __restrict__ B, int64_t ldb, int64_t ncols,
-                                                      OutT* __restrict__ C, int64_t ldc, int64_t nct) {
-  static_assert(BSZ == 16 || BSZ == 32 || BSZ == 64, "block size");
+                                                      OutT* __restrict__ C, int64_t ldc, int64_t nct, int vec) {
+  static_assert(BSZ == 8 || BSZ == 16 || BSZ == 32 || BSZ == 64, "block size");
+  constexpr int TW = BSZ == 8 ? 128 : 64;  // columns of C per wavefront
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t item = (int64_t)blockIdx.x * 4 + w;  // (block row, 64-column tile)
+  // XCD x (= blockIdx % 8) takes the x-th eighth of the workgroups in row
+  // order, so neighbouring block rows (which share the B panels of a band)
+  // run on one L2; the grid is 8 * per workgroups
+  const int64_t per = gridDim.x >> 3;
+  const int64_t wg = (int64_t)(blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  const int64_t item = wg * 4 + w;  // (block row, column tile)
   const int64_t row = item / nct;
   if (row >= mb) return;
-  const int64_t n0 = (item - row * nct) * 64;
+  const int64_t n0 = (item - row * nct) * TW;
   const int64_t start = rp[row], end = rp[row + 1];
   auto bval = [&](int64_t k, int64_t c) {
     return k < n && c < ncols ? tsp::to_acc<T>(B[k * ldb + c]) : 0.f;
   };
-  if constexpr (BSZ == 16) {
+  if constexpr (BSZ == 8) {
+    // v_mfma_f32_4x4x1_16b_f32: 16 independent 4x4 outer products (k = 1)
+    // per instruction; lane l feeds product l/4 = (row group l/32, column
+    // group (l/4) % 8): A row ra = 4 (l/32) + l%4 and one B column, and
+    // holds its C rows 4 (l/32) + i (register i) of that column. The
+    // wavefront's 128 columns are 4 groups u of 32: lane l's column in group
+    // u is n0 + 4 (l%32) + u, so one 16-byte load per lane reads a B row's
+    // 4 columns of the lane in all groups. The two lane halves load two
+    // consecutive k rows (row 2p + l/32); v_permlane32_swap of a loaded
+    // value with itself gives every lane both rows (r[0] from the low half,
+    // r[1] from the high half). Per stored block: 4 B loads, 16 swaps, 32
+    // MFMAs (k in order, so each sum runs in the generic kernel's order).
+    // Tiles at the right edge, blocks past n, or unaligned B read element by
+    // element in the same lane layout.
+    const int m32 = lane & 31, hh = lane >> 5;
+    const int ra = 4 * hh + (lane & 3);
+    const int64_t nc = n0 + 4 * m32;  // the lane's column in group 0
+    f32x4 acc[4] = {f32x4{}, f32x4{}, f32x4{}, f32x4{}};
+    const int64_t nst = end - start;
+    const bool cfull = (vec & 1) && n0 + 128 <= ncols;
+    struct Ops {
+      f32x4 a[2];
+      f32x4 b[4];  // b[p]: row kb + 2p + l/32, the lane's column in each group
+    };
+    auto load = [&](int64_t st_, Ops& o) {
+      const int64_t idx = start + (st_ < nst ? st_ : nst - 1);
+      const int64_t kb = ci[idx] * BSZ;
+      const T* ar = blocks + idx * (BSZ * BSZ) + ra * BSZ;
+      o.a[0] = load4_acc<T>(ar);
+      o.a[1] = load4_acc<T>(ar + 4);
+      if (cfull && kb + BSZ <= n) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o.b[q] = load4_acc<T>(B + (kb + 2 * q + hh) * ldb + nc);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) o.b[q][u] = bval(kb + 2 * q + hh, nc + u);
+      }
+    };
+    auto mma = [&](const Ops& o) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(o.b[q][u]), __float_as_uint(o.b[q][u]),
+                                                          false, false);
+          acc[u] = __builtin_amdgcn_mfma_f32_4x4x1f32(o.a[q >> 1][2 * (q & 1)], __uint_as_float(r[0]), acc[u], 0, 0, 0);
+          acc[u] = __builtin_amdgcn_mfma_f32_4x4x1f32(o.a[q >> 1][2 * (q & 1) + 1], __uint_as_float(r[1]), acc[u], 0, 0, 0);
+        }
+    };
+    if (nst > 0) {
+      Ops o0, o1;
+      load(0, o0);
+      int64_t st_ = 0;
+      for (; st_ + 1 < nst; st_ += 2) {
+        load(st_ + 1, o1);
+        mma(o0);
+        load(st_ + 2, o0);
+        mma(o1);
+      }
+      if (st_ < nst) mma(o0);
+    }
+    const bool vstore = cfull && (vec & 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t rr = row * BSZ + 4 * hh + i;
+      if (rr >= m) continue;
+      OutT* cr = C + rr * ldc + nc;
+      if (vstore) {
+        store4_out(cr, f32x4{acc[0][i], acc[1][i], acc[2][i], acc[3][i]});
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (nc + u < ncols) cr[u] = tsp::from_acc<OutT>(acc[u][i]);
+      }
+    }
+  } else if constexpr (BSZ == 16) {
     const int l16 = lane & 15, q = lane >> 4;
     f32x4 acc[4];
 #pragma unroll
@@ -701,13 +796,18 @@ __global__ __launch_bounds__(256) void bsr_spmm_small(const T* __restrict__ bloc
 template <typename T, typename OutT>
 int launch_small(int64_t bs, const void* blocks, const int64_t* rp, const int64_t* ci, int64_t mb, int64_t m, int64_t n,
                  const void* B, int64_t ldb, int64_t ncols, void* C, int64_t ldc, hipStream_t st) {
-  const int64_t nct = tsp::ceil_div(ncols, 64);
-  const int64_t grid = tsp::ceil_div(mb * nct, 4);
+  const int64_t nct = tsp::ceil_div(ncols, bs == 8 ? 128 : 64);
+  const int64_t grid = tsp::ceil_div(tsp::ceil_div(mb * nct, 4), 8) * 8;
   if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm: problem too large");
+  // b = 8: bit 0, B rows read 4 columns at a time (aligned); bit 1, C written 4 columns at a time
+  const int vec = (((uintptr_t)B % (4 * sizeof(T))) == 0 && ldb % 4 == 0 ? 1 : 0) |
+                  (((uintptr_t)C % (4 * sizeof(OutT))) == 0 && ldc % 4 == 0 ? 2 : 0);
 #define TSP_SMALL(BSZ)                                                                                              \
   hipLaunchKernelGGL((bsr_spmm_small<BSZ, T, OutT>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)blocks, rp, ci, \
-                     mb, m, n, (const T*)B, ldb, ncols, (OutT*)C, ldc, nct)
-  if (bs == 16)
+                     mb, m, n, (const T*)B, ldb, ncols, (OutT*)C, ldc, nct, vec)
+  if (bs == 8)
+    TSP_SMALL(8);
+  else if (bs == 16)
     TSP_SMALL(16);
   else if (bs == 32)
     TSP_SMALL(32);
@@ -859,7 +959,7 @@ extern "C" int tsp_bsr_spmm(const void* blocks, int dtype, const int64_t* block_
                        block_col_indices, mb, (int)nt, m, n, (const double*)B, ldb, ncols, (double*)C, ldc, row_order);
     return tsp::check_launch("bsr_spmm_f64_dma launch");
   }
-  if ((block_size == 16 || block_size == 32 || block_size == 64) && ((uintptr_t)blocks % 16) == 0) {
+  if ((block_size == 8 || block_size == 16 || block_size == 32 || block_size == 64) && ((uintptr_t)blocks % 16) == 0) {
     if (dtype == TSP_F32)
       return launch_small<float, float>(block_size, blocks, block_row_ptrs, block_col_indices, mb, m, n, B, ldb, ncols,
                                         C, ldc, st);

@@ -575,13 +575,20 @@ __global__ __launch_bounds__(512) void bsr_spmm_bf16_mfma(
 //   b = 32, 64: v_mfma_f32_32x32x2_f32, b/32 row subtiles x 2 column
 //     subtiles; at step 4g + c lane half h supplies k = 8g + 4h + c, so the
 //     lane's A values for four MFMAs are one 16-byte read of its block row
-//     (8 bytes for bf16) and its B values four loads of rows 8g + 4h + c,
-//     coalesced over the 32 columns of the subtile;
+//     (8 bytes for bf16); its column in subtile u is n0 + 2 (lane % 32) + u,
+//     so its B values of both subtiles are one 8-byte read of row
+//     8g + 4h + c;
 //   b = 8: v_mfma_f32_4x4x1_16b_f32 (16 products of 4x4 per instruction
-//     as 2 row groups x 8 column groups, two instructions per k for the 64
-//     columns), 8 k-steps per block;
+//     as 2 row groups x 8 column groups, 4 instructions per k for the 128
+//     columns), 8 k-steps per block; B rows as 16-byte reads split between
+//     the lane halves by v_permlane32_swap;
 //   b = 16: v_mfma_f32_16x16x4_f32, 4 column subtiles; lane group q = lane/16
-//     supplies k = 4q + c at step c, one 16-byte A read per block.
+//     supplies k = 4q + c at step c, one 16-byte A read per block; the
+//     lane's column in subtile u is n0 + 4 (lane % 16) + u, one 16-byte B
+//     read per step.
+// The output column of a lane is its B column, so the column permutation
+// needs no shuffle; full column tiles of whole blocks with aligned B use the
+// vector reads, the others read element by element in the same layout.
 // B rows at or past n read as zero, C rows past m and columns past ncols are
 // not written.
 template <typename T>
@@ -596,6 +603,20 @@ __device__ inline f32x4 load4_acc<uint16_t>(const uint16_t* p) {
                tsp::bf16_bits_to_f32(v[3])};
 }
 
+template <typename T>
+__device__ inline f32x2 load2_acc(const T* p);
+template <>
+__device__ inline f32x2 load2_acc<float>(const float* p) { return *(const f32x2*)p; }
+template <>
+__device__ inline f32x2 load2_acc<uint16_t>(const uint16_t* p) {
+  const uint32_t v = *(const uint32_t*)p;
+  return f32x2{tsp::bf16_bits_to_f32((uint16_t)(v & 0xffffu)), tsp::bf16_bits_to_f32((uint16_t)(v >> 16))};
+}
+// 2 consecutive outputs of one row as one store (8 bytes fp32, 4 bytes bf16)
+__device__ inline void store2_out(float* p, float a, float b) { *(f32x2*)p = f32x2{a, b}; }
+__device__ inline void store2_out(uint16_t* p, float a, float b) {
+  *(uint32_t*)p = (uint32_t)tsp::f32_to_bf16_bits(a) | ((uint32_t)tsp::f32_to_bf16_bits(b) << 16);
+}
 // 4 consecutive outputs of one row as one store (16 bytes fp32, 8 bytes bf16)
 __device__ inline void store4_out(float* p, f32x4 v) { *(f32x4*)p = v; }
 __device__ inline void store4_out(uint16_t* p, f32x4 v) {
@@ -703,31 +724,42 @@ __global__ __launch_bounds__(256) void bsr_spmm_small(const T* __restrict__ bloc
       }
     }
   } else if constexpr (BSZ == 16) {
+    // lane group q = lane / 16 supplies k = 4q + c at step c; lane l16's
+    // column in subtile u is n0 + 4 l16 + u, so one 16-byte load per step
+    // reads its B row's columns of all 4 subtiles
     const int l16 = lane & 15, q = lane >> 4;
+    const int64_t nc = n0 + 4 * l16;
+    const bool cfull = (vec & 1) && n0 + 64 <= ncols;
     f32x4 acc[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) acc[u] = f32x4{};
     // one step per stored block; the next block's operands load while this one's MFMAs run
     // (the last block is loaded again past the end, so the loop has no conditional loads)
     const int64_t nst = end - start;
-    auto load = [&](int64_t st_, f32x4& a, float (&bv)[4][4]) {
+    auto load = [&](int64_t st_, f32x4& a, f32x4 (&bq)[4]) {
       const int64_t idx = start + (st_ < nst ? st_ : nst - 1);
-      const int64_t kb = ci[idx] * BSZ + 4 * q;
+      const int64_t k0 = ci[idx] * BSZ;
+      const int64_t kb = k0 + 4 * q;
       a = load4_acc<T>(blocks + idx * (BSZ * BSZ) + l16 * BSZ + 4 * q);
+      if (cfull && k0 + BSZ <= n) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+        for (int c = 0; c < 4; ++c) bq[c] = load4_acc<T>(B + (kb + c) * ldb + nc);
+      } else {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) bv[u][c] = bval(kb + c, n0 + 16 * u + l16);
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) bq[c][u] = bval(kb + c, nc + u);
+      }
     };
-    auto mma = [&](const f32x4& a, const float (&bv)[4][4]) {
+    auto mma = [&](const f32x4& a, const f32x4 (&bq)[4]) {
 #pragma unroll
       for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c], bv[u][c], acc[u], 0, 0, 0);
+        for (int u = 0; u < 4; ++u) acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c], bq[c][u], acc[u], 0, 0, 0);
     };
     if (nst > 0) {
       f32x4 a0, a1;
-      float b0[4][4], b1[4][4];
+      f32x4 b0[4], b1[4];
       load(0, a0, b0);
       int64_t st_ = 0;
       for (; st_ + 1 < nst; st_ += 2) {
@@ -738,58 +770,77 @@ __global__ __launch_bounds__(256) void bsr_spmm_small(const T* __restrict__ bloc
       }
       if (st_ < nst) mma(a0, b0);
     }
-    // element r of subtile u: row 4q + r, column 16u + l16
+    // element r of subtile u: row 4q + r, column n0 + 4 l16 + u
+    const bool vstore = cfull && (vec & 2);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int64_t c = n0 + 16 * u + l16;
-      if (c >= ncols) continue;
+    for (int r = 0; r < 4; ++r) {
+      const int64_t rr = row * BSZ + 4 * q + r;
+      if (rr >= m) continue;
+      OutT* cr = C + rr * ldc + nc;
+      if (vstore) {
+        store4_out(cr, f32x4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]});
+      } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t rr = row * BSZ + 4 * q + r;
-        if (rr < m) C[rr * ldc + c] = tsp::from_acc<OutT>(acc[u][r]);
+        for (int u = 0; u < 4; ++u)
+          if (nc + u < ncols) cr[u] = tsp::from_acc<OutT>(acc[u][r]);
       }
     }
   } else {
+    // lane half h supplies k = 8g + 4h + c at step (g, c); lane l32's column
+    // in subtile u is n0 + 2 l32 + u, so one 8-byte load per step reads its
+    // B row's columns of both subtiles
     constexpr int RT = BSZ / 32;
     const int h = lane >> 5, l32 = lane & 31;
+    const int64_t nc = n0 + 2 * l32;
+    const bool cfull = (vec & 4) && n0 + 64 <= ncols;
     f32x16 acc[RT][2];
 #pragma unroll
     for (int t = 0; t < RT; ++t) acc[t][0] = acc[t][1] = f32x16{};
     for (int64_t idx = start; idx < end; ++idx) {
       const int64_t kb = ci[idx] * BSZ;
+      const bool bfull = cfull && kb + BSZ <= n;
       const T* Ab = blocks + idx * (BSZ * BSZ);
 #pragma unroll
       for (int g = 0; g < BSZ / 8; ++g) {
         f32x4 a[RT];
 #pragma unroll
         for (int t = 0; t < RT; ++t) a[t] = load4_acc<T>(Ab + (32 * t + l32) * BSZ + 8 * g + 4 * h);
-        float bv[2][4];
+        f32x2 bv[4];
+        if (bfull) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+          for (int c = 0; c < 4; ++c) bv[c] = load2_acc<T>(B + (kb + 8 * g + 4 * h + c) * ldb + nc);
+        } else {
 #pragma unroll
-          for (int c = 0; c < 4; ++c) bv[u][c] = bval(kb + 8 * g + 4 * h + c, n0 + 32 * u + l32);
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) bv[c][u] = bval(kb + 8 * g + 4 * h + c, nc + u);
+        }
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
           for (int t = 0; t < RT; ++t)
 #pragma unroll
             for (int u = 0; u < 2; ++u)
-              acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t][c], bv[u][c], acc[t][u], 0, 0, 0);
+              acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t][c], bv[c][u], acc[t][u], 0, 0, 0);
       }
     }
-    // element v of subtile (t, u): row 32t + 8(v/4) + 4h + v%4, column 32u + l32
+    // element v of subtile (t, u): row 32t + 8(v/4) + 4h + v%4, column n0 + 2 l32 + u
+    const bool vstore = cfull && (vec & 8);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int64_t c = n0 + 32 * u + l32;
-      if (c >= ncols) continue;
+    for (int t = 0; t < RT; ++t)
 #pragma unroll
-      for (int t = 0; t < RT; ++t)
+      for (int v = 0; v < 16; ++v) {
+        const int64_t rr = row * BSZ + 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (rr >= m) continue;
+        OutT* cr = C + rr * ldc + nc;
+        if (vstore) {
+          store2_out(cr, acc[t][0][v], acc[t][1][v]);
+        } else {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t rr = row * BSZ + 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
-          if (rr < m) C[rr * ldc + c] = tsp::from_acc<OutT>(acc[t][u][v]);
+          for (int u = 0; u < 2; ++u)
+            if (nc + u < ncols) cr[u] = tsp::from_acc<OutT>(acc[t][u][v]);
         }
-    }
+      }
   }
 }
 
@@ -799,9 +850,12 @@ int launch_small(int64_t bs, const void* blocks, const int64_t* rp, const int64_
   const int64_t nct = tsp::ceil_div(ncols, bs == 8 ? 128 : 64);
   const int64_t grid = tsp::ceil_div(tsp::ceil_div(mb * nct, 4), 8) * 8;
   if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm: problem too large");
-  // b = 8: bit 0, B rows read 4 columns at a time (aligned); bit 1, C written 4 columns at a time
+  // bits 0 / 1: B rows read / C rows written 4 columns at a time (b = 8, 16);
+  // bits 2 / 3: 2 columns at a time (b = 32, 64)
   const int vec = (((uintptr_t)B % (4 * sizeof(T))) == 0 && ldb % 4 == 0 ? 1 : 0) |
-                  (((uintptr_t)C % (4 * sizeof(OutT))) == 0 && ldc % 4 == 0 ? 2 : 0);
+                  (((uintptr_t)C % (4 * sizeof(OutT))) == 0 && ldc % 4 == 0 ? 2 : 0) |
+                  (((uintptr_t)B % (2 * sizeof(T))) == 0 && ldb % 2 == 0 ? 4 : 0) |
+                  (((uintptr_t)C % (2 * sizeof(OutT))) == 0 && ldc % 2 == 0 ? 8 : 0);
 #define TSP_SMALL(BSZ)                                                                                              \
   hipLaunchKernelGGL((bsr_spmm_small<BSZ, T, OutT>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)blocks, rp, ci, \
                      mb, m, n, (const T*)B, ldb, ncols, (OutT*)C, ldc, nct, vec)

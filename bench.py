@@ -347,6 +347,48 @@ def bench_bsr_bf16(steps: int, warmup: int, cpu: bool = False):
     return res
 
 
+def bench_bsr_small_backward(steps: int, warmup: int):
+    """Backward of bsr_spmm at block sizes 8, 16, 32, 64 on the workload of
+    bench_bsr_small (16384^2, 10 % blocks, N = 512, fp32): dA (SDDMM on the
+    stored pattern, bsr_sddmm_small) and dB = A^T dC (bsr_spmm_small over the
+    block-column view), each 2 * nnzb * b^2 * N flops."""
+    import torch
+
+    from trnsparse_amd import workloads as W
+    from trnsparse_amd.hip import _lib
+    from trnsparse_amd.hip import dispatch as D
+
+    out = []
+    n, N = 16384, 512
+    dev = torch.device("cuda", torch.cuda.current_device())
+    g = torch.Generator().manual_seed(21)
+    B = torch.randn(n, N, generator=g).to(dev)
+    G = torch.randn(n, N, generator=g).to(dev)
+    st = _lib.stream_handle(dev)
+    code = _lib.dtype_code(torch.float32)
+    for b in (8, 16, 32, 64):
+        mask = W.cfg3_block_mask(n // b, half_band=3 * 128 // b, density=0.10, seed=22)
+        A = W.bsr_from_block_mask(mask, b, blocks=torch.randn(int(mask.sum()), b, b, generator=g))
+        rp, ci, blk = A.block_row_ptrs.to(dev), A.block_col_indices.to(dev), A.blocks.to(dev)
+        nb = A.n_blocks
+        brow, cp, cbid, crow, corder = D._bsr_bwd_plan(rp, ci, n // b, n // b, dev)
+        gb = torch.empty_like(blk)
+        dB = torch.empty(n, N, device=dev)
+        sddmm = lambda: _lib.call("tsp_bsr_sddmm", G.data_ptr(), N, n, B.data_ptr(), N, n, N, brow.data_ptr(),
+                                  ci.data_ptr(), nb, b, code, gb.data_ptr(), st)
+        spmm_t = lambda: _lib.call("tsp_bsr_spmm_t", blk.data_ptr(), code, cp.data_ptr(), cbid.data_ptr(),
+                                   crow.data_ptr(), n // b, b, n, n, G.data_ptr(), N, N, dB.data_ptr(), N,
+                                   corder.data_ptr(), st)
+        flops = 2.0 * nb * b * b * N
+        for name, fn in ((f"bsr_spmm backward dA b={b} 16384^2 10% blocks N=512 fp32", sddmm),
+                         (f"bsr_spmm backward dB b={b} 16384^2 10% blocks N=512 fp32", spmm_t)):
+            _, ms = time_gpu(fn, steps, warmup)
+            tf = flops / (ms * 1e-3) / 1e12
+            out.append({"name": name, "value": round(tf * 1e3, 1), "unit": "GFLOP/s", "us": round(ms * 1e3, 1),
+                        "frac_fp32_mfma": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)})
+    return out
+
+
 def bench_bsr_backward(steps: int, warmup: int):
     """Backward of bsr_spmm at config 3a (fp32) and 3b (bf16): the two
     kernels the autograd backward launches, each 27.48 GFLOP — tsp_bsr_sddmm
@@ -1039,6 +1081,7 @@ def main(argv=None) -> int:
             ("bsr bf16", lambda: bench_bsr_bf16(max(5, args.steps // 2), 3, cpu=not args.no_cpu)),
             ("bsr f64", lambda: bench_bsr_f64(10, 2)),
             ("bsr small", lambda: bench_bsr_small(10, 2)),
+            ("bsr small backward", lambda: bench_bsr_small_backward(3, 1)),
             ("bsr backward", lambda: bench_bsr_backward(10, 2)),
             ("screened", lambda: bench_screened(10, 2, cpu=not args.no_cpu)),
             ("attention", lambda: bench_attention(10, 2, cpu=not args.no_cpu)),

@@ -53,7 +53,7 @@ def _check(A: ts.BSRMatrix, B: torch.Tensor, G: torch.Tensor, tol: float):
         ((384, 256), 128, 200, 0.6, torch.float32),    # N % 64 != 0: zero-filled k tail
         ((300, 260), 128, 12, 1.0, torch.float32),     # unaligned m, n (padded blocks)
         ((300, 260), 128, 10, 1.0, torch.float32),     # N % 4 != 0: generic kernels
-        ((40, 40), 8, 12, 0.4, torch.float64),         # any block size, fp64
+        ((40, 40), 8, 12, 0.4, torch.float64),         # fp64 at block size 8: generic kernels
         ((256, 384), 128, 64, 0.5, torch.float64),     # fp64 MFMA kernels
         ((384, 256), 128, 200, 0.6, torch.float64),    # N % 32 != 0: zero-filled k tail
         ((300, 260), 128, 12, 1.0, torch.float64),     # unaligned m, n
@@ -63,6 +63,20 @@ def _check(A: ts.BSRMatrix, B: torch.Tensor, G: torch.Tensor, tol: float):
         ((384, 256), 128, 200, 0.6, torch.bfloat16),   # N % 64 != 0: zero-filled k tail
         ((300, 260), 128, 24, 1.0, torch.bfloat16),    # unaligned m, n
         ((300, 260), 128, 12, 1.0, torch.bfloat16),    # N % 8 != 0: generic kernels
+        # small blocks (bsr_sddmm_small, bsr_spmm_small over the column view)
+        ((64, 64), 8, 16, 0.5, torch.float32),
+        ((200, 150), 8, 37, 0.5, torch.float32),       # ragged m, n; N % 4 != 0 (element-wise reads)
+        ((256, 512), 8, 512, 0.3, torch.float32),      # 16-byte reads, four 128-column tiles
+        ((520, 24), 8, 130, 1.0, torch.float32),       # block columns of 65 stored blocks
+        ((256, 256), 16, 130, 0.4, torch.float32),
+        ((200, 150), 16, 64, 0.5, torch.float32),      # ragged m, n
+        ((320, 200), 32, 96, 0.5, torch.float32),
+        ((256, 512), 64, 200, 0.3, torch.float32),
+        ((330, 260), 64, 12, 0.6, torch.float32),      # ragged, narrow N
+        ((256, 512), 8, 512, 0.3, torch.bfloat16),
+        ((200, 150), 16, 37, 0.5, torch.bfloat16),
+        ((256, 256), 32, 128, 0.5, torch.bfloat16),
+        ((300, 260), 64, 24, 0.8, torch.bfloat16),
     ],
 )
 def test_backward_matches_oracle(hip_backend, shape, b, N, density, dtype):

@@ -31,6 +31,11 @@
 //                        v_mfma_f32_32x32x16_bf16 (operand forms at the kernels).
 //   bsr_sddmm_f64_mfma / bsr_spmm_t_f64_mfma   b == 128, fp64: the same two
 //                        products on v_mfma_f64_16x16x4_f64.
+//   bsr_sddmm_small<b>   b in {8, 16, 32, 64}, fp32 / bf16: a wavefront per
+//                        stored block on fp32 MFMAs, operands straight from
+//                        memory (details at the kernel); dB at these block
+//                        sizes is bsr_spmm.hip's small-block kernel walking
+//                        the block-column view with A transposed.
 //   bsr_sddmm_generic / bsr_spmm_t_generic   any block size, f32 / f64 / bf16
 //                        (accumulating in f32, f64 for f64): one thread per
 //                        output element.
@@ -800,6 +805,167 @@ __global__ __launch_bounds__(256) void bsr_spmm_t_generic(const T* __restrict__ 
   out[row * ldo + c] = stv<T>(acc);
 }
 
+// ---------------------------------------------------------- small blocks
+//
+// bsr_sddmm_small<b>: dA for b = 8, 16, 32, 64 (fp32 or bf16, fp32
+// accumulation): a wavefront per stored block k = (i, j), four per
+// workgroup, XCD x taking the x-th eighth of the blocks (neighbouring blocks
+// share block rows). dA_k = dC[rows of i] . B[rows of j]^T over the N
+// columns; both operands are rows with k contiguous, so each lane reads 4
+// consecutive k of its dC row and of its B row per step (k permuted the same
+// way on both operands, so the products pair up):
+//   b = 32, 64: v_mfma_f32_32x32x2_f32, (b/32)^2 subtiles; lane half h takes
+//     k = 8g + 4h + c at step (g, c);
+//   b = 16: v_mfma_f32_16x16x4_f32; lane group q takes k = 16g + 4q + c;
+//   b = 8: v_mfma_f32_4x4x1_16b_f32, its 16 products = 2 x 2 subtiles of
+//     4x4 x 4 k-slices: lane l feeds product l/4 = (k-slice s = (l/4) % 4,
+//     subtile (l/32, (l/16) % 2)), k = 16g + 4s + c; the four k-slices are
+//     summed across lanes at the end.
+// Rows past m / n and columns past ncols read as zero.
+template <typename T>
+__device__ inline f32x4 ld4v(const T* p);
+template <>
+__device__ inline f32x4 ld4v<float>(const float* p) { return *(const f32x4*)p; }
+template <>
+__device__ inline f32x4 ld4v<uint16_t>(const uint16_t* p) {
+  typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+  const u16x4 v = *(const u16x4*)p;
+  return f32x4{tsp::bf16_bits_to_f32(v[0]), tsp::bf16_bits_to_f32(v[1]), tsp::bf16_bits_to_f32(v[2]),
+               tsp::bf16_bits_to_f32(v[3])};
+}
+
+template <int BSZ, typename T>
+__global__ __launch_bounds__(256) void bsr_sddmm_small(const T* __restrict__ G, int64_t ldg, int64_t m,
+                                                       const T* __restrict__ B, int64_t ldb, int64_t n, int64_t ncols,
+                                                       const int64_t* __restrict__ brow, const int64_t* __restrict__ ci,
+                                                       int64_t nnzb, T* __restrict__ out, int vec) {
+  static_assert(BSZ == 8 || BSZ == 16 || BSZ == 32 || BSZ == 64, "block size");
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t per = gridDim.x >> 3;
+  const int64_t kb = ((int64_t)(blockIdx.x & 7) * per + (blockIdx.x >> 3)) * 4 + w;
+  if (kb >= nnzb) return;
+  const int64_t i0 = brow[kb] * BSZ, j0 = ci[kb] * BSZ;
+  // 4 consecutive k of row r of X (vec & 1: X aligned, ld % 4 == 0)
+  auto ld4 = [&](const T* X, int64_t ldx, int64_t rows, int64_t r, int64_t k) {
+    if (r < rows && (vec & 1) && k + 4 <= ncols) return ld4v<T>(X + r * ldx + k);
+    f32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = r < rows && k + e < ncols ? ldv(X + r * ldx + k + e) : 0.f;
+    return v;
+  };
+  T* ob = out + kb * (BSZ * BSZ);
+  if constexpr (BSZ == 8) {
+    const int s4 = (lane >> 2) & 3, sc = (lane >> 4) & 1, sr = lane >> 5, l4 = lane & 3;
+    const int64_t gr = i0 + 4 * sr + l4, br = j0 + 4 * sc + l4;
+    f32x4 acc = {};
+    const int64_t ng = tsp::ceil_div(ncols, 16);
+    f32x4 a = ld4(G, ldg, m, gr, 4 * s4), b = ld4(B, ldb, n, br, 4 * s4);
+    for (int64_t g = 0; g < ng; ++g) {
+      const int64_t kn = 16 * (g + 1) + 4 * s4;  // the next group's k (past ncols reads as zero)
+      const f32x4 an = ld4(G, ldg, m, gr, kn), bn = ld4(B, ldb, n, br, kn);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a[c], b[c], acc, 0, 0, 0);
+      a = an;
+      b = bn;
+    }
+    // sum the four k-slices (lane bits 2 and 3)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      acc[r] += __shfl_xor(acc[r], 4);
+      acc[r] += __shfl_xor(acc[r], 8);
+    }
+    if (s4 == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ob[(4 * sr + r) * BSZ + 4 * sc + l4] = stv<T>(acc[r]);
+    }
+  } else if constexpr (BSZ == 16) {
+    const int l16 = lane & 15, q = lane >> 4;
+    const int64_t gr = i0 + l16, br = j0 + l16;
+    f32x4 acc = {};
+    const int64_t ng = tsp::ceil_div(ncols, 16);
+    f32x4 a = ld4(G, ldg, m, gr, 4 * q), b = ld4(B, ldb, n, br, 4 * q);
+    for (int64_t g = 0; g < ng; ++g) {
+      const int64_t kn = 16 * (g + 1) + 4 * q;
+      const f32x4 an = ld4(G, ldg, m, gr, kn), bn = ld4(B, ldb, n, br, kn);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c], b[c], acc, 0, 0, 0);
+      a = an;
+      b = bn;
+    }
+    // element r: row 4q + r, column l16
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ob[(4 * q + r) * BSZ + l16] = stv<T>(acc[r]);
+  } else {
+    constexpr int RT = BSZ / 32;
+    const int l32 = lane & 31, h = lane >> 5;
+    f32x16 acc[RT][RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+      for (int u = 0; u < RT; ++u) acc[t][u] = f32x16{};
+    const int64_t ng = tsp::ceil_div(ncols, 8);
+    f32x4 a[RT], b[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      a[t] = ld4(G, ldg, m, i0 + 32 * t + l32, 4 * h);
+      b[t] = ld4(B, ldb, n, j0 + 32 * t + l32, 4 * h);
+    }
+    for (int64_t g = 0; g < ng; ++g) {
+      const int64_t kn = 8 * (g + 1) + 4 * h;
+      f32x4 an[RT], bn[RT];
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        an[t] = ld4(G, ldg, m, i0 + 32 * t + l32, kn);
+        bn[t] = ld4(B, ldb, n, j0 + 32 * t + l32, kn);
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int t = 0; t < RT; ++t)
+#pragma unroll
+          for (int u = 0; u < RT; ++u)
+            acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t][c], b[u][c], acc[t][u], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        a[t] = an[t];
+        b[t] = bn[t];
+      }
+    }
+    // element v of subtile (t, u): row 32t + 8(v/4) + 4h + v%4, column 32u + l32
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+      for (int u = 0; u < RT; ++u)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          ob[(32 * t + 8 * (v >> 2) + 4 * h + (v & 3)) * BSZ + 32 * u + l32] = stv<T>(acc[t][u][v]);
+  }
+}
+
+template <typename T>
+int launch_sddmm_small(int64_t bs, const void* G, int64_t ldg, int64_t m, const void* B, int64_t ldb, int64_t n,
+                       int64_t ncols, const int64_t* brow, const int64_t* ci, int64_t nnzb, void* out, hipStream_t st) {
+  const int64_t grid = tsp::ceil_div(tsp::ceil_div(nnzb, 4), 8) * 8;
+  if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_sddmm: too many blocks");
+  const int vec = ((uintptr_t)G % (4 * sizeof(T))) == 0 && ((uintptr_t)B % (4 * sizeof(T))) == 0 && ldg % 4 == 0 &&
+                          ldb % 4 == 0
+                      ? 1
+                      : 0;
+#define TSP_SD_SMALL(BSZ)                                                                                    \
+  hipLaunchKernelGGL((bsr_sddmm_small<BSZ, T>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)G, ldg, m, \
+                     (const T*)B, ldb, n, ncols, brow, ci, nnzb, (T*)out, vec)
+  if (bs == 8)
+    TSP_SD_SMALL(8);
+  else if (bs == 16)
+    TSP_SD_SMALL(16);
+  else if (bs == 32)
+    TSP_SD_SMALL(32);
+  else
+    TSP_SD_SMALL(64);
+#undef TSP_SD_SMALL
+  return tsp::check_launch("bsr_sddmm_small launch");
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p % 16) == 0; }
 
 }  // namespace
@@ -838,6 +1004,14 @@ extern "C" int tsp_bsr_sddmm(const void* G, int64_t ldg, int64_t m, const void* 
     hipLaunchKernelGGL(bsr_sddmm_f64_mfma, dim3((unsigned)grid), dim3(256), 0, st, (const double*)G, ldg, m,
                        (const double*)B, ldb, n, ncols, block_rows, block_col_indices, n_blocks, (double*)grad_blocks);
     return tsp::check_launch("bsr_sddmm_f64_mfma launch");
+  }
+  if (block_size == 8 || block_size == 16 || block_size == 32 || block_size == 64) {
+    if (dtype == TSP_F32)
+      return launch_sddmm_small<float>(block_size, G, ldg, m, B, ldb, n, ncols, block_rows, block_col_indices, n_blocks,
+                                       grad_blocks, st);
+    if (dtype == TSP_BF16)
+      return launch_sddmm_small<uint16_t>(block_size, G, ldg, m, B, ldb, n, ncols, block_rows, block_col_indices,
+                                          n_blocks, grad_blocks, st);
   }
   const int64_t total = n_blocks * block_size * block_size;
   const int64_t grid = tsp::ceil_div(total, 256);
@@ -949,6 +1123,10 @@ extern "C" int tsp_bsr_spmm_t(const void* blocks, int dtype, const int64_t* col_
                        (double*)out, ldo, n, col_order);
     return tsp::check_launch("bsr_spmm_t_f64_mfma launch");
   }
+  if ((block_size == 8 || block_size == 16 || block_size == 32 || block_size == 64) &&
+      (dtype == TSP_F32 || dtype == TSP_BF16))
+    return tsp::launch_bsr_small_t(dtype, block_size, blocks, col_ptrs, col_block_rows, col_block_ids, n_block_cols, m,
+                                   n, X, ldx, ncols, out, ldo, st);
   const int64_t grid = tsp::ceil_div(n * ncols, 256);
   if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm_t: too large for the generic kernel");
 #define SPMMT_GEN(T)                                                                                                     \

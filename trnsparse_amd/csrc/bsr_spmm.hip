@@ -625,11 +625,17 @@ __device__ inline void store4_out(uint16_t* p, f32x4 v) {
                      tsp::f32_to_bf16_bits(v[3])};
 }
 
-template <int BSZ, typename T, typename OutT>
+// TA = true: the product A^T X of the backward (dB = A^T dC). rp, ci and bid
+// are then the block-column view (col_ptrs; per entry the block row, which
+// selects the rows of X, and the stored block's id), an item's "row" is a
+// block column, and each A block enters transposed at the load (element
+// (r, k) of the operand is A_block[k][r]).
+template <int BSZ, typename T, typename OutT, bool TA = false>
 __global__ __launch_bounds__(256) void bsr_spmm_small(const T* __restrict__ blocks, const int64_t* __restrict__ rp,
                                                       const int64_t* __restrict__ ci, int64_t mb, int64_t m, int64_t n,
                                                       const T* __restrict__ B, int64_t ldb, int64_t ncols,
-                                                      OutT* __restrict__ C, int64_t ldc, int64_t nct, int vec) {
+                                                      OutT* __restrict__ C, int64_t ldc, int64_t nct, int vec,
+                                                      const int64_t* __restrict__ bid = nullptr) {
   static_assert(BSZ == 8 || BSZ == 16 || BSZ == 32 || BSZ == 64, "block size");
   constexpr int TW = BSZ == 8 ? 128 : 64;  // columns of C per wavefront
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -646,6 +652,9 @@ __global__ __launch_bounds__(256) void bsr_spmm_small(const T* __restrict__ bloc
   auto bval = [&](int64_t k, int64_t c) {
     return k < n && c < ncols ? tsp::to_acc<T>(B[k * ldb + c]) : 0.f;
   };
+  // the stored block of entry idx, and element (r, k) of its A operand (TA: transposed)
+  auto block_of = [&](int64_t idx) { return blocks + (TA ? bid[idx] : idx) * (BSZ * BSZ); };
+  auto aop = [&](const T* blk, int r, int k) { return tsp::to_acc<T>(TA ? blk[k * BSZ + r] : blk[r * BSZ + k]); };
   if constexpr (BSZ == 8) {
     // v_mfma_f32_4x4x1_16b_f32: 16 independent 4x4 outer products (k = 1)
     // per instruction; lane l feeds product l/4 = (row group l/32, column
@@ -673,9 +682,14 @@ __global__ __launch_bounds__(256) void bsr_spmm_small(const T* __restrict__ bloc
     auto load = [&](int64_t st_, Ops& o) {
       const int64_t idx = start + (st_ < nst ? st_ : nst - 1);
       const int64_t kb = ci[idx] * BSZ;
-      const T* ar = blocks + idx * (BSZ * BSZ) + ra * BSZ;
-      o.a[0] = load4_acc<T>(ar);
-      o.a[1] = load4_acc<T>(ar + 4);
+      const T* blk = block_of(idx);
+      if constexpr (TA) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o.a[k >> 2][k & 3] = aop(blk, ra, k);
+      } else {
+        o.a[0] = load4_acc<T>(blk + ra * BSZ);
+        o.a[1] = load4_acc<T>(blk + ra * BSZ + 4);
+      }
       if (cfull && kb + BSZ <= n) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) o.b[q] = load4_acc<T>(B + (kb + 2 * q + hh) * ldb + nc);
@@ -740,7 +754,13 @@ __global__ __launch_bounds__(256) void bsr_spmm_small(const T* __restrict__ bloc
       const int64_t idx = start + (st_ < nst ? st_ : nst - 1);
       const int64_t k0 = ci[idx] * BSZ;
       const int64_t kb = k0 + 4 * q;
-      a = load4_acc<T>(blocks + idx * (BSZ * BSZ) + l16 * BSZ + 4 * q);
+      const T* blk = block_of(idx);
+      if constexpr (TA) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) a[c] = aop(blk, l16, 4 * q + c);
+      } else {
+        a = load4_acc<T>(blk + l16 * BSZ + 4 * q);
+      }
       if (cfull && k0 + BSZ <= n) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) bq[c] = load4_acc<T>(B + (kb + c) * ldb + nc);
@@ -799,12 +819,19 @@ __global__ __launch_bounds__(256) void bsr_spmm_small(const T* __restrict__ bloc
     for (int64_t idx = start; idx < end; ++idx) {
       const int64_t kb = ci[idx] * BSZ;
       const bool bfull = cfull && kb + BSZ <= n;
-      const T* Ab = blocks + idx * (BSZ * BSZ);
+      const T* Ab = block_of(idx);
 #pragma unroll
       for (int g = 0; g < BSZ / 8; ++g) {
         f32x4 a[RT];
 #pragma unroll
-        for (int t = 0; t < RT; ++t) a[t] = load4_acc<T>(Ab + (32 * t + l32) * BSZ + 8 * g + 4 * h);
+        for (int t = 0; t < RT; ++t) {
+          if constexpr (TA) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) a[t][c] = aop(Ab, 32 * t + l32, 8 * g + 4 * h + c);
+          } else {
+            a[t] = load4_acc<T>(Ab + (32 * t + l32) * BSZ + 8 * g + 4 * h);
+          }
+        }
         f32x2 bv[4];
         if (bfull) {
 #pragma unroll
@@ -844,9 +871,10 @@ __global__ __launch_bounds__(256) void bsr_spmm_small(const T* __restrict__ bloc
   }
 }
 
-template <typename T, typename OutT>
+template <typename T, typename OutT, bool TA = false>
 int launch_small(int64_t bs, const void* blocks, const int64_t* rp, const int64_t* ci, int64_t mb, int64_t m, int64_t n,
-                 const void* B, int64_t ldb, int64_t ncols, void* C, int64_t ldc, hipStream_t st) {
+                 const void* B, int64_t ldb, int64_t ncols, void* C, int64_t ldc, hipStream_t st,
+                 const int64_t* bid = nullptr) {
   const int64_t nct = tsp::ceil_div(ncols, bs == 8 ? 128 : 64);
   const int64_t grid = tsp::ceil_div(tsp::ceil_div(mb * nct, 4), 8) * 8;
   if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_spmm: problem too large");
@@ -856,9 +884,9 @@ int launch_small(int64_t bs, const void* blocks, const int64_t* rp, const int64_
                   (((uintptr_t)C % (4 * sizeof(OutT))) == 0 && ldc % 4 == 0 ? 2 : 0) |
                   (((uintptr_t)B % (2 * sizeof(T))) == 0 && ldb % 2 == 0 ? 4 : 0) |
                   (((uintptr_t)C % (2 * sizeof(OutT))) == 0 && ldc % 2 == 0 ? 8 : 0);
-#define TSP_SMALL(BSZ)                                                                                              \
-  hipLaunchKernelGGL((bsr_spmm_small<BSZ, T, OutT>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)blocks, rp, ci, \
-                     mb, m, n, (const T*)B, ldb, ncols, (OutT*)C, ldc, nct, vec)
+#define TSP_SMALL(BSZ)                                                                                     \
+  hipLaunchKernelGGL((bsr_spmm_small<BSZ, T, OutT, TA>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)blocks, \
+                     rp, ci, mb, m, n, (const T*)B, ldb, ncols, (OutT*)C, ldc, nct, vec, bid)
   if (bs == 8)
     TSP_SMALL(8);
   else if (bs == 16)
@@ -938,6 +966,19 @@ int launch_generic(const void* blocks, const int64_t* rp, const int64_t* ci, int
 }
 
 }  // namespace
+
+// dB = A^T X for block sizes 8, 16, 32 and 64 (the backward of bsr_spmm):
+// bsr_spmm_small over the block-column view with A transposed at the load.
+// X has m rows; dB has n rows. f32 in and out, or bf16 in and out.
+int tsp::launch_bsr_small_t(int dtype, int64_t bs, const void* blocks, const int64_t* col_ptrs,
+                            const int64_t* col_block_rows, const int64_t* col_block_ids, int64_t n_block_cols, int64_t m,
+                            int64_t n, const void* X, int64_t ldx, int64_t ncols, void* out, int64_t ldo, hipStream_t st) {
+  if (dtype == TSP_F32)
+    return launch_small<float, float, true>(bs, blocks, col_ptrs, col_block_rows, n_block_cols, n, m, X, ldx, ncols,
+                                            out, ldo, st, col_block_ids);
+  return launch_small<uint16_t, uint16_t, true>(bs, blocks, col_ptrs, col_block_rows, n_block_cols, n, m, X, ldx, ncols,
+                                                out, ldo, st, col_block_ids);
+}
 
 extern "C" int tsp_bsr_row_order(const int64_t* block_row_ptrs, int64_t n_block_rows, int32_t* order,
                                  void* stream) {

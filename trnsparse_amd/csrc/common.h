@@ -31,6 +31,12 @@ int check_launch(const char* what);
 // instead of hipMemsetAsync so callers may capture the work in a HIP graph).
 int zero_fill(void* p, int64_t bytes, hipStream_t st);
 
+// dB = A^T X of bsr_spmm's backward at block sizes 8, 16, 32, 64 (fp32 or
+// bf16 in and out), defined with the small-block forward kernel.
+int launch_bsr_small_t(int dtype, int64_t bs, const void* blocks, const int64_t* col_ptrs,
+                       const int64_t* col_block_rows, const int64_t* col_block_ids, int64_t n_block_cols, int64_t m,
+                       int64_t n, const void* X, int64_t ldx, int64_t ncols, void* out, int64_t ldo, hipStream_t st);
+
 // ---------------------------------------------------------------- bf16
 // Round-to-nearest-even fp32 -> bf16 bit pattern (NaN kept quiet), the same
 // rounding torch applies in `tensor.to(torch.bfloat16)`.

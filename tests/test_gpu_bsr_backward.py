@@ -199,3 +199,41 @@ def test_block_column_view(mb, nbc, p):
     assert np.array_equal(cbid.cpu().numpy(), order)
     assert np.array_equal(crow.cpu().numpy(), want_brow[order])
     assert sorted(corder.cpu().numpy().tolist()[:nbc]) == list(range(nbc))
+
+
+@pytest.mark.parametrize("b", [8, 16, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sddmm_blocks_in_any_order(hip_backend, b, dtype):
+    """tsp_bsr_sddmm takes (block row, block column) per stored block in any
+    order (the b = 8 kernel stages the dC rows of a chunk's first block row
+    and reads the others from memory): shuffled blocks give the same blocks
+    as CSR order, and each matches float64."""
+    from trnsparse_amd.hip import _lib
+
+    g = torch.Generator().manual_seed(b)
+    nb_r, nb_c, N = 24, 20, 96
+    mask = torch.rand(nb_r, nb_c, generator=g) < 0.4
+    A = W.bsr_from_block_mask(mask, b)
+    dev = torch.device("cuda")
+    ptr = A.block_row_ptrs.numpy()
+    brow = np.repeat(np.arange(nb_r), np.diff(ptr))
+    col = A.block_col_indices.numpy()
+    perm = torch.randperm(len(col), generator=g).numpy()
+    G = torch.randn(nb_r * b, N, generator=g).to(dtype)
+    B = torch.randn(nb_c * b, N, generator=g).to(dtype)
+    Gd, Bd = G.to(dev), B.to(dev)
+    outs = []
+    for order in (np.arange(len(col)), perm):
+        br = torch.from_numpy(brow[order].copy()).to(dev)
+        cc = torch.from_numpy(col[order].copy()).to(dev)
+        out = torch.full((len(col), b, b), float("nan"), dtype=dtype, device=dev)
+        _lib.call("tsp_bsr_sddmm", Gd.data_ptr(), N, nb_r * b, Bd.data_ptr(), N, nb_c * b, N, br.data_ptr(),
+                  cc.data_ptr(), len(col), b, _lib.dtype_code(dtype), out.data_ptr(), _lib.stream_handle(dev))
+        outs.append(out.cpu())
+    assert torch.equal(outs[1], outs[0][torch.from_numpy(perm)])
+    Gn, Bn = G.double().numpy(), B.double().numpy()
+    for k in range(len(col)):
+        i, j = brow[k], col[k]
+        exact = Gn[i * b:(i + 1) * b] @ Bn[j * b:(j + 1) * b].T
+        scale = np.abs(Gn[i * b:(i + 1) * b]) @ np.abs(Bn[j * b:(j + 1) * b]).T
+        assert ref.scaled_error(outs[0][k].double().numpy(), exact, scale) <= TOL[dtype]

@@ -834,6 +834,10 @@ __device__ inline f32x4 ld4v<uint16_t>(const uint16_t* p) {
                tsp::bf16_bits_to_f32(v[3])};
 }
 
+// k steps of operands in flight per lane (small-block dA kernels): 3 measured
+// no faster at b = 8, 16, 32 and slower at b = 64 (more registers)
+constexpr int SDDMM_PF = 1;
+
 template <int BSZ, typename T>
 __global__ __launch_bounds__(256) void bsr_sddmm_small(const T* __restrict__ G, int64_t ldg, int64_t m,
                                                        const T* __restrict__ B, int64_t ldb, int64_t n, int64_t ncols,
@@ -883,14 +887,24 @@ __global__ __launch_bounds__(256) void bsr_sddmm_small(const T* __restrict__ G, 
     const int64_t gr = i0 + l16, br = j0 + l16;
     f32x4 acc = {};
     const int64_t ng = tsp::ceil_div(ncols, 16);
-    f32x4 a = ld4(G, ldg, m, gr, 4 * q), b = ld4(B, ldb, n, br, 4 * q);
-    for (int64_t g = 0; g < ng; ++g) {
-      const int64_t kn = 16 * (g + 1) + 4 * q;
-      const f32x4 an = ld4(G, ldg, m, gr, kn), bn = ld4(B, ldb, n, br, kn);
+    f32x4 ra[SDDMM_PF], rb[SDDMM_PF];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c], b[c], acc, 0, 0, 0);
-      a = an;
-      b = bn;
+    for (int j = 0; j < SDDMM_PF; ++j) {
+      ra[j] = ld4(G, ldg, m, gr, 16 * j + 4 * q);
+      rb[j] = ld4(B, ldb, n, br, 16 * j + 4 * q);
+    }
+    for (int64_t g0 = 0; g0 < ng; g0 += SDDMM_PF) {
+#pragma unroll
+      for (int j = 0; j < SDDMM_PF; ++j) {
+        if (g0 + j < ng) {
+          const f32x4 a = ra[j], b = rb[j];
+          const int64_t kn = 16 * (g0 + j + SDDMM_PF) + 4 * q;  // past ncols reads as zero
+          ra[j] = ld4(G, ldg, m, gr, kn);
+          rb[j] = ld4(B, ldb, n, br, kn);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c], b[c], acc, 0, 0, 0);
+        }
+      }
     }
     // element r: row 4q + r, column l16
 #pragma unroll
@@ -904,31 +918,35 @@ __global__ __launch_bounds__(256) void bsr_sddmm_small(const T* __restrict__ G, 
 #pragma unroll
       for (int u = 0; u < RT; ++u) acc[t][u] = f32x16{};
     const int64_t ng = tsp::ceil_div(ncols, 8);
-    f32x4 a[RT], b[RT];
+    f32x4 ra[SDDMM_PF][RT], rb[SDDMM_PF][RT];
 #pragma unroll
-    for (int t = 0; t < RT; ++t) {
-      a[t] = ld4(G, ldg, m, i0 + 32 * t + l32, 4 * h);
-      b[t] = ld4(B, ldb, n, j0 + 32 * t + l32, 4 * h);
-    }
-    for (int64_t g = 0; g < ng; ++g) {
-      const int64_t kn = 8 * (g + 1) + 4 * h;
-      f32x4 an[RT], bn[RT];
+    for (int j = 0; j < SDDMM_PF; ++j)
 #pragma unroll
       for (int t = 0; t < RT; ++t) {
-        an[t] = ld4(G, ldg, m, i0 + 32 * t + l32, kn);
-        bn[t] = ld4(B, ldb, n, j0 + 32 * t + l32, kn);
+        ra[j][t] = ld4(G, ldg, m, i0 + 32 * t + l32, 8 * j + 4 * h);
+        rb[j][t] = ld4(B, ldb, n, j0 + 32 * t + l32, 8 * j + 4 * h);
       }
+    for (int64_t g0 = 0; g0 < ng; g0 += SDDMM_PF) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+      for (int j = 0; j < SDDMM_PF; ++j) {
+        if (g0 + j < ng) {
+          f32x4 a[RT], b[RT];
+          const int64_t kn = 8 * (g0 + j + SDDMM_PF) + 4 * h;  // past ncols reads as zero
 #pragma unroll
-        for (int t = 0; t < RT; ++t)
+          for (int t = 0; t < RT; ++t) {
+            a[t] = ra[j][t];
+            b[t] = rb[j][t];
+            ra[j][t] = ld4(G, ldg, m, i0 + 32 * t + l32, kn);
+            rb[j][t] = ld4(B, ldb, n, j0 + 32 * t + l32, kn);
+          }
 #pragma unroll
-          for (int u = 0; u < RT; ++u)
-            acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t][c], b[u][c], acc[t][u], 0, 0, 0);
+          for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int t = 0; t < RT; ++t) {
-        a[t] = an[t];
-        b[t] = bn[t];
+            for (int t = 0; t < RT; ++t)
+#pragma unroll
+              for (int u = 0; u < RT; ++u)
+                acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t][c], b[u][c], acc[t][u], 0, 0, 0);
+        }
       }
     }
     // element v of subtile (t, u): row 32t + 8(v/4) + 4h + v%4, column 32u + l32
@@ -939,6 +957,106 @@ __global__ __launch_bounds__(256) void bsr_sddmm_small(const T* __restrict__ G, 
 #pragma unroll
         for (int v = 0; v < 16; ++v)
           ob[(32 * t + 8 * (v >> 2) + 4 * h + (v & 3)) * BSZ + 32 * u + l32] = stv<T>(acc[t][u][v]);
+  }
+}
+
+// bsr_sddmm_rows<b, T>: dA at b = 8 and 16 for N up to ROWS_NMAX<b>. A
+// workgroup per 64 consecutive stored blocks (XCD x taking the x-th eighth
+// of the chunks). The dC rows of the chunk's first block row are staged in
+// LDS (fp32, zero-padded to a multiple of 16 columns, rows 4 floats apart so
+// that one read of the rows hits distinct bank groups); a lane whose block
+// is in another block row reads its dC row from memory, so any block order
+// is correct, and in CSR order dC is read from memory about once per 64
+// blocks instead of once per block. On v_mfma_f32_16x16x4_f32 each lane
+// reads 4 consecutive k of its A row and of its B row per step (16 bytes):
+//   b = 16: a wavefront per block, A = the block row's 16 dC rows, B = the
+//     block column's 16 B rows;
+//   b = 8: a wavefront per pair of blocks (k1, k2): A rows 0-7 are the dC
+//     rows of k1's block row, 8-15 those of k2's, B columns 0-7 the B rows
+//     of k1's block column, 8-15 those of k2's; the diagonal 8x8 quadrants
+//     of the 16x16 result are the two blocks' dA (the off-diagonal ones are
+//     discarded), so no operand row is read twice.
+template <int BSZ>
+constexpr int rows_nmax() { return BSZ == 8 ? 2032 : 1008; }  // BSZ rows of (N + 4) floats under 64 KiB of LDS
+constexpr int ROWS_CHUNK = 64;
+
+template <int BSZ, typename T>
+__global__ __launch_bounds__(256) void bsr_sddmm_rows(const T* __restrict__ G, int64_t ldg, int64_t m,
+                                                      const T* __restrict__ B, int64_t ldb, int64_t n, int64_t ncols,
+                                                      const int64_t* __restrict__ brow, const int64_t* __restrict__ ci,
+                                                      int64_t nnzb, T* __restrict__ out, int vec) {
+  static_assert(BSZ == 8 || BSZ == 16, "block size");
+  constexpr int PB = 16 / BSZ;  // blocks per MFMA tile
+  extern __shared__ __attribute__((aligned(16))) float gs[];  // [BSZ][ldl]
+  const int64_t per = gridDim.x >> 3;
+  const int64_t s0 = ((int64_t)(blockIdx.x & 7) * per + (blockIdx.x >> 3)) * ROWS_CHUNK;
+  if (s0 >= nnzb) return;
+  const int64_t s1 = s0 + ROWS_CHUNK < nnzb ? s0 + ROWS_CHUNK : nnzb;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int ncp = (int)((ncols + 15) & ~(int64_t)15);  // columns staged (zeros past ncols)
+  const int ldl = ncp + 4;
+  const int64_t i0 = brow[s0];
+  // 4 consecutive k of row r of X (zero past `rows` and ncols)
+  auto ld4 = [&](const T* X, int64_t ldx, int64_t rows, int64_t r, int64_t k) {
+    if (r < rows && (vec & 1) && k + 4 <= ncols) return ld4v<T>(X + r * ldx + k);
+    f32x4 v;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[c] = r < rows && k + c < ncols ? ldv(X + r * ldx + k + c) : 0.f;
+    return v;
+  };
+  for (int e = tid; e < BSZ * (ncp / 4); e += 256) {
+    const int r = e / (ncp / 4), k = 4 * (e - r * (ncp / 4));
+    *(f32x4*)(gs + r * ldl + k) = ld4(G, ldg, m, i0 * BSZ + r, k);
+  }
+  __syncthreads();
+  const int l16 = lane & 15, q = lane >> 4;
+  const int rl = l16 % BSZ;  // the lane's row within its block
+  const int ng = ncp / 16;
+  for (int64_t k1 = s0 + PB * w; k1 < s1; k1 += 4 * PB) {
+    const bool two = PB == 2 && k1 + 1 < s1;
+    const int64_t kl = l16 < 8 || !two ? k1 : k1 + 1;  // this lane's block (PB == 1: k1)
+    const int64_t il = brow[kl];
+    const int64_t br = ci[kl] * BSZ + rl;
+    const bool lds_row = il == i0;
+    const int64_t gr = il * BSZ + rl;
+    const float* arow = gs + rl * ldl + 4 * q;
+    auto lda = [&](int g) { return lds_row ? *(const f32x4*)(arow + 16 * g) : ld4(G, ldg, m, gr, 16 * (int64_t)g + 4 * q); };
+    auto ldb4 = [&](int g) { return ld4(B, ldb, n, br, 16 * (int64_t)g + 4 * q); };
+    // operands of SDDMM_PF steps in flight (a register ring; steps past the
+    // end reload the last one)
+    f32x4 acc = {};
+    f32x4 ra[SDDMM_PF], rb[SDDMM_PF];
+#pragma unroll
+    for (int j = 0; j < SDDMM_PF; ++j) {
+      ra[j] = lda(j < ng ? j : ng - 1);
+      rb[j] = ldb4(j < ng ? j : ng - 1);
+    }
+    for (int g0 = 0; g0 < ng; g0 += SDDMM_PF) {
+#pragma unroll
+      for (int j = 0; j < SDDMM_PF; ++j) {
+        if (g0 + j < ng) {
+          const f32x4 a = ra[j], b = rb[j];
+          const int gn = g0 + j + SDDMM_PF < ng ? g0 + j + SDDMM_PF : ng - 1;
+          ra[j] = lda(gn);
+          rb[j] = ldb4(gn);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c], b[c], acc, 0, 0, 0);
+        }
+      }
+    }
+    // element r: row 4q + r, column l16 of the 16x16 tile
+    if constexpr (PB == 1) {
+      T* ob = out + k1 * 256;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ob[(4 * q + r) * 16 + l16] = stv<T>(acc[r]);
+    } else {
+      // diagonal quadrants: block k1 (rows and columns 0-7), k1 + 1 (8-15)
+      if ((q < 2) == (l16 < 8) && (q < 2 || two)) {
+        T* ob = out + (q < 2 ? k1 : k1 + 1) * 64;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ob[((4 * q + r) & 7) * 8 + (l16 & 7)] = stv<T>(acc[r]);
+      }
+    }
   }
 }
 
@@ -954,6 +1072,14 @@ int launch_sddmm_small(int64_t bs, const void* G, int64_t ldg, int64_t m, const 
 #define TSP_SD_SMALL(BSZ)                                                                                    \
   hipLaunchKernelGGL((bsr_sddmm_small<BSZ, T>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)G, ldg, m, \
                      (const T*)B, ldb, n, ncols, brow, ci, nnzb, (T*)out, vec)
+  if (bs == 8 && ncols <= rows_nmax<8>()) {
+    const int64_t gr = tsp::ceil_div(tsp::ceil_div(nnzb, ROWS_CHUNK), 8) * 8;
+    if (gr > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsr_sddmm: too many blocks");
+    const size_t shmem = (size_t)bs * (((ncols + 15) & ~(int64_t)15) + 4) * sizeof(float);
+    hipLaunchKernelGGL((bsr_sddmm_rows<8, T>), dim3((unsigned)gr), dim3(256), shmem, st, (const T*)G, ldg, m,
+                       (const T*)B, ldb, n, ncols, brow, ci, nnzb, (T*)out, vec);
+    return tsp::check_launch("bsr_sddmm_rows launch");
+  }
   if (bs == 8)
     TSP_SD_SMALL(8);
   else if (bs == 16)

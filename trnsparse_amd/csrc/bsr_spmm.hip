@@ -130,9 +130,10 @@ __global__ __launch_bounds__(T32::NTHR) void bsr_spmm_f32_mfma(
 //     8-byte read land in different bank halves.
 // KC = 64 (128 KiB ring, one workgroup per CU, so the in-order dispatcher
 // list-schedules the ranked rows) measured faster on cfg3a than KC = 32
-// (64 KiB, two workgroups per CU): 237 us vs 263 us. The paired B reads took
-// cfg3a from 238.6 to 235.3 us.
-template <int KC_>
+// (64 KiB, two workgroups per CU): 237 us vs 263 us; KC = 32 with 4 or 3
+// stages (one workgroup per CU) 245 and 247 us against 235 us. The paired B
+// reads took cfg3a from 238.6 to 235.3 us.
+template <int KC_, int NST_ = 2>
 struct F32S {
   static constexpr int KC = KC_;
   static constexpr int A_ROWB = KC * 4;
@@ -140,18 +141,19 @@ struct F32S {
   static constexpr int A_BYTES = 128 * A_ROWB;
   static constexpr int B_BYTES = KC * B_ROWB;
   static constexpr int STAGE = A_BYTES + B_BYTES;
-  static constexpr int NST = 2;
+  static constexpr int NST = NST_;
+  static_assert(NST >= 2 && NST <= 4, "ring depths with a vmcnt schedule");
   static constexpr int CPR = A_ROWB / 16;     // 16-byte chunks per A row
   // A: slot of logical chunk c in row r (an involution)
   static __device__ int aswz(int c, int r) { return CPR == 16 ? (c ^ (r & 15)) : (c ^ ((r >> 1) & 7)); }
 };
 
-template <int KC_>
+template <int KC_, int NST_ = 2>
 __global__ __launch_bounds__(256) void bsr_spmm_f32_dma(
     const float* __restrict__ blocks, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci,
     int64_t mb, int nt, int64_t m, int64_t n, const float* __restrict__ B, int64_t ldb, int64_t ncols,
     float* __restrict__ C, int64_t ldc, const int32_t* __restrict__ order) {
-  typedef F32S<KC_> G;
+  typedef F32S<KC_, NST_> G;
   constexpr int SK = G::KC;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[G::NST * G::STAGE];
   int64_t row;
@@ -258,11 +260,22 @@ __global__ __launch_bounds__(256) void bsr_spmm_f32_dma(
     };
 
     const int nsteps = nblk * (BS / SK);
-    issue(0);
+    constexpr int LPS = A_INS + B_INS;  // loads per slab per wave
+    const int pre = nsteps < G::NST - 1 ? nsteps : G::NST - 1;
+    for (int s = 0; s < pre; ++s) issue(s);
     for (int s = 0; s < nsteps; ++s) {
-      tsp::dma::wait_vm<0>();  // this wave's loads of slab s are done
-      tsp::dma::barrier();     // every wave's part is in LDS; stage (s+1) % NST is free
-      if (s + 1 < nsteps) issue(s + 1);
+      // this wave's loads of slab s are done when only the later slabs
+      // already issued (at most NST - 2) are in flight
+      const int later0 = nsteps - 1 - s;
+      const int later = later0 < G::NST - 2 ? later0 : G::NST - 2;
+      if (G::NST >= 4 && later >= 2)
+        tsp::dma::wait_vm<(G::NST >= 4 ? 2 * LPS : 0)>();
+      else if (G::NST >= 3 && later >= 1)
+        tsp::dma::wait_vm<(G::NST >= 3 ? LPS : 0)>();
+      else
+        tsp::dma::wait_vm<0>();
+      tsp::dma::barrier();     // every wave's part is in LDS; stage (s - 1) % NST is free
+      if (s + G::NST - 1 < nsteps) issue(s + G::NST - 1);
       compute(lds + (s % G::NST) * G::STAGE);
     }
   }

@@ -237,3 +237,42 @@ def test_sddmm_blocks_in_any_order(hip_backend, b, dtype):
         exact = Gn[i * b:(i + 1) * b] @ Bn[j * b:(j + 1) * b].T
         scale = np.abs(Gn[i * b:(i + 1) * b]) @ np.abs(Bn[j * b:(j + 1) * b]).T
         assert ref.scaled_error(outs[0][k].double().numpy(), exact, scale) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("b", [8, 16, 64])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_small_blocks_at_scale(hip_backend, b, dtype):
+    """Small-block forward and backward at 4096^2 with cfg3's 10 % block
+    density (banded plus uniform), N = 96: every element of C, dA and dB
+    against float64 (scipy BSR products), at the fp32 / bf16 bars."""
+    import scipy.sparse as sp
+
+    n, N = 4096, 96
+    g = torch.Generator().manual_seed(40 + b)
+    mask = W.cfg3_block_mask(n // b, half_band=3 * 128 // b, density=0.10, seed=41)
+    A = W.bsr_from_block_mask(mask, b, blocks=torch.randn(int(mask.sum()), b, b, generator=g).to(dtype))
+    B = torch.randn(n, N, generator=g).to(dtype)
+    G = torch.randn(n, N, generator=g).to(dtype)
+    blocks = A.blocks.detach().clone().cuda().requires_grad_(True)
+    Bd = B.cuda().requires_grad_(True)
+    Ad = ts.BSRMatrix(blocks, A.block_col_indices, A.block_row_ptrs, A.shape, b)
+    C = ts.bsr_spmm(Ad, Bd)
+    C.backward(G.cuda().to(C.dtype))
+    blk = A.blocks.double().numpy()
+    ind, ptr = A.block_col_indices.numpy(), A.block_row_ptrs.numpy()
+    S = sp.bsr_matrix((blk, ind, ptr), shape=(n, n))
+    Sa = sp.bsr_matrix((np.abs(blk), ind, ptr), shape=(n, n))
+    Bn, Gn = B.double().numpy(), G.double().numpy()
+    tol = TOL[dtype]
+    assert ref.scaled_error(_np(C), S @ Bn, Sa @ np.abs(Bn)) <= tol
+    assert ref.scaled_error(_np(Bd.grad), S.T @ Gn, Sa.T @ np.abs(Gn)) <= tol
+    # dA block k = G[rows of i] @ B[rows of j]^T, in chunks of blocks
+    brow = np.repeat(np.arange(len(ptr) - 1), np.diff(ptr))
+    dA = _np(blocks.grad)
+    for s0 in range(0, len(ind), 4096):
+        i, j = brow[s0:s0 + 4096], ind[s0:s0 + 4096]
+        Gi = Gn.reshape(-1, b, N)[i]
+        Bj = Bn.reshape(-1, b, N)[j]
+        exact = Gi @ Bj.transpose(0, 2, 1)
+        scale = np.abs(Gi) @ np.abs(Bj).transpose(0, 2, 1)
+        assert ref.scaled_error(dA[s0:s0 + 4096], exact, scale) <= tol

@@ -68,6 +68,8 @@ def _check(A: ts.BSRMatrix, B: torch.Tensor, G: torch.Tensor, tol: float):
         ((200, 150), 8, 37, 0.5, torch.float32),       # ragged m, n; N % 4 != 0 (element-wise reads)
         ((256, 512), 8, 512, 0.3, torch.float32),      # 16-byte reads, four 128-column tiles
         ((520, 24), 8, 130, 1.0, torch.float32),       # block columns of 65 stored blocks
+        ((64, 72), 8, 2100, 0.5, torch.float32),       # N past the LDS-staged dA kernel: 4x4x1 k-split form
+        ((64, 72), 8, 2100, 0.5, torch.bfloat16),
         ((256, 256), 16, 130, 0.4, torch.float32),
         ((200, 150), 16, 64, 0.5, torch.float32),      # ragged m, n
         ((320, 200), 32, 96, 0.5, torch.float32),

@@ -21,14 +21,15 @@
 //       S^T = K Q^T and dP^T = V dO^T on v_mfma_f32_32x32x16_bf16 with the
 //       wave's Q and dO rows in registers, P and dS in registers, then
 //       dQ^T += K^T dS^T with K read through ds_read_b64_tr_b16. K/V halves
-//       stream through a 2-stage LDS ring by direct buffer loads one half
-//       ahead.
+//       stream through a 4-stage LDS ring by direct buffer loads three
+//       halves ahead.
 //   bsa_bwd_dkdv_bf16_d128  same shapes: workgroup per (head, key block
 //       column) over the block-column view of the mask, wavefront per 32 keys;
 //       per 64-query half S = Q K^T and dP = dO V^T with the wave's K and V
 //       rows in registers, then dV^T += dO^T P and dK^T += Q^T dS with Q and
 //       dO read through transpose reads. Q/dO halves and their stats stream
-//       through a 2-stage LDS ring.
+//       through a 3-stage LDS ring, two halves ahead, as one stream across
+//       the items of a persistent workgroup.
 //   bsa_bwd_dq_f32<D> / bsa_bwd_dkdv_f32<D> / bsa_bwd_reduce_f32<D>  fp32,
 //       b = 128, D in {64, 128}: the same passes on v_mfma_f32_32x32x2_f32
 //       (operand forms at the kernels); D = 256 runs the row and column

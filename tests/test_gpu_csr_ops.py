@@ -97,6 +97,44 @@ def test_sparse_add_unsorted_rows_with_repeats(hip_backend):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_sparse_add_wide_columns(hip_backend, dtype):
+    """Columns past 2^26 take the 64-bit (column, position) sort keys of the
+    wavefront kernel: rows whose union holds up to 32 entries (two rows per
+    wavefront) and 33-64 entries (one row over all lanes), a few longer
+    rows, repeats inside rows, columns spread up to n - 1."""
+    rng = np.random.default_rng(11)
+    m, n = 300, (1 << 27) + 5
+
+    def rand_csr(lo, hi):
+        lens = rng.integers(lo, hi, m)
+        lens[::9] = rng.integers(20, 31, len(lens[::9]))  # unions of 40-60 entries
+        lens[5] = 40                                      # a union past 64: the LDS kernel
+        cols, vals = [], []
+        for k in lens:
+            pool = rng.integers(0, n, max(1, int(k) // 2 + 1))
+            pool[0] = n - 1
+            cols.append(rng.choice(pool, int(k)))         # repeats inside the row
+            vals.append(rng.standard_normal(int(k)))
+        rp = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+        c = np.concatenate(cols).astype(np.int64)
+        v = np.concatenate(vals)
+        return v, c, rp
+
+    (va, ca, pa), (vb, cb, pb) = rand_csr(0, 17), rand_csr(0, 17)
+    A = ts.CSRMatrix(torch.from_numpy(va).to(dtype).cuda(), torch.from_numpy(ca).cuda(), torch.from_numpy(pa).cuda(),
+                     (m, n))
+    B = ts.CSRMatrix(torch.from_numpy(vb).to(dtype).cuda(), torch.from_numpy(cb).cuda(), torch.from_numpy(pb).cuda(),
+                     (m, n))
+    got = ts.sparse_add(A, B, alpha=2.0, beta=-0.5)
+    v, c, p = ref.sparse_add((A.values.cpu().double().numpy(), ca, pa, (m, n)),
+                             (B.values.cpu().double().numpy(), cb, pb, (m, n)), 2.0, -0.5)
+    np.testing.assert_array_equal(got.row_ptrs.cpu().numpy(), p)
+    np.testing.assert_array_equal(got.col_indices.cpu().numpy(), c)
+    tol = 1e-6 if dtype == torch.float32 else 1e-12
+    np.testing.assert_allclose(got.values.cpu().double().numpy(), v, rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 def test_sparse_add_long_rows(hip_backend, dtype):
     """Rows of every size class of the device coalesce: more than 4096
     entries (a workgroup per row, streamed through LDS in tiles), 65-4096

@@ -569,20 +569,83 @@ __device__ inline uint32_t key_col_of(K k) {
   return sizeof(K) == 4 ? (uint32_t)(k >> 6) : (uint32_t)((uint64_t)k >> 32);
 }
 
-// sort keys across groups of G lanes (G = 32: each half on its own)
+// Value of lane ^ J (J a power of two below 64) without ds_bpermute: DPP
+// quad permutes (1, 2), DPP row rotates (4: rotate by 4 or 12, picked per
+// lane; 8), and the gfx950 swaps of rows 16 apart and halves 32 apart
+// (both operands x: the pair holds the values of the two rows / halves).
+template <int J>
+__device__ inline uint32_t xor_lane32(uint32_t x) {
+  const int lane = (int)(threadIdx.x & 63);
+  if constexpr (J == 1) {
+    return __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
+  } else if constexpr (J == 2) {
+    return __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);  // quad_perm [2, 3, 0, 1]
+  } else if constexpr (J == 4) {
+    const uint32_t a = __builtin_amdgcn_mov_dpp(x, 0x124, 0xF, 0xF, false);  // row_ror:4
+    const uint32_t b = __builtin_amdgcn_mov_dpp(x, 0x12C, 0xF, 0xF, false);  // row_ror:12
+    return (lane & 4) ? a : b;
+  } else if constexpr (J == 8) {
+    return __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false);  // row_ror:8
+  } else if constexpr (J == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (lane & 16) ? r[0] : r[1];
+  } else {
+    static_assert(J == 32, "xor distance");
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (lane & 32) ? r[0] : r[1];
+  }
+}
+template <int J, typename K>
+__device__ inline K xor_lane(K x) {
+  if constexpr (sizeof(K) == 4) {
+    return (K)xor_lane32<J>((uint32_t)x);
+  } else {
+    const uint64_t u = (uint64_t)x;
+    return (K)(((uint64_t)xor_lane32<J>((uint32_t)(u >> 32)) << 32) | xor_lane32<J>((uint32_t)u));
+  }
+}
+
+// bitonic sort of one key per lane across groups of G lanes (G = 32: each
+// half on its own), ascending in every group; l = lane % G
+template <typename K, int KK, int J>
+__device__ inline K bitonic_merge(K key, int l) {
+  const K other = xor_lane<J>(key);
+  const bool keep_min = ((l & J) == 0) == ((l & KK) == 0);
+  key = keep_min ? (other < key ? other : key) : (other > key ? other : key);
+  if constexpr (J > 1)
+    return bitonic_merge<K, KK, J / 2>(key, l);
+  else
+    return key;
+}
+template <typename K, int G, int KK>
+__device__ inline K bitonic_stages(K key, int l) {
+  key = bitonic_merge<K, KK, KK / 2>(key, l);
+  if constexpr (KK < G)
+    return bitonic_stages<K, G, KK * 2>(key, l);
+  else
+    return key;
+}
 template <typename K, int G>
 __device__ inline K lane_sort(K key, int lane) {
-  const int l = lane & (G - 1);  // position within the group: every group sorts ascending
-#pragma unroll
-  for (int k = 2; k <= G; k <<= 1)
-#pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      const K other = __shfl_xor(key, j, 64);
-      const bool keep_min = ((l & j) == 0) == ((l & k) == 0);
-      key = keep_min ? (other < key ? other : key) : (other > key ? other : key);
-    }
-  return key;
+  return bitonic_stages<K, G, 2>(key, lane & (G - 1));
 }
+
+// Each wavefront takes one chunk of SUM_CHUNK consecutive rows (lane j
+// holds the row pointers of rows 2j, 2j + 1 and 2j + 2 of the chunk, loaded
+// once, read out with readlane) and sorts its row pairs in order with the
+// entry loads issued two pairs ahead: loads are branch-free (a lane past its
+// row's end reads row_ptrs[0] instead), so the wait before a pair's sort
+// covers only its own loads.
+constexpr int SUM_CHUNK = 128;  // rows per wavefront (64 pairs)
+struct SumPair {
+  int64_t a0[2], na[2], b0[2], o[2];
+  int n[2];  // entries of each row; -1: past m or not this kernel's row
+};
+template <typename T>
+struct SumEnt {
+  uint32_t c[2];
+  T v[2];  // the lane's entry in pass 0 / 1 (pass 1 only when the rows do not share the lanes)
+};
 
 template <typename T, bool WRITE, typename K>
 __global__ __launch_bounds__(256) void csr_sum_wave_kernel(const T* __restrict__ av, const int64_t* __restrict__ ac,
@@ -594,36 +657,70 @@ __global__ __launch_bounds__(256) void csr_sum_wave_kernel(const T* __restrict__
                                                            int64_t* __restrict__ out_col, T* __restrict__ out_val) {
   typedef typename tsp::Acc<T>::type AccT;
   const int lane = threadIdx.x & 63;
-  const int64_t nw = (int64_t)gridDim.x * 4;
-  for (int64_t rb = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 2; rb < m; rb += nw * 2) {
-    int64_t a0[2], na[2], b0[2];
-    int n[2];
+  const int64_t r0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * SUM_CHUNK;
+  if (r0 >= m) return;
+  const int npairs = (int)((m - r0 < SUM_CHUNK ? m - r0 : SUM_CHUNK) + 1) / 2;
+  // row pointers of rows r0 + 2 lane + {0, 1, 2} (clamped to m)
+  int64_t ra[3], rbp[3], ro[2];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int64_t i = r0 + 2 * lane + j < m ? r0 + 2 * lane + j : m;
+    ra[j] = ar[i];
+    rbp[j] = br[i];
+    if (WRITE && j < 2) ro[j] = out_rp[i];
+  }
+  auto rl64 = [](int64_t v, int l) {
+    const uint64_t u = (uint64_t)v;
+    return (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l) << 32) |
+                     (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l));
+  };
+  auto pair_of = [&](int q, SumPair& p) {
+    const int l = q < npairs ? q : npairs - 1;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      n[i] = -1;  // not this kernel's row
-      if (rb + i < m) {
-        a0[i] = ar[rb + i];
-        na[i] = ar[rb + i + 1] - a0[i];
-        b0[i] = br[rb + i];
-        const int64_t nn = na[i] + (br[rb + i + 1] - b0[i]);
-        if (nn <= WAVE_ROW) n[i] = (int)nn;
-      }
+      p.a0[i] = rl64(ra[i], l);
+      p.na[i] = rl64(ra[i + 1], l) - p.a0[i];
+      p.b0[i] = rl64(rbp[i], l);
+      if (WRITE) p.o[i] = rl64(ro[i], l);
+      const int64_t nn = p.na[i] + (rl64(rbp[i + 1], l) - p.b0[i]);
+      p.n[i] = (q < npairs && r0 + 2 * q + i < m && nn <= WAVE_ROW) ? (int)nn : -1;
     }
-    const bool halves = n[0] <= 32 && n[1] <= 32;
-    // process the rows: both at once in the halves, or one after the other
-    for (int pass = 0; pass < (halves ? 1 : 2); ++pass) {
+  };
+  auto halves_of = [](const SumPair& p) { return p.n[0] <= 32 && p.n[1] <= 32; };
+  auto load_ent = [&](const SumPair& p, SumEnt<T>& e) {
+    const bool halves = halves_of(p);
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      const int i = halves ? (lane >> 5) : pass;
+      const int pos = halves ? (lane & 31) : lane;
+      // (selects, not indexing: a lane-dependent index would put p in scratch)
+      const int ni = i ? p.n[1] : p.n[0];
+      const int64_t nai = i ? p.na[1] : p.na[0], a0i = i ? p.a0[1] : p.a0[0], b0i = i ? p.b0[1] : p.b0[0];
+      const bool valid = (!halves || pass == 0) && pos < ni;
+      const bool in_a = pos < nai;
+      const int64_t* cp = valid ? (in_a ? ac + a0i + pos : bc + b0i + (pos - nai)) : ar;
+      const T* vp = valid ? (in_a ? av + a0i + pos : bv + b0i + (pos - nai)) : (const T*)ar;
+      e.c[pass] = (uint32_t)*cp;
+      e.v[pass] = *vp;
+    }
+  };
+  auto process = [&](int64_t rb, const SumPair& p, const SumEnt<T>& e) {
+    const bool halves = halves_of(p);
+    // the rows: both at once in the halves, or one after the other
+    // (unrolled: a runtime pass index would put e in scratch)
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      if (halves && pass == 1) break;
       const int i = halves ? (lane >> 5) : pass;  // this lane's row
       const int pos = halves ? (lane & 31) : lane;
-      const int nr = n[i];
+      const int nr = i ? p.n[1] : p.n[0];
       if (!halves && nr < 0) continue;  // uniform: the whole wave serves row `pass`
       const int64_t r = rb + i;
       K key = (K)~(K)0;  // padding sorts after every entry
       AccT v = 0;
       if (pos < nr) {
-        const bool in_a = pos < na[i];
-        const uint32_t c = (uint32_t)(in_a ? ac[a0[i] + pos] : bc[b0[i] + pos - na[i]]);
-        v = tsp::to_acc(in_a ? av[a0[i] + pos] : bv[b0[i] + pos - na[i]]);
-        key = sum_key<K>(c, pos);  // equal columns keep input order
+        v = tsp::to_acc(e.v[pass]);
+        key = sum_key<K>(e.c[pass], pos);  // equal columns keep input order
       }
       key = halves ? lane_sort<K, 32>(key, lane) : lane_sort<K, 64>(key, lane);
       const int base = halves ? (lane & 32) : 0;  // first lane of this row's group
@@ -647,11 +744,31 @@ __global__ __launch_bounds__(256) void csr_sum_wave_kernel(const T* __restrict__
         if (open) sum += v2;
       }
       if (head) {
-        const int64_t o = out_rp[r] + __popcll(hb & ((1ull << pos) - 1));
+        const int64_t o = (i ? p.o[1] : p.o[0]) + __popcll(hb & ((1ull << pos) - 1));
         out_col[o] = (int64_t)col;
         out_val[o] = tsp::from_acc<T>(sum);
       }
     }
+  };
+  // three (pair, entries) slots used round robin with constant indices, so no
+  // register holding a load in flight is copied (a copy would wait for it);
+  // the pair count is padded to a multiple of 3 with empty pairs (all rows
+  // -1: no output, loads of row_ptrs[0]), so the loop body has no branch
+  SumPair P0, P1, P2;
+  SumEnt<T> E0, E1, E2;
+  auto step = [&](int q, const SumPair& pc, const SumEnt<T>& ec, SumPair& pn, SumEnt<T>& en) {
+    pair_of(q + 2, pn);
+    load_ent(pn, en);
+    process(r0 + 2 * q, pc, ec);
+  };
+  pair_of(0, P0);
+  load_ent(P0, E0);
+  pair_of(1, P1);
+  load_ent(P1, E1);
+  for (int q = 0; q < npairs; q += 3) {
+    step(q, P0, E0, P2, E2);
+    step(q + 1, P1, E1, P0, E0);
+    step(q + 2, P2, E2, P1, E1);
   }
 }
 
@@ -1502,7 +1619,10 @@ int csr_sum_t(const T* av, const int64_t* ac, const int64_t* ar, const T* bv, co
   const int64_t chunks = tsp::ceil_div(m, SUM_RPW);
   const unsigned g = (unsigned)(chunks < 65536 ? chunks : 65536);
   const unsigned gl = (unsigned)(m < 1024 ? m : 1024);
-  const unsigned gw = (unsigned)(tsp::ceil_div(m, 8) < 65536 ? tsp::ceil_div(m, 8) : 65536);
+  // csr_sum_wave: a wavefront per SUM_CHUNK rows
+  const int64_t gw64 = tsp::ceil_div(m, 4 * SUM_CHUNK);
+  if (gw64 > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_sum: too many rows");
+  const unsigned gw = (unsigned)gw64;
   const bool key32 = col_bits(n) <= 26;
   if (key32)
     hipLaunchKernelGGL((csr_sum_wave_kernel<T, false, uint32_t>), dim3(gw), dim3(256), 0, st, av, ac, ar, bv, bc, br,

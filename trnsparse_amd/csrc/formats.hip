@@ -1014,7 +1014,11 @@ __global__ __launch_bounds__(256) void tr_unpack_kernel(const RowVal<T>* __restr
   vals_out[k] = p.val;
 }
 
-// row_ptrs[c] = first k with sorted column key >= c (c = 0 .. n)
+// row_ptrs[c] = first k with sorted column key >= c (c = 0 .. n). A binary
+// search per pointer: as fast as one pass over the keys that fills each
+// gap (28 us on cfg2's 16.8 M keys either way), and unlike it independent of
+// how the keys spread (a pass that fills gaps took 431 us with every key in
+// 16 of 1 M columns).
 __global__ __launch_bounds__(256) void tr_row_ptrs_kernel(const uint32_t* __restrict__ keys, int64_t nnz, int64_t n,
                                                           int64_t* __restrict__ row_ptrs) {
   const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;

@@ -9,10 +9,15 @@
 // Sort: 8-bit digits over bits [begin_bit, end_bit), tiles of 256 threads x
 // 16 or 8 keys (striped, so round i of thread t is key i*256 + t).
 // Per pass:
-//   rs_count    per-tile digit counts into a digit-major table
-//               counts[d * ntiles + tile];
-//   scan        exclusive scan of the table: the output start of digit d's
-//               keys from each tile, tiles in order;
+//   rs_count    per-tile digit counts into a tile-major table
+//               counts[tile * 256 + d] (one coalesced row per tile);
+//   offsets     the table turned in place into the output start of digit
+//               d's keys from each tile (all of digits < d first, then the
+//               tiles before it), by a scan along the tiles of each digit
+//               (column): chunk sums of 32 or more tiles, one workgroup
+//               (4 x 256 threads) scanning the chunk sums of every digit
+//               and adding the digit bases, then each chunk's tiles in
+//               order;
 //   rs_scatter  each key's rank among equal digits of its tile: lanes of a
 //               wavefront with the same digit found by 8 ballots, counts per
 //               (round, wavefront, digit) in LDS prefixed in key order; the
@@ -172,7 +177,7 @@ __device__ inline uint32_t digit_of(K k, int shift, uint32_t mask) {
 
 template <typename K, int IPT>
 __global__ __launch_bounds__(NT) void rs_count_kernel(const K* __restrict__ keys, int64_t n, int shift,
-                                                      uint32_t mask, int64_t ntiles, uint32_t* __restrict__ counts) {
+                                                      uint32_t mask, uint32_t* __restrict__ counts) {
   __shared__ uint32_t h[NW][RADIX];
   const int tid = threadIdx.x, w = tid >> 6;
   for (int i = tid; i < NW * RADIX; i += NT) (&h[0][0])[i] = 0;
@@ -204,13 +209,118 @@ __global__ __launch_bounds__(NT) void rs_count_kernel(const K* __restrict__ keys
   uint32_t s = 0;
 #pragma unroll
   for (int i = 0; i < NW; ++i) s += h[i][tid];
-  counts[(int64_t)tid * ntiles + blockIdx.x] = s;
+  counts[(int64_t)blockIdx.x * RADIX + tid] = s;
+}
+
+// Column scan of the tile-major count table (thread d = digit d), each
+// column walk 8 loads deep:
+// csum[c][d] = sum of the counts of chunk c's tiles (ch tiles per chunk).
+template <typename C>
+__global__ __launch_bounds__(NT) void rs_chunk_sum_kernel(const C* __restrict__ counts, int64_t ntiles, int64_t ch,
+                                                          C* __restrict__ csum) {
+  const int64_t t0 = (int64_t)blockIdx.x * ch;
+  const int64_t t1 = t0 + ch < ntiles ? t0 + ch : ntiles;
+  const C* col = counts + threadIdx.x;
+  C s = 0;
+  int64_t t = t0;
+  for (; t + 8 <= t1; t += 8) {
+    C v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = col[(t + j) * RADIX];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += v[j];
+  }
+  for (; t < t1; ++t) s += col[t * RADIX];
+  csum[(int64_t)blockIdx.x * RADIX + threadIdx.x] = s;
+}
+// Exclusive scan along a column of rows [r0, r1) of a RADIX-wide table, in
+// place, starting from run, 16 loads in flight; returns run plus the total.
+template <typename C>
+__device__ inline C rs_column_scan(C* __restrict__ col, int64_t r0, int64_t r1, C run) {
+  int64_t t = r0;
+  for (; t + 16 <= r1; t += 16) {
+    C v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = col[(t + j) * RADIX];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      col[(t + j) * RADIX] = run;
+      run += v[j];
+    }
+  }
+  for (; t < r1; ++t) {
+    const C v = col[t * RADIX];
+    col[t * RADIX] = run;
+    run += v;
+  }
+  return run;
+}
+// One workgroup of 4 x 256 threads, thread (part p, digit d) owning a
+// quarter of the chunk rows: csum[c][d] <- (sum over csum of the rows of d
+// before c) + dbase[d], where dbase[d] = all keys of digits < d.
+constexpr int CB_PARTS = 4;
+template <typename C>
+__global__ __launch_bounds__(NT * CB_PARTS) void rs_chunk_base_kernel(C* __restrict__ csum, int64_t nchunks) {
+  __shared__ C part[CB_PARTS][RADIX];
+  __shared__ C dbase[RADIX];
+  const int d = threadIdx.x % RADIX, p = threadIdx.x / RADIX;
+  const int64_t per = (nchunks + CB_PARTS - 1) / CB_PARTS;
+  const int64_t r0 = p * per < nchunks ? p * per : nchunks;
+  const int64_t r1 = r0 + per < nchunks ? r0 + per : nchunks;
+  C* col = csum + d;
+  C s = 0;
+  int64_t t = r0;
+  for (; t + 16 <= r1; t += 16) {
+    C v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = col[(t + j) * RADIX];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s += v[j];
+  }
+  for (; t < r1; ++t) s += col[t * RADIX];
+  part[p][d] = s;
+  __syncthreads();
+  if (threadIdx.x < 64) {  // one wavefront: exclusive scan of the 256 digit totals, 4 per lane
+    const int l = threadIdx.x;
+    C tot[4], acc = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      tot[e] = 0;
+#pragma unroll
+      for (int q = 0; q < CB_PARTS; ++q) tot[e] += part[q][4 * l + e];
+      acc += tot[e];
+    }
+    C x = acc;  // inclusive scan of the lane sums
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const C y = __shfl_up(x, o, 64);
+      if (l >= o) x += y;
+    }
+    C run = x - acc;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      dbase[4 * l + e] = run;
+      run += tot[e];
+    }
+  }
+  __syncthreads();
+  C run = dbase[d];
+  for (int q = 0; q < p; ++q) run += part[q][d];
+  rs_column_scan<C>(col, r0, r1, run);
+}
+// counts[t][d] <- csum[c][d] + (counts of the chunk's tiles before t), in place.
+template <typename C>
+__global__ __launch_bounds__(NT) void rs_chunk_apply_kernel(C* __restrict__ counts, int64_t ntiles, int64_t ch,
+                                                            const C* __restrict__ csum) {
+  const int64_t t0 = (int64_t)blockIdx.x * ch;
+  const int64_t t1 = t0 + ch < ntiles ? t0 + ch : ntiles;
+  rs_column_scan<C>(counts + threadIdx.x, t0, t1, csum[(int64_t)blockIdx.x * RADIX + threadIdx.x]);
 }
 
 template <typename K, typename V, int IPT>
 __global__ __launch_bounds__(NT) void rs_scatter_kernel(const K* __restrict__ kin, const V* __restrict__ vin,
                                                         K* __restrict__ kout, V* __restrict__ vout, int64_t n,
-                                                        int shift, uint32_t mask, int64_t ntiles,
+                                                        int shift, uint32_t mask,
                                                         const uint32_t* __restrict__ offs) {
   constexpr int TILE = NT * IPT;
   __shared__ uint16_t cnt[IPT][NW][RADIX];  // per (round, wavefront, digit): count, then start (< TILE)
@@ -220,7 +330,7 @@ __global__ __launch_bounds__(NT) void rs_scatter_kernel(const K* __restrict__ ki
   __shared__ V sv[TILE];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   for (int i = tid; i < IPT * NW * RADIX / 2; i += NT) ((uint32_t*)&cnt[0][0][0])[i] = 0;
-  gbase[tid] = offs[(int64_t)tid * ntiles + blockIdx.x];
+  gbase[tid] = offs[(int64_t)blockIdx.x * RADIX + tid];
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * TILE;
   const uint64_t lt = (1ull << lane) - 1;
@@ -302,9 +412,13 @@ hipError_t radix_sort_pairs(void* tmp, size_t& tmp_bytes, const K* kin, K* kout,
   constexpr int TILE = NT * IPT;
   const int64_t ntiles = (n + TILE - 1) / TILE;
   const int64_t table = (int64_t)RADIX * (ntiles > 0 ? ntiles : 1);
+  // chunks of ch tiles for the column scan: at most 1024 chunks, so the
+  // one-workgroup step walks at most 1024 rows
+  const int64_t ch = ntiles > 32 * 1024 ? (ntiles + 1023) / 1024 : 32;
+  const int64_t nchunks = ntiles > 0 ? (ntiles + ch - 1) / ch : 1;
   const size_t kb = align256((size_t)n * sizeof(K)), vb = align256((size_t)n * sizeof(V));
   const size_t cb = align256((size_t)table * sizeof(uint32_t));
-  const size_t need = kb + vb + cb + scan_tmp_bytes(table, sizeof(uint32_t));
+  const size_t need = kb + vb + cb + align256((size_t)nchunks * RADIX * sizeof(uint32_t));
   if (!tmp) {
     tmp_bytes = need;
     return hipSuccess;
@@ -314,7 +428,7 @@ hipError_t radix_sort_pairs(void* tmp, size_t& tmp_bytes, const K* kin, K* kout,
   K* tk = (K*)tmp;
   V* tv = (V*)((char*)tmp + kb);
   uint32_t* counts = (uint32_t*)((char*)tmp + kb + vb);
-  void* stmp = (char*)tmp + kb + vb + cb;
+  uint32_t* csum = (uint32_t*)((char*)tmp + kb + vb + cb);
   const int passes = (end_bit - begin_bit + 7) / 8;
   if (passes == 0) {
     hipError_t e = hipMemcpyAsync(kout, kin, (size_t)n * sizeof(K), hipMemcpyDeviceToDevice, st);
@@ -331,14 +445,17 @@ hipError_t radix_sort_pairs(void* tmp, size_t& tmp_bytes, const K* kin, K* kout,
     const int shift = begin_bit + 8 * p;
     const int bits = end_bit - shift < 8 ? end_bit - shift : 8;
     const uint32_t mask = (1u << bits) - 1;
-    hipLaunchKernelGGL((rs_count_kernel<K, IPT>), dim3((unsigned)ntiles), dim3(NT), 0, st, sk, n, shift, mask, ntiles,
+    hipLaunchKernelGGL((rs_count_kernel<K, IPT>), dim3((unsigned)ntiles), dim3(NT), 0, st, sk, n, shift, mask,
                        counts);
+    hipLaunchKernelGGL(rs_chunk_sum_kernel<uint32_t>, dim3((unsigned)nchunks), dim3(NT), 0, st, (const uint32_t*)counts, ntiles,
+                       ch, csum);
+    hipLaunchKernelGGL(rs_chunk_base_kernel<uint32_t>, dim3(1), dim3(NT * CB_PARTS), 0, st, csum, nchunks);
+    hipLaunchKernelGGL(rs_chunk_apply_kernel<uint32_t>, dim3((unsigned)nchunks), dim3(NT), 0, st, counts, ntiles, ch,
+                       (const uint32_t*)csum);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    e = scan(stmp, (const uint32_t*)counts, counts, table, false, 0u, st);
-    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((rs_scatter_kernel<K, V, IPT>), dim3((unsigned)ntiles), dim3(NT), 0, st, sk, sv, dk, dv, n, shift,
-                       mask, ntiles, (const uint32_t*)counts);
+                       mask, (const uint32_t*)counts);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     sk = dk;

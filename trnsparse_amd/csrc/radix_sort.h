@@ -7,7 +7,8 @@
 // reduce / scan-of-block-sums / apply, the block sums scanned recursively.
 //
 // Sort: 8-bit digits over bits [begin_bit, end_bit), tiles of 256 threads x
-// 16 or 8 keys (striped, so round i of thread t is key i*256 + t).
+// 16 keys (4096; in the scatter, round i of lane l in wavefront w is key
+// 1024 w + 64 i + l).
 // Per pass:
 //   rs_count    per-tile digit counts into a tile-major table
 //               counts[tile * 256 + d] (one coalesced row per tile);
@@ -18,10 +19,11 @@
 //               (4 x 256 threads) scanning the chunk sums of every digit
 //               and adding the digit bases, then each chunk's tiles in
 //               order;
-//   rs_scatter  each key's rank among equal digits of its tile: lanes of a
-//               wavefront with the same digit found by 8 ballots, counts per
-//               (round, wavefront, digit) in LDS prefixed in key order; the
-//               tile is reordered by digit in LDS and written as runs, so
+//   rs_scatter  each key's rank among equal digits of its tile: each
+//               wavefront owns a contiguous quarter of the tile and keeps a
+//               running count per digit in LDS across its rounds; lanes of a
+//               round with the same digit are found by 8 ballots; the tile
+//               is reordered by digit in LDS and written as runs, so
 //               consecutive lanes write consecutive addresses.
 // Equal digits keep their input order within and across tiles, so every
 // pass and the sort are stable. Passes alternate between the output and a
@@ -40,12 +42,10 @@ constexpr int NT = 256;             // threads per block
 constexpr int NW = NT / 64;         // wavefronts per block
 constexpr int SCAN_IPT = 16;        // scan elements per thread
 constexpr int SCAN_TILE = NT * SCAN_IPT;
-// sort keys per thread: 16 (4096-key tiles) when a key and its value take at
-// most 8 bytes, else 8 (measured: 16 was faster for 4 + 4-byte pairs, 1.27 ->
-// 1.12 ms for cfg3's COO -> CSR, and slower for 4 + 8-byte ones)
+// sort keys per thread: 16 (4096-key tiles)
 template <typename K, typename V>
 constexpr int sort_ipt() {
-  return sizeof(K) + sizeof(V) <= 8 ? 16 : 8;
+  return 16;
 }
 constexpr int RADIX = 256;
 static_assert(NT == RADIX, "the sort kernels give each thread one digit's table entry");
@@ -323,23 +323,24 @@ __global__ __launch_bounds__(NT) void rs_scatter_kernel(const K* __restrict__ ki
                                                         int shift, uint32_t mask,
                                                         const uint32_t* __restrict__ offs) {
   constexpr int TILE = NT * IPT;
-  __shared__ uint16_t cnt[IPT][NW][RADIX];  // per (round, wavefront, digit): count, then start (< TILE)
-  __shared__ uint32_t gbase[RADIX];         // output start of digit d's keys from this tile
-  __shared__ uint32_t lbase[RADIX];         // start of digit d in the tile reordered by digit
+  constexpr int Q = TILE / NW;               // keys per wavefront, contiguous
+  __shared__ uint16_t hw[NW][RADIX];         // per wavefront: running count of each digit, then its start
+  __shared__ uint32_t gbase[RADIX];          // output start of digit d's keys from this tile
+  __shared__ uint32_t lbase[RADIX];          // start of digit d in the tile reordered by digit
   __shared__ K sk[TILE];
   __shared__ V sv[TILE];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  for (int i = tid; i < IPT * NW * RADIX / 2; i += NT) ((uint32_t*)&cnt[0][0][0])[i] = 0;
+  for (int i = tid; i < NW * RADIX / 2; i += NT) ((uint32_t*)&hw[0][0])[i] = 0;
   gbase[tid] = offs[(int64_t)blockIdx.x * RADIX + tid];
   __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * TILE;
+  const int64_t wbase = (int64_t)blockIdx.x * TILE + (int64_t)w * Q;  // round i, lane l: key wbase + 64 i + l
   const uint64_t lt = (1ull << lane) - 1;
   K k[IPT];
   V val[IPT];
   uint32_t dg[IPT], rk[IPT];
 #pragma unroll
   for (int i = 0; i < IPT; ++i) {
-    const int64_t idx = base + i * NT + tid;
+    const int64_t idx = wbase + 64 * i + lane;
     if (idx < n) {
       k[i] = kin[idx];
       val[i] = vin[idx];
@@ -347,10 +348,13 @@ __global__ __launch_bounds__(NT) void rs_scatter_kernel(const K* __restrict__ ki
       k[i] = K(0);
     }
   }
+  // rank of each key among the equal digits before it in the wavefront's
+  // keys: the wavefront's running count of the digit (LDS, read by every
+  // lane of the group before its leader adds the group) plus the rank among
+  // this round's lanes with the same digit (8 ballots)
 #pragma unroll
   for (int i = 0; i < IPT; ++i) {
-    const int64_t idx = base + i * NT + tid;
-    const bool valid = idx < n;
+    const bool valid = wbase + 64 * i + lane < n;
     dg[i] = digit_of(k[i], shift, mask);
     uint64_t peers = __ballot(valid);
 #pragma unroll
@@ -359,28 +363,27 @@ __global__ __launch_bounds__(NT) void rs_scatter_kernel(const K* __restrict__ ki
       const uint64_t m = __ballot(bit);
       peers &= bit ? m : ~m;
     }
-    rk[i] = (uint32_t)__popcll(peers & lt);
-    if (valid && rk[i] == 0) cnt[i][w][dg[i]] = (uint16_t)__popcll(peers);
+    const uint32_t below = (uint32_t)__popcll(peers & lt);
+    const uint32_t before = hw[w][dg[i]];
+    rk[i] = before + below;
+    if (valid && below == 0) hw[w][dg[i]] = (uint16_t)(before + __popcll(peers));
   }
   __syncthreads();
-  // digit tid: starts of its (round, wavefront) groups in key order, and its tile total
+  // digit tid: starts of its wavefront groups in key order, and its tile total
   uint32_t run = 0;
 #pragma unroll
-  for (int i = 0; i < IPT; ++i)
-#pragma unroll
-    for (int v = 0; v < NW; ++v) {
-      const uint32_t c = cnt[i][v][tid];
-      cnt[i][v][tid] = (uint16_t)run;
-      run += c;
-    }
+  for (int v = 0; v < NW; ++v) {
+    const uint32_t c = hw[v][tid];
+    hw[v][tid] = (uint16_t)run;
+    run += c;
+  }
   uint32_t total;
   lbase[tid] = block_exclusive_scan(run, total);
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < IPT; ++i) {
-    const int64_t idx = base + i * NT + tid;
-    if (idx < n) {
-      const uint32_t p = lbase[dg[i]] + cnt[i][w][dg[i]] + rk[i];
+    if (wbase + 64 * i + lane < n) {
+      const uint32_t p = lbase[dg[i]] + hw[w][dg[i]] + rk[i];
       if (p < (uint32_t)TILE) {  // always true; keeps a miscount from writing outside the tile
         sk[p] = k[i];
         sv[p] = val[i];
@@ -388,6 +391,7 @@ __global__ __launch_bounds__(NT) void rs_scatter_kernel(const K* __restrict__ ki
     }
   }
   __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * TILE;
   const int cnt_tile = (int)(n - base < TILE ? n - base : TILE);
   for (int j = tid; j < cnt_tile; j += NT) {
     const K kk = sk[j];

@@ -629,6 +629,21 @@ template <typename K, int G>
 __device__ inline K lane_sort(K key, int lane) {
   return bitonic_stages<K, G, 2>(key, lane & (G - 1));
 }
+// Ascending sort of a bitonic sequence over groups of G lanes (the
+// half-cleaner steps of the last stage only).
+template <typename K, int J>
+__device__ inline K bitonic_clean(K key, int l) {
+  const K other = xor_lane<J>(key);
+  key = (l & J) == 0 ? (other < key ? other : key) : (other > key ? other : key);
+  if constexpr (J > 1)
+    return bitonic_clean<K, J / 2>(key, l);
+  else
+    return key;
+}
+template <typename K, int G>
+__device__ inline K lane_merge(K key, int lane) {
+  return bitonic_clean<K, G / 2>(key, lane & (G - 1));
+}
 
 // Each wavefront takes one chunk of SUM_CHUNK consecutive rows (lane j
 // holds the row pointers of rows 2j, 2j + 1 and 2j + 2 of the chunk, loaded
@@ -696,10 +711,15 @@ __global__ __launch_bounds__(256) void csr_sum_wave_kernel(const T* __restrict__
       // (selects, not indexing: a lane-dependent index would put p in scratch)
       const int ni = i ? p.n[1] : p.n[0];
       const int64_t nai = i ? p.na[1] : p.na[0], a0i = i ? p.a0[1] : p.a0[0], b0i = i ? p.b0[1] : p.b0[0];
-      const bool valid = (!halves || pass == 0) && pos < ni;
-      const bool in_a = pos < nai;
-      const int64_t* cp = valid ? (in_a ? ac + a0i + pos : bc + b0i + (pos - nai)) : ar;
-      const T* vp = valid ? (in_a ? av + a0i + pos : bv + b0i + (pos - nai)) : (const T*)ar;
+      // lane pos of the row's group holds A's entry pos (pos < na) or B's
+      // entry G - 1 - pos (pos >= G - nb): A ascending, B reversed
+      const int G = halves ? 32 : 64;
+      const bool use = (!halves || pass == 0) && ni > 0;
+      const bool in_a = use && pos < nai;
+      const bool in_b = use && pos >= G - (ni - nai);
+      const int jb = G - 1 - pos;
+      const int64_t* cp = in_a ? ac + a0i + pos : (in_b ? bc + b0i + jb : ar);
+      const T* vp = in_a ? av + a0i + pos : (in_b ? bv + b0i + jb : (const T*)ar);
       e.c[pass] = (uint32_t)*cp;
       e.v[pass] = *vp;
     }
@@ -716,16 +736,32 @@ __global__ __launch_bounds__(256) void csr_sum_wave_kernel(const T* __restrict__
       const int nr = i ? p.n[1] : p.n[0];
       if (!halves && nr < 0) continue;  // uniform: the whole wave serves row `pass`
       const int64_t r = rb + i;
+      const int G = halves ? 32 : 64;
+      const int na = (int)(i ? p.na[1] : p.na[0]), nb = nr - na;
+      const bool in_a = nr > 0 && pos < na, in_b = nr > 0 && pos >= G - nb;
+      // key: column and the entry's position in the row (A's then B's, in
+      // input order), so equal columns keep input order
       K key = (K)~(K)0;  // padding sorts after every entry
       AccT v = 0;
-      if (pos < nr) {
+      const uint32_t c = e.c[pass];
+      if (in_a || in_b) {
         v = tsp::to_acc(e.v[pass]);
-        key = sum_key<K>(e.c[pass], pos);  // equal columns keep input order
+        key = sum_key<K>(c, in_a ? pos : na + (G - 1 - pos));
       }
-      key = halves ? lane_sort<K, 32>(key, lane) : lane_sort<K, 64>(key, lane);
+      // A ascending from the group's first lane, B descending to its last
+      // lane: a bitonic sequence when both rows are sorted by column, so the
+      // last stage's half-cleaners sort it; any inversion: the full network
+      const uint32_t cprev = __shfl_up(c, 1, 64);
+      const bool inv = (in_a && pos > 0 && cprev > c) || (in_b && pos > G - nb && cprev < c);
+      if (__builtin_amdgcn_ballot_w64(inv) == 0)
+        key = halves ? lane_merge<K, 32>(key, lane) : lane_merge<K, 64>(key, lane);
+      else
+        key = halves ? lane_sort<K, 32>(key, lane) : lane_sort<K, 64>(key, lane);
       const int base = halves ? (lane & 32) : 0;  // first lane of this row's group
       const uint32_t col = key_col_of(key);
-      const AccT sv = __shfl(v, base + (int)(key & 63), 64);
+      const int kp = (int)(key & 63);             // the entry's position -> the lane holding its value
+      const int src = kp < na ? kp : (G - 1 - (kp - na)) & (G - 1);
+      const AccT sv = __shfl(v, base + src, 64);
       const uint32_t prev = __shfl_up(col, 1, 64);
       const bool head = pos < nr && (pos == 0 || prev != col);
       const uint64_t hb_all = __builtin_amdgcn_ballot_w64(head);

@@ -1040,15 +1040,17 @@ struct TrKeys {
   }
 };
 
+// The sort's last pass stores a transposed entry's (row, value) payload
+// straight into the output arrays: the row as the int64 column index.
 template <typename T>
-__global__ __launch_bounds__(256) void tr_unpack_kernel(const RowVal<T>* __restrict__ payload, int64_t nnz,
-                                                        int64_t* __restrict__ cols_out, T* __restrict__ vals_out) {
-  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (k >= nnz) return;
-  const RowVal<T> p = payload[k];
-  cols_out[k] = (int64_t)p.row;
-  vals_out[k] = p.val;
-}
+struct TrOut {
+  int64_t* col;
+  T* val;
+  __device__ void operator()(int64_t i, const RowVal<T>& p) const {
+    col[i] = (int64_t)p.row;
+    val[i] = p.val;
+  }
+};
 
 // row_ptrs[c] = first k with sorted column key >= c (c = 0 .. n). A binary
 // search per pointer: as fast as one pass over the keys that fills each
@@ -1489,7 +1491,6 @@ template <typename T>
 int csr_transpose_t(const T* values, const int64_t* col_indices, const int64_t* row_ptrs, int64_t m, int64_t n,
                     int64_t nnz, int64_t* out_row_ptrs, int64_t* out_col, T* out_values, char* w,
                     int64_t workspace_bytes, hipStream_t st) {
-  const int64_t g = tsp::ceil_div(nnz, 256);
   const int64_t ka = align256(4 * nnz), pa = align256((int64_t)sizeof(RowVal<T>) * nnz);
   uint32_t* keys = (uint32_t*)w;
   uint32_t* keys_s = (uint32_t*)(w + ka);
@@ -1499,13 +1500,11 @@ int csr_transpose_t(const T* values, const int64_t* col_indices, const int64_t* 
   size_t tmp_bytes = (size_t)(workspace_bytes - (2 * ka + 2 * pa));
   int rc = launch_entry_rows(row_ptrs, m, nnz, TrKeys<T>{col_indices, values, keys, pay}, st, "tr_keys launch");
   if (rc) return rc;
-  const hipError_t se =
-      sort_pairs(tmp, tmp_bytes, (const uint32_t*)keys, keys_s, (const RowVal<T>*)pay, pay_s, nnz, col_bits(n), st);
+  // (pay_s: scratch between passes; the last pass writes out_col / out_values)
+  const hipError_t se = tsp::rsort::radix_sort_pairs_to(tmp, tmp_bytes, (const uint32_t*)keys, keys_s,
+                                                        (const RowVal<T>*)pay, pay_s, nnz, 0, col_bits(n),
+                                                        TrOut<T>{out_col, out_values}, st);
   if (se != hipSuccess) return tsp::check_hip(se, "radix_sort_pairs");
-  hipLaunchKernelGGL(tr_unpack_kernel<T>, dim3((unsigned)g), dim3(256), 0, st, (const RowVal<T>*)pay_s, nnz, out_col,
-                     out_values);
-  rc = tsp::check_launch("tr_unpack launch");
-  if (rc) return rc;
   hipLaunchKernelGGL(tr_row_ptrs_kernel, dim3((unsigned)tsp::ceil_div(n + 1, 256)), dim3(256), 0, st,
                      (const uint32_t*)keys_s, nnz, n, out_row_ptrs);
   return tsp::check_launch("tr_row_ptrs launch");

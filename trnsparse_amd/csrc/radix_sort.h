@@ -317,11 +317,18 @@ __global__ __launch_bounds__(NT) void rs_chunk_apply_kernel(C* __restrict__ coun
   rs_column_scan<C>(counts + threadIdx.x, t0, t1, csum[(int64_t)blockIdx.x * RADIX + threadIdx.x]);
 }
 
-template <typename K, typename V, int IPT>
+// Where a pass stores the value of output position i: a plain array, or in
+// the last pass a caller's writer (e.g. fields to separate arrays).
+template <typename V>
+struct VStore {
+  V* p;
+  __device__ void operator()(int64_t i, const V& v) const { p[i] = v; }
+};
+
+template <typename K, typename V, int IPT, typename VW>
 __global__ __launch_bounds__(NT) void rs_scatter_kernel(const K* __restrict__ kin, const V* __restrict__ vin,
-                                                        K* __restrict__ kout, V* __restrict__ vout, int64_t n,
-                                                        int shift, uint32_t mask,
-                                                        const uint32_t* __restrict__ offs) {
+                                                        K* __restrict__ kout, VW vout, int64_t n, int shift,
+                                                        uint32_t mask, const uint32_t* __restrict__ offs) {
   constexpr int TILE = NT * IPT;
   constexpr int Q = TILE / NW;               // keys per wavefront, contiguous
   __shared__ uint16_t hw[NW][RADIX];         // per wavefront: running count of each digit, then its start
@@ -399,17 +406,30 @@ __global__ __launch_bounds__(NT) void rs_scatter_kernel(const K* __restrict__ ki
     const int64_t pos = (int64_t)gbase[d] + (j - (int64_t)lbase[d]);
     if (pos >= 0 && pos < n) {  // always true; keeps a miscount from writing outside the output
       kout[pos] = kk;
-      vout[pos] = sv[j];
+      vout(pos, sv[j]);
     }
+  }
+}
+
+// zero key bits: the input in order, through the writer
+template <typename K, typename V, typename VW>
+__global__ __launch_bounds__(NT) void rs_copy_kernel(const K* __restrict__ kin, const V* __restrict__ vin,
+                                                     K* __restrict__ kout, VW vout, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x;
+  if (i < n) {
+    kout[i] = kin[i];
+    vout(i, vin[i]);
   }
 }
 
 // Stable sort of (kin, vin)[0, n) by key bits [begin_bit, end_bit) into (kout, vout);
 // the inputs are left unchanged. tmp == nullptr stores the temporary size.
 // Keys must be unsigned; n < 2^32.
-template <typename K, typename V>
-hipError_t radix_sort_pairs(void* tmp, size_t& tmp_bytes, const K* kin, K* kout, const V* vin, V* vout, int64_t n,
-                            int begin_bit, int end_bit, hipStream_t st = 0) {
+// radix_sort_pairs_to: the same, with the last pass's values stored by
+// `last` (vout then only serves as scratch between passes).
+template <typename K, typename V, typename LastW>
+hipError_t radix_sort_pairs_to(void* tmp, size_t& tmp_bytes, const K* kin, K* kout, const V* vin, V* vout,
+                               int64_t n, int begin_bit, int end_bit, LastW last, hipStream_t st = 0) {
   if (n < 0 || n > (int64_t)UINT32_MAX || begin_bit < 0 || end_bit > (int)(8 * sizeof(K)) || end_bit < begin_bit)
     return hipErrorInvalidValue;
   constexpr int IPT = sort_ipt<K, V>();
@@ -435,9 +455,9 @@ hipError_t radix_sort_pairs(void* tmp, size_t& tmp_bytes, const K* kin, K* kout,
   uint32_t* csum = (uint32_t*)((char*)tmp + kb + vb + cb);
   const int passes = (end_bit - begin_bit + 7) / 8;
   if (passes == 0) {
-    hipError_t e = hipMemcpyAsync(kout, kin, (size_t)n * sizeof(K), hipMemcpyDeviceToDevice, st);
-    if (e != hipSuccess) return e;
-    return hipMemcpyAsync(vout, vin, (size_t)n * sizeof(V), hipMemcpyDeviceToDevice, st);
+    hipLaunchKernelGGL((rs_copy_kernel<K, V, LastW>), dim3((unsigned)((n + NT - 1) / NT)), dim3(NT), 0, st, kin, vin,
+                       kout, last, n);
+    return hipGetLastError();
   }
   const K* sk = kin;
   const V* sv = vin;
@@ -458,14 +478,24 @@ hipError_t radix_sort_pairs(void* tmp, size_t& tmp_bytes, const K* kin, K* kout,
                        (const uint32_t*)csum);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((rs_scatter_kernel<K, V, IPT>), dim3((unsigned)ntiles), dim3(NT), 0, st, sk, sv, dk, dv, n, shift,
-                       mask, (const uint32_t*)counts);
+    if (p == passes - 1)
+      hipLaunchKernelGGL((rs_scatter_kernel<K, V, IPT, LastW>), dim3((unsigned)ntiles), dim3(NT), 0, st, sk, sv, dk,
+                         last, n, shift, mask, (const uint32_t*)counts);
+    else
+      hipLaunchKernelGGL((rs_scatter_kernel<K, V, IPT, VStore<V>>), dim3((unsigned)ntiles), dim3(NT), 0, st, sk, sv,
+                         dk, VStore<V>{dv}, n, shift, mask, (const uint32_t*)counts);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     sk = dk;
     sv = dv;
   }
   return hipSuccess;
+}
+
+template <typename K, typename V>
+hipError_t radix_sort_pairs(void* tmp, size_t& tmp_bytes, const K* kin, K* kout, const V* vin, V* vout, int64_t n,
+                            int begin_bit, int end_bit, hipStream_t st = 0) {
+  return radix_sort_pairs_to(tmp, tmp_bytes, kin, kout, vin, vout, n, begin_bit, end_bit, VStore<V>{vout}, st);
 }
 
 }  // namespace rsort

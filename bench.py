@@ -524,9 +524,9 @@ def bench_spmv(dist: str, index_bits: int, steps: int, warmup: int, cpu: bool = 
     kernels with long rows split out by length (tsp_csr_bucketed_spmv, plan
     built outside the timed region). `algorithmic_bytes` is the reference
     layout's traffic (nnz*(4+idx) + (m+1)*idx + 4n + 4m) and defines `value`
-    and `frac_hbm`; `kernel_bytes` is what the kernel itself has to move (the
-    plan's 8-byte entries and 2-byte positions, x, y and the column groups'
-    partial sums)."""
+    and `frac_hbm`; `kernel_bytes` is what the kernels themselves have to move
+    (the plan's 8-byte entries, x twice, y, the column groups' partial sums
+    and the row exponents)."""
     import numpy as np
     import torch
 
@@ -560,8 +560,9 @@ def bench_spmv(dist: str, index_bits: int, steps: int, warmup: int, cpu: bool = 
             del A2
             geom = A._hip_colplan[2]
             G = int(geom[3])
-            # 8-byte entry + 16-bit row-order position per nonzero, x, y, partials
-            kbytes = nnz * 10 + n * 4 + m * 4 + (2 * G * m * 4 if G > 1 else 0)
+            # 8-byte entry per nonzero, x (the max pre-pass and the gathers' slices), y, the
+            # column groups' partial sums written and read, the row exponents
+            kbytes = nnz * 8 + 2 * n * 4 + m * 4 + 2 * G * m * 4 + 2 * m
         if plan == "bucketed":
             ts.spmv(A, xd)  # builds the bucket plan
         flush = make_flush()

@@ -224,15 +224,27 @@ int tsp_csr_spmv(const void* values, int dtype, const void* col_indices,
  * torch.sparse_csr @ x call at :45), computed from a reordered copy of the
  * matrix built once per pattern: tiles of 2^rbits rows x 2^cbits columns,
  * each tile's entries sorted by column, 8 bytes per entry (packed row /
- * column within the tile and the fp32 value), so the x gathers of one
- * wavefront instruction share cache lines. Every sum runs in a fixed order
- * (repeated calls are bit-identical), but not in the order of tsp_csr_spmv:
- * the two paths can differ in the last bits.
+ * column within the tile and the value), so the x gathers of one wavefront
+ * instruction share cache lines.
+ *
+ * Row sums are exact int64 fixed-point sums of the fp32 products v * x:
+ * the plan keeps v * 2^(61 - e_r) with sum_j |v_rj| < 2^e_r per row, x is
+ * scaled by 2^-e_x with max |x| < 2^e_x, each product is rounded to an
+ * integer (exact when its magnitude is at least 2^23 units) and added in
+ * LDS. Integer sums do not depend on the order of the additions, so
+ * repeated calls are bit-identical; the result is the exactly rounded sum
+ * of the fp32 products of the reference, up to one rounding per column
+ * group. A row is summed from the CSR arrays instead (fp32 products in CSR
+ * order, fp64 sum) when x holds inf or NaN, when the row holds a
+ * non-finite value or values spread over more than ~2^180, or when one of
+ * its products was rounded and the row's result is below cnt * 2^23 units
+ * (so the rounding could exceed 2^-24 of it). The result can differ from
+ * tsp_csr_spmv in the last bits.
  *
  * geometry (10 int64, host memory), filled by tsp_csr_colplan_geometry:
  *   [0] rbits   [1] row blocks   [2] cbits   [3] column groups G
  *   [4] tiles   [5] sort key bits [6] plan bytes  [7] build workspace bytes
- *   [8] SpMV workspace bytes (G * m * 4; 0 when G == 1)  [9] reserved
+ *   [8] SpMV workspace bytes  [9] padded entries
  * rows_per_block_log2 (12..14) and tiles_hint tune the tiling; 0 = auto.
  * TSP_EUNSUPPORTED when nnz > 2^32 - 2. The plan holds each entry's
  * position k in the pattern (uint32) and row_ptrs[0] (any value) beside
@@ -249,15 +261,21 @@ int tsp_csr_colplan_build(const void* values, int dtype,
                           const int64_t* geometry, void* plan,
                           void* workspace, void* stream);
 
-/* Copy new values of the same pattern into the plan (one gather pass). */
-int tsp_csr_colplan_refresh(const void* values, int dtype, int64_t m,
+/* Copy new values of the same pattern into the plan (the row exponents from
+ * row_ptrs, then one gather pass). */
+int tsp_csr_colplan_refresh(const void* values, int dtype,
+                            const void* row_ptrs, int index_type, int64_t m,
                             int64_t n, int64_t nnz, const int64_t* geometry,
                             void* plan, void* stream);
 
 /* out (m,) = alpha * A @ x (+ beta * y) over the plan; x (n,), y (m,) or
- * NULL; workspace: geometry[8] bytes of device memory (NULL if 0). */
+ * NULL; values / col_indices / row_ptrs: the CSR arrays the plan was built
+ * (or last refreshed) from, read only for the rows summed from them;
+ * workspace: geometry[8] bytes of device memory. */
 int tsp_csr_colplan_spmv(const void* plan, int dtype, int64_t m, int64_t n,
-                         int64_t nnz, const int64_t* geometry, const void* x,
+                         int64_t nnz, const int64_t* geometry,
+                         const void* values, const void* col_indices,
+                         const void* row_ptrs, int index_type, const void* x,
                          double alpha, const void* y, double beta, void* out,
                          void* workspace, void* stream);
 

@@ -99,24 +99,26 @@ def test_colplan_tiling_hints_via_c_abi(hip_backend, rbits, tiles):
     xd, yd = torch.from_numpy(x).cuda(), torch.from_numpy(y).cuda()
     out = torch.empty(m, device="cuda")
     work = torch.empty(max(1, int(geom[8])), dtype=torch.uint8, device="cuda")
-    _lib.call("tsp_csr_colplan_spmv", plan.data_ptr(), _lib.TSP_F32, m, n, len(v), geom.ctypes.data, xd.data_ptr(),
-              0.5, yd.data_ptr(), -2.0, out.data_ptr(), work.data_ptr(), _lib.stream_handle(torch.device("cuda")))
+    csr = (vals.data_ptr(), cols.data_ptr(), ptrs.data_ptr(), _lib.index_code(cols.dtype))
+    _lib.call("tsp_csr_colplan_spmv", plan.data_ptr(), _lib.TSP_F32, m, n, len(v), geom.ctypes.data, *csr,
+              xd.data_ptr(), 0.5, yd.data_ptr(), -2.0, out.data_ptr(), work.data_ptr(),
+              _lib.stream_handle(torch.device("cuda")))
     _check(v, c, p, (m, n), x, out.cpu().numpy(), 0.5, y, -2.0)
     # a geometry that does not belong to the shape is refused on the host
     bad = geom.copy()
     bad[3] += 1
     with pytest.raises(RuntimeError, match="geometry"):
-        _lib.call("tsp_csr_colplan_spmv", plan.data_ptr(), _lib.TSP_F32, m, n, len(v), bad.ctypes.data,
+        _lib.call("tsp_csr_colplan_spmv", plan.data_ptr(), _lib.TSP_F32, m, n, len(v), bad.ctypes.data, *csr,
                   xd.data_ptr(), 1.0, None, 0.0, out.data_ptr(), work.data_ptr(), 0)
 
 
 @pytest.mark.parametrize("rbits,tiles", [(13, 1), (12, 0)])
 def test_colplan_runs_across_lanes_and_wavefronts(hip_backend, rbits, tiles):
-    """Rows whose entries in one epoch fill whole lanes (8 positions), cross
-    lane boundaries, and span several wavefronts (the carry slots, added in
-    wavefront order after the epoch), next to rows of one or two entries.
-    With tiles=1 a tile holds all columns, so a row of 30000 entries takes
-    most positions of its epochs. Two calls must agree bit for bit."""
+    """Rows whose entries fill most of an epoch (many lanes of one
+    instruction adding to the same LDS row sum) next to rows of one or two
+    entries. With tiles=1 a tile holds all columns, so a row of 30000
+    entries takes most positions of its epochs. Two calls must agree bit
+    for bit."""
     m, n = 8192, 60000
     rng0 = np.random.default_rng(21)
     lens = rng0.poisson(2, m)
@@ -138,8 +140,8 @@ def test_colplan_runs_across_lanes_and_wavefronts(hip_backend, rbits, tiles):
         out = torch.empty(m, device="cuda")
         work = torch.empty(max(1, int(geom[8])), dtype=torch.uint8, device="cuda")
         _lib.call("tsp_csr_colplan_spmv", plan.data_ptr(), _lib.TSP_F32, m, n, len(v), geom.ctypes.data,
-                  xd.data_ptr(), 1.0, None, 0.0, out.data_ptr(), work.data_ptr(),
-                  _lib.stream_handle(torch.device("cuda")))
+                  vals.data_ptr(), cols.data_ptr(), ptrs.data_ptr(), _lib.index_code(cols.dtype), xd.data_ptr(), 1.0,
+                  None, 0.0, out.data_ptr(), work.data_ptr(), _lib.stream_handle(torch.device("cuda")))
         outs.append(out.cpu().numpy())
     _check(v, c, p, (m, n), x, outs[0])
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
@@ -173,15 +175,16 @@ def test_colplan_view_with_nonzero_first_row_pointer(hip_backend, index_dtype):
     ws = torch.empty(max(1, int(geom[8])), dtype=torch.uint8, device=dev)
 
     def run():
-        _lib.call("tsp_csr_colplan_spmv", plan.data_ptr(), _lib.TSP_F32, m, n, nnz, geom.ctypes.data, xd.data_ptr(),
-                  1.0, None, 0.0, out.data_ptr(), ws.data_ptr(), st)
+        _lib.call("tsp_csr_colplan_spmv", plan.data_ptr(), _lib.TSP_F32, m, n, nnz, geom.ctypes.data, vals.data_ptr(),
+                  cols.data_ptr(), ptrs.data_ptr(), _lib.index_code(cols.dtype), xd.data_ptr(), 1.0, None, 0.0,
+                  out.data_ptr(), ws.data_ptr(), st)
         return out.cpu().numpy()
 
     _check(v, c, p, (m, n), x, run())
     v2 = rng.standard_normal(nnz).astype(np.float32)
     vals[base:] = torch.from_numpy(v2).to(dev)
-    _lib.call("tsp_csr_colplan_refresh", vals.data_ptr(), _lib.TSP_F32, m, n, nnz, geom.ctypes.data, plan.data_ptr(),
-              st)
+    _lib.call("tsp_csr_colplan_refresh", vals.data_ptr(), _lib.TSP_F32, ptrs.data_ptr(), _lib.index_code(ptrs.dtype),
+              m, n, nnz, geom.ctypes.data, plan.data_ptr(), st)
     _check(v2, c, p, (m, n), x, run())
 
 
@@ -212,6 +215,98 @@ def test_colplan_nan_at_unreferenced_columns(plan_always):
     got = ts.spmv(A, torch.from_numpy(x).cuda()).cpu().numpy()
     assert np.isfinite(got).all()
     _check(v, c, p, (m, n), x, got)
+
+
+def _check_nonfinite(v, c, p, shape, x, got):
+    """inf / NaN exactly where the float64 oracle has them (same sign of
+    inf), the finite rows within the tolerance."""
+    exact = ref.csr_spmv(v, c.astype(np.int64), p.astype(np.int64), shape, x)
+    scale = ref.csr_spmv(v, c.astype(np.int64), p.astype(np.int64), shape, x, absolute=True)
+    assert np.array_equal(np.isnan(got), np.isnan(exact))
+    inf = np.isinf(exact)
+    assert np.array_equal(np.isinf(got), inf) and np.array_equal(got[inf], exact[inf])
+    fin = np.isfinite(exact)
+    assert ref.scaled_error(got[fin], exact[fin], scale[fin]) <= TOL
+
+
+@pytest.mark.parametrize("index_dtype", [np.int64, np.int32])
+def test_colplan_nonfinite_x_at_referenced_columns(plan_always, index_dtype):
+    """inf and NaN in x where entries reference them: the rows that read them
+    come out inf / NaN as the reference's fp32 products make them (0 * inf
+    = NaN, inf - inf = NaN); every other row is unaffected."""
+    m, n = 6000, 9000
+    v, c, p, rng = _random(m, n, np.full(m, 6), 40, index_dtype)
+    x = rng.standard_normal(n).astype(np.float32)
+    x[c[:50]] = np.inf
+    x[c[200:230]] = -np.inf
+    x[c[400:420]] = np.nan
+    v[5] = 0.0  # a stored zero times inf
+    A = W.csr_matrix_from_arrays(v, c, p, (m, n), device="cuda")
+    got = ts.spmv(A, torch.from_numpy(x).cuda()).cpu().numpy()
+    _check_nonfinite(v, c, p, (m, n), x, got)
+
+
+def test_colplan_nonfinite_values(plan_always):
+    """inf / NaN values (rows summed from the CSR arrays) next to finite rows."""
+    m, n = 6000, 9000
+    v, c, p, rng = _random(m, n, np.full(m, 6), 41)
+    v[[10, 500, 3000]] = [np.inf, -np.inf, np.nan]
+    A = W.csr_matrix_from_arrays(v, c, p, (m, n), device="cuda")
+    x = rng.standard_normal(n).astype(np.float32)
+    got = ts.spmv(A, torch.from_numpy(x).cuda()).cpu().numpy()
+    _check_nonfinite(v, c, p, (m, n), x, got)
+
+
+@pytest.mark.parametrize("xscale", [1e-15, 1.0, 1e15])
+def test_colplan_relative_accuracy_across_scales(plan_always, xscale):
+    """The fixed-point row sums follow the scale of x and of each row: with
+    positive values and x (no cancellation) every row keeps fp32 relative
+    accuracy whatever the magnitudes, including rows whose values are 1e-20
+    of another row's and x scaled by 1e-15 or 1e15 (no fp32 product
+    underflows)."""
+    m, n = 8000, 12000
+    v, c, p, rng = _random(m, n, np.random.default_rng(42).poisson(10, m), 43)
+    v = np.abs(v) + 0.01
+    rows = np.repeat(np.arange(m), np.diff(p))
+    v = (v * np.where(rows % 3 == 0, 1e-20, 1.0)[rows]).astype(np.float32)  # every third row tiny
+    x = ((np.abs(rng.standard_normal(n)) + 0.01) * xscale).astype(np.float32)
+    A = W.csr_matrix_from_arrays(v, c, p, (m, n), device="cuda")
+    got = ts.spmv(A, torch.from_numpy(x).cuda()).cpu().numpy().astype(np.float64)
+    exact = ref.csr_spmv(v, c, p, (m, n), x)
+    nz = exact != 0
+    assert np.max(np.abs(got[nz] - exact[nz]) / exact[nz]) <= 1e-5
+    assert np.all(got[~nz] == 0)
+
+
+def test_colplan_small_products_beside_large_values(plan_always):
+    """A row whose large values meet x = 0 and whose result comes from
+    products far below the row's scale (rounded in fixed point, so the row
+    is summed again from the CSR arrays), a row with a subnormal value that
+    the plan's scaling would flush (always summed from the CSR arrays), and
+    a row whose products cancel exactly."""
+    n = 8
+    c = np.array([0, 1, 2, 3, 4, 5, 6, 7, 0, 1], dtype=np.int64)
+    p = np.array([0, 4, 6, 8, 10], dtype=np.int64)
+    v = np.array([1e30, -3e29, 2e-20, 5e-21, 1e30, 1e-40, 3.0, -3.0, 0.5, -0.5], dtype=np.float32)
+    x = np.array([0.0, 0.0, 1.0, 3.0, 0.0, 1e30, 7.0, 7.0, 2.0, 2.0], dtype=np.float32)[:n]
+    x[0], x[1] = 2.0, 2.0  # row 3: 0.5*2 - 0.5*2 = 0 exactly; row 0 reads cols 0, 1 too
+    v[0], v[1] = 1e30, -1e30  # row 0: 1e30*2 - 1e30*2 cancel, 2e-20*1 + 5e-21*3 remain
+    m = 4
+    A = W.csr_matrix_from_arrays(v, c, p, (m, n), device="cuda")
+    got = ts.spmv(A, torch.from_numpy(x).cuda()).cpu().numpy().astype(np.float64)
+    exact = ref.csr_spmv(v, c, p, (m, n), x)
+    assert abs(got[0] - exact[0]) <= 1e-6 * abs(exact[0])
+    assert abs(got[1] - exact[1]) <= 1e-6 * abs(exact[1])
+    assert got[2] == exact[2] == 0.0 and got[3] == exact[3] == 0.0
+
+
+def test_colplan_zero_x_and_beta(plan_always):
+    m, n = 3000, 4000
+    v, c, p, rng = _random(m, n, np.full(m, 7), 44)
+    A = W.csr_matrix_from_arrays(v, c, p, (m, n), device="cuda")
+    y = rng.standard_normal(m).astype(np.float32)
+    got = ts.spmv(A, torch.zeros(n, device="cuda"), alpha=2.0, y=torch.from_numpy(y).cuda(), beta=0.5)
+    assert torch.equal(got.cpu(), torch.from_numpy(y) * 0.5)
 
 
 def test_colplan_auto_mode_builds_on_reuse(hip_backend):

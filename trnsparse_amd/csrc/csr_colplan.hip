@@ -62,6 +62,8 @@
 // consecutive bytes. The three per-entry arrays hold one more epoch of zeros
 // past the last tile's, which the SpMV kernel's prefetch reads when a tile
 // has no epoch left to prefetch.
+#include <algorithm>
+
 #include "common.h"
 
 #include "radix_sort.h"
@@ -78,8 +80,15 @@ constexpr int SPMV_NT = 1024;                  // threads of the SpMV workgroup
 constexpr int SPMV_W = SPMV_NT / 64;           // wavefronts of the SpMV workgroup
 
 constexpr int SPMV_K = E / 64 / SPMV_W;       // 64-entry chunks per wavefront and epoch
-constexpr int SPMV_PL = E / SPMV_W / 64;      // phase-2 row-order positions per lane
-static_assert(SPMV_K == 4 && SPMV_PL == 4, "a lane's entries and positions are loaded in 16- and 8-byte pieces");
+static_assert(SPMV_K == 4, "a lane's entries are loaded as two 16-byte pieces");
+
+// Fixed-point row sums: a plan value of row r is v * 2^(FX_TOP - e_r), so
+// the values of a row add up to less than 2^FX_TOP; with x scaled by
+// 2^-e_x (max |x| < 2^e_x) every partial sum of a row's products stays
+// below 2^FX_TOP + (rounding), inside int64.
+constexpr int FX_TOP = 61;
+constexpr int16_t RX_REDO = 32767;  // row exponent of a row summed from the CSR arrays
+constexpr int XMAX_BLOCKS = 1024;   // partial maxima of |x| written by the pre-pass (at most)
 
 // Where column-order entry li = (j * W + w) * 64 + l of an epoch (chunk j of
 // wavefront w, lane l) is stored: wavefront w's entries are one contiguous
@@ -88,13 +97,6 @@ static_assert(SPMV_K == 4 && SPMV_PL == 4, "a lane's entries and positions are l
 __host__ __device__ constexpr int entry_slot(int li) {
   return ((li >> 6) % SPMV_W) * (E / SPMV_W) + (((li >> 6) / SPMV_W) >> 1) * 128 + 2 * (li & 63) +
          (((li >> 6) / SPMV_W) & 1);
-}
-
-// LDS slot of row-order position s: position pairs P = s/2 are XOR-swizzled
-// (P ^ ((P >> 3) & 1)) so that phase 2's 16-byte reads, lane l at pairs
-// 2l and 2l + 1, put 8 consecutive lanes on 8 different 16-byte bank groups.
-__host__ __device__ constexpr int pos_slot(int s) {
-  return ((((s >> 1) ^ ((s >> 4) & 1))) << 1) | (s & 1);
 }
 
 int ilog2_ceil(int64_t v) {
@@ -234,13 +236,52 @@ __global__ __launch_bounds__(1024) void colplan_epochs_kernel(const int64_t* __r
   if (tid == 1023) eoff[T] = s;
 }
 
-__global__ __launch_bounds__(256) void colplan_fill_kernel(uint64_t* __restrict__ ent, uint16_t* __restrict__ pinv,
-                                                           uint32_t* __restrict__ pos, int64_t n) {
+__global__ __launch_bounds__(256) void colplan_fill_kernel(uint64_t* __restrict__ ent, uint32_t* __restrict__ pos,
+                                                           int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   ent[i] = 0;
-  pinv[i] = 0;
   pos[i] = POS_PAD;
+}
+
+// Row exponent e_r of the fixed-point row sums: with cnt entries and
+// max |v| < 2^emx, sum |v| < 2^(emx + ceil(log2 cnt)) = 2^e_r, so the plan's
+// values v * 2^(FX_TOP - e_r) add up to less than 2^FX_TOP in magnitude.
+// RX_REDO marks a row the finish kernel always sums from the CSR arrays
+// instead: a non-finite value, or a smallest nonzero value that scaling
+// would push below the normal range (its products would lose bits).
+__device__ inline int16_t row_exponent(uint32_t mx, uint32_t mn, int64_t cnt) {
+  if (mx == 0) return 0;  // no nonzero value: every product is zero
+  if (mx >= 0x7f800000u) return RX_REDO;
+  const int emx = (int)(mx >> 23) == 0 ? -126 : (int)(mx >> 23) - 126;
+  const int lg = cnt > 1 ? 64 - __builtin_clzll((uint64_t)(cnt - 1)) : 0;
+  const int er = emx + lg;
+  const int emn = (int)(mn >> 23) == 0 ? -149 : (int)(mn >> 23) - 127;  // mn >= 2^emn
+  if (emn + FX_TOP - er < -126) return RX_REDO;
+  return (int16_t)er;
+}
+
+// One thread per row (build and refresh only).
+template <typename IdxT>
+__global__ __launch_bounds__(256) void colplan_rowexp_kernel(const float* __restrict__ vals,
+                                                             const IdxT* __restrict__ ptr, int64_t m,
+                                                             int16_t* __restrict__ rexp) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= m) return;
+  const int64_t p0 = (int64_t)ptr[r], p1 = (int64_t)ptr[r + 1];
+  uint32_t mx = 0, mn = 0xffffffffu;
+  for (int64_t p = p0; p < p1; ++p) {
+    const uint32_t b = __float_as_uint(vals[p]) & 0x7fffffffu;
+    mx = b > mx ? b : mx;
+    if (b != 0 && b < mn) mn = b;
+  }
+  rexp[r] = row_exponent(mx, mn, p1 - p0);
+}
+
+// The plan's form of value v in global row r: v * 2^(FX_TOP - e_r) (zero
+// for the rows summed from the CSR arrays).
+__device__ inline uint32_t plan_value(float v, int16_t er) {
+  return er == RX_REDO ? 0u : __float_as_uint(ldexpf(v, FX_TOP - (int)er));
 }
 
 // Sorted entry i of tile t is column-order entry j % E of epoch eoff[t] + j / E
@@ -248,10 +289,11 @@ __global__ __launch_bounds__(256) void colplan_fill_kernel(uint64_t* __restrict_
 template <typename K>
 __global__ __launch_bounds__(256) void colplan_scatter_kernel(const K* __restrict__ keys,
                                                               const uint64_t* __restrict__ payload,
-                                                              const float* __restrict__ vals, int64_t nnz, int cbits,
-                                                              const int64_t* __restrict__ toff,
+                                                              const float* __restrict__ vals, int64_t nnz, int rbits,
+                                                              int cbits, int64_t G, const int64_t* __restrict__ toff,
                                                               const int64_t* __restrict__ eoff, int64_t T,
                                                               const int64_t* __restrict__ plan_base,
+                                                              const int16_t* __restrict__ rexp,
                                                               uint64_t* __restrict__ ent, uint32_t* __restrict__ pos) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= nnz) return;
@@ -262,159 +304,123 @@ __global__ __launch_bounds__(256) void colplan_scatter_kernel(const K* __restric
   const uint32_t p = (uint32_t)pl;  // position k in the sort; the value sits at base + k
   const uint32_t rl = (uint32_t)(pl >> 32);
   const uint32_t cin = (uint32_t)(keys[i] & (((K)1 << cbits) - 1));
-  ent[P] = ((uint64_t)__builtin_bit_cast(uint32_t, vals[plan_base[0] + p]) << 32) | (uint64_t)((rl << cbits) | cin);
+  const int64_t row = ((t / G) << rbits) | rl;
+  ent[P] = ((uint64_t)plan_value(vals[plan_base[0] + p], rexp[row]) << 32) | (uint64_t)((rl << cbits) | cin);
   pos[P] = p;
 }
 
-// One workgroup per epoch: each entry's position in the epoch's (row,
-// column order) order, by a stable LSD radix sort in LDS of the E keys
-// row << EBITS | li on the row bits (two 8-bit passes; padding entries take
-// row 2^rbits and sort last). A pass ranks each key among equal digits: the
-// lanes of a wavefront holding the same digit come from 8 ballots, and the
-// counts per (round, wavefront, digit) are prefixed in key order, so equal
-// rows keep their column order. Column-order entry li = (j * W + w) * 64 + l
-// (chunk j of wavefront w, lane l in the SpMV kernel's phase 1) stores
-// pos_slot(its position) in uint16 (w * 64 + l) * K + j: a lane loads the
-// positions of its K entries with one 16-byte load.
-__global__ __launch_bounds__(1024) void colplan_perm_kernel(const uint64_t* __restrict__ ent,
-                                                            const int64_t* __restrict__ toff,
-                                                            const int64_t* __restrict__ eoff, int64_t T, int rbits,
-                                                            int cbits, uint16_t* __restrict__ pinv) {
-  constexpr int NR = E / 1024;  // keys per thread (rounds)
-  __shared__ uint32_t key[2][E];
-  __shared__ uint16_t cnt[NR][16][256];  // per (round, wavefront, digit): count, then start (< E)
-  __shared__ uint32_t dbase[256];
-  __shared__ uint32_t wtot[4];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t ep = blockIdx.x;
-  if (ep >= eoff[T]) return;  // the grid covers the epoch count's upper bound
-  const int64_t t = upper_bound_i64(eoff, T + 1, ep) - 1;
-  const int64_t left = (toff[t + 1] - toff[t]) - ((ep - eoff[t]) << EBITS);
-  const int count = left < E ? (int)left : E;
-  const uint64_t* __restrict__ e = ent + (ep << EBITS);
-  for (int i = tid; i < E; i += 1024) {
-    const uint32_t row = i < count ? (uint32_t)e[entry_slot(i)] >> cbits : (1u << rbits);
-    key[0][i] = (row << EBITS) | (uint32_t)i;
-  }
-  const uint64_t lt = (1ull << lane) - 1;
-#pragma unroll 1
-  for (int pass = 0; pass < 2; ++pass) {  // rows < 2^15: bits EBITS .. EBITS + 15
-    const uint32_t* src = key[pass];
-    uint32_t* dst = key[pass ^ 1];
-    const int shift = EBITS + 8 * pass;
-    for (int i = tid; i < NR * 16 * 256 / 2; i += 1024) ((uint32_t*)&cnt[0][0][0])[i] = 0;
-    __syncthreads();
-    uint32_t kv[NR], dg[NR], rk[NR];
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      kv[r] = src[r * 1024 + tid];
-      dg[r] = (kv[r] >> shift) & 255u;
-      uint64_t peers = ~0ull;
-#pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const bool bit = (dg[r] >> b) & 1;
-        const uint64_t m = __ballot(bit);
-        peers &= bit ? m : ~m;
-      }
-      rk[r] = (uint32_t)__popcll(peers & lt);
-      if (rk[r] == 0) cnt[r][w][dg[r]] = (uint16_t)__popcll(peers);
-    }
-    __syncthreads();
-    // digit tid (< 256): starts of its (round, wavefront) groups, then its start in the epoch
-    uint32_t tot = 0;
-    if (tid < 256)
-#pragma unroll
-      for (int r = 0; r < NR; ++r)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const uint32_t c = cnt[r][v][tid];
-          cnt[r][v][tid] = (uint16_t)tot;
-          tot += c;
-        }
-    uint32_t x = tot;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const uint32_t y = __shfl_up(x, d, 64);
-      if (lane >= d) x += y;
-    }
-    if (tid < 256 && lane == 63) wtot[w] = x;
-    __syncthreads();
-    if (tid < 256) {
-      uint32_t before = 0;
-      for (int i = 0; i < w; ++i) before += wtot[i];
-      dbase[tid] = before + x - tot;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < NR; ++r) dst[dbase[dg[r]] + cnt[r][w][dg[r]] + rk[r]] = kv[r];
-    __syncthreads();
-  }
-  uint16_t* __restrict__ out = pinv + (ep << EBITS);
-  for (int s = tid; s < E; s += 1024) {
-    const int i = (int)(key[0][s] & (E - 1));
-    const int c = i >> 6, j = c / SPMV_W, w2 = c % SPMV_W, l = i & 63;
-    out[(w2 * 64 + l) * SPMV_K + j] = (uint16_t)pos_slot(s);
-  }
-}
-
+// New values on the plan's pattern: plan position i holds CSR position
+// pos[i]; its row block comes from the tile of its epoch.
 __global__ __launch_bounds__(256) void colplan_refresh_kernel(const float* __restrict__ vals,
                                                               const uint32_t* __restrict__ pos, int64_t n,
                                                               const int64_t* __restrict__ plan_base,
+                                                              const int64_t* __restrict__ eoff, int64_t T, int64_t G,
+                                                              int rbits, int cbits, const int16_t* __restrict__ rexp,
                                                               uint64_t* __restrict__ ent) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const uint32_t p = pos[i];
-  const uint32_t bits = p == POS_PAD ? 0u : __builtin_bit_cast(uint32_t, vals[plan_base[0] + p]);
+  uint32_t bits = 0;
+  if (p != POS_PAD) {
+    const int64_t t = upper_bound_i64(eoff, T + 1, i >> EBITS) - 1;
+    const int64_t row = ((t / G) << rbits) | ((uint32_t)ent[i] >> cbits);
+    bits = plan_value(vals[plan_base[0] + p], rexp[row]);
+  }
   ent[i] = ((uint64_t)bits << 32) | (ent[i] & 0xffffffffull);
 }
 
 // ----------------------------------------------------------------- SpMV
 
-// One step of a segmented inclusive scan with DPP: add the value of the
-// lane the DPP control names when it holds the same row (rows ascend
-// across the lanes, so equal rows mean every lane between is in the run).
-template <int CTRL, int ROW_MASK>
-__device__ inline float seg_step(float s, uint32_t r) {
-  const uint32_t ro = (uint32_t)__builtin_amdgcn_update_dpp((int)0xffffffffu, (int)r, CTRL, ROW_MASK, 0xf, false);
-  const float so = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), CTRL, ROW_MASK,
-                                                                         0xf, false));
-  return ro == r ? s + so : s;
+// Partial maxima of |x| as float bits without the sign (an integer max
+// orders them like the values; inf and NaN come out >= 0x7f800000): one
+// 16-byte load per thread and trip (vec4, x 16-byte aligned), so a cold x
+// takes one memory round trip.
+__global__ __launch_bounds__(256) void colplan_xmax_kernel(const float* __restrict__ x, int64_t n, int vec4,
+                                                           uint32_t* __restrict__ xpart) {
+  __shared__ uint32_t wm[4];
+  uint32_t mx = 0;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  const int64_t t0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  auto take = [&](float f) {
+    const uint32_t b = __float_as_uint(f) & 0x7fffffffu;
+    mx = b > mx ? b : mx;
+  };
+  if (vec4) {
+    const int64_t n4 = n >> 2;
+    for (int64_t i = t0; i < n4; i += stride) {
+      const f32x4 v = reinterpret_cast<const f32x4*>(x)[i];
+      take(v[0]);
+      take(v[1]);
+      take(v[2]);
+      take(v[3]);
+    }
+    for (int64_t i = (n4 << 2) + t0; i < n; i += stride) take(x[i]);
+  } else {
+    for (int64_t i = t0; i < n; i += stride) take(x[i]);
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t v = (uint32_t)__shfl_xor((int)mx, o, 64);
+    mx = v > mx ? v : mx;
+  }
+  if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t v = wm[0];
+    for (int i = 1; i < 4; ++i) v = wm[i] > v ? wm[i] : v;
+    xpart[blockIdx.x] = v;
+  }
 }
 
-// Inclusive sums of runs of equal r over the 64 lanes, without LDS: shifts
-// by 1, 2, 4, 8 inside each 16-lane row, then lane 15 of each row into the
-// next row and lane 31 into the upper half (row_bcast:15 / :31).
-__device__ inline float seg_scan(float s, uint32_t r) {
-  s = seg_step<0x111, 0xf>(s, r);  // row_shr:1
-  s = seg_step<0x112, 0xf>(s, r);  // row_shr:2
-  s = seg_step<0x114, 0xf>(s, r);  // row_shr:4
-  s = seg_step<0x118, 0xf>(s, r);  // row_shr:8
-  s = seg_step<0x142, 0xa>(s, r);  // row_bcast:15 -> rows 1 and 3
-  s = seg_step<0x143, 0xc>(s, r);  // row_bcast:31 -> rows 2 and 3
-  return s;
+// Max |x| bits from the pre-pass's partial maxima, read by wavefront 0 of
+// the calling workgroup into *dst (LDS).
+__device__ inline void reduce_xmax(const uint32_t* __restrict__ xpart, int nxpart, uint32_t* dst) {
+  if (threadIdx.x < 64) {
+    uint32_t mx = 0;
+#pragma unroll 4
+    for (int i = threadIdx.x; i < nxpart; i += 64) {
+      const uint32_t v = xpart[i];
+      mx = v > mx ? v : mx;
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+      const uint32_t v = (uint32_t)__shfl_xor((int)mx, o, 64);
+      mx = v > mx ? v : mx;
+    }
+    if (threadIdx.x == 0) *dst = mx;
+  }
 }
 
+// e_x with max |x| < 2^e_x (0 when x is all zeros: every product is zero).
+__device__ inline int x_exponent(uint32_t xm) {
+  if (xm == 0) return 0;
+  return (int)(xm >> 23) == 0 ? -126 : (int)(xm >> 23) - 126;
+}
+
+// One workgroup per tile: the tile's entries in column order, epoch by
+// epoch. Each product p = v' * (x * 2^-e_x) (v' the plan's scaled value)
+// is rounded to an integer and added to the row's int64 sum in LDS with
+// ds_add_u64: integer sums do not depend on the order of the additions, so
+// the wavefronts run through their epochs without barriers and the result
+// is the same on every run. A product of magnitude >= 2^23 is an integer
+// already (the rounding is exact); a smaller nonzero one sets the row's bit
+// in the tile's inexact mask, which the finish kernel weighs against the
+// row's result. The tile writes its row sums (in units of the row's
+// 2^(e_r + e_x - FX_TOP), as fp32) and its inexact mask to the workspace.
 template <int RBITS, int NT>
-__global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restrict__ ent,
-                                                       const uint16_t* __restrict__ pinv,
-                                                       const int64_t* __restrict__ toff,
-                                                       const int64_t* __restrict__ eoff, const float* __restrict__ x,
-                                                       int64_t m, int cbits, int64_t G, int64_t nrb, int64_t pmax,
-                                                       int xcd_map,
-                                                       float alpha, const float* __restrict__ y, float beta,
-                                                       float* __restrict__ out, float* __restrict__ partial) {
+__global__ __launch_bounds__(NT) void colplan_spmv_fx(const uint64_t* __restrict__ ent,
+                                                      const int64_t* __restrict__ toff,
+                                                      const int64_t* __restrict__ eoff, const float* __restrict__ x,
+                                                      uint32_t* __restrict__ xpart, int nxpart, int cbits,
+                                                      int64_t G, int64_t nrb, int64_t pmax, int xcd_map,
+                                                      float* __restrict__ partial, uint32_t* __restrict__ inexact) {
   constexpr int R = 1 << RBITS;
   constexpr int W = NT / 64;
-  constexpr int K = E / 64 / W;  // chunks per wavefront in phase 1
-  constexpr int SPAN = E / W;    // phase-2 positions per wavefront
-  constexpr int PL = SPAN / 64;  // phase-2 positions per lane
-  static_assert(W == SPMV_W && K == SPMV_K && PL == SPMV_PL, "the plan's layout is made for this workgroup size");
-  constexpr uint32_t NONE = 0xffffffffu;
+  constexpr int K = E / 64 / W;  // chunks per wavefront and epoch
+  constexpr int SPAN = E / W;    // entries per wavefront and epoch
+  static_assert(W == SPMV_W && K == SPMV_K, "the plan's layout is made for this workgroup size");
   typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
-  __shared__ float acc[R + 1];                          // acc[R]: the padding positions' row
-  __shared__ __attribute__((aligned(16))) u32x2 slot[E];  // (product bits, row) at pos_slot(position)
-  __shared__ uint32_t crow[W];
-  __shared__ float cval[W];
+  __shared__ unsigned long long acc[R];
+  __shared__ uint32_t flag[R / 32];
+  __shared__ uint32_t xm_s;
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t T = nrb * G;
@@ -425,30 +431,24 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
   const int64_t g = q / nrb, rb = q - g * nrb;
   const int64_t t = rb * G + g;
 
-  for (int i = tid; i <= R; i += NT) acc[i] = 0.f;
+  for (int i = tid; i < R; i += NT) acc[i] = 0ull;
+  for (int i = tid; i < R / 32; i += NT) flag[i] = 0u;
+  reduce_xmax(xpart, nxpart, &xm_s);
 
   const int64_t cnt_t = toff[t + 1] - toff[t];
   const int64_t ep0 = eoff[t], nep = eoff[t + 1] - ep0;
   const float* __restrict__ xg = x + (g << cbits);
   const uint32_t cmask = (1u << cbits) - 1u;
 
-  // Software pipeline over epochs, with three register sets for the
-  // entries and positions and two for the gathered x values. In epoch k a
-  // wavefront issues the x gathers of epoch k + 1, multiplies epoch k's
-  // entries by its x values (gathered one epoch earlier), and refills
-  // epoch k's entry set with epoch k + 3. Vector memory loads complete in
-  // order, so waiting for epoch k's x covers the stream of epoch k + 1
-  // (issued two epochs earlier) but never the newer loads: the stream gets
-  // two epochs of lead and the gathers one.
+  // Software pipeline over epochs with three register sets of entries and
+  // two of gathered x values: in epoch k a wavefront issues the x gathers
+  // of epoch k + 1, adds epoch k's products (x gathered one epoch earlier)
+  // and refills epoch k's entry set with epoch k + 3. Chunks past the
+  // tile's entries read the plan's zero epoch after all tiles, so every
+  // load is unconditional and the padding is never fetched.
   uint64_t evA[K], evB[K], evC[K];
-  uint32_t pwA[K / 2], pwB[K / 2], pwC[K / 2];
   float xa[K], xb[K];
-  // k past the tile's last epoch: the plan's zero epoch after all tiles
-  // A chunk pair (or a lane's positions) holding no entry of the epoch (the
-  // padding of a tile's last epoch, every chunk past the tile's end) reads
-  // the plan's zero epoch instead: the load stays unconditional, and the
-  // padding is never fetched from HBM (about 6 % of the plan on cfg2).
-  auto load_epoch = [&](uint64_t (&ev)[K], uint32_t (&pw)[K / 2], int64_t k) {
+  auto load_epoch = [&](uint64_t (&ev)[K], int64_t k) {
     const int64_t left = cnt_t - (k << EBITS);  // entries of epoch k (<= 0 past the tile's end)
     const int64_t eb = (ep0 + k) << EBITS;
 #pragma unroll
@@ -459,120 +459,41 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
       ev[2 * h] = v.x;
       ev[2 * h + 1] = v.y;
     }
-    const int64_t psrc = (int64_t)(w * 64) < left ? eb : pmax;
-    const u32x2 pv = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(pinv + psrc) + w * 64 + lane);
-    pw[0] = pv.x;
-    pw[1] = pv.y;
   };
-  // gathers of an epoch's x (past the tile's end the zero epoch's column 0,
-  // which is inside x)
   auto gather = [&](float (&xv)[K], const uint64_t (&ev)[K]) {
 #pragma unroll
     for (int j = 0; j < K; ++j) xv[j] = xg[(uint32_t)ev[j] & cmask];
   };
   if (nep > 0) {
-    load_epoch(evA, pwA, 0);
-    load_epoch(evB, pwB, 1);
-    load_epoch(evC, pwC, 2);
+    load_epoch(evA, 0);
+    load_epoch(evB, 1);
+    load_epoch(evC, 2);
   }
   __syncthreads();
+  const uint32_t xm = xm_s;
+  if (blockIdx.x == 0 && tid == 0) xpart[XMAX_BLOCKS] = xm;  // for the finish kernel
+  if (xm >= 0x7f800000u) return;  // x holds inf or NaN: the finish kernel sums every row from the CSR arrays
+  const int nex = -x_exponent(xm);
 
-  auto epoch = [&](uint64_t (&ev)[K], uint32_t (&pw)[K / 2], const float (&xv)[K], const uint64_t (&evn)[K],
-                   float (&xvn)[K], int64_t k) {
+  auto epoch = [&](uint64_t (&ev)[K], const float (&xv)[K], const uint64_t (&evn)[K], float (&xvn)[K], int64_t k) {
     const int64_t left = cnt_t - (k << EBITS);
     const int cnt = left < E ? (int)left : E;
     gather(xvn, evn);
-    // ---- phase 1: products and rows in column order
 #pragma unroll
     for (int j = 0; j < K; ++j) {
       // column-order index (j * W + w) * 64 + lane < cnt, with the chunk
       // offset moved to the (uniform) right-hand side
-      const bool real = w * 64 + lane < cnt - j * W * 64;
-      const float pr = __builtin_bit_cast(float, (uint32_t)(ev[j] >> 32)) * xv[j];
-      if (real)  // the padding's positions (cnt .. E - 1 in row order) are never read
-        slot[(pw[j >> 1] >> (16 * (j & 1))) & 0xffffu] = u32x2{__builtin_bit_cast(uint32_t, pr), (uint32_t)ev[j] >> cbits};
+      if (w * 64 + lane < cnt - j * W * 64) {
+        const float v = __uint_as_float((uint32_t)(ev[j] >> 32));
+        const float p = v * ldexpf(xv[j], nex);
+        const uint32_t row = ((uint32_t)ev[j] >> cbits) & (R - 1);
+        atomicAdd(&acc[row], (unsigned long long)(long long)rintf(p));
+        if (fabsf(p) < 8388608.f && v != 0.f && xv[j] != 0.f) atomicOr(&flag[row >> 5], 1u << (row & 31));
+      }
     }
     // unconditional (past the tile's end it reads the zero epoch), so no
     // path without these loads makes the compiler wait for them early
-    load_epoch(ev, pw, k + 3);
-    __syncthreads();
-    // ---- phase 2: lane l adds positions pb .. pb + PL - 1 in row order
-    const int pb = w * SPAN + PL * lane;
-    uint32_t rr[PL];
-    float sm[PL];
-    const u32x4* __restrict__ s2 = reinterpret_cast<const u32x4*>(slot);
-#pragma unroll
-    for (int h = 0; h < PL / 2; ++h) {
-      const int P = (pb >> 1) + h;
-      const u32x4 v = s2[P ^ ((P >> 3) & 1)];  // pos_slot of positions 2P, 2P + 1
-      // (component by component: __builtin_bit_cast of a vector component
-      // reads component 0 with this compiler, so __uint_as_float)
-      // padding sorts after every row: positions cnt .. E - 1 (not written in
-      // phase 1) are the padding row R with nothing to add
-      const bool p0 = pb + 2 * h < cnt, p1 = pb + 2 * h + 1 < cnt;
-      sm[2 * h] = p0 ? __uint_as_float(v.x) : 0.f;
-      rr[2 * h] = p0 ? v.y : (uint32_t)R;
-      sm[2 * h + 1] = p1 ? __uint_as_float(v.z) : 0.f;
-      rr[2 * h + 1] = p1 ? v.w : (uint32_t)R;
-    }
-    float old[PL];  // the rows' sums before this epoch (only this lane writes a row it ends)
-#pragma unroll
-    for (int i = 0; i < PL; ++i) old[i] = acc[rr[i]];
-#pragma unroll
-    for (int i = 1; i < PL; ++i) sm[i] = rr[i] == rr[i - 1] ? sm[i - 1] + sm[i] : sm[i];
-    // sm[i]: sum of the lane's run through position i
-    const uint32_t r0 = rr[0], rl = rr[PL - 1];
-    // Tl: the lane's last run plus the same row's runs in the lanes before
-    // (a lane whose positions hold one row passes its whole sum on)
-    const float Tl = seg_scan(sm[PL - 1], rl);
-    const uint32_t next_r0 = (uint32_t)__builtin_amdgcn_update_dpp((int)NONE, (int)r0, 0x130, 0xf, 0xf, false);  // wave_shl:1
-    const uint32_t prev_rl = (uint32_t)__builtin_amdgcn_update_dpp((int)NONE, (int)rl, 0x138, 0xf, 0xf, false);  // wave_shr:1
-    const float prev_T =
-        __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, Tl), 0x138, 0xf, 0xf, false));
-    const float inc = r0 == prev_rl ? prev_T : 0.f;  // what flows into the lane's first run
-    const uint32_t first = __builtin_amdgcn_readfirstlane(r0);
-    // the wavefront's first row may continue the previous wavefront's last
-    // one: its sum goes to the carry slot (w > 0)
-    const bool to_carry = w > 0;
-    bool cf = false;
-    float cv = 0.f;
-#pragma unroll
-    for (int i = 0; i < PL - 1; ++i) {
-      if (rr[i] != rr[i + 1]) {  // a run ends inside the lane
-        const float v = sm[i] + (rr[i] == r0 ? inc : 0.f);
-        if (to_carry && rr[i] == first) {
-          cf = true;
-          cv = v;
-        } else {
-          acc[rr[i]] = old[i] + v;
-        }
-      }
-    }
-    if (next_r0 != rl) {  // the lane's last run ends here (lane 63: always)
-      if (to_carry && rl == first) {
-        cf = true;
-        cv = Tl;
-      } else {
-        acc[rl] = old[PL - 1] + Tl;
-      }
-    }
-    const uint64_t cm = __ballot(cf);  // at most one lane: the lane that ends the first row
-    // read that lane with the whole wavefront active: inside the lane-0 branch
-    // the compiler may compute cv for lane 0 only (a readlane of an inactive
-    // lane returns a stale register)
-    const float cvl = __builtin_bit_cast(
-        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv), cm ? (int)__builtin_ctzll(cm) : 0));
-    if (lane == 0) {
-      crow[w] = cm ? first : NONE;
-      cval[w] = cm ? cvl : 0.f;
-    }
-    __syncthreads();
-    if (w == 0) {  // the carries, in wavefront order: rows ascend with w
-      const uint32_t cr = lane < W ? crow[lane] : NONE;
-      const float cs = seg_scan(lane < W ? cval[lane] : 0.f, cr);
-      const uint32_t crn = (uint32_t)__builtin_amdgcn_update_dpp((int)NONE, (int)cr, 0x130, 0xf, 0xf, false);
-      if (cr != NONE && (lane == 63 || crn != cr)) acc[cr] += cs;
-    }
+    load_epoch(ev, k + 3);
   };
 
   // Six epochs per trip (the period of three entry sets and two x sets),
@@ -582,65 +503,104 @@ __global__ __launch_bounds__(NT) void colplan_spmv_f32(const uint64_t* __restric
   if (nep > 0) gather(xa, evA);
   int64_t k = 0;
   for (; k + 5 < nep; k += 6) {
-    epoch(evA, pwA, xa, evB, xb, k);
-    epoch(evB, pwB, xb, evC, xa, k + 1);
-    epoch(evC, pwC, xa, evA, xb, k + 2);
-    epoch(evA, pwA, xb, evB, xa, k + 3);
-    epoch(evB, pwB, xa, evC, xb, k + 4);
-    epoch(evC, pwC, xb, evA, xa, k + 5);
+    epoch(evA, xa, evB, xb, k);
+    epoch(evB, xb, evC, xa, k + 1);
+    epoch(evC, xa, evA, xb, k + 2);
+    epoch(evA, xb, evB, xa, k + 3);
+    epoch(evB, xa, evC, xb, k + 4);
+    epoch(evC, xb, evA, xa, k + 5);
   }
-  if (k < nep) epoch(evA, pwA, xa, evB, xb, k);
-  if (k + 1 < nep) epoch(evB, pwB, xb, evC, xa, k + 1);
-  if (k + 2 < nep) epoch(evC, pwC, xa, evA, xb, k + 2);
-  if (k + 3 < nep) epoch(evA, pwA, xb, evB, xa, k + 3);
-  if (k + 4 < nep) epoch(evB, pwB, xa, evC, xb, k + 4);
+  if (k < nep) epoch(evA, xa, evB, xb, k);
+  if (k + 1 < nep) epoch(evB, xb, evC, xa, k + 1);
+  if (k + 2 < nep) epoch(evC, xa, evA, xb, k + 2);
+  if (k + 3 < nep) epoch(evA, xb, evB, xa, k + 3);
+  if (k + 4 < nep) epoch(evB, xa, evC, xb, k + 4);
   __syncthreads();
 
-  const int64_t r0 = rb << RBITS;
-  if (G == 1) {
-    for (int i = tid; i < R; i += NT) {
-      const int64_t r = r0 + i;
-      if (r < m) {
-        float res = alpha * acc[i];
-        if (y) res = res + beta * y[r];
-        out[r] = res;
-      }
+  // the workspace holds nrb * R rows per group (rows past m stay zero)
+  float* __restrict__ pg = partial + (g * nrb + rb) * R;
+  for (int i = tid; i < R; i += NT) pg[i] = (float)(long long)acc[i];
+  uint32_t* __restrict__ fg = inexact + (g * nrb + rb) * (R / 32);
+  for (int i = tid; i < R / 32; i += NT) fg[i] = flag[i];
+}
+
+// Row r of the result: y_r = the sum of the G group partials (added in
+// group order) scaled by 2^(e_r + e_x - FX_TOP), then alpha * y_r (+ beta *
+// y[r]). The row is summed from the CSR arrays instead (fp32 products in
+// CSR order, an fp64 sum) when x holds inf or NaN, when the row's exponent
+// says so, or when one of its products was rounded and |y_r| is below
+// cnt * 2^23 units: then the rounding (at most half a unit per product)
+// could exceed 2^-24 of the result.
+template <typename IdxT>
+__device__ inline float finish_row(float s, bool inex, int16_t er, uint32_t xm, int64_t r,
+                                   const float* __restrict__ vals, const IdxT* __restrict__ cols,
+                                   const IdxT* __restrict__ ptr, const float* __restrict__ x) {
+  bool redo = xm >= 0x7f800000u || er == RX_REDO;
+  if (!redo) {
+    const int sh = (int)er + x_exponent(xm) - FX_TOP;
+    s = ldexpf(s, sh);
+    if (inex && fabsf(s) < ldexpf((float)((int64_t)ptr[r + 1] - (int64_t)ptr[r]), sh + 23)) redo = true;
+  }
+  if (redo) {
+    double a = 0.0;
+    for (int64_t p = (int64_t)ptr[r]; p < (int64_t)ptr[r + 1]; ++p) a += (double)(vals[p] * x[(int64_t)cols[p]]);
+    s = (float)a;
+  }
+  return s;
+}
+
+// Four rows per thread (m % 4 == 0, 16-byte aligned out and y: VEC) or one.
+template <typename IdxT, bool VEC>
+__global__ __launch_bounds__(256) void colplan_finish_fx(const float* __restrict__ partial,
+                                                         const uint32_t* __restrict__ inexact, int64_t prows,
+                                                         int64_t G, const int16_t* __restrict__ rexp,
+                                                         const uint32_t* __restrict__ xmax,
+                                                         const float* __restrict__ vals,
+                                                         const IdxT* __restrict__ cols, const IdxT* __restrict__ ptr,
+                                                         const float* __restrict__ x, int64_t m, float alpha,
+                                                         const float* __restrict__ y, float beta,
+                                                         float* __restrict__ out) {
+  constexpr int NR = VEC ? 4 : 1;
+  const int64_t r0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * NR;
+  if (r0 >= m) return;
+  const uint32_t xm = *xmax;
+  float s[NR];
+  uint32_t fl = 0;  // inexact bits of the NR rows
+  int16_t er[NR];
+  if (VEC) {
+    f32x4 acc = *reinterpret_cast<const f32x4*>(partial + r0);
+    fl = inexact[r0 >> 5];
+    for (int64_t g = 1; g < G; ++g) {
+      acc += *reinterpret_cast<const f32x4*>(partial + g * prows + r0);
+      fl |= inexact[g * (prows >> 5) + (r0 >> 5)];
+    }
+    fl >>= (r0 & 31);
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    const s16x4 e4 = *reinterpret_cast<const s16x4*>(rexp + r0);
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      s[i] = acc[i];
+      er[i] = e4[i];
     }
   } else {
-    float* __restrict__ pg = partial + g * m;
-    for (int i = tid; i < R; i += NT) {
-      const int64_t r = r0 + i;
-      if (r < m) pg[r] = acc[i];
+    s[0] = 0.f;
+    for (int64_t g = 0; g < G; ++g) {
+      s[0] += partial[g * prows + r0];
+      fl |= inexact[g * (prows >> 5) + (r0 >> 5)];
     }
+    fl >>= (r0 & 31);
+    er[0] = rexp[r0];
   }
-}
-
-// out[r] = alpha * (partial[0][r] + ... + partial[G-1][r]) (+ beta * y[r]),
-// the groups added in increasing order.
-__global__ __launch_bounds__(256) void colplan_finish_f32(const float* __restrict__ partial, int64_t m, int64_t G,
-                                                          float alpha, const float* __restrict__ y, float beta,
-                                                          float* __restrict__ out) {
-  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= m) return;
-  float s = partial[r];
-  for (int64_t g = 1; g < G; ++g) s += partial[g * m + r];
-  float res = alpha * s;
-  if (y) res = res + beta * y[r];
-  out[r] = res;
-}
-
-// The same for m a multiple of 4 with 16-byte aligned y and out: four rows
-// per thread, 16-byte loads and stores (the same additions in the same order).
-__global__ __launch_bounds__(256) void colplan_finish4_f32(const float* __restrict__ partial, int64_t m, int64_t G,
-                                                           float alpha, const float* __restrict__ y, float beta,
-                                                           float* __restrict__ out) {
-  const int64_t r = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
-  if (r >= m) return;
-  f32x4 s = *reinterpret_cast<const f32x4*>(partial + r);
-  for (int64_t g = 1; g < G; ++g) s += *reinterpret_cast<const f32x4*>(partial + g * m + r);
-  f32x4 res = alpha * s;
-  if (y) res = res + beta * *reinterpret_cast<const f32x4*>(y + r);
-  *reinterpret_cast<f32x4*>(out + r) = res;
+  float res[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    res[i] = alpha * finish_row(s[i], ((fl >> i) & 1u) != 0, er[i], xm, r0 + i, vals, cols, ptr, x);
+    if (y) res[i] = res[i] + beta * y[r0 + i];
+  }
+  if (VEC)
+    *reinterpret_cast<f32x4*>(out + r0) = f32x4{res[0], res[1 % NR], res[2 % NR], res[3 % NR]};
+  else
+    out[r0] = res[0];
 }
 
 // ------------------------------------------------------------- geometry
@@ -683,10 +643,11 @@ int geometry(int64_t m, int64_t n, int64_t nnz, int rbits_hint, int64_t tiles_hi
   g[GEOM_G] = G;
   g[GEOM_T] = T;
   g[GEOM_KEYBITS] = keybits;
-  g[GEOM_PLAN_BYTES] = 2 * align256((T + 1) * 8) + align256((pmax + E) * 8) + align256((pmax + E) * 2) +
-                        align256((pmax + E) * 4) + 256;  // + the header (row_ptrs[0] of the built pattern)
+  g[GEOM_PLAN_BYTES] = 2 * align256((T + 1) * 8) + align256((pmax + E) * 8) + align256((pmax + E) * 4) +
+                        256 + align256(m * 2);  // + the header (row_ptrs[0] of the built pattern), row exponents
   g[GEOM_BUILD_BYTES] = 2 * align256(nnz * ksz) + 2 * align256(nnz * 8) + align256((int64_t)tmp);
-  g[GEOM_SPMV_BYTES] = G > 1 ? G * m * 4 : 0;
+  const int64_t prows = nrb << rbits;  // rows of one group's partial sums
+  g[GEOM_SPMV_BYTES] = align256(G * prows * 4) + align256(G * (prows >> 5) * 4) + (XMAX_BLOCKS + 1) * 4;
   g[GEOM_PMAX] = pmax;
   return TSP_OK;
 }
@@ -695,8 +656,8 @@ struct PlanView {
   int64_t* toff;
   int64_t* eoff;
   uint64_t* ent;
-  uint16_t* pinv;
   uint32_t* pos;
+  int16_t* rexp;  // row exponents (one per row of the matrix)
   int64_t* base;  // row_ptrs[0] of the pattern the plan was built from
   int64_t pmax;
 };
@@ -712,11 +673,10 @@ PlanView plan_view(void* plan, const int64_t* g) {
   p += align256((T + 1) * 8);
   v.ent = (uint64_t*)p;
   p += align256((v.pmax + E) * 8);
-  v.pinv = (uint16_t*)p;
-  p += align256((v.pmax + E) * 2);
   v.pos = (uint32_t*)p;
   p += align256((v.pmax + E) * 4);
   v.base = (int64_t*)p;
+  v.rexp = (int16_t*)(p + 256);  // after the 256-byte header, one per row
   return v;
 }
 
@@ -756,7 +716,7 @@ int build_typed(const float* vals, const void* col, const void* ptr, int64_t m, 
   if (e != hipSuccess) return tsp::check_hip(e, "tsp_csr_colplan_build: sort size query");
   PlanView v = plan_view(plan, g);
   hipLaunchKernelGGL(colplan_fill_kernel, dim3((unsigned)tsp::ceil_div(v.pmax + E, 256)), dim3(256), 0, st, v.ent,
-                     v.pinv, v.pos, v.pmax + E);
+                     v.pos, v.pmax + E);
   int rc = tsp::check_launch("colplan_fill launch");
   if (rc) return rc;
   if (nnz > 0) {
@@ -775,25 +735,23 @@ int build_typed(const float* vals, const void* col, const void* ptr, int64_t m, 
   if (rc) return rc;
   hipLaunchKernelGGL(colplan_epochs_kernel, dim3(1), dim3(1024), 0, st, v.toff, T, v.eoff);
   rc = tsp::check_launch("colplan_epochs launch");
+  if (rc) return rc;
+  hipLaunchKernelGGL((colplan_rowexp_kernel<IdxT>), dim3((unsigned)tsp::ceil_div(m, 256)), dim3(256), 0, st, vals,
+                     (const IdxT*)ptr, m, v.rexp);
+  rc = tsp::check_launch("colplan_rowexp launch");
   if (rc || nnz == 0) return rc;
   hipLaunchKernelGGL((colplan_scatter_kernel<K>), dim3((unsigned)tsp::ceil_div(nnz, 256)), dim3(256), 0, st, kout,
-                     pout, vals, nnz, cbits, v.toff, v.eoff, T, v.base, v.ent, v.pos);
-  rc = tsp::check_launch("colplan_scatter launch");
-  if (rc) return rc;
-  // one workgroup per epoch; the grid covers the upper bound pmax / E
-  hipLaunchKernelGGL(colplan_perm_kernel, dim3((unsigned)(v.pmax >> EBITS)), dim3(1024), 0, st, v.ent, v.toff,
-                     v.eoff, T, rbits, cbits, v.pinv);
-  return tsp::check_launch("colplan_perm launch");
+                     pout, vals, nnz, rbits, cbits, G, v.toff, v.eoff, T, v.base, v.rexp, v.ent, v.pos);
+  return tsp::check_launch("colplan_scatter launch");
 }
 
 template <int RBITS>
-void launch_spmv(const PlanView& v, const float* x, int64_t m, const int64_t* g, float alpha, const float* y,
-                 float beta, float* out, float* partial, hipStream_t st) {
+void launch_spmv(const PlanView& v, const float* x, uint32_t* xpart, int nxpart, const int64_t* g,
+                 float* partial, uint32_t* inexact, hipStream_t st) {
   const int64_t T = g[GEOM_T];
   const int xcd_map = (T % 8) == 0 ? 1 : 0;
-  hipLaunchKernelGGL((colplan_spmv_f32<RBITS, SPMV_NT>), dim3((unsigned)T), dim3(SPMV_NT), 0, st, v.ent, v.pinv, v.toff,
-                     v.eoff, x, m, (int)g[GEOM_CBITS], g[GEOM_G], g[GEOM_NRB], v.pmax, xcd_map, alpha, y, beta, out,
-                     partial);
+  hipLaunchKernelGGL((colplan_spmv_fx<RBITS, SPMV_NT>), dim3((unsigned)T), dim3(SPMV_NT), 0, st, v.ent, v.toff, v.eoff,
+                     x, xpart, nxpart, (int)g[GEOM_CBITS], g[GEOM_G], g[GEOM_NRB], v.pmax, xcd_map, partial, inexact);
 }
 
 }  // namespace
@@ -823,45 +781,73 @@ extern "C" int tsp_csr_colplan_build(const void* values, int dtype, const void* 
              : build_typed<int32_t, uint64_t>((const float*)values, col_indices, row_ptrs, m, nnz, geometry, plan, workspace, st);
 }
 
-extern "C" int tsp_csr_colplan_refresh(const void* values, int dtype, int64_t m, int64_t n, int64_t nnz,
-                                       const int64_t* geometry, void* plan, void* stream) {
+extern "C" int tsp_csr_colplan_refresh(const void* values, int dtype, const void* row_ptrs, int index_type, int64_t m,
+                                       int64_t n, int64_t nnz, const int64_t* geometry, void* plan, void* stream) {
   if (dtype != TSP_F32) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_colplan_refresh: dtype %d (the plan holds fp32 values)", dtype);
+  if (index_type != TSP_I32 && index_type != TSP_I64) return tsp::fail(TSP_EINVAL, "tsp_csr_colplan_refresh: bad index_type");
   int rc = check_geom("tsp_csr_colplan_refresh", m, n, nnz, geometry);
   if (rc) return rc;
-  if (nnz == 0) return TSP_OK;
-  if (!values || !plan) return tsp::fail(TSP_EINVAL, "tsp_csr_colplan_refresh: null pointer");
+  if (!row_ptrs || !plan || (nnz > 0 && !values)) return tsp::fail(TSP_EINVAL, "tsp_csr_colplan_refresh: null pointer");
+  hipStream_t st = (hipStream_t)stream;
   PlanView v = plan_view(plan, geometry);
-  hipLaunchKernelGGL(colplan_refresh_kernel, dim3((unsigned)tsp::ceil_div(v.pmax, 256)), dim3(256), 0,
-                     (hipStream_t)stream, (const float*)values, v.pos, v.pmax, v.base, v.ent);
+  if (index_type == TSP_I64)
+    hipLaunchKernelGGL((colplan_rowexp_kernel<int64_t>), dim3((unsigned)tsp::ceil_div(m, 256)), dim3(256), 0, st,
+                       (const float*)values, (const int64_t*)row_ptrs, m, v.rexp);
+  else
+    hipLaunchKernelGGL((colplan_rowexp_kernel<int32_t>), dim3((unsigned)tsp::ceil_div(m, 256)), dim3(256), 0, st,
+                       (const float*)values, (const int32_t*)row_ptrs, m, v.rexp);
+  rc = tsp::check_launch("colplan_rowexp launch");
+  if (rc || nnz == 0) return rc;
+  hipLaunchKernelGGL(colplan_refresh_kernel, dim3((unsigned)tsp::ceil_div(v.pmax, 256)), dim3(256), 0, st,
+                     (const float*)values, v.pos, v.pmax, v.base, v.eoff, geometry[GEOM_T], geometry[GEOM_G],
+                     (int)geometry[GEOM_RBITS], (int)geometry[GEOM_CBITS], v.rexp, v.ent);
   return tsp::check_launch("colplan_refresh launch");
 }
 
 extern "C" int tsp_csr_colplan_spmv(const void* plan, int dtype, int64_t m, int64_t n, int64_t nnz,
-                                    const int64_t* geometry, const void* x, double alpha, const void* y, double beta,
-                                    void* out, void* workspace, void* stream) {
+                                    const int64_t* geometry, const void* values, const void* col_indices,
+                                    const void* row_ptrs, int index_type, const void* x, double alpha, const void* y,
+                                    double beta, void* out, void* workspace, void* stream) {
   if (dtype != TSP_F32) return tsp::fail(TSP_EUNSUPPORTED, "tsp_csr_colplan_spmv: dtype %d (the plan holds fp32 values)", dtype);
+  if (index_type != TSP_I32 && index_type != TSP_I64) return tsp::fail(TSP_EINVAL, "tsp_csr_colplan_spmv: bad index_type");
   int rc = check_geom("tsp_csr_colplan_spmv", m, n, nnz, geometry);
   if (rc) return rc;
-  if (!plan || !x || !out) return tsp::fail(TSP_EINVAL, "tsp_csr_colplan_spmv: null pointer");
-  const int64_t G = geometry[GEOM_G];
-  if (G > 1 && !workspace) return tsp::fail(TSP_EINVAL, "tsp_csr_colplan_spmv: null workspace (%lld column groups)", (long long)G);
+  if (!plan || !x || !out || !workspace || !row_ptrs || (nnz > 0 && (!values || !col_indices)))
+    return tsp::fail(TSP_EINVAL, "tsp_csr_colplan_spmv: null pointer");
   hipStream_t st = (hipStream_t)stream;
   const float* yy = (y && beta != 0.0) ? (const float*)y : nullptr;
   PlanView v = plan_view((void*)plan, geometry);
+  const int64_t G = geometry[GEOM_G], prows = geometry[GEOM_NRB] << geometry[GEOM_RBITS];
+  uint8_t* w = (uint8_t*)workspace;
+  float* partial = (float*)w;
+  w += align256(G * prows * 4);
+  uint32_t* inexact = (uint32_t*)w;
+  w += align256(G * (prows >> 5) * 4);
+  uint32_t* xpart = (uint32_t*)w;  // XMAX_BLOCKS partial maxima, then the maximum
+  const int vec4 = ((uintptr_t)x % 16) == 0;
+  const int nxpart = (int)std::min<int64_t>(XMAX_BLOCKS, tsp::ceil_div(n, vec4 ? 1024 : 256));
+  hipLaunchKernelGGL(colplan_xmax_kernel, dim3((unsigned)nxpart), dim3(256), 0, st, (const float*)x, n, vec4, xpart);
+  rc = tsp::check_launch("colplan_xmax launch");
+  if (rc) return rc;
   switch (geometry[GEOM_RBITS]) {
-    case 12: launch_spmv<12>(v, (const float*)x, m, geometry, (float)alpha, yy, (float)beta, (float*)out, (float*)workspace, st); break;
-    case 13: launch_spmv<13>(v, (const float*)x, m, geometry, (float)alpha, yy, (float)beta, (float*)out, (float*)workspace, st); break;
-    default: launch_spmv<14>(v, (const float*)x, m, geometry, (float)alpha, yy, (float)beta, (float*)out, (float*)workspace, st); break;
+    case 12: launch_spmv<12>(v, (const float*)x, xpart, nxpart, geometry, partial, inexact, st); break;
+    case 13: launch_spmv<13>(v, (const float*)x, xpart, nxpart, geometry, partial, inexact, st); break;
+    default: launch_spmv<14>(v, (const float*)x, xpart, nxpart, geometry, partial, inexact, st); break;
   }
   rc = tsp::check_launch("colplan_spmv launch");
-  if (rc || G == 1) return rc;
-  const bool vec4 = m % 4 == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)yy & 15) == 0 &&
-                    ((uintptr_t)workspace & 15) == 0;
-  if (vec4)
-    hipLaunchKernelGGL(colplan_finish4_f32, dim3((unsigned)tsp::ceil_div(m / 4, 256)), dim3(256), 0, st,
-                       (const float*)workspace, m, G, (float)alpha, yy, (float)beta, (float*)out);
-  else
-    hipLaunchKernelGGL(colplan_finish_f32, dim3((unsigned)tsp::ceil_div(m, 256)), dim3(256), 0, st,
-                       (const float*)workspace, m, G, (float)alpha, yy, (float)beta, (float*)out);
+  if (rc) return rc;
+  const bool vec = m % 4 == 0 && ((uintptr_t)out % 16) == 0 && ((uintptr_t)yy % 16) == 0;
+  const unsigned fgrid = (unsigned)tsp::ceil_div(vec ? m / 4 : m, 256);
+  const uint32_t* xm = xpart + XMAX_BLOCKS;
+#define TSP_FINISH(IT, V)                                                                                             \
+  hipLaunchKernelGGL((colplan_finish_fx<IT, V>), dim3(fgrid), dim3(256), 0, st, partial, inexact, prows, G, v.rexp, xm, \
+                     (const float*)values, (const IT*)col_indices, (const IT*)row_ptrs, (const float*)x, m,           \
+                     (float)alpha, yy, (float)beta, (float*)out)
+  if (index_type == TSP_I64) {
+    if (vec) TSP_FINISH(int64_t, true); else TSP_FINISH(int64_t, false);
+  } else {
+    if (vec) TSP_FINISH(int32_t, true); else TSP_FINISH(int32_t, false);
+  }
+#undef TSP_FINISH
   return tsp::check_launch("colplan_finish launch");
 }

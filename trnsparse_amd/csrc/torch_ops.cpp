@@ -230,15 +230,18 @@ at::Tensor csr_spmv_meta(const at::Tensor&, const at::Tensor&, const at::Tensor&
   return at::empty({m}, x.options());
 }
 
-at::Tensor csr_colplan_spmv(const at::Tensor& plan, const at::Tensor& geometry, int64_t m, int64_t n, int64_t nnz,
-                            const at::Tensor& x, double alpha, const c10::optional<at::Tensor>& y, double beta) {
+at::Tensor csr_colplan_spmv(const at::Tensor& plan, const at::Tensor& geometry, const at::Tensor& values,
+                            const at::Tensor& cols, const at::Tensor& ptrs, int64_t m, int64_t n, const at::Tensor& x,
+                            double alpha, const c10::optional<at::Tensor>& y, double beta) {
   need(plan, x, "plan");
+  for (auto* p : {&values, &cols, &ptrs}) need(*p, x, "matrix");
   need(x, x, "x");
   if (y.has_value()) need(*y, x, "y");
   TORCH_CHECK(geometry.device().is_cpu() && geometry.scalar_type() == at::kLong && geometry.numel() == 10 &&
                   geometry.is_contiguous(),
               "csr_colplan_spmv: geometry must be the 10 int64 host values of tsp_csr_colplan_geometry");
   const int64_t* geom = geometry.data_ptr<int64_t>();
+  need_csr(values, cols, ptrs, m, n, x, "csr_colplan_spmv");
   need_dtype(x, at::kFloat, "csr_colplan_spmv", "x");
   need_numel(x, n, "csr_colplan_spmv", "x");
   if (y.has_value()) {
@@ -248,17 +251,17 @@ at::Tensor csr_colplan_spmv(const at::Tensor& plan, const at::Tensor& geometry, 
   TORCH_CHECK(plan.nbytes() >= (size_t)geom[6], "csr_colplan_spmv: plan holds ", plan.nbytes(),
               " bytes, the geometry needs ", geom[6]);
   auto out = at::empty({m}, x.options());
-  at::Tensor work;
-  if (geom[8] > 0) work = at::empty({geom[8]}, x.options().dtype(at::kByte));
-  check(tsp_csr_colplan_spmv(plan.data_ptr(), dtype_code(x.scalar_type()), m, n, nnz, geom, x.data_ptr(), alpha,
-                             opt_ptr(y), beta, out.data_ptr(), work.defined() ? work.data_ptr() : nullptr,
-                             stream_of(x)),
+  at::Tensor work = at::empty({geom[8]}, x.options().dtype(at::kByte));
+  check(tsp_csr_colplan_spmv(plan.data_ptr(), dtype_code(x.scalar_type()), m, n, values.numel(), geom,
+                             values.data_ptr(), cols.data_ptr(), ptrs.data_ptr(), index_code(cols.scalar_type()),
+                             x.data_ptr(), alpha, opt_ptr(y), beta, out.data_ptr(), work.data_ptr(), stream_of(x)),
         "tsp_csr_colplan_spmv");
   return out;
 }
 
-at::Tensor csr_colplan_spmv_meta(const at::Tensor&, const at::Tensor&, int64_t m, int64_t, int64_t,
-                                 const at::Tensor& x, double, const c10::optional<at::Tensor>&, double) {
+at::Tensor csr_colplan_spmv_meta(const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+                                 const at::Tensor&, int64_t m, int64_t, const at::Tensor& x, double,
+                                 const c10::optional<at::Tensor>&, double) {
   return at::empty({m}, x.options());
 }
 
@@ -461,8 +464,8 @@ TORCH_LIBRARY(trnsparse_hip, m) {
         "int m, int n, int block_size, Tensor grad_out) -> Tensor");
   m.def("csr_spmv(Tensor values, Tensor col_indices, Tensor row_ptrs, Tensor windows, int m, int n, Tensor x, "
         "float alpha, Tensor? y, float beta) -> Tensor");
-  m.def("csr_colplan_spmv(Tensor plan, Tensor geometry, int m, int n, int nnz, Tensor x, float alpha, Tensor? y, "
-        "float beta) -> Tensor");
+  m.def("csr_colplan_spmv(Tensor plan, Tensor geometry, Tensor values, Tensor col_indices, Tensor row_ptrs, int m, "
+        "int n, Tensor x, float alpha, Tensor? y, float beta) -> Tensor");
   m.def("csr_spmm(Tensor values, Tensor col_indices, Tensor row_ptrs, int m, int n, Tensor X, float alpha, "
         "Tensor? Y, float beta) -> Tensor");
   m.def("screened_spmm(Tensor A, Tensor diag_integrals, Tensor B, float threshold_sqrt) -> Tensor");

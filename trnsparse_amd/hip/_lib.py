@@ -55,8 +55,8 @@ SIGNATURES: dict[str, tuple] = {
     "tsp_csr_spmv": (_INT, [_P, _INT, _P, _P, _INT, _I64, _I64, _I64, _P, _P, _DBL, _P, _DBL, _P, _P]),
     "tsp_csr_colplan_geometry": (_INT, [_I64, _I64, _I64, _INT, _I64, _P]),
     "tsp_csr_colplan_build": (_INT, [_P, _INT, _P, _P, _INT, _I64, _I64, _I64, _P, _P, _P, _P]),
-    "tsp_csr_colplan_refresh": (_INT, [_P, _INT, _I64, _I64, _I64, _P, _P, _P]),
-    "tsp_csr_colplan_spmv": (_INT, [_P, _INT, _I64, _I64, _I64, _P, _P, _DBL, _P, _DBL, _P, _P, _P]),
+    "tsp_csr_colplan_refresh": (_INT, [_P, _INT, _P, _INT, _I64, _I64, _I64, _P, _P, _P]),
+    "tsp_csr_colplan_spmv": (_INT, [_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _INT, _P, _DBL, _P, _DBL, _P, _P, _P]),
     "tsp_csr_spmm": (
         _INT,
         [_P, _INT, _P, _P, _INT, _I64, _I64, _I64, _P, _I64, _I64, _DBL, _P, _I64, _DBL, _P, _I64, _P],

@@ -285,8 +285,8 @@ def _csr_forward(vals, cols, ptrs, win, shape, X, alpha, Y, beta, dev, colplan=N
             return out
         if colplan is not None:
             _, geom, plan = colplan
-            return _lib.ops().csr_colplan_spmv(plan, _geometry_tensor(geom), m, n, vals.numel(), Xd, float(alpha), Yd,
-                                               float(beta))
+            return _lib.ops().csr_colplan_spmv(plan, _geometry_tensor(geom), vals, cols, ptrs, m, n, Xd, float(alpha),
+                                               Yd, float(beta))
         return _lib.ops().csr_spmv(vals, cols, ptrs, win, m, n, Xd, float(alpha), Yd, float(beta))
     ncols = Xd.shape[1]
     if use_y and Yd.shape != (m, ncols):
@@ -378,8 +378,9 @@ def _csr_colplan(A, vals, cols, ptrs, dev, rows_per_block_log2: int = 0, tiles_h
                 except AttributeError:
                     pass
                 return None
-            _lib.call("tsp_csr_colplan_refresh", vals.data_ptr(), _lib.TSP_F32, m, n, nnz, geom.ctypes.data,
-                      plan.data_ptr(), _lib.stream_handle(dev))
+            _lib.call("tsp_csr_colplan_refresh", vals.data_ptr(), _lib.TSP_F32, ptrs.data_ptr(),
+                      _lib.index_code(ptrs.dtype), m, n, nnz, geom.ctypes.data, plan.data_ptr(),
+                      _lib.stream_handle(dev))
         A._hip_colplan = (skey, vkey, geom, plan, uses + 1)
         return geom, plan
     if mode == "auto":

@@ -18,50 +18,48 @@
 // order of R rows: at cfg2 density (R = 16384 rows, 0.25 nonzeros per
 // column) about 256 columns, 8 lines of 128 bytes, coalesced by the address
 // unit into 8 requests instead of 64. Each tile still reads its whole x
-// slice through L1 once, so the x traffic is (m / R) x n x 4 bytes: 16384-
-// row tiles (64 KiB of LDS row sums, one 1024-thread workgroup per CU) read
-// half what 8192-row tiles (two 512-thread workgroups per CU) read, and
-// were measured faster on cfg2 (61.6 us against 66.8 us).
+// slice through L1 once, so the x traffic is (m / R) x n x 4 bytes. 16384-
+// row tiles (128 KiB of int64 LDS row sums, one 1024-thread workgroup per
+// CU) in 4 column groups measured fastest on cfg2 (51.8 us; 8192-row tiles
+// two per CU 61.2, 4096-row 73.2, 8 column groups 64.7).
 //
-// Row sums without atomics. Float add atomics in LDS (ds_add_f32) run at a
-// small fraction of the rate of other LDS operations on gfx950 (measured:
-// they made this kernel 2.2x slower than plain LDS read-modify-write, with
-// or without bank conflicts), so each epoch runs in two phases separated by
-// a barrier:
-//   phase 1  wavefronts take 64-entry chunks round robin, gather x, and
-//            store product and row into LDS at the entry's position in row
-//            order (the plan's per-epoch inverse permutation, 16 bits per
-//            entry);
-//   phase 2  wavefront w owns positions w*E/W .. (w+1)*E/W - 1 of the
-//            epoch and lane l of it the 4 consecutive positions from
-//            w*E/W + 4l (two 16-byte LDS reads). The lane adds its runs of
-//            equal rows in order; a run that ends inside the lane is added
-//            to the tile's LDS row sum by a plain read-modify-write. Runs
-//            that cross lanes are joined by one segmented scan of the lanes'
-//            last runs (key: row), so each row is written by exactly one
-//            lane, except the wavefront's first row, whose sum goes to a
-//            carry slot that wavefront 0 adds after the epoch's closing
-//            barrier, in wavefront order. (The first form of this phase
-//            scanned every 64-position chunk across lanes: several times
-//            the VALU work, 82 us against 67 us on cfg2.)
-// Every sum is taken in a fixed order, so results are deterministic.
-// With G > 1 column groups each tile writes its row sums to a partial
-// vector and a second kernel adds the G partials per row in group order
-// and applies alpha / beta.
+// Row sums in exact fixed point. Float add atomics in LDS (ds_add_f32) run
+// at a small fraction of the rate of integer LDS atomics on gfx950 (a tile
+// kernel built on them took 108 us on cfg2 against 46 us with ds_add_u64),
+// and integer sums do not depend on the order of the additions. So the plan
+// keeps each value scaled by a power of two per row, v' = v * 2^(61 - e_r)
+// with sum_j |v_rj| < 2^e_r (e_r from the row's largest value and entry
+// count), a pre-pass finds max |x| < 2^e_x, and the tile kernel adds
+// rint(v' * x * 2^-e_x) to the row's int64 sum in LDS with ds_add_u64: every
+// partial sum stays below 2^61 units, a product of at least 2^23 units is
+// an integer already (so the sum is the exact sum of the fp32 products), and
+// a smaller nonzero one sets the row's bit in an inexact mask. Wavefronts
+// run through their epochs with no barrier (the previous form of this
+// kernel ordered every epoch's products by row through a 16-bit row-order
+// position per entry and two LDS phases per epoch: 57.5 us on cfg2 against
+// 51.8 us now, Zipf rows 185 against 161). The sums do not depend on the
+// order of the additions, so results are the same on every run.
+// With G column groups each tile writes its row sums (as fp32, in units of
+// 2^(e_r + e_x - 61)) and its inexact mask to the workspace, and the finish
+// kernel adds the G partials per row in group order, scales them and
+// applies alpha / beta. It sums a row again from the caller's CSR arrays
+// (fp32 products in CSR order, an fp64 sum) when x holds inf or NaN, when
+// the row holds a non-finite value or a nonzero value that the scaling
+// would push below the normal range, or when one of the row's products was
+// rounded and the result is below cnt * 2^23 units (the rounding could then
+// exceed 2^-24 of it).
 //
 // Plan buffer (device): toff (T+1 int64, first sorted entry of each tile),
 // eoff (T+1 int64, first epoch of each tile), ent (8 bytes per padded entry:
-// value bits << 32 | row_in_tile << cbits | column_in_group), pinv (uint16
-// per padded entry: the entry's position in the epoch's row order, swizzled
-// for phase 2's 16-byte reads), pos (uint32 per padded entry: position k in
-// the pattern's entries, for new values on the same pattern, read at
-// values[row_ptrs[0] + k]; 0xffffffff for padding), and a 256-byte header
-// holding row_ptrs[0] (int64). Inside an epoch, ent and pos are stored in the SpMV
-// kernel's lane order (entry_slot below): one 16-byte load gives a lane two
-// of its chunks' entries, and pinv holds a lane's 4 positions in 8
-// consecutive bytes. The three per-entry arrays hold one more epoch of zeros
-// past the last tile's, which the SpMV kernel's prefetch reads when a tile
-// has no epoch left to prefetch.
+// scaled value bits << 32 | row_in_tile << cbits | column_in_group), pos
+// (uint32 per padded entry: position k in the pattern's entries, for new
+// values on the same pattern, read at values[row_ptrs[0] + k]; 0xffffffff
+// for padding), a 256-byte header holding row_ptrs[0] (int64), then the row
+// exponents (int16 per row of the matrix). Inside an epoch, ent and pos are
+// stored in the SpMV kernel's lane order (entry_slot below): one 16-byte
+// load gives a lane two of its chunks' entries. The two per-entry arrays
+// hold one more epoch of zeros past the last tile's, which the SpMV
+// kernel's prefetch reads when a tile has no epoch left to prefetch.
 #include <algorithm>
 
 #include "common.h"
@@ -431,10 +429,6 @@ __global__ __launch_bounds__(NT) void colplan_spmv_fx(const uint64_t* __restrict
   const int64_t g = q / nrb, rb = q - g * nrb;
   const int64_t t = rb * G + g;
 
-  for (int i = tid; i < R; i += NT) acc[i] = 0ull;
-  for (int i = tid; i < R / 32; i += NT) flag[i] = 0u;
-  reduce_xmax(xpart, nxpart, &xm_s);
-
   const int64_t cnt_t = toff[t + 1] - toff[t];
   const int64_t ep0 = eoff[t], nep = eoff[t + 1] - ep0;
   const float* __restrict__ xg = x + (g << cbits);
@@ -464,11 +458,17 @@ __global__ __launch_bounds__(NT) void colplan_spmv_fx(const uint64_t* __restrict
 #pragma unroll
     for (int j = 0; j < K; ++j) xv[j] = xg[(uint32_t)ev[j] & cmask];
   };
+  // the first epochs' loads go out before the row sums are cleared and the
+  // x maximum is read, so their latency overlaps both
   if (nep > 0) {
     load_epoch(evA, 0);
     load_epoch(evB, 1);
     load_epoch(evC, 2);
   }
+  for (int i = tid; i < R; i += NT) acc[i] = 0ull;
+  for (int i = tid; i < R / 32; i += NT) flag[i] = 0u;
+  reduce_xmax(xpart, nxpart, &xm_s);
+  if (nep > 0) gather(xa, evA);
   __syncthreads();
   const uint32_t xm = xm_s;
   if (blockIdx.x == 0 && tid == 0) xpart[XMAX_BLOCKS] = xm;  // for the finish kernel
@@ -500,7 +500,6 @@ __global__ __launch_bounds__(NT) void colplan_spmv_fx(const uint64_t* __restrict
   // the rest after the loop: with later epochs of a trip conditional, the
   // compiler's wait analysis assumes the paths that skip them and waits for
   // the newest stream loads.
-  if (nep > 0) gather(xa, evA);
   int64_t k = 0;
   for (; k + 5 < nep; k += 6) {
     epoch(evA, xa, evB, xb, k);
@@ -605,7 +604,7 @@ __global__ __launch_bounds__(256) void colplan_finish_fx(const float* __restrict
 
 // ------------------------------------------------------------- geometry
 
-constexpr int RBITS_MAX = 14;          // 16384 rows: 64 KiB of fp32 row sums per workgroup
+constexpr int RBITS_MAX = 14;          // 16384 rows: 128 KiB of int64 row sums per workgroup
 constexpr int RBITS_DEFAULT = 14;      // one x-slice read per 16384 rows (the gathers' L1 fill halves against 8192)
 constexpr int64_t TILES_TARGET = 256;  // one 1024-thread workgroup per CU
 

@@ -259,21 +259,33 @@ __device__ inline int16_t row_exponent(uint32_t mx, uint32_t mn, int64_t cnt) {
   return (int16_t)er;
 }
 
-// One thread per row (build and refresh only).
+// 16 lanes per row (build and refresh only): lanes stride the row's
+// entries, xor shuffles combine the max and the smallest nonzero.
+constexpr int REXP_LANES = 16;
 template <typename IdxT>
 __global__ __launch_bounds__(256) void colplan_rowexp_kernel(const float* __restrict__ vals,
                                                              const IdxT* __restrict__ ptr, int64_t m,
                                                              int16_t* __restrict__ rexp) {
-  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= m) return;
-  const int64_t p0 = (int64_t)ptr[r], p1 = (int64_t)ptr[r + 1];
+  const int64_t r = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / REXP_LANES;
+  const int sub = threadIdx.x % REXP_LANES;
+  int64_t p0 = 0, p1 = 0;
+  if (r < m) {
+    p0 = (int64_t)ptr[r];
+    p1 = (int64_t)ptr[r + 1];
+  }
   uint32_t mx = 0, mn = 0xffffffffu;
-  for (int64_t p = p0; p < p1; ++p) {
+  for (int64_t p = p0 + sub; p < p1; p += REXP_LANES) {
     const uint32_t b = __float_as_uint(vals[p]) & 0x7fffffffu;
     mx = b > mx ? b : mx;
     if (b != 0 && b < mn) mn = b;
   }
-  rexp[r] = row_exponent(mx, mn, p1 - p0);
+  for (int o = REXP_LANES / 2; o > 0; o >>= 1) {
+    const uint32_t a = (uint32_t)__shfl_xor((int)mx, o, REXP_LANES);
+    const uint32_t c = (uint32_t)__shfl_xor((int)mn, o, REXP_LANES);
+    mx = a > mx ? a : mx;
+    mn = c < mn ? c : mn;
+  }
+  if (r < m && sub == 0) rexp[r] = row_exponent(mx, mn, p1 - p0);
 }
 
 // The plan's form of value v in global row r: v * 2^(FX_TOP - e_r) (zero
@@ -735,8 +747,8 @@ int build_typed(const float* vals, const void* col, const void* ptr, int64_t m, 
   hipLaunchKernelGGL(colplan_epochs_kernel, dim3(1), dim3(1024), 0, st, v.toff, T, v.eoff);
   rc = tsp::check_launch("colplan_epochs launch");
   if (rc) return rc;
-  hipLaunchKernelGGL((colplan_rowexp_kernel<IdxT>), dim3((unsigned)tsp::ceil_div(m, 256)), dim3(256), 0, st, vals,
-                     (const IdxT*)ptr, m, v.rexp);
+  hipLaunchKernelGGL((colplan_rowexp_kernel<IdxT>), dim3((unsigned)tsp::ceil_div(m * REXP_LANES, 256)), dim3(256), 0, st,
+                     vals, (const IdxT*)ptr, m, v.rexp);
   rc = tsp::check_launch("colplan_rowexp launch");
   if (rc || nnz == 0) return rc;
   hipLaunchKernelGGL((colplan_scatter_kernel<K>), dim3((unsigned)tsp::ceil_div(nnz, 256)), dim3(256), 0, st, kout,
@@ -790,11 +802,11 @@ extern "C" int tsp_csr_colplan_refresh(const void* values, int dtype, const void
   hipStream_t st = (hipStream_t)stream;
   PlanView v = plan_view(plan, geometry);
   if (index_type == TSP_I64)
-    hipLaunchKernelGGL((colplan_rowexp_kernel<int64_t>), dim3((unsigned)tsp::ceil_div(m, 256)), dim3(256), 0, st,
-                       (const float*)values, (const int64_t*)row_ptrs, m, v.rexp);
+    hipLaunchKernelGGL((colplan_rowexp_kernel<int64_t>), dim3((unsigned)tsp::ceil_div(m * REXP_LANES, 256)), dim3(256), 0,
+                       st, (const float*)values, (const int64_t*)row_ptrs, m, v.rexp);
   else
-    hipLaunchKernelGGL((colplan_rowexp_kernel<int32_t>), dim3((unsigned)tsp::ceil_div(m, 256)), dim3(256), 0, st,
-                       (const float*)values, (const int32_t*)row_ptrs, m, v.rexp);
+    hipLaunchKernelGGL((colplan_rowexp_kernel<int32_t>), dim3((unsigned)tsp::ceil_div(m * REXP_LANES, 256)), dim3(256), 0,
+                       st, (const float*)values, (const int32_t*)row_ptrs, m, v.rexp);
   rc = tsp::check_launch("colplan_rowexp launch");
   if (rc || nnz == 0) return rc;
   hipLaunchKernelGGL(colplan_refresh_kernel, dim3((unsigned)tsp::ceil_div(v.pmax, 256)), dim3(256), 0, st,

@@ -246,6 +246,30 @@ def test_colplan_nonfinite_x_at_referenced_columns(plan_always, index_dtype):
     _check_nonfinite(v, c, p, (m, n), x, got)
 
 
+@pytest.mark.parametrize("case", ["outlier", "nan"])
+def test_colplan_long_rows_summed_again(plan_always, case):
+    """Rows longer than the finish kernel's serial limit on the slow path:
+    one huge |x| makes every row's products small against the scale (so
+    every row is summed again from the CSR arrays, the long ones by a whole
+    wavefront), or a NaN in x sends every row there; results match the
+    oracle row for row."""
+    m, n = 3000, 50000
+    rng0 = np.random.default_rng(45)
+    lens = rng0.poisson(8, m)
+    lens[rng0.choice(m, 300, replace=False)] = rng0.integers(33, 5000, 300)
+    v, c, p, rng = _random(m, n, lens, 46)
+    x = rng.standard_normal(n).astype(np.float32)
+    if case == "outlier":
+        x[n - 1] = 3e30                    # far above every other |x|
+    else:
+        x[c[p[17]]] = np.nan               # read by row 17 only (among others by chance)
+    A = W.csr_matrix_from_arrays(v, c, p, (m, n), device="cuda")
+    got = ts.spmv(A, torch.from_numpy(x).cuda()).cpu().numpy()
+    _check_nonfinite(v, c, p, (m, n), x, got)
+    again = ts.spmv(A, torch.from_numpy(x).cuda()).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+
+
 def test_colplan_nonfinite_values(plan_always):
     """inf / NaN values (rows summed from the CSR arrays) next to finite rows."""
     m, n = 6000, 9000

@@ -541,26 +541,22 @@ __global__ __launch_bounds__(NT) void colplan_spmv_fx(const uint64_t* __restrict
 // CSR order, an fp64 sum) when x holds inf or NaN, when the row's exponent
 // says so, or when one of its products was rounded and |y_r| is below
 // cnt * 2^23 units: then the rounding (at most half a unit per product)
-// could exceed 2^-24 of the result.
+// could exceed 2^-24 of the result. Rows of up to REDO_SERIAL entries are
+// summed by their own thread; longer ones by the whole wavefront (lanes
+// stride the row, fp64 partial sums, then a fixed xor tree), so a long
+// row on the slow path costs a few memory round trips, not one per entry.
+constexpr int REDO_SERIAL = 32;
+
 template <typename IdxT>
-__device__ inline float finish_row(float s, bool inex, int16_t er, uint32_t xm, int64_t r,
-                                   const float* __restrict__ vals, const IdxT* __restrict__ cols,
-                                   const IdxT* __restrict__ ptr, const float* __restrict__ x) {
-  bool redo = xm >= 0x7f800000u || er == RX_REDO;
-  if (!redo) {
-    const int sh = (int)er + x_exponent(xm) - FX_TOP;
-    s = ldexpf(s, sh);
-    if (inex && fabsf(s) < ldexpf((float)((int64_t)ptr[r + 1] - (int64_t)ptr[r]), sh + 23)) redo = true;
-  }
-  if (redo) {
-    double a = 0.0;
-    for (int64_t p = (int64_t)ptr[r]; p < (int64_t)ptr[r + 1]; ++p) a += (double)(vals[p] * x[(int64_t)cols[p]]);
-    s = (float)a;
-  }
-  return s;
+__device__ inline double redo_serial(int64_t r, const float* __restrict__ vals, const IdxT* __restrict__ cols,
+                                     const IdxT* __restrict__ ptr, const float* __restrict__ x) {
+  double a = 0.0;
+  for (int64_t p = (int64_t)ptr[r]; p < (int64_t)ptr[r + 1]; ++p) a += (double)(vals[p] * x[(int64_t)cols[p]]);
+  return a;
 }
 
 // Four rows per thread (m % 4 == 0, 16-byte aligned out and y: VEC) or one.
+// Every lane stays to the end (the wavefront-wide sums need all lanes).
 template <typename IdxT, bool VEC>
 __global__ __launch_bounds__(256) void colplan_finish_fx(const float* __restrict__ partial,
                                                          const uint32_t* __restrict__ inexact, int64_t prows,
@@ -573,39 +569,81 @@ __global__ __launch_bounds__(256) void colplan_finish_fx(const float* __restrict
                                                          float* __restrict__ out) {
   constexpr int NR = VEC ? 4 : 1;
   const int64_t r0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * NR;
-  if (r0 >= m) return;
+  const bool live = r0 < m;
+  const int lane = threadIdx.x & 63;
   const uint32_t xm = *xmax;
   float s[NR];
   uint32_t fl = 0;  // inexact bits of the NR rows
   int16_t er[NR];
-  if (VEC) {
-    f32x4 acc = *reinterpret_cast<const f32x4*>(partial + r0);
-    fl = inexact[r0 >> 5];
-    for (int64_t g = 1; g < G; ++g) {
-      acc += *reinterpret_cast<const f32x4*>(partial + g * prows + r0);
-      fl |= inexact[g * (prows >> 5) + (r0 >> 5)];
-    }
-    fl >>= (r0 & 31);
-    typedef short s16x4 __attribute__((ext_vector_type(4)));
-    const s16x4 e4 = *reinterpret_cast<const s16x4*>(rexp + r0);
+  if (live) {
+    if (VEC) {
+      f32x4 acc = *reinterpret_cast<const f32x4*>(partial + r0);
+      fl = inexact[r0 >> 5];
+      for (int64_t g = 1; g < G; ++g) {
+        acc += *reinterpret_cast<const f32x4*>(partial + g * prows + r0);
+        fl |= inexact[g * (prows >> 5) + (r0 >> 5)];
+      }
+      typedef short s16x4 __attribute__((ext_vector_type(4)));
+      const s16x4 e4 = *reinterpret_cast<const s16x4*>(rexp + r0);
 #pragma unroll
-    for (int i = 0; i < NR; ++i) {
-      s[i] = acc[i];
-      er[i] = e4[i];
-    }
-  } else {
-    s[0] = 0.f;
-    for (int64_t g = 0; g < G; ++g) {
-      s[0] += partial[g * prows + r0];
-      fl |= inexact[g * (prows >> 5) + (r0 >> 5)];
+      for (int i = 0; i < NR; ++i) {
+        s[i] = acc[i];
+        er[i] = e4[i];
+      }
+    } else {
+      s[0] = 0.f;
+      for (int64_t g = 0; g < G; ++g) {
+        s[0] += partial[g * prows + r0];
+        fl |= inexact[g * (prows >> 5) + (r0 >> 5)];
+      }
+      er[0] = rexp[r0];
     }
     fl >>= (r0 & 31);
-    er[0] = rexp[r0];
   }
+  // which rows need the CSR arrays: bit i of `lng` = long row i of this lane
+  uint32_t lng = 0;
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    if (!live) break;
+    const int64_t r = r0 + i;
+    bool redo = xm >= 0x7f800000u || er[i] == RX_REDO;
+    if (!redo) {
+      const int sh = (int)er[i] + x_exponent(xm) - FX_TOP;
+      s[i] = ldexpf(s[i], sh);
+      if (((fl >> i) & 1u) && fabsf(s[i]) < ldexpf((float)((int64_t)ptr[r + 1] - (int64_t)ptr[r]), sh + 23))
+        redo = true;
+    }
+    if (redo) {
+      if ((int64_t)ptr[r + 1] - (int64_t)ptr[r] <= REDO_SERIAL)
+        s[i] = (float)redo_serial(r, vals, cols, ptr, x);
+      else
+        lng |= 1u << i;
+    }
+  }
+  // long rows, one at a time, by the whole wavefront
+  for (;;) {
+    const int mine = lng ? __builtin_ctz(lng) : -1;
+    const uint64_t b = __ballot(mine >= 0);
+    if (b == 0) break;
+    const int src = __builtin_ctzll(b);
+    const int which = __shfl(mine, src, 64);
+    const int64_t r = ((int64_t)__shfl((int)(r0 >> 32), src, 64) << 32 | (uint32_t)__shfl((int)(uint32_t)r0, src, 64)) + which;
+    const int64_t p0 = (int64_t)ptr[r], p1 = (int64_t)ptr[r + 1];
+    double a = 0.0;
+    for (int64_t p = p0 + lane; p < p1; p += 64) a += (double)(vals[p] * x[(int64_t)cols[p]]);
+    for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o, 64);
+    if (lane == src) {
+#pragma unroll
+      for (int i = 0; i < NR; ++i)
+        if (i == which) s[i] = (float)a;
+      lng &= ~(1u << which);
+    }
+  }
+  if (!live) return;
   float res[NR];
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
-    res[i] = alpha * finish_row(s[i], ((fl >> i) & 1u) != 0, er[i], xm, r0 + i, vals, cols, ptr, x);
+    res[i] = alpha * s[i];
     if (y) res[i] = res[i] + beta * y[r0 + i];
   }
   if (VEC)

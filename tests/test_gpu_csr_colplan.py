@@ -333,6 +333,61 @@ def test_colplan_zero_x_and_beta(plan_always):
     assert torch.equal(got.cpu(), torch.from_numpy(y) * 0.5)
 
 
+def test_colplan_operator_compile_and_graph(plan_always):
+    """The plan SpMV operator (x-max pre-pass, tile kernel, finish, one
+    workspace per call) under torch.compile and in a captured HIP graph:
+    every replay with new x contents, with eager work and synchronizations
+    between replays, equals the eager call bit for bit (a solver loop
+    captures exactly this)."""
+    m, n = 40000, 33333
+    lens = np.minimum(np.random.default_rng(61).poisson(12, m), n)
+    v, c, p, rng = _random(m, n, lens, 62)
+    A = W.csr_matrix_from_arrays(v, c, p, (m, n), device="cuda")
+    vals, cols, ptrs = A.values, A.col_indices, A.row_ptrs
+    x0 = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).cuda()
+    ts.spmv(A, x0)                                   # builds and caches the plan
+    _, _, geom, plan, _ = A._hip_colplan
+    ops = _lib.ops()
+    gt = D._geometry_list(geom)
+
+    def call(x, y=None, beta=0.0):
+        return ops.csr_colplan_spmv(plan, gt, vals, cols, ptrs, m, n, x, 1.25, y, beta)
+
+    want = call(x0)
+    assert torch.equal(want, ts.spmv(A, x0, alpha=1.25))
+    _check(v, c, p, (m, n), x0.cpu().numpy(), want.cpu().numpy(), 1.25)
+
+    @torch.compile(fullgraph=True, backend="aot_eager")
+    def f(x):
+        return call(x * 2.0) + 1.0
+
+    torch.testing.assert_close(f(x0), 2.0 * want + 1.0, rtol=1e-6, atol=1e-5)
+
+    static_x = x0.clone()
+    static_y = torch.from_numpy(rng.standard_normal(m).astype(np.float32)).cuda()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        call(static_x, static_y, -0.5)               # warm up on the side stream
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = call(static_x, static_y, -0.5)
+    for rep in range(3):
+        newx = torch.from_numpy(np.random.default_rng(70 + rep).standard_normal(n).astype(np.float32)).cuda()
+        if rep == 2:
+            newx[17] = float("nan")                  # the slow path inside the graph as well
+        static_x.copy_(newx)
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = call(newx, static_y, -0.5)
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, eager) if rep < 2 else torch.equal(static_out.isnan(), eager.isnan())
+        if rep == 2:
+            keep = ~eager.isnan()
+            assert keep.any() and torch.equal(static_out[keep], eager[keep])
+
+
 def test_colplan_auto_mode_builds_on_reuse(hip_backend):
     prev = D.get_spmv_plan()
     D.set_spmv_plan("auto")

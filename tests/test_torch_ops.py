@@ -23,7 +23,7 @@ OPS = {
                   "int m, int n, int block_size, Tensor grad_out) -> Tensor",
     "csr_spmv": "(Tensor values, Tensor col_indices, Tensor row_ptrs, Tensor windows, int m, int n, Tensor x, "
                 "float alpha, Tensor? y, float beta) -> Tensor",
-    "csr_colplan_spmv": "(Tensor plan, Tensor geometry, Tensor values, Tensor col_indices, Tensor row_ptrs, int m, "
+    "csr_colplan_spmv": "(Tensor plan, int[] geometry, Tensor values, Tensor col_indices, Tensor row_ptrs, int m, "
                         "int n, Tensor x, float alpha, Tensor? y, float beta) -> Tensor",
     "csr_spmm": "(Tensor values, Tensor col_indices, Tensor row_ptrs, int m, int n, Tensor X, float alpha, "
                 "Tensor? Y, float beta) -> Tensor",
@@ -63,7 +63,7 @@ def test_meta_shapes():
                           _meta(300, 70)).shape == (512, 70)
     v, cols, ptrs = _meta(50), _meta(50, dtype=torch.int32), _meta(11, dtype=torch.int32)
     assert ops.csr_spmv(v, cols, ptrs, _meta(3, dtype=i64), 10, 20, _meta(20), 1.0, None, 0.0).shape == (10,)
-    geom = torch.zeros(10, dtype=i64)
+    geom = [0] * 10
     assert ops.csr_colplan_spmv(_meta(100, dtype=torch.uint8), geom, v, cols, ptrs, 10, 20, _meta(20), 1.0, None,
                                 0.0).shape == (10,)
     assert ops.csr_spmm(v, cols, ptrs, 10, 20, _meta(20, 3), 1.0, None, 0.0).shape == (10, 3)

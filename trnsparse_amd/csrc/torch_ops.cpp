@@ -230,17 +230,19 @@ at::Tensor csr_spmv_meta(const at::Tensor&, const at::Tensor&, const at::Tensor&
   return at::empty({m}, x.options());
 }
 
-at::Tensor csr_colplan_spmv(const at::Tensor& plan, const at::Tensor& geometry, const at::Tensor& values,
+// The geometry is the 10 host values of tsp_csr_colplan_geometry as an int
+// list (not a tensor: a CPU tensor beside device tensors cannot be traced
+// by torch.compile's fake tensors).
+at::Tensor csr_colplan_spmv(const at::Tensor& plan, at::IntArrayRef geometry, const at::Tensor& values,
                             const at::Tensor& cols, const at::Tensor& ptrs, int64_t m, int64_t n, const at::Tensor& x,
                             double alpha, const c10::optional<at::Tensor>& y, double beta) {
   need(plan, x, "plan");
   for (auto* p : {&values, &cols, &ptrs}) need(*p, x, "matrix");
   need(x, x, "x");
   if (y.has_value()) need(*y, x, "y");
-  TORCH_CHECK(geometry.device().is_cpu() && geometry.scalar_type() == at::kLong && geometry.numel() == 10 &&
-                  geometry.is_contiguous(),
+  TORCH_CHECK(geometry.size() == 10,
               "csr_colplan_spmv: geometry must be the 10 int64 host values of tsp_csr_colplan_geometry");
-  const int64_t* geom = geometry.data_ptr<int64_t>();
+  const int64_t* geom = geometry.data();
   need_csr(values, cols, ptrs, m, n, x, "csr_colplan_spmv");
   need_dtype(x, at::kFloat, "csr_colplan_spmv", "x");
   need_numel(x, n, "csr_colplan_spmv", "x");
@@ -259,7 +261,7 @@ at::Tensor csr_colplan_spmv(const at::Tensor& plan, const at::Tensor& geometry, 
   return out;
 }
 
-at::Tensor csr_colplan_spmv_meta(const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+at::Tensor csr_colplan_spmv_meta(const at::Tensor&, at::IntArrayRef, const at::Tensor&, const at::Tensor&,
                                  const at::Tensor&, int64_t m, int64_t, const at::Tensor& x, double,
                                  const c10::optional<at::Tensor>&, double) {
   return at::empty({m}, x.options());
@@ -464,7 +466,7 @@ TORCH_LIBRARY(trnsparse_hip, m) {
         "int m, int n, int block_size, Tensor grad_out) -> Tensor");
   m.def("csr_spmv(Tensor values, Tensor col_indices, Tensor row_ptrs, Tensor windows, int m, int n, Tensor x, "
         "float alpha, Tensor? y, float beta) -> Tensor");
-  m.def("csr_colplan_spmv(Tensor plan, Tensor geometry, Tensor values, Tensor col_indices, Tensor row_ptrs, int m, "
+  m.def("csr_colplan_spmv(Tensor plan, int[] geometry, Tensor values, Tensor col_indices, Tensor row_ptrs, int m, "
         "int n, Tensor x, float alpha, Tensor? y, float beta) -> Tensor");
   m.def("csr_spmm(Tensor values, Tensor col_indices, Tensor row_ptrs, int m, int n, Tensor X, float alpha, "
         "Tensor? Y, float beta) -> Tensor");

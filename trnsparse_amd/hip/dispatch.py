@@ -285,7 +285,7 @@ def _csr_forward(vals, cols, ptrs, win, shape, X, alpha, Y, beta, dev, colplan=N
             return out
         if colplan is not None:
             _, geom, plan = colplan
-            return _lib.ops().csr_colplan_spmv(plan, _geometry_tensor(geom), vals, cols, ptrs, m, n, Xd, float(alpha),
+            return _lib.ops().csr_colplan_spmv(plan, _geometry_list(geom), vals, cols, ptrs, m, n, Xd, float(alpha),
                                                Yd, float(beta))
         return _lib.ops().csr_spmv(vals, cols, ptrs, win, m, n, Xd, float(alpha), Yd, float(beta))
     ncols = Xd.shape[1]
@@ -294,10 +294,10 @@ def _csr_forward(vals, cols, ptrs, win, shape, X, alpha, Y, beta, dev, colplan=N
     return _lib.ops().csr_spmm(vals, cols, ptrs, m, n, Xd, float(alpha), Yd, float(beta))
 
 
-def _geometry_tensor(geom) -> torch.Tensor:
-    """The column plan's 10 host int64 geometry values as a CPU tensor (the
-    operator's argument form), sharing memory with the numpy array."""
-    return torch.from_numpy(geom)
+def _geometry_list(geom) -> list[int]:
+    """The column plan's 10 host int64 geometry values as the operator's
+    `int[]` argument."""
+    return [int(v) for v in geom]
 
 
 # SpMV over the column-sorted plan (tsp_csr_colplan_*): "auto" builds the

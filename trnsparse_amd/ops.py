@@ -275,20 +275,6 @@ def screened_spmm(
 # --------------------------------------------------------------- attention
 
 
-class _PatternHandle:
-    """Pattern-only stand-in for a BSRMatrix (reference ops.py:488-498)."""
-
-    def __init__(self, col_indices, row_ptrs, shape, block_size):
-        self.block_col_indices = col_indices
-        self.block_row_ptrs = row_ptrs
-        self.shape = shape
-        self.block_size = block_size
-
-    @property
-    def n_blocks(self) -> int:
-        return len(self.block_col_indices)
-
-
 def _block_sparse_attn_pytorch(Q, K, V, mask_bsr, scale: float, return_stats: bool = False):
     """Two-pass block-sparse attention, torch semantics (reference ops.py:280-357).
 
@@ -423,12 +409,16 @@ class _AttnTiledFunction(torch.autograd.Function):
     Forward runs the HIP kernel (or the torch two-pass spec) and saves
     Q, K, V, O and the row stats; backward runs the HIP backward kernels (or
     the tiled torch backward on the "pytorch" backend).
-    Q/K/V are (seq, d) or batched (..., seq, d) sharing one mask.
+    Q/K/V are (seq, d) or batched (..., seq, d) sharing one mask. The mask
+    itself is passed (not its tensors, as the reference's pattern stand-in
+    at ops.py:488-498 does): the device copies of its pattern and the row
+    order are cached on it, so repeated calls copy nothing to the device and
+    a HIP graph can capture a forward + backward step.
     """
 
     @staticmethod
-    def forward(ctx, Q, K, V, mask_col_indices, mask_row_ptrs, mask_shape, mask_block_size, scale):
-        handle = _PatternHandle(mask_col_indices, mask_row_ptrs, mask_shape, mask_block_size)
+    def forward(ctx, Q, K, V, mask_bsr, scale):
+        handle = mask_bsr
         if _use_hip():
             from .hip.dispatch import hip_block_sparse_attention
 
@@ -449,7 +439,7 @@ class _AttnTiledFunction(torch.autograd.Function):
             dQ, dK, dV = hip_block_sparse_attention_backward(
                 Q, K, V, O, dO.contiguous(), ctx.handle, ctx.scale, row_max, row_denom
             )
-            return dQ, dK, dV, None, None, None, None, None
+            return dQ, dK, dV, None, None
         lead = Q.shape[:-2]
         S, D = Q.shape[-2:]
         q, k, v, o, do = (t.reshape(-1, S, D) for t in (Q, K, V, O, dO))
@@ -460,7 +450,7 @@ class _AttnTiledFunction(torch.autograd.Function):
             for h in range(q.shape[0])
         ]
         dQ, dK, dV = (torch.stack([g[i] for g in grads]).reshape(*lead, S, D) for i in range(3))
-        return dQ, dK, dV, None, None, None, None, None
+        return dQ, dK, dV, None, None
 
 
 def _attn_pytorch_batched(Q, K, V, mask_bsr, scale, return_stats=False):
@@ -498,9 +488,7 @@ def block_sparse_attention_tiled(
     if scale is None:
         scale = head_dim**-0.5
     if torch.is_grad_enabled() and (Q.requires_grad or K.requires_grad or V.requires_grad):
-        return _AttnTiledFunction.apply(
-            Q, K, V, mask_bsr.block_col_indices, mask_bsr.block_row_ptrs, mask_bsr.shape, mask_bsr.block_size, scale
-        )
+        return _AttnTiledFunction.apply(Q, K, V, mask_bsr, scale)
     if _use_hip():
         from .hip.dispatch import hip_block_sparse_attention
 

@@ -784,7 +784,8 @@ def bench_attention_blocks(steps: int, warmup: int):
     """Config 5's mask and shape (32 heads x 8192) on the block-product path:
     bf16 backward at head_dim 256, and forward and backward at head_dim 512 in
     bf16 and fp32 (SDDMM scores, block softmax / gradient, BSR SpMMs over the
-    mask stacked over heads). FLOPs as the other attention lines: 4 (forward)
+    mask stacked over heads); the bf16 forward at 512 also on the one-pass
+    kernel the API runs. FLOPs as the other attention lines: 4 (forward)
     and 10 (backward) x nnzb x 128^2 x d x heads. Each step is the whole
     sequence of launches; `us` is the median of 5 timed segments."""
     import torch
@@ -804,11 +805,18 @@ def bench_attention_blocks(steps: int, warmup: int):
                      (FP32_MFMA_PEAK_TFLOPS, "frac_fp32_mfma"))
         O, rm, rd = Dp.hip_block_sparse_attention(Qd, Kd, Vd, mask, D**-0.5, return_stats=True)
         if fwd:
-            ms, lo, hi = time_gpu_spread(lambda: Dp._attention_blocks_fwd(Qd, Kd, Vd, mask, D**-0.5, dev), steps, warmup)
-            tf = 4.0 * mask.n_blocks * 128 * 128 * D * H / (ms * 1e-3) / 1e12
-            out.append({"name": f"block_sparse_attention cfg5 mask 32x8192x{D} {tag} (block products)",
-                        "value": round(tf * 1e3, 1), "unit": "GFLOP/s", "us": round(ms * 1e3, 1),
-                        "us_spread": [round(lo * 1e3, 1), round(hi * 1e3, 1)], key: round(tf / peak, 4)})
+            # bf16 at 512: the one-pass kernel (tsp_bsa_fwd), and the block
+            # products beside it; fp32: block products
+            runs = [("block products", lambda: Dp._attention_blocks_fwd(Qd, Kd, Vd, mask, D**-0.5, dev))]
+            if dt == torch.bfloat16:
+                runs.insert(0, ("one pass", lambda: Dp.hip_block_sparse_attention(Qd, Kd, Vd, mask, D**-0.5,
+                                                                                   return_stats=True)))
+            for how, fn in runs:
+                ms, lo, hi = time_gpu_spread(fn, steps, warmup)
+                tf = 4.0 * mask.n_blocks * 128 * 128 * D * H / (ms * 1e-3) / 1e12
+                out.append({"name": f"block_sparse_attention cfg5 mask 32x8192x{D} {tag} ({how})",
+                            "value": round(tf * 1e3, 1), "unit": "GFLOP/s", "us": round(ms * 1e3, 1),
+                            "us_spread": [round(lo * 1e3, 1), round(hi * 1e3, 1)], key: round(tf / peak, 4)})
         dO = torch.randn(Qd.shape, generator=torch.Generator().manual_seed(14)).to(dt).to(dev)
         rmf, rdf = rm.reshape(H, S), rd.reshape(H, S)
         ms, lo, hi = time_gpu_spread(lambda: Dp._attention_blocks_bwd(Qd, Kd, Vd, O, dO, mask, D**-0.5, rmf, rdf, dev),

@@ -359,7 +359,8 @@ int tsp_screened_spmm_backward(const void* A, int dtype, int64_t lda,
  *          blocks) V[h]
  * Q, K, V, O (n_heads, seq_len, head_dim) contiguous, `dtype` (TSP_BF16 and
  * TSP_F32 on the MFMA path for block_size 128, scale > 0 and head_dim 64,
- * 128 or 256; TSP_F64 and other shapes on the generic path). The mask (block_row_ptrs with at
+ * 128 or 256, TSP_BF16 also at 512; TSP_F64 and other shapes on the generic
+ * path). The mask (block_row_ptrs with at
  * least seq_len/block_size + 1 entries, block_col_indices) is shared by all
  * heads; only its pattern is used. Rows of an empty block row, and rows past
  * (seq_len/block_size)*block_size, are zero.
@@ -380,7 +381,8 @@ int tsp_bsa_fwd(const void* Q, const void* K, const void* V, int dtype,
  * Block-sparse attention as block-sparse products (any head_dim).
  *
  * For the head_dims the one-pass kernels above do not serve (head_dim over
- * 256; bf16 gradients at head_dim 256), attention runs as block-sparse
+ * 256 except the bf16 forward at 512; bf16 gradients at head_dim 256 and
+ * over), attention runs as block-sparse
  * products over the mask stacked over heads: the pattern whose block row
  * h * Mt + i holds the mask blocks of block row i shifted by h * Mt block
  * columns, so Q, K, V (n_heads, seq_len, head_dim) contiguous are its

@@ -297,21 +297,52 @@ def test_reference_head_dim_256_case(hip_backend, mask, seed):
         assert R.scaled_error(gr.cpu().double().numpy(), e, np.maximum(a, 1e-30)) <= TOL_F32
 
 
+# ------------------------------------------------ bf16 head_dim 512, one pass
+
+
+@pytest.mark.parametrize("S,D,mask,H", [
+    (640, 512, W.cfg5_block_mask(5), 3),
+    (512, 512, local_mask(4, 2), 9),                     # heads past a multiple of 8
+    (700, 512, global_mask(6, 1, 2), 2),                 # ragged S: the last key block crosses it
+    (512, 384, global_mask(4, 1, 1), 2),                 # zero-padded to 512
+    (384, 264, torch.tensor([[True, False, True], [False, False, False], [True, True, True]]), 1),  # empty row
+])
+def test_bf16_d512_forward(hip_backend, S, D, mask, H):
+    """bf16 with 256 < head_dim <= 512 runs the one-pass kernel in which the
+    two wavefronts of a pair split the head dimension and add their partial
+    scores through LDS: O and the stats of every head against the oracle,
+    with wide score ranges (rows of Q scaled by 6) so the running max
+    moves."""
+    g = torch.Generator().manual_seed(62 + D)
+    Q, K, V = (torch.randn(H, S, D, generator=g).to(torch.bfloat16) for _ in range(3))
+    Q[:, ::5] *= 6
+    mask_bsr = W.bsr_from_block_mask(mask, 128)
+    got, rmax, rden = hip_block_sparse_attention(Q.cuda(), K.cuda(), V.cuda(), mask_bsr, D**-0.5, return_stats=True)
+    assert got.dtype == torch.bfloat16 and got.shape == (H, S, D)
+    Mt = S // 128
+    for hh in range(H):
+        out, em, ed, sc = _oracle(Q[hh], K[hh], V[hh], mask_bsr, D**-0.5)
+        assert _err(got[hh].float().cpu().numpy(), out, sc) <= TOL_BF16
+        np.testing.assert_allclose(rmax[hh].cpu().numpy(), em[:Mt], rtol=1e-4, atol=2e-2)
+        np.testing.assert_allclose(rden[hh].cpu().numpy(), ed[:Mt], rtol=3e-2)
+
+
 # ------------------------------------------- head_dim over 256: block products
 
 
 @pytest.mark.parametrize("S,D,mask,H,dt", [
     (512, 512, local_mask(4, 2), 1, torch.float32),
     (512, 512, dilated_mask(4, 2), 2, torch.float32),
-    (640, 512, W.cfg5_block_mask(5), 3, torch.bfloat16),
-    (512, 384, global_mask(4, 1, 1), 2, torch.bfloat16),
+    (640, 640, W.cfg5_block_mask(5), 3, torch.bfloat16),
+    (512, 768, global_mask(4, 1, 1), 2, torch.bfloat16),
     (256, 300, local_mask(2, 1), 1, torch.float32),   # head_dim zero-padded to 304
     (384, 1024, torch.ones(3, 3, dtype=torch.bool), 1, torch.float32),
 ])
 def test_block_products_forward(hip_backend, S, D, mask, H, dt):
-    """head_dim over 256 (fp32 and bf16, 128-blocks, whole blocks) runs as
-    SDDMM scores, the block softmax and a BSR SpMM with V over the mask
-    stacked over heads: O and the stats of every head against the oracle."""
+    """head_dim over 256 (fp32, and bf16 over 512; 128-blocks, whole blocks)
+    runs as SDDMM scores, the block softmax and a BSR SpMM with V over the
+    mask stacked over heads: O and the stats of every head against the
+    oracle."""
     g = torch.Generator().manual_seed(60)
     Q, K, V = (torch.randn(H, S, D, generator=g).to(dt) for _ in range(3))
     Q[:, ::5] *= 6  # wide score ranges

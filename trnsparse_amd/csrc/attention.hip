@@ -24,12 +24,16 @@
 //       exp2, fp32 accumulation, bf16 output. Kept for operands past 4 GiB.
 //   bsa_fwd_bf16_stream<D> the same work split with K/V streamed through an
 //       LDS ring by direct loads (D in {64, 128, 256}).
+//   bsa_fwd_bf16_d512     bf16, D = 512: the streamed kernel's math with the
+//       head dimension split between the two wavefronts of a pair, which
+//       add their partial scores through LDS.
 //   bsa_fwd_f32_mfma<D>   fp32, 128-blocks, D in {64, 128, 256}: the same
 //       work split on v_mfma_f32_32x32x2_f32 with K/V streamed through an
 //       LDS ring.
 // head_dim 256 keeps the whole score product in one workgroup (16 k-steps
-// of 16 bf16 / 128 of 2 fp32 per 32-key tile); other head_dims are padded
-// with zero columns by the caller.
+// of 16 bf16 / 128 of 2 fp32 per 32-key tile), bf16 512 as well (split
+// over wavefront pairs); other head_dims are padded with zero columns by
+// the caller.
 //   bsa_fwd_generic<T>    fp32/fp64/bf16, any block size and head_dim: one
 //       thread per (query, 32-wide slice of head_dim), online softmax in
 //       the accumulation type (double for fp64).
@@ -576,6 +580,222 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void bsa_fwd_bf16_stream(
   }
 }
 
+// ------------------------------------------------- bf16 MFMA, d = 512
+//
+// bsa_fwd_bf16_d512: head_dim 512 in one pass. At 32 queries per wavefront
+// the d = 512 score tile and output rows need 16 + 256 accumulator registers
+// next to 128 of Q (more than a lane's 512), so the head dimension is split
+// between the two wavefronts of a pair: one 512-thread workgroup per
+// (head, 128-query block row), wavefront w owns queries 32 (w % 4) + [0, 32)
+// and head dims 256 (w / 4) + [0, 256) — its Q columns and its half of O —
+// the register footprint of the d = 256 kernel. Per 32-key stage a
+// wavefront forms the partial scores of its half (S^T over 16 k-steps),
+// stores them to LDS, and after a barrier adds its partner's: both
+// wavefronts of a pair then hold the same scores bit for bit (fp32
+// addition is commutative), run the same online softmax and multiply P by
+// their half of V. Keys stream through a 2-stage LDS ring (K and V, 64 KiB
+// per stage) as in bsa_fwd_bf16_stream; with the 32 KiB exchange the
+// workgroup takes the 160 KiB of a CU, two wavefronts per SIMD.
+namespace a512 {
+constexpr int D = 512, DH = 256, HK = 32, SPB = AB / HK, ROWB = D * 2;
+constexpr int HBYTES = HK * ROWB, STAGE = 2 * HBYTES, NST = 2;
+constexpr int KS = DH / 16;  // k-steps of a partial S^T
+constexpr int NU = DH / 32;  // 32-wide d subtiles of a half of O^T
+constexpr int XBYTES = 8 * 16 * 64 * 4;  // partial scores: 8 waves x 16 values x 64 lanes
+__host__ __device__ constexpr int kswz(int key) { return key & 15; }
+__host__ __device__ constexpr int vswz(int key) { return key & 3; }
+}  // namespace a512
+
+__global__ __launch_bounds__(512, 1) void bsa_fwd_bf16_d512(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V, int64_t S,
+    int64_t head_stride, int64_t H, const int64_t* __restrict__ rp, const int64_t* __restrict__ ci, int64_t Mt,
+    float scale_log2, uint16_t* __restrict__ O, float* __restrict__ rmax, float* __restrict__ rden) {
+  using namespace a512;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE + XBYTES];
+  float* xch = (float*)(lds + NST * STAGE);
+
+  const int64_t g = blockIdx.x;
+  const int64_t xcd = g & 7, slot = g >> 3;
+  const int64_t head = xcd + 8 * (slot / Mt);
+  const int64_t m = slot % Mt;
+  if (head >= H) return;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wq = w & 3, dh = w >> 2;  // query group, head-dim half
+  const int h = lane >> 5, l32 = lane & 31;
+  const int gq = lane >> 4, jq = lane & 15;
+  const uint16_t* Qh = Q + head * head_stride;
+  const uint16_t* Kh = K + head * head_stride;
+  const uint16_t* Vh = V + head * head_stride;
+  const int64_t q = m * AB + wq * 32 + l32;
+
+  // Q fragments of this half: Q[q][256 dh + 16 s + 8 h .. +7]
+  bf16x8 qf[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) qf[s] = *(const bf16x8*)(Qh + q * D + DH * dh + 16 * s + 8 * h);
+
+  f32x16 o[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) o[u] = f32x16{};
+  constexpr float RESCALE = 8.f;
+  float mtrue = -INFINITY, mref = -INFINITY, lrun = 0.f;
+
+  const int64_t start = rp[m];
+  const int nblk = (int)(rp[m + 1] - start);
+  const int nsteps = SPB * nblk;
+  const tsp::dma::i32x4 krs = tsp::dma::make_rsrc(Kh, (uint32_t)(S * D * 2));
+  const tsp::dma::i32x4 vrs = tsp::dma::make_rsrc(Vh, (uint32_t)(S * D * 2));
+  const uint32_t lds0 = tsp::dma::lds_addr(lds);
+
+  int cbase = 0, cv = 0;
+  auto load_cols = [&](int base) {
+    const int i = base + lane < nblk ? base + lane : nblk - 1;
+    return tsp::dma::load_lo32_sync(ci + start + i);
+  };
+  if (nblk > 0) cv = load_cols(0);
+  auto colblk = [&](int blk) {
+    if (blk - cbase >= 64) {
+      cbase = blk & ~63;
+      cv = load_cols(cbase);
+    }
+    return __builtin_amdgcn_readlane(cv, blk - cbase);
+  };
+  auto first_key = [&](int s) { return (int64_t)colblk(s / SPB) * AB + HK * (s % SPB); };
+
+  // ---- stage s into ring slot s % NST: one 1 KiB row per instruction,
+  // rows 4w .. 4w + 3 of K and of V per wavefront
+  auto issue = [&](int s) {
+    const int64_t key0 = first_key(s);
+    const uint32_t st = lds0 + (s % NST) * STAGE;
+#pragma unroll
+    for (int qq = 0; qq < HK / 8; ++qq) {
+      const int rr = (HK / 8) * w + qq;
+      const int64_t rowoff = (key0 + rr) * ROWB;
+      tsp::dma::buffer16(krs, (uint32_t)(rowoff + ((lane ^ kswz(rr)) * 16)), st + rr * 1024);
+      tsp::dma::buffer16(vrs, (uint32_t)(rowoff + ((lane ^ (4 * vswz(rr))) * 16)), st + HBYTES + rr * 1024);
+    }
+  };
+
+  const int vrow = 4 * (gq >> 1) + (jq >> 2);
+  const int vsw = 4 * vswz(vrow);
+  const int vcol = 16 * (gq & 1) + 4 * (jq & 3);
+  const int kx = kswz(l32) ^ h;
+  const int vlane = vrow * ROWB + ((vcol >> 3) & 3) * 16 + (vcol & 4) * 2;
+  float* xown = xch + w * (16 * 64) + lane;
+  const float* xpart = xch + (w ^ 4) * (16 * 64) + lane;
+
+  auto compute = [&](const uint8_t* st, int64_t key0) {
+    // ---- partial S^T over this half's head dims (key l32 of the stage,
+    // logical chunk 32 dh + 2 ks + h of its row)
+    const uint8_t* Ks = st + l32 * ROWB + DH * 2 * dh;
+    auto kread = [&](int ks) { return *(const bf16x8*)(Ks + (((2 * ks) ^ kx) * 16)); };
+    f32x16 sc;
+    bf16x8 ka[2];
+    ka[0] = kread(0);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) ka[(ks + 1) & 1] = kread(ks + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[ks & 1], qf[ks], ks == 0 ? f32x16{} : sc, 0, 0, 0);
+    }
+    // ---- exchange: the pair's two halves summed in both wavefronts
+#pragma unroll
+    for (int v = 0; v < 16; ++v) xown[v * 64] = sc[v];
+    tsp::dma::barrier();
+#pragma unroll
+    for (int v = 0; v < 16; ++v) sc[v] += xpart[v * 64];
+    if (key0 + HK > S) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        if (key0 + 8 * (v >> 2) + 4 * h + (v & 3) >= S) sc[v] = -INFINITY;
+    }
+    float mraw = sc[0];
+#pragma unroll
+    for (int v = 1; v < 16; ++v) mraw = fmaxf(mraw, sc[v]);
+    mraw = att::halves_max(mraw);
+    mtrue = fmaxf(mtrue, mraw * scale_log2);
+    if (__builtin_amdgcn_ballot_w64(mtrue > mref + RESCALE) != 0) {
+      const bool move = mtrue > mref + RESCALE;
+      const float alpha = move ? (mref == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mref - mtrue)) : 1.f;
+      mref = move ? mtrue : mref;
+      lrun *= alpha;
+#pragma unroll
+      for (int u = 0; u < NU; ++u) o[u] *= alpha;
+    }
+    const float nmx = mref == -INFINITY ? 0.f : -mref;
+    float lsum = 0.f;
+    bf16x8 pb[2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      typedef float f32x8 __attribute__((ext_vector_type(8)));
+      f32x8 pv;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[8 * a + i], scale_log2, nmx));
+        lsum += p;
+        pv[i] = p;
+      }
+      pb[a] = __builtin_convertvector(pv, bf16x8);
+    }
+    lrun += lsum;
+    // ---- O^T (this half) += V^T P^T; d subtile u of the half is global
+    // subtile 8 dh + u, whose swizzled 64-byte piece is 8 dh + (u ^ vx)
+    const uint8_t* Vs = st + HBYTES + vlane + DH * 2 * dh;
+    const int vx = vsw >> 2;
+    auto vread = [&](int a, int u) {
+      att::s16x4 r[2];
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const uint8_t* p = Vs + (16 * a + 8 * rr) * ROWB + ((u ^ vx) << 6);
+        r[rr] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((att::lds_s16x4*)p);
+      }
+      return __builtin_bit_cast(bf16x8, __builtin_shufflevector(r[0], r[1], 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    bf16x8 vb[2];
+    vb[0] = vread(0, 0);
+#pragma unroll
+    for (int step = 0; step < 2 * NU; ++step) {
+      const int a = step / NU, u = step % NU;
+      if (step + 1 < 2 * NU) vb[(step + 1) & 1] = vread((step + 1) / NU, (step + 1) % NU);
+      __builtin_amdgcn_sched_barrier(0);
+      o[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb[step & 1], pb[a], o[u], 0, 0, 0);
+    }
+  };
+
+  if (nsteps > 0) issue(0);
+  for (int s = 0; s < nsteps; ++s) {
+    const int64_t key0 = first_key(s);
+    tsp::dma::wait_vm<0>();
+    tsp::dma::barrier();  // stage s in LDS; slot (s+1) % NST and the exchange are free
+    if (s + 1 < nsteps) issue(s + 1);
+    compute(lds + (s % NST) * STAGE, key0);
+  }
+
+  lrun = att::halves_sum(lrun);
+  const bool empty = nblk == 0;
+  const float lref = lrun > 1e-12f ? lrun : 1e-12f;
+  const float inv = empty ? 0.f : 1.f / lref;
+  const float ltrue = mref == -INFINITY ? lrun : lrun * __builtin_amdgcn_exp2f(mref - mtrue);
+  const float den = ltrue > 1e-12f ? ltrue : 1e-12f;
+  uint16_t* Oq = O + head * head_stride + q * D + DH * dh;
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+      u16x4 t;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t[i] = tsp::f32_to_bf16_bits(o[u][4 * g4 + i] * inv);
+      *(u16x4*)(Oq + 32 * u + 8 * g4 + 4 * h) = t;
+    }
+  }
+  if (dh == 0 && h == 0 && rmax) {
+    const int64_t r = head * Mt * AB + q;
+    rmax[r] = empty ? 0.f : mtrue * 0.69314718055994531f;
+    rden[r] = empty ? 1e-12f : den;
+  }
+}
+
 // ---------------------------------------------------------------- fp32 MFMA
 //
 // bsa_fwd_f32_mfma<D>: fp32, 128-blocks, D in {64, 128, 256}. The work split and
@@ -864,7 +1084,8 @@ extern "C" int tsp_bsa_fwd(const void* Q, const void* K, const void* V, int dtyp
   if (Mt == 0) return TSP_OK;
   const bool bf16_streamed = scale > 0 && (seq_len + AB) * head_dim * 2 <= (int64_t)UINT32_MAX;
   if (dtype == TSP_BF16 && block_size == AB &&
-      (head_dim == 64 || head_dim == 128 || (head_dim == 256 && bf16_streamed)) && ((uintptr_t)Q % 16) == 0 &&
+      (head_dim == 64 || head_dim == 128 || ((head_dim == 256 || head_dim == 512) && bf16_streamed)) &&
+      ((uintptr_t)Q % 16) == 0 &&
       ((uintptr_t)K % 16) == 0 && ((uintptr_t)V % 16) == 0 && ((uintptr_t)O % 8) == 0) {
     const int64_t grid = tsp::ceil_div(n_heads, 8) * Mt * 8;
     if (grid > INT32_MAX) return tsp::fail(TSP_EUNSUPPORTED, "tsp_bsa_fwd: problem too large");
@@ -873,7 +1094,11 @@ extern "C" int tsp_bsa_fwd(const void* Q, const void* K, const void* V, int dtyp
   hipLaunchKernelGGL((KERNEL), dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)Q, (const uint16_t*)K,       \
                      (const uint16_t*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs, block_col_indices, Mt, \
                      sl2, (uint16_t*)O, (float*)row_max, (float*)row_denom)
-    if (bf16_streamed && head_dim == 256)
+    if (head_dim == 512)
+      hipLaunchKernelGGL(bsa_fwd_bf16_d512, dim3((unsigned)grid), dim3(512), 0, st, (const uint16_t*)Q,
+                         (const uint16_t*)K, (const uint16_t*)V, seq_len, seq_len * head_dim, n_heads, block_row_ptrs,
+                         block_col_indices, Mt, sl2, (uint16_t*)O, (float*)row_max, (float*)row_denom);
+    else if (bf16_streamed && head_dim == 256)
       TSP_FWD_BF16(bsa_fwd_bf16_stream<256>);
     else if (bf16_streamed && head_dim == 128)
       TSP_FWD_BF16(bsa_fwd_bf16_stream<128>);

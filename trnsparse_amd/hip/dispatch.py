@@ -570,14 +570,24 @@ def hip_screened_spmm(A, diag_integrals, B, threshold: float):
 # --------------------------------------------------------------- attention
 
 
+def _fused_d512(t: torch.Tensor, block_size: int, scale: float) -> bool:
+    """bf16 with 256 < head_dim <= 512 runs the one-pass d = 512 MFMA kernel
+    (operands zero-padded to 512); other head_dims over 256 run as block
+    products."""
+    return t.dtype == torch.bfloat16 and block_size == 128 and 256 < t.shape[-1] <= 512 and scale > 0
+
+
 def _mfma_head_dim(t: torch.Tensor, block_size: int) -> int | None:
     """The head_dim an fp32 / bf16 operand of head_dim d < 256 other than 64
-    and 128 is zero-padded to (64, 128 or 256) so that the MFMA attention
-    kernels serve it (zero columns change neither the scores nor the other
-    columns of the results); None when no padding applies."""
+    and 128 is zero-padded to (64, 128 or 256), and a bf16 one with
+    256 < d < 512 to 512, so that the MFMA attention kernels serve it (zero
+    columns change neither the scores nor the other columns of the
+    results); None when no padding applies."""
     d = t.shape[-1]
-    if block_size != 128 or t.dtype not in (torch.float32, torch.bfloat16) or d in (64, 128, 256) or d > 256 or d == 0:
+    if block_size != 128 or t.dtype not in (torch.float32, torch.bfloat16) or d in (64, 128, 256, 512) or d == 0:
         return None
+    if d > 256:
+        return 512 if t.dtype == torch.bfloat16 and d < 512 else None
     return 64 if d < 64 else (128 if d < 128 else 256)
 
 
@@ -591,11 +601,11 @@ def hip_block_sparse_attention(Q, K, V, mask_bsr, scale: float, return_stats: bo
     Honours `scale` (the reference NKI path used head_dim**-0.5 regardless).
     Stats come back as (..., S // b, b) in float32 (float64 for float64 input).
     fp32 / bf16 with 128-blocks run the MFMA kernels at head_dim 64, 128 and
-    256, and on operands zero-padded to the next of those below 256; head_dims
-    over 256 run as block products over the mask stacked over heads (SDDMM
-    scores, an elementwise block softmax, a BSR SpMM with V) when the
-    sequence is a whole number of 128-blocks; fp16 runs in fp32 (widened
-    operands, O rounded back once).
+    256 (bf16 also 512), and on operands zero-padded to the next of those;
+    the other head_dims over 256 run as block products over the mask stacked
+    over heads (SDDMM scores, an elementwise block softmax, a BSR SpMM with
+    V) when the sequence is a whole number of 128-blocks; fp16 runs in fp32
+    (widened operands, O rounded back once).
     """
     if not (Q.shape == K.shape == V.shape):
         raise RuntimeError(f"Q, K, V shapes differ: {tuple(Q.shape)}, {tuple(K.shape)}, {tuple(V.shape)}")
@@ -610,7 +620,8 @@ def hip_block_sparse_attention(Q, K, V, mask_bsr, scale: float, return_stats: bo
         if not return_stats:
             return res[..., : Q.shape[-1]].contiguous()
         return (res[0][..., : Q.shape[-1]].contiguous(),) + tuple(res[1:])
-    bd = _blocks_head_dim(Q, mask_bsr.block_size) if Q.shape[-1] > 256 else None
+    fused = _fused_d512(Q, mask_bsr.block_size, scale)
+    bd = _blocks_head_dim(Q, mask_bsr.block_size) if Q.shape[-1] > 256 and not fused else None
     if bd is not None:
         # head_dim over 256: block products over the mask stacked over heads
         d = Q.shape[-1]
@@ -846,7 +857,7 @@ def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, 
         grads = hip_block_sparse_attention_backward(*(_pad_head_dim(t, 128) for t in (Q, K, V, O, dO)), mask_bsr,
                                                     scale, row_max, row_denom)
         return tuple(gr[..., : Q.shape[-1]].contiguous() for gr in grads)
-    dp = _mfma_head_dim(Q, mask_bsr.block_size)
+    dp = _mfma_head_dim(Q, mask_bsr.block_size) if Q.shape[-1] <= 256 else None  # over 256: block products
     if dp is not None and scale > 0:
         grads = hip_block_sparse_attention_backward(*(_pad_head_dim(t, dp) for t in (Q, K, V, O, dO)), mask_bsr, scale,
                                                     row_max, row_denom)

@@ -185,3 +185,29 @@ def test_graph_attention_backward(hip_backend, dtype):
     leaves = [torch.randn(heads, S, d, device="cuda", generator=g).to(dtype).requires_grad_(True) for _ in range(3)]
     _grads_replay_match(lambda q, k, v: ts.block_sparse_attention_tiled(q, k, v, bsr), leaves, (heads, S, d), dtype,
                         12)
+
+
+def test_compiled_public_ops(hip_backend):
+    """torch.compile over code that calls the public ops (graph breaks at
+    the planning calls are allowed; results must equal eager calls)."""
+    A = _csr(20000, 15000, 9, 21)
+    gen = torch.Generator().manual_seed(22)
+    mask = torch.rand(4, 4, generator=gen) < 0.5
+    dense = torch.randn(512, 512, generator=gen) * mask.repeat_interleave(128, 0).repeat_interleave(128, 1)
+    Ab = ts.BSRMatrix.from_dense(dense.cuda(), block_size=128)
+    bsr = W.bsr_from_block_mask(W.cfg5_block_mask(4), 128)
+    g = torch.Generator(device="cuda").manual_seed(23)
+    x = torch.randn(15000, device="cuda", generator=g)
+    B = torch.randn(512, 32, device="cuda", generator=g)
+    Q = torch.randn(2, 512, 128, device="cuda", generator=g).to(torch.bfloat16)
+
+    def step(x, B, Q):
+        y = ts.spmv(A, x * 2.0)
+        C = ts.bsr_spmm(Ab, B) + 1.0
+        O = ts.block_sparse_attention_tiled(Q, Q, Q, bsr)
+        return y, C, O
+
+    want = step(x, B, Q)
+    got = torch.compile(step, backend="aot_eager")(x, B, Q)
+    for a, b in zip(got, want):
+        assert torch.equal(a, b)

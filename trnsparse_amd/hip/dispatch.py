@@ -23,6 +23,12 @@ import torch.nn.functional as F
 from . import _lib
 
 
+# Entry points the public API calls: they run the library through ctypes and
+# the registered operators, which torch.compile does not trace into; under
+# compilation each call is a graph break and runs eagerly.
+_library_call = torch.compiler.disable
+
+
 def _target_device(*tensors) -> torch.device:
     for t in tensors:
         if isinstance(t, torch.Tensor) and t.is_cuda:
@@ -175,6 +181,7 @@ def _bsr_bwd_plan(rp: torch.Tensor, ci: torch.Tensor, mb: int, nbc: int, dev: to
     return brow[:nnzb], cp, cbid[:nnzb], crow[:nnzb], corder
 
 
+@_library_call
 def hip_bsr_matvec_update(A, x: torch.Tensor, alpha: float, out: torch.Tensor, u=None, beta: float = 0.0, v=None,
                           gamma: float = 0.0, w=None, delta: float = 0.0) -> torch.Tensor:
     """out = alpha * (A @ x) + beta * u + gamma * v + delta * w in one pass
@@ -205,6 +212,7 @@ def _bsr_blocks_on(A, dev):
     return blocks
 
 
+@_library_call
 def hip_bsr_spmm(A, B: torch.Tensor, out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """BSR SpMM entry point (replaces nki_bsr_spmm, reference dispatch.py:372-381).
 
@@ -480,11 +488,13 @@ def _csr_apply(A, X, alpha, Y, beta):
         return _CSRMatMulFunction.apply(A.values, A.col_indices, A.row_ptrs, tuple(A.shape), X, alpha, Y, beta, prepared)
 
 
+@_library_call
 def hip_spmv(A, x: torch.Tensor, alpha: float = 1.0, y: torch.Tensor | None = None, beta: float = 0.0) -> torch.Tensor:
     """CSR SpMV entry point (the reference's spmv runs torch.sparse_csr @ x, ops.py:30-48)."""
     return _csr_apply(A, x, alpha, y, beta)
 
 
+@_library_call
 def hip_spmm(A, B: torch.Tensor, alpha: float = 1.0, C: torch.Tensor | None = None, beta: float = 0.0) -> torch.Tensor:
     """CSR SpMM entry point (replaces nki_spmm, reference dispatch.py:181-190)."""
     return _csr_apply(A, B, alpha, C, beta)
@@ -562,6 +572,7 @@ class _ScreenedSpMMFunction(torch.autograd.Function):
                 dB.to(B.device) if dB is not None else None)
 
 
+@_library_call
 def hip_screened_spmm(A, diag_integrals, B, threshold: float):
     """Screened SpMM entry point (replaces nki_screened_spmm, reference dispatch.py:487-494)."""
     return _ScreenedSpMMFunction.apply(A, diag_integrals, threshold, B)
@@ -595,6 +606,7 @@ def _pad_head_dim(t: torch.Tensor, dp: int) -> torch.Tensor:
     return torch.nn.functional.pad(t, (0, dp - t.shape[-1]))
 
 
+@_library_call
 def hip_block_sparse_attention(Q, K, V, mask_bsr, scale: float, return_stats: bool = False):
     """Block-sparse attention forward (replaces nki_bsr_attn_tiled, reference
     dispatch.py:580-677). Q/K/V (S, D) or (..., S, D) sharing one mask.
@@ -830,6 +842,7 @@ def _attention_blocks_bwd(q, k, v, o, do, mask_bsr, scale: float, rm, rd, dev):
     return dQ.reshape(H, S, D), dK.reshape(H, S, D), dV.reshape(H, S, D)
 
 
+@_library_call
 def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, row_max, row_denom):
     """Block-sparse attention backward (replaces nki_bsr_attn_bwd, reference
     dispatch.py:813-929, and the torch backward ops.py:360-473).

@@ -17,6 +17,12 @@ from . import _lib
 DEVICE_DTYPES = (torch.float32, torch.float64, torch.bfloat16)
 
 
+# Entry points the public API calls: they run the library through ctypes and
+# the registered operators, which torch.compile does not trace into; under
+# compilation each call is a graph break and runs eagerly.
+_library_call = torch.compiler.disable
+
+
 def _row_major(A: torch.Tensor) -> tuple[torch.Tensor, int]:
     """A with unit column stride and its row stride (elements)."""
     if A.dim() == 2 and A.stride(1) == 1 and A.stride(0) >= max(A.shape[1], 1):
@@ -29,6 +35,7 @@ def _stream(dev: torch.device) -> int:
     return _lib.stream_handle(dev)
 
 
+@_library_call
 def bsr_from_dense(A: torch.Tensor, block_size: int, threshold: float):
     """(blocks, block_col_indices, block_row_ptrs) of BSRMatrix.from_dense
     (reference formats.py:183-221) on A's device."""
@@ -52,6 +59,7 @@ def bsr_from_dense(A: torch.Tensor, block_size: int, threshold: float):
     return blocks, col, rp
 
 
+@_library_call
 def bsr_to_dense(blocks: torch.Tensor, row_ptrs: torch.Tensor, col_indices: torch.Tensor, shape, block_size: int):
     """BSRMatrix.to_dense (reference formats.py:233-251) on the blocks' device."""
     m, n = shape
@@ -66,6 +74,7 @@ def bsr_to_dense(blocks: torch.Tensor, row_ptrs: torch.Tensor, col_indices: torc
     return out
 
 
+@_library_call
 def csr_from_dense(A: torch.Tensor, threshold: float):
     """(values, col_indices, row_ptrs) of formats.from_dense (reference
     formats.py:269-278) on A's device."""
@@ -86,6 +95,7 @@ def csr_from_dense(A: torch.Tensor, threshold: float):
     return val, col, rp
 
 
+@_library_call
 def csr_to_dense(values: torch.Tensor, col_indices: torch.Tensor, row_ptrs: torch.Tensor, shape):
     """CSRMatrix.to_dense (reference formats.py:49-52; duplicates add up)."""
     m, n = shape
@@ -100,6 +110,7 @@ def csr_to_dense(values: torch.Tensor, col_indices: torch.Tensor, row_ptrs: torc
     return out
 
 
+@_library_call
 def csr_row_indices(row_ptrs: torch.Tensor, m: int, nnz: int, dev: torch.device) -> torch.Tensor:
     """Row index of every entry (the expansion in CSRMatrix.to_coo,
     reference formats.py:54-65)."""
@@ -110,6 +121,7 @@ def csr_row_indices(row_ptrs: torch.Tensor, m: int, nnz: int, dev: torch.device)
     return rows
 
 
+@_library_call
 def coo_to_csr(values: torch.Tensor, row_indices: torch.Tensor, col_indices: torch.Tensor, shape):
     """(values, col_indices, row_ptrs) of COOMatrix.to_csr (reference
     formats.py:104-124): stable sort by row*n + col on the device."""
@@ -132,6 +144,7 @@ def coo_to_csr(values: torch.Tensor, row_indices: torch.Tensor, col_indices: tor
     return val, col, rp
 
 
+@_library_call
 def coo_sum_to_csr(values: torch.Tensor, row_indices: torch.Tensor, col_indices: torch.Tensor, shape):
     """(values, col_indices, row_ptrs) with duplicate coordinates summed in
     input order — the coalesce in sparse_add (reference ops.py:107-132)."""
@@ -155,6 +168,7 @@ def coo_sum_to_csr(values: torch.Tensor, row_indices: torch.Tensor, col_indices:
     return val[:u], col[:u], rp
 
 
+@_library_call
 def csr_transpose(values: torch.Tensor, col_indices: torch.Tensor, row_ptrs: torch.Tensor, shape):
     """(values, col_indices, row_ptrs) of A^T (reference ops.py:145-154): a
     stable device sort of the entries by column, rows carried along."""
@@ -178,6 +192,7 @@ def csr_transpose(values: torch.Tensor, col_indices: torch.Tensor, row_ptrs: tor
     return out_val, out_col, out_rp
 
 
+@_library_call
 def csr_sum(a_values: torch.Tensor, a_cols: torch.Tensor, a_row_ptrs: torch.Tensor, b_values: torch.Tensor,
             b_cols: torch.Tensor, b_row_ptrs: torch.Tensor, shape):
     """(values, col_indices, row_ptrs) of the union sum of two CSR operands

@@ -211,3 +211,31 @@ def test_compiled_public_ops(hip_backend):
     got = torch.compile(step, backend="aot_eager")(x, B, Q)
     for a, b in zip(got, want):
         assert torch.equal(a, b)
+
+
+def test_graph_spmm_backward(hip_backend):
+    """Values and dense-operand gradients of the CSR product (the device
+    transpose of the pattern and the SDDMM) captured with the forward."""
+    m, n = 6000, 5000
+    rng = np.random.default_rng(31)
+    v, c, p = W.random_csr(np.minimum(rng.poisson(7, m), n), n, rng)
+    cols, ptrs = torch.from_numpy(c).cuda(), torch.from_numpy(p).cuda()
+    vals = torch.from_numpy(v).cuda().requires_grad_(True)
+    X = torch.randn(n, 8, device="cuda").requires_grad_(True)
+    mats = {}
+
+    def forward(vv, XX):
+        if id(vv) not in mats:
+            mats[id(vv)] = ts.CSRMatrix(values=vv, col_indices=cols, row_ptrs=ptrs, shape=(m, n))
+        return ts.spmm(mats[id(vv)], XX, alpha=0.75)
+
+    _grads_replay_match(forward, [vals, X], (m, 8), torch.float32, 32)
+
+
+def test_graph_screened_spmm_backward(hip_backend):
+    g = torch.Generator(device="cuda").manual_seed(33)
+    n = 384
+    diag = 10.0 ** (-8 * torch.rand(n, device="cuda", generator=g))
+    A = torch.randn(n, n, device="cuda", generator=g).requires_grad_(True)
+    B = torch.randn(n, 48, device="cuda", generator=g).requires_grad_(True)
+    _grads_replay_match(lambda AA, BB: ts.screened_spmm(AA, diag, BB, 1e-6), [A, B], (n, 48), torch.float32, 34)

@@ -717,8 +717,9 @@ def _attn_bwd_plan(mask_bsr, H: int, S: int, dev: torch.device):
 
 # ------------------------------------------- attention as block products
 #
-# Head_dims the one-pass kernels do not hold in registers (over 256; bf16
-# gradients at 256) run as block-sparse products over the mask stacked over
+# Head_dims the one-pass kernels do not hold in registers (over 256 except
+# the bf16 forward up to 512; bf16 gradients at 256 and over) run as
+# block-sparse products over the mask stacked over
 # heads: stacked block row h * Mt + i holds mask block row i shifted by h * Mt
 # block columns, so (H, S, D) operands are its (H * S, D) dense operands.
 # Scores and score gradients are SDDMMs on that pattern (tsp_bsr_sddmm_ex,

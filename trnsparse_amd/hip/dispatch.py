@@ -16,6 +16,8 @@ Kernel failures raise RuntimeError; nothing falls back to another path.
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import torch
 import torch.nn.functional as F
@@ -641,7 +643,7 @@ def hip_block_sparse_attention(Q, K, V, mask_bsr, scale: float, return_stats: bo
         orig = Q.device
         dev = _target_device(Q, K, V)
         with torch.cuda.device(dev):
-            Qd, Kd, Vd = (_pad_head_dim(_on(t, dev).reshape(-1, S, d), bd).contiguous() for t in (Q, K, V))
+            Qd, Kd, Vd = (_pad_head_dim(_on(t, dev).reshape(math.prod(lead), S, d), bd).contiguous() for t in (Q, K, V))
             O, rmax, rden = _attention_blocks_fwd(Qd, Kd, Vd, mask_bsr, scale, dev)
         out = O[..., :d].reshape(*lead, S, d).to(orig)
         if not return_stats:
@@ -659,7 +661,7 @@ def hip_block_sparse_attention(Q, K, V, mask_bsr, scale: float, return_stats: bo
                               mask_bsr.block_row_ptrs.numel() - 1, dev, holder=mask_bsr)
         if rp.numel() < Mt + 1:
             raise IndexError(f"mask has {rp.numel() - 1} block rows, attention needs {Mt}")
-        Qd, Kd, Vd = (_on(t, dev).reshape(-1, S, D) for t in (Q, K, V))
+        Qd, Kd, Vd = (_on(t, dev).reshape(math.prod(lead), S, D) for t in (Q, K, V))
         H = Qd.shape[0]
         O, rmax, rden = _lib.ops().bsa_fwd(Qd, Kd, Vd, rp, ci, b, float(scale), bool(return_stats))
     out = O.reshape(*lead, S, D).to(orig)
@@ -885,7 +887,7 @@ def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, 
         orig = Q.device
         dev = _target_device(Q, K, V, O, dO)
         with torch.cuda.device(dev):
-            q, k, v, o, do = (_pad_head_dim(_on(t, dev, Q.dtype).reshape(-1, S, d), bd).contiguous()
+            q, k, v, o, do = (_pad_head_dim(_on(t, dev, Q.dtype).reshape(math.prod(lead), S, d), bd).contiguous()
                               for t in (Q, K, V, O, dO))
             H = q.shape[0]
             rm = _on(row_max, dev, torch.float32).reshape(H, S)
@@ -906,7 +908,7 @@ def hip_block_sparse_attention_backward(Q, K, V, O, dO, mask_bsr, scale: float, 
         if mb < Mt:
             raise IndexError(f"mask has {mb} block rows, attention needs {Mt}")
         rp, ci, _ = _bsr_plan(mask_bsr.block_col_indices, mask_bsr.block_row_ptrs, mb, dev, holder=mask_bsr)
-        q, k, v, o, do = (_on(t, dev, dt).reshape(-1, S, D) for t in (Q, K, V, O, dO))
+        q, k, v, o, do = (_on(t, dev, dt).reshape(math.prod(lead), S, D) for t in (Q, K, V, O, dO))
         H = q.shape[0]
         cp, crow, nbc, plan, (n_items, n_splits, n_partials) = _attn_bwd_plan(mask_bsr, H, S, dev)
         rm = _on(row_max, dev, sdt).reshape(H, Mt * b)

@@ -442,7 +442,7 @@ class _AttnTiledFunction(torch.autograd.Function):
             return dQ, dK, dV, None, None
         lead = Q.shape[:-2]
         S, D = Q.shape[-2:]
-        q, k, v, o, do = (t.reshape(-1, S, D) for t in (Q, K, V, O, dO))
+        q, k, v, o, do = (t.reshape(math.prod(lead), S, D) for t in (Q, K, V, O, dO))
         rm = row_max.reshape(q.shape[0], -1).to(Q.dtype)
         rd = row_denom.reshape(q.shape[0], -1).to(Q.dtype)
         grads = [
@@ -458,7 +458,7 @@ def _attn_pytorch_batched(Q, K, V, mask_bsr, scale, return_stats=False):
         return _block_sparse_attn_pytorch(Q, K, V, mask_bsr, scale, return_stats=return_stats)
     lead = Q.shape[:-2]
     S, D = Q.shape[-2:]
-    q, k, v = (t.reshape(-1, S, D) for t in (Q, K, V))
+    q, k, v = (t.reshape(math.prod(lead), S, D) for t in (Q, K, V))
     res = [_block_sparse_attn_pytorch(q[h], k[h], v[h], mask_bsr, scale, return_stats=return_stats) for h in range(q.shape[0])]
     if not return_stats:
         return torch.stack(res).reshape(*lead, S, D)

@@ -121,3 +121,52 @@ def test_sweep_screened(hip_backend, seed):
     exact = ref.screened_spmm(An, dn, Bn, thr)
     scale = ref.screened_spmm(An, dn, Bn, thr, absolute=True)
     assert _err(got.double().numpy(), exact, scale) <= TOL[dt], (n, N, dt)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_sweep_bsr_spmm_backward(hip_backend, seed):
+    rng = np.random.default_rng(5000 + seed)
+    b = int(rng.choice([8, 16, 32, 64, 128, 24]))
+    m, k = int(rng.integers(1, 6 * b)), int(rng.integers(1, 6 * b))
+    N = int(rng.choice([1, 8, 33, 128, 200]))
+    dt = [torch.float32, torch.bfloat16][seed % 2]
+    mb, kb = -(-m // b), -(-k // b)
+    mask = torch.from_numpy(rng.random((mb, kb)) < rng.uniform(0.2, 0.9))
+    g = torch.Generator().manual_seed(seed)
+    dense = torch.randn(m, k, generator=g) * mask.repeat_interleave(b, 0).repeat_interleave(b, 1)[:m, :k]
+    A0 = ts.BSRMatrix.from_dense(dense.to(dt).cuda(), block_size=b)
+    blocks = A0.blocks.clone().requires_grad_(True)
+    A = ts.BSRMatrix(blocks=blocks, block_col_indices=A0.block_col_indices, block_row_ptrs=A0.block_row_ptrs,
+                     shape=A0.shape, block_size=b)
+    B = torch.randn(k, N, generator=g).to(dt).cuda().requires_grad_(True)
+    G = torch.randn(m, N, generator=g).to(dt)
+    ts.bsr_spmm(A, B).backward(G.cuda())
+    args = (A0.blocks.cpu().double().numpy(), A0.block_col_indices.cpu().numpy(), A0.block_row_ptrs.cpu().numpy(),
+            (m, k), b, B.detach().cpu().double().numpy(), G.double().numpy())
+    exact = ref.bsr_spmm_backward(*args)
+    scale = ref.bsr_spmm_backward(*args, absolute=True)
+    for got, e, sc in zip((blocks.grad, B.grad), exact, scale):
+        assert _err(got.cpu().double().numpy(), e, sc) <= TOL[dt], (b, m, k, N, dt)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_sweep_attention_backward(hip_backend, seed):
+    rng = np.random.default_rng(6000 + seed)
+    S = int(rng.integers(1, 6)) * 128 + int(rng.choice([0, 0, 60]))
+    d = int(rng.choice([32, 64, 96, 128, 256, 320, 512]))
+    dt = torch.bfloat16 if seed % 2 else torch.float32
+    nb = -(-S // 128)
+    mask = torch.from_numpy(rng.random((nb, nb)) < 0.6)
+    mask_bsr = W.bsr_from_block_mask(mask, 128)
+    g = torch.Generator().manual_seed(seed)
+    Q, K, V, dO = (torch.randn(S, d, generator=g).to(dt) for _ in range(4))
+    scale = float(rng.uniform(0.03, 0.15))
+    q, kk, v = (t.cuda().requires_grad_(True) for t in (Q, K, V))
+    O = ts.block_sparse_attention_tiled(q, kk, v, mask_bsr, scale=scale)
+    O.backward(dO.cuda())
+    ptr, col = mask_bsr.block_row_ptrs.numpy(), mask_bsr.block_col_indices.numpy()
+    args = tuple(t.float().double().numpy() for t in (Q, K, V, O.detach().cpu(), dO)) + (ptr, col, 128, scale)
+    exact = ref.block_sparse_attention_backward(*args)
+    bound = ref.block_sparse_attention_backward(*args, absolute=True)
+    for got, e, a in zip((q.grad, kk.grad, v.grad), exact, bound):
+        assert _err(got.cpu().double().numpy(), e, a) <= TOL[dt], (S, d, dt)

@@ -170,3 +170,53 @@ def test_sweep_attention_backward(hip_backend, seed):
     bound = ref.block_sparse_attention_backward(*args, absolute=True)
     for got, e, a in zip((q.grad, kk.grad, v.grad), exact, bound):
         assert _err(got.cpu().double().numpy(), e, a) <= TOL[dt], (S, d, dt)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_sweep_formats_and_csr_ops(hip_backend, seed):
+    """Structure bit-exact (indices, pointers, value order) and values exact
+    for the device format builders and CSR structure ops on random shapes."""
+    rng = np.random.default_rng(7000 + seed)
+    m, n = int(rng.integers(1, 3000)), int(rng.integers(1, 3000))
+    b = int(rng.choice([8, 16, 32, 64, 128, 40]))
+    thr = float(rng.choice([0.0, 0.5]))
+    dense = rng.standard_normal((m, n)).astype(np.float32)
+    dense[rng.random((m, n)) < rng.uniform(0.5, 0.99)] = 0.0
+    if seed % 3 == 0:
+        dense[: m // 3] = 0.0                                  # empty rows / block rows
+    Dg = torch.from_numpy(dense).cuda()
+    # BSR from_dense / to_dense
+    Ab = ts.BSRMatrix.from_dense(Dg, block_size=b, threshold=thr)
+    eb, ec, ep, _ = ref.bsr_from_dense(dense, b, thr)
+    assert np.array_equal(Ab.block_row_ptrs.cpu().numpy(), ep) and np.array_equal(Ab.block_col_indices.cpu().numpy(), ec)
+    assert np.array_equal(Ab.blocks.cpu().numpy(), eb)
+    assert torch.equal(Ab.to_dense().cpu(), torch.from_numpy(ref.bsr_to_dense(eb, ec, ep, (m, n), b)))
+    # CSR from_dense
+    Ac = ts.from_dense(Dg, threshold=thr)
+    ev, ecol, eptr = ref.csr_from_dense(dense, thr)
+    assert np.array_equal(Ac.row_ptrs.cpu().numpy(), eptr) and np.array_equal(Ac.col_indices.cpu().numpy(), ecol)
+    assert np.array_equal(Ac.values.cpu().numpy(), ev)
+    # COO with duplicates, entries shuffled -> CSR (stable order of equal keys)
+    nnz = len(ev)
+    rows = np.repeat(np.arange(m), np.diff(eptr))
+    perm = rng.permutation(nnz)
+    dup = rng.integers(0, max(nnz, 1), size=nnz // 4) if nnz else np.zeros(0, np.int64)
+    r = np.concatenate([rows[perm], rows[dup]]).astype(np.int64)
+    c = np.concatenate([ecol[perm], ecol[dup]]).astype(np.int64)
+    v = np.concatenate([ev[perm], ev[dup] * 0.5]).astype(np.float32)
+    coo = ts.COOMatrix(values=torch.from_numpy(v).cuda(), row_indices=torch.from_numpy(r).cuda(),
+                       col_indices=torch.from_numpy(c).cuda(), shape=(m, n))
+    C = coo.to_csr()
+    wv, wc, wp = ref.coo_to_csr(v, r, c, (m, n))
+    assert np.array_equal(C.row_ptrs.cpu().numpy(), wp) and np.array_equal(C.col_indices.cpu().numpy(), wc)
+    assert np.array_equal(C.values.cpu().numpy(), wv)
+    # transpose and add
+    T = ts.sparse_transpose(Ac)
+    tv, tc, tp = ref.csr_transpose(ev, ecol, eptr, (m, n))
+    assert np.array_equal(T.row_ptrs.cpu().numpy(), tp) and np.array_equal(T.col_indices.cpu().numpy(), tc)
+    assert np.array_equal(T.values.cpu().numpy(), tv)
+    if m == n:
+        S = ts.sparse_add(Ac, T, alpha=0.5, beta=2.0)
+        sv, sc, sp = ref.sparse_add((ev, ecol, eptr, (m, n)), (tv, tc, tp, (m, n)), 0.5, 2.0)
+        assert np.array_equal(S.row_ptrs.cpu().numpy(), sp) and np.array_equal(S.col_indices.cpu().numpy(), sc)
+        np.testing.assert_allclose(S.values.cpu().numpy(), sv, rtol=1e-6, atol=0)

@@ -259,29 +259,30 @@ __device__ inline int16_t row_exponent(uint32_t mx, uint32_t mn, int64_t cnt) {
   return (int16_t)er;
 }
 
-// 16 lanes per row (build and refresh only): lanes stride the row's
-// entries, xor shuffles combine the max and the smallest nonzero.
-constexpr int REXP_LANES = 16;
-template <typename IdxT>
+// LANES lanes per row (build and refresh only): lanes stride the row's
+// entries, xor shuffles combine the max and the smallest nonzero. 16 lanes
+// when rows average at most 32 entries, else 64: a wavefront then waits on
+// one row instead of on the longest of four.
+template <typename IdxT, int LANES>
 __global__ __launch_bounds__(256) void colplan_rowexp_kernel(const float* __restrict__ vals,
                                                              const IdxT* __restrict__ ptr, int64_t m,
                                                              int16_t* __restrict__ rexp) {
-  const int64_t r = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / REXP_LANES;
-  const int sub = threadIdx.x % REXP_LANES;
+  const int64_t r = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / LANES;
+  const int sub = threadIdx.x % LANES;
   int64_t p0 = 0, p1 = 0;
   if (r < m) {
     p0 = (int64_t)ptr[r];
     p1 = (int64_t)ptr[r + 1];
   }
   uint32_t mx = 0, mn = 0xffffffffu;
-  for (int64_t p = p0 + sub; p < p1; p += REXP_LANES) {
+  for (int64_t p = p0 + sub; p < p1; p += LANES) {
     const uint32_t b = __float_as_uint(vals[p]) & 0x7fffffffu;
     mx = b > mx ? b : mx;
     if (b != 0 && b < mn) mn = b;
   }
-  for (int o = REXP_LANES / 2; o > 0; o >>= 1) {
-    const uint32_t a = (uint32_t)__shfl_xor((int)mx, o, REXP_LANES);
-    const uint32_t c = (uint32_t)__shfl_xor((int)mn, o, REXP_LANES);
+  for (int o = LANES / 2; o > 0; o >>= 1) {
+    const uint32_t a = (uint32_t)__shfl_xor((int)mx, o, LANES);
+    const uint32_t c = (uint32_t)__shfl_xor((int)mn, o, LANES);
     mx = a > mx ? a : mx;
     mn = c < mn ? c : mn;
   }
@@ -701,6 +702,16 @@ int geometry(int64_t m, int64_t n, int64_t nnz, int rbits_hint, int64_t tiles_hi
   return TSP_OK;
 }
 
+template <typename IdxT>
+void launch_rowexp(const float* vals, const IdxT* ptr, int64_t m, int64_t nnz, int16_t* rexp, hipStream_t st) {
+  if (nnz > 32 * m)
+    hipLaunchKernelGGL((colplan_rowexp_kernel<IdxT, 64>), dim3((unsigned)tsp::ceil_div(m * 64, 256)), dim3(256), 0, st,
+                       vals, ptr, m, rexp);
+  else
+    hipLaunchKernelGGL((colplan_rowexp_kernel<IdxT, 16>), dim3((unsigned)tsp::ceil_div(m * 16, 256)), dim3(256), 0, st,
+                       vals, ptr, m, rexp);
+}
+
 struct PlanView {
   int64_t* toff;
   int64_t* eoff;
@@ -785,8 +796,7 @@ int build_typed(const float* vals, const void* col, const void* ptr, int64_t m, 
   hipLaunchKernelGGL(colplan_epochs_kernel, dim3(1), dim3(1024), 0, st, v.toff, T, v.eoff);
   rc = tsp::check_launch("colplan_epochs launch");
   if (rc) return rc;
-  hipLaunchKernelGGL((colplan_rowexp_kernel<IdxT>), dim3((unsigned)tsp::ceil_div(m * REXP_LANES, 256)), dim3(256), 0, st,
-                     vals, (const IdxT*)ptr, m, v.rexp);
+  launch_rowexp(vals, (const IdxT*)ptr, m, nnz, v.rexp, st);
   rc = tsp::check_launch("colplan_rowexp launch");
   if (rc || nnz == 0) return rc;
   hipLaunchKernelGGL((colplan_scatter_kernel<K>), dim3((unsigned)tsp::ceil_div(nnz, 256)), dim3(256), 0, st, kout,
@@ -840,11 +850,9 @@ extern "C" int tsp_csr_colplan_refresh(const void* values, int dtype, const void
   hipStream_t st = (hipStream_t)stream;
   PlanView v = plan_view(plan, geometry);
   if (index_type == TSP_I64)
-    hipLaunchKernelGGL((colplan_rowexp_kernel<int64_t>), dim3((unsigned)tsp::ceil_div(m * REXP_LANES, 256)), dim3(256), 0,
-                       st, (const float*)values, (const int64_t*)row_ptrs, m, v.rexp);
+    launch_rowexp((const float*)values, (const int64_t*)row_ptrs, m, nnz, v.rexp, st);
   else
-    hipLaunchKernelGGL((colplan_rowexp_kernel<int32_t>), dim3((unsigned)tsp::ceil_div(m * REXP_LANES, 256)), dim3(256), 0,
-                       st, (const float*)values, (const int32_t*)row_ptrs, m, v.rexp);
+    launch_rowexp((const float*)values, (const int32_t*)row_ptrs, m, nnz, v.rexp, st);
   rc = tsp::check_launch("colplan_rowexp launch");
   if (rc || nnz == 0) return rc;
   hipLaunchKernelGGL(colplan_refresh_kernel, dim3((unsigned)tsp::ceil_div(v.pmax, 256)), dim3(256), 0, st,

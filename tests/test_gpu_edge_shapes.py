@@ -99,3 +99,31 @@ def test_strided_views(hip_backend):
     _same(want, got, 1e-4)
     want, got = _both(lambda dev: ts.block_sparse_attention_tiled(*(t.to(dev).permute(0, 2, 1, 3) for t in qkv), bsr))
     _same(want, got, 1e-4)
+
+
+@pytest.mark.parametrize("mode", ["never", "always"])
+def test_replaced_host_values_are_not_served_from_cache(hip_backend, mode):
+    """A host-resident CSR matrix whose values tensor is replaced: the new
+    tensor may be allocated where the freed one was, with the same version
+    counter; the device copies cached on the matrix keep their source
+    tensors alive, so the key cannot match and the product uses the new
+    values."""
+    from oracle import ref
+    from trnsparse_amd.hip import dispatch as D
+
+    prev = D.get_spmv_plan()
+    D.set_spmv_plan(mode)
+    try:
+        A = _csr(3000, 2000, "cpu", density=0.01, seed=7)
+        x = torch.randn(2000, generator=torch.Generator().manual_seed(8))
+        nnz = A.values.numel()
+        for rep in range(4):
+            y = ts.spmv(A, x.cuda()).cpu()
+            want = ref.csr_spmv(A.values.numpy(), A.col_indices.numpy(), A.row_ptrs.numpy(), A.shape, x.numpy())
+            scale = ref.csr_spmv(A.values.numpy(), A.col_indices.numpy(), A.row_ptrs.numpy(), A.shape, x.numpy(),
+                                 absolute=True)
+            assert ref.scaled_error(y.numpy(), want, scale) <= 1e-4, rep
+            A.values = None                                   # free the old values first
+            A.values = torch.randn(nnz, generator=torch.Generator().manual_seed(20 + rep))
+    finally:
+        D.set_spmv_plan(prev)

@@ -72,7 +72,9 @@ def _bsr_plan(col_idx: torch.Tensor, row_ptrs: torch.Tensor, mb: int, dev: torch
     plan = (rp, ci, order)
     if holder is not None:
         try:
-            holder._hip_plan = (key, plan)
+            # the source tensors ride along: while the entry lives their
+            # addresses cannot be reused by new tensors with the same key
+            holder._hip_plan = (key, plan, (row_ptrs, col_idx))
         except AttributeError:
             pass
     return plan
@@ -263,7 +265,7 @@ def _csr_device(A, dev: torch.device):
     _lib.call("tsp_csr_plan", ptrs.data_ptr(), _lib.index_code(itype), m, nnz, win.data_ptr(), _lib.stream_handle(dev))
     res = (vals, cols, ptrs, win)
     try:
-        A._hip_csr = (key, res)
+        A._hip_csr = (key, res, (A.values, A.col_indices, A.row_ptrs))  # sources kept alive, as above
     except AttributeError:
         pass
     return res

@@ -210,7 +210,7 @@ def _bsr_blocks_on(A, dev):
         return cached[1]
     blocks = A.blocks.to(dev).contiguous()
     try:
-        A._hip_blocks = (key, blocks)
+        A._hip_blocks = (key, blocks, A.blocks)  # source kept alive, as for the pattern plans
     except AttributeError:
         pass
     return blocks

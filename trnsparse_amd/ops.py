@@ -116,7 +116,9 @@ def _strict_transpose(A: CSRMatrix) -> CSRMatrix:
                                        (A.shape[1], A.shape[0]))
     St = CSRMatrix(values=vals, col_indices=cols, row_ptrs=rp, shape=(A.shape[1], A.shape[0]))
     try:
-        A._strict_t = (key, St)
+        # the source tensors ride along, so a new tensor cannot take a freed
+        # one's address (and key) while this entry lives
+        A._strict_t = (key, St, (A.values, A.col_indices, A.row_ptrs))
     except AttributeError:
         pass
     return St

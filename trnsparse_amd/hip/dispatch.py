@@ -713,7 +713,7 @@ def _attn_bwd_plan(mask_bsr, H: int, S: int, dev: torch.device):
     out = (torch.from_numpy(cp).to(dev), torch.from_numpy(crow if crow.size else np.zeros(1, np.int64)).to(dev), nbc,
            torch.from_numpy(plan).to(dev), header)
     try:
-        ci_t._tsp_attn_bwd_plan = (key, out)
+        ci_t._tsp_attn_bwd_plan = (key, out, rp_t)  # the row pointers kept alive with the entry
     except AttributeError:
         pass
     return out
@@ -778,7 +778,7 @@ def _attn_stack_plan(mask_bsr, H: int, S: int, dev: torch.device):
     brow, cp, cbid, crow, corder = _bsr_bwd_plan(rp_d, ci_d, nbr, nbr, dev)
     out = (rp_d, ci_d, order, brow, cp, cbid, crow, corder, int(col.size))
     try:
-        ci_t._tsp_attn_stack_plan = (key, out)
+        ci_t._tsp_attn_stack_plan = (key, out, rp_t)  # the row pointers kept alive with the entry
     except AttributeError:
         pass
     return out

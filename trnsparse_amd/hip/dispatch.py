@@ -16,6 +16,7 @@ Kernel failures raise RuntimeError; nothing falls back to another path.
 
 from __future__ import annotations
 
+import functools
 import math
 
 import numpy as np
@@ -27,8 +28,22 @@ from . import _lib
 
 # Entry points the public API calls: they run the library through ctypes and
 # the registered operators, which torch.compile does not trace into; under
-# compilation each call is a graph break and runs eagerly.
-_library_call = torch.compiler.disable
+# compilation each call is a graph break and runs eagerly. The compiler's
+# disable wrapper is made only once compilation is under way: merely loading
+# the compiler stack at import (torch.compiler.disable at module level) made
+# the headline product 9 % slower, with a lower GPU clock.
+def _library_call(fn):
+    guarded = []
+
+    @functools.wraps(fn)
+    def call(*args, **kwargs):
+        if torch.compiler.is_compiling():
+            if not guarded:
+                guarded.append(torch.compiler.disable(fn))
+            return guarded[0](*args, **kwargs)
+        return fn(*args, **kwargs)
+
+    return call
 
 
 def _target_device(*tensors) -> torch.device:
